@@ -1,0 +1,32 @@
+"""dabsn_amd: MI355X (gfx950) backend for DABSN's recurrent hot path.
+
+The package registers the ``dabsn::`` operators of the core scan, the three-way read,
+the long-memory scan and the read glue with hand-written HIP kernels
+(``dabsn_amd/csrc``, C ABI in ``include/dabsn_hip.h``), and mirrors the reference's
+``DABSNCore`` / ``DABSNRead`` / seq ``DABSNBlock`` on top of them.
+"""
+
+from . import kernels
+from .core import DABSNCore
+from .events import (
+    EventCode,
+    StrictFallbackError,
+    add_event_listener,
+    remove_event_listener,
+    strict_events,
+)
+from .model import DABSNBlock, DABSNSequenceLM
+from .read import DABSNRead
+
+__all__ = [
+    "DABSNBlock",
+    "DABSNCore",
+    "DABSNRead",
+    "DABSNSequenceLM",
+    "EventCode",
+    "StrictFallbackError",
+    "add_event_listener",
+    "kernels",
+    "remove_event_listener",
+    "strict_events",
+]

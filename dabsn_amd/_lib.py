@@ -1,0 +1,125 @@
+"""ctypes binding of the C ABI in ``include/dabsn_hip.h``.
+
+The library is ``dabsn_amd/_build/libdabsn_hip.so`` (built by ``dabsn_amd.build``). It is
+loaded lazily on first use; a missing library is a hard error on any GPU call, never a
+silent fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
+ABI_VERSION = 1
+
+_lock = threading.Lock()
+_lib = None
+_load_error: str | None = None
+
+vp = ctypes.c_void_p
+i64 = ctypes.c_int64
+i32 = ctypes.c_int
+sz = ctypes.c_size_t
+
+
+class CoreParams(ctypes.Structure):
+    """Mirror of ``dabsn_core_params``."""
+
+    _fields_ = [("vec", vp * 16), ("scal", vp * 3)]
+
+
+PTR4 = vp * 4
+
+_SIGNATURES = {
+    "dabsn_hip_abi_version": ([], i32),
+    "dabsn_hip_last_error": ([], ctypes.c_char_p),
+    "dabsn_hip_zero": ([vp, sz, vp], i32),
+    "dabsn_hip_core_scan_workspace_bytes": ([i32, i64, i64, i32], sz),
+    "dabsn_hip_core_scan_layout": ([i32, i64, i64, ctypes.POINTER(i64), ctypes.POINTER(i64)], i32),
+    "dabsn_hip_core_scan_fwd": (
+        [i32, i64, i64, i64, vp, vp, vp, ctypes.POINTER(CoreParams), vp, vp, vp]
+        + [vp] * 8 + [vp, vp, vp, vp, sz, vp],
+        i32,
+    ),
+    "dabsn_hip_core_scan_bwd": (
+        [i32, i64, i64, i64, vp, ctypes.POINTER(CoreParams), vp, vp]
+        + [vp] * 6 + [vp] * 7 + [vp] * 3 + [vp] * 3 + [vp, vp] + [vp] * 3 + [vp, sz, vp],
+        i32,
+    ),
+    "dabsn_hip_linrec_fwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_linrec_workspace_bytes": ([i32, i64, i64, i64], sz),
+    "dabsn_hip_linrec_bwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
+    "dabsn_hip_long_fwd": ([i32, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_long_partials": ([i64, i64], i64),
+    "dabsn_hip_long_bwd": (
+        [i32, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+        i32,
+    ),
+    "dabsn_hip_tape_stats": ([i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_tape_stats_bwd": (
+        [i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_normalize_rows": ([i32, i64, i64, vp, vp, vp, vp], i32),
+    "dabsn_hip_normalize_rows_bwd": ([i32, i64, i64, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_bank_select": ([i64, i64, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_bank_gather": ([i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_bank_gather_bwd": (
+        [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_read3_workspace_bytes": ([i32, i64, i64, i64, i64, i32], sz),
+    "dabsn_hip_read3_fwd": (
+        [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4, vp, vp,
+         sz, vp],
+        i32,
+    ),
+    "dabsn_hip_read3_bwd": (
+        [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4]
+        + [vp] * 4 + [vp] * 5 + [vp, sz, vp],
+        i32,
+    ),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+
+def load():
+    """Load (once) and return the ctypes library; raises if it is missing."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = Path(os.environ.get("DABSN_HIP_LIB", str(LIB_PATH)))
+        if not path.exists():
+            _load_error = f"{path} is not built (run dabsn_amd.build.build())"
+            raise RuntimeError(f"DABSN HIP library unavailable: {_load_error}")
+        lib = ctypes.CDLL(str(path))
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        version = lib.dabsn_hip_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"DABSN HIP library ABI {version} != expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except Exception:  # noqa: BLE001 - reported by status()
+        return False
+
+
+def load_error() -> str | None:
+    return _load_error
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = _lib.dabsn_hip_last_error().decode(errors="replace") if _lib else "library not loaded"
+        raise RuntimeError(f"DABSN HIP {what} failed (status {rc}): {msg}")

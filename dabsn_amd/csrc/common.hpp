@@ -1,0 +1,87 @@
+// Shared device helpers for the DABSN gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace dabsn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Storage types: fp32 tapes are `float`, bf16 tapes are raw `uint16_t` bits.
+using bf16 = uint16_t;
+
+enum DType : int { kF32 = 0, kBF16 = 1 };
+
+__device__ __forceinline__ float bf2f(bf16 h) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (matches torch's .to(torch.bfloat16)).
+__device__ __forceinline__ bf16 f2bf(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16>(u >> 16);
+}
+
+template <typename E>
+__device__ __forceinline__ float ld(const E* p, size_t i);
+template <>
+__device__ __forceinline__ float ld<float>(const float* p, size_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float ld<bf16>(const bf16* p, size_t i) { return bf2f(p[i]); }
+
+template <typename E>
+__device__ __forceinline__ void st(E* p, size_t i, float v);
+template <>
+__device__ __forceinline__ void st<float>(float* p, size_t i, float v) { p[i] = v; }
+template <>
+__device__ __forceinline__ void st<bf16>(bf16* p, size_t i, float v) { p[i] = f2bf(v); }
+
+// Value as it would be stored in E (identity for fp32, RTNE round trip for bf16).
+template <typename E>
+__device__ __forceinline__ float round_to(float v);
+template <>
+__device__ __forceinline__ float round_to<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float round_to<bf16>(float v) { return bf2f(f2bf(v)); }
+
+template <typename E>
+struct is_bf16 { static constexpr bool value = false; };
+template <>
+struct is_bf16<bf16> { static constexpr bool value = true; };
+
+// Buffer resource over [base, base + bytes); out-of-range accesses are dropped (stores)
+// or return zero (loads). Third dword per the gfx9 buffer descriptor format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+// Cache-policy bit for device-coherent (cross-XCD) vector memory accesses.
+constexpr int kCoherent = 16;  // sc1
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float softplusf_(float x) {
+  return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+}
+__device__ __forceinline__ float hardsigmoidf_(float x) {
+  return fminf(fmaxf(x + 3.0f, 0.0f), 6.0f) * (1.0f / 6.0f);
+}
+__device__ __forceinline__ float clamp01(float x) { return fminf(fmaxf(x, 0.0f), 1.0f); }
+__device__ __forceinline__ float signf_(float x) {
+  return static_cast<float>((x > 0.0f) - (x < 0.0f));
+}
+
+// Spin bound for device-wide step barriers: any wait longer than this (seconds of
+// polling) sets the error flag and the kernel exits instead of hanging.
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+// Error bits reported through the workspace error word.
+constexpr uint32_t kErrBarrierTimeout = 1u;
+
+}  // namespace dabsn

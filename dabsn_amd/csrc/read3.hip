@@ -1,0 +1,625 @@
+// Three-way admitted read (short, permanent, induction) over the compact bank ABI.
+//
+// Reference math: src/dabsn/kernels/admitted.py:9-65 (forward) and 116-239 (analytic
+// backward); compact masks compact_admitted.py:176-198; CPU kernels
+// cpu_runtime.cpp:321-438 and 479-662. Op boundary: dabsn::admitted_three_way_read_
+// compact_flash and its backward op (compact_flash.py:71-107, 181-224).
+//
+// Structure (per batch row, queries t, bank slots j, width H):
+//   S = Q K^T                        MFMA GEMM, fp32, only tiles with an allowed entry
+//   softmax rows                     three masked softmaxes from S, key bias, admission,
+//                                    cocktail term; writes P_V = sg Ps + pg Pp and
+//                                    P_Vn = ig Pi (short and permanent share the values)
+//   out = P_V V + P_Vn Vn            one MFMA GEMM over both products
+// Backward recomputes S and the row statistics, forms dP = gO V^T, gO Vn^T, the score
+// gradient G row by row, then gQ = G K, gK = G^T Q, gV = P_V^T gO, gVn = P_Vn^T gO.
+// Tile ranges follow the causal staircase: a query tile only visits bank slots that
+// any of its queries may read; a bank tile only visits queries at or after its
+// earliest admitted index.
+#include "../../include/dabsn_hip.h"
+#include "capi.hpp"
+#include "common.hpp"
+#include "gemm.hpp"
+
+namespace dabsn {
+namespace read3 {
+
+constexpr int TILE = 128;   // GEMM tile rows (query tiles and bank tiles)
+constexpr int RT = 32;      // rows per workgroup in the gradient kernel
+constexpr int CC = 2048;    // columns per workgroup in the gradient kernel
+constexpr int NTH = 256;
+
+struct Gains {
+  const float* p[4];  // short, pad, induct, cocktail
+};
+
+__device__ __forceinline__ bool allow_at(int mode, int64_t idx, bool valid, int t) {
+  return valid && (mode != 0 || idx <= t);
+}
+__device__ __forceinline__ bool induct_at(int mode, int64_t idx, bool valid, int t, int T) {
+  return valid && (mode != 0 ? idx < T - 1 : idx < t);
+}
+
+// Per query tile: nhi = 1 + max allowed slot of the tile's last query; per bank tile:
+// tlo = earliest query that may read any slot of the tile.
+__global__ void ranges_kernel(int T, int N, int H, int mode, const int64_t* idx,
+                              const uint8_t* valid, int32_t* rs, int32_t* ro, int32_t* rb) {
+  const int b = blockIdx.y;
+  const int QT = (T + TILE - 1) / TILE, BT = (N + TILE - 1) / TILE;
+  const int item = blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t* ib = idx + static_cast<size_t>(b) * N;
+  const uint8_t* vb = valid + static_cast<size_t>(b) * N;
+  if (item < QT) {
+    const int tl = min(T - 1, item * TILE + TILE - 1);
+    int nhi = 0;
+    for (int j = 0; j < N; ++j)
+      if (allow_at(mode, ib[j], vb[j] != 0, tl)) nhi = j + 1;
+    int32_t* s = rs + (static_cast<size_t>(b) * QT + item) * 3;
+    s[0] = 0; s[1] = H; s[2] = nhi;
+    int32_t* o = ro + (static_cast<size_t>(b) * QT + item) * 3;
+    o[0] = 0; o[1] = nhi; o[2] = H;
+  } else if (item < QT + BT) {
+    const int bt = item - QT;
+    int64_t tlo = T;
+    for (int j = bt * TILE; j < min(N, bt * TILE + TILE); ++j) {
+      if (!vb[j]) continue;
+      const int64_t first = mode != 0 ? 0 : (ib[j] < 0 ? 0 : ib[j]);
+      tlo = first < tlo ? first : tlo;
+    }
+    int32_t* r = rb + (static_cast<size_t>(b) * BT + bt) * 3;
+    r[0] = static_cast<int32_t>(tlo); r[1] = T; r[2] = H;
+  }
+}
+
+__device__ __forceinline__ float block_max(float v, float* sh) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+}
+__device__ __forceinline__ float block_sum(float v, float* sh) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+
+struct RowCtx {
+  int T, N, mode;
+  const float* S;
+  const float* kb;
+  const float* adm;
+  const float* cb;
+  const float* ck;
+  const int64_t* idx;
+  const uint8_t* valid;
+  float scale, sg, pg, ig, cg;
+};
+
+// Scores of slot j for query t: short = scale*S + kb + adm; perm = short + cg*(ck . cb).
+__device__ __forceinline__ void scores(const RowCtx& c, int b, int t, int j, const float* ckt,
+                                       float& s_short, float& s_perm, float& cc, float& sraw) {
+  const size_t bj = static_cast<size_t>(b) * c.N + j;
+  sraw = c.S[(static_cast<size_t>(b) * c.T + t) * c.N + j];
+  const float content = sraw * c.scale + c.kb[bj];
+  const float* cbj = c.cb + bj * 4;
+  cc = ckt[0] * cbj[0] + ckt[1] * cbj[1] + ckt[2] * cbj[2] + ckt[3] * cbj[3];
+  s_short = content + c.adm[bj];
+  s_perm = content + cc * c.cg + c.adm[bj];
+}
+
+// Row statistics (max and sum of each masked softmax), one workgroup per query row.
+// stats[row] = (m_s, l_s, m_p, l_p, m_i, l_i); l = 0 marks an empty pathway.
+// When P_V is non-null also writes P_V / P_Vn for j < nhi of the row's tile.
+template <typename E>
+__global__ void __launch_bounds__(NTH) softmax_fwd_kernel(RowCtx c, Gains g, const float* scale_p,
+                                                          const int32_t* rs, float* stats, E* PV,
+                                                          E* PVn) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const int b = static_cast<int>(row / c.T), t = static_cast<int>(row % c.T);
+  c.scale = scale_p[0];
+  c.sg = g.p[0][0]; c.pg = g.p[1][0]; c.ig = g.p[2][0]; c.cg = g.p[3][0];
+  const int QT = (c.T + TILE - 1) / TILE;
+  const int nhi = rs[(static_cast<size_t>(b) * QT + t / TILE) * 3 + 2];
+  const float* ckt = c.ck + static_cast<size_t>(row) * 4;
+  const int64_t* ib = c.idx + static_cast<size_t>(b) * c.N;
+  const uint8_t* vb = c.valid + static_cast<size_t>(b) * c.N;
+  float ms = -INFINITY, mp = -INFINITY, mi = -INFINITY;
+  for (int j = threadIdx.x; j < nhi; j += NTH) {
+    float ss, sp, cc, sr;
+    scores(c, b, t, j, ckt, ss, sp, cc, sr);
+    if (allow_at(c.mode, ib[j], vb[j] != 0, t)) {
+      ms = fmaxf(ms, ss);
+      mp = fmaxf(mp, sp);
+    }
+    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) mi = fmaxf(mi, ss);
+  }
+  ms = block_max(ms, sh);
+  mp = block_max(mp, sh);
+  mi = block_max(mi, sh);
+  float ls = 0.f, lp = 0.f, li = 0.f;
+  for (int j = threadIdx.x; j < nhi; j += NTH) {
+    float ss, sp, cc, sr;
+    scores(c, b, t, j, ckt, ss, sp, cc, sr);
+    if (allow_at(c.mode, ib[j], vb[j] != 0, t)) {
+      ls += expf(ss - ms);
+      lp += expf(sp - mp);
+    }
+    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) li += expf(ss - mi);
+  }
+  ls = block_sum(ls, sh);
+  lp = block_sum(lp, sh);
+  li = block_sum(li, sh);
+  if (threadIdx.x == 0) {
+    float* o = stats + static_cast<size_t>(row) * 6;
+    o[0] = ms; o[1] = ls; o[2] = mp; o[3] = lp; o[4] = mi; o[5] = li;
+  }
+  if (PV == nullptr) return;
+  const float is = ls > 0.f ? 1.0f / ls : 0.f, ip = lp > 0.f ? 1.0f / lp : 0.f,
+              ii = li > 0.f ? 1.0f / li : 0.f;
+  for (int j = threadIdx.x; j < nhi; j += NTH) {
+    float ss, sp, cc, sr;
+    scores(c, b, t, j, ckt, ss, sp, cc, sr);
+    float pv = 0.f, pn = 0.f;
+    if (allow_at(c.mode, ib[j], vb[j] != 0, t)) pv = c.sg * (expf(ss - ms) * is) + c.pg * (expf(sp - mp) * ip);
+    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) pn = c.ig * (expf(ss - mi) * ii);
+    const size_t o = static_cast<size_t>(row) * c.N + j;
+    st(PV, o, pv);
+    st(PVn, o, pn);
+  }
+}
+
+// Per-row reductions needed by the score gradient: rs = sum Ps dPV, rp = sum Pp dPV,
+// ri = sum Pi dPVn (unscaled by the gains).
+__global__ void __launch_bounds__(NTH) grad_rows_kernel(RowCtx c, Gains g, const float* scale_p,
+                                                        const int32_t* rs_rng, const float* stats,
+                                                        const float* dPV, const float* dPVn,
+                                                        float* rowA) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const int b = static_cast<int>(row / c.T), t = static_cast<int>(row % c.T);
+  c.scale = scale_p[0];
+  c.cg = g.p[3][0];
+  const int QT = (c.T + TILE - 1) / TILE;
+  const int nhi = rs_rng[(static_cast<size_t>(b) * QT + t / TILE) * 3 + 2];
+  const float* st6 = stats + static_cast<size_t>(row) * 6;
+  const float is = st6[1] > 0.f ? 1.0f / st6[1] : 0.f, ip = st6[3] > 0.f ? 1.0f / st6[3] : 0.f,
+              ii = st6[5] > 0.f ? 1.0f / st6[5] : 0.f;
+  const float* ckt = c.ck + static_cast<size_t>(row) * 4;
+  const int64_t* ib = c.idx + static_cast<size_t>(b) * c.N;
+  const uint8_t* vb = c.valid + static_cast<size_t>(b) * c.N;
+  float rsum = 0.f, psum = 0.f, isum = 0.f;
+  for (int j = threadIdx.x; j < nhi; j += NTH) {
+    float ss, sp, cc, sr;
+    scores(c, b, t, j, ckt, ss, sp, cc, sr);
+    const size_t o = static_cast<size_t>(row) * c.N + j;
+    if (allow_at(c.mode, ib[j], vb[j] != 0, t)) {
+      const float d = dPV[o];
+      rsum += expf(ss - st6[0]) * is * d;
+      psum += expf(sp - st6[2]) * ip * d;
+    }
+    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) isum += expf(ss - st6[4]) * ii * dPVn[o];
+  }
+  rsum = block_sum(rsum, sh);
+  psum = block_sum(psum, sh);
+  isum = block_sum(isum, sh);
+  if (threadIdx.x == 0) {
+    float* o = rowA + static_cast<size_t>(row) * 3;
+    o[0] = rsum; o[1] = psum; o[2] = isum;
+  }
+}
+
+// Score gradient for a tile of RT rows x CC columns. Writes Gs = scale*G, P_V, P_Vn;
+// per-(row, column chunk) partials rowB = (G.S, dSp.cc, cg dSp cb[0..3]) and per-(row
+// tile, column) partials colp = (sum G, cg sum dSp ck[0..3]).
+template <typename E>
+__global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const float* scale_p,
+                                                        const int32_t* rs_rng, const float* stats,
+                                                        const float* rowA, const float* dPV,
+                                                        const float* dPVn, E* Gs, E* PV, E* PVn,
+                                                        float* rowB, float* colp) {
+  __shared__ float sh[4];
+  constexpr int CJ = CC / NTH;
+  const int b = blockIdx.z, rt = blockIdx.y, cch = blockIdx.x;
+  const int NCC = (c.N + CC - 1) / CC;
+  c.scale = scale_p[0];
+  c.sg = g.p[0][0]; c.pg = g.p[1][0]; c.ig = g.p[2][0]; c.cg = g.p[3][0];
+  const int QT = (c.T + TILE - 1) / TILE;
+  const int64_t* ib = c.idx + static_cast<size_t>(b) * c.N;
+  const uint8_t* vb = c.valid + static_cast<size_t>(b) * c.N;
+  float colG[CJ], colC[CJ][4];
+#pragma unroll
+  for (int q = 0; q < CJ; ++q) {
+    colG[q] = 0.f;
+    colC[q][0] = colC[q][1] = colC[q][2] = colC[q][3] = 0.f;
+  }
+  const int t0 = rt * RT, t1 = min(c.T, t0 + RT);
+  for (int t = t0; t < t1; ++t) {
+    const size_t row = static_cast<size_t>(b) * c.T + t;
+    const int nhi = rs_rng[(static_cast<size_t>(b) * QT + t / TILE) * 3 + 2];
+    const float* st6 = stats + row * 6;
+    const float is = st6[1] > 0.f ? 1.0f / st6[1] : 0.f, ip = st6[3] > 0.f ? 1.0f / st6[3] : 0.f,
+                ii = st6[5] > 0.f ? 1.0f / st6[5] : 0.f;
+    const float ra = rowA[row * 3], rp = rowA[row * 3 + 1], ri = rowA[row * 3 + 2];
+    const float* ckt = c.ck + row * 4;
+    float gsc = 0.f, gcg = 0.f, gk0 = 0.f, gk1 = 0.f, gk2 = 0.f, gk3 = 0.f;
+    // The transposed GEMMs read whole 128-wide slot tiles of any row inside their
+    // k-range, so slots in [nhi, roundup(nhi, TILE)) are written as explicit zeros.
+    const int jlim = min(c.N, ((nhi + TILE - 1) / TILE) * TILE);
+#pragma unroll
+    for (int q = 0; q < CJ; ++q) {
+      const int j = cch * CC + q * NTH + threadIdx.x;
+      if (j >= jlim) continue;
+      const size_t o = row * c.N + j;
+      if (j >= nhi) {
+        st(Gs, o, 0.0f);
+        st(PV, o, 0.0f);
+        st(PVn, o, 0.0f);
+        continue;
+      }
+      float ss, sp, cc, sr;
+      scores(c, b, t, j, ckt, ss, sp, cc, sr);
+      float ps = 0.f, pp = 0.f, pi = 0.f, dss = 0.f, dsp = 0.f, dsi = 0.f;
+      if (allow_at(c.mode, ib[j], vb[j] != 0, t)) {
+        const float d = dPV[o];
+        ps = expf(ss - st6[0]) * is;
+        pp = expf(sp - st6[2]) * ip;
+        dss = c.sg * ps * (d - ra);
+        dsp = c.pg * pp * (d - rp);
+      }
+      if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) {
+        pi = expf(ss - st6[4]) * ii;
+        dsi = c.ig * pi * (dPVn[o] - ri);
+      }
+      const float G = dss + dsp + dsi;
+      st(Gs, o, G * c.scale);
+      st(PV, o, c.sg * ps + c.pg * pp);
+      st(PVn, o, c.ig * pi);
+      gsc += G * sr;
+      gcg += dsp * cc;
+      const float* cbj = c.cb + (static_cast<size_t>(b) * c.N + j) * 4;
+      const float w = dsp * c.cg;
+      gk0 += w * cbj[0]; gk1 += w * cbj[1]; gk2 += w * cbj[2]; gk3 += w * cbj[3];
+      colG[q] += G;
+      colC[q][0] += w * ckt[0]; colC[q][1] += w * ckt[1];
+      colC[q][2] += w * ckt[2]; colC[q][3] += w * ckt[3];
+    }
+    gsc = block_sum(gsc, sh);
+    gcg = block_sum(gcg, sh);
+    gk0 = block_sum(gk0, sh);
+    gk1 = block_sum(gk1, sh);
+    gk2 = block_sum(gk2, sh);
+    gk3 = block_sum(gk3, sh);
+    if (threadIdx.x == 0) {
+      float* o = rowB + (row * NCC + cch) * 6;
+      o[0] = gsc; o[1] = gcg; o[2] = gk0; o[3] = gk1; o[4] = gk2; o[5] = gk3;
+    }
+  }
+  const int RTILES = (c.T + RT - 1) / RT;
+#pragma unroll
+  for (int q = 0; q < CJ; ++q) {
+    const int j = cch * CC + q * NTH + threadIdx.x;
+    if (j >= c.N) continue;
+    float* o = colp + ((static_cast<size_t>(b) * RTILES + rt) * c.N + j) * 5;
+    o[0] = colG[q];
+    o[1] = colC[q][0]; o[2] = colC[q][1]; o[3] = colC[q][2]; o[4] = colC[q][3];
+  }
+}
+
+// Column reductions over row tiles: gkb = gadm = sum G; gcb = cg sum dSp ck.
+__global__ void reduce_cols_kernel(int T, int N, const float* colp, float* gkb, float* gadm,
+                                   float* gcb) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= N) return;
+  const int RTILES = (T + RT - 1) / RT;
+  float s[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < RTILES; ++r) {
+    const float* p = colp + ((static_cast<size_t>(b) * RTILES + r) * N + i) * 5;
+#pragma unroll
+    for (int k = 0; k < 5; ++k) s[k] += p[k];
+  }
+  const size_t o = static_cast<size_t>(b) * N + i;
+  gkb[o] = s[0];
+  gadm[o] = s[0];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) gcb[o * 4 + k] = s[1 + k];
+}
+
+// Row reductions: gck[row] = sum over column chunks; scalar partials per block.
+__global__ void reduce_rows_kernel(int64_t rows, int NCC, const float* rowA, const float* rowB,
+                                   float* gck, float* part) {
+  __shared__ float sh[4];
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * NTH + threadIdx.x;
+  float v[5] = {0.f, 0.f, 0.f, 0.f, 0.f};  // scale, short, pad, induct, cocktail
+  if (row < rows) {
+    float k4[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int cc = 0; cc < NCC; ++cc) {
+      const float* p = rowB + (static_cast<size_t>(row) * NCC + cc) * 6;
+      v[0] += p[0];
+      v[4] += p[1];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) k4[k] += p[2 + k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) gck[static_cast<size_t>(row) * 4 + k] = k4[k];
+    v[1] = rowA[row * 3];
+    v[2] = rowA[row * 3 + 1];
+    v[3] = rowA[row * 3 + 2];
+  }
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    const float s = block_sum(v[k], sh);
+    if (threadIdx.x == 0) part[static_cast<size_t>(blockIdx.x) * 5 + k] = s;
+  }
+}
+
+__global__ void reduce_final_kernel(int nblocks, const float* part, float* out5) {
+  const int k = threadIdx.x;
+  if (k >= 5) return;
+  float s = 0.f;
+  for (int i = 0; i < nblocks; ++i) s += part[static_cast<size_t>(i) * 5 + k];
+  out5[k] = s;
+}
+
+// Workspace planning.
+struct Plan {
+  size_t off_S, off_rs, off_ro, off_rb, off_stats, off_PV, off_PVn, end_fwd;
+  size_t off_dPV, off_dPVn, off_Gs, off_rowA, off_rowB, off_colp, off_part, end_bwd;
+};
+
+static size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+static Plan plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
+  (void)H;
+  Plan p{};
+  const size_t e = dtype == kBF16 ? 2 : 4;
+  const size_t QT = (T + TILE - 1) / TILE, BT = (N + TILE - 1) / TILE;
+  const size_t TN = static_cast<size_t>(B) * T * N;
+  size_t o = 0;
+  p.off_S = o; o = align_up(o + TN * 4);
+  p.off_rs = o; o = align_up(o + B * QT * 3 * 4);
+  p.off_ro = o; o = align_up(o + B * QT * 3 * 4);
+  p.off_rb = o; o = align_up(o + B * BT * 3 * 4);
+  p.off_stats = o; o = align_up(o + static_cast<size_t>(B) * T * 6 * 4);
+  p.off_PV = o; o = align_up(o + TN * e);
+  p.off_PVn = o; o = align_up(o + TN * e);
+  p.end_fwd = o;
+  const size_t NCC = (N + CC - 1) / CC, RTILES = (T + RT - 1) / RT;
+  p.off_dPV = o; o = align_up(o + TN * 4);
+  p.off_dPVn = o; o = align_up(o + TN * 4);
+  p.off_Gs = o; o = align_up(o + TN * e);
+  p.off_rowA = o; o = align_up(o + static_cast<size_t>(B) * T * 3 * 4);
+  p.off_rowB = o; o = align_up(o + static_cast<size_t>(B) * T * NCC * 6 * 4);
+  p.off_colp = o; o = align_up(o + static_cast<size_t>(B) * RTILES * N * 5 * 4);
+  p.off_part = o; o = align_up(o + ((static_cast<size_t>(B) * T + NTH - 1) / NTH) * 5 * 4);
+  p.end_bwd = o;
+  return p;
+}
+
+template <typename E>
+static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, const E* K,
+                        const E* V, const E* Vn, const float* ck, const float* cb, const float* kb,
+                        const float* adm, const float* scale, const int64_t* idx,
+                        const uint8_t* valid, int mode, Gains g, E* out, uint8_t* ws,
+                        const Plan& p, bool write_p, hipStream_t stream) {
+  const int QT = static_cast<int>((T + TILE - 1) / TILE), BT = static_cast<int>((N + TILE - 1) / TILE);
+  float* S = reinterpret_cast<float*>(ws + p.off_S);
+  int32_t* rs = reinterpret_cast<int32_t*>(ws + p.off_rs);
+  int32_t* ro = reinterpret_cast<int32_t*>(ws + p.off_ro);
+  int32_t* rb = reinterpret_cast<int32_t*>(ws + p.off_rb);
+  float* stats = reinterpret_cast<float*>(ws + p.off_stats);
+  E* PV = reinterpret_cast<E*>(ws + p.off_PV);
+  E* PVn = reinterpret_cast<E*>(ws + p.off_PVn);
+  hipLaunchKernelGGL(ranges_kernel, dim3((QT + BT + 63) / 64, (unsigned)B), dim3(64), 0, stream,
+                     (int)T, (int)N, (int)H, mode, idx, valid, rs, ro, rb);
+  DABSN_HIP_CHECK(hipGetLastError());
+  {
+    gemm::Args<E, float> a{};
+    a.M = (int)T; a.N = (int)N; a.K = (int)H;
+    a.A = q; a.lda = H; a.sA = T * H;
+    a.B = K; a.ldb = H; a.sB = N * H;
+    a.C = S; a.ldc = N; a.sC = T * N;
+    a.alpha = 1.0f; a.beta = 0.0f;
+    a.ranges = rs; a.mtiles = QT;
+    DABSN_HIP_CHECK((gemm::launch<E, float, false, true>(a, (int)B, stream)));
+  }
+  RowCtx c{(int)T, (int)N, mode, S, kb, adm, cb, ck, idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
+  hipLaunchKernelGGL(softmax_fwd_kernel<E>, dim3((unsigned)(B * T)), dim3(NTH), 0, stream, c, g,
+                     scale, rs, stats, write_p ? PV : static_cast<E*>(nullptr),
+                     write_p ? PVn : static_cast<E*>(nullptr));
+  DABSN_HIP_CHECK(hipGetLastError());
+  if (!write_p) return DABSN_OK;
+  {
+    gemm::Args<E, E> a{};
+    a.M = (int)T; a.N = (int)H; a.K = (int)N;
+    a.A = PV; a.lda = N; a.sA = T * N;
+    a.B = V; a.ldb = H; a.sB = N * H;
+    a.A2 = PVn; a.B2 = Vn;
+    a.C = out; a.ldc = H; a.sC = T * H;
+    a.alpha = 1.0f; a.beta = 0.0f;
+    a.ranges = ro; a.mtiles = QT;
+    DABSN_HIP_CHECK((gemm::launch<E, E, false, false>(a, (int)B, stream)));
+  }
+  return DABSN_OK;
+}
+
+template <typename E>
+static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* gout, const E* q,
+                         const E* K, const E* V, const E* Vn, const float* ck, const float* cb,
+                         const float* kb, const float* adm, const float* scale, const int64_t* idx,
+                         const uint8_t* valid, int mode, Gains g, E* gq, E* gK, E* gV, E* gVn,
+                         float* gck, float* gcb, float* gkb, float* gadm, float* gscal5,
+                         uint8_t* ws, const Plan& p, hipStream_t stream) {
+  int rc = forward_impl<E>(B, T, N, H, q, K, V, Vn, ck, cb, kb, adm, scale, idx, valid, mode, g,
+                           nullptr, ws, p, false, stream);
+  if (rc != DABSN_OK) return rc;
+  const int QT = static_cast<int>((T + TILE - 1) / TILE), BT = static_cast<int>((N + TILE - 1) / TILE);
+  const float* S = reinterpret_cast<const float*>(ws + p.off_S);
+  const int32_t* rs = reinterpret_cast<const int32_t*>(ws + p.off_rs);
+  const int32_t* ro = reinterpret_cast<const int32_t*>(ws + p.off_ro);
+  const int32_t* rb = reinterpret_cast<const int32_t*>(ws + p.off_rb);
+  const float* stats = reinterpret_cast<const float*>(ws + p.off_stats);
+  E* PV = reinterpret_cast<E*>(ws + p.off_PV);
+  E* PVn = reinterpret_cast<E*>(ws + p.off_PVn);
+  float* dPV = reinterpret_cast<float*>(ws + p.off_dPV);
+  float* dPVn = reinterpret_cast<float*>(ws + p.off_dPVn);
+  E* Gs = reinterpret_cast<E*>(ws + p.off_Gs);
+  float* rowA = reinterpret_cast<float*>(ws + p.off_rowA);
+  float* rowB = reinterpret_cast<float*>(ws + p.off_rowB);
+  float* colp = reinterpret_cast<float*>(ws + p.off_colp);
+  float* part = reinterpret_cast<float*>(ws + p.off_part);
+  for (int w = 0; w < 2; ++w) {
+    gemm::Args<E, float> a{};
+    a.M = (int)T; a.N = (int)N; a.K = (int)H;
+    a.A = gout; a.lda = H; a.sA = T * H;
+    a.B = w == 0 ? V : Vn; a.ldb = H; a.sB = N * H;
+    a.C = w == 0 ? dPV : dPVn; a.ldc = N; a.sC = T * N;
+    a.alpha = 1.0f; a.beta = 0.0f;
+    a.ranges = rs; a.mtiles = QT;
+    DABSN_HIP_CHECK((gemm::launch<E, float, false, true>(a, (int)B, stream)));
+  }
+  RowCtx c{(int)T, (int)N, mode, S, kb, adm, cb, ck, idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
+  hipLaunchKernelGGL(grad_rows_kernel, dim3((unsigned)(B * T)), dim3(NTH), 0, stream, c, g, scale,
+                     rs, stats, dPV, dPVn, rowA);
+  DABSN_HIP_CHECK(hipGetLastError());
+  const int NCC = static_cast<int>((N + CC - 1) / CC), RTILES = static_cast<int>((T + RT - 1) / RT);
+  if (N > 0) {
+    hipLaunchKernelGGL(grad_tile_kernel<E>, dim3(NCC, RTILES, (unsigned)B), dim3(NTH), 0, stream, c,
+                       g, scale, rs, stats, rowA, dPV, dPVn, Gs, PV, PVn, rowB, colp);
+    DABSN_HIP_CHECK(hipGetLastError());
+  }
+  {
+    gemm::Args<E, E> a{};  // gQ = Gs K
+    a.M = (int)T; a.N = (int)H; a.K = (int)N;
+    a.A = Gs; a.lda = N; a.sA = T * N;
+    a.B = K; a.ldb = H; a.sB = N * H;
+    a.C = gq; a.ldc = H; a.sC = T * H;
+    a.alpha = 1.0f;
+    a.ranges = ro; a.mtiles = QT;
+    DABSN_HIP_CHECK((gemm::launch<E, E, false, false>(a, (int)B, stream)));
+  }
+  const E* lhs[3] = {Gs, PV, PVn};
+  const E* rhs[3] = {q, gout, gout};
+  E* dst[3] = {gK, gV, gVn};
+  for (int w = 0; w < 3; ++w) {
+    gemm::Args<E, E> a{};  // gK = Gs^T Q, gV = P_V^T gO, gVn = P_Vn^T gO
+    a.M = (int)N; a.N = (int)H; a.K = (int)T;
+    a.A = lhs[w]; a.lda = N; a.sA = T * N;
+    a.B = rhs[w]; a.ldb = H; a.sB = T * H;
+    a.C = dst[w]; a.ldc = H; a.sC = N * H;
+    a.alpha = 1.0f;
+    a.ranges = rb; a.mtiles = BT;
+    DABSN_HIP_CHECK((gemm::launch<E, E, true, false>(a, (int)B, stream)));
+  }
+  if (N > 0) {
+    hipLaunchKernelGGL(reduce_cols_kernel, dim3((unsigned)((N + NTH - 1) / NTH), (unsigned)B),
+                       dim3(NTH), 0, stream, (int)T, (int)N, colp, gkb, gadm, gcb);
+    DABSN_HIP_CHECK(hipGetLastError());
+  }
+  const int64_t rows = B * T;
+  const int nblk = static_cast<int>((rows + NTH - 1) / NTH);
+  hipLaunchKernelGGL(reduce_rows_kernel, dim3(nblk), dim3(NTH), 0, stream, rows, NCC, rowA, rowB,
+                     gck, part);
+  DABSN_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(reduce_final_kernel, dim3(1), dim3(64), 0, stream, nblk, part, gscal5);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+}  // namespace read3
+}  // namespace dabsn
+
+using namespace dabsn;
+using namespace dabsn::read3;
+
+static int read3_checks(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, int mode) {
+  DABSN_REQUIRE(dtype == kF32 || dtype == kBF16, "read3: bad dtype %d", dtype);
+  DABSN_REQUIRE(mode == 0 || mode == 1, "read3: mode must be 0 (seq) or 1 (field)");
+  DABSN_REQUIRE(B > 0 && T > 0 && N >= 0 && H > 0, "read3: bad shape");
+  DABSN_REQUIRE(T < (1 << 30) && N < (1 << 30) && H < (1 << 30) && B < 65536,
+                "read3: dimension too large");
+  DABSN_REQUIRE(B * T * N < (1ll << 40), "read3: score matrix too large");
+  return DABSN_OK;
+}
+
+extern "C" {
+
+size_t dabsn_hip_read3_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
+                                       int backward) {
+  const Plan p = plan(dtype, B, T, N, H);
+  return backward ? p.end_bwd : p.end_fwd;
+}
+
+int dabsn_hip_read3_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* q,
+                        const void* K, const void* V, const void* Vn, const float* cocktail,
+                        const float* bank_cocktail, const float* key_bias, const float* admission,
+                        const float* scale, const int64_t* idx, const uint8_t* valid, int mode,
+                        const float* const* gains, void* out, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  const int rc = read3_checks(dtype, B, T, N, H, mode);
+  if (rc != DABSN_OK) return rc;
+  DABSN_REQUIRE(q && out && cocktail && scale && gains, "read3: null pointer");
+  for (int i = 0; i < 4; ++i) DABSN_REQUIRE(gains[i], "read3: null gain %d", i);
+  if (N == 0) return dabsn_hip_zero(out, static_cast<size_t>(B * T * H) * (dtype == kBF16 ? 2 : 4), stream);
+  DABSN_REQUIRE(K && V && Vn && bank_cocktail && key_bias && admission && idx && valid && workspace,
+                "read3: null bank pointer");
+  const Plan p = plan(dtype, B, T, N, H);
+  DABSN_REQUIRE(workspace_bytes >= p.end_fwd, "read3: workspace %zu < %zu", workspace_bytes,
+                p.end_fwd);
+  Gains g{{gains[0], gains[1], gains[2], gains[3]}};
+  if (dtype == kBF16)
+    return forward_impl<bf16>(B, T, N, H, (const bf16*)q, (const bf16*)K, (const bf16*)V,
+                              (const bf16*)Vn, cocktail, bank_cocktail, key_bias, admission, scale,
+                              idx, valid, mode, g, (bf16*)out, (uint8_t*)workspace, p, true, stream);
+  return forward_impl<float>(B, T, N, H, (const float*)q, (const float*)K, (const float*)V,
+                             (const float*)Vn, cocktail, bank_cocktail, key_bias, admission, scale,
+                             idx, valid, mode, g, (float*)out, (uint8_t*)workspace, p, true, stream);
+}
+
+int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* gout,
+                        const void* q, const void* K, const void* V, const void* Vn,
+                        const float* cocktail, const float* bank_cocktail, const float* key_bias,
+                        const float* admission, const float* scale, const int64_t* idx,
+                        const uint8_t* valid, int mode, const float* const* gains, void* gq,
+                        void* gK, void* gV, void* gVn, float* gcocktail, float* gbank_cocktail,
+                        float* gkey_bias, float* gadmission, float* gscalars5, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  const int rc = read3_checks(dtype, B, T, N, H, mode);
+  if (rc != DABSN_OK) return rc;
+  DABSN_REQUIRE(gout && q && gq && cocktail && gcocktail && scale && gains && gscalars5,
+                "read3 backward: null pointer");
+  for (int i = 0; i < 4; ++i) DABSN_REQUIRE(gains[i], "read3 backward: null gain %d", i);
+  const size_t e = dtype == kBF16 ? 2 : 4;
+  if (N == 0) {
+    int z = dabsn_hip_zero(gq, static_cast<size_t>(B * T * H) * e, stream);
+    if (z == DABSN_OK) z = dabsn_hip_zero(gcocktail, static_cast<size_t>(B * T * 4) * 4, stream);
+    if (z == DABSN_OK) z = dabsn_hip_zero(gscalars5, 5 * 4, stream);
+    return z;
+  }
+  DABSN_REQUIRE(K && V && Vn && bank_cocktail && key_bias && admission && idx && valid && gK && gV &&
+                    gVn && gbank_cocktail && gkey_bias && gadmission && workspace,
+                "read3 backward: null bank pointer");
+  const Plan p = plan(dtype, B, T, N, H);
+  DABSN_REQUIRE(workspace_bytes >= p.end_bwd, "read3 backward: workspace %zu < %zu",
+                workspace_bytes, p.end_bwd);
+  Gains g{{gains[0], gains[1], gains[2], gains[3]}};
+  if (dtype == kBF16)
+    return backward_impl<bf16>(B, T, N, H, (const bf16*)gout, (const bf16*)q, (const bf16*)K,
+                               (const bf16*)V, (const bf16*)Vn, cocktail, bank_cocktail, key_bias,
+                               admission, scale, idx, valid, mode, g, (bf16*)gq, (bf16*)gK,
+                               (bf16*)gV, (bf16*)gVn, gcocktail, gbank_cocktail, gkey_bias,
+                               gadmission, gscalars5, (uint8_t*)workspace, p, stream);
+  return backward_impl<float>(B, T, N, H, (const float*)gout, (const float*)q, (const float*)K,
+                              (const float*)V, (const float*)Vn, cocktail, bank_cocktail, key_bias,
+                              admission, scale, idx, valid, mode, g, (float*)gq, (float*)gK,
+                              (float*)gV, (float*)gVn, gcocktail, gbank_cocktail, gkey_bias,
+                              gadmission, gscalars5, (uint8_t*)workspace, p, stream);
+}
+
+}  // extern "C"

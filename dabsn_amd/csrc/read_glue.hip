@@ -1,0 +1,377 @@
+// Read glue: per-position tape statistics, query normalisation, admitted-slot
+// selection and the bank gather (with their backward passes).
+//
+// Reference: src/dabsn/read.py:58-72 (admission), 154-183 (query, key bias, cocktail),
+// 185-239 (cummax floor, member, stable partition, bank width), 241-256 and 298-303
+// (bank gather, next-write gather).
+#include "../../include/dabsn_hip.h"
+#include "capi.hpp"
+#include "common.hpp"
+
+namespace dabsn {
+namespace glue {
+
+constexpr float kEps = 1e-12f;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// One wave per (b, t) row.
+template <typename E>
+__global__ void __launch_bounds__(256) stats_kernel(int64_t rows, int H, const E* nov, const E* pl,
+                                                    const E* en, const E* sat, const E* ay,
+                                                    const E* wr, float* stats) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const size_t base = static_cast<size_t>(row) * H;
+  float se = 0.f, sc = 0.f, sn = 0.f, sp = 0.f, sa = 0.f, sw = 0.f;
+  for (int h = lane; h < H; h += 64) {
+    const size_t o = base + h;
+    se += ld(en, o);
+    sc += ld(sat, o);
+    sn += ld(nov, o);
+    sp += ld(pl, o);
+    const float a = ld(ay, o), w = ld(wr, o);
+    sa += a * a;
+    sw += w * w;
+  }
+  se = wave_sum(se);
+  sc = wave_sum(sc);
+  sn = wave_sum(sn);
+  sp = wave_sum(sp);
+  sa = wave_sum(sa);
+  sw = wave_sum(sw);
+  if (lane == 0) {
+    const float inv = 1.0f / static_cast<float>(H);
+    float* o = stats + static_cast<size_t>(row) * 6;
+    o[0] = se * inv;
+    o[1] = sc * inv;
+    o[2] = sn * inv;
+    o[3] = sp * inv;
+    o[4] = sqrtf(sa);
+    o[5] = sqrtf(sw);
+  }
+}
+
+// g_tape[b,t,h] += g_mean[b,t] / H for the four averaged tapes.
+template <typename E>
+__global__ void stats_bwd_kernel(int64_t rows, int H, const float* gstats, E* gen, E* gsat, E* gnov,
+                                 E* gpl) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * H) return;
+  const int64_t row = i / H;
+  const float inv = 1.0f / static_cast<float>(H);
+  const float* g = gstats + static_cast<size_t>(row) * 6;
+  if (gen) st(gen, i, ld(gen, i) + g[0] * inv);
+  if (gsat) st(gsat, i, ld(gsat, i) + g[1] * inv);
+  if (gnov) st(gnov, i, ld(gnov, i) + g[2] * inv);
+  if (gpl) st(gpl, i, ld(gpl, i) + g[3] * inv);
+}
+
+template <typename E>
+__global__ void normalize_kernel(int64_t rows, int H, const E* x, const float* norms, E* q) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * H) return;
+  const float n = fmaxf(norms[i / H], kEps);
+  st(q, i, ld(x, i) / n);
+}
+
+// One wave per row: gx += (gq - q (q.gq)) / |x| if |x| > eps, else gq / eps.
+template <typename E>
+__global__ void __launch_bounds__(256) normalize_bwd_kernel(int64_t rows, int H, const E* q,
+                                                            const float* norms, const E* gq,
+                                                            E* gx) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const size_t base = static_cast<size_t>(row) * H;
+  const float nrm = norms[row];
+  float dot = 0.0f;
+  if (nrm > kEps) {
+    for (int h = lane; h < H; h += 64) dot += ld(q, base + h) * ld(gq, base + h);
+    dot = wave_sum(dot);
+  }
+  const float n = fmaxf(nrm, kEps);
+  for (int h = lane; h < H; h += 64) {
+    const size_t o = base + h;
+    const float g = nrm > kEps ? (ld(gq, o) - ld(q, o) * dot) / n : ld(gq, o) / n;
+    st(gx, o, ld(gx, o) + g);
+  }
+}
+
+// Admitted-slot selection, one workgroup per batch row. Each thread owns a contiguous
+// chunk of time steps; block scans combine the per-chunk running max and member counts.
+constexpr int SEL_T = 256;
+
+__global__ void __launch_bounds__(SEL_T) select_kernel(int T, const float* adm, const float* window,
+                                                       int64_t* order, int64_t* counts,
+                                                       int32_t* rank) {
+  __shared__ float smax[SEL_T];
+  __shared__ int scnt[SEL_T];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const float* a = adm + static_cast<size_t>(b) * T;
+  const int chunk = (T + SEL_T - 1) / SEL_T;
+  const int t0 = min(T, tid * chunk), t1 = min(T, t0 + chunk);
+  const float win = window[0];
+  float m = -INFINITY;
+  for (int t = t0; t < t1; ++t) m = fmaxf(m, a[t]);
+  smax[tid] = m;
+  __syncthreads();
+  // Inclusive prefix max over chunk maxima (Hillis-Steele).
+  for (int off = 1; off < SEL_T; off <<= 1) {
+    const float v = tid >= off ? smax[tid - off] : -INFINITY;
+    __syncthreads();
+    smax[tid] = fmaxf(smax[tid], v);
+    __syncthreads();
+  }
+  const float before = tid > 0 ? smax[tid - 1] : -INFINITY;
+  int cnt = 0;
+  float run = before;
+  for (int t = t0; t < t1; ++t) {
+    run = (t == 0 || a[t] > run) ? a[t] : run;
+    cnt += (a[t] >= run - win) ? 1 : 0;
+  }
+  scnt[tid] = cnt;
+  __syncthreads();
+  for (int off = 1; off < SEL_T; off <<= 1) {
+    const int v = tid >= off ? scnt[tid - off] : 0;
+    __syncthreads();
+    scnt[tid] += v;
+    __syncthreads();
+  }
+  const int total = scnt[SEL_T - 1];
+  int mpos = tid > 0 ? scnt[tid - 1] : 0;  // members before this chunk
+  run = before;
+  int64_t* o = order + static_cast<size_t>(b) * T;
+  int32_t* rk = rank + static_cast<size_t>(b) * T;
+  for (int t = t0; t < t1; ++t) {
+    run = (t == 0 || a[t] > run) ? a[t] : run;
+    int r;
+    if (a[t] >= run - win) {
+      r = mpos++;
+    } else {
+      r = total + (t - mpos);
+    }
+    o[r] = t;
+    rk[t] = r;
+  }
+  if (tid == 0) counts[b] = total;
+}
+
+// Gather K (normalised), V and Vn rows of the bank.
+template <typename E>
+__global__ void gather_kernel(int T, int N, int H, int hblocks, const E* w, const float* norm_w,
+                              const int64_t* idx, const int64_t* nidx, E* K, E* V, E* Vn) {
+  const int64_t row = blockIdx.x / hblocks;  // b * N + j
+  const int h = (blockIdx.x % hblocks) * blockDim.x + threadIdx.x;
+  if (h >= H) return;
+  const int64_t b = row / N;
+  int64_t t = idx[row];
+  int64_t tn = nidx[row];
+  t = t < 0 ? 0 : (t >= T ? T - 1 : t);
+  tn = tn < 0 ? 0 : (tn >= T ? T - 1 : tn);
+  const float v = ld(w, (static_cast<size_t>(b) * T + t) * H + h);
+  const float n = fmaxf(norm_w[static_cast<size_t>(b) * T + t], kEps);
+  const size_t o = static_cast<size_t>(row) * H + h;
+  st(K, o, v / n);
+  st(V, o, v);
+  st(Vn, o, ld(w, (static_cast<size_t>(b) * T + tn) * H + h));
+}
+
+// One workgroup per (b, t) position of the write tape.
+template <typename E>
+__global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int N, int H, const float* norm_w,
+                                                         const int32_t* rank, const E* K,
+                                                         const E* gK, const E* gV, const E* gVn,
+                                                         E* gw) {
+  __shared__ float part[4];
+  const int64_t bt = blockIdx.x;
+  const int64_t b = bt / T;
+  const int t = static_cast<int>(bt % T);
+  const int32_t* rk = rank + static_cast<size_t>(b) * T;
+  const int r0 = rk[t];
+  const int r1 = t >= 1 ? rk[t - 1] : N;
+  const int r2 = t == T - 1 ? rk[T - 1] : N;
+  const bool in0 = r0 < N, in1 = r1 < N, in2 = r2 < N;
+  if (!in0 && !in1 && !in2) return;
+  const float nrm = norm_w[bt];
+  const float n = fmaxf(nrm, kEps);
+  float dot = 0.0f;
+  if (in0 && nrm > kEps) {
+    const size_t kb = (static_cast<size_t>(b) * N + r0) * H;
+    float s = 0.0f;
+    for (int h = threadIdx.x; h < H; h += blockDim.x) s += ld(K, kb + h) * ld(gK, kb + h);
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    dot = part[0] + part[1] + part[2] + part[3];
+  }
+  for (int h = threadIdx.x; h < H; h += blockDim.x) {
+    const size_t o = static_cast<size_t>(bt) * H + h;
+    float acc = ld(gw, o);
+    if (in0) {
+      const size_t kb = (static_cast<size_t>(b) * N + r0) * H + h;
+      const float gk = ld(gK, kb);
+      acc += ld(gV, kb) + (nrm > kEps ? (gk - ld(K, kb) * dot) / n : gk / n);
+    }
+    if (in1) acc += ld(gVn, (static_cast<size_t>(b) * N + r1) * H + h);
+    if (in2) acc += ld(gVn, (static_cast<size_t>(b) * N + r2) * H + h);
+    st(gw, o, acc);
+  }
+}
+
+}  // namespace glue
+}  // namespace dabsn
+
+using namespace dabsn;
+using namespace dabsn::glue;
+
+static inline unsigned blocks_for(int64_t n, int per) {
+  return static_cast<unsigned>((n + per - 1) / per);
+}
+
+extern "C" {
+
+int dabsn_hip_tape_stats(int dtype, int64_t B, int64_t T, int64_t H, const void* nov,
+                         const void* plast, const void* energy, const void* sat, const void* expr,
+                         const void* write, float* stats, hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && T >= 0 && H > 0 && H < (1 << 30), "tape_stats: bad shape");
+  const int64_t rows = B * T;
+  if (rows == 0) return DABSN_OK;
+  DABSN_REQUIRE(nov && plast && energy && sat && expr && write && stats, "tape_stats: null pointer");
+  const dim3 grid(blocks_for(rows, 4)), block(256);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(stats_kernel<bf16>, grid, block, 0, stream, rows, (int)H, (const bf16*)nov,
+                       (const bf16*)plast, (const bf16*)energy, (const bf16*)sat,
+                       (const bf16*)expr, (const bf16*)write, stats);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(stats_kernel<float>, grid, block, 0, stream, rows, (int)H,
+                       (const float*)nov, (const float*)plast, (const float*)energy,
+                       (const float*)sat, (const float*)expr, (const float*)write, stats);
+  else
+    DABSN_REQUIRE(false, "tape_stats: bad dtype %d", dtype);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* expr,
+                             const void* write, const float* stats, const float* gstats,
+                             void* gnov, void* gplast, void* genergy, void* gsat, void* gexpr,
+                             void* gwrite, hipStream_t stream) {
+  (void)expr;
+  (void)write;
+  (void)stats;
+  DABSN_REQUIRE(gexpr == nullptr && gwrite == nullptr,
+                "tape_stats backward: norm gradients are handled by the normalisation ops");
+  const int64_t rows = B * T;
+  if (rows == 0) return DABSN_OK;
+  DABSN_REQUIRE(gstats, "tape_stats backward: null gstats");
+  const dim3 grid(blocks_for(rows * H, 256)), block(256);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(stats_bwd_kernel<bf16>, grid, block, 0, stream, rows, (int)H, gstats,
+                       (bf16*)genergy, (bf16*)gsat, (bf16*)gnov, (bf16*)gplast);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(stats_bwd_kernel<float>, grid, block, 0, stream, rows, (int)H, gstats,
+                       (float*)genergy, (float*)gsat, (float*)gnov, (float*)gplast);
+  else
+    DABSN_REQUIRE(false, "tape_stats backward: bad dtype %d", dtype);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_normalize_rows(int dtype, int64_t rows, int64_t H, const void* x, const float* norms,
+                             void* q, hipStream_t stream) {
+  if (rows == 0) return DABSN_OK;
+  DABSN_REQUIRE(x && norms && q && H > 0, "normalize_rows: bad arguments");
+  const dim3 grid(blocks_for(rows * H, 256)), block(256);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(normalize_kernel<bf16>, grid, block, 0, stream, rows, (int)H,
+                       (const bf16*)x, norms, (bf16*)q);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(normalize_kernel<float>, grid, block, 0, stream, rows, (int)H,
+                       (const float*)x, norms, (float*)q);
+  else
+    DABSN_REQUIRE(false, "normalize_rows: bad dtype %d", dtype);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_normalize_rows_bwd(int dtype, int64_t rows, int64_t H, const void* q,
+                                 const float* norms, const void* gq, void* gx, hipStream_t stream) {
+  if (rows == 0) return DABSN_OK;
+  DABSN_REQUIRE(q && norms && gq && gx && H > 0, "normalize_rows backward: bad arguments");
+  const dim3 grid(blocks_for(rows, 4)), block(256);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(normalize_bwd_kernel<bf16>, grid, block, 0, stream, rows, (int)H,
+                       (const bf16*)q, norms, (const bf16*)gq, (bf16*)gx);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(normalize_bwd_kernel<float>, grid, block, 0, stream, rows, (int)H,
+                       (const float*)q, norms, (const float*)gq, (float*)gx);
+  else
+    DABSN_REQUIRE(false, "normalize_rows backward: bad dtype %d", dtype);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_bank_select(int64_t B, int64_t T, const float* adm, const float* window,
+                          int64_t* order, int64_t* counts, int32_t* rank, hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && T > 0 && T < (1ll << 30) && B < (1ll << 31), "bank_select: bad shape");
+  DABSN_REQUIRE(adm && window && order && counts && rank, "bank_select: null pointer");
+  hipLaunchKernelGGL(select_kernel, dim3((unsigned)B), dim3(SEL_T), 0, stream, (int)T, adm, window,
+                     order, counts, rank);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_bank_gather(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* w,
+                          const float* norm_w, const int64_t* idx, const int64_t* next_idx,
+                          void* K, void* V, void* Vn, hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && T > 0 && N >= 0 && H > 0, "bank_gather: bad shape");
+  if (N == 0) return DABSN_OK;
+  DABSN_REQUIRE(w && norm_w && idx && next_idx && K && V && Vn, "bank_gather: null pointer");
+  const int hblocks = static_cast<int>(blocks_for(H, 256));
+  DABSN_REQUIRE(B * N * hblocks <= 2147483647ll, "bank_gather: too many bank rows");
+  const dim3 grid(static_cast<unsigned>(B * N * hblocks)), block(256);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(gather_kernel<bf16>, grid, block, 0, stream, (int)T, (int)N, (int)H,
+                       hblocks, (const bf16*)w, norm_w, idx, next_idx, (bf16*)K, (bf16*)V,
+                       (bf16*)Vn);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(gather_kernel<float>, grid, block, 0, stream, (int)T, (int)N, (int)H,
+                       hblocks, (const float*)w, norm_w, idx, next_idx, (float*)K, (float*)V,
+                       (float*)Vn);
+  else
+    DABSN_REQUIRE(false, "bank_gather: bad dtype %d", dtype);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
+                              const void* w, const float* norm_w, const int32_t* rank,
+                              const void* K, const void* gK, const void* gV, const void* gVn,
+                              void* gw, hipStream_t stream) {
+  (void)w;
+  DABSN_REQUIRE(B > 0 && T > 0 && N >= 0 && H > 0, "bank_gather backward: bad shape");
+  if (N == 0) return DABSN_OK;
+  DABSN_REQUIRE(norm_w && rank && K && gK && gV && gVn && gw, "bank_gather backward: null pointer");
+  DABSN_REQUIRE(B * T <= 2147483647ll, "bank_gather backward: too many positions");
+  const dim3 grid((unsigned)(B * T)), block(256);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(gather_bwd_kernel<bf16>, grid, block, 0, stream, (int)T, (int)N, (int)H,
+                       norm_w, rank, (const bf16*)K, (const bf16*)gK, (const bf16*)gV,
+                       (const bf16*)gVn, (bf16*)gw);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(gather_bwd_kernel<float>, grid, block, 0, stream, (int)T, (int)N, (int)H,
+                       norm_w, rank, (const float*)K, (const float*)gK, (const float*)gV,
+                       (const float*)gVn, (float*)gw);
+  else
+    DABSN_REQUIRE(false, "bank_gather backward: bad dtype %d", dtype);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+}  // extern "C"

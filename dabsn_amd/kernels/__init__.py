@@ -1,0 +1,132 @@
+"""Backend selection, status and primitive map for the ROCm (gfx950) backend.
+
+Mirrors the reference backend API (src/dabsn/kernels/__init__.py:38-163):
+``enable(backend, required=...)`` is process-wide and refuses to switch backends in
+one process; ``status()`` reports what is actually loaded; ``PRIMITIVES`` maps each
+hot-path primitive to its implementation. This package provides one backend, the
+hand-written HIP kernels (``"rocm"``; ``"auto"`` and ``"cuda"`` select it too, since
+PyTorch-ROCm names the device ``cuda``). There is no CPU product path: CPU tensors
+raise in every operator.
+"""
+
+from __future__ import annotations
+
+from dataclasses import asdict, dataclass
+
+import torch
+
+from .. import _lib
+from . import ops
+from .ops import (
+    admitted_three_way_read_compact_flash,
+    bank_gather,
+    bank_select,
+    check_errors,
+    core_scan_batched,
+    linear_recurrence,
+    long_scan_fused,
+    normalize_rows,
+    read_tape_stats,
+)
+
+_ACTIVE_BACKEND = "none"
+
+
+@dataclass(frozen=True)
+class Primitive:
+    name: str
+    reference: str
+    rocm: str
+    backward: str
+    geometries: tuple[str, ...]
+    validation: str
+
+
+PRIMITIVES = (
+    Primitive("core_scan", "DABSNCore.forward / DABSNCore.forward_from_state",
+              "persistent cooperative HIP scan, MFMA recurrent product, sc1 step exchange",
+              "persistent cooperative HIP reverse scan + hipBLASLt weight-gradient GEMM",
+              ("seq",), "oracle (C restatement of cpu_runtime.cpp) forward/backward parity"),
+    Primitive("admitted_three_way_read", "DABSNRead._three_way_read",
+              "MFMA score GEMM + masked softmax rows + MFMA value GEMM",
+              "MFMA GEMMs for dP, dQ, dK, dV + score-gradient rows",
+              ("seq", "field"), "oracle (cpu_runtime.cpp:321-662 restatement) parity"),
+    Primitive("recurrent_long_read", "DABSNRead._long_scan_from_state",
+              "fused three-recurrence HIP scan with fp32 checkpoints",
+              "segment-replay HIP reverse scan", ("seq",),
+              "oracle long-scan forward/backward parity"),
+    Primitive("linear_recurrence", "dabsn::linear_recurrence", "HIP channel scan",
+              "HIP analytic reverse", ("seq",), "oracle linrec parity"),
+    Primitive("admitted_selection", "DABSNRead._unified_forward (read.py:185-239)",
+              "HIP cummax/stable-partition kernel", "none (integer)", ("seq",),
+              "bit-exact against the oracle stable partition"),
+)
+
+
+def primitive_map() -> list[dict[str, object]]:
+    return [asdict(p) for p in PRIMITIVES]
+
+
+def enable(backend: str = "auto", *, required: bool = False) -> dict[str, object]:
+    """Enable the ROCm backend process-wide (see module docstring)."""
+    global _ACTIVE_BACKEND
+    normalized = backend.lower()
+    if normalized in {"auto", "cuda", "hip"}:
+        normalized = "rocm"
+    if normalized != "rocm":
+        raise ValueError("backend must be one of: auto, rocm, cuda, hip")
+    if _ACTIVE_BACKEND not in {"none", normalized}:
+        raise RuntimeError(f"DABSN backend already selected as {_ACTIVE_BACKEND}; "
+                           "select a different backend in a fresh process")
+    ok = _lib.available() and torch.cuda.is_available()
+    if required and not ok:
+        reason = _lib.load_error() or "no ROCm device is visible"
+        raise RuntimeError(f"required ROCm DABSN backend unavailable: {reason}")
+    if ok:
+        from ..core import DABSNCore
+        from ..read import DABSNRead
+
+        DABSNCore._rocm_native_enabled = True
+        DABSNRead._rocm_native_enabled = True
+        _ACTIVE_BACKEND = normalized
+    return status()
+
+
+def status() -> dict[str, object]:
+    lib_ok = _lib.available()
+    arch = None
+    if torch.cuda.is_available():
+        arch = getattr(torch.cuda.get_device_properties(0), "gcnArchName", None)
+    return {
+        "active_backend": _ACTIVE_BACKEND,
+        "torch_version": torch.__version__,
+        "hip_version": getattr(torch.version, "hip", None),
+        "device_available": torch.cuda.is_available(),
+        "device_arch": arch,
+        "rocm": {
+            "library": str(_lib.LIB_PATH),
+            "library_loaded": lib_ok,
+            "load_error": _lib.load_error(),
+            "abi_version": _lib.ABI_VERSION,
+            "operators": list(ops.OPERATORS),
+        },
+        "primitives": primitive_map(),
+    }
+
+
+__all__ = [
+    "PRIMITIVES",
+    "Primitive",
+    "admitted_three_way_read_compact_flash",
+    "bank_gather",
+    "bank_select",
+    "check_errors",
+    "core_scan_batched",
+    "enable",
+    "linear_recurrence",
+    "long_scan_fused",
+    "normalize_rows",
+    "primitive_map",
+    "read_tape_stats",
+    "status",
+]

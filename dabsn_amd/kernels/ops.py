@@ -1,0 +1,763 @@
+"""Registered ``dabsn::`` operators backed by the gfx950 HIP library.
+
+Each operator keeps the reference's schema where the reference has one, so callers
+written against the reference see the same boundary:
+
+  dabsn::core_scan_batched                    batched_runtime.py:1507-1586 (26 in, 11 out)
+  dabsn::_core_scan_batched_backward          new: the reference's core op has no registered
+                                              backward (its autograd is a Python loop,
+                                              batched_runtime.py:1589-1634)
+  dabsn::linear_recurrence / _linrec_backward long.py:392-437
+  dabsn::admitted_three_way_read_compact_flash and its backward op
+                                              compact_flash.py:71-107, 181-224
+plus fused operators for the rest of the read (long-memory scan, tape statistics,
+query normalisation, admitted-slot selection, bank gather).
+
+Only a device ("cuda" = ROCm) kernel is registered: on a CPU tensor these ops raise
+instead of silently falling back.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+
+_DTYPES = {torch.float32: 0, torch.bfloat16: 1}
+
+# Sticky device-side error words of persistent kernels, checked by check_errors().
+_STICKY: dict[int, Tensor] = {}
+
+
+def _code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPES[dt]
+    except KeyError:
+        raise TypeError(f"DABSN HIP kernels support float32 and bfloat16, not {dt}") from None
+
+
+def _stream(t: Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _p(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _sync_mode() -> str:
+    return os.environ.get("DABSN_HIP_ERROR_CHECK", "sync")
+
+
+def _record_error_word(ws: Tensor, what: str) -> None:
+    word = ws[:4].view(torch.int32)
+    if _sync_mode() == "sync":
+        value = int(word.item())
+        if value != 0:
+            raise RuntimeError(
+                f"DABSN HIP {what}: a device-wide step barrier timed out (error word {value});"
+                " the workgroups of the persistent scan were not all co-resident"
+            )
+        return
+    dev = ws.device.index or 0
+    sticky = _STICKY.get(dev)
+    if sticky is None:
+        sticky = torch.zeros(1, dtype=torch.int32, device=ws.device)
+        _STICKY[dev] = sticky
+    torch.bitwise_or(sticky, word, out=sticky)
+
+
+def check_errors() -> None:
+    """Raise if any persistent kernel launched in deferred-check mode reported an error."""
+    for dev, sticky in _STICKY.items():
+        value = int(sticky.item())
+        if value != 0:
+            sticky.zero_()
+            raise RuntimeError(f"DABSN HIP persistent scan on cuda:{dev} reported error word {value}")
+
+
+def _require_cuda(*tensors: Tensor) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("DABSN HIP operators need ROCm device tensors")
+
+
+# ---------------------------------------------------------------------------
+# Core scan
+# ---------------------------------------------------------------------------
+CoreScanOutputs = tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                        Tensor, Tensor]
+
+
+def _core_params(vecs: Sequence[Tensor], scal: Sequence[Tensor]):
+    vec_f = [v.float().contiguous() for v in vecs]
+    scal_f = [s.float().reshape(()).contiguous() for s in scal]
+    params = _lib.CoreParams()
+    for i, v in enumerate(vec_f):
+        params.vec[i] = v.data_ptr()
+    for i, s in enumerate(scal_f):
+        params.scal[i] = s.data_ptr()
+    return params, (vec_f, scal_f)
+
+
+@torch.library.custom_op("dabsn::core_scan_batched", mutates_args=(), device_types="cuda")
+def core_scan_batched(
+    Wx: Tensor, Wgx: Tensor, Ug: Tensor, A: Tensor, beta: Tensor, log_kappa: Tensor,
+    logit_recover: Tensor, k_s: Tensor, k_y: Tensor, k_b: Tensor, k_n: Tensor, k_bias: Tensor,
+    r_s: Tensor, r_y: Tensor, r_b: Tensor, r_n: Tensor, r_bias: Tensor, logit_c_decay: Tensor,
+    k_c: Tensor, r_c: Tensor, logit_alpha: Tensor, log_lambda: Tensor, logit_c_suppress: Tensor,
+    initial_b: Tensor, initial_e: Tensor, initial_c: Tensor,
+) -> CoreScanOutputs:
+    """Forward core scan (reference math core.py:171-221; CPU kernel cpu_runtime.cpp:672-837)."""
+    _require_cuda(Wx)
+    lib = _lib.load()
+    B, T, H = Wx.shape
+    if Wgx.shape != Wx.shape or Ug.shape != (H, H) or A.shape != (H, H):
+        raise ValueError("batched DABSN core received incompatible tensor shapes")
+    dt = Wx.dtype
+    code = _code(dt)
+    Wx_c = Wx.contiguous()
+    Wgx_c = Wgx.to(dt).contiguous()
+    GA = torch.cat((Ug, A), dim=0).to(dt).contiguous()
+    params, keep = _core_params(
+        (beta, log_kappa, logit_recover, k_s, k_y, k_b, k_n, k_bias, r_s, r_y, r_b, r_n, r_bias,
+         logit_c_decay, k_c, r_c),
+        (logit_alpha, log_lambda, logit_c_suppress),
+    )
+    b0, e0, c0 = (x.float().contiguous() for x in (initial_b, initial_e, initial_c))
+    for x in (b0, e0, c0):
+        if x.shape != (B, H):
+            raise ValueError(f"initial state must have shape {(B, H)}, got {tuple(x.shape)}")
+    U = torch.empty((B, T, 2 * H), device=Wx.device, dtype=dt)
+    tapes = [torch.empty((B, T, H), device=Wx.device, dtype=dt) for _ in range(7)]
+    if T == 0:
+        return (U, *tapes, *(s.clone() for s in (initial_b, initial_e, initial_c)))
+    finals = [torch.empty((B, H), device=Wx.device, dtype=torch.float32) for _ in range(3)]
+    nbytes = lib.dabsn_hip_core_scan_workspace_bytes(code, B, H, 0)
+    if nbytes == 0:
+        raise RuntimeError(f"DABSN HIP core scan does not support H={H} for {dt}")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=Wx.device)
+    rc = lib.dabsn_hip_core_scan_fwd(
+        code, B, T, H, _p(Wx_c), _p(Wgx_c), _p(GA), ctypes.byref(params),
+        _p(b0), _p(e0), _p(c0), _p(U), *[_p(t) for t in tapes], *[_p(f) for f in finals],
+        _p(ws), nbytes, _stream(Wx))
+    _lib.check(rc, "core scan forward")
+    _record_error_word(ws, "core scan forward")
+    del keep
+    fb, fe, fc = (f.to(s.dtype) for f, s in zip(finals, (initial_b, initial_e, initial_c)))
+    return (U, *tapes, fb, fe, fc)
+
+
+@core_scan_batched.register_fake
+def _core_scan_batched_fake(*inputs: Tensor) -> CoreScanOutputs:
+    Wx = inputs[0]
+    ib, ie, ic = inputs[-3:]
+    B, T, H = Wx.shape
+    sig = Wx.new_empty((B, T, H))
+    return (Wx.new_empty((B, T, 2 * H)), sig, sig.clone(), sig.clone(), sig.clone(), sig.clone(),
+            sig.clone(), sig.clone(), ib.new_empty(ib.shape), ie.new_empty(ie.shape),
+            ic.new_empty(ic.shape))
+
+
+@torch.library.custom_op("dabsn::_core_scan_batched_backward", mutates_args=(),
+                         device_types="cuda")
+def core_scan_batched_backward(
+    Ug: Tensor, A: Tensor, vecs: list[Tensor], logit_alpha: Tensor, log_lambda: Tensor,
+    logit_c_suppress: Tensor, initial_b: Tensor, initial_c: Tensor, U: Tensor,
+    plasticity: Tensor, expression: Tensor, energy: Tensor, saturation: Tensor, gate: Tensor,
+    gU: Optional[Tensor], gnovelty: Optional[Tensor], gplasticity: Optional[Tensor],
+    gexpression: Optional[Tensor], gwrite: Optional[Tensor], genergy: Optional[Tensor],
+    gsaturation: Optional[Tensor], gfinal_b: Optional[Tensor], gfinal_e: Optional[Tensor],
+    gfinal_c: Optional[Tensor],
+) -> list[Tensor]:
+    """Reverse scan of the core (reference batched_runtime.py:299-466, 1333-1504).
+
+    Returns [gWx, gWgx, gUg, gA, 16 vector grads, 3 scalar grads, gb0, ge0, gc0] in fp32
+    for parameters/states and in the tape dtype for gWx, gWgx.
+    """
+    _require_cuda(U)
+    lib = _lib.load()
+    B, T, H = plasticity.shape
+    dt = plasticity.dtype
+    code = _code(dt)
+    if T == 0:
+        z = lambda *s: torch.zeros(s, device=U.device, dtype=torch.float32)  # noqa: E731
+        fin = [z(B, H) if g is None else g.float().clone() for g in (gfinal_b, gfinal_e, gfinal_c)]
+        return [torch.zeros((B, 0, H), device=U.device, dtype=dt),
+                torch.zeros((B, 0, H), device=U.device, dtype=dt), z(H, H), z(H, H),
+                *[z(H) for _ in range(16)], *[z() for _ in range(3)], *fin]
+    GAT = torch.cat((Ug, A), dim=0).to(dt).t().contiguous()
+    params, keep = _core_params(vecs, (logit_alpha, log_lambda, logit_c_suppress))
+    b0 = initial_b.float().contiguous()
+    c0 = initial_c.float().contiguous()
+    saved = [x.to(dt).contiguous() for x in (U, plasticity, expression, energy, saturation, gate)]
+    grads = [None if g is None else g.to(dt).contiguous()
+             for g in (gU, gnovelty, gplasticity, gexpression, gwrite, genergy, gsaturation)]
+    gfin = [None if g is None else g.float().contiguous() for g in (gfinal_b, gfinal_e, gfinal_c)]
+    gWx = torch.empty((B, T, H), device=U.device, dtype=dt)
+    gWgx = torch.empty_like(gWx)
+    day = torch.empty_like(gWx)
+    nbg, nwg = _lib.i64(), _lib.i64()
+    _lib.check(lib.dabsn_hip_core_scan_layout(code, B, H, ctypes.byref(nbg), ctypes.byref(nwg)),
+               "core scan layout")
+    part_vec = torch.empty((nbg.value, 16, H), device=U.device, dtype=torch.float32)
+    part_scal = torch.empty((nwg.value, 3), device=U.device, dtype=torch.float32)
+    gb0, ge0, gc0 = (torch.empty((B, H), device=U.device, dtype=torch.float32) for _ in range(3))
+    nbytes = lib.dabsn_hip_core_scan_workspace_bytes(code, B, H, 1)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=U.device)
+    rc = lib.dabsn_hip_core_scan_bwd(
+        code, B, T, H, _p(GAT), ctypes.byref(params), _p(b0), _p(c0), *[_p(x) for x in saved],
+        *[_p(g) for g in grads], *[_p(g) for g in gfin], _p(gWx), _p(gWgx), _p(day),
+        _p(part_vec), _p(part_scal), _p(gb0), _p(ge0), _p(gc0), _p(ws), nbytes, _stream(U))
+    _lib.check(rc, "core scan backward")
+    _record_error_word(ws, "core scan backward")
+    del keep
+    gvec = part_vec.sum(0)
+    gscal = part_scal.sum(0)
+    # grad [Ug; A] = [gWgx; day]^T y: one plain GEMM per half (hipBLASLt through torch).
+    y = U[..., :H].to(dt).reshape(B * T, H)
+    gUg = (gWgx.reshape(B * T, H).t() @ y).float()
+    gA = (day.reshape(B * T, H).t() @ y).float()
+    # operator outputs must not alias each other: split into separate tensors
+    return [gWx, gWgx, gUg, gA, *[gvec[i].clone() for i in range(16)],
+            *[gscal[i].clone() for i in range(3)], gb0, ge0, gc0]
+
+
+@core_scan_batched_backward.register_fake
+def _core_scan_batched_backward_fake(Ug, A, vecs, la, ll, ls, ib, ic, U, plasticity, *rest):
+    B, T, H = plasticity.shape
+    g = plasticity.new_empty((B, T, H))
+    f = lambda *s: plasticity.new_empty(s, dtype=torch.float32)  # noqa: E731
+    return [g, g.clone(), f(H, H), f(H, H), *[f(H) for _ in range(16)], *[f() for _ in range(3)],
+            f(B, H), f(B, H), f(B, H)]
+
+
+def _core_setup(ctx, inputs, output) -> None:
+    (U, _nov, plasticity, expression, _write, energy, saturation, gate, *_finals) = output
+    ctx.save_for_backward(inputs[2], inputs[3], *inputs[4:20], inputs[20], inputs[21],
+                          inputs[22], inputs[23], inputs[25], U, plasticity, expression, energy,
+                          saturation, gate)
+    ctx.input_meta = [(x.dtype, tuple(x.shape)) for x in inputs]
+
+
+def _core_backward(ctx, *grad_outputs):
+    saved = ctx.saved_tensors
+    Ug, A = saved[0], saved[1]
+    vecs = list(saved[2:18])
+    la, ll, ls, ib, ic = saved[18:23]
+    U, plasticity, expression, energy, saturation, gate = saved[23:29]
+    g = list(grad_outputs)
+    # the gate tape (output 7) has no gradient path in the reference op (batched_runtime.py:1619-1627)
+    grads = core_scan_batched_backward(
+        Ug, A, vecs, la, ll, ls, ib, ic, U, plasticity, expression, energy, saturation, gate,
+        g[0], g[1], g[2], g[3], g[4], g[5], g[6], g[8], g[9], g[10])
+    out = []
+    for value, (dtype, shape) in zip(grads, ctx.input_meta):
+        out.append(value.reshape(shape).to(dtype))
+    return tuple(out)
+
+
+torch.library.register_autograd("dabsn::core_scan_batched", _core_backward,
+                                setup_context=_core_setup)
+
+
+# ---------------------------------------------------------------------------
+# Linear recurrence (drop-in for dabsn::linear_recurrence)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("dabsn::linear_recurrence", mutates_args=(), device_types="cuda")
+def linear_recurrence(a: Tensor, g: Tensor, y_init: Tensor) -> Tensor:
+    """y_t = a_t y_{t-1} + g_t (reference long.py:392-396; CPU cpu_runtime.cpp:92-108)."""
+    _require_cuda(a)
+    lib = _lib.load()
+    if a.dim() != 3 or g.shape != a.shape or y_init.shape != (a.shape[0], a.shape[2]):
+        raise ValueError("expected a/g [B,T,H] and y_init [B,H]")
+    dt = a.dtype
+    B, T, H = a.shape
+    a_c, g_c, y0 = a.contiguous(), g.to(dt).contiguous(), y_init.to(dt).contiguous()
+    out = torch.empty_like(a_c)
+    _lib.check(lib.dabsn_hip_linrec_fwd(_code(dt), B, T, H, _p(a_c), _p(g_c), _p(y0), _p(out),
+                                        _stream(a)), "linear recurrence")
+    return out
+
+
+@linear_recurrence.register_fake
+def _linear_recurrence_fake(a, g, y_init):
+    if a.dim() != 3 or g.shape != a.shape or y_init.shape != (a.shape[0], a.shape[2]):
+        raise ValueError("expected a/g [B,T,H] and y_init [B,H]")
+    return torch.empty_like(a)
+
+
+@torch.library.custom_op("dabsn::_linrec_backward", mutates_args=(), device_types="cuda")
+def linrec_backward(a: Tensor, g: Tensor, y_init: Tensor, grad_out: Tensor) -> list[Tensor]:
+    """Analytic reverse of the linear recurrence (reference long.py:58-98, 410-417)."""
+    _require_cuda(a)
+    lib = _lib.load()
+    dt = a.dtype
+    B, T, H = a.shape
+    a_c, g_c, y0, gy = (x.to(dt).contiguous() for x in (a, g, y_init, grad_out))
+    da, dg, dy0 = torch.empty_like(a_c), torch.empty_like(a_c), torch.empty_like(y0)
+    nbytes = lib.dabsn_hip_linrec_workspace_bytes(_code(dt), B, T, H)
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=a.device)
+    _lib.check(lib.dabsn_hip_linrec_bwd(_code(dt), B, T, H, _p(a_c), _p(g_c), _p(y0), _p(gy),
+                                        _p(da), _p(dg), _p(dy0), _p(ws), nbytes, _stream(a)),
+               "linear recurrence backward")
+    return [da, dg.to(g.dtype), dy0.to(y_init.dtype)]
+
+
+@linrec_backward.register_fake
+def _linrec_backward_fake(a, g, y_init, grad_out):
+    return [torch.empty_like(a), torch.empty_like(g), torch.empty_like(y_init)]
+
+
+def _linrec_setup(ctx, inputs, output):
+    ctx.save_for_backward(*inputs)
+
+
+def _linrec_bwd(ctx, grad_out):
+    a, g, y0 = ctx.saved_tensors
+    da, dg, dy = linrec_backward(a, g, y0, grad_out.contiguous())
+    return da, dg, dy
+
+
+torch.library.register_autograd("dabsn::linear_recurrence", _linrec_bwd, setup_context=_linrec_setup)
+
+
+# ---------------------------------------------------------------------------
+# Fused recurrent long-memory scan
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("dabsn::long_scan_fused", mutates_args=(), device_types="cuda")
+def long_scan_fused(
+    write: Tensor, plasticity: Tensor, logit_expect_retain: Tensor,
+    logit_retention_decay: Tensor, logit_retain: Tensor, logit_retention_strength: Tensor,
+    long0: Tensor, expected0: Tensor, retention0: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The three recurrences of long.py:492-579 in one pass. Returns (long [B,T,H],
+    final long, final expected, final retention [B,H] fp32, checkpoints)."""
+    _require_cuda(write)
+    lib = _lib.load()
+    B, T, H = write.shape
+    dt = write.dtype
+    w = write.contiguous()
+    p = plasticity.to(dt).contiguous()
+    logits = [x.float().reshape(()).contiguous() for x in
+              (logit_expect_retain, logit_retention_decay, logit_retain, logit_retention_strength)]
+    ptrs = _lib.PTR4(*[x.data_ptr() for x in logits])
+    L0, E0, R0 = (x.float().contiguous() for x in (long0, expected0, retention0))
+    out = torch.empty_like(w)
+    LF, EF, RF = (torch.empty((B, H), device=w.device, dtype=torch.float32) for _ in range(3))
+    nseg = (T + 31) // 32
+    ckpt = torch.empty((B, nseg, 3, H), device=w.device, dtype=torch.float32)
+    _lib.check(lib.dabsn_hip_long_fwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(L0), _p(E0),
+                                      _p(R0), _p(out), _p(LF), _p(EF), _p(RF), _p(ckpt),
+                                      _stream(w)), "long scan")
+    return out, LF, EF, RF, ckpt
+
+
+@long_scan_fused.register_fake
+def _long_scan_fused_fake(write, plasticity, l1, l2, l3, l4, long0, expected0, retention0):
+    B, T, H = write.shape
+    f = lambda *s: write.new_empty(s, dtype=torch.float32)  # noqa: E731
+    return torch.empty_like(write), f(B, H), f(B, H), f(B, H), f(B, (T + 31) // 32, 3, H)
+
+
+@torch.library.custom_op("dabsn::_long_scan_fused_backward", mutates_args=(),
+                         device_types="cuda")
+def long_scan_fused_backward(
+    write: Tensor, plasticity: Tensor, logits: list[Tensor], ckpt: Tensor, grad_long: Tensor,
+    g_long_final: Optional[Tensor], g_expected_final: Optional[Tensor],
+    g_retention_final: Optional[Tensor],
+) -> list[Tensor]:
+    """Reverse of long_scan_fused: [g_write, g_plasticity, 4 logit grads, gL0, gE0, gR0]."""
+    _require_cuda(write)
+    lib = _lib.load()
+    B, T, H = write.shape
+    dt = write.dtype
+    w = write.contiguous()
+    p = plasticity.to(dt).contiguous()
+    lg = [x.float().reshape(()).contiguous() for x in logits]
+    ptrs = _lib.PTR4(*[x.data_ptr() for x in lg])
+    gout = grad_long.to(dt).contiguous()
+    gf = [None if x is None else x.float().contiguous()
+          for x in (g_long_final, g_expected_final, g_retention_final)]
+    gw, gp = torch.empty_like(w), torch.empty_like(p)
+    g0 = [torch.empty((B, H), device=w.device, dtype=torch.float32) for _ in range(3)]
+    nparts = lib.dabsn_hip_long_partials(B, H)
+    part = torch.empty((nparts, 4), device=w.device, dtype=torch.float32)
+    _lib.check(lib.dabsn_hip_long_bwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(ckpt), _p(gout),
+                                      *[_p(x) for x in gf], _p(gw), _p(gp), *[_p(x) for x in g0],
+                                      _p(part), _stream(w)), "long scan backward")
+    glog = part.sum(0)
+    return [gw, gp.to(plasticity.dtype), *[glog[i].clone() for i in range(4)], *g0]
+
+
+@long_scan_fused_backward.register_fake
+def _long_scan_fused_backward_fake(write, plasticity, logits, ckpt, grad_long, a, b, c):
+    B, T, H = write.shape
+    f = lambda *s: write.new_empty(s, dtype=torch.float32)  # noqa: E731
+    return [torch.empty_like(write), torch.empty_like(plasticity), f(), f(), f(), f(),
+            f(B, H), f(B, H), f(B, H)]
+
+
+def _long_setup(ctx, inputs, output):
+    write, plasticity, l1, l2, l3, l4, L0, E0, R0 = inputs
+    ctx.save_for_backward(write, plasticity, l1, l2, l3, l4, output[4])
+    ctx.meta = [(x.dtype, tuple(x.shape)) for x in inputs]
+
+
+def _long_bwd(ctx, g_long, g_lf, g_ef, g_rf, _g_ckpt):
+    write, plasticity, l1, l2, l3, l4, ckpt = ctx.saved_tensors
+    if g_long is None:
+        g_long = torch.zeros_like(write)
+    grads = long_scan_fused_backward(write, plasticity, [l1, l2, l3, l4], ckpt, g_long, g_lf,
+                                     g_ef, g_rf)
+    return tuple(g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(grads, ctx.meta))
+
+
+torch.library.register_autograd("dabsn::long_scan_fused", _long_bwd, setup_context=_long_setup)
+
+
+# ---------------------------------------------------------------------------
+# Read glue
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("dabsn::read_tape_stats", mutates_args=(), device_types="cuda")
+def read_tape_stats(novelty: Tensor, plasticity: Tensor, energy: Tensor, saturation: Tensor,
+                    expression: Tensor, write: Tensor) -> Tensor:
+    """Per-position (mean e, mean c, mean n, mean p, |expression|, |write|), fp32 [B,T,6]
+    (reference read.py:58-72, 154-183). The two norms carry no gradient here: their
+    dependence is part of the normalisation operators' backward."""
+    _require_cuda(novelty)
+    lib = _lib.load()
+    B, T, H = novelty.shape
+    dt = novelty.dtype
+    xs = [x.to(dt).contiguous() for x in (novelty, plasticity, energy, saturation, expression, write)]
+    stats = torch.empty((B, T, 6), device=novelty.device, dtype=torch.float32)
+    _lib.check(lib.dabsn_hip_tape_stats(_code(dt), B, T, H, *[_p(x) for x in xs], _p(stats),
+                                        _stream(novelty)), "tape statistics")
+    return stats
+
+
+@read_tape_stats.register_fake
+def _read_tape_stats_fake(novelty, plasticity, energy, saturation, expression, write):
+    B, T, _ = novelty.shape
+    return novelty.new_empty((B, T, 6), dtype=torch.float32)
+
+
+@torch.library.custom_op("dabsn::_read_tape_stats_backward", mutates_args=(),
+                         device_types="cuda")
+def read_tape_stats_backward(gstats: Tensor, like: Tensor) -> list[Tensor]:
+    """Broadcast mean gradients back to the four averaged tapes [g_n, g_p, g_e, g_c]."""
+    lib = _lib.load()
+    B, T, H = like.shape
+    dt = like.dtype
+    gs = gstats.float().contiguous()
+    gn, gp, ge, gc = (torch.zeros((B, T, H), device=like.device, dtype=dt) for _ in range(4))
+    _lib.check(lib.dabsn_hip_tape_stats_bwd(_code(dt), B, T, H, None, None, None, _p(gs), _p(gn),
+                                            _p(gp), _p(ge), _p(gc), None, None, _stream(like)),
+               "tape statistics backward")
+    return [gn, gp, ge, gc]
+
+
+@read_tape_stats_backward.register_fake
+def _read_tape_stats_backward_fake(gstats, like):
+    return [torch.empty_like(like) for _ in range(4)]
+
+
+def _stats_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0])
+    ctx.dtypes = [x.dtype for x in inputs]
+
+
+def _stats_bwd(ctx, gstats):
+    (like,) = ctx.saved_tensors
+    gn, gp, ge, gc = read_tape_stats_backward(gstats, like)
+    d = ctx.dtypes
+    return gn.to(d[0]), gp.to(d[1]), ge.to(d[2]), gc.to(d[3]), None, None
+
+
+torch.library.register_autograd("dabsn::read_tape_stats", _stats_bwd, setup_context=_stats_setup)
+
+
+@torch.library.custom_op("dabsn::normalize_rows", mutates_args=(), device_types="cuda")
+def normalize_rows(x: Tensor, norms: Tensor) -> Tensor:
+    """x / max(norms, 1e-12) along the last dim, norms = |x| rows (F.normalize, read.py:154)."""
+    lib = _lib.load()
+    H = x.shape[-1]
+    rows = x.numel() // H
+    xc = x.contiguous()
+    n = norms.float().contiguous()
+    q = torch.empty_like(xc)
+    _lib.check(lib.dabsn_hip_normalize_rows(_code(x.dtype), rows, H, _p(xc), _p(n), _p(q),
+                                            _stream(x)), "normalize rows")
+    return q
+
+
+@normalize_rows.register_fake
+def _normalize_rows_fake(x, norms):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("dabsn::_normalize_rows_backward", mutates_args=(), device_types="cuda")
+def normalize_rows_backward(q: Tensor, norms: Tensor, gq: Tensor) -> Tensor:
+    lib = _lib.load()
+    H = q.shape[-1]
+    rows = q.numel() // H
+    qc = q.contiguous()
+    gqc = gq.to(q.dtype).contiguous()
+    gx = torch.zeros_like(qc)
+    _lib.check(lib.dabsn_hip_normalize_rows_bwd(_code(q.dtype), rows, H, _p(qc),
+                                                _p(norms.float().contiguous()), _p(gqc), _p(gx),
+                                                _stream(q)), "normalize rows backward")
+    return gx
+
+
+@normalize_rows_backward.register_fake
+def _normalize_rows_backward_fake(q, norms, gq):
+    return torch.empty_like(q)
+
+
+def _norm_setup(ctx, inputs, output):
+    ctx.save_for_backward(output, inputs[1])
+
+
+def _norm_bwd(ctx, gq):
+    q, norms = ctx.saved_tensors
+    return normalize_rows_backward(q, norms, gq), None
+
+
+torch.library.register_autograd("dabsn::normalize_rows", _norm_bwd, setup_context=_norm_setup)
+
+
+@torch.library.custom_op("dabsn::bank_select", mutates_args=(), device_types="cuda")
+def bank_select(admission: Tensor, window: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Admitted-slot selection (read.py:185-239): (order [B,T] int64, counts [B] int64,
+    rank [B,T] int32). Bit-exact integer work given the admission values."""
+    lib = _lib.load()
+    B, T = admission.shape
+    adm = admission.float().contiguous()
+    win = window.float().reshape(()).contiguous()
+    order = torch.empty((B, T), device=adm.device, dtype=torch.int64)
+    counts = torch.empty((B,), device=adm.device, dtype=torch.int64)
+    rank = torch.empty((B, T), device=adm.device, dtype=torch.int32)
+    _lib.check(lib.dabsn_hip_bank_select(B, T, _p(adm), _p(win), _p(order), _p(counts), _p(rank),
+                                         _stream(adm)), "bank selection")
+    return order, counts, rank
+
+
+@bank_select.register_fake
+def _bank_select_fake(admission, window):
+    B, T = admission.shape
+    return (admission.new_empty((B, T), dtype=torch.int64),
+            admission.new_empty((B,), dtype=torch.int64),
+            admission.new_empty((B, T), dtype=torch.int32))
+
+
+@torch.library.custom_op("dabsn::bank_gather", mutates_args=(), device_types="cuda")
+def bank_gather(write: Tensor, norm_w: Tensor, idx: Tensor, next_idx: Tensor,
+                rank: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """(normalize(write[idx]), write[idx], write[next_idx]) as in read.py:241-256, 298-303."""
+    lib = _lib.load()
+    B, T, H = write.shape
+    N = idx.shape[1]
+    w = write.contiguous()
+    K, V, Vn = (torch.empty((B, N, H), device=w.device, dtype=w.dtype) for _ in range(3))
+    _lib.check(lib.dabsn_hip_bank_gather(_code(w.dtype), B, T, N, H, _p(w),
+                                         _p(norm_w.float().contiguous()), _p(idx.contiguous()),
+                                         _p(next_idx.contiguous()), _p(K), _p(V), _p(Vn),
+                                         _stream(w)), "bank gather")
+    return K, V, Vn
+
+
+@bank_gather.register_fake
+def _bank_gather_fake(write, norm_w, idx, next_idx, rank):
+    B, T, H = write.shape
+    N = idx.shape[1]
+    return tuple(write.new_empty((B, N, H)) for _ in range(3))
+
+
+@torch.library.custom_op("dabsn::_bank_gather_backward", mutates_args=(), device_types="cuda")
+def bank_gather_backward(write: Tensor, norm_w: Tensor, rank: Tensor, K: Tensor, gK: Tensor,
+                         gV: Tensor, gVn: Tensor) -> Tensor:
+    """Deterministic inverse gather of the bank gradients onto the write tape."""
+    lib = _lib.load()
+    B, T, H = write.shape
+    N = K.shape[1]
+    dt = write.dtype
+    gw = torch.zeros((B, T, H), device=write.device, dtype=dt)
+    _lib.check(lib.dabsn_hip_bank_gather_bwd(_code(dt), B, T, N, H, None,
+                                             _p(norm_w.float().contiguous()), _p(rank.contiguous()),
+                                             _p(K.contiguous()), _p(gK.to(dt).contiguous()),
+                                             _p(gV.to(dt).contiguous()), _p(gVn.to(dt).contiguous()),
+                                             _p(gw), _stream(write)), "bank gather backward")
+    return gw
+
+
+@bank_gather_backward.register_fake
+def _bank_gather_backward_fake(write, norm_w, rank, K, gK, gV, gVn):
+    return torch.empty_like(write)
+
+
+def _gather_setup(ctx, inputs, output):
+    write, norm_w, idx, next_idx, rank = inputs
+    ctx.save_for_backward(write, norm_w, rank, output[0])
+
+
+def _gather_bwd(ctx, gK, gV, gVn):
+    write, norm_w, rank, K = ctx.saved_tensors
+    z = lambda g: torch.zeros_like(K) if g is None else g  # noqa: E731
+    gw = bank_gather_backward(write, norm_w, rank, K, z(gK), z(gV), z(gVn))
+    return gw, None, None, None, None
+
+
+torch.library.register_autograd("dabsn::bank_gather", _gather_bwd, setup_context=_gather_setup)
+
+
+# ---------------------------------------------------------------------------
+# Three-way admitted read (compact ABI)
+# ---------------------------------------------------------------------------
+def _read_common(query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail,
+                 bank_key_bias, bank_admission, scale, bank_idx, bank_valid, gains):
+    dt = query.dtype
+    q = query.contiguous()
+    K, V, Vn = (x.to(dt).contiguous() for x in (bank_keys, bank_writes, next_writes))
+    ck, cb, kb, adm = (x.float().contiguous() for x in (cocktail, bank_cocktail, bank_key_bias,
+                                                       bank_admission))
+    sc = scale.float().reshape(()).contiguous()
+    g = [x.float().reshape(()).contiguous() for x in gains]
+    idx = bank_idx.to(torch.int64).contiguous()
+    valid = bank_valid.to(torch.uint8).contiguous()
+    if cocktail.shape[-1] != 4 or bank_cocktail.shape[-1] != 4:
+        raise ValueError("the HIP read expects a 4-component cocktail")
+    return dt, q, K, V, Vn, ck, cb, kb, adm, sc, g, idx, valid
+
+
+@torch.library.custom_op("dabsn::admitted_three_way_read_compact_flash", mutates_args=(),
+                         device_types="cuda")
+def admitted_three_way_read_compact_flash(
+    query: Tensor, bank_keys: Tensor, bank_writes: Tensor, next_writes: Tensor, cocktail: Tensor,
+    bank_cocktail: Tensor, bank_key_bias: Tensor, bank_admission: Tensor, scale: Tensor,
+    bank_idx: Tensor, bank_valid: Tensor, mode: int, short_gain: Tensor, pad_gain: Tensor,
+    induct_gain: Tensor, cocktail_gain: Tensor,
+) -> Tensor:
+    """Three-way admitted read (reference compact_flash.py:71-107; math admitted.py:16-65)."""
+    _require_cuda(query)
+    lib = _lib.load()
+    if mode not in (0, 1):
+        raise ValueError("compact admitted-read mode must be 0 (seq) or 1 (field)")
+    dt, q, K, V, Vn, ck, cb, kb, adm, sc, g, idx, valid = _read_common(
+        query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+        bank_admission, scale, bank_idx, bank_valid,
+        (short_gain, pad_gain, induct_gain, cocktail_gain))
+    B, T, H = q.shape
+    N = K.shape[1]
+    code = _code(dt)
+    out = torch.empty_like(q)
+    nbytes = lib.dabsn_hip_read3_workspace_bytes(code, B, T, N, H, 0)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
+    _lib.check(lib.dabsn_hip_read3_fwd(code, B, T, N, H, _p(q), _p(K), _p(V), _p(Vn), _p(ck),
+                                       _p(cb), _p(kb), _p(adm), _p(sc), _p(idx), _p(valid), mode,
+                                       ptrs, _p(out), _p(ws), ws.numel(), _stream(q)),
+               "three-way read")
+    return out
+
+
+@admitted_three_way_read_compact_flash.register_fake
+def _read_fake(query, *rest):
+    return torch.empty_like(query)
+
+
+CompactGradients = tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                         Tensor, Tensor, Tensor, Tensor]
+
+
+@torch.library.custom_op("dabsn::_admitted_three_way_read_compact_flash_backward",
+                         mutates_args=(), device_types="cuda")
+def admitted_three_way_read_compact_flash_backward(
+    grad_output: Tensor, query: Tensor, bank_keys: Tensor, bank_writes: Tensor,
+    next_writes: Tensor, cocktail: Tensor, bank_cocktail: Tensor, bank_key_bias: Tensor,
+    bank_admission: Tensor, scale: Tensor, bank_idx: Tensor, bank_valid: Tensor, mode: int,
+    short_gain: Tensor, pad_gain: Tensor, induct_gain: Tensor, cocktail_gain: Tensor,
+) -> CompactGradients:
+    """13 gradients (compact_flash.py:181-224 order): query, bank_keys, bank_writes,
+    next_writes, cocktail, bank_cocktail, bank_key_bias, bank_admission, scale, short_gain,
+    pad_gain, induct_gain, cocktail_gain."""
+    _require_cuda(query)
+    lib = _lib.load()
+    dt, q, K, V, Vn, ck, cb, kb, adm, sc, g, idx, valid = _read_common(
+        query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+        bank_admission, scale, bank_idx, bank_valid,
+        (short_gain, pad_gain, induct_gain, cocktail_gain))
+    B, T, H = q.shape
+    N = K.shape[1]
+    code = _code(dt)
+    go = grad_output.to(dt).contiguous()
+    gq = torch.empty_like(q)
+    gK, gV, gVn = (torch.empty((B, N, H), device=q.device, dtype=dt) for _ in range(3))
+    gck = torch.empty((B, T, 4), device=q.device, dtype=torch.float32)
+    gcb = torch.empty((B, N, 4), device=q.device, dtype=torch.float32)
+    gkb = torch.empty((B, N), device=q.device, dtype=torch.float32)
+    gadm = torch.empty((B, N), device=q.device, dtype=torch.float32)
+    g5 = torch.empty((5,), device=q.device, dtype=torch.float32)
+    nbytes = lib.dabsn_hip_read3_workspace_bytes(code, B, T, N, H, 1)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
+    _lib.check(lib.dabsn_hip_read3_bwd(code, B, T, N, H, _p(go), _p(q), _p(K), _p(V), _p(Vn),
+                                       _p(ck), _p(cb), _p(kb), _p(adm), _p(sc), _p(idx),
+                                       _p(valid), mode, ptrs, _p(gq), _p(gK), _p(gV), _p(gVn),
+                                       _p(gck), _p(gcb), _p(gkb), _p(gadm), _p(g5), _p(ws),
+                                       ws.numel(), _stream(q)), "three-way read backward")
+    return (gq, gK.to(bank_keys.dtype), gV.to(bank_writes.dtype), gVn.to(next_writes.dtype),
+            gck.to(cocktail.dtype), gcb.to(bank_cocktail.dtype), gkb.to(bank_key_bias.dtype),
+            gadm.to(bank_admission.dtype),
+            g5[0].clone().reshape_as(scale).to(scale.dtype),
+            g5[1].clone().reshape_as(short_gain).to(short_gain.dtype),
+            g5[2].clone().reshape_as(pad_gain).to(pad_gain.dtype),
+            g5[3].clone().reshape_as(induct_gain).to(induct_gain.dtype),
+            g5[4].clone().reshape_as(cocktail_gain).to(cocktail_gain.dtype))
+
+
+@admitted_three_way_read_compact_flash_backward.register_fake
+def _read_backward_fake(grad_output, query, bank_keys, bank_writes, next_writes, cocktail,
+                        bank_cocktail, bank_key_bias, bank_admission, scale, bank_idx, bank_valid,
+                        mode, short_gain, pad_gain, induct_gain, cocktail_gain):
+    return tuple(torch.empty_like(v) for v in (
+        query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+        bank_admission, scale, short_gain, pad_gain, induct_gain, cocktail_gain))
+
+
+def _read_setup(ctx, inputs, output):
+    ctx.save_for_backward(*inputs[:11], *inputs[12:])
+    ctx.mode = int(inputs[11])
+
+
+def _read_bwd(ctx, grad_output):
+    t = ctx.saved_tensors
+    g = admitted_three_way_read_compact_flash_backward(grad_output, *t[:11], ctx.mode, *t[11:])
+    return (*g[:9], None, None, None, *g[9:])
+
+
+torch.library.register_autograd("dabsn::admitted_three_way_read_compact_flash", _read_bwd,
+                                setup_context=_read_setup)
+
+
+OPERATORS = (
+    "dabsn::core_scan_batched",
+    "dabsn::_core_scan_batched_backward",
+    "dabsn::linear_recurrence",
+    "dabsn::_linrec_backward",
+    "dabsn::long_scan_fused",
+    "dabsn::_long_scan_fused_backward",
+    "dabsn::read_tape_stats",
+    "dabsn::_read_tape_stats_backward",
+    "dabsn::normalize_rows",
+    "dabsn::_normalize_rows_backward",
+    "dabsn::bank_select",
+    "dabsn::bank_gather",
+    "dabsn::_bank_gather_backward",
+    "dabsn::admitted_three_way_read_compact_flash",
+    "dabsn::_admitted_three_way_read_compact_flash_backward",
+)

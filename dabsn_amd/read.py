@@ -1,0 +1,208 @@
+"""DABSN read (admitted short memory, permanent associative memory, successor induction,
+recurrent long memory) on the ROCm backend.
+
+Parameter names and initial values follow the reference (src/dabsn/read.py:42-113).
+``_unified_forward`` follows read.py:139-438 for seq geometry and
+``forward_query_bank`` follows read.py:650-838. The heavy pieces run as registered HIP
+operators: tape statistics and query normalisation, admitted-slot selection, bank
+gather, the three-way read and the fused long-memory scan. The [B,T]-sized glue
+(key bias, admission, cocktail, their parameter gradients) stays in torch.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch import Tensor
+
+from .kernels import ops
+
+
+def _parameter(value: float) -> nn.Parameter:
+    return nn.Parameter(torch.full((1,), float(value)))
+
+
+class _AdmittedReadParameters(nn.Module):
+    """Parameters shared by the three-way admitted read (read.py:42-72)."""
+
+    def __init__(self, hidden_dim: int) -> None:
+        super().__init__()
+        self.log_temp = _parameter(0.0)
+        self.p_gain = _parameter(1.0)
+        self.novelty_gain = _parameter(0.5)
+        self.null_bias = _parameter(-2.0)
+        self.out = nn.Linear(hidden_dim * 3, hidden_dim)
+        self.adm_p_gain = _parameter(1.0)
+        self.adm_novelty_gain = _parameter(0.5)
+        self.adm_saturation_gain = _parameter(0.5)
+        self.adm_energy_gain = _parameter(0.25)
+        self.adm_bias = _parameter(-2.0)
+
+    def admission_from_means(self, mean_e, mean_c, mean_n, mean_p, hidden: int) -> Tensor:
+        return (self.adm_p_gain * torch.log1p(mean_p * hidden) + self.adm_novelty_gain * mean_n
+                + self.adm_saturation_gain * mean_c + self.adm_energy_gain * mean_e + self.adm_bias)
+
+    def key_bias_from_means(self, mean_n, mean_p, hidden: int) -> Tensor:
+        return (self.p_gain * torch.log1p(mean_p * hidden) + self.novelty_gain * mean_n
+                + self.null_bias)
+
+
+def _cocktail(mean_e, mean_c, mean_n, mean_p) -> Tensor:
+    return F.normalize(torch.stack([mean_e, mean_c, mean_n, mean_p], dim=-1), dim=-1)
+
+
+class DABSNRead(nn.Module):
+    """The canonical DABSN memory read (seq geometry)."""
+
+    _rocm_native_enabled = False
+
+    def __init__(self, hidden_dim: int, read_geometry: str = "seq") -> None:
+        super().__init__()
+        if read_geometry != "seq":
+            raise ValueError("the ROCm backend implements the seq read geometry")
+        self.hidden_dim = hidden_dim
+        self.read_geometry = read_geometry
+        self.last_n_max: int | None = None
+        self.last_read_contract: dict[str, object] = {}
+        self.pad_gain = _parameter(1.0)
+        self.short_gain = _parameter(1.0)
+        self.induct_gain = _parameter(0.1)
+        self.cocktail_gain = _parameter(1.0)
+        self.admit_window = _parameter(4.0)
+        self.short_read = _AdmittedReadParameters(hidden_dim)
+        self.logit_retain = _parameter(2.2)
+        self.long_gain = _parameter(0.1)
+        self.logit_expect_retain = _parameter(2.2)
+        self.logit_retention_decay = _parameter(2.2)
+        self.logit_retention_strength = _parameter(1.4)
+        # Optional static bank width (read.py:224-231): a capture-safe, sync-free width.
+        self._capture_bank_width: int | None = None
+
+    # ---- selection ------------------------------------------------------------
+    def _select(self, admission: Tensor, length: int):
+        window = F.softplus(self.admit_window)
+        order, counts, rank = ops.bank_select(admission.detach(), window.detach())
+        if self._capture_bank_width:
+            n_max = max(1, min(int(self._capture_bank_width), length))
+        else:
+            n_max = max(int(counts.max().item()), 1)  # host sync, as read.py:233
+        idx = order[:, :n_max]
+        valid = torch.arange(n_max, device=admission.device).unsqueeze(0) < counts.clamp_min(1).unsqueeze(1)
+        next_idx = (idx + 1).clamp(max=length - 1)
+        return n_max, idx, valid, next_idx, rank
+
+    def _read_core(self, query, cocktail, bank_write, norm_w, key_bias, admission, length: int,
+                   query_start: int):
+        n_max, idx, valid, next_idx, rank = self._select(admission, length)
+        self.last_n_max = n_max
+        K, V, Vn = ops.bank_gather(bank_write, norm_w, idx, next_idx, rank)
+        bank_cocktail = torch.gather(cocktail[1], 1, idx.unsqueeze(-1).expand(-1, -1, 4))
+        bank_bias = torch.gather(key_bias, 1, idx)
+        bank_adm = torch.gather(admission, 1, idx)
+        scale = (F.softplus(self.short_read.log_temp) + 1.0) * (self.hidden_dim ** 0.5)
+        read_idx = idx if query_start == 0 else idx - query_start
+        retrieved = ops.admitted_three_way_read_compact_flash(
+            query, K, V, Vn, cocktail[0], bank_cocktail, bank_bias, bank_adm, scale, read_idx, valid,
+            0, self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain)
+        self.last_read_contract = {
+            "read_strategy": "rocm_compact_admitted_bank",
+            "exact": True,
+            "max_admitted_bank": int(n_max),
+            "bank_growth": "grows_with_T" if n_max >= length else "data_dependent",
+            "estimated_read_work": int(query.shape[0]) * int(query.shape[1]) * int(n_max) * 3,
+            "admission_policy": "causal_write_prefix_max",
+            "kernel_backend": "rocm_hip_mfma",
+            "query_start": int(query_start),
+        }
+        return retrieved
+
+    # ---- forward ---------------------------------------------------------------
+    def forward(self, y, budget, expression, write, novelty, plasticity, energy, saturation,
+                field_shape=None) -> Tensor:
+        del field_shape
+        return self._unified_forward(y, budget, expression, write, novelty, plasticity, energy,
+                                     saturation)
+
+    def _unified_forward(self, y, budget, expression, write, novelty, plasticity, energy,
+                         saturation) -> Tensor:
+        rp = self.short_read
+        _, seq_len, hidden = expression.shape
+        stats = ops.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
+        mean_e, mean_c, mean_n, mean_p = stats.unbind(-1)[:4]
+        norm_ay = stats[..., 4].detach()
+        norm_w = stats[..., 5].detach()
+        query = ops.normalize_rows(expression, norm_ay)
+        key_bias = rp.key_bias_from_means(mean_n, mean_p, hidden)
+        admission = rp.admission_from_means(mean_e, mean_c, mean_n, mean_p, hidden)
+        cocktail = _cocktail(mean_e, mean_c, mean_n, mean_p)
+        retrieved = self._read_core(query, (cocktail, cocktail), write, norm_w, key_bias,
+                                    admission, seq_len, 0)
+        output = rp.out(torch.cat([y, budget, retrieved.to(y.dtype)], dim=-1))
+        long = self._long_scan(write, plasticity, novelty)
+        return output + self.long_gain * long
+
+    # ---- long memory -------------------------------------------------------------
+    def initial_long_scan_state(self, batch_size: int, hidden_dim: int | None = None, *,
+                                device=None, dtype=None):
+        hidden = int(hidden_dim or self.hidden_dim)
+        device = self.logit_retain.device if device is None else device
+        long = torch.zeros(batch_size, hidden, device=device, dtype=torch.float32)
+        return long, torch.zeros_like(long), torch.ones_like(long)
+
+    def _long_scan_from_state(self, write, plasticity, novelty, *, initial_state=None,
+                              return_final_state: bool = False):
+        del novelty  # unused by the long channel (long.py:501)
+        batch, _, hidden = write.shape
+        if initial_state is None:
+            initial_state = self.initial_long_scan_state(batch, hidden, device=write.device)
+        else:
+            if any(s.shape != (batch, hidden) for s in initial_state):
+                raise ValueError(f"initial long-scan state must have shape {(batch, hidden)}")
+        long, lf, ef, rf, _ = ops.long_scan_fused(
+            write, plasticity, self.logit_expect_retain, self.logit_retention_decay,
+            self.logit_retain, self.logit_retention_strength, *initial_state)
+        if return_final_state:
+            return long, (lf, ef, rf)
+        return long
+
+    def _long_scan(self, write, plasticity, novelty) -> Tensor:
+        return self._long_scan_from_state(write, plasticity, novelty)
+
+    # ---- external bank ---------------------------------------------------------
+    def forward_query_bank(self, y, budget, expression, write, novelty, plasticity, energy,
+                           saturation, *, bank_y=None, bank_b=None, bank_ay=None, bank_write,
+                           bank_novelty, bank_p, bank_energy, bank_saturation, query_start: int,
+                           initial_long_state=None, return_long_state: bool = False):
+        """Exact read of a query chunk against an external bank (read.py:650-838)."""
+        del bank_y, bank_b, bank_ay
+        rp = self.short_read
+        _, _, hidden = expression.shape
+        bank_len = bank_write.shape[1]
+        if bank_len <= 0:
+            raise RuntimeError("query-bank read requires a non-empty bank")
+        q_stats = ops.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
+        b_stats = ops.read_tape_stats(bank_novelty, bank_p, bank_energy, bank_saturation,
+                                      bank_write, bank_write)
+        qe, qc, qn, qp = q_stats.unbind(-1)[:4]
+        be, bc, bn, bp = b_stats.unbind(-1)[:4]
+        query = ops.normalize_rows(expression, q_stats[..., 4].detach())
+        key_bias = rp.key_bias_from_means(bn, bp, hidden)
+        admission = rp.admission_from_means(be, bc, bn, bp, hidden)
+        cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
+        retrieved = self._read_core(query, cocktails, bank_write, b_stats[..., 5].detach(),
+                                    key_bias, admission, bank_len, int(query_start))
+        short_output = rp.out(torch.cat([y, budget, retrieved.to(y.dtype)], dim=-1))
+        result = self._long_scan_from_state(write, plasticity, novelty,
+                                            initial_state=initial_long_state,
+                                            return_final_state=return_long_state)
+        if return_long_state:
+            long, final_state = result
+            return short_output + self.long_gain * long, final_state
+        return short_output + self.long_gain * result
+
+
+def collect_traces_enabled() -> bool:
+    return os.environ.get("DABSN_COLLECT_TRACES", "0") == "1"

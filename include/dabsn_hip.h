@@ -1,0 +1,182 @@
+/*
+ * dabsn_hip.h -- C ABI of the MI355X (gfx950) DABSN hot-path library.
+ *
+ * Every entry point takes raw device pointers, sizes and a hipStream_t, enqueues its
+ * kernels on that stream (no host synchronisation inside) and returns a status code:
+ * 0 on success, negative on error (dabsn_hip_last_error() describes it). Tensors are
+ * dense row-major. `dtype` selects the activation storage type: 0 = fp32, 1 = bf16
+ * (raw 16-bit storage); per-unit parameters, carried states and reductions are fp32.
+ *
+ * Each entry point names the reference interface it replaces (paths relative to the
+ * BleedingXiko/dabsn source tree).
+ */
+#ifndef DABSN_HIP_H_
+#define DABSN_HIP_H_
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define DABSN_HIP_ABI_VERSION 1
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- library ----------------------------------------------------------------- */
+int dabsn_hip_abi_version(void);
+const char* dabsn_hip_last_error(void);
+/* Zero `bytes` (multiple of 4) of device memory with a fill kernel (graph-safe). */
+int dabsn_hip_zero(void* ptr, size_t bytes, hipStream_t stream);
+
+/* ---- core recurrence ------------------------------------------------------------
+ * Replaces the device kernels of the registered op dabsn::core_scan_batched
+ * (src/dabsn/kernels/batched_runtime.py:1507-1586; CPU kernel cpu.py:777-882 ->
+ * cpu_runtime.cpp:672-837) and its reverse recurrence (batched_runtime.py:299-466,
+ * 1333-1504), which the reference only has as a Python per-step loop.
+ *
+ * Parameter table: vec[16] are [H] fp32 vectors in op-input order 4..19 (beta, log_kappa,
+ * logit_recover, k_s, k_y, k_b, k_n, k_bias, r_s, r_y, r_b, r_n, r_bias, logit_c_decay,
+ * k_c, r_c); scal[3] point at fp32 scalars (logit_alpha, log_lambda, logit_c_suppress).
+ * The workspace's first 4 bytes hold an error word (non-zero = a step barrier timed out);
+ * the caller may read it after the stream completes. */
+typedef struct dabsn_core_params {
+  const float* vec[16];
+  const float* scal[3];
+} dabsn_core_params;
+
+size_t dabsn_hip_core_scan_workspace_bytes(int dtype, int64_t B, int64_t H, int backward);
+
+/* Number of batch groups and of workgroups: sizes of part_vec ([nbg][16][H]) and
+ * part_scal ([nwg][3]) in the backward. */
+int dabsn_hip_core_scan_layout(int dtype, int64_t B, int64_t H, int64_t* nbg, int64_t* nwg);
+
+/* Forward. Wx, Wgx [B,T,H]; GA = [Ug; A] as [2H,H]; b0, e0, c0 [B,H] fp32.
+ * Outputs: U [B,T,2H] (y, next budget), nov, plast, expr, write, energy (pre-update),
+ * sat (post-update), gate [B,T,H]; final state bF, eF, cF [B,H] fp32. */
+int dabsn_hip_core_scan_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* Wx,
+                            const void* Wgx, const void* GA, const dabsn_core_params* params,
+                            const float* b0, const float* e0, const float* c0, void* U, void* nov,
+                            void* plast, void* expr, void* write, void* energy, void* sat,
+                            void* gate, float* bF, float* eF, float* cF, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+
+/* Backward. GAT = [Ug; A]^T as [H,2H]. Saved tapes from the forward; upstream grads gU
+ * [B,T,2H], gNov, gP, gAy, gW, gE, gC [B,T,H] and gbF, geF, gcF [B,H] (any may be NULL =
+ * zeros). Outputs: gWx, gWgx (= d gate pre-activation), day (= d expression) [B,T,H];
+ * per-unit parameter partials part_vec [nbg][16][H]; scalar partials part_scal [nwg][3];
+ * initial-state grads gb0, ge0, gc0 [B,H]. grad [Ug; A] = [gWgx; day]^T y is a plain GEMM
+ * left to the caller. */
+int dabsn_hip_core_scan_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* GAT,
+                            const dabsn_core_params* params, const float* b0, const float* c0,
+                            const void* U, const void* plast, const void* expr, const void* energy,
+                            const void* sat, const void* gate, const void* gU, const void* gNov,
+                            const void* gP, const void* gAy, const void* gW, const void* gE,
+                            const void* gC, const float* gbF, const float* geF, const float* gcF,
+                            void* gWx, void* gWgx, void* day, float* part_vec, float* part_scal,
+                            float* gb0, float* ge0, float* gc0, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+
+/* ---- linear recurrence -----------------------------------------------------------
+ * Replaces dabsn::linear_recurrence / dabsn::_linrec_backward
+ * (src/dabsn/kernels/long.py:392-437; CPU cpu_runtime.cpp:92-143).
+ * y_t = a_t * y_{t-1} + g_t over [B,T,H], y_{-1} = y0 [B,H] (same dtype as a).
+ * Backward workspace: dabsn_hip_linrec_workspace_bytes() bytes. */
+int dabsn_hip_linrec_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* a, const void* g,
+                         const void* y0, void* y, hipStream_t stream);
+size_t dabsn_hip_linrec_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t H);
+int dabsn_hip_linrec_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* a, const void* g,
+                         const void* y0, const void* gy, void* da, void* dg, void* dy0,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ---- recurrent long memory ---------------------------------------------------------
+ * Fused form of the three recurrences of src/dabsn/kernels/long.py:492-579 (loop form
+ * read.py:625-636). logits[4] point at fp32 scalars (logit_expect_retain,
+ * logit_retention_decay, logit_retain, logit_retention_strength). State L0/E0/R0 [B,H]
+ * fp32 in, LF/EF/RF out. ckpt (may be NULL) receives fp32 (L,E,R) every
+ * DABSN_LONG_CKPT steps: [B][ceil(T/ckpt)][3][H]; the backward requires it. */
+#define DABSN_LONG_CKPT 32
+int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
+                       const float* const* logits, const float* L0, const float* E0,
+                       const float* R0, void* out, float* LF, float* EF, float* RF, float* ckpt,
+                       hipStream_t stream);
+/* Backward: gout [B,T,H], gLF/gEF/gRF (may be NULL). Outputs gw, gp [B,T,H], gL0, gE0, gR0
+ * [B,H], and part_logit [nblocks][4] with nblocks = dabsn_hip_long_partials(B, H): per-block
+ * partial sums of the gradient w.r.t. the four logits. */
+int64_t dabsn_hip_long_partials(int64_t B, int64_t H);
+int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
+                       const float* const* logits, const float* ckpt, const void* gout,
+                       const float* gLF, const float* gEF, const float* gRF, void* gw, void* gp,
+                       float* gL0, float* gE0, float* gR0, float* part_logit, hipStream_t stream);
+
+/* ---- read glue ----------------------------------------------------------------------
+ * Per-position statistics of the read (src/dabsn/read.py:58-72, 154-183): stats[B,T,6] =
+ * (mean energy, mean saturation, mean novelty, mean plasticity, |expression|, |write|). */
+int dabsn_hip_tape_stats(int dtype, int64_t B, int64_t T, int64_t H, const void* nov,
+                         const void* plast, const void* energy, const void* sat, const void* expr,
+                         const void* write, float* stats, hipStream_t stream);
+/* Backward of tape_stats, accumulated into the tape grads (g* += ...; NULL to skip). */
+int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* expr,
+                             const void* write, const float* stats, const float* gstats,
+                             void* gnov, void* gplast, void* genergy, void* gsat, void* gexpr,
+                             void* gwrite, hipStream_t stream);
+/* Row normalisation q = x / max(|x|, 1e-12) given norms [B*T] (F.normalize, read.py:154). */
+int dabsn_hip_normalize_rows(int dtype, int64_t rows, int64_t H, const void* x, const float* norms,
+                             void* q, hipStream_t stream);
+/* Backward: gx += (gq - q (q . gq)) / max(|x|, eps). */
+int dabsn_hip_normalize_rows_bwd(int dtype, int64_t rows, int64_t H, const void* q,
+                                 const float* norms, const void* gq, void* gx, hipStream_t stream);
+
+/* Admitted-slot selection (src/dabsn/read.py:185-239, seq geometry): per row, floor =
+ * cummax(adm) - window, member = adm >= floor, order = stable partition (members by
+ * ascending t, then the rest), counts = #members, rank[t] = position of t in order.
+ * adm [B,T] fp32; window points at an fp32 scalar (already softplus-ed). Bit-exact. */
+int dabsn_hip_bank_select(int64_t B, int64_t T, const float* adm, const float* window,
+                          int64_t* order, int64_t* counts, int32_t* rank, hipStream_t stream);
+
+/* Bank gather (read.py:241-256, 298-303): for j < N, K = w[idx]/max(|w[idx]|,eps),
+ * V = w[idx], Vn = w[next_idx] ([B,N,H]). norm_w [B,T] fp32. */
+int dabsn_hip_bank_gather(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* w,
+                          const float* norm_w, const int64_t* idx, const int64_t* next_idx,
+                          void* K, void* V, void* Vn, hipStream_t stream);
+/* Backward, as a deterministic gather over positions using rank [B,T]:
+ * gw[t] += (rank[t] < N ? gV + dnorm(gK) : 0) + sum of gVn over slots whose next index is t. */
+int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
+                              const void* w, const float* norm_w, const int32_t* rank,
+                              const void* K, const void* gK, const void* gV, const void* gVn,
+                              void* gw, hipStream_t stream);
+
+/* ---- three-way admitted read ------------------------------------------------------
+ * Replaces the device kernels of dabsn::admitted_three_way_read_compact_flash and
+ * dabsn::_admitted_three_way_read_compact_flash_backward
+ * (src/dabsn/kernels/compact_flash.py:71-107, 181-224; math admitted.py:9-239; CPU
+ * cpu_runtime.cpp:321-438, 479-662). q [B,T,H] (normalised queries), K (normalised
+ * keys), V, Vn [B,N,H] in `dtype`; cocktail [B,T,4], bank_cocktail [B,N,4], key_bias and
+ * admission [B,N] in fp32; scale and gains[4] (short, pad, induct, cocktail) point at
+ * fp32 scalars; idx [B,N] int64 and valid [B,N] uint8; mode 0 = seq (allow idx <= t,
+ * induction idx < t), 1 = field (allow valid, induction idx < T-1). */
+size_t dabsn_hip_read3_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
+                                       int backward);
+int dabsn_hip_read3_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* q,
+                        const void* K, const void* V, const void* Vn, const float* cocktail,
+                        const float* bank_cocktail, const float* key_bias, const float* admission,
+                        const float* scale, const int64_t* idx, const uint8_t* valid, int mode,
+                        const float* const* gains, void* out, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+/* Backward: gout [B,T,H] -> gq, gK, gV, gVn (dtype), gcocktail [B,T,4], gbank_cocktail
+ * [B,N,4], gkey_bias, gadmission [B,N] (fp32) and gscalars5 = (scale, short_gain,
+ * pad_gain, induct_gain, cocktail_gain). */
+int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* gout,
+                        const void* q, const void* K, const void* V, const void* Vn,
+                        const float* cocktail, const float* bank_cocktail, const float* key_bias,
+                        const float* admission, const float* scale, const int64_t* idx,
+                        const uint8_t* valid, int mode, const float* const* gains, void* gq,
+                        void* gK, void* gV, void* gVn, float* gcocktail, float* gbank_cocktail,
+                        float* gkey_bias, float* gadmission, float* gscalars5, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DABSN_HIP_H_ */

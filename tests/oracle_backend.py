@@ -1,0 +1,192 @@
+"""Test-only CPU kernels for the ``dabsn::`` operators, backed by the CPU oracle.
+
+Registering these lets the product's module code (DABSNCore/DABSNRead/DABSNBlock) run on
+CPU tensors through the oracle, so a whole block can be compared HIP-vs-oracle end to
+end. The product package never registers CPU kernels; only tests import this module.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+import oracle
+from dabsn_amd.kernels import ops
+
+_DONE = False
+
+
+def _np(x):
+    return x.detach().float().cpu().numpy()
+
+
+def _t(a, like_dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(like_dtype)
+
+
+def _core_fwd(*inputs):
+    Wx, Wgx, Ug, A = inputs[:4]
+    vec = inputs[4:20]
+    la, ll, ls = inputs[20:23]
+    b0, e0, c0 = inputs[23:26]
+    out = oracle.core_scan_fwd(_np(Wx), _np(Wgx), _np(torch.cat([Ug, A], 0)),
+                               [_np(v) for v in vec], float(la), float(ll), float(ls),
+                               _np(b0), _np(e0), _np(c0))
+    dt = Wx.dtype
+    res = [_t(o, dt) for o in out[:8]]
+    res += [_t(o, s.dtype) for o, s in zip(out[8:], (b0, e0, c0))]
+    return tuple(res)
+
+
+def _core_bwd(Ug, A, vecs, la, ll, ls, ib, ic, U, plasticity, expression, energy, saturation,
+              gate, gU, gn, gp, ga, gw, ge, gc, gbF, geF, gcF):
+    saved = tuple(_np(x) for x in (U, plasticity, expression, energy, saturation, gate))
+    grads = [None if g is None else _np(g) for g in (gU, gn, gp, ga, gw, ge, gc, gbF, geF, gcF)]
+    gWx, gWgx, gGA, gvec, gscal, gb0, ge0, gc0 = oracle.core_scan_bwd(
+        _np(torch.cat([Ug, A], 0)), [_np(v) for v in vecs], float(la), float(ll), float(ls),
+        _np(ib), _np(ic), saved, grads)
+    H = Ug.shape[0]
+    dt = plasticity.dtype
+    return [_t(gWx, dt), _t(gWgx, dt), _t(gGA[:H]), _t(gGA[H:]),
+            *[_t(gvec[i].copy()) for i in range(16)], *[_t(np.array(gscal[i])) for i in range(3)],
+            _t(gb0), _t(ge0), _t(gc0)]
+
+
+def _linrec(a, g, y0):
+    return _t(oracle.linrec_fwd(_np(a), _np(g), _np(y0)), a.dtype)
+
+
+def _linrec_bwd(a, g, y0, gy):
+    da, dg, dy = oracle.linrec_bwd(_np(a), _np(g), _np(y0), _np(gy))
+    return [_t(da, a.dtype), _t(dg, g.dtype), _t(dy, y0.dtype)]
+
+
+def _coef(l1, l2, l3, l4):
+    return np.array([float(torch.sigmoid(x.float()).reshape(())) for x in (l1, l2, l3, l4)],
+                    np.float32)
+
+
+def _long(write, plasticity, l1, l2, l3, l4, L0, E0, R0):
+    out, (LF, EF, RF) = oracle.long_fwd(_np(write), _np(plasticity), _coef(l1, l2, l3, l4),
+                                        _np(L0), _np(E0), _np(R0))
+    B, T, H = write.shape
+    ckpt = torch.zeros((B, (T + 31) // 32, 3, H))
+    ckpt[:, 0, 0] = L0.float()
+    ckpt[:, 0, 1] = E0.float()
+    ckpt[:, 0, 2] = R0.float()
+    return _t(out, write.dtype), _t(LF), _t(EF), _t(RF), ckpt
+
+
+def _long_bwd(write, plasticity, logits, ckpt, grad_long, gLF, gEF, gRF):
+    coef = _coef(*logits)
+    L0, E0, R0 = (_np(ckpt[:, 0, k]) for k in range(3))
+    gw, gp, (gL0, gE0, gR0), gcoef = oracle.long_bwd(
+        _np(write), _np(plasticity), coef, L0, E0, R0, _np(grad_long),
+        [None if g is None else _np(g) for g in (gLF, gEF, gRF)])
+    glog = gcoef * coef * (1.0 - coef)
+    return [_t(gw, write.dtype), _t(gp, plasticity.dtype),
+            *[_t(np.array(glog[i])) for i in range(4)], _t(gL0), _t(gE0), _t(gR0)]
+
+
+_STATS_GAINS = (1.0, 0.5, -2.0, 1.0, 0.5, 0.5, 0.25, -2.0)
+
+
+def _stats(nov, pl, en, sat, ay, wr):
+    st = oracle.tape_stats(_np(nov), _np(pl), _np(en), _np(sat), _np(ay), _np(wr), _STATS_GAINS)
+    out = np.concatenate([st["means"], st["norm_ay"][..., None], st["norm_w"][..., None]], -1)
+    return _t(out)
+
+
+def _stats_bwd(gstats, like):
+    H = like.shape[-1]
+    g = gstats.float() / H
+    return [g[..., k:k + 1].expand(like.shape).to(like.dtype).contiguous() for k in (2, 3, 0, 1)]
+
+
+def _normalize(x, norms):
+    return (x.float() / norms.float().clamp_min(1e-12).unsqueeze(-1)).to(x.dtype)
+
+
+def _normalize_bwd(q, norms, gq):
+    # restate via fp64 autograd of F.normalize on x = q * |x|
+    x = (q.double() * norms.double().unsqueeze(-1)).requires_grad_(True)
+    y = F.normalize(x, dim=-1)
+    (gx,) = torch.autograd.grad(y, x, gq.double())
+    return gx.to(q.dtype)
+
+
+def _select(adm, window):
+    order, counts = oracle.bank_select(_np(adm), float(window.reshape(())))
+    rank = np.empty_like(order, dtype=np.int32)
+    rows = np.arange(order.shape[0])[:, None]
+    rank[rows, order] = np.arange(order.shape[1], dtype=np.int32)[None, :]
+    return torch.from_numpy(order), torch.from_numpy(counts), torch.from_numpy(rank)
+
+
+def _gather(write, norm_w, idx, next_idx, rank):
+    H = write.shape[-1]
+    V = torch.gather(write, 1, idx.unsqueeze(-1).expand(-1, -1, H))
+    n = torch.gather(norm_w.float(), 1, idx).clamp_min(1e-12).unsqueeze(-1)
+    K = (V.float() / n).to(write.dtype)
+    Vn = torch.gather(write, 1, next_idx.unsqueeze(-1).expand(-1, -1, H))
+    return K, V.clone(), Vn
+
+
+def _gather_bwd(write, norm_w, rank, K, gK, gV, gVn):
+    B, T, H = write.shape
+    N = K.shape[1]
+    order = torch.argsort(rank.long(), dim=1)
+    idx = order[:, :N]
+    next_idx = (idx + 1).clamp(max=T - 1)
+    w = write.double().requires_grad_(True)
+    V = torch.gather(w, 1, idx.unsqueeze(-1).expand(-1, -1, H))
+    Kx = F.normalize(V, dim=-1)
+    Vn = torch.gather(w, 1, next_idx.unsqueeze(-1).expand(-1, -1, H))
+    loss = (Kx * gK.double()).sum() + (V * gV.double()).sum() + (Vn * gVn.double()).sum()
+    (gw,) = torch.autograd.grad(loss, w)
+    return gw.to(write.dtype)
+
+
+def _read_args(query, K, V, Vn, ck, cb, kb, adm, scale, idx, valid, mode, sg, pg, ig, cg):
+    return (_np(query), _np(K), _np(V), _np(Vn), _np(ck), _np(cb), _np(kb), _np(adm),
+            float(scale.reshape(())), idx.cpu().numpy(), valid.cpu().numpy(), int(mode),
+            [float(x.reshape(())) for x in (sg, pg, ig, cg)])
+
+
+def _read(query, K, V, Vn, ck, cb, kb, adm, scale, idx, valid, mode, sg, pg, ig, cg):
+    a = _read_args(query, K, V, Vn, ck, cb, kb, adm, scale, idx, valid, mode, sg, pg, ig, cg)
+    return _t(oracle.read3_fwd(*a), query.dtype)
+
+
+def _read_bwd(go, query, K, V, Vn, ck, cb, kb, adm, scale, idx, valid, mode, sg, pg, ig, cg):
+    a = _read_args(query, K, V, Vn, ck, cb, kb, adm, scale, idx, valid, mode, sg, pg, ig, cg)
+    g = oracle.read3_bwd(_np(go), *a)
+    like = (query, K, V, Vn, ck, cb, kb, adm, scale, sg, pg, ig, cg)
+    out = []
+    for val, ref in zip(g, like):
+        out.append(_t(np.array(val, dtype=np.float32)).reshape(ref.shape).to(ref.dtype))
+    return tuple(out)
+
+
+def register() -> None:
+    """Attach the oracle as the CPU kernel of every dabsn:: operator (idempotent)."""
+    global _DONE
+    if _DONE:
+        return
+    ops.core_scan_batched.register_kernel("cpu")(_core_fwd)
+    ops.core_scan_batched_backward.register_kernel("cpu")(_core_bwd)
+    ops.linear_recurrence.register_kernel("cpu")(_linrec)
+    ops.linrec_backward.register_kernel("cpu")(_linrec_bwd)
+    ops.long_scan_fused.register_kernel("cpu")(_long)
+    ops.long_scan_fused_backward.register_kernel("cpu")(_long_bwd)
+    ops.read_tape_stats.register_kernel("cpu")(_stats)
+    ops.read_tape_stats_backward.register_kernel("cpu")(_stats_bwd)
+    ops.normalize_rows.register_kernel("cpu")(_normalize)
+    ops.normalize_rows_backward.register_kernel("cpu")(_normalize_bwd)
+    ops.bank_select.register_kernel("cpu")(_select)
+    ops.bank_gather.register_kernel("cpu")(_gather)
+    ops.bank_gather_backward.register_kernel("cpu")(_gather_bwd)
+    ops.admitted_three_way_read_compact_flash.register_kernel("cpu")(_read)
+    ops.admitted_three_way_read_compact_flash_backward.register_kernel("cpu")(_read_bwd)
+    _DONE = True
