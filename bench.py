@@ -1,0 +1,247 @@
+"""Benchmark: DABSN scan+read forward+backward on one MI355X.
+
+Workload ("config 4"): one seq DABSN layer, state width 2048,
+read/hidden width 4096, vocabulary 32,000, batch 16, T = 4096, bf16, block chunking
+enabled (chunk 1024, checkpointed: each chunk's forward scan is recomputed in the
+backward). One step = forward + backward of the scan+read region: the chunked core scan
+(op dabsn::core_scan_batched), read statistics, admitted-slot selection, bank gather,
+three-way read, read output projection and the long-memory scan, from input projections
+Wx = W x, Wgx = Wg x that are already resident in HBM (the input projections are plain
+GEMMs timed separately, as the metric excludes them). Synthetic data: random token ids
+through a random embedding, random-initialised weights.
+
+Prints one JSON line (see the repository's benchmark contract).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "scan+read tokens/sec (B×T) fwd+bwd, state 2048 T=4096 bf16; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--batch", type=int, default=16)
+    p.add_argument("--seq", type=int, default=4096)
+    p.add_argument("--state", type=int, default=2048)
+    p.add_argument("--hidden", type=int, default=4096)
+    p.add_argument("--vocab", type=int, default=32000)
+    p.add_argument("--chunk", type=int, default=1024)
+    p.add_argument("--cpu-seq", type=int, default=128, help="T of the bounded CPU sample")
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+class ScanRead(torch.nn.Module):
+    """The scan+read region of one seq block (core + read), driven from Wx/Wgx."""
+
+    def __init__(self, hidden: int, state: int, chunk: int):
+        super().__init__()
+        from dabsn_amd import DABSNCore, DABSNRead
+
+        self.core = DABSNCore(hidden, state)
+        self.read = DABSNRead(state)
+        self.state = state
+        self.chunk = chunk
+
+    def scan(self, Wx, Wgx):
+        from torch.utils.checkpoint import checkpoint
+
+        from dabsn_amd.kernels.ops import core_scan_batched
+
+        B, T, H = Wx.shape
+        zeros = torch.zeros(B, H, device=Wx.device, dtype=torch.float32)
+        carry = (zeros, torch.ones_like(zeros), zeros.clone())
+        params = self.core.scan_inputs()
+        tapes = [[] for _ in range(7)]
+
+        def run(wx, wgx, b, e, c):
+            out = core_scan_batched(wx, wgx, *params, b, e, c)
+            return (*out[:7], *out[8:11])
+
+        chunk = self.chunk if 0 < self.chunk < T else T
+        for t0 in range(0, T, chunk):
+            sl = slice(t0, min(T, t0 + chunk))
+            if chunk < T and torch.is_grad_enabled():
+                outs = checkpoint(run, Wx[:, sl], Wgx[:, sl], *carry, use_reentrant=False)
+            else:
+                outs = run(Wx[:, sl], Wgx[:, sl], *carry)
+            for i in range(7):
+                tapes[i].append(outs[i])
+            carry = outs[7:10]
+        return [torch.cat(p, 1) if len(p) > 1 else p[0] for p in tapes]
+
+    def forward(self, Wx, Wgx):
+        U, nov, p, ay, w, e, c = self.scan(Wx, Wgx)
+        y, budget = U.split(self.state, dim=-1)
+        return y, self.read(y, budget, ay, w, nov, p, e, c)
+
+
+def build_workload(args, device, dtype, batch, seq):
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, args.vocab, (batch, seq), generator=g)
+    torch.manual_seed(0)
+    model = ScanRead(args.hidden, args.state, args.chunk).to(device)
+    embed = (torch.randn(args.vocab, args.hidden, generator=g) * 0.02).to(dtype)
+    x = embed[ids].to(device)
+    with torch.no_grad():
+        Wx = torch.nn.functional.linear(x, model.core.W.weight.to(dtype))
+        Wgx = torch.nn.functional.linear(x, model.core.Wg.weight.to(dtype), model.core.Wg.bias.to(dtype))
+    Wx = Wx.detach().requires_grad_(True)
+    Wgx = Wgx.detach().requires_grad_(True)
+    gy = (torch.randn(batch, seq, args.state, generator=g) * 1e-3).to(device=device, dtype=dtype)
+    gr = (torch.randn(batch, seq, args.state, generator=g) * 1e-3).to(device=device, dtype=dtype)
+    return model, Wx, Wgx, gy, gr
+
+
+def step(model, Wx, Wgx, gy, gr, device_type, dtype):
+    model.zero_grad(set_to_none=True)
+    Wx.grad = None
+    Wgx.grad = None
+    with torch.autocast(device_type, dtype=dtype, enabled=dtype != torch.float32):
+        y, read = model(Wx, Wgx)
+    torch.autograd.backward([y, read.to(dtype)], [gy, gr])
+
+
+def cpu_baseline(args):
+    """The oracle (C restatement of the reference CPU backend, fp32, OpenMP over batch)
+    running the same scan+read step on a bounded sample: config-4 widths, T=cpu_seq."""
+    import oracle
+    from oracle import torch_backend
+
+    oracle.build()
+    torch_backend.register()
+    threads = int(os.environ.get("OMP_NUM_THREADS", min(16, os.cpu_count() or 1)))
+    oracle.set_num_threads(threads)
+    torch.set_num_threads(threads)
+    seq = int(args.cpu_seq)
+    model, Wx, Wgx, gy, gr = build_workload(args, torch.device("cpu"), torch.float32, args.batch, seq)
+    t0 = time.perf_counter()
+    step(model, Wx, Wgx, gy, gr, "cpu", torch.float32)
+    dt = time.perf_counter() - t0
+    tokens = args.batch * seq
+    return {
+        "value": tokens / dt,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle C/OpenMP fp32 (restates reference cpu_runtime.cpp + registered reverse scan), "
+                   f"one fwd+bwd step at B={args.batch}, T={seq}, H={args.state}, D={args.hidden}, "
+                   f"n_max={model.read.last_n_max}; {dt:.2f} s wall; T-truncated proxy of the "
+                   f"T={args.seq} workload (scan cost scales with T, read with T*n_max)"),
+        "seconds": dt,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested).", file=sys.stderr)
+        sys.exit(2)
+    import dabsn_amd
+    from dabsn_amd.kernels import ops
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    dabsn_amd.kernels.enable("rocm", required=True)
+    os.environ.setdefault("DABSN_HIP_ERROR_CHECK", "deferred")
+    device = torch.device("cuda:0")
+    dtype = torch.bfloat16
+    model, Wx, Wgx, gy, gr = build_workload(args, device, dtype, args.batch, args.seq)
+    for _ in range(args.warmup):
+        step(model, Wx, Wgx, gy, gr, "cuda", dtype)
+    torch.cuda.synchronize()
+    ops.timing(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        step(model, Wx, Wgx, gy, gr, "cuda", dtype)
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    kernels = ops.KernelTimer.summary()
+    ops.timing(False)
+    ops.check_errors()
+    tokens = args.batch * args.seq
+    value = tokens / (ms / 1e3)
+
+    # Dominant kernel and its roofline (algorithmic bytes per launch / measured duration).
+    dom = max(kernels, key=lambda k: kernels[k]["total_ms"])
+    H = args.state
+    el = 2  # bf16
+    n_max = int(model.read.last_n_max or 0)
+    chunk = args.chunk if 0 < args.chunk < args.seq else args.seq
+    per_token = {
+        # reads U (2H), plasticity, expression, energy, saturation, gate (5H), grads of
+        # U (2H) and of 6 [B,T,H] outputs (6H); writes gWx, gWgx, d_expression (3H)
+        "core_scan_bwd": 18 * H * el,
+        # reads Wx, Wgx (2H); writes U (2H) + 7 tapes (7H)
+        "core_scan_fwd": 11 * H * el,
+    }
+    weights_bytes = 2 * H * H * el
+    if dom in per_token:
+        launch_tokens = args.batch * chunk
+        alg_bytes = per_token[dom] * launch_tokens + weights_bytes
+        achieved = alg_bytes / (kernels[dom]["avg_ms"] / 1e3) / 1e9
+        roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 2),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                    "traffic": None, "alg_bytes_per_launch": alg_bytes,
+                    "avg_launch_ms": round(kernels[dom]["avg_ms"], 4),
+                    "launch_tokens": launch_tokens}
+    else:
+        roofline = {"bound": "mfma", "kernel": dom, "achieved": None, "peak": 2500.0,
+                    "unit": "TFLOP/s", "frac": None, "traffic": None}
+    # Whole-step fraction of the HBM roofline on the algorithmic bytes of the step.
+    step_bytes = (55 + 18 * (n_max / args.seq)) * H * el * tokens + 3 * weights_bytes
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: uniform random token ids, random embedding, random-init weights",
+        "config": {"workload": "config4 scan+read fwd+bwd: one seq layer, state 2048, read/hidden 4096, "
+                               "vocab 32000, block chunking 1024 (checkpoint recompute)",
+                   "batch": args.batch, "seq_len": args.seq, "state": H, "hidden": args.hidden,
+                   "chunk_t": chunk, "n_max": n_max},
+        "roofline": roofline,
+        "step_hbm_roofline_frac": round(step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 5),
+        "kernel_ms": {k: {"avg": round(v["avg_ms"], 4), "calls_per_step": v["calls"] / args.steps,
+                          "per_step": round(v["total_ms"] / args.steps, 3)}
+                      for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["total_ms"])},
+    }
+    if not args.no_cpu:
+        try:
+            result["cpu_baseline"] = cpu_baseline(args)
+        except Exception as exc:  # noqa: BLE001 - reported, the GPU figure stands
+            result["cpu_baseline"] = {"error": f"{type(exc).__name__}: {exc}"}
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

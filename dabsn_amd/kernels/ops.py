@@ -80,6 +80,49 @@ def check_errors() -> None:
             raise RuntimeError(f"DABSN HIP persistent scan on cuda:{dev} reported error word {value}")
 
 
+class KernelTimer:
+    """Optional per-operator device timing: HIP events recorded on the launch stream
+    around each library call (enabled by ``timing(True)``; used by the benchmark)."""
+
+    enabled = False
+    records: list = []
+
+    @classmethod
+    def begin(cls, name: str, t: Tensor):
+        if not cls.enabled:
+            return None
+        stream = torch.cuda.current_stream(t.device)
+        start = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        return (name, start, stream)
+
+    @classmethod
+    def end(cls, token) -> None:
+        if token is None:
+            return
+        name, start, stream = token
+        stop = torch.cuda.Event(enable_timing=True)
+        stop.record(stream)
+        cls.records.append((name, start, stop))
+
+    @classmethod
+    def summary(cls) -> dict[str, dict[str, float]]:
+        torch.cuda.synchronize()
+        out: dict[str, dict[str, float]] = {}
+        for name, start, stop in cls.records:
+            d = out.setdefault(name, {"calls": 0, "total_ms": 0.0})
+            d["calls"] += 1
+            d["total_ms"] += start.elapsed_time(stop)
+        for d in out.values():
+            d["avg_ms"] = d["total_ms"] / max(d["calls"], 1)
+        return out
+
+
+def timing(enabled: bool) -> None:
+    KernelTimer.enabled = bool(enabled)
+    KernelTimer.records = []
+
+
 def _require_cuda(*tensors: Tensor) -> None:
     for t in tensors:
         if t is not None and t.device.type != "cuda":
@@ -141,10 +184,12 @@ def core_scan_batched(
     if nbytes == 0:
         raise RuntimeError(f"DABSN HIP core scan does not support H={H} for {dt}")
     ws = torch.empty(nbytes, dtype=torch.uint8, device=Wx.device)
+    tk = KernelTimer.begin("core_scan_fwd", Wx)
     rc = lib.dabsn_hip_core_scan_fwd(
         code, B, T, H, _p(Wx_c), _p(Wgx_c), _p(GA), ctypes.byref(params),
         _p(b0), _p(e0), _p(c0), _p(U), *[_p(t) for t in tapes], *[_p(f) for f in finals],
         _p(ws), nbytes, _stream(Wx))
+    KernelTimer.end(tk)
     _lib.check(rc, "core scan forward")
     _record_error_word(ws, "core scan forward")
     del keep
@@ -209,19 +254,23 @@ def core_scan_batched_backward(
     gb0, ge0, gc0 = (torch.empty((B, H), device=U.device, dtype=torch.float32) for _ in range(3))
     nbytes = lib.dabsn_hip_core_scan_workspace_bytes(code, B, H, 1)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=U.device)
+    tk = KernelTimer.begin("core_scan_bwd", U)
     rc = lib.dabsn_hip_core_scan_bwd(
         code, B, T, H, _p(GAT), ctypes.byref(params), _p(b0), _p(c0), *[_p(x) for x in saved],
         *[_p(g) for g in grads], *[_p(g) for g in gfin], _p(gWx), _p(gWgx), _p(day),
         _p(part_vec), _p(part_scal), _p(gb0), _p(ge0), _p(gc0), _p(ws), nbytes, _stream(U))
+    KernelTimer.end(tk)
     _lib.check(rc, "core scan backward")
     _record_error_word(ws, "core scan backward")
     del keep
     gvec = part_vec.sum(0)
     gscal = part_scal.sum(0)
     # grad [Ug; A] = [gWgx; day]^T y: one plain GEMM per half (hipBLASLt through torch).
+    tk = KernelTimer.begin("core_weight_grad_gemm", U)
     y = U[..., :H].to(dt).reshape(B * T, H)
     gUg = (gWgx.reshape(B * T, H).t() @ y).float()
     gA = (day.reshape(B * T, H).t() @ y).float()
+    KernelTimer.end(tk)
     # operator outputs must not alias each other: split into separate tensors
     return [gWx, gWgx, gUg, gA, *[gvec[i].clone() for i in range(16)],
             *[gscal[i].clone() for i in range(3)], gb0, ge0, gc0]
@@ -351,9 +400,11 @@ def long_scan_fused(
     LF, EF, RF = (torch.empty((B, H), device=w.device, dtype=torch.float32) for _ in range(3))
     nseg = (T + 31) // 32
     ckpt = torch.empty((B, nseg, 3, H), device=w.device, dtype=torch.float32)
+    tk = KernelTimer.begin("long_scan_fwd", w)
     _lib.check(lib.dabsn_hip_long_fwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(L0), _p(E0),
                                       _p(R0), _p(out), _p(LF), _p(EF), _p(RF), _p(ckpt),
                                       _stream(w)), "long scan")
+    KernelTimer.end(tk)
     return out, LF, EF, RF, ckpt
 
 
@@ -387,9 +438,11 @@ def long_scan_fused_backward(
     g0 = [torch.empty((B, H), device=w.device, dtype=torch.float32) for _ in range(3)]
     nparts = lib.dabsn_hip_long_partials(B, H)
     part = torch.empty((nparts, 4), device=w.device, dtype=torch.float32)
+    tk = KernelTimer.begin("long_scan_bwd", w)
     _lib.check(lib.dabsn_hip_long_bwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(ckpt), _p(gout),
                                       *[_p(x) for x in gf], _p(gw), _p(gp), *[_p(x) for x in g0],
                                       _p(part), _stream(w)), "long scan backward")
+    KernelTimer.end(tk)
     glog = part.sum(0)
     return [gw, gp.to(plasticity.dtype), *[glog[i].clone() for i in range(4)], *g0]
 
@@ -658,10 +711,12 @@ def admitted_three_way_read_compact_flash(
     nbytes = lib.dabsn_hip_read3_workspace_bytes(code, B, T, N, H, 0)
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
     ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
+    tk = KernelTimer.begin("read3_fwd", q)
     _lib.check(lib.dabsn_hip_read3_fwd(code, B, T, N, H, _p(q), _p(K), _p(V), _p(Vn), _p(ck),
                                        _p(cb), _p(kb), _p(adm), _p(sc), _p(idx), _p(valid), mode,
                                        ptrs, _p(out), _p(ws), ws.numel(), _stream(q)),
                "three-way read")
+    KernelTimer.end(tk)
     return out
 
 
@@ -705,11 +760,13 @@ def admitted_three_way_read_compact_flash_backward(
     nbytes = lib.dabsn_hip_read3_workspace_bytes(code, B, T, N, H, 1)
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
     ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
+    tk = KernelTimer.begin("read3_bwd", q)
     _lib.check(lib.dabsn_hip_read3_bwd(code, B, T, N, H, _p(go), _p(q), _p(K), _p(V), _p(Vn),
                                        _p(ck), _p(cb), _p(kb), _p(adm), _p(sc), _p(idx),
                                        _p(valid), mode, ptrs, _p(gq), _p(gK), _p(gV), _p(gVn),
                                        _p(gck), _p(gcb), _p(gkb), _p(gadm), _p(g5), _p(ws),
                                        ws.numel(), _stream(q)), "three-way read backward")
+    KernelTimer.end(tk)
     return (gq, gK.to(bank_keys.dtype), gV.to(bank_writes.dtype), gVn.to(next_writes.dtype),
             gck.to(cocktail.dtype), gcb.to(bank_cocktail.dtype), gkb.to(bank_key_bias.dtype),
             gadm.to(bank_admission.dtype),

@@ -1,8 +1,9 @@
-"""Test-only CPU kernels for the ``dabsn::`` operators, backed by the CPU oracle.
+"""CPU kernels for the ``dabsn::`` operators backed by the CPU oracle -- TEST INFRASTRUCTURE ONLY.
 
 Registering these lets the product's module code (DABSNCore/DABSNRead/DABSNBlock) run on
 CPU tensors through the oracle, so a whole block can be compared HIP-vs-oracle end to
-end. The product package never registers CPU kernels; only tests import this module.
+end. The product package never registers CPU kernels; only tests/, smoke() and the
+benchmark's cpu_baseline leg import this module.
 """
 
 from __future__ import annotations
@@ -108,12 +109,16 @@ def _normalize(x, norms):
     return (x.float() / norms.float().clamp_min(1e-12).unsqueeze(-1)).to(x.dtype)
 
 
+def _normalize_grad(q, n, gq):
+    """Gradient of x / max(|x|, eps) (F.normalize): (gq - q (q.gq)) / |x| above eps."""
+    q64, g64 = q.astype(np.float64), gq.astype(np.float64)
+    n = n.astype(np.float64)[..., None]
+    dot = (q64 * g64).sum(-1, keepdims=True)
+    return np.where(n > 1e-12, (g64 - q64 * dot) / np.maximum(n, 1e-12), g64 / 1e-12)
+
+
 def _normalize_bwd(q, norms, gq):
-    # restate via fp64 autograd of F.normalize on x = q * |x|
-    x = (q.double() * norms.double().unsqueeze(-1)).requires_grad_(True)
-    y = F.normalize(x, dim=-1)
-    (gx,) = torch.autograd.grad(y, x, gq.double())
-    return gx.to(q.dtype)
+    return _t(_normalize_grad(_np(q), _np(norms), _np(gq)).astype(np.float32), q.dtype)
 
 
 def _select(adm, window):
@@ -136,16 +141,17 @@ def _gather(write, norm_w, idx, next_idx, rank):
 def _gather_bwd(write, norm_w, rank, K, gK, gV, gVn):
     B, T, H = write.shape
     N = K.shape[1]
-    order = torch.argsort(rank.long(), dim=1)
+    order = np.argsort(rank.cpu().numpy().astype(np.int64), axis=1)
     idx = order[:, :N]
-    next_idx = (idx + 1).clamp(max=T - 1)
-    w = write.double().requires_grad_(True)
-    V = torch.gather(w, 1, idx.unsqueeze(-1).expand(-1, -1, H))
-    Kx = F.normalize(V, dim=-1)
-    Vn = torch.gather(w, 1, next_idx.unsqueeze(-1).expand(-1, -1, H))
-    loss = (Kx * gK.double()).sum() + (V * gV.double()).sum() + (Vn * gVn.double()).sum()
-    (gw,) = torch.autograd.grad(loss, w)
-    return gw.to(write.dtype)
+    next_idx = np.minimum(idx + 1, T - 1)
+    nrm = np.take_along_axis(_np(norm_w), idx, 1)
+    Kn = _np(K).astype(np.float64)
+    gKV = _normalize_grad(Kn, nrm, _np(gK)) + _np(gV)
+    gw = np.zeros((B, T, H), np.float64)
+    rows = np.arange(B)[:, None]
+    np.add.at(gw, (rows, idx), gKV)
+    np.add.at(gw, (rows, next_idx), _np(gVn).astype(np.float64))
+    return _t(gw.astype(np.float32), write.dtype)
 
 
 def _read_args(query, K, V, Vn, ck, cb, kb, adm, scale, idx, valid, mode, sg, pg, ig, cg):
