@@ -14,10 +14,15 @@
 //     counter use device-coherent (sc1) accesses so no L2 writeback/invalidate is
 //     needed between XCDs.
 //   * The recurrent product runs on v_mfma_f32_16x16x32_bf16 (bf16) or
-//     v_mfma_f32_16x16x4_f32 (fp32) with K split across the 4 waves; partial tiles
+//     v_mfma_f32_16x16x4_f32 (fp32) with K split across the NW waves; partial tiles
 //     are reduced through LDS in a fixed order (deterministic).
 //   * State (b, e, c) and the per-unit parameters live in registers of the thread that
 //     owns a (unit, batch row) pair; tapes are written once per step.
+//   * Only what the next exchange needs sits between two barriers: the forward
+//     publishes y_{t+1} before it updates energy/cortisol and writes tapes, and the
+//     backward prefetches its tapes two steps ahead and evaluates each reverse step as
+//     base + X * slope, where X (the tanh pre-activation grad, the one quantity that
+//     waits for the exchange) enters every output affinely through the budget grad.
 //   * Barrier waits are bounded: a wait that exceeds kSpinLimit polls sets the error
 //     word and every workgroup exits.
 #include "../../include/dabsn_hip.h"
@@ -27,9 +32,7 @@
 namespace dabsn {
 namespace core {
 
-constexpr int NW = 4;         // waves per workgroup
-constexpr int NT = NW * 64;   // threads per workgroup
-constexpr int NB = 16;        // batch rows per group (MFMA N)
+constexpr int NB = 16;  // batch rows per group (MFMA N)
 
 template <typename E>
 struct Mf;
@@ -134,7 +137,7 @@ __device__ __forceinline__ void drain_vmem() { __builtin_amdgcn_s_waitcnt(0); }
 // Publishes `nvals` values per (unit, batch) pair into slot `xs` of the exchange
 // buffer at k = kbase[i] + cl. bf16 stages through LDS so each lane stores one 16-byte
 // unit (8 consecutive k for one batch column); fp32 stores one word per value.
-template <typename E, int CH, int NV>
+template <typename E, int CH, int NV, int NT>
 __device__ __forceinline__ void publish(__amdgpu_buffer_rsrc_t xr, uint32_t slot_bytes, int xs,
                                         const int (&kbase)[NV], const float (&vals)[NV],
                                         bool is_pair, int cl, int bl, bf16 (*stage)[NB][CH]) {
@@ -229,9 +232,10 @@ __device__ __forceinline__ void tile_of(int nct, int& ct, int& bg) {
   ct = (nct % 8 == 0) ? (i % 8) * (nct / 8) + i / 8 : i;
 }
 
-template <typename E, int CH, int KSTEPS>
-__global__ void __launch_bounds__(NT, 1) core_fwd_kernel(FwdArgs<E> a) {
+template <typename E, int CH, int KSTEPS, int NW>
+__global__ void __launch_bounds__(NW * 64, 1) core_fwd_kernel(FwdArgs<E> a) {
   using M = Mf<E>;
+  constexpr int NT = NW * 64;
   constexpr int KSTEP = M::KSTEP;
   constexpr int KW = KSTEPS * KSTEP;
   constexpr int ROWS = 2 * CH;
@@ -297,7 +301,7 @@ __global__ void __launch_bounds__(NT, 1) core_fwd_kernel(FwdArgs<E> a) {
   const int kb_y[1] = {ct * CH};
   if (T > 0) {
     const float v[1] = {ycur};
-    publish<E, CH, 1>(xr, a.slot_bytes, 0, kb_y, v, is_pair, cl, bl, stage);
+    publish<E, CH, 1, NT>(xr, a.slot_bytes, 0, kb_y, v, is_pair, cl, bl, stage);
     if (tid == 0) arrive(counter);
   }
 
@@ -331,7 +335,8 @@ __global__ void __launch_bounds__(NT, 1) core_fwd_kernel(FwdArgs<E> a) {
     }
     __syncthreads();
 
-    float ynext = 0.0f, bn = 0.f, en = 0.f, cpost = 0.f, nov = 0.f, p = 0.f, s_g = 0.f, ay = 0.f;
+    // Critical path: the budget update and y_{t+1}.
+    float ynext = 0.0f, bn = 0.f, s_g = 0.f, ay = 0.f, p = 0.f;
     if (is_pair) {
       float ug = 0.0f;
       const int ra = CH + cl;
@@ -344,6 +349,18 @@ __global__ void __launch_bounds__(NT, 1) core_fwd_kernel(FwdArgs<E> a) {
       ug = round_to<E>(ug);
       ay = round_to<E>(ay);
       s_g = hardsigmoidf_(wgx + ug);
+      p = s_g * se;
+      bn = (1.0f - gate_alpha) * sb + up.beta + lam * (p * ay);
+      if (act && t + 1 < T) ynext = tanhf(wxn + bn);
+    }
+    if (t + 1 < T) {
+      const float v[1] = {ynext};
+      publish<E, CH, 1, NT>(xr, a.slot_bytes, (t + 1) & 1, kb_y, v, is_pair, cl, bl, stage);
+      if (tid == 0) arrive(counter);
+    }
+    // Off the critical path (overlaps the next barrier): energy and cortisol, tapes.
+    float en = 0.f, cpost = 0.f, nov = 0.f;
+    if (is_pair) {
       nov = tanhf(fabsf(ay - sb));
       const float stress = nov * (1.0f - se);
       cpost = up.decay * sc + (1.0f - up.decay) * stress;
@@ -355,15 +372,7 @@ __global__ void __launch_bounds__(NT, 1) core_fwd_kernel(FwdArgs<E> a) {
       r_sig += up.rc * cpost;
       const float k_t = up.kappa * expf(0.5f * tanhf(k_sig));
       const float r_t = clamp01(up.recover * expf(0.5f * tanhf(r_sig)));
-      p = s_g * se;
-      bn = (1.0f - gate_alpha) * sb + up.beta + lam * (p * ay);
       en = clamp01(se + r_t * (1.0f - se) - k_t * p);
-      if (act && t + 1 < T) ynext = tanhf(wxn + bn);
-    }
-    if (t + 1 < T) {
-      const float v[1] = {ynext};
-      publish<E, CH, 1>(xr, a.slot_bytes, (t + 1) & 1, kb_y, v, is_pair, cl, bl, stage);
-      if (tid == 0) arrive(counter);
     }
     if (act) {
       const size_t ru = (row0 + t) * 2 * H + c;
@@ -428,16 +437,180 @@ struct BwdArgs {
   uint32_t slot_bytes;
 };
 
-template <typename E, int CH, int KSTEPS>
-__global__ void __launch_bounds__(NT, 1) core_bwd_kernel(BwdArgs<E> a) {
+// Raw tape words of one time index, kept unconverted so the loads stay in flight across
+// the step barrier (bf16: the 16 storage bits; fp32: the float bits).
+struct TapeRaw {
+  uint32_t y, b_prev, e_prev, c_prev, gate, p, ay, c_t;
+  uint32_t gy0, gub, gc, gnov, gp, gay, gw, ge;
+};
+
+template <typename E>
+__device__ __forceinline__ uint32_t ldraw(const E* p, size_t i) {
+  if constexpr (is_bf16<E>::value) {
+    return static_cast<uint32_t>(p[i]);
+  } else {
+    return __builtin_bit_cast(uint32_t, p[i]);
+  }
+}
+
+template <typename E>
+__device__ __forceinline__ float cvt(uint32_t w) {
+  if constexpr (is_bf16<E>::value) {
+    return __builtin_bit_cast(float, w << 16);
+  } else {
+    return __builtin_bit_cast(float, w);
+  }
+}
+
+// Issue the loads of time index t (tapes and upstream grads; absent grads read as 0).
+template <typename E>
+__device__ __forceinline__ void load_tape(const BwdArgs<E>& a, size_t row0, int c, int t,
+                                          TapeRaw& r) {
+  const size_t H = static_cast<size_t>(a.H);
+  const size_t rt = (row0 + t) * H + c;
+  const size_t ru = (row0 + t) * 2 * H + c;
+  r.y = ldraw(a.U, ru);
+  r.b_prev = t > 0 ? ldraw(a.U, ru - H) : 0u;  // budget half of U at t - 1
+  r.e_prev = ldraw(a.et, rt);
+  r.c_prev = t > 0 ? ldraw(a.ctp, rt - H) : 0u;
+  r.gate = ldraw(a.st, rt);
+  r.p = ldraw(a.pl, rt);
+  r.ay = ldraw(a.ay, rt);
+  r.c_t = ldraw(a.ctp, rt);
+  r.gy0 = a.gU ? ldraw(a.gU, ru) : 0u;
+  r.gub = a.gU ? ldraw(a.gU, ru + H) : 0u;
+  r.gc = a.gC ? ldraw(a.gC, rt) : 0u;
+  r.gnov = a.gN ? ldraw(a.gN, rt) : 0u;
+  r.gp = a.gP ? ldraw(a.gP, rt) : 0u;
+  r.gay = a.gA ? ldraw(a.gA, rt) : 0u;
+  r.gw = a.gW ? ldraw(a.gW, rt) : 0u;
+  r.ge = a.gE ? ldraw(a.gE, rt) : 0u;
+}
+
+struct Scal {
+  float alpha, lam, sig_lam, sup;
+};
+
+// One reverse step at time t, evaluated with the carried budget grad `gbn` without the
+// pending pre-activation grad X of step t + 1, the carried energy grad `gen` and the
+// cortisol grad `gcn`. The budget grad enters every output affinely, so the outputs
+// are returned as (value at X = 0, slope in X); the per-unit parameter accumulators
+// receive the X = 0 part here and the X part when X is known.
+struct Pending {
+  float dgate0, cg, dexpr0, cx, keep_b0, keep_e0, ce, keep_c, gyx, y, a16, a17;
+};
+
+template <typename E>
+__device__ __forceinline__ Pending reverse_step(const TapeRaw& r, int t, float b0v, float c0v,
+                                                const UnitParams& up, const Scal& sc, float gbn,
+                                                float gen, float gcn, float (&acc)[19]) {
+  const float y = cvt<E>(r.y);
+  const float b_prev = t > 0 ? cvt<E>(r.b_prev) : b0v;
+  const float e_prev = cvt<E>(r.e_prev);
+  const float c_prev = t > 0 ? cvt<E>(r.c_prev) : c0v;
+  const float gate = cvt<E>(r.gate);
+  const float p = cvt<E>(r.p);
+  const float ay = cvt<E>(r.ay);
+  const float c_t = cvt<E>(r.c_t);
+  const float gy0 = cvt<E>(r.gy0);
+  const float gb_new = cvt<E>(r.gub) + gbn;
+  const float gc_new = gcn + cvt<E>(r.gc);
+  const float gnov0 = cvt<E>(r.gnov);
+  const float gp0 = cvt<E>(r.gp);
+  const float gay0 = cvt<E>(r.gay);
+  const float gwrite = cvt<E>(r.gw);
+  const float geo = cvt<E>(r.ge);
+
+  const float nov = tanhf(fabsf(ay - b_prev));
+  const float tanh_b = tanhf(b_prev);
+  const float nov_eff = nov * (1.0f - sc.sup * c_t);
+  const float k_signal = up.ks * gate + up.ky * y + up.kb * tanh_b + up.kn * nov_eff + up.kbias +
+                         up.kc * c_t;
+  const float r_signal = up.rs * gate + up.ry * y + up.rb * tanh_b + up.rn * nov_eff + up.rbias +
+                         up.rc * c_t;
+  const float tanh_k = tanhf(k_signal), tanh_r = tanhf(r_signal);
+  const float exp_k = expf(0.5f * tanh_k), exp_r = expf(0.5f * tanh_r);
+  const float write_cost = up.kappa * exp_k;
+  const float recovery_pre = up.recover * exp_r;
+  const float recovery = clamp01(recovery_pre);
+  const float rclamp = (recovery_pre >= 0.0f && recovery_pre <= 1.0f) ? 1.0f : 0.0f;
+  const float energy_pre = e_prev + recovery * (1.0f - e_prev) - write_cost * p;
+  const float ge_pre = gen * ((energy_pre >= 0.0f && energy_pre <= 1.0f) ? 1.0f : 0.0f);
+  const float g_bprev_state = gb_new * (1.0f - sc.alpha);
+  const float g_eprev_state = ge_pre * (1.0f - recovery);
+  float gp = gp0 + gb_new * sc.lam * ay - ge_pre * write_cost;
+  const float gay = gay0 + gb_new * sc.lam * p;
+  const float g_write_cost = -ge_pre * p;
+  const float g_recovery = ge_pre * (1.0f - e_prev);
+  const float d_expr_main = gay + gwrite * p;
+  gp = gp + gwrite * ay;
+  const float g_k = g_write_cost * write_cost * 0.5f * (1.0f - tanh_k * tanh_k);
+  const float g_rpre = g_recovery * rclamp;
+  const float g_r = g_rpre * recovery_pre * 0.5f * (1.0f - tanh_r * tanh_r);
+  const float g_gate_energy = g_k * up.ks + g_r * up.rs;
+  const float gy_energy = g_k * up.ky + g_r * up.ry;
+  const float gb_energy = (g_k * up.kb + g_r * up.rb) * (1.0f - tanh_b * tanh_b);
+  const float gnov_eff = g_k * up.kn + g_r * up.rn;
+  const float gc_energy = g_k * up.kc + g_r * up.rc;
+  const float gmask = ((gate > 0.0f) && (gate < 1.0f)) ? (1.0f / 6.0f) : 0.0f;
+  const float ge_gate = gp * gate;
+  const float stress = nov * (1.0f - e_prev);
+  const float c_new = up.decay * c_prev + (1.0f - up.decay) * stress;
+  const float g_c_new = gc_new + gc_energy - gnov_eff * nov * sc.sup;
+  const float g_stress = g_c_new * (1.0f - up.decay);
+  const float g_nov = gnov_eff * (1.0f - sc.sup * c_new) + g_stress * (1.0f - e_prev);
+  const float g_e_prev_cort = -g_stress * nov;
+  const float diff = ay - b_prev;
+  const float d_nov = (gnov0 + g_nov) * (1.0f - nov * nov) * signf_(diff);
+
+  Pending o;
+  o.dgate0 = (gp * e_prev + g_gate_energy) * gmask;
+  o.cg = sc.lam * ay * e_prev * gmask;
+  o.dexpr0 = d_expr_main + d_nov;
+  o.cx = sc.lam * p;
+  o.keep_b0 = g_bprev_state + gb_energy - d_nov;
+  o.keep_e0 = g_eprev_state + ge_gate + g_e_prev_cort + geo;
+  o.ce = sc.lam * ay * gate;
+  o.keep_c = g_c_new * up.decay;
+  o.gyx = gy0 + gy_energy;
+  o.y = y;
+  o.a16 = (-b_prev) * sc.alpha * (1.0f - sc.alpha);
+  o.a17 = (p * ay) * sc.sig_lam;
+
+  acc[0] += gb_new;
+  acc[1] += g_write_cost * exp_k * up.lk_sig;
+  acc[2] += g_rpre * exp_r * up.recover * (1.0f - up.recover);
+  acc[3] += g_k * gate;
+  acc[4] += g_k * y;
+  acc[5] += g_k * tanh_b;
+  acc[6] += g_k * nov_eff;
+  acc[7] += g_k;
+  acc[8] += g_r * gate;
+  acc[9] += g_r * y;
+  acc[10] += g_r * tanh_b;
+  acc[11] += g_r * nov_eff;
+  acc[12] += g_r;
+  acc[13] += g_c_new * (c_prev - stress) * up.decay * (1.0f - up.decay);
+  acc[14] += g_k * c_t;
+  acc[15] += g_r * c_t;
+  acc[16] += gb_new * o.a16;
+  acc[17] += gb_new * o.a17;
+  acc[18] += gnov_eff * nov * (-c_new) * sc.sup * (1.0f - sc.sup);
+  return o;
+}
+
+template <typename E, int CH, int KSTEPS, int NW>
+__global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
   using M = Mf<E>;
+  constexpr int NT = NW * 64;
   constexpr int KSTEP = M::KSTEP;
   constexpr int KB = 2 * KSTEPS;  // per-wave k-steps over the 2*KP adjoint input
+  constexpr int MTB = (CH + 15) / 16;
   constexpr int PAIRS = CH * NB;
   constexpr int NACC = 19;
-  static_assert(CH <= 16, "one M tile of output units");
+  static_assert(PAIRS <= NT, "one thread per (unit, batch) pair");
 
-  __shared__ float red[NW][16][16];
+  __shared__ float red[NW][MTB][16][16];
   __shared__ bf16 stage[2][NB][CH];
   __shared__ float accs[NB][CH][NACC];
   __shared__ int s_abort;
@@ -455,11 +628,13 @@ __global__ void __launch_bounds__(NT, 1) core_bwd_kernel(BwdArgs<E> a) {
 
   // A operand: rows = output units j of this tile, k = adjoint input index
   // (k < KP: gate-preactivation grad of unit k; k >= KP: expression grad of unit k-KP).
-  typename M::Reg wreg[KB];
-  {
-    const int j = ct * CH + (lane & 15);
-    const bool jok = (lane & 15) < CH && j < H;
-    const size_t jrow = static_cast<size_t>(j) * 2 * H;
+  typename M::Reg wreg[MTB][KB];
+#pragma unroll
+  for (int mt = 0; mt < MTB; ++mt) {
+    const int jr = mt * 16 + (lane & 15);
+    const int j = ct * CH + jr;
+    const bool jok = jr < CH && j < H;
+    const size_t jrow = static_cast<size_t>(jok ? j : 0) * 2 * H;
 #pragma unroll
     for (int s = 0; s < KB; ++s) {
       const int k0 = (wave * KB + s) * KSTEP;
@@ -472,12 +647,12 @@ __global__ void __launch_bounds__(NT, 1) core_bwd_kernel(BwdArgs<E> a) {
           const bool ok = jok && (k < KP ? k < H : (k - KP) < H);
           v[e] = ok ? a.GAT[jrow + r] : static_cast<bf16>(0);
         }
-        wreg[s] = __builtin_bit_cast(bf16x8, v);
+        wreg[mt][s] = __builtin_bit_cast(bf16x8, v);
       } else {
         const int k = k0 + (lane >> 4);
         const int r = k < KP ? k : H + (k - KP);
         const bool ok = jok && (k < KP ? k < H : (k - KP) < H);
-        wreg[s] = ok ? a.GAT[jrow + r] : 0.0f;
+        wreg[mt][s] = ok ? a.GAT[jrow + r] : 0.0f;
       }
     }
   }
@@ -487,115 +662,63 @@ __global__ void __launch_bounds__(NT, 1) core_bwd_kernel(BwdArgs<E> a) {
   const int c = ct * CH + cl, b = bg * NB + bl;
   const bool act = is_pair && c < H && b < B;
   const UnitParams up = load_unit(a.P, c, is_pair && c < H);
-  const float alpha = sigmoidf_(a.P.scal[0][0]);
-  const float lam = softplusf_(a.P.scal[1][0]);
-  const float sig_lam = sigmoidf_(a.P.scal[1][0]);
-  const float sup = sigmoidf_(a.P.scal[2][0]);
+  Scal sc;
+  sc.alpha = sigmoidf_(a.P.scal[0][0]);
+  sc.lam = softplusf_(a.P.scal[1][0]);
+  sc.sig_lam = sigmoidf_(a.P.scal[1][0]);
+  sc.sup = sigmoidf_(a.P.scal[2][0]);
   const size_t bh = static_cast<size_t>(b) * H + c;
-  float gbn = (act && a.gbF) ? a.gbF[bh] : 0.0f;
-  float gen = (act && a.geF) ? a.geF[bh] : 0.0f;
-  float gcn = (act && a.gcF) ? a.gcF[bh] : 0.0f;
+  const float b0v = act ? a.b0[bh] : 0.0f;
+  const float c0v = act ? a.c0[bh] : 0.0f;
   float acc[NACC];
 #pragma unroll
   for (int i = 0; i < NACC; ++i) acc[i] = 0.0f;
   const size_t row0 = static_cast<size_t>(b) * T;
   const int kb2[2] = {ct * CH, KP + ct * CH};
 
+  // Pipeline state at the top of the step for time t: dg/dx are the final adjoint inputs
+  // of t, keep_* the final carried grads towards t - 1 (budget without the pre-activation
+  // grad of t), gyx/yv the pieces of the pre-activation grad of t, xprev the
+  // pre-activation grad of t + 1 (not yet stored), nxt the raw tapes of t - 1.
+  float dg = 0.f, dx = 0.f, keep_b = 0.f, keep_e = 0.f, keep_c = 0.f, gyx = 0.f, yv = 0.f;
+  float xprev = 0.f;
+  TapeRaw nxt = {};
+  if (T > 0 && act) {
+    TapeRaw cur = {};
+    load_tape(a, row0, c, T - 1, cur);
+    if (T > 1) load_tape(a, row0, c, T - 2, nxt);
+    const float gbF = a.gbF ? a.gbF[bh] : 0.0f;
+    const float geF = a.geF ? a.geF[bh] : 0.0f;
+    const float gcF = a.gcF ? a.gcF[bh] : 0.0f;
+    const Pending pd = reverse_step<E>(cur, T - 1, b0v, c0v, up, sc, gbF, geF, gcF, acc);
+    dg = pd.dgate0;
+    dx = pd.dexpr0;
+    keep_b = pd.keep_b0;
+    keep_e = pd.keep_e0;
+    keep_c = pd.keep_c;
+    gyx = pd.gyx;
+    yv = pd.y;
+  }
+
   for (int n = 0; n < T; ++n) {
     const int t = T - 1 - n;
-    const size_t rt = (row0 + t) * H + c;
-    const size_t ru = (row0 + t) * 2 * H + c;
-    float y = 0.f, dgate = 0.f, dexpr = 0.f, keep_b = 0.f, keep_e = 0.f, keep_c = 0.f, gyx = 0.f;
-    if (act) {
-      y = ld(a.U, ru);
-      const float b_prev = t > 0 ? ld(a.U, ru - 2 * static_cast<size_t>(H) + H) : a.b0[bh];
-      const float e_prev = ld(a.et, rt);
-      const float c_prev = t > 0 ? ld(a.ctp, rt - H) : a.c0[bh];
-      const float gate = ld(a.st, rt);
-      const float p = ld(a.pl, rt);
-      const float ay = ld(a.ay, rt);
-      const float nov = tanhf(fabsf(ay - b_prev));
-      const float c_t = ld(a.ctp, rt);
-      const float gy0 = a.gU ? ld(a.gU, ru) : 0.0f;
-      const float gb_new = (a.gU ? ld(a.gU, ru + H) : 0.0f) + gbn;
-      const float gc_new = gcn + (a.gC ? ld(a.gC, rt) : 0.0f);
-      const float gnov0 = a.gN ? ld(a.gN, rt) : 0.0f;
-      const float gp0 = a.gP ? ld(a.gP, rt) : 0.0f;
-      const float gay0 = a.gA ? ld(a.gA, rt) : 0.0f;
-      const float gwrite = a.gW ? ld(a.gW, rt) : 0.0f;
-      const float geo = a.gE ? ld(a.gE, rt) : 0.0f;
-
-      const float tanh_b = tanhf(b_prev);
-      const float nov_eff = nov * (1.0f - sup * c_t);
-      const float k_signal = up.ks * gate + up.ky * y + up.kb * tanh_b + up.kn * nov_eff +
-                             up.kbias + up.kc * c_t;
-      const float r_signal = up.rs * gate + up.ry * y + up.rb * tanh_b + up.rn * nov_eff +
-                             up.rbias + up.rc * c_t;
-      const float tanh_k = tanhf(k_signal), tanh_r = tanhf(r_signal);
-      const float exp_k = expf(0.5f * tanh_k), exp_r = expf(0.5f * tanh_r);
-      const float write_cost = up.kappa * exp_k;
-      const float recovery_pre = up.recover * exp_r;
-      const float recovery = clamp01(recovery_pre);
-      const float rclamp = (recovery_pre >= 0.0f && recovery_pre <= 1.0f) ? 1.0f : 0.0f;
-      const float energy_pre = e_prev + recovery * (1.0f - e_prev) - write_cost * p;
-      const float ge_pre = gen * ((energy_pre >= 0.0f && energy_pre <= 1.0f) ? 1.0f : 0.0f);
-      const float g_bprev_state = gb_new * (1.0f - alpha);
-      const float g_eprev_state = ge_pre * (1.0f - recovery);
-      float gp = gp0 + gb_new * lam * ay - ge_pre * write_cost;
-      const float gay = gay0 + gb_new * lam * p;
-      const float g_write_cost = -ge_pre * p;
-      const float g_recovery = ge_pre * (1.0f - e_prev);
-      const float d_expr_main = gay + gwrite * p;
-      gp = gp + gwrite * ay;
-      const float g_k = g_write_cost * write_cost * 0.5f * (1.0f - tanh_k * tanh_k);
-      const float g_rpre = g_recovery * rclamp;
-      const float g_r = g_rpre * recovery_pre * 0.5f * (1.0f - tanh_r * tanh_r);
-      const float g_gate_energy = g_k * up.ks + g_r * up.rs;
-      const float gy_energy = g_k * up.ky + g_r * up.ry;
-      const float gb_energy = (g_k * up.kb + g_r * up.rb) * (1.0f - tanh_b * tanh_b);
-      const float gnov_eff = g_k * up.kn + g_r * up.rn;
-      const float gc_energy = g_k * up.kc + g_r * up.rc;
-      dgate = (gp * e_prev + g_gate_energy) *
-              (((gate > 0.0f) && (gate < 1.0f)) ? (1.0f / 6.0f) : 0.0f);
-      const float ge_gate = gp * gate;
-      const float stress = nov * (1.0f - e_prev);
-      const float c_new = up.decay * c_prev + (1.0f - up.decay) * stress;
-      const float g_c_new = gc_new + gc_energy - gnov_eff * nov * sup;
-      const float g_stress = g_c_new * (1.0f - up.decay);
-      const float g_nov = gnov_eff * (1.0f - sup * c_new) + g_stress * (1.0f - e_prev);
-      const float g_e_prev_cort = -g_stress * nov;
-      const float diff = ay - b_prev;
-      const float d_nov = (gnov0 + g_nov) * (1.0f - nov * nov) * signf_(diff);
-      dexpr = d_expr_main + d_nov;
-      keep_b = g_bprev_state + gb_energy - d_nov;
-      keep_e = g_eprev_state + ge_gate + g_e_prev_cort + geo;
-      keep_c = g_c_new * up.decay;
-      gyx = gy0 + gy_energy;
-
-      acc[0] += gb_new;
-      acc[1] += g_write_cost * exp_k * up.lk_sig;
-      acc[2] += g_rpre * exp_r * up.recover * (1.0f - up.recover);
-      acc[3] += g_k * gate;
-      acc[4] += g_k * y;
-      acc[5] += g_k * tanh_b;
-      acc[6] += g_k * nov_eff;
-      acc[7] += g_k;
-      acc[8] += g_r * gate;
-      acc[9] += g_r * y;
-      acc[10] += g_r * tanh_b;
-      acc[11] += g_r * nov_eff;
-      acc[12] += g_r;
-      acc[13] += g_c_new * (c_prev - stress) * up.decay * (1.0f - up.decay);
-      acc[14] += g_k * c_t;
-      acc[15] += g_r * c_t;
-      acc[16] += gb_new * (-b_prev) * alpha * (1.0f - alpha);
-      acc[17] += gb_new * (p * ay) * sig_lam;
-      acc[18] += gnov_eff * nov * (-c_new) * sup * (1.0f - sup);
-    }
     {
-      const float v[2] = {dgate, dexpr};
-      publish<E, CH, 2>(xr, a.slot_bytes, n & 1, kb2, v, is_pair, cl, bl, stage);
+      const float v[2] = {dg, dx};
+      publish<E, CH, 2, NT>(xr, a.slot_bytes, n & 1, kb2, v, is_pair, cl, bl, stage);
       if (tid == 0) arrive(counter);
+    }
+    // Off the critical path: outputs of t (and the pre-activation grad of t + 1), the
+    // loads of t - 2, and the X = 0 part of the reverse step at t - 1.
+    Pending pd = {};
+    if (act) {
+      const size_t rt = (row0 + t) * H + c;
+      st(a.gWgx, rt, dg);
+      st(a.day, rt, dx);
+      if (n > 0) st(a.gWx, rt + H, xprev);
+      TapeRaw nn = {};
+      if (t >= 2) load_tape(a, row0, c, t - 2, nn);
+      if (t >= 1) pd = reverse_step<E>(nxt, t - 1, b0v, c0v, up, sc, keep_b, keep_e, keep_c, acc);
+      nxt = nn;
     }
     if (tid == 0) {
       if (!wait_counter(counter, nct * static_cast<uint32_t>(n + 1), err)) s_abort = 1;
@@ -608,32 +731,50 @@ __global__ void __launch_bounds__(NT, 1) core_bwd_kernel(BwdArgs<E> a) {
 #pragma unroll
     for (int s = 0; s < KB; ++s)
       breg[s] = M::load_x(xr, sbase + static_cast<uint32_t>((wave * KB + s) * 64 + lane) * M::UNIT);
-    f32x4 accm = {0.f, 0.f, 0.f, 0.f};
+    f32x4 accm[MTB];
 #pragma unroll
-    for (int s = 0; s < KB; ++s) accm = M::mma(wreg[s], breg[s], accm);
+    for (int mt = 0; mt < MTB; ++mt) accm[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[wave][(lane >> 4) * 4 + j][lane & 15] = accm[j];
+    for (int s = 0; s < KB; ++s) {
+#pragma unroll
+      for (int mt = 0; mt < MTB; ++mt) accm[mt] = M::mma(wreg[mt][s], breg[s], accm[mt]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MTB; ++mt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[wave][mt][(lane >> 4) * 4 + j][lane & 15] = accm[mt][j];
+    }
     __syncthreads();
     if (act) {
       float adj = 0.0f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) adj += red[w][cl][bl];
+      for (int w = 0; w < NW; ++w) adj += red[w][cl >> 4][cl & 15][bl];
       adj = round_to<E>(adj);
       const float gy = gyx + adj;
-      const float gpre = gy * (1.0f - y * y);
-      st(a.gWx, rt, gpre);
-      st(a.gWgx, rt, dgate);
-      st(a.day, rt, dexpr);
-      gbn = keep_b + gpre;
-      gen = keep_e;
-      gcn = keep_c;
+      const float x = gy * (1.0f - yv * yv);  // pre-activation grad of t (gWx)
+      if (t >= 1) {
+        dg = pd.dgate0 + x * pd.cg;
+        dx = pd.dexpr0 + x * pd.cx;
+        keep_b = pd.keep_b0 + x * (1.0f - sc.alpha);
+        keep_e = pd.keep_e0 + x * pd.ce;
+        keep_c = pd.keep_c;
+        acc[0] += x;
+        acc[16] += x * pd.a16;
+        acc[17] += x * pd.a17;
+        gyx = pd.gyx;
+        yv = pd.y;
+      } else {
+        keep_b += x;
+      }
+      xprev = x;
     }
   }
 
   if (act) {
-    a.gb0[bh] = gbn;
-    a.ge0[bh] = gen;
-    a.gc0[bh] = gcn;
+    if (T > 0) st(a.gWx, row0 * H + c, xprev);
+    a.gb0[bh] = T > 0 ? keep_b : (a.gbF ? a.gbF[bh] : 0.0f);
+    a.ge0[bh] = T > 0 ? keep_e : (a.geF ? a.geF[bh] : 0.0f);
+    a.gc0[bh] = T > 0 ? keep_c : (a.gcF ? a.gcF[bh] : 0.0f);
   }
   // Per-unit parameter gradients: reduce the 16 batch rows of this tile in a fixed order.
   if (is_pair) {
@@ -660,17 +801,24 @@ __global__ void __launch_bounds__(NT, 1) core_bwd_kernel(BwdArgs<E> a) {
 // Host side: configuration, workspace and launch.
 // ---------------------------------------------------------------------------
 struct Cfg {
-  int ch = 0, ksteps = 0, kp = 0, nct = 0, nbg = 0;
+  int ch = 0, ksteps = 0, kp = 0, nct = 0, nbg = 0, nw = 0;
 };
+
+// Channel tile width for bf16 beyond H = 1024 (channels per workgroup).
+#ifndef DABSN_CORE_CH_WIDE
+#define DABSN_CORE_CH_WIDE 16
+#endif
 
 static Cfg pick(int dtype, int64_t B, int64_t H) {
   Cfg c;
   const int kstep = dtype == kBF16 ? 32 : 4;
-  const int need = static_cast<int>((H + NW * kstep - 1) / (NW * kstep));
-  static const int bf_steps[] = {1, 2, 4, 8, 16};
+  // bf16 beyond H = 1024 uses 8 waves, each holding half as many weights.
+  c.nw = (dtype == kBF16 && H > 1024) ? 8 : 4;
+  const int need = static_cast<int>((H + c.nw * kstep - 1) / (c.nw * kstep));
+  static const int bf_steps[] = {1, 2, 4, 8};
   static const int f_steps[] = {1, 2, 4, 8, 16, 32, 64};
   const int* list = dtype == kBF16 ? bf_steps : f_steps;
-  const int nlist = dtype == kBF16 ? 5 : 7;
+  const int nlist = dtype == kBF16 ? 4 : 7;
   for (int i = 0; i < nlist; ++i) {
     if (list[i] >= need) {
       c.ksteps = list[i];
@@ -678,8 +826,8 @@ static Cfg pick(int dtype, int64_t B, int64_t H) {
     }
   }
   if (c.ksteps == 0) return c;
-  c.kp = NW * c.ksteps * kstep;
-  c.ch = (dtype == kBF16 && H >= 1024) ? 16 : 8;
+  c.kp = c.nw * c.ksteps * kstep;
+  c.ch = (dtype == kBF16 && H >= 1024) ? (H > 1024 ? DABSN_CORE_CH_WIDE : 16) : 8;
   c.nct = static_cast<int>((H + c.ch - 1) / c.ch);
   c.nbg = static_cast<int>((B + NB - 1) / NB);
   return c;
@@ -695,13 +843,13 @@ static size_t workspace_bytes(int dtype, const Cfg& c, bool backward) {
 }
 
 template <typename K, typename A>
-static int launch_coop(K kernel, int grid, const A& args, hipStream_t stream) {
+static int launch_coop(K kernel, int grid, int threads, const A& args, hipStream_t stream) {
   int dev = 0;
   DABSN_HIP_CHECK(hipGetDevice(&dev));
   int cus = 0, per_cu = 0, coop = 0;
   DABSN_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
   DABSN_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  DABSN_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, NT, 0));
+  DABSN_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0));
   if (!coop || per_cu * cus < grid) {
     dabsn::set_error(
         "core scan needs %d co-resident workgroups but the device holds %d (%d per CU x %d CUs,"
@@ -711,43 +859,46 @@ static int launch_coop(K kernel, int grid, const A& args, hipStream_t stream) {
   }
   void* kargs[] = {const_cast<A*>(&args)};
   DABSN_HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), dim3(grid),
-                                             dim3(NT), kargs, 0, stream));
+                                             dim3(threads), kargs, 0, stream));
   return DABSN_OK;
 }
+
+// (CH, KSTEPS, NW) combinations compiled per dtype.
+#define DABSN_CORE_CASES_BF16(X) \
+  X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(16, 8, 4) X(16, 8, 8)
+#define DABSN_CORE_CASES_F32(X) \
+  X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(8, 16, 4) X(8, 32, 4) X(8, 64, 4)
 
 template <typename E>
 static int fwd_dispatch(const Cfg& c, const FwdArgs<E>& args, hipStream_t stream) {
   const int grid = c.nct * c.nbg;
-#define DABSN_CASE(CHV, KS)                                                    \
-  if (c.ch == CHV && c.ksteps == KS)                                           \
-    return launch_coop(core_fwd_kernel<E, CHV, KS>, grid, args, stream);
+#define DABSN_CASE(CHV, KS, NWV)                                   \
+  if (c.ch == CHV && c.ksteps == KS && c.nw == NWV)                \
+    return launch_coop(core_fwd_kernel<E, CHV, KS, NWV>, grid, NWV * 64, args, stream);
   if constexpr (is_bf16<E>::value) {
-    DABSN_CASE(8, 1) DABSN_CASE(8, 2) DABSN_CASE(8, 4) DABSN_CASE(8, 8) DABSN_CASE(8, 16)
-    DABSN_CASE(16, 8) DABSN_CASE(16, 16)
+    DABSN_CORE_CASES_BF16(DABSN_CASE)
   } else {
-    DABSN_CASE(8, 1) DABSN_CASE(8, 2) DABSN_CASE(8, 4) DABSN_CASE(8, 8) DABSN_CASE(8, 16)
-    DABSN_CASE(8, 32) DABSN_CASE(8, 64)
+    DABSN_CORE_CASES_F32(DABSN_CASE)
   }
 #undef DABSN_CASE
-  dabsn::set_error("core scan: no kernel for CH=%d KSTEPS=%d", c.ch, c.ksteps);
+  dabsn::set_error("core scan: no kernel for CH=%d KSTEPS=%d NW=%d", c.ch, c.ksteps, c.nw);
   return DABSN_ERR_UNSUPPORTED;
 }
 
 template <typename E>
 static int bwd_dispatch(const Cfg& c, const BwdArgs<E>& args, hipStream_t stream) {
   const int grid = c.nct * c.nbg;
-#define DABSN_CASE(CHV, KS)                                                    \
-  if (c.ch == CHV && c.ksteps == KS)                                           \
-    return launch_coop(core_bwd_kernel<E, CHV, KS>, grid, args, stream);
+#define DABSN_CASE(CHV, KS, NWV)                                   \
+  if (c.ch == CHV && c.ksteps == KS && c.nw == NWV)                \
+    return launch_coop(core_bwd_kernel<E, CHV, KS, NWV>, grid, NWV * 64, args, stream);
   if constexpr (is_bf16<E>::value) {
-    DABSN_CASE(8, 1) DABSN_CASE(8, 2) DABSN_CASE(8, 4) DABSN_CASE(8, 8) DABSN_CASE(8, 16)
-    DABSN_CASE(16, 8) DABSN_CASE(16, 16)
+    DABSN_CORE_CASES_BF16(DABSN_CASE)
   } else {
-    DABSN_CASE(8, 1) DABSN_CASE(8, 2) DABSN_CASE(8, 4) DABSN_CASE(8, 8) DABSN_CASE(8, 16)
-    DABSN_CASE(8, 32) DABSN_CASE(8, 64)
+    DABSN_CORE_CASES_F32(DABSN_CASE)
   }
 #undef DABSN_CASE
-  dabsn::set_error("core scan backward: no kernel for CH=%d KSTEPS=%d", c.ch, c.ksteps);
+  dabsn::set_error("core scan backward: no kernel for CH=%d KSTEPS=%d NW=%d", c.ch, c.ksteps,
+                   c.nw);
   return DABSN_ERR_UNSUPPORTED;
 }
 
