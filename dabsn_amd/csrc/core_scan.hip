@@ -10,8 +10,9 @@
 //   * Every step needs the full y_t (forward) or the full [dgate; dexpr] vector
 //     (backward) of its batch group. Workgroups publish their slice into a small
 //     exchange buffer laid out exactly as the MFMA B operand, then meet at a
-//     device-wide step barrier (a monotonic counter). Exchange traffic and the
-//     counter use device-coherent (sc1) accesses so no L2 writeback/invalidate is
+//     device-wide step barrier: monotonic step counters split kSplit ways (one 64-byte
+//     line each) so arrivals do not serialise on one address. Exchange traffic and the
+//     counters use device-coherent (sc1) accesses so no L2 writeback/invalidate is
 //     needed between XCDs.
 //   * The recurrent product runs on v_mfma_f32_16x16x32_bf16 (bf16) or
 //     v_mfma_f32_16x16x4_f32 (fp32) with K split across the NW waves; partial tiles
@@ -75,9 +76,22 @@ __device__ __forceinline__ uint32_t xoff<float>(int k, int n) {
   return static_cast<uint32_t>((k >> 2) * 64 + (k & 3) * 16 + n);
 }
 
-// Workspace layout: [0,4) error word, [4, 4 + 4*nbg) step counters, exchange slots
-// from kXOff (2 slots per batch group).
-constexpr size_t kXOff = 4096;
+// Workspace layout: [0,4) error word; from kCtrOff, kSplit step counters per batch
+// group, kCtrStride bytes apart; exchange slots (2 per batch group) from
+// xchg_offset(nbg).
+constexpr int kSplit = 8;
+constexpr size_t kCtrOff = 64;
+constexpr size_t kCtrStride = 64;
+__host__ __device__ inline size_t xchg_offset(int nbg) {
+  const size_t end = kCtrOff + static_cast<size_t>(nbg) * kSplit * kCtrStride;
+  return (end + 4095) / 4096 * 4096;
+}
+
+// Arrivals one split counter receives per step: workgroup i of a batch group (0 <= i <
+// nct) arrives on counter i % kSplit.
+__host__ __device__ inline uint32_t split_arrivals(int nct, int s) {
+  return s < nct ? static_cast<uint32_t>((nct - s + kSplit - 1) / kSplit) : 0u;
+}
 
 struct Params {
   const float* vec[16];
@@ -109,25 +123,43 @@ __device__ __forceinline__ UnitParams load_unit(const Params& P, int c, bool ok)
   return u;
 }
 
-// Thread 0 of a workgroup waits until the step counter reaches `target`.
-// Returns false (and raises the error word) if the wait exceeded the spin bound.
-__device__ __forceinline__ bool wait_counter(uint32_t* counter, uint32_t target, uint32_t* err) {
+// Called by all 64 lanes of wave 0: waits until every split counter of the batch group
+// (base `ctr`) has received `step1` rounds of arrivals. Lane s polls counter s. Returns
+// false if the error word is raised or the wait exceeded the spin bound; lane 0 then
+// raises the error word itself on a timeout.
+__device__ __forceinline__ bool wait_step(const uint32_t* ctr, int nct, uint32_t step1,
+                                          uint32_t* err) {
+  const int lane = threadIdx.x & 63;
+  const int s = lane < kSplit ? lane : 0;
+  const uint32_t target = (lane < kSplit ? split_arrivals(nct, s) : 0u) * step1;
+  const uint32_t* mine = ctr + s * (kCtrStride / 4);
   uint32_t spins = 0;
-  while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+  while (true) {
+    bool ok = true;
+    if (target != 0u) ok = __hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target;
+    if (__all(ok)) return true;
     if ((++spins & 1023u) == 0u) {
       if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return false;
       if (spins > kSpinLimit) {
-        __hip_atomic_fetch_or(err, kErrBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0)
+          __hip_atomic_fetch_or(err, kErrBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return false;
       }
     }
     __builtin_amdgcn_s_sleep(1);
   }
-  return true;
 }
 
 __device__ __forceinline__ void arrive(uint32_t* counter) {
   __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Step counters of batch group bg, and the counter this workgroup arrives on.
+__device__ __forceinline__ uint32_t* group_counters(uint8_t* ws, int bg) {
+  return reinterpret_cast<uint32_t*>(ws + kCtrOff + static_cast<size_t>(bg) * kSplit * kCtrStride);
+}
+__device__ __forceinline__ uint32_t* my_counter(uint32_t* ctr, int nct) {
+  return ctr + (static_cast<int>(blockIdx.x) % nct % kSplit) * (kCtrStride / 4);
 }
 
 // Wait for every outstanding vector memory operation of this wave (the exchange stores
@@ -252,10 +284,11 @@ __global__ void __launch_bounds__(NW * 64, 1) core_fwd_kernel(FwdArgs<E> a) {
   int ct, bg;
   tile_of(a.nct, ct, bg);
   const int H = a.H, T = a.T, B = a.B;
-  const uint32_t nct = static_cast<uint32_t>(a.nct);
   uint32_t* err = reinterpret_cast<uint32_t*>(a.ws);
-  uint32_t* counter = reinterpret_cast<uint32_t*>(a.ws + 4) + bg;
-  uint8_t* xbase = a.ws + kXOff + static_cast<size_t>(bg) * 2 * a.slot_bytes;
+  uint32_t* ctr = group_counters(a.ws, bg);
+  uint32_t* counter = my_counter(ctr, a.nct);
+  const int nbg = static_cast<int>(gridDim.x) / a.nct;
+  uint8_t* xbase = a.ws + xchg_offset(nbg) + static_cast<size_t>(bg) * 2 * a.slot_bytes;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(xbase, 2 * a.slot_bytes);
   if (tid == 0) s_abort = 0;
 
@@ -309,8 +342,8 @@ __global__ void __launch_bounds__(NW * 64, 1) core_fwd_kernel(FwdArgs<E> a) {
     const size_t rt = (row0 + t) * H + c;
     const float wgx = act ? ld(a.Wgx, rt) : 0.0f;
     const float wxn = (act && t + 1 < T) ? ld(a.Wx, rt + H) : 0.0f;
-    if (tid == 0) {
-      if (!wait_counter(counter, nct * static_cast<uint32_t>(t + 1), err)) s_abort = 1;
+    if (wave == 0) {
+      if (!wait_step(ctr, a.nct, static_cast<uint32_t>(t + 1), err) && tid == 0) s_abort = 1;
     }
     __syncthreads();
     if (s_abort) return;
@@ -619,10 +652,11 @@ __global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
   int ct, bg;
   tile_of(a.nct, ct, bg);
   const int H = a.H, T = a.T, B = a.B, KP = a.kp;
-  const uint32_t nct = static_cast<uint32_t>(a.nct);
   uint32_t* err = reinterpret_cast<uint32_t*>(a.ws);
-  uint32_t* counter = reinterpret_cast<uint32_t*>(a.ws + 4) + bg;
-  uint8_t* xbase = a.ws + kXOff + static_cast<size_t>(bg) * 2 * a.slot_bytes;
+  uint32_t* ctr = group_counters(a.ws, bg);
+  uint32_t* counter = my_counter(ctr, a.nct);
+  const int nbg = static_cast<int>(gridDim.x) / a.nct;
+  uint8_t* xbase = a.ws + xchg_offset(nbg) + static_cast<size_t>(bg) * 2 * a.slot_bytes;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(xbase, 2 * a.slot_bytes);
   if (tid == 0) s_abort = 0;
 
@@ -707,21 +741,18 @@ __global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
       publish<E, CH, 2, NT>(xr, a.slot_bytes, n & 1, kb2, v, is_pair, cl, bl, stage);
       if (tid == 0) arrive(counter);
     }
-    // Off the critical path: outputs of t (and the pre-activation grad of t + 1), the
-    // loads of t - 2, and the X = 0 part of the reverse step at t - 1.
+    // Off the critical path: outputs of t (and the pre-activation grad of t + 1) and the
+    // X = 0 part of the reverse step at t - 1.
     Pending pd = {};
     if (act) {
       const size_t rt = (row0 + t) * H + c;
       st(a.gWgx, rt, dg);
       st(a.day, rt, dx);
       if (n > 0) st(a.gWx, rt + H, xprev);
-      TapeRaw nn = {};
-      if (t >= 2) load_tape(a, row0, c, t - 2, nn);
       if (t >= 1) pd = reverse_step<E>(nxt, t - 1, b0v, c0v, up, sc, keep_b, keep_e, keep_c, acc);
-      nxt = nn;
     }
-    if (tid == 0) {
-      if (!wait_counter(counter, nct * static_cast<uint32_t>(n + 1), err)) s_abort = 1;
+    if (wave == 0) {
+      if (!wait_step(ctr, a.nct, static_cast<uint32_t>(n + 1), err) && tid == 0) s_abort = 1;
     }
     __syncthreads();
     if (s_abort) return;
@@ -731,6 +762,10 @@ __global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
 #pragma unroll
     for (int s = 0; s < KB; ++s)
       breg[s] = M::load_x(xr, sbase + static_cast<uint32_t>((wave * KB + s) * 64 + lane) * M::UNIT);
+    // Tapes of t - 2 are requested after the exchange loads: completions are counted in
+    // issue order, so waiting for the exchange does not wait for these.
+    TapeRaw nn = {};
+    if (act && t >= 2) load_tape(a, row0, c, t - 2, nn);
     f32x4 accm[MTB];
 #pragma unroll
     for (int mt = 0; mt < MTB; ++mt) accm[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -768,6 +803,7 @@ __global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
       }
       xprev = x;
     }
+    nxt = nn;
   }
 
   if (act) {
@@ -839,7 +875,7 @@ static size_t slot_bytes(int dtype, const Cfg& c, bool backward) {
 }
 
 static size_t workspace_bytes(int dtype, const Cfg& c, bool backward) {
-  return kXOff + static_cast<size_t>(c.nbg) * 2 * slot_bytes(dtype, c, backward);
+  return xchg_offset(c.nbg) + static_cast<size_t>(c.nbg) * 2 * slot_bytes(dtype, c, backward);
 }
 
 template <typename K, typename A>
@@ -924,6 +960,10 @@ static int check_common(int dtype, int64_t B, int64_t T, int64_t H, const dabsn_
     return DABSN_ERR_UNSUPPORTED;
   }
   DABSN_REQUIRE(ws_bytes >= need, "core scan: workspace %zu B < required %zu B", ws_bytes, need);
+  // Step counters are 32-bit: arrivals per counter times steps must not wrap.
+  DABSN_REQUIRE(static_cast<uint64_t>(split_arrivals(c.nct, 0)) * static_cast<uint64_t>(T + 1) <
+                    (1ull << 32),
+                "core scan: T=%lld too long for the 32-bit step counters", (long long)T);
   return DABSN_OK;
 }
 
