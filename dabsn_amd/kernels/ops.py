@@ -46,6 +46,9 @@ def _stream(t: Tensor) -> ctypes.c_void_p:
 
 
 def _p(t: Optional[Tensor]) -> Optional[int]:
+    """Device pointer of `t`. The caller must keep `t` referenced until the launch is
+    enqueued: a temporary (e.g. ``x.contiguous()`` inline in the call) may be freed and its
+    block handed to another allocation of the same call before the kernel runs."""
     return None if t is None else t.data_ptr()
 
 
@@ -560,9 +563,10 @@ def normalize_rows_backward(q: Tensor, norms: Tensor, gq: Tensor) -> Tensor:
     rows = q.numel() // H
     qc = q.contiguous()
     gqc = gq.to(q.dtype).contiguous()
+    nc = norms.float().contiguous()
     gx = torch.zeros_like(qc)
     _lib.check(lib.dabsn_hip_normalize_rows_bwd(_code(q.dtype), rows, H, _p(qc),
-                                                _p(norms.float().contiguous()), _p(gqc), _p(gx),
+                                                _p(nc), _p(gqc), _p(gx),
                                                 _stream(q)), "normalize rows backward")
     return gx
 
@@ -616,11 +620,12 @@ def bank_gather(write: Tensor, norm_w: Tensor, idx: Tensor, next_idx: Tensor,
     B, T, H = write.shape
     N = idx.shape[1]
     w = write.contiguous()
+    nw = norm_w.float().contiguous()
+    ic = idx.to(torch.int64).contiguous()
+    nc = next_idx.to(torch.int64).contiguous()
     K, V, Vn = (torch.empty((B, N, H), device=w.device, dtype=w.dtype) for _ in range(3))
-    _lib.check(lib.dabsn_hip_bank_gather(_code(w.dtype), B, T, N, H, _p(w),
-                                         _p(norm_w.float().contiguous()), _p(idx.contiguous()),
-                                         _p(next_idx.contiguous()), _p(K), _p(V), _p(Vn),
-                                         _stream(w)), "bank gather")
+    _lib.check(lib.dabsn_hip_bank_gather(_code(w.dtype), B, T, N, H, _p(w), _p(nw), _p(ic),
+                                         _p(nc), _p(K), _p(V), _p(Vn), _stream(w)), "bank gather")
     return K, V, Vn
 
 
@@ -640,11 +645,13 @@ def bank_gather_backward(write: Tensor, norm_w: Tensor, rank: Tensor, K: Tensor,
     N = K.shape[1]
     dt = write.dtype
     gw = torch.zeros((B, T, H), device=write.device, dtype=dt)
-    _lib.check(lib.dabsn_hip_bank_gather_bwd(_code(dt), B, T, N, H, None,
-                                             _p(norm_w.float().contiguous()), _p(rank.contiguous()),
-                                             _p(K.contiguous()), _p(gK.to(dt).contiguous()),
-                                             _p(gV.to(dt).contiguous()), _p(gVn.to(dt).contiguous()),
-                                             _p(gw), _stream(write)), "bank gather backward")
+    nw = norm_w.float().contiguous()
+    rk = rank.to(torch.int32).contiguous()
+    Kc = K.to(dt).contiguous()
+    gKc, gVc, gVnc = (g.to(dt).contiguous() for g in (gK, gV, gVn))
+    _lib.check(lib.dabsn_hip_bank_gather_bwd(_code(dt), B, T, N, H, None, _p(nw), _p(rk), _p(Kc),
+                                             _p(gKc), _p(gVc), _p(gVnc), _p(gw), _stream(write)),
+               "bank gather backward")
     return gw
 
 

@@ -1,0 +1,143 @@
+"""Block-level behaviour of the seq DABSN block built on the dabsn:: operators.
+
+CPU variants run the block through the test-only oracle backend (oracle/torch_backend.py
+registers the C oracle as the ops' CPU kernels); GPU variants run the HIP kernels and are
+compared with the CPU oracle evaluation of the same module.
+
+  * block time-chunking with carried state equals the full scan (reference
+    tests/test_block_chunking.py:20-51): forward to fp32 rounding, grads to 1e-5;
+  * forward_query_bank on a query chunk against the full bank equals the unified read
+    for those rows (reference tests/test_read_chunking.py:23-109): 1e-5;
+  * config 1 (two seq layers 128/96 and 192/128, input 24, residual, MLP 4.0, fp32)
+    forward+backward on GPU against the CPU oracle: normwise 1e-4 for every output and
+    parameter gradient (several fp32 ops in sequence, each within 1e-5).
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+import dabsn_amd
+from helpers import rel_err
+from oracle import torch_backend
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _oracle_cpu_kernels():
+    torch_backend.register()
+
+
+def _block(seed, din, hidden, state, chunk=None):
+    torch.manual_seed(seed)
+    blk = dabsn_amd.DABSNBlock(din, hidden, state, "seq", residual=True, mlp_ratio=2.0,
+                               block_chunk_t=chunk)
+    blk.read.admit_window.data.fill_(0.3)  # a partially admitted bank
+    return blk
+
+
+def _fwd_bwd(block, x, w):
+    x = x.clone().requires_grad_(True)
+    out = block(x)
+    (out * w).sum().backward()
+    grads = {n: p.grad.detach().clone() for n, p in block.named_parameters() if p.grad is not None}
+    return out.detach(), x.grad.detach(), grads
+
+
+def _check_same(a, b, tol):
+    out_a, gx_a, g_a = a
+    out_b, gx_b, g_b = b
+    assert rel_err(out_a.cpu(), out_b.cpu()) <= tol
+    assert rel_err(gx_a.cpu(), gx_b.cpu()) <= tol
+    assert g_a.keys() == g_b.keys()
+    for n in g_a:
+        assert rel_err(g_a[n].cpu(), g_b[n].cpu()) <= tol, f"{n}: {rel_err(g_a[n].cpu(), g_b[n].cpu()):.3e}"
+
+
+def _chunk_case(device):
+    full = _block(1, 16, 24, 24).to(device)
+    chunked = copy.deepcopy(full)
+    chunked.block_chunk_t = 7
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(2, 30, 16, generator=g).to(device)
+    w = torch.randn(2, 30, 24, generator=g).to(device)
+    return _fwd_bwd(full, x, w), _fwd_bwd(chunked, x, w)
+
+
+def test_block_chunking_equals_full_cpu():
+    a, b = _chunk_case("cpu")
+    _check_same(a, b, 1e-5)
+
+
+@pytest.mark.gpu
+def test_block_chunking_equals_full_gpu(cuda_device):
+    a, b = _chunk_case(cuda_device)
+    _check_same(a, b, 1e-5)
+
+
+def _query_bank_case(device):
+    torch.manual_seed(3)
+    blk = _block(3, 16, 24, 24).to(device)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 40, 16, generator=g).to(device)
+    with torch.no_grad():
+        traj, nov, p, ay, wr, en, sat = blk.core_tapes(x)
+        y, b = traj.split(24, dim=-1)
+        full = blk.read(y, b, ay, wr, nov, p, en, sat)
+        t0 = 25
+        _, long_state = blk.read._long_scan_from_state(wr[:, :t0], p[:, :t0], nov[:, :t0],
+                                                        return_final_state=True)
+        sl = slice(t0, None)
+        part = blk.read.forward_query_bank(
+            y[:, sl], b[:, sl], ay[:, sl], wr[:, sl], nov[:, sl], p[:, sl], en[:, sl], sat[:, sl],
+            bank_write=wr, bank_novelty=nov, bank_p=p, bank_energy=en, bank_saturation=sat,
+            query_start=t0, initial_long_state=long_state)
+    return full[:, t0:], part
+
+
+def test_forward_query_bank_matches_unified_read_cpu():
+    full, part = _query_bank_case("cpu")
+    assert rel_err(part, full) <= 1e-5
+
+
+@pytest.mark.gpu
+def test_forward_query_bank_matches_unified_read_gpu(cuda_device):
+    full, part = _query_bank_case(cuda_device)
+    assert rel_err(part.cpu(), full.cpu()) <= 1e-5
+
+
+@pytest.mark.gpu
+def test_config1_two_layer_model_gpu_matches_cpu_oracle(cuda_device):
+    """input 24, layers (hidden 128, state 96) and (192, 128)."""
+    torch.manual_seed(0)
+    layers = torch.nn.Sequential(
+        dabsn_amd.DABSNBlock(24, 128, 96, "seq", residual=True, mlp_ratio=4.0),
+        dabsn_amd.DABSNBlock(128, 192, 128, "seq", residual=True, mlp_ratio=4.0),
+        torch.nn.Linear(192, 10))
+    gpu = copy.deepcopy(layers).to(cuda_device)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(8, 256, 24, generator=g)
+    target = torch.randint(0, 10, (8, 256), generator=g)
+
+    def run(model, xx, tt):
+        xx = xx.clone().requires_grad_(True)
+        logits = model(xx)
+        loss = torch.nn.functional.cross_entropy(logits.reshape(-1, 10), tt.reshape(-1))
+        loss.backward()
+        return loss.detach(), {n: p.grad.detach().clone() for n, p in model.named_parameters()
+                               if p.grad is not None}
+
+    loss_c, grads_c = run(layers, x, target)
+    loss_g, grads_g = run(gpu, x.to(cuda_device), target.to(cuda_device))
+    assert abs(float(loss_g) - float(loss_c)) <= 1e-5 * abs(float(loss_c))
+    assert grads_c.keys() == grads_g.keys()
+    # Some parameters have an exactly zero gradient in exact arithmetic (null_bias shifts
+    # every logit of a softmax equally), so both sides hold rounding noise there; the
+    # normwise denominator is floored at 1e-3 of the largest gradient in the model.
+    floor = 1e-3 * max(float(g.abs().max()) for g in grads_c.values())
+    for n in grads_c:
+        a, e = grads_g[n].cpu().double(), grads_c[n].double()
+        err = float((a - e).abs().max()) / max(float(e.abs().max()), floor)
+        assert err <= 1e-4, f"{n}: {err:.3e} (max|grad| {float(e.abs().max()):.3e})"

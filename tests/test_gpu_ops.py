@@ -301,3 +301,25 @@ def test_read3_bf16_within_tolerance_of_fp32_oracle(cuda_device):
     gb = ops.admitted_three_way_read_compact_flash_backward(bf(go), *args)
     for i, (a, b) in enumerate(zip(gb, refb)):
         assert rel_fro(a, b) <= 2e-2, f"grad {i}: {rel_fro(a, b):.3e}"
+
+
+@pytest.mark.parametrize("B,T,H", [(2, 48, 24), (3, 50, 72), (1, 7, 5)])
+def test_bank_gather_with_strided_inputs_matches_torch(cuda_device, B, T, H):
+    """Strided norm and index views, as the read passes them (stats[..., 5], order[:, :n]):
+    every operand pointer must outlive its conversion until the kernel is enqueued."""
+    g = torch.Generator().manual_seed(B * 1000 + T)
+    tapes = [torch.randn(B, T, H, generator=g).to(cuda_device) for _ in range(6)]
+    st = ops.read_tape_stats(*tapes)
+    norm_w = st[..., 5]
+    assert not norm_w.is_contiguous()
+    adm = torch.randn(B, T, generator=g).to(cuda_device)
+    order, counts, rank = ops.bank_select(adm, torch.tensor([0.3], device=cuda_device))
+    n = max(int(counts.max()), 1)
+    idx = order[:, :n]
+    nidx = (idx + 1).clamp(max=T - 1)
+    K, V, Vn = ops.bank_gather(tapes[5], norm_w, idx, nidx, rank)
+    w = tapes[5].cpu().double()
+    Vr = torch.gather(w, 1, idx.cpu()[..., None].expand(-1, -1, H))
+    assert_rel(K, F.normalize(Vr, dim=-1), 1e-6, "K")
+    assert torch.equal(V.cpu(), Vr.float())
+    assert torch.equal(Vn.cpu(), torch.gather(w, 1, nidx.cpu()[..., None].expand(-1, -1, H)).float())

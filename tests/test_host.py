@@ -1,0 +1,156 @@
+"""Host-side checks (CPU only, no GPU compute).
+
+  * the C-ABI library loads and exports every entry point include/dabsn_hip.h declares,
+    and the ctypes table matches the header;
+  * the product package never imports the oracle and never falls back to CPU: without the
+    test-only oracle backend, a CPU tensor raises in every operator;
+  * backend registry (enable/status/PRIMITIVES) and routing-event semantics
+    (reference kernels/__init__.py:38-163, runtime/dispatch.py:40-101, events.py:66-86).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "dabsn_hip.h"
+
+
+def _header_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dabsn_hip_\w+)\s*\(", text)))
+
+
+def _built_library() -> Path:
+    from dabsn_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        from dabsn_amd import build
+
+        build.build()
+    return _lib.LIB_PATH
+
+
+def _run(code: str) -> subprocess.CompletedProcess:
+    env = dict(os.environ)
+    env["PYTHONPATH"] = str(ROOT) + os.pathsep + env.get("PYTHONPATH", "")
+    return subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env,
+                          cwd=str(ROOT), timeout=300)
+
+
+def test_header_declares_the_ctypes_table():
+    from dabsn_amd import _lib
+
+    assert _header_symbols() == sorted(_lib.EXPORTED)
+
+
+def test_library_loads_and_exports_every_header_symbol():
+    lib = ctypes.CDLL(str(_built_library()))
+    missing = [s for s in _header_symbols() if not hasattr(lib, s)]
+    assert not missing, f"missing exports: {missing}"
+    lib.dabsn_hip_abi_version.restype = ctypes.c_int
+    from dabsn_amd import _lib
+
+    assert lib.dabsn_hip_abi_version() == _lib.ABI_VERSION
+    m = re.search(r"#define DABSN_HIP_ABI_VERSION (\d+)", HEADER.read_text())
+    assert m and int(m.group(1)) == _lib.ABI_VERSION
+
+
+def test_header_entry_points_cite_the_reference():
+    """Every group of declarations in the header names the reference code it replaces."""
+    text = HEADER.read_text()
+    sections = re.split(r"/\* ---- ", text)[1:]
+    assert len(sections) >= 5
+    for sec in sections[1:]:  # the first section is the library housekeeping
+        assert re.search(r"\.(py|cpp):\d+", sec), sec.splitlines()[0]
+
+
+def test_product_package_does_not_import_the_oracle():
+    r = _run("import sys, dabsn_amd, dabsn_amd.kernels.ops, dabsn_amd.model\n"
+             "bad = [m for m in sys.modules if m == 'oracle' or m.startswith('oracle.')]\n"
+             "assert not bad, bad\nprint('ok')")
+    assert r.returncode == 0 and "ok" in r.stdout, r.stderr
+    src = "\n".join(p.read_text() for p in (ROOT / "dabsn_amd").rglob("*.py"))
+    assert not re.search(r"^\s*(from|import)\s+oracle\b", src, flags=re.M)
+
+
+def test_cpu_tensors_raise_instead_of_falling_back():
+    code = (
+        "import torch\n"
+        "from dabsn_amd.kernels import ops\n"
+        "def expect_fail(fn, *a):\n"
+        "    try:\n"
+        "        fn(*a)\n"
+        "    except (RuntimeError, NotImplementedError) as e:\n"
+        "        return\n"
+        "    raise SystemExit('no error for ' + fn.__name__)\n"
+        "B, T, H = 2, 3, 8\n"
+        "x = torch.randn(B, T, H)\n"
+        "vec = [torch.zeros(H) for _ in range(16)]\n"
+        "sc = [torch.zeros(()) for _ in range(3)]\n"
+        "st = [torch.zeros(B, H) for _ in range(3)]\n"
+        "expect_fail(ops.core_scan_batched, x, x, torch.eye(H), torch.eye(H), *vec, *sc, *st)\n"
+        "expect_fail(ops.linear_recurrence, x, x, torch.zeros(B, H))\n"
+        "expect_fail(ops.bank_select, torch.randn(B, T), torch.tensor([1.0]))\n"
+        "expect_fail(ops.read_tape_stats, *[x] * 6)\n"
+        "print('ok')\n")
+    r = _run(code)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
+
+
+def test_enable_and_status_semantics_without_a_device():
+    code = (
+        "import torch, dabsn_amd\n"
+        "from dabsn_amd import kernels\n"
+        "assert not torch.cuda.is_available()\n"
+        "try:\n"
+        "    kernels.enable('tpu')\n"
+        "    raise SystemExit('bad backend accepted')\n"
+        "except ValueError:\n"
+        "    pass\n"
+        "try:\n"
+        "    kernels.enable('rocm', required=True)\n"
+        "    raise SystemExit('required backend did not raise')\n"
+        "except RuntimeError as e:\n"
+        "    assert 'unavailable' in str(e)\n"
+        "st = kernels.enable('auto')\n"
+        "assert st['active_backend'] == 'none' and st['device_available'] is False\n"
+        "assert set(st['rocm']) >= {'library', 'library_loaded', 'abi_version', 'operators'}\n"
+        "names = {p['name'] for p in st['primitives']}\n"
+        "assert {'core_scan', 'admitted_three_way_read', 'recurrent_long_read'} <= names, names\n"
+        "print('ok')\n")
+    r = _run(code)
+    if r.returncode != 0 and "assert not torch.cuda.is_available()" in r.stderr:
+        pytest.skip("a device is visible; this test covers the CPU-only path")
+    assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
+
+
+def test_routing_events_once_and_strict_fallback():
+    from dabsn_amd import events
+
+    seen = []
+    events.reset_routing_log()
+    events.add_event_listener(seen.append)
+    try:
+        events.log_routing_once("core", "rocm", B=2, T=3)
+        events.log_routing_once("core", "rocm", B=2, T=3)
+        events.log_routing_once("core", "rocm", B=2, T=4)
+        assert [e.code for e in seen] == [events.EventCode.KERNEL_SELECTION] * 2
+        with pytest.raises(ValueError):
+            events.emit_event(events.EventCode.PERFORMANCE_FALLBACK, fallback=True, reason="x")
+        with events.strict_events():
+            with pytest.raises(events.StrictFallbackError):
+                events.warn_routing_once("read", "bank too wide", requested_path="rocm_native")
+        events.warn_routing_once("read", "other", requested_path="rocm_native")
+        assert seen[-1].fallback and seen[-1].fields["corrective_action"]
+    finally:
+        events.remove_event_listener(seen.append)
+        events.reset_routing_log()

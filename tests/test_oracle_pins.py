@@ -17,7 +17,13 @@ import torch
 import oracle
 from oracle import autograd_ref as ar
 
-torch.set_default_dtype(torch.float64)
+@pytest.fixture(autouse=True)
+def _fp64_default():
+    """fp64 factory default inside this module only (restored for other modules)."""
+    previous = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(previous)
 
 
 def _core_case(seed, B, T, H, din=None, scale_params=0.3):
