@@ -118,6 +118,32 @@ def step(model, Wx, Wgx, gy, gr, device_type, dtype):
     torch.autograd.backward([y, read.to(dtype)], [gy, gr])
 
 
+PMC_FILE = os.path.join(ROOT, "profiles", "core_scan_config4_pmc.json")
+
+
+def measured_traffic(kernel: str, args, chunk: int):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (copy-kernel calibrated), when it was measured on this workload and kernel."""
+    try:
+        with open(PMC_FILE) as fh:
+            doc = json.load(fh)
+    except OSError:
+        return None, None
+    w = doc.get("workload", {})
+    if (w.get("batch"), w.get("seq_len"), w.get("state"), w.get("chunk_t")) != (
+            args.batch, args.seq, args.state, chunk):
+        return None, None
+    entry = doc.get("kernels", {}).get(kernel)
+    if not entry:
+        return None, None
+    from dabsn_amd.kernels import ops
+
+    symbol = ops.kernel_symbol(kernel, args.batch, args.state)
+    if symbol is not None and symbol != entry.get("kernel_symbol"):
+        return None, None  # the counters were taken on a different kernel configuration
+    return int(entry["traffic_bytes"]), "profiles/core_scan_config4_pmc.md"
+
+
 def cpu_baseline(args):
     """The oracle (C restatement of the reference CPU backend, fp32, OpenMP over batch)
     running the same scan+read step on a bounded sample: config-4 widths, T=cpu_seq."""
@@ -201,9 +227,11 @@ def main():
         launch_tokens = args.batch * chunk
         alg_bytes = per_token[dom] * launch_tokens + weights_bytes
         achieved = alg_bytes / (kernels[dom]["avg_ms"] / 1e3) / 1e9
+        traffic, traffic_src = measured_traffic(dom, args, chunk)
         roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 2),
                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
-                    "traffic": None, "alg_bytes_per_launch": alg_bytes,
+                    "traffic": traffic, "traffic_source": traffic_src,
+                    "alg_bytes_per_launch": alg_bytes,
                     "avg_launch_ms": round(kernels[dom]["avg_ms"], 4),
                     "launch_tokens": launch_tokens}
     else:

@@ -39,6 +39,8 @@ _SIGNATURES = {
     "dabsn_hip_zero": ([vp, sz, vp], i32),
     "dabsn_hip_core_scan_workspace_bytes": ([i32, i64, i64, i32], sz),
     "dabsn_hip_core_scan_layout": ([i32, i64, i64, ctypes.POINTER(i64), ctypes.POINTER(i64)], i32),
+    "dabsn_hip_core_scan_config": (
+        [i32, i64, i64, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i32)], i32),
     "dabsn_hip_core_scan_fwd": (
         [i32, i64, i64, i64, vp, vp, vp, ctypes.POINTER(CoreParams), vp, vp, vp]
         + [vp] * 8 + [vp, vp, vp, vp, sz, vp],

@@ -992,6 +992,18 @@ int dabsn_hip_core_scan_layout(int dtype, int64_t B, int64_t H, int64_t* nbg, in
   return DABSN_OK;
 }
 
+int dabsn_hip_core_scan_config(int dtype, int64_t B, int64_t H, int* ch, int* ksteps, int* waves) {
+  const Cfg c = pick(dtype, B, H);
+  if (c.ksteps == 0) {
+    dabsn::set_error("core scan: unsupported H=%lld", (long long)H);
+    return DABSN_ERR_UNSUPPORTED;
+  }
+  if (ch) *ch = c.ch;
+  if (ksteps) *ksteps = c.ksteps;
+  if (waves) *waves = c.nw;
+  return DABSN_OK;
+}
+
 int dabsn_hip_core_scan_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* Wx,
                             const void* Wgx, const void* GA, const dabsn_core_params* params,
                             const float* b0, const float* e0, const float* c0, void* U, void* nov,

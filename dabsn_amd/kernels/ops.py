@@ -808,6 +808,21 @@ torch.library.register_autograd("dabsn::admitted_three_way_read_compact_flash", 
                                 setup_context=_read_setup)
 
 
+def kernel_symbol(kernel: str, B: int, H: int, dtype: torch.dtype = torch.bfloat16) -> Optional[str]:
+    """Profiler symbol of the core-scan kernel instance used for (B, H, dtype)."""
+    if kernel not in ("core_scan_fwd", "core_scan_bwd"):
+        return None
+    lib = _lib.load()
+    ch, ks, nw = _lib.i32(), _lib.i32(), _lib.i32()
+    if lib.dabsn_hip_core_scan_config(_code(dtype), B, H, ctypes.byref(ch), ctypes.byref(ks),
+                                      ctypes.byref(nw)) != 0:
+        return None
+    e = "unsigned short" if dtype == torch.bfloat16 else "float"
+    which, args = ("fwd", "FwdArgs") if kernel == "core_scan_fwd" else ("bwd", "BwdArgs")
+    return (f"void dabsn::core::core_{which}_kernel<{e}, {ch.value}, {ks.value}, {nw.value}>"
+            f"(dabsn::core::{args}<{e}>)")
+
+
 OPERATORS = (
     "dabsn::core_scan_batched",
     "dabsn::_core_scan_batched_backward",

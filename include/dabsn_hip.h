@@ -51,6 +51,10 @@ size_t dabsn_hip_core_scan_workspace_bytes(int dtype, int64_t B, int64_t H, int 
  * part_scal ([nwg][3]) in the backward. */
 int dabsn_hip_core_scan_layout(int dtype, int64_t B, int64_t H, int64_t* nbg, int64_t* nwg);
 
+/* Launch configuration chosen for (dtype, B, H): channels per workgroup, MFMA k-steps per
+ * wave and waves per workgroup (names the kernel instance in profiler output). */
+int dabsn_hip_core_scan_config(int dtype, int64_t B, int64_t H, int* ch, int* ksteps, int* waves);
+
 /* Forward. Wx, Wgx [B,T,H]; GA = [Ug; A] as [2H,H]; b0, e0, c0 [B,H] fp32.
  * Outputs: U [B,T,2H] (y, next budget), nov, plast, expr, write, energy (pre-update),
  * sat (post-update), gate [B,T,H]; final state bF, eF, cF [B,H] fp32. */
