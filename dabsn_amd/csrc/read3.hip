@@ -13,6 +13,10 @@
 //   out = P_V V + P_Vn Vn            one MFMA GEMM over both products
 // Backward recomputes S and the row statistics, forms dP = gO V^T, gO Vn^T, the score
 // gradient G row by row, then gQ = G K, gK = G^T Q, gV = P_V^T gO, gVn = P_Vn^T gO.
+// Every GEMM runs with both operands K-contiguous: operands whose natural layout is not
+// (V, Vn, K for the products over slots; G, P_V, P_Vn, Q, gO for the products over
+// queries) are first transposed into the workspace, which costs one extra read and write
+// of each instead of transposing element by element inside every GEMM tile.
 // Tile ranges follow the causal staircase: a query tile only visits bank slots that
 // any of its queries may read; a bank tile only visits queries at or after its
 // earliest admitted index.
@@ -20,6 +24,7 @@
 #include "capi.hpp"
 #include "common.hpp"
 #include "gemm.hpp"
+#include "transpose.hpp"
 
 namespace dabsn {
 namespace read3 {
@@ -369,14 +374,14 @@ __global__ void reduce_final_kernel(int nblocks, const float* part, float* out5)
 
 // Workspace planning.
 struct Plan {
-  size_t off_S, off_rs, off_ro, off_rb, off_stats, off_PV, off_PVn, end_fwd;
-  size_t off_dPV, off_dPVn, off_Gs, off_rowA, off_rowB, off_colp, off_part, end_bwd;
+  size_t off_S, off_rs, off_ro, off_rb, off_stats, off_PV, off_PVn, off_VT, off_VnT, end_fwd;
+  size_t off_dPV, off_dPVn, off_Gs, off_rowA, off_rowB, off_colp, off_part, off_KT, off_QT,
+      off_gOT, off_GsT, off_PVT, off_PVnT, end_bwd;
 };
 
 static size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 static Plan plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
-  (void)H;
   Plan p{};
   const size_t e = dtype == kBF16 ? 2 : 4;
   const size_t QT = (T + TILE - 1) / TILE, BT = (N + TILE - 1) / TILE;
@@ -389,6 +394,9 @@ static Plan plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
   p.off_stats = o; o = align_up(o + static_cast<size_t>(B) * T * 6 * 4);
   p.off_PV = o; o = align_up(o + TN * e);
   p.off_PVn = o; o = align_up(o + TN * e);
+  const size_t NH = static_cast<size_t>(B) * N * H, TH = static_cast<size_t>(B) * T * H;
+  p.off_VT = o; o = align_up(o + NH * e);
+  p.off_VnT = o; o = align_up(o + NH * e);
   p.end_fwd = o;
   const size_t NCC = (N + CC - 1) / CC, RTILES = (T + RT - 1) / RT;
   p.off_dPV = o; o = align_up(o + TN * 4);
@@ -398,6 +406,12 @@ static Plan plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
   p.off_rowB = o; o = align_up(o + static_cast<size_t>(B) * T * NCC * 6 * 4);
   p.off_colp = o; o = align_up(o + static_cast<size_t>(B) * RTILES * N * 5 * 4);
   p.off_part = o; o = align_up(o + ((static_cast<size_t>(B) * T + NTH - 1) / NTH) * 5 * 4);
+  p.off_KT = o; o = align_up(o + NH * e);
+  p.off_QT = o; o = align_up(o + TH * e);
+  p.off_gOT = o; o = align_up(o + TH * e);
+  p.off_GsT = o; o = align_up(o + TN * e);
+  p.off_PVT = o; o = align_up(o + TN * e);
+  p.off_PVnT = o; o = align_up(o + TN * e);
   p.end_bwd = o;
   return p;
 }
@@ -436,15 +450,19 @@ static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, 
   DABSN_HIP_CHECK(hipGetLastError());
   if (!write_p) return DABSN_OK;
   {
-    gemm::Args<E, E> a{};
+    E* VT = reinterpret_cast<E*>(ws + p.off_VT);
+    E* VnT = reinterpret_cast<E*>(ws + p.off_VnT);
+    DABSN_HIP_CHECK(xpose::transpose<E>(V, VT, (int)B, (int)N, (int)H, stream));
+    DABSN_HIP_CHECK(xpose::transpose<E>(Vn, VnT, (int)B, (int)N, (int)H, stream));
+    gemm::Args<E, E> a{};  // out = P_V V + P_Vn Vn, B operands as V^T [H][N]
     a.M = (int)T; a.N = (int)H; a.K = (int)N;
     a.A = PV; a.lda = N; a.sA = T * N;
-    a.B = V; a.ldb = H; a.sB = N * H;
-    a.A2 = PVn; a.B2 = Vn;
+    a.B = VT; a.ldb = N; a.sB = H * N;
+    a.A2 = PVn; a.B2 = VnT;
     a.C = out; a.ldc = H; a.sC = T * H;
     a.alpha = 1.0f; a.beta = 0.0f;
     a.ranges = ro; a.mtiles = QT;
-    DABSN_HIP_CHECK((gemm::launch<E, E, false, false>(a, (int)B, stream)));
+    DABSN_HIP_CHECK((gemm::launch<E, E, false, true>(a, (int)B, stream)));
   }
   return DABSN_OK;
 }
@@ -494,28 +512,43 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
                        g, scale, rs, stats, rowA, dPV, dPVn, Gs, PV, PVn, rowB, colp);
     DABSN_HIP_CHECK(hipGetLastError());
   }
+  E* KT = reinterpret_cast<E*>(ws + p.off_KT);
+  E* QTr = reinterpret_cast<E*>(ws + p.off_QT);
+  E* gOT = reinterpret_cast<E*>(ws + p.off_gOT);
+  E* GsT = reinterpret_cast<E*>(ws + p.off_GsT);
+  E* PVT = reinterpret_cast<E*>(ws + p.off_PVT);
+  E* PVnT = reinterpret_cast<E*>(ws + p.off_PVnT);
+  DABSN_HIP_CHECK(xpose::transpose<E>(K, KT, (int)B, (int)N, (int)H, stream));
+  DABSN_HIP_CHECK(xpose::transpose<E>(q, QTr, (int)B, (int)T, (int)H, stream));
+  DABSN_HIP_CHECK(xpose::transpose<E>(gout, gOT, (int)B, (int)T, (int)H, stream));
+  DABSN_HIP_CHECK(xpose::transpose<E>(Gs, GsT, (int)B, (int)T, (int)N, stream));
+  DABSN_HIP_CHECK(xpose::transpose<E>(PV, PVT, (int)B, (int)T, (int)N, stream));
+  DABSN_HIP_CHECK(xpose::transpose<E>(PVn, PVnT, (int)B, (int)T, (int)N, stream));
   {
-    gemm::Args<E, E> a{};  // gQ = Gs K
+    gemm::Args<E, E> a{};  // gQ = Gs K, B operand as K^T [H][N]
     a.M = (int)T; a.N = (int)H; a.K = (int)N;
     a.A = Gs; a.lda = N; a.sA = T * N;
-    a.B = K; a.ldb = H; a.sB = N * H;
+    a.B = KT; a.ldb = N; a.sB = H * N;
     a.C = gq; a.ldc = H; a.sC = T * H;
     a.alpha = 1.0f;
     a.ranges = ro; a.mtiles = QT;
-    DABSN_HIP_CHECK((gemm::launch<E, E, false, false>(a, (int)B, stream)));
+    DABSN_HIP_CHECK((gemm::launch<E, E, false, true>(a, (int)B, stream)));
   }
-  const E* lhs[3] = {Gs, PV, PVn};
-  const E* rhs[3] = {q, gout, gout};
+  // Entries of G, P_V, P_Vn the GEMMs read (rows t >= the bank tile's earliest query,
+  // whole 128-slot tiles below roundup(nhi)) are all written by grad_tile_kernel; the
+  // transposes copy them unchanged.
+  const E* lhs[3] = {GsT, PVT, PVnT};
+  const E* rhs[3] = {QTr, gOT, gOT};
   E* dst[3] = {gK, gV, gVn};
   for (int w = 0; w < 3; ++w) {
-    gemm::Args<E, E> a{};  // gK = Gs^T Q, gV = P_V^T gO, gVn = P_Vn^T gO
+    gemm::Args<E, E> a{};  // gK = Gs^T Q, gV = P_V^T gO, gVn = P_Vn^T gO over k = t
     a.M = (int)N; a.N = (int)H; a.K = (int)T;
-    a.A = lhs[w]; a.lda = N; a.sA = T * N;
-    a.B = rhs[w]; a.ldb = H; a.sB = T * H;
+    a.A = lhs[w]; a.lda = T; a.sA = N * T;
+    a.B = rhs[w]; a.ldb = T; a.sB = H * T;
     a.C = dst[w]; a.ldc = H; a.sC = N * H;
     a.alpha = 1.0f;
     a.ranges = rb; a.mtiles = BT;
-    DABSN_HIP_CHECK((gemm::launch<E, E, true, false>(a, (int)B, stream)));
+    DABSN_HIP_CHECK((gemm::launch<E, E, false, true>(a, (int)B, stream)));
   }
   if (N > 0) {
     hipLaunchKernelGGL(reduce_cols_kernel, dim3((unsigned)((N + NTH - 1) / NTH), (unsigned)B),
