@@ -46,44 +46,64 @@ __device__ __forceinline__ bool induct_at(int mode, int64_t idx, bool valid, int
 }
 
 // Per query tile: nhi = 1 + max allowed slot of the tile's last query; per bank tile:
-// tlo = earliest query that may read any slot of the tile.
-__global__ void ranges_kernel(int T, int N, int H, int mode, const int64_t* idx,
-                              const uint8_t* valid, int32_t* rs, int32_t* ro, int32_t* rb) {
+// tlo = earliest query that may read any slot of the tile. One workgroup per tile, the
+// slots split over its threads and combined with a wave/LDS max (min) reduction.
+__global__ void __launch_bounds__(256) ranges_kernel(int T, int N, int H, int mode,
+                                                     const int64_t* idx, const uint8_t* valid,
+                                                     int32_t* rs, int32_t* ro, int32_t* rb) {
+  __shared__ int sh[4];
   const int b = blockIdx.y;
   const int QT = (T + TILE - 1) / TILE, BT = (N + TILE - 1) / TILE;
-  const int item = blockIdx.x * blockDim.x + threadIdx.x;
+  const int item = blockIdx.x;
   const int64_t* ib = idx + static_cast<size_t>(b) * N;
   const uint8_t* vb = valid + static_cast<size_t>(b) * N;
-  if (item < QT) {
+  const bool query_tile = item < QT;
+  int v;
+  if (query_tile) {
     const int tl = min(T - 1, item * TILE + TILE - 1);
-    int nhi = 0;
-    for (int j = 0; j < N; ++j)
-      if (allow_at(mode, ib[j], vb[j] != 0, tl)) nhi = j + 1;
-    int32_t* s = rs + (static_cast<size_t>(b) * QT + item) * 3;
-    s[0] = 0; s[1] = H; s[2] = nhi;
-    int32_t* o = ro + (static_cast<size_t>(b) * QT + item) * 3;
-    o[0] = 0; o[1] = nhi; o[2] = H;
-  } else if (item < QT + BT) {
+    v = 0;
+    for (int j = threadIdx.x; j < N; j += blockDim.x)
+      if (allow_at(mode, ib[j], vb[j] != 0, tl)) v = j + 1;
+  } else {
     const int bt = item - QT;
-    int64_t tlo = T;
-    for (int j = bt * TILE; j < min(N, bt * TILE + TILE); ++j) {
+    v = T;
+    for (int j = bt * TILE + threadIdx.x; j < min(N, bt * TILE + TILE); j += blockDim.x) {
       if (!vb[j]) continue;
       const int64_t first = mode != 0 ? 0 : (ib[j] < 0 ? 0 : ib[j]);
-      tlo = first < tlo ? first : tlo;
+      v = first < v ? static_cast<int>(first) : v;
     }
-    int32_t* r = rb + (static_cast<size_t>(b) * BT + bt) * 3;
-    r[0] = static_cast<int32_t>(tlo); r[1] = T; r[2] = H;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const int o = __shfl_xor(v, m, 64);
+    v = query_tile ? max(v, o) : min(v, o);
+  }
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  v = sh[0];
+  for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) v = query_tile ? max(v, sh[w]) : min(v, sh[w]);
+  if (query_tile) {
+    int32_t* s = rs + (static_cast<size_t>(b) * QT + item) * 3;
+    s[0] = 0; s[1] = H; s[2] = v;
+    int32_t* o = ro + (static_cast<size_t>(b) * QT + item) * 3;
+    o[0] = 0; o[1] = v; o[2] = H;
+  } else {
+    int32_t* r = rb + (static_cast<size_t>(b) * BT + (item - QT)) * 3;
+    r[0] = v; r[1] = T; r[2] = H;
   }
 }
 
-__device__ __forceinline__ float block_max(float v, float* sh) {
+__device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
 }
+
+// Waves per workgroup of the row kernels; per-row partials of the score gradient are
+// kept per (column chunk, wave) and summed by reduce_rows_kernel.
+constexpr int NWV = NTH / 64;
+
 __device__ __forceinline__ float block_sum(float v, float* sh) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
@@ -117,15 +137,40 @@ __device__ __forceinline__ void scores(const RowCtx& c, int b, int t, int j, con
   s_perm = content + cc * c.cg + c.adm[bj];
 }
 
-// Row statistics (max and sum of each masked softmax), one workgroup per query row.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// Online (max, sum) update of one softmax with score x.
+__device__ __forceinline__ void online_add(float x, float& m, float& l) {
+  if (x > m) {
+    l = l * expf(m - x) + 1.0f;  // m = -inf gives l * 0 + 1
+    m = x;
+  } else {
+    l += expf(x - m);
+  }
+}
+
+// Combine the per-lane (max, sum) of one softmax across the wave.
+__device__ __forceinline__ void wave_softmax_stats(float& m, float& l) {
+  const float M = wave_max(m);
+  l = (m == -INFINITY) ? 0.0f : l * expf(m - M);
+  l = wave_sum(l);
+  m = M;
+}
+
+// Row statistics (max and sum of each masked softmax), one wave per query row.
 // stats[row] = (m_s, l_s, m_p, l_p, m_i, l_i); l = 0 marks an empty pathway.
 // When P_V is non-null also writes P_V / P_Vn for j < nhi of the row's tile.
 template <typename E>
-__global__ void __launch_bounds__(NTH) softmax_fwd_kernel(RowCtx c, Gains g, const float* scale_p,
-                                                          const int32_t* rs, float* stats, E* PV,
-                                                          E* PVn) {
-  __shared__ float sh[4];
-  const int64_t row = blockIdx.x;
+__global__ void __launch_bounds__(NTH) softmax_fwd_kernel(int64_t rows, RowCtx c, Gains g,
+                                                          const float* scale_p, const int32_t* rs,
+                                                          float* stats, E* PV, E* PVn) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * NWV + (threadIdx.x >> 6);
+  if (row >= rows) return;
   const int b = static_cast<int>(row / c.T), t = static_cast<int>(row % c.T);
   c.scale = scale_p[0];
   c.sg = g.p[0][0]; c.pg = g.p[1][0]; c.ig = g.p[2][0]; c.cg = g.p[3][0];
@@ -134,40 +179,27 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_kernel(RowCtx c, Gains g, con
   const float* ckt = c.ck + static_cast<size_t>(row) * 4;
   const int64_t* ib = c.idx + static_cast<size_t>(b) * c.N;
   const uint8_t* vb = c.valid + static_cast<size_t>(b) * c.N;
-  float ms = -INFINITY, mp = -INFINITY, mi = -INFINITY;
-  for (int j = threadIdx.x; j < nhi; j += NTH) {
+  float ms = -INFINITY, mp = -INFINITY, mi = -INFINITY, ls = 0.f, lp = 0.f, li = 0.f;
+  for (int j = lane; j < nhi; j += 64) {
     float ss, sp, cc, sr;
     scores(c, b, t, j, ckt, ss, sp, cc, sr);
     if (allow_at(c.mode, ib[j], vb[j] != 0, t)) {
-      ms = fmaxf(ms, ss);
-      mp = fmaxf(mp, sp);
+      online_add(ss, ms, ls);
+      online_add(sp, mp, lp);
     }
-    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) mi = fmaxf(mi, ss);
+    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) online_add(ss, mi, li);
   }
-  ms = block_max(ms, sh);
-  mp = block_max(mp, sh);
-  mi = block_max(mi, sh);
-  float ls = 0.f, lp = 0.f, li = 0.f;
-  for (int j = threadIdx.x; j < nhi; j += NTH) {
-    float ss, sp, cc, sr;
-    scores(c, b, t, j, ckt, ss, sp, cc, sr);
-    if (allow_at(c.mode, ib[j], vb[j] != 0, t)) {
-      ls += expf(ss - ms);
-      lp += expf(sp - mp);
-    }
-    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) li += expf(ss - mi);
-  }
-  ls = block_sum(ls, sh);
-  lp = block_sum(lp, sh);
-  li = block_sum(li, sh);
-  if (threadIdx.x == 0) {
+  wave_softmax_stats(ms, ls);
+  wave_softmax_stats(mp, lp);
+  wave_softmax_stats(mi, li);
+  if (lane == 0) {
     float* o = stats + static_cast<size_t>(row) * 6;
     o[0] = ms; o[1] = ls; o[2] = mp; o[3] = lp; o[4] = mi; o[5] = li;
   }
   if (PV == nullptr) return;
   const float is = ls > 0.f ? 1.0f / ls : 0.f, ip = lp > 0.f ? 1.0f / lp : 0.f,
               ii = li > 0.f ? 1.0f / li : 0.f;
-  for (int j = threadIdx.x; j < nhi; j += NTH) {
+  for (int j = lane; j < nhi; j += 64) {
     float ss, sp, cc, sr;
     scores(c, b, t, j, ckt, ss, sp, cc, sr);
     float pv = 0.f, pn = 0.f;
@@ -180,13 +212,15 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_kernel(RowCtx c, Gains g, con
 }
 
 // Per-row reductions needed by the score gradient: rs = sum Ps dPV, rp = sum Pp dPV,
-// ri = sum Pi dPVn (unscaled by the gains).
-__global__ void __launch_bounds__(NTH) grad_rows_kernel(RowCtx c, Gains g, const float* scale_p,
+// ri = sum Pi dPVn (unscaled by the gains). One wave per query row.
+__global__ void __launch_bounds__(NTH) grad_rows_kernel(int64_t rows, RowCtx c, Gains g,
+                                                        const float* scale_p,
                                                         const int32_t* rs_rng, const float* stats,
                                                         const float* dPV, const float* dPVn,
                                                         float* rowA) {
-  __shared__ float sh[4];
-  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * NWV + (threadIdx.x >> 6);
+  if (row >= rows) return;
   const int b = static_cast<int>(row / c.T), t = static_cast<int>(row % c.T);
   c.scale = scale_p[0];
   c.cg = g.p[3][0];
@@ -199,7 +233,7 @@ __global__ void __launch_bounds__(NTH) grad_rows_kernel(RowCtx c, Gains g, const
   const int64_t* ib = c.idx + static_cast<size_t>(b) * c.N;
   const uint8_t* vb = c.valid + static_cast<size_t>(b) * c.N;
   float rsum = 0.f, psum = 0.f, isum = 0.f;
-  for (int j = threadIdx.x; j < nhi; j += NTH) {
+  for (int j = lane; j < nhi; j += 64) {
     float ss, sp, cc, sr;
     scores(c, b, t, j, ckt, ss, sp, cc, sr);
     const size_t o = static_cast<size_t>(row) * c.N + j;
@@ -210,25 +244,24 @@ __global__ void __launch_bounds__(NTH) grad_rows_kernel(RowCtx c, Gains g, const
     }
     if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) isum += expf(ss - st6[4]) * ii * dPVn[o];
   }
-  rsum = block_sum(rsum, sh);
-  psum = block_sum(psum, sh);
-  isum = block_sum(isum, sh);
-  if (threadIdx.x == 0) {
+  rsum = wave_sum(rsum);
+  psum = wave_sum(psum);
+  isum = wave_sum(isum);
+  if (lane == 0) {
     float* o = rowA + static_cast<size_t>(row) * 3;
     o[0] = rsum; o[1] = psum; o[2] = isum;
   }
 }
 
 // Score gradient for a tile of RT rows x CC columns. Writes Gs = scale*G, P_V, P_Vn;
-// per-(row, column chunk) partials rowB = (G.S, dSp.cc, cg dSp cb[0..3]) and per-(row
-// tile, column) partials colp = (sum G, cg sum dSp ck[0..3]).
+// per-(row, column chunk, wave) partials rowB = (G.S, dSp.cc, cg dSp cb[0..3]) and
+// per-(row tile, column) partials colp = (sum G, cg sum dSp ck[0..3]).
 template <typename E>
 __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const float* scale_p,
                                                         const int32_t* rs_rng, const float* stats,
                                                         const float* rowA, const float* dPV,
                                                         const float* dPVn, E* Gs, E* PV, E* PVn,
                                                         float* rowB, float* colp) {
-  __shared__ float sh[4];
   constexpr int CJ = CC / NTH;
   const int b = blockIdx.z, rt = blockIdx.y, cch = blockIdx.x;
   const int NCC = (c.N + CC - 1) / CC;
@@ -294,14 +327,14 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
       colC[q][0] += w * ckt[0]; colC[q][1] += w * ckt[1];
       colC[q][2] += w * ckt[2]; colC[q][3] += w * ckt[3];
     }
-    gsc = block_sum(gsc, sh);
-    gcg = block_sum(gcg, sh);
-    gk0 = block_sum(gk0, sh);
-    gk1 = block_sum(gk1, sh);
-    gk2 = block_sum(gk2, sh);
-    gk3 = block_sum(gk3, sh);
-    if (threadIdx.x == 0) {
-      float* o = rowB + (row * NCC + cch) * 6;
+    gsc = wave_sum(gsc);
+    gcg = wave_sum(gcg);
+    gk0 = wave_sum(gk0);
+    gk1 = wave_sum(gk1);
+    gk2 = wave_sum(gk2);
+    gk3 = wave_sum(gk3);
+    if ((threadIdx.x & 63) == 0) {
+      float* o = rowB + ((row * NCC + cch) * NWV + (threadIdx.x >> 6)) * 6;
       o[0] = gsc; o[1] = gcg; o[2] = gk0; o[3] = gk1; o[4] = gk2; o[5] = gk3;
     }
   }
@@ -344,8 +377,8 @@ __global__ void reduce_rows_kernel(int64_t rows, int NCC, const float* rowA, con
   float v[5] = {0.f, 0.f, 0.f, 0.f, 0.f};  // scale, short, pad, induct, cocktail
   if (row < rows) {
     float k4[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int cc = 0; cc < NCC; ++cc) {
-      const float* p = rowB + (static_cast<size_t>(row) * NCC + cc) * 6;
+    for (int cc = 0; cc < NCC * NWV; ++cc) {
+      const float* p = rowB + (static_cast<size_t>(row) * NCC * NWV + cc) * 6;
       v[0] += p[0];
       v[4] += p[1];
 #pragma unroll
@@ -403,7 +436,7 @@ static Plan plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
   p.off_dPVn = o; o = align_up(o + TN * 4);
   p.off_Gs = o; o = align_up(o + TN * e);
   p.off_rowA = o; o = align_up(o + static_cast<size_t>(B) * T * 3 * 4);
-  p.off_rowB = o; o = align_up(o + static_cast<size_t>(B) * T * NCC * 6 * 4);
+  p.off_rowB = o; o = align_up(o + static_cast<size_t>(B) * T * NCC * NWV * 6 * 4);
   p.off_colp = o; o = align_up(o + static_cast<size_t>(B) * RTILES * N * 5 * 4);
   p.off_part = o; o = align_up(o + ((static_cast<size_t>(B) * T + NTH - 1) / NTH) * 5 * 4);
   p.off_KT = o; o = align_up(o + NH * e);
@@ -430,7 +463,7 @@ static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, 
   float* stats = reinterpret_cast<float*>(ws + p.off_stats);
   E* PV = reinterpret_cast<E*>(ws + p.off_PV);
   E* PVn = reinterpret_cast<E*>(ws + p.off_PVn);
-  hipLaunchKernelGGL(ranges_kernel, dim3((QT + BT + 63) / 64, (unsigned)B), dim3(64), 0, stream,
+  hipLaunchKernelGGL(ranges_kernel, dim3((unsigned)(QT + BT), (unsigned)B), dim3(256), 0, stream,
                      (int)T, (int)N, (int)H, mode, idx, valid, rs, ro, rb);
   DABSN_HIP_CHECK(hipGetLastError());
   {
@@ -444,7 +477,8 @@ static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, 
     DABSN_HIP_CHECK((gemm::launch<E, float, false, true>(a, (int)B, stream)));
   }
   RowCtx c{(int)T, (int)N, mode, S, kb, adm, cb, ck, idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
-  hipLaunchKernelGGL(softmax_fwd_kernel<E>, dim3((unsigned)(B * T)), dim3(NTH), 0, stream, c, g,
+  const unsigned row_blocks = static_cast<unsigned>((B * T + NWV - 1) / NWV);
+  hipLaunchKernelGGL(softmax_fwd_kernel<E>, dim3(row_blocks), dim3(NTH), 0, stream, B * T, c, g,
                      scale, rs, stats, write_p ? PV : static_cast<E*>(nullptr),
                      write_p ? PVn : static_cast<E*>(nullptr));
   DABSN_HIP_CHECK(hipGetLastError());
@@ -503,8 +537,8 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
     DABSN_HIP_CHECK((gemm::launch<E, float, false, true>(a, (int)B, stream)));
   }
   RowCtx c{(int)T, (int)N, mode, S, kb, adm, cb, ck, idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
-  hipLaunchKernelGGL(grad_rows_kernel, dim3((unsigned)(B * T)), dim3(NTH), 0, stream, c, g, scale,
-                     rs, stats, dPV, dPVn, rowA);
+  hipLaunchKernelGGL(grad_rows_kernel, dim3((unsigned)((B * T + NWV - 1) / NWV)), dim3(NTH), 0,
+                     stream, B * T, c, g, scale, rs, stats, dPV, dPVn, rowA);
   DABSN_HIP_CHECK(hipGetLastError());
   const int NCC = static_cast<int>((N + CC - 1) / CC), RTILES = static_cast<int>((T + RT - 1) / RT);
   if (N > 0) {
