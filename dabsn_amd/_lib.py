@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib = None
@@ -54,10 +54,12 @@ _SIGNATURES = {
     "dabsn_hip_linrec_fwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_linrec_workspace_bytes": ([i32, i64, i64, i64], sz),
     "dabsn_hip_linrec_bwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
-    "dabsn_hip_long_fwd": ([i32, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),
-    "dabsn_hip_long_partials": ([i64, i64], i64),
+    "dabsn_hip_long_workspace_bytes": ([i64, i64, i64, i32], sz),
+    "dabsn_hip_long_fwd": (
+        [i32, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
+    "dabsn_hip_long_partials": ([i64, i64, i64], i64),
     "dabsn_hip_long_bwd": (
-        [i32, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+        [i32, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp],
         i32,
     ),
     "dabsn_hip_tape_stats": ([i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),

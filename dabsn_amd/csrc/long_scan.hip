@@ -5,10 +5,20 @@
 // reverse), long.py:492-579 (long memory as three recurrences plus glue), loop form in
 // src/dabsn/read.py:625-636; CPU kernels cpu_runtime.cpp:92-143.
 //
-// Every (batch row, unit) channel is an independent scalar recurrence over time, so
-// one thread owns one channel and walks T; consecutive threads own consecutive units,
-// so each time step is one coalesced row access. Loads for a block of time steps are
-// issued before the dependent arithmetic so their latency overlaps.
+// linear_recurrence: one thread owns one (batch row, unit) channel and walks T;
+// consecutive threads own consecutive units, so each time step is one coalesced row
+// access, with a block of time steps loaded ahead of the dependent arithmetic.
+//
+// Long memory, parallel over time as well as channels. Per channel the forward is three
+// chained recurrences: E_t = er E + (1-er) w (constant coefficient), R_t = rd R +
+// (1-rd)(1 - pe_t) with pe_t = tanh|w_t - E_{t-1}| (constant coefficient, input known once
+// E is), and L_t = eff_t L + (1 - eff_t) sal_t w_t (coefficient eff_t known once R is).
+// T is cut into chunks of CK steps. For each recurrence in turn, a chunk-parallel pass
+// computes every chunk's end value from a zero start (plus the product of eff_t for L),
+// and a per-channel pass over the chunks turns those into the true chunk-start values
+// (a checkpoint in the workspace). A last chunk pass writes the output and, for the
+// backward, the states entering every step. The backward composes each chunk's affine map of the three adjoints (see the
+// backward kernels below) and carries the maps across chunks in one per-channel pass.
 #include "../../include/dabsn_hip.h"
 #include "capi.hpp"
 #include "common.hpp"
@@ -91,133 +101,308 @@ struct Logits {
   const float* p[4];
 };
 
-template <typename E>
-__global__ void __launch_bounds__(NT) long_fwd_kernel(int B, int T, int H, const E* w, const E* p,
-                                                      Logits lg, const float* L0, const float* E0,
-                                                      const float* R0, E* out, float* LF, float* EF,
-                                                      float* RF, float* ckpt) {
-  const int64_t ch = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
-  if (ch >= static_cast<int64_t>(B) * H) return;
+// er^n for n <= CK by repeated multiplication (fixed order).
+__device__ __forceinline__ float powi(float x, int n) {
+  float r = 1.0f;
+  for (int i = 0; i < n; ++i) r *= x;
+  return r;
+}
+
+struct ChunkIdx {
+  int64_t ch;       // b * H + h
+  int b, h, k, t0, len, nseg;
+  size_t base;      // offset of (b, 0, h) in [B, T, H]
+  size_t cbase;     // offset of (b, k, 0, h) in the checkpoint [B][nseg][3][H]
+};
+
+__device__ __forceinline__ bool chunk_idx(int B, int T, int H, ChunkIdx& c) {
+  c.ch = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
+  if (c.ch >= static_cast<int64_t>(B) * H) return false;
+  c.b = static_cast<int>(c.ch / H);
+  c.h = static_cast<int>(c.ch % H);
+  c.k = blockIdx.y;
+  c.t0 = c.k * CK;
+  c.len = min(CK, T - c.t0);
+  c.nseg = (T + CK - 1) / CK;
+  c.base = static_cast<size_t>(c.b) * T * H + c.h;
+  c.cbase = (static_cast<size_t>(c.b) * c.nseg + c.k) * 3 * H + c.h;
+  return true;
+}
+
+// Forward chunk pass. PHASE 0: E from 0 -> loc0 = E end. PHASE 1: E from its true start,
+// R from 0 -> loc0 = R end. PHASE 2: E, R from true starts, L from 0 -> loc0 = L end,
+// loc1 = prod eff. PHASE 3: all from true starts -> out, and (if `states` is given) the
+// states entering every step, [3][B][T][H] fp32 = (L, E, R)_{t-1}, for the backward.
+template <typename E, int PHASE>
+__global__ void __launch_bounds__(NT) long_fwd_chunk(int B, int T, int H, const E* w, const E* p,
+                                                     Logits lg, const float* ckpt, float* loc0,
+                                                     float* loc1, E* out, float* states) {
+  ChunkIdx c;
+  if (!chunk_idx(B, T, H, c)) return;
   const Coef k = load_coef(lg.p);
-  const int64_t b = ch / H, h = ch % H;
-  const size_t base = static_cast<size_t>(b) * T * H + h;
-  const int nseg = (T + CK - 1) / CK;
-  float L = L0[ch], Ev = E0[ch], R = R0[ch];
-  for (int t0 = 0; t0 < T; t0 += TB) {
-    if (ckpt && (t0 % CK) == 0) {
-      const size_t cbase = (static_cast<size_t>(b) * nseg + t0 / CK) * 3 * H + h;
-      ckpt[cbase] = L;
-      ckpt[cbase + H] = Ev;
-      ckpt[cbase + 2 * H] = R;
-    }
-    float wv[TB], pv[TB];
+  float wv[CK], pv[CK];
 #pragma unroll
-    for (int i = 0; i < TB; ++i) {
-      const int t = t0 + i;
-      wv[i] = t < T ? ld(w, base + static_cast<size_t>(t) * H) : 0.0f;
-      pv[i] = t < T ? ld(p, base + static_cast<size_t>(t) * H) : 0.0f;
-    }
+  for (int i = 0; i < CK; ++i) {
+    wv[i] = i < c.len ? ld(w, c.base + static_cast<size_t>(c.t0 + i) * H) : 0.0f;
+    if (PHASE >= 2) pv[i] = i < c.len ? ld(p, c.base + static_cast<size_t>(c.t0 + i) * H) : 0.0f;
+  }
+  float Ev = PHASE >= 1 ? ckpt[c.cbase + H] : 0.0f;
+  float R = PHASE >= 2 ? ckpt[c.cbase + 2 * H] : 0.0f;
+  float L = PHASE >= 3 ? ckpt[c.cbase] : 0.0f;
+  float prod = 1.0f;
+  const size_t bth = static_cast<size_t>(B) * T * H;
 #pragma unroll
-    for (int i = 0; i < TB; ++i) {
-      const int t = t0 + i;
-      if (t < T) {
-        const float pe = tanhf(fabsf(wv[i] - Ev));
+  for (int i = 0; i < CK; ++i) {
+    if (i < c.len) {
+      if (PHASE == 3 && states) {
+        const size_t o = c.base + static_cast<size_t>(c.t0 + i) * H;
+        states[o] = L;
+        states[bth + o] = Ev;
+        states[2 * bth + o] = R;
+      }
+      const float pe = PHASE >= 1 ? tanhf(fabsf(wv[i] - Ev)) : 0.0f;
+      Ev = k.er * Ev + (1.0f - k.er) * wv[i];
+      if (PHASE >= 1) R = k.rd * R + (1.0f - k.rd) * (1.0f - pe);
+      if (PHASE >= 2) {
         const float sal = pv[i] * pe;
-        Ev = k.er * Ev + (1.0f - k.er) * wv[i];
-        R = k.rd * R + (1.0f - k.rd) * (1.0f - pe);
         const float eff = k.ret + (1.0f - k.ret) * k.rs * R;
         L = eff * L + (1.0f - eff) * (sal * wv[i]);
-        st(out, base + static_cast<size_t>(t) * H, L);
+        prod *= eff;
+        if (PHASE == 3) st(out, c.base + static_cast<size_t>(c.t0 + i) * H, L);
       }
     }
   }
-  LF[ch] = L;
-  EF[ch] = Ev;
-  RF[ch] = R;
+  const size_t li = static_cast<size_t>(c.k) * B * H + c.ch;
+  if (PHASE == 0) loc0[li] = Ev;
+  if (PHASE == 1) loc0[li] = R;
+  if (PHASE == 2) {
+    loc0[li] = L;
+    loc1[li] = prod;
+  }
 }
 
-// Reverse scan. Segments of CK steps are replayed forward from their fp32 checkpoint
-// into registers (fully unrolled, so the per-step arrays stay in VGPRs), then walked
-// backward. Gradients w.r.t. the four logits are reduced per block (fixed order).
-template <typename E>
-__global__ void __launch_bounds__(NT) long_bwd_kernel(int B, int T, int H, const E* w, const E* p,
-                                                      Logits lg, const float* ckpt, const E* gout,
-                                                      const float* gLF, const float* gEF,
-                                                      const float* gRF, E* gw, E* gp, float* gL0,
-                                                      float* gE0, float* gR0, float* part) {
-  __shared__ float red[4][NT];
+// Per-channel pass over chunks for state S (0 = L, 1 = E, 2 = R): the chunk-start value
+// goes to the checkpoint slot S; the state after the last chunk to `fin`.
+// x_{k+1} = a_k x_k + loc[k] with a_k = prod[k] (L) or coef^len_k (E: er, R: rd).
+template <int S>
+__global__ void __launch_bounds__(NT) long_fwd_carry(int B, int T, int H, Logits lg,
+                                                     const float* x0, const float* loc,
+                                                     const float* prod, float* ckpt, float* fin) {
   const int64_t ch = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
-  const bool ok = ch < static_cast<int64_t>(B) * H;
+  if (ch >= static_cast<int64_t>(B) * H) return;
+  const Coef k = load_coef(lg.p);
+  const int b = static_cast<int>(ch / H), h = static_cast<int>(ch % H);
+  const int nseg = (T + CK - 1) / CK;
+  const float coef = S == 1 ? k.er : k.rd;
+  const float a_full = powi(coef, CK);
+  float x = x0[ch];
+  for (int kk = 0; kk < nseg; ++kk) {
+    ckpt[(static_cast<size_t>(b) * nseg + kk) * 3 * H + S * H + h] = x;
+    const size_t li = static_cast<size_t>(kk) * B * H + ch;
+    const int len = min(CK, T - kk * CK);
+    const float a = S == 0 ? prod[li] : (len == CK ? a_full : powi(coef, len));
+    x = a * x + loc[li];
+  }
+  fin[ch] = x;
+}
+
+// Backward. Walking time in reverse, one step maps the carried adjoints x = (gL, gR, gE)
+// (coming from step t + 1) to the ones leaving step t, affinely:
+//   gL' = eff (gL + g_t)
+//   gR' = rd gR + rd k a (gL + g_t)                          k = (1 - ret) rs, a = L_{t-1} - sal w
+//   gE' = er gE + s (1 - rd) gR + c (gL + g_t)               s = (1 - pe^2) sign(w - E_{t-1})
+//                                                              c = s ((1 - rd) k a - (1 - eff) w p)
+// i.e. x' = M_t (x + g_t e0) with M_t lower triangular. Over a chunk, x_out = A x_in + v
+// with A = M_0 ... M_{len-1} and v = sum_i (M_0 ... M_{i-1}) M_i g_i e0, both accumulated
+// in forward time order, so one forward pass over each chunk yields its map; a per-channel pass over the chunks then gives the exact
+// adjoints entering each chunk, and a last pass walks each chunk backward with those
+// adjoints to produce gw, gp and the logit partials. Both chunk passes read the forward
+// values around each step from the per-step states the forward wrote, so they stream
+// instead of replaying the recurrence.
+
+// Per-step coefficients of M_t from the forward values around step t.
+struct StepMap {
+  float m00, m10, m11, m20, m21, m22;
+};
+
+__device__ __forceinline__ StepMap step_map(const Coef& k, float wt, float pt, float Lp, float Ep,
+                                            float pe, float eff) {
+  const float kap = (1.0f - k.ret) * k.rs;
+  const float sal = pt * pe;
+  const float a = Lp - sal * wt;
+  const float sgn = (1.0f - pe * pe) * signf_(wt - Ep);
+  StepMap m;
+  m.m00 = eff;
+  m.m10 = k.rd * kap * a;
+  m.m11 = k.rd;
+  m.m20 = sgn * ((1.0f - k.rd) * kap * a - (1.0f - eff) * wt * pt);
+  m.m21 = sgn * (1.0f - k.rd);
+  m.m22 = k.er;
+  return m;
+}
+
+// Chunk maps: A (lower triangular, 6 entries) and v (3 entries), stored component-major
+// in `maps` [9][nseg][B*H]. The forward values around each step are read from `states`.
+template <typename E>
+__global__ void __launch_bounds__(NT) long_bwd_map(int B, int T, int H, const E* w, const E* p,
+                                                   Logits lg, const float* states, const E* gout,
+                                                   float* maps) {
+  ChunkIdx c;
+  if (!chunk_idx(B, T, H, c)) return;
+  const Coef k = load_coef(lg.p);
+  const size_t bth = static_cast<size_t>(B) * T * H;
+  float p00 = 1.f, p10 = 0.f, p11 = 1.f, p20 = 0.f, p21 = 0.f, p22 = 1.f;
+  float v0 = 0.f, v1 = 0.f, v2 = 0.f;
+  constexpr int LB = 8;  // steps loaded ahead
+  for (int i0 = 0; i0 < c.len; i0 += LB) {
+    float wv[LB], pv[LB], gv[LB], Lv[LB], Ev[LB], Rv[LB];
+#pragma unroll
+    for (int j = 0; j < LB; ++j) {
+      const int i = i0 + j;
+      const size_t o = c.base + static_cast<size_t>(c.t0 + i) * H;
+      const bool in = i < c.len;
+      wv[j] = in ? ld(w, o) : 0.0f;
+      pv[j] = in ? ld(p, o) : 0.0f;
+      gv[j] = in ? ld(gout, o) : 0.0f;
+      Lv[j] = in ? states[o] : 0.0f;
+      Ev[j] = in ? states[bth + o] : 0.0f;
+      Rv[j] = in ? states[2 * bth + o] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < LB; ++j) {
+      if (i0 + j < c.len) {
+        const float pe = tanhf(fabsf(wv[j] - Ev[j]));
+        const float Rcur = k.rd * Rv[j] + (1.0f - k.rd) * (1.0f - pe);
+        const float eff = k.ret + (1.0f - k.ret) * k.rs * Rcur;
+        const StepMap m = step_map(k, wv[j], pv[j], Lv[j], Ev[j], pe, eff);
+        // v += P (M_i g_i e0)
+        const float u0 = m.m00 * gv[j], u1 = m.m10 * gv[j], u2 = m.m20 * gv[j];
+        v0 += p00 * u0;
+        v1 += p10 * u0 + p11 * u1;
+        v2 += p20 * u0 + p21 * u1 + p22 * u2;
+        // P = P M_i
+        const float n20 = p20 * m.m00 + p21 * m.m10 + p22 * m.m20;
+        const float n21 = p21 * m.m11 + p22 * m.m21;
+        const float n10 = p10 * m.m00 + p11 * m.m10;
+        p00 *= m.m00;
+        p10 = n10;
+        p11 *= m.m11;
+        p20 = n20;
+        p21 = n21;
+        p22 *= m.m22;
+      }
+    }
+  }
+  const size_t stride = static_cast<size_t>(c.nseg) * B * H;
+  const size_t li = static_cast<size_t>(c.k) * B * H + c.ch;
+  maps[li] = p00;
+  maps[li + stride] = p10;
+  maps[li + 2 * stride] = p11;
+  maps[li + 3 * stride] = p20;
+  maps[li + 4 * stride] = p21;
+  maps[li + 5 * stride] = p22;
+  maps[li + 6 * stride] = v0;
+  maps[li + 7 * stride] = v1;
+  maps[li + 8 * stride] = v2;
+}
+
+// Per-channel reverse pass over the chunk maps: x_in(k) = adjoints entering chunk k (from
+// chunk k + 1), written over the map's first three components; x leaving chunk 0 goes to
+// gL0, gR0, gE0.
+__global__ void __launch_bounds__(NT) long_bwd_carry(int B, int T, int H, const float* gLF,
+                                                     const float* gRF, const float* gEF,
+                                                     float* maps, float* gL0, float* gR0,
+                                                     float* gE0) {
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
+  if (ch >= static_cast<int64_t>(B) * H) return;
+  const int nseg = (T + CK - 1) / CK;
+  const size_t stride = static_cast<size_t>(nseg) * B * H;
+  float x0 = gLF ? gLF[ch] : 0.0f, x1 = gRF ? gRF[ch] : 0.0f, x2 = gEF ? gEF[ch] : 0.0f;
+  for (int kk = nseg - 1; kk >= 0; --kk) {
+    float* m = maps + static_cast<size_t>(kk) * B * H + ch;
+    const float a00 = m[0], a10 = m[stride], a11 = m[2 * stride], a20 = m[3 * stride],
+                a21 = m[4 * stride], a22 = m[5 * stride], v0 = m[6 * stride],
+                v1 = m[7 * stride], v2 = m[8 * stride];
+    m[0] = x0;
+    m[stride] = x1;
+    m[2 * stride] = x2;
+    const float y0 = a00 * x0 + v0;
+    const float y1 = a10 * x0 + a11 * x1 + v1;
+    const float y2 = a20 * x0 + a21 * x1 + a22 * x2 + v2;
+    x0 = y0;
+    x1 = y1;
+    x2 = y2;
+  }
+  gL0[ch] = x0;
+  gR0[ch] = x1;
+  gE0[ch] = x2;
+}
+
+// Final pass: walk each chunk backward from the exact entering adjoints (maps components
+// 0..2), reading the forward values from `states`; writes gw, gp and reduces the logit
+// gradients per block (fixed order).
+template <typename E>
+__global__ void __launch_bounds__(NT) long_bwd_final(int B, int T, int H, const E* w, const E* p,
+                                                     Logits lg, const float* states,
+                                                     const E* gout, const float* maps, E* gw,
+                                                     E* gp, float* part) {
+  __shared__ float red[4][NT];
+  ChunkIdx c;
+  const bool ok = chunk_idx(B, T, H, c);
   const Coef k = load_coef(lg.p);
   float d_er = 0.f, d_rd = 0.f, d_ret = 0.f, d_rs = 0.f;
   if (ok) {
-    const int64_t b = ch / H, h = ch % H;
-    const size_t base = static_cast<size_t>(b) * T * H + h;
-    const int nseg = (T + CK - 1) / CK;
-    float gLc = gLF ? gLF[ch] : 0.0f;
-    float gEc = gEF ? gEF[ch] : 0.0f;
-    float gRc = gRF ? gRF[ch] : 0.0f;
-    for (int sg = nseg - 1; sg >= 0; --sg) {
-      const int t0 = sg * CK;
-      const size_t cbase = (static_cast<size_t>(b) * nseg + sg) * 3 * H + h;
-      float L = ckpt[cbase], Ev = ckpt[cbase + H], R = ckpt[cbase + 2 * H];
-      float Lp[CK], Ep[CK], Rp[CK], wv[CK], pv[CK];
+    const size_t bth = static_cast<size_t>(B) * T * H;
+    const size_t stride = static_cast<size_t>(c.nseg) * B * H;
+    const size_t li = static_cast<size_t>(c.k) * B * H + c.ch;
+    float gLc = maps[li], gRc = maps[li + stride], gEc = maps[li + 2 * stride];
+    constexpr int LB = 8;  // steps loaded ahead (walking backward)
+    for (int i1 = c.len - 1; i1 >= 0; i1 -= LB) {
+      float wv[LB], pv[LB], gv[LB], Lv[LB], Ev[LB], Rv[LB];
 #pragma unroll
-      for (int i = 0; i < CK; ++i) {
-        const int t = t0 + i;
-        wv[i] = t < T ? ld(w, base + static_cast<size_t>(t) * H) : 0.0f;
-        pv[i] = t < T ? ld(p, base + static_cast<size_t>(t) * H) : 0.0f;
+      for (int j = 0; j < LB; ++j) {
+        const int i = i1 - j;
+        const size_t o = c.base + static_cast<size_t>(c.t0 + (i < 0 ? 0 : i)) * H;
+        const bool in = i >= 0;
+        wv[j] = in ? ld(w, o) : 0.0f;
+        pv[j] = in ? ld(p, o) : 0.0f;
+        gv[j] = in ? ld(gout, o) : 0.0f;
+        Lv[j] = in ? states[o] : 0.0f;
+        Ev[j] = in ? states[bth + o] : 0.0f;
+        Rv[j] = in ? states[2 * bth + o] : 0.0f;
       }
 #pragma unroll
-      for (int i = 0; i < CK; ++i) {
-        Lp[i] = L;
-        Ep[i] = Ev;
-        Rp[i] = R;
-        const float pe = tanhf(fabsf(wv[i] - Ev));
-        const float sal = pv[i] * pe;
-        Ev = k.er * Ev + (1.0f - k.er) * wv[i];
-        R = k.rd * R + (1.0f - k.rd) * (1.0f - pe);
-        const float eff = k.ret + (1.0f - k.ret) * k.rs * R;
-        L = eff * L + (1.0f - eff) * (sal * wv[i]);
-      }
-#pragma unroll
-      for (int i = CK - 1; i >= 0; --i) {
-        const int t = t0 + i;
-        if (t < T) {
-          const size_t o = base + static_cast<size_t>(t) * H;
-          const float wt = wv[i], pt = pv[i];
-          const float diff = wt - Ep[i];
+      for (int j = 0; j < LB; ++j) {
+        const int i = i1 - j;
+        if (i >= 0) {
+          const float wt = wv[j], pt = pv[j];
+          const float diff = wt - Ev[j];
           const float pe = tanhf(fabsf(diff));
           const float sal = pt * pe;
-          const float Rcur = k.rd * Rp[i] + (1.0f - k.rd) * (1.0f - pe);
+          const float Rcur = k.rd * Rv[j] + (1.0f - k.rd) * (1.0f - pe);
           const float eff = k.ret + (1.0f - k.ret) * k.rs * Rcur;
-          const float gL = ld(gout, o) + gLc;
-          const float deff = gL * (Lp[i] - sal * wt);
+          const float gL = gv[j] + gLc;
+          const float deff = gL * (Lv[j] - sal * wt);
           const float dsal = gL * (1.0f - eff) * wt;
-          float dw = gL * (1.0f - eff) * sal;
           gLc = gL * eff;
           const float dR = gRc + deff * (1.0f - k.ret) * k.rs;
           gRc = dR * k.rd;
           const float dpe = dsal * pt - dR * (1.0f - k.rd);
-          st(gp, o, dsal * pe);
           const float darg = dpe * (1.0f - pe * pe) * signf_(diff);
-          dw += darg;
           const float dE = gEc;
-          dw += (1.0f - k.er) * dE;
           gEc = k.er * dE - darg;
-          st(gw, o, dw);
-          d_er += dE * (Ep[i] - wt);
-          d_rd += dR * (Rp[i] - (1.0f - pe));
+          const size_t o = c.base + static_cast<size_t>(c.t0 + i) * H;
+          st(gp, o, dsal * pe);
+          st(gw, o, gL * (1.0f - eff) * sal + darg + (1.0f - k.er) * dE);
+          d_er += dE * (Ev[j] - wt);
+          d_rd += dR * (Rv[j] - (1.0f - pe));
           d_ret += deff * (1.0f - k.rs * Rcur);
           d_rs += deff * (1.0f - k.ret) * Rcur;
         }
       }
     }
-    gL0[ch] = gLc;
-    gE0[ch] = gEc;
-    gR0[ch] = gRc;
   }
-  // d logit = d coef * sigmoid'(logit)
+  // d logit = d coef * sigmoid'(logit), reduced per block in a fixed order.
   red[0][threadIdx.x] = d_er * k.er * (1.0f - k.er);
   red[1][threadIdx.x] = d_rd * k.rd * (1.0f - k.rd);
   red[2][threadIdx.x] = d_ret * k.ret * (1.0f - k.ret);
@@ -226,7 +411,7 @@ __global__ void __launch_bounds__(NT) long_bwd_kernel(int B, int T, int H, const
   if (threadIdx.x < 4) {
     float s = 0.0f;
     for (int i = 0; i < NT; ++i) s += red[threadIdx.x][i];
-    part[static_cast<size_t>(blockIdx.x) * 4 + threadIdx.x] = s;
+    part[(static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x) * 4 + threadIdx.x] = s;
   }
 }
 
@@ -242,6 +427,46 @@ using namespace dabsn::longmem;
   DABSN_REQUIRE((B) > 0 && (T) >= 0 && (H) > 0 && (B) * (T) * (H) < (1ll << 46) &&          \
                     (B) * (H) < (1ll << 31) && (T) < (1ll << 30),                            \
                 "bad shape B=%lld T=%lld H=%lld", (long long)(B), (long long)(T), (long long)(H))
+
+template <typename E>
+static int long_fwd_impl(int B, int T, int H, const E* w, const E* p, Logits lg, const float* L0,
+                         const float* E0, const float* R0, E* out, float* LF, float* EF, float* RF,
+                         float* states, float* ws, hipStream_t stream) {
+  const int gx = grid_for(B, H);
+  const int nseg = (T + CK - 1) / CK;
+  float* loc0 = ws;
+  float* loc1 = ws + static_cast<size_t>(nseg) * B * H;
+  float* ckpt = ws + 2 * static_cast<size_t>(nseg) * B * H;  // [B][nseg][3][H]
+  const dim3 cg(gx, nseg), blk(NT);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 0>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out, states);
+  hipLaunchKernelGGL(long_fwd_carry<1>, dim3(gx), blk, 0, stream, B, T, H, lg, E0, loc0, loc1, ckpt, EF);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 1>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out, states);
+  hipLaunchKernelGGL(long_fwd_carry<2>, dim3(gx), blk, 0, stream, B, T, H, lg, R0, loc0, loc1, ckpt, RF);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 2>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out, states);
+  hipLaunchKernelGGL(long_fwd_carry<0>, dim3(gx), blk, 0, stream, B, T, H, lg, L0, loc0, loc1, ckpt, LF);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 3>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out, states);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+template <typename E>
+static int long_bwd_impl(int B, int T, int H, const E* w, const E* p, Logits lg,
+                         const float* states, const E* gout, const float* gLF, const float* gEF,
+                         const float* gRF, E* gw, E* gp, float* gL0, float* gE0, float* gR0,
+                         float* part, float* ws, hipStream_t stream) {
+  const int gx = grid_for(B, H);
+  const int nseg = (T + CK - 1) / CK;
+  const dim3 cg(gx, nseg), blk(NT);
+  if (nseg > 0)
+    hipLaunchKernelGGL(long_bwd_map<E>, cg, blk, 0, stream, B, T, H, w, p, lg, states, gout, ws);
+  hipLaunchKernelGGL(long_bwd_carry, dim3(gx), blk, 0, stream, B, T, H, gLF, gRF, gEF, ws, gL0,
+                     gR0, gE0);
+  if (nseg > 0)
+    hipLaunchKernelGGL(long_bwd_final<E>, cg, blk, 0, stream, B, T, H, w, p, lg, states, gout,
+                       ws, gw, gp, part);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
 
 extern "C" {
 
@@ -290,54 +515,66 @@ int dabsn_hip_linrec_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void*
   return DABSN_OK;
 }
 
+size_t dabsn_hip_long_workspace_bytes(int64_t B, int64_t T, int64_t H, int backward) {
+  const int64_t nseg = (T + CK - 1) / CK;
+  // forward: two chunk-end arrays + the chunk-start checkpoint (3 per chunk);
+  // backward: the 9-component chunk maps.
+  return static_cast<size_t>(backward ? 9 : 5) * static_cast<size_t>(nseg) * B * H * sizeof(float);
+}
+
 int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
                        const float* const* logits, const float* L0, const float* E0,
-                       const float* R0, void* out, float* LF, float* EF, float* RF, float* ckpt,
-                       hipStream_t stream) {
+                       const float* R0, void* out, float* LF, float* EF, float* RF, float* states,
+                       void* workspace, size_t workspace_bytes, hipStream_t stream) {
   DABSN_SHAPE_CHECK(B, T, H);
-  DABSN_REQUIRE(w && p && logits && L0 && E0 && R0 && (out || T == 0) && LF && EF && RF,
+  DABSN_REQUIRE(w && p && logits && L0 && E0 && R0 && (out || T == 0) && LF && EF && RF &&
+                    (workspace || T == 0),
                 "long scan: null pointer");
   for (int i = 0; i < 4; ++i) DABSN_REQUIRE(logits[i], "long scan: null logit %d", i);
+  DABSN_REQUIRE(workspace_bytes >= dabsn_hip_long_workspace_bytes(B, T, H, 0),
+                "long scan: workspace %zu B < required %zu B", workspace_bytes,
+                dabsn_hip_long_workspace_bytes(B, T, H, 0));
+  DABSN_REQUIRE((T + CK - 1) / CK < 65536, "long scan: T too long");
   Logits lg{{logits[0], logits[1], logits[2], logits[3]}};
-  const int grid = grid_for(B, H);
   if (dtype == kBF16)
-    hipLaunchKernelGGL(long_fwd_kernel<bf16>, dim3(grid), dim3(NT), 0, stream, (int)B, (int)T,
-                       (int)H, (const bf16*)w, (const bf16*)p, lg, L0, E0, R0, (bf16*)out, LF, EF,
-                       RF, ckpt);
-  else if (dtype == kF32)
-    hipLaunchKernelGGL(long_fwd_kernel<float>, dim3(grid), dim3(NT), 0, stream, (int)B, (int)T,
-                       (int)H, (const float*)w, (const float*)p, lg, L0, E0, R0, (float*)out, LF,
-                       EF, RF, ckpt);
-  else
-    DABSN_REQUIRE(false, "long scan: bad dtype %d", dtype);
-  DABSN_HIP_CHECK(hipGetLastError());
+    return long_fwd_impl<bf16>((int)B, (int)T, (int)H, (const bf16*)w, (const bf16*)p, lg, L0,
+                               E0, R0, (bf16*)out, LF, EF, RF, states, (float*)workspace, stream);
+  if (dtype == kF32)
+    return long_fwd_impl<float>((int)B, (int)T, (int)H, (const float*)w, (const float*)p, lg, L0,
+                                E0, R0, (float*)out, LF, EF, RF, states, (float*)workspace,
+                                stream);
+  DABSN_REQUIRE(false, "long scan: bad dtype %d", dtype);
   return DABSN_OK;
 }
 
-int64_t dabsn_hip_long_partials(int64_t B, int64_t H) { return grid_for(B, H); }
+int64_t dabsn_hip_long_partials(int64_t B, int64_t T, int64_t H) {
+  return static_cast<int64_t>(grid_for(B, H)) * ((T + CK - 1) / CK);
+}
 
 int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
-                       const float* const* logits, const float* ckpt, const void* gout,
+                       const float* const* logits, const float* states, const void* gout,
                        const float* gLF, const float* gEF, const float* gRF, void* gw, void* gp,
-                       float* gL0, float* gE0, float* gR0, float* part_logit, hipStream_t stream) {
+                       float* gL0, float* gE0, float* gR0, float* part_logit, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
   DABSN_SHAPE_CHECK(B, T, H);
-  DABSN_REQUIRE(w && p && logits && (ckpt || T == 0) && (gout || T == 0) && gL0 && gE0 && gR0 &&
-                    part_logit,
+  DABSN_REQUIRE(w && p && logits && (states || T == 0) && (gout || T == 0) && gL0 && gE0 && gR0 &&
+                    (part_logit || T == 0) && (workspace || T == 0) && ((gw && gp) || T == 0),
                 "long scan backward: null pointer");
   for (int i = 0; i < 4; ++i) DABSN_REQUIRE(logits[i], "long scan backward: null logit %d", i);
+  DABSN_REQUIRE(workspace_bytes >= dabsn_hip_long_workspace_bytes(B, T, H, 1),
+                "long scan backward: workspace %zu B < required %zu B", workspace_bytes,
+                dabsn_hip_long_workspace_bytes(B, T, H, 1));
+  DABSN_REQUIRE((T + CK - 1) / CK < 65536, "long scan backward: T too long");
   Logits lg{{logits[0], logits[1], logits[2], logits[3]}};
-  const int grid = grid_for(B, H);
   if (dtype == kBF16)
-    hipLaunchKernelGGL(long_bwd_kernel<bf16>, dim3(grid), dim3(NT), 0, stream, (int)B, (int)T,
-                       (int)H, (const bf16*)w, (const bf16*)p, lg, ckpt, (const bf16*)gout, gLF,
-                       gEF, gRF, (bf16*)gw, (bf16*)gp, gL0, gE0, gR0, part_logit);
-  else if (dtype == kF32)
-    hipLaunchKernelGGL(long_bwd_kernel<float>, dim3(grid), dim3(NT), 0, stream, (int)B, (int)T,
-                       (int)H, (const float*)w, (const float*)p, lg, ckpt, (const float*)gout, gLF,
-                       gEF, gRF, (float*)gw, (float*)gp, gL0, gE0, gR0, part_logit);
-  else
-    DABSN_REQUIRE(false, "long scan backward: bad dtype %d", dtype);
-  DABSN_HIP_CHECK(hipGetLastError());
+    return long_bwd_impl<bf16>((int)B, (int)T, (int)H, (const bf16*)w, (const bf16*)p, lg, states,
+                               (const bf16*)gout, gLF, gEF, gRF, (bf16*)gw, (bf16*)gp, gL0, gE0,
+                               gR0, part_logit, (float*)workspace, stream);
+  if (dtype == kF32)
+    return long_bwd_impl<float>((int)B, (int)T, (int)H, (const float*)w, (const float*)p, lg, states,
+                                (const float*)gout, gLF, gEF, gRF, (float*)gw, (float*)gp, gL0,
+                                gE0, gR0, part_logit, (float*)workspace, stream);
+  DABSN_REQUIRE(false, "long scan backward: bad dtype %d", dtype);
   return DABSN_OK;
 }
 

@@ -387,8 +387,9 @@ def long_scan_fused(
     logit_retention_decay: Tensor, logit_retain: Tensor, logit_retention_strength: Tensor,
     long0: Tensor, expected0: Tensor, retention0: Tensor,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """The three recurrences of long.py:492-579 in one pass. Returns (long [B,T,H],
-    final long, final expected, final retention [B,H] fp32, checkpoints)."""
+    """The three recurrences of long.py:492-579, chunked over time. Returns (long [B,T,H],
+    final long, final expected, final retention [B,H] fp32, per-step states [3,B,T,H] fp32
+    saved for the backward)."""
     _require_cuda(write)
     lib = _lib.load()
     B, T, H = write.shape
@@ -401,27 +402,28 @@ def long_scan_fused(
     L0, E0, R0 = (x.float().contiguous() for x in (long0, expected0, retention0))
     out = torch.empty_like(w)
     LF, EF, RF = (torch.empty((B, H), device=w.device, dtype=torch.float32) for _ in range(3))
-    nseg = (T + 31) // 32
-    ckpt = torch.empty((B, nseg, 3, H), device=w.device, dtype=torch.float32)
+    states = torch.empty((3, B, T, H), device=w.device, dtype=torch.float32)
+    nbytes = lib.dabsn_hip_long_workspace_bytes(B, T, H, 0)
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=w.device)
     tk = KernelTimer.begin("long_scan_fwd", w)
     _lib.check(lib.dabsn_hip_long_fwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(L0), _p(E0),
-                                      _p(R0), _p(out), _p(LF), _p(EF), _p(RF), _p(ckpt),
-                                      _stream(w)), "long scan")
+                                      _p(R0), _p(out), _p(LF), _p(EF), _p(RF), _p(states),
+                                      _p(ws), nbytes, _stream(w)), "long scan")
     KernelTimer.end(tk)
-    return out, LF, EF, RF, ckpt
+    return out, LF, EF, RF, states
 
 
 @long_scan_fused.register_fake
 def _long_scan_fused_fake(write, plasticity, l1, l2, l3, l4, long0, expected0, retention0):
     B, T, H = write.shape
     f = lambda *s: write.new_empty(s, dtype=torch.float32)  # noqa: E731
-    return torch.empty_like(write), f(B, H), f(B, H), f(B, H), f(B, (T + 31) // 32, 3, H)
+    return torch.empty_like(write), f(B, H), f(B, H), f(B, H), f(3, B, T, H)
 
 
 @torch.library.custom_op("dabsn::_long_scan_fused_backward", mutates_args=(),
                          device_types="cuda")
 def long_scan_fused_backward(
-    write: Tensor, plasticity: Tensor, logits: list[Tensor], ckpt: Tensor, grad_long: Tensor,
+    write: Tensor, plasticity: Tensor, logits: list[Tensor], states: Tensor, grad_long: Tensor,
     g_long_final: Optional[Tensor], g_expected_final: Optional[Tensor],
     g_retention_final: Optional[Tensor],
 ) -> list[Tensor]:
@@ -439,19 +441,23 @@ def long_scan_fused_backward(
           for x in (g_long_final, g_expected_final, g_retention_final)]
     gw, gp = torch.empty_like(w), torch.empty_like(p)
     g0 = [torch.empty((B, H), device=w.device, dtype=torch.float32) for _ in range(3)]
-    nparts = lib.dabsn_hip_long_partials(B, H)
-    part = torch.empty((nparts, 4), device=w.device, dtype=torch.float32)
+    nparts = lib.dabsn_hip_long_partials(B, T, H)
+    part = torch.empty((max(nparts, 1), 4), device=w.device, dtype=torch.float32)
+    part[nparts:].zero_()
+    nbytes = lib.dabsn_hip_long_workspace_bytes(B, T, H, 1)
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=w.device)
     tk = KernelTimer.begin("long_scan_bwd", w)
-    _lib.check(lib.dabsn_hip_long_bwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(ckpt), _p(gout),
+    st = states.float().contiguous()
+    _lib.check(lib.dabsn_hip_long_bwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(st), _p(gout),
                                       *[_p(x) for x in gf], _p(gw), _p(gp), *[_p(x) for x in g0],
-                                      _p(part), _stream(w)), "long scan backward")
+                                      _p(part), _p(ws), nbytes, _stream(w)), "long scan backward")
     KernelTimer.end(tk)
     glog = part.sum(0)
     return [gw, gp.to(plasticity.dtype), *[glog[i].clone() for i in range(4)], *g0]
 
 
 @long_scan_fused_backward.register_fake
-def _long_scan_fused_backward_fake(write, plasticity, logits, ckpt, grad_long, a, b, c):
+def _long_scan_fused_backward_fake(write, plasticity, logits, states, grad_long, a, b, c):
     B, T, H = write.shape
     f = lambda *s: write.new_empty(s, dtype=torch.float32)  # noqa: E731
     return [torch.empty_like(write), torch.empty_like(plasticity), f(), f(), f(), f(),
@@ -464,11 +470,11 @@ def _long_setup(ctx, inputs, output):
     ctx.meta = [(x.dtype, tuple(x.shape)) for x in inputs]
 
 
-def _long_bwd(ctx, g_long, g_lf, g_ef, g_rf, _g_ckpt):
-    write, plasticity, l1, l2, l3, l4, ckpt = ctx.saved_tensors
+def _long_bwd(ctx, g_long, g_lf, g_ef, g_rf, _g_states):
+    write, plasticity, l1, l2, l3, l4, states = ctx.saved_tensors
     if g_long is None:
         g_long = torch.zeros_like(write)
-    grads = long_scan_fused_backward(write, plasticity, [l1, l2, l3, l4], ckpt, g_long, g_lf,
+    grads = long_scan_fused_backward(write, plasticity, [l1, l2, l3, l4], states, g_long, g_lf,
                                      g_ef, g_rf)
     return tuple(g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(grads, ctx.meta))
 

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 1
+#define DABSN_HIP_ABI_VERSION 2
 
 #ifdef __cplusplus
 extern "C" {
@@ -97,21 +97,26 @@ int dabsn_hip_linrec_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void*
  * Fused form of the three recurrences of src/dabsn/kernels/long.py:492-579 (loop form
  * read.py:625-636). logits[4] point at fp32 scalars (logit_expect_retain,
  * logit_retention_decay, logit_retain, logit_retention_strength). State L0/E0/R0 [B,H]
- * fp32 in, LF/EF/RF out. ckpt (may be NULL) receives fp32 (L,E,R) every
- * DABSN_LONG_CKPT steps: [B][ceil(T/ckpt)][3][H]; the backward requires it. */
+ * fp32 in, LF/EF/RF out. `states` (may be NULL) receives the fp32 states entering every
+ * step, [3][B][T][H] = (L, E, R)_{t-1}; the backward reads them. Both directions are
+ * chunked over time (chunks of DABSN_LONG_CKPT steps) and need
+ * dabsn_hip_long_workspace_bytes() bytes of workspace. */
 #define DABSN_LONG_CKPT 32
+size_t dabsn_hip_long_workspace_bytes(int64_t B, int64_t T, int64_t H, int backward);
 int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
                        const float* const* logits, const float* L0, const float* E0,
-                       const float* R0, void* out, float* LF, float* EF, float* RF, float* ckpt,
-                       hipStream_t stream);
-/* Backward: gout [B,T,H], gLF/gEF/gRF (may be NULL). Outputs gw, gp [B,T,H], gL0, gE0, gR0
- * [B,H], and part_logit [nblocks][4] with nblocks = dabsn_hip_long_partials(B, H): per-block
- * partial sums of the gradient w.r.t. the four logits. */
-int64_t dabsn_hip_long_partials(int64_t B, int64_t H);
+                       const float* R0, void* out, float* LF, float* EF, float* RF, float* states,
+                       void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* Backward: gout [B,T,H], gLF/gEF/gRF (may be NULL), the forward's `states`. Outputs gw, gp
+ * [B,T,H], gL0, gE0, gR0 [B,H], and part_logit [nblocks][4] with nblocks =
+ * dabsn_hip_long_partials(B, T, H): per-block partial sums of the gradient w.r.t. the four
+ * logits. */
+int64_t dabsn_hip_long_partials(int64_t B, int64_t T, int64_t H);
 int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
-                       const float* const* logits, const float* ckpt, const void* gout,
+                       const float* const* logits, const float* states, const void* gout,
                        const float* gLF, const float* gEF, const float* gRF, void* gw, void* gp,
-                       float* gL0, float* gE0, float* gR0, float* part_logit, hipStream_t stream);
+                       float* gL0, float* gE0, float* gR0, float* part_logit, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
 
 /* ---- read glue ----------------------------------------------------------------------
  * Per-position statistics of the read (src/dabsn/read.py:58-72, 154-183): stats[B,T,6] =

@@ -125,9 +125,11 @@ def test_core_scan_empty_time_returns_initial_state(cuda_device):
         assert torch.equal(out[k], x[s])
 
 
-def test_long_scan_and_linear_recurrence_match_oracle(cuda_device):
-    g = torch.Generator().manual_seed(3)
-    B, T, H = 4, 200, 96
+@pytest.mark.parametrize("T", [1, 32, 33, 200, 1000])
+def test_long_scan_and_linear_recurrence_match_oracle(cuda_device, T):
+    """The long scan runs in 32-step chunks: lengths below, at and across chunk edges."""
+    g = torch.Generator().manual_seed(3 + T)
+    B, H = 4, 96
     w = torch.randn(B, T, H, generator=g) * 0.7
     p = torch.rand(B, T, H, generator=g)
     logits = [torch.tensor([v]) for v in (2.2, 2.0, 2.4, 1.4)]
