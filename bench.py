@@ -62,12 +62,16 @@ class ScanRead(torch.nn.Module):
     def scan(self, Wx, Wgx):
         from torch.utils.checkpoint import checkpoint
 
+        from dabsn_amd.kernels.chunked import chunked_core_scan
         from dabsn_amd.kernels.ops import core_scan_batched
 
         B, T, H = Wx.shape
         zeros = torch.zeros(B, H, device=Wx.device, dtype=torch.float32)
         carry = (zeros, torch.ones_like(zeros), zeros.clone())
         params = self.core.scan_inputs()
+        if Wx.is_cuda and 0 < self.chunk < T and torch.is_grad_enabled():
+            # Checkpointed chunks; the backward overlaps each recompute with a reverse scan.
+            return list(chunked_core_scan(self.chunk, Wx, Wgx, *params, *carry)[:7])
         tapes = [[] for _ in range(7)]
 
         def run(wx, wgx, b, e, c):

@@ -33,6 +33,28 @@ class CoreParams(ctypes.Structure):
 
 PTR4 = vp * 4
 
+
+class CoreFwdCall(ctypes.Structure):
+    """Mirror of ``dabsn_core_fwd_call``."""
+
+    _fields_ = ([("dtype", i32), ("B", i64), ("T", i64), ("H", i64), ("Wx", vp), ("Wgx", vp),
+                 ("GA", vp), ("params", ctypes.POINTER(CoreParams))]
+                + [(n, vp) for n in ("b0", "e0", "c0", "U", "nov", "plast", "expr", "write",
+                                     "energy", "sat", "gate", "bF", "eF", "cF", "workspace")]
+                + [("workspace_bytes", sz)])
+
+
+class CoreBwdCall(ctypes.Structure):
+    """Mirror of ``dabsn_core_bwd_call``."""
+
+    _fields_ = ([("dtype", i32), ("B", i64), ("T", i64), ("H", i64), ("GAT", vp),
+                 ("params", ctypes.POINTER(CoreParams))]
+                + [(n, vp) for n in ("b0", "c0", "U", "plast", "expr", "energy", "sat", "gate",
+                                     "gU", "gNov", "gP", "gAy", "gW", "gE", "gC", "gbF", "geF",
+                                     "gcF", "gWx", "gWgx", "day", "part_vec", "part_scal", "gb0",
+                                     "ge0", "gc0", "workspace")]
+                + [("workspace_bytes", sz)])
+
 _SIGNATURES = {
     "dabsn_hip_abi_version": ([], i32),
     "dabsn_hip_last_error": ([], ctypes.c_char_p),
@@ -51,6 +73,8 @@ _SIGNATURES = {
         + [vp] * 6 + [vp] * 7 + [vp] * 3 + [vp] * 3 + [vp, vp] + [vp] * 3 + [vp, sz, vp],
         i32,
     ),
+    "dabsn_hip_core_scan_pair": (
+        [ctypes.POINTER(CoreFwdCall), ctypes.POINTER(CoreBwdCall), vp], i32),
     "dabsn_hip_linrec_fwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_linrec_workspace_bytes": ([i32, i64, i64, i64], sz),
     "dabsn_hip_linrec_bwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),

@@ -108,6 +108,20 @@ class DABSNCore(nn.Module):
             return result, tuple(outputs[8:11])
         return result
 
+    def chunked_tapes(self, inputs: Tensor, chunk_t: int):
+        """Block time-chunked scan from the zero state (model.py:274-307): chunks of
+        `chunk_t` steps with the state carried between them, each checkpointed. On the
+        device the recompute of chunk k - 1 overlaps the reverse scan of chunk k. Returns
+        the 7 tapes of forward_from_state(..., return_cocktail=True)."""
+        from .kernels.chunked import chunked_core_scan
+
+        batch = inputs.shape[0]
+        zeros = torch.zeros(batch, self.hidden_dim, device=inputs.device, dtype=torch.float32)
+        outputs = chunked_core_scan(chunk_t, self.W(inputs), self.Wg(inputs), *self.scan_inputs(),
+                                    zeros, torch.ones_like(zeros), zeros.clone())
+        self._last_core_backend = "rocm_native_hip_chunked"
+        return tuple(outputs[:7])
+
     def forward(self, inputs: Tensor, return_writes: bool = False, return_cocktail: bool = False):
         return self.forward_from_state(inputs, return_writes=return_writes,
                                        return_cocktail=return_cocktail)

@@ -3,18 +3,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include "../../include/dabsn_hip.h"
+
 namespace dabsn {
 
 // Records a printf-style message returned by dabsn_hip_last_error().
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 
 }  // namespace dabsn
-
-// Status codes returned by every entry point.
-#define DABSN_OK 0
-#define DABSN_ERR_HIP (-1)
-#define DABSN_ERR_ARG (-2)
-#define DABSN_ERR_UNSUPPORTED (-3)
 
 #define DABSN_HIP_CHECK(expr)                                                        \
   do {                                                                               \

@@ -158,8 +158,8 @@ __device__ __forceinline__ void arrive(uint32_t* counter) {
 __device__ __forceinline__ uint32_t* group_counters(uint8_t* ws, int bg) {
   return reinterpret_cast<uint32_t*>(ws + kCtrOff + static_cast<size_t>(bg) * kSplit * kCtrStride);
 }
-__device__ __forceinline__ uint32_t* my_counter(uint32_t* ctr, int nct) {
-  return ctr + (static_cast<int>(blockIdx.x) % nct % kSplit) * (kCtrStride / 4);
+__device__ __forceinline__ uint32_t* my_counter(uint32_t* ctr, int nct, int bid) {
+  return ctr + (bid % nct % kSplit) * (kCtrStride / 4);
 }
 
 // Wait for every outstanding vector memory operation of this wave (the exchange stores
@@ -255,17 +255,18 @@ __device__ __forceinline__ float gate_tape_value(float s) {
   }
 }
 
-__device__ __forceinline__ void tile_of(int nct, int& ct, int& bg) {
+__device__ __forceinline__ void tile_of(int bid, int nct, int& ct, int& bg) {
   // Consecutive channel tiles go to the same XCD (workgroups are dealt round-robin over
   // the 8 XCDs), so the tape rows a step writes are merged in one L2.
-  const int bid = blockIdx.x;
   bg = bid / nct;
   const int i = bid % nct;
   ct = (nct % 8 == 0) ? (i % 8) * (nct / 8) + i / 8 : i;
 }
 
+// Forward scan of one workgroup: `bid` is its index among the `grid` workgroups of this
+// scan (the kernel may host another scan in its other workgroups).
 template <typename E, int CH, int KSTEPS, int NW>
-__global__ void __launch_bounds__(NW * 64, 1) core_fwd_kernel(FwdArgs<E> a) {
+__device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid) {
   using M = Mf<E>;
   constexpr int NT = NW * 64;
   constexpr int KSTEP = M::KSTEP;
@@ -282,12 +283,12 @@ __global__ void __launch_bounds__(NW * 64, 1) core_fwd_kernel(FwdArgs<E> a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int ct, bg;
-  tile_of(a.nct, ct, bg);
+  tile_of(bid, a.nct, ct, bg);
   const int H = a.H, T = a.T, B = a.B;
   uint32_t* err = reinterpret_cast<uint32_t*>(a.ws);
   uint32_t* ctr = group_counters(a.ws, bg);
-  uint32_t* counter = my_counter(ctr, a.nct);
-  const int nbg = static_cast<int>(gridDim.x) / a.nct;
+  uint32_t* counter = my_counter(ctr, a.nct, bid);
+  const int nbg = grid / a.nct;
   uint8_t* xbase = a.ws + xchg_offset(nbg) + static_cast<size_t>(bg) * 2 * a.slot_bytes;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(xbase, 2 * a.slot_bytes);
   if (tid == 0) s_abort = 0;
@@ -632,8 +633,9 @@ __device__ __forceinline__ Pending reverse_step(const TapeRaw& r, int t, float b
   return o;
 }
 
+// Reverse scan of one workgroup (`bid` among `grid`, as fwd_body).
 template <typename E, int CH, int KSTEPS, int NW>
-__global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
+__device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid) {
   using M = Mf<E>;
   constexpr int NT = NW * 64;
   constexpr int KSTEP = M::KSTEP;
@@ -650,12 +652,12 @@ __global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int ct, bg;
-  tile_of(a.nct, ct, bg);
+  tile_of(bid, a.nct, ct, bg);
   const int H = a.H, T = a.T, B = a.B, KP = a.kp;
   uint32_t* err = reinterpret_cast<uint32_t*>(a.ws);
   uint32_t* ctr = group_counters(a.ws, bg);
-  uint32_t* counter = my_counter(ctr, a.nct);
-  const int nbg = static_cast<int>(gridDim.x) / a.nct;
+  uint32_t* counter = my_counter(ctr, a.nct, bid);
+  const int nbg = grid / a.nct;
   uint8_t* xbase = a.ws + xchg_offset(nbg) + static_cast<size_t>(bg) * 2 * a.slot_bytes;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(xbase, 2 * a.slot_bytes);
   if (tid == 0) s_abort = 0;
@@ -829,7 +831,32 @@ __global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
     float s = 0.0f;
     for (int u = 0; u < CH; ++u)
       for (int r = 0; r < NB; ++r) s += accs[r][u][16 + tid];
-    a.part_scal[static_cast<size_t>(blockIdx.x) * 3 + tid] = s;
+    a.part_scal[static_cast<size_t>(bid) * 3 + tid] = s;
+  }
+}
+
+template <typename E, int CH, int KSTEPS, int NW>
+__global__ void __launch_bounds__(NW * 64, 1) core_fwd_kernel(FwdArgs<E> a) {
+  fwd_body<E, CH, KSTEPS, NW>(a, blockIdx.x, gridDim.x);
+}
+
+template <typename E, int CH, int KSTEPS, int NW>
+__global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
+  bwd_body<E, CH, KSTEPS, NW>(a, blockIdx.x, gridDim.x);
+}
+
+// A forward scan and an independent reverse scan in one cooperative launch: workgroups
+// [0, gf) run the forward (e.g. the recompute of chunk k-1 of a checkpointed chunked scan),
+// [gf, gf + gb) the reverse scan of another chunk. Each has its own workspace (counters and
+// exchange slots); one launch guarantees both halves are co-resident.
+template <typename E, int CH, int KSTEPS, int NW>
+__global__ void __launch_bounds__(NW * 64, 1) core_pair_kernel(FwdArgs<E> fa, BwdArgs<E> ba,
+                                                               int gf, int gb) {
+  const int bid = blockIdx.x;
+  if (bid < gf) {
+    fwd_body<E, CH, KSTEPS, NW>(fa, bid, gf);
+  } else {
+    bwd_body<E, CH, KSTEPS, NW>(ba, bid - gf, gb);
   }
 }
 
@@ -938,6 +965,44 @@ static int bwd_dispatch(const Cfg& c, const BwdArgs<E>& args, hipStream_t stream
   return DABSN_ERR_UNSUPPORTED;
 }
 
+template <typename E>
+static int pair_dispatch(const Cfg& c, const FwdArgs<E>& fa, const BwdArgs<E>& ba, int gf, int gb,
+                         hipStream_t stream) {
+  struct PairArgs {
+    FwdArgs<E> fa;
+    BwdArgs<E> ba;
+    int gf, gb;
+  };
+#define DABSN_CASE(CHV, KS, NWV)                                                         \
+  if (c.ch == CHV && c.ksteps == KS && c.nw == NWV) {                                    \
+    auto kern = core_pair_kernel<E, CHV, KS, NWV>;                                       \
+    int dev = 0, cus = 0, per_cu = 0, coop = 0;                                          \
+    DABSN_HIP_CHECK(hipGetDevice(&dev));                                                 \
+    DABSN_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev)); \
+    DABSN_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)); \
+    DABSN_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NWV * 64, 0)); \
+    if (!coop || per_cu * cus < gf + gb) {                                               \
+      dabsn::set_error("core scan pair needs %d co-resident workgroups, device holds %d", \
+                       gf + gb, per_cu * cus);                                           \
+      return DABSN_ERR_UNSUPPORTED;                                                      \
+    }                                                                                    \
+    PairArgs pa{fa, ba, gf, gb};                                                         \
+    void* kargs[] = {&pa.fa, &pa.ba, &pa.gf, &pa.gb};                                    \
+    DABSN_HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern),       \
+                                               dim3(gf + gb), dim3(NWV * 64), kargs, 0,  \
+                                               stream));                                 \
+    return DABSN_OK;                                                                     \
+  }
+  if constexpr (is_bf16<E>::value) {
+    DABSN_CORE_CASES_BF16(DABSN_CASE)
+  } else {
+    DABSN_CORE_CASES_F32(DABSN_CASE)
+  }
+#undef DABSN_CASE
+  dabsn::set_error("core scan pair: no kernel for CH=%d KSTEPS=%d NW=%d", c.ch, c.ksteps, c.nw);
+  return DABSN_ERR_UNSUPPORTED;
+}
+
 static Params to_params(const dabsn_core_params* p) {
   Params q;
   for (int i = 0; i < 16; ++i) q.vec[i] = p->vec[i];
@@ -965,6 +1030,78 @@ static int check_common(int dtype, int64_t B, int64_t T, int64_t H, const dabsn_
                     (1ull << 32),
                 "core scan: T=%lld too long for the 32-bit step counters", (long long)T);
   return DABSN_OK;
+}
+
+static int check_fwd(const dabsn_core_fwd_call& f, Cfg& c) {
+  c = pick(f.dtype, f.B, f.H);
+  const int rc = check_common(f.dtype, f.B, f.T, f.H, f.params, c, f.workspace_bytes,
+                              c.ksteps ? workspace_bytes(f.dtype, c, false) : 0);
+  if (rc != DABSN_OK) return rc;
+  DABSN_REQUIRE(f.Wx && f.Wgx && f.GA && f.b0 && f.e0 && f.c0 && f.bF && f.eF && f.cF &&
+                    f.workspace,
+                "core scan: null pointer argument");
+  DABSN_REQUIRE(f.T == 0 || (f.U && f.nov && f.plast && f.expr && f.write && f.energy && f.sat &&
+                             f.gate),
+                "core scan: null tape pointer");
+  return DABSN_OK;
+}
+
+static int check_bwd(const dabsn_core_bwd_call& b, Cfg& c) {
+  c = pick(b.dtype, b.B, b.H);
+  const int rc = check_common(b.dtype, b.B, b.T, b.H, b.params, c, b.workspace_bytes,
+                              c.ksteps ? workspace_bytes(b.dtype, c, true) : 0);
+  if (rc != DABSN_OK) return rc;
+  DABSN_REQUIRE(b.GAT && b.b0 && b.c0 && b.part_vec && b.part_scal && b.gb0 && b.ge0 && b.gc0 &&
+                    b.workspace,
+                "core scan backward: null pointer argument");
+  DABSN_REQUIRE(b.T == 0 || (b.U && b.plast && b.expr && b.energy && b.sat && b.gate && b.gWx &&
+                             b.gWgx && b.day),
+                "core scan backward: null tape pointer");
+  if (b.dtype == kF32 && c.ksteps > 32) {
+    dabsn::set_error("core scan backward: fp32 supports H <= 512 per workgroup register budget");
+    return DABSN_ERR_UNSUPPORTED;
+  }
+  return DABSN_OK;
+}
+
+static int prepare_fwd(const dabsn_core_fwd_call& f, Cfg& c, hipStream_t stream) {
+  const int rc = check_fwd(f, c);
+  if (rc != DABSN_OK) return rc;
+  return dabsn_hip_zero(f.workspace, workspace_bytes(f.dtype, c, false), stream);
+}
+
+static int prepare_bwd(const dabsn_core_bwd_call& b, Cfg& c, hipStream_t stream) {
+  const int rc = check_bwd(b, c);
+  if (rc != DABSN_OK) return rc;
+  return dabsn_hip_zero(b.workspace, workspace_bytes(b.dtype, c, true), stream);
+}
+
+template <typename E>
+static FwdArgs<E> fwd_args(const dabsn_core_fwd_call& f, const Cfg& c) {
+  return FwdArgs<E>{static_cast<int>(f.B), static_cast<int>(f.T), static_cast<int>(f.H), c.nct,
+                    static_cast<const E*>(f.Wx), static_cast<const E*>(f.Wgx),
+                    static_cast<const E*>(f.GA), to_params(f.params), f.b0, f.e0, f.c0,
+                    static_cast<E*>(f.U), static_cast<E*>(f.nov), static_cast<E*>(f.plast),
+                    static_cast<E*>(f.expr), static_cast<E*>(f.write), static_cast<E*>(f.energy),
+                    static_cast<E*>(f.sat), static_cast<E*>(f.gate), f.bF, f.eF, f.cF,
+                    static_cast<uint8_t*>(f.workspace),
+                    static_cast<uint32_t>(slot_bytes(f.dtype, c, false))};
+}
+
+template <typename E>
+static BwdArgs<E> bwd_args(const dabsn_core_bwd_call& b, const Cfg& c) {
+  return BwdArgs<E>{static_cast<int>(b.B), static_cast<int>(b.T), static_cast<int>(b.H), c.nct,
+                    c.kp, static_cast<const E*>(b.GAT), to_params(b.params), b.b0, b.c0,
+                    static_cast<const E*>(b.U), static_cast<const E*>(b.plast),
+                    static_cast<const E*>(b.expr), static_cast<const E*>(b.energy),
+                    static_cast<const E*>(b.sat), static_cast<const E*>(b.gate),
+                    static_cast<const E*>(b.gU), static_cast<const E*>(b.gNov),
+                    static_cast<const E*>(b.gP), static_cast<const E*>(b.gAy),
+                    static_cast<const E*>(b.gW), static_cast<const E*>(b.gE),
+                    static_cast<const E*>(b.gC), b.gbF, b.geF, b.gcF, static_cast<E*>(b.gWx),
+                    static_cast<E*>(b.gWgx), static_cast<E*>(b.day), b.part_vec, b.part_scal,
+                    b.gb0, b.ge0, b.gc0, static_cast<uint8_t*>(b.workspace),
+                    static_cast<uint32_t>(slot_bytes(b.dtype, c, true))};
 }
 
 }  // namespace core
@@ -1010,36 +1147,14 @@ int dabsn_hip_core_scan_fwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
                             void* plast, void* expr, void* write, void* energy, void* sat,
                             void* gate, float* bF, float* eF, float* cF, void* workspace,
                             size_t workspace_bytes_, hipStream_t stream) {
-  const Cfg c = pick(dtype, B, H);
-  const int rc = check_common(dtype, B, T, H, params, c, workspace_bytes_,
-                              c.ksteps ? workspace_bytes(dtype, c, false) : 0);
+  const dabsn_core_fwd_call f{dtype, B, T, H, Wx, Wgx, GA, params, b0, e0, c0, U, nov, plast,
+                              expr, write, energy, sat, gate, bF, eF, cF, workspace,
+                              workspace_bytes_};
+  Cfg c;
+  int rc = prepare_fwd(f, c, stream);
   if (rc != DABSN_OK) return rc;
-  DABSN_REQUIRE(Wx && Wgx && GA && b0 && e0 && c0 && bF && eF && cF && workspace,
-                "core scan: null pointer argument");
-  DABSN_REQUIRE(T == 0 || (U && nov && plast && expr && write && energy && sat && gate),
-                "core scan: null tape pointer");
-  int zr = dabsn_hip_zero(workspace, workspace_bytes(dtype, c, false), stream);
-  if (zr != DABSN_OK) return zr;
-  if (dtype == kBF16) {
-    FwdArgs<bf16> a{static_cast<int>(B), static_cast<int>(T), static_cast<int>(H), c.nct,
-                    static_cast<const bf16*>(Wx), static_cast<const bf16*>(Wgx),
-                    static_cast<const bf16*>(GA), to_params(params), b0, e0, c0,
-                    static_cast<bf16*>(U), static_cast<bf16*>(nov), static_cast<bf16*>(plast),
-                    static_cast<bf16*>(expr), static_cast<bf16*>(write),
-                    static_cast<bf16*>(energy), static_cast<bf16*>(sat), static_cast<bf16*>(gate),
-                    bF, eF, cF, static_cast<uint8_t*>(workspace),
-                    static_cast<uint32_t>(slot_bytes(dtype, c, false))};
-    return fwd_dispatch(c, a, stream);
-  }
-  FwdArgs<float> a{static_cast<int>(B), static_cast<int>(T), static_cast<int>(H), c.nct,
-                   static_cast<const float*>(Wx), static_cast<const float*>(Wgx),
-                   static_cast<const float*>(GA), to_params(params), b0, e0, c0,
-                   static_cast<float*>(U), static_cast<float*>(nov), static_cast<float*>(plast),
-                   static_cast<float*>(expr), static_cast<float*>(write),
-                   static_cast<float*>(energy), static_cast<float*>(sat), static_cast<float*>(gate),
-                   bF, eF, cF, static_cast<uint8_t*>(workspace),
-                   static_cast<uint32_t>(slot_bytes(dtype, c, false))};
-  return fwd_dispatch(c, a, stream);
+  if (dtype == kBF16) return fwd_dispatch(c, fwd_args<bf16>(f, c), stream);
+  return fwd_dispatch(c, fwd_args<float>(f, c), stream);
 }
 
 int dabsn_hip_core_scan_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* GAT,
@@ -1051,50 +1166,45 @@ int dabsn_hip_core_scan_bwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
                             void* gWx, void* gWgx, void* day, float* part_vec, float* part_scal,
                             float* gb0, float* ge0, float* gc0, void* workspace,
                             size_t workspace_bytes_, hipStream_t stream) {
-  const Cfg c = pick(dtype, B, H);
-  const int rc = check_common(dtype, B, T, H, params, c, workspace_bytes_,
-                              c.ksteps ? workspace_bytes(dtype, c, true) : 0);
+  const dabsn_core_bwd_call b{dtype, B, T, H, GAT, params, b0, c0, U, plast, expr, energy, sat,
+                              gate, gU, gNov, gP, gAy, gW, gE, gC, gbF, geF, gcF, gWx, gWgx, day,
+                              part_vec, part_scal, gb0, ge0, gc0, workspace, workspace_bytes_};
+  Cfg c;
+  int rc = prepare_bwd(b, c, stream);
   if (rc != DABSN_OK) return rc;
-  DABSN_REQUIRE(GAT && b0 && c0 && part_vec && part_scal && gb0 && ge0 && gc0 && workspace,
-                "core scan backward: null pointer argument");
-  DABSN_REQUIRE(T == 0 || (U && plast && expr && energy && sat && gate && gWx && gWgx && day),
-                "core scan backward: null tape pointer");
-  if (dtype == kF32 && c.ksteps > 32) {
-    dabsn::set_error("core scan backward: fp32 supports H <= 512 per workgroup register budget");
-    return DABSN_ERR_UNSUPPORTED;
+  if (dtype == kBF16) return bwd_dispatch(c, bwd_args<bf16>(b, c), stream);
+  return bwd_dispatch(c, bwd_args<float>(b, c), stream);
+}
+
+int dabsn_hip_core_scan_pair(const dabsn_core_fwd_call* f, const dabsn_core_bwd_call* b,
+                             hipStream_t stream) {
+  DABSN_REQUIRE(f && b, "core scan pair: null call");
+  DABSN_REQUIRE(f->dtype == b->dtype && f->B == b->B && f->H == b->H,
+                "core scan pair: the two scans must share dtype, B and H");
+  DABSN_REQUIRE(f->T > 0 && b->T > 0, "core scan pair: both scans need T > 0");
+  Cfg c, cb;
+  int rc = check_fwd(*f, c);
+  if (rc != DABSN_OK) return rc;
+  rc = check_bwd(*b, cb);
+  if (rc != DABSN_OK) return rc;
+  const int grid = c.nct * c.nbg;
+  // Nothing is enqueued unless both grids fit on the device at once.
+  {
+    int dev = 0, cus = 0;
+    DABSN_HIP_CHECK(hipGetDevice(&dev));
+    DABSN_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    if (cus < 2 * grid) {
+      dabsn::set_error("core scan pair needs %d CUs, device has %d", 2 * grid, cus);
+      return DABSN_ERR_UNSUPPORTED;
+    }
   }
-  int zr = dabsn_hip_zero(workspace, workspace_bytes(dtype, c, true), stream);
-  if (zr != DABSN_OK) return zr;
-  if (dtype == kBF16) {
-    using E = bf16;
-    BwdArgs<E> a{static_cast<int>(B), static_cast<int>(T), static_cast<int>(H), c.nct, c.kp,
-                 static_cast<const E*>(GAT), to_params(params), b0, c0,
-                 static_cast<const E*>(U), static_cast<const E*>(plast),
-                 static_cast<const E*>(expr), static_cast<const E*>(energy),
-                 static_cast<const E*>(sat), static_cast<const E*>(gate),
-                 static_cast<const E*>(gU), static_cast<const E*>(gNov),
-                 static_cast<const E*>(gP), static_cast<const E*>(gAy),
-                 static_cast<const E*>(gW), static_cast<const E*>(gE),
-                 static_cast<const E*>(gC), gbF, geF, gcF, static_cast<E*>(gWx),
-                 static_cast<E*>(gWgx), static_cast<E*>(day), part_vec, part_scal, gb0, ge0, gc0,
-                 static_cast<uint8_t*>(workspace),
-                 static_cast<uint32_t>(slot_bytes(dtype, c, true))};
-    return bwd_dispatch(c, a, stream);
-  }
-  using E = float;
-  BwdArgs<E> a{static_cast<int>(B), static_cast<int>(T), static_cast<int>(H), c.nct, c.kp,
-               static_cast<const E*>(GAT), to_params(params), b0, c0,
-               static_cast<const E*>(U), static_cast<const E*>(plast),
-               static_cast<const E*>(expr), static_cast<const E*>(energy),
-               static_cast<const E*>(sat), static_cast<const E*>(gate),
-               static_cast<const E*>(gU), static_cast<const E*>(gNov),
-               static_cast<const E*>(gP), static_cast<const E*>(gAy),
-               static_cast<const E*>(gW), static_cast<const E*>(gE),
-               static_cast<const E*>(gC), gbF, geF, gcF, static_cast<E*>(gWx),
-               static_cast<E*>(gWgx), static_cast<E*>(day), part_vec, part_scal, gb0, ge0, gc0,
-               static_cast<uint8_t*>(workspace),
-               static_cast<uint32_t>(slot_bytes(dtype, c, true))};
-  return bwd_dispatch(c, a, stream);
+  rc = dabsn_hip_zero(f->workspace, workspace_bytes(f->dtype, c, false), stream);
+  if (rc != DABSN_OK) return rc;
+  rc = dabsn_hip_zero(b->workspace, workspace_bytes(b->dtype, c, true), stream);
+  if (rc != DABSN_OK) return rc;
+  if (f->dtype == kBF16)
+    return pair_dispatch(c, fwd_args<bf16>(*f, c), bwd_args<bf16>(*b, c), grid, grid, stream);
+  return pair_dispatch(c, fwd_args<float>(*f, c), bwd_args<float>(*b, c), grid, grid, stream);
 }
 
 }  // extern "C"

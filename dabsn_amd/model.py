@@ -103,6 +103,8 @@ class DABSNBlock(nn.Module):
     def core_tapes(self, inputs: Tensor):
         chunk_t = self._resolve_block_chunk_t(inputs)
         if chunk_t and chunk_t < int(inputs.shape[1]):
+            if inputs.is_cuda and self.training and torch.is_grad_enabled():
+                return self.core.chunked_tapes(inputs, chunk_t)
             return self._chunked_core(inputs, chunk_t)
         return self.core(inputs, return_writes=True, return_cocktail=True)
 

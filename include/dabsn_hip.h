@@ -19,6 +19,12 @@
 
 #define DABSN_HIP_ABI_VERSION 2
 
+/* Status codes returned by every entry point. */
+#define DABSN_OK 0
+#define DABSN_ERR_HIP (-1)         /* a HIP runtime call failed */
+#define DABSN_ERR_ARG (-2)         /* invalid argument (shape, pointer, workspace size) */
+#define DABSN_ERR_UNSUPPORTED (-3) /* configuration this build or device cannot run */
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -80,6 +86,42 @@ int dabsn_hip_core_scan_bwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
                             void* gWx, void* gWgx, void* day, float* part_vec, float* part_scal,
                             float* gb0, float* ge0, float* gc0, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
+
+/* One forward scan and one independent reverse scan of the same (dtype, B, H) in a single
+ * cooperative launch. This is the schedule of a checkpointed, time-chunked core scan
+ * (src/dabsn/model.py:274-307): while chunk k runs its reverse scan, chunk k - 1 is
+ * recomputed. Fields mirror the arguments of dabsn_hip_core_scan_fwd / _bwd; each call
+ * has its own workspace. Returns DABSN_ERR_UNSUPPORTED (nothing launched) when the device
+ * cannot hold both grids at once; the caller then runs the two calls one after the other. */
+typedef struct dabsn_core_fwd_call {
+  int dtype;
+  int64_t B, T, H;
+  const void *Wx, *Wgx, *GA;
+  const dabsn_core_params* params;
+  const float *b0, *e0, *c0;
+  void *U, *nov, *plast, *expr, *write, *energy, *sat, *gate;
+  float *bF, *eF, *cF;
+  void* workspace;
+  size_t workspace_bytes;
+} dabsn_core_fwd_call;
+
+typedef struct dabsn_core_bwd_call {
+  int dtype;
+  int64_t B, T, H;
+  const void* GAT;
+  const dabsn_core_params* params;
+  const float *b0, *c0;
+  const void *U, *plast, *expr, *energy, *sat, *gate;
+  const void *gU, *gNov, *gP, *gAy, *gW, *gE, *gC;
+  const float *gbF, *geF, *gcF;
+  void *gWx, *gWgx, *day;
+  float *part_vec, *part_scal, *gb0, *ge0, *gc0;
+  void* workspace;
+  size_t workspace_bytes;
+} dabsn_core_bwd_call;
+
+int dabsn_hip_core_scan_pair(const dabsn_core_fwd_call* fwd, const dabsn_core_bwd_call* bwd,
+                             hipStream_t stream);
 
 /* ---- linear recurrence -----------------------------------------------------------
  * Replaces dabsn::linear_recurrence / dabsn::_linrec_backward

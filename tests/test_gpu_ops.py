@@ -325,3 +325,36 @@ def test_bank_gather_with_strided_inputs_matches_torch(cuda_device, B, T, H):
     assert_rel(K, F.normalize(Vr, dim=-1), 1e-6, "K")
     assert torch.equal(V.cpu(), Vr.float())
     assert torch.equal(Vn.cpu(), torch.gather(w, 1, nidx.cpu()[..., None].expand(-1, -1, H)).float())
+
+
+@pytest.mark.parametrize("dtype,B,T,H,chunk,tol", [(torch.float32, 3, 37, 40, 8, 1e-5),
+                                                   (torch.bfloat16, 16, 70, 2048, 16, 5e-3)])
+def test_chunked_core_scan_matches_full_op(cuda_device, dtype, B, T, H, chunk, tol):
+    """Checkpointed time chunks whose backward overlaps each recompute with the reverse scan
+    of the next chunk (one paired launch) against one full-length forward and backward.
+    Forward outputs are bit-identical. Gradients differ only in rounding: at a chunk boundary
+    the carried budget gradient is summed in a different order, which in bf16 can move a
+    stored gradient element by one bf16 ulp (2^-8 relative), hence 5e-3 Frobenius there."""
+    from dabsn_amd.kernels.chunked import chunked_core_scan
+
+    inp = core_case(300 + H, B, T, H)
+    x = [t.to(cuda_device) for t in inp]
+    x[0], x[1] = x[0].to(dtype), x[1].to(dtype)
+    leaves = [t.detach().requires_grad_(True) for t in x]
+    full = ops.core_scan_batched(*leaves)
+    leaves_c = [t.detach().requires_grad_(True) for t in x]
+    part = chunked_core_scan(chunk, *leaves_c)
+    for n, a, b in zip(OUT_NAMES, part[:8], full[:8]):
+        assert torch.equal(a, b), n
+    for n, a, b in zip(OUT_NAMES[8:], part[8:], full[8:]):
+        assert torch.equal(a, b), n
+    g = torch.Generator().manual_seed(21)
+    ups = [torch.randn(o.shape, generator=g).to(cuda_device).to(o.dtype) for o in full]
+    ups[7] = torch.zeros_like(ups[7])  # no gradient path through the gate tape
+    gf = torch.autograd.grad(full, leaves, ups, allow_unused=True)
+    gc = torch.autograd.grad(part, leaves_c, ups, allow_unused=True)
+    for i, (a, b) in enumerate(zip(gc, gf)):
+        assert (a is None) == (b is None), i
+        if a is not None:
+            err = rel_fro(a.float().cpu(), b.float().cpu())
+            assert err <= tol, f"input {i}: {err:.3e}"
