@@ -37,7 +37,7 @@ PTR4 = vp * 4
 class CoreFwdCall(ctypes.Structure):
     """Mirror of ``dabsn_core_fwd_call``."""
 
-    _fields_ = ([("dtype", i32), ("B", i64), ("T", i64), ("H", i64), ("Wx", vp), ("Wgx", vp),
+    _fields_ = ([("dtype", i32), ("B", i64), ("T", i64), ("H", i64), ("ldt", i64), ("Wx", vp), ("Wgx", vp),
                  ("GA", vp), ("params", ctypes.POINTER(CoreParams))]
                 + [(n, vp) for n in ("b0", "e0", "c0", "U", "nov", "plast", "expr", "write",
                                      "energy", "sat", "gate", "bF", "eF", "cF", "workspace")]
@@ -47,7 +47,7 @@ class CoreFwdCall(ctypes.Structure):
 class CoreBwdCall(ctypes.Structure):
     """Mirror of ``dabsn_core_bwd_call``."""
 
-    _fields_ = ([("dtype", i32), ("B", i64), ("T", i64), ("H", i64), ("GAT", vp),
+    _fields_ = ([("dtype", i32), ("B", i64), ("T", i64), ("H", i64), ("ldt", i64), ("GAT", vp),
                  ("params", ctypes.POINTER(CoreParams))]
                 + [(n, vp) for n in ("b0", "c0", "U", "plast", "expr", "energy", "sat", "gate",
                                      "gU", "gNov", "gP", "gAy", "gW", "gE", "gC", "gbF", "geF",
@@ -73,6 +73,8 @@ _SIGNATURES = {
         + [vp] * 6 + [vp] * 7 + [vp] * 3 + [vp] * 3 + [vp, vp] + [vp] * 3 + [vp, sz, vp],
         i32,
     ),
+    "dabsn_hip_core_scan_fwd_call": ([ctypes.POINTER(CoreFwdCall), vp], i32),
+    "dabsn_hip_core_scan_bwd_call": ([ctypes.POINTER(CoreBwdCall), vp], i32),
     "dabsn_hip_core_scan_pair": (
         [ctypes.POINTER(CoreFwdCall), ctypes.POINTER(CoreBwdCall), vp], i32),
     "dabsn_hip_linrec_fwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp], i32),

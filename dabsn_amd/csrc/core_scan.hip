@@ -217,6 +217,7 @@ __device__ __forceinline__ void publish(__amdgpu_buffer_rsrc_t xr, uint32_t slot
 template <typename E>
 struct FwdArgs {
   int B, T, H, nct;
+  int64_t ldt;  // time steps between consecutive batch rows of every [B, *, .] tensor (>= T)
   const E* Wx;
   const E* Wgx;
   const E* GA;  // [2H][H]: Ug rows then A rows
@@ -329,7 +330,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   float sb = act ? a.b0[static_cast<size_t>(b) * H + c] : 0.0f;
   float se = act ? a.e0[static_cast<size_t>(b) * H + c] : 0.0f;
   float sc = act ? a.c0[static_cast<size_t>(b) * H + c] : 0.0f;
-  const size_t row0 = static_cast<size_t>(b) * T;
+  const size_t row0 = static_cast<size_t>(b) * static_cast<size_t>(a.ldt);
 
   float ycur = (act && T > 0) ? tanhf(ld(a.Wx, row0 * H + c) + sb) : 0.0f;
   const int kb_y[1] = {ct * CH};
@@ -439,6 +440,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
 template <typename E>
 struct BwdArgs {
   int B, T, H, nct, kp;
+  int64_t ldt;  // as in FwdArgs
   const E* GAT;  // [H][2H]: transpose of [Ug; A]
   Params P;
   const float* b0;
@@ -709,7 +711,7 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
   float acc[NACC];
 #pragma unroll
   for (int i = 0; i < NACC; ++i) acc[i] = 0.0f;
-  const size_t row0 = static_cast<size_t>(b) * T;
+  const size_t row0 = static_cast<size_t>(b) * static_cast<size_t>(a.ldt);
   const int kb2[2] = {ct * CH, KP + ct * CH};
 
   // Pipeline state at the top of the step for time t: dg/dx are the final adjoint inputs
@@ -1037,6 +1039,9 @@ static int check_fwd(const dabsn_core_fwd_call& f, Cfg& c) {
   const int rc = check_common(f.dtype, f.B, f.T, f.H, f.params, c, f.workspace_bytes,
                               c.ksteps ? workspace_bytes(f.dtype, c, false) : 0);
   if (rc != DABSN_OK) return rc;
+  DABSN_REQUIRE(f.ldt == 0 || (f.ldt >= f.T && f.B * f.ldt * 2 * f.H < (1ll << 46)),
+                "core scan: bad time stride ldt=%lld for T=%lld", (long long)f.ldt,
+                (long long)f.T);
   DABSN_REQUIRE(f.Wx && f.Wgx && f.GA && f.b0 && f.e0 && f.c0 && f.bF && f.eF && f.cF &&
                     f.workspace,
                 "core scan: null pointer argument");
@@ -1051,6 +1056,9 @@ static int check_bwd(const dabsn_core_bwd_call& b, Cfg& c) {
   const int rc = check_common(b.dtype, b.B, b.T, b.H, b.params, c, b.workspace_bytes,
                               c.ksteps ? workspace_bytes(b.dtype, c, true) : 0);
   if (rc != DABSN_OK) return rc;
+  DABSN_REQUIRE(b.ldt == 0 || (b.ldt >= b.T && b.B * b.ldt * 2 * b.H < (1ll << 46)),
+                "core scan backward: bad time stride ldt=%lld for T=%lld", (long long)b.ldt,
+                (long long)b.T);
   DABSN_REQUIRE(b.GAT && b.b0 && b.c0 && b.part_vec && b.part_scal && b.gb0 && b.ge0 && b.gc0 &&
                     b.workspace,
                 "core scan backward: null pointer argument");
@@ -1079,7 +1087,7 @@ static int prepare_bwd(const dabsn_core_bwd_call& b, Cfg& c, hipStream_t stream)
 template <typename E>
 static FwdArgs<E> fwd_args(const dabsn_core_fwd_call& f, const Cfg& c) {
   return FwdArgs<E>{static_cast<int>(f.B), static_cast<int>(f.T), static_cast<int>(f.H), c.nct,
-                    static_cast<const E*>(f.Wx), static_cast<const E*>(f.Wgx),
+                    f.ldt > 0 ? f.ldt : f.T, static_cast<const E*>(f.Wx), static_cast<const E*>(f.Wgx),
                     static_cast<const E*>(f.GA), to_params(f.params), f.b0, f.e0, f.c0,
                     static_cast<E*>(f.U), static_cast<E*>(f.nov), static_cast<E*>(f.plast),
                     static_cast<E*>(f.expr), static_cast<E*>(f.write), static_cast<E*>(f.energy),
@@ -1091,7 +1099,7 @@ static FwdArgs<E> fwd_args(const dabsn_core_fwd_call& f, const Cfg& c) {
 template <typename E>
 static BwdArgs<E> bwd_args(const dabsn_core_bwd_call& b, const Cfg& c) {
   return BwdArgs<E>{static_cast<int>(b.B), static_cast<int>(b.T), static_cast<int>(b.H), c.nct,
-                    c.kp, static_cast<const E*>(b.GAT), to_params(b.params), b.b0, b.c0,
+                    c.kp, b.ldt > 0 ? b.ldt : b.T, static_cast<const E*>(b.GAT), to_params(b.params), b.b0, b.c0,
                     static_cast<const E*>(b.U), static_cast<const E*>(b.plast),
                     static_cast<const E*>(b.expr), static_cast<const E*>(b.energy),
                     static_cast<const E*>(b.sat), static_cast<const E*>(b.gate),
@@ -1147,14 +1155,19 @@ int dabsn_hip_core_scan_fwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
                             void* plast, void* expr, void* write, void* energy, void* sat,
                             void* gate, float* bF, float* eF, float* cF, void* workspace,
                             size_t workspace_bytes_, hipStream_t stream) {
-  const dabsn_core_fwd_call f{dtype, B, T, H, Wx, Wgx, GA, params, b0, e0, c0, U, nov, plast,
-                              expr, write, energy, sat, gate, bF, eF, cF, workspace,
+  const dabsn_core_fwd_call f{dtype, B, T, H, 0, Wx, Wgx, GA, params, b0, e0, c0, U, nov,
+                              plast, expr, write, energy, sat, gate, bF, eF, cF, workspace,
                               workspace_bytes_};
+  return dabsn_hip_core_scan_fwd_call(&f, stream);
+}
+
+int dabsn_hip_core_scan_fwd_call(const dabsn_core_fwd_call* f, hipStream_t stream) {
+  DABSN_REQUIRE(f, "core scan: null call");
   Cfg c;
-  int rc = prepare_fwd(f, c, stream);
+  int rc = prepare_fwd(*f, c, stream);
   if (rc != DABSN_OK) return rc;
-  if (dtype == kBF16) return fwd_dispatch(c, fwd_args<bf16>(f, c), stream);
-  return fwd_dispatch(c, fwd_args<float>(f, c), stream);
+  if (f->dtype == kBF16) return fwd_dispatch(c, fwd_args<bf16>(*f, c), stream);
+  return fwd_dispatch(c, fwd_args<float>(*f, c), stream);
 }
 
 int dabsn_hip_core_scan_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* GAT,
@@ -1166,14 +1179,20 @@ int dabsn_hip_core_scan_bwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
                             void* gWx, void* gWgx, void* day, float* part_vec, float* part_scal,
                             float* gb0, float* ge0, float* gc0, void* workspace,
                             size_t workspace_bytes_, hipStream_t stream) {
-  const dabsn_core_bwd_call b{dtype, B, T, H, GAT, params, b0, c0, U, plast, expr, energy, sat,
-                              gate, gU, gNov, gP, gAy, gW, gE, gC, gbF, geF, gcF, gWx, gWgx, day,
-                              part_vec, part_scal, gb0, ge0, gc0, workspace, workspace_bytes_};
+  const dabsn_core_bwd_call b{dtype, B, T, H, 0, GAT, params, b0, c0, U, plast, expr, energy,
+                              sat, gate, gU, gNov, gP, gAy, gW, gE, gC, gbF, geF, gcF, gWx, gWgx,
+                              day, part_vec, part_scal, gb0, ge0, gc0, workspace,
+                              workspace_bytes_};
+  return dabsn_hip_core_scan_bwd_call(&b, stream);
+}
+
+int dabsn_hip_core_scan_bwd_call(const dabsn_core_bwd_call* b, hipStream_t stream) {
+  DABSN_REQUIRE(b, "core scan backward: null call");
   Cfg c;
-  int rc = prepare_bwd(b, c, stream);
+  int rc = prepare_bwd(*b, c, stream);
   if (rc != DABSN_OK) return rc;
-  if (dtype == kBF16) return bwd_dispatch(c, bwd_args<bf16>(b, c), stream);
-  return bwd_dispatch(c, bwd_args<float>(b, c), stream);
+  if (b->dtype == kBF16) return bwd_dispatch(c, bwd_args<bf16>(*b, c), stream);
+  return bwd_dispatch(c, bwd_args<float>(*b, c), stream);
 }
 
 int dabsn_hip_core_scan_pair(const dabsn_core_fwd_call* f, const dabsn_core_bwd_call* b,

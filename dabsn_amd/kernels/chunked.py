@@ -3,11 +3,18 @@
 Reference behaviour: src/dabsn/model.py:274-307. The block scan runs in time chunks of
 ``chunk_t`` steps with the (b, e, c) state carried from chunk to chunk, and every chunk is
 checkpointed, so the backward recomputes a chunk's forward scan right before running its
-reverse scan. The same work is scheduled differently here: the recompute of chunk k - 1
-depends only on the saved start state of that chunk, not on the reverse scan of chunk k,
-so the two run as one cooperative launch on disjoint halves of the device
-(``dabsn_hip_core_scan_pair``). When the device cannot hold both grids at once the two
-launches run one after the other. Outputs and gradients are the same either way.
+reverse scan. The same work is scheduled differently here:
+
+* every chunk reads and writes its time window of full-length tensors in place (the C call
+  descriptors carry a time stride ``ldt``), so there are no per-chunk copies or
+  concatenations;
+* the recompute of chunk k - 1 depends only on the saved start state of that chunk, not on
+  the reverse scan of chunk k, so the two run as one cooperative launch on disjoint halves
+  of the device (``dabsn_hip_core_scan_pair``). When the device cannot hold both grids at
+  once the two launches run one after the other.
+
+Outputs equal the single full-length scan bit for bit; gradients equal it up to the
+rounding of the carried state gradient at chunk boundaries.
 """
 
 from __future__ import annotations
@@ -22,76 +29,80 @@ from .. import _lib
 from . import ops
 
 
+def _ptr(t: Optional[Tensor], off: int = 0) -> Optional[int]:
+    """Device address of element `off` of `t` (None for an absent tensor)."""
+    return None if t is None else t.data_ptr() + off * t.element_size()
+
+
 def _empty(shape, like: Tensor, dtype=None) -> Tensor:
     return torch.empty(shape, device=like.device, dtype=dtype or like.dtype)
 
 
+class _Tapes:
+    """Full-length forward outputs: U [B, T, 2H] and the 7 tapes [B, T, H]."""
+
+    def __init__(self, like: Tensor, B: int, T: int, H: int) -> None:
+        self.U = _empty((B, T, 2 * H), like)
+        self.tapes = [_empty((B, T, H), like) for _ in range(7)]
+
+
 class _Fwd:
-    """Outputs, workspace and C call descriptor of one forward scan."""
+    """C call descriptor, workspace and final state of the forward scan of steps [t0, t1)."""
 
     def __init__(self, code: int, Wx: Tensor, Wgx: Tensor, GA: Tensor, params, b0: Tensor,
-                 e0: Tensor, c0: Tensor) -> None:
+                 e0: Tensor, c0: Tensor, out: _Tapes, t0: int, t1: int) -> None:
         lib = _lib.load()
         B, T, H = Wx.shape
-        self.inputs = (Wx, Wgx, GA, b0, e0, c0)
-        self.U = _empty((B, T, 2 * H), Wx)
-        self.tapes = [_empty((B, T, H), Wx) for _ in range(7)]
+        self.keep = (Wx, Wgx, GA, b0, e0, c0, out)
         self.finals = [_empty((B, H), Wx, torch.float32) for _ in range(3)]
         nbytes = lib.dabsn_hip_core_scan_workspace_bytes(code, B, H, 0)
         self.ws = _empty((nbytes,), Wx, torch.uint8)
         self.params = params
+        o = t0 * H
         self.call = _lib.CoreFwdCall(
-            code, B, T, H, Wx.data_ptr(), Wgx.data_ptr(), GA.data_ptr(), ctypes.pointer(params),
-            b0.data_ptr(), e0.data_ptr(), c0.data_ptr(), self.U.data_ptr(),
-            *[t.data_ptr() for t in self.tapes], *[f.data_ptr() for f in self.finals],
-            self.ws.data_ptr(), nbytes)
+            code, B, t1 - t0, H, T, _ptr(Wx, o), _ptr(Wgx, o), _ptr(GA), ctypes.pointer(params),
+            _ptr(b0), _ptr(e0), _ptr(c0), _ptr(out.U, 2 * o), *[_ptr(t, o) for t in out.tapes],
+            *[_ptr(f) for f in self.finals], _ptr(self.ws), nbytes)
 
     def launch(self, stream) -> None:
-        c = self.call
-        _lib.check(_lib.load().dabsn_hip_core_scan_fwd(
-            c.dtype, c.B, c.T, c.H, c.Wx, c.Wgx, c.GA, c.params, c.b0, c.e0, c.c0, c.U, c.nov,
-            c.plast, c.expr, c.write, c.energy, c.sat, c.gate, c.bF, c.eF, c.cF, c.workspace,
-            c.workspace_bytes, stream), "core scan forward")
+        _lib.check(_lib.load().dabsn_hip_core_scan_fwd_call(ctypes.byref(self.call), stream),
+                   "core scan forward")
 
 
 class _Bwd:
-    """Outputs, workspace and C call descriptor of one reverse scan."""
+    """C call descriptor, workspace and partial sums of the reverse scan of steps [t0, t1).
 
-    def __init__(self, code: int, GAT: Tensor, params, b0: Tensor, c0: Tensor,
-                 saved: Sequence[Tensor], grads: Sequence[Optional[Tensor]],
-                 gfin: Sequence[Optional[Tensor]]) -> None:
+    `outs` = (gWx, gWgx, day), full-length [B, T, H]; the scan writes its window of each."""
+
+    def __init__(self, code: int, GAT: Tensor, params, b0: Tensor, c0: Tensor, rec: _Tapes,
+                 grads: Sequence[Optional[Tensor]], gfin: Sequence[Optional[Tensor]],
+                 outs: Sequence[Tensor], t0: int, t1: int) -> None:
         lib = _lib.load()
-        U, plast = saved[0], saved[1]
-        B, T, H = plast.shape
-        self.keep = (GAT, b0, c0, *saved, *[g for g in grads if g is not None],
-                     *[g for g in gfin if g is not None])
-        self.gWx = _empty((B, T, H), plast)
-        self.gWgx = _empty((B, T, H), plast)
-        self.day = _empty((B, T, H), plast)
+        B, T, H = outs[0].shape
+        self.keep = (GAT, b0, c0, rec, *[g for g in grads if g is not None],
+                     *[g for g in gfin if g is not None], *outs)
         nbg, nwg = _lib.i64(), _lib.i64()
         _lib.check(lib.dabsn_hip_core_scan_layout(code, B, H, ctypes.byref(nbg), ctypes.byref(nwg)),
                    "core scan layout")
-        self.part_vec = _empty((nbg.value, 16, H), plast, torch.float32)
-        self.part_scal = _empty((nwg.value, 3), plast, torch.float32)
-        self.g0 = [_empty((B, H), plast, torch.float32) for _ in range(3)]
+        like = outs[0]
+        self.part_vec = _empty((nbg.value, 16, H), like, torch.float32)
+        self.part_scal = _empty((nwg.value, 3), like, torch.float32)
+        self.g0 = [_empty((B, H), like, torch.float32) for _ in range(3)]
         nbytes = lib.dabsn_hip_core_scan_workspace_bytes(code, B, H, 1)
-        self.ws = _empty((nbytes,), plast, torch.uint8)
+        self.ws = _empty((nbytes,), like, torch.uint8)
         self.params = params
-        ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        o = t0 * H
+        saved = (rec.tapes[1], rec.tapes[2], rec.tapes[4], rec.tapes[5], rec.tapes[6])
         self.call = _lib.CoreBwdCall(
-            code, B, T, H, GAT.data_ptr(), ctypes.pointer(params), b0.data_ptr(), c0.data_ptr(),
-            *[x.data_ptr() for x in saved], *[ptr(g) for g in grads], *[ptr(g) for g in gfin],
-            self.gWx.data_ptr(), self.gWgx.data_ptr(), self.day.data_ptr(),
-            self.part_vec.data_ptr(), self.part_scal.data_ptr(), *[g.data_ptr() for g in self.g0],
-            self.ws.data_ptr(), nbytes)
+            code, B, t1 - t0, H, T, _ptr(GAT), ctypes.pointer(params), _ptr(b0), _ptr(c0),
+            _ptr(rec.U, 2 * o), *[_ptr(x, o) for x in saved],
+            _ptr(grads[0], 2 * o), *[_ptr(g, o) for g in grads[1:]],
+            *[_ptr(g) for g in gfin], *[_ptr(x, o) for x in outs], _ptr(self.part_vec),
+            _ptr(self.part_scal), *[_ptr(g) for g in self.g0], _ptr(self.ws), nbytes)
 
     def launch(self, stream) -> None:
-        c = self.call
-        _lib.check(_lib.load().dabsn_hip_core_scan_bwd(
-            c.dtype, c.B, c.T, c.H, c.GAT, c.params, c.b0, c.c0, c.U, c.plast, c.expr, c.energy,
-            c.sat, c.gate, c.gU, c.gNov, c.gP, c.gAy, c.gW, c.gE, c.gC, c.gbF, c.geF, c.gcF,
-            c.gWx, c.gWgx, c.day, c.part_vec, c.part_scal, c.gb0, c.ge0, c.gc0, c.workspace,
-            c.workspace_bytes, stream), "core scan backward")
+        _lib.check(_lib.load().dabsn_hip_core_scan_bwd_call(ctypes.byref(self.call), stream),
+                   "core scan backward")
 
 
 def _launch_pair(fwd: _Fwd, bwd: _Bwd, stream) -> None:
@@ -123,34 +134,31 @@ class _ChunkedCoreScan(torch.autograd.Function):
         GA = torch.cat((Ug, A), dim=0).to(dt).contiguous()
         params, keep = ops._core_params(vecs, scal)
         carry = [x.float().contiguous() for x in (b0, e0, c0)]
-        starts, outs = [], []
         Wx_c, Wgx_c = Wx.contiguous(), Wgx.to(dt).contiguous()
+        out = _Tapes(Wx_c, B, T, H)
+        starts = []
         for t0, t1 in _chunks(T, chunk):
             starts.append(torch.stack(carry))
-            f = _Fwd(code, Wx_c[:, t0:t1].contiguous(), Wgx_c[:, t0:t1].contiguous(), GA, params,
-                     *carry)
+            f = _Fwd(code, Wx_c, Wgx_c, GA, params, *carry, out, t0, t1)
             tk = ops.KernelTimer.begin("core_scan_fwd", Wx)
             f.launch(stream)
             ops.KernelTimer.end(tk)
             ops._record_error_word(f.ws, "core scan forward")
-            outs.append(f)
             carry = f.finals
         del keep
-        U = torch.cat([f.U for f in outs], 1)
-        tapes = [torch.cat([f.tapes[i] for f in outs], 1) for i in range(7)]
         finals = [f.to(x.dtype) for f, x in zip(carry, (b0, e0, c0))]
         ctx.chunk = chunk
         ctx.meta = [(x.dtype, tuple(x.shape)) for x in inputs]
         ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, torch.stack(starts))
         ctx.set_materialize_grads(False)
-        return (U, *tapes, *finals)
+        return (out.U, *out.tapes, *finals)
 
     @staticmethod
     def backward(ctx, *grads):
         saved = ctx.saved_tensors
         Wx, Wgx, Ug, A = saved[:4]
         vecs, scal = saved[4:20], saved[20:23]
-        starts = saved[23]  # [K, 3, B, H]
+        starts = saved[23]  # [K, 3, B, H] chunk start states
         B, T, H = Wx.shape
         dt = Wx.dtype
         code = ops._code(dt)
@@ -160,35 +168,29 @@ class _ChunkedCoreScan(torch.autograd.Function):
         params, keep = ops._core_params(vecs, scal)
         bounds = _chunks(T, ctx.chunk)
         K = len(bounds)
-
-        def slice_grad(g: Optional[Tensor], t0: int, t1: int) -> Optional[Tensor]:
-            return None if g is None else g[:, t0:t1].to(dt).contiguous()
+        up = [None if g is None else g.to(dt).contiguous() for g in grads[:7]]
+        carry = [None if g is None else g.float().contiguous() for g in grads[8:11]]
+        gWx, gWgx, day = (_empty((B, T, H), Wx) for _ in range(3))
+        rec = _Tapes(Wx, B, T, H)  # recomputed forward outputs, filled window by window
 
         def fwd_of(k: int) -> _Fwd:
-            t0, t1 = bounds[k]
-            return _Fwd(code, Wx[:, t0:t1].contiguous(), Wgx[:, t0:t1].contiguous(), GA, params,
-                        starts[k, 0].contiguous(), starts[k, 1].contiguous(),
-                        starts[k, 2].contiguous())
+            return _Fwd(code, Wx, Wgx, GA, params, starts[k, 0].contiguous(),
+                        starts[k, 1].contiguous(), starts[k, 2].contiguous(), rec, *bounds[k])
 
-        carry = [None if g is None else g.float().contiguous() for g in grads[8:11]]
-        gWx, gWgx = [None] * K, [None] * K
         gvec = torch.zeros((16, H), device=Wx.device, dtype=torch.float32)
         gscal = torch.zeros((3,), device=Wx.device, dtype=torch.float32)
-        gUg = torch.zeros((H, H), device=Wx.device, dtype=torch.float32)
-        gA = torch.zeros((H, H), device=Wx.device, dtype=torch.float32)
-        rec = fwd_of(K - 1)
+        first = fwd_of(K - 1)
         tk = ops.KernelTimer.begin("core_scan_fwd", Wx)
-        rec.launch(stream)
+        first.launch(stream)
         ops.KernelTimer.end(tk)
-        ops._record_error_word(rec.ws, "core scan forward")
+        ops._record_error_word(first.ws, "core scan forward")
         for k in range(K - 1, -1, -1):
-            t0, t1 = bounds[k]
-            up = [slice_grad(g, t0, t1) for g in grads[:7]]
-            saved_k = (rec.U, rec.tapes[1], rec.tapes[2], rec.tapes[4], rec.tapes[5], rec.tapes[6])
             bw = _Bwd(code, GAT, params, starts[k, 0].contiguous(), starts[k, 2].contiguous(),
-                      saved_k, up, carry)
-            nxt = fwd_of(k - 1) if k > 0 else None
-            if nxt is not None:
+                      rec, up, carry, (gWx, gWgx, day), *bounds[k])
+            if k > 0:
+                # The recompute writes window k - 1 of `rec` while this reverse scan reads
+                # window k: disjoint rows of the same buffers.
+                nxt = fwd_of(k - 1)
                 tk = ops.KernelTimer.begin("core_scan_pair", Wx)
                 _launch_pair(nxt, bw, stream)
                 ops.KernelTimer.end(tk)
@@ -198,17 +200,16 @@ class _ChunkedCoreScan(torch.autograd.Function):
                 bw.launch(stream)
                 ops.KernelTimer.end(tk)
             ops._record_error_word(bw.ws, "core scan backward")
-            gWx[k], gWgx[k] = bw.gWx, bw.gWgx
             gvec += bw.part_vec.sum(0)
             gscal += bw.part_scal.sum(0)
-            y = rec.U[..., :H].reshape(-1, H)
-            gUg += (bw.gWgx.reshape(-1, H).t() @ y).float()
-            gA += (bw.day.reshape(-1, H).t() @ y).float()
             carry = bw.g0
-            rec = nxt
         del keep
-        out = [torch.cat(gWx, 1), torch.cat(gWgx, 1), gUg, gA, *[gvec[i] for i in range(16)],
-               *[gscal[i] for i in range(3)], *carry]
+        # grad [Ug; A] = [gWgx; day]^T y over the whole sequence (y = first half of U).
+        y = rec.U.view(B * T, 2 * H)[:, :H]
+        gUg = (gWgx.view(B * T, H).t() @ y).float()
+        gA = (day.view(B * T, H).t() @ y).float()
+        out = [gWx, gWgx, gUg, gA, *[gvec[i] for i in range(16)], *[gscal[i] for i in range(3)],
+               *carry]
         return (None, *[g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(out, ctx.meta)])
 
 

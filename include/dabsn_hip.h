@@ -87,15 +87,13 @@ int dabsn_hip_core_scan_bwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
                             float* gb0, float* ge0, float* gc0, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
-/* One forward scan and one independent reverse scan of the same (dtype, B, H) in a single
- * cooperative launch. This is the schedule of a checkpointed, time-chunked core scan
- * (src/dabsn/model.py:274-307): while chunk k runs its reverse scan, chunk k - 1 is
- * recomputed. Fields mirror the arguments of dabsn_hip_core_scan_fwd / _bwd; each call
- * has its own workspace. Returns DABSN_ERR_UNSUPPORTED (nothing launched) when the device
- * cannot hold both grids at once; the caller then runs the two calls one after the other. */
+/* Call descriptors: the arguments of dabsn_hip_core_scan_fwd / _bwd, plus `ldt`, the
+ * number of time steps between consecutive batch rows of every [B, *, .] tensor of the
+ * call (0 = T, i.e. dense). With ldt > T the call scans a time window [t0, t0 + T) of
+ * longer sequences in place: every pointer is offset to step t0 and rows are ldt apart. */
 typedef struct dabsn_core_fwd_call {
   int dtype;
-  int64_t B, T, H;
+  int64_t B, T, H, ldt;
   const void *Wx, *Wgx, *GA;
   const dabsn_core_params* params;
   const float *b0, *e0, *c0;
@@ -107,7 +105,7 @@ typedef struct dabsn_core_fwd_call {
 
 typedef struct dabsn_core_bwd_call {
   int dtype;
-  int64_t B, T, H;
+  int64_t B, T, H, ldt;
   const void* GAT;
   const dabsn_core_params* params;
   const float *b0, *c0;
@@ -120,6 +118,15 @@ typedef struct dabsn_core_bwd_call {
   size_t workspace_bytes;
 } dabsn_core_bwd_call;
 
+int dabsn_hip_core_scan_fwd_call(const dabsn_core_fwd_call* fwd, hipStream_t stream);
+int dabsn_hip_core_scan_bwd_call(const dabsn_core_bwd_call* bwd, hipStream_t stream);
+
+/* One forward scan and one independent reverse scan of the same (dtype, B, H) in a single
+ * cooperative launch. This is the schedule of a checkpointed, time-chunked core scan
+ * (src/dabsn/model.py:274-307): while chunk k runs its reverse scan, chunk k - 1 is
+ * recomputed. Each call has its own workspace. Returns DABSN_ERR_UNSUPPORTED (nothing
+ * launched) when the device cannot hold both grids at once; the caller then runs the two
+ * calls one after the other. */
 int dabsn_hip_core_scan_pair(const dabsn_core_fwd_call* fwd, const dabsn_core_bwd_call* bwd,
                              hipStream_t stream);
 
