@@ -167,37 +167,35 @@ __device__ __forceinline__ uint32_t* my_counter(uint32_t* ctr, int nct, int bid)
 __device__ __forceinline__ void drain_vmem() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Publishes `nvals` values per (unit, batch) pair into slot `xs` of the exchange
-// buffer at k = kbase[i] + cl. bf16 stages through LDS so each lane stores one 16-byte
-// unit (8 consecutive k for one batch column); fp32 stores one word per value.
-template <typename E, int CH, int NV, int NT>
+// buffer at k = kbase[i] + cl; every thread of the workgroup calls it. bf16: the 8
+// consecutive lanes that hold units 8g..8g+7 of one batch row pack their values with
+// lane shuffles and the first of them stores the 16-byte unit; fp32 stores one word per
+// value. Returns once every store of the workgroup is complete.
+template <typename E, int CH, int NV>
 __device__ __forceinline__ void publish(__amdgpu_buffer_rsrc_t xr, uint32_t slot_bytes, int xs,
                                         const int (&kbase)[NV], const float (&vals)[NV],
-                                        bool is_pair, int cl, int bl, bf16 (*stage)[NB][CH]) {
-  const int tid = threadIdx.x;
+                                        bool is_pair, int cl, int bl) {
   if constexpr (is_bf16<E>::value) {
+    // Pair threads fill whole waves (tid = bl * CH + cl), so `is_pair` is wave-uniform
+    // and lane & 7 == cl & 7.
+    static_assert(CH % 8 == 0 && (CH * NB) % 64 == 0, "pair threads must fill whole waves");
     if (is_pair) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) stage[i][bl][cl] = f2bf(vals[i]);
-    }
-    __syncthreads();
-    constexpr int GROUPS = CH / 8;
-    constexpr int UNITS = NV * GROUPS * NB;
-    for (int u = tid; u < UNITS; u += NT) {
-      const int i = u / (GROUPS * NB);
-      const int rem = u % (GROUPS * NB);
-      const int g = rem / NB, n = rem % NB;
-      const int k0 = kbase[i] + g * 8;
-      uint32_t w[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        w[q] = static_cast<uint32_t>(stage[i][n][g * 8 + 2 * q]) |
-               (static_cast<uint32_t>(stage[i][n][g * 8 + 2 * q + 1]) << 16);
-      u32x4 v = {w[0], w[1], w[2], w[3]};
-      const uint32_t off = xs * slot_bytes + xoff<bf16>(k0, n) * 2u;
-      __builtin_amdgcn_raw_buffer_store_b128(v, xr, static_cast<int>(off), 0, kCoherent);
+      for (int i = 0; i < NV; ++i) {
+        const int h = static_cast<int>(f2bf(vals[i]));
+        const int w0 = h | (__shfl_down(h, 1, 8) << 16);
+        const int w1 = __shfl_down(w0, 2, 8);
+        const int w2 = __shfl_down(w0, 4, 8);
+        const int w3 = __shfl_down(w0, 6, 8);
+        if ((cl & 7) == 0) {
+          const u32x4 v = {static_cast<uint32_t>(w0), static_cast<uint32_t>(w1),
+                           static_cast<uint32_t>(w2), static_cast<uint32_t>(w3)};
+          const uint32_t off = xs * slot_bytes + xoff<bf16>(kbase[i] + cl, bl) * 2u;
+          __builtin_amdgcn_raw_buffer_store_b128(v, xr, static_cast<int>(off), 0, kCoherent);
+        }
+      }
     }
   } else {
-    (void)stage;
     if (is_pair) {
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
@@ -278,8 +276,10 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   static_assert(ROWS % 16 == 0, "CH must be a multiple of 8");
   static_assert(PAIRS <= NT, "one thread per (unit, batch) pair");
 
-  __shared__ float red[NW][MT][16][16];
-  __shared__ bf16 stage[1][NB][CH];
+  // Partial products of the NW waves, [wave][tile][batch column][row]: each lane writes
+  // its 4 accumulator rows as one 16-byte vector and each pair thread reads 64
+  // consecutive words per wave, so neither side has LDS bank conflicts.
+  __shared__ __attribute__((aligned(16))) float red[NW][MT][16][16];
   __shared__ int s_abort;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -336,7 +336,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   const int kb_y[1] = {ct * CH};
   if (T > 0) {
     const float v[1] = {ycur};
-    publish<E, CH, 1, NT>(xr, a.slot_bytes, 0, kb_y, v, is_pair, cl, bl, stage);
+    publish<E, CH, 1>(xr, a.slot_bytes, 0, kb_y, v, is_pair, cl, bl);
     if (tid == 0) arrive(counter);
   }
 
@@ -365,8 +365,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) red[wave][mt][(lane >> 4) * 4 + j][lane & 15] = acc[mt][j];
+      *reinterpret_cast<f32x4*>(&red[wave][mt][lane & 15][(lane >> 4) * 4]) = acc[mt];
     }
     __syncthreads();
 
@@ -377,8 +376,8 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
       const int ra = CH + cl;
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        ug += red[w][cl >> 4][cl & 15][bl];
-        ay += red[w][ra >> 4][ra & 15][bl];
+        ug += red[w][cl >> 4][bl][cl & 15];
+        ay += red[w][ra >> 4][bl][ra & 15];
       }
       // The reference's recurrent GEMM returns the activation dtype.
       ug = round_to<E>(ug);
@@ -390,7 +389,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
     }
     if (t + 1 < T) {
       const float v[1] = {ynext};
-      publish<E, CH, 1, NT>(xr, a.slot_bytes, (t + 1) & 1, kb_y, v, is_pair, cl, bl, stage);
+      publish<E, CH, 1>(xr, a.slot_bytes, (t + 1) & 1, kb_y, v, is_pair, cl, bl);
       if (tid == 0) arrive(counter);
     }
     // Off the critical path (overlaps the next barrier): energy and cortisol, tapes.
@@ -647,8 +646,7 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
   constexpr int NACC = 19;
   static_assert(PAIRS <= NT, "one thread per (unit, batch) pair");
 
-  __shared__ float red[NW][MTB][16][16];
-  __shared__ bf16 stage[2][NB][CH];
+  __shared__ __attribute__((aligned(16))) float red[NW][MTB][16][16];  // as in the forward
   __shared__ float accs[NB][CH][NACC];
   __shared__ int s_abort;
 
@@ -742,7 +740,7 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
     const int t = T - 1 - n;
     {
       const float v[2] = {dg, dx};
-      publish<E, CH, 2, NT>(xr, a.slot_bytes, n & 1, kb2, v, is_pair, cl, bl, stage);
+      publish<E, CH, 2>(xr, a.slot_bytes, n & 1, kb2, v, is_pair, cl, bl);
       if (tid == 0) arrive(counter);
     }
     // Off the critical path: outputs of t (and the pre-activation grad of t + 1) and the
@@ -780,14 +778,13 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
     }
 #pragma unroll
     for (int mt = 0; mt < MTB; ++mt) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) red[wave][mt][(lane >> 4) * 4 + j][lane & 15] = accm[mt][j];
+      *reinterpret_cast<f32x4*>(&red[wave][mt][lane & 15][(lane >> 4) * 4]) = accm[mt];
     }
     __syncthreads();
     if (act) {
       float adj = 0.0f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) adj += red[w][cl >> 4][cl & 15][bl];
+      for (int w = 0; w < NW; ++w) adj += red[w][cl >> 4][bl][cl & 15];
       adj = round_to<E>(adj);
       const float gy = gyx + adj;
       const float x = gy * (1.0f - yv * yv);  // pre-activation grad of t (gWx)
