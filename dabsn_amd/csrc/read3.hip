@@ -472,9 +472,9 @@ static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, 
     a.A = q; a.lda = H; a.sA = T * H;
     a.B = K; a.ldb = H; a.sB = N * H;
     a.C = S; a.ldc = N; a.sC = T * N;
-    a.alpha = 1.0f; a.beta = 0.0f;
+    a.alpha = 1.0f;
     a.ranges = rs; a.mtiles = QT;
-    DABSN_HIP_CHECK((gemm::launch<E, float, false, true>(a, (int)B, stream)));
+    DABSN_HIP_CHECK((gemm::launch<E, float>(a, (int)B, stream)));
   }
   RowCtx c{(int)T, (int)N, mode, S, kb, adm, cb, ck, idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
   const unsigned row_blocks = static_cast<unsigned>((B * T + NWV - 1) / NWV);
@@ -494,9 +494,9 @@ static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, 
     a.B = VT; a.ldb = N; a.sB = H * N;
     a.A2 = PVn; a.B2 = VnT;
     a.C = out; a.ldc = H; a.sC = T * H;
-    a.alpha = 1.0f; a.beta = 0.0f;
+    a.alpha = 1.0f;
     a.ranges = ro; a.mtiles = QT;
-    DABSN_HIP_CHECK((gemm::launch<E, E, false, true>(a, (int)B, stream)));
+    DABSN_HIP_CHECK((gemm::launch<E, E>(a, (int)B, stream)));
   }
   return DABSN_OK;
 }
@@ -532,9 +532,9 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
     a.A = gout; a.lda = H; a.sA = T * H;
     a.B = w == 0 ? V : Vn; a.ldb = H; a.sB = N * H;
     a.C = w == 0 ? dPV : dPVn; a.ldc = N; a.sC = T * N;
-    a.alpha = 1.0f; a.beta = 0.0f;
+    a.alpha = 1.0f;
     a.ranges = rs; a.mtiles = QT;
-    DABSN_HIP_CHECK((gemm::launch<E, float, false, true>(a, (int)B, stream)));
+    DABSN_HIP_CHECK((gemm::launch<E, float>(a, (int)B, stream)));
   }
   RowCtx c{(int)T, (int)N, mode, S, kb, adm, cb, ck, idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
   hipLaunchKernelGGL(grad_rows_kernel, dim3((unsigned)((B * T + NWV - 1) / NWV)), dim3(NTH), 0,
@@ -566,7 +566,7 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
     a.C = gq; a.ldc = H; a.sC = T * H;
     a.alpha = 1.0f;
     a.ranges = ro; a.mtiles = QT;
-    DABSN_HIP_CHECK((gemm::launch<E, E, false, true>(a, (int)B, stream)));
+    DABSN_HIP_CHECK((gemm::launch<E, E>(a, (int)B, stream)));
   }
   // Entries of G, P_V, P_Vn the GEMMs read (rows t >= the bank tile's earliest query,
   // whole 128-slot tiles below roundup(nhi)) are all written by grad_tile_kernel; the
@@ -582,7 +582,7 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
     a.C = dst[w]; a.ldc = H; a.sC = N * H;
     a.alpha = 1.0f;
     a.ranges = rb; a.mtiles = BT;
-    DABSN_HIP_CHECK((gemm::launch<E, E, false, true>(a, (int)B, stream)));
+    DABSN_HIP_CHECK((gemm::launch<E, E>(a, (int)B, stream)));
   }
   if (N > 0) {
     hipLaunchKernelGGL(reduce_cols_kernel, dim3((unsigned)((N + NTH - 1) / NTH), (unsigned)B),
