@@ -20,13 +20,9 @@ __device__ __forceinline__ float bf2f(bf16 h) {
   return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 (matches torch's .to(torch.bfloat16)).
-__device__ __forceinline__ bf16 f2bf(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<bf16>(u >> 16);
-}
+// Round-to-nearest-even fp32 -> bf16 (matches torch's .to(torch.bfloat16)); one
+// v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ bf16 f2bf(float f) { return __builtin_bit_cast(bf16, static_cast<__bf16>(f)); }
 
 template <typename E>
 __device__ __forceinline__ float ld(const E* p, size_t i);
@@ -64,6 +60,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 // Cache-policy bit for device-coherent (cross-XCD) vector memory accesses.
 constexpr int kCoherent = 16;  // sc1
+
+// Wave-wide reductions over 64 lanes on DPP: butterflies inside quads and rows of 16
+// lanes (quad_perm, row_half_mirror, row_mirror), then row_bcast15 / row_bcast31 fold
+// the four rows into lane 63, whose value every lane receives through v_readlane.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_mov(float x, float old) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, x), CTRL,
+                                                               ROW_MASK, 0xF, false));
+}
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, float identity, Op op) {
+  v = op(v, dpp_mov<0xB1, 0xF>(v, identity));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_mov<0x4E, 0xF>(v, identity));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_mov<0x141, 0xF>(v, identity));  // row_half_mirror
+  v = op(v, dpp_mov<0x140, 0xF>(v, identity));  // row_mirror
+  v = op(v, dpp_mov<0x142, 0xA>(v, identity));  // row_bcast15 into rows 1, 3
+  v = op(v, dpp_mov<0x143, 0xC>(v, identity));  // row_bcast31 into rows 2, 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_reduce(v, 0.0f, [](float a, float b) { return a + b; });
+}
+__device__ __forceinline__ float wave_max(float v) {
+  return wave_reduce(v, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+}
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float softplusf_(float x) {

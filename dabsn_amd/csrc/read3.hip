@@ -31,7 +31,7 @@ namespace read3 {
 
 constexpr int TILE = 128;   // GEMM tile rows (query tiles and bank tiles)
 constexpr int RT = 32;      // rows per workgroup in the gradient kernel
-constexpr int CC = 2048;    // columns per workgroup in the gradient kernel
+constexpr int CC = 1024;    // columns per workgroup in the gradient kernel
 constexpr int NTH = 256;
 
 struct Gains {
@@ -94,19 +94,12 @@ __global__ void __launch_bounds__(256) ranges_kernel(int T, int N, int H, int mo
   }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
-
 // Waves per workgroup of the row kernels; per-row partials of the score gradient are
 // kept per (column chunk, wave) and summed by reduce_rows_kernel.
 constexpr int NWV = NTH / 64;
 
 __device__ __forceinline__ float block_sum(float v, float* sh) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  v = wave_sum(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
   __syncthreads();
@@ -137,26 +130,20 @@ __device__ __forceinline__ void scores(const RowCtx& c, int b, int t, int j, con
   s_perm = content + cc * c.cg + c.adm[bj];
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
-}
-
 // Online (max, sum) update of one softmax with score x.
 __device__ __forceinline__ void online_add(float x, float& m, float& l) {
   if (x > m) {
-    l = l * expf(m - x) + 1.0f;  // m = -inf gives l * 0 + 1
+    l = l * __expf(m - x) + 1.0f;  // m = -inf gives l * 0 + 1
     m = x;
   } else {
-    l += expf(x - m);
+    l += __expf(x - m);
   }
 }
 
 // Combine the per-lane (max, sum) of one softmax across the wave.
 __device__ __forceinline__ void wave_softmax_stats(float& m, float& l) {
   const float M = wave_max(m);
-  l = (m == -INFINITY) ? 0.0f : l * expf(m - M);
+  l = (m == -INFINITY) ? 0.0f : l * __expf(m - M);
   l = wave_sum(l);
   m = M;
 }
@@ -203,8 +190,8 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_kernel(int64_t rows, RowCtx c
     float ss, sp, cc, sr;
     scores(c, b, t, j, ckt, ss, sp, cc, sr);
     float pv = 0.f, pn = 0.f;
-    if (allow_at(c.mode, ib[j], vb[j] != 0, t)) pv = c.sg * (expf(ss - ms) * is) + c.pg * (expf(sp - mp) * ip);
-    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) pn = c.ig * (expf(ss - mi) * ii);
+    if (allow_at(c.mode, ib[j], vb[j] != 0, t)) pv = c.sg * (__expf(ss - ms) * is) + c.pg * (__expf(sp - mp) * ip);
+    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) pn = c.ig * (__expf(ss - mi) * ii);
     const size_t o = static_cast<size_t>(row) * c.N + j;
     st(PV, o, pv);
     st(PVn, o, pn);
@@ -239,10 +226,10 @@ __global__ void __launch_bounds__(NTH) grad_rows_kernel(int64_t rows, RowCtx c, 
     const size_t o = static_cast<size_t>(row) * c.N + j;
     if (allow_at(c.mode, ib[j], vb[j] != 0, t)) {
       const float d = dPV[o];
-      rsum += expf(ss - st6[0]) * is * d;
-      psum += expf(sp - st6[2]) * ip * d;
+      rsum += __expf(ss - st6[0]) * is * d;
+      psum += __expf(sp - st6[2]) * ip * d;
     }
-    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) isum += expf(ss - st6[4]) * ii * dPVn[o];
+    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) isum += __expf(ss - st6[4]) * ii * dPVn[o];
   }
   rsum = wave_sum(rsum);
   psum = wave_sum(psum);
@@ -256,6 +243,10 @@ __global__ void __launch_bounds__(NTH) grad_rows_kernel(int64_t rows, RowCtx c, 
 // Score gradient for a tile of RT rows x CC columns. Writes Gs = scale*G, P_V, P_Vn;
 // per-(row, column chunk, wave) partials rowB = (G.S, dSp.cc, cg dSp cb[0..3]) and
 // per-(row tile, column) partials colp = (sum G, cg sum dSp ck[0..3]).
+// Each thread owns CJ columns: their per-slot operands (key bias + admission, bank
+// cocktail, index, validity) are loaded once, and the next row's S / dP_V / dP_Vn are
+// requested before the current row is evaluated, so a wave always has a row of loads in
+// flight.
 template <typename E>
 __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const float* scale_p,
                                                         const int32_t* rs_rng, const float* stats,
@@ -265,67 +256,140 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
   constexpr int CJ = CC / NTH;
   const int b = blockIdx.z, rt = blockIdx.y, cch = blockIdx.x;
   const int NCC = (c.N + CC - 1) / CC;
+  const int RTILES = (c.T + RT - 1) / RT;
   c.scale = scale_p[0];
   c.sg = g.p[0][0]; c.pg = g.p[1][0]; c.ig = g.p[2][0]; c.cg = g.p[3][0];
   const int QT = (c.T + TILE - 1) / TILE;
+  const int t0 = rt * RT, t1 = min(c.T, t0 + RT);
+  const int wave = threadIdx.x >> 6;
+  auto jlim_of = [&](int t) {
+    const int nhi = rs_rng[(static_cast<size_t>(b) * QT + t / TILE) * 3 + 2];
+    // The transposed GEMMs read whole 128-wide slot tiles of any row inside their
+    // k-range, so slots in [nhi, roundup(nhi, TILE)) are written as explicit zeros.
+    return min(c.N, ((nhi + TILE - 1) / TILE) * TILE);
+  };
+  // Slot ranges grow with t, so a chunk beyond the last row's limit has nothing to write
+  // but zero partials.
+  if (cch * CC >= jlim_of(t1 - 1)) {
+    for (int t = t0 + wave; t < t1; t += NWV) {
+      if ((threadIdx.x & 63) < 6) {
+        const size_t row = static_cast<size_t>(b) * c.T + t;
+        for (int w = 0; w < NWV; ++w) rowB[((row * NCC + cch) * NWV + w) * 6 + (threadIdx.x & 63)] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < CJ; ++q) {
+      const int j = cch * CC + q * NTH + threadIdx.x;
+      if (j >= c.N) continue;
+      float* o = colp + ((static_cast<size_t>(b) * RTILES + rt) * c.N + j) * 5;
+      o[0] = o[1] = o[2] = o[3] = o[4] = 0.f;
+    }
+    return;
+  }
+  // Per-row scalars of the tile, staged once: stats (6), row sums (3), cocktail (4), the
+  // row's slot limit nhi and write limit jlim.
+  __shared__ float rsc[RT][13];
+  __shared__ int rlim[RT][2];
+  for (int i = threadIdx.x; i < RT * 15; i += NTH) {
+    const int r = i / 15, k = i % 15, t = t0 + r;
+    if (t >= t1) continue;
+    const size_t row = static_cast<size_t>(b) * c.T + t;
+    if (k < 6) rsc[r][k] = stats[row * 6 + k];
+    else if (k < 9) rsc[r][k] = rowA[row * 3 + (k - 6)];
+    else if (k < 13) rsc[r][k] = c.ck[row * 4 + (k - 9)];
+    else if (k == 13) rlim[r][0] = rs_rng[(static_cast<size_t>(b) * QT + t / TILE) * 3 + 2];
+    else rlim[r][1] = jlim_of(t);
+  }
+  __syncthreads();
   const int64_t* ib = c.idx + static_cast<size_t>(b) * c.N;
   const uint8_t* vb = c.valid + static_cast<size_t>(b) * c.N;
+  // Slot index per column, with invalid slots folded into INT_MAX (no query may read
+  // them). Indices are sequence positions (|idx| < 2^31).
+  float kbadm[CJ], cbv[CJ][4];
+  int slot[CJ];
+#pragma unroll
+  for (int q = 0; q < CJ; ++q) {
+    const int j = cch * CC + q * NTH + threadIdx.x;
+    const bool ok = j < c.N && vb[min(j, c.N - 1)] != 0;
+    const size_t bj = static_cast<size_t>(b) * c.N + min(j, c.N - 1);
+    kbadm[q] = c.kb[bj] + c.adm[bj];
+    slot[q] = ok ? static_cast<int>(ib[min(j, c.N - 1)]) : INT_MAX;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cbv[q][k] = c.cb[bj * 4 + k];
+  }
   float colG[CJ], colC[CJ][4];
 #pragma unroll
   for (int q = 0; q < CJ; ++q) {
     colG[q] = 0.f;
     colC[q][0] = colC[q][1] = colC[q][2] = colC[q][3] = 0.f;
   }
-  const int t0 = rt * RT, t1 = min(c.T, t0 + RT);
+  float nS[CJ], nD[CJ], nDn[CJ];
+  int njl = 0;
+  auto fetch = [&](int t) {
+    njl = rlim[t - t0][1];
+    const size_t rowoff = (static_cast<size_t>(b) * c.T + t) * c.N;
+#pragma unroll
+    for (int q = 0; q < CJ; ++q) {
+      const int j = cch * CC + q * NTH + threadIdx.x;
+      const bool in = j < njl;
+      nS[q] = in ? c.S[rowoff + j] : 0.f;
+      nD[q] = in ? dPV[rowoff + j] : 0.f;
+      nDn[q] = in ? dPVn[rowoff + j] : 0.f;
+    }
+  };
+  fetch(t0);
   for (int t = t0; t < t1; ++t) {
+    float cS[CJ], cD[CJ], cDn[CJ];
+#pragma unroll
+    for (int q = 0; q < CJ; ++q) {
+      cS[q] = nS[q];
+      cD[q] = nD[q];
+      cDn[q] = nDn[q];
+    }
+    const int jlim = njl;
+    if (t + 1 < t1) fetch(t + 1);
     const size_t row = static_cast<size_t>(b) * c.T + t;
-    const int nhi = rs_rng[(static_cast<size_t>(b) * QT + t / TILE) * 3 + 2];
-    const float* st6 = stats + row * 6;
+    const float* sr = rsc[t - t0];
+    const int nhi = rlim[t - t0][0];
+    const float st6[6] = {sr[0], sr[1], sr[2], sr[3], sr[4], sr[5]};
     const float is = st6[1] > 0.f ? 1.0f / st6[1] : 0.f, ip = st6[3] > 0.f ? 1.0f / st6[3] : 0.f,
                 ii = st6[5] > 0.f ? 1.0f / st6[5] : 0.f;
-    const float ra = rowA[row * 3], rp = rowA[row * 3 + 1], ri = rowA[row * 3 + 2];
-    const float* ckt = c.ck + row * 4;
+    const float ra = sr[6], rp = sr[7], ri = sr[8];
+    const float ck0 = sr[9], ck1 = sr[10], ck2 = sr[11], ck3 = sr[12];
     float gsc = 0.f, gcg = 0.f, gk0 = 0.f, gk1 = 0.f, gk2 = 0.f, gk3 = 0.f;
-    // The transposed GEMMs read whole 128-wide slot tiles of any row inside their
-    // k-range, so slots in [nhi, roundup(nhi, TILE)) are written as explicit zeros.
-    const int jlim = min(c.N, ((nhi + TILE - 1) / TILE) * TILE);
 #pragma unroll
     for (int q = 0; q < CJ; ++q) {
       const int j = cch * CC + q * NTH + threadIdx.x;
       if (j >= jlim) continue;
       const size_t o = row * c.N + j;
-      if (j >= nhi) {
-        st(Gs, o, 0.0f);
-        st(PV, o, 0.0f);
-        st(PVn, o, 0.0f);
-        continue;
+      float ps = 0.f, pp = 0.f, pi = 0.f, G = 0.f, dsp = 0.f;
+      if (j < nhi) {
+        const float cc = ck0 * cbv[q][0] + ck1 * cbv[q][1] + ck2 * cbv[q][2] + ck3 * cbv[q][3];
+        const float s_short = cS[q] * c.scale + kbadm[q];
+        const float s_perm = s_short + cc * c.cg;
+        float dss = 0.f, dsi = 0.f;
+        if (allow_at(c.mode, slot[q], slot[q] != INT_MAX, t)) {
+          ps = __expf(s_short - st6[0]) * is;
+          pp = __expf(s_perm - st6[2]) * ip;
+          dss = c.sg * ps * (cD[q] - ra);
+          dsp = c.pg * pp * (cD[q] - rp);
+        }
+        if (induct_at(c.mode, slot[q], slot[q] != INT_MAX, t, c.T)) {
+          pi = __expf(s_short - st6[4]) * ii;
+          dsi = c.ig * pi * (cDn[q] - ri);
+        }
+        G = dss + dsp + dsi;
+        gsc += G * cS[q];
+        gcg += dsp * cc;
+        const float w = dsp * c.cg;
+        gk0 += w * cbv[q][0]; gk1 += w * cbv[q][1]; gk2 += w * cbv[q][2]; gk3 += w * cbv[q][3];
+        colG[q] += G;
+        colC[q][0] += w * ck0; colC[q][1] += w * ck1;
+        colC[q][2] += w * ck2; colC[q][3] += w * ck3;
       }
-      float ss, sp, cc, sr;
-      scores(c, b, t, j, ckt, ss, sp, cc, sr);
-      float ps = 0.f, pp = 0.f, pi = 0.f, dss = 0.f, dsp = 0.f, dsi = 0.f;
-      if (allow_at(c.mode, ib[j], vb[j] != 0, t)) {
-        const float d = dPV[o];
-        ps = expf(ss - st6[0]) * is;
-        pp = expf(sp - st6[2]) * ip;
-        dss = c.sg * ps * (d - ra);
-        dsp = c.pg * pp * (d - rp);
-      }
-      if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) {
-        pi = expf(ss - st6[4]) * ii;
-        dsi = c.ig * pi * (dPVn[o] - ri);
-      }
-      const float G = dss + dsp + dsi;
       st(Gs, o, G * c.scale);
       st(PV, o, c.sg * ps + c.pg * pp);
       st(PVn, o, c.ig * pi);
-      gsc += G * sr;
-      gcg += dsp * cc;
-      const float* cbj = c.cb + (static_cast<size_t>(b) * c.N + j) * 4;
-      const float w = dsp * c.cg;
-      gk0 += w * cbj[0]; gk1 += w * cbj[1]; gk2 += w * cbj[2]; gk3 += w * cbj[3];
-      colG[q] += G;
-      colC[q][0] += w * ckt[0]; colC[q][1] += w * ckt[1];
-      colC[q][2] += w * ckt[2]; colC[q][3] += w * ckt[3];
     }
     gsc = wave_sum(gsc);
     gcg = wave_sum(gcg);
@@ -334,11 +398,10 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
     gk2 = wave_sum(gk2);
     gk3 = wave_sum(gk3);
     if ((threadIdx.x & 63) == 0) {
-      float* o = rowB + ((row * NCC + cch) * NWV + (threadIdx.x >> 6)) * 6;
+      float* o = rowB + ((row * NCC + cch) * NWV + wave) * 6;
       o[0] = gsc; o[1] = gcg; o[2] = gk0; o[3] = gk1; o[4] = gk2; o[5] = gk3;
     }
   }
-  const int RTILES = (c.T + RT - 1) / RT;
 #pragma unroll
   for (int q = 0; q < CJ; ++q) {
     const int j = cch * CC + q * NTH + threadIdx.x;

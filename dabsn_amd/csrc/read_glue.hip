@@ -13,12 +13,6 @@ namespace glue {
 
 constexpr float kEps = 1e-12f;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
-
 // One wave per (b, t) row.
 template <typename E>
 __global__ void __launch_bounds__(256) stats_kernel(int64_t rows, int H, const E* nov, const E* pl,
