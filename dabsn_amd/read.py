@@ -45,6 +45,19 @@ class _AdmittedReadParameters(nn.Module):
         return (self.adm_p_gain * torch.log1p(mean_p * hidden) + self.adm_novelty_gain * mean_n
                 + self.adm_saturation_gain * mean_c + self.adm_energy_gain * mean_e + self.adm_bias)
 
+    def project(self, y: Tensor, budget: Tensor, retrieved: Tensor) -> Tensor:
+        """out(cat([y, budget, retrieved], -1)) (read.py:435, 821) without materialising the
+        [.., 3H] concatenation: each column block of the weight multiplies its own input
+        and the products accumulate through addmm."""
+        h = y.shape[-1]
+        lead = y.shape[:-1]
+        w = self.out.weight
+        y2, b2, r2 = (x.reshape(-1, h) for x in (y, budget, retrieved))
+        out = F.linear(r2, w[:, 2 * h:], self.out.bias)
+        out = torch.addmm(out, y2, w[:, :h].t())
+        out = torch.addmm(out, b2, w[:, h:2 * h].t())
+        return out.reshape(*lead, out.shape[-1])
+
     def key_bias_from_means(self, mean_n, mean_p, hidden: int) -> Tensor:
         return (self.p_gain * torch.log1p(mean_p * hidden) + self.novelty_gain * mean_n
                 + self.null_bias)
@@ -140,9 +153,9 @@ class DABSNRead(nn.Module):
         cocktail = _cocktail(mean_e, mean_c, mean_n, mean_p)
         retrieved = self._read_core(query, (cocktail, cocktail), write, norm_w, key_bias,
                                     admission, seq_len, 0)
-        output = rp.out(torch.cat([y, budget, retrieved.to(y.dtype)], dim=-1))
+        output = rp.project(y, budget, retrieved.to(y.dtype))
         long = self._long_scan(write, plasticity, novelty)
-        return output + self.long_gain * long
+        return torch.addcmul(output, self.long_gain, long)
 
     # ---- long memory -------------------------------------------------------------
     def initial_long_scan_state(self, batch_size: int, hidden_dim: int | None = None, *,
@@ -194,14 +207,14 @@ class DABSNRead(nn.Module):
         cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
         retrieved = self._read_core(query, cocktails, bank_write, b_stats[..., 5].detach(),
                                     key_bias, admission, bank_len, int(query_start))
-        short_output = rp.out(torch.cat([y, budget, retrieved.to(y.dtype)], dim=-1))
+        short_output = rp.project(y, budget, retrieved.to(y.dtype))
         result = self._long_scan_from_state(write, plasticity, novelty,
                                             initial_state=initial_long_state,
                                             return_final_state=return_long_state)
         if return_long_state:
             long, final_state = result
-            return short_output + self.long_gain * long, final_state
-        return short_output + self.long_gain * result
+            return torch.addcmul(short_output, self.long_gain, long), final_state
+        return torch.addcmul(short_output, self.long_gain, result)
 
 
 def collect_traces_enabled() -> bool:
