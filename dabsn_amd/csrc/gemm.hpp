@@ -33,10 +33,17 @@ template <typename E>
 struct G;
 template <>
 struct G<bf16> {
-  static constexpr int BK = 64, PAD = 8, VEC = 8, KSTEP = 32;
+  // LDS rows are 64 elements (8 chunks of 16 bytes) with no padding; chunk c of row r is
+  // stored at position c ^ ((r >> 1) & 7). The 16 lanes of one b128 read (rows r..r+15,
+  // one logical chunk) and the 16 lanes of one b128 write (two rows) then touch 16
+  // distinct 16-byte bank groups.
+  static constexpr int BK = 64, PAD = 0, VEC = 8, KSTEP = 32;
   using R = bf16x8;
+  __device__ static int pos(int c, int r) { return c ^ ((r >> 1) & 7); }
+  // Fragment of k-step ks for the lane's row (row & 15 == lane & 15).
   __device__ static R frag(const bf16* row, int ks, int lane) {
-    return __builtin_bit_cast(R, *reinterpret_cast<const u32x4*>(row + ks * KSTEP + (lane >> 4) * 8));
+    return __builtin_bit_cast(
+        R, *reinterpret_cast<const u32x4*>(row + pos(ks * 4 + (lane >> 4), lane & 15) * 8));
   }
   __device__ static f32x4 mma(R a, R b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -46,6 +53,7 @@ template <>
 struct G<float> {
   static constexpr int BK = 32, PAD = 4, VEC = 4, KSTEP = 4;
   using R = float;
+  __device__ static int pos(int c, int) { return c; }
   __device__ static R frag(const float* row, int ks, int lane) { return row[ks * KSTEP + (lane >> 4)]; }
   __device__ static f32x4 mma(R a, R b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -256,7 +264,8 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_kernel(Args<E, OUT> a, int 
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         const int q = tid + i * NTH;
-        *reinterpret_cast<u32x4*>(&lds[buf][q / CPR][(q % CPR) * VEC]) = stage[i];
+        const int row = q / CPR;
+        *reinterpret_cast<u32x4*>(&lds[buf][row][G<E>::pos(q % CPR, row) * VEC]) = stage[i];
       }
     };
 
