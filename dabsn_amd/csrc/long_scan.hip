@@ -42,9 +42,11 @@ __global__ void __launch_bounds__(NT) linrec_fwd_kernel(int B, int T, int H, con
     float av[TB], gv[TB];
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
-      const int t = t0 + i;
-      av[i] = t < T ? ld(a, base + static_cast<size_t>(t) * H) : 0.0f;
-      gv[i] = t < T ? ld(g, base + static_cast<size_t>(t) * H) : 0.0f;
+      // Clamped, unconditional loads: all TB requests are issued before the first use
+      // (values past T are never used).
+      const size_t o = base + static_cast<size_t>(min(t0 + i, T - 1)) * H;
+      av[i] = ld(a, o);
+      gv[i] = ld(g, o);
     }
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
@@ -143,8 +145,11 @@ __global__ void __launch_bounds__(NT) long_fwd_chunk(int B, int T, int H, const 
   float wv[CK], pv[CK];
 #pragma unroll
   for (int i = 0; i < CK; ++i) {
-    wv[i] = i < c.len ? ld(w, c.base + static_cast<size_t>(c.t0 + i) * H) : 0.0f;
-    if (PHASE >= 2) pv[i] = i < c.len ? ld(p, c.base + static_cast<size_t>(c.t0 + i) * H) : 0.0f;
+    // Clamped, unconditional loads so all CK requests are in flight at once (steps past
+    // the chunk end are never used).
+    const size_t o = c.base + static_cast<size_t>(c.t0 + min(i, c.len - 1)) * H;
+    wv[i] = ld(w, o);
+    if (PHASE >= 2) pv[i] = ld(p, o);
   }
   float Ev = PHASE >= 1 ? ckpt[c.cbase + H] : 0.0f;
   float R = PHASE >= 2 ? ckpt[c.cbase + 2 * H] : 0.0f;
@@ -258,15 +263,14 @@ __global__ void __launch_bounds__(NT) long_bwd_map(int B, int T, int H, const E*
     float wv[LB], pv[LB], gv[LB], Lv[LB], Ev[LB], Rv[LB];
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
-      const int i = i0 + j;
-      const size_t o = c.base + static_cast<size_t>(c.t0 + i) * H;
-      const bool in = i < c.len;
-      wv[j] = in ? ld(w, o) : 0.0f;
-      pv[j] = in ? ld(p, o) : 0.0f;
-      gv[j] = in ? ld(gout, o) : 0.0f;
-      Lv[j] = in ? states[o] : 0.0f;
-      Ev[j] = in ? states[bth + o] : 0.0f;
-      Rv[j] = in ? states[2 * bth + o] : 0.0f;
+      // Clamped, unconditional loads (steps past the chunk end are never used).
+      const size_t o = c.base + static_cast<size_t>(c.t0 + min(i0 + j, c.len - 1)) * H;
+      wv[j] = ld(w, o);
+      pv[j] = ld(p, o);
+      gv[j] = ld(gout, o);
+      Lv[j] = states[o];
+      Ev[j] = states[bth + o];
+      Rv[j] = states[2 * bth + o];
     }
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
@@ -362,14 +366,14 @@ __global__ void __launch_bounds__(NT) long_bwd_final(int B, int T, int H, const 
 #pragma unroll
       for (int j = 0; j < LB; ++j) {
         const int i = i1 - j;
+        // Clamped, unconditional loads (steps before the chunk start are never used).
         const size_t o = c.base + static_cast<size_t>(c.t0 + (i < 0 ? 0 : i)) * H;
-        const bool in = i >= 0;
-        wv[j] = in ? ld(w, o) : 0.0f;
-        pv[j] = in ? ld(p, o) : 0.0f;
-        gv[j] = in ? ld(gout, o) : 0.0f;
-        Lv[j] = in ? states[o] : 0.0f;
-        Ev[j] = in ? states[bth + o] : 0.0f;
-        Rv[j] = in ? states[2 * bth + o] : 0.0f;
+        wv[j] = ld(w, o);
+        pv[j] = ld(p, o);
+        gv[j] = ld(gout, o);
+        Lv[j] = states[o];
+        Ev[j] = states[bth + o];
+        Rv[j] = states[2 * bth + o];
       }
 #pragma unroll
       for (int j = 0; j < LB; ++j) {
