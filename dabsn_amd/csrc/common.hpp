@@ -25,6 +25,11 @@ __device__ __forceinline__ float bf2f(bf16 h) {
 __device__ __forceinline__ bf16 f2bf(float f) { return __builtin_bit_cast(bf16, static_cast<__bf16>(f)); }
 
 template <typename E>
+struct is_bf16 { static constexpr bool value = false; };
+template <>
+struct is_bf16<bf16> { static constexpr bool value = true; };
+
+template <typename E>
 __device__ __forceinline__ float ld(const E* p, size_t i);
 template <>
 __device__ __forceinline__ float ld<float>(const float* p, size_t i) { return p[i]; }
@@ -38,6 +43,48 @@ __device__ __forceinline__ void st<float>(float* p, size_t i, float v) { p[i] = 
 template <>
 __device__ __forceinline__ void st<bf16>(bf16* p, size_t i, float v) { p[i] = f2bf(v); }
 
+// V consecutive elements at p as floats (V = 1, or 8: one 16-byte access for bf16, two for
+// fp32; p must then be 16-byte aligned).
+template <typename E, int V>
+__device__ __forceinline__ void ldv(const E* p, float (&v)[V]) {
+  if constexpr (V == 1) {
+    v[0] = ld(p, 0);
+  } else if constexpr (is_bf16<E>::value) {
+    static_assert(V == 8, "bf16 vectors are 8 wide");
+    const u32x4 u = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = __builtin_bit_cast(float, u[k] << 16);
+      v[2 * k + 1] = __builtin_bit_cast(float, u[k] & 0xffff0000u);
+    }
+  } else {
+    static_assert(V == 8, "fp32 vectors are 8 wide");
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[k] = a[k];
+      v[4 + k] = b[k];
+    }
+  }
+}
+template <typename E, int V>
+__device__ __forceinline__ void stv(E* p, const float (&v)[V]) {
+  if constexpr (V == 1) {
+    st(p, 0, v[0]);
+  } else if constexpr (is_bf16<E>::value) {
+    static_assert(V == 8, "bf16 vectors are 8 wide");
+    u32x4 u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      u[k] = static_cast<uint32_t>(f2bf(v[2 * k])) | (static_cast<uint32_t>(f2bf(v[2 * k + 1])) << 16);
+    *reinterpret_cast<u32x4*>(p) = u;
+  } else {
+    static_assert(V == 8, "fp32 vectors are 8 wide");
+    *reinterpret_cast<f32x4*>(p) = (f32x4){v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = (f32x4){v[4], v[5], v[6], v[7]};
+  }
+}
+
 // Value as it would be stored in E (identity for fp32, RTNE round trip for bf16).
 template <typename E>
 __device__ __forceinline__ float round_to(float v);
@@ -46,10 +93,6 @@ __device__ __forceinline__ float round_to<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ float round_to<bf16>(float v) { return bf2f(f2bf(v)); }
 
-template <typename E>
-struct is_bf16 { static constexpr bool value = false; };
-template <>
-struct is_bf16<bf16> { static constexpr bool value = true; };
 
 // Buffer resource over [base, base + bytes); out-of-range accesses are dropped (stores)
 // or return zero (loads). Third dword per the gfx9 buffer descriptor format.

@@ -8,13 +8,19 @@
 #include "capi.hpp"
 #include "common.hpp"
 
+#include <initializer_list>
+
 namespace dabsn {
 namespace glue {
 
 constexpr float kEps = 1e-12f;
 
+// Element kernels take V = 8 (16-byte vector accesses, H % 8 == 0 and aligned operands) or
+// V = 1. Elementwise kernels index V-element chunks with 32-bit arithmetic; row kernels put
+// one wave on a (b, t) row.
+
 // One wave per (b, t) row.
-template <typename E>
+template <typename E, int V>
 __global__ void __launch_bounds__(256) stats_kernel(int64_t rows, int H, const E* nov, const E* pl,
                                                     const E* en, const E* sat, const E* ay,
                                                     const E* wr, float* stats) {
@@ -23,15 +29,24 @@ __global__ void __launch_bounds__(256) stats_kernel(int64_t rows, int H, const E
   if (row >= rows) return;
   const size_t base = static_cast<size_t>(row) * H;
   float se = 0.f, sc = 0.f, sn = 0.f, sp = 0.f, sa = 0.f, sw = 0.f;
-  for (int h = lane; h < H; h += 64) {
+  for (int h = lane * V; h < H; h += 64 * V) {
     const size_t o = base + h;
-    se += ld(en, o);
-    sc += ld(sat, o);
-    sn += ld(nov, o);
-    sp += ld(pl, o);
-    const float a = ld(ay, o), w = ld(wr, o);
-    sa += a * a;
-    sw += w * w;
+    float e[V], c[V], n[V], q[V], a[V], w[V];
+    ldv<E, V>(en + o, e);
+    ldv<E, V>(sat + o, c);
+    ldv<E, V>(nov + o, n);
+    ldv<E, V>(pl + o, q);
+    ldv<E, V>(ay + o, a);
+    ldv<E, V>(wr + o, w);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      se += e[k];
+      sc += c[k];
+      sn += n[k];
+      sp += q[k];
+      sa += a[k] * a[k];
+      sw += w[k] * w[k];
+    }
   }
   se = wave_sum(se);
   sc = wave_sum(sc);
@@ -51,31 +66,46 @@ __global__ void __launch_bounds__(256) stats_kernel(int64_t rows, int H, const E
   }
 }
 
-// g_tape[b,t,h] += g_mean[b,t] / H for the four averaged tapes.
-template <typename E>
-__global__ void stats_bwd_kernel(int64_t rows, int H, const float* gstats, E* gen, E* gsat, E* gnov,
-                                 E* gpl) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= rows * H) return;
-  const int64_t row = i / H;
+// g_tape[b,t,h] += g_mean[b,t] / H for the four averaged tapes; one thread per V elements.
+template <typename E, int V>
+__global__ void __launch_bounds__(256) stats_bwd_kernel(uint32_t chunks, uint32_t cpr, int H,
+                                                        const float* gstats, E* gen, E* gsat,
+                                                        E* gnov, E* gpl) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= chunks) return;
+  const uint32_t row = i / cpr;
+  const size_t o = static_cast<size_t>(i) * V;
   const float inv = 1.0f / static_cast<float>(H);
   const float* g = gstats + static_cast<size_t>(row) * 6;
-  if (gen) st(gen, i, ld(gen, i) + g[0] * inv);
-  if (gsat) st(gsat, i, ld(gsat, i) + g[1] * inv);
-  if (gnov) st(gnov, i, ld(gnov, i) + g[2] * inv);
-  if (gpl) st(gpl, i, ld(gpl, i) + g[3] * inv);
+  E* dst[4] = {gen, gsat, gnov, gpl};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (!dst[k]) continue;
+    float v[V];
+    ldv<E, V>(dst[k] + o, v);
+    const float add = g[k] * inv;
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] += add;
+    stv<E, V>(dst[k] + o, v);
+  }
 }
 
-template <typename E>
-__global__ void normalize_kernel(int64_t rows, int H, const E* x, const float* norms, E* q) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= rows * H) return;
-  const float n = fmaxf(norms[i / H], kEps);
-  st(q, i, ld(x, i) / n);
+template <typename E, int V>
+__global__ void __launch_bounds__(256) normalize_kernel(uint32_t chunks, uint32_t cpr, const E* x,
+                                                        const float* norms, E* q) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= chunks) return;
+  const float n = fmaxf(norms[i / cpr], kEps);
+  const size_t o = static_cast<size_t>(i) * V;
+  float v[V];
+  ldv<E, V>(x + o, v);
+#pragma unroll
+  for (int e = 0; e < V; ++e) v[e] = v[e] / n;
+  stv<E, V>(q + o, v);
 }
 
 // One wave per row: gx += (gq - q (q.gq)) / |x| if |x| > eps, else gq / eps.
-template <typename E>
+template <typename E, int V>
 __global__ void __launch_bounds__(256) normalize_bwd_kernel(int64_t rows, int H, const E* q,
                                                             const float* norms, const E* gq,
                                                             E* gx) {
@@ -86,14 +116,25 @@ __global__ void __launch_bounds__(256) normalize_bwd_kernel(int64_t rows, int H,
   const float nrm = norms[row];
   float dot = 0.0f;
   if (nrm > kEps) {
-    for (int h = lane; h < H; h += 64) dot += ld(q, base + h) * ld(gq, base + h);
+    for (int h = lane * V; h < H; h += 64 * V) {
+      float a[V], g[V];
+      ldv<E, V>(q + base + h, a);
+      ldv<E, V>(gq + base + h, g);
+#pragma unroll
+      for (int e = 0; e < V; ++e) dot += a[e] * g[e];
+    }
     dot = wave_sum(dot);
   }
   const float n = fmaxf(nrm, kEps);
-  for (int h = lane; h < H; h += 64) {
+  for (int h = lane * V; h < H; h += 64 * V) {
     const size_t o = base + h;
-    const float g = nrm > kEps ? (ld(gq, o) - ld(q, o) * dot) / n : ld(gq, o) / n;
-    st(gx, o, ld(gx, o) + g);
+    float a[V], g[V], acc[V];
+    ldv<E, V>(q + o, a);
+    ldv<E, V>(gq + o, g);
+    ldv<E, V>(gx + o, acc);
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[e] += nrm > kEps ? (g[e] - a[e] * dot) / n : g[e] / n;
+    stv<E, V>(gx + o, acc);
   }
 }
 
@@ -156,28 +197,33 @@ __global__ void __launch_bounds__(SEL_T) select_kernel(int T, const float* adm, 
   if (tid == 0) counts[b] = total;
 }
 
-// Gather K (normalised), V and Vn rows of the bank.
-template <typename E>
-__global__ void gather_kernel(int T, int N, int H, int hblocks, const E* w, const float* norm_w,
-                              const int64_t* idx, const int64_t* nidx, E* K, E* V, E* Vn) {
+// Gather K (normalised), V and Vn rows of the bank; one thread per V elements.
+template <typename E, int V>
+__global__ void __launch_bounds__(256) gather_kernel(int T, int N, int H, int hblocks, const E* w,
+                                                     const float* norm_w, const int64_t* idx,
+                                                     const int64_t* nidx, E* K, E* Vv, E* Vn) {
   const int64_t row = blockIdx.x / hblocks;  // b * N + j
-  const int h = (blockIdx.x % hblocks) * blockDim.x + threadIdx.x;
+  const int h = ((blockIdx.x % hblocks) * 256 + threadIdx.x) * V;
   if (h >= H) return;
   const int64_t b = row / N;
   int64_t t = idx[row];
   int64_t tn = nidx[row];
   t = t < 0 ? 0 : (t >= T ? T - 1 : t);
   tn = tn < 0 ? 0 : (tn >= T ? T - 1 : tn);
-  const float v = ld(w, (static_cast<size_t>(b) * T + t) * H + h);
+  float v[V], vn[V], k[V];
+  ldv<E, V>(w + (static_cast<size_t>(b) * T + t) * H + h, v);
+  ldv<E, V>(w + (static_cast<size_t>(b) * T + tn) * H + h, vn);
   const float n = fmaxf(norm_w[static_cast<size_t>(b) * T + t], kEps);
+#pragma unroll
+  for (int e = 0; e < V; ++e) k[e] = v[e] / n;
   const size_t o = static_cast<size_t>(row) * H + h;
-  st(K, o, v / n);
-  st(V, o, v);
-  st(Vn, o, ld(w, (static_cast<size_t>(b) * T + tn) * H + h));
+  stv<E, V>(K + o, k);
+  stv<E, V>(Vv + o, v);
+  stv<E, V>(Vn + o, vn);
 }
 
 // One workgroup per (b, t) position of the write tape.
-template <typename E>
+template <typename E, int V>
 __global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int N, int H, const float* norm_w,
                                                          const int32_t* rank, const E* K,
                                                          const E* gK, const E* gV, const E* gVn,
@@ -198,23 +244,45 @@ __global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int N, int H, co
   if (in0 && nrm > kEps) {
     const size_t kb = (static_cast<size_t>(b) * N + r0) * H;
     float s = 0.0f;
-    for (int h = threadIdx.x; h < H; h += blockDim.x) s += ld(K, kb + h) * ld(gK, kb + h);
+    for (int h = threadIdx.x * V; h < H; h += 256 * V) {
+      float k[V], g[V];
+      ldv<E, V>(K + kb + h, k);
+      ldv<E, V>(gK + kb + h, g);
+#pragma unroll
+      for (int e = 0; e < V; ++e) s += k[e] * g[e];
+    }
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
     __syncthreads();
     dot = part[0] + part[1] + part[2] + part[3];
   }
-  for (int h = threadIdx.x; h < H; h += blockDim.x) {
+  for (int h = threadIdx.x * V; h < H; h += 256 * V) {
     const size_t o = static_cast<size_t>(bt) * H + h;
-    float acc = ld(gw, o);
+    float acc[V];
+    ldv<E, V>(gw + o, acc);
     if (in0) {
       const size_t kb = (static_cast<size_t>(b) * N + r0) * H + h;
-      const float gk = ld(gK, kb);
-      acc += ld(gV, kb) + (nrm > kEps ? (gk - ld(K, kb) * dot) / n : gk / n);
+      float gk[V], gv[V], k[V];
+      ldv<E, V>(gK + kb, gk);
+      ldv<E, V>(gV + kb, gv);
+      ldv<E, V>(K + kb, k);
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        acc[e] += gv[e] + (nrm > kEps ? (gk[e] - k[e] * dot) / n : gk[e] / n);
     }
-    if (in1) acc += ld(gVn, (static_cast<size_t>(b) * N + r1) * H + h);
-    if (in2) acc += ld(gVn, (static_cast<size_t>(b) * N + r2) * H + h);
-    st(gw, o, acc);
+    if (in1) {
+      float g[V];
+      ldv<E, V>(gVn + (static_cast<size_t>(b) * N + r1) * H + h, g);
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[e] += g[e];
+    }
+    if (in2) {
+      float g[V];
+      ldv<E, V>(gVn + (static_cast<size_t>(b) * N + r2) * H + h, g);
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[e] += g[e];
+    }
+    stv<E, V>(gw + o, acc);
   }
 }
 
@@ -228,6 +296,26 @@ static inline unsigned blocks_for(int64_t n, int per) {
   return static_cast<unsigned>((n + per - 1) / per);
 }
 
+// 16-byte vector accesses need H % 8 == 0 and 16-byte aligned row bases.
+static inline bool vec_ok(int64_t H, std::initializer_list<const void*> ptrs) {
+  if (H % 8 != 0) return false;
+  for (const void* q : ptrs)
+    if (q && (reinterpret_cast<uintptr_t>(q) & 15u) != 0) return false;
+  return true;
+}
+
+// Runs LAUNCH(E, V) for the dtype code, with V = 8 when `vec` holds and V = 1 otherwise.
+#define GLUE_DISPATCH(what, dtype, vec, LAUNCH)                       \
+  do {                                                                \
+    if ((dtype) == kBF16) {                                           \
+      if (vec) { LAUNCH(bf16, 8); } else { LAUNCH(bf16, 1); }         \
+    } else if ((dtype) == kF32) {                                     \
+      if (vec) { LAUNCH(float, 8); } else { LAUNCH(float, 1); }       \
+    } else {                                                          \
+      DABSN_REQUIRE(false, what ": bad dtype %d", dtype);             \
+    }                                                                 \
+  } while (0)
+
 extern "C" {
 
 int dabsn_hip_tape_stats(int dtype, int64_t B, int64_t T, int64_t H, const void* nov,
@@ -238,16 +326,13 @@ int dabsn_hip_tape_stats(int dtype, int64_t B, int64_t T, int64_t H, const void*
   if (rows == 0) return DABSN_OK;
   DABSN_REQUIRE(nov && plast && energy && sat && expr && write && stats, "tape_stats: null pointer");
   const dim3 grid(blocks_for(rows, 4)), block(256);
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(stats_kernel<bf16>, grid, block, 0, stream, rows, (int)H, (const bf16*)nov,
-                       (const bf16*)plast, (const bf16*)energy, (const bf16*)sat,
-                       (const bf16*)expr, (const bf16*)write, stats);
-  else if (dtype == kF32)
-    hipLaunchKernelGGL(stats_kernel<float>, grid, block, 0, stream, rows, (int)H,
-                       (const float*)nov, (const float*)plast, (const float*)energy,
-                       (const float*)sat, (const float*)expr, (const float*)write, stats);
-  else
-    DABSN_REQUIRE(false, "tape_stats: bad dtype %d", dtype);
+  const bool vec = vec_ok(H, {nov, plast, energy, sat, expr, write});
+#define L(E, V)                                                                                  \
+  hipLaunchKernelGGL((stats_kernel<E, V>), grid, block, 0, stream, rows, (int)H, (const E*)nov, \
+                     (const E*)plast, (const E*)energy, (const E*)sat, (const E*)expr,          \
+                     (const E*)write, stats)
+  GLUE_DISPATCH("tape_stats", dtype, vec, L);
+#undef L
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
@@ -261,18 +346,21 @@ int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const v
   (void)stats;
   DABSN_REQUIRE(gexpr == nullptr && gwrite == nullptr,
                 "tape_stats backward: norm gradients are handled by the normalisation ops");
+  DABSN_REQUIRE(B > 0 && T >= 0 && H > 0, "tape_stats backward: bad shape");
   const int64_t rows = B * T;
   if (rows == 0) return DABSN_OK;
   DABSN_REQUIRE(gstats, "tape_stats backward: null gstats");
-  const dim3 grid(blocks_for(rows * H, 256)), block(256);
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(stats_bwd_kernel<bf16>, grid, block, 0, stream, rows, (int)H, gstats,
-                       (bf16*)genergy, (bf16*)gsat, (bf16*)gnov, (bf16*)gplast);
-  else if (dtype == kF32)
-    hipLaunchKernelGGL(stats_bwd_kernel<float>, grid, block, 0, stream, rows, (int)H, gstats,
-                       (float*)genergy, (float*)gsat, (float*)gnov, (float*)gplast);
-  else
-    DABSN_REQUIRE(false, "tape_stats backward: bad dtype %d", dtype);
+  const bool vec = vec_ok(H, {gnov, gplast, genergy, gsat});
+  const int64_t V = vec ? 8 : 1;
+  const int64_t chunks = rows * (H / V);
+  DABSN_REQUIRE(chunks < (1ll << 32), "tape_stats backward: too many elements");
+  const dim3 grid(blocks_for(chunks, 256)), block(256);
+#define L(E, VV)                                                                                \
+  hipLaunchKernelGGL((stats_bwd_kernel<E, VV>), grid, block, 0, stream, (uint32_t)chunks,      \
+                     (uint32_t)(H / VV), (int)H, gstats, (E*)genergy, (E*)gsat, (E*)gnov,      \
+                     (E*)gplast)
+  GLUE_DISPATCH("tape_stats backward", dtype, vec, L);
+#undef L
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
@@ -280,16 +368,17 @@ int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const v
 int dabsn_hip_normalize_rows(int dtype, int64_t rows, int64_t H, const void* x, const float* norms,
                              void* q, hipStream_t stream) {
   if (rows == 0) return DABSN_OK;
-  DABSN_REQUIRE(x && norms && q && H > 0, "normalize_rows: bad arguments");
-  const dim3 grid(blocks_for(rows * H, 256)), block(256);
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(normalize_kernel<bf16>, grid, block, 0, stream, rows, (int)H,
-                       (const bf16*)x, norms, (bf16*)q);
-  else if (dtype == kF32)
-    hipLaunchKernelGGL(normalize_kernel<float>, grid, block, 0, stream, rows, (int)H,
-                       (const float*)x, norms, (float*)q);
-  else
-    DABSN_REQUIRE(false, "normalize_rows: bad dtype %d", dtype);
+  DABSN_REQUIRE(x && norms && q && H > 0 && rows > 0, "normalize_rows: bad arguments");
+  const bool vec = vec_ok(H, {x, q});
+  const int64_t V = vec ? 8 : 1;
+  const int64_t chunks = rows * (H / V);
+  DABSN_REQUIRE(chunks < (1ll << 32), "normalize_rows: too many elements");
+  const dim3 grid(blocks_for(chunks, 256)), block(256);
+#define L(E, VV)                                                                                \
+  hipLaunchKernelGGL((normalize_kernel<E, VV>), grid, block, 0, stream, (uint32_t)chunks,      \
+                     (uint32_t)(H / VV), (const E*)x, norms, (E*)q)
+  GLUE_DISPATCH("normalize_rows", dtype, vec, L);
+#undef L
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
@@ -299,14 +388,12 @@ int dabsn_hip_normalize_rows_bwd(int dtype, int64_t rows, int64_t H, const void*
   if (rows == 0) return DABSN_OK;
   DABSN_REQUIRE(q && norms && gq && gx && H > 0, "normalize_rows backward: bad arguments");
   const dim3 grid(blocks_for(rows, 4)), block(256);
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(normalize_bwd_kernel<bf16>, grid, block, 0, stream, rows, (int)H,
-                       (const bf16*)q, norms, (const bf16*)gq, (bf16*)gx);
-  else if (dtype == kF32)
-    hipLaunchKernelGGL(normalize_bwd_kernel<float>, grid, block, 0, stream, rows, (int)H,
-                       (const float*)q, norms, (const float*)gq, (float*)gx);
-  else
-    DABSN_REQUIRE(false, "normalize_rows backward: bad dtype %d", dtype);
+  const bool vec = vec_ok(H, {q, gq, gx});
+#define L(E, V)                                                                                 \
+  hipLaunchKernelGGL((normalize_bwd_kernel<E, V>), grid, block, 0, stream, rows, (int)H,       \
+                     (const E*)q, norms, (const E*)gq, (E*)gx)
+  GLUE_DISPATCH("normalize_rows backward", dtype, vec, L);
+#undef L
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
@@ -327,19 +414,15 @@ int dabsn_hip_bank_gather(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
   DABSN_REQUIRE(B > 0 && T > 0 && N >= 0 && H > 0, "bank_gather: bad shape");
   if (N == 0) return DABSN_OK;
   DABSN_REQUIRE(w && norm_w && idx && next_idx && K && V && Vn, "bank_gather: null pointer");
-  const int hblocks = static_cast<int>(blocks_for(H, 256));
+  const bool vec = vec_ok(H, {w, K, V, Vn});
+  const int hblocks = static_cast<int>(blocks_for(H, 256 * (vec ? 8 : 1)));
   DABSN_REQUIRE(B * N * hblocks <= 2147483647ll, "bank_gather: too many bank rows");
   const dim3 grid(static_cast<unsigned>(B * N * hblocks)), block(256);
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(gather_kernel<bf16>, grid, block, 0, stream, (int)T, (int)N, (int)H,
-                       hblocks, (const bf16*)w, norm_w, idx, next_idx, (bf16*)K, (bf16*)V,
-                       (bf16*)Vn);
-  else if (dtype == kF32)
-    hipLaunchKernelGGL(gather_kernel<float>, grid, block, 0, stream, (int)T, (int)N, (int)H,
-                       hblocks, (const float*)w, norm_w, idx, next_idx, (float*)K, (float*)V,
-                       (float*)Vn);
-  else
-    DABSN_REQUIRE(false, "bank_gather: bad dtype %d", dtype);
+#define L(E, VV)                                                                                \
+  hipLaunchKernelGGL((gather_kernel<E, VV>), grid, block, 0, stream, (int)T, (int)N, (int)H,   \
+                     hblocks, (const E*)w, norm_w, idx, next_idx, (E*)K, (E*)V, (E*)Vn)
+  GLUE_DISPATCH("bank_gather", dtype, vec, L);
+#undef L
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
@@ -354,16 +437,13 @@ int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_
   DABSN_REQUIRE(norm_w && rank && K && gK && gV && gVn && gw, "bank_gather backward: null pointer");
   DABSN_REQUIRE(B * T <= 2147483647ll, "bank_gather backward: too many positions");
   const dim3 grid((unsigned)(B * T)), block(256);
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(gather_bwd_kernel<bf16>, grid, block, 0, stream, (int)T, (int)N, (int)H,
-                       norm_w, rank, (const bf16*)K, (const bf16*)gK, (const bf16*)gV,
-                       (const bf16*)gVn, (bf16*)gw);
-  else if (dtype == kF32)
-    hipLaunchKernelGGL(gather_bwd_kernel<float>, grid, block, 0, stream, (int)T, (int)N, (int)H,
-                       norm_w, rank, (const float*)K, (const float*)gK, (const float*)gV,
-                       (const float*)gVn, (float*)gw);
-  else
-    DABSN_REQUIRE(false, "bank_gather backward: bad dtype %d", dtype);
+  const bool vec = vec_ok(H, {K, gK, gV, gVn, gw});
+#define L(E, VV)                                                                                \
+  hipLaunchKernelGGL((gather_bwd_kernel<E, VV>), grid, block, 0, stream, (int)T, (int)N,       \
+                     (int)H, norm_w, rank, (const E*)K, (const E*)gK, (const E*)gV,             \
+                     (const E*)gVn, (E*)gw)
+  GLUE_DISPATCH("bank_gather backward", dtype, vec, L);
+#undef L
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
