@@ -36,6 +36,9 @@ __device__ __forceinline__ float ld<float>(const float* p, size_t i) { return p[
 template <>
 __device__ __forceinline__ float ld<bf16>(const bf16* p, size_t i) { return bf2f(p[i]); }
 
+__device__ __forceinline__ float to_f(float v) { return v; }
+__device__ __forceinline__ float to_f(bf16 v) { return bf2f(v); }
+
 template <typename E>
 __device__ __forceinline__ void st(E* p, size_t i, float v);
 template <>

@@ -124,9 +124,11 @@ __device__ __forceinline__ UnitParams load_unit(const Params& P, int c, bool ok)
 }
 
 // Called by all 64 lanes of wave 0: waits until every split counter of the batch group
-// (base `ctr`) has received `step1` rounds of arrivals. Lane s polls counter s. Returns
-// false if the error word is raised or the wait exceeded the spin bound; lane 0 then
-// raises the error word itself on a timeout.
+// (base `ctr`) has received `step1` rounds of arrivals. Lane s < kSplit polls counter s
+// (the other lanes read counter 0 against a zero target, so the load needs no branch).
+// One poll is in flight at a time: a load left pending at return would hold up the
+// workgroup's next store drain. Returns false if the error word is raised or the wait
+// exceeded the spin bound; lane 0 then raises the error word itself on a timeout.
 __device__ __forceinline__ bool wait_step(const uint32_t* ctr, int nct, uint32_t step1,
                                           uint32_t* err) {
   const int lane = threadIdx.x & 63;
@@ -135,9 +137,8 @@ __device__ __forceinline__ bool wait_step(const uint32_t* ctr, int nct, uint32_t
   const uint32_t* mine = ctr + s * (kCtrStride / 4);
   uint32_t spins = 0;
   while (true) {
-    bool ok = true;
-    if (target != 0u) ok = __hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target;
-    if (__all(ok)) return true;
+    if (__all(__hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target))
+      return true;
     if ((++spins & 1023u) == 0u) {
       if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return false;
       if (spins > kSpinLimit) {
@@ -340,10 +341,17 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
     if (tid == 0) arrive(counter);
   }
 
+  // Wgx_t and Wx_{t+1} are requested one step ahead, unconditionally (threads without a
+  // pair read element 0; the last step rereads its own row), so no select waits on them.
+  const size_t lrow0 = act ? row0 : 0;
+  const int lc = act ? c : 0;
+  auto in_row = [&](int t) { return (lrow0 + static_cast<size_t>(t)) * H + lc; };
+  E wgx_next = a.Wgx[in_row(0)];
+  E wxn_next = a.Wx[in_row(T > 1 ? 1 : 0)];
   for (int t = 0; t < T; ++t) {
     const size_t rt = (row0 + t) * H + c;
-    const float wgx = act ? ld(a.Wgx, rt) : 0.0f;
-    const float wxn = (act && t + 1 < T) ? ld(a.Wx, rt + H) : 0.0f;
+    const float wgx = to_f(wgx_next);
+    const float wxn = to_f(wxn_next);
     if (wave == 0) {
       if (!wait_step(ctr, a.nct, static_cast<uint32_t>(t + 1), err) && tid == 0) s_abort = 1;
     }
@@ -420,6 +428,8 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
       st(a.ctp, rt, cpost);
       st(a.st, rt, gate_tape_value<E>(s_g));
     }
+    wgx_next = a.Wgx[in_row(t + 1 < T ? t + 1 : t)];
+    wxn_next = a.Wx[in_row(t + 2 < T ? t + 2 : (t + 1 < T ? t + 1 : t))];
     sb = bn;
     se = en;
     sc = cpost;
