@@ -507,33 +507,43 @@ __device__ __forceinline__ float cvt(uint32_t w) {
   }
 }
 
-// Issue the loads of time index t (tapes and upstream grads; absent grads read as 0).
+// Issue the loads of time index t (tapes and upstream grads). Every load is issued
+// unconditionally: t is clamped to 0, the t - 1 neighbours of t = 0 read row t itself,
+// and an absent grad reads a stand-in tensor of the same layout. reverse_step masks those
+// values at use (Scal::gpresent, t > 0), so no select on a pending load forces a wait.
 template <typename E>
 __device__ __forceinline__ void load_tape(const BwdArgs<E>& a, size_t row0, int c, int t,
                                           TapeRaw& r) {
   const size_t H = static_cast<size_t>(a.H);
-  const size_t rt = (row0 + t) * H + c;
-  const size_t ru = (row0 + t) * 2 * H + c;
+  const int tc = t > 0 ? t : 0;
+  const size_t rt = (row0 + tc) * H + c;
+  const size_t ru = (row0 + tc) * 2 * H + c;
+  const size_t rtp = tc > 0 ? rt - H : rt;  // row t - 1 (cortisol)
+  const size_t rup = tc > 0 ? ru - H : ru;  // budget half of U at t - 1
   r.y = ldraw(a.U, ru);
-  r.b_prev = t > 0 ? ldraw(a.U, ru - H) : 0u;  // budget half of U at t - 1
+  r.b_prev = ldraw(a.U, rup);
   r.e_prev = ldraw(a.et, rt);
-  r.c_prev = t > 0 ? ldraw(a.ctp, rt - H) : 0u;
+  r.c_prev = ldraw(a.ctp, rtp);
   r.gate = ldraw(a.st, rt);
   r.p = ldraw(a.pl, rt);
   r.ay = ldraw(a.ay, rt);
   r.c_t = ldraw(a.ctp, rt);
-  r.gy0 = a.gU ? ldraw(a.gU, ru) : 0u;
-  r.gub = a.gU ? ldraw(a.gU, ru + H) : 0u;
-  r.gc = a.gC ? ldraw(a.gC, rt) : 0u;
-  r.gnov = a.gN ? ldraw(a.gN, rt) : 0u;
-  r.gp = a.gP ? ldraw(a.gP, rt) : 0u;
-  r.gay = a.gA ? ldraw(a.gA, rt) : 0u;
-  r.gw = a.gW ? ldraw(a.gW, rt) : 0u;
-  r.ge = a.gE ? ldraw(a.gE, rt) : 0u;
+  r.gy0 = ldraw(a.gU ? a.gU : a.U, ru);
+  r.gub = ldraw(a.gU ? a.gU : a.U, ru + H);
+  r.gc = ldraw(a.gC ? a.gC : a.pl, rt);
+  r.gnov = ldraw(a.gN ? a.gN : a.pl, rt);
+  r.gp = ldraw(a.gP ? a.gP : a.pl, rt);
+  r.gay = ldraw(a.gA ? a.gA : a.pl, rt);
+  r.gw = ldraw(a.gW ? a.gW : a.pl, rt);
+  r.ge = ldraw(a.gE ? a.gE : a.pl, rt);
 }
+
+// Bits of Scal::gpresent: which upstream grads the call provides.
+enum : uint32_t { G_U = 1, G_C = 2, G_N = 4, G_P = 8, G_A = 16, G_W = 32, G_E = 64 };
 
 struct Scal {
   float alpha, lam, sig_lam, sup;
+  uint32_t gpresent;  // G_* bits
 };
 
 // One reverse step at time t, evaluated with the carried budget grad `gbn` without the
@@ -557,14 +567,15 @@ __device__ __forceinline__ Pending reverse_step(const TapeRaw& r, int t, float b
   const float p = cvt<E>(r.p);
   const float ay = cvt<E>(r.ay);
   const float c_t = cvt<E>(r.c_t);
-  const float gy0 = cvt<E>(r.gy0);
-  const float gb_new = cvt<E>(r.gub) + gbn;
-  const float gc_new = gcn + cvt<E>(r.gc);
-  const float gnov0 = cvt<E>(r.gnov);
-  const float gp0 = cvt<E>(r.gp);
-  const float gay0 = cvt<E>(r.gay);
-  const float gwrite = cvt<E>(r.gw);
-  const float geo = cvt<E>(r.ge);
+  auto gin = [&](uint32_t w, uint32_t bit) { return (sc.gpresent & bit) ? cvt<E>(w) : 0.0f; };
+  const float gy0 = gin(r.gy0, G_U);
+  const float gb_new = gin(r.gub, G_U) + gbn;
+  const float gc_new = gcn + gin(r.gc, G_C);
+  const float gnov0 = gin(r.gnov, G_N);
+  const float gp0 = gin(r.gp, G_P);
+  const float gay0 = gin(r.gay, G_A);
+  const float gwrite = gin(r.gw, G_W);
+  const float geo = gin(r.ge, G_E);
 
   const float nov = tanhf(fabsf(ay - b_prev));
   const float tanh_b = tanhf(b_prev);
@@ -644,6 +655,46 @@ __device__ __forceinline__ Pending reverse_step(const TapeRaw& r, int t, float b
   return o;
 }
 
+// Staged tape prefetch (bf16, 16-unit tiles, H % 16 == 0). The 16 values a reverse step
+// reads per (unit, batch) pair come from 16 streams (TapeRaw order). For one tile and
+// time they are 16 streams x 16 batch rows x 32 bytes = 512 chunks of 16 bytes, fetched
+// with one vector load per chunk by all threads, parked in LDS as [stream][row][unit]
+// and read back per pair. Per stream: source tensor (a stand-in of the same layout for an
+// absent grad), row stride in units of H, column offset, and whether it reads row t - 1.
+constexpr int kTapeStreams = 16;
+constexpr int kTapeChunks = kTapeStreams * NB * 2;
+
+template <typename E>
+struct TapeStream {
+  const E* src;
+  int mul;   // row stride in units of H (2 for U and its grad)
+  int col;   // column offset (H for the budget half)
+  int prev;  // 1: the row of t - 1 (t = 0 reads row 0)
+};
+
+template <typename E>
+__device__ __forceinline__ TapeStream<E> tape_stream(const BwdArgs<E>& a, int s) {
+  const E* gu = a.gU ? a.gU : a.U;
+  switch (s) {
+    case 0: return {a.U, 2, 0, 0};
+    case 1: return {a.U, 2, a.H, 1};
+    case 2: return {a.et, 1, 0, 0};
+    case 3: return {a.ctp, 1, 0, 1};
+    case 4: return {a.st, 1, 0, 0};
+    case 5: return {a.pl, 1, 0, 0};
+    case 6: return {a.ay, 1, 0, 0};
+    case 7: return {a.ctp, 1, 0, 0};
+    case 8: return {gu, 2, 0, 0};
+    case 9: return {gu, 2, a.H, 0};
+    case 10: return {a.gC ? a.gC : a.pl, 1, 0, 0};
+    case 11: return {a.gN ? a.gN : a.pl, 1, 0, 0};
+    case 12: return {a.gP ? a.gP : a.pl, 1, 0, 0};
+    case 13: return {a.gA ? a.gA : a.pl, 1, 0, 0};
+    case 14: return {a.gW ? a.gW : a.pl, 1, 0, 0};
+    default: return {a.gE ? a.gE : a.pl, 1, 0, 0};
+  }
+}
+
 // Reverse scan of one workgroup (`bid` among `grid`, as fwd_body).
 template <typename E, int CH, int KSTEPS, int NW>
 __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid) {
@@ -659,6 +710,12 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
   __shared__ __attribute__((aligned(16))) float red[NW][MTB][16][16];  // as in the forward
   __shared__ float accs[NB][CH][NACC];
   __shared__ int s_abort;
+  constexpr bool STAGE = is_bf16<E>::value && CH == 16;
+  constexpr int CPT = STAGE ? (kTapeChunks + NT - 1) / NT : 1;  // chunks per thread
+  __shared__ __attribute__((aligned(16))) bf16 tape[STAGE ? kTapeStreams : 1][NB][16];
+  // Per-unit parameters of the tile, shared by its 16 batch rows: read from LDS at each
+  // reverse step instead of holding 17 registers per thread for the whole scan.
+  __shared__ UnitParams upar[CH];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int ct, bg;
@@ -708,11 +765,14 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
   const int c = ct * CH + cl, b = bg * NB + bl;
   const bool act = is_pair && c < H && b < B;
   const UnitParams up = load_unit(a.P, c, is_pair && c < H);
+  if (is_pair && bl == 0) upar[cl] = up;
   Scal sc;
   sc.alpha = sigmoidf_(a.P.scal[0][0]);
   sc.lam = softplusf_(a.P.scal[1][0]);
   sc.sig_lam = sigmoidf_(a.P.scal[1][0]);
   sc.sup = sigmoidf_(a.P.scal[2][0]);
+  sc.gpresent = (a.gU ? G_U : 0u) | (a.gC ? G_C : 0u) | (a.gN ? G_N : 0u) | (a.gP ? G_P : 0u) |
+                (a.gA ? G_A : 0u) | (a.gW ? G_W : 0u) | (a.gE ? G_E : 0u);
   const size_t bh = static_cast<size_t>(b) * H + c;
   const float b0v = act ? a.b0[bh] : 0.0f;
   const float c0v = act ? a.c0[bh] : 0.0f;
@@ -720,7 +780,61 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
 #pragma unroll
   for (int i = 0; i < NACC; ++i) acc[i] = 0.0f;
   const size_t row0 = static_cast<size_t>(b) * static_cast<size_t>(a.ldt);
+  // Load coordinates: threads without a (unit, batch) pair read row 0, unit 0 (values
+  // unused), so the tape loads need no branch.
+  const size_t lrow0 = act ? row0 : 0;
+  const int lc = act ? c : 0;
   const int kb2[2] = {ct * CH, KP + ct * CH};
+
+  // Staged prefetch: per chunk, its stream and the element offset of its time-0 row
+  // (batch rows beyond B read batch 0; their values are never used).
+  // Per chunk: the address of its time-0 element, its row stride (elements) and whether
+  // it reads the row of t - 1.
+  const E* ch_ptr[CPT];
+  uint32_t ch_rs[CPT];
+  bool ch_prev[CPT];
+  if constexpr (STAGE) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int q = min(tid + i * NT, kTapeChunks - 1);
+      const int sidx = q / (NB * 2), r = (q / 2) % NB, hh = q & 1;
+      const TapeStream<E> ts = tape_stream(a, sidx);
+      const int bb = bg * NB + r;
+      const size_t brow = static_cast<size_t>(bb < B ? bb : 0) * static_cast<size_t>(a.ldt);
+      ch_rs[i] = static_cast<uint32_t>(ts.mul * H);
+      ch_ptr[i] = ts.src + brow * ch_rs[i] + ts.col + ct * 16 + hh * 8;
+      ch_prev[i] = ts.prev != 0;
+    }
+  }
+  // 16-byte chunk loads of time t (clamped to 0; a t - 1 stream at t = 0 reads row 0).
+  auto load_chunks = [&](int t, u32x4 (&v)[CPT]) {
+    const int tc = t > 0 ? t : 0;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int tr = ch_prev[i] && tc > 0 ? tc - 1 : tc;
+      v[i] = *reinterpret_cast<const u32x4*>(ch_ptr[i] + static_cast<size_t>(tr) * ch_rs[i]);
+    }
+  };
+  auto park_chunks = [&](const u32x4 (&v)[CPT]) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int q = tid + i * NT;
+      if (q < kTapeChunks)
+        *reinterpret_cast<u32x4*>(&tape[q / (NB * 2)][(q / 2) % NB][(q & 1) * 8]) = v[i];
+    }
+  };
+  auto read_parked = [&]() {
+    uint32_t w[kTapeStreams];
+#pragma unroll
+    for (int k = 0; k < kTapeStreams; ++k) w[k] = tape[STAGE ? k : 0][bl % NB][cl % 16];
+    TapeRaw r;
+    r.y = w[0]; r.b_prev = w[1]; r.e_prev = w[2]; r.c_prev = w[3];
+    r.gate = w[4]; r.p = w[5]; r.ay = w[6]; r.c_t = w[7];
+    r.gy0 = w[8]; r.gub = w[9]; r.gc = w[10]; r.gnov = w[11];
+    r.gp = w[12]; r.gay = w[13]; r.gw = w[14]; r.ge = w[15];
+    return r;
+  };
+  u32x4 chunk[CPT];
 
   // Pipeline state at the top of the step for time t: dg/dx are the final adjoint inputs
   // of t, keep_* the final carried grads towards t - 1 (budget without the pre-activation
@@ -737,6 +851,14 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
     const float geF = a.geF ? a.geF[bh] : 0.0f;
     const float gcF = a.gcF ? a.gcF[bh] : 0.0f;
     const Pending pd = reverse_step<E>(cur, T - 1, b0v, c0v, up, sc, gbF, geF, gcF, acc);
+    if constexpr (STAGE) {
+      // The tapes of T - 2 go where the staged prefetch parks later steps' tapes.
+      const uint32_t w[kTapeStreams] = {nxt.y, nxt.b_prev, nxt.e_prev, nxt.c_prev, nxt.gate,
+                                        nxt.p, nxt.ay, nxt.c_t, nxt.gy0, nxt.gub, nxt.gc,
+                                        nxt.gnov, nxt.gp, nxt.gay, nxt.gw, nxt.ge};
+#pragma unroll
+      for (int k = 0; k < kTapeStreams; ++k) tape[k][bl][cl] = static_cast<bf16>(w[k]);
+    }
     dg = pd.dgate0;
     dx = pd.dexpr0;
     keep_b = pd.keep_b0;
@@ -748,6 +870,11 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
 
   for (int n = 0; n < T; ++n) {
     const int t = T - 1 - n;
+    // Staged: the tapes of t - 1, fetched during the previous step, go to LDS; the barrier
+    // inside the publish makes them visible (step 0 uses the tapes loaded before the loop).
+    if constexpr (STAGE) {
+      if (n > 0) park_chunks(chunk);
+    }
     {
       const float v[2] = {dg, dx};
       publish<E, CH, 2>(xr, a.slot_bytes, n & 1, kb2, v, is_pair, cl, bl);
@@ -761,7 +888,14 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
       st(a.gWgx, rt, dg);
       st(a.day, rt, dx);
       if (n > 0) st(a.gWx, rt + H, xprev);
-      if (t >= 1) pd = reverse_step<E>(nxt, t - 1, b0v, c0v, up, sc, keep_b, keep_e, keep_c, acc);
+      if (t >= 1) {
+        const UnitParams upl = upar[cl];
+        if constexpr (STAGE) {
+          pd = reverse_step<E>(read_parked(), t - 1, b0v, c0v, upl, sc, keep_b, keep_e, keep_c, acc);
+        } else {
+          pd = reverse_step<E>(nxt, t - 1, b0v, c0v, upl, sc, keep_b, keep_e, keep_c, acc);
+        }
+      }
     }
     if (wave == 0) {
       if (!wait_step(ctr, a.nct, static_cast<uint32_t>(n + 1), err) && tid == 0) s_abort = 1;
@@ -774,10 +908,17 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
 #pragma unroll
     for (int s = 0; s < KB; ++s)
       breg[s] = M::load_x(xr, sbase + static_cast<uint32_t>((wave * KB + s) * 64 + lane) * M::UNIT);
-    // Tapes of t - 2 are requested after the exchange loads: completions are counted in
-    // issue order, so waiting for the exchange does not wait for these.
-    TapeRaw nn = {};
-    if (act && t >= 2) load_tape(a, row0, c, t - 2, nn);
+    // Keep every exchange load ahead of the first MFMA (all in flight at once).
+    __builtin_amdgcn_sched_barrier(0);
+    // Tapes of t - 2 are requested after the exchange loads. Completions are counted in
+    // issue order and the loads are unconditional in every wave (clamped indices), so the
+    // waits before the MFMAs count the exchange loads exactly and do not wait for these.
+    // Staged: one 16-byte load per chunk instead of 16 scattered loads per pair.
+    if constexpr (STAGE) {
+      load_chunks(t - 2, chunk);
+    } else {
+      load_tape(a, lrow0, lc, t - 2, nxt);
+    }
     f32x4 accm[MTB];
 #pragma unroll
     for (int mt = 0; mt < MTB; ++mt) accm[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -814,7 +955,6 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
       }
       xprev = x;
     }
-    nxt = nn;
   }
 
   if (act) {
@@ -1075,6 +1215,16 @@ static int check_bwd(const dabsn_core_bwd_call& b, Cfg& c) {
   if (b.dtype == kF32 && c.ksteps > 32) {
     dabsn::set_error("core scan backward: fp32 supports H <= 512 per workgroup register budget");
     return DABSN_ERR_UNSUPPORTED;
+  }
+  if (b.dtype == kBF16 && c.ch == 16 && b.T > 0) {
+    // The 16-unit bf16 kernels fetch tapes and grads as 16-byte chunks of 8 units.
+    DABSN_REQUIRE(b.H % 16 == 0, "core scan backward: bf16 with H >= 1024 needs H %% 16 == 0 (H=%lld)",
+                  (long long)b.H);
+    const void* streams[] = {b.U, b.plast, b.expr, b.energy, b.sat, b.gate, b.gU, b.gNov,
+                             b.gP, b.gAy, b.gW, b.gE, b.gC};
+    for (const void* q : streams)
+      DABSN_REQUIRE(q == nullptr || (reinterpret_cast<uintptr_t>(q) & 15u) == 0,
+                    "core scan backward: bf16 tape and grad pointers must be 16-byte aligned");
   }
   return DABSN_OK;
 }
