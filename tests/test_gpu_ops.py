@@ -104,6 +104,26 @@ def test_core_scan_bf16_within_tolerance_of_fp32_oracle(cuda_device, B, T, H):
     _compare_core_bwd(res, ob, H, 5e-2, 5e-2, rel_fro)
 
 
+@pytest.mark.parametrize("absent", [(0, 1, 5, 6), (2, 3, 4)])
+def test_core_scan_bf16_absent_grads_equal_zero_grads(cuda_device, absent):
+    """Absent upstream grads (None) must give exactly the results of explicit zeros. At
+    H >= 1024 in bf16 the reverse scan reads tapes and grads as 16-byte chunks and an absent
+    grad reads a stand-in tensor that is masked at use."""
+    B, T, H = 16, 24, 1024
+    inp = core_case(31, B, T, H)
+    x, out = _run_core(inp, torch.bfloat16, cuda_device)
+    grads = [g.to(cuda_device).to(torch.bfloat16) for g in _core_grads(5, out)[:7]]
+    fin = [g.to(cuda_device) for g in _core_grads(5, out)[7:]]
+    with_none = [None if k in absent else g for k, g in enumerate(grads)]
+    with_zero = [torch.zeros_like(g) if k in absent else g for k, g in enumerate(grads)]
+    args = (x[2], x[3], x[4:20], x[20], x[21], x[22], x[23], x[25], out[0], out[2], out[3],
+            out[5], out[6], out[7])
+    a = ops.core_scan_batched_backward(*args, *with_none, *fin)
+    b = ops.core_scan_batched_backward(*args, *with_zero, *fin)
+    for i, (u, v) in enumerate(zip(a, b)):
+        assert torch.equal(u, v), f"output {i} differs"
+
+
 def test_core_scan_chunked_equals_full_on_device(cuda_device):
     """Carried (b, e, c): two chunks equal one pass exactly (same kernel, same state)."""
     inp = core_case(5, 4, 50, 64)
