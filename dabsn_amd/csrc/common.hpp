@@ -46,6 +46,16 @@ __device__ __forceinline__ void st<float>(float* p, size_t i, float v) { p[i] = 
 template <>
 __device__ __forceinline__ void st<bf16>(bf16* p, size_t i, float v) { p[i] = f2bf(v); }
 
+// 16-byte global load / store through an explicit global-address-space pointer. Pointers
+// picked at run time from a table of tensors lose their address space in the compiler and
+// would become FLAT accesses, which also count against the LDS wait counter.
+__device__ __forceinline__ u32x4 gload16(const void* p) {
+  return *(const __attribute__((address_space(1))) u32x4*)p;  // address-space cast
+}
+__device__ __forceinline__ void gstore16(void* p, u32x4 v) {
+  *(__attribute__((address_space(1))) u32x4*)p = v;  // address-space cast
+}
+
 // V consecutive elements at p as floats (V = 1, or 8: one 16-byte access for bf16, two for
 // fp32; p must then be 16-byte aligned).
 template <typename E, int V>

@@ -324,6 +324,46 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   const int cl = tid % CH, bl = tid / CH;
   const int c = ct * CH + cl, b = bg * NB + bl;
   const bool act = is_pair && c < H && b < B;
+
+  // Staged tape stores (bf16, 16-unit tiles, H % 16 == 0). A step's 9 outputs per pair
+  // are parked in LDS as [stream][row][unit] (two buffers, alternating by step) and
+  // written out during the next step's shadow as 16-byte chunks (8 units of one batch
+  // row) by the threads of waves 1.. -- never by the polling wave 0, whose counter loads
+  // would otherwise queue behind the stores.
+  constexpr bool OSTAGE = is_bf16<E>::value && CH == 16;
+  constexpr int OSN = 9;                       // U (y), U (budget), n, p, ay, w, e, c, s
+  constexpr int OCH = OSN * NB * 2;            // chunks per step
+  constexpr int OCPT = OSTAGE ? (OCH + NT - 65) / (NT - 64) : 1;  // chunks per thread
+  __shared__ __attribute__((aligned(16))) bf16 otape[OSTAGE ? 2 : 1][OSTAGE ? OSN : 1][NB][16];
+  E* o_ptr[OCPT];
+  uint32_t o_rs[OCPT];
+  int o_q[OCPT];
+  if constexpr (OSTAGE) {
+#pragma unroll
+    for (int i = 0; i < OCPT; ++i) {
+      const int q = tid - 64 + i * (NT - 64);
+      const int sidx = q / (NB * 2), r = (q / 2) % NB, hh = q & 1;
+      const int bb = bg * NB + r;
+      E* const dst[OSN] = {a.U, a.U, a.nov, a.pl, a.ay, a.wr, a.et, a.ctp, a.st};
+      const bool ok = tid >= 64 && q < OCH && bb < B;
+      o_q[i] = ok ? q : -1;
+      o_rs[i] = static_cast<uint32_t>((sidx < 2 ? 2 : 1) * H);
+      o_ptr[i] = ok ? dst[sidx] + static_cast<size_t>(bb) * static_cast<size_t>(a.ldt) * o_rs[i] +
+                          (sidx == 1 ? H : 0) + ct * 16 + hh * 8
+                    : nullptr;
+    }
+  }
+  // Write out the chunks parked for step t.
+  auto flush = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < OCPT; ++i) {
+      const int q = o_q[i];
+      if (q >= 0)
+        gstore16(o_ptr[i] + static_cast<size_t>(t) * o_rs[i],
+                 *reinterpret_cast<const u32x4*>(&otape[t & 1][q / (NB * 2)][(q / 2) % NB][(q & 1) * 8]));
+    }
+  };
+
   const UnitParams up = load_unit(a.P, c, is_pair && c < H);
   const float gate_alpha = sigmoidf_(a.P.scal[0][0]);
   const float lam = softplusf_(a.P.scal[1][0]);
@@ -350,8 +390,6 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   E wxn_next = a.Wx[in_row(T > 1 ? 1 : 0)];
   for (int t = 0; t < T; ++t) {
     const size_t rt = (row0 + t) * H + c;
-    const float wgx = to_f(wgx_next);
-    const float wxn = to_f(wxn_next);
     if (wave == 0) {
       if (!wait_step(ctr, a.nct, static_cast<uint32_t>(t + 1), err) && tid == 0) s_abort = 1;
     }
@@ -363,6 +401,8 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
       breg[s] = M::load_x(xr, sbase + static_cast<uint32_t>((wave * KSTEPS + s) * 64 + lane) * M::UNIT);
+    // Keep every exchange load ahead of the first MFMA (all in flight at once).
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -390,10 +430,12 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
       // The reference's recurrent GEMM returns the activation dtype.
       ug = round_to<E>(ug);
       ay = round_to<E>(ay);
-      s_g = hardsigmoidf_(wgx + ug);
+      // The prefetched inputs are first read here, so their loads need not land before the
+      // next barrier wait starts.
+      s_g = hardsigmoidf_(to_f(wgx_next) + ug);
       p = s_g * se;
       bn = (1.0f - gate_alpha) * sb + up.beta + lam * (p * ay);
-      if (act && t + 1 < T) ynext = tanhf(wxn + bn);
+      if (act && t + 1 < T) ynext = tanhf(to_f(wxn_next) + bn);
     }
     if (t + 1 < T) {
       const float v[1] = {ynext};
@@ -416,7 +458,14 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
       const float r_t = clamp01(up.recover * expf(0.5f * tanhf(r_sig)));
       en = clamp01(se + r_t * (1.0f - se) - k_t * p);
     }
-    if (act) {
+    if constexpr (OSTAGE) {
+      if (t > 0) flush(t - 1);
+      if (act) {
+        const float v[OSN] = {ycur, bn, nov, p, ay, p * ay, se, cpost, gate_tape_value<E>(s_g)};
+#pragma unroll
+        for (int k = 0; k < OSN; ++k) otape[t & 1][k][bl][cl] = f2bf(v[k]);
+      }
+    } else if (act) {
       const size_t ru = (row0 + t) * 2 * H + c;
       st(a.U, ru, ycur);
       st(a.U, ru + H, bn);
@@ -434,6 +483,12 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
     se = en;
     sc = cpost;
     ycur = ynext;
+  }
+  if constexpr (OSTAGE) {
+    if (T > 0) {
+      __syncthreads();
+      flush(T - 1);
+    }
   }
   if (act) {
     const size_t i = static_cast<size_t>(b) * H + c;
@@ -812,7 +867,7 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int tr = ch_prev[i] && tc > 0 ? tc - 1 : tc;
-      v[i] = *reinterpret_cast<const u32x4*>(ch_ptr[i] + static_cast<size_t>(tr) * ch_rs[i]);
+      v[i] = gload16(ch_ptr[i] + static_cast<size_t>(tr) * ch_rs[i]);
     }
   };
   auto park_chunks = [&](const u32x4 (&v)[CPT]) {
@@ -1195,6 +1250,15 @@ static int check_fwd(const dabsn_core_fwd_call& f, Cfg& c) {
   DABSN_REQUIRE(f.T == 0 || (f.U && f.nov && f.plast && f.expr && f.write && f.energy && f.sat &&
                              f.gate),
                 "core scan: null tape pointer");
+  if (f.dtype == kBF16 && c.ch == 16 && f.T > 0) {
+    // The 16-unit bf16 kernels write tapes as 16-byte chunks of 8 units.
+    DABSN_REQUIRE(f.H % 16 == 0, "core scan: bf16 with H >= 1024 needs H %% 16 == 0 (H=%lld)",
+                  (long long)f.H);
+    const void* outs[] = {f.U, f.nov, f.plast, f.expr, f.write, f.energy, f.sat, f.gate};
+    for (const void* q : outs)
+      DABSN_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15u) == 0,
+                    "core scan: bf16 tape pointers must be 16-byte aligned");
+  }
   return DABSN_OK;
 }
 
