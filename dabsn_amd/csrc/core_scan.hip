@@ -386,8 +386,27 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   const size_t lrow0 = act ? row0 : 0;
   const int lc = act ? c : 0;
   auto in_row = [&](int t) { return (lrow0 + static_cast<size_t>(t)) * H + lc; };
-  E wgx_next = a.Wgx[in_row(0)];
-  E wxn_next = a.Wx[in_row(T > 1 ? 1 : 0)];
+  // With 8 waves (16-unit bf16 tiles), wave 4 -- no pairs, no polling -- fetches the next
+  // step's Wgx_t and Wx_{t+1} for the tile as 16-byte chunks (2 streams x 16 rows x 2)
+  // during the shadow and parks them in LDS after the step barrier; the polling wave 0 then
+  // has no loads queued ahead of its counter polls.
+  constexpr bool INSTAGE = OSTAGE && NW == 8;
+  __shared__ __attribute__((aligned(16))) bf16 inbuf[INSTAGE ? 2 : 1][NB][16];
+  const bool in_loader = INSTAGE && wave == 4;
+  const int iq = lane;  // chunk of a loader lane: stream iq / 32, row (iq / 2) % 16, half iq & 1
+  const E* in_src = iq < 32 ? a.Wgx : a.Wx;
+  const int in_bb = bg * NB + (iq / 2) % NB;
+  const size_t in_base = static_cast<size_t>(in_bb < B ? in_bb : 0) * static_cast<size_t>(a.ldt) *
+                             static_cast<size_t>(H) + ct * 16 + (iq & 1) * 8;
+  // Chunk of step t: Wgx_t or Wx_{t+1} (clamped to the last row).
+  auto in_load = [&](int t) {
+    const int tr = min(iq < 32 ? t : t + 1, T - 1);
+    return gload16(in_src + in_base + static_cast<size_t>(tr) * H);
+  };
+  u32x4 in_chunk = {0u, 0u, 0u, 0u};
+  if (in_loader && T > 0) in_chunk = in_load(0);
+  E wgx_next = INSTAGE ? static_cast<E>(0) : a.Wgx[in_row(0)];
+  E wxn_next = INSTAGE ? static_cast<E>(0) : a.Wx[in_row(T > 1 ? 1 : 0)];
   for (int t = 0; t < T; ++t) {
     const size_t rt = (row0 + t) * H + c;
     if (wave == 0) {
@@ -395,6 +414,11 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
     }
     __syncthreads();
     if (s_abort) return;
+    if constexpr (INSTAGE) {
+      // Visible to the pairs after the reduction barrier below.
+      if (in_loader)
+        *reinterpret_cast<u32x4*>(&inbuf[iq / 32][(iq / 2) % NB][(iq & 1) * 8]) = in_chunk;
+    }
 
     const uint32_t sbase = static_cast<uint32_t>(t & 1) * a.slot_bytes;
     typename M::Reg breg[KSTEPS];
@@ -432,6 +456,10 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
       ay = round_to<E>(ay);
       // The prefetched inputs are first read here, so their loads need not land before the
       // next barrier wait starts.
+      if constexpr (INSTAGE) {
+        wgx_next = inbuf[0][bl][cl];
+        wxn_next = inbuf[1][bl][cl];
+      }
       s_g = hardsigmoidf_(to_f(wgx_next) + ug);
       p = s_g * se;
       bn = (1.0f - gate_alpha) * sb + up.beta + lam * (p * ay);
@@ -477,8 +505,12 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
       st(a.ctp, rt, cpost);
       st(a.st, rt, gate_tape_value<E>(s_g));
     }
-    wgx_next = a.Wgx[in_row(t + 1 < T ? t + 1 : t)];
-    wxn_next = a.Wx[in_row(t + 2 < T ? t + 2 : (t + 1 < T ? t + 1 : t))];
+    if constexpr (INSTAGE) {
+      if (in_loader) in_chunk = in_load(t + 1 < T ? t + 1 : t);
+    } else {
+      wgx_next = a.Wgx[in_row(t + 1 < T ? t + 1 : t)];
+      wxn_next = a.Wx[in_row(t + 2 < T ? t + 2 : (t + 1 < T ? t + 1 : t))];
+    }
     sb = bn;
     se = en;
     sc = cpost;
