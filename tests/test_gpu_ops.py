@@ -104,12 +104,14 @@ def test_core_scan_bf16_within_tolerance_of_fp32_oracle(cuda_device, B, T, H):
     _compare_core_bwd(res, ob, H, 5e-2, 5e-2, rel_fro)
 
 
+@pytest.mark.parametrize("H", [1024, 2048])
 @pytest.mark.parametrize("absent", [(0, 1, 5, 6), (2, 3, 4)])
-def test_core_scan_bf16_absent_grads_equal_zero_grads(cuda_device, absent):
+def test_core_scan_bf16_absent_grads_equal_zero_grads(cuda_device, absent, H):
     """Absent upstream grads (None) must give exactly the results of explicit zeros. At
     H >= 1024 in bf16 the reverse scan reads tapes and grads as 16-byte chunks and an absent
-    grad reads a stand-in tensor that is masked at use."""
-    B, T, H = 16, 24, 1024
+    grad reads a stand-in tensor that is masked at use; beyond H = 1024 two threads share
+    each (unit, batch) pair."""
+    B, T = 16, 24
     inp = core_case(31, B, T, H)
     x, out = _run_core(inp, torch.bfloat16, cuda_device)
     grads = [g.to(cuda_device).to(torch.bfloat16) for g in _core_grads(5, out)[:7]]
