@@ -14,6 +14,12 @@ launch), so the same counters read on it give the scale between counter units an
     python -m dabsn_amd.profiling <results.db> [--top N] [--match REGEX]
     python -m dabsn_amd.profiling --pmc-summary <dir> [--match REGEX]
     python -m dabsn_amd.profiling --copy-probe <MiB>
+    python -m dabsn_amd.profiling --pmc-json <out.json> --fetch <dir> --write <dir> \
+        --copy-fetch <dir> --copy-write <dir> --copy-mib 512 --batch B --seq T --state H --chunk C
+
+``pmc_json`` turns the four counter runs (FETCH_SIZE and WRITE_SIZE on the core scan kernels
+and on the copy probe) into the per-launch HBM traffic file bench.py reports as
+``roofline.traffic``: counter KiB per dispatch scaled to bytes by the copy probe's known size.
 """
 
 from __future__ import annotations
@@ -88,6 +94,50 @@ def copy_probe(mib: int, reps: int = 5) -> None:
           f"{n * 2} bytes read and {n * 2} bytes written per launch")
 
 
+# Core scan kernels by the names bench.py reports them under.
+_CORE_KERNELS = {"core_fwd_kernel": "core_scan_fwd", "core_bwd_kernel": "core_scan_bwd",
+                 "core_pair_kernel": "core_scan_pair"}
+
+
+def _one(rows: list[dict[str, object]], counter: str, match: str) -> dict[str, object]:
+    hits = [r for r in rows if r["counter"] == counter and re.search(match, r["kernel"])]
+    if len(hits) != 1:
+        raise SystemExit(f"expected one {counter} entry for {match!r}, found {len(hits)}")
+    return hits[0]
+
+
+def pmc_json(out: str, fetch_dir: str, write_dir: str, copy_fetch_dir: str, copy_write_dir: str,
+             copy_mib: int, workload: dict[str, object]) -> dict[str, object]:
+    """Per-launch HBM traffic of the core scan kernels, calibrated on the copy probe."""
+    import json
+
+    nbytes = copy_mib * 1024 * 1024
+    cf = _one(pmc_summary(copy_fetch_dir), "FETCH_SIZE", "neg")["mean"]
+    cw = _one(pmc_summary(copy_write_dir), "WRITE_SIZE", "neg")["mean"]
+    ff, wf = nbytes / (cf * 1024.0), nbytes / (cw * 1024.0)
+    fetch, write = pmc_summary(fetch_dir), pmc_summary(write_dir)
+    kernels = {}
+    for sym, name in _CORE_KERNELS.items():
+        try:
+            f, w = _one(fetch, "FETCH_SIZE", sym), _one(write, "WRITE_SIZE", sym)
+        except SystemExit:
+            continue
+        fb, wb = f["mean"] * 1024.0 * ff, w["mean"] * 1024.0 * wf
+        kernels[name] = {"kernel_symbol": f["kernel"], "fetch_size_kib": round(f["mean"], 1),
+                         "write_size_kib": round(w["mean"], 1), "fetch_bytes": int(fb),
+                         "write_bytes": int(wb), "traffic_bytes": int(fb + wb),
+                         "dispatches": int(f["dispatches"])}
+    doc = {"workload": workload,
+           "copy_calibration": {"bytes_read_and_written": nbytes, "fetch_size_kib": round(cf, 1),
+                                "write_size_kib": round(cw, 1), "fetch_factor": round(ff, 5),
+                                "write_factor": round(wf, 5)},
+           "kernels": kernels}
+    with open(out, "w") as fh:
+        json.dump(doc, fh, indent=1)
+        fh.write("\n")
+    return doc
+
+
 def main() -> None:
     p = argparse.ArgumentParser()
     p.add_argument("db", nargs="?")
@@ -95,8 +145,23 @@ def main() -> None:
     p.add_argument("--match", default=None)
     p.add_argument("--pmc-summary", default=None)
     p.add_argument("--copy-probe", type=int, default=None)
+    p.add_argument("--pmc-json", default=None)
+    for k in ("fetch", "write", "copy-fetch", "copy-write"):
+        p.add_argument(f"--{k}", default=None)
+    p.add_argument("--copy-mib", type=int, default=512)
+    for k, d in (("batch", 16), ("seq", 4096), ("state", 2048), ("chunk", 1024)):
+        p.add_argument(f"--{k}", type=int, default=d)
+    p.add_argument("--dtype", default="bf16")
     args = p.parse_args()
-    if args.copy_probe:
+    if args.pmc_json:
+        doc = pmc_json(args.pmc_json, args.fetch, args.write, args.copy_fetch, args.copy_write,
+                       args.copy_mib, {"batch": args.batch, "seq_len": args.seq,
+                                       "state": args.state, "chunk_t": args.chunk,
+                                       "dtype": args.dtype})
+        for name, k in doc["kernels"].items():
+            print(f"{name}: {k['traffic_bytes'] / 1e9:.3f} GB per launch "
+                  f"({k['dispatches']} dispatches)")
+    elif args.copy_probe:
         copy_probe(args.copy_probe)
     elif args.pmc_summary:
         for r in pmc_summary(args.pmc_summary, args.match):
