@@ -1283,13 +1283,15 @@ static int check_fwd(const dabsn_core_fwd_call& f, Cfg& c) {
                              f.gate),
                 "core scan: null tape pointer");
   if (f.dtype == kBF16 && c.ch == 16 && f.T > 0) {
-    // The 16-unit bf16 kernels write tapes as 16-byte chunks of 8 units.
+    // The 16-unit bf16 kernels write tapes (and, with 8 waves, read Wx/Wgx) as 16-byte
+    // chunks of 8 units.
     DABSN_REQUIRE(f.H % 16 == 0, "core scan: bf16 with H >= 1024 needs H %% 16 == 0 (H=%lld)",
                   (long long)f.H);
-    const void* outs[] = {f.U, f.nov, f.plast, f.expr, f.write, f.energy, f.sat, f.gate};
+    const void* outs[] = {f.U, f.nov, f.plast, f.expr, f.write, f.energy, f.sat, f.gate,
+                          f.Wx, f.Wgx};
     for (const void* q : outs)
       DABSN_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15u) == 0,
-                    "core scan: bf16 tape pointers must be 16-byte aligned");
+                    "core scan: bf16 input and tape pointers must be 16-byte aligned");
   }
   return DABSN_OK;
 }

@@ -63,7 +63,10 @@ int dabsn_hip_core_scan_config(int dtype, int64_t B, int64_t H, int* ch, int* ks
 
 /* Forward. Wx, Wgx [B,T,H]; GA = [Ug; A] as [2H,H]; b0, e0, c0 [B,H] fp32.
  * Outputs: U [B,T,2H] (y, next budget), nov, plast, expr, write, energy (pre-update),
- * sat (post-update), gate [B,T,H]; final state bF, eF, cF [B,H] fp32. */
+ * sat (post-update), gate [B,T,H]; final state bF, eF, cF [B,H] fp32.
+ * bf16 with H >= 1024 moves rows as 16-byte chunks: H must be a multiple of 16 and Wx, Wgx
+ * and the tape pointers 16-byte aligned (DABSN_ERR_ARG otherwise); the backward asks
+ * the same of its tapes, grads and outputs. */
 int dabsn_hip_core_scan_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* Wx,
                             const void* Wgx, const void* GA, const dabsn_core_params* params,
                             const float* b0, const float* e0, const float* c0, void* U, void* nov,
