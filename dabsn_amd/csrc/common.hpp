@@ -126,6 +126,12 @@ __device__ __forceinline__ float dpp_mov(float x, float old) {
                                                                __builtin_bit_cast(int, x), CTRL,
                                                                ROW_MASK, 0xF, false));
 }
+// Lane i receives lane i + N of its 16-lane row (DPP row_shl); lanes past the row's end
+// keep their own value. A VALU move: no LDS round trip, unlike ds_bpermute.
+template <int N>
+__device__ __forceinline__ int row_shl(int x) {
+  return __builtin_amdgcn_update_dpp(x, x, 0x100 + N, 0xF, 0xF, false);
+}
 template <typename Op>
 __device__ __forceinline__ float wave_reduce(float v, float identity, Op op) {
   v = op(v, dpp_mov<0xB1, 0xF>(v, identity));   // quad_perm [1,0,3,2]

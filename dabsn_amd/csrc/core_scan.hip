@@ -183,11 +183,13 @@ __device__ __forceinline__ void publish(__amdgpu_buffer_rsrc_t xr, uint32_t slot
     if (is_pair) {
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
+        // Groups of 8 lanes lie inside 16-lane rows, so in-row DPP shifts gather the
+        // group for its first lane (the lanes whose shifts leave the row are not stored).
         const int h = static_cast<int>(f2bf(vals[i]));
-        const int w0 = h | (__shfl_down(h, 1, 8) << 16);
-        const int w1 = __shfl_down(w0, 2, 8);
-        const int w2 = __shfl_down(w0, 4, 8);
-        const int w3 = __shfl_down(w0, 6, 8);
+        const int w0 = h | (row_shl<1>(h) << 16);
+        const int w1 = row_shl<2>(w0);
+        const int w2 = row_shl<4>(w0);
+        const int w3 = row_shl<6>(w0);
         if ((cl & 7) == 0) {
           const u32x4 v = {static_cast<uint32_t>(w0), static_cast<uint32_t>(w1),
                            static_cast<uint32_t>(w2), static_cast<uint32_t>(w3)};
