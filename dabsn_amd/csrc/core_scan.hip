@@ -26,6 +26,9 @@
 //     waits for the exchange) enters every output affinely through the budget grad.
 //   * Barrier waits are bounded: a wait that exceeds kSpinLimit polls sets the error
 //     word and every workgroup exits.
+#include <algorithm>
+#include <initializer_list>
+
 #include "../../include/dabsn_hip.h"
 #include "capi.hpp"
 #include "common.hpp"
@@ -1164,6 +1167,78 @@ static int launch_coop(K kernel, int grid, int threads, const A& args, hipStream
   return DABSN_OK;
 }
 
+// Batch rows are independent, so a batch whose workgroups cannot all be resident at once is
+// scanned in slabs of whole batch groups, one cooperative launch per slab, each on the
+// rows of its slab (pointer offsets) and the same workspace with its step counters
+// cleared in between (the error word at its start is kept).
+template <typename P>
+static P* adv(P* p, size_t n) {
+  return p ? p + n : p;
+}
+
+template <typename E>
+static FwdArgs<E> slab_of(const FwdArgs<E>& a, int g0, int ng) {
+  FwdArgs<E> s = a;
+  const size_t b0 = static_cast<size_t>(g0) * NB, row = static_cast<size_t>(a.ldt) * a.H;
+  s.B = static_cast<int>(std::min<size_t>(static_cast<size_t>(ng) * NB, a.B - b0));
+  s.Wx = adv(a.Wx, b0 * row);
+  s.Wgx = adv(a.Wgx, b0 * row);
+  s.b0 = adv(a.b0, b0 * a.H);
+  s.e0 = adv(a.e0, b0 * a.H);
+  s.c0 = adv(a.c0, b0 * a.H);
+  s.U = adv(a.U, b0 * 2 * row);
+  for (E** t : {&s.nov, &s.pl, &s.ay, &s.wr, &s.et, &s.ctp, &s.st}) *t = adv(*t, b0 * row);
+  s.bF = adv(a.bF, b0 * a.H);
+  s.eF = adv(a.eF, b0 * a.H);
+  s.cF = adv(a.cF, b0 * a.H);
+  return s;
+}
+
+template <typename E>
+static BwdArgs<E> slab_of(const BwdArgs<E>& a, int g0, int ng) {
+  BwdArgs<E> s = a;
+  const size_t b0 = static_cast<size_t>(g0) * NB, row = static_cast<size_t>(a.ldt) * a.H;
+  s.B = static_cast<int>(std::min<size_t>(static_cast<size_t>(ng) * NB, a.B - b0));
+  s.b0 = adv(a.b0, b0 * a.H);
+  s.c0 = adv(a.c0, b0 * a.H);
+  s.U = adv(a.U, b0 * 2 * row);
+  s.gU = adv(a.gU, b0 * 2 * row);
+  for (const E** t : {&s.pl, &s.ay, &s.et, &s.ctp, &s.st, &s.gN, &s.gP, &s.gA, &s.gW, &s.gE,
+                      &s.gC})
+    *t = adv(*t, b0 * row);
+  s.gbF = adv(a.gbF, b0 * a.H);
+  s.geF = adv(a.geF, b0 * a.H);
+  s.gcF = adv(a.gcF, b0 * a.H);
+  for (E** t : {&s.gWx, &s.gWgx, &s.day}) *t = adv(*t, b0 * row);
+  s.part_vec = adv(a.part_vec, static_cast<size_t>(g0) * 16 * a.H);
+  s.part_scal = adv(a.part_scal, static_cast<size_t>(g0) * a.nct * 3);
+  s.gb0 = adv(a.gb0, b0 * a.H);
+  s.ge0 = adv(a.ge0, b0 * a.H);
+  s.gc0 = adv(a.gc0, b0 * a.H);
+  return s;
+}
+
+template <typename K, typename A>
+static int launch_slabs(K kernel, int threads, const Cfg& c, const A& args, hipStream_t stream) {
+  int dev = 0, cus = 0, per_cu = 0;
+  DABSN_HIP_CHECK(hipGetDevice(&dev));
+  DABSN_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  DABSN_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0));
+  const int per_launch = per_cu * cus / c.nct;  // batch groups one launch can hold
+  if (per_launch < 1 || c.nbg <= per_launch)
+    return launch_coop(kernel, c.nct * c.nbg, threads, args, stream);  // reports a misfit
+  for (int g0 = 0; g0 < c.nbg; g0 += per_launch) {
+    const int ng = std::min(per_launch, c.nbg - g0);
+    if (g0 > 0) {
+      const int rc = dabsn_hip_zero(args.ws + kCtrOff, xchg_offset(ng) - kCtrOff, stream);
+      if (rc != DABSN_OK) return rc;
+    }
+    const int rc = launch_coop(kernel, c.nct * ng, threads, slab_of(args, g0, ng), stream);
+    if (rc != DABSN_OK) return rc;
+  }
+  return DABSN_OK;
+}
+
 // (CH, KSTEPS, NW) combinations compiled per dtype.
 #define DABSN_CORE_CASES_BF16(X) \
   X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(16, 8, 4) X(16, 8, 8)
@@ -1172,10 +1247,9 @@ static int launch_coop(K kernel, int grid, int threads, const A& args, hipStream
 
 template <typename E>
 static int fwd_dispatch(const Cfg& c, const FwdArgs<E>& args, hipStream_t stream) {
-  const int grid = c.nct * c.nbg;
 #define DABSN_CASE(CHV, KS, NWV)                                   \
   if (c.ch == CHV && c.ksteps == KS && c.nw == NWV)                \
-    return launch_coop(core_fwd_kernel<E, CHV, KS, NWV>, grid, NWV * 64, args, stream);
+    return launch_slabs(core_fwd_kernel<E, CHV, KS, NWV>, NWV * 64, c, args, stream);
   if constexpr (is_bf16<E>::value) {
     DABSN_CORE_CASES_BF16(DABSN_CASE)
   } else {
@@ -1188,10 +1262,9 @@ static int fwd_dispatch(const Cfg& c, const FwdArgs<E>& args, hipStream_t stream
 
 template <typename E>
 static int bwd_dispatch(const Cfg& c, const BwdArgs<E>& args, hipStream_t stream) {
-  const int grid = c.nct * c.nbg;
 #define DABSN_CASE(CHV, KS, NWV)                                   \
   if (c.ch == CHV && c.ksteps == KS && c.nw == NWV)                \
-    return launch_coop(core_bwd_kernel<E, CHV, KS, NWV>, grid, NWV * 64, args, stream);
+    return launch_slabs(core_bwd_kernel<E, CHV, KS, NWV>, NWV * 64, c, args, stream);
   if constexpr (is_bf16<E>::value) {
     DABSN_CORE_CASES_BF16(DABSN_CASE)
   } else {

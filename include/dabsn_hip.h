@@ -66,7 +66,8 @@ int dabsn_hip_core_scan_config(int dtype, int64_t B, int64_t H, int* ch, int* ks
  * sat (post-update), gate [B,T,H]; final state bF, eF, cF [B,H] fp32.
  * bf16 with H >= 1024 moves rows as 16-byte chunks: H must be a multiple of 16 and Wx, Wgx
  * and the tape pointers 16-byte aligned (DABSN_ERR_ARG otherwise); the backward asks
- * the same of its tapes, grads and outputs. */
+ * the same of its tapes, grads and outputs. Any B: batch groups that do not fit on the
+ * device at once run as consecutive launches on the same stream. */
 int dabsn_hip_core_scan_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* Wx,
                             const void* Wgx, const void* GA, const dabsn_core_params* params,
                             const float* b0, const float* e0, const float* c0, void* U, void* nov,

@@ -126,6 +126,54 @@ def test_core_scan_bf16_absent_grads_equal_zero_grads(cuda_device, absent, H):
         assert torch.equal(u, v), f"output {i} differs"
 
 
+@pytest.mark.parametrize("chunk", [None, 8])
+def test_core_scan_batch_beyond_one_launch_equals_row_blocks(cuda_device, chunk):
+    """At H = 2048 in bf16 one cooperative launch holds two 16-row batch groups (128
+    workgroups each on 256 CUs), so B = 40 runs as two slabs (rows 0-31, then the 8 rows
+    32-39). Chunked (chunk=8), the paired recompute + reverse launch does not fit either,
+    so the two run one after the other, each in slabs, while the 16- and 8-row blocks use
+    the paired launch. Rows are independent: forward outputs, per-row input grads and
+    initial-state grads equal separate calls on rows 0-15, 16-31 and 32-39 bit for bit.
+    Parameter grads add the same per-group partials in another grouping: fp32 vectors and
+    scalars to 1e-5; grad [Ug; A] is a bf16 GEMM over all rows, whose bf16 output rounding
+    differs from the sum of three (normwise 1e-2)."""
+    from dabsn_amd.kernels.chunked import chunked_core_scan
+
+    def run(*a):
+        return ops.core_scan_batched(*a) if chunk is None else chunked_core_scan(chunk, *a)
+
+    B, T, H = 40, 24, 2048
+    inp = core_case(401, B, T, H)
+    x = [t.to(cuda_device) for t in inp]
+    x[0], x[1] = x[0].to(torch.bfloat16), x[1].to(torch.bfloat16)
+    rows = (0, 1, 23, 24, 25)  # Wx, Wgx, b0, e0, c0: per batch row
+    leaves = [t.detach().requires_grad_(True) for t in x]
+    full = run(*leaves)
+    g = torch.Generator().manual_seed(402)
+    ups = [torch.randn(o.shape, generator=g).to(cuda_device).to(o.dtype) for o in full]
+    ups[7] = torch.zeros_like(ups[7])  # no gradient path through the gate tape
+    gfull = torch.autograd.grad(full, leaves, ups, allow_unused=True)
+    psum = [None] * len(x)
+    for r0, r1 in ((0, 16), (16, 32), (32, 40)):
+        xs = [t[r0:r1].contiguous() if i in rows else t for i, t in enumerate(x)]
+        lp = [t.detach().requires_grad_(True) for t in xs]
+        part = run(*lp)
+        for n, a, b in zip(OUT_NAMES, part, full):
+            assert torch.equal(a, b[r0:r1]), f"{n} rows {r0}-{r1}"
+        gp = torch.autograd.grad(part, lp, [u[r0:r1] for u in ups], allow_unused=True)
+        for i in rows:
+            assert torch.equal(gp[i], gfull[i][r0:r1]), f"grad input {i} rows {r0}-{r1}"
+        for i in range(len(x)):
+            if i not in rows and gp[i] is not None:
+                psum[i] = gp[i] if psum[i] is None else psum[i] + gp[i]
+    for i in (2, 3):
+        err = rel_fro(psum[i].float().cpu(), gfull[i].float().cpu())
+        assert err <= 1e-2, f"grad input {i}: {err:.3e}"
+    for i in range(4, 23):
+        a, b = psum[i].float().cpu(), gfull[i].float().cpu()
+        assert rel_err(a, b) <= 1e-5, f"grad input {i}: {rel_err(a, b):.3e}"
+
+
 def test_core_scan_chunked_equals_full_on_device(cuda_device):
     """Carried (b, e, c): two chunks equal one pass exactly (same kernel, same state)."""
     inp = core_case(5, 4, 50, 64)
