@@ -112,14 +112,18 @@ class DABSNBlock(nn.Module):
         trajectory, novelty, plasticity, expression, write, energy, saturation = self.core_tapes(inputs)
         y, budget = trajectory.split(self.state_dim, dim=-1)
         read = self.read(y, budget, expression, write, novelty, plasticity, energy, saturation)
-        out = self.state_to_hidden(y + self.read_gain * read)
-        if self.residual:
-            skip = inputs if self.residual_skip is None else self.residual_skip(inputs)
-            out = skip + out
+        out = self.finish(inputs, self.state_to_hidden(y + self.read_gain * read))
         self.last_trace = {"read_geometry": self.read_geometry,
                            "admitted_n_max": self.read.last_n_max,
                            "read_contract": self.read.last_read_contract}
         return out
+
+    def finish(self, inputs: Tensor, dabsn_output: Tensor) -> Tensor:
+        """The block output before the MLP: the DABSN path plus the residual skip, if any."""
+        if not self.residual:
+            return dabsn_output
+        skip = inputs if self.residual_skip is None else self.residual_skip(inputs)
+        return skip + dabsn_output
 
     def forward_mlp(self, hidden: Tensor) -> Tensor:
         if self.mlp_fc2 is None:

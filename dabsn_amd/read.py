@@ -216,6 +216,41 @@ class DABSNRead(nn.Module):
             return torch.addcmul(short_output, self.long_gain, long), final_state
         return torch.addcmul(short_output, self.long_gain, result)
 
+    def forward_query_bank_stats(self, y, budget, expression, write, plasticity, *,
+                                 query_stats, bank_write, bank_stats, query_start: int,
+                                 initial_long_state=None):
+        """forward_query_bank with the bank given as its write vectors plus per-position
+        statistics instead of full-width tapes.
+
+        The read uses the bank's novelty, plasticity, energy and saturation only through
+        their means over H, and its writes through their row norms (read.py:58-72, 161-183).
+        A carried bank therefore keeps, per position, the row of ``ops.read_tape_stats``
+        computed when that position was a query: means of energy, saturation, novelty and
+        plasticity, the query norm and the write norm ([B, N, 6] fp32). Those are the rows
+        one dense pass computes for the same positions, so this is the dense read.
+        ``query_stats`` are the rows of the query chunk itself (which the caller has
+        already appended to the bank, ending at ``query_start + T``).
+
+        Returns (output, final long state)."""
+        rp = self.short_read
+        _, _, hidden = expression.shape
+        bank_len = bank_write.shape[1]
+        if bank_len <= 0:
+            raise RuntimeError("query-bank read requires a non-empty bank")
+        qe, qc, qn, qp = query_stats.unbind(-1)[:4]
+        be, bc, bn, bp = bank_stats.unbind(-1)[:4]
+        query = ops.normalize_rows(expression, query_stats[..., 4].detach())
+        key_bias = rp.key_bias_from_means(bn, bp, hidden)
+        admission = rp.admission_from_means(be, bc, bn, bp, hidden)
+        cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
+        retrieved = self._read_core(query, cocktails, bank_write, bank_stats[..., 5].detach(),
+                                    key_bias, admission, bank_len, int(query_start))
+        short_output = rp.project(y, budget, retrieved.to(y.dtype))
+        long, final_state = self._long_scan_from_state(write, plasticity, None,
+                                                       initial_state=initial_long_state,
+                                                       return_final_state=True)
+        return torch.addcmul(short_output, self.long_gain, long), final_state
+
 
 def collect_traces_enabled() -> bool:
     return os.environ.get("DABSN_COLLECT_TRACES", "0") == "1"

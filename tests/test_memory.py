@@ -1,0 +1,131 @@
+"""Carried memory (ingest / forward_with_memory) against one dense pass of the same model.
+
+Reference behaviour: src/dabsn/memory.py and its exactness claim (tests/test_memory_carry.py
+of the reference: chunked ingest against a growing bank reproduces one dense pass to
+float32 rounding). CPU variants run through the test-only oracle backend
+(oracle/torch_backend.py registers the C oracle as the ops' CPU kernels); GPU variants run
+the HIP kernels. fp32 throughout; tolerance normwise 1e-5 (the chunked read sums over a
+bank of a different width, so reductions differ in order).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import dabsn_amd
+from dabsn_amd import memory as mem
+from helpers import rel_err
+from oracle import torch_backend
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _oracle_cpu_kernels():
+    torch_backend.register()
+
+
+def _model(device):
+    torch.manual_seed(7)
+    model = dabsn_amd.DABSNSequenceLM(40, 24, [(24, 24), (32, 16)], residual=True, mlp_ratio=2.0)
+    for block in model.blocks:
+        block.read.admit_window.data.fill_(0.3)  # a partially admitted bank
+    return model.to(device).eval()
+
+
+def _dense(model, ids):
+    with torch.no_grad():
+        h = model.embed(ids)
+        for block in model.blocks:
+            h = block(h)
+        return h, model.readout(h)
+
+
+def _ids(B, T, seed=8):
+    return torch.randint(0, 40, (B, T), generator=torch.Generator().manual_seed(seed))
+
+
+def _chunked_ingest(device):
+    model = _model(device)
+    ids = _ids(2, 45).to(device)
+    want, _ = _dense(model, ids)
+    got, memory = mem.forward_with_memory(model, ids, None, chunk_size=8, return_hidden=True)
+    assert memory.position == 45 and memory.entries == 45
+    assert [layer.bank.length for layer in memory.layers] == [45, 45]
+    return got, want
+
+
+def _decode(device):
+    model = _model(device)
+    ids = _ids(3, 26, seed=9).to(device)
+    _, want = _dense(model, ids)
+    memory = mem.ingest(model, ids[:, :20], chunk_size=6)
+    memory.reserve(26)
+    logits = []
+    for t in range(20, 26):
+        step, memory = mem.forward_with_memory(model, ids[:, t:t + 1], memory, extend=True)
+        logits.append(step)
+    assert memory.position == 26
+    return torch.cat(logits, dim=1), want[:, 20:]
+
+
+def test_bank_store_appends_in_place_and_doubles():
+    bank = mem.BankStore(2, 3, device="cpu", dtype=torch.float32, capacity=2)
+    rows = torch.arange(2 * 5 * 3, dtype=torch.float32).reshape(2, 5, 3)
+    stats = torch.arange(2 * 5 * 6, dtype=torch.float32).reshape(2, 5, 6)
+    bank.append(rows[:, :2], stats[:, :2])
+    storage = bank.write
+    bank.append(rows[:, 2:3], stats[:, 2:3])  # full: grows to max(3, 2 * 2) = 4
+    assert bank.capacity == 4 and bank.write is not storage
+    storage = bank.write
+    bank.append(rows[:, 3:4], stats[:, 3:4])  # fits: written in place
+    assert bank.write is storage and bank.length == 4
+    bank.reserve(16)
+    bank.append(rows[:, 4:], stats[:, 4:])
+    w, s = bank.live()
+    assert bank.capacity == 16 and torch.equal(w, rows) and torch.equal(s, stats)
+
+
+def test_memory_refuses_other_architecture_or_batch():
+    model = _model("cpu")
+    memory = mem.DABSNMemory(layers=[], position=0, batch_size=2,
+                             fingerprint=mem.fingerprint_of(model))
+    with pytest.raises(ValueError, match="batch"):
+        mem.forward_with_memory(model, _ids(3, 4), memory)
+    other = dabsn_amd.DABSNSequenceLM(40, 24, [(24, 24)], residual=True, mlp_ratio=2.0)
+    with pytest.raises(ValueError, match="different architecture"):
+        mem.forward_with_memory(other, _ids(2, 4), memory)
+
+
+def test_chunked_ingest_equals_dense_pass_cpu():
+    got, want = _chunked_ingest("cpu")
+    assert rel_err(got, want) <= 1e-5
+
+
+def test_decode_token_by_token_equals_dense_pass_cpu():
+    got, want = _decode("cpu")
+    assert rel_err(got, want) <= 1e-5
+
+
+def test_read_only_query_leaves_memory_unchanged_cpu():
+    model = _model("cpu")
+    ids = _ids(2, 30)
+    memory = mem.ingest(model, ids[:, :24], chunk_size=10)
+    a, m1 = mem.forward_with_memory(model, ids[:, 24:], memory)
+    b, m2 = mem.forward_with_memory(model, ids[:, 24:], memory)
+    assert m1 is memory and m2 is memory and memory.position == 24
+    assert [layer.bank.length for layer in memory.layers] == [24, 24]
+    assert torch.equal(a, b)
+    c, grown = mem.forward_with_memory(model, ids[:, 24:], memory, extend=True)
+    assert torch.equal(a, c) and grown.position == 30 and grown.entries == 30
+
+
+@pytest.mark.gpu
+def test_chunked_ingest_equals_dense_pass_gpu(cuda_device):
+    got, want = _chunked_ingest(cuda_device)
+    assert rel_err(got.cpu(), want.cpu()) <= 1e-5
+
+
+@pytest.mark.gpu
+def test_decode_token_by_token_equals_dense_pass_gpu(cuda_device):
+    got, want = _decode(cuda_device)
+    assert rel_err(got.cpu(), want.cpu()) <= 1e-5
