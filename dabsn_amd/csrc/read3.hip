@@ -20,6 +20,8 @@
 // Tile ranges follow the causal staircase: a query tile only visits bank slots that
 // any of its queries may read; a bank tile only visits queries at or after its
 // earliest admitted index.
+#include <algorithm>
+
 #include "../../include/dabsn_hip.h"
 #include "capi.hpp"
 #include "common.hpp"
@@ -668,6 +670,214 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
 using namespace dabsn;
 using namespace dabsn::read3;
 
+// ---------------------------------------------------------------------------
+// Decode read: a few query rows (T <= kDecodeRows) against a long bank, reading the bank's
+// write rows in place through an index list and a row stride, with no gathered K/V/Vn
+// copies and no transposes. Same masks, softmaxes and dtype policy as forward_impl:
+// K = E(write / max(norm, eps)) as bank_gather stores it, scores in fp32, P_V / P_Vn stored
+// in E, the output accumulated in fp32 (per slot split, then summed in split order) and
+// stored in E. Inference only (no backward).
+// ---------------------------------------------------------------------------
+constexpr int kDecodeRows = 8;
+constexpr int kDecodeSlotsPerBlock = 16;  // 4 waves x 4 slots
+constexpr float kNormEps = 1e-12f;        // as bank_gather
+
+// Bank row of slot index i of batch row b (indices are clamped into the bank).
+template <typename E>
+__device__ __forceinline__ const E* bank_row(const E* bank, int b, int64_t rowld, int64_t Nb,
+                                             int64_t i, int H) {
+  const int64_t r = i < 0 ? 0 : (i >= Nb ? Nb - 1 : i);
+  return bank + (static_cast<size_t>(b) * rowld + r) * H;
+}
+
+// S[b, t, j] = q[b, t] . K_j for every slot j. One wave per slot; the T query rows of
+// batch row b are staged in LDS (dynamic, T * H elements).
+template <typename E>
+__global__ void __launch_bounds__(256) decode_score_kernel(int T, int N, int H, int64_t Nb,
+                                                           int64_t rowld, const E* q, const E* bank,
+                                                           const float* norm_w,
+                                                           const int64_t* idx, float* S) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char qraw[];
+  E* qs = reinterpret_cast<E*>(qraw);
+  const int b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nch = H / 8;  // 8-element chunks per row
+  for (int c = tid; c < T * nch; c += 256)
+    *reinterpret_cast<u32x4*>(qs + c * 8) =
+        *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(b) * T * H + c * 8);
+  if constexpr (sizeof(E) == 4) {
+    for (int c = tid; c < T * nch; c += 256)
+      *reinterpret_cast<u32x4*>(qs + c * 8 + 4) =
+          *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(b) * T * H + c * 8 + 4);
+  }
+  __syncthreads();
+  for (int k = 0; k < kDecodeSlotsPerBlock / 4; ++k) {
+    const int j = blockIdx.x * kDecodeSlotsPerBlock + wave * (kDecodeSlotsPerBlock / 4) + k;
+    if (j >= N) break;  // wave-uniform
+    const int64_t i = idx[static_cast<size_t>(b) * N + j];
+    const E* row = bank_row(bank, b, rowld, Nb, i, H);
+    const int64_t ic = i < 0 ? 0 : (i >= Nb ? Nb - 1 : i);
+    const float n = fmaxf(norm_w[static_cast<size_t>(b) * Nb + ic], kNormEps);
+    float acc[kDecodeRows];
+#pragma unroll
+    for (int t = 0; t < kDecodeRows; ++t) acc[t] = 0.0f;
+    for (int c = lane; c < nch; c += 64) {
+      float v[8];
+      ldv<E, 8>(row + c * 8, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = round_to<E>(v[e] / n);
+#pragma unroll
+      for (int t = 0; t < kDecodeRows; ++t) {
+        if (t < T) {
+          float qv[8];
+          ldv<E, 8>(qs + (t * nch + c) * 8, qv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[t] += qv[e] * v[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kDecodeRows; ++t) {
+      if (t < T) {
+        const float sum = wave_sum(acc[t]);
+        if (lane == 0) S[(static_cast<size_t>(b) * T + t) * N + j] = sum;
+      }
+    }
+  }
+}
+
+// part[s][b][t][h] = sum over the slots j < nhi of split s of P_V[t, j] V_j[h] +
+// P_Vn[t, j] Vn_j[h], with V_j the bank row of idx[j] and Vn_j that of next_idx[j]. A
+// thread owns 8 consecutive h; blocks: (h chunk, b, split).
+template <typename E>
+__global__ void __launch_bounds__(256) decode_out_kernel(int T, int N, int H, int64_t Nb,
+                                                         int64_t rowld, int per_split,
+                                                         const E* bank, const int64_t* idx,
+                                                         const int64_t* next_idx, const E* PV,
+                                                         const E* PVn, const int32_t* rs,
+                                                         float* part) {
+  const int b = blockIdx.y, s = blockIdx.z;
+  const int h0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (h0 >= H) return;
+  const int QT = (T + TILE - 1) / TILE;
+  const int nhi = min(N, rs[(static_cast<size_t>(b) * QT) * 3 + 2]);  // T <= TILE: one tile
+  const int j0 = s * per_split, j1 = min(nhi, j0 + per_split);
+  float acc[kDecodeRows][8];
+#pragma unroll
+  for (int t = 0; t < kDecodeRows; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[t][e] = 0.0f;
+  const size_t prow = static_cast<size_t>(b) * T * N;
+  for (int j = j0; j < j1; ++j) {
+    float v[8], vn[8];
+    ldv<E, 8>(bank_row(bank, b, rowld, Nb, idx[static_cast<size_t>(b) * N + j], H) + h0, v);
+    ldv<E, 8>(bank_row(bank, b, rowld, Nb, next_idx[static_cast<size_t>(b) * N + j], H) + h0, vn);
+#pragma unroll
+    for (int t = 0; t < kDecodeRows; ++t) {
+      if (t < T) {
+        const float pv = ld(PV, prow + static_cast<size_t>(t) * N + j);
+        const float pn = ld(PVn, prow + static_cast<size_t>(t) * N + j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[t][e] += pv * v[e] + pn * vn[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kDecodeRows; ++t) {
+    if (t < T) {
+      float* o = part + ((static_cast<size_t>(s) * gridDim.y + b) * T + t) * H + h0;
+      *reinterpret_cast<f32x4*>(o) = (f32x4){acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
+      *reinterpret_cast<f32x4*>(o + 4) = (f32x4){acc[t][4], acc[t][5], acc[t][6], acc[t][7]};
+    }
+  }
+}
+
+// out = sum over splits of part, in split order; 8 elements per thread.
+template <typename E>
+__global__ void __launch_bounds__(256) decode_reduce_kernel(int64_t chunks, int splits,
+                                                            int64_t stride, const float* part,
+                                                            E* out) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  float acc[8];
+  ldv<float, 8>(part + c * 8, acc);
+  for (int s = 1; s < splits; ++s) {
+    float v[8];
+    ldv<float, 8>(part + s * stride + c * 8, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += v[e];
+  }
+  stv<E, 8>(out + c * 8, acc);
+}
+
+struct DecodePlan {
+  size_t off_S, off_rs, off_ro, off_rb, off_stats, off_PV, off_PVn, off_part, end;
+  int splits, per_split;
+};
+
+static DecodePlan decode_plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
+  DecodePlan p{};
+  const size_t e = dtype == kBF16 ? 2 : 4;
+  const size_t QT = (T + TILE - 1) / TILE, BT = (N + TILE - 1) / TILE;
+  const size_t TN = static_cast<size_t>(B) * T * N;
+  const int64_t hblocks = (H + 2047) / 2048;
+  // Enough (h chunk, b, split) blocks to fill the device, at least 64 slots per split.
+  int64_t splits = (512 + hblocks * B - 1) / (hblocks * B);
+  splits = std::max<int64_t>(1, std::min<int64_t>(splits, (N + 63) / 64));
+  p.splits = static_cast<int>(splits);
+  p.per_split = static_cast<int>((N + splits - 1) / splits);
+  size_t o = 0;
+  p.off_S = o; o = align_up(o + TN * 4);
+  p.off_rs = o; o = align_up(o + B * QT * 3 * 4);
+  p.off_ro = o; o = align_up(o + B * QT * 3 * 4);
+  p.off_rb = o; o = align_up(o + B * BT * 3 * 4);
+  p.off_stats = o; o = align_up(o + static_cast<size_t>(B) * T * 6 * 4);
+  p.off_PV = o; o = align_up(o + TN * e);
+  p.off_PVn = o; o = align_up(o + TN * e);
+  p.off_part = o; o = align_up(o + static_cast<size_t>(splits) * B * T * H * 4);
+  p.end = o;
+  return p;
+}
+
+template <typename E>
+static int decode_impl(int64_t B, int64_t T, int64_t N, int64_t H, int64_t Nb, int64_t rowld,
+                       const E* q, const E* bank, const float* norm_w, const int64_t* idx,
+                       const int64_t* next_idx, const int64_t* read_idx, const uint8_t* valid,
+                       const float* ck, const float* cb, const float* kb, const float* adm,
+                       const float* scale, Gains g, E* out, uint8_t* ws, const DecodePlan& p,
+                       hipStream_t stream) {
+  const int QT = static_cast<int>((T + TILE - 1) / TILE), BT = static_cast<int>((N + TILE - 1) / TILE);
+  float* S = reinterpret_cast<float*>(ws + p.off_S);
+  int32_t* rs = reinterpret_cast<int32_t*>(ws + p.off_rs);
+  int32_t* ro = reinterpret_cast<int32_t*>(ws + p.off_ro);
+  int32_t* rb = reinterpret_cast<int32_t*>(ws + p.off_rb);
+  float* stats = reinterpret_cast<float*>(ws + p.off_stats);
+  E* PV = reinterpret_cast<E*>(ws + p.off_PV);
+  E* PVn = reinterpret_cast<E*>(ws + p.off_PVn);
+  float* part = reinterpret_cast<float*>(ws + p.off_part);
+  hipLaunchKernelGGL(ranges_kernel, dim3((unsigned)(QT + BT), (unsigned)B), dim3(256), 0, stream,
+                     (int)T, (int)N, (int)H, 0, read_idx, valid, rs, ro, rb);
+  DABSN_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(decode_score_kernel<E>,
+                     dim3((unsigned)((N + kDecodeSlotsPerBlock - 1) / kDecodeSlotsPerBlock), (unsigned)B),
+                     dim3(256), static_cast<unsigned>(T * H * sizeof(E)), stream, (int)T, (int)N,
+                     (int)H, Nb, rowld, q, bank, norm_w, idx, S);
+  DABSN_HIP_CHECK(hipGetLastError());
+  RowCtx c{(int)T, (int)N, 0, S, kb, adm, cb, ck, read_idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
+  hipLaunchKernelGGL(softmax_fwd_kernel<E>, dim3((unsigned)((B * T + NWV - 1) / NWV)), dim3(NTH), 0,
+                     stream, B * T, c, g, scale, rs, stats, PV, PVn);
+  DABSN_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(decode_out_kernel<E>,
+                     dim3((unsigned)((H + 2047) / 2048), (unsigned)B, (unsigned)p.splits), dim3(256), 0,
+                     stream, (int)T, (int)N, (int)H, Nb, rowld, p.per_split, bank, idx, next_idx, PV,
+                     PVn, rs, part);
+  DABSN_HIP_CHECK(hipGetLastError());
+  const int64_t chunks = B * T * H / 8;
+  hipLaunchKernelGGL(decode_reduce_kernel<E>, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                     stream, chunks, p.splits, B * T * H, part, out);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
 static int read3_checks(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, int mode) {
   DABSN_REQUIRE(dtype == kF32 || dtype == kBF16, "read3: bad dtype %d", dtype);
   DABSN_REQUIRE(mode == 0 || mode == 1, "read3: mode must be 0 (seq) or 1 (field)");
@@ -750,6 +960,50 @@ int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
                               admission, scale, idx, valid, mode, g, (float*)gq, (float*)gK,
                               (float*)gV, (float*)gVn, gcocktail, gbank_cocktail, gkey_bias,
                               gadmission, gscalars5, (uint8_t*)workspace, p, stream);
+}
+
+
+size_t dabsn_hip_read3_decode_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t N,
+                                              int64_t H) {
+  return decode_plan(dtype, B, T, N, H).end;
+}
+
+int dabsn_hip_read3_decode(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* q,
+                           const void* bank, int64_t bank_len, int64_t bank_ld,
+                           const float* norm_w, const int64_t* idx, const int64_t* next_idx,
+                           const int64_t* read_idx, const uint8_t* valid, const float* cocktail,
+                           const float* bank_cocktail, const float* key_bias,
+                           const float* admission, const float* scale,
+                           const float* const* gains, void* out, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+  const int rc = read3_checks(dtype, B, T, N, H, 0);
+  if (rc != DABSN_OK) return rc;
+  DABSN_REQUIRE(T <= kDecodeRows, "read3 decode: T=%lld query rows > %d", (long long)T, kDecodeRows);
+  DABSN_REQUIRE(N > 0 && bank_len > 0 && bank_ld >= bank_len, "read3 decode: bad bank shape");
+  DABSN_REQUIRE(H % 8 == 0, "read3 decode: H=%lld must be a multiple of 8", (long long)H);
+  DABSN_REQUIRE(T * H * (dtype == kBF16 ? 2 : 4) <= 65536,
+                "read3 decode: T*H too large for the query staging");
+  DABSN_REQUIRE(q && bank && norm_w && idx && next_idx && read_idx && valid && cocktail &&
+                    bank_cocktail && key_bias && admission && scale && gains && out && workspace,
+                "read3 decode: null pointer");
+  for (int i = 0; i < 4; ++i) DABSN_REQUIRE(gains[i], "read3 decode: null gain %d", i);
+  const void* vec[] = {q, bank, out};
+  for (const void* v : vec)
+    DABSN_REQUIRE((reinterpret_cast<uintptr_t>(v) & 15u) == 0,
+                  "read3 decode: q, bank and out must be 16-byte aligned");
+  const DecodePlan p = decode_plan(dtype, B, T, N, H);
+  DABSN_REQUIRE(workspace_bytes >= p.end, "read3 decode: workspace %zu < %zu", workspace_bytes,
+                p.end);
+  Gains g{{gains[0], gains[1], gains[2], gains[3]}};
+  if (dtype == kBF16)
+    return decode_impl<bf16>(B, T, N, H, bank_len, bank_ld, (const bf16*)q, (const bf16*)bank,
+                             norm_w, idx, next_idx, read_idx, valid, cocktail, bank_cocktail,
+                             key_bias, admission, scale, g, (bf16*)out, (uint8_t*)workspace, p,
+                             stream);
+  return decode_impl<float>(B, T, N, H, bank_len, bank_ld, (const float*)q, (const float*)bank,
+                            norm_w, idx, next_idx, read_idx, valid, cocktail, bank_cocktail,
+                            key_bias, admission, scale, g, (float*)out, (uint8_t*)workspace, p,
+                            stream);
 }
 
 }  // extern "C"

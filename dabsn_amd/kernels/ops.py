@@ -738,6 +738,48 @@ def _read_fake(query, *rest):
     return torch.empty_like(query)
 
 
+def read3_decode(query: Tensor, bank_write: Tensor, norm_w: Tensor, idx: Tensor,
+                 next_idx: Tensor, read_idx: Tensor, valid: Tensor, cocktail: Tensor,
+                 bank_cocktail: Tensor, bank_key_bias: Tensor, bank_admission: Tensor,
+                 scale: Tensor, gains: tuple[Tensor, Tensor, Tensor, Tensor]) -> Tensor:
+    """The seq three-way read of a few query rows (T <= 8) against a bank read in place
+    (inference only; no autograd). Equals bank_gather followed by
+    admitted_three_way_read_compact_flash in mode 0 up to the summation order of the dot
+    products and of the slot sum.
+
+    ``bank_write`` [B, N_bank, H] may be a view of a longer per-row buffer (unit stride over
+    H, rows H apart); ``norm_w`` [B, N_bank] are its write norms; ``idx`` / ``next_idx``
+    [B, N] address the bank, ``read_idx`` [B, N] are the query-relative slot indices the
+    masks use. ``gains`` = (short, pad, induct, cocktail)."""
+    _require_cuda(query)
+    lib = _lib.load()
+    dt = query.dtype
+    q = query.contiguous()
+    B, T, H = q.shape
+    N = idx.shape[1]
+    if bank_write.dtype != dt or bank_write.stride(2) != 1 or bank_write.stride(1) != H \
+            or bank_write.stride(0) % H != 0:
+        raise ValueError("read3_decode: bank_write must be rows of H contiguous elements")
+    bank_len, bank_ld = int(bank_write.shape[1]), int(bank_write.stride(0) // H)
+    nw = norm_w.float().contiguous()
+    ic, nc, rc = (x.to(torch.int64).contiguous() for x in (idx, next_idx, read_idx))
+    vc = valid.to(torch.uint8).contiguous()
+    ck, cb, kb, adm = (x.float().contiguous() for x in (cocktail, bank_cocktail, bank_key_bias,
+                                                       bank_admission))
+    sc = scale.float().reshape(()).contiguous()
+    g = [x.float().reshape(()).contiguous() for x in gains]
+    out = torch.empty_like(q)
+    code = _code(dt)
+    nbytes = lib.dabsn_hip_read3_decode_workspace_bytes(code, B, T, N, H)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
+    _lib.check(lib.dabsn_hip_read3_decode(code, B, T, N, H, _p(q), _p(bank_write), bank_len,
+                                          bank_ld, _p(nw), _p(ic), _p(nc), _p(rc), _p(vc),
+                                          _p(ck), _p(cb), _p(kb), _p(adm), _p(sc), ptrs, _p(out),
+                                          _p(ws), ws.numel(), _stream(q)), "three-way decode read")
+    return out
+
+
 CompactGradients = tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
                          Tensor, Tensor, Tensor, Tensor]
 

@@ -111,17 +111,29 @@ class DABSNRead(nn.Module):
                    query_start: int):
         n_max, idx, valid, next_idx, rank = self._select(admission, length)
         self.last_n_max = n_max
-        K, V, Vn = ops.bank_gather(bank_write, norm_w, idx, next_idx, rank)
         bank_cocktail = torch.gather(cocktail[1], 1, idx.unsqueeze(-1).expand(-1, -1, 4))
         bank_bias = torch.gather(key_bias, 1, idx)
         bank_adm = torch.gather(admission, 1, idx)
         scale = (F.softplus(self.short_read.log_temp) + 1.0) * (self.hidden_dim ** 0.5)
         read_idx = idx if query_start == 0 else idx - query_start
-        retrieved = ops.admitted_three_way_read_compact_flash(
-            query, K, V, Vn, cocktail[0], bank_cocktail, bank_bias, bank_adm, scale, read_idx, valid,
-            0, self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain)
+        hidden = int(query.shape[-1])
+        # A few query rows without autograd (streaming decode): read the bank in place
+        # instead of gathering K, V, Vn copies of the admitted slots.
+        decode = (not torch.is_grad_enabled() and query.is_cuda and int(query.shape[1]) <= 8
+                  and hidden % 8 == 0 and bank_write.stride(-1) == 1
+                  and bank_write.stride(1) == hidden and bank_write.stride(0) % hidden == 0)
+        if decode:
+            retrieved = ops.read3_decode(
+                query, bank_write, norm_w, idx, next_idx, read_idx, valid, cocktail[0],
+                bank_cocktail, bank_bias, bank_adm, scale,
+                (self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain))
+        else:
+            K, V, Vn = ops.bank_gather(bank_write, norm_w, idx, next_idx, rank)
+            retrieved = ops.admitted_three_way_read_compact_flash(
+                query, K, V, Vn, cocktail[0], bank_cocktail, bank_bias, bank_adm, scale, read_idx,
+                valid, 0, self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain)
         self.last_read_contract = {
-            "read_strategy": "rocm_compact_admitted_bank",
+            "read_strategy": "rocm_decode_bank_in_place" if decode else "rocm_compact_admitted_bank",
             "exact": True,
             "max_admitted_bank": int(n_max),
             "bank_growth": "grows_with_T" if n_max >= length else "data_dependent",

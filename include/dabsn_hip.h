@@ -237,6 +237,29 @@ int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
                         float* gkey_bias, float* gadmission, float* gscalars5, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
 
+/* Decode read: the forward of dabsn_hip_read3_fwd (mode 0, seq) for a few query rows
+ * (T <= 8) against a long bank, reading the bank in place instead of from gathered K, V,
+ * Vn copies. Replaces bank gather + three-way read on the streaming path of the carried
+ * memory (src/dabsn/memory.py:215-290 -> read.py:650-838), where the bank is a growing
+ * buffer: bank [B, bank_ld, H] in `dtype` with the first bank_len positions per batch row
+ * live (bank_ld >= bank_len), norm_w [B, bank_len] fp32 write norms, idx / next_idx
+ * [B, N] int64 bank positions of the admitted slots and their successors (addressing),
+ * read_idx [B, N] int64 the slots' query-relative indices (masks: allow read_idx <= t,
+ * induction read_idx < t), valid [B, N] uint8; the other arguments as in
+ * dabsn_hip_read3_fwd. K = normalize(write) is rounded to `dtype` as the gather stores
+ * it. H % 8 == 0; q, bank and out 16-byte aligned; T * H * sizeof(dtype) <= 64 KiB.
+ * Inference only: there is no backward. */
+size_t dabsn_hip_read3_decode_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t N,
+                                              int64_t H);
+int dabsn_hip_read3_decode(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* q,
+                           const void* bank, int64_t bank_len, int64_t bank_ld,
+                           const float* norm_w, const int64_t* idx, const int64_t* next_idx,
+                           const int64_t* read_idx, const uint8_t* valid, const float* cocktail,
+                           const float* bank_cocktail, const float* key_bias,
+                           const float* admission, const float* scale,
+                           const float* const* gains, void* out, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -428,3 +428,50 @@ def test_chunked_core_scan_matches_full_op(cuda_device, dtype, B, T, H, chunk, t
         if a is not None:
             err = rel_fro(a.float().cpu(), b.float().cpu())
             assert err <= tol, f"input {i}: {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype,T", [(torch.float32, 1), (torch.float32, 3), (torch.bfloat16, 1),
+                                     (torch.bfloat16, 3)])
+def test_read3_decode_matches_gather_and_read(cuda_device, dtype, T):
+    """The decode read (bank read in place through idx and a row stride) against bank gather
+    + the three-way read on the same inputs: the bank is the first 40 positions of a
+    64-position buffer, queries sit at the end of it (query_start = 40 - T), rows admit
+    different slot counts. fp32: normwise 1e-5 (dot products and the slot sum are summed in
+    another order). bf16: P_V, P_Vn and K are rounded to bf16 on both sides, so an order
+    difference can move a rounding; Frobenius 5e-3."""
+    g = torch.Generator().manual_seed(77)
+    B, H, cap, Nb = 3, 64, 64, 40
+    qs = Nb - T
+    buf = torch.randn(B, cap, H, generator=g).to(dtype)
+    bank = buf.to(cuda_device)[:, :Nb]
+    counts = [Nb, 23, 9]
+    n = max(counts)
+    idx = torch.zeros(B, n, dtype=torch.int64)
+    for b in range(B):
+        perm = torch.randperm(Nb, generator=g)
+        chosen = torch.sort(perm[:counts[b]]).values
+        rest = torch.sort(perm[counts[b]:]).values
+        idx[b] = torch.cat([chosen, rest])[:n]
+    valid = (torch.arange(n).unsqueeze(0) < torch.tensor(counts).unsqueeze(1)).to(torch.uint8)
+    next_idx = (idx + 1).clamp(max=Nb - 1)
+    read_idx = idx - qs
+    norm_w = bank.float().norm(dim=-1).cpu() * (0.5 + torch.rand(B, Nb, generator=g))
+    q = F.normalize(torch.randn(B, T, H, generator=g), dim=-1).to(dtype)
+    ck = F.normalize(torch.randn(B, T, 4, generator=g), dim=-1)
+    cb = F.normalize(torch.randn(B, n, 4, generator=g), dim=-1)
+    kb, adm = 0.3 * torch.randn(B, n, generator=g), 0.3 * torch.randn(B, n, generator=g)
+    scale = torch.tensor(2.5)
+    gains = tuple(torch.tensor(v) for v in (1.0, 0.7, 0.2, 0.9))
+    d = lambda x: x.to(cuda_device)  # noqa: E731
+    with torch.no_grad():
+        got = ops.read3_decode(d(q), bank, d(norm_w), d(idx), d(next_idx), d(read_idx), d(valid),
+                               d(ck), d(cb), d(kb), d(adm), d(scale), tuple(d(x) for x in gains))
+        rank = torch.zeros(B, Nb, dtype=torch.int32, device=cuda_device)
+        K, V, Vn = ops.bank_gather(bank.contiguous(), d(norm_w), d(idx), d(next_idx), rank)
+        want = ops.admitted_three_way_read_compact_flash(
+            d(q), K, V, Vn, d(ck), d(cb), d(kb), d(adm), d(scale), d(read_idx), d(valid), 0,
+            *(d(x) for x in gains))
+    if dtype == torch.float32:
+        assert rel_err(got.cpu(), want.cpu()) <= 1e-5
+    else:
+        assert rel_fro(got.float().cpu(), want.float().cpu()) <= 5e-3
