@@ -710,36 +710,53 @@ __global__ void __launch_bounds__(256) decode_score_kernel(int T, int N, int H, 
           *reinterpret_cast<const u32x4*>(q + static_cast<size_t>(b) * T * H + c * 8 + 4);
   }
   __syncthreads();
-  for (int k = 0; k < kDecodeSlotsPerBlock / 4; ++k) {
-    const int j = blockIdx.x * kDecodeSlotsPerBlock + wave * (kDecodeSlotsPerBlock / 4) + k;
-    if (j >= N) break;  // wave-uniform
+  // The wave's slots are processed together so their row loads are in flight at once;
+  // slots past N read the last slot's row and are not stored.
+  constexpr int KW = kDecodeSlotsPerBlock / 4;
+  const int jw = blockIdx.x * kDecodeSlotsPerBlock + wave * KW;
+  if (jw >= N) return;  // wave-uniform; no barrier follows
+  const E* row[KW];
+  float n[KW];
+#pragma unroll
+  for (int k = 0; k < KW; ++k) {
+    const int j = min(jw + k, N - 1);
     const int64_t i = idx[static_cast<size_t>(b) * N + j];
-    const E* row = bank_row(bank, b, rowld, Nb, i, H);
     const int64_t ic = i < 0 ? 0 : (i >= Nb ? Nb - 1 : i);
-    const float n = fmaxf(norm_w[static_cast<size_t>(b) * Nb + ic], kNormEps);
-    float acc[kDecodeRows];
+    row[k] = bank_row(bank, b, rowld, Nb, i, H);
+    n[k] = fmaxf(norm_w[static_cast<size_t>(b) * Nb + ic], kNormEps);
+  }
+  float acc[KW][kDecodeRows];
 #pragma unroll
-    for (int t = 0; t < kDecodeRows; ++t) acc[t] = 0.0f;
-    for (int c = lane; c < nch; c += 64) {
-      float v[8];
-      ldv<E, 8>(row + c * 8, v);
+  for (int k = 0; k < KW; ++k)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = round_to<E>(v[e] / n);
+    for (int t = 0; t < kDecodeRows; ++t) acc[k][t] = 0.0f;
+  for (int c = lane; c < nch; c += 64) {
+    float v[KW][8];
 #pragma unroll
-      for (int t = 0; t < kDecodeRows; ++t) {
-        if (t < T) {
-          float qv[8];
-          ldv<E, 8>(qs + (t * nch + c) * 8, qv);
+    for (int k = 0; k < KW; ++k) ldv<E, 8>(row[k] + c * 8, v[k]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[t] += qv[e] * v[e];
-        }
-      }
-    }
+    for (int k = 0; k < KW; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[k][e] = round_to<E>(v[k][e] / n[k]);  // K as gathered
 #pragma unroll
     for (int t = 0; t < kDecodeRows; ++t) {
       if (t < T) {
-        const float sum = wave_sum(acc[t]);
-        if (lane == 0) S[(static_cast<size_t>(b) * T + t) * N + j] = sum;
+        float qv[8];
+        ldv<E, 8>(qs + (t * nch + c) * 8, qv);
+#pragma unroll
+        for (int k = 0; k < KW; ++k)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[k][t] += qv[e] * v[k][e];
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < KW; ++k) {
+#pragma unroll
+    for (int t = 0; t < kDecodeRows; ++t) {
+      if (t < T) {
+        const float sum = wave_sum(acc[k][t]);
+        if (lane == 0 && jw + k < N) S[(static_cast<size_t>(b) * T + t) * N + jw + k] = sum;
       }
     }
   }
@@ -767,17 +784,31 @@ __global__ void __launch_bounds__(256) decode_out_kernel(int T, int N, int H, in
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[t][e] = 0.0f;
   const size_t prow = static_cast<size_t>(b) * T * N;
-  for (int j = j0; j < j1; ++j) {
-    float v[8], vn[8];
-    ldv<E, 8>(bank_row(bank, b, rowld, Nb, idx[static_cast<size_t>(b) * N + j], H) + h0, v);
-    ldv<E, 8>(bank_row(bank, b, rowld, Nb, next_idx[static_cast<size_t>(b) * N + j], H) + h0, vn);
+  // Slots are taken U at a time so their 2U row loads are in flight together; the slots
+  // in a group are summed in order, as in the one-at-a-time loop.
+  constexpr int U = 4;
+  for (int jb = j0; jb < j1; jb += U) {
+    float v[U][8], vn[U][8];
 #pragma unroll
-    for (int t = 0; t < kDecodeRows; ++t) {
-      if (t < T) {
-        const float pv = ld(PV, prow + static_cast<size_t>(t) * N + j);
-        const float pn = ld(PVn, prow + static_cast<size_t>(t) * N + j);
+    for (int u = 0; u < U; ++u) {
+      const int j = min(jb + u, j1 - 1);
+      ldv<E, 8>(bank_row(bank, b, rowld, Nb, idx[static_cast<size_t>(b) * N + j], H) + h0, v[u]);
+      ldv<E, 8>(bank_row(bank, b, rowld, Nb, next_idx[static_cast<size_t>(b) * N + j], H) + h0,
+                vn[u]);
+    }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[t][e] += pv * v[e] + pn * vn[e];
+    for (int u = 0; u < U; ++u) {
+      if (jb + u < j1) {
+        const int j = jb + u;
+#pragma unroll
+        for (int t = 0; t < kDecodeRows; ++t) {
+          if (t < T) {
+            const float pv = ld(PV, prow + static_cast<size_t>(t) * N + j);
+            const float pn = ld(PVn, prow + static_cast<size_t>(t) * N + j);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[t][e] += pv * v[u][e] + pn * vn[u][e];
+          }
+        }
       }
     }
   }
