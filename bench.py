@@ -36,7 +36,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--batch", type=int, default=16)
+    p.add_argument("--batch", type=int, default=None, help="default 16 (train), 256 (decode)")
     p.add_argument("--seq", type=int, default=4096)
     p.add_argument("--state", type=int, default=2048)
     p.add_argument("--hidden", type=int, default=4096)
@@ -44,7 +44,15 @@ def parse():
     p.add_argument("--chunk", type=int, default=1024)
     p.add_argument("--cpu-seq", type=int, default=128, help="T of the bounded CPU sample")
     p.add_argument("--no-cpu", action="store_true")
-    return p.parse_args()
+    p.add_argument("--workload", choices=("train", "decode"), default="train",
+                   help="train: the config-4 headline step (default); decode: config-5 streaming "
+                        "decode through the carried memory")
+    p.add_argument("--prompt", type=int, default=2048, help="decode: prompt tokens ingested")
+    p.add_argument("--layers", type=int, default=4, help="decode: seq layers")
+    args = p.parse_args()
+    if args.batch is None:
+        args.batch = 256 if args.workload == "decode" else 16
+    return args
 
 
 class ScanRead(torch.nn.Module):
@@ -178,6 +186,80 @@ def cpu_baseline(args):
     }
 
 
+DECODE_METRIC = "decode tokens/sec (B x steps), config 5: 4 seq layers 2048/2048, prompt 2048"
+
+
+def decode_main(args):
+    """Config 5: DABSNSequenceLM(vocab 32000, hidden 2048, 4 x
+    seq 2048/2048, residual, MLP ratio 4.0) in bf16, B=256 (pass --batch 256). A prompt of
+    --prompt random tokens is ingested in chunks of 512 (``dabsn_amd.ingest``), the banks are
+    reserved for the whole run, then each timed step decodes one token per row with
+    ``forward_with_memory(extend=True)``: the core steps from the carried state, the read
+    scans each layer's bank in place (``dabsn_hip_read3_decode``) and the bank grows by one
+    row. value = B x steps / time."""
+    import dabsn_amd
+    from dabsn_amd import memory as mem
+    from dabsn_amd.kernels import ops
+
+    dabsn_amd.kernels.enable("rocm", required=True)
+    os.environ.setdefault("DABSN_HIP_ERROR_CHECK", "deferred")
+    device = torch.device("cuda:0")
+    H, B, L = args.state, args.batch, args.layers
+    torch.manual_seed(0)
+    model = dabsn_amd.DABSNSequenceLM(args.vocab, H, [(H, H)] * L, residual=True, mlp_ratio=4.0)
+    model = model.to(device).to(torch.bfloat16).eval()
+    total = args.prompt + args.warmup + args.steps
+    ids = torch.randint(0, args.vocab, (B, total), generator=torch.Generator().manual_seed(1))
+    ids = ids.to(device)
+    memory = mem.ingest(model, ids[:, :args.prompt], chunk_size=512)
+    memory.reserve(total)
+    pos = args.prompt
+    for _ in range(args.warmup):
+        _, memory = mem.forward_with_memory(model, ids[:, pos:pos + 1], memory, extend=True)
+        pos += 1
+    torch.cuda.synchronize()
+    ops.timing(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        _, memory = mem.forward_with_memory(model, ids[:, pos:pos + 1], memory, extend=True)
+        pos += 1
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    kernels = ops.KernelTimer.summary()
+    ops.timing(False)
+    ops.check_errors()
+    n_mean = args.prompt + args.warmup + (args.steps + 1) / 2  # bank rows per layer, mean
+    bank_bytes = B * n_mean * H * 2  # one pass over one layer's bank
+    dec = kernels.get("read3_decode")
+    roofline = None
+    if dec:
+        # The decode read passes over the bank rows of the admitted slots twice (scores, then
+        # the P V output whose successor rows are mostly the next slot's): algorithmic bytes =
+        # one bank pass per launch when every slot is admitted.
+        achieved = bank_bytes / (dec["avg_ms"] / 1e3) / 1e9
+        roofline = {"bound": "hbm", "kernel": "read3_decode", "achieved": round(achieved, 2),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                    "traffic": None, "alg_bytes_per_launch": int(bank_bytes),
+                    "avg_launch_ms": round(dec["avg_ms"], 4)}
+    result = {
+        "metric": DECODE_METRIC, "value": round(B * 1e3 / ms, 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: uniform random token ids, random-init weights",
+        "config": {"workload": "config5 streaming decode: 4 seq layers 2048/2048, MLP 4.0, "
+                               "vocab 32000, prompt ingested in chunks of 512",
+                   "batch": B, "prompt": args.prompt, "layers": L, "state": H,
+                   "bank_rows_mean": n_mean},
+        "roofline": roofline,
+        "kernel_ms": {k: {"avg": round(v["avg_ms"], 4), "calls_per_step": v["calls"] / args.steps,
+                          "per_step": round(v["total_ms"] / args.steps, 3)}
+                      for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["total_ms"])},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -190,6 +272,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
+    if args.workload == "decode":
+        decode_main(args)
+        return
     dabsn_amd.kernels.enable("rocm", required=True)
     os.environ.setdefault("DABSN_HIP_ERROR_CHECK", "deferred")
     device = torch.device("cuda:0")

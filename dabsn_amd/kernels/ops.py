@@ -773,10 +773,12 @@ def read3_decode(query: Tensor, bank_write: Tensor, norm_w: Tensor, idx: Tensor,
     nbytes = lib.dabsn_hip_read3_decode_workspace_bytes(code, B, T, N, H)
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
     ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
+    tk = KernelTimer.begin("read3_decode", q)
     _lib.check(lib.dabsn_hip_read3_decode(code, B, T, N, H, _p(q), _p(bank_write), bank_len,
                                           bank_ld, _p(nw), _p(ic), _p(nc), _p(rc), _p(vc),
                                           _p(ck), _p(cb), _p(kb), _p(adm), _p(sc), ptrs, _p(out),
                                           _p(ws), ws.numel(), _stream(q)), "three-way decode read")
+    KernelTimer.end(tk)
     return out
 
 
