@@ -192,10 +192,12 @@ def _block_step(block: DABSNBlock, inputs: Tensor, layer: LayerMemory | None,
         bank = layer.bank
     bank.append(write, stats)
     bank_write, bank_stats = bank.live()
+    # Decode-sized steps read at the full bank width (no host sync per layer and token).
+    width = bank.length if int(inputs.shape[1]) <= 8 else None
     retrieved, final_long = block.read.forward_query_bank_stats(
         y, budget, expression, write, plasticity, query_stats=stats, bank_write=bank_write,
         bank_stats=bank_stats, query_start=position,
-        initial_long_state=None if layer is None else layer.long)
+        initial_long_state=None if layer is None else layer.long, bank_width=width)
     out = block.finish(inputs, block.state_to_hidden(y + block.read_gain * retrieved))
     return block.forward_mlp(out), LayerMemory(bank=bank, core=final_core, long=final_long)
 

@@ -95,11 +95,13 @@ class DABSNRead(nn.Module):
         self._capture_bank_width: int | None = None
 
     # ---- selection ------------------------------------------------------------
-    def _select(self, admission: Tensor, length: int):
+    def _select(self, admission: Tensor, length: int, width: int | None = None):
         window = F.softplus(self.admit_window)
         order, counts, rank = ops.bank_select(admission.detach(), window.detach())
-        if self._capture_bank_width:
-            n_max = max(1, min(int(self._capture_bank_width), length))
+        if width or self._capture_bank_width:
+            # A fixed width needs no host sync; slots past a row's admitted count are
+            # masked out by `valid`.
+            n_max = max(1, min(int(width or self._capture_bank_width), length))
         else:
             n_max = max(int(counts.max().item()), 1)  # host sync, as read.py:233
         idx = order[:, :n_max]
@@ -108,8 +110,8 @@ class DABSNRead(nn.Module):
         return n_max, idx, valid, next_idx, rank
 
     def _read_core(self, query, cocktail, bank_write, norm_w, key_bias, admission, length: int,
-                   query_start: int):
-        n_max, idx, valid, next_idx, rank = self._select(admission, length)
+                   query_start: int, width: int | None = None):
+        n_max, idx, valid, next_idx, rank = self._select(admission, length, width)
         self.last_n_max = n_max
         bank_cocktail = torch.gather(cocktail[1], 1, idx.unsqueeze(-1).expand(-1, -1, 4))
         bank_bias = torch.gather(key_bias, 1, idx)
@@ -230,7 +232,7 @@ class DABSNRead(nn.Module):
 
     def forward_query_bank_stats(self, y, budget, expression, write, plasticity, *,
                                  query_stats, bank_write, bank_stats, query_start: int,
-                                 initial_long_state=None):
+                                 initial_long_state=None, bank_width: int | None = None):
         """forward_query_bank with the bank given as its write vectors plus per-position
         statistics instead of full-width tapes.
 
@@ -241,7 +243,8 @@ class DABSNRead(nn.Module):
         plasticity, the query norm and the write norm ([B, N, 6] fp32). Those are the rows
         one dense pass computes for the same positions, so this is the dense read.
         ``query_stats`` are the rows of the query chunk itself (which the caller has
-        already appended to the bank, ending at ``query_start + T``).
+        already appended to the bank, ending at ``query_start + T``). ``bank_width`` fixes
+        the slot-list width (no host sync for the admitted count).
 
         Returns (output, final long state)."""
         rp = self.short_read
@@ -256,7 +259,7 @@ class DABSNRead(nn.Module):
         admission = rp.admission_from_means(be, bc, bn, bp, hidden)
         cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
         retrieved = self._read_core(query, cocktails, bank_write, bank_stats[..., 5].detach(),
-                                    key_bias, admission, bank_len, int(query_start))
+                                    key_bias, admission, bank_len, int(query_start), bank_width)
         short_output = rp.project(y, budget, retrieved.to(y.dtype))
         long, final_state = self._long_scan_from_state(write, plasticity, None,
                                                        initial_state=initial_long_state,
