@@ -26,7 +26,8 @@ Only seq read geometry is supported, as in the reference (memory.py:184-196).
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Iterator
+from pathlib import Path
+from typing import Iterator, Mapping, Sequence
 
 import torch
 from torch import Tensor
@@ -35,7 +36,16 @@ from .kernels import ops
 from .model import DABSNBlock, DABSNSequenceLM
 
 __all__ = ["BankStore", "LayerMemory", "DABSNMemory", "ingest", "forward_with_memory",
-           "fingerprint_of"]
+           "fingerprint_of", "save", "load", "embed_in_checkpoint", "extract_from_checkpoint",
+           "memory_cost"]
+
+#: File format tag and bank field names of the reference's memory files (memory.py:55-87).
+FORMAT = "dabsn_memory_v1"
+MEAN_FIELDS = ("novelty", "plasticity", "energy", "saturation")
+BANK_FIELDS = ("write",) + tuple(f"{name}_mean" for name in MEAN_FIELDS)
+# Column of each mean in a read_tape_stats row: (energy, saturation, novelty, plasticity,
+# query norm, write norm).
+_STATS_COLUMN = {"energy": 0, "saturation": 1, "novelty": 2, "plasticity": 3}
 
 
 class BankStore:
@@ -110,6 +120,13 @@ class LayerMemory:
         return self.bank.nbytes() + sum(t.numel() * t.element_size()
                                         for t in (*self.core, *self.long))
 
+    def to(self, *, device=None, dtype=None) -> "LayerMemory":
+        """A copy on ``device``; ``dtype`` applies to the bank's write vectors (the
+        statistics and the carried core and long states stay fp32)."""
+        return LayerMemory(bank=self.bank.to(device=device, dtype=dtype),
+                           core=tuple(t.to(device=device) for t in self.core),
+                           long=tuple(t.to(device=device) for t in self.long))
+
 
 @dataclass
 class DABSNMemory:
@@ -127,6 +144,11 @@ class DABSNMemory:
 
     def nbytes(self) -> int:
         return sum(layer.nbytes() for layer in self.layers)
+
+    def to(self, device=None, dtype=None) -> "DABSNMemory":
+        return DABSNMemory(layers=[layer.to(device=device, dtype=dtype) for layer in self.layers],
+                           position=self.position, batch_size=self.batch_size,
+                           fingerprint=dict(self.fingerprint))
 
     def reserve(self, tokens: int) -> None:
         """Preallocate every bank for ``tokens`` positions in total (no regrowth below it)."""
@@ -258,3 +280,142 @@ def forward_with_memory(model: DABSNSequenceLM, ids: Tensor, memory: DABSNMemory
     if return_hidden:
         return hidden, result
     return model.readout(hidden), result
+
+
+# ---- files ----------------------------------------------------------------------------
+def _to_payload(memory: DABSNMemory) -> dict[str, object]:
+    """The reference's payload (memory.py:389-403): per layer the five bank fields, core and
+    long. The bank also carries ``stats``, the fp32 rows this package reads, so its own
+    round trip is exact; the reference's loader takes only its five fields."""
+    layers = []
+    for layer in memory.layers:
+        write, stats = layer.bank.live()
+        bank = {"write": write.detach().cpu()}
+        for name in MEAN_FIELDS:
+            bank[f"{name}_mean"] = stats[..., _STATS_COLUMN[name]].detach().cpu().to(write.dtype)
+        bank["stats"] = stats.detach().cpu()
+        layers.append({"bank": bank, "core": [t.detach().cpu() for t in layer.core],
+                       "long": [t.detach().cpu() for t in layer.long]})
+    return {"format": FORMAT, "position": int(memory.position),
+            "batch_size": int(memory.batch_size), "fingerprint": dict(memory.fingerprint),
+            "layers": layers}
+
+
+def _from_payload(payload) -> DABSNMemory:
+    if not isinstance(payload, Mapping) or payload.get("format") != FORMAT:
+        fmt = payload.get("format") if isinstance(payload, Mapping) else type(payload).__name__
+        raise ValueError(f"not a DABSN memory payload: format={fmt!r}, expected {FORMAT!r}")
+    raw_layers = payload.get("layers")
+    if not isinstance(raw_layers, Sequence):
+        raise ValueError("memory payload layers must be a sequence")
+    layers = []
+    for entry in raw_layers:
+        bank = entry.get("bank") if isinstance(entry, Mapping) else None
+        if not isinstance(bank, Mapping):
+            raise ValueError("memory payload layer bank must be an object")
+        missing = [k for k in BANK_FIELDS if k not in bank]
+        if missing:
+            raise ValueError(f"memory payload is missing bank fields: {missing}")
+        core, long = entry.get("core"), entry.get("long")
+        if not (isinstance(core, Sequence) and len(core) == 3 and isinstance(long, Sequence)
+                and len(long) == 3):
+            raise ValueError("memory payload core and long states must hold three tensors each")
+        write = bank["write"]
+        if not isinstance(write, Tensor) or write.dim() != 3:
+            raise ValueError("memory payload bank write must be a [B, N, H] tensor")
+        stats = bank.get("stats")
+        if not isinstance(stats, Tensor):
+            # A file written by the reference: the means are stored, the write norms are not.
+            stats = torch.zeros(*write.shape[:2], 6, dtype=torch.float32)
+            for name in MEAN_FIELDS:
+                stats[..., _STATS_COLUMN[name]] = bank[f"{name}_mean"].float()
+            stats[..., 5] = torch.linalg.vector_norm(write.float(), dim=-1)
+        store = BankStore(write.shape[0], write.shape[2], device=write.device, dtype=write.dtype,
+                          capacity=write.shape[1])
+        store.append(write, stats.float())
+        layers.append(LayerMemory(bank=store, core=tuple(t.float() for t in core),
+                                  long=tuple(t.float() for t in long)))
+    return DABSNMemory(layers=layers, position=int(payload["position"]),
+                       batch_size=int(payload["batch_size"]),
+                       fingerprint=dict(payload.get("fingerprint") or {}))
+
+
+def _check_loaded(memory: DABSNMemory, model: DABSNSequenceLM) -> None:
+    """Architecture check for a loaded memory: the identity fields both packages record
+    (vocab, width, depth) must match the model, and each bank's width must be a block's
+    state width."""
+    want = fingerprint_of(model)
+    for key in ("vocab", "hidden_dim", "depth"):
+        if key in memory.fingerprint and memory.fingerprint[key] != want[key]:
+            raise ValueError(f"memory was built by a different architecture: {key}: "
+                             f"memory={memory.fingerprint[key]!r} model={want[key]!r}")
+    blocks = list(model.blocks)
+    if len(memory.layers) != len(blocks) or any(
+            layer.bank.hidden != int(block.state_dim) for layer, block in zip(memory.layers, blocks)):
+        raise ValueError("memory layers do not match the model's blocks")
+    memory.fingerprint = want
+
+
+def save(memory: DABSNMemory, path) -> Path:
+    """Write ``memory`` to its own file (memory.py:461-466)."""
+    destination = Path(path)
+    destination.parent.mkdir(parents=True, exist_ok=True)
+    torch.save(_to_payload(memory), destination)
+    return destination
+
+
+def load(path, *, model: DABSNSequenceLM | None = None, map_location="cpu", device=None,
+         dtype=None) -> DABSNMemory:
+    """Read a memory file (memory.py:469-491), written by this package or by the reference.
+    The file is read with ``weights_only=True``: a payload of tensors, numbers, strings,
+    lists and dicts, nothing executed. With ``model`` it is checked against the model and
+    moved to its device, the bank's writes cast to its dtype."""
+    payload = torch.load(Path(path), map_location=map_location, weights_only=True)
+    if isinstance(payload, Mapping) and "dabsn_memory" in payload:
+        payload = payload["dabsn_memory"]
+    memory = _from_payload(payload)
+    if model is not None:
+        _check_loaded(memory, model)
+        ref = next(model.parameters())
+        memory = memory.to(device=device or ref.device, dtype=dtype or ref.dtype)
+    elif device is not None or dtype is not None:
+        memory = memory.to(device=device, dtype=dtype)
+    return memory
+
+
+def embed_in_checkpoint(memory: DABSNMemory, checkpoint, *, destination=None) -> Path:
+    """Attach ``memory`` to a dict checkpoint under ``dabsn_memory`` (memory.py:494-514)."""
+    source = Path(checkpoint)
+    target = Path(destination) if destination is not None else source
+    payload = torch.load(source, map_location="cpu", weights_only=True)
+    if not isinstance(payload, dict):
+        raise ValueError(f"can only embed memory into a dict checkpoint; {source} holds "
+                         f"{type(payload).__name__}")
+    payload["dabsn_memory"] = _to_payload(memory)
+    torch.save(payload, target)
+    return target
+
+
+def extract_from_checkpoint(checkpoint, *, model: DABSNSequenceLM | None = None,
+                            map_location="cpu") -> DABSNMemory | None:
+    """The memory embedded in a checkpoint, or None (memory.py:517-532)."""
+    payload = torch.load(Path(checkpoint), map_location=map_location, weights_only=True)
+    if not isinstance(payload, dict) or "dabsn_memory" not in payload:
+        return None
+    memory = _from_payload(payload["dabsn_memory"])
+    if model is not None:
+        _check_loaded(memory, model)
+        ref = next(model.parameters())
+        memory = memory.to(device=ref.device, dtype=ref.dtype)
+    return memory
+
+
+def memory_cost(model: DABSNSequenceLM, tokens: int, *, batch_size: int = 1,
+                bytes_per_element: int = 2) -> dict[str, object]:
+    """Bank bytes for ``tokens`` ingested tokens (memory.py:535-549, with this package's
+    layout: per layer one write vector in the activation dtype plus a six-float statistics
+    row per position)."""
+    per_token = sum(int(block.state_dim) * bytes_per_element + 6 * 4 for block in model.blocks)
+    total = per_token * tokens * batch_size
+    return {"bytes_per_token": per_token * batch_size, "total_bytes": total,
+            "total_mib": total / 1024 / 1024}

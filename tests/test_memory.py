@@ -129,3 +129,59 @@ def test_chunked_ingest_equals_dense_pass_gpu(cuda_device):
 def test_decode_token_by_token_equals_dense_pass_gpu(cuda_device):
     got, want = _decode(cuda_device)
     assert rel_err(got.cpu(), want.cpu()) <= 1e-5
+
+
+def _continue(model, memory, ids):
+    out = []
+    for t in range(ids.shape[1]):
+        step, memory = mem.forward_with_memory(model, ids[:, t:t + 1], memory, extend=True)
+        out.append(step)
+    return torch.cat(out, dim=1), memory
+
+
+def test_saved_memory_reloads_and_continues_exactly_cpu(tmp_path):
+    """save -> load (weights_only) -> decode equals decoding the memory that was saved."""
+    model = _model("cpu")
+    ids = _ids(2, 24)
+    memory = mem.ingest(model, ids[:, :18], chunk_size=7)
+    path = mem.save(memory, tmp_path / "ctx.dmem")
+    loaded = mem.load(path, model=model)
+    assert loaded.position == 18 and loaded.entries == 18 and loaded.batch_size == 2
+    a, _ = _continue(model, memory, ids[:, 18:])
+    b, _ = _continue(model, loaded, ids[:, 18:])
+    assert torch.equal(a, b)
+
+
+def test_reference_format_file_loads_cpu(tmp_path):
+    """A file in the reference's payload (five bank fields, no statistics rows): the means
+    come from the file and the write norms are recomputed, so decoding continues to fp32
+    rounding of the norms (1e-5)."""
+    model = _model("cpu")
+    ids = _ids(2, 24, seed=11)
+    memory = mem.ingest(model, ids[:, :18], chunk_size=9)
+    payload = mem._to_payload(memory)
+    for layer in payload["layers"]:
+        del layer["bank"]["stats"]
+        for k in mem.MEAN_FIELDS:  # the reference stores the means in the tape dtype
+            layer["bank"][f"{k}_mean"] = layer["bank"][f"{k}_mean"].float()
+    torch.save(payload, tmp_path / "ref.dmem")
+    loaded = mem.load(tmp_path / "ref.dmem", model=model)
+    a, _ = _continue(model, memory, ids[:, 18:])
+    b, _ = _continue(model, loaded, ids[:, 18:])
+    assert rel_err(b, a) <= 1e-5
+
+
+def test_memory_embeds_in_checkpoint_and_rejects_foreign_payload_cpu(tmp_path):
+    model = _model("cpu")
+    memory = mem.ingest(model, _ids(2, 10), chunk_size=None)
+    ckpt = tmp_path / "model.pt"
+    torch.save({"state_dict": model.state_dict()}, ckpt)
+    assert mem.extract_from_checkpoint(ckpt) is None
+    mem.embed_in_checkpoint(memory, ckpt)
+    back = mem.extract_from_checkpoint(ckpt, model=model)
+    assert back is not None and back.position == 10
+    assert torch.equal(back.layers[0].bank.live()[0], memory.layers[0].bank.live()[0])
+    assert "state_dict" in torch.load(ckpt, weights_only=True)
+    torch.save({"format": "something_else"}, tmp_path / "bad.dmem")
+    with pytest.raises(ValueError, match="not a DABSN memory payload"):
+        mem.load(tmp_path / "bad.dmem")
