@@ -674,9 +674,10 @@ using namespace dabsn::read3;
 // Decode read: a few query rows (T <= kDecodeRows) against a long bank, reading the bank's
 // write rows in place through an index list and a row stride, with no gathered K/V/Vn
 // copies and no transposes. Same masks, softmaxes and dtype policy as forward_impl:
-// K = E(write / max(norm, eps)) as bank_gather stores it, scores in fp32, P_V / P_Vn stored
-// in E, the output accumulated in fp32 (per slot split, then summed in split order) and
-// stored in E. Inference only (no backward).
+// K = E(write / max(norm, eps)) as bank_gather stores it (here as a product with the
+// reciprocal, within one fp32 ulp before the rounding to E), scores in fp32, P_V / P_Vn
+// stored in E, the output accumulated in fp32 (per slot split, then summed in split order)
+// and stored in E. Inference only (no backward).
 // ---------------------------------------------------------------------------
 constexpr int kDecodeRows = 8;
 constexpr int kDecodeSlotsPerBlock = 16;  // 4 waves x 4 slots
@@ -690,8 +691,9 @@ __device__ __forceinline__ const E* bank_row(const E* bank, int b, int64_t rowld
   return bank + (static_cast<size_t>(b) * rowld + r) * H;
 }
 
-// S[b, t, j] = q[b, t] . K_j for every slot j. One wave per slot; the T query rows of
-// batch row b are staged in LDS (dynamic, T * H elements).
+// S[b, t, j] = q[b, t] . K_j for every slot j, K_j = E(write_j * (1 / norm_j)) (the
+// gather's E(write_j / norm_j) up to one fp32 ulp before the rounding to E). One wave per
+// slot; the T query rows of batch row b are staged in LDS (dynamic, T * H elements).
 template <typename E>
 __global__ void __launch_bounds__(256) decode_score_kernel(int T, int N, int H, int64_t Nb,
                                                            int64_t rowld, const E* q, const E* bank,
@@ -716,14 +718,14 @@ __global__ void __launch_bounds__(256) decode_score_kernel(int T, int N, int H, 
   const int jw = blockIdx.x * kDecodeSlotsPerBlock + wave * KW;
   if (jw >= N) return;  // wave-uniform; no barrier follows
   const E* row[KW];
-  float n[KW];
+  float rn[KW];  // 1 / norm, once per slot (the gather divides per element: <= 1 ulp apart)
 #pragma unroll
   for (int k = 0; k < KW; ++k) {
     const int j = min(jw + k, N - 1);
     const int64_t i = idx[static_cast<size_t>(b) * N + j];
     const int64_t ic = i < 0 ? 0 : (i >= Nb ? Nb - 1 : i);
     row[k] = bank_row(bank, b, rowld, Nb, i, H);
-    n[k] = fmaxf(norm_w[static_cast<size_t>(b) * Nb + ic], kNormEps);
+    rn[k] = 1.0f / fmaxf(norm_w[static_cast<size_t>(b) * Nb + ic], kNormEps);
   }
   float acc[KW][kDecodeRows];
 #pragma unroll
@@ -737,7 +739,7 @@ __global__ void __launch_bounds__(256) decode_score_kernel(int T, int N, int H, 
 #pragma unroll
     for (int k = 0; k < KW; ++k)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[k][e] = round_to<E>(v[k][e] / n[k]);  // K as gathered
+      for (int e = 0; e < 8; ++e) v[k][e] = round_to<E>(v[k][e] * rn[k]);  // K
 #pragma unroll
     for (int t = 0; t < kDecodeRows; ++t) {
       if (t < T) {
@@ -851,8 +853,9 @@ static DecodePlan decode_plan(int dtype, int64_t B, int64_t T, int64_t N, int64_
   const size_t QT = (T + TILE - 1) / TILE, BT = (N + TILE - 1) / TILE;
   const size_t TN = static_cast<size_t>(B) * T * N;
   const int64_t hblocks = (H + 2047) / 2048;
-  // Enough (h chunk, b, split) blocks to fill the device, at least 64 slots per split.
-  int64_t splits = (512 + hblocks * B - 1) / (hblocks * B);
+  // Enough (h chunk, b, split) blocks to keep about 8 per CU with loads in flight, at
+  // least 64 slots per split.
+  int64_t splits = (2048 + hblocks * B - 1) / (hblocks * B);
   splits = std::max<int64_t>(1, std::min<int64_t>(splits, (N + 63) / 64));
   p.splits = static_cast<int>(splits);
   p.per_split = static_cast<int>((N + splits - 1) / splits);
