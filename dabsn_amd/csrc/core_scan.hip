@@ -270,7 +270,11 @@ __device__ __forceinline__ void tile_of(int bid, int nct, int& ct, int& bg) {
 
 // Forward scan of one workgroup: `bid` is its index among the `grid` workgroups of this
 // scan (the kernel may host another scan in its other workgroups).
-template <typename E, int CH, int KSTEPS, int NW>
+// LOCAL0 (one-step scans only, T == 1): y_0 was written into every batch group's exchange
+// slot by a previous launch (publish_y0_kernel: E(tanh(Wx_0 + b_0)), the expression each
+// owner publishes), so no workgroup publishes or waits: any grid size runs as one ordinary
+// launch.
+template <typename E, int CH, int KSTEPS, int NW, bool LOCAL0 = false>
 __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid) {
   using M = Mf<E>;
   constexpr int NT = NW * 64;
@@ -380,7 +384,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
 
   float ycur = (act && T > 0) ? tanhf(ld(a.Wx, row0 * H + c) + sb) : 0.0f;
   const int kb_y[1] = {ct * CH};
-  if (T > 0) {
+  if (T > 0 && !LOCAL0) {
     const float v[1] = {ycur};
     publish<E, CH, 1>(xr, a.slot_bytes, 0, kb_y, v, is_pair, cl, bl);
     if (tid == 0) arrive(counter);
@@ -414,8 +418,10 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   E wxn_next = INSTAGE ? static_cast<E>(0) : a.Wx[in_row(T > 1 ? 1 : 0)];
   for (int t = 0; t < T; ++t) {
     const size_t rt = (row0 + t) * H + c;
-    if (wave == 0) {
-      if (!wait_step(ctr, a.nct, static_cast<uint32_t>(t + 1), err) && tid == 0) s_abort = 1;
+    if constexpr (!LOCAL0) {
+      if (wave == 0) {
+        if (!wait_step(ctr, a.nct, static_cast<uint32_t>(t + 1), err) && tid == 0) s_abort = 1;
+      }
     }
     __syncthreads();
     if (s_abort) return;
@@ -1081,6 +1087,27 @@ __global__ void __launch_bounds__(NW * 64, 1) core_fwd_kernel(FwdArgs<E> a) {
   fwd_body<E, CH, KSTEPS, NW>(a, blockIdx.x, gridDim.x);
 }
 
+// y_0 = E(tanh(Wx_0 + b_0)) of every (batch row, unit) into slot 0 of its batch group's
+// exchange, in the slot layout the scan reads (launched before core_fwd1_kernel; the
+// units past H stay zero from the workspace clear). One thread per element.
+template <typename E>
+__global__ void __launch_bounds__(256) publish_y0_kernel(FwdArgs<E> a, int nbg) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(a.B) * a.H) return;
+  const int b = static_cast<int>(i / a.H), k = static_cast<int>(i % a.H);
+  const float y = tanhf(ld(a.Wx, static_cast<size_t>(b) * static_cast<size_t>(a.ldt) * a.H + k) +
+                        a.b0[i]);
+  E* slot = reinterpret_cast<E*>(a.ws + xchg_offset(nbg) +
+                                 static_cast<size_t>(b / NB) * 2 * a.slot_bytes);
+  st(slot, xoff<E>(k, b % NB), y);
+}
+
+// One-step scan (T == 1) reading y_0 from publish_y0_kernel: an ordinary launch of any size.
+template <typename E, int CH, int KSTEPS, int NW>
+__global__ void __launch_bounds__(NW * 64, 1) core_fwd1_kernel(FwdArgs<E> a) {
+  fwd_body<E, CH, KSTEPS, NW, true>(a, blockIdx.x, gridDim.x);
+}
+
 template <typename E, int CH, int KSTEPS, int NW>
 __global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
   bwd_body<E, CH, KSTEPS, NW>(a, blockIdx.x, gridDim.x);
@@ -1245,11 +1272,31 @@ static int launch_slabs(K kernel, int threads, const Cfg& c, const A& args, hipS
 #define DABSN_CORE_CASES_F32(X) \
   X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(8, 16, 4) X(8, 32, 4) X(8, 64, 4)
 
+template <typename K, typename A>
+static int launch_plain(K kernel, int grid, int threads, const A& args, hipStream_t stream) {
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, stream, args);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+// One-step scans: y_0 into every group's slot, then the scan without waits.
+template <typename K, typename E>
+static int launch_one_step(K kernel, int threads, const Cfg& c, const FwdArgs<E>& args,
+                           hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(args.B) * args.H;
+  hipLaunchKernelGGL(publish_y0_kernel<E>, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
+                     0, stream, args, c.nbg);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return launch_plain(kernel, c.nct * c.nbg, threads, args, stream);
+}
+
 template <typename E>
 static int fwd_dispatch(const Cfg& c, const FwdArgs<E>& args, hipStream_t stream) {
-#define DABSN_CASE(CHV, KS, NWV)                                   \
-  if (c.ch == CHV && c.ksteps == KS && c.nw == NWV)                \
-    return launch_slabs(core_fwd_kernel<E, CHV, KS, NWV>, NWV * 64, c, args, stream);
+#define DABSN_CASE(CHV, KS, NWV)                                                           \
+  if (c.ch == CHV && c.ksteps == KS && c.nw == NWV)                                        \
+    return args.T == 1                                                                     \
+               ? launch_one_step(core_fwd1_kernel<E, CHV, KS, NWV>, NWV * 64, c, args, stream) \
+               : launch_slabs(core_fwd_kernel<E, CHV, KS, NWV>, NWV * 64, c, args, stream);
   if constexpr (is_bf16<E>::value) {
     DABSN_CORE_CASES_BF16(DABSN_CASE)
   } else {

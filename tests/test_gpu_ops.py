@@ -174,6 +174,28 @@ def test_core_scan_batch_beyond_one_launch_equals_row_blocks(cuda_device, chunk)
         assert rel_err(a, b) <= 1e-5, f"grad input {i}: {rel_err(a, b):.3e}"
 
 
+@pytest.mark.parametrize("dtype,B,H", [(torch.float32, 5, 40), (torch.bfloat16, 40, 2048)])
+def test_core_scan_one_step_without_exchange_equals_first_step(cuda_device, dtype, B, H):
+    """A one-step scan (T = 1) runs without the step exchange: each workgroup computes the
+    y_0 values of its K slice itself, so all batch groups go in one ordinary launch. Its
+    outputs equal step 0 of a longer scan bit for bit, and continuing from its final state
+    reproduces the rest of the longer scan bit for bit."""
+    T = 5
+    inp = core_case(501, B, T, H)
+    x = [t.to(cuda_device) for t in inp]
+    x[0], x[1] = x[0].to(dtype), x[1].to(dtype)
+    full = ops.core_scan_batched(*x)
+    one = ops.core_scan_batched(x[0][:, :1].contiguous(), x[1][:, :1].contiguous(), *x[2:])
+    for k in range(8):
+        assert torch.equal(one[k], full[k][:, :1]), OUT_NAMES[k]
+    rest = ops.core_scan_batched(x[0][:, 1:].contiguous(), x[1][:, 1:].contiguous(), *x[2:23],
+                                 *one[8:11])
+    for k in range(8):
+        assert torch.equal(torch.cat([one[k], rest[k]], 1), full[k]), OUT_NAMES[k]
+    for k in range(8, 11):
+        assert torch.equal(rest[k], full[k]), OUT_NAMES[k]
+
+
 def test_core_scan_chunked_equals_full_on_device(cuda_device):
     """Carried (b, e, c): two chunks equal one pass exactly (same kernel, same state)."""
     inp = core_case(5, 4, 50, 64)
