@@ -842,16 +842,408 @@ __global__ void __launch_bounds__(256) decode_reduce_kernel(int64_t chunks, int 
   stv<E, 8>(out + c * 8, acc);
 }
 
+// ---------------------------------------------------------------------------
+// One-query decode read in a single pass over the bank (T == 1, H <= 2048): one wave per
+// (batch row, slot split) streams its slots' write rows once; each row gives the slot's
+// score (K = E(write * 1/norm) as above) and, through online softmaxes, feeds the short,
+// permanent and induction accumulators. The induction value of slot j is the row after
+// idx[j]; when that row is slot j+1's row (consecutive admitted positions) it is taken
+// from the registers that row is already in, one slot later. decode_combine_kernel merges
+// the splits' (max, sum, accumulator) triples. Scores and sums are the softmaxes of
+// softmax_fwd_kernel evaluated in one pass; the products with V run in fp32 from the
+// exact softmax weights (the two-pass path rounds P_V / P_Vn to E first).
+// ---------------------------------------------------------------------------
+constexpr int kFusedMaxChunks = 4;  // 8-element chunks per lane: H <= 64 * 8 * 4
+
+// Per-slot inputs of the single-pass read (8 dwords, read with one scalar load).
+struct SlotMeta {
+  uint32_t row, nrow;  // bank rows (b * rowld + index) of V and of the induction value
+  float rn;            // 1 / max(norm, eps) of the V row
+  float kb, adm, ccg;  // key bias, admission, cocktail gain * (cocktail . bank cocktail)
+  uint32_t flags;      // bit 0: short / permanent read allowed, bit 1: induction allowed
+  uint32_t pad;
+};
+
+__global__ void __launch_bounds__(256) decode_meta_kernel(int N, int64_t Nb, int64_t rowld,
+                                                          const float* norm_w, const int64_t* idx,
+                                                          const int64_t* next_idx,
+                                                          const int64_t* read_idx,
+                                                          const uint8_t* valid, const float* ck,
+                                                          const float* cb, const float* kb,
+                                                          const float* adm, Gains g,
+                                                          SlotMeta* meta) {
+  const int b = blockIdx.y;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= N) return;
+  const size_t bj = static_cast<size_t>(b) * N + j;
+  const int64_t i = idx[bj], n = next_idx[bj];
+  const int64_t ic = i < 0 ? 0 : (i >= Nb ? Nb - 1 : i);
+  const int64_t nc = n < 0 ? 0 : (n >= Nb ? Nb - 1 : n);
+  const float* ckt = ck + static_cast<size_t>(b) * 4;
+  const float* cbj = cb + bj * 4;
+  const float cc = ckt[0] * cbj[0] + ckt[1] * cbj[1] + ckt[2] * cbj[2] + ckt[3] * cbj[3];
+  const bool v = valid[bj] != 0;
+  SlotMeta m;
+  m.row = static_cast<uint32_t>(static_cast<int64_t>(b) * rowld + ic);
+  m.nrow = static_cast<uint32_t>(static_cast<int64_t>(b) * rowld + nc);
+  m.rn = 1.0f / fmaxf(norm_w[static_cast<size_t>(b) * Nb + ic], kNormEps);
+  m.kb = kb[bj];
+  m.adm = adm[bj];
+  m.ccg = cc * g.p[3][0];
+  m.flags = (allow_at(0, read_idx[bj], v, 0) ? 1u : 0u) | (induct_at(0, read_idx[bj], v, 0, 1) ? 2u : 0u);
+  m.pad = 0u;
+  meta[bj] = m;
+}
+
+// NC chunks of 8 elements of one bank row, chunk k at element 8 * (lane + 64 k) (clamped
+// to the row's last chunk; lanes past the row hold a copy and a zero query).
+template <typename E, int NC>
+struct RowChunks {
+  static constexpr int W = sizeof(E) == 2 ? 1 : 2;  // 16-byte words per chunk
+  u32x4 d[NC * W];
+  __device__ __forceinline__ void load(const E* row, int lane, int nch) {
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const E* p = row + static_cast<size_t>(min(lane + 64 * k, nch - 1)) * 8;
+#pragma unroll
+      for (int w = 0; w < W; ++w) d[k * W + w] = gload16(p + w * 4);
+    }
+  }
+  __device__ __forceinline__ void unpack(int k, float (&v)[8]) const {
+    if constexpr (W == 1) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = __builtin_bit_cast(float, d[k][e] << 16);
+        v[2 * e + 1] = __builtin_bit_cast(float, d[k][e] & 0xffff0000u);
+      }
+    } else {
+      // Whole-vector casts: hipcc's __builtin_bit_cast of a single vector element (an
+      // lvalue) reads element 0.
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const f32x4 f = __builtin_bit_cast(f32x4, d[2 * k + w]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * w + e] = f[e];
+      }
+    }
+  }
+};
+
+// Online softmax step with score x: updates (m, l), returns x's weight and sets `alpha`,
+// the factor the accumulator must be scaled by first (1 unless x is a new maximum).
+__device__ __forceinline__ float online_weight(float x, float& m, float& l, float& alpha) {
+  if (x > m) {
+    alpha = __expf(m - x);  // m = -inf: 0
+    l = l * alpha + 1.0f;
+    m = x;
+    return 1.0f;
+  }
+  alpha = 1.0f;
+  const float w = __expf(x - m);
+  l += w;
+  return w;
+}
+
+template <typename E, int NC>
+__device__ __forceinline__ void acc_add(float (&acc)[NC][8], const RowChunks<E, NC>& r, float w) {
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    float v[8];
+    r.unpack(k, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[k][e] = fmaf(w, v[e], acc[k][e]);
+  }
+}
+
+template <int NC>
+__device__ __forceinline__ void acc_scale(float (&acc)[NC][8], float a) {
+#pragma unroll
+  for (int k = 0; k < NC; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[k][e] *= a;
+}
+
+template <typename E>
+struct FusedArgs {
+  int N, H, splits, per_split;
+  const E* q;
+  const E* bank;
+  const SlotMeta* meta;
+  const int32_t* rs;
+  const float* scale;
+  float* pacc;    // [waves][3][H]: short, permanent, induction accumulators
+  float* pstats;  // [waves][6]: (m, l) of the three softmaxes
+};
+
+// Query row b, lane's chunks: bf16 as packed pairs (the score uses v_dot2_f32_bf16 on the
+// packed K pairs), fp32 as floats. Chunks past the row are zero.
+template <typename E, int NC>
+struct QueryChunks {
+  static constexpr bool BF = sizeof(E) == 2;
+  uint32_t w[BF ? NC * 4 : 1];
+  float f[BF ? 1 : NC * 8];
+  __device__ __forceinline__ void load(const E* q, int lane, int nch) {
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int c = lane + 64 * k;
+      if constexpr (BF) {
+        const u32x4 u = c < nch ? gload16(q + c * 8) : (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[k * 4 + e] = u[e];
+      } else {
+        float v[8];
+        if (c < nch) {
+          ldv<E, 8>(q + c * 8, v);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[k * 8 + e] = v[e];
+      }
+    }
+  }
+};
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Lane's part of q . K with K = E(row * rn).
+template <typename E, int NC>
+__device__ __forceinline__ float row_dot(const RowChunks<E, NC>& r, const QueryChunks<E, NC>& q,
+                                         float rn) {
+  float dot = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    if constexpr (sizeof(E) == 2) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t u = r.d[k][e];
+        const float lo = __builtin_bit_cast(float, u << 16) * rn;
+        const float hi = __builtin_bit_cast(float, u & 0xffff0000u) * rn;
+        const bf16x2 kp = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};  // RTNE
+        dot = __builtin_amdgcn_fdot2_f32_bf16(kp, __builtin_bit_cast(bf16x2, q.w[k * 4 + e]), dot,
+                                              false);
+      }
+    } else {
+      float v[8];
+      r.unpack(k, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot = fmaf(q.f[k * 8 + e], v[e] * rn, dot);
+    }
+  }
+  return dot;
+}
+
+// One wave (= one workgroup) per (batch row b, split s); slots [s * per_split, ...) below
+// the row's nhi. Rows stream through D register buffers (D - 1 rows in flight ahead of
+// the one in use); the loop is unrolled D times so every buffer keeps a fixed role and no
+// in-flight register is copied. Slot metadata comes through scalar loads D slots ahead.
+template <typename E, int NC>
+__global__ void __launch_bounds__(64) decode_fused_kernel(FusedArgs<E> a) {
+  constexpr int D = sizeof(E) == 2 ? 3 : 2;
+  using Row = RowChunks<E, NC>;
+  const int lane = threadIdx.x;
+  const int w = blockIdx.x;
+  const int b = w / a.splits, s = w % a.splits;
+  const int H = a.H, nch = H / 8;
+  const int nhi = min(a.N, a.rs[static_cast<size_t>(b) * 3 + 2]);
+  const int j0 = s * a.per_split, j1 = min(nhi, j0 + a.per_split);
+  const float scale = a.scale[0];
+  QueryChunks<E, NC> qc;
+  qc.load(a.q + static_cast<size_t>(b) * H, lane, nch);
+  float acc[3][NC][8];
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int k = 0; k < NC; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[p][k][e] = 0.0f;
+  float m[3] = {-INFINITY, -INFINITY, -INFINITY}, l[3] = {0.f, 0.f, 0.f};
+  const SlotMeta* mb = a.meta + static_cast<size_t>(b) * a.N;
+  const size_t rowH = static_cast<size_t>(H);
+  float pend_w = 0.0f;     // induction weight of the previous slot, not yet added
+  uint32_t pend_row = 0u;  // its induction row
+  if (j0 < j1) {
+    SlotMeta ring[D];  // metadata of slots j .. j + D - 1
+#pragma unroll
+    for (int d = 0; d < D; ++d) ring[d] = mb[min(j0 + d, j1 - 1)];
+    Row r[D];
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d) r[d].load(a.bank + ring[d].row * rowH, lane, nch);
+    // Slot j with its row in `cur`; requests slot j + D - 1's row into `pf`.
+    auto step = [&](Row& cur, Row& pf, int j) __attribute__((always_inline)) {
+      const SlotMeta mc = ring[0];
+#pragma unroll
+      for (int d = 0; d + 1 < D; ++d) ring[d] = ring[d + 1];
+      ring[D - 1] = mb[min(j + D, j1 - 1)];
+      pf.load(a.bank + ring[D - 2].row * rowH, lane, nch);  // the last slots reread theirs
+      // The previous slot's induction value, from this slot's row when it is that row.
+      if (pend_w != 0.0f) {
+        if (pend_row == mc.row) {
+          acc_add<E, NC>(acc[2], cur, pend_w);
+          // Keeps this branch from being merged with the other one: the merged block
+          // would carry the other branch's wait for its own load (a drain of every row
+          // in flight) onto this path.
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          Row vn;
+          vn.load(a.bank + pend_row * rowH, lane, nch);
+          acc_add<E, NC>(acc[2], vn, pend_w);
+        }
+      }
+      pend_w = 0.0f;
+      if (mc.flags != 0u) {
+        const float sraw = wave_sum(row_dot<E, NC>(cur, qc, mc.rn));
+        const float content = sraw * scale + mc.kb;
+        const float ss = content + mc.adm;
+        const float sp = content + mc.ccg + mc.adm;
+        float alpha;
+        if (mc.flags & 1u) {
+          const float ws = online_weight(ss, m[0], l[0], alpha);
+          if (alpha != 1.0f) acc_scale<NC>(acc[0], alpha);
+          const float wp = online_weight(sp, m[1], l[1], alpha);
+          if (alpha != 1.0f) acc_scale<NC>(acc[1], alpha);
+#pragma unroll
+          for (int k = 0; k < NC; ++k) {
+            float v[8];
+            cur.unpack(k, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              acc[0][k][e] = fmaf(ws, v[e], acc[0][k][e]);
+              acc[1][k][e] = fmaf(wp, v[e], acc[1][k][e]);
+            }
+          }
+        }
+        if (mc.flags & 2u) {
+          pend_w = online_weight(ss, m[2], l[2], alpha);
+          if (alpha != 1.0f) acc_scale<NC>(acc[2], alpha);
+          pend_row = mc.nrow;
+        }
+      }
+    };
+    // Whole groups of D slots in a loop with one exit (an exit between the steps would
+    // leave the next group's requests in flight on the loop's back edge, and the wait
+    // placement would then drain them at the top of every group), the rest after it.
+    const int full = j0 + (j1 - j0) / D * D;
+    int j = j0;
+    if constexpr (D == 3) {
+      for (; j < full; j += 3) {
+        step(r[0], r[2], j);
+        step(r[1], r[0], j + 1);
+        step(r[2], r[1], j + 2);
+      }
+      if (j < j1) step(r[0], r[2], j);
+      if (j + 1 < j1) step(r[1], r[0], j + 1);
+    } else {
+      for (; j < full; j += 2) {
+        step(r[0], r[1], j);
+        step(r[1], r[0], j + 1);
+      }
+      if (j < j1) step(r[0], r[1], j);
+    }
+    if (pend_w != 0.0f) {
+      Row vn;
+      vn.load(a.bank + pend_row * rowH, lane, nch);
+      acc_add<E, NC>(acc[2], vn, pend_w);
+    }
+  }
+  float* pa = a.pacc + static_cast<size_t>(w) * 3 * H;
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int c = lane + 64 * k;
+      if (c < nch) stv<float, 8>(pa + static_cast<size_t>(p) * H + c * 8, acc[p][k]);
+    }
+  if (lane == 0) {
+    float* ps = a.pstats + static_cast<size_t>(w) * 6;
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      ps[2 * p] = m[p];
+      ps[2 * p + 1] = l[p];
+    }
+  }
+}
+
+// out[b] = sg * Ps V + pg * Pp V + ig * Pi Vn from the splits' partial softmaxes: each
+// split's accumulator is rescaled to the row maximum and divided by the row sum.
+template <typename E>
+__global__ void __launch_bounds__(256) decode_combine_kernel(int H, int splits, const float* pacc,
+                                                             const float* pstats, Gains g, E* out) {
+  const int b = blockIdx.y;
+  const int h0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (h0 >= H) return;
+  const float* st6 = pstats + static_cast<size_t>(b) * splits * 6;
+  float M[3] = {-INFINITY, -INFINITY, -INFINITY}, L[3] = {0.f, 0.f, 0.f};
+  for (int s = 0; s < splits; ++s)
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+      if (st6[s * 6 + 2 * p + 1] > 0.f) M[p] = fmaxf(M[p], st6[s * 6 + 2 * p]);
+  for (int s = 0; s < splits; ++s)
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      const float ls = st6[s * 6 + 2 * p + 1];
+      if (ls > 0.f) L[p] += ls * __expf(st6[s * 6 + 2 * p] - M[p]);
+    }
+  const float gain[3] = {g.p[0][0], g.p[1][0], g.p[2][0]};
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+  for (int s = 0; s < splits; ++s) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      const float ls = st6[s * 6 + 2 * p + 1];
+      if (ls > 0.f) {
+        const float c = gain[p] * (__expf(st6[s * 6 + 2 * p] - M[p]) / L[p]);
+        float v[8];
+        ldv<float, 8>(pacc + ((static_cast<size_t>(b) * splits + s) * 3 + p) * H + h0, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += c * v[e];
+      }
+    }
+  }
+  stv<E, 8>(out + static_cast<size_t>(b) * H + h0, o);
+}
+
 struct DecodePlan {
   size_t off_S, off_rs, off_ro, off_rb, off_stats, off_PV, off_PVn, off_part, end;
   int splits, per_split;
+  bool fused;
+  size_t off_meta, off_pacc, off_pstats;
 };
+
+// Workgroups (one wave each) per CU the single-pass read aims for: two waves per SIMD.
+constexpr int kFusedWavesPerCU = 8;
+
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
 
 static DecodePlan decode_plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
   DecodePlan p{};
   const size_t e = dtype == kBF16 ? 2 : 4;
   const size_t QT = (T + TILE - 1) / TILE, BT = (N + TILE - 1) / TILE;
   const size_t TN = static_cast<size_t>(B) * T * N;
+  if (T == 1 && H <= 64 * 8 * kFusedMaxChunks) {
+    // Single pass: enough (b, split) waves to fill the CUs, at least 16 slots per split.
+    p.fused = true;
+    const int64_t want = (static_cast<int64_t>(kFusedWavesPerCU) * device_cus() + B - 1) / B;
+    const int64_t splits = std::max<int64_t>(1, std::min<int64_t>(want, (N + 15) / 16));
+    p.splits = static_cast<int>(splits);
+    p.per_split = static_cast<int>((N + splits - 1) / splits);
+    size_t o = 0;
+    p.off_rs = o; o = align_up(o + B * QT * 3 * 4);
+    p.off_ro = o; o = align_up(o + B * QT * 3 * 4);
+    p.off_meta = o; o = align_up(o + static_cast<size_t>(B) * N * sizeof(SlotMeta));
+    p.off_pacc = o; o = align_up(o + static_cast<size_t>(B) * splits * 3 * H * 4);
+    p.off_pstats = o; o = align_up(o + static_cast<size_t>(B) * splits * 6 * 4);
+    p.end = o;
+    return p;
+  }
   const int64_t hblocks = (H + 2047) / 2048;
   // Enough (h chunk, b, split) blocks to keep about 8 per CU with loads in flight, at
   // least 64 slots per split.
@@ -880,6 +1272,34 @@ static int decode_impl(int64_t B, int64_t T, int64_t N, int64_t H, int64_t Nb, i
                        const float* scale, Gains g, E* out, uint8_t* ws, const DecodePlan& p,
                        hipStream_t stream) {
   const int QT = static_cast<int>((T + TILE - 1) / TILE), BT = static_cast<int>((N + TILE - 1) / TILE);
+  if (p.fused) {
+    int32_t* rs = reinterpret_cast<int32_t*>(ws + p.off_rs);
+    int32_t* ro = reinterpret_cast<int32_t*>(ws + p.off_ro);
+    SlotMeta* meta = reinterpret_cast<SlotMeta*>(ws + p.off_meta);
+    float* pacc = reinterpret_cast<float*>(ws + p.off_pacc);
+    float* pstats = reinterpret_cast<float*>(ws + p.off_pstats);
+    // Query tiles only (grid QT): nhi per batch row; no bank-tile ranges are needed.
+    hipLaunchKernelGGL(ranges_kernel, dim3((unsigned)QT, (unsigned)B), dim3(256), 0, stream,
+                       (int)T, (int)N, (int)H, 0, read_idx, valid, rs, ro, nullptr);
+    DABSN_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(decode_meta_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)B), dim3(256),
+                       0, stream, (int)N, Nb, rowld, norm_w, idx, next_idx, read_idx, valid, ck, cb,
+                       kb, adm, g, meta);
+    DABSN_HIP_CHECK(hipGetLastError());
+    FusedArgs<E> fa{(int)N, (int)H, p.splits, p.per_split, q, bank, meta, rs, scale, pacc, pstats};
+    const dim3 grid((unsigned)(B * p.splits));
+    if (H <= 512)
+      hipLaunchKernelGGL((decode_fused_kernel<E, 1>), grid, dim3(64), 0, stream, fa);
+    else if (H <= 1024)
+      hipLaunchKernelGGL((decode_fused_kernel<E, 2>), grid, dim3(64), 0, stream, fa);
+    else
+      hipLaunchKernelGGL((decode_fused_kernel<E, 4>), grid, dim3(64), 0, stream, fa);
+    DABSN_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(decode_combine_kernel<E>, dim3((unsigned)((H + 2047) / 2048), (unsigned)B),
+                       dim3(256), 0, stream, (int)H, p.splits, pacc, pstats, g, out);
+    DABSN_HIP_CHECK(hipGetLastError());
+    return DABSN_OK;
+  }
   float* S = reinterpret_cast<float*>(ws + p.off_S);
   int32_t* rs = reinterpret_cast<int32_t*>(ws + p.off_rs);
   int32_t* ro = reinterpret_cast<int32_t*>(ws + p.off_ro);
@@ -1014,6 +1434,8 @@ int dabsn_hip_read3_decode(int dtype, int64_t B, int64_t T, int64_t N, int64_t H
   if (rc != DABSN_OK) return rc;
   DABSN_REQUIRE(T <= kDecodeRows, "read3 decode: T=%lld query rows > %d", (long long)T, kDecodeRows);
   DABSN_REQUIRE(N > 0 && bank_len > 0 && bank_ld >= bank_len, "read3 decode: bad bank shape");
+  DABSN_REQUIRE(B * bank_ld <= static_cast<int64_t>(UINT32_MAX),
+                "read3 decode: B * bank_ld = %lld bank rows exceeds 2^32 - 1", (long long)(B * bank_ld));
   DABSN_REQUIRE(H % 8 == 0, "read3 decode: H=%lld must be a multiple of 8", (long long)H);
   DABSN_REQUIRE(T * H * (dtype == kBF16 ? 2 : 4) <= 65536,
                 "read3 decode: T*H too large for the query staging");

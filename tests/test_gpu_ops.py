@@ -452,21 +452,14 @@ def test_chunked_core_scan_matches_full_op(cuda_device, dtype, B, T, H, chunk, t
             assert err <= tol, f"input {i}: {err:.3e}"
 
 
-@pytest.mark.parametrize("dtype,T", [(torch.float32, 1), (torch.float32, 3), (torch.bfloat16, 1),
-                                     (torch.bfloat16, 3)])
-def test_read3_decode_matches_gather_and_read(cuda_device, dtype, T):
-    """The decode read (bank read in place through idx and a row stride) against bank gather
-    + the three-way read on the same inputs: the bank is the first 40 positions of a
-    64-position buffer, queries sit at the end of it (query_start = 40 - T), rows admit
-    different slot counts. fp32: normwise 1e-5 (dot products and the slot sum are summed in
-    another order). bf16: P_V, P_Vn and K are rounded to bf16 on both sides, so an order
-    difference can move a rounding; Frobenius 5e-3."""
-    g = torch.Generator().manual_seed(77)
-    B, H, cap, Nb = 3, 64, 64, 40
+def _decode_case(cuda_device, dtype, T, B, H, cap, Nb, counts, seed):
+    """read3_decode and bank gather + three-way read on one bank: the first Nb positions of
+    a cap-position buffer, queries at its end (query_start = Nb - T); row b admits counts[b]
+    slots (a sorted random subset, then the rest masked by `valid`)."""
+    g = torch.Generator().manual_seed(seed)
     qs = Nb - T
     buf = torch.randn(B, cap, H, generator=g).to(dtype)
     bank = buf.to(cuda_device)[:, :Nb]
-    counts = [Nb, 23, 9]
     n = max(counts)
     idx = torch.zeros(B, n, dtype=torch.int64)
     for b in range(B):
@@ -493,7 +486,43 @@ def test_read3_decode_matches_gather_and_read(cuda_device, dtype, T):
         want = ops.admitted_three_way_read_compact_flash(
             d(q), K, V, Vn, d(ck), d(cb), d(kb), d(adm), d(scale), d(read_idx), d(valid), 0,
             *(d(x) for x in gains))
+    return got.float().cpu(), want.float().cpu()
+
+
+@pytest.mark.parametrize("dtype,T", [(torch.float32, 1), (torch.float32, 3), (torch.bfloat16, 1),
+                                     (torch.bfloat16, 3)])
+def test_read3_decode_matches_gather_and_read(cuda_device, dtype, T):
+    """The decode read (bank read in place through idx and a row stride) against bank gather
+    + the three-way read on the same inputs: the bank is the first 40 positions of a
+    64-position buffer and rows admit different slot counts (non-consecutive admitted
+    positions: induction rows that are not the next slot's row). T = 1 runs the single-pass
+    read, T = 3 the score / softmax / product passes. fp32: normwise 1e-5 (dot products and
+    the slot sum are summed in another order). bf16: K is rounded to bf16 on both sides and
+    the two-pass paths round P_V, P_Vn to bf16, so an order difference can move a rounding;
+    Frobenius 5e-3."""
+    got, want = _decode_case(cuda_device, dtype, T, 3, 64, 64, 40, [40, 23, 9], 77)
     if dtype == torch.float32:
-        assert rel_err(got.cpu(), want.cpu()) <= 1e-5
+        assert rel_err(got, want) <= 1e-5
     else:
-        assert rel_fro(got.float().cpu(), want.float().cpu()) <= 5e-3
+        assert rel_fro(got, want) <= 5e-3
+
+
+@pytest.mark.parametrize("dtype,B,H,Nb,admit", [
+    (torch.float32, 4, 1000, 300, 1.0),    # 2 chunks per lane, lanes past the row
+    (torch.bfloat16, 4, 2048, 700, 1.0),   # 4 chunks per lane, consecutive slots
+    (torch.bfloat16, 4, 1024, 500, 0.6),   # scattered admitted positions
+    (torch.float32, 4, 2048, 257, 0.6),
+    (torch.bfloat16, 64, 2048, 2100, 1.0),  # 32 splits per row of 66 slots
+    (torch.bfloat16, 3, 2056, 200, 1.0),   # H > 2048: the two-pass read
+    (torch.bfloat16, 2, 512, 5, 1.0),      # fewer slots than one group
+])
+def test_read3_decode_single_pass_shapes(cuda_device, dtype, B, H, Nb, admit):
+    """One query row (streaming decode) at widths and bank lengths that exercise the
+    single-pass read's chunk counts, split remainders and both induction-row paths, against
+    bank gather + the three-way read. Tolerances as the decode test above."""
+    counts = [Nb, max(1, int(admit * Nb)), max(1, Nb // 3), 1] * ((B + 3) // 4)
+    got, want = _decode_case(cuda_device, dtype, 1, B, H, Nb + 7, Nb, counts[:B], 91 + H)
+    if dtype == torch.float32:
+        assert rel_err(got, want) <= 1e-5
+    else:
+        assert rel_fro(got, want) <= 5e-3
