@@ -32,6 +32,7 @@
 #include "../../include/dabsn_hip.h"
 #include "capi.hpp"
 #include "common.hpp"
+#include "gemm.hpp"
 
 namespace dabsn {
 namespace core {
@@ -124,6 +125,43 @@ __device__ __forceinline__ UnitParams load_unit(const Params& P, int c, bool ok)
   u.decay = sigmoidf_(g(V_LOGIT_CDECAY));
   u.kc = g(V_KC); u.rc = g(V_RC);
   return u;
+}
+
+// Scalar gains shared by every unit: gate mixing, budget write gain, cortisol suppression.
+struct StepGains {
+  float gate_alpha, lam, c_sup;
+};
+__device__ __forceinline__ StepGains load_gains(const Params& P) {
+  return StepGains{sigmoidf_(P.scal[0][0]), softplusf_(P.scal[1][0]), sigmoidf_(P.scal[2][0])};
+}
+
+// One step of a unit after the recurrent products ug (gate rows) and ay (A rows), both
+// already rounded to the activation dtype: the gate s_g, plasticity p and next budget bn.
+__device__ __forceinline__ float budget_next(const UnitParams& up, const StepGains& sg, float sb,
+                                             float se, float wgx, float ug, float ay, float& s_g,
+                                             float& p) {
+  s_g = hardsigmoidf_(wgx + ug);
+  p = s_g * se;
+  return (1.0f - sg.gate_alpha) * sb + up.beta + sg.lam * (p * ay);
+}
+
+// The rest of the step from the same inputs: novelty, cortisol after the step (cpost) and
+// the next energy.
+__device__ __forceinline__ float energy_next(const UnitParams& up, const StepGains& sg, float sb,
+                                             float se, float sc, float y, float s_g, float p,
+                                             float ay, float& nov, float& cpost) {
+  nov = tanhf(fabsf(ay - sb));
+  const float stress = nov * (1.0f - se);
+  cpost = up.decay * sc + (1.0f - up.decay) * stress;
+  const float nov_eff = nov * (1.0f - sg.c_sup * cpost);
+  const float tb = tanhf(sb);
+  float k_sig = up.ks * s_g + up.ky * y + up.kb * tb + up.kn * nov_eff + up.kbias;
+  float r_sig = up.rs * s_g + up.ry * y + up.rb * tb + up.rn * nov_eff + up.rbias;
+  k_sig += up.kc * cpost;
+  r_sig += up.rc * cpost;
+  const float k_t = up.kappa * expf(0.5f * tanhf(k_sig));
+  const float r_t = clamp01(up.recover * expf(0.5f * tanhf(r_sig)));
+  return clamp01(se + r_t * (1.0f - se) - k_t * p);
 }
 
 // Called by all 64 lanes of wave 0: waits until every split counter of the batch group
@@ -270,11 +308,7 @@ __device__ __forceinline__ void tile_of(int bid, int nct, int& ct, int& bg) {
 
 // Forward scan of one workgroup: `bid` is its index among the `grid` workgroups of this
 // scan (the kernel may host another scan in its other workgroups).
-// LOCAL0 (one-step scans only, T == 1): y_0 was written into every batch group's exchange
-// slot by a previous launch (publish_y0_kernel: E(tanh(Wx_0 + b_0)), the expression each
-// owner publishes), so no workgroup publishes or waits: any grid size runs as one ordinary
-// launch.
-template <typename E, int CH, int KSTEPS, int NW, bool LOCAL0 = false>
+template <typename E, int CH, int KSTEPS, int NW>
 __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid) {
   using M = Mf<E>;
   constexpr int NT = NW * 64;
@@ -374,9 +408,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   };
 
   const UnitParams up = load_unit(a.P, c, is_pair && c < H);
-  const float gate_alpha = sigmoidf_(a.P.scal[0][0]);
-  const float lam = softplusf_(a.P.scal[1][0]);
-  const float c_sup = sigmoidf_(a.P.scal[2][0]);
+  const StepGains sg = load_gains(a.P);
   float sb = act ? a.b0[static_cast<size_t>(b) * H + c] : 0.0f;
   float se = act ? a.e0[static_cast<size_t>(b) * H + c] : 0.0f;
   float sc = act ? a.c0[static_cast<size_t>(b) * H + c] : 0.0f;
@@ -384,7 +416,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
 
   float ycur = (act && T > 0) ? tanhf(ld(a.Wx, row0 * H + c) + sb) : 0.0f;
   const int kb_y[1] = {ct * CH};
-  if (T > 0 && !LOCAL0) {
+  if (T > 0) {
     const float v[1] = {ycur};
     publish<E, CH, 1>(xr, a.slot_bytes, 0, kb_y, v, is_pair, cl, bl);
     if (tid == 0) arrive(counter);
@@ -418,10 +450,8 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   E wxn_next = INSTAGE ? static_cast<E>(0) : a.Wx[in_row(T > 1 ? 1 : 0)];
   for (int t = 0; t < T; ++t) {
     const size_t rt = (row0 + t) * H + c;
-    if constexpr (!LOCAL0) {
-      if (wave == 0) {
-        if (!wait_step(ctr, a.nct, static_cast<uint32_t>(t + 1), err) && tid == 0) s_abort = 1;
-      }
+    if (wave == 0) {
+      if (!wait_step(ctr, a.nct, static_cast<uint32_t>(t + 1), err) && tid == 0) s_abort = 1;
     }
     __syncthreads();
     if (s_abort) return;
@@ -471,9 +501,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
         wgx_next = inbuf[0][bl][cl];
         wxn_next = inbuf[1][bl][cl];
       }
-      s_g = hardsigmoidf_(to_f(wgx_next) + ug);
-      p = s_g * se;
-      bn = (1.0f - gate_alpha) * sb + up.beta + lam * (p * ay);
+      bn = budget_next(up, sg, sb, se, to_f(wgx_next), ug, ay, s_g, p);
       if (act && t + 1 < T) ynext = tanhf(to_f(wxn_next) + bn);
     }
     if (t + 1 < T) {
@@ -483,20 +511,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
     }
     // Off the critical path (overlaps the next barrier): energy and cortisol, tapes.
     float en = 0.f, cpost = 0.f, nov = 0.f;
-    if (is_pair) {
-      nov = tanhf(fabsf(ay - sb));
-      const float stress = nov * (1.0f - se);
-      cpost = up.decay * sc + (1.0f - up.decay) * stress;
-      const float nov_eff = nov * (1.0f - c_sup * cpost);
-      const float tb = tanhf(sb);
-      float k_sig = up.ks * s_g + up.ky * ycur + up.kb * tb + up.kn * nov_eff + up.kbias;
-      float r_sig = up.rs * s_g + up.ry * ycur + up.rb * tb + up.rn * nov_eff + up.rbias;
-      k_sig += up.kc * cpost;
-      r_sig += up.rc * cpost;
-      const float k_t = up.kappa * expf(0.5f * tanhf(k_sig));
-      const float r_t = clamp01(up.recover * expf(0.5f * tanhf(r_sig)));
-      en = clamp01(se + r_t * (1.0f - se) - k_t * p);
-    }
+    if (is_pair) en = energy_next(up, sg, sb, se, sc, ycur, s_g, p, ay, nov, cpost);
     if constexpr (OSTAGE) {
       if (t > 0) flush(t - 1);
       if (act) {
@@ -1087,25 +1102,51 @@ __global__ void __launch_bounds__(NW * 64, 1) core_fwd_kernel(FwdArgs<E> a) {
   fwd_body<E, CH, KSTEPS, NW>(a, blockIdx.x, gridDim.x);
 }
 
-// y_0 = E(tanh(Wx_0 + b_0)) of every (batch row, unit) into slot 0 of its batch group's
-// exchange, in the slot layout the scan reads (launched before core_fwd1_kernel; the
-// units past H stay zero from the workspace clear). One thread per element.
+// One-step scans (T == 1) have no exchange: y_0 = E(tanh(Wx_0 + b_0)) for every (batch
+// row, unit) (y0_kernel), the recurrent products of all rows at once as one GEMM
+// [B, H] x [2H, H]^T (gemm.hpp), then every unit's step from them (step1_kernel) through
+// the same budget_next / energy_next as the scan.
 template <typename E>
-__global__ void __launch_bounds__(256) publish_y0_kernel(FwdArgs<E> a, int nbg) {
+__global__ void __launch_bounds__(256) y0_kernel(FwdArgs<E> a, E* y0) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i == 0) *reinterpret_cast<uint32_t*>(a.ws) = 0u;  // error word: no barriers to time out
   if (i >= static_cast<int64_t>(a.B) * a.H) return;
-  const int b = static_cast<int>(i / a.H), k = static_cast<int>(i % a.H);
-  const float y = tanhf(ld(a.Wx, static_cast<size_t>(b) * static_cast<size_t>(a.ldt) * a.H + k) +
-                        a.b0[i]);
-  E* slot = reinterpret_cast<E*>(a.ws + xchg_offset(nbg) +
-                                 static_cast<size_t>(b / NB) * 2 * a.slot_bytes);
-  st(slot, xoff<E>(k, b % NB), y);
+  const int b = static_cast<int>(i / a.H), c = static_cast<int>(i % a.H);
+  st(y0, static_cast<size_t>(i),
+     tanhf(ld(a.Wx, static_cast<size_t>(b) * static_cast<size_t>(a.ldt) * a.H + c) + a.b0[i]));
 }
 
-// One-step scan (T == 1) reading y_0 from publish_y0_kernel: an ordinary launch of any size.
-template <typename E, int CH, int KSTEPS, int NW>
-__global__ void __launch_bounds__(NW * 64, 1) core_fwd1_kernel(FwdArgs<E> a) {
-  fwd_body<E, CH, KSTEPS, NW, true>(a, blockIdx.x, gridDim.x);
+template <typename E>
+__global__ void __launch_bounds__(256) step1_kernel(FwdArgs<E> a, const float* G) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int H = a.H;
+  if (i >= static_cast<int64_t>(a.B) * H) return;
+  const int b = static_cast<int>(i / H), c = static_cast<int>(i % H);
+  const UnitParams up = load_unit(a.P, c, true);
+  const StepGains sg = load_gains(a.P);
+  const float sb = a.b0[i], se = a.e0[i], sc = a.c0[i];
+  const size_t row0 = static_cast<size_t>(b) * static_cast<size_t>(a.ldt);
+  const size_t rt = row0 * H + c;
+  const float y = tanhf(ld(a.Wx, rt) + sb);
+  // The reference's recurrent GEMM returns the activation dtype.
+  const float ug = round_to<E>(G[static_cast<size_t>(b) * 2 * H + c]);
+  const float ay = round_to<E>(G[static_cast<size_t>(b) * 2 * H + H + c]);
+  float s_g, p, nov, cpost;
+  const float bn = budget_next(up, sg, sb, se, ld(a.Wgx, rt), ug, ay, s_g, p);
+  const float en = energy_next(up, sg, sb, se, sc, y, s_g, p, ay, nov, cpost);
+  const size_t ru = row0 * 2 * H + c;
+  st(a.U, ru, y);
+  st(a.U, ru + H, bn);
+  st(a.nov, rt, nov);
+  st(a.pl, rt, p);
+  st(a.ay, rt, ay);
+  st(a.wr, rt, p * ay);
+  st(a.et, rt, se);
+  st(a.ctp, rt, cpost);
+  st(a.st, rt, gate_tape_value<E>(s_g));
+  a.bF[i] = bn;
+  a.eF[i] = en;
+  a.cF[i] = cpost;
 }
 
 template <typename E, int CH, int KSTEPS, int NW>
@@ -1169,8 +1210,24 @@ static size_t slot_bytes(int dtype, const Cfg& c, bool backward) {
   return (backward ? 2 : 1) * static_cast<size_t>(c.kp) * NB * e;
 }
 
-static size_t workspace_bytes(int dtype, const Cfg& c, bool backward) {
+// Counters and exchange slots of the scan kernels (cleared before every scan).
+static size_t scan_bytes(int dtype, const Cfg& c, bool backward) {
   return xchg_offset(c.nbg) + static_cast<size_t>(c.nbg) * 2 * slot_bytes(dtype, c, backward);
+}
+
+static size_t align4k(size_t x) { return (x + 4095) / 4096 * 4096; }
+
+// One-step forward scans: y_0 [B][H] in E, then the recurrent products [B][2H] in fp32,
+// after the scan region (B rounded up to whole batch groups).
+static size_t y0_offset(int dtype, const Cfg& c) { return align4k(scan_bytes(dtype, c, false)); }
+static size_t g_offset(int dtype, const Cfg& c, int64_t H) {
+  return y0_offset(dtype, c) +
+         align4k(static_cast<size_t>(c.nbg) * NB * H * (dtype == kBF16 ? 2 : 4));
+}
+
+static size_t workspace_bytes(int dtype, const Cfg& c, bool backward, int64_t H) {
+  if (backward) return scan_bytes(dtype, c, true);
+  return g_offset(dtype, c, H) + static_cast<size_t>(c.nbg) * NB * 2 * H * 4;
 }
 
 template <typename K, typename A>
@@ -1272,31 +1329,35 @@ static int launch_slabs(K kernel, int threads, const Cfg& c, const A& args, hipS
 #define DABSN_CORE_CASES_F32(X) \
   X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(8, 16, 4) X(8, 32, 4) X(8, 64, 4)
 
-template <typename K, typename A>
-static int launch_plain(K kernel, int grid, int threads, const A& args, hipStream_t stream) {
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, stream, args);
+// One-step scans: y_0, the recurrent products as one GEMM (128 x 128 tiles: a few hundred
+// batch rows give tens of workgroups), the step.
+template <typename E>
+static int launch_one_step(const Cfg& c, const FwdArgs<E>& args, hipStream_t stream) {
+  const int dtype = is_bf16<E>::value ? kBF16 : kF32;
+  const int64_t H = args.H, n = static_cast<int64_t>(args.B) * H;
+  E* y0 = reinterpret_cast<E*>(args.ws + y0_offset(dtype, c));
+  float* G = reinterpret_cast<float*>(args.ws + g_offset(dtype, c, H));
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  hipLaunchKernelGGL(y0_kernel<E>, grid, dim3(256), 0, stream, args, y0);
+  DABSN_HIP_CHECK(hipGetLastError());
+  gemm::Args<E, float> g{};
+  g.M = args.B; g.N = static_cast<int>(2 * H); g.K = static_cast<int>(H);
+  g.A = y0; g.lda = H; g.sA = n;
+  g.B = args.GA; g.ldb = H; g.sB = 2 * H * H;
+  g.C = G; g.ldc = 2 * H; g.sC = 2 * n;
+  g.alpha = 1.0f;
+  DABSN_HIP_CHECK((gemm::launch_shape<E, float, 128, 128, 2, 2>(g, 1, stream)));
+  hipLaunchKernelGGL(step1_kernel<E>, grid, dim3(256), 0, stream, args, G);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
 
-// One-step scans: y_0 into every group's slot, then the scan without waits.
-template <typename K, typename E>
-static int launch_one_step(K kernel, int threads, const Cfg& c, const FwdArgs<E>& args,
-                           hipStream_t stream) {
-  const int64_t n = static_cast<int64_t>(args.B) * args.H;
-  hipLaunchKernelGGL(publish_y0_kernel<E>, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
-                     0, stream, args, c.nbg);
-  DABSN_HIP_CHECK(hipGetLastError());
-  return launch_plain(kernel, c.nct * c.nbg, threads, args, stream);
-}
-
 template <typename E>
 static int fwd_dispatch(const Cfg& c, const FwdArgs<E>& args, hipStream_t stream) {
+  if (args.T == 1) return launch_one_step(c, args, stream);
 #define DABSN_CASE(CHV, KS, NWV)                                                           \
   if (c.ch == CHV && c.ksteps == KS && c.nw == NWV)                                        \
-    return args.T == 1                                                                     \
-               ? launch_one_step(core_fwd1_kernel<E, CHV, KS, NWV>, NWV * 64, c, args, stream) \
-               : launch_slabs(core_fwd_kernel<E, CHV, KS, NWV>, NWV * 64, c, args, stream);
+    return launch_slabs(core_fwd_kernel<E, CHV, KS, NWV>, NWV * 64, c, args, stream);
   if constexpr (is_bf16<E>::value) {
     DABSN_CORE_CASES_BF16(DABSN_CASE)
   } else {
@@ -1393,7 +1454,7 @@ static int check_common(int dtype, int64_t B, int64_t T, int64_t H, const dabsn_
 static int check_fwd(const dabsn_core_fwd_call& f, Cfg& c) {
   c = pick(f.dtype, f.B, f.H);
   const int rc = check_common(f.dtype, f.B, f.T, f.H, f.params, c, f.workspace_bytes,
-                              c.ksteps ? workspace_bytes(f.dtype, c, false) : 0);
+                              c.ksteps ? workspace_bytes(f.dtype, c, false, f.H) : 0);
   if (rc != DABSN_OK) return rc;
   DABSN_REQUIRE(f.ldt == 0 || (f.ldt >= f.T && f.B * f.ldt * 2 * f.H < (1ll << 46)),
                 "core scan: bad time stride ldt=%lld for T=%lld", (long long)f.ldt,
@@ -1421,7 +1482,7 @@ static int check_fwd(const dabsn_core_fwd_call& f, Cfg& c) {
 static int check_bwd(const dabsn_core_bwd_call& b, Cfg& c) {
   c = pick(b.dtype, b.B, b.H);
   const int rc = check_common(b.dtype, b.B, b.T, b.H, b.params, c, b.workspace_bytes,
-                              c.ksteps ? workspace_bytes(b.dtype, c, true) : 0);
+                              c.ksteps ? workspace_bytes(b.dtype, c, true, b.H) : 0);
   if (rc != DABSN_OK) return rc;
   DABSN_REQUIRE(b.ldt == 0 || (b.ldt >= b.T && b.B * b.ldt * 2 * b.H < (1ll << 46)),
                 "core scan backward: bad time stride ldt=%lld for T=%lld", (long long)b.ldt,
@@ -1452,13 +1513,14 @@ static int check_bwd(const dabsn_core_bwd_call& b, Cfg& c) {
 static int prepare_fwd(const dabsn_core_fwd_call& f, Cfg& c, hipStream_t stream) {
   const int rc = check_fwd(f, c);
   if (rc != DABSN_OK) return rc;
-  return dabsn_hip_zero(f.workspace, workspace_bytes(f.dtype, c, false), stream);
+  if (f.T == 1) return DABSN_OK;  // no counters or exchange; y0_kernel clears the error word
+  return dabsn_hip_zero(f.workspace, scan_bytes(f.dtype, c, false), stream);
 }
 
 static int prepare_bwd(const dabsn_core_bwd_call& b, Cfg& c, hipStream_t stream) {
   const int rc = check_bwd(b, c);
   if (rc != DABSN_OK) return rc;
-  return dabsn_hip_zero(b.workspace, workspace_bytes(b.dtype, c, true), stream);
+  return dabsn_hip_zero(b.workspace, scan_bytes(b.dtype, c, true), stream);
 }
 
 template <typename E>
@@ -1500,7 +1562,7 @@ extern "C" {
 size_t dabsn_hip_core_scan_workspace_bytes(int dtype, int64_t B, int64_t H, int backward) {
   const Cfg c = pick(dtype, B, H);
   if (c.ksteps == 0) return 0;
-  return workspace_bytes(dtype, c, backward != 0);
+  return workspace_bytes(dtype, c, backward != 0, H);
 }
 
 int dabsn_hip_core_scan_layout(int dtype, int64_t B, int64_t H, int64_t* nbg, int64_t* nwg) {
@@ -1594,9 +1656,9 @@ int dabsn_hip_core_scan_pair(const dabsn_core_fwd_call* f, const dabsn_core_bwd_
       return DABSN_ERR_UNSUPPORTED;
     }
   }
-  rc = dabsn_hip_zero(f->workspace, workspace_bytes(f->dtype, c, false), stream);
+  rc = dabsn_hip_zero(f->workspace, scan_bytes(f->dtype, c, false), stream);
   if (rc != DABSN_OK) return rc;
-  rc = dabsn_hip_zero(b->workspace, workspace_bytes(b->dtype, c, true), stream);
+  rc = dabsn_hip_zero(b->workspace, scan_bytes(b->dtype, c, true), stream);
   if (rc != DABSN_OK) return rc;
   if (f->dtype == kBF16)
     return pair_dispatch(c, fwd_args<bf16>(*f, c), bwd_args<bf16>(*b, c), grid, grid, stream);
