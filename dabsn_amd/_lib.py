@@ -104,6 +104,13 @@ _SIGNATURES = {
         i32,
     ),
     "dabsn_hip_read3_decode_workspace_bytes": ([i32, i64, i64, i64, i64], sz),
+    "dabsn_hip_permanent_scan_fwd": ([i64, i64, i64, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_permanent_scan_workspace_bytes": ([i64, i64, i64], sz),
+    "dabsn_hip_permanent_scan_bwd": ([i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
+    "dabsn_hip_local_field_workspace_bytes": ([i64, i64, i64, i32], sz),
+    "dabsn_hip_local_field_gather": ([i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, sz, vp], i32),
+    "dabsn_hip_local_field_gather_bwd": (
+        [i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_read3_decode": (
         [i32, i64, i64, i64, i64, vp, vp, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, PTR4,
          vp, vp, sz, vp],

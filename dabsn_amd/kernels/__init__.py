@@ -14,6 +14,8 @@ from __future__ import annotations
 from dataclasses import asdict, dataclass
 
 import torch
+import torch.nn.functional as F
+from torch import Tensor
 
 from .. import _lib
 from . import ops
@@ -24,8 +26,10 @@ from .ops import (
     check_errors,
     core_scan_batched,
     linear_recurrence,
+    local_field_gather_backward,
     long_scan_fused,
     normalize_rows,
+    permanent_delta_scan,
     read_tape_stats,
 )
 
@@ -60,7 +64,40 @@ PRIMITIVES = (
     Primitive("admitted_selection", "DABSNRead._unified_forward (read.py:185-239)",
               "HIP cummax/stable-partition kernel", "none (integer)", ("seq",),
               "bit-exact against the oracle stable partition"),
+    Primitive("permanent_delta_read", "permanent_delta_scan",
+              "HIP delta scan: one wave per value row, state row in registers",
+              "HIP state-tape recompute + reverse adjoint, deterministic row sums", ("seq",),
+              "oracle (cpu_runtime.cpp:1075-1188 restatement) forward/backward parity"),
+    Primitive("local_field_gather", "inputs[:, patch]", "HIP 16-byte row gather",
+              "HIP inverse-index scatter-add in the reference loop's order", ("field", "hybrid"),
+              "bit-exact against the oracle gather/scatter"),
 )
+
+_PRIMITIVE_HITS = {"permanent_delta_scan": 0, "local_field_gather": 0}
+
+
+def permanent_delta_read(expression: Tensor, long_state: Tensor, progress: Tensor,
+                         plasticity: Tensor, energy: Tensor, saturation: Tensor, *,
+                         phase_gain: Tensor, progress_gain: Tensor, beta_gain: Tensor,
+                         consolidation_energy_gain: Tensor,
+                         consolidation_saturation_gain: Tensor, beta_bias: Tensor) -> Tensor:
+    """Permanent read (reference permanent.py:457-484): keys are the normalised
+    expression shifted by the long state and progress, the write strength is a sigmoid of
+    the mean plasticity, energy and saturation, and the scan runs on the HIP kernel."""
+    key = F.normalize(expression + phase_gain * long_state + progress_gain * progress, dim=-1)
+    beta = torch.sigmoid(beta_gain * plasticity.mean(dim=-1)
+                         + consolidation_energy_gain * energy.mean(dim=-1)
+                         + consolidation_saturation_gain * saturation.mean(dim=-1) + beta_bias)
+    _PRIMITIVE_HITS["permanent_delta_scan"] += 1
+    return permanent_delta_scan(key, expression, beta)
+
+
+def local_field_gather(inputs: Tensor, patch: Tensor) -> tuple[Tensor, str]:
+    """``inputs[:, patch]`` with the route label the reference's helper returns
+    (local_field.py:257-274)."""
+    _PRIMITIVE_HITS["local_field_gather"] += 1
+    return ops.local_field_gather(inputs, patch), "rocm_hip_patch_gather_then_shared_core"
+
 
 
 def primitive_map() -> list[dict[str, object]]:
@@ -110,6 +147,8 @@ def status() -> dict[str, object]:
             "abi_version": _lib.ABI_VERSION,
             "operators": list(ops.OPERATORS),
         },
+        "permanent": {"hip_available": lib_ok, "hits": _PRIMITIVE_HITS["permanent_delta_scan"]},
+        "local_field": {"hip_available": lib_ok, "hits": _PRIMITIVE_HITS["local_field_gather"]},
         "primitives": primitive_map(),
     }
 
@@ -124,8 +163,12 @@ __all__ = [
     "core_scan_batched",
     "enable",
     "linear_recurrence",
+    "local_field_gather",
+    "local_field_gather_backward",
     "long_scan_fused",
     "normalize_rows",
+    "permanent_delta_read",
+    "permanent_delta_scan",
     "primitive_map",
     "read_tape_stats",
     "status",

@@ -8,6 +8,10 @@ written against the reference see the same boundary:
                                               backward (its autograd is a Python loop,
                                               batched_runtime.py:1589-1634)
   dabsn::linear_recurrence / _linrec_backward long.py:392-437
+  dabsn::permanent_delta_scan and its backward op
+                                              permanent.py:384-433
+  dabsn::local_field_gather and its backward op
+                                              local_field.py:208-244
   dabsn::admitted_three_way_read_compact_flash and its backward op
                                               compact_flash.py:71-107, 181-224
 plus fused operators for the rest of the read (long-memory scan, tape statistics,
@@ -56,14 +60,15 @@ def _sync_mode() -> str:
     return os.environ.get("DABSN_HIP_ERROR_CHECK", "sync")
 
 
-def _record_error_word(ws: Tensor, what: str) -> None:
+def _record_error_word(ws: Tensor, what: str, meaning: str | None = None) -> None:
     word = ws[:4].view(torch.int32)
     if _sync_mode() == "sync":
         value = int(word.item())
         if value != 0:
             raise RuntimeError(
-                f"DABSN HIP {what}: a device-wide step barrier timed out (error word {value});"
-                " the workgroups of the persistent scan were not all co-resident"
+                f"DABSN HIP {what}: "
+                + (meaning or "a device-wide step barrier timed out; the workgroups of the "
+                   "persistent scan were not all co-resident") + f" (error word {value})"
             )
         return
     dev = ws.device.index or 0
@@ -75,12 +80,13 @@ def _record_error_word(ws: Tensor, what: str) -> None:
 
 
 def check_errors() -> None:
-    """Raise if any persistent kernel launched in deferred-check mode reported an error."""
+    """Raise if any kernel launched in deferred-check mode reported an error (a persistent
+    scan's barrier timeout, or an out-of-range local-field patch index)."""
     for dev, sticky in _STICKY.items():
         value = int(sticky.item())
         if value != 0:
             sticky.zero_()
-            raise RuntimeError(f"DABSN HIP persistent scan on cuda:{dev} reported error word {value}")
+            raise RuntimeError(f"DABSN HIP kernel on cuda:{dev} reported error word {value}")
 
 
 class KernelTimer:
@@ -376,6 +382,171 @@ def _linrec_bwd(ctx, grad_out):
 
 
 torch.library.register_autograd("dabsn::linear_recurrence", _linrec_bwd, setup_context=_linrec_setup)
+
+
+# ---------------------------------------------------------------------------
+# Permanent associative delta scan (drop-in for dabsn::permanent_delta_scan)
+# ---------------------------------------------------------------------------
+def _permanent_shapes(k: Tensor, v: Tensor, beta: Tensor) -> tuple[int, int, int]:
+    if k.dim() != 3 or v.shape != k.shape or beta.shape != k.shape[:2]:
+        raise ValueError("expected k/v [B,T,H] and beta [B,T]")
+    return tuple(int(x) for x in k.shape)
+
+
+@torch.library.custom_op("dabsn::permanent_delta_scan", mutates_args=(), device_types="cuda")
+def permanent_delta_scan(k: Tensor, v: Tensor, beta: Tensor) -> Tensor:
+    """out_t = S k_t, S += beta_t (v_t - out_t) k_t^T from S = 0 (reference permanent.py:39-51,
+    op 384-397; CPU cpu_runtime.cpp:1075-1109). fp32 state and arithmetic; the output takes
+    v's dtype."""
+    _require_cuda(k)
+    B, T, H = _permanent_shapes(k, v, beta)
+    lib = _lib.load()
+    kf, vf, bf = (x.float().contiguous() for x in (k, v, beta))
+    out = torch.empty((B, T, H), device=k.device, dtype=torch.float32)
+    tk = KernelTimer.begin("permanent_scan_fwd", k)
+    _lib.check(lib.dabsn_hip_permanent_scan_fwd(B, T, H, _p(kf), _p(vf), _p(bf), _p(out),
+                                                _stream(k)), "permanent scan")
+    KernelTimer.end(tk)
+    return out.to(v.dtype)
+
+
+@permanent_delta_scan.register_fake
+def _permanent_delta_scan_fake(k, v, beta):
+    _permanent_shapes(k, v, beta)
+    return torch.empty_like(v)
+
+
+@torch.library.custom_op("dabsn::_permanent_delta_scan_backward", mutates_args=(),
+                         device_types="cuda")
+def permanent_delta_scan_backward(k: Tensor, v: Tensor, beta: Tensor,
+                                  grad_out: Tensor) -> list[Tensor]:
+    """Analytic reverse of the delta scan (reference permanent.py:70-119, 403-426; CPU
+    cpu_runtime.cpp:1112-1188): (dk, dv, dbeta) in the inputs' dtypes."""
+    _require_cuda(k)
+    B, T, H = _permanent_shapes(k, v, beta)
+    lib = _lib.load()
+    kf, vf, bf, gf = (x.float().contiguous() for x in (k, v, beta, grad_out))
+    dk, dv = torch.empty_like(kf), torch.empty_like(vf)
+    db = torch.empty_like(bf)
+    nbytes = lib.dabsn_hip_permanent_scan_workspace_bytes(B, T, H)
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=k.device)
+    tk = KernelTimer.begin("permanent_scan_bwd", k)
+    _lib.check(lib.dabsn_hip_permanent_scan_bwd(B, T, H, _p(kf), _p(vf), _p(bf), _p(gf), _p(dk),
+                                                _p(dv), _p(db), _p(ws), nbytes, _stream(k)),
+               "permanent scan backward")
+    KernelTimer.end(tk)
+    return [dk.to(k.dtype), dv.to(v.dtype), db.to(beta.dtype)]
+
+
+@permanent_delta_scan_backward.register_fake
+def _permanent_delta_scan_backward_fake(k, v, beta, grad_out):
+    return [torch.empty_like(k), torch.empty_like(v), torch.empty_like(beta)]
+
+
+def _permanent_setup(ctx, inputs, output):
+    ctx.save_for_backward(*inputs)
+
+
+def _permanent_bwd(ctx, grad_out):
+    k, v, beta = ctx.saved_tensors
+    dk, dv, db = permanent_delta_scan_backward(k, v, beta, grad_out.contiguous())
+    return dk, dv, db
+
+
+torch.library.register_autograd("dabsn::permanent_delta_scan", _permanent_bwd,
+                                setup_context=_permanent_setup)
+
+
+# ---------------------------------------------------------------------------
+# Local field patch gather (drop-in for dabsn::local_field_gather)
+# ---------------------------------------------------------------------------
+_FIELD_INDEX_ERROR = "a patch index lies outside [0, N)"
+
+
+def _field_shapes(inputs: Tensor, patch: Tensor) -> tuple[int, int, int, int, int]:
+    if inputs.dim() != 3 or patch.dim() != 2:
+        raise ValueError("expected inputs [B,N,D] and patch [N,K]")
+    B, N, D = (int(x) for x in inputs.shape)
+    P, K = (int(x) for x in patch.shape)
+    return B, N, D, P, K
+
+
+def _field_dtype(t: Tensor) -> torch.dtype:
+    """Storage dtype of the HIP kernels for t: fp32 and bf16 natively, fp16 through fp32."""
+    if t.dtype in (torch.float32, torch.bfloat16):
+        return t.dtype
+    if t.dtype == torch.float16:
+        return torch.float32
+    raise TypeError(f"local field gather on the HIP path supports fp32/bf16/fp16, not {t.dtype}")
+
+
+@torch.library.custom_op("dabsn::local_field_gather", mutates_args=(), device_types="cuda")
+def local_field_gather(inputs: Tensor, patch: Tensor) -> Tensor:
+    """inputs[:, patch] -> [B, P, K, D] (reference local_field.py:208-214; CPU
+    cpu_runtime.cpp:1191-1211)."""
+    _require_cuda(inputs)
+    B, N, D, P, K = _field_shapes(inputs, patch)
+    lib = _lib.load()
+    dt = _field_dtype(inputs)
+    x = inputs.to(dt).contiguous()
+    idx = patch.to(device=inputs.device, dtype=torch.int64).contiguous()
+    out = torch.empty((B, P, K, D), device=inputs.device, dtype=dt)
+    nbytes = lib.dabsn_hip_local_field_workspace_bytes(N, P, K, 0)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=inputs.device)
+    _lib.check(lib.dabsn_hip_local_field_gather(_code(dt), B, N, D, P, K, _p(x), _p(idx), _p(out),
+                                                _p(ws), nbytes, _stream(inputs)),
+               "local field gather")
+    _record_error_word(ws, "local field gather", _FIELD_INDEX_ERROR)
+    return out.to(inputs.dtype)
+
+
+@local_field_gather.register_fake
+def _local_field_gather_fake(inputs, patch):
+    B, N, D, P, K = _field_shapes(inputs, patch)
+    return inputs.new_empty((B, P, K, D))
+
+
+@torch.library.custom_op("dabsn::_local_field_gather_backward", mutates_args=(),
+                         device_types="cuda")
+def local_field_gather_backward(grad_out: Tensor, patch: Tensor, cells: int) -> Tensor:
+    """Scatter-add of grad_out [B, P, K, D] into [B, cells, D], each source cell summed over
+    its entries in increasing (p, j) order (reference local_field.py:230-236; CPU
+    cpu_runtime.cpp:1214-1237)."""
+    _require_cuda(grad_out)
+    B, P, K, D = (int(x) for x in grad_out.shape)
+    if tuple(patch.shape) != (P, K):
+        raise ValueError("patch does not match grad_out")
+    lib = _lib.load()
+    dt = _field_dtype(grad_out)
+    g = grad_out.to(dt).contiguous()
+    idx = patch.to(device=grad_out.device, dtype=torch.int64).contiguous()
+    gx = torch.empty((B, cells, D), device=grad_out.device, dtype=dt)
+    nbytes = lib.dabsn_hip_local_field_workspace_bytes(cells, P, K, 1)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=grad_out.device)
+    _lib.check(lib.dabsn_hip_local_field_gather_bwd(_code(dt), B, cells, D, P, K, _p(g), _p(idx),
+                                                    _p(gx), _p(ws), nbytes, _stream(grad_out)),
+               "local field gather backward")
+    _record_error_word(ws, "local field gather backward", _FIELD_INDEX_ERROR)
+    return gx.to(grad_out.dtype)
+
+
+@local_field_gather_backward.register_fake
+def _local_field_gather_backward_fake(grad_out, patch, cells):
+    return grad_out.new_empty((grad_out.shape[0], cells, grad_out.shape[3]))
+
+
+def _field_setup(ctx, inputs, output):
+    values, patch = inputs
+    ctx.save_for_backward(patch)
+    ctx.cells = int(values.shape[1])
+
+
+def _field_bwd(ctx, grad_out):
+    (patch,) = ctx.saved_tensors
+    return local_field_gather_backward(grad_out.contiguous(), patch, ctx.cells), None
+
+
+torch.library.register_autograd("dabsn::local_field_gather", _field_bwd, setup_context=_field_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -878,6 +1049,10 @@ OPERATORS = (
     "dabsn::_core_scan_batched_backward",
     "dabsn::linear_recurrence",
     "dabsn::_linrec_backward",
+    "dabsn::permanent_delta_scan",
+    "dabsn::_permanent_delta_scan_backward",
+    "dabsn::local_field_gather",
+    "dabsn::_local_field_gather_backward",
     "dabsn::long_scan_fused",
     "dabsn::_long_scan_fused_backward",
     "dabsn::read_tape_stats",

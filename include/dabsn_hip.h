@@ -247,7 +247,10 @@ int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
  * read_idx [B, N] int64 the slots' query-relative indices (masks: allow read_idx <= t,
  * induction read_idx < t), valid [B, N] uint8; the other arguments as in
  * dabsn_hip_read3_fwd. K = normalize(write) is rounded to `dtype` as the gather stores
- * it. H % 8 == 0; q, bank and out 16-byte aligned; T * H * sizeof(dtype) <= 64 KiB.
+ * it. H % 8 == 0; q, bank and out 16-byte aligned; T * H * sizeof(dtype) <= 64 KiB;
+ * B * bank_ld < 2^32. One query row (T == 1) with H <= 2048 reads the bank once (online
+ * softmaxes per pathway, the P V products from the exact fp32 weights); otherwise scores,
+ * softmax rows and products run as separate passes with P_V / P_Vn rounded to `dtype`.
  * Inference only: there is no backward. */
 size_t dabsn_hip_read3_decode_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t N,
                                               int64_t H);
@@ -259,6 +262,43 @@ int dabsn_hip_read3_decode(int dtype, int64_t B, int64_t T, int64_t N, int64_t H
                            const float* admission, const float* scale,
                            const float* const* gains, void* out, void* workspace,
                            size_t workspace_bytes, hipStream_t stream);
+
+/* ---- permanent associative delta scan --------------------------------------------
+ * Replaces dabsn::permanent_delta_scan and its registered backward
+ * (src/dabsn/kernels/permanent.py:39-119, 384-433; CPU cpu_runtime.cpp:1075-1188).
+ * key, value [B,T,H], beta [B,T], fp32 (the op converts other dtypes). Per batch row a
+ * state S [H,H] starts at zero; out_t = S k_t, then S += beta_t (v_t - out_t) k_t^T.
+ * H <= 2048. Backward: dkey, dvalue [B,T,H], dbeta [B,T] fp32 from grad_out [B,T,H]; it
+ * recomputes the per-row state trajectory into the workspace
+ * (dabsn_hip_permanent_scan_workspace_bytes(): 4 B T H^2 bytes plus partial sums), as the
+ * reference's reverse pass keeps its state tape. Results are deterministic. */
+int dabsn_hip_permanent_scan_fwd(int64_t B, int64_t T, int64_t H, const float* key,
+                                 const float* value, const float* beta, float* out,
+                                 hipStream_t stream);
+size_t dabsn_hip_permanent_scan_workspace_bytes(int64_t B, int64_t T, int64_t H);
+int dabsn_hip_permanent_scan_bwd(int64_t B, int64_t T, int64_t H, const float* key,
+                                 const float* value, const float* beta, const float* grad_out,
+                                 float* dkey, float* dvalue, float* dbeta, void* workspace,
+                                 size_t workspace_bytes, hipStream_t stream);
+
+/* ---- local field patch gather ----------------------------------------------------
+ * Replaces dabsn::local_field_gather and its registered backward
+ * (src/dabsn/kernels/local_field.py:208-244; CPU cpu_runtime.cpp:1191-1237).
+ * out [B,P,K,D] = x [B,N,D] gathered at patch [P,K] (int64, values in [0, N)). Backward:
+ * grad_x [B,N,D] = scatter-add of grad_out [B,P,K,D], each source summed over its entries
+ * p*K + j in increasing order (the reference CPU loop's order: fp32 results equal it
+ * bit for bit). dtype 0 (fp32) or 1 (bf16; sums in fp32, one rounding). An index
+ * outside [0, N) sets the first workspace word to 1 (its entries give zero) and the call
+ * still returns DABSN_OK; the caller reads the word. Workspace:
+ * dabsn_hip_local_field_workspace_bytes(N, P, K, backward). */
+size_t dabsn_hip_local_field_workspace_bytes(int64_t N, int64_t P, int64_t K, int backward);
+int dabsn_hip_local_field_gather(int dtype, int64_t B, int64_t N, int64_t D, int64_t P,
+                                 int64_t K, const void* x, const int64_t* patch, void* out,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
+int dabsn_hip_local_field_gather_bwd(int dtype, int64_t B, int64_t N, int64_t D, int64_t P,
+                                     int64_t K, const void* grad_out, const int64_t* patch,
+                                     void* grad_x, void* workspace, size_t workspace_bytes,
+                                     hipStream_t stream);
 
 #ifdef __cplusplus
 }

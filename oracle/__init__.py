@@ -18,6 +18,10 @@ Parity pins (what checks this oracle, see ``tests/test_oracle_pins.py``):
     fp64 autograd of the loop at read.py:625-636.
   * bank selection: Python ``sorted`` stable partition (read.py:198-203).
   * tape stats: numpy means/norms (read.py:58-72, 154-183).
+  * permanent delta scan fwd/bwd: fp64 autograd of the reference's einsum loop
+    (permanent.py:39-51), closed forms (T = 1 gives 0; T = 2 gives beta_0 (k_0 . k_1) v_0;
+    beta = 0 gives 0).
+  * local field gather/scatter: numpy fancy indexing and ``np.add.at``.
 The reference ships no golden vectors for this path, and its C++ backend needs
 libtorch to build, so it is not compiled here.
 """
@@ -328,3 +332,51 @@ def _ensure_env():
 
 
 _ensure_env()
+
+
+def permanent_fwd(k, v, beta):
+    """Restates cpu_runtime.cpp:1075-1109 (permanent.py:39-51). Returns out [B,T,H]."""
+    k, v, beta = _f32(k), _f32(v), _f32(beta)
+    B, T, H = k.shape
+    out = np.empty_like(k)
+    lib().oracle_permanent_fwd(ctypes.c_int64(B), ctypes.c_int64(T), ctypes.c_int64(H),
+                               _ptr(k), _ptr(v), _ptr(beta), _ptr(out))
+    return out
+
+
+def permanent_bwd(k, v, beta, g):
+    """Restates cpu_runtime.cpp:1112-1188 (permanent.py:70-119). Returns (dk, dv, dbeta)."""
+    k, v, beta, g = _f32(k), _f32(v), _f32(beta), _f32(g)
+    B, T, H = k.shape
+    dk, dv, db = np.empty_like(k), np.empty_like(v), np.empty_like(beta)
+    lib().oracle_permanent_bwd(ctypes.c_int64(B), ctypes.c_int64(T), ctypes.c_int64(H),
+                               _ptr(k), _ptr(v), _ptr(beta), _ptr(g), _ptr(dk), _ptr(dv), _ptr(db))
+    return dk, dv, db
+
+
+def field_gather(x, patch):
+    """Restates cpu_runtime.cpp:1191-1211: x [B,N,D], patch [P,K] -> [B,P,K,D]."""
+    x = _f32(x)
+    patch = np.ascontiguousarray(np.asarray(patch, dtype=np.int64))
+    B, N, D = x.shape
+    P, K = patch.shape
+    if patch.size and (patch.min() < 0 or patch.max() >= N):
+        raise IndexError("patch index outside [0, N)")
+    out = np.empty((B, P, K, D), np.float32)
+    lib().oracle_field_gather(ctypes.c_int64(B), ctypes.c_int64(N), ctypes.c_int64(D),
+                              ctypes.c_int64(P), ctypes.c_int64(K), _ptr(x), _ptr(patch), _ptr(out))
+    return out
+
+
+def field_gather_bwd(gout, patch, cells):
+    """Restates cpu_runtime.cpp:1214-1237: scatter-add of gout [B,P,K,D] -> [B,cells,D]."""
+    gout = _f32(gout)
+    patch = np.ascontiguousarray(np.asarray(patch, dtype=np.int64))
+    B, P, K, D = gout.shape
+    if patch.size and (patch.min() < 0 or patch.max() >= cells):
+        raise IndexError("patch index outside [0, N)")
+    gx = np.empty((B, cells, D), np.float32)
+    lib().oracle_field_gather_bwd(ctypes.c_int64(B), ctypes.c_int64(cells), ctypes.c_int64(D),
+                                  ctypes.c_int64(P), ctypes.c_int64(K), _ptr(gout), _ptr(patch),
+                                  _ptr(gx))
+    return gx

@@ -121,3 +121,16 @@ def linrec_loop(a, g, y0):
         y = a[:, i] * y + g[:, i]
         outs.append(y)
     return torch.stack(outs, dim=1)
+
+
+def permanent_loop(k, v, beta):
+    """permanent.py:39-51: S = 0; per step out = S k, S += beta (v - out) k^T."""
+    B, T, H = k.shape
+    S = torch.zeros(B, H, H, dtype=k.dtype)
+    outs = []
+    for t in range(T):
+        kt = k[:, t]
+        r = torch.matmul(S, kt.unsqueeze(-1)).squeeze(-1)
+        outs.append(r)
+        S = S + (beta[:, t, None] * (v[:, t] - r)).unsqueeze(-1) * kt.unsqueeze(1)
+    return torch.stack(outs, dim=1)

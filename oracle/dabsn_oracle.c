@@ -26,6 +26,8 @@
  *   oracle_tape_stats      read.py:58-72, 154-183 (means over H, norms, key bias,
  *                          admission, cocktail).
  *   oracle_bank_select     read.py:185-239 (cummax floor, member, stable partition).
+ *   oracle_permanent_fwd/bwd  cpu_runtime.cpp:1075-1188 (delta scan and its reverse).
+ *   oracle_field_gather/_bwd  cpu_runtime.cpp:1191-1237 (patch gather, scatter-add).
  *
  * Deliberate deviation: cpu_runtime.cpp:381 and :571 skip a pathway whose gain is
  * exactly 0, which also zeroes that gain's gradient. The read's math oracle
@@ -763,4 +765,121 @@ void oracle_bank_select(int64_t B, int64_t T, const float* adm, float window, in
       else o[npos++] = t;
     }
   }
+}
+
+/* ---------------------------------------------------------------------------
+ * Permanent associative delta scan (cpu_runtime.cpp:1075-1109; definition
+ * permanent.py:39-51). Per batch row: S [H][H] = 0; for each step the output row
+ * is S k (serial dot over the key index), then every value row moves by
+ * beta * (v - out) along k.
+ * ------------------------------------------------------------------------- */
+void oracle_permanent_fwd(int64_t B, int64_t T, int64_t H, const float* k, const float* v,
+                          const float* beta, float* out) {
+  int64_t bi;
+#pragma omp parallel for schedule(static)
+  for (bi = 0; bi < B; ++bi) {
+    float* S = (float*)calloc((size_t)(H * H), sizeof(float));
+    for (int64_t t = 0; t < T; ++t) {
+      const float* kt = k + (bi * T + t) * H;
+      const float* vt = v + (bi * T + t) * H;
+      float* rt = out + (bi * T + t) * H;
+      for (int64_t i = 0; i < H; ++i) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < H; ++j) acc += S[i * H + j] * kt[j];
+        rt[i] = acc;
+      }
+      const float bt = beta[bi * T + t];
+      for (int64_t i = 0; i < H; ++i) {
+        const float step = bt * (vt[i] - rt[i]);
+        for (int64_t j = 0; j < H; ++j) S[i * H + j] += step * kt[j];
+      }
+    }
+    free(S);
+  }
+}
+
+/* Reverse of the delta scan (cpu_runtime.cpp:1112-1188; permanent.py:70-119). The states
+ * before each step are kept (T H^2 floats per batch row), then the adjoint A = dL/dS walks
+ * back: Ak = A k, dv = beta Ak, dbeta = sum_i Ak_i (v_i - r_i), dk_j = sum_i (S_ij g_i +
+ * beta A_ij v_i - beta S_ij Ak_i - beta A_ij r_i), A += g k^T - beta Ak k^T. */
+void oracle_permanent_bwd(int64_t B, int64_t T, int64_t H, const float* k, const float* v,
+                          const float* beta, const float* g, float* dk, float* dv, float* db) {
+  int64_t bi;
+#pragma omp parallel for schedule(static)
+  for (bi = 0; bi < B; ++bi) {
+    const size_t HH = (size_t)(H * H);
+    float* tape = (float*)malloc(sizeof(float) * (size_t)T * HH);
+    float* r = (float*)malloc(sizeof(float) * (size_t)(T * H));
+    float* S = (float*)calloc(HH, sizeof(float));
+    float* A = (float*)calloc(HH, sizeof(float));
+    float* ak = (float*)malloc(sizeof(float) * (size_t)H);
+    for (int64_t t = 0; t < T; ++t) {
+      const float* kt = k + (bi * T + t) * H;
+      const float* vt = v + (bi * T + t) * H;
+      memcpy(tape + (size_t)t * HH, S, sizeof(float) * HH);
+      for (int64_t i = 0; i < H; ++i) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < H; ++j) acc += S[i * H + j] * kt[j];
+        r[t * H + i] = acc;
+      }
+      const float bt = beta[bi * T + t];
+      for (int64_t i = 0; i < H; ++i) {
+        const float step = bt * (vt[i] - r[t * H + i]);
+        for (int64_t j = 0; j < H; ++j) S[i * H + j] += step * kt[j];
+      }
+    }
+    for (int64_t t = T - 1; t >= 0; --t) {
+      const float* kt = k + (bi * T + t) * H;
+      const float* vt = v + (bi * T + t) * H;
+      const float* gt = g + (bi * T + t) * H;
+      const float* St = tape + (size_t)t * HH;
+      const float* rt = r + t * H;
+      const float bt = beta[bi * T + t];
+      float dbt = 0.0f;
+      for (int64_t i = 0; i < H; ++i) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < H; ++j) acc += A[i * H + j] * kt[j];
+        ak[i] = acc;
+        dv[(bi * T + t) * H + i] = bt * acc;
+        dbt += acc * (vt[i] - rt[i]);
+      }
+      db[bi * T + t] = dbt;
+      for (int64_t j = 0; j < H; ++j) {
+        float acc = 0.0f;
+        for (int64_t i = 0; i < H; ++i) {
+          acc += St[i * H + j] * gt[i];
+          acc += bt * A[i * H + j] * vt[i];
+          acc -= bt * St[i * H + j] * ak[i];
+          acc -= bt * A[i * H + j] * rt[i];
+        }
+        dk[(bi * T + t) * H + j] = acc;
+      }
+      for (int64_t i = 0; i < H; ++i)
+        for (int64_t j = 0; j < H; ++j)
+          A[i * H + j] = gt[i] * kt[j] + A[i * H + j] - bt * ak[i] * kt[j];
+    }
+    free(tape); free(r); free(S); free(A); free(ak);
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * Local field patch gather (cpu_runtime.cpp:1191-1237): out[b,p,j,:] = x[b,patch[p,j],:];
+ * the backward adds grad rows back to their source cells, visiting (p, j) in order.
+ * ------------------------------------------------------------------------- */
+void oracle_field_gather(int64_t B, int64_t N, int64_t D, int64_t P, int64_t K, const float* x,
+                         const int64_t* patch, float* out) {
+  for (int64_t bi = 0; bi < B; ++bi)
+    for (int64_t e = 0; e < P * K; ++e)
+      memcpy(out + (bi * P * K + e) * D, x + (bi * N + patch[e]) * D, sizeof(float) * (size_t)D);
+}
+
+void oracle_field_gather_bwd(int64_t B, int64_t N, int64_t D, int64_t P, int64_t K,
+                             const float* gout, const int64_t* patch, float* gx) {
+  memset(gx, 0, sizeof(float) * (size_t)(B * N * D));
+  for (int64_t bi = 0; bi < B; ++bi)
+    for (int64_t e = 0; e < P * K; ++e) {
+      float* dst = gx + (bi * N + patch[e]) * D;
+      const float* src = gout + (bi * P * K + e) * D;
+      for (int64_t d = 0; d < D; ++d) dst[d] += src[d];
+    }
 }

@@ -178,6 +178,23 @@ def _read_bwd(go, query, K, V, Vn, ck, cb, kb, adm, scale, idx, valid, mode, sg,
     return tuple(out)
 
 
+def _permanent(k, v, beta):
+    return _t(oracle.permanent_fwd(_np(k), _np(v), _np(beta)), v.dtype)
+
+
+def _permanent_bwd(k, v, beta, g):
+    dk, dv, db = oracle.permanent_bwd(_np(k), _np(v), _np(beta), _np(g))
+    return [_t(dk, k.dtype), _t(dv, v.dtype), _t(db, beta.dtype)]
+
+
+def _field(inputs, patch):
+    return _t(oracle.field_gather(_np(inputs), patch.cpu().numpy()), inputs.dtype)
+
+
+def _field_bwd(grad_out, patch, cells):
+    return _t(oracle.field_gather_bwd(_np(grad_out), patch.cpu().numpy(), cells), grad_out.dtype)
+
+
 def register() -> None:
     """Attach the oracle as the CPU kernel of every dabsn:: operator (idempotent)."""
     global _DONE
@@ -198,4 +215,8 @@ def register() -> None:
     ops.bank_gather_backward.register_kernel("cpu")(_gather_bwd)
     ops.admitted_three_way_read_compact_flash.register_kernel("cpu")(_read)
     ops.admitted_three_way_read_compact_flash_backward.register_kernel("cpu")(_read_bwd)
+    ops.permanent_delta_scan.register_kernel("cpu")(_permanent)
+    ops.permanent_delta_scan_backward.register_kernel("cpu")(_permanent_bwd)
+    ops.local_field_gather.register_kernel("cpu")(_field)
+    ops.local_field_gather_backward.register_kernel("cpu")(_field_bwd)
     _DONE = True

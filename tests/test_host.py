@@ -101,6 +101,8 @@ def test_cpu_tensors_raise_instead_of_falling_back():
         "expect_fail(ops.linear_recurrence, x, x, torch.zeros(B, H))\n"
         "expect_fail(ops.bank_select, torch.randn(B, T), torch.tensor([1.0]))\n"
         "expect_fail(ops.read_tape_stats, *[x] * 6)\n"
+        "expect_fail(ops.permanent_delta_scan, x, x, torch.rand(B, T))\n"
+        "expect_fail(ops.local_field_gather, x, torch.zeros(T, 2, dtype=torch.long))\n"
         "print('ok')\n")
     r = _run(code)
     assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr

@@ -330,3 +330,62 @@ def test_tape_stats_match_numpy():
     ck = np.stack([me, mc, mn, mp], -1)
     ck = ck / np.maximum(np.linalg.norm(ck, axis=-1, keepdims=True), 1e-12)
     _close(st["cocktail"], ck, 1e-5, 1e-7, "cocktail")
+
+
+def _permanent_case(seed, B, T, H, unit_keys=False):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(B, T, H, generator=g)
+    if unit_keys:
+        k = k / k.norm(dim=-1, keepdim=True)
+    v = torch.randn(B, T, H, generator=g)
+    beta = torch.sigmoid(torch.randn(B, T, generator=g))
+    return k, v, beta
+
+
+@pytest.mark.parametrize("seed,B,T,H,unit", [(81, 2, 7, 6, False), (82, 3, 12, 9, True),
+                                             (83, 1, 1, 4, False)])
+def test_permanent_scan_matches_fp64_loop_and_autograd(seed, B, T, H, unit):
+    """Release-gate shape (2, 7, 6) with raw keys, as in tools/release_gate.py:456-472."""
+    k, v, beta = _permanent_case(seed, B, T, H, unit)
+    want = ar.permanent_loop(k, v, beta)
+    got = oracle.permanent_fwd(_np(k), _np(v), _np(beta))
+    scale = float(want.abs().max()) + 1e-30
+    _close(got, want.numpy(), 1e-5, 1e-6 * scale, "permanent forward")
+    leaves = [x.clone().requires_grad_(True) for x in (k, v, beta)]
+    out = ar.permanent_loop(*leaves)
+    up = torch.randn(out.shape, generator=torch.Generator().manual_seed(seed + 100))
+    grads = torch.autograd.grad((out * up).sum(), leaves, allow_unused=True)  # T = 1: no v, beta
+    grads = [torch.zeros_like(x) if d is None else d for x, d in zip(leaves, grads)]
+    mine = oracle.permanent_bwd(_np(k), _np(v), _np(beta), _np(up))
+    for name, x, y in zip(("dk", "dv", "dbeta"), mine, grads):
+        _close(x, y.numpy(), 1e-4, 1e-5 * (float(y.abs().max()) + 1e-30), name)
+
+
+def test_permanent_scan_closed_forms():
+    """T = 1 reads the empty state (0); the second step reads beta_0 (k_0 . k_1) v_0; with
+    beta = 0 nothing is ever written."""
+    k, v, beta = _permanent_case(84, 3, 2, 5)
+    out = oracle.permanent_fwd(_np(k), _np(v), _np(beta))
+    assert np.all(out[:, 0] == 0.0)
+    want = (beta[:, 0] * (k[:, 0] * k[:, 1]).sum(-1))[:, None] * v[:, 0]
+    _close(out[:, 1], want.numpy(), 1e-6, 1e-7, "second step")
+    k, v, beta = _permanent_case(85, 2, 6, 4)
+    assert np.all(oracle.permanent_fwd(_np(k), _np(v), _np(beta * 0.0)) == 0.0)
+
+
+def test_field_gather_and_scatter_match_numpy():
+    """Release-gate patch (tools/release_gate.py:474-493: 9 cells, neighbours n, n+1, n+3)
+    and a random patch with more rows than cells; the scatter is np.add.at, which adds in
+    index order, so fp32 results agree exactly."""
+    g = np.random.default_rng(86)
+    gate = np.array([[n, (n + 1) % 9, (n + 3) % 9] for n in range(9)], np.int64)
+    for B, N, D, patch in ((2, 9, 6, gate), (3, 7, 5, g.integers(0, 7, size=(11, 4)))):
+        x = g.standard_normal((B, N, D)).astype(np.float32)
+        assert np.array_equal(oracle.field_gather(x, patch), x[:, patch])
+        gout = g.standard_normal((B,) + patch.shape + (D,)).astype(np.float32)
+        want = np.zeros((B, N, D), np.float32)
+        for b in range(B):
+            np.add.at(want[b], patch.reshape(-1), gout[b].reshape(-1, D))
+        assert np.array_equal(oracle.field_gather_bwd(gout, patch, N), want)
+    with pytest.raises(IndexError):
+        oracle.field_gather(np.zeros((1, 3, 2), np.float32), np.array([[3]]))

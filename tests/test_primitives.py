@@ -1,0 +1,171 @@
+"""The two standalone primitives of the reference's PRIMITIVES table that sit outside the
+model path: dabsn::permanent_delta_scan (permanent.py:384-433) and dabsn::local_field_gather
+(local_field.py:208-244). CPU tests check the registered boundary through the oracle's CPU
+kernels (schema, fake tensors, autograd registration, as the reference's own
+tests/test_native_scan_ops_v2.py:616-686 do with opcheck) and the backend registry; GPU
+tests compare the HIP kernels with the oracle on identical inputs.
+
+Tolerances: permanent scan fp32, normwise relative 1e-5 (forward, dv) and 1e-4 (dk, dbeta:
+sums over H rows per element, summed in another order); bf16 inputs against the oracle on
+the same rounded inputs, Frobenius 1e-2 (outputs and gradients stored in bf16). Local field
+gather and its scatter-add: bit-exact (a copy; sums in the oracle's order).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import dabsn_amd.kernels as K
+import oracle
+from dabsn_amd.kernels import ops
+from helpers import rel_err
+from oracle import torch_backend
+
+
+def _rel_fro(a, b) -> float:
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def _permanent_case(seed, B, T, H, unit_keys=True, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(B, T, H, generator=g)
+    if unit_keys:
+        k = k / k.norm(dim=-1, keepdim=True)
+    v = torch.randn(B, T, H, generator=g)
+    beta = torch.sigmoid(torch.randn(B, T, generator=g))
+    up = torch.randn(B, T, H, generator=g)
+    return k.to(dtype), v.to(dtype), beta.to(dtype), up.to(dtype)
+
+
+GATE_PATCH = torch.tensor([[n, (n + 1) % 9, (n + 3) % 9] for n in range(9)], dtype=torch.long)
+
+
+# ---- CPU: boundary and registry ----------------------------------------------------
+
+def test_registered_ops_pass_opcheck_on_the_oracle_cpu_kernels():
+    torch_backend.register()
+    k, v, beta, _ = _permanent_case(1, 1, 3, 2, unit_keys=False)
+    for x in (k, v, beta):
+        x.requires_grad_(True)
+    res = torch.library.opcheck(torch.ops.dabsn.permanent_delta_scan.default, (k, v, beta))
+    assert all(r == "SUCCESS" for r in res.values()), res
+    x = torch.randn(2, 9, 3, requires_grad=True)
+    res = torch.library.opcheck(torch.ops.dabsn.local_field_gather.default, (x, GATE_PATCH))
+    assert all(r == "SUCCESS" for r in res.values()), res
+
+
+def test_backend_registry_lists_the_primitives():
+    st = K.status()
+    names = {p["name"] for p in st["primitives"]}
+    assert {"permanent_delta_read", "local_field_gather"} <= names
+    assert "permanent" in st and "local_field" in st
+    for op in ("dabsn::permanent_delta_scan", "dabsn::local_field_gather"):
+        assert op in st["rocm"]["operators"]
+
+
+# ---- GPU: HIP against the oracle -----------------------------------------------------
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,T,H,unit", [(2, 7, 6, False), (3, 40, 64, True), (2, 33, 100, True),
+                                        (1, 16, 300, True), (2, 1, 16, True), (1, 6, 2048, True)])
+def test_permanent_scan_matches_oracle(cuda_device, B, T, H, unit):
+    """(2, 7, 6) with raw keys is the reference's release-gate case; unit keys elsewhere
+    keep long scans bounded (|1 - beta| < 1 along k)."""
+    k, v, beta, up = _permanent_case(10 + H + T, B, T, H, unit)
+    want = oracle.permanent_fwd(k.numpy(), v.numpy(), beta.numpy())
+    wdk, wdv, wdb = oracle.permanent_bwd(k.numpy(), v.numpy(), beta.numpy(), up.numpy())
+    leaves = [x.to(cuda_device).requires_grad_(True) for x in (k, v, beta)]
+    out = ops.permanent_delta_scan(*leaves)
+    dk, dv, db = torch.autograd.grad((out * up.to(cuda_device)).sum(), leaves)
+    assert rel_err(out.detach().cpu(), want) <= 1e-5
+    assert rel_err(dv.cpu(), wdv) <= 1e-5
+    assert rel_err(dk.cpu(), wdk) <= 1e-4
+    assert rel_err(db.cpu(), wdb) <= 1e-4
+
+
+@pytest.mark.gpu
+def test_permanent_scan_backward_is_deterministic(cuda_device):
+    k, v, beta, up = (x.to(cuda_device) for x in _permanent_case(3, 2, 24, 200))
+    first = ops.permanent_delta_scan_backward(k, v, beta, up)
+    second = ops.permanent_delta_scan_backward(k, v, beta, up)
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_permanent_scan_bf16_matches_oracle_on_rounded_inputs(cuda_device):
+    k, v, beta, up = _permanent_case(4, 2, 20, 128, dtype=torch.bfloat16)
+    f = [x.float().numpy() for x in (k, v, beta, up)]
+    want = oracle.permanent_fwd(*f[:3])
+    wgrads = oracle.permanent_bwd(*f)
+    kd, vd, bd = (x.to(cuda_device) for x in (k, v, beta))
+    out = ops.permanent_delta_scan(kd, vd, bd)
+    assert out.dtype == torch.bfloat16
+    assert _rel_fro(out.float().cpu(), want) <= 1e-2
+    grads = ops.permanent_delta_scan_backward(kd, vd, bd, up.to(cuda_device))
+    for got, w in zip(grads, wgrads):
+        assert got.dtype == torch.bfloat16
+        assert _rel_fro(got.float().cpu(), w) <= 1e-2
+
+
+@pytest.mark.gpu
+def test_permanent_delta_read_matches_the_same_read_on_the_oracle(cuda_device):
+    torch_backend.register()
+    g = torch.Generator().manual_seed(5)
+    B, T, H = 2, 12, 64
+    ins = [torch.randn(B, T, H, generator=g) for _ in range(6)]
+    gains = {n: torch.tensor(float(x)) for n, x in (
+        ("phase_gain", 0.3), ("progress_gain", -0.2), ("beta_gain", 0.7),
+        ("consolidation_energy_gain", 0.5), ("consolidation_saturation_gain", -0.4),
+        ("beta_bias", 0.1))}
+    cpu = K.permanent_delta_read(*ins, **gains)
+    dev = K.permanent_delta_read(*(x.to(cuda_device) for x in ins),
+                                 **{n: x.to(cuda_device) for n, x in gains.items()})
+    assert rel_err(dev.cpu(), cpu) <= 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,N,D,P,K", [(2, 9, 6, 9, 3), (2, 4096, 64, 4096, 9), (3, 50, 5, 70, 4),
+                                       (1, 17, 8, 0, 3)])
+def test_local_field_gather_and_scatter_are_exact(cuda_device, dtype, B, N, D, P, K):
+    """The release-gate patch (9 cells, neighbours n, n+1, n+3), a 64 x 64 field with
+    3 x 3 neighbourhoods (16-byte row copies), an odd D with more patch rows than cells
+    (element copies), and an empty patch."""
+    g = torch.Generator().manual_seed(N + D)
+    if P == 9 and K == 3:
+        patch = GATE_PATCH
+    else:
+        patch = torch.randint(0, N, (P, K), generator=g)
+    x = torch.randn(B, N, D, generator=g).to(dtype)
+    gout = torch.randn(B, P, K, D, generator=g).to(dtype)
+    xd = x.to(cuda_device).requires_grad_(True)
+    out = ops.local_field_gather(xd, patch.to(cuda_device))
+    assert torch.equal(out.detach().cpu(), x[:, patch])
+    (gx,) = torch.autograd.grad(out, xd, gout.to(cuda_device))
+    want = oracle.field_gather_bwd(gout.float().numpy(), patch.numpy(), N)
+    assert torch.equal(gx.cpu(), torch.from_numpy(want).to(dtype))
+
+
+@pytest.mark.gpu
+def test_local_field_gather_rejects_out_of_range_indices(cuda_device):
+    """An index outside [0, N) is caught on the device (its entries read nothing) and
+    reported through the error word."""
+    x = torch.randn(1, 5, 4, device=cuda_device)
+    for bad in (5, -1):
+        patch = torch.tensor([[0, bad]], device=cuda_device)
+        with pytest.raises(RuntimeError, match="outside"):
+            ops.local_field_gather(x, patch)
+        with pytest.raises(RuntimeError, match="outside"):
+            ops.local_field_gather_backward(torch.ones(1, 1, 2, 4, device=cuda_device), patch, 5)
+
+
+@pytest.mark.gpu
+def test_local_field_helper_reports_its_route(cuda_device):
+    x = torch.randn(2, 9, 6, device=cuda_device)
+    out, route = K.local_field_gather(x, GATE_PATCH.to(cuda_device))
+    assert route == "rocm_hip_patch_gather_then_shared_core"
+    assert torch.equal(out, x[:, GATE_PATCH.to(cuda_device)])
