@@ -44,9 +44,10 @@ def parse():
     p.add_argument("--chunk", type=int, default=1024)
     p.add_argument("--cpu-seq", type=int, default=128, help="T of the bounded CPU sample")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--workload", choices=("train", "decode"), default="train",
+    p.add_argument("--workload", choices=("train", "decode", "primitives"), default="train",
                    help="train: the config-4 headline step (default); decode: config-5 streaming "
-                        "decode through the carried memory")
+                        "decode through the carried memory; primitives: the permanent delta "
+                        "scan and local field gather kernels")
     p.add_argument("--prompt", type=int, default=2048, help="decode: prompt tokens ingested")
     p.add_argument("--layers", type=int, default=4, help="decode: seq layers")
     args = p.parse_args()
@@ -196,7 +197,9 @@ def decode_main(args):
     reserved for the whole run, then each timed step decodes one token per row with
     ``forward_with_memory(extend=True)``: the core steps from the carried state, the read
     scans each layer's bank in place (``dabsn_hip_read3_decode``) and the bank grows by one
-    row. value = B x steps / time."""
+    row. value = B x steps / time. The timed steps run without per-kernel timers (their
+    event records cost host time in a host-bound step); --steps further steps then run with
+    them to measure the kernels."""
     import dabsn_amd
     from dabsn_amd import memory as mem
     from dabsn_amd.kernels import ops
@@ -208,7 +211,8 @@ def decode_main(args):
     torch.manual_seed(0)
     model = dabsn_amd.DABSNSequenceLM(args.vocab, H, [(H, H)] * L, residual=True, mlp_ratio=4.0)
     model = model.to(device).to(torch.bfloat16).eval()
-    total = args.prompt + args.warmup + args.steps
+    meas = min(args.steps, 8)  # steps with per-kernel timers, after the timed ones
+    total = args.prompt + args.warmup + args.steps + meas
     ids = torch.randint(0, args.vocab, (B, total), generator=torch.Generator().manual_seed(1))
     ids = ids.to(device)
     memory = mem.ingest(model, ids[:, :args.prompt], chunk_size=512)
@@ -218,7 +222,6 @@ def decode_main(args):
         _, memory = mem.forward_with_memory(model, ids[:, pos:pos + 1], memory, extend=True)
         pos += 1
     torch.cuda.synchronize()
-    ops.timing(True)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(args.steps):
@@ -227,17 +230,23 @@ def decode_main(args):
     stop.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / args.steps
+    ops.timing(True)
+    for _ in range(meas):
+        _, memory = mem.forward_with_memory(model, ids[:, pos:pos + 1], memory, extend=True)
+        pos += 1
+    torch.cuda.synchronize()
     kernels = ops.KernelTimer.summary()
     ops.timing(False)
     ops.check_errors()
-    n_mean = args.prompt + args.warmup + (args.steps + 1) / 2  # bank rows per layer, mean
+    # bank rows per layer, mean over the measured steps
+    n_mean = args.prompt + args.warmup + args.steps + (meas + 1) / 2
     bank_bytes = B * n_mean * H * 2  # one pass over one layer's bank
     dec = kernels.get("read3_decode")
     roofline = None
     if dec:
-        # The decode read passes over the bank rows of the admitted slots twice (scores, then
-        # the P V output whose successor rows are mostly the next slot's): algorithmic bytes =
-        # one bank pass per launch when every slot is admitted.
+        # One query row per batch row: the single-pass read streams every admitted slot's
+        # write row once (its induction value is the next slot's row, already in registers):
+        # algorithmic bytes = one bank pass per launch when every slot is admitted.
         achieved = bank_bytes / (dec["avg_ms"] / 1e3) / 1e9
         roofline = {"bound": "hbm", "kernel": "read3_decode", "achieved": round(achieved, 2),
                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
@@ -253,10 +262,88 @@ def decode_main(args):
                    "batch": B, "prompt": args.prompt, "layers": L, "state": H,
                    "bank_rows_mean": n_mean},
         "roofline": roofline,
-        "kernel_ms": {k: {"avg": round(v["avg_ms"], 4), "calls_per_step": v["calls"] / args.steps,
-                          "per_step": round(v["total_ms"] / args.steps, 3)}
+        "kernel_ms": {k: {"avg": round(v["avg_ms"], 4), "calls_per_step": v["calls"] / meas,
+                          "per_step": round(v["total_ms"] / meas, 3)}
                       for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["total_ms"])},
     }
+    print(json.dumps(result), flush=True)
+
+
+PRIMITIVES_METRIC = "standalone primitives: permanent delta scan, local field gather"
+FP32_VALU_PEAK_TFLOPS = 78.6  # non-packed fp32 FMA rate (packed fp32 is not used)
+
+
+def primitives_main(args):
+    """The two primitives outside the model path (reference PRIMITIVES, kernels/__init__.py:
+    56-83), at sizes of their own: permanent_delta_scan fwd + bwd at B=16, T=1024, H=256
+    (unit keys), fp32; local_field_gather fwd + bwd on a 256 x 256 torus with 3 x 3
+    neighbourhoods (K = 9), B=8, D=64, fp32. Prints per-kernel averages over --steps and each
+    kernel's roofline: the delta scan against the fp32 VALU rate (algorithmic flops: 4 H^2
+    per (b, t) forward, 14 H^2 backward with its recompute), the gather and its scatter-add
+    against HBM (algorithmic bytes: every gathered element written once and every source
+    element read once; the backward the reverse)."""
+    import dabsn_amd
+    from dabsn_amd.kernels import ops
+
+    dabsn_amd.kernels.enable("rocm", required=True)
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(3)
+    B, T, H = 16, 1024, 256
+    k = torch.randn(B, T, H, generator=g)
+    k = (k / k.norm(dim=-1, keepdim=True)).to(dev)
+    v = torch.randn(B, T, H, generator=g).to(dev)
+    beta = torch.sigmoid(torch.randn(B, T, generator=g)).to(dev)
+    up = torch.randn(B, T, H, generator=g).to(dev)
+    side = 256
+    n = torch.arange(side * side)
+    r, c = n // side, n % side
+    patch = torch.stack([((r + dr) % side) * side + (c + dc) % side
+                         for dr in (-1, 0, 1) for dc in (-1, 0, 1)], dim=1).to(dev)
+    FB, D = 8, 64
+    x = torch.randn(FB, side * side, D, generator=g).to(dev)
+    gout = torch.randn(FB, side * side, 9, D, generator=g).to(dev)
+
+    def run():
+        ops.permanent_delta_scan(k, v, beta)
+        ops.permanent_delta_scan_backward(k, v, beta, up)
+        ops.local_field_gather(x, patch)
+        ops.local_field_gather_backward(gout, patch, side * side)
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    ops.timing(True)
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    kernels = ops.KernelTimer.summary()
+    ops.timing(False)
+    cells = side * side
+    work = {
+        "permanent_scan_fwd": ("valu", 4.0 * B * T * H * H),
+        "permanent_scan_bwd": ("valu", 14.0 * B * T * H * H),
+        "local_field_gather": ("hbm", 4.0 * FB * cells * D * (9 + 1)),
+        "local_field_scatter": ("hbm", 4.0 * FB * cells * D * (9 + 1)),
+    }
+    out = {}
+    for name, (bound, amount) in work.items():
+        avg = kernels[name]["avg_ms"] / 1e3
+        if bound == "hbm":
+            ach = amount / avg / 1e9
+            out[name] = {"avg_ms": round(avg * 1e3, 4), "bound": "hbm", "achieved": round(ach, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "alg_bytes": int(amount)}
+        else:
+            ach = amount / avg / 1e12
+            out[name] = {"avg_ms": round(avg * 1e3, 4), "bound": "fp32 valu",
+                         "achieved": round(ach, 3), "peak": FP32_VALU_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(ach / FP32_VALU_PEAK_TFLOPS, 4),
+                         "alg_flops": int(amount)}
+    result = {"metric": PRIMITIVES_METRIC, "unit": "ms", "n_gpus": 1, "steps": args.steps,
+              "warmup": args.warmup, "dtype": "f32", "data": "synthetic",
+              "config": {"workload": "permanent B=16 T=1024 H=256; local field 256x256 torus, "
+                                     "K=9, B=8, D=64"},
+              "kernels": out}
     print(json.dumps(result), flush=True)
 
 
@@ -274,6 +361,9 @@ def main():
         sys.exit(1)
     if args.workload == "decode":
         decode_main(args)
+        return
+    if args.workload == "primitives":
+        primitives_main(args)
         return
     dabsn_amd.kernels.enable("rocm", required=True)
     os.environ.setdefault("DABSN_HIP_ERROR_CHECK", "deferred")

@@ -23,32 +23,52 @@ constexpr uint32_t kErrIndex = 1u;
 
 __device__ __forceinline__ bool in_range(int64_t s, int N) { return s >= 0 && s < N; }
 
-// Elements copied per thread: V (16 bytes) when every row of D elements is 16-byte aligned.
+// V consecutive elements at p (V = 1, or 16 bytes).
 template <typename E, int V>
-__global__ void __launch_bounds__(256) gather_kernel(int64_t total, int N, int D, int PK,
+struct Vec {
+  E e[V];
+};
+template <typename E, int V>
+__device__ __forceinline__ Vec<E, V> vload(const E* p) {
+  Vec<E, V> r;
+  if constexpr (V * sizeof(E) == 16) {
+    r = __builtin_bit_cast(Vec<E, V>, gload16(p));
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) r.e[v] = p[v];
+  }
+  return r;
+}
+template <typename E, int V>
+__device__ __forceinline__ void vstore(E* p, const Vec<E, V>& r) {
+  if constexpr (V * sizeof(E) == 16) {
+    gstore16(p, __builtin_bit_cast(u32x4, r));
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) p[v] = r.e[v];
+  }
+}
+
+// Grid (vectors of one batch row, B): thread j copies V elements (16 bytes when every row of
+// D elements is 16-byte aligned) of entry e = j / (D / V). 32-bit index math (P K D < 2^31).
+template <typename E, int V>
+__global__ void __launch_bounds__(256) gather_kernel(int N, int D, int PK,
                                                      const E* __restrict__ x,
                                                      const int64_t* __restrict__ patch,
                                                      E* __restrict__ out, uint32_t* err) {
-  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * V;  // element
-  if (i >= total) return;
-  const int d = static_cast<int>(i % D);
-  const int64_t row = i / D;  // (b, e)
-  const int e = static_cast<int>(row % PK);
-  const int64_t b = row / PK;
+  const int b = blockIdx.y;
+  const int dv = D / V;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= PK * dv) return;
+  const int e = j / dv, d = (j - e * dv) * V;
+  E* dst = out + (static_cast<size_t>(b) * PK + e) * D + d;
   const int64_t s = patch[e];
   if (!in_range(s, N)) {
     if (d == 0) atomicOr(err, kErrIndex);
-#pragma unroll
-    for (int v = 0; v < V; ++v) out[i + v] = E(0);
+    vstore<E, V>(dst, Vec<E, V>{});
     return;
   }
-  const E* src = x + (b * N + s) * D + d;
-  if constexpr (V * sizeof(E) == 16) {
-    gstore16(out + i, gload16(src));
-  } else {
-#pragma unroll
-    for (int v = 0; v < V; ++v) out[i + v] = src[v];
-  }
+  vstore<E, V>(dst, vload<E, V>(x + (static_cast<size_t>(b) * N + s) * D + d));
 }
 
 // Workspace of the backward: error word, counts[N], cursor[N], offsets[N + 1], list[P K]
@@ -135,47 +155,79 @@ __global__ void __launch_bounds__(256) sort_kernel(int N, const int* __restrict_
   }
 }
 
-// gx[b, n, d] = sum over the entries e of source n, in list order, of gout[b, e, d].
-template <typename E>
-__global__ void __launch_bounds__(256) scatter_sum_kernel(int64_t total, int N, int D, int PK,
+// gx[b, n, d..d+V) = sum over the entries e of source n, in list order, of gout[b, e, ...].
+// Grid (vectors of one batch row, B), as gather_kernel.
+template <typename E, int V>
+__global__ void __launch_bounds__(256) scatter_sum_kernel(int N, int D, int PK,
                                                           const E* __restrict__ gout,
                                                           const int* __restrict__ offsets,
                                                           const int* __restrict__ list,
                                                           E* __restrict__ gx) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= total) return;
-  const int d = static_cast<int>(i % D);
-  const int64_t bn = i / D;
-  const int n = static_cast<int>(bn % N);
-  const int64_t b = bn / N;
-  float acc = 0.0f;
-  for (int p = offsets[n]; p < offsets[n + 1]; ++p)
-    acc += to_f(gout[(b * PK + list[p]) * D + d]);
-  st(gx, static_cast<size_t>(i), acc);
+  const int b = blockIdx.y;
+  const int dv = D / V;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= N * dv) return;
+  const int n = j / dv, d = (j - n * dv) * V;
+  float acc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] = 0.0f;
+  const E* gb = gout + static_cast<size_t>(b) * PK * D + d;
+  for (int p = offsets[n]; p < offsets[n + 1]; ++p) {
+    const Vec<E, V> g = vload<E, V>(gb + static_cast<size_t>(list[p]) * D);
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] += to_f(g.e[v]);
+  }
+  Vec<E, V> r;
+#pragma unroll
+  for (int v = 0; v < V; ++v) r.e[v] = is_bf16<E>::value ? E(f2bf(acc[v])) : E(acc[v]);
+  vstore<E, V>(gx + (static_cast<size_t>(b) * N + n) * D + d, r);
 }
 
 static int checks(int dtype, int64_t B, int64_t N, int64_t D, int64_t P, int64_t K) {
   DABSN_REQUIRE(dtype == kF32 || dtype == kBF16, "local field gather: bad dtype %d", dtype);
   DABSN_REQUIRE(B > 0 && N > 0 && D > 0 && P >= 0 && K >= 0, "local field gather: bad shape");
-  DABSN_REQUIRE(N < (1ll << 31) && P * K < (1ll << 31) && D < (1ll << 31),
+  DABSN_REQUIRE(B < 65536 && N * D < (1ll << 31) && P * K * D < (1ll << 31),
                 "local field gather: dimension too large");
   return DABSN_OK;
+}
+
+// 16-byte vectors when rows of D elements keep both pointers 16-byte aligned.
+template <typename E>
+static bool vec_ok(int64_t D, const void* a, const void* b) {
+  return D % (16 / sizeof(E)) == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(b) % 16 == 0;
 }
 
 template <typename E>
 static int gather_impl(int64_t B, int64_t N, int64_t D, int64_t PK, const E* x,
                        const int64_t* patch, E* out, uint32_t* err, hipStream_t stream) {
-  const int64_t total = B * PK * D;
-  if (total == 0) return DABSN_OK;
+  if (PK == 0) return DABSN_OK;
   constexpr int V = 16 / sizeof(E);
-  const bool vec = (D % V == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
-                   (reinterpret_cast<uintptr_t>(out) % 16 == 0);
-  if (vec) {
-    hipLaunchKernelGGL((gather_kernel<E, V>), dim3(static_cast<unsigned>((total / V + 255) / 256)),
-                       dim3(256), 0, stream, total, (int)N, (int)D, (int)PK, x, patch, out, err);
+  if (vec_ok<E>(D, x, out)) {
+    hipLaunchKernelGGL((gather_kernel<E, V>), dim3(static_cast<unsigned>((PK * D / V + 255) / 256),
+                       static_cast<unsigned>(B)), dim3(256), 0, stream, (int)N, (int)D, (int)PK, x,
+                       patch, out, err);
   } else {
-    hipLaunchKernelGGL((gather_kernel<E, 1>), dim3(static_cast<unsigned>((total + 255) / 256)),
-                       dim3(256), 0, stream, total, (int)N, (int)D, (int)PK, x, patch, out, err);
+    hipLaunchKernelGGL((gather_kernel<E, 1>), dim3(static_cast<unsigned>((PK * D + 255) / 256),
+                       static_cast<unsigned>(B)), dim3(256), 0, stream, (int)N, (int)D, (int)PK, x,
+                       patch, out, err);
+  }
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+template <typename E>
+static int scatter_impl(int64_t B, int64_t N, int64_t D, int64_t PK, const E* gout,
+                        const int* offsets, const int* list, E* gx, hipStream_t stream) {
+  constexpr int V = 16 / sizeof(E);
+  if (vec_ok<E>(D, gout ? static_cast<const void*>(gout) : gx, gx)) {
+    hipLaunchKernelGGL((scatter_sum_kernel<E, V>), dim3(static_cast<unsigned>((N * D / V + 255) / 256),
+                       static_cast<unsigned>(B)), dim3(256), 0, stream, (int)N, (int)D, (int)PK, gout,
+                       offsets, list, gx);
+  } else {
+    hipLaunchKernelGGL((scatter_sum_kernel<E, 1>), dim3(static_cast<unsigned>((N * D + 255) / 256),
+                       static_cast<unsigned>(B)), dim3(256), 0, stream, (int)N, (int)D, (int)PK, gout,
+                       offsets, list, gx);
   }
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
@@ -248,18 +300,11 @@ int dabsn_hip_local_field_gather_bwd(int dtype, int64_t B, int64_t N, int64_t D,
                        stream, (int)N, offsets, list);
     DABSN_HIP_CHECK(hipGetLastError());
   }
-  const int64_t total = B * N * D;
-  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
   if (dtype == kBF16)
-    hipLaunchKernelGGL(scatter_sum_kernel<bf16>, grid, dim3(256), 0, stream, total, (int)N, (int)D,
-                       (int)PK, static_cast<const bf16*>(grad_out), offsets, list,
-                       static_cast<bf16*>(grad_x));
-  else
-    hipLaunchKernelGGL(scatter_sum_kernel<float>, grid, dim3(256), 0, stream, total, (int)N,
-                       (int)D, (int)PK, static_cast<const float*>(grad_out), offsets, list,
-                       static_cast<float*>(grad_x));
-  DABSN_HIP_CHECK(hipGetLastError());
-  return DABSN_OK;
+    return scatter_impl<bf16>(B, N, D, PK, static_cast<const bf16*>(grad_out), offsets, list,
+                              static_cast<bf16*>(grad_x), stream);
+  return scatter_impl<float>(B, N, D, PK, static_cast<const float*>(grad_out), offsets, list,
+                             static_cast<float*>(grad_x), stream);
 }
 
 }  // extern "C"

@@ -493,9 +493,11 @@ def local_field_gather(inputs: Tensor, patch: Tensor) -> Tensor:
     out = torch.empty((B, P, K, D), device=inputs.device, dtype=dt)
     nbytes = lib.dabsn_hip_local_field_workspace_bytes(N, P, K, 0)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=inputs.device)
+    tk = KernelTimer.begin("local_field_gather", inputs)
     _lib.check(lib.dabsn_hip_local_field_gather(_code(dt), B, N, D, P, K, _p(x), _p(idx), _p(out),
                                                 _p(ws), nbytes, _stream(inputs)),
                "local field gather")
+    KernelTimer.end(tk)
     _record_error_word(ws, "local field gather", _FIELD_INDEX_ERROR)
     return out.to(inputs.dtype)
 
@@ -523,9 +525,11 @@ def local_field_gather_backward(grad_out: Tensor, patch: Tensor, cells: int) -> 
     gx = torch.empty((B, cells, D), device=grad_out.device, dtype=dt)
     nbytes = lib.dabsn_hip_local_field_workspace_bytes(cells, P, K, 1)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=grad_out.device)
+    tk = KernelTimer.begin("local_field_scatter", grad_out)
     _lib.check(lib.dabsn_hip_local_field_gather_bwd(_code(dt), B, cells, D, P, K, _p(g), _p(idx),
                                                     _p(gx), _p(ws), nbytes, _stream(grad_out)),
                "local field gather backward")
+    KernelTimer.end(tk)
     _record_error_word(ws, "local field gather backward", _FIELD_INDEX_ERROR)
     return gx.to(grad_out.dtype)
 
