@@ -68,7 +68,14 @@ __global__ void __launch_bounds__(256) gather_kernel(int N, int D, int PK,
     vstore<E, V>(dst, Vec<E, V>{});
     return;
   }
-  vstore<E, V>(dst, vload<E, V>(x + (static_cast<size_t>(b) * N + s) * D + d));
+  const Vec<E, V> v = vload<E, V>(x + (static_cast<size_t>(b) * N + s) * D + d);
+  if constexpr (V * sizeof(E) == 16) {
+    // Written once and not read back here: a streaming (non-temporal) store keeps the
+    // output out of the caches the neighbours' source rows are read through.
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
+  } else {
+    vstore<E, V>(dst, v);
+  }
 }
 
 // Workspace of the backward: error word, counts[N], cursor[N], offsets[N + 1], list[P K]
@@ -102,30 +109,50 @@ __global__ void __launch_bounds__(256) count_kernel(int PK, int N, const int64_t
   atomicAdd(&counts[s], 1);
 }
 
-// offsets = exclusive prefix sum of counts (N + 1 entries), one workgroup: each thread sums
-// a contiguous range, the 1024 range totals are scanned in LDS, then each range is written.
+// offsets = exclusive prefix sum of counts (N + 1 entries), one workgroup, over tiles of
+// 16 Ki counts staged in LDS with coalesced loads and stores: each thread scans 16
+// consecutive counts, the 1024 thread totals are scanned in LDS, and a running carry links
+// the tiles. Row i of the tile is stored at i + i / 16 (one pad word per 16) so the
+// per-thread runs of 16 fall in different banks.
+constexpr int kScanPer = 16, kScanTile = 1024 * kScanPer;
+
+__device__ __forceinline__ int scan_slot(int i) { return i + i / kScanPer; }
+
 __global__ void __launch_bounds__(1024) scan_kernel(int N, const int* __restrict__ counts,
                                                     int* __restrict__ offsets) {
+  __shared__ int tile[kScanTile + kScanTile / kScanPer];
   __shared__ int part[1024];
   const int tid = threadIdx.x;
-  const int per = (N + 1023) / 1024;
-  const int lo = min(N, tid * per), hi = min(N, lo + per);
-  int sum = 0;
-  for (int n = lo; n < hi; ++n) sum += counts[n];
-  part[tid] = sum;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan
-    const int v = tid >= off ? part[tid - off] : 0;
+  int carry = 0;
+  for (int base = 0; base < N; base += kScanTile) {
+    const int len = min(kScanTile, N - base);
+    for (int i = tid; i < kScanTile; i += 1024) tile[scan_slot(i)] = i < len ? counts[base + i] : 0;
     __syncthreads();
-    part[tid] += v;
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < kScanPer; ++j) sum += tile[scan_slot(tid * kScanPer + j)];
+    part[tid] = sum;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan
+      const int v = tid >= off ? part[tid - off] : 0;
+      __syncthreads();
+      part[tid] += v;
+      __syncthreads();
+    }
+    int run = carry + (tid > 0 ? part[tid - 1] : 0);
+#pragma unroll
+    for (int j = 0; j < kScanPer; ++j) {
+      const int k = scan_slot(tid * kScanPer + j);
+      const int c = tile[k];
+      tile[k] = run;
+      run += c;
+    }
+    carry += part[1023];
+    __syncthreads();
+    for (int i = tid; i < len; i += 1024) offsets[base + i] = tile[scan_slot(i)];
     __syncthreads();
   }
-  int run = tid > 0 ? part[tid - 1] : 0;
-  for (int n = lo; n < hi; ++n) {
-    offsets[n] = run;
-    run += counts[n];
-  }
-  if (tid == 1023) offsets[N] = part[1023];
+  if (tid == 0) offsets[N] = carry;
 }
 
 __global__ void __launch_bounds__(256) fill_kernel(int PK, int N, const int64_t* __restrict__ patch,

@@ -130,11 +130,12 @@ def test_permanent_delta_read_matches_the_same_read_on_the_oracle(cuda_device):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,N,D,P,K", [(2, 9, 6, 9, 3), (2, 4096, 64, 4096, 9), (3, 50, 5, 70, 4),
-                                       (1, 17, 8, 0, 3)])
+                                       (1, 17, 8, 0, 3), (1, 40000, 4, 40000, 2)])
 def test_local_field_gather_and_scatter_are_exact(cuda_device, dtype, B, N, D, P, K):
     """The release-gate patch (9 cells, neighbours n, n+1, n+3), a 64 x 64 field with
     3 x 3 neighbourhoods (16-byte row copies), an odd D with more patch rows than cells
-    (element copies), and an empty patch."""
+    (element copies), an empty patch, and more cells than one tile of the index build's
+    offset scan (16 Ki)."""
     g = torch.Generator().manual_seed(N + D)
     if P == 9 and K == 3:
         patch = GATE_PATCH
