@@ -25,7 +25,8 @@ from __future__ import annotations
 
 import ctypes
 import os
-from typing import Optional, Sequence
+import weakref
+from typing import Callable, Optional, Sequence
 
 import torch
 from torch import Tensor
@@ -58,6 +59,42 @@ def _p(t: Optional[Tensor]) -> Optional[int]:
 
 def _sync_mode() -> str:
     return os.environ.get("DABSN_HIP_ERROR_CHECK", "sync")
+
+
+# Derived copies of parameters (fp32 copies of bf16 parameter vectors and scalars, the
+# [Ug; A] concatenation). Streaming decode calls every op once per token with the same
+# parameters, and these copies were a third of its kernel launches. An entry is reused
+# only while every source is the same nn.Parameter object with the same storage and
+# version counter, so an in-place optimizer step, a `.data` swap or a new module rebuilds
+# it; other tensors are never cached.
+_DERIVED: dict[tuple, tuple] = {}
+
+
+def _derived(tag: str, sources: Sequence[Tensor], build: Callable[..., Tensor]) -> Tensor:
+    if not all(isinstance(t, torch.nn.Parameter) for t in sources):
+        return build(*sources)
+    key = (tag,) + tuple(id(t) for t in sources)
+    stamp = tuple((t.data_ptr(), t._version, t.dtype, str(t.device)) for t in sources)
+    hit = _DERIVED.get(key)
+    if hit is not None and hit[1] == stamp and all(r() is t for r, t in zip(hit[0], sources)):
+        return hit[2]
+    value = build(*sources)
+    if len(_DERIVED) >= 4096:  # drop entries whose parameters are gone
+        for k in [k for k, v in _DERIVED.items() if any(r() is None for r in v[0])]:
+            del _DERIVED[k]
+    _DERIVED[key] = (tuple(weakref.ref(t) for t in sources), stamp, value)
+    return value
+
+
+def _f32(t: Tensor) -> Tensor:
+    """t as a contiguous fp32 tensor (a cached copy for a bf16 parameter)."""
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t
+    return _derived("f32", (t,), lambda x: x.float().contiguous())
+
+
+def _f32_scalar(t: Tensor) -> Tensor:
+    return _f32(t).reshape(())
 
 
 def _record_error_word(ws: Tensor, what: str, meaning: str | None = None) -> None:
@@ -146,8 +183,8 @@ CoreScanOutputs = tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, 
 
 
 def _core_params(vecs: Sequence[Tensor], scal: Sequence[Tensor]):
-    vec_f = [v.float().contiguous() for v in vecs]
-    scal_f = [s.float().reshape(()).contiguous() for s in scal]
+    vec_f = [_f32(v) for v in vecs]
+    scal_f = [_f32_scalar(s) for s in scal]
     params = _lib.CoreParams()
     for i, v in enumerate(vec_f):
         params.vec[i] = v.data_ptr()
@@ -174,7 +211,7 @@ def core_scan_batched(
     code = _code(dt)
     Wx_c = Wx.contiguous()
     Wgx_c = Wgx.to(dt).contiguous()
-    GA = torch.cat((Ug, A), dim=0).to(dt).contiguous()
+    GA = _derived(f"GA:{dt}", (Ug, A), lambda u, a: torch.cat((u, a), dim=0).to(dt).contiguous())
     params, keep = _core_params(
         (beta, log_kappa, logit_recover, k_s, k_y, k_b, k_n, k_bias, r_s, r_y, r_b, r_n, r_bias,
          logit_c_decay, k_c, r_c),
@@ -571,7 +608,7 @@ def long_scan_fused(
     dt = write.dtype
     w = write.contiguous()
     p = plasticity.to(dt).contiguous()
-    logits = [x.float().reshape(()).contiguous() for x in
+    logits = [_f32_scalar(x) for x in
               (logit_expect_retain, logit_retention_decay, logit_retain, logit_retention_strength)]
     ptrs = _lib.PTR4(*[x.data_ptr() for x in logits])
     L0, E0, R0 = (x.float().contiguous() for x in (long0, expected0, retention0))
@@ -609,7 +646,7 @@ def long_scan_fused_backward(
     dt = write.dtype
     w = write.contiguous()
     p = plasticity.to(dt).contiguous()
-    lg = [x.float().reshape(()).contiguous() for x in logits]
+    lg = [_f32_scalar(x) for x in logits]
     ptrs = _lib.PTR4(*[x.data_ptr() for x in lg])
     gout = grad_long.to(dt).contiguous()
     gf = [None if x is None else x.float().contiguous()
@@ -867,7 +904,7 @@ def _read_common(query, bank_keys, bank_writes, next_writes, cocktail, bank_cock
     ck, cb, kb, adm = (x.float().contiguous() for x in (cocktail, bank_cocktail, bank_key_bias,
                                                        bank_admission))
     sc = scale.float().reshape(()).contiguous()
-    g = [x.float().reshape(()).contiguous() for x in gains]
+    g = [_f32_scalar(x) for x in gains]
     idx = bank_idx.to(torch.int64).contiguous()
     valid = bank_valid.to(torch.uint8).contiguous()
     if cocktail.shape[-1] != 4 or bank_cocktail.shape[-1] != 4:
@@ -942,7 +979,7 @@ def read3_decode(query: Tensor, bank_write: Tensor, norm_w: Tensor, idx: Tensor,
     ck, cb, kb, adm = (x.float().contiguous() for x in (cocktail, bank_cocktail, bank_key_bias,
                                                        bank_admission))
     sc = scale.float().reshape(()).contiguous()
-    g = [x.float().reshape(()).contiguous() for x in gains]
+    g = [_f32_scalar(x) for x in gains]
     out = torch.empty_like(q)
     code = _code(dt)
     nbytes = lib.dabsn_hip_read3_decode_workspace_bytes(code, B, T, N, H)
