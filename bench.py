@@ -269,7 +269,8 @@ def decode_main(args):
     print(json.dumps(result), flush=True)
 
 
-PRIMITIVES_METRIC = "standalone primitives: permanent delta scan, local field gather"
+PRIMITIVES_METRIC = ("standalone primitives: permanent delta scan, local field gather, chunked "
+                     "readout cross-entropy rows")
 FP32_VALU_PEAK_TFLOPS = 78.6  # non-packed fp32 FMA rate (packed fp32 is not used)
 
 
@@ -277,15 +278,20 @@ def primitives_main(args):
     """The two primitives outside the model path (reference PRIMITIVES, kernels/__init__.py:
     56-83), at sizes of their own: permanent_delta_scan fwd + bwd at B=16, T=1024, H=256
     (unit keys), fp32; local_field_gather fwd + bwd on a 256 x 256 torus with 3 x 3
-    neighbourhoods (K = 9), B=8, D=64, fp32. Prints per-kernel averages over --steps and each
-    kernel's roofline: the delta scan against the fp32 VALU rate (algorithmic flops: 4 H^2
-    per (b, t) forward, 14 H^2 backward with its recompute), the gather and its scatter-add
+    neighbourhoods (K = 9), B=8, D=64, fp32; and the row kernels of the chunked readout
+    cross-entropy (``dabsn_amd.loss``, forward + backward, N=8192 rows, V=32000, hidden 2048,
+    bf16, 2**24-element chunks). Prints per-kernel averages over --steps and each kernel's
+    roofline: the delta scan against the fp32 VALU rate (algorithmic flops: 4 H^2 per
+    (b, t) forward, 14 H^2 backward with its recompute), the gather and its scatter-add
     against HBM (algorithmic bytes: every gathered element written once and every source
-    element read once; the backward the reverse)."""
+    element read once; the backward the reverse), the cross-entropy rows against HBM
+    (forward: the bf16 logits read once; backward: read once, fp32 gradient written)."""
     import dabsn_amd
+    from dabsn_amd import loss as dloss
     from dabsn_amd.kernels import ops
 
     dabsn_amd.kernels.enable("rocm", required=True)
+    os.environ.setdefault("DABSN_HIP_ERROR_CHECK", "deferred")
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(3)
     B, T, H = 16, 1024, 256
@@ -303,11 +309,17 @@ def primitives_main(args):
     x = torch.randn(FB, side * side, D, generator=g).to(dev)
     gout = torch.randn(FB, side * side, 9, D, generator=g).to(dev)
 
+    NR, V, HR = 8192, 32000, 2048
+    hid = torch.randn(NR, HR, generator=g).to(dev, torch.bfloat16).requires_grad_(True)
+    wro = (torch.randn(V, HR, generator=g) / HR ** 0.5).to(dev, torch.bfloat16).requires_grad_(True)
+    tgt = torch.randint(0, V, (NR,), generator=g).to(dev)
+
     def run():
         ops.permanent_delta_scan(k, v, beta)
         ops.permanent_delta_scan_backward(k, v, beta, up)
         ops.local_field_gather(x, patch)
         ops.local_field_gather_backward(gout, patch, side * side)
+        dloss.chunked_linear_cross_entropy(hid, wro, None, tgt).backward()
 
     for _ in range(args.warmup):
         run()
@@ -318,12 +330,16 @@ def primitives_main(args):
     torch.cuda.synchronize()
     kernels = ops.KernelTimer.summary()
     ops.timing(False)
+    ops.check_errors()
     cells = side * side
     work = {
         "permanent_scan_fwd": ("valu", 4.0 * B * T * H * H),
         "permanent_scan_bwd": ("valu", 14.0 * B * T * H * H),
         "local_field_gather": ("hbm", 4.0 * FB * cells * D * (9 + 1)),
         "local_field_scatter": ("hbm", 4.0 * FB * cells * D * (9 + 1)),
+        # per launch: one 2**24-element chunk (524 rows of 32000)
+        "ce_rows_fwd": ("hbm", 2.0 * (1 << 24) // V * V),
+        "ce_rows_bwd": ("hbm", 6.0 * (1 << 24) // V * V),
     }
     out = {}
     for name, (bound, amount) in work.items():
@@ -342,7 +358,7 @@ def primitives_main(args):
     result = {"metric": PRIMITIVES_METRIC, "unit": "ms", "n_gpus": 1, "steps": args.steps,
               "warmup": args.warmup, "dtype": "f32", "data": "synthetic",
               "config": {"workload": "permanent B=16 T=1024 H=256; local field 256x256 torus, "
-                                     "K=9, B=8, D=64"},
+                                     "K=9, B=8, D=64; readout CE N=8192 V=32000 H=2048 bf16"},
               "kernels": out}
     print(json.dumps(result), flush=True)
 

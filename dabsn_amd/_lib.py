@@ -111,6 +111,8 @@ _SIGNATURES = {
     "dabsn_hip_local_field_gather": ([i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_local_field_gather_bwd": (
         [i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, sz, vp], i32),
+    "dabsn_hip_ce_fwd": ([i32, i64, i64, vp, i64, vp, i64, vp, vp, vp, vp], i32),
+    "dabsn_hip_ce_bwd": ([i32, i64, i64, vp, i64, vp, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_read3_decode": (
         [i32, i64, i64, i64, i64, vp, vp, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, PTR4,
          vp, vp, sz, vp],

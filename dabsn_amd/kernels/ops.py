@@ -591,6 +591,76 @@ torch.library.register_autograd("dabsn::local_field_gather", _field_bwd, setup_c
 
 
 # ---------------------------------------------------------------------------
+# Cross-entropy row kernels of the chunked readout loss (loss.py)
+# ---------------------------------------------------------------------------
+_TARGET_ERROR = "a target lies outside [0, V) and is not ignore_index"
+
+
+def _ce_logits(logits: Tensor) -> Tensor:
+    if logits.dim() != 2:
+        raise ValueError("expected logits [rows, V]")
+    if logits.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"cross-entropy rows on the HIP path take fp32/bf16 logits, not {logits.dtype}")
+    return logits if logits.stride(1) == 1 else logits.contiguous()
+
+
+@torch.library.custom_op("dabsn::_ce_rows", mutates_args=(), device_types="cuda")
+def ce_rows(logits: Tensor, targets: Tensor, ignore_index: int) -> tuple[Tensor, Tensor]:
+    """Per row of logits [rows, V]: (logsumexp, lse - logit[target] or 0 where ignored), fp32
+    (reference loss.py:83-93 for one chunk)."""
+    _require_cuda(logits)
+    x = _ce_logits(logits)
+    rows, V = (int(d) for d in x.shape)
+    lib = _lib.load()
+    t = targets.to(device=x.device, dtype=torch.int64).contiguous()
+    lse = torch.empty(rows, device=x.device, dtype=torch.float32)
+    nll = torch.empty_like(lse)
+    err = torch.zeros(1, device=x.device, dtype=torch.int32)
+    tk = KernelTimer.begin("ce_rows_fwd", x)
+    _lib.check(lib.dabsn_hip_ce_fwd(_code(x.dtype), rows, V, _p(x), int(x.stride(0)) if rows else V,
+                                    _p(t), int(ignore_index), _p(lse), _p(nll), _p(err),
+                                    _stream(x)), "cross entropy")
+    KernelTimer.end(tk)
+    _record_error_word(err, "cross entropy", _TARGET_ERROR)
+    return lse, nll
+
+
+@ce_rows.register_fake
+def _ce_rows_fake(logits, targets, ignore_index):
+    rows = logits.shape[0]
+    return (logits.new_empty((rows,), dtype=torch.float32),
+            logits.new_empty((rows,), dtype=torch.float32))
+
+
+@torch.library.custom_op("dabsn::_ce_rows_backward", mutates_args=(), device_types="cuda")
+def ce_rows_backward(logits: Tensor, targets: Tensor, ignore_index: int, lse: Tensor,
+                     scale: Tensor) -> Tensor:
+    """(softmax(logits) - onehot(target)) * scale, fp32 [rows, V], zero rows where ignored
+    (reference loss.py:105-133 for one chunk); scale is a device scalar."""
+    _require_cuda(logits)
+    x = _ce_logits(logits)
+    rows, V = (int(d) for d in x.shape)
+    lib = _lib.load()
+    t = targets.to(device=x.device, dtype=torch.int64).contiguous()
+    l = lse.to(torch.float32).contiguous()
+    sc = scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
+    d = torch.empty((rows, V), device=x.device, dtype=torch.float32)
+    err = torch.zeros(1, device=x.device, dtype=torch.int32)
+    tk = KernelTimer.begin("ce_rows_bwd", x)
+    _lib.check(lib.dabsn_hip_ce_bwd(_code(x.dtype), rows, V, _p(x), int(x.stride(0)) if rows else V,
+                                    _p(t), int(ignore_index), _p(l), _p(sc), _p(d), _p(err),
+                                    _stream(x)), "cross entropy backward")
+    KernelTimer.end(tk)
+    _record_error_word(err, "cross entropy backward", _TARGET_ERROR)
+    return d
+
+
+@ce_rows_backward.register_fake
+def _ce_rows_backward_fake(logits, targets, ignore_index, lse, scale):
+    return logits.new_empty(logits.shape, dtype=torch.float32)
+
+
+# ---------------------------------------------------------------------------
 # Fused recurrent long-memory scan
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("dabsn::long_scan_fused", mutates_args=(), device_types="cuda")
@@ -1094,6 +1164,8 @@ OPERATORS = (
     "dabsn::_permanent_delta_scan_backward",
     "dabsn::local_field_gather",
     "dabsn::_local_field_gather_backward",
+    "dabsn::_ce_rows",
+    "dabsn::_ce_rows_backward",
     "dabsn::long_scan_fused",
     "dabsn::_long_scan_fused_backward",
     "dabsn::read_tape_stats",

@@ -300,6 +300,22 @@ int dabsn_hip_local_field_gather_bwd(int dtype, int64_t B, int64_t N, int64_t D,
                                      void* grad_x, void* workspace, size_t workspace_bytes,
                                      hipStream_t stream);
 
+/* ---- chunked readout cross-entropy: row kernels ----------------------------------
+ * Replace the per-chunk row math of ChunkedLinearCrossEntropy
+ * (src/dabsn/runtime/loss.py:52-137): the readout GEMM stays a plain GEMM; these take its
+ * logits [rows, V] (row stride ldl >= V, `dtype` 0 fp32 / 1 bf16, read as fp32) and int64
+ * targets [rows]. Forward: lse [rows] = logsumexp of the row, nll [rows] = lse -
+ * logit[target] (0 where target == ignore_index). Backward: dlogits [rows, V] fp32 =
+ * (exp(logit - lse) - onehot(target)) * scale[0] (0 rows where ignored); scale is a device
+ * fp32 scalar (grad / valid count). A target outside [0, V) other than ignore_index sets
+ * *err to 1 and the row counts as ignored; the caller reads the word. */
+int dabsn_hip_ce_fwd(int dtype, int64_t rows, int64_t V, const void* logits, int64_t ldl,
+                     const int64_t* targets, int64_t ignore_index, float* lse, float* nll,
+                     uint32_t* err, hipStream_t stream);
+int dabsn_hip_ce_bwd(int dtype, int64_t rows, int64_t V, const void* logits, int64_t ldl,
+                     const int64_t* targets, int64_t ignore_index, const float* lse,
+                     const float* scale, float* dlogits, uint32_t* err, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

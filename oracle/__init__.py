@@ -22,6 +22,7 @@ Parity pins (what checks this oracle, see ``tests/test_oracle_pins.py``):
     (permanent.py:39-51), closed forms (T = 1 gives 0; T = 2 gives beta_0 (k_0 . k_1) v_0;
     beta = 0 gives 0).
   * local field gather/scatter: numpy fancy indexing and ``np.add.at``.
+  * cross-entropy rows: fp64 torch ``F.cross_entropy`` and its autograd gradient.
 The reference ships no golden vectors for this path, and its C++ backend needs
 libtorch to build, so it is not compiled here.
 """
@@ -380,3 +381,29 @@ def field_gather_bwd(gout, patch, cells):
                                   ctypes.c_int64(P), ctypes.c_int64(K), _ptr(gout), _ptr(patch),
                                   _ptr(gx))
     return gx
+
+
+def ce_fwd(logits, targets, ignore_index):
+    """Restates runtime/loss.py:83-93 for one chunk. Returns (lse, nll) per row."""
+    x = _f32(logits)
+    t = np.ascontiguousarray(np.asarray(targets, dtype=np.int64))
+    rows, V = x.shape
+    bad = (t != ignore_index) & ((t < 0) | (t >= V))
+    if bad.any():
+        raise IndexError("target outside [0, V)")
+    lse, nll = np.empty(rows, np.float32), np.empty(rows, np.float32)
+    lib().oracle_ce_fwd(ctypes.c_int64(rows), ctypes.c_int64(V), _ptr(x), _ptr(t),
+                        ctypes.c_int64(ignore_index), _ptr(lse), _ptr(nll))
+    return lse, nll
+
+
+def ce_bwd(logits, targets, ignore_index, lse, scale):
+    """Restates runtime/loss.py:105-133 for one chunk: (softmax - onehot) * scale."""
+    x = _f32(logits)
+    t = np.ascontiguousarray(np.asarray(targets, dtype=np.int64))
+    rows, V = x.shape
+    d = np.empty_like(x)
+    lib().oracle_ce_bwd(ctypes.c_int64(rows), ctypes.c_int64(V), _ptr(x), _ptr(t),
+                        ctypes.c_int64(ignore_index), _ptr(_f32(lse)), ctypes.c_float(scale),
+                        _ptr(d))
+    return d

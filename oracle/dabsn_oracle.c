@@ -28,6 +28,7 @@
  *   oracle_bank_select     read.py:185-239 (cummax floor, member, stable partition).
  *   oracle_permanent_fwd/bwd  cpu_runtime.cpp:1075-1188 (delta scan and its reverse).
  *   oracle_field_gather/_bwd  cpu_runtime.cpp:1191-1237 (patch gather, scatter-add).
+ *   oracle_ce_fwd/bwd      runtime/loss.py:83-93, 105-133 (cross-entropy rows).
  *
  * Deliberate deviation: cpu_runtime.cpp:381 and :571 skip a pathway whose gain is
  * exactly 0, which also zeroes that gain's gradient. The read's math oracle
@@ -882,4 +883,31 @@ void oracle_field_gather_bwd(int64_t B, int64_t N, int64_t D, int64_t P, int64_t
       const float* src = gout + (bi * P * K + e) * D;
       for (int64_t d = 0; d < D; ++d) dst[d] += src[d];
     }
+}
+
+/* ---------------------------------------------------------------------------
+ * Cross-entropy rows of the chunked readout loss (runtime/loss.py:83-93, 105-133): per
+ * row, lse = max + log(sum exp(x - max)) (serial over the vocabulary), nll = lse - x[t]
+ * (0 for ignored rows); backward d = (exp(x - lse) - [c == t]) * scale (0 rows ignored).
+ * ------------------------------------------------------------------------- */
+void oracle_ce_fwd(int64_t rows, int64_t V, const float* x, const int64_t* t, int64_t ignore,
+                   float* lse, float* nll) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * V;
+    float m = -INFINITY;
+    for (int64_t c = 0; c < V; ++c) m = fmaxf(m, xr[c]);
+    float s = 0.0f;
+    for (int64_t c = 0; c < V; ++c) s += expf(xr[c] - m);
+    lse[r] = m + logf(s);
+    nll[r] = (t[r] == ignore) ? 0.0f : lse[r] - xr[t[r]];
+  }
+}
+
+void oracle_ce_bwd(int64_t rows, int64_t V, const float* x, const int64_t* t, int64_t ignore,
+                   const float* lse, float scale, float* d) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float sc = (t[r] == ignore) ? 0.0f : scale;
+    for (int64_t c = 0; c < V; ++c)
+      d[r * V + c] = (expf(x[r * V + c] - lse[r]) - (c == t[r] ? 1.0f : 0.0f)) * sc;
+  }
 }

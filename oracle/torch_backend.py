@@ -195,6 +195,16 @@ def _field_bwd(grad_out, patch, cells):
     return _t(oracle.field_gather_bwd(_np(grad_out), patch.cpu().numpy(), cells), grad_out.dtype)
 
 
+def _ce(logits, targets, ignore_index):
+    lse, nll = oracle.ce_fwd(_np(logits), targets.cpu().numpy(), ignore_index)
+    return _t(lse), _t(nll)
+
+
+def _ce_bwd(logits, targets, ignore_index, lse, scale):
+    return _t(oracle.ce_bwd(_np(logits), targets.cpu().numpy(), ignore_index, _np(lse),
+                            float(scale.reshape(()))))
+
+
 def register() -> None:
     """Attach the oracle as the CPU kernel of every dabsn:: operator (idempotent)."""
     global _DONE
@@ -219,4 +229,6 @@ def register() -> None:
     ops.permanent_delta_scan_backward.register_kernel("cpu")(_permanent_bwd)
     ops.local_field_gather.register_kernel("cpu")(_field)
     ops.local_field_gather_backward.register_kernel("cpu")(_field_bwd)
+    ops.ce_rows.register_kernel("cpu")(_ce)
+    ops.ce_rows_backward.register_kernel("cpu")(_ce_bwd)
     _DONE = True

@@ -389,3 +389,21 @@ def test_field_gather_and_scatter_match_numpy():
         assert np.array_equal(oracle.field_gather_bwd(gout, patch, N), want)
     with pytest.raises(IndexError):
         oracle.field_gather(np.zeros((1, 3, 2), np.float32), np.array([[3]]))
+
+
+def test_cross_entropy_rows_match_fp64_torch():
+    """lse and masked NLL against torch.logsumexp / F.cross_entropy(reduction='none'); the
+    backward against autograd of scale * sum(NLL)."""
+    g = torch.Generator().manual_seed(91)
+    rows, V = 13, 37
+    x = torch.randn(rows, V, generator=g) * 3
+    t = torch.randint(0, V, (rows,), generator=g)
+    t[::4] = -100
+    lse, nll = oracle.ce_fwd(_np(x), t.numpy(), -100)
+    _close(lse, torch.logsumexp(x, -1).numpy(), 1e-6, 1e-6, "lse")
+    want = torch.nn.functional.cross_entropy(x, t, ignore_index=-100, reduction="none")
+    _close(nll, want.numpy(), 1e-5, 1e-6, "nll")
+    xl = x.clone().requires_grad_(True)
+    (0.37 * torch.nn.functional.cross_entropy(xl, t, ignore_index=-100, reduction="sum")).backward()
+    d = oracle.ce_bwd(_np(x), t.numpy(), -100, lse, 0.37)
+    _close(d, xl.grad.numpy(), 1e-5, 1e-7, "dlogits")
