@@ -17,6 +17,7 @@ from .events import (
     remove_event_listener,
     strict_events,
 )
+from .loss import chunked_cross_entropy_from_logits, chunked_linear_cross_entropy
 from .memory import DABSNMemory, LayerMemory, forward_with_memory, ingest
 from .model import DABSNBlock, DABSNSequenceLM
 from .read import DABSNRead
@@ -30,6 +31,8 @@ __all__ = [
     "EventCode",
     "StrictFallbackError",
     "LayerMemory",
+    "chunked_cross_entropy_from_logits",
+    "chunked_linear_cross_entropy",
     "add_event_listener",
     "forward_with_memory",
     "ingest",
