@@ -63,15 +63,37 @@ def _sync_mode() -> str:
 
 # Derived copies of parameters (fp32 copies of bf16 parameter vectors and scalars, the
 # [Ug; A] concatenation). Streaming decode calls every op once per token with the same
-# parameters, and these copies were a third of its kernel launches. An entry is reused
-# only while every source is the same nn.Parameter object with the same storage and
-# version counter, so an in-place optimizer step, a `.data` swap or a new module rebuilds
-# it; other tensors are never cached.
+# parameters, and these copies were a third of its kernel launches. Inside
+# `reuse_parameter_copies()` (the carried-memory inference entry points) an entry is
+# reused while every source is the same nn.Parameter object with the same storage and
+# version counter: an in-place update, a `.data` swap or a new module rebuilds it. An edit
+# through `p.data` in place (`p.data.copy_(...)`) leaves the version counter alone, so
+# such edits must not happen between calls inside the context. Elsewhere nothing is
+# cached.
 _DERIVED: dict[tuple, tuple] = {}
+_REUSE_DEPTH = 0
+
+
+class reuse_parameter_copies:
+    """Context manager enabling the parameter-copy reuse described above."""
+
+    def __enter__(self):
+        global _REUSE_DEPTH
+        _REUSE_DEPTH += 1
+        return self
+
+    def __exit__(self, *exc):
+        global _REUSE_DEPTH
+        _REUSE_DEPTH -= 1
+        return False
+
+
+def clear_parameter_copies() -> None:
+    _DERIVED.clear()
 
 
 def _derived(tag: str, sources: Sequence[Tensor], build: Callable[..., Tensor]) -> Tensor:
-    if not all(isinstance(t, torch.nn.Parameter) for t in sources):
+    if _REUSE_DEPTH == 0 or not all(isinstance(t, torch.nn.Parameter) for t in sources):
         return build(*sources)
     key = (tag,) + tuple(id(t) for t in sources)
     stamp = tuple((t.data_ptr(), t._version, t.dtype, str(t.device)) for t in sources)

@@ -241,7 +241,7 @@ def _run(model: DABSNSequenceLM, ids: Tensor, memory: DABSNMemory | None, *,
         position = memory.position
     lengths = [layer.bank.length for layer in memory.layers] if memory is not None else []
     outputs = []
-    with torch.no_grad():
+    with torch.no_grad(), ops.reuse_parameter_copies():
         for start, stop in _chunks(int(ids.shape[1]), chunk_size):
             hidden = model.embed(ids[:, start:stop])
             for i, block in enumerate(blocks):
@@ -275,7 +275,10 @@ def forward_with_memory(model: DABSNSequenceLM, ids: Tensor, memory: DABSNMemory
     (memory.py:368-386). With ``extend=False`` the memory passed in is returned unchanged,
     so repeated independent queries see the same context; with ``extend=True`` the query
     tokens are appended (streaming decode). Banks are extended in place: a memory that was
-    extended should not be used through an older handle afterwards."""
+    extended should not be used through an older handle afterwards. The ops reuse their
+    fp32 copies of the model's parameters across calls while each parameter keeps its
+    storage and version counter; a weight edited in place through ``.data`` between calls
+    needs ``dabsn_amd.kernels.ops.clear_parameter_copies()``."""
     hidden, result = _run(model, ids, memory, chunk_size=chunk_size, extend=extend)
     if return_hidden:
         return hidden, result

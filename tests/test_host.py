@@ -156,3 +156,26 @@ def test_routing_events_once_and_strict_fallback():
     finally:
         events.remove_event_listener(seen.append)
         events.reset_routing_log()
+
+
+def test_parameter_copies_are_reused_only_inside_the_context():
+    """fp32 copies of bf16 parameters are rebuilt on every call outside
+    ``reuse_parameter_copies``; inside it they are reused until the parameter's version or
+    storage changes."""
+    import torch
+
+    from dabsn_amd.kernels import ops
+
+    p = torch.nn.Parameter(torch.randn(5).to(torch.bfloat16))
+    ops.clear_parameter_copies()
+    assert ops._f32(p) is not ops._f32(p)
+    with ops.reuse_parameter_copies():
+        a = ops._f32(p)
+        assert ops._f32(p) is a
+        with torch.no_grad():
+            p.mul_(2)  # in-place update: version bump
+        b = ops._f32(p)
+        assert b is not a and torch.equal(b, p.float())
+        p.data = torch.randn(5).to(torch.bfloat16)  # new storage
+        assert torch.equal(ops._f32(p), p.float())
+    ops.clear_parameter_copies()
