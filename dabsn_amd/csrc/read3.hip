@@ -854,6 +854,9 @@ __global__ void __launch_bounds__(256) decode_reduce_kernel(int64_t chunks, int 
 // exact softmax weights (the two-pass path rounds P_V / P_Vn to E first).
 // ---------------------------------------------------------------------------
 constexpr int kFusedMaxChunks = 4;  // 8-element chunks per lane: H <= 64 * 8 * 4
+#ifndef DABSN_DECODE_DEPTH
+#define DABSN_DECODE_DEPTH 2  // bf16 row buffers per wave (depth - 1 rows in flight)
+#endif
 
 // Per-slot inputs of the single-pass read (8 dwords, read with one scalar load).
 struct SlotMeta {
@@ -1040,7 +1043,8 @@ __device__ __forceinline__ float row_dot(const RowChunks<E, NC>& r, const QueryC
 // in-flight register is copied. Slot metadata comes through scalar loads D slots ahead.
 template <typename E, int NC>
 __global__ void __launch_bounds__(64) decode_fused_kernel(FusedArgs<E> a) {
-  constexpr int D = sizeof(E) == 2 ? 3 : 2;
+  constexpr int D = sizeof(E) == 2 ? DABSN_DECODE_DEPTH : 2;
+  static_assert(D == 2 || D == 3 || D == 4, "row buffer depth");
   using Row = RowChunks<E, NC>;
   const int lane = threadIdx.x;
   const int w = blockIdx.x;
@@ -1077,56 +1081,70 @@ __global__ void __launch_bounds__(64) decode_fused_kernel(FusedArgs<E> a) {
       for (int d = 0; d + 1 < D; ++d) ring[d] = ring[d + 1];
       ring[D - 1] = mb[min(j + D, j1 - 1)];
       pf.load(a.bank + ring[D - 2].row * rowH, lane, nch);  // the last slots reread theirs
-      // The previous slot's induction value, from this slot's row when it is that row.
-      if (pend_w != 0.0f) {
-        if (pend_row == mc.row) {
-          acc_add<E, NC>(acc[2], cur, pend_w);
-          // Keeps this branch from being merged with the other one: the merged block
-          // would carry the other branch's wait for its own load (a drain of every row
-          // in flight) onto this path.
-          __builtin_amdgcn_sched_barrier(0);
-        } else {
-          Row vn;
-          vn.load(a.bank + pend_row * rowH, lane, nch);
-          acc_add<E, NC>(acc[2], vn, pend_w);
-        }
+      // The previous slot's induction value is this slot's row when it is that row (added
+      // in the update below); otherwise it is loaded and added here.
+      float wi = pend_w;
+      if (pend_w != 0.0f && pend_row != mc.row) {
+        Row vn;
+        vn.load(a.bank + pend_row * rowH, lane, nch);
+        acc_add<E, NC>(acc[2], vn, pend_w);
+        wi = 0.0f;
       }
       pend_w = 0.0f;
+      float ws = 0.0f, wp = 0.0f, as = 1.0f, ap = 1.0f, ai = 1.0f;
       if (mc.flags != 0u) {
         const float sraw = wave_sum(row_dot<E, NC>(cur, qc, mc.rn));
         const float content = sraw * scale + mc.kb;
         const float ss = content + mc.adm;
         const float sp = content + mc.ccg + mc.adm;
-        float alpha;
         if (mc.flags & 1u) {
-          const float ws = online_weight(ss, m[0], l[0], alpha);
-          if (alpha != 1.0f) acc_scale<NC>(acc[0], alpha);
-          const float wp = online_weight(sp, m[1], l[1], alpha);
-          if (alpha != 1.0f) acc_scale<NC>(acc[1], alpha);
-#pragma unroll
-          for (int k = 0; k < NC; ++k) {
-            float v[8];
-            cur.unpack(k, v);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              acc[0][k][e] = fmaf(ws, v[e], acc[0][k][e]);
-              acc[1][k][e] = fmaf(wp, v[e], acc[1][k][e]);
-            }
-          }
+          ws = online_weight(ss, m[0], l[0], as);
+          wp = online_weight(sp, m[1], l[1], ap);
         }
         if (mc.flags & 2u) {
-          pend_w = online_weight(ss, m[2], l[2], alpha);
-          if (alpha != 1.0f) acc_scale<NC>(acc[2], alpha);
+          pend_w = online_weight(ss, m[2], l[2], ai);
           pend_row = mc.nrow;
         }
       }
+      // One pass over the row for the three accumulators: the short and permanent ones
+      // rescaled to a new maximum before their term is added, the induction one after the
+      // previous slot's term (weighted against the old maximum) is in.
+      if (ws != 0.0f || wp != 0.0f || wi != 0.0f) {
+        if (as != 1.0f) acc_scale<NC>(acc[0], as);
+        if (ap != 1.0f) acc_scale<NC>(acc[1], ap);
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+          float v[8];
+          cur.unpack(k, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            acc[0][k][e] = fmaf(ws, v[e], acc[0][k][e]);
+            acc[1][k][e] = fmaf(wp, v[e], acc[1][k][e]);
+            acc[2][k][e] = fmaf(wi, v[e], acc[2][k][e]);
+          }
+        }
+      } else {
+        if (as != 1.0f) acc_scale<NC>(acc[0], as);
+        if (ap != 1.0f) acc_scale<NC>(acc[1], ap);
+      }
+      if (ai != 1.0f) acc_scale<NC>(acc[2], ai);
     };
     // Whole groups of D slots in a loop with one exit (an exit between the steps would
     // leave the next group's requests in flight on the loop's back edge, and the wait
     // placement would then drain them at the top of every group), the rest after it.
     const int full = j0 + (j1 - j0) / D * D;
     int j = j0;
-    if constexpr (D == 3) {
+    if constexpr (D == 4) {
+      for (; j < full; j += 4) {
+        step(r[0], r[3], j);
+        step(r[1], r[0], j + 1);
+        step(r[2], r[1], j + 2);
+        step(r[3], r[2], j + 3);
+      }
+      if (j < j1) step(r[0], r[3], j);
+      if (j + 1 < j1) step(r[1], r[0], j + 1);
+      if (j + 2 < j1) step(r[2], r[1], j + 2);
+    } else if constexpr (D == 3) {
       for (; j < full; j += 3) {
         step(r[0], r[2], j);
         step(r[1], r[0], j + 1);
