@@ -123,6 +123,11 @@ _SIGNATURES = {
         + [vp] * 4 + [vp] * 5 + [vp, sz, vp],
         i32,
     ),
+    "dabsn_hip_read3_bwd_after_fwd": (
+        [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4]
+        + [vp] * 4 + [vp] * 5 + [vp, sz, vp],
+        i32,
+    ),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -572,10 +572,14 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
                          const float* kb, const float* adm, const float* scale, const int64_t* idx,
                          const uint8_t* valid, int mode, Gains g, E* gq, E* gK, E* gV, E* gVn,
                          float* gck, float* gcb, float* gkb, float* gadm, float* gscal5,
-                         uint8_t* ws, const Plan& p, hipStream_t stream) {
-  int rc = forward_impl<E>(B, T, N, H, q, K, V, Vn, ck, cb, kb, adm, scale, idx, valid, mode, g,
-                           nullptr, ws, p, false, stream);
-  if (rc != DABSN_OK) return rc;
+                         uint8_t* ws, const Plan& p, bool recompute, hipStream_t stream) {
+  // The tile ranges, S and the row statistics: recomputed here, or left in the workspace
+  // by the forward call on the same inputs (which also wrote P_V / P_Vn, rebuilt below).
+  if (recompute) {
+    const int rc = forward_impl<E>(B, T, N, H, q, K, V, Vn, ck, cb, kb, adm, scale, idx, valid,
+                                   mode, g, nullptr, ws, p, false, stream);
+    if (rc != DABSN_OK) return rc;
+  }
   const int QT = static_cast<int>((T + TILE - 1) / TILE), BT = static_cast<int>((N + TILE - 1) / TILE);
   const float* S = reinterpret_cast<const float*>(ws + p.off_S);
   const int32_t* rs = reinterpret_cast<const int32_t*>(ws + p.off_rs);
@@ -1394,14 +1398,18 @@ int dabsn_hip_read3_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
                              idx, valid, mode, g, (float*)out, (uint8_t*)workspace, p, true, stream);
 }
 
-int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* gout,
-                        const void* q, const void* K, const void* V, const void* Vn,
-                        const float* cocktail, const float* bank_cocktail, const float* key_bias,
-                        const float* admission, const float* scale, const int64_t* idx,
-                        const uint8_t* valid, int mode, const float* const* gains, void* gq,
-                        void* gK, void* gV, void* gVn, float* gcocktail, float* gbank_cocktail,
-                        float* gkey_bias, float* gadmission, float* gscalars5, void* workspace,
-                        size_t workspace_bytes, hipStream_t stream) {
+// The backward entry points: with recompute, from the inputs alone; without, on the
+// workspace a forward call with the same inputs filled.
+static int read3_bwd_entry(bool recompute, int dtype, int64_t B, int64_t T, int64_t N,
+                           int64_t H, const void* gout, const void* q, const void* K,
+                           const void* V, const void* Vn, const float* cocktail,
+                           const float* bank_cocktail, const float* key_bias,
+                           const float* admission, const float* scale, const int64_t* idx,
+                           const uint8_t* valid, int mode, const float* const* gains, void* gq,
+                           void* gK, void* gV, void* gVn, float* gcocktail,
+                           float* gbank_cocktail, float* gkey_bias, float* gadmission,
+                           float* gscalars5, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream) {
   const int rc = read3_checks(dtype, B, T, N, H, mode);
   if (rc != DABSN_OK) return rc;
   DABSN_REQUIRE(gout && q && gq && cocktail && gcocktail && scale && gains && gscalars5,
@@ -1426,12 +1434,42 @@ int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
                                (const bf16*)V, (const bf16*)Vn, cocktail, bank_cocktail, key_bias,
                                admission, scale, idx, valid, mode, g, (bf16*)gq, (bf16*)gK,
                                (bf16*)gV, (bf16*)gVn, gcocktail, gbank_cocktail, gkey_bias,
-                               gadmission, gscalars5, (uint8_t*)workspace, p, stream);
+                               gadmission, gscalars5, (uint8_t*)workspace, p, recompute, stream);
   return backward_impl<float>(B, T, N, H, (const float*)gout, (const float*)q, (const float*)K,
                               (const float*)V, (const float*)Vn, cocktail, bank_cocktail, key_bias,
                               admission, scale, idx, valid, mode, g, (float*)gq, (float*)gK,
                               (float*)gV, (float*)gVn, gcocktail, gbank_cocktail, gkey_bias,
-                              gadmission, gscalars5, (uint8_t*)workspace, p, stream);
+                              gadmission, gscalars5, (uint8_t*)workspace, p, recompute, stream);
+}
+
+int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* gout,
+                        const void* q, const void* K, const void* V, const void* Vn,
+                        const float* cocktail, const float* bank_cocktail, const float* key_bias,
+                        const float* admission, const float* scale, const int64_t* idx,
+                        const uint8_t* valid, int mode, const float* const* gains, void* gq,
+                        void* gK, void* gV, void* gVn, float* gcocktail, float* gbank_cocktail,
+                        float* gkey_bias, float* gadmission, float* gscalars5, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  return read3_bwd_entry(true, dtype, B, T, N, H, gout, q, K, V, Vn, cocktail, bank_cocktail,
+                         key_bias, admission, scale, idx, valid, mode, gains, gq, gK, gV, gVn,
+                         gcocktail, gbank_cocktail, gkey_bias, gadmission, gscalars5, workspace,
+                         workspace_bytes, stream);
+}
+
+int dabsn_hip_read3_bwd_after_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
+                                  const void* gout, const void* q, const void* K, const void* V,
+                                  const void* Vn, const float* cocktail,
+                                  const float* bank_cocktail, const float* key_bias,
+                                  const float* admission, const float* scale,
+                                  const int64_t* idx, const uint8_t* valid, int mode,
+                                  const float* const* gains, void* gq, void* gK, void* gV,
+                                  void* gVn, float* gcocktail, float* gbank_cocktail,
+                                  float* gkey_bias, float* gadmission, float* gscalars5,
+                                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return read3_bwd_entry(false, dtype, B, T, N, H, gout, q, K, V, Vn, cocktail, bank_cocktail,
+                         key_bias, admission, scale, idx, valid, mode, gains, gq, gK, gV, gVn,
+                         gcocktail, gbank_cocktail, gkey_bias, gadmission, gscalars5, workspace,
+                         workspace_bytes, stream);
 }
 
 

@@ -1162,6 +1162,127 @@ torch.library.register_autograd("dabsn::admitted_three_way_read_compact_flash", 
                                 setup_context=_read_setup)
 
 
+# The training path of the read: the forward keeps its workspace (tile ranges, scores and
+# row statistics) for the backward, which then skips the recompute of the score GEMM and
+# the softmax rows. The registered op above keeps the reference's one-output schema for
+# external callers; the read module uses ``admitted_three_way_read_train``.
+@torch.library.custom_op("dabsn::_read3_fwd_keep", mutates_args=(), device_types="cuda")
+def read3_fwd_keep(
+    query: Tensor, bank_keys: Tensor, bank_writes: Tensor, next_writes: Tensor, cocktail: Tensor,
+    bank_cocktail: Tensor, bank_key_bias: Tensor, bank_admission: Tensor, scale: Tensor,
+    bank_idx: Tensor, bank_valid: Tensor, mode: int, short_gain: Tensor, pad_gain: Tensor,
+    induct_gain: Tensor, cocktail_gain: Tensor,
+) -> tuple[Tensor, Tensor]:
+    """The three-way read forward; returns (out, workspace) with the workspace sized for the
+    backward and holding what ``read3_bwd_kept`` reuses."""
+    _require_cuda(query)
+    lib = _lib.load()
+    if mode not in (0, 1):
+        raise ValueError("compact admitted-read mode must be 0 (seq) or 1 (field)")
+    dt, q, K, V, Vn, ck, cb, kb, adm, sc, g, idx, valid = _read_common(
+        query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+        bank_admission, scale, bank_idx, bank_valid,
+        (short_gain, pad_gain, induct_gain, cocktail_gain))
+    B, T, H = q.shape
+    N = K.shape[1]
+    code = _code(dt)
+    out = torch.empty_like(q)
+    nbytes = lib.dabsn_hip_read3_workspace_bytes(code, B, T, N, H, 1)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
+    tk = KernelTimer.begin("read3_fwd", q)
+    _lib.check(lib.dabsn_hip_read3_fwd(code, B, T, N, H, _p(q), _p(K), _p(V), _p(Vn), _p(ck),
+                                       _p(cb), _p(kb), _p(adm), _p(sc), _p(idx), _p(valid), mode,
+                                       ptrs, _p(out), _p(ws), ws.numel(), _stream(q)),
+               "three-way read")
+    KernelTimer.end(tk)
+    return out, ws
+
+
+@read3_fwd_keep.register_fake
+def _read3_fwd_keep_fake(query, *rest):
+    return torch.empty_like(query), query.new_empty((256,), dtype=torch.uint8)
+
+
+@torch.library.custom_op("dabsn::_read3_bwd_kept", mutates_args=("workspace",),
+                         device_types="cuda")
+def read3_bwd_kept(
+    grad_output: Tensor, query: Tensor, bank_keys: Tensor, bank_writes: Tensor,
+    next_writes: Tensor, cocktail: Tensor, bank_cocktail: Tensor, bank_key_bias: Tensor,
+    bank_admission: Tensor, scale: Tensor, bank_idx: Tensor, bank_valid: Tensor, mode: int,
+    short_gain: Tensor, pad_gain: Tensor, induct_gain: Tensor, cocktail_gain: Tensor,
+    workspace: Tensor,
+) -> CompactGradients:
+    """``admitted_three_way_read_compact_flash_backward`` on the workspace of a
+    ``read3_fwd_keep`` call with the same inputs (``dabsn_hip_read3_bwd_after_fwd``)."""
+    _require_cuda(query)
+    lib = _lib.load()
+    dt, q, K, V, Vn, ck, cb, kb, adm, sc, g, idx, valid = _read_common(
+        query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+        bank_admission, scale, bank_idx, bank_valid,
+        (short_gain, pad_gain, induct_gain, cocktail_gain))
+    B, T, H = q.shape
+    N = K.shape[1]
+    go = grad_output.to(dt).contiguous()
+    gq = torch.empty_like(q)
+    gK, gV, gVn = (torch.empty((B, N, H), device=q.device, dtype=dt) for _ in range(3))
+    gck = torch.empty((B, T, 4), device=q.device, dtype=torch.float32)
+    gcb = torch.empty((B, N, 4), device=q.device, dtype=torch.float32)
+    gkb = torch.empty((B, N), device=q.device, dtype=torch.float32)
+    gadm = torch.empty((B, N), device=q.device, dtype=torch.float32)
+    g5 = torch.empty((5,), device=q.device, dtype=torch.float32)
+    ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
+    tk = KernelTimer.begin("read3_bwd", q)
+    _lib.check(lib.dabsn_hip_read3_bwd_after_fwd(
+        _code(dt), B, T, N, H, _p(go), _p(q), _p(K), _p(V), _p(Vn), _p(ck), _p(cb), _p(kb),
+        _p(adm), _p(sc), _p(idx), _p(valid), mode, ptrs, _p(gq), _p(gK), _p(gV), _p(gVn),
+        _p(gck), _p(gcb), _p(gkb), _p(gadm), _p(g5), _p(workspace), workspace.numel(),
+        _stream(q)), "three-way read backward")
+    KernelTimer.end(tk)
+    return (gq, gK.to(bank_keys.dtype), gV.to(bank_writes.dtype), gVn.to(next_writes.dtype),
+            gck.to(cocktail.dtype), gcb.to(bank_cocktail.dtype), gkb.to(bank_key_bias.dtype),
+            gadm.to(bank_admission.dtype),
+            g5[0].clone().reshape_as(scale).to(scale.dtype),
+            g5[1].clone().reshape_as(short_gain).to(short_gain.dtype),
+            g5[2].clone().reshape_as(pad_gain).to(pad_gain.dtype),
+            g5[3].clone().reshape_as(induct_gain).to(induct_gain.dtype),
+            g5[4].clone().reshape_as(cocktail_gain).to(cocktail_gain.dtype))
+
+
+@read3_bwd_kept.register_fake
+def _read3_bwd_kept_fake(grad_output, query, bank_keys, bank_writes, next_writes, cocktail,
+                         bank_cocktail, bank_key_bias, bank_admission, scale, bank_idx, bank_valid,
+                         mode, short_gain, pad_gain, induct_gain, cocktail_gain, workspace):
+    return tuple(torch.empty_like(v) for v in (
+        query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+        bank_admission, scale, short_gain, pad_gain, induct_gain, cocktail_gain))
+
+
+class _Read3Train(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, *inputs):
+        out, ws = read3_fwd_keep(*inputs)
+        ctx.save_for_backward(*inputs[:11], *inputs[12:], ws)
+        ctx.mode = int(inputs[11])
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        t = ctx.saved_tensors
+        g = read3_bwd_kept(grad_output.contiguous(), *t[:11], ctx.mode, *t[11:15], t[15])
+        return (*g[:9], None, None, None, *g[9:])
+
+
+def admitted_three_way_read_train(*inputs) -> Tensor:
+    """``admitted_three_way_read_compact_flash`` (same 16 inputs and result) for callers
+    that will differentiate it: under autograd the forward's workspace is kept for the
+    backward; otherwise this is the registered op."""
+    if inputs[0].is_cuda and torch.is_grad_enabled() and any(
+            isinstance(x, Tensor) and x.requires_grad for x in inputs):
+        return _Read3Train.apply(*inputs)
+    return admitted_three_way_read_compact_flash(*inputs)
+
+
 def kernel_symbol(kernel: str, B: int, H: int, dtype: torch.dtype = torch.bfloat16) -> Optional[str]:
     """Profiler symbol of the core-scan kernel instance used for (B, H, dtype)."""
     if kernel not in ("core_scan_fwd", "core_scan_bwd"):
@@ -1199,4 +1320,6 @@ OPERATORS = (
     "dabsn::_bank_gather_backward",
     "dabsn::admitted_three_way_read_compact_flash",
     "dabsn::_admitted_three_way_read_compact_flash_backward",
+    "dabsn::_read3_fwd_keep",
+    "dabsn::_read3_bwd_kept",
 )

@@ -131,7 +131,7 @@ class DABSNRead(nn.Module):
                 (self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain))
         else:
             K, V, Vn = ops.bank_gather(bank_write, norm_w, idx, next_idx, rank)
-            retrieved = ops.admitted_three_way_read_compact_flash(
+            retrieved = ops.admitted_three_way_read_train(
                 query, K, V, Vn, cocktail[0], bank_cocktail, bank_bias, bank_adm, scale, read_idx,
                 valid, 0, self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain)
         self.last_read_contract = {

@@ -236,6 +236,21 @@ int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
                         void* gK, void* gV, void* gVn, float* gcocktail, float* gbank_cocktail,
                         float* gkey_bias, float* gadmission, float* gscalars5, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
+/* The same backward without recomputing the forward's scores and row statistics: the
+ * workspace (at least dabsn_hip_read3_workspace_bytes(..., backward = 1) bytes) must be
+ * the one a dabsn_hip_read3_fwd call on the same inputs used, untouched since. Saves the
+ * score GEMM and softmax-row pass of the recompute at the cost of keeping the workspace
+ * (B*T*N*4 bytes of scores and more) between forward and backward. */
+int dabsn_hip_read3_bwd_after_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
+                                  const void* gout, const void* q, const void* K, const void* V,
+                                  const void* Vn, const float* cocktail,
+                                  const float* bank_cocktail, const float* key_bias,
+                                  const float* admission, const float* scale,
+                                  const int64_t* idx, const uint8_t* valid, int mode,
+                                  const float* const* gains, void* gq, void* gK, void* gV,
+                                  void* gVn, float* gcocktail, float* gbank_cocktail,
+                                  float* gkey_bias, float* gadmission, float* gscalars5,
+                                  void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Decode read: the forward of dabsn_hip_read3_fwd (mode 0, seq) for a few query rows
  * (T <= 8) against a long bank, reading the bank in place instead of from gathered K, V,

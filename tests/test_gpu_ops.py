@@ -386,6 +386,30 @@ def test_read3_fp32_matches_oracle(cuda_device, mode, B, T, H, window, offset):
         assert abs(a - b) <= 2e-5 * max(abs(b), 1e-3), f"{n}: hip {a} fp64 {b} oracle {float(o)}"
 
 
+@pytest.mark.parametrize("dtype,mode", [(torch.float32, 0), (torch.bfloat16, 0),
+                                        (torch.float32, 1)])
+def test_read3_backward_on_the_kept_forward_equals_the_recompute(cuda_device, dtype, mode):
+    """The training path keeps the forward's workspace (tile ranges, scores, row statistics)
+    and the backward skips their recompute; the same kernels on the same inputs give the
+    same results, so every gradient is bit-identical to the recomputing backward, and the
+    forward output to the registered op's."""
+    B, T, H = 2, 300, 136
+    c = _read_case(88, B, T, H)
+    d = lambda x: x.to(cuda_device)  # noqa: E731
+    act = lambda x: d(x).to(dtype)  # noqa: E731
+    args = (act(c["q"]), act(c["K"]), act(c["V"]), act(c["Vn"]), d(c["ck"]), d(c["cb"]),
+            d(c["kb"]), d(c["adm"]), torch.tensor([1.9], device=cuda_device),
+            d(torch.from_numpy(c["idx"])), d(torch.from_numpy(c["valid"])), mode,
+            *[torch.tensor([v], device=cuda_device) for v in (1.0, 0.7, 0.1, 1.3)])
+    out, ws = ops.read3_fwd_keep(*args)
+    assert torch.equal(out, ops.admitted_three_way_read_compact_flash(*args))
+    go = act(torch.randn(B, T, H, generator=torch.Generator().manual_seed(9)))
+    kept = ops.read3_bwd_kept(go, *args, ws)
+    fresh = ops.admitted_three_way_read_compact_flash_backward(go, *args)
+    for i, (a, b) in enumerate(zip(kept, fresh)):
+        assert torch.equal(a, b), f"grad {i}"
+
+
 def test_read3_bf16_within_tolerance_of_fp32_oracle(cuda_device):
     B, T, H = 2, 300, 256
     c = _read_case(77, B, T, H)
