@@ -102,7 +102,7 @@ class ChunkedLinearCrossEntropy(torch.autograd.Function):
             logits = F.linear(hid, weight, bias)
             d = ops.ce_rows_backward(logits, targets[s:e], ctx.ignore_index, lse[s:e], scale)
             grad_hidden[s:e] = torch.mm(d, weight_acc).to(hidden.dtype)
-            grad_weight += torch.mm(d.t(), hid.to(acc))
+            grad_weight.addmm_(d.t(), hid.to(acc))  # accumulated inside the GEMM
             if grad_bias is not None:
                 grad_bias += d.sum(dim=0)
         grad_weight = grad_weight.to(weight.dtype)

@@ -11,7 +11,7 @@ Counters: ``pmc_summary`` averages each counter per dispatch and kernel over the
 launches a plain elementwise copy of known size (reads and writes ``mib`` MiB once per
 launch), so the same counters read on it give the scale between counter units and bytes.
 
-    python -m dabsn_amd.profiling <results.db> [--top N] [--match REGEX]
+    python -m dabsn_amd.profiling <results.db> [--top N] [--match REGEX] [--tail MARKER:N]
     python -m dabsn_amd.profiling --pmc-summary <dir> [--match REGEX]
     python -m dabsn_amd.profiling --copy-probe <MiB>
     python -m dabsn_amd.profiling --pmc-json <out.json> --fetch <dir> --write <dir> \
@@ -30,13 +30,25 @@ import sqlite3
 from collections import defaultdict
 
 
-def kernel_stats(db_path: str, match: str | None = None) -> list[dict[str, object]]:
+def kernel_stats(db_path: str, match: str | None = None,
+                 tail: tuple[str, int] | None = None) -> list[dict[str, object]]:
+    """Per-kernel statistics of a trace. ``tail = (marker, n)`` keeps only the dispatches
+    between the end of the (n+1)-th last dispatch whose name matches ``marker`` and the end
+    of the last one: the last n repetitions of a step that launches the marker once (e.g.
+    the timed steps of a benchmark after its warm-up and set-up)."""
     con = sqlite3.connect(db_path)
-    rows = con.execute("select name, duration from kernels").fetchall()
+    rows = con.execute("select name, duration, start, end from kernels order by start").fetchall()
     con.close()
+    if tail is not None:
+        marker, n = re.compile(tail[0]), int(tail[1])
+        ends = [e for name, _, _, e in rows if marker.search(name)]
+        if len(ends) <= n:
+            raise ValueError(f"trace has {len(ends)} dispatches matching {tail[0]!r}, need {n + 1}")
+        lo, hi = ends[-n - 1], ends[-1]
+        rows = [r for r in rows if r[2] >= lo and r[3] <= hi]
     pattern = re.compile(match) if match else None
     agg: dict[str, list[int]] = defaultdict(list)
-    for name, duration in rows:
+    for name, duration, _, _ in rows:
         if pattern and not pattern.search(name):
             continue
         agg[name].append(int(duration))
@@ -143,6 +155,8 @@ def main() -> None:
     p.add_argument("db", nargs="?")
     p.add_argument("--top", type=int, default=25)
     p.add_argument("--match", default=None)
+    p.add_argument("--tail", default=None, metavar="MARKER:N",
+                   help="only the last N repetitions of a step launching MARKER once")
     p.add_argument("--pmc-summary", default=None)
     p.add_argument("--copy-probe", type=int, default=None)
     p.add_argument("--pmc-json", default=None)
@@ -168,7 +182,11 @@ def main() -> None:
             name = r["kernel"] if len(r["kernel"]) <= 90 else r["kernel"][:87] + "..."
             print(f"{r['counter']:>12} {r['mean']:16.1f} {r['dispatches']:6d}  {name}")
     else:
-        print(format_table(kernel_stats(args.db, args.match), args.top))
+        tail = None
+        if args.tail:
+            marker, _, n = args.tail.rpartition(":")
+            tail = (marker, int(n))
+        print(format_table(kernel_stats(args.db, args.match, tail), args.top))
 
 
 if __name__ == "__main__":
