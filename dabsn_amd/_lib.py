@@ -32,6 +32,7 @@ class CoreParams(ctypes.Structure):
 
 
 PTR4 = vp * 4
+PTR8 = vp * 8
 
 
 class CoreFwdCall(ctypes.Structure):
@@ -111,6 +112,7 @@ _SIGNATURES = {
     "dabsn_hip_local_field_gather": ([i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_local_field_gather_bwd": (
         [i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, sz, vp], i32),
+    "dabsn_hip_means_glue": ([i64, i64, i64, vp, i64, PTR8, vp, vp, vp, vp], i32),
     "dabsn_hip_ce_fwd": ([i32, i64, i64, vp, i64, vp, i64, vp, vp, vp, vp], i32),
     "dabsn_hip_ce_bwd": ([i32, i64, i64, vp, i64, vp, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_read3_decode": (

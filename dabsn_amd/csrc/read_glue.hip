@@ -1,7 +1,8 @@
 // Read glue: per-position tape statistics, query normalisation, admitted-slot
 // selection and the bank gather (with their backward passes).
 //
-// Reference: src/dabsn/read.py:58-72 (admission), 154-183 (query, key bias, cocktail),
+// Reference: src/dabsn/read.py:58-72 (admission), 154-183 (query, key bias, cocktail; the
+// same on a bank 680-700),
 // 185-239 (cummax floor, member, stable partition, bank width), 241-256 and 298-303
 // (bank gather, next-write gather).
 #include "../../include/dabsn_hip.h"
@@ -14,6 +15,10 @@ namespace dabsn {
 namespace glue {
 
 constexpr float kEps = 1e-12f;
+
+struct Ptr8 {
+  const float* p[8];
+};
 
 // Element kernels take V = 8 (16-byte vector accesses, H % 8 == 0 and aligned operands) or
 // V = 1. Elementwise kernels index V-element chunks with 32-bit arithmetic; row kernels put
@@ -316,6 +321,32 @@ static inline bool vec_ok(int64_t H, std::initializer_list<const void*> ptrs) {
     }                                                                 \
   } while (0)
 
+// Key bias, admission and cocktail from rows of tape statistics (mean energy, saturation,
+// novelty, plasticity, ...; 6 floats per row, rows of batch b `ld` floats apart): the
+// expressions of read.py:58-72 and 155-180 / 680-700 on the means, with the same operation
+// order (products of gains and means added left to right, no contraction), so the results
+// match the torch expressions up to the last-bit rounding of log1p and the norm.
+// prm = 8 fp32 scalars: p_gain, novelty_gain, null_bias, adm_p_gain, adm_novelty_gain,
+// adm_saturation_gain, adm_energy_gain, adm_bias. One thread per row.
+__global__ void __launch_bounds__(256) means_glue_kernel(int64_t rows, int N, int64_t ld,
+                                                         const float* __restrict__ stats,
+                                                         float hidden, Ptr8 prm, float* kb,
+                                                         float* adm, float* ck) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows) return;
+  const float* s = stats + (i / N) * ld + (i % N) * 6;
+  const float me = s[0], mc = s[1], mn = s[2], mp = s[3];
+  const float lp = log1pf(mp * hidden);
+  float P[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) P[k] = prm.p[k][0];
+  if (kb) kb[i] = P[0] * lp + P[1] * mn + P[2];
+  if (adm) adm[i] = P[3] * lp + P[4] * mn + P[5] * mc + P[6] * me + P[7];
+  const float d = fmaxf(sqrtf(me * me + mc * mc + mn * mn + mp * mp), kEps);
+  float4* o = reinterpret_cast<float4*>(ck + i * 4);
+  *o = make_float4(me / d, mc / d, mn / d, mp / d);
+}
+
 extern "C" {
 
 int dabsn_hip_tape_stats(int dtype, int64_t B, int64_t T, int64_t H, const void* nov,
@@ -444,6 +475,28 @@ int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_
                      (const E*)gVn, (E*)gw)
   GLUE_DISPATCH("bank_gather backward", dtype, vec, L);
 #undef L
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_means_glue(int64_t B, int64_t N, int64_t ld, const float* stats, int64_t hidden,
+                         const float* const* params, float* key_bias, float* admission,
+                         float* cocktail, hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && N >= 0 && N < (1 << 30) && ld >= 6 * N && hidden > 0,
+                "means_glue: bad shape");
+  const int64_t rows = B * N;
+  if (rows == 0) return DABSN_OK;
+  DABSN_REQUIRE(stats && params && cocktail, "means_glue: null pointer");
+  DABSN_REQUIRE((reinterpret_cast<uintptr_t>(cocktail) & 15u) == 0,
+                "means_glue: cocktail must be 16-byte aligned");
+  Ptr8 prm;
+  for (int k = 0; k < 8; ++k) {
+    DABSN_REQUIRE(params[k], "means_glue: null parameter %d", k);
+    prm.p[k] = params[k];
+  }
+  hipLaunchKernelGGL(means_glue_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256),
+                     0, stream, rows, (int)N, ld, stats, static_cast<float>(hidden), prm, key_bias,
+                     admission, cocktail);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }

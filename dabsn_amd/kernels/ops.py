@@ -613,6 +613,31 @@ torch.library.register_autograd("dabsn::local_field_gather", _field_bwd, setup_c
 
 
 # ---------------------------------------------------------------------------
+# Key bias, admission and cocktail from tape statistics (no autograd)
+# ---------------------------------------------------------------------------
+def means_glue(stats: Tensor, hidden: int, params: Sequence[Tensor]) -> tuple[Tensor, Tensor, Tensor]:
+    """(key_bias [B, N], admission [B, N], cocktail [B, N, 4]) of statistics rows
+    ``stats`` [B, N, 6] (rows contiguous within a batch row; the batch stride may be
+    longer, e.g. the live prefix of a bank buffer): read.py:58-72, 155-180, 680-700 in one
+    kernel, for callers without autograd. ``params`` = (p_gain, novelty_gain, null_bias,
+    adm_p_gain, adm_novelty_gain, adm_saturation_gain, adm_energy_gain, adm_bias)."""
+    _require_cuda(stats)
+    if stats.dim() != 3 or stats.shape[-1] != 6 or stats.dtype != torch.float32 \
+            or stats.stride(2) != 1 or stats.stride(1) != 6:
+        raise ValueError("means_glue: stats must be fp32 [B, N, 6] with contiguous rows")
+    B, N, _ = (int(d) for d in stats.shape)
+    lib = _lib.load()
+    prm = [_f32_scalar(x) for x in params]
+    kb = torch.empty((B, N), device=stats.device, dtype=torch.float32)
+    adm = torch.empty_like(kb)
+    ck = torch.empty((B, N, 4), device=stats.device, dtype=torch.float32)
+    ptrs = _lib.PTR8(*[x.data_ptr() for x in prm])
+    _lib.check(lib.dabsn_hip_means_glue(B, N, int(stats.stride(0)), _p(stats), int(hidden), ptrs,
+                                        _p(kb), _p(adm), _p(ck), _stream(stats)), "means glue")
+    return kb, adm, ck
+
+
+# ---------------------------------------------------------------------------
 # Cross-entropy row kernels of the chunked readout loss (loss.py)
 # ---------------------------------------------------------------------------
 _TARGET_ERROR = "a target lies outside [0, V) and is not ignore_index"

@@ -252,12 +252,20 @@ class DABSNRead(nn.Module):
         bank_len = bank_write.shape[1]
         if bank_len <= 0:
             raise RuntimeError("query-bank read requires a non-empty bank")
-        qe, qc, qn, qp = query_stats.unbind(-1)[:4]
-        be, bc, bn, bp = bank_stats.unbind(-1)[:4]
         query = ops.normalize_rows(expression, query_stats[..., 4].detach())
-        key_bias = rp.key_bias_from_means(bn, bp, hidden)
-        admission = rp.admission_from_means(be, bc, bn, bp, hidden)
-        cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
+        if not torch.is_grad_enabled() and bank_stats.is_cuda:
+            # Inference (streaming decode): the per-position glue of the whole bank in one
+            # kernel instead of ~25 small ones per layer and token.
+            prm = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain,
+                   rp.adm_novelty_gain, rp.adm_saturation_gain, rp.adm_energy_gain, rp.adm_bias)
+            key_bias, admission, bank_cocktail = ops.means_glue(bank_stats, hidden, prm)
+            cocktails = (ops.means_glue(query_stats, hidden, prm)[2], bank_cocktail)
+        else:
+            qe, qc, qn, qp = query_stats.unbind(-1)[:4]
+            be, bc, bn, bp = bank_stats.unbind(-1)[:4]
+            key_bias = rp.key_bias_from_means(bn, bp, hidden)
+            admission = rp.admission_from_means(be, bc, bn, bp, hidden)
+            cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
         retrieved = self._read_core(query, cocktails, bank_write, bank_stats[..., 5].detach(),
                                     key_bias, admission, bank_len, int(query_start), bank_width)
         short_output = rp.project(y, budget, retrieved.to(y.dtype))

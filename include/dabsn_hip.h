@@ -189,6 +189,15 @@ int dabsn_hip_normalize_rows(int dtype, int64_t rows, int64_t H, const void* x, 
 int dabsn_hip_normalize_rows_bwd(int dtype, int64_t rows, int64_t H, const void* q,
                                  const float* norms, const void* gq, void* gx, hipStream_t stream);
 
+/* Key bias, admission and cocktail from rows of tape statistics (read.py:58-72, 155-180,
+ * 680-700): stats rows of 6 fp32 (mean energy, saturation, novelty, plasticity, query
+ * norm, write norm), row n of batch b at stats + b * ld + 6 n; params = 8 fp32 device
+ * scalars (p_gain, novelty_gain, null_bias, adm_p_gain, adm_novelty_gain,
+ * adm_saturation_gain, adm_energy_gain, adm_bias); outputs key_bias, admission [B, N]
+ * (either may be NULL) and cocktail [B, N, 4] = normalize(means) (16-byte aligned). */
+int dabsn_hip_means_glue(int64_t B, int64_t N, int64_t ld, const float* stats, int64_t hidden,
+                         const float* const* params, float* key_bias, float* admission,
+                         float* cocktail, hipStream_t stream);
 /* Admitted-slot selection (src/dabsn/read.py:185-239, seq geometry): per row, floor =
  * cummax(adm) - window, member = adm >= floor, order = stable partition (members by
  * ascending t, then the rest), counts = #members, rank[t] = position of t in order.

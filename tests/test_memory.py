@@ -185,3 +185,32 @@ def test_memory_embeds_in_checkpoint_and_rejects_foreign_payload_cpu(tmp_path):
     torch.save({"format": "something_else"}, tmp_path / "bad.dmem")
     with pytest.raises(ValueError, match="not a DABSN memory payload"):
         mem.load(tmp_path / "bad.dmem")
+
+
+@pytest.mark.gpu
+def test_means_glue_matches_the_read_modules_expressions(cuda_device):
+    """The fused key bias / admission / cocktail kernel of the inference path against the
+    torch expressions the training path uses (read.py key_bias_from_means,
+    admission_from_means, _cocktail), on the live prefix of a longer bank buffer and with
+    non-default gains: fp32, relative 1e-6 (log1p and the norm may round differently)."""
+    from dabsn_amd import read as R
+    from dabsn_amd.kernels import ops
+
+    g = torch.Generator().manual_seed(12)
+    read = R.DABSNRead(64).to(cuda_device)
+    rp = read.short_read
+    with torch.no_grad():
+        for prm in (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain, rp.adm_novelty_gain,
+                    rp.adm_saturation_gain, rp.adm_energy_gain, rp.adm_bias):
+            prm.copy_(torch.randn(prm.shape, generator=g).to(cuda_device))
+    buf = torch.rand(3, 50, 6, generator=g).to(cuda_device)
+    stats = buf[:, :37]
+    prm = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain, rp.adm_novelty_gain,
+           rp.adm_saturation_gain, rp.adm_energy_gain, rp.adm_bias)
+    with torch.no_grad():
+        kb, adm, ck = ops.means_glue(stats, 64, prm)
+        e, c, n, p = stats.unbind(-1)[:4]
+        want = (rp.key_bias_from_means(n, p, 64), rp.admission_from_means(e, c, n, p, 64),
+                R._cocktail(e, c, n, p))
+    for got, w in zip((kb, adm, ck), want):
+        assert rel_err(got.cpu(), w.cpu()) <= 1e-6
