@@ -12,7 +12,7 @@ import torch
 import torch.nn as nn
 from torch import Tensor
 
-from .kernels.ops import core_scan_batched
+from .kernels import ops
 
 
 def _parameter(shape: int | tuple[int, ...], value: float) -> nn.Parameter:
@@ -94,8 +94,8 @@ class DABSNCore(nn.Module):
                 shapes = tuple(tuple(v.shape) for v in values)
                 raise ValueError(f"initial_state tensors must have shape {expected}, got {shapes}")
             initial_state = values
-        outputs = core_scan_batched(self.W(inputs), self.Wg(inputs), *self.scan_inputs(),
-                                    *initial_state)
+        outputs = ops.direct.core_scan_batched(self.W(inputs), self.Wg(inputs),
+                                               *self.scan_inputs(), *initial_state)
         self._last_core_backend = "rocm_native_hip"
         trajectory, novelty, plasticity, expression, write = outputs[:5]
         if return_cocktail:

@@ -92,19 +92,35 @@ def clear_parameter_copies() -> None:
     _DERIVED.clear()
 
 
-def _derived(tag: str, sources: Sequence[Tensor], build: Callable[..., Tensor]) -> Tensor:
-    if _REUSE_DEPTH == 0 or not all(isinstance(t, torch.nn.Parameter) for t in sources):
+def _derived(tag: str, sources: Sequence[Tensor], build: Callable[..., object]):
+    if _REUSE_DEPTH == 0:
         return build(*sources)
-    key = (tag,) + tuple(id(t) for t in sources)
-    stamp = tuple((t.data_ptr(), t._version, t.dtype, str(t.device)) for t in sources)
+    # Each source is a parameter or a view of one (``p.reshape(())``, ``p.expand(H)``): the
+    # entry is tied to the parameter, and a view adds its geometry to the key.
+    owners, key = [], [tag]
+    for t in sources:
+        if isinstance(t, torch.nn.Parameter):
+            owners.append(t)
+            key.append(id(t))
+        else:
+            o = t._base
+            if not isinstance(o, torch.nn.Parameter):
+                return build(*sources)
+            owners.append(o)
+            key.append((id(o), tuple(t.shape), t.stride(), t.storage_offset()))
+    key = tuple(key)
+    # Device pointers are unique across devices, so the pointer also stands for the device.
+    stamp = tuple((o.data_ptr(), o._version, o.dtype) for o in owners)
     hit = _DERIVED.get(key)
-    if hit is not None and hit[1] == stamp and all(r() is t for r, t in zip(hit[0], sources)):
+    if hit is not None and hit[1] == stamp and all(r() is o for r, o in zip(hit[0], owners)):
         return hit[2]
     value = build(*sources)
     if len(_DERIVED) >= 4096:  # drop entries whose parameters are gone
         for k in [k for k, v in _DERIVED.items() if any(r() is None for r in v[0])]:
             del _DERIVED[k]
-    _DERIVED[key] = (tuple(weakref.ref(t) for t in sources), stamp, value)
+    # An entry goes when one of its parameters does (values hold no reference to them).
+    drop = lambda _ref, k=key: _DERIVED.pop(k, None)  # noqa: E731
+    _DERIVED[key] = (tuple(weakref.ref(o, drop) for o in owners), stamp, value)
     return value
 
 
@@ -112,7 +128,7 @@ def _f32(t: Tensor) -> Tensor:
     """t as a contiguous fp32 tensor (a cached copy for a bf16 parameter)."""
     if t.dtype == torch.float32 and t.is_contiguous():
         return t
-    return _derived("f32", (t,), lambda x: x.float().contiguous())
+    return _derived("f32", (t,), lambda x: x.detach().float().contiguous())
 
 
 def _f32_scalar(t: Tensor) -> Tensor:
@@ -205,14 +221,20 @@ CoreScanOutputs = tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, 
 
 
 def _core_params(vecs: Sequence[Tensor], scal: Sequence[Tensor]):
-    vec_f = [_f32(v) for v in vecs]
-    scal_f = [_f32_scalar(s) for s in scal]
-    params = _lib.CoreParams()
-    for i, v in enumerate(vec_f):
-        params.vec[i] = v.data_ptr()
-    for i, s in enumerate(scal_f):
-        params.scal[i] = s.data_ptr()
-    return params, (vec_f, scal_f)
+    """The kernel's parameter table (fp32 copies of the 16 vectors and 3 scalars and the
+    ctypes struct pointing at them), one cache entry for all 19 parameters."""
+
+    def build(*ts):
+        vec_f = [v.detach().float().contiguous() for v in ts[:16]]
+        scal_f = [x.detach().float().reshape(()).contiguous() for x in ts[16:]]
+        params = _lib.CoreParams()
+        for i, v in enumerate(vec_f):
+            params.vec[i] = v.data_ptr()
+        for i, x in enumerate(scal_f):
+            params.scal[i] = x.data_ptr()
+        return params, (vec_f, scal_f)
+
+    return _derived("core_params", (*vecs, *scal), build)
 
 
 @torch.library.custom_op("dabsn::core_scan_batched", mutates_args=(), device_types="cuda")
@@ -1349,3 +1371,29 @@ OPERATORS = (
     "dabsn::_read3_fwd_keep",
     "dabsn::_read3_bwd_kept",
 )
+
+
+def _direct(op):
+    """``op`` with the dispatcher skipped where nothing needs it: inside
+    ``reuse_parameter_copies()`` with autograd off and device inputs, the op's body is
+    called as a plain function (about 15 µs less host time per call, and streaming decode
+    makes ~30 such calls per token); anywhere else the registered operator runs."""
+    body = op._init_fn
+
+    def call(*args):
+        if _REUSE_DEPTH and not torch.is_grad_enabled() and args[0].is_cuda:
+            return body(*args)
+        return op(*args)
+
+    call.__name__ = call.__qualname__ = body.__name__
+    return call
+
+
+class direct:
+    """The inference call sites' entry to the operators above (see ``_direct``)."""
+
+    core_scan_batched = staticmethod(_direct(core_scan_batched))
+    long_scan_fused = staticmethod(_direct(long_scan_fused))
+    read_tape_stats = staticmethod(_direct(read_tape_stats))
+    normalize_rows = staticmethod(_direct(normalize_rows))
+    bank_select = staticmethod(_direct(bank_select))

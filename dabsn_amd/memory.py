@@ -206,7 +206,7 @@ def _block_step(block: DABSNBlock, inputs: Tensor, layer: LayerMemory | None,
         return_final_state=True)
     trajectory, novelty, plasticity, expression, write, energy, saturation = result
     y, budget = trajectory.split(block.state_dim, dim=-1)
-    stats = ops.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
+    stats = ops.direct.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
     if layer is None:
         bank = BankStore(batch, block.state_dim, device=write.device, dtype=write.dtype,
                          capacity=int(write.shape[1]))

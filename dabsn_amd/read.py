@@ -97,7 +97,7 @@ class DABSNRead(nn.Module):
     # ---- selection ------------------------------------------------------------
     def _select(self, admission: Tensor, length: int, width: int | None = None):
         window = F.softplus(self.admit_window)
-        order, counts, rank = ops.bank_select(admission.detach(), window.detach())
+        order, counts, rank = ops.direct.bank_select(admission.detach(), window.detach())
         if width or self._capture_bank_width:
             # A fixed width needs no host sync; slots past a row's admitted count are
             # masked out by `valid`.
@@ -157,11 +157,11 @@ class DABSNRead(nn.Module):
                          saturation) -> Tensor:
         rp = self.short_read
         _, seq_len, hidden = expression.shape
-        stats = ops.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
+        stats = ops.direct.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
         mean_e, mean_c, mean_n, mean_p = stats.unbind(-1)[:4]
         norm_ay = stats[..., 4].detach()
         norm_w = stats[..., 5].detach()
-        query = ops.normalize_rows(expression, norm_ay)
+        query = ops.direct.normalize_rows(expression, norm_ay)
         key_bias = rp.key_bias_from_means(mean_n, mean_p, hidden)
         admission = rp.admission_from_means(mean_e, mean_c, mean_n, mean_p, hidden)
         cocktail = _cocktail(mean_e, mean_c, mean_n, mean_p)
@@ -188,7 +188,7 @@ class DABSNRead(nn.Module):
         else:
             if any(s.shape != (batch, hidden) for s in initial_state):
                 raise ValueError(f"initial long-scan state must have shape {(batch, hidden)}")
-        long, lf, ef, rf, _ = ops.long_scan_fused(
+        long, lf, ef, rf, _ = ops.direct.long_scan_fused(
             write, plasticity, self.logit_expect_retain, self.logit_retention_decay,
             self.logit_retain, self.logit_retention_strength, *initial_state)
         if return_final_state:
@@ -210,12 +210,12 @@ class DABSNRead(nn.Module):
         bank_len = bank_write.shape[1]
         if bank_len <= 0:
             raise RuntimeError("query-bank read requires a non-empty bank")
-        q_stats = ops.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
-        b_stats = ops.read_tape_stats(bank_novelty, bank_p, bank_energy, bank_saturation,
+        q_stats = ops.direct.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
+        b_stats = ops.direct.read_tape_stats(bank_novelty, bank_p, bank_energy, bank_saturation,
                                       bank_write, bank_write)
         qe, qc, qn, qp = q_stats.unbind(-1)[:4]
         be, bc, bn, bp = b_stats.unbind(-1)[:4]
-        query = ops.normalize_rows(expression, q_stats[..., 4].detach())
+        query = ops.direct.normalize_rows(expression, q_stats[..., 4].detach())
         key_bias = rp.key_bias_from_means(bn, bp, hidden)
         admission = rp.admission_from_means(be, bc, bn, bp, hidden)
         cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
@@ -252,7 +252,7 @@ class DABSNRead(nn.Module):
         bank_len = bank_write.shape[1]
         if bank_len <= 0:
             raise RuntimeError("query-bank read requires a non-empty bank")
-        query = ops.normalize_rows(expression, query_stats[..., 4].detach())
+        query = ops.direct.normalize_rows(expression, query_stats[..., 4].detach())
         if not torch.is_grad_enabled() and bank_stats.is_cuda:
             # Inference (streaming decode): the per-position glue of the whole bank in one
             # kernel instead of ~25 small ones per layer and token.
