@@ -1329,8 +1329,10 @@ static int launch_slabs(K kernel, int threads, const Cfg& c, const A& args, hipS
 #define DABSN_CORE_CASES_F32(X) \
   X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(8, 16, 4) X(8, 32, 4) X(8, 64, 4)
 
-// One-step scans: y_0, the recurrent products as one GEMM (128 x 128 tiles: a few hundred
-// batch rows give tens of workgroups), the step.
+// One-step scans: y_0, the recurrent products as one GEMM, the step. Decode batches of a
+// few hundred rows give only tens of 128 x 128 tiles (B=256, H=2048: 64 workgroups on 256
+// CUs), so such GEMMs take 64 x 64 tiles (256 workgroups); the tile shape does not change
+// any output's summation order over K.
 template <typename E>
 static int launch_one_step(const Cfg& c, const FwdArgs<E>& args, hipStream_t stream) {
   const int dtype = is_bf16<E>::value ? kBF16 : kF32;
@@ -1346,7 +1348,11 @@ static int launch_one_step(const Cfg& c, const FwdArgs<E>& args, hipStream_t str
   g.B = args.GA; g.ldb = H; g.sB = 2 * H * H;
   g.C = G; g.ldc = 2 * H; g.sC = 2 * n;
   g.alpha = 1.0f;
-  DABSN_HIP_CHECK((gemm::launch_shape<E, float, 128, 128, 2, 2>(g, 1, stream)));
+  const int64_t big_tiles = ((g.M + 127) / 128) * ((static_cast<int64_t>(g.N) + 127) / 128);
+  if (big_tiles >= 1024)  // four 128 x 128 tiles per CU of MI355X's 256
+    DABSN_HIP_CHECK((gemm::launch_shape<E, float, 128, 128, 2, 2>(g, 1, stream)));
+  else
+    DABSN_HIP_CHECK((gemm::launch_shape<E, float, 64, 64, 2, 2>(g, 1, stream)));
   hipLaunchKernelGGL(step1_kernel<E>, grid, dim3(256), 0, stream, args, G);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
