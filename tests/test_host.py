@@ -179,3 +179,59 @@ def test_parameter_copies_are_reused_only_inside_the_context():
         p.data = torch.randn(5).to(torch.bfloat16)  # new storage
         assert torch.equal(ops._f32(p), p.float())
     ops.clear_parameter_copies()
+
+
+def test_views_of_parameters_are_cached_and_entries_go_with_their_parameter():
+    """A view (``p.reshape(())``, ``p.expand(n)``) is cached under its parameter plus its
+    geometry; a view of a plain tensor is never cached; freeing the parameter drops the
+    entry."""
+    import gc
+
+    import torch
+
+    from dabsn_amd.kernels import ops
+
+    ops.clear_parameter_copies()
+    p = torch.nn.Parameter(torch.randn(1).to(torch.bfloat16))
+    builds = []
+
+    def build(*ts):
+        builds.append(1)
+        return [t.detach().float() for t in ts]
+
+    with ops.reuse_parameter_copies(), torch.no_grad():
+        a = ops._derived("t", (p.reshape(()), p.expand(4)), build)
+        b = ops._derived("t", (p.reshape(()), p.expand(4)), build)
+        assert a is b and len(builds) == 1
+        c = ops._derived("t", (p.reshape(()), p.expand(6)), build)  # other geometry
+        assert c is not a and len(builds) == 2 and c[1].shape == (6,)
+        plain = torch.randn(3)
+        ops._derived("t", (plain.reshape(3, 1),), build)
+        ops._derived("t", (plain.reshape(3, 1),), build)
+        assert len(builds) == 4
+        assert len(ops._DERIVED) == 2
+    del p
+    gc.collect()
+    assert len(ops._DERIVED) == 0
+
+
+def test_direct_calls_dispatch_outside_inference_and_for_host_tensors():
+    """``ops.direct`` runs the registered operator unless the reuse context is active,
+    autograd is off and the inputs are device tensors: host tensors still raise (fresh
+    process, so no test-only CPU kernel is registered)."""
+    code = (
+        "import torch\n"
+        "from dabsn_amd.kernels import ops\n"
+        "x = torch.randn(2, 3, 8)\n"
+        "n = x.norm(dim=-1)\n"
+        "for ctx in (torch.enable_grad, torch.no_grad):\n"
+        "    with ops.reuse_parameter_copies(), ctx():\n"
+        "        try:\n"
+        "            ops.direct.normalize_rows(x, n)\n"
+        "            raise SystemExit('no error')\n"
+        "        except (RuntimeError, NotImplementedError):\n"
+        "            pass\n"
+        "assert ops.direct.normalize_rows.__name__ == 'normalize_rows'\n"
+        "print('ok')\n")
+    r = _run(code)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
