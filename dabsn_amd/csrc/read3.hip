@@ -1189,11 +1189,13 @@ __global__ void __launch_bounds__(64) decode_fused_kernel(FusedArgs<E> a) {
 
 // out[b] = sg * Ps V + pg * Pp V + ig * Pi Vn from the splits' partial softmaxes: each
 // split's accumulator is rescaled to the row maximum and divided by the row sum.
+// Four columns per thread (B * H / 4 threads: twice the waves of an 8-wide split, for a
+// loop that waits on one partial load per split and pathway).
 template <typename E>
 __global__ void __launch_bounds__(256) decode_combine_kernel(int H, int splits, const float* pacc,
                                                              const float* pstats, Gains g, E* out) {
   const int b = blockIdx.y;
-  const int h0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  const int h0 = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (h0 >= H) return;
   const float* st6 = pstats + static_cast<size_t>(b) * splits * 6;
   float M[3] = {-INFINITY, -INFINITY, -INFINITY}, L[3] = {0.f, 0.f, 0.f};
@@ -1208,23 +1210,23 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(int H, int splits, 
       if (ls > 0.f) L[p] += ls * __expf(st6[s * 6 + 2 * p] - M[p]);
     }
   const float gain[3] = {g.p[0][0], g.p[1][0], g.p[2][0]};
-  float o[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+  float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int s = 0; s < splits; ++s) {
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
       const float ls = st6[s * 6 + 2 * p + 1];
       if (ls > 0.f) {
         const float c = gain[p] * (__expf(st6[s * 6 + 2 * p] - M[p]) / L[p]);
-        float v[8];
-        ldv<float, 8>(pacc + ((static_cast<size_t>(b) * splits + s) * 3 + p) * H + h0, v);
+        const f32x4 v = *reinterpret_cast<const f32x4*>(
+            pacc + ((static_cast<size_t>(b) * splits + s) * 3 + p) * H + h0);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] += c * v[e];
+        for (int e = 0; e < 4; ++e) o[e] += c * v[e];
       }
     }
   }
-  stv<E, 8>(out + static_cast<size_t>(b) * H + h0, o);
+  E* dst = out + static_cast<size_t>(b) * H + h0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) st(dst, e, o[e]);
 }
 
 struct DecodePlan {
@@ -1317,7 +1319,7 @@ static int decode_impl(int64_t B, int64_t T, int64_t N, int64_t H, int64_t Nb, i
     else
       hipLaunchKernelGGL((decode_fused_kernel<E, 4>), grid, dim3(64), 0, stream, fa);
     DABSN_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(decode_combine_kernel<E>, dim3((unsigned)((H + 2047) / 2048), (unsigned)B),
+    hipLaunchKernelGGL(decode_combine_kernel<E>, dim3((unsigned)((H + 1023) / 1024), (unsigned)B),
                        dim3(256), 0, stream, (int)H, p.splits, pacc, pstats, g, out);
     DABSN_HIP_CHECK(hipGetLastError());
     return DABSN_OK;
