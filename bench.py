@@ -209,7 +209,7 @@ def decode_main(args):
     device = torch.device("cuda:0")
     H, B, L = args.state, args.batch, args.layers
     torch.manual_seed(0)
-    model = dabsn_amd.DABSNSequenceLM(args.vocab, H, [(H, H)] * L, residual=True, mlp_ratio=4.0)
+    model = dabsn_amd.DABSNSequenceLM(args.vocab, H, L, layers=[(H, H)] * L, residual=True, mlp_ratio=4.0)
     model = model.to(device).to(torch.bfloat16).eval()
     meas = min(args.steps, 8)  # steps with per-kernel timers, after the timed ones
     total = args.prompt + args.warmup + args.steps + meas

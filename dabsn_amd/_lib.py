@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib = None
@@ -94,7 +94,7 @@ _SIGNATURES = {
         [i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_normalize_rows": ([i32, i64, i64, vp, vp, vp, vp], i32),
     "dabsn_hip_normalize_rows_bwd": ([i32, i64, i64, vp, vp, vp, vp, vp], i32),
-    "dabsn_hip_bank_select": ([i64, i64, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_bank_select": ([i32, i64, i64, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_gather": ([i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_gather_bwd": (
         [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),
@@ -112,7 +112,7 @@ _SIGNATURES = {
     "dabsn_hip_local_field_gather": ([i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_local_field_gather_bwd": (
         [i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, sz, vp], i32),
-    "dabsn_hip_means_glue": ([i64, i64, i64, vp, i64, PTR8, vp, vp, vp, vp], i32),
+    "dabsn_hip_means_glue": ([i64, i64, i64, vp, i64, PTR8, i32, vp, vp, vp, vp], i32),
     "dabsn_hip_ce_fwd": ([i32, i64, i64, vp, i64, vp, i64, vp, vp, vp, vp], i32),
     "dabsn_hip_ce_bwd": ([i32, i64, i64, vp, i64, vp, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_read3_decode": (

@@ -147,9 +147,11 @@ __global__ void __launch_bounds__(256) normalize_bwd_kernel(int64_t rows, int H,
 // chunk of time steps; block scans combine the per-chunk running max and member counts.
 constexpr int SEL_T = 256;
 
+// With floor_bf16 the floor cummax - window is rounded to bf16, as the reference evaluates
+// it when the admission values are bf16 (read.py:185-188 in the tapes' dtype).
 __global__ void __launch_bounds__(SEL_T) select_kernel(int T, const float* adm, const float* window,
-                                                       int64_t* order, int64_t* counts,
-                                                       int32_t* rank) {
+                                                       int floor_bf16, int64_t* order,
+                                                       int64_t* counts, int32_t* rank) {
   __shared__ float smax[SEL_T];
   __shared__ int scnt[SEL_T];
   const int b = blockIdx.x, tid = threadIdx.x;
@@ -171,9 +173,10 @@ __global__ void __launch_bounds__(SEL_T) select_kernel(int T, const float* adm, 
   const float before = tid > 0 ? smax[tid - 1] : -INFINITY;
   int cnt = 0;
   float run = before;
+  auto floor_of = [&](float m) { return floor_bf16 ? round_to<bf16>(m - win) : m - win; };
   for (int t = t0; t < t1; ++t) {
     run = (t == 0 || a[t] > run) ? a[t] : run;
-    cnt += (a[t] >= run - win) ? 1 : 0;
+    cnt += (a[t] >= floor_of(run)) ? 1 : 0;
   }
   scnt[tid] = cnt;
   __syncthreads();
@@ -191,7 +194,7 @@ __global__ void __launch_bounds__(SEL_T) select_kernel(int T, const float* adm, 
   for (int t = t0; t < t1; ++t) {
     run = (t == 0 || a[t] > run) ? a[t] : run;
     int r;
-    if (a[t] >= run - win) {
+    if (a[t] >= floor_of(run)) {
       r = mpos++;
     } else {
       r = total + (t - mpos);
@@ -328,23 +331,32 @@ static inline bool vec_ok(int64_t H, std::initializer_list<const void*> ptrs) {
 // match the torch expressions up to the last-bit rounding of log1p and the norm.
 // prm = 8 fp32 scalars: p_gain, novelty_gain, null_bias, adm_p_gain, adm_novelty_gain,
 // adm_saturation_gain, adm_energy_gain, adm_bias. One thread per row.
+// `mode` reproduces the dtype the reference evaluates these expressions in: bit 0 = the
+// tapes are bf16, so the means and every tape-dtype intermediate (mean_p * H, its log1p,
+// the cocktail's norm and quotients) are rounded to bf16; bit 1 = the gains are bf16
+// too, so every product and sum is rounded as well (with fp32 gains, type promotion makes
+// them fp32). Operation order is that of read.py:58-72, 161-183.
 __global__ void __launch_bounds__(256) means_glue_kernel(int64_t rows, int N, int64_t ld,
                                                          const float* __restrict__ stats,
-                                                         float hidden, Ptr8 prm, float* kb,
-                                                         float* adm, float* ck) {
+                                                         float hidden, Ptr8 prm, int mode,
+                                                         float* kb, float* adm, float* ck) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= rows) return;
+  const bool tb = mode & 1, pb = (mode & 2) && tb;
+  auto rt = [tb](float v) { return tb ? round_to<bf16>(v) : v; };
+  auto rp = [pb](float v) { return pb ? round_to<bf16>(v) : v; };
   const float* s = stats + (i / N) * ld + (i % N) * 6;
-  const float me = s[0], mc = s[1], mn = s[2], mp = s[3];
-  const float lp = log1pf(mp * hidden);
+  const float me = rt(s[0]), mc = rt(s[1]), mn = rt(s[2]), mp = rt(s[3]);
+  const float lp = rt(log1pf(rt(mp * hidden)));
   float P[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) P[k] = prm.p[k][0];
-  if (kb) kb[i] = P[0] * lp + P[1] * mn + P[2];
-  if (adm) adm[i] = P[3] * lp + P[4] * mn + P[5] * mc + P[6] * me + P[7];
-  const float d = fmaxf(sqrtf(me * me + mc * mc + mn * mn + mp * mp), kEps);
+  if (kb) kb[i] = rp(rp(rp(P[0] * lp) + rp(P[1] * mn)) + P[2]);
+  if (adm)
+    adm[i] = rp(rp(rp(rp(rp(P[3] * lp) + rp(P[4] * mn)) + rp(P[5] * mc)) + rp(P[6] * me)) + P[7]);
+  const float d = rt(fmaxf(rt(sqrtf(me * me + mc * mc + mn * mn + mp * mp)), kEps));
   float4* o = reinterpret_cast<float4*>(ck + i * 4);
-  *o = make_float4(me / d, mc / d, mn / d, mp / d);
+  *o = make_float4(rt(me / d), rt(mc / d), rt(mn / d), rt(mp / d));
 }
 
 extern "C" {
@@ -429,12 +441,14 @@ int dabsn_hip_normalize_rows_bwd(int dtype, int64_t rows, int64_t H, const void*
   return DABSN_OK;
 }
 
-int dabsn_hip_bank_select(int64_t B, int64_t T, const float* adm, const float* window,
-                          int64_t* order, int64_t* counts, int32_t* rank, hipStream_t stream) {
+int dabsn_hip_bank_select(int adm_dtype, int64_t B, int64_t T, const float* adm,
+                          const float* window, int64_t* order, int64_t* counts, int32_t* rank,
+                          hipStream_t stream) {
   DABSN_REQUIRE(B > 0 && T > 0 && T < (1ll << 30) && B < (1ll << 31), "bank_select: bad shape");
+  DABSN_REQUIRE(adm_dtype == 0 || adm_dtype == 1, "bank_select: adm_dtype must be 0 or 1");
   DABSN_REQUIRE(adm && window && order && counts && rank, "bank_select: null pointer");
   hipLaunchKernelGGL(select_kernel, dim3((unsigned)B), dim3(SEL_T), 0, stream, (int)T, adm, window,
-                     order, counts, rank);
+                     adm_dtype, order, counts, rank);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
@@ -480,8 +494,9 @@ int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_
 }
 
 int dabsn_hip_means_glue(int64_t B, int64_t N, int64_t ld, const float* stats, int64_t hidden,
-                         const float* const* params, float* key_bias, float* admission,
+                         const float* const* params, int mode, float* key_bias, float* admission,
                          float* cocktail, hipStream_t stream) {
+  DABSN_REQUIRE(mode >= 0 && mode <= 3, "means_glue: mode must be 0..3");
   DABSN_REQUIRE(B > 0 && N >= 0 && N < (1 << 30) && ld >= 6 * N && hidden > 0,
                 "means_glue: bad shape");
   const int64_t rows = B * N;
@@ -495,8 +510,8 @@ int dabsn_hip_means_glue(int64_t B, int64_t N, int64_t ld, const float* stats, i
     prm.p[k] = params[k];
   }
   hipLaunchKernelGGL(means_glue_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256),
-                     0, stream, rows, (int)N, ld, stats, static_cast<float>(hidden), prm, key_bias,
-                     admission, cocktail);
+                     0, stream, rows, (int)N, ld, stats, static_cast<float>(hidden), prm, mode,
+                     key_bias, admission, cocktail);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }

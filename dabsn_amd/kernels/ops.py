@@ -638,12 +638,18 @@ torch.library.register_autograd("dabsn::local_field_gather", _field_bwd, setup_c
 # ---------------------------------------------------------------------------
 # Key bias, admission and cocktail from tape statistics (no autograd)
 # ---------------------------------------------------------------------------
-def means_glue(stats: Tensor, hidden: int, params: Sequence[Tensor]) -> tuple[Tensor, Tensor, Tensor]:
+def means_glue(stats: Tensor, hidden: int, params: Sequence[Tensor],
+               tape_dtype: torch.dtype = torch.float32) -> tuple[Tensor, Tensor, Tensor]:
     """(key_bias [B, N], admission [B, N], cocktail [B, N, 4]) of statistics rows
     ``stats`` [B, N, 6] (rows contiguous within a batch row; the batch stride may be
     longer, e.g. the live prefix of a bank buffer): read.py:58-72, 155-180, 680-700 in one
     kernel, for callers without autograd. ``params`` = (p_gain, novelty_gain, null_bias,
-    adm_p_gain, adm_novelty_gain, adm_saturation_gain, adm_energy_gain, adm_bias)."""
+    adm_p_gain, adm_novelty_gain, adm_saturation_gain, adm_energy_gain, adm_bias).
+
+    The values are those of the reference's expressions in the dtype they run in there:
+    with bf16 tapes (``tape_dtype``) the means and tape-dtype intermediates are bf16, and
+    with bf16 gains as well every step is; the outputs are returned as fp32 holding those
+    values."""
     _require_cuda(stats)
     if stats.dim() != 3 or stats.shape[-1] != 6 or stats.dtype != torch.float32 \
             or stats.stride(2) != 1 or stats.stride(1) != 6:
@@ -655,8 +661,12 @@ def means_glue(stats: Tensor, hidden: int, params: Sequence[Tensor]) -> tuple[Te
     adm = torch.empty_like(kb)
     ck = torch.empty((B, N, 4), device=stats.device, dtype=torch.float32)
     ptrs = _lib.PTR8(*[x.data_ptr() for x in prm])
+    mode = 0
+    if tape_dtype == torch.bfloat16:
+        mode = 1 | (2 if all(x.dtype == torch.bfloat16 for x in params) else 0)
     _lib.check(lib.dabsn_hip_means_glue(B, N, int(stats.stride(0)), _p(stats), int(hidden), ptrs,
-                                        _p(kb), _p(adm), _p(ck), _stream(stats)), "means glue")
+                                        mode, _p(kb), _p(adm), _p(ck), _stream(stats)),
+               "means glue")
     return kb, adm, ck
 
 
@@ -949,16 +959,21 @@ torch.library.register_autograd("dabsn::normalize_rows", _norm_bwd, setup_contex
 @torch.library.custom_op("dabsn::bank_select", mutates_args=(), device_types="cuda")
 def bank_select(admission: Tensor, window: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     """Admitted-slot selection (read.py:185-239): (order [B,T] int64, counts [B] int64,
-    rank [B,T] int32). Bit-exact integer work given the admission values."""
+    rank [B,T] int32). Bit-exact integer work given the admission values. The floor
+    ``cummax(admission) - window`` is evaluated in the admission's dtype, as the reference
+    does (bf16 admission: the difference is rounded to bf16)."""
     lib = _lib.load()
     B, T = admission.shape
+    if admission.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"bank_select: admission must be fp32 or bf16, not {admission.dtype}")
+    adm_code = 1 if admission.dtype == torch.bfloat16 else 0
     adm = admission.float().contiguous()
     win = window.float().reshape(()).contiguous()
     order = torch.empty((B, T), device=adm.device, dtype=torch.int64)
     counts = torch.empty((B,), device=adm.device, dtype=torch.int64)
     rank = torch.empty((B, T), device=adm.device, dtype=torch.int32)
-    _lib.check(lib.dabsn_hip_bank_select(B, T, _p(adm), _p(win), _p(order), _p(counts), _p(rank),
-                                         _stream(adm)), "bank selection")
+    _lib.check(lib.dabsn_hip_bank_select(adm_code, B, T, _p(adm), _p(win), _p(order), _p(counts),
+                                         _p(rank), _stream(adm)), "bank selection")
     return order, counts, rank
 
 

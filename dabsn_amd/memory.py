@@ -87,8 +87,20 @@ class BankStore:
         self.stats[:, self.length:need].copy_(stats)
         self.length = need
 
-    def live(self) -> tuple[Tensor, Tensor]:
-        return self.write[:, :self.length], self.stats[:, :self.length]
+    def live(self, length: int | None = None) -> tuple[Tensor, Tensor]:
+        n = self.length if length is None else int(length)
+        return self.write[:, :n], self.stats[:, :n]
+
+    def fork(self, length: int, extra: int = 0) -> "BankStore":
+        """A new store holding a copy of the first ``length`` positions, with room for
+        ``extra`` more: used when a handle whose live prefix is shorter than the storage's
+        (another handle extended the bank past it) extends or queries again."""
+        out = BankStore(self.batch, self.hidden, device=self.write.device,
+                        dtype=self.write.dtype, capacity=int(length) + int(extra))
+        if length:
+            w, st = self.live(length)
+            out.append(w, st)
+        return out
 
     def to(self, *, device=None, dtype=None) -> "BankStore":
         out = BankStore(self.batch, self.hidden, device=device or self.write.device,
@@ -111,21 +123,33 @@ class LayerMemory:
     bank: BankStore
     core: tuple[Tensor, Tensor, Tensor]
     long: tuple[Tensor, Tensor, Tensor]
+    #: Live bank positions as seen by this handle. The storage is shared by every handle
+    #: derived from one prefix and may hold more rows (written by a later extension).
+    length: int = -1
+
+    def __post_init__(self) -> None:
+        if self.length < 0:
+            self.length = self.bank.length
 
     @property
     def entries(self) -> int:
-        return self.bank.length
+        return self.length
+
+    def live(self) -> tuple[Tensor, Tensor]:
+        return self.bank.live(self.length)
 
     def nbytes(self) -> int:
-        return self.bank.nbytes() + sum(t.numel() * t.element_size()
-                                        for t in (*self.core, *self.long))
+        w, st = self.live()
+        return (w.numel() * w.element_size() + st.numel() * st.element_size()
+                + sum(t.numel() * t.element_size() for t in (*self.core, *self.long)))
 
     def to(self, *, device=None, dtype=None) -> "LayerMemory":
         """A copy on ``device``; ``dtype`` applies to the bank's write vectors (the
         statistics and the carried core and long states stay fp32)."""
-        return LayerMemory(bank=self.bank.to(device=device, dtype=dtype),
-                           core=tuple(t.to(device=device) for t in self.core),
-                           long=tuple(t.to(device=device) for t in self.long))
+        bank = self.bank.fork(self.length).to(device=device, dtype=dtype)
+        return LayerMemory(bank=bank, core=tuple(t.to(device=device) for t in self.core),
+                           long=tuple(t.to(device=device) for t in self.long),
+                           length=self.length)
 
 
 @dataclass
@@ -161,24 +185,41 @@ class DABSNMemory:
 
 
 def fingerprint_of(model: DABSNSequenceLM) -> dict[str, object]:
-    """Architecture identity a memory must match (memory.py:149-161)."""
-    blocks = list(model.blocks)
+    """Architecture identity a memory must match: the reference's dictionary, key for key
+    (memory.py:149-161), so files cross-load in both directions."""
     return {
-        "vocab": int(model.embed.num_embeddings),
-        "hidden_dim": int(model.embed.embedding_dim),
-        "depth": len(blocks),
-        "layers": [[int(b.hidden_dim), int(b.state_dim), b.read_geometry] for b in blocks],
-        "residual": bool(blocks[0].residual) if blocks else False,
-        "mlp_ratio": blocks[0].mlp_ratio if blocks else None,
+        "vocab": int(model.vocab),
+        "hidden_dim": int(model.hidden_dim),
+        "depth": int(model.depth),
+        "layers": [spec.to_metadata() for spec in model.layers],
+        "tie_embeddings": bool(model.tie_embeddings),
+        "residual": bool(model.residual),
+        "mlp_ratio": model.mlp_ratio,
+        "mlp_middle_depth": int(model.mlp_middle_depth),
+        "mlp_depth_index": int(model.mlp_depth_index),
     }
 
 
-def _check(memory: DABSNMemory, model: DABSNSequenceLM, batch: int) -> None:
+def _check_fingerprint(memory: DABSNMemory, model: DABSNSequenceLM) -> None:
+    """The reference's rule (memory.py:164-181): an empty fingerprint passes; keys that
+    predate residual/MLP support default to the disabled architecture; anything else must
+    equal the model's fingerprint."""
+    if not memory.fingerprint:
+        return
     expected = fingerprint_of(model)
-    if memory.fingerprint and dict(memory.fingerprint) != expected:
-        bad = [f"{k}: memory={memory.fingerprint.get(k)!r} model={v!r}"
-               for k, v in expected.items() if memory.fingerprint.get(k) != v]
+    observed = dict(memory.fingerprint)
+    observed.setdefault("residual", False)
+    observed.setdefault("mlp_ratio", None)
+    observed.setdefault("mlp_middle_depth", 0)
+    observed.setdefault("mlp_depth_index", 0)
+    if observed != expected:
+        bad = [f"{k}: memory={observed.get(k)!r} model={v!r}"
+               for k, v in expected.items() if observed.get(k) != v]
         raise ValueError("memory was built by a different architecture: " + "; ".join(bad))
+
+
+def _check(memory: DABSNMemory, model: DABSNSequenceLM, batch: int) -> None:
+    _check_fingerprint(memory, model)
     if memory.batch_size != batch:
         raise ValueError(f"memory holds batch {memory.batch_size} but ids are batch {batch}; "
                          "a bank is per-lane and cannot be rebatched")
@@ -210,6 +251,10 @@ def _block_step(block: DABSNBlock, inputs: Tensor, layer: LayerMemory | None,
     if layer is None:
         bank = BankStore(batch, block.state_dim, device=write.device, dtype=write.dtype,
                          capacity=int(write.shape[1]))
+    elif layer.bank.length != layer.length:
+        # Another handle extended this storage past our prefix: copy the prefix, so the
+        # two continuations never read each other's rows.
+        bank = layer.bank.fork(layer.length, int(write.shape[1]))
     else:
         bank = layer.bank
     bank.append(write, stats)
@@ -239,7 +284,7 @@ def _run(model: DABSNSequenceLM, ids: Tensor, memory: DABSNMemory | None, *,
         _check(memory, model, batch)
         state = list(memory.layers)
         position = memory.position
-    lengths = [layer.bank.length for layer in memory.layers] if memory is not None else []
+    lengths = [layer.length for layer in memory.layers] if memory is not None else []
     outputs = []
     with torch.no_grad(), ops.reuse_parameter_copies():
         for start, stop in _chunks(int(ids.shape[1]), chunk_size):
@@ -251,9 +296,11 @@ def _run(model: DABSNSequenceLM, ids: Tensor, memory: DABSNMemory | None, *,
     hidden = outputs[0] if len(outputs) == 1 else torch.cat(outputs, dim=1)
     if memory is not None and not extend:
         # A read-only query (memory.py:340-345): the rows appended past each bank's live
-        # prefix are dropped, and the carried core/long states were never modified.
-        for layer, n in zip(memory.layers, lengths):
-            layer.bank.length = n
+        # prefix are dropped (the storage's length returns to the handle's), and the
+        # carried core/long states were never modified.
+        for layer, new_state, n in zip(memory.layers, state, lengths):
+            if new_state is not None and new_state.bank is layer.bank:
+                layer.bank.length = n
         return hidden, memory
     result = DABSNMemory(layers=[s for s in state if s is not None], position=position,
                          batch_size=batch, fingerprint=fingerprint_of(model))
@@ -292,7 +339,7 @@ def _to_payload(memory: DABSNMemory) -> dict[str, object]:
     round trip is exact; the reference's loader takes only its five fields."""
     layers = []
     for layer in memory.layers:
-        write, stats = layer.bank.live()
+        write, stats = layer.live()
         bank = {"write": write.detach().cpu()}
         for name in MEAN_FIELDS:
             bank[f"{name}_mean"] = stats[..., _STATS_COLUMN[name]].detach().cpu().to(write.dtype)
@@ -344,19 +391,14 @@ def _from_payload(payload) -> DABSNMemory:
 
 
 def _check_loaded(memory: DABSNMemory, model: DABSNSequenceLM) -> None:
-    """Architecture check for a loaded memory: the identity fields both packages record
-    (vocab, width, depth) must match the model, and each bank's width must be a block's
-    state width."""
-    want = fingerprint_of(model)
-    for key in ("vocab", "hidden_dim", "depth"):
-        if key in memory.fingerprint and memory.fingerprint[key] != want[key]:
-            raise ValueError(f"memory was built by a different architecture: {key}: "
-                             f"memory={memory.fingerprint[key]!r} model={want[key]!r}")
+    """A loaded memory must match the model (memory.py:164-181, 479-486), and each bank's
+    width must be its block's state width."""
+    _check_fingerprint(memory, model)
     blocks = list(model.blocks)
     if len(memory.layers) != len(blocks) or any(
             layer.bank.hidden != int(block.state_dim) for layer, block in zip(memory.layers, blocks)):
         raise ValueError("memory layers do not match the model's blocks")
-    memory.fingerprint = want
+    memory.fingerprint = fingerprint_of(model)
 
 
 def save(memory: DABSNMemory, path) -> Path:

@@ -3,14 +3,16 @@
 ``DABSNBlock`` follows the reference block (src/dabsn/model.py:110-378): core scan
 (optionally time-chunked with a carried (b, e, c) state and a per-chunk checkpoint,
 model.py:197-307), read, ``state_to_hidden(y + read_gain * read)``, residual and the
-optional squared-ReLU MLP. ``DABSNSequenceLM`` is a small token-in/logits-out harness
-around a stack of seq blocks, used to drive the hot path in tests and the benchmark;
-it is not a port of the reference's backbone/graph machinery.
+optional squared-ReLU MLP. ``DABSNSequenceLM`` keeps the reference LM's constructor and state-dict
+layout around a stack of seq blocks (model.py:381-436, 804-860); the reference's
+graph machinery and non-seq geometries are not part of this backend.
 """
 
 from __future__ import annotations
 
 import os
+from dataclasses import dataclass
+from typing import Mapping
 
 import torch
 import torch.nn as nn
@@ -134,27 +136,152 @@ class DABSNBlock(nn.Module):
         return self.forward_mlp(self.forward_world(inputs))
 
 
-class DABSNSequenceLM(nn.Module):
-    """Token embedding -> seq DABSN blocks -> readout (test/benchmark harness)."""
+@dataclass(frozen=True)
+class DABSNLayerSpec:
+    """Width and read geometry of one block (reference config.py:34-58)."""
 
-    def __init__(self, vocab: int, hidden_dim: int, layers: list[tuple[int, int]], *,
-                 residual: bool = False, mlp_ratio: float | None = None,
-                 block_chunk_t: int | None = None) -> None:
+    hidden_dim: int
+    state_dim: int | None = None
+    read_geometry: str = "seq"
+
+    def __post_init__(self) -> None:
+        if int(self.hidden_dim) <= 0:
+            raise ValueError("hidden_dim must be positive")
+        if self.state_dim is not None and int(self.state_dim) <= 0:
+            raise ValueError("state_dim must be positive")
+        if self.read_geometry not in {"seq", "field", "hybrid"}:
+            raise ValueError("read_geometry must be seq, field, or hybrid")
+
+    @property
+    def resolved_state_dim(self) -> int:
+        return int(self.hidden_dim if self.state_dim is None else self.state_dim)
+
+    def to_metadata(self) -> dict[str, object]:
+        return {"hidden_dim": int(self.hidden_dim),
+                "state_dim": None if self.state_dim is None else int(self.state_dim),
+                "read_geometry": self.read_geometry}
+
+
+def parse_layer_specs(spec) -> list[DABSNLayerSpec]:
+    """Layer specs from the reference's compact form ``geometry:hidden[:state]`` (comma or
+    semicolon separated), from mappings with ``hidden_dim``/``state_dim``/``read_geometry``
+    (or ``hidden``/``state``/``geometry``), from ``DABSNLayerSpec`` objects, or from
+    ``(hidden, state)`` pairs (seq geometry). Mirrors config.py:61-116."""
+    if spec is None:
+        return []
+    if isinstance(spec, str):
+        out = []
+        for part in (x.strip() for x in spec.replace(";", ",").split(",")):
+            if not part:
+                continue
+            fields = [f.strip() for f in part.split(":")]
+            if len(fields) not in (2, 3):
+                raise ValueError(f"compact DABSN layer specs must be geometry:hidden[:state], "
+                                 f"got {part!r}")
+            state = int(fields[2]) if len(fields) == 3 and fields[2] else None
+            out.append(DABSNLayerSpec(int(fields[1]), state, fields[0]))
+        return out
+    out = []
+    for item in spec:
+        if isinstance(item, DABSNLayerSpec):
+            out.append(item)
+        elif isinstance(item, Mapping):
+            hidden = item.get("hidden", item.get("hidden_dim"))
+            if hidden is None:
+                raise ValueError(f"DABSN layer spec missing hidden/hidden_dim: {item!r}")
+            state = item.get("state", item.get("state_dim"))
+            geometry = str(item.get("geometry", item.get("read_geometry", "seq")))
+            out.append(DABSNLayerSpec(int(hidden), None if state is None else int(state), geometry))
+        elif isinstance(item, (tuple, list)) and len(item) == 2:
+            out.append(DABSNLayerSpec(int(item[0]), int(item[1]), "seq"))
+        else:
+            raise ValueError(f"unsupported DABSN layer spec entry {item!r}")
+    return out
+
+
+class DABSNBackbone(nn.Module):
+    """The stack of blocks (reference model.py:381-436 for seq blocks without middle MLPs):
+    each block's world view followed by its inline MLP."""
+
+    def __init__(self, input_dim: int, layers, *, residual: bool = False,
+                 mlp_ratio: float | None = None, block_chunk_t: int | None = None) -> None:
         super().__init__()
-        self.embed = nn.Embedding(vocab, hidden_dim)
+        self.input_dim = int(input_dim)
+        self.layer_specs = parse_layer_specs(layers)
+        if not self.layer_specs:
+            raise ValueError("DABSN needs at least one layer spec")
         blocks = []
-        width = hidden_dim
-        for hidden, state in layers:
-            blocks.append(DABSNBlock(width, hidden, state, "seq", residual=residual,
-                                     mlp_ratio=mlp_ratio, block_chunk_t=block_chunk_t))
-            width = hidden
+        width = self.input_dim
+        for spec in self.layer_specs:
+            blocks.append(DABSNBlock(width, spec.hidden_dim, spec.resolved_state_dim,
+                                     spec.read_geometry, residual=residual, mlp_ratio=mlp_ratio,
+                                     block_chunk_t=block_chunk_t))
+            width = spec.hidden_dim
         self.blocks = nn.ModuleList(blocks)
-        self.readout = nn.Linear(width, vocab)
+        self.output_dim = width
+
+    def forward(self, inputs: Tensor) -> Tensor:
+        h = inputs
+        for block in self.blocks:
+            h = block(h)
+        return h
+
+
+class DABSNSequenceLM(nn.Module):
+    """Token embedding -> seq DABSN blocks -> readout.
+
+    Same constructor, attributes and state-dict layout (``embed``, ``backbone.blocks.<k>``,
+    ``readout``) as the reference's ``DABSNSequenceLM`` (model.py:804-860), so its weights
+    and carried-memory files are interchangeable. ``layers`` takes the reference's layer
+    specs (e.g. ``"seq:2048:2048,seq:2048:2048"``); without it, ``depth`` blocks of
+    ``hidden_dim`` (state ``state_dim``) are built. Only the seq read geometry is built
+    here; the field/hybrid geometries and the middle MLP stack are outside this backend.
+    """
+
+    is_dabsn_sequence_lm = True
+
+    def __init__(self, vocab: int, hidden_dim: int, depth: int = 1, layer_geometries=None, *,
+                 layers=None, state_dim: int | None = None, tie_embeddings: bool = False,
+                 grad_checkpoint: bool = False, residual: bool = False,
+                 mlp_ratio: float | None = None, mlp_middle_depth: int = 0,
+                 mlp_depth_index: int = 0, block_chunk_t: int | None = None) -> None:
+        super().__init__()
+        del grad_checkpoint  # block time-chunking (block_chunk_t) is this backend's checkpoint
+        if int(mlp_middle_depth) != 0:
+            raise NotImplementedError("middle MLP stacks are outside the ROCm scan+read backend")
+        self.vocab = int(vocab)
+        self.hidden_dim = int(hidden_dim)
+        self.state_dim = None if state_dim is None else int(state_dim)
+        self.tie_embeddings = bool(tie_embeddings)
+        self.residual = bool(residual)
+        self.mlp_ratio = None if mlp_ratio is None else float(mlp_ratio)
+        self.mlp_middle_depth = int(mlp_middle_depth)
+        self.mlp_depth_index = int(mlp_depth_index)
+        specs = parse_layer_specs(layers)
+        if not specs:
+            geoms = layer_geometries or "seq"
+            if isinstance(geoms, str):
+                geoms = [g for g in geoms.replace(",", " ").split() if g]
+            specs = [DABSNLayerSpec(self.hidden_dim, self.state_dim, geoms[i % len(geoms)])
+                     for i in range(int(depth))]
+        self.layers = specs
+        self.depth = len(specs)
+        self.layer_geometries = [s.read_geometry for s in specs]
+        self.embed = nn.Embedding(self.vocab, self.hidden_dim)
+        self.backbone = DABSNBackbone(self.hidden_dim, specs, residual=self.residual,
+                                      mlp_ratio=self.mlp_ratio, block_chunk_t=block_chunk_t)
+        self.readout = nn.Linear(self.backbone.output_dim, self.vocab)
+        if self.tie_embeddings and self.backbone.output_dim == self.hidden_dim:
+            self.readout.weight = self.embed.weight
         nn.init.normal_(self.embed.weight, mean=0.0, std=0.02)
         nn.init.zeros_(self.readout.bias)
 
+    @property
+    def blocks(self) -> nn.ModuleList:
+        return self.backbone.blocks
+
+    def forward_hidden(self, ids: Tensor) -> Tensor:
+        return self.backbone(self.embed(ids))
+
     def forward(self, ids: Tensor) -> Tensor:
-        h = self.embed(ids)
-        for block in self.blocks:
-            h = block(h)
-        return self.readout(h)
+        return self.readout(self.forward_hidden(ids))

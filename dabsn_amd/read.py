@@ -67,6 +67,20 @@ def _cocktail(mean_e, mean_c, mean_n, mean_p) -> Tensor:
     return F.normalize(torch.stack([mean_e, mean_c, mean_n, mean_p], dim=-1), dim=-1)
 
 
+def _tape_means(stats: Tensor, energy: Tensor, saturation: Tensor, novelty: Tensor,
+                plasticity: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """The four means of a ``read_tape_stats`` row, each in its tape's dtype.
+
+    The reference takes ``x.mean(dim=-1)`` of the tapes (read.py:58-72, 161-183), which
+    returns the tape dtype: with bf16 tapes the key bias, admission, cocktail and the
+    admission floor are evaluated from bf16-rounded means, in bf16 arithmetic wherever type
+    promotion keeps them there. The stats kernel sums in fp32; rounding its means to the
+    tape dtype gives the reference's values, so slot selection sees the same admission.
+    """
+    means = stats.unbind(-1)[:4]
+    return tuple(m.to(t.dtype) for m, t in zip(means, (energy, saturation, novelty, plasticity)))
+
+
 class DABSNRead(nn.Module):
     """The canonical DABSN memory read (seq geometry)."""
 
@@ -158,7 +172,7 @@ class DABSNRead(nn.Module):
         rp = self.short_read
         _, seq_len, hidden = expression.shape
         stats = ops.direct.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
-        mean_e, mean_c, mean_n, mean_p = stats.unbind(-1)[:4]
+        mean_e, mean_c, mean_n, mean_p = _tape_means(stats, energy, saturation, novelty, plasticity)
         norm_ay = stats[..., 4].detach()
         norm_w = stats[..., 5].detach()
         query = ops.direct.normalize_rows(expression, norm_ay)
@@ -213,8 +227,8 @@ class DABSNRead(nn.Module):
         q_stats = ops.direct.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
         b_stats = ops.direct.read_tape_stats(bank_novelty, bank_p, bank_energy, bank_saturation,
                                       bank_write, bank_write)
-        qe, qc, qn, qp = q_stats.unbind(-1)[:4]
-        be, bc, bn, bp = b_stats.unbind(-1)[:4]
+        qe, qc, qn, qp = _tape_means(q_stats, energy, saturation, novelty, plasticity)
+        be, bc, bn, bp = _tape_means(b_stats, bank_energy, bank_saturation, bank_novelty, bank_p)
         query = ops.direct.normalize_rows(expression, q_stats[..., 4].detach())
         key_bias = rp.key_bias_from_means(bn, bp, hidden)
         admission = rp.admission_from_means(be, bc, bn, bp, hidden)
@@ -253,16 +267,20 @@ class DABSNRead(nn.Module):
         if bank_len <= 0:
             raise RuntimeError("query-bank read requires a non-empty bank")
         query = ops.direct.normalize_rows(expression, query_stats[..., 4].detach())
+        tape_dtype = bank_write.dtype
         if not torch.is_grad_enabled() and bank_stats.is_cuda:
             # Inference (streaming decode): the per-position glue of the whole bank in one
             # kernel instead of ~25 small ones per layer and token.
             prm = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain,
                    rp.adm_novelty_gain, rp.adm_saturation_gain, rp.adm_energy_gain, rp.adm_bias)
-            key_bias, admission, bank_cocktail = ops.means_glue(bank_stats, hidden, prm)
-            cocktails = (ops.means_glue(query_stats, hidden, prm)[2], bank_cocktail)
+            key_bias, admission, bank_cocktail = ops.means_glue(bank_stats, hidden, prm, tape_dtype)
+            cocktails = (ops.means_glue(query_stats, hidden, prm, tape_dtype)[2], bank_cocktail)
+            if tape_dtype == torch.bfloat16 and rp.adm_bias.dtype == torch.bfloat16:
+                # The reference's admission is a bf16 tensor here: its floor is bf16 too.
+                admission = admission.to(torch.bfloat16)
         else:
-            qe, qc, qn, qp = query_stats.unbind(-1)[:4]
-            be, bc, bn, bp = bank_stats.unbind(-1)[:4]
+            qe, qc, qn, qp = (m.to(tape_dtype) for m in query_stats.unbind(-1)[:4])
+            be, bc, bn, bp = (m.to(tape_dtype) for m in bank_stats.unbind(-1)[:4])
             key_bias = rp.key_bias_from_means(bn, bp, hidden)
             admission = rp.admission_from_means(be, bc, bn, bp, hidden)
             cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))

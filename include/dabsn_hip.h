@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 2
+#define DABSN_HIP_ABI_VERSION 3
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -194,16 +194,22 @@ int dabsn_hip_normalize_rows_bwd(int dtype, int64_t rows, int64_t H, const void*
  * norm, write norm), row n of batch b at stats + b * ld + 6 n; params = 8 fp32 device
  * scalars (p_gain, novelty_gain, null_bias, adm_p_gain, adm_novelty_gain,
  * adm_saturation_gain, adm_energy_gain, adm_bias); outputs key_bias, admission [B, N]
- * (either may be NULL) and cocktail [B, N, 4] = normalize(means) (16-byte aligned). */
+ * (either may be NULL) and cocktail [B, N, 4] = normalize(means) (16-byte aligned).
+ * `mode` gives the dtype the reference evaluates the expressions in: 0 = fp32; bit 0 =
+ * bf16 tapes (the means and the tape-dtype intermediates are rounded to bf16); bit 1 (with
+ * bit 0) = bf16 gains as well (every product and sum rounded to bf16). */
 int dabsn_hip_means_glue(int64_t B, int64_t N, int64_t ld, const float* stats, int64_t hidden,
-                         const float* const* params, float* key_bias, float* admission,
+                         const float* const* params, int mode, float* key_bias, float* admission,
                          float* cocktail, hipStream_t stream);
 /* Admitted-slot selection (src/dabsn/read.py:185-239, seq geometry): per row, floor =
  * cummax(adm) - window, member = adm >= floor, order = stable partition (members by
  * ascending t, then the rest), counts = #members, rank[t] = position of t in order.
- * adm [B,T] fp32; window points at an fp32 scalar (already softplus-ed). Bit-exact. */
-int dabsn_hip_bank_select(int64_t B, int64_t T, const float* adm, const float* window,
-                          int64_t* order, int64_t* counts, int32_t* rank, hipStream_t stream);
+ * adm [B,T] as fp32 values; window points at an fp32 scalar (already softplus-ed).
+ * adm_dtype = the dtype the admission was computed in: 1 (bf16) rounds the floor to bf16
+ * as the reference's bf16 subtraction does, 0 (fp32) keeps it fp32. Bit-exact. */
+int dabsn_hip_bank_select(int adm_dtype, int64_t B, int64_t T, const float* adm,
+                          const float* window, int64_t* order, int64_t* counts, int32_t* rank,
+                          hipStream_t stream);
 
 /* Bank gather (read.py:241-256, 298-303): for j < N, K = w[idx]/max(|w[idx]|,eps),
  * V = w[idx], Vn = w[next_idx] ([B,N,H]). norm_w [B,T] fp32. */

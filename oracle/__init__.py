@@ -298,8 +298,26 @@ def tape_stats(nov, pl, en, sat, ay, wr, gains):
             "admission": adm, "cocktail": cock}
 
 
-def bank_select(adm, window):
-    """Restates read.py:185-239 (seq). Returns (order [B,T] int64, counts [B] int64)."""
+def round_bf16(x) -> np.ndarray:
+    """fp32 -> nearest bf16 (ties to even), returned as fp32 values: what
+    ``tensor.to(torch.bfloat16)`` stores for finite inputs."""
+    bits = _f32(x).view(np.uint32).astype(np.uint64)
+    bits = (bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000
+    return bits.astype(np.uint32).view(np.float32)
+
+
+def bank_select(adm, window, floor_bf16: bool = False):
+    """Restates read.py:185-239 (seq). Returns (order [B,T] int64, counts [B] int64).
+
+    With ``floor_bf16`` the admission values are bf16 values and the floor
+    ``cummax(adm) - window`` is rounded to bf16, as the reference's bf16 subtraction does
+    (its result is computed in fp32 and rounded once)."""
+    if floor_bf16:
+        a = _f32(adm)
+        floor = round_bf16(np.maximum.accumulate(a, axis=1) - np.float32(window))
+        member = a >= floor
+        order = np.argsort(~member, axis=1, kind="stable").astype(np.int64)
+        return order, member.sum(axis=1).astype(np.int64)
     adm = _f32(adm)
     B, T = adm.shape
     order = np.empty((B, T), np.int64)

@@ -5,7 +5,8 @@ Their gradients come from torch autograd, independently of the hand-derived
 analytic backward passes in ``dabsn_oracle.c``, so a dropped term, a wrong sign or
 a transposed operand in the C backward shows up as a mismatch.
 
-  core_loop      core.py:171-221 (DABSNCore._reference_forward_from_state loop)
+  core_loop      core.py:171-221 (DABSNCore._reference_forward_from_state loop); core_op
+                 and core_module_forward wrap it as the registered op and the module
   dense_read     admitted.py:9-65 (dense-mask three-way read)
   long_loop      read.py:625-636 (DABSNRead._long_scan_from_state loop)
   linrec_loop    long.py:24-32 (_linrec_reference)
@@ -58,6 +59,35 @@ def core_loop(Wx, Wgx, Ug, A, vec, logit_alpha, log_lambda, logit_c_suppress, b0
     st = {k: torch.stack(v, dim=1) for k, v in outs.items()}
     return (st["U"], st["n"], st["p"], st["ay"], st["w"], st["e"], st["c"], st["s"],
             budget, energy, saturation)
+
+
+def core_op(*inputs):
+    """The registered op's 26 inputs in schema order (batched_runtime.py:1507-1535) ->
+    its 11 outputs, through ``core_loop``."""
+    Wx, Wgx, Ug, A = inputs[:4]
+    vec = inputs[4:20]
+    la, ll, ls = inputs[20:23]
+    b0, e0, c0 = inputs[23:26]
+    return core_loop(Wx, Wgx, Ug, A, vec, la, ll, ls, b0, e0, c0)
+
+
+_MODULE_VECS = ("beta", "log_kappa", "logit_recover", "k_s", "k_y", "k_b", "k_n", "k_bias",
+                "r_s", "r_y", "r_b", "r_n", "r_bias", None, "k_saturation", "r_saturation")
+
+
+def core_module_forward(params, x, state):
+    """``DABSNCore._reference_forward_from_state`` with return_writes, return_cocktail and
+    return_final_state (core.py:111-246, projections at 281-282): ``params`` maps the
+    module's parameter names to tensors. Returns (trajectory, novelty, plasticity,
+    expression, write, energy, saturation, final b, final e, final c)."""
+    H = params["beta"].shape[0]
+    Wx = F.linear(x, params["W.weight"])
+    Wgx = F.linear(x, params["Wg.weight"], params["Wg.bias"])
+    vec = [params[n] if n else params["logit_saturation_decay"].expand(H) for n in _MODULE_VECS]
+    out = core_loop(Wx, Wgx, params["Ug.weight"], params["A.weight"], vec,
+                    params["logit_alpha"].reshape(()), params["log_lambda"].reshape(()),
+                    params["logit_saturation_suppress"].reshape(()), *state)
+    return out[:7] + out[8:]
 
 
 def _masked_softmax(scores, allow, eligible):

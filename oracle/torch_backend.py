@@ -125,7 +125,8 @@ def _normalize_bwd(q, norms, gq):
 
 
 def _select(adm, window):
-    order, counts = oracle.bank_select(_np(adm), float(window.reshape(())))
+    order, counts = oracle.bank_select(_np(adm), float(window.reshape(())),
+                                       floor_bf16=adm.dtype == torch.bfloat16)
     rank = np.empty_like(order, dtype=np.int32)
     rows = np.arange(order.shape[0])[:, None]
     rank[rows, order] = np.arange(order.shape[1], dtype=np.int32)[None, :]

@@ -1,0 +1,136 @@
+"""The HIP path against vectors the reference itself produced (tests/golden/ref/).
+
+The fixtures come from the reference's Python (tests/golden/make_ref_golden.py); the CPU
+oracle is pinned to the same files by tests/test_ref_pins.py. Here the product's HIP
+operators and modules reproduce them on the GPU:
+
+  * ``dabsn::core_scan_batched`` forward and its registered backward (fp32): 1e-5;
+  * a seq ``DABSNRead.forward`` on a partially admitted bank: n_max exact, output and
+    gradients 1e-5 (parameter gradients against a floor of 1e-3 x the largest one);
+  * the bf16 read: admission values and slot selection bit-exact, through the HIP tape
+    statistics, the training-path glue and the fused decode glue;
+  * ``forward_query_bank`` with ``query_start > 0`` and a carried long state: 1e-5;
+  * the config-1-shaped model, block by block: 1e-4 (MFMA products and several fp32 ops
+    in sequence, each within 1e-5);
+  * a ``.dmem`` file written by the reference, continued on the GPU: 1e-5.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import dabsn_amd
+from dabsn_amd import kernels
+from dabsn_amd.kernels import ops
+from helpers import rel_err
+from test_ref_pins import (_bf16, _load, _read_module, _tapes, c1_block_check, grad_err,
+                           memory_lm_check)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _rocm(cuda_device):
+    kernels.enable("rocm", required=True)
+
+
+def test_core_op_vs_reference_fixture_gpu(cuda_device):
+    z = _load("core_op_fp32")
+    inputs = [torch.from_numpy(z[f"in{i}"]).to(cuda_device).requires_grad_(True)
+              for i in range(26)]
+    outs = ops.core_scan_batched(*inputs)
+    for i in range(11):
+        assert rel_err(outs[i].detach().cpu(), z[f"out{i}"]) <= 1e-5, f"output {i}"
+    loss = sum((o * torch.from_numpy(z[f"gout{i}"]).to(cuda_device)).sum()
+               for i, o in enumerate(outs) if i != 7)
+    grads = torch.autograd.grad(loss, inputs, allow_unused=True)
+    for i, g in enumerate(grads):
+        key = f"grad{i}"
+        if key in z:
+            assert g is not None and rel_err(g.cpu(), z[key]) <= 1e-5, f"grad {i}"
+
+
+def test_read_seq_vs_reference_fixture_gpu(cuda_device):
+    z = _load("read_seq_fp32")
+    H = z["y"].shape[-1]
+    read = _read_module(z, H).to(cuda_device)
+    tapes = [t.to(cuda_device).requires_grad_(True) for t in _tapes(z)]
+    out = read(*tapes)
+    assert read.last_n_max == int(z["n_max"])
+    assert rel_err(out.detach().cpu(), z["out"]) <= 1e-5
+    names = [n for n, _ in read.named_parameters()]
+    grads = torch.autograd.grad((out * torch.from_numpy(z["gout"]).to(cuda_device)).sum(),
+                                [*tapes, *read.parameters()], allow_unused=True)
+    tape_names = ("y", "budget", "expression", "write", "novelty", "plasticity", "energy",
+                  "saturation")
+    scale = max(float(np.abs(z[k]).max()) for k in z if k.startswith("grad.param."))
+    for n, g in zip(list(tape_names) + [f"param.{n}" for n in names], grads):
+        key = f"grad.{n}"
+        if key not in z:
+            continue
+        err = grad_err(g.cpu(), z[key], scale) if n.startswith("param.") else rel_err(g.cpu(), z[key])
+        assert err <= 1e-5, f"{n}: {err:.3e}"
+
+
+def test_bf16_selection_bit_exact_vs_reference_fixture_gpu(cuda_device):
+    """HIP tape statistics (fp32 sums, then rounded to bf16 like the reference's bf16
+    means), the module's glue, and the HIP selection kernel with its bf16 floor: the
+    admission and the slot order equal the reference's bit for bit. The fused decode glue
+    in its bf16 modes gives the same admission."""
+    from dabsn_amd.read import _tape_means
+
+    z = _load("read_seq_bf16")
+    names = ("y", "budget", "expression", "write", "novelty", "plasticity", "energy", "saturation")
+    tapes = [_bf16(z[f"{n}_bf16"]).to(cuda_device) for n in names]
+    H = tapes[0].shape[-1]
+    read = dabsn_amd.DABSNRead(H).to(cuda_device, torch.bfloat16)
+    with torch.no_grad():
+        for n, p in read.named_parameters():
+            p.copy_(_bf16(z[f"param.{n}_bf16"]).to(cuda_device))
+    _, _, ay, w, nov, pl, en, sat = tapes
+    with torch.no_grad():
+        stats = ops.read_tape_stats(nov, pl, en, sat, ay, w)
+        me, mc, mn, mp = _tape_means(stats, en, sat, nov, pl)
+        adm = read.short_read.admission_from_means(me, mc, mn, mp, H)
+        want = _bf16(z["admission_bf16"])
+        assert torch.equal(adm.cpu(), want)
+        order, counts, _ = ops.bank_select(adm, F.softplus(read.admit_window))
+        assert np.array_equal(order.cpu().numpy(), z["order"])
+        assert max(int(counts.max()), 1) == int(z["n_max"])
+        rp = read.short_read
+        prm = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain, rp.adm_novelty_gain,
+               rp.adm_saturation_gain, rp.adm_energy_gain, rp.adm_bias)
+        _, adm_fused, _ = ops.means_glue(stats, H, prm, torch.bfloat16)
+        assert torch.equal(adm_fused.cpu(), want.float())
+
+
+def test_query_bank_vs_reference_fixture_gpu(cuda_device):
+    z = _load("query_bank_fp32")
+    H = z["y"].shape[-1]
+    start = int(z["query_start"])
+    read = _read_module(z, H).to(cuda_device)
+    tapes = [t.to(cuda_device) for t in _tapes(z)]
+    y, budget, ay, w, nov, pl, en, sat = tapes
+    long0 = tuple(torch.from_numpy(z[f"long0_{i}"]).to(cuda_device) for i in range(3))
+    with torch.no_grad():
+        out, state = read.forward_query_bank(
+            *(t[:, start:] for t in tapes), bank_write=w, bank_novelty=nov, bank_p=pl,
+            bank_energy=en, bank_saturation=sat, query_start=start, initial_long_state=long0,
+            return_long_state=True)
+    assert read.last_n_max == int(z["n_max"])
+    assert rel_err(out.cpu(), z["out"]) <= 1e-5
+    for i, s in enumerate(state):
+        assert rel_err(s.cpu(), z[f"long1_{i}"]) <= 1e-5
+
+
+@pytest.mark.parametrize("k", [0, 1])
+def test_config1_blocks_vs_reference_fixture_gpu(cuda_device, k):
+    c1_block_check(_load("model_c1"), k, cuda_device, tol=1e-4)
+
+
+def test_reference_written_memory_file_continues_exactly_gpu(cuda_device):
+    got, want = memory_lm_check(cuda_device)
+    assert rel_err(got, want) <= 1e-5

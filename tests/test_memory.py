@@ -26,7 +26,7 @@ def _oracle_cpu_kernels():
 
 def _model(device):
     torch.manual_seed(7)
-    model = dabsn_amd.DABSNSequenceLM(40, 24, [(24, 24), (32, 16)], residual=True, mlp_ratio=2.0)
+    model = dabsn_amd.DABSNSequenceLM(40, 24, layers="seq:24:24,seq:32:16", residual=True, mlp_ratio=2.0)
     for block in model.blocks:
         block.read.admit_window.data.fill_(0.3)  # a partially admitted bank
     return model.to(device).eval()
@@ -91,7 +91,7 @@ def test_memory_refuses_other_architecture_or_batch():
                              fingerprint=mem.fingerprint_of(model))
     with pytest.raises(ValueError, match="batch"):
         mem.forward_with_memory(model, _ids(3, 4), memory)
-    other = dabsn_amd.DABSNSequenceLM(40, 24, [(24, 24)], residual=True, mlp_ratio=2.0)
+    other = dabsn_amd.DABSNSequenceLM(40, 24, layers="seq:24:24", residual=True, mlp_ratio=2.0)
     with pytest.raises(ValueError, match="different architecture"):
         mem.forward_with_memory(other, _ids(2, 4), memory)
 
@@ -117,6 +117,37 @@ def test_read_only_query_leaves_memory_unchanged_cpu():
     assert torch.equal(a, b)
     c, grown = mem.forward_with_memory(model, ids[:, 24:], memory, extend=True)
     assert torch.equal(a, c) and grown.position == 30 and grown.entries == 30
+
+
+def _branches(device):
+    """Two continuations extended from one prefix handle, each against a fresh ingest of
+    its own full sequence (the reference rebuilds the bank per call, memory.py:250-254, so
+    branching from a shared prefix is valid there)."""
+    model = _model(device)
+    ids = _ids(2, 16, seed=13).to(device)
+    alt = ids.clone()
+    alt[:, 12:] = (alt[:, 12:] + 7) % 40
+    base = mem.ingest(model, ids[:, :12], chunk_size=5)
+    out_a, mem_a = mem.forward_with_memory(model, ids[:, 12:], base, extend=True)
+    out_b, mem_b = mem.forward_with_memory(model, alt[:, 12:], base, extend=True)
+    assert base.position == 12 and [layer.entries for layer in base.layers] == [12, 12]
+    assert mem_a.position == mem_b.position == 16
+    fresh_a, _ = mem.forward_with_memory(model, ids, None, chunk_size=None)
+    fresh_b, _ = mem.forward_with_memory(model, alt, None, chunk_size=None)
+    # The first branch again, after the second one extended the shared prefix.
+    again, _ = mem.forward_with_memory(model, ids[:, 12:], base, extend=True)
+    return (out_a, fresh_a[:, 12:]), (out_b, fresh_b[:, 12:]), (again, fresh_a[:, 12:])
+
+
+def test_branching_from_one_prefix_equals_fresh_ingest_cpu():
+    for got, want in _branches("cpu"):
+        assert rel_err(got, want) <= 1e-5
+
+
+@pytest.mark.gpu
+def test_branching_from_one_prefix_equals_fresh_ingest_gpu(cuda_device):
+    for got, want in _branches(cuda_device):
+        assert rel_err(got.cpu(), want.cpu()) <= 1e-5
 
 
 @pytest.mark.gpu

@@ -1,0 +1,465 @@
+"""The oracle pinned to the reference implementation itself (CPU).
+
+Two sources, neither of them this build's code:
+
+1. ``oracle/_ref`` -- the reference's own C++ CPU backend
+   (src/dabsn/kernels/cpu_runtime.cpp), compiled from its source by ``oracle/ref.mk``.
+   The C restatement ``oracle/dabsn_oracle.c`` must reproduce it:
+     * core forward (cpu_runtime.cpp:672-837): bit-exact, all ten outputs;
+     * core backward: the reference's analytic C++ reverse (cpu_runtime.cpp:844-1072)
+       is a different algorithm from the Python reverse the oracle restates
+       (batched_runtime.py:299-466), so the two agree to fp32 rounding: 1e-5 normwise
+       for every one of the 25 gradients;
+     * three-way read forward/backward (cpu_runtime.cpp:321-438, 479-662) with dense masks
+       built as compact_admitted.py:176-198, seq and field modes, query offsets:
+       forward bit-exact, backward 1e-6;
+     * linear recurrence forward/backward (cpu_runtime.cpp:92-143): bit-exact;
+     * permanent delta scan (cpu_runtime.cpp:1075-1188) and local-field gather/scatter
+       (cpu_runtime.cpp:1191-1237): bit-exact forward, backward 1e-6.
+   These tests skip when ``oracle/_ref`` has not been built (it needs the reference
+   source tree, present only in the build container).
+
+2. ``tests/golden/ref/*.npz`` -- vectors the reference's Python produced
+   (tests/golden/make_ref_golden.py). The oracle, and the product's modules running on the
+   oracle's CPU kernels, must reproduce them:
+     * the registered core op and its Python reverse, fp32: 1e-5;
+     * the per-step loop ``_reference_forward_from_state`` in fp64 against the fp64
+       autograd restatement: 1e-10;
+     * a seq ``DABSNRead.forward`` on a partially admitted bank: slot order and n_max
+       bit-exact, output and every gradient 1e-5 (parameter gradients relative to a floor
+       of 1e-3 x the largest one, see ``grad_err``);
+     * the bf16 read's admission values and slot selection: bit-exact;
+     * ``forward_query_bank`` with ``query_start > 0`` and a carried long state;
+     * a config-1-shaped model, block by block: world-view outputs, the gradient passed
+       back to each block's input and every DABSN-path parameter gradient;
+     * a ``.dmem`` file written by the reference's ``memory.save``: loaded here and
+       continued, the next token's logits equal the reference's.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import dabsn_amd
+import oracle
+from dabsn_amd import memory as mem
+from helpers import core_case, np32, oracle_core_bwd, oracle_core_fwd, rel_err
+from oracle import autograd_ref
+from oracle import ref as oracle_ref
+from oracle import torch_backend
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "ref"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _oracle_cpu_kernels():
+    torch_backend.register()
+
+
+@pytest.fixture(scope="module")
+def R():
+    mod = oracle_ref.load()
+    if mod is None:
+        pytest.skip("oracle/_ref not built: it compiles the reference's cpu_runtime.cpp, "
+                    "which only the build container has (make -f oracle/ref.mk)")
+    return mod
+
+
+def _load(name: str) -> dict:
+    with np.load(GOLDEN / f"{name}.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _bf16(bits: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# 1. The compiled reference CPU backend
+# ---------------------------------------------------------------------------
+def _ref_scalars(inputs):
+    la, ll, ls = inputs[20:23]
+    return (float(torch.sigmoid(la)), float(F.softplus(ll)), float(torch.sigmoid(ls)))
+
+
+@pytest.mark.parametrize("B,T,H,init", [(3, 13, 20, True), (2, 1, 7, True), (1, 40, 33, False)])
+def test_core_forward_bit_exact_vs_reference_cpp(R, B, T, H, init):
+    inputs = core_case(30 + T, B, T, H, init=init)
+    Wx, Wgx, Ug, A = inputs[:4]
+    vec = inputs[4:20]
+    b0, e0, c0 = inputs[23:26]
+    out = R.dabsn_core_scan_fwd_train(Wx, Wgx, torch.cat([Ug, A], 0), *vec, b0, e0, c0,
+                                      *_ref_scalars(inputs))
+    mine = oracle_core_fwd(inputs)
+    # reference outputs: U, nov, p, ay, w, e(pre), c(post), b_pre, c_pre, bF, eF, cF
+    pairs = [(0, 0), (1, 1), (2, 2), (3, 3), (4, 4), (5, 5), (6, 6), (9, 8), (10, 9), (11, 10)]
+    for ri, mi in pairs:
+        assert np.array_equal(out[ri].numpy(), mine[mi]), f"output {mi} differs"
+    # The gate tape is not a C++ output; cpu.py:866-869 recomputes it as
+    # hardsigmoid(Wgx + y Ug^T). The oracle stores it from the step itself.
+    y = out[0][..., :H]
+    gate = F.hardsigmoid(Wgx + F.linear(y, Ug))
+    assert rel_err(mine[7], gate) <= 1e-6
+
+
+def test_core_backward_vs_reference_cpp_reverse(R):
+    B, T, H = 3, 17, 24
+    inputs = core_case(41, B, T, H)
+    Wx, Wgx, Ug, A = inputs[:4]
+    vec = inputs[4:20]
+    b0, e0, c0 = inputs[23:26]
+    sa, sl, sc = _ref_scalars(inputs)
+    GA = torch.cat([Ug, A], 0)
+    out = R.dabsn_core_scan_fwd_train(Wx, Wgx, GA, *vec, b0, e0, c0, sa, sl, sc)
+    g = torch.Generator().manual_seed(42)
+    grads = [torch.randn(out[i].shape, generator=g) for i in range(7)]
+    gfinal = [torch.randn(B, H, generator=g) for _ in range(3)]
+    rb = R.dabsn_core_scan_bwd(*grads, *gfinal, out[7], out[5], out[8], Wx, Wgx, GA, *vec,
+                               sa, sl, sc)
+    fwd = oracle_core_fwd(inputs)
+    gWx, gWgx, gGA, gvec, gscal, gb0, ge0, gc0 = oracle_core_bwd(inputs, fwd, grads + gfinal)
+    assert rel_err(gWx, rb[0]) <= 1e-5
+    assert rel_err(gWgx, rb[1]) <= 1e-5
+    assert rel_err(gGA, rb[2]) <= 1e-5
+    for i in range(16):
+        assert rel_err(gvec[i], rb[3 + i]) <= 1e-5, oracle.VEC_NAMES[i]
+    for a, b in zip((gb0, ge0, gc0), rb[19:22]):
+        assert rel_err(a, b) <= 1e-5
+    # The C++ takes the scalars after sigmoid / softplus / sigmoid: chain rule back to
+    # the registered op's logits.
+    la, ll, ls = (float(x) for x in inputs[20:23])
+    sig = lambda x: 1.0 / (1.0 + np.exp(-x))  # noqa: E731
+    want = [float(rb[22]) * sa * (1 - sa), float(rb[23]) * sig(ll), float(rb[24]) * sc * (1 - sc)]
+    assert rel_err(gscal, np.array(want, np.float32)) <= 1e-5
+
+
+def _read_case(seed, B, T, N, H, mode, offset=0):
+    g = torch.Generator().manual_seed(seed)
+    q = F.normalize(torch.randn(B, T, H, generator=g), dim=-1)
+    V = torch.randn(B, N, H, generator=g)
+    K = F.normalize(V, dim=-1)
+    Vn = torch.randn(B, N, H, generator=g)
+    ck = F.normalize(torch.rand(B, T, 4, generator=g), dim=-1)
+    cb = F.normalize(torch.rand(B, N, 4, generator=g), dim=-1)
+    kb = torch.randn(B, N, generator=g) * 0.5
+    adm = torch.randn(B, N, generator=g) * 0.5
+    total = T + offset + 2
+    idx = torch.stack([torch.randperm(total, generator=g)[:N].sort().values for _ in range(B)])
+    if mode == 0:
+        idx = idx - offset  # negative positions: bank rows before the query chunk
+    valid = torch.rand(B, N, generator=g) < 0.8
+    return q, K, V, Vn, ck, cb, kb, adm, idx, valid, total
+
+
+def _dense_masks(idx, valid, T, mode, total):
+    """compact_admitted.py:176-198 (query offset already folded into idx)."""
+    pos = torch.arange(T).view(1, T, 1)
+    v = valid.unsqueeze(1)
+    p = idx.unsqueeze(1)
+    if mode == 0:
+        allow = v & (p <= pos)
+        induct = v & (p < pos)
+    else:
+        allow = v.expand(-1, T, -1)
+        induct = (v & (p < total - 1)).expand(-1, T, -1)
+    allow, induct = allow.contiguous(), induct.contiguous()
+    return allow, induct, allow.any(-1), induct.any(-1)
+
+
+@pytest.mark.parametrize("mode,offset", [(0, 0), (0, 5), (1, 0)])
+def test_read3_vs_reference_cpp(R, mode, offset):
+    B, T, N, H = 2, 11, 7, 9
+    q, K, V, Vn, ck, cb, kb, adm, idx, valid, total = _read_case(50 + mode + offset, B, T, N, H,
+                                                                 mode, offset)
+    allow, induct, elig, ielig = _dense_masks(idx, valid, T, mode, total)
+    scale, cg, sg, pg, ig = 2.7, 0.8, 1.1, 0.9, 0.3
+    ref_out = R.three_way_read_cpu(q, K, V, Vn, ck, cb, kb, adm, allow, induct, elig, ielig,
+                                   scale, cg, sg, pg, ig)
+    mine = oracle.read3_fwd(np32(q), np32(K), np32(V), np32(Vn), np32(ck), np32(cb), np32(kb),
+                            np32(adm), scale, idx.numpy(), valid.numpy(), mode, (sg, pg, ig, cg),
+                            total_steps=total)
+    assert np.array_equal(mine, ref_out.numpy())
+    go = torch.randn(B, T, H, generator=torch.Generator().manual_seed(7))
+    rb = R.three_way_read_bwd(go, q, K, V, Vn, ck, cb, kb, adm, allow, induct, elig, ielig,
+                              scale, cg, sg, pg, ig)
+    mb = oracle.read3_bwd(np32(go), np32(q), np32(K), np32(V), np32(Vn), np32(ck), np32(cb),
+                          np32(kb), np32(adm), scale, idx.numpy(), valid.numpy(), mode,
+                          (sg, pg, ig, cg), total_steps=total)
+    # reference: gq, gK, gV, gVn, gck, gcb, gkb, gadm, gscale, gcocktail_gain, gshort, gpad, ginduct
+    # oracle:    gq, gK, gV, gVn, gck, gcb, gkb, gadm, gscale, gshort, gpad, ginduct, gcocktail_gain
+    order = [0, 1, 2, 3, 4, 5, 6, 7, 8, 10, 11, 12, 9]
+    for mi, ri in enumerate(order):
+        assert rel_err(np.asarray(mb[mi]), rb[ri].numpy()) <= 1e-6, f"grad {mi}"
+
+
+def test_linrec_bit_exact_vs_reference_cpp(R):
+    g = torch.Generator().manual_seed(60)
+    a = torch.rand(3, 37, 10, generator=g)
+    x = torch.randn(3, 37, 10, generator=g)
+    y0 = torch.randn(3, 10, generator=g)
+    gy = torch.randn(3, 37, 10, generator=g)
+    assert np.array_equal(oracle.linrec_fwd(np32(a), np32(x), np32(y0)),
+                          R.linrec_forward_cpu(a, x, y0).numpy())
+    ref = R.linrec_backward_cpu(a, x, y0, gy)
+    mine = oracle.linrec_bwd(np32(a), np32(x), np32(y0), np32(gy))
+    for m, r in zip(mine, ref):
+        assert np.array_equal(m, r.numpy())
+
+
+def test_permanent_and_local_field_vs_reference_cpp(R):
+    g = torch.Generator().manual_seed(61)
+    k = F.normalize(torch.randn(2, 9, 6, generator=g), dim=-1)
+    v = torch.randn(2, 9, 6, generator=g)
+    beta = torch.rand(2, 9, generator=g)
+    go = torch.randn(2, 9, 6, generator=g)
+    assert np.array_equal(oracle.permanent_fwd(np32(k), np32(v), np32(beta)),
+                          R.permanent_delta_scan_cpu(k, v, beta).numpy())
+    ref = R.permanent_delta_scan_bwd_cpu(k, v, beta, go)
+    mine = oracle.permanent_bwd(np32(k), np32(v), np32(beta), np32(go))
+    for m, r in zip(mine, ref):
+        assert rel_err(m, r.numpy()) <= 1e-6
+    # The reference's CPU gather takes one patch row per cell (patch [N, K]).
+    x = torch.randn(3, 10, 5, generator=g)
+    patch = torch.randint(0, 10, (10, 3), generator=g)
+    assert np.array_equal(oracle.field_gather(np32(x), patch.numpy()),
+                          R.local_field_gather_cpu(x, patch).numpy())
+    gout = torch.randn(3, 10, 3, 5, generator=g)
+    assert rel_err(oracle.field_gather_bwd(np32(gout), patch.numpy(), 10),
+                   R.local_field_gather_bwd_cpu(gout, patch, 10).numpy()) <= 1e-6
+
+
+# ---------------------------------------------------------------------------
+# 2. Vectors produced by the reference's Python
+# ---------------------------------------------------------------------------
+def _core_op_case(z):
+    inputs = [torch.from_numpy(z[f"in{i}"]) for i in range(26)]
+    outs = [z[f"out{i}"] for i in range(11)]
+    gouts = [None if i == 7 else z[f"gout{i}"] for i in range(11)]
+    grads = [z.get(f"grad{i}") for i in range(26)]
+    return inputs, outs, gouts, grads
+
+
+def test_oracle_core_op_vs_reference_fixture_fp32():
+    inputs, outs, gouts, grads = _core_op_case(_load("core_op_fp32"))
+    mine = oracle_core_fwd(inputs)
+    for i in range(11):
+        assert rel_err(mine[i], outs[i]) <= 1e-5, f"output {i}"
+    up = [gouts[i] for i in (0, 1, 2, 3, 4, 5, 6, 8, 9, 10)]
+    gWx, gWgx, gGA, gvec, gscal, gb0, ge0, gc0 = oracle_core_bwd(inputs, mine, up)
+    H = inputs[0].shape[-1]
+    assert rel_err(gWx, grads[0]) <= 1e-5
+    assert rel_err(gWgx, grads[1]) <= 1e-5
+    assert rel_err(gGA[:H], grads[2]) <= 1e-5 and rel_err(gGA[H:], grads[3]) <= 1e-5
+    for i in range(16):
+        assert rel_err(gvec[i], grads[4 + i]) <= 1e-5, oracle.VEC_NAMES[i]
+    for i in range(3):
+        assert rel_err(gscal[i], grads[20 + i]) <= 1e-5
+    for a, i in zip((gb0, ge0, gc0), (23, 24, 25)):
+        assert rel_err(a, grads[i]) <= 1e-5
+
+
+def test_fp64_autograd_restatement_vs_reference_loop_fixture():
+    """oracle/autograd_ref.py (fp64) against the reference's per-step loop
+    ``_reference_forward_from_state`` run in fp64 and differentiated by autograd. (The
+    registered op itself computes in fp32 whatever its input dtype, batched_runtime.py:
+    1403-1410, so only the loop gives an fp64 reference.)"""
+    z = _load("core_loop_fp64")
+    params = {k[len("param."):]: torch.from_numpy(v).requires_grad_(True)
+              for k, v in z.items() if k.startswith("param.")}
+    x = torch.from_numpy(z["x"]).requires_grad_(True)
+    state = [torch.from_numpy(z[n]).requires_grad_(True) for n in ("b0", "e0", "c0")]
+    outs = autograd_ref.core_module_forward(params, x, state)
+    for i, o in enumerate(outs):
+        assert rel_err(o.detach().numpy(), z[f"out{i}"]) <= 1e-10, f"loop output {i}"
+    loss = sum((o * torch.from_numpy(z[f"gout{i}"])).sum() for i, o in enumerate(outs))
+    names = ["x", "b0", "e0", "c0"] + [f"param.{n}" for n in params]
+    got = torch.autograd.grad(loss, [x, *state, *params.values()], allow_unused=True)
+    for n, g in zip(names, got):
+        if f"grad.{n}" in z:
+            assert g is not None and rel_err(g.numpy(), z[f"grad.{n}"]) <= 1e-10, n
+
+
+def _tapes(z, dtype=torch.float32, grad=False):
+    names = ("y", "budget", "expression", "write", "novelty", "plasticity", "energy", "saturation")
+    ts = [torch.from_numpy(z[n]).to(dtype) for n in names]
+    return [t.requires_grad_(grad) for t in ts]
+
+
+def _read_module(z, H, suffix=""):
+    read = dabsn_amd.DABSNRead(H)
+    with torch.no_grad():
+        for n, p in read.named_parameters():
+            src = z[f"param.{n}{suffix}"]
+            p.copy_(_bf16(src).float() if suffix else torch.from_numpy(src))
+    return read
+
+
+def grad_err(got, want, scale: float) -> float:
+    """Normwise error of a parameter gradient, relative to max(max|want|, 1e-3 * scale)
+    where ``scale`` is the largest parameter gradient of the module. A scalar gain's
+    gradient is a sum over all (query, slot) terms; where those cancel (null_bias and
+    adm_bias shift every score of a softmax row equally, so their exact gradient is 0;
+    cocktail_gain sums O(1) terms to O(1e-3)), both sides carry fp32 rounding of the
+    terms, not of the small total."""
+    g = np.asarray(np32(got), np.float64)
+    w = np.asarray(np32(want), np.float64)
+    return float(np.abs(g - w).max()) / max(float(np.abs(w).max()), 1e-3 * scale, 1e-30)
+
+
+def test_read_seq_vs_reference_fixture():
+    z = _load("read_seq_fp32")
+    H = z["y"].shape[-1]
+    read = _read_module(z, H)
+    tapes = _tapes(z, grad=True)
+    out = read(*tapes)
+    assert read.last_n_max == int(z["n_max"])
+    assert rel_err(out.detach(), z["out"]) <= 1e-5
+    # Slot order: the selection the product runs equals the reference's argsort.
+    stats = oracle.tape_stats(*(np32(t) for t in tapes[4:8]), np32(tapes[2]), np32(tapes[3]),
+                              _gains(read))
+    order, _ = oracle.bank_select(stats["admission"], float(F.softplus(read.admit_window)))
+    assert np.array_equal(order, z["order"])
+    names = [n for n, _ in read.named_parameters()]
+    grads = torch.autograd.grad((out * torch.from_numpy(z["gout"])).sum(),
+                                [*tapes, *read.parameters()], allow_unused=True)
+    tape_names = ("y", "budget", "expression", "write", "novelty", "plasticity", "energy",
+                  "saturation")
+    scale = max(float(np.abs(z[k]).max()) for k in z if k.startswith("grad.param."))
+    for n, g in zip(list(tape_names) + [f"param.{n}" for n in names], grads):
+        key = f"grad.{n}"
+        if key not in z:
+            continue
+        err = grad_err(g, z[key], scale) if n.startswith("param.") else rel_err(g, z[key])
+        assert err <= 1e-5, f"{n}: {err:.3e}"
+
+
+def _gains(read):
+    rp = read.short_read
+    return [float(x) for x in (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain,
+                               rp.adm_novelty_gain, rp.adm_saturation_gain, rp.adm_energy_gain,
+                               rp.adm_bias)]
+
+
+def test_bf16_admission_and_selection_bit_exact_vs_reference_fixture():
+    """The bf16 read: admission from bf16 tape means in bf16 arithmetic (read.py:58-72),
+    the floor in bf16, and the stable partition -- bit for bit. The same selection made from
+    fp32 means (what this package did before) differs on this fixture, so the test has
+    teeth."""
+    z = _load("read_seq_bf16")
+    names = ("y", "budget", "expression", "write", "novelty", "plasticity", "energy", "saturation")
+    tapes = [_bf16(z[f"{n}_bf16"]) for n in names]
+    H = tapes[0].shape[-1]
+    read = dabsn_amd.DABSNRead(H).to(torch.bfloat16)
+    with torch.no_grad():
+        for n, p in read.named_parameters():
+            p.copy_(_bf16(z[f"param.{n}_bf16"]))
+    want_adm = _bf16(z["admission_bf16"])
+    # The product's glue: means from the stats op (CPU oracle kernel), rounded to the tape
+    # dtype, then the module's expressions.
+    from dabsn_amd.read import _tape_means
+
+    _, _, ay, w, nov, pl, en, sat = tapes
+    stats = torch.ops.dabsn.read_tape_stats(nov, pl, en, sat, ay, w)
+    me, mc, mn, mp = _tape_means(stats, en, sat, nov, pl)
+    adm = read.short_read.admission_from_means(me, mc, mn, mp, H)
+    assert adm.dtype == torch.bfloat16
+    assert torch.equal(adm, want_adm)
+    window = F.softplus(read.admit_window)
+    order, counts, _ = torch.ops.dabsn.bank_select(adm, window)
+    assert np.array_equal(order.numpy(), z["order"])
+    assert max(int(counts.max()), 1) == int(z["n_max"])
+    # Teeth: fp32 means and an fp32 floor select differently here.
+    m32 = stats.unbind(-1)[:4]
+    adm32 = read.short_read.float().admission_from_means(*m32, H)
+    o32, _ = oracle.bank_select(np32(adm32), float(F.softplus(read.admit_window.float())))
+    assert not np.array_equal(o32, z["order"])
+
+
+def test_query_bank_vs_reference_fixture():
+    z = _load("query_bank_fp32")
+    H = z["y"].shape[-1]
+    start = int(z["query_start"])
+    read = _read_module(z, H)
+    tapes = _tapes(z)
+    y, budget, ay, w, nov, pl, en, sat = tapes
+    long0 = tuple(torch.from_numpy(z[f"long0_{i}"]) for i in range(3))
+    with torch.no_grad():
+        out, state = read.forward_query_bank(
+            *(t[:, start:] for t in tapes), bank_write=w, bank_novelty=nov, bank_p=pl,
+            bank_energy=en, bank_saturation=sat, query_start=start, initial_long_state=long0,
+            return_long_state=True)
+    assert read.last_n_max == int(z["n_max"])
+    assert rel_err(out, z["out"]) <= 1e-5
+    for i, s in enumerate(state):
+        assert rel_err(s, z[f"long1_{i}"]) <= 1e-5
+
+
+def _c1_block(z, k):
+    spec = [(24, 128, 96), (128, 192, 128)][k]
+    blk = dabsn_amd.DABSNBlock(*spec, "seq", residual=True, mlp_ratio=4.0)
+    prefix = f"b{k}.param."
+    with torch.no_grad():
+        for n, p in blk.named_parameters():
+            key = f"{prefix}{n}_bf16"
+            if key in z:
+                p.copy_(_bf16(z[key]).float())
+    return blk
+
+
+def c1_block_check(z, k, device, tol=1e-5):
+    """Block k of the config-1 fixture on ``device``: world-view output, gradient passed back
+    to the block input, and the DABSN-path parameter gradients."""
+    blk = _c1_block(z, k).to(device)
+    x = torch.from_numpy(z[f"b{k}.in"]).to(device).requires_grad_(True)
+    out = blk.forward_world(x)
+    assert blk.read.last_n_max == int(z[f"b{k}.n_max"])
+    assert rel_err(out.detach().cpu(), z[f"b{k}.out"]) <= tol
+    (out * torch.from_numpy(z[f"b{k}.gout"]).to(device)).sum().backward()
+    want_gx = z["grad.x"] if k == 0 else z["b1.grad_in"]
+    assert rel_err(x.grad.cpu(), want_gx) <= tol
+    scale = max(float(np.abs(z[key]).max()) for key in z if key.startswith(f"b{k}.grad."))
+    for n, p in blk.named_parameters():
+        key = f"b{k}.grad.{n}"
+        if key not in z:
+            continue
+        err = grad_err(p.grad, z[key], scale)
+        assert err <= tol, f"{n}: {err:.3e}"
+
+
+@pytest.mark.parametrize("k", [0, 1])
+def test_config1_blocks_vs_reference_fixture(k):
+    c1_block_check(_load("model_c1"), k, "cpu")
+
+
+def memory_lm_check(device):
+    z = _load("memory_lm")
+    model = dabsn_amd.DABSNSequenceLM(40, 24, 2, layers="seq:24:24,seq:32:16", residual=True,
+                                      mlp_ratio=2.0)
+    state = {k[len("param."):]: torch.from_numpy(v) for k, v in z.items() if k.startswith("param.")}
+    model.load_state_dict(state, strict=True)
+    model = model.to(device).eval()
+    memory = mem.load(GOLDEN / "memory_lm.dmem", model=model)
+    assert memory.position == int(z["position"])
+    assert memory.fingerprint == mem.fingerprint_of(model)
+    logits, _ = mem.forward_with_memory(model, torch.from_numpy(z["next"]).to(device), memory)
+    return logits.cpu(), z["logits"]
+
+
+def test_reference_written_memory_file_continues_exactly():
+    got, want = memory_lm_check("cpu")
+    assert rel_err(got, want) <= 1e-5
+
+
+def test_fingerprint_is_the_references():
+    """A file written here carries the reference's fingerprint dictionary key for key, so
+    the reference's _check_fingerprint (memory.py:164-181) accepts it."""
+    torch.serialization.add_safe_globals([])
+    payload = torch.load(GOLDEN / "memory_lm.dmem", map_location="cpu", weights_only=True)
+    model = dabsn_amd.DABSNSequenceLM(40, 24, 2, layers="seq:24:24,seq:32:16", residual=True,
+                                      mlp_ratio=2.0)
+    assert mem.fingerprint_of(model) == payload["fingerprint"]
