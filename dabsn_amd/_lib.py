@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib = None
@@ -98,10 +98,16 @@ _SIGNATURES = {
     "dabsn_hip_bank_gather": ([i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_gather_bwd": (
         [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_core_scan_launches": ([i32, i64, i64, i64, i32, vp], i32),
     "dabsn_hip_read3_workspace_bytes": ([i32, i64, i64, i64, i64, i32], sz),
     "dabsn_hip_read3_fwd": (
         [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4, vp, vp,
          sz, vp],
+        i32,
+    ),
+    "dabsn_hip_read3_fwd_keep": (
+        [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4, vp, vp,
+         sz, vp, sz, vp],
         i32,
     ),
     "dabsn_hip_read3_decode_workspace_bytes": ([i32, i64, i64, i64, i64], sz),
@@ -127,7 +133,7 @@ _SIGNATURES = {
     ),
     "dabsn_hip_read3_bwd_after_fwd": (
         [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4]
-        + [vp] * 4 + [vp] * 5 + [vp, sz, vp],
+        + [vp] * 4 + [vp] * 5 + [vp, sz, vp, sz, vp],
         i32,
     ),
 }

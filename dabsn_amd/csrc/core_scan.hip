@@ -1323,6 +1323,19 @@ static int launch_slabs(K kernel, int threads, const Cfg& c, const A& args, hipS
   return DABSN_OK;
 }
 
+// Number of cooperative launches launch_slabs makes for this configuration on the
+// current device (1 when every batch group fits one launch).
+template <typename K>
+static int slab_count(K kernel, int threads, const Cfg& c, int64_t* launches) {
+  int dev = 0, cus = 0, per_cu = 0;
+  DABSN_HIP_CHECK(hipGetDevice(&dev));
+  DABSN_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  DABSN_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0));
+  const int per_launch = per_cu * cus / c.nct;
+  *launches = (per_launch < 1 || c.nbg <= per_launch) ? 1 : (c.nbg + per_launch - 1) / per_launch;
+  return DABSN_OK;
+}
+
 // (CH, KSTEPS, NW) combinations compiled per dtype.
 #define DABSN_CORE_CASES_BF16(X) \
   X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(16, 8, 4) X(16, 8, 8)
@@ -1580,6 +1593,39 @@ int dabsn_hip_core_scan_layout(int dtype, int64_t B, int64_t H, int64_t* nbg, in
   if (nbg) *nbg = c.nbg;
   if (nwg) *nwg = static_cast<int64_t>(c.nbg) * c.nct;
   return DABSN_OK;
+}
+
+int dabsn_hip_core_scan_launches(int dtype, int64_t B, int64_t T, int64_t H, int backward,
+                                 int64_t* launches) {
+  DABSN_REQUIRE(launches, "core scan launches: null pointer");
+  DABSN_REQUIRE(dtype == kF32 || dtype == kBF16, "core scan launches: bad dtype");
+  const Cfg c = pick(dtype, B, H);
+  if (c.ksteps == 0) {
+    dabsn::set_error("core scan: unsupported H=%lld", (long long)H);
+    return DABSN_ERR_UNSUPPORTED;
+  }
+  if (T <= 0 || (T == 1 && !backward)) {
+    *launches = 0;  // nothing to scan, or the one-step path (no cooperative launch)
+    return DABSN_OK;
+  }
+#define DABSN_CASE(CHV, KS, NWV)                                                      \
+  if (c.ch == CHV && c.ksteps == KS && c.nw == NWV) {                                 \
+    if (dtype == kBF16)                                                               \
+      return backward ? slab_count(core_bwd_kernel<bf16, CHV, KS, NWV>, NWV * 64, c, launches) \
+                      : slab_count(core_fwd_kernel<bf16, CHV, KS, NWV>, NWV * 64, c, launches); \
+  }
+  DABSN_CORE_CASES_BF16(DABSN_CASE)
+#undef DABSN_CASE
+#define DABSN_CASE(CHV, KS, NWV)                                                      \
+  if (c.ch == CHV && c.ksteps == KS && c.nw == NWV) {                                 \
+    if (dtype == kF32)                                                                \
+      return backward ? slab_count(core_bwd_kernel<float, CHV, KS, NWV>, NWV * 64, c, launches) \
+                      : slab_count(core_fwd_kernel<float, CHV, KS, NWV>, NWV * 64, c, launches); \
+  }
+  DABSN_CORE_CASES_F32(DABSN_CASE)
+#undef DABSN_CASE
+  dabsn::set_error("core scan: no kernel for CH=%d KSTEPS=%d NW=%d", c.ch, c.ksteps, c.nw);
+  return DABSN_ERR_UNSUPPORTED;
 }
 
 int dabsn_hip_core_scan_config(int dtype, int64_t B, int64_t H, int* ch, int* ksteps, int* waves) {

@@ -514,20 +514,39 @@ static Plan plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
   return p;
 }
 
+// A workspace in two parts. `kept` holds the plan's regions below off_PV -- the scores,
+// the tile ranges and the row statistics, which a forward leaves for a later backward and
+// which that backward only reads; `scratch` holds every region from off_PV on. A single
+// buffer is the case scratch = kept + off_PV.
+struct Ws {
+  uint8_t* kept;
+  uint8_t* scratch;
+  size_t split;
+  template <typename X>
+  X* at(size_t off) const {
+    return reinterpret_cast<X*>(off < split ? kept + off : scratch + (off - split));
+  }
+};
+
+static Ws single_ws(void* ws, const Plan& p) {
+  uint8_t* b = static_cast<uint8_t*>(ws);
+  return Ws{b, b + p.off_PV, p.off_PV};
+}
+
 template <typename E>
 static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, const E* K,
                         const E* V, const E* Vn, const float* ck, const float* cb, const float* kb,
                         const float* adm, const float* scale, const int64_t* idx,
-                        const uint8_t* valid, int mode, Gains g, E* out, uint8_t* ws,
+                        const uint8_t* valid, int mode, Gains g, E* out, const Ws& ws,
                         const Plan& p, bool write_p, hipStream_t stream) {
   const int QT = static_cast<int>((T + TILE - 1) / TILE), BT = static_cast<int>((N + TILE - 1) / TILE);
-  float* S = reinterpret_cast<float*>(ws + p.off_S);
-  int32_t* rs = reinterpret_cast<int32_t*>(ws + p.off_rs);
-  int32_t* ro = reinterpret_cast<int32_t*>(ws + p.off_ro);
-  int32_t* rb = reinterpret_cast<int32_t*>(ws + p.off_rb);
-  float* stats = reinterpret_cast<float*>(ws + p.off_stats);
-  E* PV = reinterpret_cast<E*>(ws + p.off_PV);
-  E* PVn = reinterpret_cast<E*>(ws + p.off_PVn);
+  float* S = ws.at<float>(p.off_S);
+  int32_t* rs = ws.at<int32_t>(p.off_rs);
+  int32_t* ro = ws.at<int32_t>(p.off_ro);
+  int32_t* rb = ws.at<int32_t>(p.off_rb);
+  float* stats = ws.at<float>(p.off_stats);
+  E* PV = ws.at<E>(p.off_PV);
+  E* PVn = ws.at<E>(p.off_PVn);
   hipLaunchKernelGGL(ranges_kernel, dim3((unsigned)(QT + BT), (unsigned)B), dim3(256), 0, stream,
                      (int)T, (int)N, (int)H, mode, idx, valid, rs, ro, rb);
   DABSN_HIP_CHECK(hipGetLastError());
@@ -549,8 +568,8 @@ static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, 
   DABSN_HIP_CHECK(hipGetLastError());
   if (!write_p) return DABSN_OK;
   {
-    E* VT = reinterpret_cast<E*>(ws + p.off_VT);
-    E* VnT = reinterpret_cast<E*>(ws + p.off_VnT);
+    E* VT = ws.at<E>(p.off_VT);
+    E* VnT = ws.at<E>(p.off_VnT);
     DABSN_HIP_CHECK(xpose::transpose<E>(V, VT, (int)B, (int)N, (int)H, stream));
     DABSN_HIP_CHECK(xpose::transpose<E>(Vn, VnT, (int)B, (int)N, (int)H, stream));
     gemm::Args<E, E> a{};  // out = P_V V + P_Vn Vn, B operands as V^T [H][N]
@@ -572,7 +591,7 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
                          const float* kb, const float* adm, const float* scale, const int64_t* idx,
                          const uint8_t* valid, int mode, Gains g, E* gq, E* gK, E* gV, E* gVn,
                          float* gck, float* gcb, float* gkb, float* gadm, float* gscal5,
-                         uint8_t* ws, const Plan& p, bool recompute, hipStream_t stream) {
+                         const Ws& ws, const Plan& p, bool recompute, hipStream_t stream) {
   // The tile ranges, S and the row statistics: recomputed here, or left in the workspace
   // by the forward call on the same inputs (which also wrote P_V / P_Vn, rebuilt below).
   if (recompute) {
@@ -581,20 +600,20 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
     if (rc != DABSN_OK) return rc;
   }
   const int QT = static_cast<int>((T + TILE - 1) / TILE), BT = static_cast<int>((N + TILE - 1) / TILE);
-  const float* S = reinterpret_cast<const float*>(ws + p.off_S);
-  const int32_t* rs = reinterpret_cast<const int32_t*>(ws + p.off_rs);
-  const int32_t* ro = reinterpret_cast<const int32_t*>(ws + p.off_ro);
-  const int32_t* rb = reinterpret_cast<const int32_t*>(ws + p.off_rb);
-  const float* stats = reinterpret_cast<const float*>(ws + p.off_stats);
-  E* PV = reinterpret_cast<E*>(ws + p.off_PV);
-  E* PVn = reinterpret_cast<E*>(ws + p.off_PVn);
-  float* dPV = reinterpret_cast<float*>(ws + p.off_dPV);
-  float* dPVn = reinterpret_cast<float*>(ws + p.off_dPVn);
-  E* Gs = reinterpret_cast<E*>(ws + p.off_Gs);
-  float* rowA = reinterpret_cast<float*>(ws + p.off_rowA);
-  float* rowB = reinterpret_cast<float*>(ws + p.off_rowB);
-  float* colp = reinterpret_cast<float*>(ws + p.off_colp);
-  float* part = reinterpret_cast<float*>(ws + p.off_part);
+  const float* S = ws.at<const float>(p.off_S);
+  const int32_t* rs = ws.at<const int32_t>(p.off_rs);
+  const int32_t* ro = ws.at<const int32_t>(p.off_ro);
+  const int32_t* rb = ws.at<const int32_t>(p.off_rb);
+  const float* stats = ws.at<const float>(p.off_stats);
+  E* PV = ws.at<E>(p.off_PV);
+  E* PVn = ws.at<E>(p.off_PVn);
+  float* dPV = ws.at<float>(p.off_dPV);
+  float* dPVn = ws.at<float>(p.off_dPVn);
+  E* Gs = ws.at<E>(p.off_Gs);
+  float* rowA = ws.at<float>(p.off_rowA);
+  float* rowB = ws.at<float>(p.off_rowB);
+  float* colp = ws.at<float>(p.off_colp);
+  float* part = ws.at<float>(p.off_part);
   for (int w = 0; w < 2; ++w) {
     gemm::Args<E, float> a{};
     a.M = (int)T; a.N = (int)N; a.K = (int)H;
@@ -615,12 +634,12 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
                        g, scale, rs, stats, rowA, dPV, dPVn, Gs, PV, PVn, rowB, colp);
     DABSN_HIP_CHECK(hipGetLastError());
   }
-  E* KT = reinterpret_cast<E*>(ws + p.off_KT);
-  E* QTr = reinterpret_cast<E*>(ws + p.off_QT);
-  E* gOT = reinterpret_cast<E*>(ws + p.off_gOT);
-  E* GsT = reinterpret_cast<E*>(ws + p.off_GsT);
-  E* PVT = reinterpret_cast<E*>(ws + p.off_PVT);
-  E* PVnT = reinterpret_cast<E*>(ws + p.off_PVnT);
+  E* KT = ws.at<E>(p.off_KT);
+  E* QTr = ws.at<E>(p.off_QT);
+  E* gOT = ws.at<E>(p.off_gOT);
+  E* GsT = ws.at<E>(p.off_GsT);
+  E* PVT = ws.at<E>(p.off_PVT);
+  E* PVnT = ws.at<E>(p.off_PVnT);
   DABSN_HIP_CHECK(xpose::transpose<E>(K, KT, (int)B, (int)N, (int)H, stream));
   DABSN_HIP_CHECK(xpose::transpose<E>(q, QTr, (int)B, (int)T, (int)H, stream));
   DABSN_HIP_CHECK(xpose::transpose<E>(gout, gOT, (int)B, (int)T, (int)H, stream));
@@ -1369,9 +1388,52 @@ static int read3_checks(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, i
 extern "C" {
 
 size_t dabsn_hip_read3_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
-                                       int backward) {
+                                       int part) {
   const Plan p = plan(dtype, B, T, N, H);
-  return backward ? p.end_bwd : p.end_fwd;
+  switch (part) {
+    case 0: return p.end_fwd;
+    case 1: return p.end_bwd;
+    case 2: return p.off_PV;
+    case 3: return p.end_fwd - p.off_PV;
+    case 4: return p.end_bwd - p.off_PV;
+    default: return 0;
+  }
+}
+
+static int read3_fwd_entry(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* q,
+                           const void* K, const void* V, const void* Vn, const float* cocktail,
+                           const float* bank_cocktail, const float* key_bias,
+                           const float* admission, const float* scale, const int64_t* idx,
+                           const uint8_t* valid, int mode, const float* const* gains, void* out,
+                           void* kept, size_t kept_bytes, void* scratch, size_t scratch_bytes,
+                           bool single, hipStream_t stream) {
+  const int rc = read3_checks(dtype, B, T, N, H, mode);
+  if (rc != DABSN_OK) return rc;
+  DABSN_REQUIRE(q && out && cocktail && scale && gains, "read3: null pointer");
+  for (int i = 0; i < 4; ++i) DABSN_REQUIRE(gains[i], "read3: null gain %d", i);
+  if (N == 0) return dabsn_hip_zero(out, static_cast<size_t>(B * T * H) * (dtype == kBF16 ? 2 : 4), stream);
+  DABSN_REQUIRE(K && V && Vn && bank_cocktail && key_bias && admission && idx && valid && kept &&
+                    (single || scratch),
+                "read3: null bank or workspace pointer");
+  const Plan p = plan(dtype, B, T, N, H);
+  Ws w;
+  if (single) {
+    DABSN_REQUIRE(kept_bytes >= p.end_fwd, "read3: workspace %zu < %zu", kept_bytes, p.end_fwd);
+    w = single_ws(kept, p);
+  } else {
+    DABSN_REQUIRE(kept_bytes >= p.off_PV && scratch_bytes >= p.end_fwd - p.off_PV,
+                  "read3: kept %zu < %zu or scratch %zu < %zu", kept_bytes, p.off_PV,
+                  scratch_bytes, p.end_fwd - p.off_PV);
+    w = Ws{static_cast<uint8_t*>(kept), static_cast<uint8_t*>(scratch), p.off_PV};
+  }
+  Gains g{{gains[0], gains[1], gains[2], gains[3]}};
+  if (dtype == kBF16)
+    return forward_impl<bf16>(B, T, N, H, (const bf16*)q, (const bf16*)K, (const bf16*)V,
+                              (const bf16*)Vn, cocktail, bank_cocktail, key_bias, admission, scale,
+                              idx, valid, mode, g, (bf16*)out, w, p, true, stream);
+  return forward_impl<float>(B, T, N, H, (const float*)q, (const float*)K, (const float*)V,
+                             (const float*)Vn, cocktail, bank_cocktail, key_bias, admission, scale,
+                             idx, valid, mode, g, (float*)out, w, p, true, stream);
 }
 
 int dabsn_hip_read3_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* q,
@@ -1380,28 +1442,26 @@ int dabsn_hip_read3_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
                         const float* scale, const int64_t* idx, const uint8_t* valid, int mode,
                         const float* const* gains, void* out, void* workspace,
                         size_t workspace_bytes, hipStream_t stream) {
-  const int rc = read3_checks(dtype, B, T, N, H, mode);
-  if (rc != DABSN_OK) return rc;
-  DABSN_REQUIRE(q && out && cocktail && scale && gains, "read3: null pointer");
-  for (int i = 0; i < 4; ++i) DABSN_REQUIRE(gains[i], "read3: null gain %d", i);
-  if (N == 0) return dabsn_hip_zero(out, static_cast<size_t>(B * T * H) * (dtype == kBF16 ? 2 : 4), stream);
-  DABSN_REQUIRE(K && V && Vn && bank_cocktail && key_bias && admission && idx && valid && workspace,
-                "read3: null bank pointer");
-  const Plan p = plan(dtype, B, T, N, H);
-  DABSN_REQUIRE(workspace_bytes >= p.end_fwd, "read3: workspace %zu < %zu", workspace_bytes,
-                p.end_fwd);
-  Gains g{{gains[0], gains[1], gains[2], gains[3]}};
-  if (dtype == kBF16)
-    return forward_impl<bf16>(B, T, N, H, (const bf16*)q, (const bf16*)K, (const bf16*)V,
-                              (const bf16*)Vn, cocktail, bank_cocktail, key_bias, admission, scale,
-                              idx, valid, mode, g, (bf16*)out, (uint8_t*)workspace, p, true, stream);
-  return forward_impl<float>(B, T, N, H, (const float*)q, (const float*)K, (const float*)V,
-                             (const float*)Vn, cocktail, bank_cocktail, key_bias, admission, scale,
-                             idx, valid, mode, g, (float*)out, (uint8_t*)workspace, p, true, stream);
+  return read3_fwd_entry(dtype, B, T, N, H, q, K, V, Vn, cocktail, bank_cocktail, key_bias,
+                         admission, scale, idx, valid, mode, gains, out, workspace,
+                         workspace_bytes, nullptr, 0, true, stream);
 }
 
-// The backward entry points: with recompute, from the inputs alone; without, on the
-// workspace a forward call with the same inputs filled.
+int dabsn_hip_read3_fwd_keep(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
+                             const void* q, const void* K, const void* V, const void* Vn,
+                             const float* cocktail, const float* bank_cocktail,
+                             const float* key_bias, const float* admission, const float* scale,
+                             const int64_t* idx, const uint8_t* valid, int mode,
+                             const float* const* gains, void* out, void* kept, size_t kept_bytes,
+                             void* scratch, size_t scratch_bytes, hipStream_t stream) {
+  return read3_fwd_entry(dtype, B, T, N, H, q, K, V, Vn, cocktail, bank_cocktail, key_bias,
+                         admission, scale, idx, valid, mode, gains, out, kept, kept_bytes,
+                         scratch, scratch_bytes, false, stream);
+}
+
+// The backward entry points: with recompute, from the inputs alone (one workspace); without,
+// on the kept part a forward call with the same inputs filled, which is only read, plus a
+// scratch buffer.
 static int read3_bwd_entry(bool recompute, int dtype, int64_t B, int64_t T, int64_t N,
                            int64_t H, const void* gout, const void* q, const void* K,
                            const void* V, const void* Vn, const float* cocktail,
@@ -1410,8 +1470,8 @@ static int read3_bwd_entry(bool recompute, int dtype, int64_t B, int64_t T, int6
                            const uint8_t* valid, int mode, const float* const* gains, void* gq,
                            void* gK, void* gV, void* gVn, float* gcocktail,
                            float* gbank_cocktail, float* gkey_bias, float* gadmission,
-                           float* gscalars5, void* workspace, size_t workspace_bytes,
-                           hipStream_t stream) {
+                           float* gscalars5, void* kept, size_t kept_bytes, void* scratch,
+                           size_t scratch_bytes, hipStream_t stream) {
   const int rc = read3_checks(dtype, B, T, N, H, mode);
   if (rc != DABSN_OK) return rc;
   DABSN_REQUIRE(gout && q && gq && cocktail && gcocktail && scale && gains && gscalars5,
@@ -1425,23 +1485,33 @@ static int read3_bwd_entry(bool recompute, int dtype, int64_t B, int64_t T, int6
     return z;
   }
   DABSN_REQUIRE(K && V && Vn && bank_cocktail && key_bias && admission && idx && valid && gK && gV &&
-                    gVn && gbank_cocktail && gkey_bias && gadmission && workspace,
-                "read3 backward: null bank pointer");
+                    gVn && gbank_cocktail && gkey_bias && gadmission && kept &&
+                    (recompute || scratch),
+                "read3 backward: null bank or workspace pointer");
   const Plan p = plan(dtype, B, T, N, H);
-  DABSN_REQUIRE(workspace_bytes >= p.end_bwd, "read3 backward: workspace %zu < %zu",
-                workspace_bytes, p.end_bwd);
+  Ws w;
+  if (recompute) {
+    DABSN_REQUIRE(kept_bytes >= p.end_bwd, "read3 backward: workspace %zu < %zu", kept_bytes,
+                  p.end_bwd);
+    w = single_ws(kept, p);
+  } else {
+    DABSN_REQUIRE(kept_bytes >= p.off_PV && scratch_bytes >= p.end_bwd - p.off_PV,
+                  "read3 backward: kept %zu < %zu or scratch %zu < %zu", kept_bytes, p.off_PV,
+                  scratch_bytes, p.end_bwd - p.off_PV);
+    w = Ws{static_cast<uint8_t*>(kept), static_cast<uint8_t*>(scratch), p.off_PV};
+  }
   Gains g{{gains[0], gains[1], gains[2], gains[3]}};
   if (dtype == kBF16)
     return backward_impl<bf16>(B, T, N, H, (const bf16*)gout, (const bf16*)q, (const bf16*)K,
                                (const bf16*)V, (const bf16*)Vn, cocktail, bank_cocktail, key_bias,
                                admission, scale, idx, valid, mode, g, (bf16*)gq, (bf16*)gK,
                                (bf16*)gV, (bf16*)gVn, gcocktail, gbank_cocktail, gkey_bias,
-                               gadmission, gscalars5, (uint8_t*)workspace, p, recompute, stream);
+                               gadmission, gscalars5, w, p, recompute, stream);
   return backward_impl<float>(B, T, N, H, (const float*)gout, (const float*)q, (const float*)K,
                               (const float*)V, (const float*)Vn, cocktail, bank_cocktail, key_bias,
                               admission, scale, idx, valid, mode, g, (float*)gq, (float*)gK,
                               (float*)gV, (float*)gVn, gcocktail, gbank_cocktail, gkey_bias,
-                              gadmission, gscalars5, (uint8_t*)workspace, p, recompute, stream);
+                              gadmission, gscalars5, w, p, recompute, stream);
 }
 
 int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* gout,
@@ -1455,7 +1525,7 @@ int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
   return read3_bwd_entry(true, dtype, B, T, N, H, gout, q, K, V, Vn, cocktail, bank_cocktail,
                          key_bias, admission, scale, idx, valid, mode, gains, gq, gK, gV, gVn,
                          gcocktail, gbank_cocktail, gkey_bias, gadmission, gscalars5, workspace,
-                         workspace_bytes, stream);
+                         workspace_bytes, nullptr, 0, stream);
 }
 
 int dabsn_hip_read3_bwd_after_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
@@ -1467,11 +1537,12 @@ int dabsn_hip_read3_bwd_after_fwd(int dtype, int64_t B, int64_t T, int64_t N, in
                                   const float* const* gains, void* gq, void* gK, void* gV,
                                   void* gVn, float* gcocktail, float* gbank_cocktail,
                                   float* gkey_bias, float* gadmission, float* gscalars5,
-                                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                                  const void* kept, size_t kept_bytes, void* scratch,
+                                  size_t scratch_bytes, hipStream_t stream) {
   return read3_bwd_entry(false, dtype, B, T, N, H, gout, q, K, V, Vn, cocktail, bank_cocktail,
                          key_bias, admission, scale, idx, valid, mode, gains, gq, gK, gV, gVn,
-                         gcocktail, gbank_cocktail, gkey_bias, gadmission, gscalars5, workspace,
-                         workspace_bytes, stream);
+                         gcocktail, gbank_cocktail, gkey_bias, gadmission, gscalars5,
+                         const_cast<void*>(kept), kept_bytes, scratch, scratch_bytes, stream);
 }
 
 

@@ -25,7 +25,7 @@ from typing import Optional, Sequence
 import torch
 from torch import Tensor
 
-from .. import _lib
+from .. import _lib, events
 from . import ops
 
 
@@ -110,6 +110,16 @@ def _launch_pair(fwd: _Fwd, bwd: _Bwd, stream) -> None:
     lib = _lib.load()
     rc = lib.dabsn_hip_core_scan_pair(ctypes.byref(fwd.call), ctypes.byref(bwd.call), stream)
     if rc == -3:  # DABSN_ERR_UNSUPPORTED: nothing was enqueued
+        c = fwd.call
+        events.report_fallback(
+            "core_scan_chunked",
+            "the recompute and reverse-scan grids do not fit the device together",
+            requested_path="recompute of chunk k-1 beside the reverse scan of chunk k, one "
+                           "cooperative launch",
+            selected_path="the recompute, then the reverse scan, as separate launches",
+            corrective_action="call with fewer batch rows per device so that both grids are "
+                              "resident at once (each takes its own CUs)",
+            B=int(c.B), H=int(c.H), dtype="bf16" if c.dtype == 1 else "fp32")
         fwd.launch(stream)
         bwd.launch(stream)
     else:
@@ -131,6 +141,9 @@ class _ChunkedCoreScan(torch.autograd.Function):
         dt = Wx.dtype
         code = ops._code(dt)
         stream = ops._stream(Wx)
+        events.announce("core_scan_chunked", "rocm_checkpointed_pair_pipeline", B=B, H=H,
+                        chunk=int(chunk), dtype="bf16" if code == 1 else "fp32")
+        ops.core_launch_check(code, B, min(T, chunk), H, False)
         GA = torch.cat((Ug, A), dim=0).to(dt).contiguous()
         params, keep = ops._core_params(vecs, scal)
         carry = [x.float().contiguous() for x in (b0, e0, c0)]
@@ -168,6 +181,7 @@ class _ChunkedCoreScan(torch.autograd.Function):
         params, keep = ops._core_params(vecs, scal)
         bounds = _chunks(T, ctx.chunk)
         K = len(bounds)
+        ops.core_launch_check(code, B, min(T, ctx.chunk), H, True)
         up = [None if g is None else g.to(dt).contiguous() for g in grads[:7]]
         carry = [None if g is None else g.float().contiguous() for g in grads[8:11]]
         gWx, gWgx, day = (_empty((B, T, H), Wx) for _ in range(3))

@@ -31,7 +31,7 @@ from typing import Callable, Optional, Sequence
 import torch
 from torch import Tensor
 
-from .. import _lib
+from .. import _lib, events
 
 _DTYPES = {torch.float32: 0, torch.bfloat16: 1}
 
@@ -237,6 +237,38 @@ def _core_params(vecs: Sequence[Tensor], scal: Sequence[Tensor]):
     return _derived("core_params", (*vecs, *scal), build)
 
 
+# Cooperative launches per scan, by (device, dtype code, B, H, backward, one-step forward).
+_LAUNCHES: dict[tuple, int] = {}
+
+
+def core_launch_check(code: int, B: int, T: int, H: int, backward: bool) -> int:
+    """Announce the core scan's path and report the batch-slab fallback: a batch whose
+    groups of 16 rows do not all fit one cooperative launch runs as consecutive launches
+    over slabs of the batch (each slab re-walks every time step). Returns the number of
+    launches one scan makes."""
+    key = (torch.cuda.current_device(), code, B, H, bool(backward), T == 1 and not backward)
+    n = _LAUNCHES.get(key)
+    if n is None:
+        out = ctypes.c_int64(0)
+        _lib.check(_lib.load().dabsn_hip_core_scan_launches(code, B, T, H, int(backward),
+                                                            ctypes.byref(out)),
+                   "core scan launch count")
+        n = _LAUNCHES[key] = int(out.value)
+    dtype = "bf16" if code == 1 else "fp32"
+    path = ("rocm_one_step_gemm" if key[-1] else
+            "rocm_cooperative_reverse_scan" if backward else "rocm_cooperative_scan")
+    events.announce("core_scan", path, B=B, H=H, dtype=dtype)
+    if n > 1:
+        events.report_fallback(
+            "core_scan", "the batch's row groups do not all fit one cooperative launch",
+            requested_path="one cooperative launch per scan",
+            selected_path=f"{n} consecutive cooperative launches over batch slabs",
+            corrective_action="call with fewer batch rows per device (the rows are "
+                              "independent, so the batch can be split across calls or GPUs)",
+            B=B, H=H, dtype=dtype, backward=bool(backward))
+    return n
+
+
 @torch.library.custom_op("dabsn::core_scan_batched", mutates_args=(), device_types="cuda")
 def core_scan_batched(
     Wx: Tensor, Wgx: Tensor, Ug: Tensor, A: Tensor, beta: Tensor, log_kappa: Tensor,
@@ -273,6 +305,7 @@ def core_scan_batched(
     nbytes = lib.dabsn_hip_core_scan_workspace_bytes(code, B, H, 0)
     if nbytes == 0:
         raise RuntimeError(f"DABSN HIP core scan does not support H={H} for {dt}")
+    core_launch_check(code, B, T, H, False)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=Wx.device)
     tk = KernelTimer.begin("core_scan_fwd", Wx)
     rc = lib.dabsn_hip_core_scan_fwd(
@@ -344,6 +377,7 @@ def core_scan_batched_backward(
     part_scal = torch.empty((nwg.value, 3), device=U.device, dtype=torch.float32)
     gb0, ge0, gc0 = (torch.empty((B, H), device=U.device, dtype=torch.float32) for _ in range(3))
     nbytes = lib.dabsn_hip_core_scan_workspace_bytes(code, B, H, 1)
+    core_launch_check(code, B, T, H, True)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=U.device)
     tk = KernelTimer.begin("core_scan_bwd", U)
     rc = lib.dabsn_hip_core_scan_bwd(
@@ -1236,8 +1270,9 @@ def read3_fwd_keep(
     bank_idx: Tensor, bank_valid: Tensor, mode: int, short_gain: Tensor, pad_gain: Tensor,
     induct_gain: Tensor, cocktail_gain: Tensor,
 ) -> tuple[Tensor, Tensor]:
-    """The three-way read forward; returns (out, workspace) with the workspace sized for the
-    backward and holding what ``read3_bwd_kept`` reuses."""
+    """The three-way read forward; returns (out, kept) where ``kept`` holds the scores, tile
+    ranges and row statistics that ``read3_bwd_kept`` reads (the forward's other scratch is
+    released when the call returns)."""
     _require_cuda(query)
     lib = _lib.load()
     if mode not in (0, 1):
@@ -1250,16 +1285,18 @@ def read3_fwd_keep(
     N = K.shape[1]
     code = _code(dt)
     out = torch.empty_like(q)
-    nbytes = lib.dabsn_hip_read3_workspace_bytes(code, B, T, N, H, 1)
-    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    kept = torch.empty(max(lib.dabsn_hip_read3_workspace_bytes(code, B, T, N, H, 2), 256),
+                       dtype=torch.uint8, device=q.device)
+    scratch = torch.empty(max(lib.dabsn_hip_read3_workspace_bytes(code, B, T, N, H, 3), 256),
+                          dtype=torch.uint8, device=q.device)
     ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
     tk = KernelTimer.begin("read3_fwd", q)
-    _lib.check(lib.dabsn_hip_read3_fwd(code, B, T, N, H, _p(q), _p(K), _p(V), _p(Vn), _p(ck),
-                                       _p(cb), _p(kb), _p(adm), _p(sc), _p(idx), _p(valid), mode,
-                                       ptrs, _p(out), _p(ws), ws.numel(), _stream(q)),
-               "three-way read")
+    _lib.check(lib.dabsn_hip_read3_fwd_keep(
+        code, B, T, N, H, _p(q), _p(K), _p(V), _p(Vn), _p(ck), _p(cb), _p(kb), _p(adm), _p(sc),
+        _p(idx), _p(valid), mode, ptrs, _p(out), _p(kept), kept.numel(), _p(scratch),
+        scratch.numel(), _stream(q)), "three-way read")
     KernelTimer.end(tk)
-    return out, ws
+    return out, kept
 
 
 @read3_fwd_keep.register_fake
@@ -1267,8 +1304,7 @@ def _read3_fwd_keep_fake(query, *rest):
     return torch.empty_like(query), query.new_empty((256,), dtype=torch.uint8)
 
 
-@torch.library.custom_op("dabsn::_read3_bwd_kept", mutates_args=("workspace",),
-                         device_types="cuda")
+@torch.library.custom_op("dabsn::_read3_bwd_kept", mutates_args=(), device_types="cuda")
 def read3_bwd_kept(
     grad_output: Tensor, query: Tensor, bank_keys: Tensor, bank_writes: Tensor,
     next_writes: Tensor, cocktail: Tensor, bank_cocktail: Tensor, bank_key_bias: Tensor,
@@ -1276,8 +1312,10 @@ def read3_bwd_kept(
     short_gain: Tensor, pad_gain: Tensor, induct_gain: Tensor, cocktail_gain: Tensor,
     workspace: Tensor,
 ) -> CompactGradients:
-    """``admitted_three_way_read_compact_flash_backward`` on the workspace of a
-    ``read3_fwd_keep`` call with the same inputs (``dabsn_hip_read3_bwd_after_fwd``)."""
+    """``admitted_three_way_read_compact_flash_backward`` on the kept buffer of a
+    ``read3_fwd_keep`` call with the same inputs (``dabsn_hip_read3_bwd_after_fwd``). The
+    kept buffer is only read, so a second backward through the same graph sees it
+    unchanged."""
     _require_cuda(query)
     lib = _lib.load()
     dt, q, K, V, Vn, ck, cb, kb, adm, sc, g, idx, valid = _read_common(
@@ -1294,13 +1332,15 @@ def read3_bwd_kept(
     gkb = torch.empty((B, N), device=q.device, dtype=torch.float32)
     gadm = torch.empty((B, N), device=q.device, dtype=torch.float32)
     g5 = torch.empty((5,), device=q.device, dtype=torch.float32)
+    scratch = torch.empty(max(lib.dabsn_hip_read3_workspace_bytes(_code(dt), B, T, N, H, 4), 256),
+                          dtype=torch.uint8, device=q.device)
     ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
     tk = KernelTimer.begin("read3_bwd", q)
     _lib.check(lib.dabsn_hip_read3_bwd_after_fwd(
         _code(dt), B, T, N, H, _p(go), _p(q), _p(K), _p(V), _p(Vn), _p(ck), _p(cb), _p(kb),
         _p(adm), _p(sc), _p(idx), _p(valid), mode, ptrs, _p(gq), _p(gK), _p(gV), _p(gVn),
         _p(gck), _p(gcb), _p(gkb), _p(gadm), _p(g5), _p(workspace), workspace.numel(),
-        _stream(q)), "three-way read backward")
+        _p(scratch), scratch.numel(), _stream(q)), "three-way read backward")
     KernelTimer.end(tk)
     return (gq, gK.to(bank_keys.dtype), gV.to(bank_writes.dtype), gVn.to(next_writes.dtype),
             gck.to(cocktail.dtype), gcb.to(bank_cocktail.dtype), gkb.to(bank_key_bias.dtype),

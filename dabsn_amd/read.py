@@ -18,6 +18,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch import Tensor
 
+from . import events
 from .kernels import ops
 
 
@@ -123,21 +124,59 @@ class DABSNRead(nn.Module):
         next_idx = (idx + 1).clamp(max=length - 1)
         return n_max, idx, valid, next_idx, rank
 
+    def _bank(self, cocktail_bank: Tensor, key_bias: Tensor, admission: Tensor, length: int,
+              query_start: int, width: int | None = None) -> dict[str, object]:
+        """Slot selection and the per-slot glue gathered for the read (read.py:185-256,
+        298-303): n_max, idx, valid, next_idx, rank, the bank's cocktail, key bias and
+        admission, the read scale and the slot positions relative to the query chunk."""
+        n_max, idx, valid, next_idx, rank = self._select(admission, length, width)
+        return {
+            "n_max": n_max, "idx": idx, "valid": valid, "next_idx": next_idx, "rank": rank,
+            "cocktail": torch.gather(cocktail_bank, 1, idx.unsqueeze(-1).expand(-1, -1, 4)),
+            "key_bias": torch.gather(key_bias, 1, idx),
+            "admission": torch.gather(admission, 1, idx),
+            "scale": (F.softplus(self.short_read.log_temp) + 1.0) * (self.hidden_dim ** 0.5),
+            "read_idx": idx if query_start == 0 else idx - query_start,
+        }
+
     def _read_core(self, query, cocktail, bank_write, norm_w, key_bias, admission, length: int,
                    query_start: int, width: int | None = None):
-        n_max, idx, valid, next_idx, rank = self._select(admission, length, width)
+        bank = self._bank(cocktail[1], key_bias, admission, length, query_start, width)
+        n_max, idx, valid, next_idx, rank = (bank[k] for k in ("n_max", "idx", "valid",
+                                                                "next_idx", "rank"))
         self.last_n_max = n_max
-        bank_cocktail = torch.gather(cocktail[1], 1, idx.unsqueeze(-1).expand(-1, -1, 4))
-        bank_bias = torch.gather(key_bias, 1, idx)
-        bank_adm = torch.gather(admission, 1, idx)
-        scale = (F.softplus(self.short_read.log_temp) + 1.0) * (self.hidden_dim ** 0.5)
-        read_idx = idx if query_start == 0 else idx - query_start
+        bank_cocktail, bank_bias, bank_adm = bank["cocktail"], bank["key_bias"], bank["admission"]
+        scale, read_idx = bank["scale"], bank["read_idx"]
         hidden = int(query.shape[-1])
+        rows = int(query.shape[1])
         # A few query rows without autograd (streaming decode): read the bank in place
         # instead of gathering K, V, Vn copies of the admitted slots.
-        decode = (not torch.is_grad_enabled() and query.is_cuda and int(query.shape[1]) <= 8
-                  and hidden % 8 == 0 and bank_write.stride(-1) == 1
+        streaming = not torch.is_grad_enabled() and query.is_cuda and rows <= 8
+        decode = (streaming and hidden % 8 == 0 and bank_write.stride(-1) == 1
                   and bank_write.stride(1) == hidden and bank_write.stride(0) % hidden == 0)
+        dtype = "bf16" if query.dtype == torch.bfloat16 else "fp32"
+        if streaming and not decode:
+            events.report_fallback(
+                "admitted_three_way_read",
+                "the bank cannot be read in place (H not a multiple of 8, or its rows are "
+                "not contiguous)",
+                requested_path="in-place streaming read of the bank",
+                selected_path="bank gather + three-way read",
+                corrective_action="use a state width that is a multiple of 8 and a bank "
+                                  "with contiguous rows",
+                H=hidden, dtype=dtype)
+        elif decode and (rows != 1 or hidden > 2048):
+            events.report_fallback(
+                "admitted_three_way_read",
+                "the one-pass streaming read takes one query row with H <= 2048",
+                requested_path="one-pass streaming read",
+                selected_path="three-pass streaming read (scores, softmax rows, products)",
+                corrective_action="decode one token per call, or use H <= 2048",
+                rows=rows, H=hidden, dtype=dtype)
+        if query.is_cuda:
+            events.announce("admitted_three_way_read",
+                            "rocm_decode_bank_in_place" if decode else "rocm_compact_admitted_bank",
+                            B=int(query.shape[0]), T=rows, H=hidden, dtype=dtype)
         if decode:
             retrieved = ops.read3_decode(
                 query, bank_write, norm_w, idx, next_idx, read_idx, valid, cocktail[0],
@@ -167,20 +206,27 @@ class DABSNRead(nn.Module):
         return self._unified_forward(y, budget, expression, write, novelty, plasticity, energy,
                                      saturation)
 
-    def _unified_forward(self, y, budget, expression, write, novelty, plasticity, energy,
-                         saturation) -> Tensor:
+    def _glue(self, expression, write, novelty, plasticity, energy, saturation):
+        """Per-position glue of the read (read.py:154-183): the tape statistics rows, the
+        normalised query, key bias, admission and cocktail."""
         rp = self.short_read
-        _, seq_len, hidden = expression.shape
+        hidden = int(expression.shape[-1])
         stats = ops.direct.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
         mean_e, mean_c, mean_n, mean_p = _tape_means(stats, energy, saturation, novelty, plasticity)
-        norm_ay = stats[..., 4].detach()
-        norm_w = stats[..., 5].detach()
-        query = ops.direct.normalize_rows(expression, norm_ay)
+        query = ops.direct.normalize_rows(expression, stats[..., 4].detach())
         key_bias = rp.key_bias_from_means(mean_n, mean_p, hidden)
         admission = rp.admission_from_means(mean_e, mean_c, mean_n, mean_p, hidden)
         cocktail = _cocktail(mean_e, mean_c, mean_n, mean_p)
-        retrieved = self._read_core(query, (cocktail, cocktail), write, norm_w, key_bias,
-                                    admission, seq_len, 0)
+        return stats, query, key_bias, admission, cocktail
+
+    def _unified_forward(self, y, budget, expression, write, novelty, plasticity, energy,
+                         saturation) -> Tensor:
+        rp = self.short_read
+        seq_len = int(expression.shape[1])
+        stats, query, key_bias, admission, cocktail = self._glue(
+            expression, write, novelty, plasticity, energy, saturation)
+        retrieved = self._read_core(query, (cocktail, cocktail), write, stats[..., 5].detach(),
+                                    key_bias, admission, seq_len, 0)
         output = rp.project(y, budget, retrieved.to(y.dtype))
         long = self._long_scan(write, plasticity, novelty)
         return torch.addcmul(output, self.long_gain, long)
@@ -202,6 +248,10 @@ class DABSNRead(nn.Module):
         else:
             if any(s.shape != (batch, hidden) for s in initial_state):
                 raise ValueError(f"initial long-scan state must have shape {(batch, hidden)}")
+        if write.is_cuda:
+            events.announce("recurrent_long_read", "rocm_chunk_parallel_scan", B=batch,
+                            T=int(write.shape[1]), H=hidden,
+                            dtype="bf16" if write.dtype == torch.bfloat16 else "fp32")
         long, lf, ef, rf, _ = ops.direct.long_scan_fused(
             write, plasticity, self.logit_expect_retain, self.logit_retention_decay,
             self.logit_retain, self.logit_retention_strength, *initial_state)

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 3
+#define DABSN_HIP_ABI_VERSION 5
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -56,6 +56,13 @@ size_t dabsn_hip_core_scan_workspace_bytes(int dtype, int64_t B, int64_t H, int 
 /* Number of batch groups and of workgroups: sizes of part_vec ([nbg][16][H]) and
  * part_scal ([nwg][3]) in the backward. */
 int dabsn_hip_core_scan_layout(int dtype, int64_t B, int64_t H, int64_t* nbg, int64_t* nwg);
+
+/* Number of cooperative launches a scan of (dtype, B, T, H) makes on the current device:
+ * 1 when every batch group is resident in one launch; more when the batch runs as
+ * consecutive launches over slabs of batch groups; 0 for T == 0 and for the forward of
+ * T == 1, which runs the one-step path without a cooperative launch. */
+int dabsn_hip_core_scan_launches(int dtype, int64_t B, int64_t T, int64_t H, int backward,
+                                 int64_t* launches);
 
 /* Launch configuration chosen for (dtype, B, H): channels per workgroup, MFMA k-steps per
  * wave and waves per workgroup (names the kernel instance in profiler output). */
@@ -231,9 +238,15 @@ int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_
  * keys), V, Vn [B,N,H] in `dtype`; cocktail [B,T,4], bank_cocktail [B,N,4], key_bias and
  * admission [B,N] in fp32; scale and gains[4] (short, pad, induct, cocktail) point at
  * fp32 scalars; idx [B,N] int64 and valid [B,N] uint8; mode 0 = seq (allow idx <= t,
- * induction idx < t), 1 = field (allow valid, induction idx < T-1). */
+ * induction idx < t), 1 = field (allow valid, induction idx < T-1).
+ *
+ * Workspace sizes by `part`: 0 = one buffer for dabsn_hip_read3_fwd, 1 = one buffer for
+ * dabsn_hip_read3_bwd (which recomputes the forward), 2 = the kept part (scores, tile
+ * ranges, row statistics) that dabsn_hip_read3_fwd_keep fills for
+ * dabsn_hip_read3_bwd_after_fwd, 3 = the forward scratch beside it, 4 = the backward
+ * scratch beside it. */
 size_t dabsn_hip_read3_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
-                                       int backward);
+                                       int part);
 int dabsn_hip_read3_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* q,
                         const void* K, const void* V, const void* Vn, const float* cocktail,
                         const float* bank_cocktail, const float* key_bias, const float* admission,
@@ -251,11 +264,22 @@ int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
                         void* gK, void* gV, void* gVn, float* gcocktail, float* gbank_cocktail,
                         float* gkey_bias, float* gadmission, float* gscalars5, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
-/* The same backward without recomputing the forward's scores and row statistics: the
- * workspace (at least dabsn_hip_read3_workspace_bytes(..., backward = 1) bytes) must be
- * the one a dabsn_hip_read3_fwd call on the same inputs used, untouched since. Saves the
- * score GEMM and softmax-row pass of the recompute at the cost of keeping the workspace
- * (B*T*N*4 bytes of scores and more) between forward and backward. */
+/* The forward for a caller that will run the backward on the same inputs: as
+ * dabsn_hip_read3_fwd, with the workspace in two buffers. `kept` (part 2 bytes) receives
+ * the scores, tile ranges and row statistics; `scratch` (part 3 bytes) is free once the
+ * call's work has completed. */
+int dabsn_hip_read3_fwd_keep(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
+                             const void* q, const void* K, const void* V, const void* Vn,
+                             const float* cocktail, const float* bank_cocktail,
+                             const float* key_bias, const float* admission, const float* scale,
+                             const int64_t* idx, const uint8_t* valid, int mode,
+                             const float* const* gains, void* out, void* kept, size_t kept_bytes,
+                             void* scratch, size_t scratch_bytes, hipStream_t stream);
+/* The backward without recomputing the forward's scores and row statistics: `kept` is the
+ * buffer a dabsn_hip_read3_fwd_keep call on the same inputs filled; it is only read, so
+ * the backward can run again on it. `scratch` holds part 4 bytes. Saves the score GEMM
+ * and softmax-row pass of the recompute at the cost of keeping B*T*N*4 bytes of scores
+ * (plus the row statistics) between forward and backward. */
 int dabsn_hip_read3_bwd_after_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
                                   const void* gout, const void* q, const void* K, const void* V,
                                   const void* Vn, const float* cocktail,
@@ -265,7 +289,8 @@ int dabsn_hip_read3_bwd_after_fwd(int dtype, int64_t B, int64_t T, int64_t N, in
                                   const float* const* gains, void* gq, void* gK, void* gV,
                                   void* gVn, float* gcocktail, float* gbank_cocktail,
                                   float* gkey_bias, float* gadmission, float* gscalars5,
-                                  void* workspace, size_t workspace_bytes, hipStream_t stream);
+                                  const void* kept, size_t kept_bytes, void* scratch,
+                                  size_t scratch_bytes, hipStream_t stream);
 
 /* Decode read: the forward of dabsn_hip_read3_fwd (mode 0, seq) for a few query rows
  * (T <= 8) against a long bank, reading the bank in place instead of from gathered K, V,

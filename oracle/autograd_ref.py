@@ -113,8 +113,12 @@ def compact_masks(idx, valid, T, mode, query_offset=0, total_steps=None):
     return allow, induct, allow.any(-1), induct.any(-1)
 
 
-def dense_read(q, K, V, Vn, ck, cb, kb, adm, scale, allow, induct, gains):
-    """admitted.py:16-65 output (gains = short, pad, induct, cocktail)."""
+def dense_read(q, K, V, Vn, ck, cb, kb, adm, scale, allow, induct, gains, capture=None):
+    """admitted.py:16-65 output (gains = short, pad, induct, cocktail). With a ``capture``
+    dict, the permanent pathway's scores ("perm") and the scaled query-key products
+    ("compat") are stored there with their gradients retained, plus the unscaled
+    products "qk" and "cocktail_compat": the terms that the cocktail, scale and
+    cocktail-gain gradients sum."""
     sg, pg, ig, cg = gains
     eligible, induct_eligible = allow.any(-1), induct.any(-1)
     compat = torch.bmm(q, K.transpose(1, 2)) * scale
@@ -122,6 +126,12 @@ def dense_read(q, K, V, Vn, ck, cb, kb, adm, scale, allow, induct, gains):
     content = compat + kb.unsqueeze(1)
     short = content + adm.unsqueeze(1)
     perm = content + cocktail_compat + adm.unsqueeze(1)
+    if capture is not None and perm.requires_grad:
+        for name, t in (("perm", perm), ("compat", compat)):
+            t.retain_grad()
+            capture[name] = t
+        capture["qk"] = (compat / scale).detach()
+        capture["cocktail_compat"] = (cocktail_compat / cg).detach() if cg else None
     ws = _masked_softmax(short, allow, eligible)
     wp = _masked_softmax(perm, allow, eligible)
     wi = _masked_softmax(short, induct, induct_eligible)

@@ -90,3 +90,15 @@ def assert_rel(actual, expected, tol: float, name: str = "") -> None:
     if not np.isfinite(a).all():
         raise AssertionError(f"{name}: non-finite values in the HIP result")
     assert r <= tol, f"{name}: normwise relative error {r:.3e} > {tol}"
+
+
+def grad_err(got, want, scale: float) -> float:
+    """Normwise error of a parameter gradient, relative to max(max|want|, 1e-3 * scale)
+    where ``scale`` is the largest parameter gradient of the module. A scalar gain's
+    gradient is a sum over all (query, slot) terms; where those cancel (null_bias and
+    adm_bias shift every score of a softmax row equally, so their exact gradient is 0;
+    cocktail_gain sums O(1) terms to O(1e-3)), both sides carry fp32 rounding of the
+    terms, not of the small total."""
+    g = np.asarray(np32(got), np.float64)
+    w = np.asarray(np32(want), np.float64)
+    return float(np.abs(g - w).max()) / max(float(np.abs(w).max()), 1e-3 * scale, 1e-30)

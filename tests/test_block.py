@@ -7,7 +7,8 @@ compared with the CPU oracle evaluation of the same module.
   * block time-chunking with carried state equals the full scan (reference
     tests/test_block_chunking.py:20-51): forward to fp32 rounding, grads to 1e-5;
   * forward_query_bank on a query chunk against the full bank equals the unified read
-    for those rows (reference tests/test_read_chunking.py:23-109): 1e-5;
+    for those rows (reference tests/test_read_chunking.py:23-109): 1e-5; on the GPU the
+    chunk read runs on the device and the unified read is the CPU oracle run;
   * config 1 (two seq layers 128/96 and 192/128, input 24, residual, MLP 4.0, fp32)
     forward+backward on GPU against the CPU oracle: normwise 1e-4 for every output and
     parameter gradient (several fp32 ops in sequence, each within 1e-5).
@@ -78,23 +79,27 @@ def test_block_chunking_equals_full_gpu(cuda_device):
 
 
 def _query_bank_case(device):
+    """The unified read of the full sequence on the CPU oracle, and on ``device`` the query
+    chunk [25, 40) read against the whole bank with the long state carried to 25."""
     torch.manual_seed(3)
-    blk = _block(3, 16, 24, 24).to(device)
+    blk = _block(3, 16, 24, 24)
     g = torch.Generator().manual_seed(4)
-    x = torch.randn(2, 40, 16, generator=g).to(device)
+    x = torch.randn(2, 40, 16, generator=g)
     with torch.no_grad():
         traj, nov, p, ay, wr, en, sat = blk.core_tapes(x)
         y, b = traj.split(24, dim=-1)
         full = blk.read(y, b, ay, wr, nov, p, en, sat)
+        dev = copy.deepcopy(blk).to(device)
+        y, b, ay, wr, nov, p, en, sat = (t.to(device) for t in (y, b, ay, wr, nov, p, en, sat))
         t0 = 25
-        _, long_state = blk.read._long_scan_from_state(wr[:, :t0], p[:, :t0], nov[:, :t0],
+        _, long_state = dev.read._long_scan_from_state(wr[:, :t0], p[:, :t0], nov[:, :t0],
                                                         return_final_state=True)
         sl = slice(t0, None)
-        part = blk.read.forward_query_bank(
+        part = dev.read.forward_query_bank(
             y[:, sl], b[:, sl], ay[:, sl], wr[:, sl], nov[:, sl], p[:, sl], en[:, sl], sat[:, sl],
             bank_write=wr, bank_novelty=nov, bank_p=p, bank_energy=en, bank_saturation=sat,
             query_start=t0, initial_long_state=long_state)
-    return full[:, t0:], part
+    return full[:, t0:], part.cpu()
 
 
 def test_forward_query_bank_matches_unified_read_cpu():
@@ -103,9 +108,9 @@ def test_forward_query_bank_matches_unified_read_cpu():
 
 
 @pytest.mark.gpu
-def test_forward_query_bank_matches_unified_read_gpu(cuda_device):
+def test_forward_query_bank_matches_oracle_unified_read_gpu(cuda_device):
     full, part = _query_bank_case(cuda_device)
-    assert rel_err(part.cpu(), full.cpu()) <= 1e-5
+    assert rel_err(part, full) <= 1e-5
 
 
 @pytest.mark.gpu

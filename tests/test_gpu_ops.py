@@ -410,6 +410,24 @@ def test_read3_backward_on_the_kept_forward_equals_the_recompute(cuda_device, dt
         assert torch.equal(a, b), f"grad {i}"
 
 
+def test_read3_training_path_backward_twice_with_retain_graph(cuda_device):
+    """The kept buffer is only read by the backward, so a second backward through the same
+    graph (retain_graph=True) runs and gives the same gradients bit for bit."""
+    B, T, H = 2, 200, 64
+    c = _read_case(89, B, T, H)
+    d = lambda x: x.to(cuda_device)  # noqa: E731
+    leaves = [d(c[k]).requires_grad_(True) for k in ("q", "K", "V", "Vn", "ck", "cb", "kb", "adm")]
+    scale = torch.tensor([1.9], device=cuda_device, requires_grad=True)
+    gains = [torch.tensor([v], device=cuda_device, requires_grad=True) for v in (1.0, 0.7, 0.1, 1.3)]
+    out = ops.admitted_three_way_read_train(*leaves, scale, d(torch.from_numpy(c["idx"])),
+                                            d(torch.from_numpy(c["valid"])), 0, *gains)
+    go = d(torch.randn(B, T, H, generator=torch.Generator().manual_seed(10)))
+    first = torch.autograd.grad(out, [*leaves, scale, *gains], go, retain_graph=True)
+    second = torch.autograd.grad(out, [*leaves, scale, *gains], go)
+    for i, (a, b) in enumerate(zip(first, second)):
+        assert torch.equal(a, b), f"grad {i}"
+
+
 def test_read3_bf16_within_tolerance_of_fp32_oracle(cuda_device):
     B, T, H = 2, 300, 256
     c = _read_case(77, B, T, H)

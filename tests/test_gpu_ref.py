@@ -6,7 +6,8 @@ operators and modules reproduce them on the GPU:
 
   * ``dabsn::core_scan_batched`` forward and its registered backward (fp32): 1e-5;
   * a seq ``DABSNRead.forward`` on a partially admitted bank: n_max exact, output and
-    gradients 1e-5 (parameter gradients against a floor of 1e-3 x the largest one);
+    gradients 1e-5 (parameter gradients against a floor of 1e-3 x the largest one; the
+    scalar gains, sums of O(T * N) signed terms, 1e-4);
   * the bf16 read: admission values and slot selection bit-exact, through the HIP tape
     statistics, the training-path glue and the fused decode glue;
   * ``forward_query_bank`` with ``query_start > 0`` and a carried long state: 1e-5;
@@ -25,9 +26,8 @@ import torch.nn.functional as F
 import dabsn_amd
 from dabsn_amd import kernels
 from dabsn_amd.kernels import ops
-from helpers import rel_err
-from test_ref_pins import (_bf16, _load, _read_module, _tapes, c1_block_check, grad_err,
-                           memory_lm_check)
+from helpers import grad_err, rel_err
+from test_ref_pins import _bf16, _load, _read_module, _tapes, c1_block_check, memory_lm_check
 
 pytestmark = pytest.mark.gpu
 
@@ -72,7 +72,10 @@ def test_read_seq_vs_reference_fixture_gpu(cuda_device):
         if key not in z:
             continue
         err = grad_err(g.cpu(), z[key], scale) if n.startswith("param.") else rel_err(g.cpu(), z[key])
-        assert err <= 1e-5, f"{n}: {err:.3e}"
+        # A scalar gain's gradient sums O(T * N) signed terms, accumulated here in tile
+        # partials: 1e-4, the scalar-gradient bar of the other GPU parity tests.
+        tol = 1e-4 if z[key].size == 1 else 1e-5
+        assert err <= tol, f"{n}: {err:.3e}"
 
 
 def test_bf16_selection_bit_exact_vs_reference_fixture_gpu(cuda_device):

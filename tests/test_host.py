@@ -135,29 +135,6 @@ def test_enable_and_status_semantics_without_a_device():
     assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
 
 
-def test_routing_events_once_and_strict_fallback():
-    from dabsn_amd import events
-
-    seen = []
-    events.reset_routing_log()
-    events.add_event_listener(seen.append)
-    try:
-        events.log_routing_once("core", "rocm", B=2, T=3)
-        events.log_routing_once("core", "rocm", B=2, T=3)
-        events.log_routing_once("core", "rocm", B=2, T=4)
-        assert [e.code for e in seen] == [events.EventCode.KERNEL_SELECTION] * 2
-        with pytest.raises(ValueError):
-            events.emit_event(events.EventCode.PERFORMANCE_FALLBACK, fallback=True, reason="x")
-        with events.strict_events():
-            with pytest.raises(events.StrictFallbackError):
-                events.warn_routing_once("read", "bank too wide", requested_path="rocm_native")
-        events.warn_routing_once("read", "other", requested_path="rocm_native")
-        assert seen[-1].fallback and seen[-1].fields["corrective_action"]
-    finally:
-        events.remove_event_listener(seen.append)
-        events.reset_routing_log()
-
-
 def test_parameter_copies_are_reused_only_inside_the_context():
     """fp32 copies of bf16 parameters are rebuilt on every call outside
     ``reuse_parameter_copies``; inside it they are reused until the parameter's version or

@@ -4,11 +4,14 @@ Reference behaviour: src/dabsn/memory.py and its exactness claim (tests/test_mem
 of the reference: chunked ingest against a growing bank reproduces one dense pass to
 float32 rounding). CPU variants run through the test-only oracle backend
 (oracle/torch_backend.py registers the C oracle as the ops' CPU kernels); GPU variants run
-the HIP kernels. fp32 throughout; tolerance normwise 1e-5 (the chunked read sums over a
-bank of a different width, so reductions differ in order).
+the HIP kernels, and every expected value -- the dense pass or the fresh ingest -- is the
+CPU oracle run of the same weights. fp32 throughout; tolerance normwise 1e-5 (the chunked
+read sums over a bank of a different width, so reductions differ in order).
 """
 
 from __future__ import annotations
+
+import copy
 
 import pytest
 import torch
@@ -32,6 +35,13 @@ def _model(device):
     return model.to(device).eval()
 
 
+def _pair(device):
+    """The model on ``device`` and the same weights on the CPU, where the ops run the
+    oracle: every expected value below comes from the CPU oracle run."""
+    cpu = _model("cpu")
+    return copy.deepcopy(cpu).to(device), cpu
+
+
 def _dense(model, ids):
     with torch.no_grad():
         h = model.embed(ids)
@@ -45,19 +55,21 @@ def _ids(B, T, seed=8):
 
 
 def _chunked_ingest(device):
-    model = _model(device)
-    ids = _ids(2, 45).to(device)
-    want, _ = _dense(model, ids)
-    got, memory = mem.forward_with_memory(model, ids, None, chunk_size=8, return_hidden=True)
+    model, cpu = _pair(device)
+    ids = _ids(2, 45)
+    want, _ = _dense(cpu, ids)
+    got, memory = mem.forward_with_memory(model, ids.to(device), None, chunk_size=8,
+                                          return_hidden=True)
     assert memory.position == 45 and memory.entries == 45
     assert [layer.bank.length for layer in memory.layers] == [45, 45]
-    return got, want
+    return got.cpu(), want
 
 
 def _decode(device):
-    model = _model(device)
-    ids = _ids(3, 26, seed=9).to(device)
-    _, want = _dense(model, ids)
+    model, cpu = _pair(device)
+    ids = _ids(3, 26, seed=9)
+    _, want = _dense(cpu, ids)
+    ids = ids.to(device)
     memory = mem.ingest(model, ids[:, :20], chunk_size=6)
     memory.reserve(26)
     logits = []
@@ -65,7 +77,7 @@ def _decode(device):
         step, memory = mem.forward_with_memory(model, ids[:, t:t + 1], memory, extend=True)
         logits.append(step)
     assert memory.position == 26
-    return torch.cat(logits, dim=1), want[:, 20:]
+    return torch.cat(logits, dim=1).cpu(), want[:, 20:]
 
 
 def test_bank_store_appends_in_place_and_doubles():
@@ -123,20 +135,22 @@ def _branches(device):
     """Two continuations extended from one prefix handle, each against a fresh ingest of
     its own full sequence (the reference rebuilds the bank per call, memory.py:250-254, so
     branching from a shared prefix is valid there)."""
-    model = _model(device)
-    ids = _ids(2, 16, seed=13).to(device)
+    model, cpu = _pair(device)
+    ids = _ids(2, 16, seed=13)
     alt = ids.clone()
     alt[:, 12:] = (alt[:, 12:] + 7) % 40
+    fresh_a, _ = mem.forward_with_memory(cpu, ids, None, chunk_size=None)
+    fresh_b, _ = mem.forward_with_memory(cpu, alt, None, chunk_size=None)
+    ids, alt = ids.to(device), alt.to(device)
     base = mem.ingest(model, ids[:, :12], chunk_size=5)
     out_a, mem_a = mem.forward_with_memory(model, ids[:, 12:], base, extend=True)
     out_b, mem_b = mem.forward_with_memory(model, alt[:, 12:], base, extend=True)
     assert base.position == 12 and [layer.entries for layer in base.layers] == [12, 12]
     assert mem_a.position == mem_b.position == 16
-    fresh_a, _ = mem.forward_with_memory(model, ids, None, chunk_size=None)
-    fresh_b, _ = mem.forward_with_memory(model, alt, None, chunk_size=None)
     # The first branch again, after the second one extended the shared prefix.
     again, _ = mem.forward_with_memory(model, ids[:, 12:], base, extend=True)
-    return (out_a, fresh_a[:, 12:]), (out_b, fresh_b[:, 12:]), (again, fresh_a[:, 12:])
+    return ((out_a.cpu(), fresh_a[:, 12:]), (out_b.cpu(), fresh_b[:, 12:]),
+            (again.cpu(), fresh_a[:, 12:]))
 
 
 def test_branching_from_one_prefix_equals_fresh_ingest_cpu():
@@ -145,21 +159,21 @@ def test_branching_from_one_prefix_equals_fresh_ingest_cpu():
 
 
 @pytest.mark.gpu
-def test_branching_from_one_prefix_equals_fresh_ingest_gpu(cuda_device):
+def test_branching_from_one_prefix_equals_fresh_oracle_ingest_gpu(cuda_device):
     for got, want in _branches(cuda_device):
-        assert rel_err(got.cpu(), want.cpu()) <= 1e-5
+        assert rel_err(got, want) <= 1e-5
 
 
 @pytest.mark.gpu
-def test_chunked_ingest_equals_dense_pass_gpu(cuda_device):
+def test_chunked_ingest_equals_oracle_dense_pass_gpu(cuda_device):
     got, want = _chunked_ingest(cuda_device)
-    assert rel_err(got.cpu(), want.cpu()) <= 1e-5
+    assert rel_err(got, want) <= 1e-5
 
 
 @pytest.mark.gpu
-def test_decode_token_by_token_equals_dense_pass_gpu(cuda_device):
+def test_decode_token_by_token_equals_oracle_dense_pass_gpu(cuda_device):
     got, want = _decode(cuda_device)
-    assert rel_err(got.cpu(), want.cpu()) <= 1e-5
+    assert rel_err(got, want) <= 1e-5
 
 
 def _continue(model, memory, ids):

@@ -48,7 +48,7 @@ import torch.nn.functional as F
 import dabsn_amd
 import oracle
 from dabsn_amd import memory as mem
-from helpers import core_case, np32, oracle_core_bwd, oracle_core_fwd, rel_err
+from helpers import core_case, grad_err, np32, oracle_core_bwd, oracle_core_fwd, rel_err
 from oracle import autograd_ref
 from oracle import ref as oracle_ref
 from oracle import torch_backend
@@ -297,18 +297,6 @@ def _read_module(z, H, suffix=""):
             src = z[f"param.{n}{suffix}"]
             p.copy_(_bf16(src).float() if suffix else torch.from_numpy(src))
     return read
-
-
-def grad_err(got, want, scale: float) -> float:
-    """Normwise error of a parameter gradient, relative to max(max|want|, 1e-3 * scale)
-    where ``scale`` is the largest parameter gradient of the module. A scalar gain's
-    gradient is a sum over all (query, slot) terms; where those cancel (null_bias and
-    adm_bias shift every score of a softmax row equally, so their exact gradient is 0;
-    cocktail_gain sums O(1) terms to O(1e-3)), both sides carry fp32 rounding of the
-    terms, not of the small total."""
-    g = np.asarray(np32(got), np.float64)
-    w = np.asarray(np32(want), np.float64)
-    return float(np.abs(g - w).max()) / max(float(np.abs(w).max()), 1e-3 * scale, 1e-30)
 
 
 def test_read_seq_vs_reference_fixture():
