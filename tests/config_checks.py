@@ -131,7 +131,7 @@ def check_stats_rows(P, tapes, rows, tol=1e-5):
 
 def check_selection(P, read):
     adm = P["admission"]
-    window = float(F.softplus(read.admit_window))
+    window = float(F.softplus(read.admit_window.detach()))
     order, counts = oracle.bank_select(np32(adm), window, floor_bf16=adm.dtype == torch.bfloat16)
     n_max = max(int(counts.max()), 1)
     assert P["bank_n_max"] == n_max
