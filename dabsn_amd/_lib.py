@@ -126,6 +126,11 @@ _SIGNATURES = {
          vp, vp, sz, vp],
         i32,
     ),
+    "dabsn_hip_read3_decode_noalloc": (
+        [i32, i64, i64, i64, i64, vp, vp, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, PTR4,
+         vp, vp],
+        i32,
+    ),
     "dabsn_hip_read3_bwd": (
         [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4]
         + [vp] * 4 + [vp] * 5 + [vp, sz, vp],

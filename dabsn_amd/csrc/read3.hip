@@ -21,6 +21,7 @@
 // any of its queries may read; a bank tile only visits queries at or after its
 // earliest admitted index.
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/dabsn_hip.h"
 #include "capi.hpp"
@@ -1589,6 +1590,69 @@ int dabsn_hip_read3_decode(int dtype, int64_t B, int64_t T, int64_t N, int64_t H
                             norm_w, idx, next_idx, read_idx, valid, cocktail, bank_cocktail,
                             key_bias, admission, scale, g, (float*)out, (uint8_t*)workspace, p,
                             stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// The decode read without a workspace argument, for callers that cannot allocate device
+// memory: code under HIP graph capture, serving loops whose buffers are all planned ahead.
+// The scratch is a file-scope device array, so every device the library runs on holds its
+// own kNoAllocScratchBytes from module load until the process ends. Every call on a device
+// uses that device's copy: calls that overlap on one device (other streams, other threads)
+// race. Nothing needs clearing between calls -- each kernel of the decode read writes every
+// scratch element it or a later kernel of the same call reads.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = DABSN_READ3_DECODE_NOALLOC_MAX_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t decode_scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mutex;
+static uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's copy of decode_scratch, looked up once per device
+// (the array's host-side name is not a device address).
+static int scratch_of_current_device(uint8_t** out) {
+  int dev = 0;
+  DABSN_HIP_CHECK(hipGetDevice(&dev));
+  DABSN_REQUIRE(dev >= 0 && dev < kMaxDevices, "read3 decode (no allocation): device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    DABSN_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(decode_scratch)));
+    DABSN_REQUIRE(ptr != nullptr, "read3 decode (no allocation): no scratch on device %d", dev);
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return DABSN_OK;
+}
+
+extern "C" {
+
+int dabsn_hip_read3_decode_noalloc(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
+                                   const void* q, const void* bank, int64_t bank_len,
+                                   int64_t bank_ld, const float* norm_w, const int64_t* idx,
+                                   const int64_t* next_idx, const int64_t* read_idx,
+                                   const uint8_t* valid, const float* cocktail,
+                                   const float* bank_cocktail, const float* key_bias,
+                                   const float* admission, const float* scale,
+                                   const float* const* gains, void* out, hipStream_t stream) {
+  const int rc = read3_checks(dtype, B, T, N, H, 0);
+  if (rc != DABSN_OK) return rc;
+  DABSN_REQUIRE(T <= kDecodeRows, "read3 decode: T=%lld query rows > %d", (long long)T, kDecodeRows);
+  const DecodePlan p = decode_plan(dtype, B, T, N, H);
+  DABSN_REQUIRE(p.end <= kNoAllocScratchBytes,
+                "read3 decode (no allocation): B=%lld, T=%lld, N=%lld, H=%lld needs %zu bytes of "
+                "scratch, more than the %zu bytes the library holds per device; call "
+                "dabsn_hip_read3_decode with a workspace instead",
+                (long long)B, (long long)T, (long long)N, (long long)H, p.end,
+                kNoAllocScratchBytes);
+  uint8_t* ws = nullptr;
+  const int sc = scratch_of_current_device(&ws);
+  if (sc != DABSN_OK) return sc;
+  return dabsn_hip_read3_decode(dtype, B, T, N, H, q, bank, bank_len, bank_ld, norm_w, idx,
+                                next_idx, read_idx, valid, cocktail, bank_cocktail, key_bias,
+                                admission, scale, gains, out, ws, kNoAllocScratchBytes, stream);
 }
 
 }  // extern "C"

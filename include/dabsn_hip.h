@@ -318,6 +318,26 @@ int dabsn_hip_read3_decode(int dtype, int64_t B, int64_t T, int64_t N, int64_t H
                            const float* const* gains, void* out, void* workspace,
                            size_t workspace_bytes, hipStream_t stream);
 
+/* The decode read for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops whose buffers are all planned ahead). This entry point has no
+ * counterpart in the reference. Same arguments and result as dabsn_hip_read3_decode
+ * without the workspace: the library keeps a scratch array of
+ * DABSN_READ3_DECODE_NOALLOC_MAX_BYTES on every device it runs on, from module load until
+ * the process ends, and calls nothing that allocates. A call whose decode plan needs more
+ * scratch than that returns DABSN_ERR_ARG with nothing enqueued (at H = 2048 in bf16 a
+ * one-row read of batch 256 fits banks of about 10,000 slots). Calls that overlap on one
+ * device -- on other streams or threads -- share the array and race; the array keeps the
+ * last call's contents, none of which a later call reads. */
+#define DABSN_READ3_DECODE_NOALLOC_MAX_BYTES ((size_t)128 << 20)
+int dabsn_hip_read3_decode_noalloc(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
+                                   const void* q, const void* bank, int64_t bank_len,
+                                   int64_t bank_ld, const float* norm_w, const int64_t* idx,
+                                   const int64_t* next_idx, const int64_t* read_idx,
+                                   const uint8_t* valid, const float* cocktail,
+                                   const float* bank_cocktail, const float* key_bias,
+                                   const float* admission, const float* scale,
+                                   const float* const* gains, void* out, hipStream_t stream);
+
 /* ---- permanent associative delta scan --------------------------------------------
  * Replaces dabsn::permanent_delta_scan and its registered backward
  * (src/dabsn/kernels/permanent.py:39-119, 384-433; CPU cpu_runtime.cpp:1075-1188).
