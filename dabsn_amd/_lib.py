@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib = None
@@ -90,8 +90,11 @@ _SIGNATURES = {
         i32,
     ),
     "dabsn_hip_tape_stats": ([i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),
-    "dabsn_hip_tape_stats_bwd": (
-        [i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_tape_stats_bwd": ([i32, i64, i64, i64, vp, i32, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_read_output": ([i32, i32, i32, i32, i64, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_read_output_partials": ([i64], sz),
+    "dabsn_hip_read_output_bwd": (
+        [i32, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_normalize_rows": ([i32, i64, i64, vp, vp, vp, vp], i32),
     "dabsn_hip_normalize_rows_bwd": ([i32, i64, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_select": ([i32, i64, i64, vp, vp, vp, vp, vp, vp], i32),

@@ -72,10 +72,12 @@ __global__ void __launch_bounds__(256) stats_kernel(int64_t rows, int H, const E
 }
 
 // g_tape[b,t,h] += g_mean[b,t] / H for the four averaged tapes; one thread per V elements.
+// Mean gradients broadcast over H: g = gstats / H, written (accumulate = 0) or added to
+// what the buffers hold (accumulate = 1).
 template <typename E, int V>
 __global__ void __launch_bounds__(256) stats_bwd_kernel(uint32_t chunks, uint32_t cpr, int H,
-                                                        const float* gstats, E* gen, E* gsat,
-                                                        E* gnov, E* gpl) {
+                                                        const float* gstats, int accumulate,
+                                                        E* gen, E* gsat, E* gnov, E* gpl) {
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   if (i >= chunks) return;
   const uint32_t row = i / cpr;
@@ -87,10 +89,15 @@ __global__ void __launch_bounds__(256) stats_bwd_kernel(uint32_t chunks, uint32_
   for (int k = 0; k < 4; ++k) {
     if (!dst[k]) continue;
     float v[V];
-    ldv<E, V>(dst[k] + o, v);
     const float add = g[k] * inv;
+    if (accumulate) {
+      ldv<E, V>(dst[k] + o, v);
 #pragma unroll
-    for (int e = 0; e < V; ++e) v[e] += add;
+      for (int e = 0; e < V; ++e) v[e] += add;
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[e] = add;
+    }
     stv<E, V>(dst[k] + o, v);
   }
 }
@@ -312,6 +319,78 @@ static inline bool vec_ok(int64_t H, std::initializer_list<const void*> ptrs) {
   return true;
 }
 
+// Read output (read.py:435-438, 821-823): out = proj + gain * long, evaluated as the
+// reference's two tensor operations under type promotion -- the product in the dtype of
+// (gain, long), rounded to bf16 when prod_bf16, then the sum in the dtype of (proj, product),
+// rounded by the store to O. No contraction into a fused multiply-add.
+template <typename P, typename L, typename O, int V>
+__global__ void __launch_bounds__(256) read_out_kernel(uint32_t chunks, const P* proj, const L* lng,
+                                                       const float* gain, int prod_bf16, O* out) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= chunks) return;
+  const size_t o = static_cast<size_t>(i) * V;
+  const float g = gain[0];
+  float a[V], l[V];
+  ldv<P, V>(proj + o, a);
+  ldv<L, V>(lng + o, l);
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    float prod = g * l[e];
+    if (prod_bf16) prod = round_to<bf16>(prod);
+    a[e] = a[e] + prod;
+  }
+  stv<O, V>(out + o, a);
+}
+
+// Its backward, as autograd evaluates it: gproj = gout cast to P; the product's gradient
+// gp = gout cast to the product dtype; glong = gp * gain in that dtype, cast to L; the gain's
+// gradient sums gp * long (each term in the product dtype, the sum in fp32), one partial per
+// workgroup, reduced in a fixed order by read_out_reduce_kernel.
+template <typename O, typename P, typename L, int V>
+__global__ void __launch_bounds__(256) read_out_bwd_kernel(uint32_t chunks, const O* gout,
+                                                           const L* lng, const float* gain,
+                                                           int prod_bf16, P* gproj, L* glong,
+                                                           float* partial) {
+  __shared__ float sh[4];
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  float acc = 0.0f;
+  if (i < chunks) {
+    const size_t o = static_cast<size_t>(i) * V;
+    const float g = gain[0];
+    float go[V], l[V], gl[V];
+    ldv<O, V>(gout + o, go);
+    ldv<L, V>(lng + o, l);
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float gp = prod_bf16 ? round_to<bf16>(go[e]) : go[e];
+      float x = gp * g;
+      if (prod_bf16) x = round_to<bf16>(x);
+      gl[e] = x;
+      float t = gp * l[e];
+      if (prod_bf16) t = round_to<bf16>(t);
+      acc += t;
+    }
+    stv<P, V>(gproj + o, go);
+    stv<L, V>(glong + o, gl);
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+
+// One workgroup: strided partial sums per thread, then the wave/LDS tree; fixed order.
+__global__ void __launch_bounds__(256) read_out_reduce_kernel(uint32_t n, const float* partial,
+                                                              float* out) {
+  __shared__ float sh[4];
+  float acc = 0.0f;
+  for (uint32_t k = threadIdx.x; k < n; k += 256u) acc += partial[k];
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) out[0] = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+
 // Runs LAUNCH(E, V) for the dtype code, with V = 8 when `vec` holds and V = 1 otherwise.
 #define GLUE_DISPATCH(what, dtype, vec, LAUNCH)                       \
   do {                                                                \
@@ -380,15 +459,9 @@ int dabsn_hip_tape_stats(int dtype, int64_t B, int64_t T, int64_t H, const void*
   return DABSN_OK;
 }
 
-int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* expr,
-                             const void* write, const float* stats, const float* gstats,
-                             void* gnov, void* gplast, void* genergy, void* gsat, void* gexpr,
-                             void* gwrite, hipStream_t stream) {
-  (void)expr;
-  (void)write;
-  (void)stats;
-  DABSN_REQUIRE(gexpr == nullptr && gwrite == nullptr,
-                "tape_stats backward: norm gradients are handled by the normalisation ops");
+int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const float* gstats,
+                             int accumulate, void* gnov, void* gplast, void* genergy, void* gsat,
+                             hipStream_t stream) {
   DABSN_REQUIRE(B > 0 && T >= 0 && H > 0, "tape_stats backward: bad shape");
   const int64_t rows = B * T;
   if (rows == 0) return DABSN_OK;
@@ -400,8 +473,8 @@ int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const v
   const dim3 grid(blocks_for(chunks, 256)), block(256);
 #define L(E, VV)                                                                                \
   hipLaunchKernelGGL((stats_bwd_kernel<E, VV>), grid, block, 0, stream, (uint32_t)chunks,      \
-                     (uint32_t)(H / VV), (int)H, gstats, (E*)genergy, (E*)gsat, (E*)gnov,      \
-                     (E*)gplast)
+                     (uint32_t)(H / VV), (int)H, gstats, accumulate ? 1 : 0, (E*)genergy,      \
+                     (E*)gsat, (E*)gnov, (E*)gplast)
   GLUE_DISPATCH("tape_stats backward", dtype, vec, L);
 #undef L
   DABSN_HIP_CHECK(hipGetLastError());
@@ -489,6 +562,93 @@ int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_
                      (const E*)gVn, (E*)gw)
   GLUE_DISPATCH("bank_gather backward", dtype, vec, L);
 #undef L
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+static bool read_out_vec(int64_t n, std::initializer_list<const void*> ptrs) {
+  if (n % 8 != 0) return false;
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) & 15u) return false;
+  return true;
+}
+
+// Calls LAUNCH(A, B, C, V) with A, B, C the element types of three dtype codes.
+#define READ_OUT_TYPES(what, da, db, dc, vec, LAUNCH)                                     \
+  do {                                                                                    \
+    DABSN_REQUIRE((da == kF32 || da == kBF16) && (db == kF32 || db == kBF16) &&           \
+                      (dc == kF32 || dc == kBF16),                                        \
+                  what ": dtype codes must be 0 (fp32) or 1 (bf16)");                     \
+    const int code = (da == kBF16 ? 4 : 0) | (db == kBF16 ? 2 : 0) | (dc == kBF16 ? 1 : 0); \
+    switch (code * 2 + (vec ? 1 : 0)) {                                                   \
+      case 0: LAUNCH(float, float, float, 1); break;                                      \
+      case 1: LAUNCH(float, float, float, 8); break;                                      \
+      case 2: LAUNCH(float, float, bf16, 1); break;                                       \
+      case 3: LAUNCH(float, float, bf16, 8); break;                                       \
+      case 4: LAUNCH(float, bf16, float, 1); break;                                       \
+      case 5: LAUNCH(float, bf16, float, 8); break;                                       \
+      case 6: LAUNCH(float, bf16, bf16, 1); break;                                        \
+      case 7: LAUNCH(float, bf16, bf16, 8); break;                                        \
+      case 8: LAUNCH(bf16, float, float, 1); break;                                       \
+      case 9: LAUNCH(bf16, float, float, 8); break;                                       \
+      case 10: LAUNCH(bf16, float, bf16, 1); break;                                       \
+      case 11: LAUNCH(bf16, float, bf16, 8); break;                                       \
+      case 12: LAUNCH(bf16, bf16, float, 1); break;                                       \
+      case 13: LAUNCH(bf16, bf16, float, 8); break;                                       \
+      case 14: LAUNCH(bf16, bf16, bf16, 1); break;                                        \
+      default: LAUNCH(bf16, bf16, bf16, 8); break;                                        \
+    }                                                                                     \
+  } while (0)
+
+int dabsn_hip_read_output(int proj_dtype, int long_dtype, int prod_dtype, int out_dtype,
+                          int64_t n, const void* proj, const void* lng, const float* gain,
+                          void* out, hipStream_t stream) {
+  DABSN_REQUIRE(n >= 0, "read_output: bad size");
+  if (n == 0) return DABSN_OK;
+  DABSN_REQUIRE(proj && lng && gain && out, "read_output: null pointer");
+  DABSN_REQUIRE(prod_dtype == kF32 || prod_dtype == kBF16, "read_output: bad product dtype");
+  const bool vec = read_out_vec(n, {proj, lng, out});
+  const int64_t chunks = n / (vec ? 8 : 1);
+  DABSN_REQUIRE(chunks < (1ll << 32), "read_output: too many elements");
+  const dim3 grid(blocks_for(chunks, 256)), block(256);
+#define L(P, Lt, O, V)                                                                      \
+  hipLaunchKernelGGL((read_out_kernel<P, Lt, O, V>), grid, block, 0, stream, (uint32_t)chunks, \
+                     (const P*)proj, (const Lt*)lng, gain, prod_dtype == kBF16 ? 1 : 0, (O*)out)
+  READ_OUT_TYPES("read_output", proj_dtype, long_dtype, out_dtype, vec, L);
+#undef L
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+size_t dabsn_hip_read_output_partials(int64_t n) {
+  // One partial per workgroup of 256 threads; the unvectorised count bounds both cases.
+  return static_cast<size_t>(blocks_for(n > 0 ? n : 1, 256));
+}
+
+int dabsn_hip_read_output_bwd(int out_dtype, int proj_dtype, int long_dtype, int prod_dtype,
+                              int64_t n, const void* gout, const void* lng, const float* gain,
+                              void* gproj, void* glong, float* ggain, float* partials,
+                              size_t partial_count, hipStream_t stream) {
+  DABSN_REQUIRE(n >= 0, "read_output backward: bad size");
+  DABSN_REQUIRE(ggain && partials, "read_output backward: null pointer");
+  if (n == 0) return dabsn_hip_zero(ggain, 4, stream);
+  DABSN_REQUIRE(gout && lng && gain && gproj && glong, "read_output backward: null pointer");
+  DABSN_REQUIRE(prod_dtype == kF32 || prod_dtype == kBF16, "read_output backward: bad product dtype");
+  const bool vec = read_out_vec(n, {gout, lng, gproj, glong});
+  const int64_t chunks = n / (vec ? 8 : 1);
+  DABSN_REQUIRE(chunks < (1ll << 32), "read_output backward: too many elements");
+  const unsigned nblk = blocks_for(chunks, 256);
+  DABSN_REQUIRE(partial_count >= nblk, "read_output backward: %zu partials < %u", partial_count,
+                nblk);
+  const dim3 grid(nblk), block(256);
+#define L(O, P, Lt, V)                                                                          \
+  hipLaunchKernelGGL((read_out_bwd_kernel<O, P, Lt, V>), grid, block, 0, stream,               \
+                     (uint32_t)chunks, (const O*)gout, (const Lt*)lng, gain,                   \
+                     prod_dtype == kBF16 ? 1 : 0, (P*)gproj, (Lt*)glong, partials)
+  READ_OUT_TYPES("read_output backward", out_dtype, proj_dtype, long_dtype, vec, L);
+#undef L
+  DABSN_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(read_out_reduce_kernel, dim3(1), dim3(256), 0, stream, nblk, partials, ggain);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }

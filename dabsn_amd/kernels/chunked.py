@@ -11,7 +11,10 @@ reverse scan. The same work is scheduled differently here:
 * the recompute of chunk k - 1 depends only on the saved start state of that chunk, not on
   the reverse scan of chunk k, so the two run as one cooperative launch on disjoint halves
   of the device (``dabsn_hip_core_scan_pair``). When the device cannot hold both grids at
-  once the two launches run one after the other.
+  once the two launches run one after the other;
+* the last chunk is not recomputed: its reverse scan, which runs first, reads the tapes
+  the forward wrote (the way ``torch.utils.checkpoint.checkpoint_sequential`` leaves its
+  last segment un-checkpointed).
 
 Outputs equal the single full-length scan bit for bit; gradients equal it up to the
 rounding of the carried state gradient at chunk boundaries.
@@ -39,9 +42,13 @@ def _empty(shape, like: Tensor, dtype=None) -> Tensor:
 
 
 class _Tapes:
-    """Full-length forward outputs: U [B, T, 2H] and the 7 tapes [B, T, H]."""
+    """Full-length forward outputs: U [B, T, 2H] and the 7 tapes [B, T, H] (novelty,
+    plasticity, expression, write, energy, saturation, gate); new, or existing tensors."""
 
-    def __init__(self, like: Tensor, B: int, T: int, H: int) -> None:
+    def __init__(self, like: Tensor, B: int, T: int, H: int, existing=None) -> None:
+        if existing is not None:
+            self.U, self.tapes = existing[0], list(existing[1:])
+            return
         self.U = _empty((B, T, 2 * H), like)
         self.tapes = [_empty((B, T, H), like) for _ in range(7)]
 
@@ -162,7 +169,13 @@ class _ChunkedCoreScan(torch.autograd.Function):
         finals = [f.to(x.dtype) for f, x in zip(carry, (b0, e0, c0))]
         ctx.chunk = chunk
         ctx.meta = [(x.dtype, tuple(x.shape)) for x in inputs]
-        ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, torch.stack(starts))
+        # The forward's own outputs are kept for the backward: the last chunk's reverse scan
+        # reads its window there instead of recomputing tapes that were written just before
+        # (as torch.utils.checkpoint.checkpoint_sequential leaves its last segment
+        # un-checkpointed), and the grad [Ug; A] GEMM reads y from U. Every other chunk is
+        # recomputed from its saved start state, as the block checkpoint does.
+        ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, torch.stack(starts), out.U,
+                              *out.tapes)
         ctx.set_materialize_grads(False)
         return (out.U, *out.tapes, *finals)
 
@@ -172,6 +185,7 @@ class _ChunkedCoreScan(torch.autograd.Function):
         Wx, Wgx, Ug, A = saved[:4]
         vecs, scal = saved[4:20], saved[20:23]
         starts = saved[23]  # [K, 3, B, H] chunk start states
+        fwd_out = _Tapes(None, 0, 0, 0, existing=saved[24:32])
         B, T, H = Wx.shape
         dt = Wx.dtype
         code = ops._code(dt)
@@ -185,7 +199,8 @@ class _ChunkedCoreScan(torch.autograd.Function):
         up = [None if g is None else g.to(dt).contiguous() for g in grads[:7]]
         carry = [None if g is None else g.float().contiguous() for g in grads[8:11]]
         gWx, gWgx, day = (_empty((B, T, H), Wx) for _ in range(3))
-        rec = _Tapes(Wx, B, T, H)  # recomputed forward outputs, filled window by window
+        # Recomputed forward outputs, filled window by window (none when there is one chunk).
+        rec = _Tapes(Wx, B, T, H) if K > 1 else None
 
         def fwd_of(k: int) -> _Fwd:
             return _Fwd(code, Wx, Wgx, GA, params, starts[k, 0].contiguous(),
@@ -193,14 +208,12 @@ class _ChunkedCoreScan(torch.autograd.Function):
 
         gvec = torch.zeros((16, H), device=Wx.device, dtype=torch.float32)
         gscal = torch.zeros((3,), device=Wx.device, dtype=torch.float32)
-        first = fwd_of(K - 1)
-        tk = ops.KernelTimer.begin("core_scan_fwd", Wx)
-        first.launch(stream)
-        ops.KernelTimer.end(tk)
-        ops._record_error_word(first.ws, "core scan forward")
         for k in range(K - 1, -1, -1):
+            # The last chunk reads the forward's own tapes; every earlier one reads the
+            # window its recompute wrote during the previous (paired) launch.
+            src = fwd_out if k == K - 1 else rec
             bw = _Bwd(code, GAT, params, starts[k, 0].contiguous(), starts[k, 2].contiguous(),
-                      rec, up, carry, (gWx, gWgx, day), *bounds[k])
+                      src, up, carry, (gWx, gWgx, day), *bounds[k])
             if k > 0:
                 # The recompute writes window k - 1 of `rec` while this reverse scan reads
                 # window k: disjoint rows of the same buffers.
@@ -219,7 +232,7 @@ class _ChunkedCoreScan(torch.autograd.Function):
             carry = bw.g0
         del keep
         # grad [Ug; A] = [gWgx; day]^T y over the whole sequence (y = first half of U).
-        y = rec.U.view(B * T, 2 * H)[:, :H]
+        y = fwd_out.U.reshape(B * T, 2 * H)[:, :H]
         gUg = (gWgx.view(B * T, H).t() @ y).float()
         gA = (day.view(B * T, H).t() @ y).float()
         out = [gWx, gWgx, gUg, gA, *[gvec[i] for i in range(16)], *[gscal[i] for i in range(3)],

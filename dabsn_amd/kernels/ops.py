@@ -775,6 +775,88 @@ def _ce_rows_backward_fake(logits, targets, ignore_index, lse, scale):
 
 
 # ---------------------------------------------------------------------------
+# Read output: proj + long_gain * long (read.py:435-438, 821-823)
+# ---------------------------------------------------------------------------
+def _read_output_dtypes(proj: Tensor, long: Tensor, gain: Tensor) -> tuple[torch.dtype, torch.dtype]:
+    prod = torch.result_type(gain, long)
+    return prod, torch.promote_types(proj.dtype, prod)
+
+
+@torch.library.custom_op("dabsn::read_output", mutates_args=(), device_types="cuda")
+def read_output(proj: Tensor, long: Tensor, gain: Tensor) -> Tensor:
+    """``proj + gain * long`` as the reference evaluates ``out(...) + long_gain * long``: two
+    tensor operations under type promotion (the product in the dtype of gain and long, the
+    sum in the dtype of proj and the product), here in one pass over the elements."""
+    _require_cuda(proj)
+    if proj.shape != long.shape or gain.numel() != 1:
+        raise ValueError("read_output: proj and long must match and gain hold one value")
+    lib = _lib.load()
+    prod_dt, out_dt = _read_output_dtypes(proj, long, gain)
+    pc, lc = proj.contiguous(), long.contiguous()
+    g = _f32_scalar(gain)
+    out = torch.empty(proj.shape, device=proj.device, dtype=out_dt)
+    _lib.check(lib.dabsn_hip_read_output(_code(pc.dtype), _code(lc.dtype), _code(prod_dt),
+                                         _code(out_dt), pc.numel(), _p(pc), _p(lc), _p(g), _p(out),
+                                         _stream(pc)), "read output")
+    return out
+
+
+@read_output.register_fake
+def _read_output_fake(proj, long, gain):
+    return proj.new_empty(proj.shape, dtype=_read_output_dtypes(proj, long, gain)[1])
+
+
+_DTYPE_OF_CODE = {0: torch.float32, 1: torch.bfloat16}
+
+
+@torch.library.custom_op("dabsn::_read_output_backward", mutates_args=(), device_types="cuda")
+def read_output_backward(grad: Tensor, long: Tensor, gain: Tensor,
+                         proj_dtype: int) -> tuple[Tensor, Tensor, Tensor]:
+    """(g_proj, g_long, g_gain) of ``read_output`` (``proj_dtype`` = the dtype code of proj):
+    the gradients autograd forms for the two tensor operations, the gain's summed in a fixed
+    order."""
+    lib = _lib.load()
+    pdt = _DTYPE_OF_CODE[int(proj_dtype)]
+    prod_dt = torch.result_type(gain, long)
+    out_dt = torch.promote_types(pdt, prod_dt)
+    go = grad.to(out_dt).contiguous()
+    lc = long.contiguous()
+    g = _f32_scalar(gain)
+    n = go.numel()
+    gproj = torch.empty(go.shape, device=go.device, dtype=pdt)
+    glong = torch.empty_like(lc)
+    ggain = torch.empty((1,), device=go.device, dtype=torch.float32)
+    count = lib.dabsn_hip_read_output_partials(n)
+    partials = torch.empty((max(count, 1),), device=go.device, dtype=torch.float32)
+    _lib.check(lib.dabsn_hip_read_output_bwd(
+        _code(out_dt), _code(pdt), _code(lc.dtype), _code(prod_dt), n, _p(go), _p(lc), _p(g),
+        _p(gproj), _p(glong), _p(ggain), _p(partials), partials.numel(), _stream(go)),
+        "read output backward")
+    return gproj, glong, ggain.reshape(gain.shape).to(gain.dtype)
+
+
+@read_output_backward.register_fake
+def _read_output_backward_fake(grad, long, gain, proj_dtype):
+    return (grad.new_empty(grad.shape, dtype=_DTYPE_OF_CODE[int(proj_dtype)]),
+            torch.empty_like(long), torch.empty_like(gain))
+
+
+def _read_output_setup(ctx, inputs, output):
+    proj, long, gain = inputs
+    ctx.save_for_backward(long, gain)
+    ctx.proj_dtype = _code(proj.dtype)
+
+
+def _read_output_bwd(ctx, grad):
+    long, gain = ctx.saved_tensors
+    return read_output_backward(grad, long, gain, ctx.proj_dtype)
+
+
+torch.library.register_autograd("dabsn::read_output", _read_output_bwd,
+                                setup_context=_read_output_setup)
+
+
+# ---------------------------------------------------------------------------
 # Fused recurrent long-memory scan
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("dabsn::long_scan_fused", mutates_args=(), device_types="cuda")
@@ -864,6 +946,10 @@ def _long_setup(ctx, inputs, output):
     write, plasticity, l1, l2, l3, l4, L0, E0, R0 = inputs
     ctx.save_for_backward(write, plasticity, l1, l2, l3, l4, output[4])
     ctx.meta = [(x.dtype, tuple(x.shape)) for x in inputs]
+    # The per-step states are saved for the backward, not a result anyone differentiates;
+    # with grads left unmaterialised, unused outputs bring None instead of zero tensors.
+    ctx.mark_non_differentiable(output[4])
+    ctx.set_materialize_grads(False)
 
 
 def _long_bwd(ctx, g_long, g_lf, g_ef, g_rf, _g_states):
@@ -912,9 +998,9 @@ def read_tape_stats_backward(gstats: Tensor, like: Tensor) -> list[Tensor]:
     B, T, H = like.shape
     dt = like.dtype
     gs = gstats.float().contiguous()
-    gn, gp, ge, gc = (torch.zeros((B, T, H), device=like.device, dtype=dt) for _ in range(4))
-    _lib.check(lib.dabsn_hip_tape_stats_bwd(_code(dt), B, T, H, None, None, None, _p(gs), _p(gn),
-                                            _p(gp), _p(ge), _p(gc), None, None, _stream(like)),
+    gn, gp, ge, gc = (torch.empty((B, T, H), device=like.device, dtype=dt) for _ in range(4))
+    _lib.check(lib.dabsn_hip_tape_stats_bwd(_code(dt), B, T, H, _p(gs), 0, _p(gn), _p(gp),
+                                            _p(ge), _p(gc), _stream(like)),
                "tape statistics backward")
     return [gn, gp, ge, gc]
 
@@ -1425,6 +1511,8 @@ OPERATORS = (
     "dabsn::_admitted_three_way_read_compact_flash_backward",
     "dabsn::_read3_fwd_keep",
     "dabsn::_read3_bwd_kept",
+    "dabsn::read_output",
+    "dabsn::_read_output_backward",
 )
 
 
@@ -1454,3 +1542,4 @@ class direct:
     read_tape_stats = staticmethod(_direct(read_tape_stats))
     normalize_rows = staticmethod(_direct(normalize_rows))
     bank_select = staticmethod(_direct(bank_select))
+    read_output = staticmethod(_direct(read_output))

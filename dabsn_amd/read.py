@@ -229,7 +229,7 @@ class DABSNRead(nn.Module):
                                     key_bias, admission, seq_len, 0)
         output = rp.project(y, budget, retrieved.to(y.dtype))
         long = self._long_scan(write, plasticity, novelty)
-        return torch.addcmul(output, self.long_gain, long)
+        return ops.direct.read_output(output, long, self.long_gain)
 
     # ---- long memory -------------------------------------------------------------
     def initial_long_scan_state(self, batch_size: int, hidden_dim: int | None = None, *,
@@ -291,8 +291,8 @@ class DABSNRead(nn.Module):
                                             return_final_state=return_long_state)
         if return_long_state:
             long, final_state = result
-            return torch.addcmul(short_output, self.long_gain, long), final_state
-        return torch.addcmul(short_output, self.long_gain, result)
+            return ops.direct.read_output(short_output, long, self.long_gain), final_state
+        return ops.direct.read_output(short_output, result, self.long_gain)
 
     def forward_query_bank_stats(self, y, budget, expression, write, plasticity, *,
                                  query_stats, bank_write, bank_stats, query_start: int,
@@ -340,7 +340,7 @@ class DABSNRead(nn.Module):
         long, final_state = self._long_scan_from_state(write, plasticity, None,
                                                        initial_state=initial_long_state,
                                                        return_final_state=True)
-        return torch.addcmul(short_output, self.long_gain, long), final_state
+        return ops.direct.read_output(short_output, long, self.long_gain), final_state
 
 
 def collect_traces_enabled() -> bool:

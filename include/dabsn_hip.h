@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 5
+#define DABSN_HIP_ABI_VERSION 6
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -184,11 +184,28 @@ int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w
 int dabsn_hip_tape_stats(int dtype, int64_t B, int64_t T, int64_t H, const void* nov,
                          const void* plast, const void* energy, const void* sat, const void* expr,
                          const void* write, float* stats, hipStream_t stream);
-/* Backward of tape_stats, accumulated into the tape grads (g* += ...; NULL to skip). */
-int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* expr,
-                             const void* write, const float* stats, const float* gstats,
-                             void* gnov, void* gplast, void* genergy, void* gsat, void* gexpr,
-                             void* gwrite, hipStream_t stream);
+/* Backward of tape_stats' means: each of gnov, gplast, genergy, gsat [B,T,H] (NULL to skip)
+ * receives its mean's gradient / H, written (accumulate = 0) or added (accumulate = 1).
+ * The norms' gradients belong to the normalisation and gather backward passes. */
+int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const float* gstats,
+                             int accumulate, void* gnov, void* gplast, void* genergy, void* gsat,
+                             hipStream_t stream);
+/* Read output (src/dabsn/read.py:435-438, 821-823): out = proj + gain * long over n
+ * elements, as the reference's two tensor operations under type promotion: the product in
+ * prod_dtype (the promotion of gain and long), the sum in out_dtype (the promotion of proj
+ * and the product); no fused multiply-add. gain points at one fp32 value. */
+int dabsn_hip_read_output(int proj_dtype, int long_dtype, int prod_dtype, int out_dtype,
+                          int64_t n, const void* proj, const void* lng, const float* gain,
+                          void* out, hipStream_t stream);
+/* Its backward: gproj = gout in proj_dtype; glong = (gout in prod_dtype) * gain in
+ * prod_dtype, stored in long_dtype; ggain (one fp32 value) = the sum of (gout in prod_dtype)
+ * * long, reduced in a fixed order through `partials`, partial_count >=
+ * dabsn_hip_read_output_partials(n) floats of scratch. */
+size_t dabsn_hip_read_output_partials(int64_t n);
+int dabsn_hip_read_output_bwd(int out_dtype, int proj_dtype, int long_dtype, int prod_dtype,
+                              int64_t n, const void* gout, const void* lng, const float* gain,
+                              void* gproj, void* glong, float* ggain, float* partials,
+                              size_t partial_count, hipStream_t stream);
 /* Row normalisation q = x / max(|x|, 1e-12) given norms [B*T] (F.normalize, read.py:154). */
 int dabsn_hip_normalize_rows(int dtype, int64_t rows, int64_t H, const void* x, const float* norms,
                              void* q, hipStream_t stream);

@@ -206,6 +206,20 @@ def _ce_bwd(logits, targets, ignore_index, lse, scale):
                             float(scale.reshape(()))))
 
 
+def _read_output(proj, long, gain):
+    """The reference's expression ``out(...) + long_gain * long`` (read.py:435-438)."""
+    return proj + gain * long
+
+
+def _read_output_bwd(grad, long, gain, proj_dtype):
+    """What autograd forms for ``proj + gain * long``: the sum passes the gradient through
+    (cast to each operand's dtype), the product multiplies it by the other factor."""
+    pdt = ops._DTYPE_OF_CODE[int(proj_dtype)]
+    gp = grad.to(torch.result_type(gain, long))
+    ggain = (gp * long).sum().reshape(gain.shape).to(gain.dtype)
+    return grad.to(pdt, copy=True), (gp * gain).to(long.dtype), ggain
+
+
 def register() -> None:
     """Attach the oracle as the CPU kernel of every dabsn:: operator (idempotent)."""
     global _DONE
@@ -232,4 +246,6 @@ def register() -> None:
     ops.local_field_gather_backward.register_kernel("cpu")(_field_bwd)
     ops.ce_rows.register_kernel("cpu")(_ce)
     ops.ce_rows_backward.register_kernel("cpu")(_ce_bwd)
+    ops.read_output.register_kernel("cpu")(_read_output)
+    ops.read_output_backward.register_kernel("cpu")(_read_output_bwd)
     _DONE = True

@@ -581,3 +581,35 @@ def test_read3_decode_single_pass_shapes(cuda_device, dtype, B, H, Nb, admit):
         assert rel_err(got, want) <= 1e-5
     else:
         assert rel_fro(got, want) <= 5e-3
+
+
+@pytest.mark.parametrize("pdt,ldt,gdt", [(torch.float32, torch.float32, torch.float32),
+                                         (torch.float32, torch.bfloat16, torch.float32),
+                                         (torch.bfloat16, torch.bfloat16, torch.bfloat16),
+                                         (torch.bfloat16, torch.float32, torch.float32)])
+@pytest.mark.parametrize("shape,offset", [((2, 33, 64), 0), ((3, 7, 5), 0), ((2, 16, 64), 3)])
+def test_read_output_equals_the_two_tensor_operations(cuda_device, pdt, ldt, gdt, shape, offset):
+    """``proj + long_gain * long`` (read.py:438, 835) in one pass: bit-exact forward and
+    operand gradients against torch evaluating the same two operations; the gain's gradient
+    (a sum over every element, in another order) to 1e-5 relative."""
+    g = torch.Generator().manual_seed(5)
+    n = int(np.prod(shape))
+    base_p = torch.randn(n + offset, generator=g).to(cuda_device, pdt)
+    base_l = torch.randn(n + offset, generator=g).to(cuda_device, ldt)
+    # offset > 0 misaligns both operands (16-byte vector loads off) and keeps them 1-D views
+    proj = base_p[offset:].view(shape).clone() if offset == 0 else base_p[offset:].view(shape)
+    long = base_l[offset:].view(shape)
+    gain = torch.tensor([0.1], device=cuda_device, dtype=gdt)
+    args = [t.detach().clone().requires_grad_(True) for t in (proj, long, gain)]
+    ref = [t.detach().clone().requires_grad_(True) for t in (proj, long, gain)]
+    out = ops.read_output(*args)
+    want = ref[0] + ref[2] * ref[1]
+    assert out.dtype == want.dtype and torch.equal(out, want)
+    gout = torch.randn(shape, generator=g).to(cuda_device, out.dtype)
+    got = torch.autograd.grad(out, args, gout)
+    exp = torch.autograd.grad(want, ref, gout)
+    for name, a, b in zip(("proj", "long"), got[:2], exp[:2]):
+        assert a.dtype == b.dtype and torch.equal(a, b), f"g_{name} differs"
+    assert got[2].dtype == exp[2].dtype and got[2].shape == exp[2].shape
+    tol = 1e-5 if gdt == torch.float32 else 1e-2
+    assert abs(float(got[2]) - float(exp[2])) <= tol * max(abs(float(exp[2])), 1e-6)
