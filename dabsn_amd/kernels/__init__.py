@@ -19,6 +19,7 @@ from torch import Tensor
 
 from .. import _lib
 from . import ops
+from . import vmap_rules  # noqa: F401  (registers the operators' vmap rules)
 from .ops import (
     admitted_three_way_read_compact_flash,
     bank_gather,

@@ -1345,6 +1345,140 @@ torch.library.register_autograd("dabsn::admitted_three_way_read_compact_flash", 
                                 setup_context=_read_setup)
 
 
+# ---------------------------------------------------------------------------
+# Dense-mask three-way read (admitted.py:383-622)
+# ---------------------------------------------------------------------------
+def _dense_inputs(query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail,
+                  bank_key_bias, bank_admission, scale, allow, induct_allow, eligible,
+                  induct_eligible, short_gain, pad_gain, induct_gain, cocktail_gain):
+    """fp32 contiguous operands (the reference's compute dtype), byte masks and the [5]
+    device scalars in schema order, after the reference's shape contract."""
+    _require_cuda(query)
+    if query.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise TypeError(f"admitted_three_way_read_native: unsupported dtype {query.dtype} on "
+                        "the device (fp32, bf16 and fp16 compute in fp32)")
+    B, T, H = query.shape
+    N = bank_keys.shape[1]
+    shapes = {"bank_keys": (B, N, H), "bank_writes": (B, N, H), "next_writes": (B, N, H),
+              "cocktail": (B, T, 4), "bank_cocktail": (B, N, 4), "bank_key_bias": (B, N),
+              "bank_admission": (B, N), "allow": (B, T, N), "induct_allow": (B, T, N),
+              "eligible": (B, T), "induct_eligible": (B, T)}
+    given = dict(bank_keys=bank_keys, bank_writes=bank_writes, next_writes=next_writes,
+                 cocktail=cocktail, bank_cocktail=bank_cocktail, bank_key_bias=bank_key_bias,
+                 bank_admission=bank_admission, allow=allow, induct_allow=induct_allow,
+                 eligible=eligible, induct_eligible=induct_eligible)
+    for name, want in shapes.items():
+        if tuple(given[name].shape) != want:
+            raise ValueError(f"admitted_three_way_read_native: {name} has shape "
+                             f"{tuple(given[name].shape)}, expected {want}")
+    for name in ("allow", "induct_allow", "eligible", "induct_eligible"):
+        if given[name].dtype != torch.bool:
+            raise TypeError(f"admitted_three_way_read_native: {name} must be torch.bool")
+    floats = [x.float().contiguous() for x in (query, bank_keys, bank_writes, next_writes,
+                                               cocktail, bank_cocktail, bank_key_bias,
+                                               bank_admission)]
+    masks = [x.contiguous().view(torch.uint8) for x in (allow, induct_allow, eligible,
+                                                        induct_eligible)]
+    scal = torch.stack([_f32_scalar(x) for x in (scale, short_gain, pad_gain, induct_gain,
+                                                 cocktail_gain)])
+    return (B, T, N, H), floats, masks, scal
+
+
+@torch.library.custom_op("dabsn::admitted_three_way_read_native", mutates_args=(),
+                         device_types="cuda")
+def admitted_three_way_read_native(
+    query: Tensor, bank_keys: Tensor, bank_writes: Tensor, next_writes: Tensor, cocktail: Tensor,
+    bank_cocktail: Tensor, bank_key_bias: Tensor, bank_admission: Tensor, scale: Tensor,
+    allow: Tensor, induct_allow: Tensor, eligible: Tensor, induct_eligible: Tensor,
+    short_gain: Tensor, pad_gain: Tensor, induct_gain: Tensor, cocktail_gain: Tensor,
+) -> Tensor:
+    """The three-way admitted read with explicit dense masks (reference admitted.py:509-546;
+    math admitted.py:16-65): fp32 compute, output in the query's dtype."""
+    (B, T, N, H), f, m, scal = _dense_inputs(
+        query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+        bank_admission, scale, allow, induct_allow, eligible, induct_eligible, short_gain,
+        pad_gain, induct_gain, cocktail_gain)
+    if min(B, T, N, H) == 0:
+        return torch.zeros(query.shape, device=query.device, dtype=query.dtype)
+    lib = _lib.load()
+    out = torch.empty((B, T, H), device=query.device, dtype=torch.float32)
+    nbytes = lib.dabsn_hip_read_dense_workspace_bytes(B, T, N, H, 0)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=query.device)
+    tk = KernelTimer.begin("read_dense_fwd", out)
+    _lib.check(lib.dabsn_hip_read_dense_fwd(B, T, N, H, *[_p(x) for x in f], *[_p(x) for x in m],
+                                            _p(scal), _p(out), _p(ws), ws.numel(), _stream(out)),
+               "dense three-way read")
+    KernelTimer.end(tk)
+    return out.to(query.dtype)
+
+
+@admitted_three_way_read_native.register_fake
+def _dense_read_fake(query, *rest):
+    return torch.empty_like(query)
+
+
+@torch.library.custom_op("dabsn::_admitted_three_way_read_backward", mutates_args=(),
+                         device_types="cuda")
+def admitted_three_way_read_native_backward(
+    grad_output: Tensor, query: Tensor, bank_keys: Tensor, bank_writes: Tensor,
+    next_writes: Tensor, cocktail: Tensor, bank_cocktail: Tensor, bank_key_bias: Tensor,
+    bank_admission: Tensor, scale: Tensor, allow: Tensor, induct_allow: Tensor,
+    eligible: Tensor, induct_eligible: Tensor, short_gain: Tensor, pad_gain: Tensor,
+    induct_gain: Tensor, cocktail_gain: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+           Tensor, Tensor, Tensor]:
+    """Gradients of the 13 float inputs (reference admitted.py:383-453, math :126-236), each
+    in its input's dtype: query, bank_keys, bank_writes, next_writes, cocktail,
+    bank_cocktail, bank_key_bias, bank_admission, scale, short_gain, pad_gain, induct_gain,
+    cocktail_gain."""
+    inputs = (query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+              bank_admission)
+    gains = (scale, short_gain, pad_gain, induct_gain, cocktail_gain)
+    (B, T, N, H), f, m, scal = _dense_inputs(*inputs, scale, allow, induct_allow, eligible,
+                                             induct_eligible, short_gain, pad_gain, induct_gain,
+                                             cocktail_gain)
+    dev = query.device
+    grads = [torch.zeros(x.shape, device=dev, dtype=torch.float32) for x in inputs]
+    gscal = torch.zeros(5, device=dev, dtype=torch.float32)
+    if min(B, T, N, H) > 0:
+        lib = _lib.load()
+        go = grad_output.float().contiguous()
+        nbytes = lib.dabsn_hip_read_dense_workspace_bytes(B, T, N, H, 1)
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+        tk = KernelTimer.begin("read_dense_bwd", go)
+        _lib.check(lib.dabsn_hip_read_dense_bwd(
+            B, T, N, H, _p(go), *[_p(x) for x in f], *[_p(x) for x in m], _p(scal),
+            *[_p(g) for g in grads], _p(gscal), _p(ws), ws.numel(), _stream(go)),
+            "dense three-way read backward")
+        KernelTimer.end(tk)
+    out = [g.to(x.dtype) for g, x in zip(grads, inputs)]
+    out += [gscal[i].reshape(x.shape).to(x.dtype, copy=True) for i, x in enumerate(gains)]
+    return tuple(out)
+
+
+@admitted_three_way_read_native_backward.register_fake
+def _dense_read_backward_fake(grad_output, query, bank_keys, bank_writes, next_writes, cocktail,
+                              bank_cocktail, bank_key_bias, bank_admission, scale, allow,
+                              induct_allow, eligible, induct_eligible, short_gain, pad_gain,
+                              induct_gain, cocktail_gain):
+    return tuple(torch.empty_like(x) for x in (
+        query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+        bank_admission, scale, short_gain, pad_gain, induct_gain, cocktail_gain))
+
+
+def _dense_read_setup(ctx, inputs, output):
+    ctx.save_for_backward(*inputs)
+
+
+def _dense_read_bwd(ctx, grad_output):
+    g = admitted_three_way_read_native_backward(grad_output, *ctx.saved_tensors)
+    return (*g[:9], None, None, None, None, *g[9:])
+
+
+torch.library.register_autograd("dabsn::admitted_three_way_read_native", _dense_read_bwd,
+                                setup_context=_dense_read_setup)
+
+
 # The training path of the read: the forward keeps its workspace (tile ranges, scores and
 # row statistics) for the backward, which then skips the recompute of the score GEMM and
 # the softmax rows. The registered op above keeps the reference's one-output schema for
@@ -1513,6 +1647,8 @@ OPERATORS = (
     "dabsn::_read3_bwd_kept",
     "dabsn::read_output",
     "dabsn::_read_output_backward",
+    "dabsn::admitted_three_way_read_native",
+    "dabsn::_admitted_three_way_read_backward",
 )
 
 

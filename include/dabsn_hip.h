@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 6
+#define DABSN_HIP_ABI_VERSION 7
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -354,6 +354,42 @@ int dabsn_hip_read3_decode_noalloc(int dtype, int64_t B, int64_t T, int64_t N, i
                                    const float* bank_cocktail, const float* key_bias,
                                    const float* admission, const float* scale,
                                    const float* const* gains, void* out, hipStream_t stream);
+
+/* ---- dense-mask three-way admitted read --------------------------------------------
+ * Replace the device kernels of dabsn::admitted_three_way_read_native and
+ * dabsn::_admitted_three_way_read_backward (src/dabsn/kernels/admitted.py:383-622; the
+ * math of admitted.py:16-65 and :126-236, the CPU form three_way_read_cpu /
+ * three_way_read_bwd in src/dabsn/kernels/cpu_runtime.cpp). Every float operand is fp32
+ * and contiguous (the reference's compute dtype): query [B,T,H], bank_keys, bank_writes,
+ * next_writes [B,N,H], cocktail [B,T,4], bank_cocktail [B,N,4], bank_key_bias and
+ * bank_admission [B,N]; allow and induct_allow [B,T,N] and eligible and induct_eligible
+ * [B,T] are bytes (0 / 1, torch.bool). `scalars` is a device fp32 [5] array in the op's
+ * schema order: scale, short_gain, pad_gain, induct_gain, cocktail_gain. The forward
+ * writes out [B,T,H]; the backward takes grad_out [B,T,H] and writes every float input's
+ * gradient (g_scalars [5] in the same order). B, T, N, H > 0 (callers return empty or zero
+ * results for empty shapes). Workspace: dabsn_hip_read_dense_workspace_bytes(B, T, N, H,
+ * backward) bytes, owned by the call. */
+size_t dabsn_hip_read_dense_workspace_bytes(int64_t B, int64_t T, int64_t N, int64_t H,
+                                            int backward);
+int dabsn_hip_read_dense_fwd(int64_t B, int64_t T, int64_t N, int64_t H, const float* query,
+                             const float* bank_keys, const float* bank_writes,
+                             const float* next_writes, const float* cocktail,
+                             const float* bank_cocktail, const float* bank_key_bias,
+                             const float* bank_admission, const uint8_t* allow,
+                             const uint8_t* induct_allow, const uint8_t* eligible,
+                             const uint8_t* induct_eligible, const float* scalars, float* out,
+                             void* workspace, size_t workspace_bytes, hipStream_t stream);
+int dabsn_hip_read_dense_bwd(int64_t B, int64_t T, int64_t N, int64_t H, const float* grad_out,
+                             const float* query, const float* bank_keys, const float* bank_writes,
+                             const float* next_writes, const float* cocktail,
+                             const float* bank_cocktail, const float* bank_key_bias,
+                             const float* bank_admission, const uint8_t* allow,
+                             const uint8_t* induct_allow, const uint8_t* eligible,
+                             const uint8_t* induct_eligible, const float* scalars, float* g_query,
+                             float* g_keys, float* g_writes, float* g_next, float* g_cocktail,
+                             float* g_bank_cocktail, float* g_key_bias, float* g_admission,
+                             float* g_scalars, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
 
 /* ---- permanent associative delta scan --------------------------------------------
  * Replaces dabsn::permanent_delta_scan and its registered backward

@@ -113,14 +113,19 @@ def compact_masks(idx, valid, T, mode, query_offset=0, total_steps=None):
     return allow, induct, allow.any(-1), induct.any(-1)
 
 
-def dense_read(q, K, V, Vn, ck, cb, kb, adm, scale, allow, induct, gains, capture=None):
-    """admitted.py:16-65 output (gains = short, pad, induct, cocktail). With a ``capture``
-    dict, the permanent pathway's scores ("perm") and the scaled query-key products
-    ("compat") are stored there with their gradients retained, plus the unscaled
-    products "qk" and "cocktail_compat": the terms that the cocktail, scale and
-    cocktail-gain gradients sum."""
+def dense_read(q, K, V, Vn, ck, cb, kb, adm, scale, allow, induct, gains, capture=None,
+               eligible=None, induct_eligible=None):
+    """admitted.py:16-65 output (gains = short, pad, induct, cocktail). The row
+    eligibilities default to "any slot allowed" (what the compact read derives,
+    compact_admitted.py:176-198). With a ``capture`` dict, the permanent pathway's scores
+    ("perm") and the scaled query-key products ("compat") are stored there with their
+    gradients retained, plus the unscaled products "qk" and "cocktail_compat": the terms
+    that the cocktail, scale and cocktail-gain gradients sum."""
     sg, pg, ig, cg = gains
-    eligible, induct_eligible = allow.any(-1), induct.any(-1)
+    if eligible is None:
+        eligible = allow.any(-1)
+    if induct_eligible is None:
+        induct_eligible = induct.any(-1)
     compat = torch.bmm(q, K.transpose(1, 2)) * scale
     cocktail_compat = torch.bmm(ck, cb.transpose(1, 2)) * cg
     content = compat + kb.unsqueeze(1)

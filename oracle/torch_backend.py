@@ -13,6 +13,7 @@ import torch
 import torch.nn.functional as F
 
 import oracle
+from oracle import autograd_ref
 from dabsn_amd.kernels import ops
 
 _DONE = False
@@ -220,6 +221,56 @@ def _read_output_bwd(grad, long, gain, proj_dtype):
     return grad.to(pdt, copy=True), (gp * gain).to(long.dtype), ggain
 
 
+def _dense_floats(inputs):
+    (q, K, V, Vn, ck, cb, kb, adm, scale, allow, iallow, elig, ielig, sg, pg, ig, cg) = inputs
+    return [x.float() for x in (q, K, V, Vn, ck, cb, kb, adm, scale, sg, pg, ig, cg)], \
+        (allow, iallow, elig, ielig)
+
+
+def _dense_eval(f, masks):
+    q, K, V, Vn, ck, cb, kb, adm, scale, sg, pg, ig, cg = f
+    allow, iallow, elig, ielig = masks
+    return autograd_ref.dense_read(q, K, V, Vn, ck, cb, kb, adm, scale, allow, iallow,
+                                   (sg, pg, ig, cg), eligible=elig, induct_eligible=ielig)
+
+
+def _dense_read(*inputs):
+    """admitted.py:16-65 restated in fp32 (the reference's compute dtype)."""
+    f, masks = _dense_floats(inputs)
+    return _dense_eval(f, masks).to(inputs[0].dtype)
+
+
+def _dense_read_bwd(grad_output, *inputs):
+    """The analytic backward of admitted.py:126-236 in fp32 (autograd is not available
+    inside an operator's kernel): the 13 float inputs' gradients in their dtypes."""
+    f, (allow, iallow, elig, ielig) = _dense_floats(inputs)
+    q, K, V, Vn, ck, cb, kb, adm, scale, sg, pg, ig, cg = f
+    go = grad_output.float()
+    compat = torch.bmm(q, K.transpose(1, 2))
+    ccomp = torch.bmm(ck, cb.transpose(1, 2))
+    content = compat * scale + kb.unsqueeze(1)
+    short = content + adm.unsqueeze(1)
+    perm = content + ccomp * cg + adm.unsqueeze(1)
+    sm = autograd_ref._masked_softmax
+    ws, wp, wi = sm(short, allow, elig), sm(perm, allow, elig), sm(short, iallow, ielig)
+    G, Gn = torch.bmm(go, V.transpose(1, 2)), torch.bmm(go, Vn.transpose(1, 2))
+
+    def soft_bwd(gw, w, a, e):
+        d = w * (gw - (gw * w).sum(-1, keepdim=True))
+        return d.masked_fill(~a, 0.0).masked_fill(~e.unsqueeze(-1), 0.0)
+
+    ds, dp, di = soft_bwd(G * sg, ws, allow, elig), soft_bwd(G * pg, wp, allow, elig), \
+        soft_bwd(Gn * ig, wi, iallow, ielig)
+    D = ds + dp + di
+    grads = [torch.bmm(D, K) * scale, torch.bmm(D.transpose(1, 2), q) * scale,
+             torch.bmm(ws.transpose(1, 2), go) * sg + torch.bmm(wp.transpose(1, 2), go) * pg,
+             torch.bmm(wi.transpose(1, 2), go) * ig, torch.bmm(dp, cb) * cg,
+             torch.bmm(dp.transpose(1, 2), ck) * cg, D.sum(1), D.sum(1), (D * compat).sum(),
+             (ws * G).sum(), (wp * G).sum(), (wi * Gn).sum(), (dp * ccomp).sum()]
+    like = [x for i, x in enumerate(inputs) if i not in (9, 10, 11, 12)]
+    return tuple(g.reshape(x.shape).to(x.dtype) for g, x in zip(grads, like))
+
+
 def register() -> None:
     """Attach the oracle as the CPU kernel of every dabsn:: operator (idempotent)."""
     global _DONE
@@ -248,4 +299,6 @@ def register() -> None:
     ops.ce_rows_backward.register_kernel("cpu")(_ce_bwd)
     ops.read_output.register_kernel("cpu")(_read_output)
     ops.read_output_backward.register_kernel("cpu")(_read_output_bwd)
+    ops.admitted_three_way_read_native.register_kernel("cpu")(_dense_read)
+    ops.admitted_three_way_read_native_backward.register_kernel("cpu")(_dense_read_bwd)
     _DONE = True
