@@ -60,7 +60,7 @@ PRIMITIVES = (
               "fused three-recurrence HIP scan with fp32 checkpoints",
               "segment-replay HIP reverse scan", ("seq",),
               "oracle long-scan forward/backward parity"),
-    Primitive("linear_recurrence", "dabsn::linear_recurrence", "HIP channel scan",
+    Primitive("linear_recurrence", ops._q("linear_recurrence"), "HIP channel scan",
               "HIP analytic reverse", ("seq",), "oracle linrec parity"),
     Primitive("admitted_selection", "DABSNRead._unified_forward (read.py:185-239)",
               "HIP cummax/stable-partition kernel", "none (integer)", ("seq",),
@@ -146,6 +146,7 @@ def status() -> dict[str, object]:
             "library_loaded": lib_ok,
             "load_error": _lib.load_error(),
             "abi_version": _lib.ABI_VERSION,
+            "namespace": ops.NAMESPACE,
             "operators": list(ops.OPERATORS),
         },
         "permanent": {"hip_available": lib_ok, "hits": _PRIMITIVE_HITS["permanent_delta_scan"]},

@@ -19,6 +19,12 @@ query normalisation, admitted-slot selection, bank gather).
 
 Only a device ("cuda" = ROCm) kernel is registered: on a CPU tensor these ops raise
 instead of silently falling back.
+
+The operators live in the ``dabsn`` namespace, the reference's own, unless the process has
+already registered the reference's operators (``dabsn::core_scan_batched`` exists when
+this module is imported) or ``DABSN_AMD_OP_NAMESPACE`` names another namespace: then they
+register under ``dabsn_amd`` (or the named one), a ``PROVIDER_RESOLUTION`` event records
+it, and the two packages share the process. ``NAMESPACE`` holds the one in use.
 """
 
 from __future__ import annotations
@@ -32,6 +38,26 @@ import torch
 from torch import Tensor
 
 from .. import _lib, events
+
+
+def _choose_namespace() -> str:
+    named = os.environ.get("DABSN_AMD_OP_NAMESPACE")
+    if named:
+        return named
+    try:
+        taken = hasattr(torch.ops.dabsn, "core_scan_batched")
+    except Exception:  # noqa: BLE001 - an unknown namespace reads as free
+        taken = False
+    return "dabsn_amd" if taken else "dabsn"
+
+
+NAMESPACE = _choose_namespace()
+
+
+def _q(name: str) -> str:
+    """Qualified operator name in this module's namespace."""
+    return f"{NAMESPACE}::{name}"
+
 
 _DTYPES = {torch.float32: 0, torch.bfloat16: 1}
 
@@ -269,7 +295,7 @@ def core_launch_check(code: int, B: int, T: int, H: int, backward: bool) -> int:
     return n
 
 
-@torch.library.custom_op("dabsn::core_scan_batched", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("core_scan_batched"), mutates_args=(), device_types="cuda")
 def core_scan_batched(
     Wx: Tensor, Wgx: Tensor, Ug: Tensor, A: Tensor, beta: Tensor, log_kappa: Tensor,
     logit_recover: Tensor, k_s: Tensor, k_y: Tensor, k_b: Tensor, k_n: Tensor, k_bias: Tensor,
@@ -332,7 +358,7 @@ def _core_scan_batched_fake(*inputs: Tensor) -> CoreScanOutputs:
             ic.new_empty(ic.shape))
 
 
-@torch.library.custom_op("dabsn::_core_scan_batched_backward", mutates_args=(),
+@torch.library.custom_op(_q("_core_scan_batched_backward"), mutates_args=(),
                          device_types="cuda")
 def core_scan_batched_backward(
     Ug: Tensor, A: Tensor, vecs: list[Tensor], logit_alpha: Tensor, log_lambda: Tensor,
@@ -435,14 +461,14 @@ def _core_backward(ctx, *grad_outputs):
     return tuple(out)
 
 
-torch.library.register_autograd("dabsn::core_scan_batched", _core_backward,
+torch.library.register_autograd(_q("core_scan_batched"), _core_backward,
                                 setup_context=_core_setup)
 
 
 # ---------------------------------------------------------------------------
 # Linear recurrence (drop-in for dabsn::linear_recurrence)
 # ---------------------------------------------------------------------------
-@torch.library.custom_op("dabsn::linear_recurrence", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("linear_recurrence"), mutates_args=(), device_types="cuda")
 def linear_recurrence(a: Tensor, g: Tensor, y_init: Tensor) -> Tensor:
     """y_t = a_t y_{t-1} + g_t (reference long.py:392-396; CPU cpu_runtime.cpp:92-108)."""
     _require_cuda(a)
@@ -465,7 +491,7 @@ def _linear_recurrence_fake(a, g, y_init):
     return torch.empty_like(a)
 
 
-@torch.library.custom_op("dabsn::_linrec_backward", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("_linrec_backward"), mutates_args=(), device_types="cuda")
 def linrec_backward(a: Tensor, g: Tensor, y_init: Tensor, grad_out: Tensor) -> list[Tensor]:
     """Analytic reverse of the linear recurrence (reference long.py:58-98, 410-417)."""
     _require_cuda(a)
@@ -497,7 +523,7 @@ def _linrec_bwd(ctx, grad_out):
     return da, dg, dy
 
 
-torch.library.register_autograd("dabsn::linear_recurrence", _linrec_bwd, setup_context=_linrec_setup)
+torch.library.register_autograd(_q("linear_recurrence"), _linrec_bwd, setup_context=_linrec_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -509,7 +535,7 @@ def _permanent_shapes(k: Tensor, v: Tensor, beta: Tensor) -> tuple[int, int, int
     return tuple(int(x) for x in k.shape)
 
 
-@torch.library.custom_op("dabsn::permanent_delta_scan", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("permanent_delta_scan"), mutates_args=(), device_types="cuda")
 def permanent_delta_scan(k: Tensor, v: Tensor, beta: Tensor) -> Tensor:
     """out_t = S k_t, S += beta_t (v_t - out_t) k_t^T from S = 0 (reference permanent.py:39-51,
     op 384-397; CPU cpu_runtime.cpp:1075-1109). fp32 state and arithmetic; the output takes
@@ -532,7 +558,7 @@ def _permanent_delta_scan_fake(k, v, beta):
     return torch.empty_like(v)
 
 
-@torch.library.custom_op("dabsn::_permanent_delta_scan_backward", mutates_args=(),
+@torch.library.custom_op(_q("_permanent_delta_scan_backward"), mutates_args=(),
                          device_types="cuda")
 def permanent_delta_scan_backward(k: Tensor, v: Tensor, beta: Tensor,
                                   grad_out: Tensor) -> list[Tensor]:
@@ -569,7 +595,7 @@ def _permanent_bwd(ctx, grad_out):
     return dk, dv, db
 
 
-torch.library.register_autograd("dabsn::permanent_delta_scan", _permanent_bwd,
+torch.library.register_autograd(_q("permanent_delta_scan"), _permanent_bwd,
                                 setup_context=_permanent_setup)
 
 
@@ -596,7 +622,7 @@ def _field_dtype(t: Tensor) -> torch.dtype:
     raise TypeError(f"local field gather on the HIP path supports fp32/bf16/fp16, not {t.dtype}")
 
 
-@torch.library.custom_op("dabsn::local_field_gather", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("local_field_gather"), mutates_args=(), device_types="cuda")
 def local_field_gather(inputs: Tensor, patch: Tensor) -> Tensor:
     """inputs[:, patch] -> [B, P, K, D] (reference local_field.py:208-214; CPU
     cpu_runtime.cpp:1191-1211)."""
@@ -624,7 +650,7 @@ def _local_field_gather_fake(inputs, patch):
     return inputs.new_empty((B, P, K, D))
 
 
-@torch.library.custom_op("dabsn::_local_field_gather_backward", mutates_args=(),
+@torch.library.custom_op(_q("_local_field_gather_backward"), mutates_args=(),
                          device_types="cuda")
 def local_field_gather_backward(grad_out: Tensor, patch: Tensor, cells: int) -> Tensor:
     """Scatter-add of grad_out [B, P, K, D] into [B, cells, D], each source cell summed over
@@ -666,7 +692,7 @@ def _field_bwd(ctx, grad_out):
     return local_field_gather_backward(grad_out.contiguous(), patch, ctx.cells), None
 
 
-torch.library.register_autograd("dabsn::local_field_gather", _field_bwd, setup_context=_field_setup)
+torch.library.register_autograd(_q("local_field_gather"), _field_bwd, setup_context=_field_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -718,7 +744,7 @@ def _ce_logits(logits: Tensor) -> Tensor:
     return logits if logits.stride(1) == 1 else logits.contiguous()
 
 
-@torch.library.custom_op("dabsn::_ce_rows", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("_ce_rows"), mutates_args=(), device_types="cuda")
 def ce_rows(logits: Tensor, targets: Tensor, ignore_index: int) -> tuple[Tensor, Tensor]:
     """Per row of logits [rows, V]: (logsumexp, lse - logit[target] or 0 where ignored), fp32
     (reference loss.py:83-93 for one chunk)."""
@@ -746,7 +772,7 @@ def _ce_rows_fake(logits, targets, ignore_index):
             logits.new_empty((rows,), dtype=torch.float32))
 
 
-@torch.library.custom_op("dabsn::_ce_rows_backward", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("_ce_rows_backward"), mutates_args=(), device_types="cuda")
 def ce_rows_backward(logits: Tensor, targets: Tensor, ignore_index: int, lse: Tensor,
                      scale: Tensor) -> Tensor:
     """(softmax(logits) - onehot(target)) * scale, fp32 [rows, V], zero rows where ignored
@@ -782,7 +808,7 @@ def _read_output_dtypes(proj: Tensor, long: Tensor, gain: Tensor) -> tuple[torch
     return prod, torch.promote_types(proj.dtype, prod)
 
 
-@torch.library.custom_op("dabsn::read_output", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("read_output"), mutates_args=(), device_types="cuda")
 def read_output(proj: Tensor, long: Tensor, gain: Tensor) -> Tensor:
     """``proj + gain * long`` as the reference evaluates ``out(...) + long_gain * long``: two
     tensor operations under type promotion (the product in the dtype of gain and long, the
@@ -809,7 +835,7 @@ def _read_output_fake(proj, long, gain):
 _DTYPE_OF_CODE = {0: torch.float32, 1: torch.bfloat16}
 
 
-@torch.library.custom_op("dabsn::_read_output_backward", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("_read_output_backward"), mutates_args=(), device_types="cuda")
 def read_output_backward(grad: Tensor, long: Tensor, gain: Tensor,
                          proj_dtype: int) -> tuple[Tensor, Tensor, Tensor]:
     """(g_proj, g_long, g_gain) of ``read_output`` (``proj_dtype`` = the dtype code of proj):
@@ -852,14 +878,14 @@ def _read_output_bwd(ctx, grad):
     return read_output_backward(grad, long, gain, ctx.proj_dtype)
 
 
-torch.library.register_autograd("dabsn::read_output", _read_output_bwd,
+torch.library.register_autograd(_q("read_output"), _read_output_bwd,
                                 setup_context=_read_output_setup)
 
 
 # ---------------------------------------------------------------------------
 # Fused recurrent long-memory scan
 # ---------------------------------------------------------------------------
-@torch.library.custom_op("dabsn::long_scan_fused", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("long_scan_fused"), mutates_args=(), device_types="cuda")
 def long_scan_fused(
     write: Tensor, plasticity: Tensor, logit_expect_retain: Tensor,
     logit_retention_decay: Tensor, logit_retain: Tensor, logit_retention_strength: Tensor,
@@ -898,7 +924,7 @@ def _long_scan_fused_fake(write, plasticity, l1, l2, l3, l4, long0, expected0, r
     return torch.empty_like(write), f(B, H), f(B, H), f(B, H), f(3, B, T, H)
 
 
-@torch.library.custom_op("dabsn::_long_scan_fused_backward", mutates_args=(),
+@torch.library.custom_op(_q("_long_scan_fused_backward"), mutates_args=(),
                          device_types="cuda")
 def long_scan_fused_backward(
     write: Tensor, plasticity: Tensor, logits: list[Tensor], states: Tensor, grad_long: Tensor,
@@ -961,13 +987,13 @@ def _long_bwd(ctx, g_long, g_lf, g_ef, g_rf, _g_states):
     return tuple(g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(grads, ctx.meta))
 
 
-torch.library.register_autograd("dabsn::long_scan_fused", _long_bwd, setup_context=_long_setup)
+torch.library.register_autograd(_q("long_scan_fused"), _long_bwd, setup_context=_long_setup)
 
 
 # ---------------------------------------------------------------------------
 # Read glue
 # ---------------------------------------------------------------------------
-@torch.library.custom_op("dabsn::read_tape_stats", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("read_tape_stats"), mutates_args=(), device_types="cuda")
 def read_tape_stats(novelty: Tensor, plasticity: Tensor, energy: Tensor, saturation: Tensor,
                     expression: Tensor, write: Tensor) -> Tensor:
     """Per-position (mean e, mean c, mean n, mean p, |expression|, |write|), fp32 [B,T,6]
@@ -990,7 +1016,7 @@ def _read_tape_stats_fake(novelty, plasticity, energy, saturation, expression, w
     return novelty.new_empty((B, T, 6), dtype=torch.float32)
 
 
-@torch.library.custom_op("dabsn::_read_tape_stats_backward", mutates_args=(),
+@torch.library.custom_op(_q("_read_tape_stats_backward"), mutates_args=(),
                          device_types="cuda")
 def read_tape_stats_backward(gstats: Tensor, like: Tensor) -> list[Tensor]:
     """Broadcast mean gradients back to the four averaged tapes [g_n, g_p, g_e, g_c]."""
@@ -1022,10 +1048,10 @@ def _stats_bwd(ctx, gstats):
     return gn.to(d[0]), gp.to(d[1]), ge.to(d[2]), gc.to(d[3]), None, None
 
 
-torch.library.register_autograd("dabsn::read_tape_stats", _stats_bwd, setup_context=_stats_setup)
+torch.library.register_autograd(_q("read_tape_stats"), _stats_bwd, setup_context=_stats_setup)
 
 
-@torch.library.custom_op("dabsn::normalize_rows", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("normalize_rows"), mutates_args=(), device_types="cuda")
 def normalize_rows(x: Tensor, norms: Tensor) -> Tensor:
     """x / max(norms, 1e-12) along the last dim, norms = |x| rows (F.normalize, read.py:154)."""
     lib = _lib.load()
@@ -1044,7 +1070,7 @@ def _normalize_rows_fake(x, norms):
     return torch.empty_like(x)
 
 
-@torch.library.custom_op("dabsn::_normalize_rows_backward", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("_normalize_rows_backward"), mutates_args=(), device_types="cuda")
 def normalize_rows_backward(q: Tensor, norms: Tensor, gq: Tensor) -> Tensor:
     lib = _lib.load()
     H = q.shape[-1]
@@ -1073,10 +1099,10 @@ def _norm_bwd(ctx, gq):
     return normalize_rows_backward(q, norms, gq), None
 
 
-torch.library.register_autograd("dabsn::normalize_rows", _norm_bwd, setup_context=_norm_setup)
+torch.library.register_autograd(_q("normalize_rows"), _norm_bwd, setup_context=_norm_setup)
 
 
-@torch.library.custom_op("dabsn::bank_select", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("bank_select"), mutates_args=(), device_types="cuda")
 def bank_select(admission: Tensor, window: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     """Admitted-slot selection (read.py:185-239): (order [B,T] int64, counts [B] int64,
     rank [B,T] int32). Bit-exact integer work given the admission values. The floor
@@ -1105,7 +1131,7 @@ def _bank_select_fake(admission, window):
             admission.new_empty((B, T), dtype=torch.int32))
 
 
-@torch.library.custom_op("dabsn::bank_gather", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("bank_gather"), mutates_args=(), device_types="cuda")
 def bank_gather(write: Tensor, norm_w: Tensor, idx: Tensor, next_idx: Tensor,
                 rank: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     """(normalize(write[idx]), write[idx], write[next_idx]) as in read.py:241-256, 298-303."""
@@ -1129,7 +1155,7 @@ def _bank_gather_fake(write, norm_w, idx, next_idx, rank):
     return tuple(write.new_empty((B, N, H)) for _ in range(3))
 
 
-@torch.library.custom_op("dabsn::_bank_gather_backward", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("_bank_gather_backward"), mutates_args=(), device_types="cuda")
 def bank_gather_backward(write: Tensor, norm_w: Tensor, rank: Tensor, K: Tensor, gK: Tensor,
                          gV: Tensor, gVn: Tensor) -> Tensor:
     """Deterministic inverse gather of the bank gradients onto the write tape."""
@@ -1165,7 +1191,7 @@ def _gather_bwd(ctx, gK, gV, gVn):
     return gw, None, None, None, None
 
 
-torch.library.register_autograd("dabsn::bank_gather", _gather_bwd, setup_context=_gather_setup)
+torch.library.register_autograd(_q("bank_gather"), _gather_bwd, setup_context=_gather_setup)
 
 
 # ---------------------------------------------------------------------------
@@ -1187,7 +1213,7 @@ def _read_common(query, bank_keys, bank_writes, next_writes, cocktail, bank_cock
     return dt, q, K, V, Vn, ck, cb, kb, adm, sc, g, idx, valid
 
 
-@torch.library.custom_op("dabsn::admitted_three_way_read_compact_flash", mutates_args=(),
+@torch.library.custom_op(_q("admitted_three_way_read_compact_flash"), mutates_args=(),
                          device_types="cuda")
 def admitted_three_way_read_compact_flash(
     query: Tensor, bank_keys: Tensor, bank_writes: Tensor, next_writes: Tensor, cocktail: Tensor,
@@ -1273,7 +1299,7 @@ CompactGradients = tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
                          Tensor, Tensor, Tensor, Tensor]
 
 
-@torch.library.custom_op("dabsn::_admitted_three_way_read_compact_flash_backward",
+@torch.library.custom_op(_q("_admitted_three_way_read_compact_flash_backward"),
                          mutates_args=(), device_types="cuda")
 def admitted_three_way_read_compact_flash_backward(
     grad_output: Tensor, query: Tensor, bank_keys: Tensor, bank_writes: Tensor,
@@ -1341,7 +1367,7 @@ def _read_bwd(ctx, grad_output):
     return (*g[:9], None, None, None, *g[9:])
 
 
-torch.library.register_autograd("dabsn::admitted_three_way_read_compact_flash", _read_bwd,
+torch.library.register_autograd(_q("admitted_three_way_read_compact_flash"), _read_bwd,
                                 setup_context=_read_setup)
 
 
@@ -1384,7 +1410,7 @@ def _dense_inputs(query, bank_keys, bank_writes, next_writes, cocktail, bank_coc
     return (B, T, N, H), floats, masks, scal
 
 
-@torch.library.custom_op("dabsn::admitted_three_way_read_native", mutates_args=(),
+@torch.library.custom_op(_q("admitted_three_way_read_native"), mutates_args=(),
                          device_types="cuda")
 def admitted_three_way_read_native(
     query: Tensor, bank_keys: Tensor, bank_writes: Tensor, next_writes: Tensor, cocktail: Tensor,
@@ -1417,7 +1443,7 @@ def _dense_read_fake(query, *rest):
     return torch.empty_like(query)
 
 
-@torch.library.custom_op("dabsn::_admitted_three_way_read_backward", mutates_args=(),
+@torch.library.custom_op(_q("_admitted_three_way_read_backward"), mutates_args=(),
                          device_types="cuda")
 def admitted_three_way_read_native_backward(
     grad_output: Tensor, query: Tensor, bank_keys: Tensor, bank_writes: Tensor,
@@ -1475,7 +1501,7 @@ def _dense_read_bwd(ctx, grad_output):
     return (*g[:9], None, None, None, None, *g[9:])
 
 
-torch.library.register_autograd("dabsn::admitted_three_way_read_native", _dense_read_bwd,
+torch.library.register_autograd(_q("admitted_three_way_read_native"), _dense_read_bwd,
                                 setup_context=_dense_read_setup)
 
 
@@ -1483,7 +1509,7 @@ torch.library.register_autograd("dabsn::admitted_three_way_read_native", _dense_
 # row statistics) for the backward, which then skips the recompute of the score GEMM and
 # the softmax rows. The registered op above keeps the reference's one-output schema for
 # external callers; the read module uses ``admitted_three_way_read_train``.
-@torch.library.custom_op("dabsn::_read3_fwd_keep", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("_read3_fwd_keep"), mutates_args=(), device_types="cuda")
 def read3_fwd_keep(
     query: Tensor, bank_keys: Tensor, bank_writes: Tensor, next_writes: Tensor, cocktail: Tensor,
     bank_cocktail: Tensor, bank_key_bias: Tensor, bank_admission: Tensor, scale: Tensor,
@@ -1524,7 +1550,7 @@ def _read3_fwd_keep_fake(query, *rest):
     return torch.empty_like(query), query.new_empty((256,), dtype=torch.uint8)
 
 
-@torch.library.custom_op("dabsn::_read3_bwd_kept", mutates_args=(), device_types="cuda")
+@torch.library.custom_op(_q("_read3_bwd_kept"), mutates_args=(), device_types="cuda")
 def read3_bwd_kept(
     grad_output: Tensor, query: Tensor, bank_keys: Tensor, bank_writes: Tensor,
     next_writes: Tensor, cocktail: Tensor, bank_cocktail: Tensor, bank_key_bias: Tensor,
@@ -1622,34 +1648,42 @@ def kernel_symbol(kernel: str, B: int, H: int, dtype: torch.dtype = torch.bfloat
 
 
 OPERATORS = (
-    "dabsn::core_scan_batched",
-    "dabsn::_core_scan_batched_backward",
-    "dabsn::linear_recurrence",
-    "dabsn::_linrec_backward",
-    "dabsn::permanent_delta_scan",
-    "dabsn::_permanent_delta_scan_backward",
-    "dabsn::local_field_gather",
-    "dabsn::_local_field_gather_backward",
-    "dabsn::_ce_rows",
-    "dabsn::_ce_rows_backward",
-    "dabsn::long_scan_fused",
-    "dabsn::_long_scan_fused_backward",
-    "dabsn::read_tape_stats",
-    "dabsn::_read_tape_stats_backward",
-    "dabsn::normalize_rows",
-    "dabsn::_normalize_rows_backward",
-    "dabsn::bank_select",
-    "dabsn::bank_gather",
-    "dabsn::_bank_gather_backward",
-    "dabsn::admitted_three_way_read_compact_flash",
-    "dabsn::_admitted_three_way_read_compact_flash_backward",
-    "dabsn::_read3_fwd_keep",
-    "dabsn::_read3_bwd_kept",
-    "dabsn::read_output",
-    "dabsn::_read_output_backward",
-    "dabsn::admitted_three_way_read_native",
-    "dabsn::_admitted_three_way_read_backward",
+    _q("core_scan_batched"),
+    _q("_core_scan_batched_backward"),
+    _q("linear_recurrence"),
+    _q("_linrec_backward"),
+    _q("permanent_delta_scan"),
+    _q("_permanent_delta_scan_backward"),
+    _q("local_field_gather"),
+    _q("_local_field_gather_backward"),
+    _q("_ce_rows"),
+    _q("_ce_rows_backward"),
+    _q("long_scan_fused"),
+    _q("_long_scan_fused_backward"),
+    _q("read_tape_stats"),
+    _q("_read_tape_stats_backward"),
+    _q("normalize_rows"),
+    _q("_normalize_rows_backward"),
+    _q("bank_select"),
+    _q("bank_gather"),
+    _q("_bank_gather_backward"),
+    _q("admitted_three_way_read_compact_flash"),
+    _q("_admitted_three_way_read_compact_flash_backward"),
+    _q("_read3_fwd_keep"),
+    _q("_read3_bwd_kept"),
+    _q("read_output"),
+    _q("_read_output_backward"),
+    _q("admitted_three_way_read_native"),
+    _q("_admitted_three_way_read_backward"),
 )
+
+
+if NAMESPACE != "dabsn":
+    events.emit_event(events.EventCode.PROVIDER_RESOLUTION, component_id="dabsn_amd.kernels.ops",
+                      namespace=NAMESPACE,
+                      reason="DABSN_AMD_OP_NAMESPACE is set" if os.environ.get(
+                          "DABSN_AMD_OP_NAMESPACE") else
+                      "the reference's dabsn:: operators are registered in this process")
 
 
 def _direct(op):

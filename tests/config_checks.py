@@ -264,7 +264,7 @@ def cancelling_bound(g64, terms, tol):
 
 
 def check_long_rows(read, write, plasticity, long, rows, tol):
-    coef = np.array([float(torch.sigmoid(p)) for p in (
+    coef = np.array([float(torch.sigmoid(p.detach())) for p in (
         read.logit_expect_retain, read.logit_retention_decay, read.logit_retain,
         read.logit_retention_strength)], np.float32)
     H = write.shape[-1]

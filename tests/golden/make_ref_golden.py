@@ -33,6 +33,12 @@ Fixtures (reference file:line of the function evaluated):
   ``memory.save`` after ``ingest`` of a prompt into a small ``DABSNSequenceLM``
   (memory.py:389-470), the LM's state dict, the prompt, and the logits of the next
   ``forward_with_memory`` token.
+* ``op_schemas.json`` -- the dispatcher schema of every registered ``dabsn::`` operator
+  this build replaces (kernels/batched_runtime.py:1507, compact_flash.py:71 and 182,
+  long.py:392 and 410, permanent.py:384, local_field.py:208, admitted.py:384 and 509), as
+  ``torch`` prints it: the interface a backend's kernels must accept.
+
+``python tests/golden/make_ref_golden.py NAME ...`` writes only the named fixtures.
 """
 
 from __future__ import annotations
@@ -378,6 +384,35 @@ def memory_lm() -> None:
     print(f"  fingerprint: {mem.fingerprint}")
 
 
+SCHEMA_OPS = ("core_scan_batched", "admitted_three_way_read_compact_flash",
+              "_admitted_three_way_read_compact_flash_backward", "linear_recurrence",
+              "_linrec_backward", "permanent_delta_scan", "local_field_gather",
+              "admitted_three_way_read_native", "_admitted_three_way_read_backward")
+
+
+def op_schemas() -> None:
+    import json
+
+    import torch
+
+    import dabsn.kernels.admitted  # noqa: F401  (each import registers its operators)
+    import dabsn.kernels.batched_runtime  # noqa: F401
+    import dabsn.kernels.compact_flash  # noqa: F401
+    import dabsn.kernels.local_field  # noqa: F401
+    import dabsn.kernels.long  # noqa: F401
+    import dabsn.kernels.permanent  # noqa: F401
+
+    schemas = {name: str(getattr(torch.ops.dabsn, name).default._schema) for name in SCHEMA_OPS}
+    OUT.mkdir(parents=True, exist_ok=True)
+    (OUT / "op_schemas.json").write_text(json.dumps(schemas, indent=1) + "\n")
+    print(f"wrote op_schemas.json ({len(schemas)} operators)")
+
+
+FIXTURES = {"core_op": lambda: core_op("fp32"), "core_loop": core_loop, "read_seq": read_seq,
+            "read_seq_bf16": read_seq_bf16, "query_bank": query_bank, "model_c1": model_c1,
+            "memory_lm": memory_lm, "op_schemas": op_schemas}
+
+
 def main() -> None:
     if not REF_SRC.exists():
         raise SystemExit(f"reference source not found at {REF_SRC}")
@@ -386,13 +421,8 @@ def main() -> None:
     import torch
 
     torch.set_num_threads(min(8, os.cpu_count() or 1))
-    core_op("fp32")
-    core_loop()
-    read_seq()
-    read_seq_bf16()
-    query_bank()
-    model_c1()
-    memory_lm()
+    for name in sys.argv[1:] or list(FIXTURES):
+        FIXTURES[name]()
 
 
 if __name__ == "__main__":
