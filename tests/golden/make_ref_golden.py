@@ -15,6 +15,10 @@ Fixtures (reference file:line of the function evaluated):
   forward (kernels/batched_runtime.py:1507-1560) and its registered autograd, i.e. the
   Python reverse recurrence ``DABSNCoreScanBatched.backward`` (batched_runtime.py:1333-1504),
   from a random carried state with every per-unit term active.
+* ``core_op_bf16`` -- the same op with bf16 activations and recurrent weights (the
+  reference's own bf16 path, tests/test_batched_runtime.py:83-162) and, on the same
+  values, in fp32: outputs and gradients of both, so the reference's bf16-vs-fp32 gap is
+  known per gradient.
 * ``core_loop_fp64`` -- ``DABSNCore._reference_forward_from_state`` (core.py:111-246), the
   per-step torch loop, differentiated by autograd.
 * ``read_seq_fp32`` -- ``DABSNRead.forward`` in seq geometry (read.py:139-438) on a
@@ -124,6 +128,44 @@ def core_op(dtype_name: str) -> None:
     arrays.update({f"gout{i}": _np(g) for i, g in enumerate(grads_out) if i != 7})
     arrays.update({f"grad{i}": _np(g) for i, g in enumerate(grads) if g is not None})
     _save(f"core_op_{dtype_name}", arrays)
+
+
+def core_op_bf16() -> None:
+    """The registered core op with the reference's bf16 activations (Wx, Wgx, Ug, A in
+    bf16, as tests/test_batched_runtime.py:83-113 drives it; fp32 state and vectors), and
+    the same op on the same values in fp32: how far the reference's own bf16 path lands
+    from fp32."""
+    import torch
+    from dabsn.core import DABSNCore
+
+    os.environ["DABSN_BATCHED_STEP_COMPILE"] = "0"
+    torch.manual_seed(0)
+    gen = torch.Generator().manual_seed(13)
+    B, T, H = 4, 48, 32
+    core = DABSNCore(input_dim=5, hidden_dim=H)
+    _perturbed_core(core, gen)
+    Wx, Wgx, b0, e0, c0, vecs, scal = _core_op_inputs(core, B, T, gen, torch.float32)
+    bf = torch.bfloat16
+    base = [Wx.to(bf), Wgx.to(bf), core.Ug.weight.to(bf), core.A.weight.to(bf), *vecs, *scal,
+            b0, e0, c0]
+    leaves16 = [x.detach().clone().requires_grad_(True) for x in base]
+    leaves32 = [x.detach().float().clone().requires_grad_(True) for x in base]
+    outs16 = torch.ops.dabsn.core_scan_batched(*leaves16)
+    outs32 = torch.ops.dabsn.core_scan_batched(*leaves32)
+    gout = [torch.randn(o.shape, generator=gen) for o in outs32]
+
+    def loss(outs):
+        return sum((o.float() * g).sum() for i, (o, g) in enumerate(zip(outs, gout)) if i != 7)
+
+    g16 = torch.autograd.grad(loss(outs16), leaves16, allow_unused=True)
+    g32 = torch.autograd.grad(loss(outs32), leaves32, allow_unused=True)
+    arrays = {f"in{i}": _np(x) for i, x in enumerate(leaves32)}
+    arrays.update({f"out16_{i}": _np(o) for i, o in enumerate(outs16)})
+    arrays.update({f"out32_{i}": _np(o) for i, o in enumerate(outs32)})
+    arrays.update({f"gout{i}": _np(g) for i, g in enumerate(gout) if i != 7})
+    arrays.update({f"grad16_{i}": _np(g) for i, g in enumerate(g16) if g is not None})
+    arrays.update({f"grad32_{i}": _np(g) for i, g in enumerate(g32) if g is not None})
+    _save("core_op_bf16", arrays)
 
 
 def core_loop() -> None:
@@ -408,7 +450,8 @@ def op_schemas() -> None:
     print(f"wrote op_schemas.json ({len(schemas)} operators)")
 
 
-FIXTURES = {"core_op": lambda: core_op("fp32"), "core_loop": core_loop, "read_seq": read_seq,
+FIXTURES = {"core_op": lambda: core_op("fp32"), "core_op_bf16": core_op_bf16,
+            "core_loop": core_loop, "read_seq": read_seq,
             "read_seq_bf16": read_seq_bf16, "query_bank": query_bank, "model_c1": model_c1,
             "memory_lm": memory_lm, "op_schemas": op_schemas}
 

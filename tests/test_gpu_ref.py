@@ -53,6 +53,47 @@ def test_core_op_vs_reference_fixture_gpu(cuda_device):
             assert g is not None and rel_err(g.cpu(), z[key]) <= 1e-5, f"grad {i}"
 
 
+CORE_GRAD_NAMES = (["Wx", "Wgx", "Ug", "A"] + [f"vec{i}" for i in range(16)]
+                   + ["logit_alpha", "log_lambda", "logit_c_suppress", "b0", "e0", "c0"])
+
+
+def _fro(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def test_core_bf16_gap_against_the_references_own_bf16_path(cuda_device):
+    """bf16 activations and recurrent weights, fp32 state (the reference's bf16 path,
+    tests/test_batched_runtime.py:83-162). Per gradient, the HIP bf16 result's Frobenius
+    distance from the reference's fp32 result must stay within 2e-2 or, where the
+    reference's own bf16 result is farther than 2e-2 / 1.5 from its fp32 one, within
+    1.5x the reference's own gap (both bf16 paths round the same tapes and GEMM outputs,
+    in different summation orders). Forward outputs: within 2e-2 normwise of fp32."""
+    z = _load("core_op_bf16")
+    leaves = []
+    for i in range(26):
+        t = torch.from_numpy(z[f"in{i}"]).to(cuda_device)
+        leaves.append((t.to(torch.bfloat16) if i < 4 else t).requires_grad_(True))
+    outs = ops.core_scan_batched(*leaves)
+    for i in range(11):
+        assert rel_err(outs[i].detach().float().cpu(), z[f"out32_{i}"]) <= 2e-2, f"output {i}"
+    loss = sum((o.float() * torch.from_numpy(z[f"gout{i}"]).to(cuda_device)).sum()
+               for i, o in enumerate(outs) if i != 7)
+    grads = torch.autograd.grad(loss, leaves, allow_unused=True)
+    rows = []
+    for i, g in enumerate(grads):
+        if f"grad32_{i}" not in z:
+            continue
+        want = z[f"grad32_{i}"]
+        e_hip = _fro(g.detach().float().cpu().numpy(), want)
+        e_ref = _fro(z[f"grad16_{i}"], want)
+        rows.append((CORE_GRAD_NAMES[i], e_hip, e_ref))
+    print("\n".join(f"{n}: hip bf16 {a:.2e}, reference bf16 {b:.2e}" for n, a, b in rows))
+    for n, e_hip, e_ref in rows:
+        assert e_hip <= max(2e-2, 1.5 * e_ref), f"g_{n}: {e_hip:.3e} (reference {e_ref:.3e})"
+
+
 def test_read_seq_vs_reference_fixture_gpu(cuda_device):
     z = _load("read_seq_fp32")
     H = z["y"].shape[-1]
