@@ -42,7 +42,11 @@ def parse():
     p.add_argument("--hidden", type=int, default=4096)
     p.add_argument("--vocab", type=int, default=32000)
     p.add_argument("--chunk", type=int, default=1024)
-    p.add_argument("--cpu-seq", type=int, default=128, help="T of the bounded CPU sample")
+    p.add_argument("--cpu-seq", type=int, default=64, help="T of the bounded CPU sample")
+    p.add_argument("--no-proj", action="store_true",
+                   help="skip the separate timing of the input projections (profiling runs)")
+    p.add_argument("--cpu-trials", type=int, default=5,
+                   help="timed CPU steps after one untimed warm-up step")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--workload", choices=("train", "decode", "primitives"), default="train",
                    help="train: the config-4 headline step (default); decode: config-5 streaming "
@@ -157,6 +161,47 @@ def measured_traffic(kernel: str, args, chunk: int):
     return int(entry["traffic_bytes"]), "profiles/core_scan_config4_pmc.md"
 
 
+def time_projections(args, model, device, dtype, reps: int = 5):
+    """The block's input projections Wx = W x and Wgx = Wg x + b (core.py:281-282), which
+    the scan+read step takes as resident inputs, timed on their own: forward (two GEMMs)
+    and backward (input gradient as two accumulating GEMMs, two weight-gradient GEMMs) on
+    hipBLASLt through torch, bf16, [B*T, hidden] x [hidden, state]."""
+    F = torch.nn.functional
+    rows, D, H = args.batch * args.seq, args.hidden, args.state
+    g = torch.Generator(device=device).manual_seed(3)
+    x = torch.randn(rows, D, device=device, dtype=dtype, generator=g)
+    gy = torch.randn(rows, H, device=device, dtype=dtype, generator=g)
+    gz = torch.randn(rows, H, device=device, dtype=dtype, generator=g)
+    W = model.core.W.weight.detach().to(dtype)
+    Wg = model.core.Wg.weight.detach().to(dtype)
+    bg = model.core.Wg.bias.detach().to(dtype)
+
+    def fwd():
+        return F.linear(x, W), F.linear(x, Wg, bg)
+
+    def bwd():
+        gx = torch.addmm(gy @ W, gz, Wg)
+        return gx, gy.t() @ x, gz.t() @ x
+
+    out = {}
+    for name, fn, gemms in (("forward", fwd, 2), ("backward", bwd, 4)):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / reps
+        tflops = gemms * 2.0 * rows * D * H / (ms / 1e3) / 1e12
+        out[name] = {"ms": round(ms, 3), "tflops": round(tflops, 1),
+                     "frac_bf16_peak": round(tflops / 2500.0, 4)}
+    out["note"] = ("not part of value: the scan+read step starts from resident Wx, Wgx; "
+                   f"rows {rows}, hidden {D}, state {H}, bf16, hipBLASLt via torch")
+    return out
+
+
 def cpu_baseline(args):
     """The oracle (C restatement of the reference CPU backend, fp32, OpenMP over batch)
     running the same scan+read step on a bounded sample: config-4 widths, T=cpu_seq."""
@@ -170,20 +215,34 @@ def cpu_baseline(args):
     torch.set_num_threads(threads)
     seq = int(args.cpu_seq)
     model, Wx, Wgx, gy, gr = build_workload(args, torch.device("cpu"), torch.float32, args.batch, seq)
-    t0 = time.perf_counter()
-    step(model, Wx, Wgx, gy, gr, "cpu", torch.float32)
-    dt = time.perf_counter() - t0
+    step(model, Wx, Wgx, gy, gr, "cpu", torch.float32)  # warm-up (page-in, thread pools)
+    times = []
+    for _ in range(max(1, int(args.cpu_trials))):
+        t0 = time.perf_counter()
+        step(model, Wx, Wgx, gy, gr, "cpu", torch.float32)
+        times.append(time.perf_counter() - t0)
     tokens = args.batch * seq
+    rates = [tokens / t for t in times]
+    n = len(rates)
+    mean = sum(rates) / n
+    sd = (sum((r - mean) ** 2 for r in rates) / (n - 1)) ** 0.5 if n > 1 else 0.0
+    # Student t, 95 %, n - 1 degrees of freedom (n <= 10 here)
+    t95 = {1: 12.71, 2: 4.303, 3: 3.182, 4: 2.776, 5: 2.571, 6: 2.447, 7: 2.365, 8: 2.306,
+           9: 2.262}.get(n - 1, 2.0)
+    half = t95 * sd / n ** 0.5 if n > 1 else None
     return {
-        "value": tokens / dt,
+        "value": mean,
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
+        "ci95": [mean - half, mean + half] if half is not None else None,
+        "trials": n,
         "sample": (f"oracle C/OpenMP fp32 (restates reference cpu_runtime.cpp + registered reverse scan), "
-                   f"one fwd+bwd step at B={args.batch}, T={seq}, H={args.state}, D={args.hidden}, "
-                   f"n_max={model.read.last_n_max}; {dt:.2f} s wall; T-truncated proxy of the "
-                   f"T={args.seq} workload (scan cost scales with T, read with T*n_max)"),
-        "seconds": dt,
+                   f"fwd+bwd steps at B={args.batch}, T={seq}, H={args.state}, D={args.hidden}, "
+                   f"n_max={model.read.last_n_max}: 1 warm-up + {n} timed, mean "
+                   f"{sum(times) / n:.2f} s each; T-truncated proxy of the T={args.seq} workload "
+                   f"(scan cost scales with T, read with T*n_max)"),
+        "seconds": sum(times),
     }
 
 
@@ -461,6 +520,8 @@ def main():
                           "per_step": round(v["total_ms"] / args.steps, 3)}
                       for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["total_ms"])},
     }
+    if not args.no_proj:
+        result["projections"] = time_projections(args, model, device, dtype)
     if not args.no_cpu:
         try:
             result["cpu_baseline"] = cpu_baseline(args)
