@@ -155,9 +155,10 @@ __global__ void __launch_bounds__(256) normalize_bwd_kernel(int64_t rows, int H,
 constexpr int SEL_T = 256;
 
 // With floor_bf16 the floor cummax - window is rounded to bf16, as the reference evaluates
-// it when the admission values are bf16 (read.py:185-188 in the tapes' dtype).
+// it when the admission values are bf16 (read.py:185-188 in the tapes' dtype). With `whole`
+// the floor is the whole row's max - window (field and hybrid geometry, read.py:189-191).
 __global__ void __launch_bounds__(SEL_T) select_kernel(int T, const float* adm, const float* window,
-                                                       int floor_bf16, int64_t* order,
+                                                       int floor_bf16, int whole, int64_t* order,
                                                        int64_t* counts, int32_t* rank) {
   __shared__ float smax[SEL_T];
   __shared__ int scnt[SEL_T];
@@ -178,11 +179,12 @@ __global__ void __launch_bounds__(SEL_T) select_kernel(int T, const float* adm, 
     __syncthreads();
   }
   const float before = tid > 0 ? smax[tid - 1] : -INFINITY;
+  const float row_max = smax[SEL_T - 1];
   int cnt = 0;
   float run = before;
   auto floor_of = [&](float m) { return floor_bf16 ? round_to<bf16>(m - win) : m - win; };
   for (int t = t0; t < t1; ++t) {
-    run = (t == 0 || a[t] > run) ? a[t] : run;
+    run = whole ? row_max : ((t == 0 || a[t] > run) ? a[t] : run);
     cnt += (a[t] >= floor_of(run)) ? 1 : 0;
   }
   scnt[tid] = cnt;
@@ -199,7 +201,7 @@ __global__ void __launch_bounds__(SEL_T) select_kernel(int T, const float* adm, 
   int64_t* o = order + static_cast<size_t>(b) * T;
   int32_t* rk = rank + static_cast<size_t>(b) * T;
   for (int t = t0; t < t1; ++t) {
-    run = (t == 0 || a[t] > run) ? a[t] : run;
+    run = whole ? row_max : ((t == 0 || a[t] > run) ? a[t] : run);
     int r;
     if (a[t] >= floor_of(run)) {
       r = mpos++;
@@ -514,14 +516,15 @@ int dabsn_hip_normalize_rows_bwd(int dtype, int64_t rows, int64_t H, const void*
   return DABSN_OK;
 }
 
-int dabsn_hip_bank_select(int adm_dtype, int64_t B, int64_t T, const float* adm,
+int dabsn_hip_bank_select(int adm_dtype, int whole, int64_t B, int64_t T, const float* adm,
                           const float* window, int64_t* order, int64_t* counts, int32_t* rank,
                           hipStream_t stream) {
   DABSN_REQUIRE(B > 0 && T > 0 && T < (1ll << 30) && B < (1ll << 31), "bank_select: bad shape");
   DABSN_REQUIRE(adm_dtype == 0 || adm_dtype == 1, "bank_select: adm_dtype must be 0 or 1");
+  DABSN_REQUIRE(whole == 0 || whole == 1, "bank_select: whole must be 0 or 1");
   DABSN_REQUIRE(adm && window && order && counts && rank, "bank_select: null pointer");
   hipLaunchKernelGGL(select_kernel, dim3((unsigned)B), dim3(SEL_T), 0, stream, (int)T, adm, window,
-                     adm_dtype, order, counts, rank);
+                     adm_dtype, whole, order, counts, rank);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }

@@ -1103,11 +1103,14 @@ torch.library.register_autograd(_q("normalize_rows"), _norm_bwd, setup_context=_
 
 
 @torch.library.custom_op(_q("bank_select"), mutates_args=(), device_types="cuda")
-def bank_select(admission: Tensor, window: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+def bank_select(admission: Tensor, window: Tensor,
+                whole: int = 0) -> tuple[Tensor, Tensor, Tensor]:
     """Admitted-slot selection (read.py:185-239): (order [B,T] int64, counts [B] int64,
     rank [B,T] int32). Bit-exact integer work given the admission values. The floor
-    ``cummax(admission) - window`` is evaluated in the admission's dtype, as the reference
-    does (bf16 admission: the difference is rounded to bf16)."""
+    ``cummax(admission) - window`` (``whole`` = 0, seq geometry) or ``max(admission) -
+    window`` over the whole row (``whole`` = 1, field and hybrid geometry) is evaluated in
+    the admission's dtype, as the reference does (bf16 admission: the difference is rounded
+    to bf16)."""
     lib = _lib.load()
     B, T = admission.shape
     if admission.dtype not in (torch.float32, torch.bfloat16):
@@ -1118,13 +1121,13 @@ def bank_select(admission: Tensor, window: Tensor) -> tuple[Tensor, Tensor, Tens
     order = torch.empty((B, T), device=adm.device, dtype=torch.int64)
     counts = torch.empty((B,), device=adm.device, dtype=torch.int64)
     rank = torch.empty((B, T), device=adm.device, dtype=torch.int32)
-    _lib.check(lib.dabsn_hip_bank_select(adm_code, B, T, _p(adm), _p(win), _p(order), _p(counts),
-                                         _p(rank), _stream(adm)), "bank selection")
+    _lib.check(lib.dabsn_hip_bank_select(adm_code, int(whole), B, T, _p(adm), _p(win), _p(order),
+                                         _p(counts), _p(rank), _stream(adm)), "bank selection")
     return order, counts, rank
 
 
 @bank_select.register_fake
-def _bank_select_fake(admission, window):
+def _bank_select_fake(admission, window, whole=0):
     B, T = admission.shape
     return (admission.new_empty((B, T), dtype=torch.int64),
             admission.new_empty((B,), dtype=torch.int64),

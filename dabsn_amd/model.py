@@ -2,10 +2,11 @@
 
 ``DABSNBlock`` follows the reference block (src/dabsn/model.py:110-378): core scan
 (optionally time-chunked with a carried (b, e, c) state and a per-chunk checkpoint,
-model.py:197-307), read, ``state_to_hidden(y + read_gain * read)``, residual and the
-optional squared-ReLU MLP. ``DABSNSequenceLM`` keeps the reference LM's constructor and state-dict
-layout around a stack of seq blocks (model.py:381-436, 804-860); the reference's
-graph machinery and non-seq geometries are not part of this backend.
+model.py:197-307), read in seq, field or hybrid geometry,
+``state_to_hidden(y + read_gain * read)``, residual and the optional squared-ReLU MLP.
+``DABSNSequenceLM`` keeps the reference LM's constructor and state-dict layout around a
+stack of blocks (model.py:381-436, 804-860); the reference's graph machinery is not part of
+this backend.
 """
 
 from __future__ import annotations
@@ -36,7 +37,8 @@ class MLPRMSNorm(nn.Module):
 
 
 class DABSNBlock(nn.Module):
-    """One core plus admitted/permanent/induction/long read (seq geometry)."""
+    """One core plus admitted/permanent/induction/long read (seq, field or hybrid
+    geometry)."""
 
     def __init__(self, input_dim: int, hidden_dim: int, state_dim: int, read_geometry: str = "seq",
                  *, residual: bool = False, mlp_ratio: float | None = None,
@@ -47,6 +49,10 @@ class DABSNBlock(nn.Module):
         self.core = DABSNCore(input_dim=input_dim, hidden_dim=state_dim)
         self.read = DABSNRead(hidden_dim=state_dim, read_geometry=read_geometry)
         self.read_gain = nn.Parameter(torch.full((1,), 0.01))
+        # Present (and unused by the forward) for field blocks, as in the reference
+        # (model.py:145-147), so state dicts stay interchangeable.
+        self.field_read_gain = (nn.Parameter(torch.full((1,), 1.0)) if read_geometry == "field"
+                                else None)
         self.state_to_hidden = (nn.Identity() if state_dim == hidden_dim
                                 else nn.Linear(state_dim, hidden_dim))
         self.residual = bool(residual)

@@ -2,8 +2,9 @@
 recurrent long memory) on the ROCm backend.
 
 Parameter names and initial values follow the reference (src/dabsn/read.py:42-113).
-``_unified_forward`` follows read.py:139-438 for seq geometry and
-``forward_query_bank`` follows read.py:650-838. The heavy pieces run as registered HIP
+``_unified_forward`` follows read.py:139-438 in all three geometries (seq: causal prefix;
+field: the whole sequence; hybrid: both, mixed by a learned gate) and
+``forward_query_bank`` follows read.py:650-838 (seq only, as there). The heavy pieces run as registered HIP
 operators: tape statistics and query normalisation, admitted-slot selection, bank
 gather, the three-way read and the fused long-memory scan. The [B,T]-sized glue
 (key bias, admission, cocktail, their parameter gradients) stays in torch.
@@ -83,22 +84,31 @@ def _tape_means(stats: Tensor, energy: Tensor, saturation: Tensor, novelty: Tens
 
 
 class DABSNRead(nn.Module):
-    """The canonical DABSN memory read (seq geometry)."""
+    """The canonical DABSN memory read: ``seq`` (causal prefix), ``field`` (the whole
+    sequence) or ``hybrid`` (both, mixed by ``sigmoid(hybrid_gate)``)."""
 
     _rocm_native_enabled = False
 
     def __init__(self, hidden_dim: int, read_geometry: str = "seq") -> None:
         super().__init__()
-        if read_geometry != "seq":
-            raise ValueError("the ROCm backend implements the seq read geometry")
+        if read_geometry not in {"seq", "field", "hybrid"}:
+            raise ValueError(f"read_geometry must be seq, field, or hybrid; got {read_geometry}")
         self.hidden_dim = hidden_dim
         self.read_geometry = read_geometry
+        self.last_hybrid_gate: float | None = None
+        self.last_seq_norm: float | None = None
+        self.last_field_norm: float | None = None
+        self.last_field_neighbors: float | None = None
+        self.collect_traces = os.environ.get("DABSN_COLLECT_TRACES", "0") == "1"
+        self.hybrid_gate_override: float | None = None
         self.last_n_max: int | None = None
         self.last_read_contract: dict[str, object] = {}
         self.pad_gain = _parameter(1.0)
         self.short_gain = _parameter(1.0)
         self.induct_gain = _parameter(0.1)
         self.cocktail_gain = _parameter(1.0)
+        if read_geometry == "hybrid":
+            self.hybrid_gate = _parameter(0.0)
         self.admit_window = _parameter(4.0)
         self.short_read = _AdmittedReadParameters(hidden_dim)
         self.logit_retain = _parameter(2.2)
@@ -112,7 +122,10 @@ class DABSNRead(nn.Module):
     # ---- selection ------------------------------------------------------------
     def _select(self, admission: Tensor, length: int, width: int | None = None):
         window = F.softplus(self.admit_window)
-        order, counts, rank = ops.direct.bank_select(admission.detach(), window.detach())
+        # seq: floor from the causal prefix max; field / hybrid: the whole sequence's max
+        # (read.py:185-191)
+        whole = 0 if self.read_geometry == "seq" else 1
+        order, counts, rank = ops.direct.bank_select(admission.detach(), window.detach(), whole)
         if width or self._capture_bank_width:
             # A fixed width needs no host sync; slots past a row's admitted count are
             # masked out by `valid`.
@@ -151,7 +164,8 @@ class DABSNRead(nn.Module):
         rows = int(query.shape[1])
         # A few query rows without autograd (streaming decode): read the bank in place
         # instead of gathering K, V, Vn copies of the admitted slots.
-        streaming = not torch.is_grad_enabled() and query.is_cuda and rows <= 8
+        streaming = (not torch.is_grad_enabled() and query.is_cuda and rows <= 8
+                     and self.read_geometry == "seq")
         decode = (streaming and hidden % 8 == 0 and bank_write.stride(-1) == 1
                   and bank_write.stride(1) == hidden and bank_write.stride(0) % hidden == 0)
         dtype = "bf16" if query.dtype == torch.bfloat16 else "fp32"
@@ -184,20 +198,70 @@ class DABSNRead(nn.Module):
                 (self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain))
         else:
             K, V, Vn = ops.bank_gather(bank_write, norm_w, idx, next_idx, rank)
-            retrieved = ops.admitted_three_way_read_train(
-                query, K, V, Vn, cocktail[0], bank_cocktail, bank_bias, bank_adm, scale, read_idx,
-                valid, 0, self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain)
+
+            def read(mode: int) -> Tensor:
+                # mode 0: causal masks (seq); mode 1: every admitted slot for every query
+                # (field), read.py:283-314
+                return ops.admitted_three_way_read_train(
+                    query, K, V, Vn, cocktail[0], bank_cocktail, bank_bias, bank_adm, scale,
+                    read_idx, valid, mode, self.short_gain, self.pad_gain, self.induct_gain,
+                    self.cocktail_gain)
+
+            retrieved = self._geometry_mix(read, valid, query)
+        paths = 2 if self.read_geometry == "hybrid" else 1
         self.last_read_contract = {
             "read_strategy": "rocm_decode_bank_in_place" if decode else "rocm_compact_admitted_bank",
             "exact": True,
             "max_admitted_bank": int(n_max),
             "bank_growth": "grows_with_T" if n_max >= length else "data_dependent",
-            "estimated_read_work": int(query.shape[0]) * int(query.shape[1]) * int(n_max) * 3,
-            "admission_policy": "causal_write_prefix_max",
+            "estimated_read_work": int(query.shape[0]) * int(query.shape[1]) * int(n_max) * 3
+            * paths,
+            "admission_policy": ("causal_write_prefix_max" if self.read_geometry == "seq"
+                                 else "whole_sequence_max"),
             "kernel_backend": "rocm_hip_mfma",
             "query_start": int(query_start),
         }
         return retrieved
+
+    def _require_seq(self) -> None:
+        if self.read_geometry != "seq":
+            raise RuntimeError("query-bank read is exact only for seq geometry")
+
+    def _traces_on(self, query: Tensor) -> bool:
+        """Host-side trace values (read.py:290-292): on CPU, or with DABSN_COLLECT_TRACES."""
+        return not torch.compiler.is_compiling() and (self.collect_traces or not query.is_cuda)
+
+    def _geometry_mix(self, read, valid: Tensor, query: Tensor) -> Tensor:
+        """The read of this module's geometry from ``read(mode)`` (read.py:323-420): seq
+        reads causally, field reads every admitted slot, hybrid mixes the two with
+        ``gate = sigmoid(hybrid_gate)`` (or ``hybrid_gate_override``) as
+        ``(1 - gate) * seq + gate * field``."""
+        trace = self._traces_on(query)
+        self.last_hybrid_gate = None
+        self.last_field_neighbors = (float(valid.sum(dim=1).float().mean().cpu())
+                                     if trace and self.read_geometry != "seq" else None)
+        if self.read_geometry == "seq":
+            retrieved = read(0)
+            self.last_seq_norm = float(retrieved.detach().norm().cpu()) if trace else None
+            self.last_field_norm = None
+            return retrieved
+        if self.read_geometry == "field":
+            retrieved = read(1)
+            self.last_seq_norm = None
+            self.last_field_norm = float(retrieved.detach().norm().cpu()) if trace else None
+            return retrieved
+        seq_retrieved, field_retrieved = read(0), read(1)
+        if self.hybrid_gate_override is None:
+            gate = torch.sigmoid(self.hybrid_gate)
+        else:
+            gate = torch.as_tensor(float(self.hybrid_gate_override), device=query.device,
+                                   dtype=query.dtype)
+        self.last_hybrid_gate = float(gate.detach().cpu()) if trace else None
+        seq_part = (1.0 - gate) * seq_retrieved
+        field_part = gate * field_retrieved
+        self.last_seq_norm = float(seq_part.detach().norm().cpu()) if trace else None
+        self.last_field_norm = float(field_part.detach().norm().cpu()) if trace else None
+        return seq_part + field_part
 
     # ---- forward ---------------------------------------------------------------
     def forward(self, y, budget, expression, write, novelty, plasticity, energy, saturation,
@@ -269,6 +333,7 @@ class DABSNRead(nn.Module):
                            initial_long_state=None, return_long_state: bool = False):
         """Exact read of a query chunk against an external bank (read.py:650-838)."""
         del bank_y, bank_b, bank_ay
+        self._require_seq()
         rp = self.short_read
         _, _, hidden = expression.shape
         bank_len = bank_write.shape[1]
@@ -311,6 +376,7 @@ class DABSNRead(nn.Module):
         the slot-list width (no host sync for the admitted count).
 
         Returns (output, final long state)."""
+        self._require_seq()
         rp = self.short_read
         _, _, hidden = expression.shape
         bank_len = bank_write.shape[1]

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 7
+#define DABSN_HIP_ABI_VERSION 8
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -225,13 +225,14 @@ int dabsn_hip_normalize_rows_bwd(int dtype, int64_t rows, int64_t H, const void*
 int dabsn_hip_means_glue(int64_t B, int64_t N, int64_t ld, const float* stats, int64_t hidden,
                          const float* const* params, int mode, float* key_bias, float* admission,
                          float* cocktail, hipStream_t stream);
-/* Admitted-slot selection (src/dabsn/read.py:185-239, seq geometry): per row, floor =
- * cummax(adm) - window, member = adm >= floor, order = stable partition (members by
- * ascending t, then the rest), counts = #members, rank[t] = position of t in order.
- * adm [B,T] as fp32 values; window points at an fp32 scalar (already softplus-ed).
+/* Admitted-slot selection (src/dabsn/read.py:185-239): per row, floor = cummax(adm) -
+ * window (whole = 0, seq geometry) or max over the row of adm - window (whole = 1, field
+ * and hybrid geometry, read.py:189-191), member = adm >= floor, order = stable partition
+ * (members by ascending t, then the rest), counts = #members, rank[t] = position of t in
+ * order. adm [B,T] as fp32 values; window points at an fp32 scalar (already softplus-ed).
  * adm_dtype = the dtype the admission was computed in: 1 (bf16) rounds the floor to bf16
  * as the reference's bf16 subtraction does, 0 (fp32) keeps it fp32. Bit-exact. */
-int dabsn_hip_bank_select(int adm_dtype, int64_t B, int64_t T, const float* adm,
+int dabsn_hip_bank_select(int adm_dtype, int whole, int64_t B, int64_t T, const float* adm,
                           const float* window, int64_t* order, int64_t* counts, int32_t* rank,
                           hipStream_t stream);
 

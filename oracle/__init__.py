@@ -306,15 +306,19 @@ def round_bf16(x) -> np.ndarray:
     return bits.astype(np.uint32).view(np.float32)
 
 
-def bank_select(adm, window, floor_bf16: bool = False):
-    """Restates read.py:185-239 (seq). Returns (order [B,T] int64, counts [B] int64).
+def bank_select(adm, window, floor_bf16: bool = False, whole: bool = False):
+    """Restates read.py:185-239. Returns (order [B,T] int64, counts [B] int64).
 
-    With ``floor_bf16`` the admission values are bf16 values and the floor
-    ``cummax(adm) - window`` is rounded to bf16, as the reference's bf16 subtraction does
-    (its result is computed in fp32 and rounded once)."""
-    if floor_bf16:
+    The floor is ``cummax(adm) - window`` (seq geometry) or, with ``whole``, the row's
+    ``max(adm) - window`` (field and hybrid, read.py:189-191). With ``floor_bf16`` the
+    admission values are bf16 values and the floor is rounded to bf16, as the reference's
+    bf16 subtraction does (its result is computed in fp32 and rounded once)."""
+    if floor_bf16 or whole:
         a = _f32(adm)
-        floor = round_bf16(np.maximum.accumulate(a, axis=1) - np.float32(window))
+        top = (np.max(a, axis=1, keepdims=True) if whole else np.maximum.accumulate(a, axis=1))
+        floor = top - np.float32(window)
+        if floor_bf16:
+            floor = round_bf16(floor)
         member = a >= floor
         order = np.argsort(~member, axis=1, kind="stable").astype(np.int64)
         return order, member.sum(axis=1).astype(np.int64)

@@ -125,9 +125,9 @@ def _normalize_bwd(q, norms, gq):
     return _t(_normalize_grad(_np(q), _np(norms), _np(gq)).astype(np.float32), q.dtype)
 
 
-def _select(adm, window):
+def _select(adm, window, whole=0):
     order, counts = oracle.bank_select(_np(adm), float(window.reshape(())),
-                                       floor_bf16=adm.dtype == torch.bfloat16)
+                                       floor_bf16=adm.dtype == torch.bfloat16, whole=bool(whole))
     rank = np.empty_like(order, dtype=np.int32)
     rows = np.arange(order.shape[0])[:, None]
     rank[rows, order] = np.arange(order.shape[1], dtype=np.int32)[None, :]

@@ -24,6 +24,10 @@ Fixtures (reference file:line of the function evaluated):
 * ``read_seq_fp32`` -- ``DABSNRead.forward`` in seq geometry (read.py:139-438) on a
   partially admitted bank (admission window shrunk), with the slot order and counts the
   call produced, ``last_n_max`` and the gradients of every tape and parameter.
+* ``read_field_fp32``, ``read_hybrid_fp32`` -- the same read in field geometry
+  (whole-sequence admission floor, every admitted slot visible to every query,
+  read.py:185-191, 283-314, 346-367) and in hybrid geometry (both reads over the
+  whole-sequence bank mixed by sigmoid(hybrid_gate), read.py:368-420).
 * ``read_seq_bf16`` -- the same read with the module and tapes in bfloat16: the admission
   values, the selection order and counts it made (bf16 tape means, read.py:58-72,
   161-192) and its output.
@@ -254,14 +258,14 @@ def _perturbed_read(read, gen, scale=0.2):
             p.add_(scale * torch.randn(p.shape, generator=gen, dtype=p.dtype))
 
 
-def read_seq() -> None:
+def read_seq(geometry: str = "seq") -> None:
     import torch
     from dabsn.read import DABSNRead
 
     torch.manual_seed(0)
     gen = torch.Generator().manual_seed(13)
     B, T, H = 2, 24, 16
-    read = DABSNRead(hidden_dim=H, read_geometry="seq")
+    read = DABSNRead(hidden_dim=H, read_geometry=geometry)
     _perturbed_read(read, gen)
     with torch.no_grad():
         read.admit_window.fill_(-1.2)  # softplus = 0.26: a partially admitted bank
@@ -280,8 +284,8 @@ def read_seq() -> None:
     for n, g in zip(list(TAPE_NAMES) + [f"param.{n}" for n in names], grads):
         if g is not None:
             arrays[f"grad.{n}"] = _np(g)
-    print(f"  read_seq: n_max={read.last_n_max} of T={T}")
-    _save("read_seq_fp32", arrays)
+    print(f"  read_{geometry}: n_max={read.last_n_max} of T={T}")
+    _save(f"read_{geometry}_fp32", arrays)
 
 
 def read_seq_bf16() -> None:
@@ -452,6 +456,7 @@ def op_schemas() -> None:
 
 FIXTURES = {"core_op": lambda: core_op("fp32"), "core_op_bf16": core_op_bf16,
             "core_loop": core_loop, "read_seq": read_seq,
+            "read_field": lambda: read_seq("field"), "read_hybrid": lambda: read_seq("hybrid"),
             "read_seq_bf16": read_seq_bf16, "query_bank": query_bank, "model_c1": model_c1,
             "memory_lm": memory_lm, "op_schemas": op_schemas}
 

@@ -114,6 +114,43 @@ def test_forward_query_bank_matches_oracle_unified_read_gpu(cuda_device):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("geometry", ["field", "hybrid"])
+def test_field_and_hybrid_read_gpu_match_cpu_oracle(cuda_device, geometry):
+    """The field and hybrid reads at T=300 (several 256-row tiles, a partially admitted
+    whole-sequence bank) on the GPU against the same module on the CPU oracle kernels:
+    output and tape gradients 1e-5, parameter gradients 1e-4 (scalar sums)."""
+    torch.manual_seed(3)
+    B, T, H = 2, 300, 64
+    read = dabsn_amd.DABSNRead(H, read_geometry=geometry)
+    with torch.no_grad():
+        read.admit_window.fill_(-2.0)  # about 45 of 300 positions admitted
+        if geometry == "hybrid":
+            read.hybrid_gate.fill_(0.4)
+    g = torch.Generator().manual_seed(4)
+    tapes = [torch.randn(B, T, H, generator=g) for _ in range(3)]
+    tapes += [torch.rand(B, T, H, generator=g) for _ in range(5)]
+    tapes[3] = tapes[5] * tapes[2]  # write = plasticity * expression
+    gout = torch.randn(B, T, H, generator=g)
+
+    def run(module, device):
+        xs = [t.to(device).requires_grad_(True) for t in tapes]
+        out = module(*xs)
+        grads = torch.autograd.grad((out * gout.to(device)).sum(), [*xs, *module.parameters()],
+                                    allow_unused=True)
+        return out.detach().cpu(), [None if x is None else x.cpu() for x in grads], module.last_n_max
+
+    out_c, g_c, n_c = run(read, "cpu")
+    out_g, g_g, n_g = run(copy.deepcopy(read).to(cuda_device), cuda_device)
+    assert n_c == n_g and 1 < n_c < T
+    assert rel_err(out_g, out_c) <= 1e-5
+    for i, (a, b) in enumerate(zip(g_g, g_c)):
+        if b is None:
+            continue
+        tol = 1e-5 if i < 8 else 1e-4
+        assert rel_err(a, b) <= tol or float((a - b).abs().max()) <= 1e-6, f"grad {i}"
+
+
+@pytest.mark.gpu
 def test_config1_two_layer_model_gpu_matches_cpu_oracle(cuda_device):
     """input 24, layers (hidden 128, state 96) and (192, 128)."""
     torch.manual_seed(0)

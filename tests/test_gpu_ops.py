@@ -270,15 +270,17 @@ def test_long_scan_and_linear_recurrence_match_oracle(cuda_device, T):
         assert_rel(x, y, 1e-6, n)
 
 
+@pytest.mark.parametrize("whole", [0, 1])
 @pytest.mark.parametrize("T", [1, 255, 256, 257, 3000, 16384])
-def test_bank_select_bit_exact(cuda_device, T):
+def test_bank_select_bit_exact(cuda_device, T, whole):
+    """Causal prefix floor (seq) and whole-sequence floor (field / hybrid)."""
     rng = np.random.default_rng(T)
     adm = (rng.integers(-40, 40, size=(5, T)) / 8.0).astype(np.float32)
-    adm[0] = np.sort(adm[0])  # monotone row: everything is a member
+    adm[0] = np.sort(adm[0])  # monotone row: everything is a member of the causal floor
     adm[1] = adm[1][0]        # constant row: ties everywhere
     order, counts, rank = ops.bank_select(torch.from_numpy(adm).to(cuda_device),
-                                          torch.tensor([1.5], device=cuda_device))
-    oo, oc = oracle.bank_select(adm, 1.5)
+                                          torch.tensor([1.5], device=cuda_device), whole)
+    oo, oc = oracle.bank_select(adm, 1.5, whole=bool(whole))
     np.testing.assert_array_equal(order.cpu().numpy(), oo)
     np.testing.assert_array_equal(counts.cpu().numpy(), oc)
     np.testing.assert_array_equal(np.take_along_axis(rank.cpu().numpy(), oo, 1),

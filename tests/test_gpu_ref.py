@@ -27,7 +27,8 @@ import dabsn_amd
 from dabsn_amd import kernels
 from dabsn_amd.kernels import ops
 from helpers import grad_err, rel_err
-from test_ref_pins import _bf16, _load, _read_module, _tapes, c1_block_check, memory_lm_check
+from test_ref_pins import (_bf16, _load, _read_module, _tapes, c1_block_check, memory_lm_check,
+                           read_fixture_check)
 
 pytestmark = pytest.mark.gpu
 
@@ -94,29 +95,16 @@ def test_core_bf16_gap_against_the_references_own_bf16_path(cuda_device):
         assert e_hip <= max(2e-2, 1.5 * e_ref), f"g_{n}: {e_hip:.3e} (reference {e_ref:.3e})"
 
 
-def test_read_seq_vs_reference_fixture_gpu(cuda_device):
-    z = _load("read_seq_fp32")
+@pytest.mark.parametrize("geometry", ["seq", "field", "hybrid"])
+def test_read_vs_reference_fixture_gpu(cuda_device, geometry):
+    """The three read geometries on the GPU against the reference's DABSNRead. A scalar
+    gain's gradient sums O(T * N) signed terms, accumulated here in tile partials: 1e-4,
+    the scalar-gradient bar of the other GPU parity tests."""
+    z = _load(f"read_{geometry}_fp32")
     H = z["y"].shape[-1]
-    read = _read_module(z, H).to(cuda_device)
+    read = _read_module(z, H, geometry=geometry).to(cuda_device)
     tapes = [t.to(cuda_device).requires_grad_(True) for t in _tapes(z)]
-    out = read(*tapes)
-    assert read.last_n_max == int(z["n_max"])
-    assert rel_err(out.detach().cpu(), z["out"]) <= 1e-5
-    names = [n for n, _ in read.named_parameters()]
-    grads = torch.autograd.grad((out * torch.from_numpy(z["gout"]).to(cuda_device)).sum(),
-                                [*tapes, *read.parameters()], allow_unused=True)
-    tape_names = ("y", "budget", "expression", "write", "novelty", "plasticity", "energy",
-                  "saturation")
-    scale = max(float(np.abs(z[k]).max()) for k in z if k.startswith("grad.param."))
-    for n, g in zip(list(tape_names) + [f"param.{n}" for n in names], grads):
-        key = f"grad.{n}"
-        if key not in z:
-            continue
-        err = grad_err(g.cpu(), z[key], scale) if n.startswith("param.") else rel_err(g.cpu(), z[key])
-        # A scalar gain's gradient sums O(T * N) signed terms, accumulated here in tile
-        # partials: 1e-4, the scalar-gradient bar of the other GPU parity tests.
-        tol = 1e-4 if z[key].size == 1 else 1e-5
-        assert err <= tol, f"{n}: {err:.3e}"
+    read_fixture_check(z, read, tapes, scalar_tol=1e-4)
 
 
 def test_bf16_selection_bit_exact_vs_reference_fixture_gpu(cuda_device):
