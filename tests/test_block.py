@@ -118,7 +118,9 @@ def test_forward_query_bank_matches_oracle_unified_read_gpu(cuda_device):
 def test_field_and_hybrid_read_gpu_match_cpu_oracle(cuda_device, geometry):
     """The field and hybrid reads at T=300 (several 256-row tiles, a partially admitted
     whole-sequence bank) on the GPU against the same module on the CPU oracle kernels:
-    output and tape gradients 1e-5, parameter gradients 1e-4 (scalar sums)."""
+    output, tape gradients and the output projection's gradients 1e-5 normwise. A scalar
+    gain's gradient sums O(T * N) signed terms that partly cancel (here every query reads
+    every admitted slot): |diff| <= 1e-4 x the largest scalar gradient of the module."""
     torch.manual_seed(3)
     B, T, H = 2, 300, 64
     read = dabsn_amd.DABSNRead(H, read_geometry=geometry)
@@ -143,11 +145,15 @@ def test_field_and_hybrid_read_gpu_match_cpu_oracle(cuda_device, geometry):
     out_g, g_g, n_g = run(copy.deepcopy(read).to(cuda_device), cuda_device)
     assert n_c == n_g and 1 < n_c < T
     assert rel_err(out_g, out_c) <= 1e-5
+    scalar = [b for b in g_c[8:] if b is not None and b.numel() == 1]
+    s_max = max(float(b.abs()) for b in scalar)
     for i, (a, b) in enumerate(zip(g_g, g_c)):
         if b is None:
             continue
-        tol = 1e-5 if i < 8 else 1e-4
-        assert rel_err(a, b) <= tol or float((a - b).abs().max()) <= 1e-6, f"grad {i}"
+        if b.numel() == 1:
+            assert float((a - b).abs()) <= 1e-4 * s_max, f"grad {i}: {float(a)} vs {float(b)}"
+        else:
+            assert rel_err(a, b) <= 1e-5, f"grad {i}: {rel_err(a, b):.3e}"
 
 
 @pytest.mark.gpu
