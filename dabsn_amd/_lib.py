@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib = None
@@ -98,6 +98,7 @@ _SIGNATURES = {
     "dabsn_hip_normalize_rows": ([i32, i64, i64, vp, vp, vp, vp], i32),
     "dabsn_hip_normalize_rows_bwd": ([i32, i64, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_select": ([i32, i32, i64, i64, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_admit_append": ([i32, i64, i64, i64, vp, i64, vp, vp, vp, vp, i64, vp], i32),
     "dabsn_hip_bank_gather": ([i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_gather_bwd": (
         [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),

@@ -214,6 +214,33 @@ __global__ void __launch_bounds__(SEL_T) select_kernel(int T, const float* adm, 
   if (tid == 0) counts[b] = total;
 }
 
+// Incremental admission of positions appended to a carried bank (streaming decode): the
+// seq floor of position p is cummax(admission[0..p]) - window, so a position's membership
+// is final when it is appended. One thread per batch row walks the n new positions, keeps
+// the running prefix max and appends member positions to the row's slot list -- the same
+// floor, comparison and order as select_kernel over the whole bank.
+__global__ void __launch_bounds__(256) admit_append_kernel(int B, int64_t n, int64_t base,
+                                                           const float* adm, int64_t adm_ld,
+                                                           const float* window, int floor_bf16,
+                                                           float* amax, int64_t* mcount,
+                                                           int64_t* members, int64_t ld) {
+  const int b = blockIdx.x * 256 + threadIdx.x;
+  if (b >= B) return;
+  const float win = window[0];
+  const float* a = adm + static_cast<size_t>(b) * adm_ld;
+  int64_t* mem = members + static_cast<size_t>(b) * ld;
+  float run = amax[b];
+  int64_t c = mcount[b];
+  for (int64_t t = 0; t < n; ++t) {
+    const float v = a[t];
+    run = (base + t == 0 || v > run) ? v : run;
+    const float fl = floor_bf16 ? round_to<bf16>(run - win) : run - win;
+    if (v >= fl) mem[c++] = base + t;
+  }
+  amax[b] = run;
+  mcount[b] = c;
+}
+
 // Gather K (normalised), V and Vn rows of the bank; one thread per V elements.
 template <typename E, int V>
 __global__ void __launch_bounds__(256) gather_kernel(int T, int N, int H, int hblocks, const E* w,
@@ -525,6 +552,24 @@ int dabsn_hip_bank_select(int adm_dtype, int whole, int64_t B, int64_t T, const 
   DABSN_REQUIRE(adm && window && order && counts && rank, "bank_select: null pointer");
   hipLaunchKernelGGL(select_kernel, dim3((unsigned)B), dim3(SEL_T), 0, stream, (int)T, adm, window,
                      adm_dtype, whole, order, counts, rank);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_admit_append(int adm_dtype, int64_t B, int64_t n, int64_t base, const float* adm,
+                           int64_t adm_ld, const float* window, float* amax, int64_t* mcount,
+                           int64_t* members, int64_t members_ld, hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && B < (1ll << 31) && n >= 0 && base >= 0, "admit_append: bad shape");
+  DABSN_REQUIRE(adm_dtype == 0 || adm_dtype == 1, "admit_append: adm_dtype must be 0 or 1");
+  DABSN_REQUIRE(members_ld >= base + n, "admit_append: slot list of %lld < %lld positions",
+                (long long)members_ld, (long long)(base + n));
+  DABSN_REQUIRE(adm_ld >= n, "admit_append: adm row stride %lld < %lld", (long long)adm_ld,
+                (long long)n);
+  if (n == 0) return DABSN_OK;
+  DABSN_REQUIRE(adm && window && amax && mcount && members, "admit_append: null pointer");
+  hipLaunchKernelGGL(admit_append_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, stream,
+                     (int)B, n, base, adm, adm_ld, window, adm_dtype, amax, mcount, members,
+                     members_ld);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }

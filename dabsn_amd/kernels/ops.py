@@ -1126,6 +1126,30 @@ def bank_select(admission: Tensor, window: Tensor,
     return order, counts, rank
 
 
+def admit_append(admission: Tensor, window: Tensor, base: int, amax: Tensor, mcount: Tensor,
+                 members: Tensor, adm_bf16: bool) -> None:
+    """Incremental admission (streaming decode, inference only): positions ``base`` ..
+    ``base + n - 1`` with admission values ``admission`` [B, n] (fp32 values) extend each
+    row's slot list ``members`` [B, cap] int64, the member counts ``mcount`` [B] int64 and
+    the running prefix max ``amax`` [B] fp32, in place. ``adm_bf16``: the admission is a
+    bf16 tensor in the reference, so the floor is rounded to bf16 (as ``bank_select``)."""
+    _require_cuda(admission)
+    lib = _lib.load()
+    B, n = (int(d) for d in admission.shape)
+    a = admission.float()
+    if a.stride(1) != 1:
+        a = a.contiguous()
+    win = window.float().reshape(()).contiguous()
+    if not (amax.dtype == torch.float32 and mcount.dtype == torch.int64
+            and members.dtype == torch.int64 and members.stride(1) == 1
+            and amax.is_contiguous() and mcount.is_contiguous()):
+        raise ValueError("admit_append: amax fp32 [B], mcount int64 [B], members int64 [B, cap]")
+    _lib.check(lib.dabsn_hip_admit_append(1 if adm_bf16 else 0, B, n, int(base), _p(a),
+                                          int(a.stride(0)), _p(win), _p(amax), _p(mcount),
+                                          _p(members), int(members.stride(0)), _stream(a)),
+               "incremental admission")
+
+
 @bank_select.register_fake
 def _bank_select_fake(admission, window, whole=0):
     B, T = admission.shape

@@ -50,15 +50,34 @@ _STATS_COLUMN = {"energy": 0, "saturation": 1, "novelty": 2, "plasticity": 3}
 
 class BankStore:
     """One block's bank: write vectors [B, cap, H] and statistics rows [B, cap, 6] (fp32),
-    of which the first ``length`` positions are live."""
+    of which the first ``length`` positions are live.
+
+    For inference on the device it also keeps, per position, the read glue (key bias,
+    admission, cocktail) and, per batch row, the admitted-slot list with its count and the
+    running admission prefix max (``admission``): in seq geometry a position's floor and
+    membership depend only on the positions before it, so each decode step computes them for
+    its new positions alone. They are recomputed from the statistics rows whenever the read
+    parameters changed (storage or version) since they were computed."""
 
     def __init__(self, batch: int, hidden: int, *, device, dtype, capacity: int = 0) -> None:
         self.batch, self.hidden = int(batch), int(hidden)
         self.length = 0
-        self.write = torch.empty((batch, max(int(capacity), 0), hidden), device=device,
-                                 dtype=dtype)
-        self.stats = torch.empty((batch, max(int(capacity), 0), 6), device=device,
-                                 dtype=torch.float32)
+        cap = max(int(capacity), 0)
+        self.write = torch.empty((batch, cap, hidden), device=device, dtype=dtype)
+        self.stats = torch.empty((batch, cap, 6), device=device, dtype=torch.float32)
+        self._glue_arrays(cap)
+        self.admitted = 0          # positions whose glue and membership are current
+        self._glue_key: tuple | None = None
+
+    def _glue_arrays(self, cap: int) -> None:
+        dev = self.stats.device
+        self.key_bias = torch.empty((self.batch, cap), device=dev, dtype=torch.float32)
+        self.adm = torch.empty((self.batch, cap), device=dev, dtype=torch.float32)
+        self.cocktail = torch.empty((self.batch, cap, 4), device=dev, dtype=torch.float32)
+        # positions past a row's count stay 0: a valid index for the reads, masked by `valid`
+        self.members = torch.zeros((self.batch, cap), device=dev, dtype=torch.int64)
+        self.mcount = torch.zeros((self.batch,), device=dev, dtype=torch.int64)
+        self.amax = torch.zeros((self.batch,), device=dev, dtype=torch.float32)
 
     @property
     def capacity(self) -> int:
@@ -75,7 +94,46 @@ class BankStore:
         if self.length:
             write[:, :self.length].copy_(self.write[:, :self.length])
             stats[:, :self.length].copy_(self.stats[:, :self.length])
+        old = (self.key_bias, self.adm, self.cocktail, self.members, self.mcount, self.amax)
         self.write, self.stats = write, stats
+        self._glue_arrays(capacity)
+        n = self.admitted
+        if n:
+            self.key_bias[:, :n].copy_(old[0][:, :n])
+            self.adm[:, :n].copy_(old[1][:, :n])
+            self.cocktail[:, :n].copy_(old[2][:, :n])
+            self.members[:, :n].copy_(old[3][:, :n])
+            self.mcount.copy_(old[4])
+            self.amax.copy_(old[5])
+
+    def admission(self, read, hidden: int, tape_dtype: torch.dtype, length: int):
+        """(key_bias [B, L], admission [B, L], cocktail [B, L, 4], (slot list [B, cap],
+        counts [B])) of the first ``length`` live positions for ``read`` (a DABSNRead in seq
+        geometry), extending the kept glue and admitted-slot lists by the positions appended
+        since the last call: read.py:58-72, 155-191 for each new position, then its
+        membership under the causal floor. Inference on the device only."""
+        rp = read.short_read
+        prm = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain, rp.adm_novelty_gain,
+               rp.adm_saturation_gain, rp.adm_energy_gain, rp.adm_bias)
+        key = tuple((p.data_ptr(), p._version, p.dtype) for p in (*prm, read.admit_window)) \
+            + (tape_dtype, int(hidden))
+        if key != self._glue_key or self.admitted > length:
+            self._glue_key, self.admitted = key, 0
+            self.mcount.zero_()
+        lo = self.admitted
+        if lo < length:
+            kb, adm, ck = ops.means_glue(self.stats[:, lo:length], hidden, prm, tape_dtype)
+            self.key_bias[:, lo:length].copy_(kb)
+            self.adm[:, lo:length].copy_(adm)
+            self.cocktail[:, lo:length].copy_(ck)
+            # The reference's admission is a bf16 tensor when tapes and gains are: its floor
+            # is rounded to bf16 too (as in bank_select).
+            adm_bf16 = tape_dtype == torch.bfloat16 and rp.adm_bias.dtype == torch.bfloat16
+            window = torch.nn.functional.softplus(read.admit_window.detach())
+            ops.admit_append(adm, window, lo, self.amax, self.mcount, self.members, adm_bf16)
+            self.admitted = length
+        return (self.key_bias[:, :length], self.adm[:, :length], self.cocktail[:, :length],
+                (self.members, self.mcount))
 
     def append(self, write: Tensor, stats: Tensor) -> None:
         """Write a chunk's rows after the live prefix (doubling the storage when full)."""
@@ -90,6 +148,13 @@ class BankStore:
     def live(self, length: int | None = None) -> tuple[Tensor, Tensor]:
         n = self.length if length is None else int(length)
         return self.write[:, :n], self.stats[:, :n]
+
+    def truncate(self, length: int) -> None:
+        """Drop the positions from ``length`` on (a read-only query's rows). Glue and slot
+        lists that cover dropped positions are rebuilt on the next ``admission`` call."""
+        self.length = int(length)
+        if self.admitted > self.length:
+            self.admitted, self._glue_key = 0, None
 
     def fork(self, length: int, extra: int = 0) -> "BankStore":
         """A new store holding a copy of the first ``length`` positions, with room for
@@ -233,6 +298,11 @@ def _chunks(total: int, size: int | None) -> Iterator[tuple[int, int]]:
         yield start, min(total, start + size)
 
 
+#: Extend each bank's glue and admitted-slot lists by the new positions only (the default);
+#: False recomputes them over the whole bank every step, as the reference does.
+_INCREMENTAL_ADMISSION = True
+
+
 def _block_step(block: DABSNBlock, inputs: Tensor, layer: LayerMemory | None,
                 position: int) -> tuple[Tensor, LayerMemory]:
     """One block over a chunk from carried state, extending its bank (memory.py:215-290):
@@ -264,7 +334,8 @@ def _block_step(block: DABSNBlock, inputs: Tensor, layer: LayerMemory | None,
     retrieved, final_long = block.read.forward_query_bank_stats(
         y, budget, expression, write, plasticity, query_stats=stats, bank_write=bank_write,
         bank_stats=bank_stats, query_start=position,
-        initial_long_state=None if layer is None else layer.long, bank_width=width)
+        initial_long_state=None if layer is None else layer.long, bank_width=width,
+        bank_store=bank if _INCREMENTAL_ADMISSION else None)
     out = block.finish(inputs, block.state_to_hidden(y + block.read_gain * retrieved))
     return block.forward_mlp(out), LayerMemory(bank=bank, core=final_core, long=final_long)
 
@@ -300,7 +371,7 @@ def _run(model: DABSNSequenceLM, ids: Tensor, memory: DABSNMemory | None, *,
         # carried core/long states were never modified.
         for layer, new_state, n in zip(memory.layers, state, lengths):
             if new_state is not None and new_state.bank is layer.bank:
-                layer.bank.length = n
+                layer.bank.truncate(n)
         return hidden, memory
     result = DABSNMemory(layers=[s for s in state if s is not None], position=position,
                          batch_size=batch, fingerprint=fingerprint_of(model))

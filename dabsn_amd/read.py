@@ -138,11 +138,26 @@ class DABSNRead(nn.Module):
         return n_max, idx, valid, next_idx, rank
 
     def _bank(self, cocktail_bank: Tensor, key_bias: Tensor, admission: Tensor, length: int,
-              query_start: int, width: int | None = None) -> dict[str, object]:
+              query_start: int, width: int | None = None,
+              members: tuple[Tensor, Tensor] | None = None) -> dict[str, object]:
         """Slot selection and the per-slot glue gathered for the read (read.py:185-256,
         298-303): n_max, idx, valid, next_idx, rank, the bank's cocktail, key bias and
-        admission, the read scale and the slot positions relative to the query chunk."""
-        n_max, idx, valid, next_idx, rank = self._select(admission, length, width)
+        admission, the read scale and the slot positions relative to the query chunk.
+        ``members`` = (slot list [B, cap], counts [B]) kept incrementally by a carried bank
+        (inference): the selection is read from it instead of rerun over the bank."""
+        if members is None:
+            n_max, idx, valid, next_idx, rank = self._select(admission, length, width)
+        else:
+            slots, counts = members
+            if width or self._capture_bank_width:
+                n_max = max(1, min(int(width or self._capture_bank_width), length))
+            else:
+                n_max = max(int(counts.max().item()), 1)  # host sync, as read.py:233
+            idx = slots[:, :n_max]
+            valid = (torch.arange(n_max, device=idx.device).unsqueeze(0)
+                     < counts.clamp_min(1).unsqueeze(1))
+            next_idx = (idx + 1).clamp(max=length - 1)
+            rank = idx.new_empty((0,), dtype=torch.int32)  # the gather's backward only
         return {
             "n_max": n_max, "idx": idx, "valid": valid, "next_idx": next_idx, "rank": rank,
             "cocktail": torch.gather(cocktail_bank, 1, idx.unsqueeze(-1).expand(-1, -1, 4)),
@@ -153,8 +168,9 @@ class DABSNRead(nn.Module):
         }
 
     def _read_core(self, query, cocktail, bank_write, norm_w, key_bias, admission, length: int,
-                   query_start: int, width: int | None = None):
-        bank = self._bank(cocktail[1], key_bias, admission, length, query_start, width)
+                   query_start: int, width: int | None = None,
+                   members: tuple[Tensor, Tensor] | None = None):
+        bank = self._bank(cocktail[1], key_bias, admission, length, query_start, width, members)
         n_max, idx, valid, next_idx, rank = (bank[k] for k in ("n_max", "idx", "valid",
                                                                 "next_idx", "rank"))
         self.last_n_max = n_max
@@ -361,7 +377,8 @@ class DABSNRead(nn.Module):
 
     def forward_query_bank_stats(self, y, budget, expression, write, plasticity, *,
                                  query_stats, bank_write, bank_stats, query_start: int,
-                                 initial_long_state=None, bank_width: int | None = None):
+                                 initial_long_state=None, bank_width: int | None = None,
+                                 bank_store=None):
         """forward_query_bank with the bank given as its write vectors plus per-position
         statistics instead of full-width tapes.
 
@@ -373,7 +390,10 @@ class DABSNRead(nn.Module):
         one dense pass computes for the same positions, so this is the dense read.
         ``query_stats`` are the rows of the query chunk itself (which the caller has
         already appended to the bank, ending at ``query_start + T``). ``bank_width`` fixes
-        the slot-list width (no host sync for the admitted count).
+        the slot-list width (no host sync for the admitted count). ``bank_store`` (a
+        carried bank, inference on the device) keeps the glue and the admitted-slot list of
+        every position it holds and extends them with the new positions only
+        (``BankStore.admission``) instead of recomputing them over the bank.
 
         Returns (output, final long state)."""
         self._require_seq()
@@ -384,7 +404,13 @@ class DABSNRead(nn.Module):
             raise RuntimeError("query-bank read requires a non-empty bank")
         query = ops.direct.normalize_rows(expression, query_stats[..., 4].detach())
         tape_dtype = bank_write.dtype
-        if not torch.is_grad_enabled() and bank_stats.is_cuda:
+        members = None
+        if bank_store is not None and not torch.is_grad_enabled() and bank_stats.is_cuda:
+            key_bias, admission, bank_cocktail, members = bank_store.admission(
+                self, hidden, tape_dtype, int(bank_len))
+            rows = int(expression.shape[1])
+            cocktails = (bank_cocktail[:, bank_len - rows:], bank_cocktail)
+        elif not torch.is_grad_enabled() and bank_stats.is_cuda:
             # Inference (streaming decode): the per-position glue of the whole bank in one
             # kernel instead of ~25 small ones per layer and token.
             prm = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain,
@@ -401,7 +427,8 @@ class DABSNRead(nn.Module):
             admission = rp.admission_from_means(be, bc, bn, bp, hidden)
             cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
         retrieved = self._read_core(query, cocktails, bank_write, bank_stats[..., 5].detach(),
-                                    key_bias, admission, bank_len, int(query_start), bank_width)
+                                    key_bias, admission, bank_len, int(query_start), bank_width,
+                                    members)
         short_output = rp.project(y, budget, retrieved.to(y.dtype))
         long, final_state = self._long_scan_from_state(write, plasticity, None,
                                                        initial_state=initial_long_state,

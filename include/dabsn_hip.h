@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 8
+#define DABSN_HIP_ABI_VERSION 9
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -235,6 +235,18 @@ int dabsn_hip_means_glue(int64_t B, int64_t N, int64_t ld, const float* stats, i
 int dabsn_hip_bank_select(int adm_dtype, int whole, int64_t B, int64_t T, const float* adm,
                           const float* window, int64_t* order, int64_t* counts, int32_t* rank,
                           hipStream_t stream);
+/* Incremental admission for a carried bank (streaming decode; src/dabsn/memory.py:215-290
+ * reruns read.py:185-239 over the whole bank each step). In seq geometry the floor of a
+ * position depends only on the positions before it, so its membership is final when it is
+ * appended. Per batch row: the n positions base .. base + n - 1 with admission values adm
+ * [B, n] (row stride adm_ld), the running prefix max amax [B] (fp32; any value when
+ * base = 0), the member count mcount [B] and the row's slot list members [B, members_ld]
+ * (int64 positions, ascending). Appends each member position, as bank_select orders them;
+ * members[b, :mcount[b]] then equals bank_select's order[b, :counts[b]] over the whole
+ * bank, bit for bit. adm_dtype as for bank_select. members_ld >= base + n. */
+int dabsn_hip_admit_append(int adm_dtype, int64_t B, int64_t n, int64_t base, const float* adm,
+                           int64_t adm_ld, const float* window, float* amax, int64_t* mcount,
+                           int64_t* members, int64_t members_ld, hipStream_t stream);
 
 /* Bank gather (read.py:241-256, 298-303): for j < N, K = w[idx]/max(|w[idx]|,eps),
  * V = w[idx], Vn = w[next_idx] ([B,N,H]). norm_w [B,T] fp32. */

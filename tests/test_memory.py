@@ -259,3 +259,70 @@ def test_means_glue_matches_the_read_modules_expressions(cuda_device):
                 R._cocktail(e, c, n, p))
     for got, w in zip((kb, adm, ck), want):
         assert rel_err(got.cpu(), w.cpu()) <= 1e-6
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("adm_bf16", [False, True])
+def test_incremental_admission_equals_bank_select(cuda_device, adm_bf16):
+    """Slot lists built position chunk by position chunk (1, 7, 300, 1 ... positions at a
+    time) equal bank_select over the whole bank at every length: counts and the member
+    prefix of the order, bit for bit (ties and a constant row included)."""
+    from dabsn_amd.kernels import ops
+    g = torch.Generator().manual_seed(21)
+    B, T = 5, 700
+    adm = torch.randint(-40, 40, (B, T), generator=g).float() / 8.0
+    adm[1] = adm[1, 0]
+    if adm_bf16:
+        adm = adm.bfloat16().float()
+    adm = adm.to(cuda_device)
+    window = torch.tensor([1.5], device=cuda_device)
+    members = torch.zeros((B, T), device=cuda_device, dtype=torch.int64)
+    mcount = torch.zeros((B,), device=cuda_device, dtype=torch.int64)
+    amax = torch.zeros((B,), device=cuda_device, dtype=torch.float32)
+    lo = 0
+    for n in (1, 7, 300, 1, 1, 90, 300):
+        ops.admit_append(adm[:, lo:lo + n], window, lo, amax, mcount, members, adm_bf16)
+        lo += n
+        ref = adm[:, :lo].bfloat16() if adm_bf16 else adm[:, :lo]
+        order, counts, _ = ops.bank_select(ref, window)
+        assert torch.equal(mcount, counts)
+        for b in range(B):
+            c = int(counts[b])
+            assert torch.equal(members[b, :c], order[b, :c]), (lo, b)
+            assert not members[b, c:lo].any()
+
+
+@pytest.mark.gpu
+def test_incremental_admission_decode_is_bit_identical_to_full_recompute(cuda_device):
+    """Streaming decode with the kept glue and slot lists against the same decode that
+    recomputes them over the whole bank every step (the reference's way): identical logits,
+    through a prompt, token-by-token steps, a read-only query (rows appended then dropped)
+    and a change of a read parameter between steps (the kept glue is rebuilt)."""
+    model = _model(cuda_device)
+    ids = _ids(3, 40, seed=17).to(cuda_device)
+
+    def run():
+        out = []
+        memory = mem.ingest(model, ids[:, :24], chunk_size=10)
+        for t in range(24, 32):
+            step, memory = mem.forward_with_memory(model, ids[:, t:t + 1], memory, extend=True)
+            out.append(step)
+        peek, _ = mem.forward_with_memory(model, ids[:, 32:35], memory)  # read-only
+        out.append(peek)
+        with torch.no_grad():
+            model.blocks[0].read.short_read.adm_bias.add_(0.25)
+        for t in range(32, 40):
+            step, memory = mem.forward_with_memory(model, ids[:, t:t + 1], memory, extend=True)
+            out.append(step)
+        with torch.no_grad():
+            model.blocks[0].read.short_read.adm_bias.sub_(0.25)
+        return torch.cat(out, dim=1)
+
+    assert mem._INCREMENTAL_ADMISSION
+    got = run()
+    try:
+        mem._INCREMENTAL_ADMISSION = False
+        want = run()
+    finally:
+        mem._INCREMENTAL_ADMISSION = True
+    assert torch.equal(got, want)
