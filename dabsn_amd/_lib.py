@@ -98,7 +98,8 @@ _SIGNATURES = {
     "dabsn_hip_normalize_rows": ([i32, i64, i64, vp, vp, vp, vp], i32),
     "dabsn_hip_normalize_rows_bwd": ([i32, i64, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_select": ([i32, i32, i64, i64, vp, vp, vp, vp, vp, vp], i32),
-    "dabsn_hip_admit_append": ([i32, i64, i64, i64, vp, i64, vp, vp, vp, vp, i64, vp], i32),
+    "dabsn_hip_admit_step": (
+        [i32, i64, i64, i64, i64, vp, i64, PTR8, vp, i32, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_gather": ([i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_gather_bwd": (
         [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),

@@ -214,33 +214,6 @@ __global__ void __launch_bounds__(SEL_T) select_kernel(int T, const float* adm, 
   if (tid == 0) counts[b] = total;
 }
 
-// Incremental admission of positions appended to a carried bank (streaming decode): the
-// seq floor of position p is cummax(admission[0..p]) - window, so a position's membership
-// is final when it is appended. One thread per batch row walks the n new positions, keeps
-// the running prefix max and appends member positions to the row's slot list -- the same
-// floor, comparison and order as select_kernel over the whole bank.
-__global__ void __launch_bounds__(256) admit_append_kernel(int B, int64_t n, int64_t base,
-                                                           const float* adm, int64_t adm_ld,
-                                                           const float* window, int floor_bf16,
-                                                           float* amax, int64_t* mcount,
-                                                           int64_t* members, int64_t ld) {
-  const int b = blockIdx.x * 256 + threadIdx.x;
-  if (b >= B) return;
-  const float win = window[0];
-  const float* a = adm + static_cast<size_t>(b) * adm_ld;
-  int64_t* mem = members + static_cast<size_t>(b) * ld;
-  float run = amax[b];
-  int64_t c = mcount[b];
-  for (int64_t t = 0; t < n; ++t) {
-    const float v = a[t];
-    run = (base + t == 0 || v > run) ? v : run;
-    const float fl = floor_bf16 ? round_to<bf16>(run - win) : run - win;
-    if (v >= fl) mem[c++] = base + t;
-  }
-  amax[b] = run;
-  mcount[b] = c;
-}
-
 // Gather K (normalised), V and Vn rows of the bank; one thread per V elements.
 template <typename E, int V>
 __global__ void __launch_bounds__(256) gather_kernel(int T, int N, int H, int hblocks, const E* w,
@@ -444,27 +417,70 @@ __global__ void __launch_bounds__(256) read_out_reduce_kernel(uint32_t n, const 
 // the cocktail's norm and quotients) are rounded to bf16; bit 1 = the gains are bf16
 // too, so every product and sum is rounded as well (with fp32 gains, type promotion makes
 // them fp32). Operation order is that of read.py:58-72, 161-183.
+// Key bias, admission and cocktail of one statistics row s (6 floats).
+__device__ __forceinline__ void glue_row(const float* s, float hidden, const Ptr8& prm, int mode,
+                                         float* kb, float* adm, float* ck) {
+  const bool tb = mode & 1, pb = (mode & 2) && tb;
+  auto rt = [tb](float v) { return tb ? round_to<bf16>(v) : v; };
+  auto rp = [pb](float v) { return pb ? round_to<bf16>(v) : v; };
+  const float me = rt(s[0]), mc = rt(s[1]), mn = rt(s[2]), mp = rt(s[3]);
+  const float lp = rt(log1pf(rt(mp * hidden)));
+  float P[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) P[k] = prm.p[k][0];
+  if (kb) *kb = rp(rp(rp(P[0] * lp) + rp(P[1] * mn)) + P[2]);
+  if (adm)
+    *adm = rp(rp(rp(rp(rp(P[3] * lp) + rp(P[4] * mn)) + rp(P[5] * mc)) + rp(P[6] * me)) + P[7]);
+  const float d = rt(fmaxf(rt(sqrtf(me * me + mc * mc + mn * mn + mp * mp)), kEps));
+  *reinterpret_cast<float4*>(ck) = make_float4(rt(me / d), rt(mc / d), rt(mn / d), rt(mp / d));
+}
+
 __global__ void __launch_bounds__(256) means_glue_kernel(int64_t rows, int N, int64_t ld,
                                                          const float* __restrict__ stats,
                                                          float hidden, Ptr8 prm, int mode,
                                                          float* kb, float* adm, float* ck) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= rows) return;
-  const bool tb = mode & 1, pb = (mode & 2) && tb;
-  auto rt = [tb](float v) { return tb ? round_to<bf16>(v) : v; };
-  auto rp = [pb](float v) { return pb ? round_to<bf16>(v) : v; };
-  const float* s = stats + (i / N) * ld + (i % N) * 6;
-  const float me = rt(s[0]), mc = rt(s[1]), mn = rt(s[2]), mp = rt(s[3]);
-  const float lp = rt(log1pf(rt(mp * hidden)));
-  float P[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) P[k] = prm.p[k][0];
-  if (kb) kb[i] = rp(rp(rp(P[0] * lp) + rp(P[1] * mn)) + P[2]);
-  if (adm)
-    adm[i] = rp(rp(rp(rp(rp(P[3] * lp) + rp(P[4] * mn)) + rp(P[5] * mc)) + rp(P[6] * me)) + P[7]);
-  const float d = rt(fmaxf(rt(sqrtf(me * me + mc * mc + mn * mn + mp * mp)), kEps));
-  float4* o = reinterpret_cast<float4*>(ck + i * 4);
-  *o = make_float4(rt(me / d), rt(mc / d), rt(mn / d), rt(mp / d));
+  glue_row(stats + (i / N) * ld + (i % N) * 6, hidden, prm, mode, kb ? kb + i : nullptr,
+           adm ? adm + i : nullptr, ck + i * 4);
+}
+
+// Incremental admission of the positions base .. base + n - 1 appended to a carried bank
+// (streaming decode). One workgroup per batch row: its threads compute the new positions'
+// glue into the bank's glue arrays (unless `stats` is null: the admission values are then
+// already there), then thread 0 walks them in order, keeping the running prefix max, and
+// appends each member position to the row's slot list. In seq geometry the floor of a
+// position depends only on the positions before it, so this equals bank_select over the
+// whole bank: the same floor, comparison and order.
+__global__ void __launch_bounds__(256) admit_step_kernel(int64_t n, int64_t base, int64_t cap,
+                                                         const float* __restrict__ stats,
+                                                         float hidden, Ptr8 prm, int mode,
+                                                         const float* window, int floor_bf16,
+                                                         float* kb, float* adm, float* ck,
+                                                         float* amax, int64_t* mcount,
+                                                         int64_t* members) {
+  const int64_t b = blockIdx.x;
+  const size_t row0 = static_cast<size_t>(b) * cap + base;
+  if (stats) {
+    for (int64_t t = threadIdx.x; t < n; t += 256)
+      glue_row(stats + (row0 + t) * 6, hidden, prm, mode, kb + row0 + t, adm + row0 + t,
+               ck + (row0 + t) * 4);
+  }
+  __syncthreads();  // the glue rows of this batch row, visible to thread 0
+  if (threadIdx.x != 0) return;
+  const float win = window[0];
+  const float* a = adm + row0;
+  int64_t* mem = members + static_cast<size_t>(b) * cap;
+  float run = amax[b];
+  int64_t c = base == 0 ? 0 : mcount[b];
+  for (int64_t t = 0; t < n; ++t) {
+    const float v = a[t];
+    run = (base + t == 0 || v > run) ? v : run;
+    const float fl = floor_bf16 ? round_to<bf16>(run - win) : run - win;
+    if (v >= fl) mem[c++] = base + t;
+  }
+  amax[b] = run;
+  mcount[b] = c;
 }
 
 extern "C" {
@@ -552,24 +568,6 @@ int dabsn_hip_bank_select(int adm_dtype, int whole, int64_t B, int64_t T, const 
   DABSN_REQUIRE(adm && window && order && counts && rank, "bank_select: null pointer");
   hipLaunchKernelGGL(select_kernel, dim3((unsigned)B), dim3(SEL_T), 0, stream, (int)T, adm, window,
                      adm_dtype, whole, order, counts, rank);
-  DABSN_HIP_CHECK(hipGetLastError());
-  return DABSN_OK;
-}
-
-int dabsn_hip_admit_append(int adm_dtype, int64_t B, int64_t n, int64_t base, const float* adm,
-                           int64_t adm_ld, const float* window, float* amax, int64_t* mcount,
-                           int64_t* members, int64_t members_ld, hipStream_t stream) {
-  DABSN_REQUIRE(B > 0 && B < (1ll << 31) && n >= 0 && base >= 0, "admit_append: bad shape");
-  DABSN_REQUIRE(adm_dtype == 0 || adm_dtype == 1, "admit_append: adm_dtype must be 0 or 1");
-  DABSN_REQUIRE(members_ld >= base + n, "admit_append: slot list of %lld < %lld positions",
-                (long long)members_ld, (long long)(base + n));
-  DABSN_REQUIRE(adm_ld >= n, "admit_append: adm row stride %lld < %lld", (long long)adm_ld,
-                (long long)n);
-  if (n == 0) return DABSN_OK;
-  DABSN_REQUIRE(adm && window && amax && mcount && members, "admit_append: null pointer");
-  hipLaunchKernelGGL(admit_append_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, stream,
-                     (int)B, n, base, adm, adm_ld, window, adm_dtype, amax, mcount, members,
-                     members_ld);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
@@ -697,6 +695,35 @@ int dabsn_hip_read_output_bwd(int out_dtype, int proj_dtype, int long_dtype, int
 #undef L
   DABSN_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(read_out_reduce_kernel, dim3(1), dim3(256), 0, stream, nblk, partials, ggain);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_admit_step(int mode, int64_t B, int64_t n, int64_t base, int64_t cap,
+                         const float* stats, int64_t hidden, const float* const* params,
+                         const float* window, int adm_dtype, float* key_bias, float* admission,
+                         float* cocktail, float* amax, int64_t* mcount, int64_t* members,
+                         hipStream_t stream) {
+  DABSN_REQUIRE(mode >= 0 && mode <= 3, "admit_step: mode must be 0..3");
+  DABSN_REQUIRE(adm_dtype == 0 || adm_dtype == 1, "admit_step: adm_dtype must be 0 or 1");
+  DABSN_REQUIRE(B > 0 && B < (1ll << 31) && n >= 0 && base >= 0 && base + n <= cap && hidden > 0,
+                "admit_step: bad shape (B %lld, n %lld, base %lld, cap %lld)", (long long)B,
+                (long long)n, (long long)base, (long long)cap);
+  if (n == 0) return DABSN_OK;
+  DABSN_REQUIRE(window && admission && amax && mcount && members, "admit_step: null pointer");
+  Ptr8 prm{};
+  if (stats) {
+    DABSN_REQUIRE(params && key_bias && cocktail, "admit_step: null glue pointer");
+    DABSN_REQUIRE((reinterpret_cast<uintptr_t>(cocktail) & 15u) == 0,
+                  "admit_step: cocktail must be 16-byte aligned");
+    for (int k = 0; k < 8; ++k) {
+      DABSN_REQUIRE(params[k], "admit_step: null parameter %d", k);
+      prm.p[k] = params[k];
+    }
+  }
+  hipLaunchKernelGGL(admit_step_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, stream, n,
+                     base, cap, stats, static_cast<float>(hidden), prm, mode, window, adm_dtype,
+                     key_bias, admission, cocktail, amax, mcount, members);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }

@@ -1126,27 +1126,39 @@ def bank_select(admission: Tensor, window: Tensor,
     return order, counts, rank
 
 
-def admit_append(admission: Tensor, window: Tensor, base: int, amax: Tensor, mcount: Tensor,
-                 members: Tensor, adm_bf16: bool) -> None:
-    """Incremental admission (streaming decode, inference only): positions ``base`` ..
-    ``base + n - 1`` with admission values ``admission`` [B, n] (fp32 values) extend each
-    row's slot list ``members`` [B, cap] int64, the member counts ``mcount`` [B] int64 and
-    the running prefix max ``amax`` [B] fp32, in place. ``adm_bf16``: the admission is a
-    bf16 tensor in the reference, so the floor is rounded to bf16 (as ``bank_select``)."""
+def admit_step(stats: Optional[Tensor], hidden: int, params: Sequence[Tensor],
+               tape_dtype: torch.dtype, window: Tensor, base: int, n: int, key_bias: Tensor,
+               admission: Tensor, cocktail: Tensor, amax: Tensor, mcount: Tensor,
+               members: Tensor, adm_bf16: bool) -> None:
+    """Incremental admission of a carried bank (streaming decode, inference only), in
+    place: for positions ``base`` .. ``base + n - 1``, their glue from the statistics rows
+    ``stats`` [B, cap, 6] (as ``means_glue``; with ``stats`` None the values already in
+    ``admission`` are used) into ``key_bias`` / ``admission`` [B, cap] and ``cocktail``
+    [B, cap, 4], then their membership under the causal floor, extending each row's slot
+    list ``members`` [B, cap] int64, the counts ``mcount`` [B] int64 and the running prefix
+    max ``amax`` [B] fp32. ``adm_bf16``: the reference's admission is a bf16 tensor, so the
+    floor is rounded to bf16 (as ``bank_select``)."""
     _require_cuda(admission)
     lib = _lib.load()
-    B, n = (int(d) for d in admission.shape)
-    a = admission.float()
-    if a.stride(1) != 1:
-        a = a.contiguous()
-    win = window.float().reshape(()).contiguous()
-    if not (amax.dtype == torch.float32 and mcount.dtype == torch.int64
-            and members.dtype == torch.int64 and members.stride(1) == 1
-            and amax.is_contiguous() and mcount.is_contiguous()):
-        raise ValueError("admit_append: amax fp32 [B], mcount int64 [B], members int64 [B, cap]")
-    _lib.check(lib.dabsn_hip_admit_append(1 if adm_bf16 else 0, B, n, int(base), _p(a),
-                                          int(a.stride(0)), _p(win), _p(amax), _p(mcount),
-                                          _p(members), int(members.stride(0)), _stream(a)),
+    B, cap = (int(d) for d in admission.shape)
+    for t, shape, dt in ((key_bias, (B, cap), torch.float32), (admission, (B, cap), torch.float32),
+                         (cocktail, (B, cap, 4), torch.float32), (amax, (B,), torch.float32),
+                         (mcount, (B,), torch.int64), (members, (B, cap), torch.int64)):
+        if tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"admit_step: expected a contiguous {dt} tensor of shape {shape}")
+    if stats is not None and (tuple(stats.shape) != (B, cap, 6) or stats.dtype != torch.float32
+                              or not stats.is_contiguous()):
+        raise ValueError("admit_step: stats must be contiguous fp32 [B, cap, 6]")
+    prm = [_f32_scalar(x) for x in params]
+    ptrs = _lib.PTR8(*[x.data_ptr() for x in prm])
+    mode = 0
+    if tape_dtype == torch.bfloat16:
+        mode = 1 | (2 if all(x.dtype == torch.bfloat16 for x in params) else 0)
+    win = _f32_scalar(window)
+    _lib.check(lib.dabsn_hip_admit_step(mode, B, int(n), int(base), cap, _p(stats), int(hidden),
+                                        ptrs, _p(win), 1 if adm_bf16 else 0, _p(key_bias),
+                                        _p(admission), _p(cocktail), _p(amax), _p(mcount),
+                                        _p(members), _stream(admission)),
                "incremental admission")
 
 

@@ -110,27 +110,24 @@ class BankStore:
         """(key_bias [B, L], admission [B, L], cocktail [B, L, 4], (slot list [B, cap],
         counts [B])) of the first ``length`` live positions for ``read`` (a DABSNRead in seq
         geometry), extending the kept glue and admitted-slot lists by the positions appended
-        since the last call: read.py:58-72, 155-191 for each new position, then its
-        membership under the causal floor. Inference on the device only."""
+        since the last call in one kernel (read.py:58-72, 155-191 for each new position,
+        then its membership under the causal floor). Inference on the device only."""
         rp = read.short_read
         prm = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain, rp.adm_novelty_gain,
                rp.adm_saturation_gain, rp.adm_energy_gain, rp.adm_bias)
-        key = tuple((p.data_ptr(), p._version, p.dtype) for p in (*prm, read.admit_window)) \
-            + (tape_dtype, int(hidden))
+        watched = (*prm, read.admit_window)
+        key = (tuple((p.data_ptr(), p._version, p.dtype) for p in watched), tape_dtype, hidden)
         if key != self._glue_key or self.admitted > length:
             self._glue_key, self.admitted = key, 0
-            self.mcount.zero_()
         lo = self.admitted
         if lo < length:
-            kb, adm, ck = ops.means_glue(self.stats[:, lo:length], hidden, prm, tape_dtype)
-            self.key_bias[:, lo:length].copy_(kb)
-            self.adm[:, lo:length].copy_(adm)
-            self.cocktail[:, lo:length].copy_(ck)
             # The reference's admission is a bf16 tensor when tapes and gains are: its floor
             # is rounded to bf16 too (as in bank_select).
             adm_bf16 = tape_dtype == torch.bfloat16 and rp.adm_bias.dtype == torch.bfloat16
             window = torch.nn.functional.softplus(read.admit_window.detach())
-            ops.admit_append(adm, window, lo, self.amax, self.mcount, self.members, adm_bf16)
+            ops.admit_step(self.stats, hidden, prm, tape_dtype, window, lo, length - lo,
+                           self.key_bias, self.adm, self.cocktail, self.amax, self.mcount,
+                           self.members, adm_bf16)
             self.admitted = length
         return (self.key_bias[:, :length], self.adm[:, :length], self.cocktail[:, :length],
                 (self.members, self.mcount))

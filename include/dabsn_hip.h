@@ -236,17 +236,24 @@ int dabsn_hip_bank_select(int adm_dtype, int whole, int64_t B, int64_t T, const 
                           const float* window, int64_t* order, int64_t* counts, int32_t* rank,
                           hipStream_t stream);
 /* Incremental admission for a carried bank (streaming decode; src/dabsn/memory.py:215-290
- * reruns read.py:185-239 over the whole bank each step). In seq geometry the floor of a
- * position depends only on the positions before it, so its membership is final when it is
- * appended. Per batch row: the n positions base .. base + n - 1 with admission values adm
- * [B, n] (row stride adm_ld), the running prefix max amax [B] (fp32; any value when
- * base = 0), the member count mcount [B] and the row's slot list members [B, members_ld]
- * (int64 positions, ascending). Appends each member position, as bank_select orders them;
- * members[b, :mcount[b]] then equals bank_select's order[b, :counts[b]] over the whole
- * bank, bit for bit. adm_dtype as for bank_select. members_ld >= base + n. */
-int dabsn_hip_admit_append(int adm_dtype, int64_t B, int64_t n, int64_t base, const float* adm,
-                           int64_t adm_ld, const float* window, float* amax, int64_t* mcount,
-                           int64_t* members, int64_t members_ld, hipStream_t stream);
+ * reruns read.py:58-72, 155-191 over the whole bank each step). In seq geometry the floor
+ * of a position depends only on the positions before it, so its glue and membership are
+ * final when it is appended. Per batch row, for the n positions base .. base + n - 1 of a
+ * bank of capacity cap: computes their key bias, admission and cocktail from the
+ * statistics rows stats [B, cap, 6] exactly as dabsn_hip_means_glue (`mode`, `params`)
+ * into key_bias [B, cap], admission [B, cap] and cocktail [B, cap, 4] (16-byte aligned);
+ * then, in position order, updates the running prefix max amax [B] and the member count
+ * mcount [B] (fp32 / int64; both restart when base = 0), appending each member position to the row's
+ * slot list members [B, cap] (int64, ascending). members[b, :mcount[b]] then equals
+ * dabsn_hip_bank_select's order[b, :counts[b]] over the first base + n positions, bit for
+ * bit. adm_dtype as for bank_select; window as there. With stats = NULL the admission
+ * values are taken from `admission` as they stand (params, key_bias and cocktail unused).
+ * base + n <= cap. */
+int dabsn_hip_admit_step(int mode, int64_t B, int64_t n, int64_t base, int64_t cap,
+                         const float* stats, int64_t hidden, const float* const* params,
+                         const float* window, int adm_dtype, float* key_bias, float* admission,
+                         float* cocktail, float* amax, int64_t* mcount, int64_t* members,
+                         hipStream_t stream);
 
 /* Bank gather (read.py:241-256, 298-303): for j < N, K = w[idx]/max(|w[idx]|,eps),
  * V = w[idx], Vn = w[next_idx] ([B,N,H]). norm_w [B,T] fp32. */

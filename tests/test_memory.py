@@ -277,11 +277,15 @@ def test_incremental_admission_equals_bank_select(cuda_device, adm_bf16):
     adm = adm.to(cuda_device)
     window = torch.tensor([1.5], device=cuda_device)
     members = torch.zeros((B, T), device=cuda_device, dtype=torch.int64)
-    mcount = torch.zeros((B,), device=cuda_device, dtype=torch.int64)
+    mcount = torch.full((B,), 99, device=cuda_device, dtype=torch.int64)  # restarts at base 0
     amax = torch.zeros((B,), device=cuda_device, dtype=torch.float32)
+    kb = torch.zeros((B, T), device=cuda_device)
+    ck = torch.zeros((B, T, 4), device=cuda_device)
     lo = 0
     for n in (1, 7, 300, 1, 1, 90, 300):
-        ops.admit_append(adm[:, lo:lo + n], window, lo, amax, mcount, members, adm_bf16)
+        # stats None: membership of the admission values already in `adm`
+        ops.admit_step(None, 1, [], torch.float32, window, lo, n, kb, adm, ck, amax, mcount,
+                       members, adm_bf16)
         lo += n
         ref = adm[:, :lo].bfloat16() if adm_bf16 else adm[:, :lo]
         order, counts, _ = ops.bank_select(ref, window)
