@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lock = threading.Lock()
 _lib = None
@@ -38,8 +38,8 @@ PTR8 = vp * 8
 class CoreFwdCall(ctypes.Structure):
     """Mirror of ``dabsn_core_fwd_call``."""
 
-    _fields_ = ([("dtype", i32), ("B", i64), ("T", i64), ("H", i64), ("ldt", i64), ("Wx", vp), ("Wgx", vp),
-                 ("GA", vp), ("params", ctypes.POINTER(CoreParams))]
+    _fields_ = ([("dtype", i32), ("B", i64), ("T", i64), ("H", i64), ("ldt", i64), ("ldx", i64),
+                 ("Wx", vp), ("Wgx", vp), ("GA", vp), ("params", ctypes.POINTER(CoreParams))]
                 + [(n, vp) for n in ("b0", "e0", "c0", "U", "nov", "plast", "expr", "write",
                                      "energy", "sat", "gate", "bF", "eF", "cF", "workspace")]
                 + [("workspace_bytes", sz)])

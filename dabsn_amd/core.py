@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 from torch import Tensor
 
 from .kernels import ops
@@ -78,6 +79,25 @@ class DABSNCore(nn.Module):
             self.log_lambda.reshape(()), self.logit_saturation_suppress.reshape(()),
         )
 
+    def projections(self, inputs: Tensor) -> tuple[Tensor, Tensor]:
+        """(W x, Wg x + b) (core.py:281-282) as one GEMM over the stacked weight [W; Wg]:
+        the [B, T, 2H] result holds Wx and Wgx side by side, and the scan reads the two
+        halves in place through its input row stride. Without autograd (inference) the
+        stacked weight and bias are built once per parameter version."""
+        H = self.hidden_dim
+
+        def stack(w, wg, bg):
+            return torch.cat((w, wg), dim=0), torch.cat((bg.new_zeros(H), bg), dim=0)
+
+        params = (self.W.weight, self.Wg.weight, self.Wg.bias)
+        if torch.is_grad_enabled():
+            weight, bias = stack(*params)
+        else:
+            weight, bias = ops._derived("proj", params, stack)
+        both = F.linear(inputs, weight, bias)
+        Wx, Wgx = both.split(H, dim=-1)
+        return Wx, Wgx
+
     def forward_from_state(self, inputs: Tensor, *, initial_state=None, return_writes: bool = False,
                            return_cocktail: bool = False, return_final_state: bool = False):
         if inputs.dim() != 3:
@@ -94,8 +114,8 @@ class DABSNCore(nn.Module):
                 shapes = tuple(tuple(v.shape) for v in values)
                 raise ValueError(f"initial_state tensors must have shape {expected}, got {shapes}")
             initial_state = values
-        outputs = ops.direct.core_scan_batched(self.W(inputs), self.Wg(inputs),
-                                               *self.scan_inputs(), *initial_state)
+        outputs = ops.direct.core_scan_batched(*self.projections(inputs), *self.scan_inputs(),
+                                               *initial_state)
         self._last_core_backend = "rocm_native_hip"
         trajectory, novelty, plasticity, expression, write = outputs[:5]
         if return_cocktail:
@@ -117,7 +137,7 @@ class DABSNCore(nn.Module):
 
         batch = inputs.shape[0]
         zeros = torch.zeros(batch, self.hidden_dim, device=inputs.device, dtype=torch.float32)
-        outputs = chunked_core_scan(chunk_t, self.W(inputs), self.Wg(inputs), *self.scan_inputs(),
+        outputs = chunked_core_scan(chunk_t, *self.projections(inputs), *self.scan_inputs(),
                                     zeros, torch.ones_like(zeros), zeros.clone())
         self._last_core_backend = "rocm_native_hip_chunked"
         return tuple(outputs[:7])

@@ -260,6 +260,7 @@ template <typename E>
 struct FwdArgs {
   int B, T, H, nct;
   int64_t ldt;  // time steps between consecutive batch rows of every [B, *, .] tensor (>= T)
+  int64_t ldx;  // elements between consecutive time steps of Wx and Wgx (>= H)
   const E* Wx;
   const E* Wgx;
   const E* GA;  // [2H][H]: Ug rows then A rows
@@ -414,7 +415,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   float sc = act ? a.c0[static_cast<size_t>(b) * H + c] : 0.0f;
   const size_t row0 = static_cast<size_t>(b) * static_cast<size_t>(a.ldt);
 
-  float ycur = (act && T > 0) ? tanhf(ld(a.Wx, row0 * H + c) + sb) : 0.0f;
+  float ycur = (act && T > 0) ? tanhf(ld(a.Wx, row0 * a.ldx + c) + sb) : 0.0f;
   const int kb_y[1] = {ct * CH};
   if (T > 0) {
     const float v[1] = {ycur};
@@ -426,7 +427,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   // pair read element 0; the last step rereads its own row), so no select waits on them.
   const size_t lrow0 = act ? row0 : 0;
   const int lc = act ? c : 0;
-  auto in_row = [&](int t) { return (lrow0 + static_cast<size_t>(t)) * H + lc; };
+  auto in_row = [&](int t) { return (lrow0 + static_cast<size_t>(t)) * a.ldx + lc; };
   // With 8 waves (16-unit bf16 tiles), wave 4 -- no pairs, no polling -- fetches the next
   // step's Wgx_t and Wx_{t+1} for the tile as 16-byte chunks (2 streams x 16 rows x 2)
   // during the shadow and parks them in LDS after the step barrier; the polling wave 0 then
@@ -438,11 +439,11 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   const E* in_src = iq < 32 ? a.Wgx : a.Wx;
   const int in_bb = bg * NB + (iq / 2) % NB;
   const size_t in_base = static_cast<size_t>(in_bb < B ? in_bb : 0) * static_cast<size_t>(a.ldt) *
-                             static_cast<size_t>(H) + ct * 16 + (iq & 1) * 8;
+                             static_cast<size_t>(a.ldx) + ct * 16 + (iq & 1) * 8;
   // Chunk of step t: Wgx_t or Wx_{t+1} (clamped to the last row).
   auto in_load = [&](int t) {
     const int tr = min(iq < 32 ? t : t + 1, T - 1);
-    return gload16(in_src + in_base + static_cast<size_t>(tr) * H);
+    return gload16(in_src + in_base + static_cast<size_t>(tr) * a.ldx);
   };
   u32x4 in_chunk = {0u, 0u, 0u, 0u};
   if (in_loader && T > 0) in_chunk = in_load(0);
@@ -1113,7 +1114,7 @@ __global__ void __launch_bounds__(256) y0_kernel(FwdArgs<E> a, E* y0) {
   if (i >= static_cast<int64_t>(a.B) * a.H) return;
   const int b = static_cast<int>(i / a.H), c = static_cast<int>(i % a.H);
   st(y0, static_cast<size_t>(i),
-     tanhf(ld(a.Wx, static_cast<size_t>(b) * static_cast<size_t>(a.ldt) * a.H + c) + a.b0[i]));
+     tanhf(ld(a.Wx, static_cast<size_t>(b) * static_cast<size_t>(a.ldt) * a.ldx + c) + a.b0[i]));
 }
 
 template <typename E>
@@ -1127,12 +1128,13 @@ __global__ void __launch_bounds__(256) step1_kernel(FwdArgs<E> a, const float* G
   const float sb = a.b0[i], se = a.e0[i], sc = a.c0[i];
   const size_t row0 = static_cast<size_t>(b) * static_cast<size_t>(a.ldt);
   const size_t rt = row0 * H + c;
-  const float y = tanhf(ld(a.Wx, rt) + sb);
+  const size_t rx = row0 * a.ldx + c;
+  const float y = tanhf(ld(a.Wx, rx) + sb);
   // The reference's recurrent GEMM returns the activation dtype.
   const float ug = round_to<E>(G[static_cast<size_t>(b) * 2 * H + c]);
   const float ay = round_to<E>(G[static_cast<size_t>(b) * 2 * H + H + c]);
   float s_g, p, nov, cpost;
-  const float bn = budget_next(up, sg, sb, se, ld(a.Wgx, rt), ug, ay, s_g, p);
+  const float bn = budget_next(up, sg, sb, se, ld(a.Wgx, rx), ug, ay, s_g, p);
   const float en = energy_next(up, sg, sb, se, sc, y, s_g, p, ay, nov, cpost);
   const size_t ru = row0 * 2 * H + c;
   st(a.U, ru, y);
@@ -1265,8 +1267,8 @@ static FwdArgs<E> slab_of(const FwdArgs<E>& a, int g0, int ng) {
   FwdArgs<E> s = a;
   const size_t b0 = static_cast<size_t>(g0) * NB, row = static_cast<size_t>(a.ldt) * a.H;
   s.B = static_cast<int>(std::min<size_t>(static_cast<size_t>(ng) * NB, a.B - b0));
-  s.Wx = adv(a.Wx, b0 * row);
-  s.Wgx = adv(a.Wgx, b0 * row);
+  s.Wx = adv(a.Wx, b0 * static_cast<size_t>(a.ldt) * a.ldx);
+  s.Wgx = adv(a.Wgx, b0 * static_cast<size_t>(a.ldt) * a.ldx);
   s.b0 = adv(a.b0, b0 * a.H);
   s.e0 = adv(a.e0, b0 * a.H);
   s.c0 = adv(a.c0, b0 * a.H);
@@ -1478,6 +1480,11 @@ static int check_fwd(const dabsn_core_fwd_call& f, Cfg& c) {
   DABSN_REQUIRE(f.ldt == 0 || (f.ldt >= f.T && f.B * f.ldt * 2 * f.H < (1ll << 46)),
                 "core scan: bad time stride ldt=%lld for T=%lld", (long long)f.ldt,
                 (long long)f.T);
+  DABSN_REQUIRE(f.ldx == 0 || f.ldx == f.H ||
+                    (f.ldx > f.H && f.ldx % 8 == 0 &&
+                     f.B * (f.ldt > 0 ? f.ldt : f.T) * f.ldx < (1ll << 46)),
+                "core scan: bad input row stride ldx=%lld for H=%lld (H, or above H and a "
+                "multiple of 8)", (long long)f.ldx, (long long)f.H);
   DABSN_REQUIRE(f.Wx && f.Wgx && f.GA && f.b0 && f.e0 && f.c0 && f.bF && f.eF && f.cF &&
                     f.workspace,
                 "core scan: null pointer argument");
@@ -1545,7 +1552,8 @@ static int prepare_bwd(const dabsn_core_bwd_call& b, Cfg& c, hipStream_t stream)
 template <typename E>
 static FwdArgs<E> fwd_args(const dabsn_core_fwd_call& f, const Cfg& c) {
   return FwdArgs<E>{static_cast<int>(f.B), static_cast<int>(f.T), static_cast<int>(f.H), c.nct,
-                    f.ldt > 0 ? f.ldt : f.T, static_cast<const E*>(f.Wx), static_cast<const E*>(f.Wgx),
+                    f.ldt > 0 ? f.ldt : f.T, f.ldx > 0 ? f.ldx : f.H, static_cast<const E*>(f.Wx),
+                    static_cast<const E*>(f.Wgx),
                     static_cast<const E*>(f.GA), to_params(f.params), f.b0, f.e0, f.c0,
                     static_cast<E*>(f.U), static_cast<E*>(f.nov), static_cast<E*>(f.plast),
                     static_cast<E*>(f.expr), static_cast<E*>(f.write), static_cast<E*>(f.energy),
@@ -1646,7 +1654,7 @@ int dabsn_hip_core_scan_fwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
                             void* plast, void* expr, void* write, void* energy, void* sat,
                             void* gate, float* bF, float* eF, float* cF, void* workspace,
                             size_t workspace_bytes_, hipStream_t stream) {
-  const dabsn_core_fwd_call f{dtype, B, T, H, 0, Wx, Wgx, GA, params, b0, e0, c0, U, nov,
+  const dabsn_core_fwd_call f{dtype, B, T, H, 0, 0, Wx, Wgx, GA, params, b0, e0, c0, U, nov,
                               plast, expr, write, energy, sat, gate, bF, eF, cF, workspace,
                               workspace_bytes_};
   return dabsn_hip_core_scan_fwd_call(&f, stream);

@@ -57,7 +57,7 @@ class _Fwd:
     """C call descriptor, workspace and final state of the forward scan of steps [t0, t1)."""
 
     def __init__(self, code: int, Wx: Tensor, Wgx: Tensor, GA: Tensor, params, b0: Tensor,
-                 e0: Tensor, c0: Tensor, out: _Tapes, t0: int, t1: int) -> None:
+                 e0: Tensor, c0: Tensor, out: _Tapes, t0: int, t1: int, ldx: int) -> None:
         lib = _lib.load()
         B, T, H = Wx.shape
         self.keep = (Wx, Wgx, GA, b0, e0, c0, out)
@@ -65,11 +65,12 @@ class _Fwd:
         nbytes = lib.dabsn_hip_core_scan_workspace_bytes(code, B, H, 0)
         self.ws = _empty((nbytes,), Wx, torch.uint8)
         self.params = params
-        o = t0 * H
+        o, ox = t0 * H, t0 * ldx  # first step of the window in the tapes / in Wx, Wgx
         self.call = _lib.CoreFwdCall(
-            code, B, t1 - t0, H, T, _ptr(Wx, o), _ptr(Wgx, o), _ptr(GA), ctypes.pointer(params),
-            _ptr(b0), _ptr(e0), _ptr(c0), _ptr(out.U, 2 * o), *[_ptr(t, o) for t in out.tapes],
-            *[_ptr(f) for f in self.finals], _ptr(self.ws), nbytes)
+            code, B, t1 - t0, H, T, ldx, _ptr(Wx, ox), _ptr(Wgx, ox), _ptr(GA),
+            ctypes.pointer(params), _ptr(b0), _ptr(e0), _ptr(c0), _ptr(out.U, 2 * o),
+            *[_ptr(t, o) for t in out.tapes], *[_ptr(f) for f in self.finals], _ptr(self.ws),
+            nbytes)
 
     def launch(self, stream) -> None:
         _lib.check(_lib.load().dabsn_hip_core_scan_fwd_call(ctypes.byref(self.call), stream),
@@ -154,12 +155,12 @@ class _ChunkedCoreScan(torch.autograd.Function):
         GA = torch.cat((Ug, A), dim=0).to(dt).contiguous()
         params, keep = ops._core_params(vecs, scal)
         carry = [x.float().contiguous() for x in (b0, e0, c0)]
-        Wx_c, Wgx_c = Wx.contiguous(), Wgx.to(dt).contiguous()
+        Wx_c, Wgx_c, ldx = ops.scan_inputs(Wx, Wgx, dt)
         out = _Tapes(Wx_c, B, T, H)
         starts = []
         for t0, t1 in _chunks(T, chunk):
             starts.append(torch.stack(carry))
-            f = _Fwd(code, Wx_c, Wgx_c, GA, params, *carry, out, t0, t1)
+            f = _Fwd(code, Wx_c, Wgx_c, GA, params, *carry, out, t0, t1, ldx)
             tk = ops.KernelTimer.begin("core_scan_fwd", Wx)
             f.launch(stream)
             ops.KernelTimer.end(tk)
@@ -168,6 +169,7 @@ class _ChunkedCoreScan(torch.autograd.Function):
         del keep
         finals = [f.to(x.dtype) for f, x in zip(carry, (b0, e0, c0))]
         ctx.chunk = chunk
+        ctx.ldx = ldx
         ctx.meta = [(x.dtype, tuple(x.shape)) for x in inputs]
         # The forward's own outputs are kept for the backward: the last chunk's reverse scan
         # reads its window there instead of recomputing tapes that were written just before
@@ -204,7 +206,8 @@ class _ChunkedCoreScan(torch.autograd.Function):
 
         def fwd_of(k: int) -> _Fwd:
             return _Fwd(code, Wx, Wgx, GA, params, starts[k, 0].contiguous(),
-                        starts[k, 1].contiguous(), starts[k, 2].contiguous(), rec, *bounds[k])
+                        starts[k, 1].contiguous(), starts[k, 2].contiguous(), rec, *bounds[k],
+                        ctx.ldx)
 
         gvec = torch.zeros((16, H), device=Wx.device, dtype=torch.float32)
         gscal = torch.zeros((3,), device=Wx.device, dtype=torch.float32)

@@ -295,6 +295,19 @@ def core_launch_check(code: int, B: int, T: int, H: int, backward: bool) -> int:
     return n
 
 
+def scan_inputs(Wx: Tensor, Wgx: Tensor, dt: torch.dtype) -> tuple[Tensor, Tensor, int]:
+    """(Wx, Wgx, ldx) as the scan reads them: unchanged when both are row-strided views
+    with unit element stride and a common time stride ldx (the two halves of one
+    [B, T, 2H] projection over [W; Wg]), else contiguous copies with ldx = H."""
+    B, T, H = Wx.shape
+    ldx = Wx.stride(1)
+    if (Wx.dtype == dt and Wgx.dtype == dt and Wx.stride(2) == 1 and Wgx.stride(2) == 1
+            and Wgx.stride(1) == ldx and ldx >= H and ldx % 8 == 0
+            and (B == 1 or (Wx.stride(0) == T * ldx and Wgx.stride(0) == T * ldx))):
+        return Wx, Wgx, ldx
+    return Wx.contiguous(), Wgx.to(dt).contiguous(), H
+
+
 @torch.library.custom_op(_q("core_scan_batched"), mutates_args=(), device_types="cuda")
 def core_scan_batched(
     Wx: Tensor, Wgx: Tensor, Ug: Tensor, A: Tensor, beta: Tensor, log_kappa: Tensor,
@@ -311,8 +324,7 @@ def core_scan_batched(
         raise ValueError("batched DABSN core received incompatible tensor shapes")
     dt = Wx.dtype
     code = _code(dt)
-    Wx_c = Wx.contiguous()
-    Wgx_c = Wgx.to(dt).contiguous()
+    Wx_c, Wgx_c, ldx = scan_inputs(Wx, Wgx, dt)
     GA = _derived(f"GA:{dt}", (Ug, A), lambda u, a: torch.cat((u, a), dim=0).to(dt).contiguous())
     params, keep = _core_params(
         (beta, log_kappa, logit_recover, k_s, k_y, k_b, k_n, k_bias, r_s, r_y, r_b, r_n, r_bias,
@@ -333,11 +345,11 @@ def core_scan_batched(
         raise RuntimeError(f"DABSN HIP core scan does not support H={H} for {dt}")
     core_launch_check(code, B, T, H, False)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=Wx.device)
+    call = _lib.CoreFwdCall(code, B, T, H, T, ldx, _p(Wx_c), _p(Wgx_c), _p(GA),
+                            ctypes.pointer(params), _p(b0), _p(e0), _p(c0), _p(U),
+                            *[_p(t) for t in tapes], *[_p(f) for f in finals], _p(ws), nbytes)
     tk = KernelTimer.begin("core_scan_fwd", Wx)
-    rc = lib.dabsn_hip_core_scan_fwd(
-        code, B, T, H, _p(Wx_c), _p(Wgx_c), _p(GA), ctypes.byref(params),
-        _p(b0), _p(e0), _p(c0), _p(U), *[_p(t) for t in tapes], *[_p(f) for f in finals],
-        _p(ws), nbytes, _stream(Wx))
+    rc = lib.dabsn_hip_core_scan_fwd_call(ctypes.byref(call), _stream(Wx))
     KernelTimer.end(tk)
     _lib.check(rc, "core scan forward")
     if T > 1:  # one-step scans have no step barrier that could time out

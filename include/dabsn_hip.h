@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 9
+#define DABSN_HIP_ABI_VERSION 10
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -105,6 +105,9 @@ int dabsn_hip_core_scan_bwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
 typedef struct dabsn_core_fwd_call {
   int dtype;
   int64_t B, T, H, ldt;
+  int64_t ldx; /* elements between consecutive time steps of Wx and Wgx: 0 = H (dense);
+                  2H reads the two halves of one [B, T, 2H] projection (core.py:281-282 as
+                  one GEMM over [W; Wg]). Above H it must be a multiple of 8. */
   const void *Wx, *Wgx, *GA;
   const dabsn_core_params* params;
   const float *b0, *e0, *c0;

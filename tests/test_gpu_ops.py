@@ -615,3 +615,47 @@ def test_read_output_equals_the_two_tensor_operations(cuda_device, pdt, ldt, gdt
     assert got[2].dtype == exp[2].dtype and got[2].shape == exp[2].shape
     tol = 1e-5 if gdt == torch.float32 else 1e-2
     assert abs(float(got[2]) - float(exp[2])) <= tol * max(abs(float(exp[2])), 1e-6)
+
+
+@pytest.mark.parametrize("dtype,B,T,H,chunk", [(torch.float32, 3, 37, 40, None),
+                                               (torch.bfloat16, 16, 70, 2048, None),
+                                               (torch.bfloat16, 16, 70, 2048, 32),
+                                               (torch.bfloat16, 40, 1, 2048, None),
+                                               (torch.float32, 5, 1, 64, None)])
+def test_core_scan_reads_the_two_halves_of_one_projection(cuda_device, dtype, B, T, H, chunk):
+    """Wx and Wgx as the two halves of one [B, T, 2H] tensor (the fused projection over
+    [W; Wg]) are read in place through the input row stride: outputs and gradients equal
+    the op on contiguous copies bit for bit (persistent scan, chunked pipeline, one-step
+    path)."""
+    from dabsn_amd.kernels.chunked import chunked_core_scan
+    inp = [t.to(cuda_device) for t in core_case(31, B, T, H)]
+    both = torch.cat([inp[0], inp[1]], dim=-1).to(dtype)
+    g = torch.Generator().manual_seed(32)
+
+    def run(wx, wgx):
+        leaves = [wx, wgx]
+        rest = [t.detach().clone().requires_grad_(True) for t in inp[2:]]
+        if chunk:
+            outs = chunked_core_scan(chunk, *leaves, *rest)
+        else:
+            outs = ops.core_scan_batched(*leaves, *rest)
+        seeds = [torch.randn(o.shape, generator=torch.Generator().manual_seed(40 + i)).to(o)
+                 for i, o in enumerate(outs)]
+        loss = sum((o.float() * s.float()).sum() for i, (o, s) in enumerate(zip(outs, seeds))
+                   if i != 7)
+        return [o.detach() for o in outs], torch.autograd.grad(loss, [*leaves, *rest],
+                                                               allow_unused=True)
+
+    strided = both.detach().clone().requires_grad_(True)
+    wx_v, wgx_v = strided.split(H, dim=-1)
+    assert wx_v.stride(1) == 2 * H
+    out_v, g_v = run(wx_v, wgx_v)
+    wx_c = both[..., :H].detach().contiguous().requires_grad_(True)
+    wgx_c = both[..., H:].detach().contiguous().requires_grad_(True)
+    out_c, g_c = run(wx_c, wgx_c)
+    for i, (a, b) in enumerate(zip(out_v, out_c)):
+        assert torch.equal(a, b), f"output {i}"
+    for i, (a, b) in enumerate(zip(g_v, g_c)):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.equal(a, b), f"grad {i}"
