@@ -186,6 +186,42 @@ __global__ void __launch_bounds__(NT) long_fwd_chunk(int B, int T, int H, const 
   }
 }
 
+// A sequence of at most one chunk (T <= CK: streaming decode, short query chunks): the
+// three recurrences walked once per channel from the given initial state, in the step
+// order of long.py:492-579 (as phase 3 above), with the final state taken from the walk.
+template <typename E>
+__global__ void __launch_bounds__(NT) long_fwd_single(int B, int T, int H, const E* w, const E* p,
+                                                      Logits lg, const float* L0, const float* E0,
+                                                      const float* R0, E* out, float* LF,
+                                                      float* EF, float* RF, float* states) {
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
+  if (ch >= static_cast<int64_t>(B) * H) return;
+  const Coef k = load_coef(lg.p);
+  const int b = static_cast<int>(ch / H), h = static_cast<int>(ch % H);
+  const size_t base = static_cast<size_t>(b) * T * H + h;
+  const size_t bth = static_cast<size_t>(B) * T * H;
+  float L = L0[ch], Ev = E0[ch], R = R0[ch];
+  for (int t = 0; t < T; ++t) {
+    const size_t o = base + static_cast<size_t>(t) * H;
+    const float wv = ld(w, o), pv = ld(p, o);
+    if (states) {
+      states[o] = L;
+      states[bth + o] = Ev;
+      states[2 * bth + o] = R;
+    }
+    const float pe = tanhf(fabsf(wv - Ev));
+    Ev = k.er * Ev + (1.0f - k.er) * wv;
+    R = k.rd * R + (1.0f - k.rd) * (1.0f - pe);
+    const float sal = pv * pe;
+    const float eff = k.ret + (1.0f - k.ret) * k.rs * R;
+    L = eff * L + (1.0f - eff) * (sal * wv);
+    st(out, o, L);
+  }
+  LF[ch] = L;
+  EF[ch] = Ev;
+  RF[ch] = R;
+}
+
 // Per-channel pass over chunks for state S (0 = L, 1 = E, 2 = R): the chunk-start value
 // goes to the checkpoint slot S; the state after the last chunk to `fin`.
 // x_{k+1} = a_k x_k + loc[k] with a_k = prod[k] (L) or coef^len_k (E: er, R: rd).
@@ -442,6 +478,12 @@ static int long_fwd_impl(int B, int T, int H, const E* w, const E* p, Logits lg,
   float* loc1 = ws + static_cast<size_t>(nseg) * B * H;
   float* ckpt = ws + 2 * static_cast<size_t>(nseg) * B * H;  // [B][nseg][3][H]
   const dim3 cg(gx, nseg), blk(NT);
+  if (nseg == 1) {  // one chunk: a single walk, no chunk-parallel passes
+    hipLaunchKernelGGL((long_fwd_single<E>), dim3(gx), blk, 0, stream, B, T, H, w, p, lg, L0, E0,
+                       R0, out, LF, EF, RF, states);
+    DABSN_HIP_CHECK(hipGetLastError());
+    return DABSN_OK;
+  }
   if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 0>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out, states);
   hipLaunchKernelGGL(long_fwd_carry<1>, dim3(gx), blk, 0, stream, B, T, H, lg, E0, loc0, loc1, ckpt, EF);
   if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 1>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out, states);
