@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _lock = threading.Lock()
 _lib = None
@@ -42,7 +42,7 @@ class CoreFwdCall(ctypes.Structure):
                  ("Wx", vp), ("Wgx", vp), ("GA", vp), ("params", ctypes.POINTER(CoreParams))]
                 + [(n, vp) for n in ("b0", "e0", "c0", "U", "nov", "plast", "expr", "write",
                                      "energy", "sat", "gate", "bF", "eF", "cF", "workspace")]
-                + [("workspace_bytes", sz)])
+                + [("workspace_bytes", sz), ("state_dtype", i32)])
 
 
 class CoreBwdCall(ctypes.Structure):
@@ -95,6 +95,9 @@ _SIGNATURES = {
     "dabsn_hip_read_output_partials": ([i64], sz),
     "dabsn_hip_read_output_bwd": (
         [i32, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
+    "dabsn_hip_read_mix": ([i32, i64, vp, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_rms_norm": ([i32, i64, i64, vp, vp, ctypes.c_float, vp, vp], i32),
+    "dabsn_hip_relu_square": ([i32, i64, vp, vp, vp], i32),
     "dabsn_hip_normalize_rows": ([i32, i64, i64, vp, vp, vp, vp], i32),
     "dabsn_hip_normalize_rows_bwd": ([i32, i64, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_select": ([i32, i32, i64, i64, vp, vp, vp, vp, vp, vp], i32),
@@ -133,6 +136,11 @@ _SIGNATURES = {
     "dabsn_hip_read3_decode": (
         [i32, i64, i64, i64, i64, vp, vp, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, PTR4,
          vp, vp, sz, vp],
+        i32,
+    ),
+    "dabsn_hip_read3_decode_members": (
+        [i32, i64, i64, i64, vp, vp, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, PTR4, vp, vp, sz,
+         vp],
         i32,
     ),
     "dabsn_hip_read3_decode_noalloc": (

@@ -28,6 +28,7 @@
 //     word and every workgroup exits.
 #include <algorithm>
 #include <initializer_list>
+#include <type_traits>
 
 #include "../../include/dabsn_hip.h"
 #include "capi.hpp"
@@ -281,7 +282,20 @@ struct FwdArgs {
   float* cF;
   uint8_t* ws;
   uint32_t slot_bytes;
+  int sbf;  // initial and final states are bf16 (else fp32), addressed through ld/st_state
 };
+
+// Carried-state elements: fp32, or bf16 when the state is carried in the activation dtype
+// (the final state rounded to nearest even, as a dtype conversion of the fp32 value).
+__device__ __forceinline__ float ld_state(const float* p, size_t i, int sbf) {
+  return sbf ? bf2f(reinterpret_cast<const bf16*>(p)[i]) : p[i];
+}
+__device__ __forceinline__ void st_state(float* p, size_t i, float v, int sbf) {
+  if (sbf)
+    reinterpret_cast<bf16*>(p)[i] = f2bf(v);
+  else
+    p[i] = v;
+}
 
 // The reverse scan reads the hard-sigmoid gradient mask (0 < s < 1) back from the gate
 // tape. A gate strictly inside (0, 1) whose nearest bf16 is exactly 0 or 1 is stored one
@@ -410,9 +424,9 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
 
   const UnitParams up = load_unit(a.P, c, is_pair && c < H);
   const StepGains sg = load_gains(a.P);
-  float sb = act ? a.b0[static_cast<size_t>(b) * H + c] : 0.0f;
-  float se = act ? a.e0[static_cast<size_t>(b) * H + c] : 0.0f;
-  float sc = act ? a.c0[static_cast<size_t>(b) * H + c] : 0.0f;
+  float sb = act ? ld_state(a.b0, static_cast<size_t>(b) * H + c, a.sbf) : 0.0f;
+  float se = act ? ld_state(a.e0, static_cast<size_t>(b) * H + c, a.sbf) : 0.0f;
+  float sc = act ? ld_state(a.c0, static_cast<size_t>(b) * H + c, a.sbf) : 0.0f;
   const size_t row0 = static_cast<size_t>(b) * static_cast<size_t>(a.ldt);
 
   float ycur = (act && T > 0) ? tanhf(ld(a.Wx, row0 * a.ldx + c) + sb) : 0.0f;
@@ -551,9 +565,9 @@ __device__ __forceinline__ void fwd_body(const FwdArgs<E>& a, int bid, int grid)
   }
   if (act) {
     const size_t i = static_cast<size_t>(b) * H + c;
-    a.bF[i] = sb;
-    a.eF[i] = se;
-    a.cF[i] = sc;
+    st_state(a.bF, i, sb, a.sbf);
+    st_state(a.eF, i, se, a.sbf);
+    st_state(a.cF, i, sc, a.sbf);
   }
 }
 
@@ -1114,7 +1128,8 @@ __global__ void __launch_bounds__(256) y0_kernel(FwdArgs<E> a, E* y0) {
   if (i >= static_cast<int64_t>(a.B) * a.H) return;
   const int b = static_cast<int>(i / a.H), c = static_cast<int>(i % a.H);
   st(y0, static_cast<size_t>(i),
-     tanhf(ld(a.Wx, static_cast<size_t>(b) * static_cast<size_t>(a.ldt) * a.ldx + c) + a.b0[i]));
+     tanhf(ld(a.Wx, static_cast<size_t>(b) * static_cast<size_t>(a.ldt) * a.ldx + c) +
+           ld_state(a.b0, static_cast<size_t>(i), a.sbf)));
 }
 
 template <typename E>
@@ -1125,7 +1140,8 @@ __global__ void __launch_bounds__(256) step1_kernel(FwdArgs<E> a, const float* G
   const int b = static_cast<int>(i / H), c = static_cast<int>(i % H);
   const UnitParams up = load_unit(a.P, c, true);
   const StepGains sg = load_gains(a.P);
-  const float sb = a.b0[i], se = a.e0[i], sc = a.c0[i];
+  const float sb = ld_state(a.b0, i, a.sbf), se = ld_state(a.e0, i, a.sbf),
+              sc = ld_state(a.c0, i, a.sbf);
   const size_t row0 = static_cast<size_t>(b) * static_cast<size_t>(a.ldt);
   const size_t rt = row0 * H + c;
   const size_t rx = row0 * a.ldx + c;
@@ -1146,9 +1162,9 @@ __global__ void __launch_bounds__(256) step1_kernel(FwdArgs<E> a, const float* G
   st(a.et, rt, se);
   st(a.ctp, rt, cpost);
   st(a.st, rt, gate_tape_value<E>(s_g));
-  a.bF[i] = bn;
-  a.eF[i] = en;
-  a.cF[i] = cpost;
+  st_state(a.bF, i, bn, a.sbf);
+  st_state(a.eF, i, en, a.sbf);
+  st_state(a.cF, i, cpost, a.sbf);
 }
 
 template <typename E, int CH, int KSTEPS, int NW>
@@ -1262,6 +1278,14 @@ static P* adv(P* p, size_t n) {
   return p ? p + n : p;
 }
 
+// A carried-state pointer advanced by n elements of the state's type (bf16 when sbf).
+template <typename P>
+static P* adv_state(P* p, size_t n, int sbf) {
+  if (!p || !sbf) return adv(p, n);
+  using B = std::conditional_t<std::is_const_v<P>, const uint16_t, uint16_t>;
+  return reinterpret_cast<P*>(reinterpret_cast<B*>(p) + n);
+}
+
 template <typename E>
 static FwdArgs<E> slab_of(const FwdArgs<E>& a, int g0, int ng) {
   FwdArgs<E> s = a;
@@ -1269,14 +1293,14 @@ static FwdArgs<E> slab_of(const FwdArgs<E>& a, int g0, int ng) {
   s.B = static_cast<int>(std::min<size_t>(static_cast<size_t>(ng) * NB, a.B - b0));
   s.Wx = adv(a.Wx, b0 * static_cast<size_t>(a.ldt) * a.ldx);
   s.Wgx = adv(a.Wgx, b0 * static_cast<size_t>(a.ldt) * a.ldx);
-  s.b0 = adv(a.b0, b0 * a.H);
-  s.e0 = adv(a.e0, b0 * a.H);
-  s.c0 = adv(a.c0, b0 * a.H);
+  s.b0 = adv_state(a.b0, b0 * a.H, a.sbf);
+  s.e0 = adv_state(a.e0, b0 * a.H, a.sbf);
+  s.c0 = adv_state(a.c0, b0 * a.H, a.sbf);
   s.U = adv(a.U, b0 * 2 * row);
   for (E** t : {&s.nov, &s.pl, &s.ay, &s.wr, &s.et, &s.ctp, &s.st}) *t = adv(*t, b0 * row);
-  s.bF = adv(a.bF, b0 * a.H);
-  s.eF = adv(a.eF, b0 * a.H);
-  s.cF = adv(a.cF, b0 * a.H);
+  s.bF = adv_state(a.bF, b0 * a.H, a.sbf);
+  s.eF = adv_state(a.eF, b0 * a.H, a.sbf);
+  s.cF = adv_state(a.cF, b0 * a.H, a.sbf);
   return s;
 }
 
@@ -1488,6 +1512,8 @@ static int check_fwd(const dabsn_core_fwd_call& f, Cfg& c) {
   DABSN_REQUIRE(f.Wx && f.Wgx && f.GA && f.b0 && f.e0 && f.c0 && f.bF && f.eF && f.cF &&
                     f.workspace,
                 "core scan: null pointer argument");
+  DABSN_REQUIRE(f.state_dtype == kF32 || f.state_dtype == kBF16,
+                "core scan: bad state dtype %d (0 = fp32, 1 = bf16)", f.state_dtype);
   DABSN_REQUIRE(f.T == 0 || (f.U && f.nov && f.plast && f.expr && f.write && f.energy && f.sat &&
                              f.gate),
                 "core scan: null tape pointer");
@@ -1559,7 +1585,8 @@ static FwdArgs<E> fwd_args(const dabsn_core_fwd_call& f, const Cfg& c) {
                     static_cast<E*>(f.expr), static_cast<E*>(f.write), static_cast<E*>(f.energy),
                     static_cast<E*>(f.sat), static_cast<E*>(f.gate), f.bF, f.eF, f.cF,
                     static_cast<uint8_t*>(f.workspace),
-                    static_cast<uint32_t>(slot_bytes(f.dtype, c, false))};
+                    static_cast<uint32_t>(slot_bytes(f.dtype, c, false)),
+                    f.state_dtype == kBF16 ? 1 : 0};
 }
 
 template <typename E>
@@ -1656,7 +1683,7 @@ int dabsn_hip_core_scan_fwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
                             size_t workspace_bytes_, hipStream_t stream) {
   const dabsn_core_fwd_call f{dtype, B, T, H, 0, 0, Wx, Wgx, GA, params, b0, e0, c0, U, nov,
                               plast, expr, write, energy, sat, gate, bF, eF, cF, workspace,
-                              workspace_bytes_};
+                              workspace_bytes_, kF32};
   return dabsn_hip_core_scan_fwd_call(&f, stream);
 }
 

@@ -922,6 +922,50 @@ __global__ void __launch_bounds__(256) decode_meta_kernel(int N, int64_t Nb, int
   meta[bj] = m;
 }
 
+// The same metadata read straight from a carried bank's kept glue and admitted-slot lists
+// (one query row, the bank's last live position Nb - 1): slot j of batch row b is
+// members[b, j], valid below max(count[b], 1); next_idx = min(idx + 1, Nb - 1), read_idx =
+// idx - qstart, and the bank cocktail, key bias and admission are taken at idx. Every
+// per-position array has row stride ld (stats: ld * 6, the write norm in column 5; cocktail:
+// ld * 4). Thread 0 of each batch row also writes the row's slot bound nhi = min(N,
+// max(count, 1)): every allowed slot is valid, so it bounds them, and slots below it that
+// are not allowed carry flags 0.
+__global__ void __launch_bounds__(256) decode_meta_members_kernel(
+    int N, int64_t Nb, int64_t ld, int64_t qstart, const float* stats, const int64_t* members,
+    const int64_t* counts, const float* cocktail, const float* key_bias, const float* admission,
+    Gains g, SlotMeta* meta, int32_t* rs) {
+  const int b = blockIdx.y;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const int64_t cnt = counts[b] < 1 ? 1 : counts[b];
+  if (j == 0) {
+    int32_t* s = rs + static_cast<size_t>(b) * 3;
+    s[0] = 0;
+    s[1] = 0;
+    s[2] = static_cast<int32_t>(cnt < N ? cnt : N);
+  }
+  if (j >= N) return;
+  const size_t bl = static_cast<size_t>(b) * ld;
+  const int64_t i = members[bl + j];
+  const int64_t n = i + 1 < Nb - 1 ? i + 1 : Nb - 1;
+  const int64_t ic = i < 0 ? 0 : (i >= Nb ? Nb - 1 : i);
+  const int64_t nc = n < 0 ? 0 : n;
+  const float* ckt = cocktail + (bl + Nb - 1) * 4;
+  const float* cbj = cocktail + (bl + ic) * 4;
+  const float cc = ckt[0] * cbj[0] + ckt[1] * cbj[1] + ckt[2] * cbj[2] + ckt[3] * cbj[3];
+  const bool v = j < cnt;
+  const int64_t ri = i - qstart;
+  SlotMeta m;
+  m.row = static_cast<uint32_t>(bl + ic);
+  m.nrow = static_cast<uint32_t>(bl + nc);
+  m.rn = 1.0f / fmaxf(stats[(bl + ic) * 6 + 5], kNormEps);
+  m.kb = key_bias[bl + ic];
+  m.adm = admission[bl + ic];
+  m.ccg = cc * g.p[3][0];
+  m.flags = (allow_at(0, ri, v, 0) ? 1u : 0u) | (induct_at(0, ri, v, 0, 1) ? 2u : 0u);
+  m.pad = 0u;
+  meta[static_cast<size_t>(b) * N + j] = m;
+}
+
 // NC chunks of 8 elements of one bank row, chunk k at element 8 * (lane + 64 k) (clamped
 // to the row's last chunk; lanes past the row hold a copy and a zero query).
 template <typename E, int NC>
@@ -1308,6 +1352,29 @@ static DecodePlan decode_plan(int dtype, int64_t B, int64_t T, int64_t N, int64_
   return p;
 }
 
+// The single pass and the split combine, from slot metadata and row bounds already in the
+// workspace (decode_meta_kernel after ranges_kernel, or decode_meta_members_kernel).
+template <typename E>
+static int decode_pass(int64_t B, int64_t N, int64_t H, const E* q, const E* bank,
+                       const SlotMeta* meta, const int32_t* rs, const float* scale, Gains g, E* out,
+                       uint8_t* ws, const DecodePlan& p, hipStream_t stream) {
+  float* pacc = reinterpret_cast<float*>(ws + p.off_pacc);
+  float* pstats = reinterpret_cast<float*>(ws + p.off_pstats);
+  FusedArgs<E> fa{(int)N, (int)H, p.splits, p.per_split, q, bank, meta, rs, scale, pacc, pstats};
+  const dim3 grid((unsigned)(B * p.splits));
+  if (H <= 512)
+    hipLaunchKernelGGL((decode_fused_kernel<E, 1>), grid, dim3(64), 0, stream, fa);
+  else if (H <= 1024)
+    hipLaunchKernelGGL((decode_fused_kernel<E, 2>), grid, dim3(64), 0, stream, fa);
+  else
+    hipLaunchKernelGGL((decode_fused_kernel<E, 4>), grid, dim3(64), 0, stream, fa);
+  DABSN_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(decode_combine_kernel<E>, dim3((unsigned)((H + 1023) / 1024), (unsigned)B),
+                     dim3(256), 0, stream, (int)H, p.splits, pacc, pstats, g, out);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
 template <typename E>
 static int decode_impl(int64_t B, int64_t T, int64_t N, int64_t H, int64_t Nb, int64_t rowld,
                        const E* q, const E* bank, const float* norm_w, const int64_t* idx,
@@ -1320,8 +1387,6 @@ static int decode_impl(int64_t B, int64_t T, int64_t N, int64_t H, int64_t Nb, i
     int32_t* rs = reinterpret_cast<int32_t*>(ws + p.off_rs);
     int32_t* ro = reinterpret_cast<int32_t*>(ws + p.off_ro);
     SlotMeta* meta = reinterpret_cast<SlotMeta*>(ws + p.off_meta);
-    float* pacc = reinterpret_cast<float*>(ws + p.off_pacc);
-    float* pstats = reinterpret_cast<float*>(ws + p.off_pstats);
     // Query tiles only (grid QT): nhi per batch row; no bank-tile ranges are needed.
     hipLaunchKernelGGL(ranges_kernel, dim3((unsigned)QT, (unsigned)B), dim3(256), 0, stream,
                        (int)T, (int)N, (int)H, 0, read_idx, valid, rs, ro, nullptr);
@@ -1330,19 +1395,7 @@ static int decode_impl(int64_t B, int64_t T, int64_t N, int64_t H, int64_t Nb, i
                        0, stream, (int)N, Nb, rowld, norm_w, idx, next_idx, read_idx, valid, ck, cb,
                        kb, adm, g, meta);
     DABSN_HIP_CHECK(hipGetLastError());
-    FusedArgs<E> fa{(int)N, (int)H, p.splits, p.per_split, q, bank, meta, rs, scale, pacc, pstats};
-    const dim3 grid((unsigned)(B * p.splits));
-    if (H <= 512)
-      hipLaunchKernelGGL((decode_fused_kernel<E, 1>), grid, dim3(64), 0, stream, fa);
-    else if (H <= 1024)
-      hipLaunchKernelGGL((decode_fused_kernel<E, 2>), grid, dim3(64), 0, stream, fa);
-    else
-      hipLaunchKernelGGL((decode_fused_kernel<E, 4>), grid, dim3(64), 0, stream, fa);
-    DABSN_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(decode_combine_kernel<E>, dim3((unsigned)((H + 1023) / 1024), (unsigned)B),
-                       dim3(256), 0, stream, (int)H, p.splits, pacc, pstats, g, out);
-    DABSN_HIP_CHECK(hipGetLastError());
-    return DABSN_OK;
+    return decode_pass<E>(B, N, H, q, bank, meta, rs, scale, g, out, ws, p, stream);
   }
   float* S = reinterpret_cast<float*>(ws + p.off_S);
   int32_t* rs = reinterpret_cast<int32_t*>(ws + p.off_rs);
@@ -1590,6 +1643,50 @@ int dabsn_hip_read3_decode(int dtype, int64_t B, int64_t T, int64_t N, int64_t H
                             norm_w, idx, next_idx, read_idx, valid, cocktail, bank_cocktail,
                             key_bias, admission, scale, g, (float*)out, (uint8_t*)workspace, p,
                             stream);
+}
+
+int dabsn_hip_read3_decode_members(int dtype, int64_t B, int64_t N, int64_t H, const void* q,
+                                   const void* bank, int64_t bank_len, int64_t bank_ld,
+                                   const float* stats, const int64_t* members,
+                                   const int64_t* counts, int64_t query_start,
+                                   const float* cocktail, const float* key_bias,
+                                   const float* admission, const float* scale,
+                                   const float* const* gains, void* out, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream) {
+  const int rc = read3_checks(dtype, B, 1, N, H, 0);
+  if (rc != DABSN_OK) return rc;
+  DABSN_REQUIRE(H % 8 == 0 && H <= 64 * 8 * kFusedMaxChunks,
+                "read3 decode (members): H=%lld must be a multiple of 8 and at most %d",
+                (long long)H, 64 * 8 * kFusedMaxChunks);
+  DABSN_REQUIRE(N > 0 && N <= bank_ld && bank_len > 0 && bank_ld >= bank_len,
+                "read3 decode (members): bad bank shape");
+  DABSN_REQUIRE(B * bank_ld <= static_cast<int64_t>(UINT32_MAX),
+                "read3 decode (members): B * bank_ld = %lld bank rows exceeds 2^32 - 1",
+                (long long)(B * bank_ld));
+  DABSN_REQUIRE(q && bank && stats && members && counts && cocktail && key_bias && admission &&
+                    scale && gains && out && workspace,
+                "read3 decode (members): null pointer");
+  for (int i = 0; i < 4; ++i) DABSN_REQUIRE(gains[i], "read3 decode (members): null gain %d", i);
+  const void* vec[] = {q, bank, out};
+  for (const void* v : vec)
+    DABSN_REQUIRE((reinterpret_cast<uintptr_t>(v) & 15u) == 0,
+                  "read3 decode (members): q, bank and out must be 16-byte aligned");
+  const DecodePlan p = decode_plan(dtype, B, 1, N, H);
+  DABSN_REQUIRE(p.fused, "read3 decode (members): no single-pass plan");
+  DABSN_REQUIRE(workspace_bytes >= p.end, "read3 decode (members): workspace %zu < %zu",
+                workspace_bytes, p.end);
+  Gains g{{gains[0], gains[1], gains[2], gains[3]}};
+  int32_t* rs = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + p.off_rs);
+  SlotMeta* meta = reinterpret_cast<SlotMeta*>(static_cast<uint8_t*>(workspace) + p.off_meta);
+  hipLaunchKernelGGL(decode_meta_members_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)B),
+                     dim3(256), 0, stream, (int)N, bank_len, bank_ld, query_start, stats, members,
+                     counts, cocktail, key_bias, admission, g, meta, rs);
+  DABSN_HIP_CHECK(hipGetLastError());
+  if (dtype == kBF16)
+    return decode_pass<bf16>(B, N, H, (const bf16*)q, (const bf16*)bank, meta, rs, scale, g,
+                             (bf16*)out, (uint8_t*)workspace, p, stream);
+  return decode_pass<float>(B, N, H, (const float*)q, (const float*)bank, meta, rs, scale, g,
+                            (float*)out, (uint8_t*)workspace, p, stream);
 }
 
 }  // extern "C"

@@ -331,15 +331,19 @@ def core_scan_batched(
          logit_c_decay, k_c, r_c),
         (logit_alpha, log_lambda, logit_c_suppress),
     )
-    b0, e0, c0 = (x.float().contiguous() for x in (initial_b, initial_e, initial_c))
+    states = (initial_b, initial_e, initial_c)
+    # A state carried in bf16 is read and written in bf16 by the kernels (the final state
+    # rounded as the fp32 result's conversion would round it); any other mix runs in fp32.
+    sdt = (torch.bfloat16 if all(x.dtype == torch.bfloat16 for x in states) else torch.float32)
+    b0, e0, c0 = (x.to(sdt).contiguous() for x in states)
     for x in (b0, e0, c0):
         if x.shape != (B, H):
             raise ValueError(f"initial state must have shape {(B, H)}, got {tuple(x.shape)}")
     U = torch.empty((B, T, 2 * H), device=Wx.device, dtype=dt)
     tapes = [torch.empty((B, T, H), device=Wx.device, dtype=dt) for _ in range(7)]
     if T == 0:
-        return (U, *tapes, *(s.clone() for s in (initial_b, initial_e, initial_c)))
-    finals = [torch.empty((B, H), device=Wx.device, dtype=torch.float32) for _ in range(3)]
+        return (U, *tapes, *(s.clone() for s in states))
+    finals = [torch.empty((B, H), device=Wx.device, dtype=sdt) for _ in range(3)]
     nbytes = lib.dabsn_hip_core_scan_workspace_bytes(code, B, H, 0)
     if nbytes == 0:
         raise RuntimeError(f"DABSN HIP core scan does not support H={H} for {dt}")
@@ -347,7 +351,8 @@ def core_scan_batched(
     ws = torch.empty(nbytes, dtype=torch.uint8, device=Wx.device)
     call = _lib.CoreFwdCall(code, B, T, H, T, ldx, _p(Wx_c), _p(Wgx_c), _p(GA),
                             ctypes.pointer(params), _p(b0), _p(e0), _p(c0), _p(U),
-                            *[_p(t) for t in tapes], *[_p(f) for f in finals], _p(ws), nbytes)
+                            *[_p(t) for t in tapes], *[_p(f) for f in finals], _p(ws), nbytes,
+                            _code(sdt))
     tk = KernelTimer.begin("core_scan_fwd", Wx)
     rc = lib.dabsn_hip_core_scan_fwd_call(ctypes.byref(call), _stream(Wx))
     KernelTimer.end(tk)
@@ -355,7 +360,7 @@ def core_scan_batched(
     if T > 1:  # one-step scans have no step barrier that could time out
         _record_error_word(ws, "core scan forward")
     del keep
-    fb, fe, fc = (f.to(s.dtype) for f, s in zip(finals, (initial_b, initial_e, initial_c)))
+    fb, fe, fc = (f.to(s.dtype) for f, s in zip(finals, states))
     return (U, *tapes, fb, fe, fc)
 
 
@@ -1346,6 +1351,48 @@ def read3_decode(query: Tensor, bank_write: Tensor, norm_w: Tensor, idx: Tensor,
     return out
 
 
+def read3_decode_members(query: Tensor, write: Tensor, stats: Tensor, length: int, width: int,
+                         members: Tensor, counts: Tensor, query_start: int, cocktail: Tensor,
+                         key_bias: Tensor, admission: Tensor, scale: Tensor,
+                         gains: tuple[Tensor, Tensor, Tensor, Tensor]) -> Tensor:
+    """``read3_decode`` of one query row per batch row with the slots taken from a carried
+    bank's admitted-slot lists: ``write`` [B, cap, H], ``stats`` [B, cap, 6], ``members``
+    [B, cap], ``cocktail`` [B, cap, 4], ``key_bias`` / ``admission`` [B, cap] are the bank's
+    whole storage (the first ``length`` positions live), ``counts`` [B] the members per row;
+    the read covers the first ``width`` slots. Equals ``read3_decode`` on idx =
+    members[:, :width], valid = j < max(count, 1), next_idx = min(idx + 1, length - 1),
+    read_idx = idx - query_start and the glue gathered at idx, without materialising them."""
+    _require_cuda(query)
+    lib = _lib.load()
+    dt = query.dtype
+    B, T, H = query.shape
+    cap = int(write.shape[1])
+    if T != 1 or not query.is_contiguous() or write.dtype != dt or not write.is_contiguous():
+        raise ValueError("read3_decode_members: one contiguous query row per batch row and a "
+                         "contiguous bank of the query's dtype")
+    for t, shape, tdt in ((stats, (B, cap, 6), torch.float32), (members, (B, cap), torch.int64),
+                          (counts, (B,), torch.int64), (cocktail, (B, cap, 4), torch.float32),
+                          (key_bias, (B, cap), torch.float32),
+                          (admission, (B, cap), torch.float32)):
+        if tuple(t.shape) != shape or t.dtype != tdt or not t.is_contiguous():
+            raise ValueError(f"read3_decode_members: expected a contiguous {tdt} tensor of "
+                             f"shape {shape}, got {tuple(t.shape)} {t.dtype}")
+    g = [_f32_scalar(x) for x in gains]
+    sc = _f32_scalar(scale)
+    out = torch.empty_like(query)
+    code = _code(dt)
+    nbytes = lib.dabsn_hip_read3_decode_workspace_bytes(code, B, 1, width, H)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=query.device)
+    ptrs = _lib.PTR4(*[x.data_ptr() for x in g])
+    tk = KernelTimer.begin("read3_decode", query)
+    _lib.check(lib.dabsn_hip_read3_decode_members(
+        code, B, int(width), H, _p(query), _p(write), int(length), cap, _p(stats), _p(members),
+        _p(counts), int(query_start), _p(cocktail), _p(key_bias), _p(admission), _p(sc), ptrs,
+        _p(out), _p(ws), ws.numel(), _stream(query)), "three-way decode read (members)")
+    KernelTimer.end(tk)
+    return out
+
+
 CompactGradients = tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
                          Tensor, Tensor, Tensor, Tensor]
 
@@ -1735,6 +1782,57 @@ if NAMESPACE != "dabsn":
                       reason="DABSN_AMD_OP_NAMESPACE is set" if os.environ.get(
                           "DABSN_AMD_OP_NAMESPACE") else
                       "the reference's dabsn:: operators are registered in this process")
+
+
+# ---- block glue (inference on the device, no autograd) ----------------------------------
+def _same_dtype(*ts: Tensor) -> bool:
+    dt = ts[0].dtype
+    return dt in _DTYPES and all(t.dtype == dt and t.is_cuda for t in ts)
+
+
+def read_mix(proj: Tensor, long: Tensor, long_gain: Tensor, y: Tensor,
+             read_gain: Tensor) -> Tensor:
+    """``y + read_gain * (proj + long_gain * long)`` in one pass: the read's output
+    (read.py:435, 821) fed into the block's mix (model.py:336), each product and sum
+    rounded to the common dtype as the unfused tensor operations round them. All five
+    tensors share one dtype (the gains hold one element each)."""
+    if not _same_dtype(proj, long, long_gain, y, read_gain) or proj.shape != long.shape \
+            or proj.shape != y.shape or long_gain.numel() != 1 or read_gain.numel() != 1:
+        raise ValueError("read_mix: proj, long and y must match and share the gains' dtype")
+    lib = _lib.load()
+    pc, lc, yc = proj.contiguous(), long.contiguous(), y.contiguous()
+    # held until the launch: a temporary's block could be handed to the next allocation
+    lg, rg = _f32_scalar(long_gain), _f32_scalar(read_gain)
+    out = torch.empty_like(yc)
+    _lib.check(lib.dabsn_hip_read_mix(_code(pc.dtype), pc.numel(), _p(pc), _p(lc), _p(lg),
+                                      _p(yc), _p(rg), _p(out), _stream(pc)), "read mix")
+    return out
+
+
+def rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    """MLPRMSNorm (model.py:35-45) in one kernel: ``(x.float() * rsqrt(mean(x^2) + eps))``
+    rounded to x's dtype, times ``weight`` (same dtype as x)."""
+    if not _same_dtype(x, weight) or weight.dim() != 1 or weight.shape[0] != x.shape[-1]:
+        raise ValueError("rms_norm: x and weight [H] must share a dtype on the device")
+    lib = _lib.load()
+    xc, wc = x.contiguous(), weight.contiguous()
+    H = int(x.shape[-1])
+    out = torch.empty_like(xc)
+    _lib.check(lib.dabsn_hip_rms_norm(_code(xc.dtype), xc.numel() // H, H, _p(xc), _p(wc),
+                                      float(eps), _p(out), _stream(xc)), "rms norm")
+    return out
+
+
+def relu_square(x: Tensor) -> Tensor:
+    """``F.relu(x).square()`` in one kernel."""
+    if not _same_dtype(x):
+        raise ValueError("relu_square: a float32 or bfloat16 device tensor is required")
+    lib = _lib.load()
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    _lib.check(lib.dabsn_hip_relu_square(_code(xc.dtype), xc.numel(), _p(xc), _p(out),
+                                         _stream(xc)), "relu square")
+    return out
 
 
 def _direct(op):

@@ -124,7 +124,8 @@ class BankStore:
             # The reference's admission is a bf16 tensor when tapes and gains are: its floor
             # is rounded to bf16 too (as in bank_select).
             adm_bf16 = tape_dtype == torch.bfloat16 and rp.adm_bias.dtype == torch.bfloat16
-            window = torch.nn.functional.softplus(read.admit_window.detach())
+            window = ops._derived("admit_window_f32", (read.admit_window,),
+                                  lambda w: torch.nn.functional.softplus(w).float().reshape(()))
             ops.admit_step(self.stats, hidden, prm, tape_dtype, window, lo, length - lo,
                            self.key_bias, self.adm, self.cocktail, self.amax, self.mcount,
                            self.members, adm_bf16)
@@ -328,12 +329,12 @@ def _block_step(block: DABSNBlock, inputs: Tensor, layer: LayerMemory | None,
     bank_write, bank_stats = bank.live()
     # Decode-sized steps read at the full bank width (no host sync per layer and token).
     width = bank.length if int(inputs.shape[1]) <= 8 else None
-    retrieved, final_long = block.read.forward_query_bank_stats(
+    mixed, final_long = block.read.forward_query_bank_stats(
         y, budget, expression, write, plasticity, query_stats=stats, bank_write=bank_write,
         bank_stats=bank_stats, query_start=position,
         initial_long_state=None if layer is None else layer.long, bank_width=width,
-        bank_store=bank if _INCREMENTAL_ADMISSION else None)
-    out = block.finish(inputs, block.state_to_hidden(y + block.read_gain * retrieved))
+        bank_store=bank if _INCREMENTAL_ADMISSION else None, mix=(y, block.read_gain))
+    out = block.finish(inputs, block.state_to_hidden(mixed))
     return block.forward_mlp(out), LayerMemory(bank=bank, core=final_core, long=final_long)
 
 

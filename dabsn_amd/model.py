@@ -22,6 +22,7 @@ from torch import Tensor
 from torch.utils.checkpoint import checkpoint
 
 from .core import DABSNCore
+from .kernels import ops
 from .read import DABSNRead
 
 
@@ -136,6 +137,10 @@ class DABSNBlock(nn.Module):
     def forward_mlp(self, hidden: Tensor) -> Tensor:
         if self.mlp_fc2 is None:
             return hidden
+        if not torch.is_grad_enabled() and ops._same_dtype(hidden, self.mlp_norm.weight):
+            # Inference on the device: the norm and the squared ReLU as one kernel each.
+            normed = ops.rms_norm(hidden, self.mlp_norm.weight, self.mlp_norm.eps)
+            return hidden + self.mlp_fc2(ops.relu_square(self.mlp_fc1(normed)))
         return hidden + self.mlp_fc2(F.relu(self.mlp_fc1(self.mlp_norm(hidden))).square())
 
     def forward(self, inputs: Tensor) -> Tensor:

@@ -54,7 +54,15 @@ class _AdmittedReadParameters(nn.Module):
         h = y.shape[-1]
         lead = y.shape[:-1]
         w = self.out.weight
-        y2, b2, r2 = (x.reshape(-1, h) for x in (y, budget, retrieved))
+        r2 = retrieved.reshape(-1, h)
+        if not torch.is_grad_enabled() and _side_by_side(y, budget):
+            # Inference on the core's trajectory: y and budget are its two halves, so
+            # [y, budget] is one [.., 2H] view and its block of the weight one product.
+            yb = torch.as_strided(y, (*lead, 2 * h), y.stride(), y.storage_offset())
+            out = F.linear(yb.reshape(-1, 2 * h), w[:, :2 * h], self.out.bias)
+            out = torch.addmm(out, r2, w[:, 2 * h:].t())
+            return out.reshape(*lead, out.shape[-1])
+        y2, b2 = (x.reshape(-1, h) for x in (y, budget))
         out = F.linear(r2, w[:, 2 * h:], self.out.bias)
         out = torch.addmm(out, y2, w[:, :h].t())
         out = torch.addmm(out, b2, w[:, h:2 * h].t())
@@ -63,6 +71,14 @@ class _AdmittedReadParameters(nn.Module):
     def key_bias_from_means(self, mean_n, mean_p, hidden: int) -> Tensor:
         return (self.p_gain * torch.log1p(mean_p * hidden) + self.novelty_gain * mean_n
                 + self.null_bias)
+
+
+def _side_by_side(a: Tensor, b: Tensor) -> bool:
+    """b starts right after a's last element along the unit-stride last dim, with a's
+    shape and strides: [a, b] is one view of twice the width."""
+    return (a.shape == b.shape and a.stride() == b.stride() and a.dim() > 0
+            and a.stride(-1) == 1 and a.dtype == b.dtype and a.device == b.device
+            and b.data_ptr() == a.data_ptr() + a.shape[-1] * a.element_size())
 
 
 def _cocktail(mean_e, mean_c, mean_n, mean_p) -> Tensor:
@@ -163,8 +179,55 @@ class DABSNRead(nn.Module):
             "cocktail": torch.gather(cocktail_bank, 1, idx.unsqueeze(-1).expand(-1, -1, 4)),
             "key_bias": torch.gather(key_bias, 1, idx),
             "admission": torch.gather(admission, 1, idx),
-            "scale": (F.softplus(self.short_read.log_temp) + 1.0) * (self.hidden_dim ** 0.5),
+            "scale": self._scale(),
             "read_idx": idx if query_start == 0 else idx - query_start,
+        }
+
+    def _scale(self, fp32: bool = False) -> Tensor:
+        """The read's score scale (softplus(log_temp) + 1) * sqrt(H) (read.py:240), in
+        log_temp's dtype (``fp32``: then converted to an fp32 scalar); without autograd, a
+        copy kept while log_temp is unchanged."""
+        h = self.hidden_dim ** 0.5
+        build = lambda t: (F.softplus(t) + 1.0) * h  # noqa: E731
+        if torch.is_grad_enabled():
+            return build(self.short_read.log_temp)
+        if fp32:
+            return ops._derived(f"read_scale_f32:{self.hidden_dim}", (self.short_read.log_temp,),
+                                lambda t: build(t).float().reshape(()).contiguous())
+        return ops._derived(f"read_scale:{self.hidden_dim}", (self.short_read.log_temp,), build)
+
+    def _read_members(self, query: Tensor, store, length: int, width: int,
+                      query_start: int) -> Tensor:
+        """The one-row decode read with the slots taken from ``store``'s admitted-slot
+        lists inside the kernel (``ops.read3_decode_members``): the streaming step's
+        selection, glue gathers and read in three launches."""
+        n_max = max(1, min(int(width), length))
+        self.last_n_max = n_max
+        hidden = int(query.shape[-1])
+        dtype = "bf16" if query.dtype == torch.bfloat16 else "fp32"
+        events.announce("admitted_three_way_read", "rocm_decode_bank_in_place",
+                        B=int(query.shape[0]), T=1, H=hidden, dtype=dtype)
+        retrieved = ops.read3_decode_members(
+            query, store.write, store.stats, length, n_max, store.members, store.mcount,
+            int(query_start), store.cocktail, store.key_bias, store.adm, self._scale(True),
+            (self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain))
+        self.last_read_contract = self._contract(True, n_max, length, query, query_start)
+        return retrieved
+
+    def _contract(self, decode: bool, n_max: int, length: int, query: Tensor,
+                  query_start: int) -> dict[str, object]:
+        paths = 2 if self.read_geometry == "hybrid" else 1
+        return {
+            "read_strategy": "rocm_decode_bank_in_place" if decode else "rocm_compact_admitted_bank",
+            "exact": True,
+            "max_admitted_bank": int(n_max),
+            "bank_growth": "grows_with_T" if n_max >= length else "data_dependent",
+            "estimated_read_work": int(query.shape[0]) * int(query.shape[1]) * int(n_max) * 3
+            * paths,
+            "admission_policy": ("causal_write_prefix_max" if self.read_geometry == "seq"
+                                 else "whole_sequence_max"),
+            "kernel_backend": "rocm_hip_mfma",
+            "query_start": int(query_start),
         }
 
     def _read_core(self, query, cocktail, bank_write, norm_w, key_bias, admission, length: int,
@@ -224,19 +287,7 @@ class DABSNRead(nn.Module):
                     self.cocktail_gain)
 
             retrieved = self._geometry_mix(read, valid, query)
-        paths = 2 if self.read_geometry == "hybrid" else 1
-        self.last_read_contract = {
-            "read_strategy": "rocm_decode_bank_in_place" if decode else "rocm_compact_admitted_bank",
-            "exact": True,
-            "max_admitted_bank": int(n_max),
-            "bank_growth": "grows_with_T" if n_max >= length else "data_dependent",
-            "estimated_read_work": int(query.shape[0]) * int(query.shape[1]) * int(n_max) * 3
-            * paths,
-            "admission_policy": ("causal_write_prefix_max" if self.read_geometry == "seq"
-                                 else "whole_sequence_max"),
-            "kernel_backend": "rocm_hip_mfma",
-            "query_start": int(query_start),
-        }
+        self.last_read_contract = self._contract(decode, n_max, length, query, query_start)
         return retrieved
 
     def _require_seq(self) -> None:
@@ -378,7 +429,7 @@ class DABSNRead(nn.Module):
     def forward_query_bank_stats(self, y, budget, expression, write, plasticity, *,
                                  query_stats, bank_write, bank_stats, query_start: int,
                                  initial_long_state=None, bank_width: int | None = None,
-                                 bank_store=None):
+                                 bank_store=None, mix: tuple[Tensor, Tensor] | None = None):
         """forward_query_bank with the bank given as its write vectors plus per-position
         statistics instead of full-width tapes.
 
@@ -393,7 +444,9 @@ class DABSNRead(nn.Module):
         the slot-list width (no host sync for the admitted count). ``bank_store`` (a
         carried bank, inference on the device) keeps the glue and the admitted-slot list of
         every position it holds and extends them with the new positions only
-        (``BankStore.admission``) instead of recomputing them over the bank.
+        (``BankStore.admission``) instead of recomputing them over the bank. ``mix`` =
+        (y, read_gain) returns the block's ``y + read_gain * output`` (model.py:336) in
+        place of the output (one kernel without autograd).
 
         Returns (output, final long state)."""
         self._require_seq()
@@ -405,10 +458,16 @@ class DABSNRead(nn.Module):
         query = ops.direct.normalize_rows(expression, query_stats[..., 4].detach())
         tape_dtype = bank_write.dtype
         members = None
+        retrieved = None
         if bank_store is not None and not torch.is_grad_enabled() and bank_stats.is_cuda:
             key_bias, admission, bank_cocktail, members = bank_store.admission(
                 self, hidden, tape_dtype, int(bank_len))
             rows = int(expression.shape[1])
+            width = bank_width or self._capture_bank_width
+            if (rows == 1 and width and hidden % 8 == 0 and hidden <= 2048
+                    and query.dtype == bank_store.write.dtype):
+                retrieved = self._read_members(query, bank_store, int(bank_len), int(width),
+                                               int(query_start))
             cocktails = (bank_cocktail[:, bank_len - rows:], bank_cocktail)
         elif not torch.is_grad_enabled() and bank_stats.is_cuda:
             # Inference (streaming decode): the per-position glue of the whole bank in one
@@ -426,14 +485,22 @@ class DABSNRead(nn.Module):
             key_bias = rp.key_bias_from_means(bn, bp, hidden)
             admission = rp.admission_from_means(be, bc, bn, bp, hidden)
             cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
-        retrieved = self._read_core(query, cocktails, bank_write, bank_stats[..., 5].detach(),
-                                    key_bias, admission, bank_len, int(query_start), bank_width,
-                                    members)
+        if retrieved is None:
+            retrieved = self._read_core(query, cocktails, bank_write,
+                                        bank_stats[..., 5].detach(), key_bias, admission,
+                                        bank_len, int(query_start), bank_width, members)
         short_output = rp.project(y, budget, retrieved.to(y.dtype))
         long, final_state = self._long_scan_from_state(write, plasticity, None,
                                                        initial_state=initial_long_state,
                                                        return_final_state=True)
-        return ops.direct.read_output(short_output, long, self.long_gain), final_state
+        if mix is None:
+            return ops.direct.read_output(short_output, long, self.long_gain), final_state
+        y_mix, gain = mix
+        if not torch.is_grad_enabled() and ops._same_dtype(short_output, long, self.long_gain,
+                                                           y_mix, gain):
+            return ops.read_mix(short_output, long, self.long_gain, y_mix, gain), final_state
+        read = ops.direct.read_output(short_output, long, self.long_gain)
+        return y_mix + gain * read, final_state
 
 
 def collect_traces_enabled() -> bool:

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 10
+#define DABSN_HIP_ABI_VERSION 11
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -115,6 +115,10 @@ typedef struct dabsn_core_fwd_call {
   float *bF, *eF, *cF;
   void* workspace;
   size_t workspace_bytes;
+  int state_dtype; /* type of b0, e0, c0 and of bF, eF, cF: 0 = fp32, 1 = bf16 (the state
+                      carried in the activation dtype, as the reference's streaming memory
+                      does, src/dabsn/memory.py:228-232; the final state rounded to nearest
+                      even). The pointers keep their float* type either way. */
 } dabsn_core_fwd_call;
 
 typedef struct dabsn_core_bwd_call {
@@ -270,6 +274,23 @@ int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_
                               const void* K, const void* gK, const void* gV, const void* gVn,
                               void* gw, hipStream_t stream);
 
+/* ---- block glue (inference) ---------------------------------------------------------
+ * The element work around one block's read and its MLP branch, each as one kernel, for the
+ * streaming step (no backward). All tensors dense in `dtype`; every intermediate the
+ * reference stores in that dtype is rounded to it here too. */
+/* out = y + read_gain * (proj + long_gain * long): the read's output (read.py:435, 821:
+ * out(...) + long_gain * long) fed into the block's mix (model.py:336:
+ * y + read_gain * read). n elements; gains are fp32 scalars holding values of `dtype`. */
+int dabsn_hip_read_mix(int dtype, int64_t n, const void* proj, const void* lng,
+                       const float* long_gain, const void* y, const float* read_gain, void* out,
+                       hipStream_t stream);
+/* MLPRMSNorm (model.py:35-45) over rows of H: rsqrt(mean(x^2) + eps) in fp32, the
+ * normalised row rounded to `dtype`, times weight [H] (same dtype). */
+int dabsn_hip_rms_norm(int dtype, int64_t rows, int64_t H, const void* x, const void* weight,
+                       float eps, void* out, hipStream_t stream);
+/* relu(x).square() of the MLP branch (model.py:188-195); NaN stays NaN. */
+int dabsn_hip_relu_square(int dtype, int64_t n, const void* x, void* out, hipStream_t stream);
+
 /* ---- three-way admitted read ------------------------------------------------------
  * Replaces the device kernels of dabsn::admitted_three_way_read_compact_flash and
  * dabsn::_admitted_three_way_read_compact_flash_backward
@@ -357,6 +378,28 @@ int dabsn_hip_read3_decode(int dtype, int64_t B, int64_t T, int64_t N, int64_t H
                            const float* admission, const float* scale,
                            const float* const* gains, void* out, void* workspace,
                            size_t workspace_bytes, hipStream_t stream);
+
+/* The one-query decode read (T == 1, H % 8 == 0, H <= 2048) taking its slots straight from
+ * a carried bank's admitted-slot lists and kept per-position glue, as the streaming step of
+ * the carried memory holds them (src/dabsn/memory.py:215-290 -> read.py:185-256 and
+ * :650-838: the reference gathers the admitted slots' cocktail, key bias and admission with
+ * torch ops per step, then reads). Every per-position array has bank_ld positions per batch
+ * row: bank [B, bank_ld, H], stats [B, bank_ld, 6] fp32 (write norm in column 5),
+ * members [B, bank_ld] int64 (row b's admitted positions, ascending), cocktail
+ * [B, bank_ld, 4], key_bias and admission [B, bank_ld] fp32; counts [B] int64 members per
+ * row. The read covers slots j < N: slot j is members[b, j], valid below max(counts[b], 1);
+ * its successor is min(idx + 1, bank_len - 1), its query-relative index idx - query_start;
+ * the query's cocktail is the bank's at bank_len - 1. Equals dabsn_hip_read3_decode on
+ * those arrays. N <= bank_ld; workspace: dabsn_hip_read3_decode_workspace_bytes(dtype, B,
+ * 1, N, H). */
+int dabsn_hip_read3_decode_members(int dtype, int64_t B, int64_t N, int64_t H, const void* q,
+                                   const void* bank, int64_t bank_len, int64_t bank_ld,
+                                   const float* stats, const int64_t* members,
+                                   const int64_t* counts, int64_t query_start,
+                                   const float* cocktail, const float* key_bias,
+                                   const float* admission, const float* scale,
+                                   const float* const* gains, void* out, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
 
 /* The decode read for callers that cannot allocate device memory (code under HIP graph
  * capture, serving loops whose buffers are all planned ahead). This entry point has no

@@ -297,12 +297,15 @@ def test_incremental_admission_equals_bank_select(cuda_device, adm_bf16):
 
 
 @pytest.mark.gpu
-def test_incremental_admission_decode_is_bit_identical_to_full_recompute(cuda_device):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_incremental_admission_decode_is_bit_identical_to_full_recompute(cuda_device, dtype):
     """Streaming decode with the kept glue and slot lists against the same decode that
     recomputes them over the whole bank every step (the reference's way): identical logits,
     through a prompt, token-by-token steps, a read-only query (rows appended then dropped)
-    and a change of a read parameter between steps (the kept glue is rebuilt)."""
-    model = _model(cuda_device)
+    and a change of a read parameter between steps (the kept glue is rebuilt). One-row
+    steps read the slots from the kept lists inside the decode kernel; the recompute builds
+    the slot arrays with torch first."""
+    model = _model(cuda_device).to(dtype)
     ids = _ids(3, 40, seed=17).to(cuda_device)
 
     def run():

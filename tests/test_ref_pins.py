@@ -354,7 +354,7 @@ def test_read_vs_reference_fixture(geometry):
 
 def _gains(read):
     rp = read.short_read
-    return [float(x) for x in (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain,
+    return [float(x.detach()) for x in (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain,
                                rp.adm_novelty_gain, rp.adm_saturation_gain, rp.adm_energy_gain,
                                rp.adm_bias)]
 
