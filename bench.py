@@ -475,14 +475,11 @@ def main():
         "core_scan_bwd": 18 * H * el,
         # reads Wx, Wgx (2H); writes U (2H) + 7 tapes (7H)
         "core_scan_fwd": 11 * H * el,
-        # one launch = the recompute forward of chunk k-1 beside the reverse scan of chunk k
-        "core_scan_pair": (11 + 18) * H * el,
     }
     weights_bytes = 2 * H * H * el
     if dom in per_token:
         launch_tokens = args.batch * chunk
-        weight_reads = 2 if dom == "core_scan_pair" else 1
-        alg_bytes = per_token[dom] * launch_tokens + weight_reads * weights_bytes
+        alg_bytes = per_token[dom] * launch_tokens + weights_bytes
         achieved = alg_bytes / (kernels[dom]["avg_ms"] / 1e3) / 1e9
         traffic, traffic_src = measured_traffic(dom, args, chunk)
         roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 2),
@@ -511,7 +508,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: uniform random token ids, random embedding, random-init weights",
         "config": {"workload": "config4 scan+read fwd+bwd: one seq layer, state 2048, read/hidden 4096, "
-                               "vocab 32000, block chunking 1024 (checkpoint recompute)",
+                               "vocab 32000, block chunking 1024 (tapes kept in HBM for the reverse scans)",
                    "batch": args.batch, "seq_len": args.seq, "state": H, "hidden": args.hidden,
                    "chunk_t": chunk, "n_max": n_max},
         "roofline": roofline,

@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _lock = threading.Lock()
 _lib = None
@@ -76,8 +76,6 @@ _SIGNATURES = {
     ),
     "dabsn_hip_core_scan_fwd_call": ([ctypes.POINTER(CoreFwdCall), vp], i32),
     "dabsn_hip_core_scan_bwd_call": ([ctypes.POINTER(CoreBwdCall), vp], i32),
-    "dabsn_hip_core_scan_pair": (
-        [ctypes.POINTER(CoreFwdCall), ctypes.POINTER(CoreBwdCall), vp], i32),
     "dabsn_hip_linrec_fwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_linrec_workspace_bytes": ([i32, i64, i64, i64], sz),
     "dabsn_hip_linrec_bwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
@@ -103,6 +101,7 @@ _SIGNATURES = {
     "dabsn_hip_bank_select": ([i32, i32, i64, i64, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_admit_step": (
         [i32, i64, i64, i64, i64, vp, i64, PTR8, vp, i32, vp, vp, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_bank_fold": ([i64, i64, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_gather": ([i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_gather_bwd": (
         [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),
@@ -114,8 +113,8 @@ _SIGNATURES = {
         i32,
     ),
     "dabsn_hip_read3_fwd_keep": (
-        [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4, vp, vp,
-         sz, vp, sz, vp],
+        [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4, vp,
+         vp, sz, vp, sz, vp],
         i32,
     ),
     "dabsn_hip_read3_decode_workspace_bytes": ([i32, i64, i64, i64, i64], sz),
@@ -154,7 +153,7 @@ _SIGNATURES = {
         i32,
     ),
     "dabsn_hip_read3_bwd_after_fwd": (
-        [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4]
+        [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, PTR4]
         + [vp] * 4 + [vp] * 5 + [vp, sz, vp, sz, vp],
         i32,
     ),

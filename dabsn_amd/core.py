@@ -130,9 +130,10 @@ class DABSNCore(nn.Module):
 
     def chunked_tapes(self, inputs: Tensor, chunk_t: int):
         """Block time-chunked scan from the zero state (model.py:274-307): chunks of
-        `chunk_t` steps with the state carried between them, each checkpointed. On the
-        device the recompute of chunk k - 1 overlaps the reverse scan of chunk k. Returns
-        the 7 tapes of forward_from_state(..., return_cocktail=True)."""
+        `chunk_t` steps with the state carried between them. On the device the tapes stay
+        resident for the chunks' reverse scans instead of being recomputed per chunk (the
+        reference's checkpoint trades that memory for a second forward scan). Returns the
+        7 tapes of forward_from_state(..., return_cocktail=True)."""
         from .kernels.chunked import chunked_core_scan
 
         batch = inputs.shape[0]

@@ -1172,21 +1172,6 @@ __global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
   bwd_body<E, CH, KSTEPS, NW>(a, blockIdx.x, gridDim.x);
 }
 
-// A forward scan and an independent reverse scan in one cooperative launch: workgroups
-// [0, gf) run the forward (e.g. the recompute of chunk k-1 of a checkpointed chunked scan),
-// [gf, gf + gb) the reverse scan of another chunk. Each has its own workspace (counters and
-// exchange slots); one launch guarantees both halves are co-resident.
-template <typename E, int CH, int KSTEPS, int NW>
-__global__ void __launch_bounds__(NW * 64, 1) core_pair_kernel(FwdArgs<E> fa, BwdArgs<E> ba,
-                                                               int gf, int gb) {
-  const int bid = blockIdx.x;
-  if (bid < gf) {
-    fwd_body<E, CH, KSTEPS, NW>(fa, bid, gf);
-  } else {
-    bwd_body<E, CH, KSTEPS, NW>(ba, bid - gf, gb);
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Host side: configuration, workspace and launch.
 // ---------------------------------------------------------------------------
@@ -1426,44 +1411,6 @@ static int bwd_dispatch(const Cfg& c, const BwdArgs<E>& args, hipStream_t stream
 #undef DABSN_CASE
   dabsn::set_error("core scan backward: no kernel for CH=%d KSTEPS=%d NW=%d", c.ch, c.ksteps,
                    c.nw);
-  return DABSN_ERR_UNSUPPORTED;
-}
-
-template <typename E>
-static int pair_dispatch(const Cfg& c, const FwdArgs<E>& fa, const BwdArgs<E>& ba, int gf, int gb,
-                         hipStream_t stream) {
-  struct PairArgs {
-    FwdArgs<E> fa;
-    BwdArgs<E> ba;
-    int gf, gb;
-  };
-#define DABSN_CASE(CHV, KS, NWV)                                                         \
-  if (c.ch == CHV && c.ksteps == KS && c.nw == NWV) {                                    \
-    auto kern = core_pair_kernel<E, CHV, KS, NWV>;                                       \
-    int dev = 0, cus = 0, per_cu = 0, coop = 0;                                          \
-    DABSN_HIP_CHECK(hipGetDevice(&dev));                                                 \
-    DABSN_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev)); \
-    DABSN_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)); \
-    DABSN_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NWV * 64, 0)); \
-    if (!coop || per_cu * cus < gf + gb) {                                               \
-      dabsn::set_error("core scan pair needs %d co-resident workgroups, device holds %d", \
-                       gf + gb, per_cu * cus);                                           \
-      return DABSN_ERR_UNSUPPORTED;                                                      \
-    }                                                                                    \
-    PairArgs pa{fa, ba, gf, gb};                                                         \
-    void* kargs[] = {&pa.fa, &pa.ba, &pa.gf, &pa.gb};                                    \
-    DABSN_HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern),       \
-                                               dim3(gf + gb), dim3(NWV * 64), kargs, 0,  \
-                                               stream));                                 \
-    return DABSN_OK;                                                                     \
-  }
-  if constexpr (is_bf16<E>::value) {
-    DABSN_CORE_CASES_BF16(DABSN_CASE)
-  } else {
-    DABSN_CORE_CASES_F32(DABSN_CASE)
-  }
-#undef DABSN_CASE
-  dabsn::set_error("core scan pair: no kernel for CH=%d KSTEPS=%d NW=%d", c.ch, c.ksteps, c.nw);
   return DABSN_ERR_UNSUPPORTED;
 }
 
@@ -1719,37 +1666,6 @@ int dabsn_hip_core_scan_bwd_call(const dabsn_core_bwd_call* b, hipStream_t strea
   if (rc != DABSN_OK) return rc;
   if (b->dtype == kBF16) return bwd_dispatch(c, bwd_args<bf16>(*b, c), stream);
   return bwd_dispatch(c, bwd_args<float>(*b, c), stream);
-}
-
-int dabsn_hip_core_scan_pair(const dabsn_core_fwd_call* f, const dabsn_core_bwd_call* b,
-                             hipStream_t stream) {
-  DABSN_REQUIRE(f && b, "core scan pair: null call");
-  DABSN_REQUIRE(f->dtype == b->dtype && f->B == b->B && f->H == b->H,
-                "core scan pair: the two scans must share dtype, B and H");
-  DABSN_REQUIRE(f->T > 0 && b->T > 0, "core scan pair: both scans need T > 0");
-  Cfg c, cb;
-  int rc = check_fwd(*f, c);
-  if (rc != DABSN_OK) return rc;
-  rc = check_bwd(*b, cb);
-  if (rc != DABSN_OK) return rc;
-  const int grid = c.nct * c.nbg;
-  // Nothing is enqueued unless both grids fit on the device at once.
-  {
-    int dev = 0, cus = 0;
-    DABSN_HIP_CHECK(hipGetDevice(&dev));
-    DABSN_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    if (cus < 2 * grid) {
-      dabsn::set_error("core scan pair needs %d CUs, device has %d", 2 * grid, cus);
-      return DABSN_ERR_UNSUPPORTED;
-    }
-  }
-  rc = dabsn_hip_zero(f->workspace, scan_bytes(f->dtype, c, false), stream);
-  if (rc != DABSN_OK) return rc;
-  rc = dabsn_hip_zero(b->workspace, scan_bytes(b->dtype, c, true), stream);
-  if (rc != DABSN_OK) return rc;
-  if (f->dtype == kBF16)
-    return pair_dispatch(c, fwd_args<bf16>(*f, c), bwd_args<bf16>(*b, c), grid, grid, stream);
-  return pair_dispatch(c, fwd_args<float>(*f, c), bwd_args<float>(*b, c), grid, grid, stream);
 }
 
 }  // extern "C"

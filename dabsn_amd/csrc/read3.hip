@@ -153,11 +153,14 @@ __device__ __forceinline__ void wave_softmax_stats(float& m, float& l) {
 
 // Row statistics (max and sum of each masked softmax), one wave per query row.
 // stats[row] = (m_s, l_s, m_p, l_p, m_i, l_i); l = 0 marks an empty pathway.
-// When P_V is non-null also writes P_V / P_Vn for j < nhi of the row's tile.
+// When P_V is non-null also writes P_V / P_Vn for j < nhi of the row's tile. With a
+// successor fold (`fold` non-null; see SuccFold) the induction weight of slot j is added to
+// P_V at column j + fold[j] instead of being written to P_Vn (not written).
 template <typename E>
 __global__ void __launch_bounds__(NTH) softmax_fwd_kernel(int64_t rows, RowCtx c, Gains g,
                                                           const float* scale_p, const int32_t* rs,
-                                                          float* stats, E* PV, E* PVn) {
+                                                          const int8_t* fold, float* stats, E* PV,
+                                                          E* PVn) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * NWV + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -189,15 +192,34 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_kernel(int64_t rows, RowCtx c
   if (PV == nullptr) return;
   const float is = ls > 0.f ? 1.0f / ls : 0.f, ip = lp > 0.f ? 1.0f / lp : 0.f,
               ii = li > 0.f ? 1.0f / li : 0.f;
-  for (int j = lane; j < nhi; j += 64) {
-    float ss, sp, cc, sr;
-    scores(c, b, t, j, ckt, ss, sp, cc, sr);
+  const int8_t* fb = fold ? fold + static_cast<size_t>(b) * c.N : nullptr;
+  // Folded: the weight slot j hands to column j + 1 reaches lane + 1 by a shuffle, and
+  // lane 63's to lane 0 of the next 64 columns through `carry`. A weight is non-zero only
+  // when slot j's induction is allowed, which makes slot j + 1 readable by this query, so
+  // column j + 1 < nhi and nothing is carried past the row's last column.
+  float carry = 0.f;
+  for (int j0 = 0; j0 < nhi; j0 += 64) {
+    const int j = j0 + lane;
     float pv = 0.f, pn = 0.f;
-    if (allow_at(c.mode, ib[j], vb[j] != 0, t)) pv = c.sg * (__expf(ss - ms) * is) + c.pg * (__expf(sp - mp) * ip);
-    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) pn = c.ig * (__expf(ss - mi) * ii);
+    int fj = 0;
+    if (j < nhi) {
+      float ss, sp, cc, sr;
+      scores(c, b, t, j, ckt, ss, sp, cc, sr);
+      if (allow_at(c.mode, ib[j], vb[j] != 0, t)) pv = c.sg * (__expf(ss - ms) * is) + c.pg * (__expf(sp - mp) * ip);
+      if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) pn = c.ig * (__expf(ss - mi) * ii);
+      if (fb) fj = fb[j];
+    }
     const size_t o = static_cast<size_t>(row) * c.N + j;
-    st(PV, o, pv);
-    st(PVn, o, pn);
+    if (fb) {
+      const float ahead = fj == 1 ? pn : 0.f;
+      float from_prev = __shfl_up(ahead, 1, 64);
+      if (lane == 0) from_prev = carry;
+      carry = __shfl(ahead, 63, 64);
+      if (j < nhi) st(PV, o, (pv + (fj == 0 ? pn : 0.f)) + from_prev);
+    } else if (j < nhi) {
+      st(PV, o, pv);
+      st(PVn, o, pn);
+    }
   }
 }
 
@@ -206,8 +228,8 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_kernel(int64_t rows, RowCtx c
 __global__ void __launch_bounds__(NTH) grad_rows_kernel(int64_t rows, RowCtx c, Gains g,
                                                         const float* scale_p,
                                                         const int32_t* rs_rng, const float* stats,
-                                                        const float* dPV, const float* dPVn,
-                                                        float* rowA) {
+                                                        const int8_t* fold, const float* dPV,
+                                                        const float* dPVn, float* rowA) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * NWV + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -222,6 +244,7 @@ __global__ void __launch_bounds__(NTH) grad_rows_kernel(int64_t rows, RowCtx c, 
   const float* ckt = c.ck + static_cast<size_t>(row) * 4;
   const int64_t* ib = c.idx + static_cast<size_t>(b) * c.N;
   const uint8_t* vb = c.valid + static_cast<size_t>(b) * c.N;
+  const int8_t* fb = fold ? fold + static_cast<size_t>(b) * c.N : nullptr;
   float rsum = 0.f, psum = 0.f, isum = 0.f;
   for (int j = lane; j < nhi; j += 64) {
     float ss, sp, cc, sr;
@@ -232,7 +255,8 @@ __global__ void __launch_bounds__(NTH) grad_rows_kernel(int64_t rows, RowCtx c, 
       rsum += __expf(ss - st6[0]) * is * d;
       psum += __expf(sp - st6[2]) * ip * d;
     }
-    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T)) isum += __expf(ss - st6[4]) * ii * dPVn[o];
+    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T))
+      isum += __expf(ss - st6[4]) * ii * (fb ? dPV[o + fb[j]] : dPVn[o]);
   }
   rsum = wave_sum(rsum);
   psum = wave_sum(psum);
@@ -253,9 +277,9 @@ __global__ void __launch_bounds__(NTH) grad_rows_kernel(int64_t rows, RowCtx c, 
 template <typename E>
 __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const float* scale_p,
                                                         const int32_t* rs_rng, const float* stats,
-                                                        const float* rowA, const float* dPV,
-                                                        const float* dPVn, E* Gs, E* PV, E* PVn,
-                                                        float* rowB, float* colp) {
+                                                        const float* rowA, const int8_t* fold,
+                                                        const float* dPV, const float* dPVn, E* Gs,
+                                                        E* PV, E* PVn, float* rowB, float* colp) {
   constexpr int CJ = CC / NTH;
   const int b = blockIdx.z, rt = blockIdx.y, cch = blockIdx.x;
   const int NCC = (c.N + CC - 1) / CC;
@@ -308,8 +332,10 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
   const uint8_t* vb = c.valid + static_cast<size_t>(b) * c.N;
   // Slot index per column, with invalid slots folded into INT_MAX (no query may read
   // them). Indices are sequence positions (|idx| < 2^31).
+  // With a successor fold the induction product of slot j uses column j + fold[j] of dP_V
+  // (dP_Vn is not formed).
   float kbadm[CJ], cbv[CJ][4];
-  int slot[CJ];
+  int slot[CJ], dnoff[CJ];
 #pragma unroll
   for (int q = 0; q < CJ; ++q) {
     const int j = cch * CC + q * NTH + threadIdx.x;
@@ -317,6 +343,7 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
     const size_t bj = static_cast<size_t>(b) * c.N + min(j, c.N - 1);
     kbadm[q] = c.kb[bj] + c.adm[bj];
     slot[q] = ok ? static_cast<int>(ib[min(j, c.N - 1)]) : INT_MAX;
+    dnoff[q] = fold && ok ? fold[bj] : 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) cbv[q][k] = c.cb[bj * 4 + k];
   }
@@ -337,7 +364,7 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
       const bool in = j < njl;
       nS[q] = in ? c.S[rowoff + j] : 0.f;
       nD[q] = in ? dPV[rowoff + j] : 0.f;
-      nDn[q] = in ? dPVn[rowoff + j] : 0.f;
+      nDn[q] = in ? (fold ? dPV[rowoff + j + dnoff[q]] : dPVn[rowoff + j]) : 0.f;
     }
   };
   fetch(t0);
@@ -471,6 +498,54 @@ __global__ void reduce_final_kernel(int nblocks, const float* part, float* out5)
   out5[k] = s;
 }
 
+// Successor fold. The read module's banks hold V[j] = write[idx[j]] and Vn[j] =
+// write[next(idx[j])]. When next(idx[j]) is the position of slot j + 1 (consecutive admitted
+// positions) Vn[j] is V[j + 1]; when next(idx[j]) = idx[j] (the clamped last position) it is
+// V[j]. A fold array of one code per slot, fold[b][j] in {0, 1}, states Vn[j] = V[j +
+// fold[j]] for every valid slot; then P_Vn Vn = P_V' V with the induction weights moved to
+// column j + fold[j], so the reads and products over Vn disappear: one product in the output
+// GEMM, no dP_Vn GEMM (dP_Vn[:, j] = dP_V[:, j + fold[j]]) and no gVn GEMM (its rows are
+// part of gV).
+//
+// out[b][j][t] = PV[b][t][j] + (fold[j] == 0 ? PVn[b][t][j] : 0)
+//                            + (fold[j - 1] == 1 ? PVn[b][t][j - 1] : 0),
+// a transpose of the folded P_V for the gV GEMM (64 x 64 tiles as xpose::transpose_kernel,
+// with the P_Vn tile staged one column wider on the left).
+template <typename E>
+__global__ void __launch_bounds__(xpose::TNT) fold_transpose_kernel(int R, int C, const E* PV,
+                                                                   const E* PVn,
+                                                                   const int8_t* fold, E* out) {
+  constexpr int TT = xpose::TT, PITCH = TT + 2;
+  __shared__ float tile[TT][PITCH];
+  __shared__ int8_t fl[TT + 1];
+  const int b = blockIdx.z;
+  const int r0 = blockIdx.y * TT, c0 = blockIdx.x * TT;
+  const E* pv = PV + static_cast<size_t>(b) * R * C;
+  const E* pn = PVn + static_cast<size_t>(b) * R * C;
+  const int8_t* fb = fold + static_cast<size_t>(b) * C;
+  for (int i = threadIdx.x; i < TT + 1; i += xpose::TNT) {
+    const int c = c0 - 1 + i;
+    fl[i] = (c >= 0 && c < C) ? fb[c] : int8_t(2);  // 2: nothing folds from or into here
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < TT * TT; q += xpose::TNT) {
+    const int r = q / TT, cc = q % TT;
+    const int rr = r0 + r, c = c0 + cc;
+    if (rr >= R || c >= C) continue;
+    const size_t o = static_cast<size_t>(rr) * C + c;
+    float v = to_f(pv[o]);
+    if (fl[cc + 1] == 0) v += to_f(pn[o]);
+    if (fl[cc] == 1) v += to_f(pn[o - 1]);
+    tile[r][cc] = v;
+  }
+  __syncthreads();
+  E* dst = out + static_cast<size_t>(b) * R * C;
+  for (int q = threadIdx.x; q < TT * TT; q += xpose::TNT) {
+    const int c = q / TT, r = q % TT;
+    if (r0 + r < R && c0 + c < C) st(dst, static_cast<size_t>(c0 + c) * R + r0 + r, tile[r][c]);
+  }
+}
+
 // Workspace planning.
 struct Plan {
   size_t off_S, off_rs, off_ro, off_rb, off_stats, off_PV, off_PVn, off_VT, off_VnT, end_fwd;
@@ -538,8 +613,8 @@ template <typename E>
 static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, const E* K,
                         const E* V, const E* Vn, const float* ck, const float* cb, const float* kb,
                         const float* adm, const float* scale, const int64_t* idx,
-                        const uint8_t* valid, int mode, Gains g, E* out, const Ws& ws,
-                        const Plan& p, bool write_p, hipStream_t stream) {
+                        const uint8_t* valid, const int8_t* fold, int mode, Gains g, E* out,
+                        const Ws& ws, const Plan& p, bool write_p, hipStream_t stream) {
   const int QT = static_cast<int>((T + TILE - 1) / TILE), BT = static_cast<int>((N + TILE - 1) / TILE);
   float* S = ws.at<float>(p.off_S);
   int32_t* rs = ws.at<int32_t>(p.off_rs);
@@ -564,20 +639,23 @@ static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, 
   RowCtx c{(int)T, (int)N, mode, S, kb, adm, cb, ck, idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
   const unsigned row_blocks = static_cast<unsigned>((B * T + NWV - 1) / NWV);
   hipLaunchKernelGGL(softmax_fwd_kernel<E>, dim3(row_blocks), dim3(NTH), 0, stream, B * T, c, g,
-                     scale, rs, stats, write_p ? PV : static_cast<E*>(nullptr),
-                     write_p ? PVn : static_cast<E*>(nullptr));
+                     scale, rs, fold, stats, write_p ? PV : static_cast<E*>(nullptr),
+                     write_p && !fold ? PVn : static_cast<E*>(nullptr));
   DABSN_HIP_CHECK(hipGetLastError());
   if (!write_p) return DABSN_OK;
   {
     E* VT = ws.at<E>(p.off_VT);
     E* VnT = ws.at<E>(p.off_VnT);
     DABSN_HIP_CHECK(xpose::transpose<E>(V, VT, (int)B, (int)N, (int)H, stream));
-    DABSN_HIP_CHECK(xpose::transpose<E>(Vn, VnT, (int)B, (int)N, (int)H, stream));
-    gemm::Args<E, E> a{};  // out = P_V V + P_Vn Vn, B operands as V^T [H][N]
+    if (!fold) DABSN_HIP_CHECK(xpose::transpose<E>(Vn, VnT, (int)B, (int)N, (int)H, stream));
+    gemm::Args<E, E> a{};  // out = P_V V + P_Vn Vn (folded: P_V' V), B operands as V^T [H][N]
     a.M = (int)T; a.N = (int)H; a.K = (int)N;
     a.A = PV; a.lda = N; a.sA = T * N;
     a.B = VT; a.ldb = N; a.sB = H * N;
-    a.A2 = PVn; a.B2 = VnT;
+    if (!fold) {
+      a.A2 = PVn;
+      a.B2 = VnT;
+    }
     a.C = out; a.ldc = H; a.sC = T * H;
     a.alpha = 1.0f;
     a.ranges = ro; a.mtiles = QT;
@@ -590,14 +668,15 @@ template <typename E>
 static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* gout, const E* q,
                          const E* K, const E* V, const E* Vn, const float* ck, const float* cb,
                          const float* kb, const float* adm, const float* scale, const int64_t* idx,
-                         const uint8_t* valid, int mode, Gains g, E* gq, E* gK, E* gV, E* gVn,
+                         const uint8_t* valid, const int8_t* fold, int mode, Gains g, E* gq,
+                         E* gK, E* gV, E* gVn,
                          float* gck, float* gcb, float* gkb, float* gadm, float* gscal5,
                          const Ws& ws, const Plan& p, bool recompute, hipStream_t stream) {
   // The tile ranges, S and the row statistics: recomputed here, or left in the workspace
   // by the forward call on the same inputs (which also wrote P_V / P_Vn, rebuilt below).
   if (recompute) {
     const int rc = forward_impl<E>(B, T, N, H, q, K, V, Vn, ck, cb, kb, adm, scale, idx, valid,
-                                   mode, g, nullptr, ws, p, false, stream);
+                                   fold, mode, g, nullptr, ws, p, false, stream);
     if (rc != DABSN_OK) return rc;
   }
   const int QT = static_cast<int>((T + TILE - 1) / TILE), BT = static_cast<int>((N + TILE - 1) / TILE);
@@ -615,7 +694,7 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
   float* rowB = ws.at<float>(p.off_rowB);
   float* colp = ws.at<float>(p.off_colp);
   float* part = ws.at<float>(p.off_part);
-  for (int w = 0; w < 2; ++w) {
+  for (int w = 0; w < (fold ? 1 : 2); ++w) {
     gemm::Args<E, float> a{};
     a.M = (int)T; a.N = (int)N; a.K = (int)H;
     a.A = gout; a.lda = H; a.sA = T * H;
@@ -627,12 +706,12 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
   }
   RowCtx c{(int)T, (int)N, mode, S, kb, adm, cb, ck, idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
   hipLaunchKernelGGL(grad_rows_kernel, dim3((unsigned)((B * T + NWV - 1) / NWV)), dim3(NTH), 0,
-                     stream, B * T, c, g, scale, rs, stats, dPV, dPVn, rowA);
+                     stream, B * T, c, g, scale, rs, stats, fold, dPV, dPVn, rowA);
   DABSN_HIP_CHECK(hipGetLastError());
   const int NCC = static_cast<int>((N + CC - 1) / CC), RTILES = static_cast<int>((T + RT - 1) / RT);
   if (N > 0) {
     hipLaunchKernelGGL(grad_tile_kernel<E>, dim3(NCC, RTILES, (unsigned)B), dim3(NTH), 0, stream, c,
-                       g, scale, rs, stats, rowA, dPV, dPVn, Gs, PV, PVn, rowB, colp);
+                       g, scale, rs, stats, rowA, fold, dPV, dPVn, Gs, PV, PVn, rowB, colp);
     DABSN_HIP_CHECK(hipGetLastError());
   }
   E* KT = ws.at<E>(p.off_KT);
@@ -645,8 +724,16 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
   DABSN_HIP_CHECK(xpose::transpose<E>(q, QTr, (int)B, (int)T, (int)H, stream));
   DABSN_HIP_CHECK(xpose::transpose<E>(gout, gOT, (int)B, (int)T, (int)H, stream));
   DABSN_HIP_CHECK(xpose::transpose<E>(Gs, GsT, (int)B, (int)T, (int)N, stream));
-  DABSN_HIP_CHECK(xpose::transpose<E>(PV, PVT, (int)B, (int)T, (int)N, stream));
-  DABSN_HIP_CHECK(xpose::transpose<E>(PVn, PVnT, (int)B, (int)T, (int)N, stream));
+  if (fold) {
+    const dim3 grid((unsigned)((N + xpose::TT - 1) / xpose::TT),
+                    (unsigned)((T + xpose::TT - 1) / xpose::TT), (unsigned)B);
+    hipLaunchKernelGGL(fold_transpose_kernel<E>, grid, dim3(xpose::TNT), 0, stream, (int)T,
+                       (int)N, PV, PVn, fold, PVT);
+    DABSN_HIP_CHECK(hipGetLastError());
+  } else {
+    DABSN_HIP_CHECK(xpose::transpose<E>(PV, PVT, (int)B, (int)T, (int)N, stream));
+    DABSN_HIP_CHECK(xpose::transpose<E>(PVn, PVnT, (int)B, (int)T, (int)N, stream));
+  }
   {
     gemm::Args<E, E> a{};  // gQ = Gs K, B operand as K^T [H][N]
     a.M = (int)T; a.N = (int)H; a.K = (int)N;
@@ -663,7 +750,7 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
   const E* lhs[3] = {GsT, PVT, PVnT};
   const E* rhs[3] = {QTr, gOT, gOT};
   E* dst[3] = {gK, gV, gVn};
-  for (int w = 0; w < 3; ++w) {
+  for (int w = 0; w < (fold ? 2 : 3); ++w) {
     gemm::Args<E, E> a{};  // gK = Gs^T Q, gV = P_V^T gO, gVn = P_Vn^T gO over k = t
     a.M = (int)N; a.N = (int)H; a.K = (int)T;
     a.A = lhs[w]; a.lda = T; a.sA = N * T;
@@ -1415,7 +1502,8 @@ static int decode_impl(int64_t B, int64_t T, int64_t N, int64_t H, int64_t Nb, i
   DABSN_HIP_CHECK(hipGetLastError());
   RowCtx c{(int)T, (int)N, 0, S, kb, adm, cb, ck, read_idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
   hipLaunchKernelGGL(softmax_fwd_kernel<E>, dim3((unsigned)((B * T + NWV - 1) / NWV)), dim3(NTH), 0,
-                     stream, B * T, c, g, scale, rs, stats, PV, PVn);
+                     stream, B * T, c, g, scale, rs, static_cast<const int8_t*>(nullptr), stats,
+                     PV, PVn);
   DABSN_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(decode_out_kernel<E>,
                      dim3((unsigned)((H + 2047) / 2048), (unsigned)B, (unsigned)p.splits), dim3(256), 0,
@@ -1458,16 +1546,16 @@ static int read3_fwd_entry(int dtype, int64_t B, int64_t T, int64_t N, int64_t H
                            const void* K, const void* V, const void* Vn, const float* cocktail,
                            const float* bank_cocktail, const float* key_bias,
                            const float* admission, const float* scale, const int64_t* idx,
-                           const uint8_t* valid, int mode, const float* const* gains, void* out,
-                           void* kept, size_t kept_bytes, void* scratch, size_t scratch_bytes,
-                           bool single, hipStream_t stream) {
+                           const uint8_t* valid, const int8_t* fold, int mode,
+                           const float* const* gains, void* out, void* kept, size_t kept_bytes,
+                           void* scratch, size_t scratch_bytes, bool single, hipStream_t stream) {
   const int rc = read3_checks(dtype, B, T, N, H, mode);
   if (rc != DABSN_OK) return rc;
   DABSN_REQUIRE(q && out && cocktail && scale && gains, "read3: null pointer");
   for (int i = 0; i < 4; ++i) DABSN_REQUIRE(gains[i], "read3: null gain %d", i);
   if (N == 0) return dabsn_hip_zero(out, static_cast<size_t>(B * T * H) * (dtype == kBF16 ? 2 : 4), stream);
-  DABSN_REQUIRE(K && V && Vn && bank_cocktail && key_bias && admission && idx && valid && kept &&
-                    (single || scratch),
+  DABSN_REQUIRE(K && V && (Vn || fold) && bank_cocktail && key_bias && admission && idx && valid &&
+                    kept && (single || scratch),
                 "read3: null bank or workspace pointer");
   const Plan p = plan(dtype, B, T, N, H);
   Ws w;
@@ -1484,10 +1572,10 @@ static int read3_fwd_entry(int dtype, int64_t B, int64_t T, int64_t N, int64_t H
   if (dtype == kBF16)
     return forward_impl<bf16>(B, T, N, H, (const bf16*)q, (const bf16*)K, (const bf16*)V,
                               (const bf16*)Vn, cocktail, bank_cocktail, key_bias, admission, scale,
-                              idx, valid, mode, g, (bf16*)out, w, p, true, stream);
+                              idx, valid, fold, mode, g, (bf16*)out, w, p, true, stream);
   return forward_impl<float>(B, T, N, H, (const float*)q, (const float*)K, (const float*)V,
                              (const float*)Vn, cocktail, bank_cocktail, key_bias, admission, scale,
-                             idx, valid, mode, g, (float*)out, w, p, true, stream);
+                             idx, valid, fold, mode, g, (float*)out, w, p, true, stream);
 }
 
 int dabsn_hip_read3_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* q,
@@ -1497,7 +1585,7 @@ int dabsn_hip_read3_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
                         const float* const* gains, void* out, void* workspace,
                         size_t workspace_bytes, hipStream_t stream) {
   return read3_fwd_entry(dtype, B, T, N, H, q, K, V, Vn, cocktail, bank_cocktail, key_bias,
-                         admission, scale, idx, valid, mode, gains, out, workspace,
+                         admission, scale, idx, valid, nullptr, mode, gains, out, workspace,
                          workspace_bytes, nullptr, 0, true, stream);
 }
 
@@ -1505,11 +1593,12 @@ int dabsn_hip_read3_fwd_keep(int dtype, int64_t B, int64_t T, int64_t N, int64_t
                              const void* q, const void* K, const void* V, const void* Vn,
                              const float* cocktail, const float* bank_cocktail,
                              const float* key_bias, const float* admission, const float* scale,
-                             const int64_t* idx, const uint8_t* valid, int mode,
-                             const float* const* gains, void* out, void* kept, size_t kept_bytes,
-                             void* scratch, size_t scratch_bytes, hipStream_t stream) {
+                             const int64_t* idx, const uint8_t* valid, const int8_t* fold,
+                             int mode, const float* const* gains, void* out, void* kept,
+                             size_t kept_bytes, void* scratch, size_t scratch_bytes,
+                             hipStream_t stream) {
   return read3_fwd_entry(dtype, B, T, N, H, q, K, V, Vn, cocktail, bank_cocktail, key_bias,
-                         admission, scale, idx, valid, mode, gains, out, kept, kept_bytes,
+                         admission, scale, idx, valid, fold, mode, gains, out, kept, kept_bytes,
                          scratch, scratch_bytes, false, stream);
 }
 
@@ -1521,8 +1610,9 @@ static int read3_bwd_entry(bool recompute, int dtype, int64_t B, int64_t T, int6
                            const void* V, const void* Vn, const float* cocktail,
                            const float* bank_cocktail, const float* key_bias,
                            const float* admission, const float* scale, const int64_t* idx,
-                           const uint8_t* valid, int mode, const float* const* gains, void* gq,
-                           void* gK, void* gV, void* gVn, float* gcocktail,
+                           const uint8_t* valid, const int8_t* fold, int mode,
+                           const float* const* gains, void* gq, void* gK, void* gV, void* gVn,
+                           float* gcocktail,
                            float* gbank_cocktail, float* gkey_bias, float* gadmission,
                            float* gscalars5, void* kept, size_t kept_bytes, void* scratch,
                            size_t scratch_bytes, hipStream_t stream) {
@@ -1538,9 +1628,9 @@ static int read3_bwd_entry(bool recompute, int dtype, int64_t B, int64_t T, int6
     if (z == DABSN_OK) z = dabsn_hip_zero(gscalars5, 5 * 4, stream);
     return z;
   }
-  DABSN_REQUIRE(K && V && Vn && bank_cocktail && key_bias && admission && idx && valid && gK && gV &&
-                    gVn && gbank_cocktail && gkey_bias && gadmission && kept &&
-                    (recompute || scratch),
+  DABSN_REQUIRE(K && V && (Vn || fold) && bank_cocktail && key_bias && admission && idx && valid &&
+                    gK && gV && (gVn || fold) && gbank_cocktail && gkey_bias && gadmission &&
+                    kept && (recompute || scratch),
                 "read3 backward: null bank or workspace pointer");
   const Plan p = plan(dtype, B, T, N, H);
   Ws w;
@@ -1558,12 +1648,12 @@ static int read3_bwd_entry(bool recompute, int dtype, int64_t B, int64_t T, int6
   if (dtype == kBF16)
     return backward_impl<bf16>(B, T, N, H, (const bf16*)gout, (const bf16*)q, (const bf16*)K,
                                (const bf16*)V, (const bf16*)Vn, cocktail, bank_cocktail, key_bias,
-                               admission, scale, idx, valid, mode, g, (bf16*)gq, (bf16*)gK,
+                               admission, scale, idx, valid, fold, mode, g, (bf16*)gq, (bf16*)gK,
                                (bf16*)gV, (bf16*)gVn, gcocktail, gbank_cocktail, gkey_bias,
                                gadmission, gscalars5, w, p, recompute, stream);
   return backward_impl<float>(B, T, N, H, (const float*)gout, (const float*)q, (const float*)K,
                               (const float*)V, (const float*)Vn, cocktail, bank_cocktail, key_bias,
-                              admission, scale, idx, valid, mode, g, (float*)gq, (float*)gK,
+                              admission, scale, idx, valid, fold, mode, g, (float*)gq, (float*)gK,
                               (float*)gV, (float*)gVn, gcocktail, gbank_cocktail, gkey_bias,
                               gadmission, gscalars5, w, p, recompute, stream);
 }
@@ -1577,7 +1667,8 @@ int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
                         float* gkey_bias, float* gadmission, float* gscalars5, void* workspace,
                         size_t workspace_bytes, hipStream_t stream) {
   return read3_bwd_entry(true, dtype, B, T, N, H, gout, q, K, V, Vn, cocktail, bank_cocktail,
-                         key_bias, admission, scale, idx, valid, mode, gains, gq, gK, gV, gVn,
+                         key_bias, admission, scale, idx, valid, nullptr, mode, gains, gq, gK, gV,
+                         gVn,
                          gcocktail, gbank_cocktail, gkey_bias, gadmission, gscalars5, workspace,
                          workspace_bytes, nullptr, 0, stream);
 }
@@ -1587,14 +1678,15 @@ int dabsn_hip_read3_bwd_after_fwd(int dtype, int64_t B, int64_t T, int64_t N, in
                                   const void* Vn, const float* cocktail,
                                   const float* bank_cocktail, const float* key_bias,
                                   const float* admission, const float* scale,
-                                  const int64_t* idx, const uint8_t* valid, int mode,
-                                  const float* const* gains, void* gq, void* gK, void* gV,
-                                  void* gVn, float* gcocktail, float* gbank_cocktail,
-                                  float* gkey_bias, float* gadmission, float* gscalars5,
-                                  const void* kept, size_t kept_bytes, void* scratch,
-                                  size_t scratch_bytes, hipStream_t stream) {
+                                  const int64_t* idx, const uint8_t* valid,
+                                  const int8_t* fold, int mode, const float* const* gains,
+                                  void* gq, void* gK, void* gV, void* gVn, float* gcocktail,
+                                  float* gbank_cocktail, float* gkey_bias, float* gadmission,
+                                  float* gscalars5, const void* kept, size_t kept_bytes,
+                                  void* scratch, size_t scratch_bytes, hipStream_t stream) {
   return read3_bwd_entry(false, dtype, B, T, N, H, gout, q, K, V, Vn, cocktail, bank_cocktail,
-                         key_bias, admission, scale, idx, valid, mode, gains, gq, gK, gV, gVn,
+                         key_bias, admission, scale, idx, valid, fold, mode, gains, gq, gK, gV,
+                         gVn,
                          gcocktail, gbank_cocktail, gkey_bias, gadmission, gscalars5,
                          const_cast<void*>(kept), kept_bytes, scratch, scratch_bytes, stream);
 }

@@ -224,22 +224,26 @@ __global__ void __launch_bounds__(256) gather_kernel(int T, int N, int H, int hb
   if (h >= H) return;
   const int64_t b = row / N;
   int64_t t = idx[row];
-  int64_t tn = nidx[row];
   t = t < 0 ? 0 : (t >= T ? T - 1 : t);
-  tn = tn < 0 ? 0 : (tn >= T ? T - 1 : tn);
-  float v[V], vn[V], k[V];
+  float v[V], k[V];
   ldv<E, V>(w + (static_cast<size_t>(b) * T + t) * H + h, v);
-  ldv<E, V>(w + (static_cast<size_t>(b) * T + tn) * H + h, vn);
   const float n = fmaxf(norm_w[static_cast<size_t>(b) * T + t], kEps);
 #pragma unroll
   for (int e = 0; e < V; ++e) k[e] = v[e] / n;
   const size_t o = static_cast<size_t>(row) * H + h;
   stv<E, V>(K + o, k);
   stv<E, V>(Vv + o, v);
-  stv<E, V>(Vn + o, vn);
+  if (Vn) {  // absent when the read folds successor rows into V (no next rows needed)
+    int64_t tn = nidx[row];
+    tn = tn < 0 ? 0 : (tn >= T ? T - 1 : tn);
+    float vn[V];
+    ldv<E, V>(w + (static_cast<size_t>(b) * T + tn) * H + h, vn);
+    stv<E, V>(Vn + o, vn);
+  }
 }
 
-// One workgroup per (b, t) position of the write tape.
+// One workgroup per (b, t) position of the write tape; writes gw[t] (zero where no slot
+// maps to t). gVn may be null (no successor-row gradients).
 template <typename E, int V>
 __global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int N, int H, const float* norm_w,
                                                          const int32_t* rank, const E* K,
@@ -251,10 +255,9 @@ __global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int N, int H, co
   const int t = static_cast<int>(bt % T);
   const int32_t* rk = rank + static_cast<size_t>(b) * T;
   const int r0 = rk[t];
-  const int r1 = t >= 1 ? rk[t - 1] : N;
-  const int r2 = t == T - 1 ? rk[T - 1] : N;
+  const int r1 = gVn && t >= 1 ? rk[t - 1] : N;
+  const int r2 = gVn && t == T - 1 ? rk[T - 1] : N;
   const bool in0 = r0 < N, in1 = r1 < N, in2 = r2 < N;
-  if (!in0 && !in1 && !in2) return;
   const float nrm = norm_w[bt];
   const float n = fmaxf(nrm, kEps);
   float dot = 0.0f;
@@ -276,7 +279,8 @@ __global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int N, int H, co
   for (int h = threadIdx.x * V; h < H; h += 256 * V) {
     const size_t o = static_cast<size_t>(bt) * H + h;
     float acc[V];
-    ldv<E, V>(gw + o, acc);
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[e] = 0.0f;
     if (in0) {
       const size_t kb = (static_cast<size_t>(b) * N + r0) * H + h;
       float gk[V], gv[V], k[V];
@@ -301,6 +305,30 @@ __global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int N, int H, co
     }
     stv<E, V>(gw + o, acc);
   }
+}
+
+// Successor-fold codes of a bank selected by select_kernel (slot order = admitted positions
+// ascending; next position = min(idx + 1, T - 1), as the read builds it): for slot j of row
+// b, 1 when its next position is the position of slot j + 1, 0 when the next position is
+// its own (the clamped last position) or the slot is past the row's count, 2 otherwise (no
+// fold). One thread per slot; `codes` (width N) and `unfoldable` (set to 1 when any valid
+// slot codes 2, never cleared here) are each optional.
+__global__ void __launch_bounds__(256) fold_kernel(int T, int N, const int64_t* order,
+                                                   const int64_t* counts, int8_t* codes,
+                                                   uint32_t* unfoldable) {
+  const int b = blockIdx.y;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const int64_t cnt = counts[b];
+  int code = 0;
+  if (j < T && j < cnt) {
+    const int64_t* ob = order + static_cast<size_t>(b) * T;
+    const int64_t i = ob[j];
+    const int64_t nx = i + 1 < T ? i + 1 : T - 1;
+    code = nx == i ? 0 : (j + 1 < cnt && ob[j + 1] == nx ? 1 : 2);
+  }
+  if (codes && j < N) codes[static_cast<size_t>(b) * N + j] = static_cast<int8_t>(code);
+  if (unfoldable && __any(code == 2) && (threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_or(unfoldable, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace glue
@@ -572,12 +600,30 @@ int dabsn_hip_bank_select(int adm_dtype, int whole, int64_t B, int64_t T, const 
   return DABSN_OK;
 }
 
+int dabsn_hip_bank_fold(int64_t B, int64_t T, int64_t N, const int64_t* order,
+                        const int64_t* counts, int8_t* codes, uint32_t* unfoldable,
+                        hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && B < 65536 && T > 0 && N >= 0 && N <= T && T < (1ll << 31),
+                "bank_fold: bad shape");
+  DABSN_REQUIRE(order && counts && (codes || unfoldable), "bank_fold: null pointer");
+  if (unfoldable) {
+    const int rc = dabsn_hip_zero(unfoldable, 4, stream);
+    if (rc != DABSN_OK) return rc;
+  }
+  const int64_t width = unfoldable ? T : N;  // the flag covers every admitted slot
+  if (width == 0) return DABSN_OK;
+  hipLaunchKernelGGL(fold_kernel, dim3(blocks_for(width, 256), (unsigned)B), dim3(256), 0, stream,
+                     (int)T, (int)N, order, counts, codes, unfoldable);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
 int dabsn_hip_bank_gather(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* w,
                           const float* norm_w, const int64_t* idx, const int64_t* next_idx,
                           void* K, void* V, void* Vn, hipStream_t stream) {
   DABSN_REQUIRE(B > 0 && T > 0 && N >= 0 && H > 0, "bank_gather: bad shape");
   if (N == 0) return DABSN_OK;
-  DABSN_REQUIRE(w && norm_w && idx && next_idx && K && V && Vn, "bank_gather: null pointer");
+  DABSN_REQUIRE(w && norm_w && idx && K && V && (next_idx || !Vn), "bank_gather: null pointer");
   const bool vec = vec_ok(H, {w, K, V, Vn});
   const int hblocks = static_cast<int>(blocks_for(H, 256 * (vec ? 8 : 1)));
   DABSN_REQUIRE(B * N * hblocks <= 2147483647ll, "bank_gather: too many bank rows");
@@ -597,8 +643,9 @@ int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_
                               void* gw, hipStream_t stream) {
   (void)w;
   DABSN_REQUIRE(B > 0 && T > 0 && N >= 0 && H > 0, "bank_gather backward: bad shape");
-  if (N == 0) return DABSN_OK;
-  DABSN_REQUIRE(norm_w && rank && K && gK && gV && gVn && gw, "bank_gather backward: null pointer");
+  // Every position is written (zero where no slot maps to it), N == 0 included.
+  DABSN_REQUIRE(gw && norm_w && rank && (N == 0 || (K && gK && gV)),
+                "bank_gather backward: null pointer");
   DABSN_REQUIRE(B * T <= 2147483647ll, "bank_gather backward: too many positions");
   const dim3 grid((unsigned)(B * T)), block(256);
   const bool vec = vec_ok(H, {K, gK, gV, gVn, gw});

@@ -1,20 +1,17 @@
-"""Time-chunked core scan with a checkpointed, pipelined reverse pass.
+"""Time-chunked core scan: one launch per chunk, carried state, reverse scans on kept tapes.
 
 Reference behaviour: src/dabsn/model.py:274-307. The block scan runs in time chunks of
 ``chunk_t`` steps with the (b, e, c) state carried from chunk to chunk, and every chunk is
-checkpointed, so the backward recomputes a chunk's forward scan right before running its
-reverse scan. The same work is scheduled differently here:
+checkpointed, so the reference's backward recomputes a chunk's forward scan right before
+running its reverse scan. Checkpointing is a memory policy, not part of the result, and
+the three-way read needs the tapes of the whole sequence at once, so here:
 
 * every chunk reads and writes its time window of full-length tensors in place (the C call
   descriptors carry a time stride ``ldt``), so there are no per-chunk copies or
   concatenations;
-* the recompute of chunk k - 1 depends only on the saved start state of that chunk, not on
-  the reverse scan of chunk k, so the two run as one cooperative launch on disjoint halves
-  of the device (``dabsn_hip_core_scan_pair``). When the device cannot hold both grids at
-  once the two launches run one after the other;
-* the last chunk is not recomputed: its reverse scan, which runs first, reads the tapes
-  the forward wrote (the way ``torch.utils.checkpoint.checkpoint_sequential`` leaves its
-  last segment un-checkpointed).
+* the full-length tapes stay resident in HBM from the forward to the backward (config 4
+  holds 2.3 GB of them on a 288 GB device) and every chunk's reverse scan reads its window
+  there, so no chunk is recomputed.
 
 Outputs equal the single full-length scan bit for bit; gradients equal it up to the
 rounding of the carried state gradient at chunk boundaries.
@@ -82,12 +79,12 @@ class _Bwd:
 
     `outs` = (gWx, gWgx, day), full-length [B, T, H]; the scan writes its window of each."""
 
-    def __init__(self, code: int, GAT: Tensor, params, b0: Tensor, c0: Tensor, rec: _Tapes,
+    def __init__(self, code: int, GAT: Tensor, params, b0: Tensor, c0: Tensor, src: _Tapes,
                  grads: Sequence[Optional[Tensor]], gfin: Sequence[Optional[Tensor]],
                  outs: Sequence[Tensor], t0: int, t1: int) -> None:
         lib = _lib.load()
         B, T, H = outs[0].shape
-        self.keep = (GAT, b0, c0, rec, *[g for g in grads if g is not None],
+        self.keep = (GAT, b0, c0, src, *[g for g in grads if g is not None],
                      *[g for g in gfin if g is not None], *outs)
         nbg, nwg = _lib.i64(), _lib.i64()
         _lib.check(lib.dabsn_hip_core_scan_layout(code, B, H, ctypes.byref(nbg), ctypes.byref(nwg)),
@@ -100,10 +97,10 @@ class _Bwd:
         self.ws = _empty((nbytes,), like, torch.uint8)
         self.params = params
         o = t0 * H
-        saved = (rec.tapes[1], rec.tapes[2], rec.tapes[4], rec.tapes[5], rec.tapes[6])
+        saved = (src.tapes[1], src.tapes[2], src.tapes[4], src.tapes[5], src.tapes[6])
         self.call = _lib.CoreBwdCall(
             code, B, t1 - t0, H, T, _ptr(GAT), ctypes.pointer(params), _ptr(b0), _ptr(c0),
-            _ptr(rec.U, 2 * o), *[_ptr(x, o) for x in saved],
+            _ptr(src.U, 2 * o), *[_ptr(x, o) for x in saved],
             _ptr(grads[0], 2 * o), *[_ptr(g, o) for g in grads[1:]],
             *[_ptr(g) for g in gfin], *[_ptr(x, o) for x in outs], _ptr(self.part_vec),
             _ptr(self.part_scal), *[_ptr(g) for g in self.g0], _ptr(self.ws), nbytes)
@@ -111,27 +108,6 @@ class _Bwd:
     def launch(self, stream) -> None:
         _lib.check(_lib.load().dabsn_hip_core_scan_bwd_call(ctypes.byref(self.call), stream),
                    "core scan backward")
-
-
-def _launch_pair(fwd: _Fwd, bwd: _Bwd, stream) -> None:
-    """Recompute `fwd` while `bwd` runs; one after the other if the device is too small."""
-    lib = _lib.load()
-    rc = lib.dabsn_hip_core_scan_pair(ctypes.byref(fwd.call), ctypes.byref(bwd.call), stream)
-    if rc == -3:  # DABSN_ERR_UNSUPPORTED: nothing was enqueued
-        c = fwd.call
-        events.report_fallback(
-            "core_scan_chunked",
-            "the recompute and reverse-scan grids do not fit the device together",
-            requested_path="recompute of chunk k-1 beside the reverse scan of chunk k, one "
-                           "cooperative launch",
-            selected_path="the recompute, then the reverse scan, as separate launches",
-            corrective_action="call with fewer batch rows per device so that both grids are "
-                              "resident at once (each takes its own CUs)",
-            B=int(c.B), H=int(c.H), dtype="bf16" if c.dtype == 1 else "fp32")
-        fwd.launch(stream)
-        bwd.launch(stream)
-    else:
-        _lib.check(rc, "core scan pair")
 
 
 def _chunks(T: int, chunk: int) -> list[tuple[int, int]]:
@@ -149,7 +125,7 @@ class _ChunkedCoreScan(torch.autograd.Function):
         dt = Wx.dtype
         code = ops._code(dt)
         stream = ops._stream(Wx)
-        events.announce("core_scan_chunked", "rocm_checkpointed_pair_pipeline", B=B, H=H,
+        events.announce("core_scan_chunked", "rocm_chunked_kept_tapes", B=B, H=H,
                         chunk=int(chunk), dtype="bf16" if code == 1 else "fp32")
         ops.core_launch_check(code, B, min(T, chunk), H, False)
         GA = torch.cat((Ug, A), dim=0).to(dt).contiguous()
@@ -171,11 +147,9 @@ class _ChunkedCoreScan(torch.autograd.Function):
         ctx.chunk = chunk
         ctx.ldx = ldx
         ctx.meta = [(x.dtype, tuple(x.shape)) for x in inputs]
-        # The forward's own outputs are kept for the backward: the last chunk's reverse scan
-        # reads its window there instead of recomputing tapes that were written just before
-        # (as torch.utils.checkpoint.checkpoint_sequential leaves its last segment
-        # un-checkpointed), and the grad [Ug; A] GEMM reads y from U. Every other chunk is
-        # recomputed from its saved start state, as the block checkpoint does.
+        # The forward's own outputs are kept for the backward: every chunk's reverse scan
+        # reads its window of them, and the grad [Ug; A] GEMM reads y from U. Only the chunk
+        # start states are added (the reverse step of a chunk's first step needs them).
         ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, torch.stack(starts), out.U,
                               *out.tapes)
         ctx.set_materialize_grads(False)
@@ -201,34 +175,14 @@ class _ChunkedCoreScan(torch.autograd.Function):
         up = [None if g is None else g.to(dt).contiguous() for g in grads[:7]]
         carry = [None if g is None else g.float().contiguous() for g in grads[8:11]]
         gWx, gWgx, day = (_empty((B, T, H), Wx) for _ in range(3))
-        # Recomputed forward outputs, filled window by window (none when there is one chunk).
-        rec = _Tapes(Wx, B, T, H) if K > 1 else None
-
-        def fwd_of(k: int) -> _Fwd:
-            return _Fwd(code, Wx, Wgx, GA, params, starts[k, 0].contiguous(),
-                        starts[k, 1].contiguous(), starts[k, 2].contiguous(), rec, *bounds[k],
-                        ctx.ldx)
-
         gvec = torch.zeros((16, H), device=Wx.device, dtype=torch.float32)
         gscal = torch.zeros((3,), device=Wx.device, dtype=torch.float32)
         for k in range(K - 1, -1, -1):
-            # The last chunk reads the forward's own tapes; every earlier one reads the
-            # window its recompute wrote during the previous (paired) launch.
-            src = fwd_out if k == K - 1 else rec
             bw = _Bwd(code, GAT, params, starts[k, 0].contiguous(), starts[k, 2].contiguous(),
-                      src, up, carry, (gWx, gWgx, day), *bounds[k])
-            if k > 0:
-                # The recompute writes window k - 1 of `rec` while this reverse scan reads
-                # window k: disjoint rows of the same buffers.
-                nxt = fwd_of(k - 1)
-                tk = ops.KernelTimer.begin("core_scan_pair", Wx)
-                _launch_pair(nxt, bw, stream)
-                ops.KernelTimer.end(tk)
-                ops._record_error_word(nxt.ws, "core scan forward")
-            else:
-                tk = ops.KernelTimer.begin("core_scan_bwd", Wx)
-                bw.launch(stream)
-                ops.KernelTimer.end(tk)
+                      fwd_out, up, carry, (gWx, gWgx, day), *bounds[k])
+            tk = ops.KernelTimer.begin("core_scan_bwd", Wx)
+            bw.launch(stream)
+            ops.KernelTimer.end(tk)
             ops._record_error_word(bw.ws, "core scan backward")
             gvec += bw.part_vec.sum(0)
             gscal += bw.part_scal.sum(0)
@@ -245,8 +199,9 @@ class _ChunkedCoreScan(torch.autograd.Function):
 
 def chunked_core_scan(chunk: int, Wx: Tensor, Wgx: Tensor, Ug: Tensor, A: Tensor,
                       *rest: Tensor) -> tuple[Tensor, ...]:
-    """dabsn::core_scan_batched over time chunks of `chunk` steps (checkpointed: the
-    backward recomputes each chunk's forward scan). Same 26 inputs and 11 outputs as the op."""
+    """dabsn::core_scan_batched over time chunks of `chunk` steps with the (b, e, c) state
+    carried between them; the backward runs the chunks' reverse scans, last chunk first, on
+    the tapes the forward kept. Same 26 inputs and 11 outputs as the op."""
     if len(rest) != 22:
         raise TypeError("chunked_core_scan takes the 26 inputs of dabsn::core_scan_batched")
     if Wx.shape[1] == 0:

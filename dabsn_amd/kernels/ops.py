@@ -1213,17 +1213,19 @@ def _bank_gather_fake(write, norm_w, idx, next_idx, rank):
 
 @torch.library.custom_op(_q("_bank_gather_backward"), mutates_args=(), device_types="cuda")
 def bank_gather_backward(write: Tensor, norm_w: Tensor, rank: Tensor, K: Tensor, gK: Tensor,
-                         gV: Tensor, gVn: Tensor) -> Tensor:
-    """Deterministic inverse gather of the bank gradients onto the write tape."""
+                         gV: Tensor, gVn: Optional[Tensor]) -> Tensor:
+    """Deterministic inverse gather of the bank gradients onto the write tape (gVn None: no
+    successor-row gradients)."""
     lib = _lib.load()
     B, T, H = write.shape
     N = K.shape[1]
     dt = write.dtype
-    gw = torch.zeros((B, T, H), device=write.device, dtype=dt)
+    gw = torch.empty((B, T, H), device=write.device, dtype=dt)
     nw = norm_w.float().contiguous()
     rk = rank.to(torch.int32).contiguous()
     Kc = K.to(dt).contiguous()
-    gKc, gVc, gVnc = (g.to(dt).contiguous() for g in (gK, gV, gVn))
+    gKc, gVc = (g.to(dt).contiguous() for g in (gK, gV))
+    gVnc = None if gVn is None else gVn.to(dt).contiguous()
     _lib.check(lib.dabsn_hip_bank_gather_bwd(_code(dt), B, T, N, H, None, _p(nw), _p(rk), _p(Kc),
                                              _p(gKc), _p(gVc), _p(gVnc), _p(gw), _stream(write)),
                "bank gather backward")
@@ -1243,11 +1245,71 @@ def _gather_setup(ctx, inputs, output):
 def _gather_bwd(ctx, gK, gV, gVn):
     write, norm_w, rank, K = ctx.saved_tensors
     z = lambda g: torch.zeros_like(K) if g is None else g  # noqa: E731
-    gw = bank_gather_backward(write, norm_w, rank, K, z(gK), z(gV), z(gVn))
+    gw = bank_gather_backward(write, norm_w, rank, K, z(gK), z(gV), gVn)
     return gw, None, None, None, None
 
 
 torch.library.register_autograd(_q("bank_gather"), _gather_bwd, setup_context=_gather_setup)
+
+
+@torch.library.custom_op(_q("bank_gather_kv"), mutates_args=(), device_types="cuda")
+def bank_gather_kv(write: Tensor, norm_w: Tensor, idx: Tensor, rank: Tensor) -> tuple[Tensor, Tensor]:
+    """(normalize(write[idx]), write[idx]): ``bank_gather`` without the successor rows, for
+    a read that folds them into V (``bank_fold``)."""
+    lib = _lib.load()
+    B, T, H = write.shape
+    N = idx.shape[1]
+    w = write.contiguous()
+    nw = norm_w.float().contiguous()
+    ic = idx.to(torch.int64).contiguous()
+    K, V = (torch.empty((B, N, H), device=w.device, dtype=w.dtype) for _ in range(2))
+    _lib.check(lib.dabsn_hip_bank_gather(_code(w.dtype), B, T, N, H, _p(w), _p(nw), _p(ic), None,
+                                         _p(K), _p(V), None, _stream(w)), "bank gather")
+    return K, V
+
+
+@bank_gather_kv.register_fake
+def _bank_gather_kv_fake(write, norm_w, idx, rank):
+    B, T, H = write.shape
+    N = idx.shape[1]
+    return write.new_empty((B, N, H)), write.new_empty((B, N, H))
+
+
+def _gather_kv_setup(ctx, inputs, output):
+    write, norm_w, idx, rank = inputs
+    ctx.save_for_backward(write, norm_w, rank, output[0])
+
+
+def _gather_kv_bwd(ctx, gK, gV):
+    write, norm_w, rank, K = ctx.saved_tensors
+    z = lambda g: torch.zeros_like(K) if g is None else g  # noqa: E731
+    gw = bank_gather_backward(write, norm_w, rank, K, z(gK), z(gV), None)
+    return gw, None, None, None
+
+
+torch.library.register_autograd(_q("bank_gather_kv"), _gather_kv_bwd, setup_context=_gather_kv_setup)
+
+
+def bank_fold(order: Tensor, counts: Tensor, width: Optional[int] = None):
+    """Successor-fold codes of a ``bank_select`` result (``dabsn_hip_bank_fold``).
+
+    width None: returns a one-element int32 device tensor, 1 when some admitted slot's next
+    position (min(idx + 1, T - 1)) is neither the next slot's position nor its own, else 0
+    (no host sync). width N: returns the int8 codes [B, N] (1: the next position is slot
+    j + 1's; 0: its own, or past the row's count; 2: neither)."""
+    lib = _lib.load()
+    B, T = order.shape
+    o = order.contiguous()
+    c = counts.contiguous()
+    if width is None:
+        flag = torch.empty((1,), device=order.device, dtype=torch.int32)
+        _lib.check(lib.dabsn_hip_bank_fold(B, T, T, _p(o), _p(c), None, _p(flag), _stream(o)),
+                   "bank fold")
+        return flag
+    codes = torch.empty((B, int(width)), device=order.device, dtype=torch.int8)
+    _lib.check(lib.dabsn_hip_bank_fold(B, T, int(width), _p(o), _p(c), _p(codes), None,
+                                       _stream(o)), "bank fold")
+    return codes
 
 
 # ---------------------------------------------------------------------------
@@ -1257,7 +1319,8 @@ def _read_common(query, bank_keys, bank_writes, next_writes, cocktail, bank_cock
                  bank_key_bias, bank_admission, scale, bank_idx, bank_valid, gains):
     dt = query.dtype
     q = query.contiguous()
-    K, V, Vn = (x.to(dt).contiguous() for x in (bank_keys, bank_writes, next_writes))
+    K, V = (x.to(dt).contiguous() for x in (bank_keys, bank_writes))
+    Vn = None if next_writes is None else next_writes.to(dt).contiguous()
     ck, cb, kb, adm = (x.float().contiguous() for x in (cocktail, bank_cocktail, bank_key_bias,
                                                        bank_admission))
     sc = scale.float().reshape(()).contiguous()
@@ -1609,14 +1672,15 @@ torch.library.register_autograd(_q("admitted_three_way_read_native"), _dense_rea
 # external callers; the read module uses ``admitted_three_way_read_train``.
 @torch.library.custom_op(_q("_read3_fwd_keep"), mutates_args=(), device_types="cuda")
 def read3_fwd_keep(
-    query: Tensor, bank_keys: Tensor, bank_writes: Tensor, next_writes: Tensor, cocktail: Tensor,
-    bank_cocktail: Tensor, bank_key_bias: Tensor, bank_admission: Tensor, scale: Tensor,
-    bank_idx: Tensor, bank_valid: Tensor, mode: int, short_gain: Tensor, pad_gain: Tensor,
-    induct_gain: Tensor, cocktail_gain: Tensor,
+    query: Tensor, bank_keys: Tensor, bank_writes: Tensor, next_writes: Optional[Tensor],
+    cocktail: Tensor, bank_cocktail: Tensor, bank_key_bias: Tensor, bank_admission: Tensor,
+    scale: Tensor, bank_idx: Tensor, bank_valid: Tensor, mode: int, short_gain: Tensor,
+    pad_gain: Tensor, induct_gain: Tensor, cocktail_gain: Tensor, fold: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor]:
     """The three-way read forward; returns (out, kept) where ``kept`` holds the scores, tile
     ranges and row statistics that ``read3_bwd_kept`` reads (the forward's other scratch is
-    released when the call returns)."""
+    released when the call returns). ``fold`` (int8 [B, N], ``bank_fold`` codes 0/1 only)
+    states next_writes[j] = bank_writes[j + fold[j]]; next_writes may then be None."""
     _require_cuda(query)
     lib = _lib.load()
     if mode not in (0, 1):
@@ -1628,6 +1692,7 @@ def read3_fwd_keep(
     B, T, H = q.shape
     N = K.shape[1]
     code = _code(dt)
+    fc = _fold_codes(fold, B, N, Vn)
     out = torch.empty_like(q)
     kept = torch.empty(max(lib.dabsn_hip_read3_workspace_bytes(code, B, T, N, H, 2), 256),
                        dtype=torch.uint8, device=q.device)
@@ -1637,7 +1702,7 @@ def read3_fwd_keep(
     tk = KernelTimer.begin("read3_fwd", q)
     _lib.check(lib.dabsn_hip_read3_fwd_keep(
         code, B, T, N, H, _p(q), _p(K), _p(V), _p(Vn), _p(ck), _p(cb), _p(kb), _p(adm), _p(sc),
-        _p(idx), _p(valid), mode, ptrs, _p(out), _p(kept), kept.numel(), _p(scratch),
+        _p(idx), _p(valid), _p(fc), mode, ptrs, _p(out), _p(kept), kept.numel(), _p(scratch),
         scratch.numel(), _stream(q)), "three-way read")
     KernelTimer.end(tk)
     return out, kept
@@ -1648,18 +1713,31 @@ def _read3_fwd_keep_fake(query, *rest):
     return torch.empty_like(query), query.new_empty((256,), dtype=torch.uint8)
 
 
+def _fold_codes(fold: Optional[Tensor], B: int, N: int, Vn: Optional[Tensor]) -> Optional[Tensor]:
+    """The fold codes as the kernels take them (int8 [B, N], contiguous), or None; without
+    them the successor rows must be given."""
+    if fold is None:
+        if Vn is None:
+            raise ValueError("three-way read: next_writes may be None only with a fold")
+        return None
+    if fold.shape != (B, N):
+        raise ValueError(f"three-way read: fold must be [B, N] = {(B, N)}, got {tuple(fold.shape)}")
+    return fold.to(torch.int8).contiguous()
+
+
 @torch.library.custom_op(_q("_read3_bwd_kept"), mutates_args=(), device_types="cuda")
 def read3_bwd_kept(
     grad_output: Tensor, query: Tensor, bank_keys: Tensor, bank_writes: Tensor,
-    next_writes: Tensor, cocktail: Tensor, bank_cocktail: Tensor, bank_key_bias: Tensor,
+    next_writes: Optional[Tensor], cocktail: Tensor, bank_cocktail: Tensor, bank_key_bias: Tensor,
     bank_admission: Tensor, scale: Tensor, bank_idx: Tensor, bank_valid: Tensor, mode: int,
     short_gain: Tensor, pad_gain: Tensor, induct_gain: Tensor, cocktail_gain: Tensor,
-    workspace: Tensor,
+    workspace: Tensor, fold: Optional[Tensor] = None,
 ) -> CompactGradients:
     """``admitted_three_way_read_compact_flash_backward`` on the kept buffer of a
     ``read3_fwd_keep`` call with the same inputs (``dabsn_hip_read3_bwd_after_fwd``). The
     kept buffer is only read, so a second backward through the same graph sees it
-    unchanged."""
+    unchanged. With ``fold`` the successor-row gradient is part of the bank-write gradient
+    and the next_writes gradient comes back empty ([0])."""
     _require_cuda(query)
     lib = _lib.load()
     dt, q, K, V, Vn, ck, cb, kb, adm, sc, g, idx, valid = _read_common(
@@ -1668,9 +1746,12 @@ def read3_bwd_kept(
         (short_gain, pad_gain, induct_gain, cocktail_gain))
     B, T, H = q.shape
     N = K.shape[1]
+    fc = _fold_codes(fold, B, N, Vn)
     go = grad_output.to(dt).contiguous()
     gq = torch.empty_like(q)
-    gK, gV, gVn = (torch.empty((B, N, H), device=q.device, dtype=dt) for _ in range(3))
+    gK, gV = (torch.empty((B, N, H), device=q.device, dtype=dt) for _ in range(2))
+    gVn = (torch.empty((B, N, H), device=q.device, dtype=dt) if fc is None
+           else q.new_empty((0,)))
     gck = torch.empty((B, T, 4), device=q.device, dtype=torch.float32)
     gcb = torch.empty((B, N, 4), device=q.device, dtype=torch.float32)
     gkb = torch.empty((B, N), device=q.device, dtype=torch.float32)
@@ -1682,11 +1763,13 @@ def read3_bwd_kept(
     tk = KernelTimer.begin("read3_bwd", q)
     _lib.check(lib.dabsn_hip_read3_bwd_after_fwd(
         _code(dt), B, T, N, H, _p(go), _p(q), _p(K), _p(V), _p(Vn), _p(ck), _p(cb), _p(kb),
-        _p(adm), _p(sc), _p(idx), _p(valid), mode, ptrs, _p(gq), _p(gK), _p(gV), _p(gVn),
-        _p(gck), _p(gcb), _p(gkb), _p(gadm), _p(g5), _p(workspace), workspace.numel(),
-        _p(scratch), scratch.numel(), _stream(q)), "three-way read backward")
+        _p(adm), _p(sc), _p(idx), _p(valid), _p(fc), mode, ptrs, _p(gq), _p(gK), _p(gV),
+        None if fc is not None else _p(gVn), _p(gck), _p(gcb), _p(gkb), _p(gadm), _p(g5),
+        _p(workspace), workspace.numel(), _p(scratch), scratch.numel(), _stream(q)),
+        "three-way read backward")
     KernelTimer.end(tk)
-    return (gq, gK.to(bank_keys.dtype), gV.to(bank_writes.dtype), gVn.to(next_writes.dtype),
+    return (gq, gK.to(bank_keys.dtype), gV.to(bank_writes.dtype),
+            gVn if next_writes is None else gVn.to(next_writes.dtype),
             gck.to(cocktail.dtype), gcb.to(bank_cocktail.dtype), gkb.to(bank_key_bias.dtype),
             gadm.to(bank_admission.dtype),
             g5[0].clone().reshape_as(scale).to(scale.dtype),
@@ -1699,34 +1782,46 @@ def read3_bwd_kept(
 @read3_bwd_kept.register_fake
 def _read3_bwd_kept_fake(grad_output, query, bank_keys, bank_writes, next_writes, cocktail,
                          bank_cocktail, bank_key_bias, bank_admission, scale, bank_idx, bank_valid,
-                         mode, short_gain, pad_gain, induct_gain, cocktail_gain, workspace):
-    return tuple(torch.empty_like(v) for v in (
-        query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+                         mode, short_gain, pad_gain, induct_gain, cocktail_gain, workspace,
+                         fold=None):
+    gvn = query.new_empty((0,)) if fold is not None else torch.empty_like(next_writes)
+    return tuple(torch.empty_like(v) if v is not None else gvn for v in (
+        query, bank_keys, bank_writes, None, cocktail, bank_cocktail, bank_key_bias,
         bank_admission, scale, short_gain, pad_gain, induct_gain, cocktail_gain))
 
 
 class _Read3Train(torch.autograd.Function):
+    """Inputs: the 16 of the compact read (next_writes may be None with a fold), then the
+    fold codes or None."""
+
     @staticmethod
     def forward(ctx, *inputs):
-        out, ws = read3_fwd_keep(*inputs)
-        ctx.save_for_backward(*inputs[:11], *inputs[12:], ws)
+        fold = inputs[16]
+        out, ws = read3_fwd_keep(*inputs[:16], fold)
+        ctx.save_for_backward(*inputs[:11], *inputs[12:16], ws, fold)
         ctx.mode = int(inputs[11])
         return out
 
     @staticmethod
     def backward(ctx, grad_output):
         t = ctx.saved_tensors
-        g = read3_bwd_kept(grad_output.contiguous(), *t[:11], ctx.mode, *t[11:15], t[15])
-        return (*g[:9], None, None, None, *g[9:])
+        fold = t[16]
+        g = read3_bwd_kept(grad_output.contiguous(), *t[:11], ctx.mode, *t[11:15], t[15], fold)
+        gvn = None if fold is not None else g[3]
+        return (*g[:3], gvn, *g[4:9], None, None, None, *g[9:], None)
 
 
-def admitted_three_way_read_train(*inputs) -> Tensor:
+def admitted_three_way_read_train(*inputs, fold: Optional[Tensor] = None) -> Tensor:
     """``admitted_three_way_read_compact_flash`` (same 16 inputs and result) for callers
     that will differentiate it: under autograd the forward's workspace is kept for the
-    backward; otherwise this is the registered op."""
+    backward; otherwise this is the registered op. ``fold``: successor-fold codes
+    (``bank_fold``) for a bank whose successor rows are bank rows; inputs[3] (next_writes)
+    may then be None."""
     if inputs[0].is_cuda and torch.is_grad_enabled() and any(
             isinstance(x, Tensor) and x.requires_grad for x in inputs):
-        return _Read3Train.apply(*inputs)
+        return _Read3Train.apply(*inputs, fold)
+    if fold is not None:
+        return read3_fwd_keep(*inputs, fold)[0]
     return admitted_three_way_read_compact_flash(*inputs)
 
 
@@ -1764,6 +1859,7 @@ OPERATORS = (
     _q("_normalize_rows_backward"),
     _q("bank_select"),
     _q("bank_gather"),
+    _q("bank_gather_kv"),
     _q("_bank_gather_backward"),
     _q("admitted_three_way_read_compact_flash"),
     _q("_admitted_three_way_read_compact_flash_backward"),

@@ -107,8 +107,7 @@ def copy_probe(mib: int, reps: int = 5) -> None:
 
 
 # Core scan kernels by the names bench.py reports them under.
-_CORE_KERNELS = {"core_fwd_kernel": "core_scan_fwd", "core_bwd_kernel": "core_scan_bwd",
-                 "core_pair_kernel": "core_scan_pair"}
+_CORE_KERNELS = {"core_fwd_kernel": "core_scan_fwd", "core_bwd_kernel": "core_scan_bwd"}
 
 
 def _one(rows: list[dict[str, object]], counter: str, match: str) -> dict[str, object]:

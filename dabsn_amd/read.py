@@ -136,22 +136,34 @@ class DABSNRead(nn.Module):
         self._capture_bank_width: int | None = None
 
     # ---- selection ------------------------------------------------------------
-    def _select(self, admission: Tensor, length: int, width: int | None = None):
+    def _select(self, admission: Tensor, length: int, width: int | None = None,
+                want_fold: bool = False):
+        """Slot selection: (n_max, idx, valid, next_idx, rank, fold). ``fold`` is the
+        successor-fold code array [B, n_max] when ``want_fold`` and every admitted slot's next
+        position is a bank row (``ops.bank_fold``), else None; the check rides on the host
+        sync of the bank width."""
         window = F.softplus(self.admit_window)
         # seq: floor from the causal prefix max; field / hybrid: the whole sequence's max
         # (read.py:185-191)
         whole = 0 if self.read_geometry == "seq" else 1
         order, counts, rank = ops.direct.bank_select(admission.detach(), window.detach(), whole)
+        fold = None
         if width or self._capture_bank_width:
             # A fixed width needs no host sync; slots past a row's admitted count are
             # masked out by `valid`.
             n_max = max(1, min(int(width or self._capture_bank_width), length))
+        elif want_fold:
+            unfoldable = ops.bank_fold(order, counts)
+            top, bad = torch.stack((counts.max(), unfoldable[0].to(counts.dtype))).tolist()
+            n_max = max(int(top), 1)  # one host sync, as read.py:233
+            if not bad:
+                fold = ops.bank_fold(order, counts, n_max)
         else:
             n_max = max(int(counts.max().item()), 1)  # host sync, as read.py:233
         idx = order[:, :n_max]
         valid = torch.arange(n_max, device=admission.device).unsqueeze(0) < counts.clamp_min(1).unsqueeze(1)
         next_idx = (idx + 1).clamp(max=length - 1)
-        return n_max, idx, valid, next_idx, rank
+        return n_max, idx, valid, next_idx, rank, fold
 
     def _bank(self, cocktail_bank: Tensor, key_bias: Tensor, admission: Tensor, length: int,
               query_start: int, width: int | None = None,
@@ -161,8 +173,12 @@ class DABSNRead(nn.Module):
         admission, the read scale and the slot positions relative to the query chunk.
         ``members`` = (slot list [B, cap], counts [B]) kept incrementally by a carried bank
         (inference): the selection is read from it instead of rerun over the bank."""
+        fold = None
         if members is None:
-            n_max, idx, valid, next_idx, rank = self._select(admission, length, width)
+            # The successor fold serves the training read (gather + read under autograd).
+            want_fold = torch.is_grad_enabled() and admission.is_cuda
+            n_max, idx, valid, next_idx, rank, fold = self._select(admission, length, width,
+                                                                   want_fold)
         else:
             slots, counts = members
             if width or self._capture_bank_width:
@@ -176,6 +192,7 @@ class DABSNRead(nn.Module):
             rank = idx.new_empty((0,), dtype=torch.int32)  # the gather's backward only
         return {
             "n_max": n_max, "idx": idx, "valid": valid, "next_idx": next_idx, "rank": rank,
+            "fold": fold,
             "cocktail": torch.gather(cocktail_bank, 1, idx.unsqueeze(-1).expand(-1, -1, 4)),
             "key_bias": torch.gather(key_bias, 1, idx),
             "admission": torch.gather(admission, 1, idx),
@@ -276,7 +293,14 @@ class DABSNRead(nn.Module):
                 bank_cocktail, bank_bias, bank_adm, scale,
                 (self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain))
         else:
-            K, V, Vn = ops.bank_gather(bank_write, norm_w, idx, next_idx, rank)
+            fold = bank["fold"]
+            if fold is not None:
+                # Every admitted slot's successor row is a bank row (Vn[j] = V[j + fold[j]]):
+                # the read folds the induction products into V and needs no successor rows.
+                K, V = ops.bank_gather_kv(bank_write, norm_w, idx, rank)
+                Vn = None
+            else:
+                K, V, Vn = ops.bank_gather(bank_write, norm_w, idx, next_idx, rank)
 
             def read(mode: int) -> Tensor:
                 # mode 0: causal masks (seq); mode 1: every admitted slot for every query
@@ -284,7 +308,7 @@ class DABSNRead(nn.Module):
                 return ops.admitted_three_way_read_train(
                     query, K, V, Vn, cocktail[0], bank_cocktail, bank_bias, bank_adm, scale,
                     read_idx, valid, mode, self.short_gain, self.pad_gain, self.induct_gain,
-                    self.cocktail_gain)
+                    self.cocktail_gain, fold=fold)
 
             retrieved = self._geometry_mix(read, valid, query)
         self.last_read_contract = self._contract(decode, n_max, length, query, query_start)

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 11
+#define DABSN_HIP_ABI_VERSION 12
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -139,15 +139,6 @@ typedef struct dabsn_core_bwd_call {
 int dabsn_hip_core_scan_fwd_call(const dabsn_core_fwd_call* fwd, hipStream_t stream);
 int dabsn_hip_core_scan_bwd_call(const dabsn_core_bwd_call* bwd, hipStream_t stream);
 
-/* One forward scan and one independent reverse scan of the same (dtype, B, H) in a single
- * cooperative launch. This is the schedule of a checkpointed, time-chunked core scan
- * (src/dabsn/model.py:274-307): while chunk k runs its reverse scan, chunk k - 1 is
- * recomputed. Each call has its own workspace. Returns DABSN_ERR_UNSUPPORTED (nothing
- * launched) when the device cannot hold both grids at once; the caller then runs the two
- * calls one after the other. */
-int dabsn_hip_core_scan_pair(const dabsn_core_fwd_call* fwd, const dabsn_core_bwd_call* bwd,
-                             hipStream_t stream);
-
 /* ---- linear recurrence -----------------------------------------------------------
  * Replaces dabsn::linear_recurrence / dabsn::_linrec_backward
  * (src/dabsn/kernels/long.py:392-437; CPU cpu_runtime.cpp:92-143).
@@ -262,13 +253,25 @@ int dabsn_hip_admit_step(int mode, int64_t B, int64_t n, int64_t base, int64_t c
                          float* cocktail, float* amax, int64_t* mcount, int64_t* members,
                          hipStream_t stream);
 
+/* Successor-fold codes of a selected bank (no reference counterpart: they let the read skip
+ * its successor-row products, see dabsn_hip_read3_fwd_keep). order [B,T] and counts [B]
+ * as dabsn_hip_bank_select returns them; the bank's next positions are min(idx + 1, T - 1).
+ * codes [B,N] (optional): 1 when slot j's next position is slot j + 1's position, 0 when it
+ * is its own position or j >= counts[b], 2 otherwise. unfoldable (optional, one uint32) is
+ * set to 1 when any admitted slot of any row codes 2, else 0. */
+int dabsn_hip_bank_fold(int64_t B, int64_t T, int64_t N, const int64_t* order,
+                        const int64_t* counts, int8_t* codes, uint32_t* unfoldable,
+                        hipStream_t stream);
+
 /* Bank gather (read.py:241-256, 298-303): for j < N, K = w[idx]/max(|w[idx]|,eps),
- * V = w[idx], Vn = w[next_idx] ([B,N,H]). norm_w [B,T] fp32. */
+ * V = w[idx], Vn = w[next_idx] ([B,N,H]). norm_w [B,T] fp32. Vn may be null (then
+ * next_idx is not read): a folded read needs no successor rows. */
 int dabsn_hip_bank_gather(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, const void* w,
                           const float* norm_w, const int64_t* idx, const int64_t* next_idx,
                           void* K, void* V, void* Vn, hipStream_t stream);
 /* Backward, as a deterministic gather over positions using rank [B,T]:
- * gw[t] += (rank[t] < N ? gV + dnorm(gK) : 0) + sum of gVn over slots whose next index is t. */
+ * gw[t] = (rank[t] < N ? gV + dnorm(gK) : 0) + sum of gVn over slots whose next index is t
+ * (written for every position; gVn may be null). */
 int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
                               const void* w, const float* norm_w, const int32_t* rank,
                               const void* K, const void* gK, const void* gV, const void* gVn,
@@ -328,30 +331,38 @@ int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
 /* The forward for a caller that will run the backward on the same inputs: as
  * dabsn_hip_read3_fwd, with the workspace in two buffers. `kept` (part 2 bytes) receives
  * the scores, tile ranges and row statistics; `scratch` (part 3 bytes) is free once the
- * call's work has completed. */
+ * call's work has completed.
+ * `fold` (optional, int8 [B,N]; the successor fold): fold[b][j] in {0, 1} states that the
+ * successor row of every valid slot is a bank row, Vn[j] = V[j + fold[j]] (1: slot j + 1
+ * holds the next position; 0: the clamped last position, Vn[j] = V[j]). The induction
+ * weights then join P_V at those columns and Vn is not read (it may be null): one product
+ * in the output GEMM instead of two. The same `fold` must reach the backward. */
 int dabsn_hip_read3_fwd_keep(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
                              const void* q, const void* K, const void* V, const void* Vn,
                              const float* cocktail, const float* bank_cocktail,
                              const float* key_bias, const float* admission, const float* scale,
-                             const int64_t* idx, const uint8_t* valid, int mode,
-                             const float* const* gains, void* out, void* kept, size_t kept_bytes,
-                             void* scratch, size_t scratch_bytes, hipStream_t stream);
+                             const int64_t* idx, const uint8_t* valid, const int8_t* fold,
+                             int mode, const float* const* gains, void* out, void* kept,
+                             size_t kept_bytes, void* scratch, size_t scratch_bytes,
+                             hipStream_t stream);
 /* The backward without recomputing the forward's scores and row statistics: `kept` is the
  * buffer a dabsn_hip_read3_fwd_keep call on the same inputs filled; it is only read, so
  * the backward can run again on it. `scratch` holds part 4 bytes. Saves the score GEMM
  * and softmax-row pass of the recompute at the cost of keeping B*T*N*4 bytes of scores
- * (plus the row statistics) between forward and backward. */
+ * (plus the row statistics) between forward and backward. With the forward's `fold`, Vn
+ * and gVn may be null: gVn is not formed, the gradient of slot j's successor row is added
+ * to gV[j + fold[j]] (no gO Vn^T and no P_Vn^T gO GEMM). */
 int dabsn_hip_read3_bwd_after_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
                                   const void* gout, const void* q, const void* K, const void* V,
                                   const void* Vn, const float* cocktail,
                                   const float* bank_cocktail, const float* key_bias,
                                   const float* admission, const float* scale,
-                                  const int64_t* idx, const uint8_t* valid, int mode,
-                                  const float* const* gains, void* gq, void* gK, void* gV,
-                                  void* gVn, float* gcocktail, float* gbank_cocktail,
-                                  float* gkey_bias, float* gadmission, float* gscalars5,
-                                  const void* kept, size_t kept_bytes, void* scratch,
-                                  size_t scratch_bytes, hipStream_t stream);
+                                  const int64_t* idx, const uint8_t* valid,
+                                  const int8_t* fold, int mode, const float* const* gains,
+                                  void* gq, void* gK, void* gV, void* gVn, float* gcocktail,
+                                  float* gbank_cocktail, float* gkey_bias, float* gadmission,
+                                  float* gscalars5, const void* kept, size_t kept_bytes,
+                                  void* scratch, size_t scratch_bytes, hipStream_t stream);
 
 /* Decode read: the forward of dabsn_hip_read3_fwd (mode 0, seq) for a few query rows
  * (T <= 8) against a long bank, reading the bank in place instead of from gathered K, V,

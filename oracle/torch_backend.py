@@ -155,7 +155,8 @@ def _gather_bwd(write, norm_w, rank, K, gK, gV, gVn):
     gw = np.zeros((B, T, H), np.float64)
     rows = np.arange(B)[:, None]
     np.add.at(gw, (rows, idx), gKV)
-    np.add.at(gw, (rows, next_idx), _np(gVn).astype(np.float64))
+    if gVn is not None:
+        np.add.at(gw, (rows, next_idx), _np(gVn).astype(np.float64))
     return _t(gw.astype(np.float32), write.dtype)
 
 

@@ -295,7 +295,7 @@ def _window_upstream(outs, r, t0, t1, seed):
 
 
 def test_config4_core_backward_window_vs_oracle(c4):
-    """Upstream gradients on row 3, steps [0, 16), through the checkpointed 1024-step
+    """Upstream gradients on row 3, steps [0, 16), through the 1024-step
     chunked backward, against the oracle's reverse scan of row 3 over those steps on the
     same bf16 tapes."""
     outs = c4["outs"]
@@ -310,9 +310,9 @@ def test_config4_core_backward_window_vs_oracle(c4):
 
 def test_config4_core_backward_across_chunk_boundary_vs_oracle(c4):
     """The same config-4 tensors scanned in 64-step chunks, so a window across a chunk
-    boundary, [56, 72), is reached by a short reverse scan: the backward runs one pair
-    launch (reverse scan of chunk 1 beside the recompute of chunk 0) and the final
-    reverse launch, with the same H = 2048 kernel instances as the 1024-step schedule.
+    boundary, [56, 72), is reached by a short reverse scan: the backward runs the reverse
+    scans of chunks 1 and 0 on the kept tapes, with the same H = 2048 kernel instances as
+    the 1024-step schedule.
     The oracle's reverse scan covers [0, 72) of row 3 (the oracle takes ~70 s per 1000
     steps at this width, so a boundary at 1024 is out of a test's reach)."""
     z = c4["z"]
@@ -329,8 +329,8 @@ def test_config4_core_backward_across_chunk_boundary_vs_oracle(c4):
 
 
 def test_config4_chunked_backward_equals_unchunked(c4):
-    """Random upstream gradients on every output at full size: the 1024-step chunked,
-    checkpointed backward (pair launches) against the unchunked op's backward. They differ
+    """Random upstream gradients on every output at full size: the 1024-step chunked
+    backward against the unchunked op's backward. They differ
     only by the bf16 rounding of the carried state gradient at the chunk boundaries:
     Frobenius 5e-3."""
     outs = c4["outs"]

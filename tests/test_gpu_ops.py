@@ -135,9 +135,7 @@ def test_core_scan_bf16_absent_grads_equal_zero_grads(cuda_device, absent, H):
 def test_core_scan_batch_beyond_one_launch_equals_row_blocks(cuda_device, chunk):
     """At H = 2048 in bf16 one cooperative launch holds two 16-row batch groups (128
     workgroups each on 256 CUs), so B = 40 runs as two slabs (rows 0-31, then the 8 rows
-    32-39). Chunked (chunk=8), the paired recompute + reverse launch does not fit either,
-    so the two run one after the other, each in slabs, while the 16- and 8-row blocks use
-    the paired launch. Rows are independent: forward outputs, per-row input grads and
+    32-39), chunked (chunk=8) or not. Rows are independent: forward outputs, per-row input grads and
     initial-state grads equal separate calls on rows 0-15, 16-31 and 32-39 bit for bit.
     Parameter grads add the same per-group partials in another grouping: fp32 vectors and
     scalars to 1e-5; grad [Ug; A] is a bf16 GEMM over all rows, whose bf16 output rounding
@@ -479,8 +477,8 @@ def test_bank_gather_with_strided_inputs_matches_torch(cuda_device, B, T, H):
 @pytest.mark.parametrize("dtype,B,T,H,chunk,tol", [(torch.float32, 3, 37, 40, 8, 1e-5),
                                                    (torch.bfloat16, 16, 70, 2048, 16, 5e-3)])
 def test_chunked_core_scan_matches_full_op(cuda_device, dtype, B, T, H, chunk, tol):
-    """Checkpointed time chunks whose backward overlaps each recompute with the reverse scan
-    of the next chunk (one paired launch) against one full-length forward and backward.
+    """Time chunks with a carried state, whose backward runs each chunk's reverse scan on the
+    tapes the forward kept, against one full-length forward and backward.
     Forward outputs are bit-identical. Gradients differ only in rounding: at a chunk boundary
     the carried budget gradient is summed in a different order, which in bf16 can move a
     stored gradient element by one bf16 ulp (2^-8 relative), hence 5e-3 Frobenius there."""
