@@ -43,6 +43,8 @@ def parse():
     p.add_argument("--vocab", type=int, default=32000)
     p.add_argument("--chunk", type=int, default=1024)
     p.add_argument("--cpu-seq", type=int, default=64, help="T of the bounded CPU sample")
+    p.add_argument("--no-pipeline", action="store_true",
+                   help="train: scan and read one after the other on the whole device")
     p.add_argument("--no-proj", action="store_true",
                    help="skip the separate timing of the input projections (profiling runs)")
     p.add_argument("--cpu-trials", type=int, default=5,
@@ -71,6 +73,7 @@ class ScanRead(torch.nn.Module):
         self.read = DABSNRead(state)
         self.state = state
         self.chunk = chunk
+        self.pipelined = True
 
     def scan(self, Wx, Wgx):
         from torch.utils.checkpoint import checkpoint
@@ -104,6 +107,14 @@ class ScanRead(torch.nn.Module):
         return [torch.cat(p, 1) if len(p) > 1 else p[0] for p in tapes]
 
     def forward(self, Wx, Wgx):
+        from dabsn_amd.kernels import pipeline
+
+        if self.pipelined and pipeline.pipeline_applies(self.read, Wx, self.chunk):
+            # The read of query chunk k beside the scan of chunk k + 1 (and in reverse in the
+            # backward), on the two halves of the device.
+            U, read = pipeline.pipelined_scan_read(self.read, self.chunk, Wx, Wgx,
+                                                   self.core.scan_inputs())
+            return U.split(self.state, dim=-1)[0], read
         U, nov, p, ay, w, e, c = self.scan(Wx, Wgx)
         y, budget = U.split(self.state, dim=-1)
         return y, self.read(y, budget, ay, w, nov, p, e, c)
@@ -445,6 +456,7 @@ def main():
     device = torch.device("cuda:0")
     dtype = torch.bfloat16
     model, Wx, Wgx, gy, gr = build_workload(args, device, dtype, args.batch, args.seq)
+    model.pipelined = not args.no_pipeline
     for _ in range(args.warmup):
         step(model, Wx, Wgx, gy, gr, "cuda", dtype)
     torch.cuda.synchronize()

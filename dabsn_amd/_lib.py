@@ -42,7 +42,7 @@ class CoreFwdCall(ctypes.Structure):
                  ("Wx", vp), ("Wgx", vp), ("GA", vp), ("params", ctypes.POINTER(CoreParams))]
                 + [(n, vp) for n in ("b0", "e0", "c0", "U", "nov", "plast", "expr", "write",
                                      "energy", "sat", "gate", "bF", "eF", "cF", "workspace")]
-                + [("workspace_bytes", sz), ("state_dtype", i32)])
+                + [("workspace_bytes", sz), ("state_dtype", i32), ("coresident_cus", i32)])
 
 
 class CoreBwdCall(ctypes.Structure):
@@ -54,7 +54,7 @@ class CoreBwdCall(ctypes.Structure):
                                      "gU", "gNov", "gP", "gAy", "gW", "gE", "gC", "gbF", "geF",
                                      "gcF", "gWx", "gWgx", "day", "part_vec", "part_scal", "gb0",
                                      "ge0", "gc0", "workspace")]
-                + [("workspace_bytes", sz)])
+                + [("workspace_bytes", sz), ("coresident_cus", i32)])
 
 _SIGNATURES = {
     "dabsn_hip_abi_version": ([], i32),
@@ -74,6 +74,12 @@ _SIGNATURES = {
         + [vp] * 6 + [vp] * 7 + [vp] * 3 + [vp] * 3 + [vp, vp] + [vp] * 3 + [vp, sz, vp],
         i32,
     ),
+    "dabsn_hip_stream_pair": (
+        [ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(i32), ctypes.POINTER(i32)], i32),
+    "dabsn_hip_tape_stats_window": (
+        [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i64, vp], i32),
+    "dabsn_hip_tape_stats_bwd_window": (
+        [i32, i64, i64, i64, i64, vp, i64, i32, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_core_scan_fwd_call": ([ctypes.POINTER(CoreFwdCall), vp], i32),
     "dabsn_hip_core_scan_bwd_call": ([ctypes.POINTER(CoreBwdCall), vp], i32),
     "dabsn_hip_linrec_fwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp], i32),
@@ -102,6 +108,8 @@ _SIGNATURES = {
     "dabsn_hip_admit_step": (
         [i32, i64, i64, i64, i64, vp, i64, PTR8, vp, i32, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_fold": ([i64, i64, i64, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_bank_gather_bwd_prefix": (
+        [i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, i32, vp, vp], i32),
     "dabsn_hip_bank_gather": ([i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_gather_bwd": (
         [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),

@@ -2,6 +2,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <hip/hip_ext.h>
+
 #include "../../include/dabsn_hip.h"
 #include "capi.hpp"
 #include "common.hpp"
@@ -40,6 +42,40 @@ int dabsn_hip_zero(void* ptr, size_t bytes, hipStream_t stream) {
   hipLaunchKernelGGL(dabsn::zero_words_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      stream, static_cast<uint32_t*>(ptr), words);
   DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+// CU masks of hipExtStreamCreateWithCUMask: bits in alternating groups of 8. The runtime
+// deals mask bits round-robin over the XCDs (8 on MI355X), so a group of 8 consecutive bits
+// is one CU of every XCD and each stream gets half of every XCD's CUs.
+int dabsn_hip_stream_pair(hipStream_t* a, hipStream_t* b, int* cus_a, int* cus_b) {
+  DABSN_REQUIRE(a && b && cus_a && cus_b, "stream pair: null pointer");
+  int dev = 0, cus = 0;
+  DABSN_HIP_CHECK(hipGetDevice(&dev));
+  DABSN_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  DABSN_REQUIRE(cus >= 2 && cus <= 1024, "stream pair: %d CUs", cus);
+  uint32_t ma[32] = {0}, mb[32] = {0};
+  int na = 0, nb = 0;
+  for (int i = 0; i < cus; ++i) {
+    if ((i / 8) % 2 == 0) {
+      ma[i / 32] |= 1u << (i % 32);
+      ++na;
+    } else {
+      mb[i / 32] |= 1u << (i % 32);
+      ++nb;
+    }
+  }
+  DABSN_REQUIRE(na > 0 && nb > 0, "stream pair: %d CUs cannot be split", cus);
+  const uint32_t words = static_cast<uint32_t>((cus + 31) / 32);
+  DABSN_HIP_CHECK(hipExtStreamCreateWithCUMask(a, words, ma));
+  const hipError_t e = hipExtStreamCreateWithCUMask(b, words, mb);
+  if (e != hipSuccess) {
+    (void)hipStreamDestroy(*a);
+    dabsn::set_error("stream pair: %s", hipGetErrorString(e));
+    return DABSN_ERR_HIP;
+  }
+  *cus_a = na;
+  *cus_b = nb;
   return DABSN_OK;
 }
 

@@ -1177,6 +1177,7 @@ __global__ void __launch_bounds__(NW * 64, 1) core_bwd_kernel(BwdArgs<E> a) {
 // ---------------------------------------------------------------------------
 struct Cfg {
   int ch = 0, ksteps = 0, kp = 0, nct = 0, nbg = 0, nw = 0;
+  int plain_cus = 0;  // > 0: plain launches on a stream owning that many CUs (see the header)
 };
 
 // Channel tile width for bf16 beyond H = 1024 (channels per workgroup).
@@ -1233,14 +1234,32 @@ static size_t workspace_bytes(int dtype, const Cfg& c, bool backward, int64_t H)
   return g_offset(dtype, c, H) + static_cast<size_t>(c.nbg) * NB * 2 * H * 4;
 }
 
+// The persistent kernels need every workgroup resident at once. A cooperative launch
+// guarantees it (and the runtime then runs nothing beside it). With plain_cus > 0 the
+// caller guarantees it instead: the stream owns plain_cus CUs (a CU-masked stream) on which
+// nothing else runs while the scan does, so work on the other CUs can overlap the scan.
+// Either way every barrier wait is bounded, so a misplaced launch ends with the error word
+// set rather than a hang.
 template <typename K, typename A>
-static int launch_coop(K kernel, int grid, int threads, const A& args, hipStream_t stream) {
+static int launch_coop(K kernel, int grid, int threads, const A& args, int plain_cus,
+                       hipStream_t stream) {
   int dev = 0;
   DABSN_HIP_CHECK(hipGetDevice(&dev));
   int cus = 0, per_cu = 0, coop = 0;
   DABSN_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
   DABSN_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   DABSN_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0));
+  void* kargs[] = {const_cast<A*>(&args)};
+  if (plain_cus > 0) {
+    if (per_cu * std::min(plain_cus, cus) < grid) {
+      dabsn::set_error("core scan needs %d co-resident workgroups but the stream's %d CUs hold %d",
+                       grid, plain_cus, per_cu * std::min(plain_cus, cus));
+      return DABSN_ERR_UNSUPPORTED;
+    }
+    DABSN_HIP_CHECK(hipLaunchKernel(reinterpret_cast<const void*>(kernel), dim3(grid),
+                                    dim3(threads), kargs, 0, stream));
+    return DABSN_OK;
+  }
   if (!coop || per_cu * cus < grid) {
     dabsn::set_error(
         "core scan needs %d co-resident workgroups but the device holds %d (%d per CU x %d CUs,"
@@ -1248,7 +1267,6 @@ static int launch_coop(K kernel, int grid, int threads, const A& args, hipStream
         grid, per_cu * cus, per_cu, cus, coop);
     return DABSN_ERR_UNSUPPORTED;
   }
-  void* kargs[] = {const_cast<A*>(&args)};
   DABSN_HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), dim3(grid),
                                              dim3(threads), kargs, 0, stream));
   return DABSN_OK;
@@ -1319,16 +1337,18 @@ static int launch_slabs(K kernel, int threads, const Cfg& c, const A& args, hipS
   DABSN_HIP_CHECK(hipGetDevice(&dev));
   DABSN_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   DABSN_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0));
+  if (c.plain_cus > 0) cus = std::min(cus, c.plain_cus);
   const int per_launch = per_cu * cus / c.nct;  // batch groups one launch can hold
-  if (per_launch < 1 || c.nbg <= per_launch)
-    return launch_coop(kernel, c.nct * c.nbg, threads, args, stream);  // reports a misfit
+  if (per_launch < 1 || c.nbg <= per_launch)  // (reports a misfit)
+    return launch_coop(kernel, c.nct * c.nbg, threads, args, c.plain_cus, stream);
   for (int g0 = 0; g0 < c.nbg; g0 += per_launch) {
     const int ng = std::min(per_launch, c.nbg - g0);
     if (g0 > 0) {
       const int rc = dabsn_hip_zero(args.ws + kCtrOff, xchg_offset(ng) - kCtrOff, stream);
       if (rc != DABSN_OK) return rc;
     }
-    const int rc = launch_coop(kernel, c.nct * ng, threads, slab_of(args, g0, ng), stream);
+    const int rc =
+        launch_coop(kernel, c.nct * ng, threads, slab_of(args, g0, ng), c.plain_cus, stream);
     if (rc != DABSN_OK) return rc;
   }
   return DABSN_OK;
@@ -1445,6 +1465,8 @@ static int check_common(int dtype, int64_t B, int64_t T, int64_t H, const dabsn_
 
 static int check_fwd(const dabsn_core_fwd_call& f, Cfg& c) {
   c = pick(f.dtype, f.B, f.H);
+  DABSN_REQUIRE(f.coresident_cus >= 0, "core scan: coresident_cus must be >= 0");
+  c.plain_cus = f.coresident_cus;
   const int rc = check_common(f.dtype, f.B, f.T, f.H, f.params, c, f.workspace_bytes,
                               c.ksteps ? workspace_bytes(f.dtype, c, false, f.H) : 0);
   if (rc != DABSN_OK) return rc;
@@ -1480,6 +1502,8 @@ static int check_fwd(const dabsn_core_fwd_call& f, Cfg& c) {
 
 static int check_bwd(const dabsn_core_bwd_call& b, Cfg& c) {
   c = pick(b.dtype, b.B, b.H);
+  DABSN_REQUIRE(b.coresident_cus >= 0, "core scan backward: coresident_cus must be >= 0");
+  c.plain_cus = b.coresident_cus;
   const int rc = check_common(b.dtype, b.B, b.T, b.H, b.params, c, b.workspace_bytes,
                               c.ksteps ? workspace_bytes(b.dtype, c, true, b.H) : 0);
   if (rc != DABSN_OK) return rc;
@@ -1630,7 +1654,7 @@ int dabsn_hip_core_scan_fwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
                             size_t workspace_bytes_, hipStream_t stream) {
   const dabsn_core_fwd_call f{dtype, B, T, H, 0, 0, Wx, Wgx, GA, params, b0, e0, c0, U, nov,
                               plast, expr, write, energy, sat, gate, bF, eF, cF, workspace,
-                              workspace_bytes_, kF32};
+                              workspace_bytes_, kF32, 0};
   return dabsn_hip_core_scan_fwd_call(&f, stream);
 }
 
@@ -1655,7 +1679,7 @@ int dabsn_hip_core_scan_bwd(int dtype, int64_t B, int64_t T, int64_t H, const vo
   const dabsn_core_bwd_call b{dtype, B, T, H, 0, GAT, params, b0, c0, U, plast, expr, energy,
                               sat, gate, gU, gNov, gP, gAy, gW, gE, gC, gbF, geF, gcF, gWx, gWgx,
                               day, part_vec, part_scal, gb0, ge0, gc0, workspace,
-                              workspace_bytes_};
+                              workspace_bytes_, 0};
   return dabsn_hip_core_scan_bwd_call(&b, stream);
 }
 

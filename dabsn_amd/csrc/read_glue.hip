@@ -25,14 +25,18 @@ struct Ptr8 {
 // one wave on a (b, t) row.
 
 // One wave per (b, t) row.
+// Rows (b, t), t < T, of tapes whose batch rows are ldt time steps apart (a time window of
+// longer sequences); statistics rows lds apart per batch row.
 template <typename E, int V>
-__global__ void __launch_bounds__(256) stats_kernel(int64_t rows, int H, const E* nov, const E* pl,
-                                                    const E* en, const E* sat, const E* ay,
-                                                    const E* wr, float* stats) {
+__global__ void __launch_bounds__(256) stats_kernel(int64_t rows, int T, int64_t ldt, int64_t lds,
+                                                    int H, const E* nov, const E* pl, const E* en,
+                                                    const E* sat, const E* ay, const E* wr,
+                                                    float* stats) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
-  const size_t base = static_cast<size_t>(row) * H;
+  const int64_t b = row / T, t = row % T;
+  const size_t base = static_cast<size_t>(b * ldt + t) * H;
   float se = 0.f, sc = 0.f, sn = 0.f, sp = 0.f, sa = 0.f, sw = 0.f;
   for (int h = lane * V; h < H; h += 64 * V) {
     const size_t o = base + h;
@@ -61,7 +65,7 @@ __global__ void __launch_bounds__(256) stats_kernel(int64_t rows, int H, const E
   sw = wave_sum(sw);
   if (lane == 0) {
     const float inv = 1.0f / static_cast<float>(H);
-    float* o = stats + static_cast<size_t>(row) * 6;
+    float* o = stats + static_cast<size_t>(b * lds + t) * 6;
     o[0] = se * inv;
     o[1] = sc * inv;
     o[2] = sn * inv;
@@ -75,15 +79,17 @@ __global__ void __launch_bounds__(256) stats_kernel(int64_t rows, int H, const E
 // Mean gradients broadcast over H: g = gstats / H, written (accumulate = 0) or added to
 // what the buffers hold (accumulate = 1).
 template <typename E, int V>
-__global__ void __launch_bounds__(256) stats_bwd_kernel(uint32_t chunks, uint32_t cpr, int H,
+__global__ void __launch_bounds__(256) stats_bwd_kernel(uint32_t chunks, uint32_t cpr, int H, int T,
+                                                        int64_t ldt, int64_t lds,
                                                         const float* gstats, int accumulate,
                                                         E* gen, E* gsat, E* gnov, E* gpl) {
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   if (i >= chunks) return;
   const uint32_t row = i / cpr;
-  const size_t o = static_cast<size_t>(i) * V;
+  const int64_t b = row / T, t = row % T;
+  const size_t o = static_cast<size_t>(b * ldt + t) * H + static_cast<size_t>(i % cpr) * V;
   const float inv = 1.0f / static_cast<float>(H);
-  const float* g = gstats + static_cast<size_t>(row) * 6;
+  const float* g = gstats + static_cast<size_t>(b * lds + t) * 6;
   E* dst[4] = {gen, gsat, gnov, gpl};
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -245,20 +251,22 @@ __global__ void __launch_bounds__(256) gather_kernel(int T, int N, int H, int hb
 // One workgroup per (b, t) position of the write tape; writes gw[t] (zero where no slot
 // maps to t). gVn may be null (no successor-row gradients).
 template <typename E, int V>
-__global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int N, int H, const float* norm_w,
+__global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int ldg, int N, int H,
+                                                         const float* norm_w,
                                                          const int32_t* rank, const E* K,
                                                          const E* gK, const E* gV, const E* gVn,
-                                                         E* gw) {
+                                                         int accumulate, E* gw) {
   __shared__ float part[4];
   const int64_t bt = blockIdx.x;
   const int64_t b = bt / T;
   const int t = static_cast<int>(bt % T);
+  const int64_t pos = b * ldg + t;  // row of norm_w and gw (rows ldg positions apart)
   const int32_t* rk = rank + static_cast<size_t>(b) * T;
   const int r0 = rk[t];
   const int r1 = gVn && t >= 1 ? rk[t - 1] : N;
   const int r2 = gVn && t == T - 1 ? rk[T - 1] : N;
   const bool in0 = r0 < N, in1 = r1 < N, in2 = r2 < N;
-  const float nrm = norm_w[bt];
+  const float nrm = norm_w[pos];
   const float n = fmaxf(nrm, kEps);
   float dot = 0.0f;
   if (in0 && nrm > kEps) {
@@ -277,10 +285,14 @@ __global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int N, int H, co
     dot = part[0] + part[1] + part[2] + part[3];
   }
   for (int h = threadIdx.x * V; h < H; h += 256 * V) {
-    const size_t o = static_cast<size_t>(bt) * H + h;
+    const size_t o = static_cast<size_t>(pos) * H + h;
     float acc[V];
+    if (accumulate) {
+      ldv<E, V>(gw + o, acc);
+    } else {
 #pragma unroll
-    for (int e = 0; e < V; ++e) acc[e] = 0.0f;
+      for (int e = 0; e < V; ++e) acc[e] = 0.0f;
+    }
     if (in0) {
       const size_t kb = (static_cast<size_t>(b) * N + r0) * H + h;
       float gk[V], gv[V], k[V];
@@ -513,29 +525,40 @@ __global__ void __launch_bounds__(256) admit_step_kernel(int64_t n, int64_t base
 
 extern "C" {
 
-int dabsn_hip_tape_stats(int dtype, int64_t B, int64_t T, int64_t H, const void* nov,
-                         const void* plast, const void* energy, const void* sat, const void* expr,
-                         const void* write, float* stats, hipStream_t stream) {
-  DABSN_REQUIRE(B > 0 && T >= 0 && H > 0 && H < (1 << 30), "tape_stats: bad shape");
+int dabsn_hip_tape_stats_window(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldt,
+                                const void* nov, const void* plast, const void* energy,
+                                const void* sat, const void* expr, const void* write,
+                                float* stats, int64_t lds, hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && T >= 0 && H > 0 && H < (1 << 30) && T < (1ll << 31), "tape_stats: bad shape");
+  DABSN_REQUIRE(ldt >= T && lds >= T, "tape_stats: row strides ldt=%lld, lds=%lld below T=%lld",
+                (long long)ldt, (long long)lds, (long long)T);
   const int64_t rows = B * T;
   if (rows == 0) return DABSN_OK;
   DABSN_REQUIRE(nov && plast && energy && sat && expr && write && stats, "tape_stats: null pointer");
   const dim3 grid(blocks_for(rows, 4)), block(256);
   const bool vec = vec_ok(H, {nov, plast, energy, sat, expr, write});
 #define L(E, V)                                                                                  \
-  hipLaunchKernelGGL((stats_kernel<E, V>), grid, block, 0, stream, rows, (int)H, (const E*)nov, \
-                     (const E*)plast, (const E*)energy, (const E*)sat, (const E*)expr,          \
-                     (const E*)write, stats)
+  hipLaunchKernelGGL((stats_kernel<E, V>), grid, block, 0, stream, rows, (int)T, ldt, lds, (int)H, \
+                     (const E*)nov, (const E*)plast, (const E*)energy, (const E*)sat,           \
+                     (const E*)expr, (const E*)write, stats)
   GLUE_DISPATCH("tape_stats", dtype, vec, L);
 #undef L
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
 
-int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const float* gstats,
-                             int accumulate, void* gnov, void* gplast, void* genergy, void* gsat,
-                             hipStream_t stream) {
-  DABSN_REQUIRE(B > 0 && T >= 0 && H > 0, "tape_stats backward: bad shape");
+int dabsn_hip_tape_stats(int dtype, int64_t B, int64_t T, int64_t H, const void* nov,
+                         const void* plast, const void* energy, const void* sat, const void* expr,
+                         const void* write, float* stats, hipStream_t stream) {
+  return dabsn_hip_tape_stats_window(dtype, B, T, H, T, nov, plast, energy, sat, expr, write,
+                                     stats, T, stream);
+}
+
+int dabsn_hip_tape_stats_bwd_window(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldt,
+                                    const float* gstats, int64_t lds, int accumulate, void* gnov,
+                                    void* gplast, void* genergy, void* gsat, hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && T >= 0 && H > 0 && T < (1ll << 31), "tape_stats backward: bad shape");
+  DABSN_REQUIRE(ldt >= T && lds >= T, "tape_stats backward: row strides below T");
   const int64_t rows = B * T;
   if (rows == 0) return DABSN_OK;
   DABSN_REQUIRE(gstats, "tape_stats backward: null gstats");
@@ -546,12 +569,19 @@ int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const f
   const dim3 grid(blocks_for(chunks, 256)), block(256);
 #define L(E, VV)                                                                                \
   hipLaunchKernelGGL((stats_bwd_kernel<E, VV>), grid, block, 0, stream, (uint32_t)chunks,      \
-                     (uint32_t)(H / VV), (int)H, gstats, accumulate ? 1 : 0, (E*)genergy,      \
-                     (E*)gsat, (E*)gnov, (E*)gplast)
+                     (uint32_t)(H / VV), (int)H, (int)T, ldt, lds, gstats, accumulate ? 1 : 0, \
+                     (E*)genergy, (E*)gsat, (E*)gnov, (E*)gplast)
   GLUE_DISPATCH("tape_stats backward", dtype, vec, L);
 #undef L
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
+}
+
+int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const float* gstats,
+                             int accumulate, void* gnov, void* gplast, void* genergy, void* gsat,
+                             hipStream_t stream) {
+  return dabsn_hip_tape_stats_bwd_window(dtype, B, T, H, T, gstats, T, accumulate, gnov, gplast,
+                                         genergy, gsat, stream);
 }
 
 int dabsn_hip_normalize_rows(int dtype, int64_t rows, int64_t H, const void* x, const float* norms,
@@ -646,13 +676,26 @@ int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_
   // Every position is written (zero where no slot maps to it), N == 0 included.
   DABSN_REQUIRE(gw && norm_w && rank && (N == 0 || (K && gK && gV)),
                 "bank_gather backward: null pointer");
-  DABSN_REQUIRE(B * T <= 2147483647ll, "bank_gather backward: too many positions");
+  return dabsn_hip_bank_gather_bwd_prefix(dtype, B, T, T, N, H, norm_w, rank, K, gK, gV, gVn, 0,
+                                          gw, stream);
+}
+
+int dabsn_hip_bank_gather_bwd_prefix(int dtype, int64_t B, int64_t T, int64_t ldg, int64_t N,
+                                     int64_t H, const float* norm_w, const int32_t* rank,
+                                     const void* K, const void* gK, const void* gV,
+                                     const void* gVn, int accumulate, void* gw,
+                                     hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && T > 0 && ldg >= T && N >= 0 && H > 0, "bank_gather backward: bad shape");
+  DABSN_REQUIRE(gw && norm_w && rank && (N == 0 || (K && gK && gV)),
+                "bank_gather backward: null pointer");
+  DABSN_REQUIRE(B * T <= 2147483647ll && B * ldg < (1ll << 40),
+                "bank_gather backward: too many positions");
   const dim3 grid((unsigned)(B * T)), block(256);
   const bool vec = vec_ok(H, {K, gK, gV, gVn, gw});
 #define L(E, VV)                                                                                \
-  hipLaunchKernelGGL((gather_bwd_kernel<E, VV>), grid, block, 0, stream, (int)T, (int)N,       \
-                     (int)H, norm_w, rank, (const E*)K, (const E*)gK, (const E*)gV,             \
-                     (const E*)gVn, (E*)gw)
+  hipLaunchKernelGGL((gather_bwd_kernel<E, VV>), grid, block, 0, stream, (int)T, (int)ldg,     \
+                     (int)N, (int)H, norm_w, rank, (const E*)K, (const E*)gK, (const E*)gV,     \
+                     (const E*)gVn, accumulate ? 1 : 0, (E*)gw)
   GLUE_DISPATCH("bank_gather backward", dtype, vec, L);
 #undef L
   DABSN_HIP_CHECK(hipGetLastError());

@@ -54,7 +54,8 @@ class _Fwd:
     """C call descriptor, workspace and final state of the forward scan of steps [t0, t1)."""
 
     def __init__(self, code: int, Wx: Tensor, Wgx: Tensor, GA: Tensor, params, b0: Tensor,
-                 e0: Tensor, c0: Tensor, out: _Tapes, t0: int, t1: int, ldx: int) -> None:
+                 e0: Tensor, c0: Tensor, out: _Tapes, t0: int, t1: int, ldx: int,
+                 coresident_cus: int = 0) -> None:
         lib = _lib.load()
         B, T, H = Wx.shape
         self.keep = (Wx, Wgx, GA, b0, e0, c0, out)
@@ -68,6 +69,7 @@ class _Fwd:
             ctypes.pointer(params), _ptr(b0), _ptr(e0), _ptr(c0), _ptr(out.U, 2 * o),
             *[_ptr(t, o) for t in out.tapes], *[_ptr(f) for f in self.finals], _ptr(self.ws),
             nbytes)
+        self.call.coresident_cus = int(coresident_cus)
 
     def launch(self, stream) -> None:
         _lib.check(_lib.load().dabsn_hip_core_scan_fwd_call(ctypes.byref(self.call), stream),
@@ -81,7 +83,7 @@ class _Bwd:
 
     def __init__(self, code: int, GAT: Tensor, params, b0: Tensor, c0: Tensor, src: _Tapes,
                  grads: Sequence[Optional[Tensor]], gfin: Sequence[Optional[Tensor]],
-                 outs: Sequence[Tensor], t0: int, t1: int) -> None:
+                 outs: Sequence[Tensor], t0: int, t1: int, coresident_cus: int = 0) -> None:
         lib = _lib.load()
         B, T, H = outs[0].shape
         self.keep = (GAT, b0, c0, src, *[g for g in grads if g is not None],
@@ -104,6 +106,7 @@ class _Bwd:
             _ptr(grads[0], 2 * o), *[_ptr(g, o) for g in grads[1:]],
             *[_ptr(g) for g in gfin], *[_ptr(x, o) for x in outs], _ptr(self.part_vec),
             _ptr(self.part_scal), *[_ptr(g) for g in self.g0], _ptr(self.ws), nbytes)
+        self.call.coresident_cus = int(coresident_cus)
 
     def launch(self, stream) -> None:
         _lib.check(_lib.load().dabsn_hip_core_scan_bwd_call(ctypes.byref(self.call), stream),

@@ -1,0 +1,386 @@
+"""Scan + read of one seq block, pipelined over time chunks on the two halves of the device.
+
+Reference behaviour: the block's time-chunked scan (src/dabsn/model.py:274-307) followed by
+its read over the whole sequence (read.py:139-438), and the read of a query chunk against
+the bank that ends with it (read.py:650-838), which gives the same rows as the whole-sequence
+read. The core scan is a persistent kernel that needs half of MI355X's CUs (128 workgroups
+at B = 16, H = 2048) and is bound by its per-step exchange, so the other half is idle while
+it runs. Here the scan runs on one CU-masked stream (16 CUs of every XCD, plain launches with
+``coresident_cus``) and the read on the other:
+
+* forward: the scan of chunk k + 1 runs while the read of query chunk k (its statistics,
+  selection, bank gather, three-way read and output projection against the bank of
+  positions [0, end of chunk k)) runs beside it; the last chunk's read, the long channel
+  (one scan over the whole sequence) and the read output follow on the whole device;
+* backward: the read output and the long channel first, then per chunk, last chunk first,
+  the read backward of query chunk k completes the tape gradients of window k (its query
+  rows, and the bank rows of window k, which only query chunks >= k read), the reverse scan
+  of chunk k starts on the scan's half, and the read backward of chunk k - 1 runs beside it.
+
+Each query chunk's read is its own small autograd graph built under ``enable_grad`` inside
+this function's forward, on detached leaves (the chunk's y, budget and expression windows,
+the statistics rows, the write tape and the read's parameters); the backward walks those
+graphs in reverse chunk order on the streams their forwards ran on. The bank-write gradient
+of a chunk (its bank gather's backward) is added in place into a full-length buffer over
+the bank's positions only, so no stream writes a window that the reverse scan is reading.
+Outputs equal the unpipelined block's up to summation order (the read of a query chunk is
+the whole-sequence read's rows; the tape gradients sum their chunk contributions).
+"""
+
+from __future__ import annotations
+
+import contextlib
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import torch
+from torch import Tensor
+
+from .. import _lib, events
+from . import chunked, ops
+
+_PAIRS: dict[int, tuple] = {}
+
+
+def stream_pair(device: torch.device):
+    """(scan stream, read stream, CUs of the scan stream, whole-device stream) for
+    ``device``: two CU-masked streams on complementary halves of the device
+    (``dabsn_hip_stream_pair``) and a non-blocking stream for the pipeline's whole-device
+    work, created once per device and kept for the process.
+
+    HIP creates CU-masked streams as blocking streams: work on the legacy default stream
+    waits for all of their earlier work and they wait for it. The pipeline therefore keeps
+    its own work off the default stream (on the third stream) between its entry and exit
+    synchronisations, or the scan half would hold the read half back."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    pair = _PAIRS.get(idx)
+    if pair is None:
+        lib = _lib.load()
+        a, b = ctypes.c_void_p(), ctypes.c_void_p()
+        ca, cb = _lib.i32(), _lib.i32()
+        with torch.cuda.device(idx):
+            _lib.check(lib.dabsn_hip_stream_pair(ctypes.byref(a), ctypes.byref(b), ctypes.byref(ca),
+                                                 ctypes.byref(cb)), "stream pair")
+        dev = torch.device("cuda", idx)
+        pair = (torch.cuda.ExternalStream(a.value, device=dev),
+                torch.cuda.ExternalStream(b.value, device=dev), int(ca.value),
+                torch.cuda.Stream(device=dev))
+        _PAIRS[idx] = pair
+    return pair
+
+
+@contextlib.contextmanager
+def _parameters_as(module: torch.nn.Module, leaves: dict[str, Tensor]):
+    """Run ``module`` with its parameters replaced by ``leaves`` (same names)."""
+    saved = []
+    try:
+        for name, leaf in leaves.items():
+            path, _, attr = name.rpartition(".")
+            mod = module.get_submodule(path) if path else module
+            saved.append((mod, attr, mod._parameters[attr]))
+            mod._parameters[attr] = leaf
+        yield
+    finally:
+        for mod, attr, p in reversed(saved):
+            mod._parameters[attr] = p
+
+
+class _SinkGather(torch.autograd.Function):
+    """Bank gather over a prefix of a full-length write tape whose backward adds the bank
+    rows' gradient into ``sink`` (the write tape's gradient buffer) over the bank's positions
+    only, instead of returning a full-length gradient. Returns (K, V, Vn or None)."""
+
+    @staticmethod
+    def forward(ctx, sink: Tensor, write: Tensor, norm_w: Tensor, idx: Tensor,
+                next_idx: Optional[Tensor], rank: Tensor):
+        lib = _lib.load()
+        B, T, H = write.shape
+        N = idx.shape[1]
+        nw = norm_w.float().contiguous()
+        ic = idx.to(torch.int64).contiguous()
+        nc = None if next_idx is None else next_idx.to(torch.int64).contiguous()
+        K, V = (torch.empty((B, N, H), device=write.device, dtype=write.dtype) for _ in range(2))
+        Vn = None if nc is None else torch.empty_like(K)
+        _lib.check(lib.dabsn_hip_bank_gather(ops._code(write.dtype), B, T, N, H, ops._p(write),
+                                             ops._p(nw), ops._p(ic), ops._p(nc), ops._p(K),
+                                             ops._p(V), ops._p(Vn), ops._stream(write)),
+                   "bank gather")
+        ctx.save_for_backward(nw, rank, K)
+        ctx.sink = sink
+        ctx.shape = (B, T, H)
+        ctx.set_materialize_grads(False)
+        return K, V, Vn
+
+    @staticmethod
+    def backward(ctx, gK, gV, gVn):
+        nw, rank, K = ctx.saved_tensors
+        B, T, H = ctx.shape
+        N = K.shape[1]
+        dt = K.dtype
+        z = lambda g: torch.zeros_like(K) if g is None else g.to(dt).contiguous()  # noqa: E731
+        gKc, gVc = z(gK), z(gV)
+        gVnc = None if gVn is None else gVn.to(dt).contiguous()
+        rk = rank.to(torch.int32).contiguous()
+        lib = _lib.load()
+        _lib.check(lib.dabsn_hip_bank_gather_bwd_prefix(
+            ops._code(dt), B, int(rk.shape[1]), T, N, H, ops._p(nw), ops._p(rk), ops._p(K),
+            ops._p(gKc), ops._p(gVc), ops._p(gVnc), 1, ops._p(ctx.sink), ops._stream(K)),
+            "bank gather backward")
+        return None, None, None, None, None, None
+
+
+def _stats_window(tapes: chunked._Tapes, stats: Tensor, t0: int, t1: int, stream) -> None:
+    """stats[:, t0:t1] = read_tape_stats of the tapes' window [t0, t1), in place."""
+    lib = _lib.load()
+    B, T, H = tapes.tapes[0].shape
+    o = t0 * H
+    nov, pl, ay, w, en, sat = (tapes.tapes[i] for i in (0, 1, 2, 3, 4, 5))
+    ptr = lambda t: t.data_ptr() + o * t.element_size()  # noqa: E731
+    _lib.check(lib.dabsn_hip_tape_stats_window(
+        ops._code(nov.dtype), B, t1 - t0, H, T, ptr(nov), ptr(pl), ptr(en), ptr(sat), ptr(ay),
+        ptr(w), stats.data_ptr() + t0 * 6 * 4, T, stream), "tape statistics")
+
+
+def _stats_bwd_window(gstats: Tensor, outs: Sequence[Optional[Tensor]], accumulate: bool,
+                      t0: int, t1: int, stream) -> None:
+    """Mean gradients of window [t0, t1) broadcast into the full-length gradients
+    outs = (g_novelty, g_plasticity, g_energy, g_saturation) (None to skip)."""
+    lib = _lib.load()
+    like = next(x for x in outs if x is not None)
+    B, T, H = like.shape
+    o = t0 * H
+    ptr = lambda t: None if t is None else t.data_ptr() + o * t.element_size()  # noqa: E731
+    gs = gstats.data_ptr() + t0 * 6 * 4
+    _lib.check(lib.dabsn_hip_tape_stats_bwd_window(
+        ops._code(like.dtype), B, t1 - t0, H, T, gs, T, 1 if accumulate else 0, *map(ptr, outs),
+        stream), "tape statistics backward")
+
+
+class _PipelinedScanRead(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, read, chunk: int, names: tuple, Wx: Tensor, Wgx: Tensor, *rest: Tensor):
+        core_in, read_params = rest[:21], rest[21:]
+        Ug, A = core_in[:2]
+        vecs, scal = core_in[2:18], core_in[18:21]
+        ops._require_cuda(Wx)
+        B, T, H = Wx.shape
+        dt = Wx.dtype
+        code = ops._code(dt)
+        dev = Wx.device
+        S, R, cus, M = stream_pair(dev)
+        ambient = torch.cuda.current_stream(dev)
+        events.announce("core_scan_chunked", "rocm_pipelined_scan_read", B=B, H=H,
+                        chunk=int(chunk), dtype="bf16" if code == 1 else "fp32")
+        ops.core_launch_check(code, B, min(T, chunk), H, False)
+        # Buffers that outlive the call come from the caller's stream, before any work.
+        GA = torch.cat((Ug, A), dim=0).to(dt).contiguous()
+        params, keep = ops._core_params(vecs, scal)
+        Wx_c, Wgx_c, ldx = ops.scan_inputs(Wx, Wgx, dt)
+        out = chunked._Tapes(Wx_c, B, T, H)
+        stats = torch.empty((B, T, 6), device=dev, dtype=torch.float32)
+        short = torch.empty((B, T, H), device=dev, dtype=dt)
+        sink = torch.zeros((B, T, H), device=dev, dtype=dt)  # bank-write gradient (backward)
+        bounds = chunked._chunks(T, chunk)
+        K = len(bounds)
+        for st in (M, S, R):
+            st.wait_stream(ambient)
+
+        with torch.cuda.stream(M):
+            # Scan of every chunk on the scan half; an event after each.
+            scan_done, starts, fwd_calls = [], [], []
+            with torch.cuda.stream(S):
+                zeros = torch.zeros(B, H, device=dev, dtype=torch.float32)
+                carry = [zeros, torch.ones_like(zeros), zeros.clone()]
+                for t0, t1 in bounds:
+                    starts.append(torch.stack(carry))
+                    f = chunked._Fwd(code, Wx_c, Wgx_c, GA, params, *carry, out, t0, t1, ldx, cus)
+                    tk = ops.KernelTimer.begin("core_scan_fwd", Wx)
+                    f.launch(S)
+                    ops.KernelTimer.end(tk)
+                    ops._record_error_word(f.ws, "core scan forward")
+                    e = torch.cuda.Event()
+                    e.record(S)
+                    scan_done.append(e)
+                    fwd_calls.append(f)
+                    carry = f.finals
+                starts = torch.stack(starts)
+
+            # Leaves of the per-chunk read graphs.
+            U = out.U
+            ay, w, pl = out.tapes[2], out.tapes[3], out.tapes[1]
+            w_leaf = w.detach().requires_grad_(True)
+            p_leaf = pl.detach().requires_grad_(True)
+            stats_leaf = stats.detach().requires_grad_(True)
+            short_leaf = short.detach().requires_grad_(True)
+            param_leaves = {n: p.detach().requires_grad_(p.requires_grad)
+                            for n, p in zip(names, read_params)}
+            norms = stats_leaf[..., 5].detach()
+
+            def gather(bank_write, norm_w, idx, next_idx, rank, fold):
+                return _SinkGather.apply(sink, bank_write, norm_w, idx,
+                                         None if fold is not None else next_idx, rank)
+
+            chunks = []
+            with _parameters_as(read, param_leaves):
+                for k, (t0, t1) in enumerate(bounds):
+                    last = k == K - 1
+                    st = M if last else R
+                    with torch.cuda.stream(st):
+                        st.wait_event(scan_done[k])
+                        if last and K > 1:
+                            M.wait_stream(R)
+                        _stats_window(out, stats, t0, t1, st.cuda_stream)
+                        with torch.enable_grad():
+                            win = [U[:, t0:t1, :H], U[:, t0:t1, H:], ay[:, t0:t1]]
+                            leaves = [x.detach().requires_grad_(True) for x in win]
+                            sh = read.query_bank_short(
+                                *leaves, query_stats=stats_leaf[:, t0:t1], bank_write=w_leaf,
+                                bank_norms=norms, bank_stats=stats_leaf[:, :t1], query_start=t0,
+                                gather=gather)
+                        short[:, t0:t1].copy_(sh.detach())
+                        chunks.append((sh, leaves))
+                # The long channel over the whole sequence and the read output, whole device.
+                with torch.enable_grad():
+                    long = read._long_scan(w_leaf, p_leaf, None)
+                    read_out = ops.direct.read_output(short_leaf, long, read.long_gain)
+            M.wait_stream(S)
+        ambient.wait_stream(M)
+        read_out.record_stream(ambient)
+        del keep
+
+        ctx.read, ctx.chunk, ctx.names = read, chunk, names
+        ctx.bounds = bounds
+        ctx.meta = [(x.dtype, tuple(x.shape)) for x in (Wx, Wgx, *core_in)]
+        ctx.graph = (chunks, read_out, w_leaf, p_leaf, stats_leaf, short_leaf, param_leaves, sink)
+        ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, starts, out.U, *out.tapes)
+        ctx.set_materialize_grads(False)
+        return U, read_out.detach()
+
+    @staticmethod
+    def backward(ctx, gU_out, g_read):
+        saved = ctx.saved_tensors
+        Wx, Wgx, Ug, A = saved[:4]
+        vecs, scal = saved[4:20], saved[20:23]
+        starts = saved[23]
+        fwd_out = chunked._Tapes(None, 0, 0, 0, existing=saved[24:32])
+        chunks, read_out, w_leaf, p_leaf, stats_leaf, short_leaf, param_leaves, sink = ctx.graph
+        B, T, H = Wx.shape
+        dt = Wx.dtype
+        code = ops._code(dt)
+        dev = Wx.device
+        S, R, cus, M = stream_pair(dev)
+        ambient = torch.cuda.current_stream(dev)
+        bounds = ctx.bounds
+        K = len(bounds)
+        ops.core_launch_check(code, B, min(T, ctx.chunk), H, True)
+        GA = torch.cat((Ug, A), dim=0).to(dt).contiguous()
+        GAT = GA.t().contiguous()
+        params, keep = ops._core_params(vecs, scal)
+        pleaves = list(param_leaves.values())
+        trainable = [p for p in pleaves if p.requires_grad]
+        # Tape gradients of the reverse scans, full length, filled window by window.
+        gU = (torch.zeros((B, T, 2 * H), device=dev, dtype=dt) if gU_out is None
+              else gU_out.to(dt).contiguous().clone())
+        g_nov, g_ay, g_e, g_c = (torch.empty((B, T, H), device=dev, dtype=dt) for _ in range(4))
+        gWx, gWgx, day = (torch.empty((B, T, H), device=dev, dtype=dt) for _ in range(3))
+        g_read = torch.zeros_like(read_out) if g_read is None else g_read.contiguous()
+        for st in (M, S, R):
+            st.wait_stream(ambient)
+
+        with torch.cuda.stream(M):
+            # Read output and long channel (whole device).
+            torch.autograd.backward([read_out], [g_read],
+                                    inputs=[short_leaf, w_leaf, p_leaf, *trainable])
+            g_short = short_leaf.grad
+            if w_leaf.grad is not None:
+                sink.add_(w_leaf.grad)  # the long channel's write gradient
+            g_p = p_leaf.grad if p_leaf.grad is not None else torch.zeros_like(p_leaf)
+            S.wait_stream(M)
+            R.wait_stream(M)
+
+            carry = [None, None, None]
+            bws = []
+            for k in range(K - 1, -1, -1):
+                t0, t1 = bounds[k]
+                sh, leaves = chunks[k]
+                st = M if k == K - 1 else R
+                with torch.cuda.stream(st):
+                    # w_leaf is listed so that the engine runs the gather's backward, whose
+                    # gradient goes to the sink (it returns none for w_leaf itself).
+                    torch.autograd.backward([sh], [g_short[:, t0:t1]],
+                                            inputs=[*leaves, w_leaf, stats_leaf, *trainable])
+                    gy, gb, gay = (x.grad for x in leaves)
+                    if gy is not None:
+                        gU[:, t0:t1, :H] += gy
+                    if gb is not None:
+                        gU[:, t0:t1, H:] += gb
+                    if gay is not None:
+                        g_ay[:, t0:t1].copy_(gay)
+                    else:
+                        g_ay[:, t0:t1].zero_()
+                    gs = stats_leaf.grad
+                    gs = torch.zeros_like(stats_leaf) if gs is None else gs.contiguous()
+                    _stats_bwd_window(gs, (g_nov, None, g_e, g_c), False, t0, t1, st.cuda_stream)
+                    _stats_bwd_window(gs, (None, g_p, None, None), True, t0, t1, st.cuda_stream)
+                    tapes_ready = torch.cuda.Event()
+                    tapes_ready.record(st)
+                if st is not R:
+                    # The next chunks' read backward (on R) adds into the same gradient
+                    # buffers (sink, statistics, parameters) as this one.
+                    R.wait_event(tapes_ready)
+                with torch.cuda.stream(S):
+                    S.wait_event(tapes_ready)
+                    up = [gU, g_nov, g_p, g_ay, sink, g_e, g_c]
+                    bw = chunked._Bwd(code, GAT, params, starts[k, 0].contiguous(),
+                                      starts[k, 2].contiguous(), fwd_out, up, carry,
+                                      (gWx, gWgx, day), t0, t1, cus)
+                    tk = ops.KernelTimer.begin("core_scan_bwd", Wx)
+                    bw.launch(S)
+                    ops.KernelTimer.end(tk)
+                    ops._record_error_word(bw.ws, "core scan backward")
+                    bws.append(bw)
+                    carry = bw.g0
+            M.wait_stream(S)
+            M.wait_stream(R)
+            gvec = torch.stack([bw.part_vec.sum(0) for bw in bws]).sum(0)
+            gscal = torch.stack([bw.part_scal.sum(0) for bw in bws]).sum(0)
+            y = fwd_out.U.reshape(B * T, 2 * H)[:, :H]
+            gUg = (gWgx.view(B * T, H).t() @ y).float()
+            gA = (day.view(B * T, H).t() @ y).float()
+            core = [gWx, gWgx, gUg, gA, *[gvec[i] for i in range(16)],
+                    *[gscal[i] for i in range(3)]]
+            core = [g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(core, ctx.meta)]
+            grads = [p.grad for p in pleaves]
+        ambient.wait_stream(M)
+        for g in (*core, *grads):
+            if g is not None:
+                g.record_stream(ambient)
+        del keep
+        ctx.graph = None
+        return (None, None, None, *core, *grads)
+
+
+def pipelined_scan_read(read, chunk: int, Wx: Tensor, Wgx: Tensor,
+                        core_params: Sequence[Tensor]) -> tuple[Tensor, Tensor]:
+    """(U [B, T, 2H], read output [B, T, H]) of a seq block's core scan over ``chunk``-step
+    windows from the zero state and its read, with the read of query chunk k overlapping
+    the scan of chunk k + 1 (forward) and the reverse scan of chunk k overlapping the read
+    backward of chunk k - 1 (backward). ``core_params``: the 21 parameter inputs of
+    dabsn::core_scan_batched (``DABSNCore.scan_inputs()``)."""
+    if read.read_geometry != "seq":
+        raise ValueError("the pipelined scan + read is the seq geometry's (causal banks)")
+    names = tuple(n for n, _ in read.named_parameters())
+    params = [p for _, p in read.named_parameters()]
+    return _PipelinedScanRead.apply(read, int(chunk), names, Wx, Wgx, *core_params, *params)
+
+
+def enabled() -> bool:
+    """``DABSN_PIPELINE=0`` runs the block's scan and read one after the other instead."""
+    return os.environ.get("DABSN_PIPELINE", "1") != "0"
+
+
+def pipeline_applies(read, Wx: Tensor, chunk: int) -> bool:
+    """The pipelined path serves training of a seq block on the device with 2+ chunks."""
+    return (Wx.is_cuda and torch.is_grad_enabled() and read.read_geometry == "seq"
+            and 0 < chunk < int(Wx.shape[1]))

@@ -22,7 +22,7 @@ from torch import Tensor
 from torch.utils.checkpoint import checkpoint
 
 from .core import DABSNCore
-from .kernels import ops
+from .kernels import ops, pipeline
 from .read import DABSNRead
 
 
@@ -118,9 +118,20 @@ class DABSNBlock(nn.Module):
         return self.core(inputs, return_writes=True, return_cocktail=True)
 
     def forward_world(self, inputs: Tensor) -> Tensor:
-        trajectory, novelty, plasticity, expression, write, energy, saturation = self.core_tapes(inputs)
-        y, budget = trajectory.split(self.state_dim, dim=-1)
-        read = self.read(y, budget, expression, write, novelty, plasticity, energy, saturation)
+        chunk_t = self._resolve_block_chunk_t(inputs)
+        if self.training and pipeline.enabled() and pipeline.pipeline_applies(self.read, inputs,
+                                                                              chunk_t):
+            # Training on the device with block chunking: the read of query chunk k runs
+            # beside the scan of chunk k + 1 on the other half of the device.
+            Wx, Wgx = self.core.projections(inputs)
+            trajectory, read = pipeline.pipelined_scan_read(self.read, chunk_t, Wx, Wgx,
+                                                            self.core.scan_inputs())
+            y = trajectory.split(self.state_dim, dim=-1)[0]
+        else:
+            trajectory, novelty, plasticity, expression, write, energy, saturation = (
+                self.core_tapes(inputs))
+            y, budget = trajectory.split(self.state_dim, dim=-1)
+            read = self.read(y, budget, expression, write, novelty, plasticity, energy, saturation)
         out = self.finish(inputs, self.state_to_hidden(y + self.read_gain * read))
         self.last_trace = {"read_geometry": self.read_geometry,
                            "admitted_n_max": self.read.last_n_max,

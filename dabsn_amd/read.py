@@ -249,7 +249,9 @@ class DABSNRead(nn.Module):
 
     def _read_core(self, query, cocktail, bank_write, norm_w, key_bias, admission, length: int,
                    query_start: int, width: int | None = None,
-                   members: tuple[Tensor, Tensor] | None = None):
+                   members: tuple[Tensor, Tensor] | None = None, gather=None):
+        """``gather`` (optional): called as gather(bank_write, norm_w, idx, next_idx, rank,
+        fold) -> (K, V, Vn or None) in place of the bank gather op on the training path."""
         bank = self._bank(cocktail[1], key_bias, admission, length, query_start, width, members)
         n_max, idx, valid, next_idx, rank = (bank[k] for k in ("n_max", "idx", "valid",
                                                                 "next_idx", "rank"))
@@ -294,7 +296,9 @@ class DABSNRead(nn.Module):
                 (self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain))
         else:
             fold = bank["fold"]
-            if fold is not None:
+            if gather is not None:
+                K, V, Vn = gather(bank_write, norm_w, idx, next_idx, rank, fold)
+            elif fold is not None:
                 # Every admitted slot's successor row is a bank row (Vn[j] = V[j + fold[j]]):
                 # the read folds the induction products into V and needs no successor rows.
                 K, V = ops.bank_gather_kv(bank_write, norm_w, idx, rank)
@@ -504,11 +508,8 @@ class DABSNRead(nn.Module):
                 # The reference's admission is a bf16 tensor here: its floor is bf16 too.
                 admission = admission.to(torch.bfloat16)
         else:
-            qe, qc, qn, qp = (m.to(tape_dtype) for m in query_stats.unbind(-1)[:4])
-            be, bc, bn, bp = (m.to(tape_dtype) for m in bank_stats.unbind(-1)[:4])
-            key_bias = rp.key_bias_from_means(bn, bp, hidden)
-            admission = rp.admission_from_means(be, bc, bn, bp, hidden)
-            cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
+            key_bias, admission, cocktails = self._glue_from_stats(query_stats, bank_stats,
+                                                                   tape_dtype, hidden)
         if retrieved is None:
             retrieved = self._read_core(query, cocktails, bank_write,
                                         bank_stats[..., 5].detach(), key_bias, admission,
@@ -525,6 +526,34 @@ class DABSNRead(nn.Module):
             return ops.read_mix(short_output, long, self.long_gain, y_mix, gain), final_state
         read = ops.direct.read_output(short_output, long, self.long_gain)
         return y_mix + gain * read, final_state
+
+
+    def _glue_from_stats(self, query_stats, bank_stats, tape_dtype, hidden: int):
+        """Key bias and admission of the bank rows and the (query, bank) cocktails from
+        statistics rows, with the means in the tape dtype (read.py:58-72, 161-183)."""
+        rp = self.short_read
+        qe, qc, qn, qp = (m.to(tape_dtype) for m in query_stats.unbind(-1)[:4])
+        be, bc, bn, bp = (m.to(tape_dtype) for m in bank_stats.unbind(-1)[:4])
+        key_bias = rp.key_bias_from_means(bn, bp, hidden)
+        admission = rp.admission_from_means(be, bc, bn, bp, hidden)
+        return key_bias, admission, (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
+
+    def query_bank_short(self, y, budget, expression, *, query_stats, bank_write, bank_norms,
+                         bank_stats, query_start: int, gather=None) -> Tensor:
+        """The short-memory output ``out(cat[y, budget, retrieved])`` of a seq query chunk
+        against the bank of positions [0, bank_stats.shape[1]) (forward_query_bank_stats
+        without the long channel, read.py:650-823). ``bank_write`` [B, >= bank length, H] may
+        be the whole write tape with the bank as its prefix; ``bank_norms`` are the write
+        norms of its rows ([B, bank_write.shape[1]]). ``gather`` replaces the bank gather
+        (see ``_read_core``)."""
+        self._require_seq()
+        hidden = int(expression.shape[-1])
+        query = ops.direct.normalize_rows(expression, query_stats[..., 4].detach())
+        key_bias, admission, cocktails = self._glue_from_stats(query_stats, bank_stats,
+                                                               bank_write.dtype, hidden)
+        retrieved = self._read_core(query, cocktails, bank_write, bank_norms, key_bias, admission,
+                                    int(bank_stats.shape[1]), int(query_start), gather=gather)
+        return self.short_read.project(y, budget, retrieved.to(y.dtype))
 
 
 def collect_traces_enabled() -> bool:

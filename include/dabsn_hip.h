@@ -119,6 +119,12 @@ typedef struct dabsn_core_fwd_call {
                       carried in the activation dtype, as the reference's streaming memory
                       does, src/dabsn/memory.py:228-232; the final state rounded to nearest
                       even). The pointers keep their float* type either way. */
+  int coresident_cus; /* 0: cooperative launches (the runtime guarantees that every
+                         workgroup is resident; nothing else runs beside them). > 0: plain
+                         launches, for a stream restricted to that many CUs (e.g. one of
+                         dabsn_hip_stream_pair's) on which nothing else runs during the scan:
+                         the caller guarantees residency and work on the other CUs overlaps
+                         the scan. Barrier waits stay bounded either way. */
 } dabsn_core_fwd_call;
 
 typedef struct dabsn_core_bwd_call {
@@ -134,10 +140,18 @@ typedef struct dabsn_core_bwd_call {
   float *part_vec, *part_scal, *gb0, *ge0, *gc0;
   void* workspace;
   size_t workspace_bytes;
+  int coresident_cus; /* as in dabsn_core_fwd_call */
 } dabsn_core_bwd_call;
 
 int dabsn_hip_core_scan_fwd_call(const dabsn_core_fwd_call* fwd, hipStream_t stream);
 int dabsn_hip_core_scan_bwd_call(const dabsn_core_bwd_call* bwd, hipStream_t stream);
+
+/* Two streams on complementary halves of the device's CUs (hipExtStreamCreateWithCUMask;
+ * on MI355X each gets 16 CUs of every XCD), for overlapping the persistent core scan
+ * (plain launches with coresident_cus = *cus_a) with other work. No reference
+ * counterpart: the reference's scan is a sequence of per-step launches. *cus_a and *cus_b
+ * receive the CU counts of the two masks. Release with hipStreamDestroy. */
+int dabsn_hip_stream_pair(hipStream_t* a, hipStream_t* b, int* cus_a, int* cus_b);
 
 /* ---- linear recurrence -----------------------------------------------------------
  * Replaces dabsn::linear_recurrence / dabsn::_linrec_backward
@@ -188,6 +202,16 @@ int dabsn_hip_tape_stats(int dtype, int64_t B, int64_t T, int64_t H, const void*
 int dabsn_hip_tape_stats_bwd(int dtype, int64_t B, int64_t T, int64_t H, const float* gstats,
                              int accumulate, void* gnov, void* gplast, void* genergy, void* gsat,
                              hipStream_t stream);
+/* The two above on a time window [t0, t0 + T) of longer sequences, in place: the tape (and
+ * tape-gradient) pointers point at step t0 of batch row 0 with batch rows ldt steps apart,
+ * the statistics rows lds rows apart (no copies of the window). */
+int dabsn_hip_tape_stats_window(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldt,
+                                const void* nov, const void* plast, const void* energy,
+                                const void* sat, const void* expr, const void* write,
+                                float* stats, int64_t lds, hipStream_t stream);
+int dabsn_hip_tape_stats_bwd_window(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldt,
+                                    const float* gstats, int64_t lds, int accumulate, void* gnov,
+                                    void* gplast, void* genergy, void* gsat, hipStream_t stream);
 /* Read output (src/dabsn/read.py:435-438, 821-823): out = proj + gain * long over n
  * elements, as the reference's two tensor operations under type promotion: the product in
  * prod_dtype (the promotion of gain and long), the sum in out_dtype (the promotion of proj
@@ -276,6 +300,15 @@ int dabsn_hip_bank_gather_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_
                               const void* w, const float* norm_w, const int32_t* rank,
                               const void* K, const void* gK, const void* gV, const void* gVn,
                               void* gw, hipStream_t stream);
+/* The same over the first T positions of each row of a longer write tape (a bank that is the
+ * prefix of the sequence, as a time-chunked read builds it): norm_w and gw rows are ldg
+ * positions apart, rank is [B,T]; positions >= T are not touched. accumulate = 1 adds into
+ * gw instead of writing it. */
+int dabsn_hip_bank_gather_bwd_prefix(int dtype, int64_t B, int64_t T, int64_t ldg, int64_t N,
+                                     int64_t H, const float* norm_w, const int32_t* rank,
+                                     const void* K, const void* gK, const void* gV,
+                                     const void* gVn, int accumulate, void* gw,
+                                     hipStream_t stream);
 
 /* ---- block glue (inference) ---------------------------------------------------------
  * The element work around one block's read and its MLP branch, each as one kernel, for the

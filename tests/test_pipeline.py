@@ -1,0 +1,146 @@
+"""The pipelined scan + read (``dabsn_amd/kernels/pipeline.py``) against the same block run
+one piece after the other (time-chunked core scan, then the whole-sequence read).
+
+The pipeline reads each query chunk against the bank that ends with it (read.py:650-838,
+the same rows as the whole-sequence read) and sums the tape gradients chunk by chunk, so
+only summation orders differ:
+  * the trajectory U: bit-identical (the same scan kernels, launched plainly on a CU-masked
+    stream instead of cooperatively);
+  * fp32: read output and every gradient (input projections, core and read parameters)
+    normwise 1e-5 (scalar parameter gradients that sum O(B*T*N) terms 1e-4);
+  * bf16 at state width 2048 (the config-4 kernel instances): Frobenius 2e-2;
+  * dense banks (the successor fold) and partially admitted ones (no fold, a bank width
+    that grows chunk by chunk); a DABSNBlock with block chunking, pipelined or not.
+"""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+
+import dabsn_amd
+from dabsn_amd.kernels import pipeline
+from dabsn_amd.kernels.chunked import chunked_core_scan
+
+pytestmark = pytest.mark.gpu
+
+
+def _modules(seed, din, H, window, dev):
+    torch.manual_seed(seed)
+    core = dabsn_amd.DABSNCore(din, H).to(dev)
+    read = dabsn_amd.DABSNRead(H).to(dev)
+    read.admit_window.data.fill_(window)
+    return core, read
+
+
+def _sequential(core, read, chunk, Wx, Wgx):
+    B, T, H = Wx.shape
+    z = torch.zeros(B, H, device=Wx.device, dtype=torch.float32)
+    outs = chunked_core_scan(chunk, Wx, Wgx, *core.scan_inputs(), z, torch.ones_like(z), z.clone())
+    U, nov, p, ay, w, e, c = outs[:7]
+    y, budget = U.split(H, dim=-1)
+    return U, read(y, budget, ay, w, nov, p, e, c)
+
+
+def _run(fn, core, read, x, gU, gr, dtype):
+    core.zero_grad(set_to_none=True)
+    read.zero_grad(set_to_none=True)
+    xl = x.clone().requires_grad_(True)
+    with torch.autocast("cuda", dtype=dtype, enabled=dtype != torch.float32):
+        Wx, Wgx = core.projections(xl)
+        U, r = fn(core, read, Wx, Wgx)
+    torch.autograd.backward([U, r], [gU.to(U.dtype), gr.to(r.dtype)])
+    grads = {"x": xl.grad}
+    for prefix, m in (("core", core), ("read", read)):
+        for n, p in m.named_parameters():
+            if p.grad is not None:
+                grads[f"{prefix}.{n}"] = p.grad.detach().clone()
+    return U.detach(), r.detach(), grads, read.last_n_max
+
+
+def _rel(a, b, fro, floor=1e-30):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    if fro:
+        return float((a - b).norm() / max(float(b.norm()), floor * b.numel() ** 0.5))
+    return float((a - b).abs().max() / max(float(b.abs().max()), floor))
+
+
+def _floor(grads):
+    """Parameters such as null_bias and adm_bias shift every logit of a softmax equally: their
+    exact gradient is zero and both runs hold rounding noise, so gradient errors are taken
+    relative to max(|grad|, 1e-3 x the largest parameter gradient)."""
+    return 1e-3 * max(float(g.abs().max()) for g in grads.values())
+
+
+@pytest.mark.parametrize("dtype,B,T,H,chunk,window", [
+    (torch.float32, 3, 96, 64, 32, 50.0),
+    (torch.float32, 3, 96, 64, 32, 0.3),
+    (torch.float32, 2, 100, 48, 24, 50.0),
+    (torch.bfloat16, 16, 512, 2048, 128, 50.0),
+    (torch.bfloat16, 16, 384, 2048, 128, 0.3),
+])
+def test_pipelined_scan_read_matches_sequential(cuda_device, dtype, B, T, H, chunk, window):
+    din = 32
+    core, read = _modules(11 + T, din, H, window, cuda_device)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(B, T, din, generator=g).to(cuda_device)
+    gU = (torch.randn(B, T, 2 * H, generator=g) * 1e-2).to(cuda_device)
+    gr = torch.randn(B, T, H, generator=g).to(cuda_device)
+
+    def piped(c, r, Wx, Wgx):
+        return pipeline.pipelined_scan_read(r, chunk, Wx, Wgx, c.scan_inputs())
+
+    def seq(c, r, Wx, Wgx):
+        return _sequential(c, r, chunk, Wx, Wgx)
+
+    U1, r1, g1, n1 = _run(piped, core, read, x, gU, gr, dtype)
+    U0, r0, g0, n0 = _run(seq, core, read, x, gU, gr, dtype)
+    assert n1 == n0
+    assert torch.equal(U1, U0), "trajectory"
+    fro = dtype != torch.float32
+    tol = 2e-2 if fro else 1e-5
+    assert _rel(r1, r0, fro) <= tol, f"read output {_rel(r1, r0, fro):.3e}"
+    assert g1.keys() == g0.keys()
+    worst = ("", 0.0)
+    floor = _floor(g0)
+    for n in g0:
+        err = _rel(g1[n], g0[n], fro, floor)
+        limit = tol if (fro or g0[n].numel() > 1) else 1e-4
+        assert err <= limit, f"gradient {n}: {err:.3e}"
+        worst = max(worst, (n, err), key=lambda v: v[1])
+    print(f"pipelined vs sequential ({dtype}, B={B} T={T} H={H}, n_max={n1}): "
+          f"output {_rel(r1, r0, fro):.2e}, worst gradient {worst[0]} {worst[1]:.2e}")
+
+
+def test_block_pipelined_matches_sequential(cuda_device, monkeypatch):
+    """A seq DABSNBlock with block chunking in training mode takes the pipeline; with
+    DABSN_PIPELINE=0 it runs the chunked scan and then the read (fp32, 1e-5 / scalars 1e-4)."""
+    torch.manual_seed(3)
+    blk = dabsn_amd.DABSNBlock(24, 48, 40, "seq", residual=True, mlp_ratio=2.0,
+                               block_chunk_t=32).to(cuda_device)
+    blk.train()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 100, 24, generator=g).to(cuda_device)
+    w = torch.randn(2, 100, 48, generator=g).to(cuda_device)
+
+    def run(flag):
+        monkeypatch.setenv("DABSN_PIPELINE", flag)
+        blk.zero_grad(set_to_none=True)
+        xl = x.clone().requires_grad_(True)
+        out = blk(xl)
+        (out * w).sum().backward()
+        grads = {n: p.grad.detach().clone() for n, p in blk.named_parameters() if p.grad is not None}
+        return out.detach(), xl.grad, grads
+
+    o1, gx1, g1 = run("1")
+    o0, gx0, g0 = run("0")
+    assert _rel(o1, o0, False) <= 1e-5
+    assert _rel(gx1, gx0, False) <= 1e-5
+    assert g1.keys() == g0.keys()
+    floor = _floor(g0)
+    for n in g0:
+        limit = 1e-4 if g0[n].numel() == 1 else 1e-5
+        err = _rel(g1[n], g0[n], False, floor)
+        assert err <= limit, f"{n}: {err:.3e}"
