@@ -179,8 +179,9 @@ class _PipelinedScanRead(torch.autograd.Function):
         Wx_c, Wgx_c, ldx = ops.scan_inputs(Wx, Wgx, dt)
         out = chunked._Tapes(Wx_c, B, T, H)
         stats = torch.empty((B, T, 6), device=dev, dtype=torch.float32)
-        short = torch.empty((B, T, H), device=dev, dtype=dt)
-        sink = torch.zeros((B, T, H), device=dev, dtype=dt)  # bank-write gradient (backward)
+        retr = torch.empty((B, T, H), device=dev, dtype=dt)    # the three-way read
+        short = torch.empty((B, T, H), device=dev, dtype=dt)   # its output projection
+        sink = torch.zeros((B, T, H), device=dev, dtype=dt)    # bank-write gradient (backward)
         bounds = chunked._chunks(T, chunk)
         K = len(bounds)
         for st in (M, S, R):
@@ -206,7 +207,6 @@ class _PipelinedScanRead(torch.autograd.Function):
                     carry = f.finals
                 starts = torch.stack(starts)
 
-            # Leaves of the per-chunk read graphs.
             U = out.U
             ay, w, pl = out.tapes[2], out.tapes[3], out.tapes[1]
             w_leaf = w.detach().requires_grad_(True)
@@ -221,29 +221,49 @@ class _PipelinedScanRead(torch.autograd.Function):
                 return _SinkGather.apply(sink, bank_write, norm_w, idx,
                                          None if fold is not None else next_idx, rank)
 
+            def read_chunk(k: int):
+                # Statistics of window k, the three-way read of query chunk k against the
+                # bank [0, t1) (its own autograd graph) and, without autograd, its output
+                # projection (differentiated by hand in the backward).
+                t0, t1 = bounds[k]
+                st = torch.cuda.current_stream(dev)
+                _stats_window(out, stats, t0, t1, st.cuda_stream)
+                with torch.enable_grad():
+                    ay_leaf = ay[:, t0:t1].detach().requires_grad_(True)
+                    r = read.query_bank_retrieved(
+                        ay_leaf, query_stats=stats_leaf[:, t0:t1], bank_write=w_leaf,
+                        bank_norms=norms, bank_stats=stats_leaf[:, :t1], query_start=t0,
+                        gather=gather)
+                rd = r.detach().to(dt)
+                retr[:, t0:t1].copy_(rd)
+                # The projection as the training path evaluates it (three products in the
+                # same order, so the output rounds the same); its graph is dropped at once.
+                with torch.enable_grad():
+                    sh = read.short_read.project(U[:, t0:t1, :H], U[:, t0:t1, H:], rd)
+                short[:, t0:t1].copy_(sh.detach())
+                return r, ay_leaf
+
             chunks = []
             with _parameters_as(read, param_leaves):
-                for k, (t0, t1) in enumerate(bounds):
-                    last = k == K - 1
-                    st = M if last else R
-                    with torch.cuda.stream(st):
-                        st.wait_event(scan_done[k])
-                        if last and K > 1:
-                            M.wait_stream(R)
-                        _stats_window(out, stats, t0, t1, st.cuda_stream)
-                        with torch.enable_grad():
-                            win = [U[:, t0:t1, :H], U[:, t0:t1, H:], ay[:, t0:t1]]
-                            leaves = [x.detach().requires_grad_(True) for x in win]
-                            sh = read.query_bank_short(
-                                *leaves, query_stats=stats_leaf[:, t0:t1], bank_write=w_leaf,
-                                bank_norms=norms, bank_stats=stats_leaf[:, :t1], query_start=t0,
-                                gather=gather)
-                        short[:, t0:t1].copy_(sh.detach())
-                        chunks.append((sh, leaves))
-                # The long channel over the whole sequence and the read output, whole device.
+                with torch.cuda.stream(R):
+                    for k in range(K - 1):
+                        R.wait_event(scan_done[k])
+                        chunks.append(read_chunk(k))
+                    r_chunks = torch.cuda.Event()
+                    r_chunks.record(R)
+                    # The long channel over the whole sequence, beside the last chunk's read.
+                    R.wait_event(scan_done[K - 1])
+                    with torch.enable_grad():
+                        long = read._long_scan(w_leaf, p_leaf, None)
+                    r_long = torch.cuda.Event()
+                    r_long.record(R)
+                M.wait_event(scan_done[K - 1])
+                M.wait_event(r_chunks)
+                chunks.append(read_chunk(K - 1))
+                M.wait_event(r_long)
+                long_leaf = long.detach().requires_grad_(True)
                 with torch.enable_grad():
-                    long = read._long_scan(w_leaf, p_leaf, None)
-                    read_out = ops.direct.read_output(short_leaf, long, read.long_gain)
+                    read_out = ops.direct.read_output(short_leaf, long_leaf, read.long_gain)
             M.wait_stream(S)
         ambient.wait_stream(M)
         read_out.record_stream(ambient)
@@ -252,8 +272,9 @@ class _PipelinedScanRead(torch.autograd.Function):
         ctx.read, ctx.chunk, ctx.names = read, chunk, names
         ctx.bounds = bounds
         ctx.meta = [(x.dtype, tuple(x.shape)) for x in (Wx, Wgx, *core_in)]
-        ctx.graph = (chunks, read_out, w_leaf, p_leaf, stats_leaf, short_leaf, param_leaves, sink)
-        ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, starts, out.U, *out.tapes)
+        ctx.graph = (chunks, read_out, long, w_leaf, p_leaf, stats_leaf, short_leaf, long_leaf,
+                     param_leaves, sink)
+        ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, starts, retr, out.U, *out.tapes)
         ctx.set_materialize_grads(False)
         return U, read_out.detach()
 
@@ -262,9 +283,11 @@ class _PipelinedScanRead(torch.autograd.Function):
         saved = ctx.saved_tensors
         Wx, Wgx, Ug, A = saved[:4]
         vecs, scal = saved[4:20], saved[20:23]
-        starts = saved[23]
-        fwd_out = chunked._Tapes(None, 0, 0, 0, existing=saved[24:32])
-        chunks, read_out, w_leaf, p_leaf, stats_leaf, short_leaf, param_leaves, sink = ctx.graph
+        starts, retr = saved[23], saved[24]
+        fwd_out = chunked._Tapes(None, 0, 0, 0, existing=saved[25:33])
+        (chunks, read_out, long, w_leaf, p_leaf, stats_leaf, short_leaf, long_leaf, param_leaves,
+         sink) = ctx.graph
+        read = ctx.read
         B, T, H = Wx.shape
         dt = Wx.dtype
         code = ops._code(dt)
@@ -279,56 +302,67 @@ class _PipelinedScanRead(torch.autograd.Function):
         params, keep = ops._core_params(vecs, scal)
         pleaves = list(param_leaves.values())
         trainable = [p for p in pleaves if p.requires_grad]
+        W = param_leaves["short_read.out.weight"]
+        bias = param_leaves["short_read.out.bias"]
+        Wd = W.detach().to(dt)
         # Tape gradients of the reverse scans, full length, filled window by window.
         gU = (torch.zeros((B, T, 2 * H), device=dev, dtype=dt) if gU_out is None
               else gU_out.to(dt).contiguous().clone())
-        g_nov, g_ay, g_e, g_c = (torch.empty((B, T, H), device=dev, dtype=dt) for _ in range(4))
+        g_nov, g_ay, g_e, g_c, g_r = (torch.empty((B, T, H), device=dev, dtype=dt)
+                                      for _ in range(5))
         gWx, gWgx, day = (torch.empty((B, T, H), device=dev, dtype=dt) for _ in range(3))
         g_read = torch.zeros_like(read_out) if g_read is None else g_read.contiguous()
         for st in (M, S, R):
             st.wait_stream(ambient)
 
         with torch.cuda.stream(M):
-            # Read output and long channel (whole device).
-            torch.autograd.backward([read_out], [g_read],
-                                    inputs=[short_leaf, w_leaf, p_leaf, *trainable])
-            g_short = short_leaf.grad
-            if w_leaf.grad is not None:
-                sink.add_(w_leaf.grad)  # the long channel's write gradient
-            g_p = p_leaf.grad if p_leaf.grad is not None else torch.zeros_like(p_leaf)
-            S.wait_stream(M)
-            R.wait_stream(M)
+            # The read output's backward, then the long channel's on the read half beside
+            # the projection and last chunk's read backward on the whole device.
+            torch.autograd.backward([read_out], [g_read], inputs=[short_leaf, long_leaf, *trainable])
+            g_short = short_leaf.grad.reshape(B * T, H).to(dt)
+            head = torch.cuda.Event()
+            head.record(M)
+            R.wait_event(head)
+            with torch.cuda.stream(R):
+                if long_leaf.grad is not None:
+                    torch.autograd.backward([long], [long_leaf.grad],
+                                            inputs=[w_leaf, p_leaf, *trainable])
+            # out(cat[y, budget, retrieved]): gradients of its inputs (the [y, budget] half
+            # straight into U's layout).
+            gU.view(B * T, 2 * H).addmm_(g_short, Wd[:, :2 * H])
+            torch.mm(g_short, Wd[:, 2 * H:], out=g_r.view(B * T, H))
 
             carry = [None, None, None]
             bws = []
             for k in range(K - 1, -1, -1):
                 t0, t1 = bounds[k]
-                sh, leaves = chunks[k]
+                r, ay_leaf = chunks[k]
                 st = M if k == K - 1 else R
                 with torch.cuda.stream(st):
                     # w_leaf is listed so that the engine runs the gather's backward, whose
                     # gradient goes to the sink (it returns none for w_leaf itself).
-                    torch.autograd.backward([sh], [g_short[:, t0:t1]],
-                                            inputs=[*leaves, w_leaf, stats_leaf, *trainable])
-                    gy, gb, gay = (x.grad for x in leaves)
-                    if gy is not None:
-                        gU[:, t0:t1, :H] += gy
-                    if gb is not None:
-                        gU[:, t0:t1, H:] += gb
-                    if gay is not None:
-                        g_ay[:, t0:t1].copy_(gay)
+                    torch.autograd.backward([r], [g_r[:, t0:t1]],
+                                            inputs=[ay_leaf, w_leaf, stats_leaf, *trainable])
+                    if ay_leaf.grad is not None:
+                        g_ay[:, t0:t1].copy_(ay_leaf.grad)
                     else:
                         g_ay[:, t0:t1].zero_()
+                if st is not R:
+                    done = torch.cuda.Event()
+                    done.record(st)
+                    R.wait_event(done)
+                with torch.cuda.stream(R):
+                    if k == K - 1 and w_leaf.grad is not None:
+                        sink.add_(w_leaf.grad)  # the long channel's write gradient
+                    if p_leaf.grad is None:
+                        p_leaf.grad = torch.zeros_like(p_leaf)
+                    g_p = p_leaf.grad
                     gs = stats_leaf.grad
                     gs = torch.zeros_like(stats_leaf) if gs is None else gs.contiguous()
-                    _stats_bwd_window(gs, (g_nov, None, g_e, g_c), False, t0, t1, st.cuda_stream)
-                    _stats_bwd_window(gs, (None, g_p, None, None), True, t0, t1, st.cuda_stream)
+                    _stats_bwd_window(gs, (g_nov, None, g_e, g_c), False, t0, t1, R.cuda_stream)
+                    _stats_bwd_window(gs, (None, g_p, None, None), True, t0, t1, R.cuda_stream)
                     tapes_ready = torch.cuda.Event()
-                    tapes_ready.record(st)
-                if st is not R:
-                    # The next chunks' read backward (on R) adds into the same gradient
-                    # buffers (sink, statistics, parameters) as this one.
-                    R.wait_event(tapes_ready)
+                    tapes_ready.record(R)
                 with torch.cuda.stream(S):
                     S.wait_event(tapes_ready)
                     up = [gU, g_nov, g_p, g_ay, sink, g_e, g_c]
@@ -341,6 +375,12 @@ class _PipelinedScanRead(torch.autograd.Function):
                     ops._record_error_word(bw.ws, "core scan backward")
                     bws.append(bw)
                     carry = bw.g0
+            with torch.cuda.stream(R):
+                # The projection's weight gradients, beside the last reverse scan.
+                U2 = fwd_out.U.reshape(B * T, 2 * H)
+                gw = torch.cat((g_short.t() @ U2, g_short.t() @ retr.reshape(B * T, H)), dim=1)
+                W.grad = gw.to(W.dtype)
+                bias.grad = g_short.float().sum(0).to(bias.dtype)
             M.wait_stream(S)
             M.wait_stream(R)
             gvec = torch.stack([bw.part_vec.sum(0) for bw in bws]).sum(0)

@@ -538,22 +538,21 @@ class DABSNRead(nn.Module):
         admission = rp.admission_from_means(be, bc, bn, bp, hidden)
         return key_bias, admission, (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
 
-    def query_bank_short(self, y, budget, expression, *, query_stats, bank_write, bank_norms,
-                         bank_stats, query_start: int, gather=None) -> Tensor:
-        """The short-memory output ``out(cat[y, budget, retrieved])`` of a seq query chunk
-        against the bank of positions [0, bank_stats.shape[1]) (forward_query_bank_stats
-        without the long channel, read.py:650-823). ``bank_write`` [B, >= bank length, H] may
-        be the whole write tape with the bank as its prefix; ``bank_norms`` are the write
-        norms of its rows ([B, bank_write.shape[1]]). ``gather`` replaces the bank gather
-        (see ``_read_core``)."""
+    def query_bank_retrieved(self, expression, *, query_stats, bank_write, bank_norms,
+                             bank_stats, query_start: int, gather=None) -> Tensor:
+        """The three-way read ``retrieved`` of a seq query chunk against the bank of positions
+        [0, bank_stats.shape[1]) (forward_query_bank_stats before its output projection and
+        long channel, read.py:650-823). ``bank_write`` [B, >= bank length, H] may be the
+        whole write tape with the bank as its prefix; ``bank_norms`` are the write norms of
+        its rows ([B, bank_write.shape[1]]). ``gather`` replaces the bank gather (see
+        ``_read_core``)."""
         self._require_seq()
         hidden = int(expression.shape[-1])
         query = ops.direct.normalize_rows(expression, query_stats[..., 4].detach())
         key_bias, admission, cocktails = self._glue_from_stats(query_stats, bank_stats,
                                                                bank_write.dtype, hidden)
-        retrieved = self._read_core(query, cocktails, bank_write, bank_norms, key_bias, admission,
-                                    int(bank_stats.shape[1]), int(query_start), gather=gather)
-        return self.short_read.project(y, budget, retrieved.to(y.dtype))
+        return self._read_core(query, cocktails, bank_write, bank_norms, key_bias, admission,
+                               int(bank_stats.shape[1]), int(query_start), gather=gather)
 
 
 def collect_traces_enabled() -> bool:

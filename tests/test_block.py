@@ -48,13 +48,20 @@ def _fwd_bwd(block, x, w):
 
 
 def _check_same(a, b, tol):
+    """Outputs and input gradients relative to their own size; parameter gradients relative
+    to max(|grad|, 1e-3 x the largest parameter gradient): null_bias and adm_bias shift every
+    logit of a softmax equally, so their exact gradient is zero and both runs hold rounding
+    noise."""
     out_a, gx_a, g_a = a
     out_b, gx_b, g_b = b
     assert rel_err(out_a.cpu(), out_b.cpu()) <= tol
     assert rel_err(gx_a.cpu(), gx_b.cpu()) <= tol
     assert g_a.keys() == g_b.keys()
+    floor = 1e-3 * max(float(g.abs().max()) for g in g_b.values())
     for n in g_a:
-        assert rel_err(g_a[n].cpu(), g_b[n].cpu()) <= tol, f"{n}: {rel_err(g_a[n].cpu(), g_b[n].cpu()):.3e}"
+        d = float((g_a[n].cpu() - g_b[n].cpu()).abs().max())
+        err = d / max(float(g_b[n].abs().max()), floor)
+        assert err <= tol, f"{n}: {err:.3e}"
 
 
 def _chunk_case(device):

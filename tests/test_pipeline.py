@@ -8,7 +8,12 @@ only summation orders differ:
     stream instead of cooperatively);
   * fp32: read output and every gradient (input projections, core and read parameters)
     normwise 1e-5 (scalar parameter gradients that sum O(B*T*N) terms 1e-4);
-  * bf16 at state width 2048 (the config-4 kernel instances): Frobenius 2e-2;
+  * bf16 at state width 2048 (the config-4 kernel instances): read output and gradients
+    Frobenius 2e-2 from the sequential bf16 run;
+  * bf16 at width 512, where the fp32 scan runs too: every gradient within max(2e-2, 1.5 x
+    the sequential bf16 run's own distance) of the block run in fp32 (scalar gradients that
+    sum many cancelling terms move by up to a few 1e-2 under bf16 rounding in either
+    schedule);
   * dense banks (the successor fold) and partially admitted ones (no fold, a bank width
     that grows chunk by chunk); a DABSNBlock with block chunking, pipelined or not.
 """
@@ -74,14 +79,16 @@ def _floor(grads):
     return 1e-3 * max(float(g.abs().max()) for g in grads.values())
 
 
-@pytest.mark.parametrize("dtype,B,T,H,chunk,window", [
-    (torch.float32, 3, 96, 64, 32, 50.0),
-    (torch.float32, 3, 96, 64, 32, 0.3),
-    (torch.float32, 2, 100, 48, 24, 50.0),
-    (torch.bfloat16, 16, 512, 2048, 128, 50.0),
-    (torch.bfloat16, 16, 384, 2048, 128, 0.3),
+@pytest.mark.parametrize("dtype,B,T,H,chunk,window,ref32", [
+    (torch.float32, 3, 96, 64, 32, 50.0, False),
+    (torch.float32, 3, 96, 64, 32, 0.3, False),
+    (torch.float32, 2, 100, 48, 24, 50.0, False),
+    (torch.bfloat16, 16, 512, 2048, 128, 50.0, False),
+    (torch.bfloat16, 16, 384, 2048, 128, 0.3, False),
+    (torch.bfloat16, 16, 512, 512, 128, 50.0, True),
 ])
-def test_pipelined_scan_read_matches_sequential(cuda_device, dtype, B, T, H, chunk, window):
+def test_pipelined_scan_read_matches_sequential(cuda_device, dtype, B, T, H, chunk, window,
+                                                ref32):
     din = 32
     core, read = _modules(11 + T, din, H, window, cuda_device)
     g = torch.Generator().manual_seed(12)
@@ -104,12 +111,21 @@ def test_pipelined_scan_read_matches_sequential(cuda_device, dtype, B, T, H, chu
     assert _rel(r1, r0, fro) <= tol, f"read output {_rel(r1, r0, fro):.3e}"
     assert g1.keys() == g0.keys()
     worst = ("", 0.0)
-    floor = _floor(g0)
-    for n in g0:
-        err = _rel(g1[n], g0[n], fro, floor)
-        limit = tol if (fro or g0[n].numel() > 1) else 1e-4
-        assert err <= limit, f"gradient {n}: {err:.3e}"
-        worst = max(worst, (n, err), key=lambda v: v[1])
+    if not ref32:
+        floor = _floor(g0)
+        for n in g0:
+            err = _rel(g1[n], g0[n], fro, floor)
+            limit = tol if (fro or g0[n].numel() > 1) else 1e-4
+            assert err <= limit, f"gradient {n}: {err:.3e}"
+            worst = max(worst, (n, err), key=lambda v: v[1])
+    else:
+        _, _, gf, _ = _run(seq, core, read, x, gU, gr, torch.float32)
+        floor = _floor(gf)
+        for n in gf:
+            err = _rel(g1[n], gf[n], True, floor)
+            ref = _rel(g0[n], gf[n], True, floor)
+            assert err <= max(tol, 1.5 * ref), f"gradient {n}: {err:.3e} (sequential bf16 {ref:.3e})"
+            worst = max(worst, (n, err), key=lambda v: v[1])
     print(f"pipelined vs sequential ({dtype}, B={B} T={T} H={H}, n_max={n1}): "
           f"output {_rel(r1, r0, fro):.2e}, worst gradient {worst[0]} {worst[1]:.2e}")
 
