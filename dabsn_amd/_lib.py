@@ -108,6 +108,11 @@ _SIGNATURES = {
     "dabsn_hip_admit_step": (
         [i32, i64, i64, i64, i64, vp, i64, PTR8, vp, i32, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_fold": ([i64, i64, i64, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_glue_slots": ([i64, i64, i64, i64, vp, vp, i64, PTR8, i32, vp, vp, vp, vp], i32),
+    "dabsn_hip_glue_slots_partials": ([i64, i64], sz),
+    "dabsn_hip_glue_slots_bwd": (
+        [i64, i64, i64, i64, vp, vp, i64, PTR8, i32, vp, vp, vp, vp, i64, vp, vp, vp], i32),
+    "dabsn_hip_glue_rows_bwd": ([i64, i64, i64, vp, i32, vp, vp, i64, vp], i32),
     "dabsn_hip_bank_gather_bwd_prefix": (
         [i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, i32, vp, vp], i32),
     "dabsn_hip_bank_gather": ([i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),

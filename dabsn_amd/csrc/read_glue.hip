@@ -485,6 +485,128 @@ __global__ void __launch_bounds__(256) means_glue_kernel(int64_t rows, int N, in
            adm ? adm + i : nullptr, ck + i * 4);
 }
 
+// Per-slot glue of the training read: key bias, admission and cocktail of bank row idx[b][j]
+// for every slot j (glue_row, gathered inside the kernel). One thread per (b, j).
+__global__ void __launch_bounds__(256) glue_slots_kernel(int64_t n, int N, int L, int64_t ld,
+                                                         const float* __restrict__ stats,
+                                                         const int64_t* __restrict__ idx,
+                                                         float hidden, Ptr8 prm, int mode,
+                                                         float* kb, float* adm, float* cb) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t b = i / N;
+  int64_t pos = idx[i];
+  pos = pos < 0 ? 0 : (pos >= L ? L - 1 : pos);
+  glue_row(stats + b * ld + pos * 6, hidden, prm, mode, kb + i, adm + i, cb + i * 4);
+}
+
+// Gradient of one row's glue with respect to its four means (g4 = mean e, c, n, p) and the
+// eight parameters (added to gp), given the gradients of key bias, admission and cocktail
+// (gkb, gadm; gc4 may be null). Evaluated in fp32 from the means and intermediates of the
+// forward (rounded as the forward rounds them): the chain rule of the expressions in
+// glue_row, i.e. of read.py:58-72, 161-183.
+__device__ __forceinline__ void glue_row_bwd(const float* s, float hidden, const float* P,
+                                             int mode, float gkb, float gadm, const float* gc4,
+                                             float* g4, float* gp) {
+  const bool tb = mode & 1;
+  auto rt = [tb](float v) { return tb ? round_to<bf16>(v) : v; };
+  const float m[4] = {rt(s[0]), rt(s[1]), rt(s[2]), rt(s[3])};  // e, c, n, p
+  const float x = rt(m[3] * hidden);
+  const float lp = rt(log1pf(x));
+  gp[0] += gkb * lp;
+  gp[1] += gkb * m[2];
+  gp[2] += gkb;
+  gp[3] += gadm * lp;
+  gp[4] += gadm * m[2];
+  gp[5] += gadm * m[1];
+  gp[6] += gadm * m[0];
+  gp[7] += gadm;
+  const float glp = gkb * P[0] + gadm * P[3];
+  float g[4] = {gadm * P[6], gadm * P[5], gkb * P[1] + gadm * P[4], glp * hidden / (1.0f + x)};
+  if (gc4) {
+    // c = m / max(|m|, eps): dc/dm = (I - c c^T) / |m| above eps, I / eps below.
+    const float nrm = sqrtf(m[0] * m[0] + m[1] * m[1] + m[2] * m[2] + m[3] * m[3]);
+    if (nrm > kEps) {
+      const float inv = 1.0f / nrm;
+      float c[4], dot = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        c[k] = m[k] * inv;
+        dot += c[k] * gc4[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) g[k] += (gc4[k] - c[k] * dot) * inv;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) g[k] += gc4[k] / kEps;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) g4[k] = g[k];
+}
+
+// Backward of glue_slots_kernel: the means gradient of each slot's bank row is written to
+// gstats[b][idx[b][j]][0..3] (slots of a row are distinct positions; the caller zeroes the
+// other rows), and per-workgroup partial sums of the eight parameter gradients go to
+// partial[block][8] (summed in a fixed order by glue_params_reduce_kernel).
+__global__ void __launch_bounds__(256) glue_slots_bwd_kernel(
+    int64_t n, int N, int L, int64_t ld, const float* __restrict__ stats,
+    const int64_t* __restrict__ idx, float hidden, Ptr8 prm, int mode, const float* gkb,
+    const float* gadm, const float* gcb, float* gstats, int64_t ldg, float* partial) {
+  __shared__ float sh[4][8];
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  float gp[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (i < n) {
+    const int64_t b = i / N;
+    int64_t pos = idx[i];
+    pos = pos < 0 ? 0 : (pos >= L ? L - 1 : pos);
+    float P[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) P[k] = prm.p[k][0];
+    float g4[4];
+    glue_row_bwd(stats + b * ld + pos * 6, hidden, P, mode, gkb[i], gadm[i], gcb + i * 4, g4, gp);
+    float* o = gstats + b * ldg + pos * 6;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = g4[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float v = wave_sum(gp[k]);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6][k] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < 8) {
+    const int k = threadIdx.x;
+    partial[static_cast<size_t>(blockIdx.x) * 8 + k] = (sh[0][k] + sh[1][k]) + (sh[2][k] + sh[3][k]);
+  }
+}
+
+__global__ void glue_params_reduce_kernel(int nblocks, const float* partial, float* gparams) {
+  const int k = threadIdx.x;
+  if (k >= 8) return;
+  float acc = 0.0f;
+  for (int i = 0; i < nblocks; ++i) acc += partial[static_cast<size_t>(i) * 8 + k];
+  gparams[k] = acc;
+}
+
+// Backward of the query cocktails (means_glue rows with only the cocktail output): rows
+// (b, t), t < T, ld floats apart per batch row; gstats rows ldg apart.
+__global__ void __launch_bounds__(256) glue_rows_bwd_kernel(int64_t n, int T, int64_t ld,
+                                                            const float* __restrict__ stats,
+                                                            int mode, const float* gck,
+                                                            float* gstats, int64_t ldg) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t b = i / T, t = i % T;
+  const float P[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float gp[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float g4[4];
+  glue_row_bwd(stats + b * ld + t * 6, 1.0f, P, mode, 0.0f, 0.0f, gck + i * 4, g4, gp);
+  float* o = gstats + b * ldg + t * 6;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = g4[k];
+}
+
 // Incremental admission of the positions base .. base + n - 1 appended to a carried bank
 // (streaming decode). One workgroup per batch row: its threads compute the new positions'
 // glue into the bank's glue arrays (unless `stats` is null: the admission values are then
@@ -814,6 +936,81 @@ int dabsn_hip_admit_step(int mode, int64_t B, int64_t n, int64_t base, int64_t c
   hipLaunchKernelGGL(admit_step_kernel, dim3(static_cast<unsigned>(B)), dim3(256), 0, stream, n,
                      base, cap, stats, static_cast<float>(hidden), prm, mode, window, adm_dtype,
                      key_bias, admission, cocktail, amax, mcount, members);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+static int ptr8_of(const float* const* params, Ptr8& prm, const char* what) {
+  for (int k = 0; k < 8; ++k) {
+    DABSN_REQUIRE(params[k], "%s: null parameter %d", what, k);
+    prm.p[k] = params[k];
+  }
+  return DABSN_OK;
+}
+
+int dabsn_hip_glue_slots(int64_t B, int64_t N, int64_t L, int64_t ld, const float* stats,
+                         const int64_t* idx, int64_t hidden, const float* const* params, int mode,
+                         float* key_bias, float* admission, float* cocktail, hipStream_t stream) {
+  DABSN_REQUIRE(mode >= 0 && mode <= 3, "glue_slots: mode must be 0..3");
+  DABSN_REQUIRE(B > 0 && N >= 0 && L > 0 && ld >= 6 * L && hidden > 0 && B * N < (1ll << 40),
+                "glue_slots: bad shape");
+  if (N == 0) return DABSN_OK;
+  DABSN_REQUIRE(stats && idx && params && key_bias && admission && cocktail,
+                "glue_slots: null pointer");
+  DABSN_REQUIRE((reinterpret_cast<uintptr_t>(cocktail) & 15u) == 0,
+                "glue_slots: cocktail must be 16-byte aligned");
+  Ptr8 prm;
+  if (ptr8_of(params, prm, "glue_slots") != DABSN_OK) return DABSN_ERR_ARG;
+  const int64_t n = B * N;
+  hipLaunchKernelGGL(glue_slots_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n, (int)N,
+                     (int)L, ld, stats, idx, static_cast<float>(hidden), prm, mode, key_bias,
+                     admission, cocktail);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+size_t dabsn_hip_glue_slots_partials(int64_t B, int64_t N) {
+  return static_cast<size_t>(blocks_for(B * N, 256)) * 8 * sizeof(float);
+}
+
+int dabsn_hip_glue_slots_bwd(int64_t B, int64_t N, int64_t L, int64_t ld, const float* stats,
+                             const int64_t* idx, int64_t hidden, const float* const* params,
+                             int mode, const float* gkey_bias, const float* gadmission,
+                             const float* gcocktail, float* gstats, int64_t ldg, float* partial,
+                             float* gparams, hipStream_t stream) {
+  DABSN_REQUIRE(mode >= 0 && mode <= 3, "glue_slots backward: mode must be 0..3");
+  DABSN_REQUIRE(B > 0 && N >= 0 && L > 0 && ld >= 6 * L && ldg >= 6 * L && hidden > 0 &&
+                    B * N < (1ll << 40),
+                "glue_slots backward: bad shape");
+  DABSN_REQUIRE(gparams, "glue_slots backward: null gparams");
+  if (N == 0) return dabsn_hip_zero(gparams, 8 * sizeof(float), stream);
+  DABSN_REQUIRE(stats && idx && params && gkey_bias && gadmission && gcocktail && gstats && partial,
+                "glue_slots backward: null pointer");
+  Ptr8 prm;
+  if (ptr8_of(params, prm, "glue_slots backward") != DABSN_OK) return DABSN_ERR_ARG;
+  const int64_t n = B * N;
+  const unsigned nblk = blocks_for(n, 256);
+  hipLaunchKernelGGL(glue_slots_bwd_kernel, dim3(nblk), dim3(256), 0, stream, n, (int)N, (int)L,
+                     ld, stats, idx, static_cast<float>(hidden), prm, mode, gkey_bias, gadmission,
+                     gcocktail, gstats, ldg, partial);
+  DABSN_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(glue_params_reduce_kernel, dim3(1), dim3(64), 0, stream, (int)nblk, partial,
+                     gparams);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_glue_rows_bwd(int64_t B, int64_t T, int64_t ld, const float* stats, int mode,
+                            const float* gcocktail, float* gstats, int64_t ldg,
+                            hipStream_t stream) {
+  DABSN_REQUIRE(mode >= 0 && mode <= 3, "glue_rows backward: mode must be 0..3");
+  DABSN_REQUIRE(B > 0 && T >= 0 && ld >= 6 * T && ldg >= 6 * T && T < (1ll << 31),
+                "glue_rows backward: bad shape");
+  if (T == 0) return DABSN_OK;
+  DABSN_REQUIRE(stats && gcocktail && gstats, "glue_rows backward: null pointer");
+  const int64_t n = B * T;
+  hipLaunchKernelGGL(glue_rows_bwd_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, n,
+                     (int)T, ld, stats, mode, gcocktail, gstats, ldg);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }

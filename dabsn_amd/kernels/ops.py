@@ -747,6 +747,92 @@ def means_glue(stats: Tensor, hidden: int, params: Sequence[Tensor],
     return kb, adm, ck
 
 
+def glue_mode(tape_dtype: torch.dtype, params: Sequence[Tensor]) -> int:
+    """The dtype code of the glue kernels: bit 0 = bf16 tapes, bit 1 = bf16 gains too."""
+    if tape_dtype != torch.bfloat16:
+        return 0
+    return 1 | (2 if all(x.dtype == torch.bfloat16 for x in params) else 0)
+
+
+def _stats_rows(stats: Tensor) -> Tensor:
+    """Statistics rows as the glue kernels read them: fp32 [B, L, 6] with contiguous rows
+    (any batch stride)."""
+    if (stats.dim() != 3 or stats.shape[-1] != 6 or stats.dtype != torch.float32
+            or stats.stride(2) != 1 or stats.stride(1) != 6):
+        stats = stats.float().contiguous()
+    return stats
+
+
+class _SlotGlue(torch.autograd.Function):
+    """(key bias [B, N], admission [B, N], cocktail [B, N, 4]) of the bank rows idx of
+    ``bank_stats`` and the cocktails [B, C, 4] of ``query_stats`` (read.py:58-72, 155-183,
+    241-256), with the statistics rows' and the eight gains' gradients."""
+
+    @staticmethod
+    def forward(ctx, bank_stats: Tensor, query_stats: Tensor, idx: Tensor, hidden: int, mode: int,
+                *params: Tensor):
+        lib = _lib.load()
+        bs, qs = _stats_rows(bank_stats), _stats_rows(query_stats)
+        B, L, _ = bs.shape
+        C = qs.shape[1]
+        N = idx.shape[1]
+        ic = idx.to(torch.int64).contiguous()
+        prm = [_f32_scalar(x) for x in params]
+        ptrs = _lib.PTR8(*[x.data_ptr() for x in prm])
+        kb = torch.empty((B, N), device=bs.device, dtype=torch.float32)
+        adm = torch.empty_like(kb)
+        cb = torch.empty((B, N, 4), device=bs.device, dtype=torch.float32)
+        ck = torch.empty((B, C, 4), device=bs.device, dtype=torch.float32)
+        st = _stream(bs)
+        _lib.check(lib.dabsn_hip_glue_slots(B, N, L, int(bs.stride(0)), _p(bs), _p(ic), int(hidden),
+                                            ptrs, mode, _p(kb), _p(adm), _p(cb), st), "slot glue")
+        _lib.check(lib.dabsn_hip_means_glue(B, C, int(qs.stride(0)), _p(qs), int(hidden), ptrs, mode,
+                                            None, None, _p(ck), st), "query cocktail")
+        ctx.save_for_backward(bs, qs, ic, *prm)
+        ctx.hidden, ctx.mode = int(hidden), int(mode)
+        ctx.meta = [(x.dtype, tuple(x.shape)) for x in params]
+        ctx.set_materialize_grads(False)
+        return kb, adm, cb, ck
+
+    @staticmethod
+    def backward(ctx, gkb, gadm, gcb, gck):
+        bs, qs, ic, *prm = ctx.saved_tensors
+        lib = _lib.load()
+        B, L, _ = bs.shape
+        C = qs.shape[1]
+        N = ic.shape[1]
+        z = lambda g, shape: (torch.zeros(shape, device=bs.device, dtype=torch.float32) if g is None  # noqa: E731
+                              else g.float().contiguous())
+        gkb, gadm = z(gkb, (B, N)), z(gadm, (B, N))
+        gcb, gck = z(gcb, (B, N, 4)), z(gck, (B, C, 4))
+        gbank = torch.zeros((B, L, 6), device=bs.device, dtype=torch.float32)
+        gquery = torch.zeros((B, C, 6), device=bs.device, dtype=torch.float32)
+        partial = torch.empty(max(lib.dabsn_hip_glue_slots_partials(B, N) // 4, 1),
+                              device=bs.device, dtype=torch.float32)
+        gparams = torch.empty((8,), device=bs.device, dtype=torch.float32)
+        ptrs = _lib.PTR8(*[x.data_ptr() for x in prm])
+        st = _stream(bs)
+        _lib.check(lib.dabsn_hip_glue_slots_bwd(
+            B, N, L, int(bs.stride(0)), _p(bs), _p(ic), ctx.hidden, ptrs, ctx.mode, _p(gkb),
+            _p(gadm), _p(gcb), _p(gbank), 6 * L, _p(partial), _p(gparams), st), "slot glue backward")
+        _lib.check(lib.dabsn_hip_glue_rows_bwd(B, C, int(qs.stride(0)), _p(qs), ctx.mode, _p(gck),
+                                               _p(gquery), 6 * C, st), "query cocktail backward")
+        gp = [gparams[k].reshape(shape).to(dtype) for k, (dtype, shape) in enumerate(ctx.meta)]
+        return (gbank, gquery, None, None, None, *gp)
+
+
+def slot_glue(bank_stats: Tensor, query_stats: Tensor, idx: Tensor, hidden: int,
+              params: Sequence[Tensor], tape_dtype: torch.dtype) -> tuple[Tensor, ...]:
+    """The read's per-slot glue in one kernel and its backward in two (see _SlotGlue):
+    returns (key bias, admission, bank cocktail [B, N, 4], query cocktail [B, C, 4]) as
+    fp32 holding the values of the reference's expressions in their dtypes. ``params`` =
+    (p_gain, novelty_gain, null_bias, adm_p_gain, adm_novelty_gain, adm_saturation_gain,
+    adm_energy_gain, adm_bias)."""
+    _require_cuda(bank_stats)
+    return _SlotGlue.apply(bank_stats, query_stats, idx, int(hidden),
+                           glue_mode(tape_dtype, params), *params)
+
+
 # ---------------------------------------------------------------------------
 # Cross-entropy row kernels of the chunked readout loss (loss.py)
 # ---------------------------------------------------------------------------

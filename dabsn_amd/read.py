@@ -99,6 +99,53 @@ def _tape_means(stats: Tensor, energy: Tensor, saturation: Tensor, novelty: Tens
     return tuple(m.to(t.dtype) for m, t in zip(means, (energy, saturation, novelty, plasticity)))
 
 
+class _ArrayGlue:
+    """Read glue held as arrays over the bank positions (key bias, admission, cocktail) plus
+    the query cocktails, gathered per admitted slot with torch (read.py:241-256). Used on
+    the CPU and by the inference paths that build the arrays in one kernel or keep them per
+    bank position."""
+
+    def __init__(self, key_bias: Tensor, admission: Tensor, bank_cocktail: Tensor,
+                 query_cocktail: Tensor) -> None:
+        self.kb, self.adm, self.cb, self.ck = key_bias, admission, bank_cocktail, query_cocktail
+
+    def admission_for_select(self) -> Tensor:
+        return self.adm
+
+    def slots(self, idx: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+        """(bank cocktail [B, N, 4], key bias [B, N], admission [B, N], query cocktail)."""
+        return (torch.gather(self.cb, 1, idx.unsqueeze(-1).expand(-1, -1, 4)),
+                torch.gather(self.kb, 1, idx), torch.gather(self.adm, 1, idx), self.ck)
+
+
+class _StatsGlue:
+    """Read glue evaluated from statistics rows on the device: the admission of every bank
+    position for the selection (``ops.means_glue``, no gradient; the same values as the torch
+    expressions, so the same slots), then per admitted slot its key bias, admission and
+    cocktail and the query cocktails in one differentiable kernel (``ops.slot_glue``) instead
+    of some forty small tensor operations and their backward."""
+
+    def __init__(self, read: "DABSNRead", query_stats: Tensor, bank_stats: Tensor,
+                 tape_dtype: torch.dtype, hidden: int) -> None:
+        rp = read.short_read
+        self.params = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain,
+                       rp.adm_novelty_gain, rp.adm_saturation_gain, rp.adm_energy_gain,
+                       rp.adm_bias)
+        self.qs, self.bs, self.dtype, self.hidden = query_stats, bank_stats, tape_dtype, hidden
+
+    def admission_for_select(self) -> Tensor:
+        _, adm, _ = ops.means_glue(self.bs.detach(), self.hidden, [p.detach() for p in self.params],
+                                   self.dtype)
+        if ops.glue_mode(self.dtype, self.params) == 3:
+            adm = adm.to(torch.bfloat16)  # the reference's admission is a bf16 tensor here
+        return adm
+
+    def slots(self, idx: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+        kb, adm, cb, ck = ops.slot_glue(self.bs, self.qs, idx, self.hidden, self.params,
+                                        self.dtype)
+        return cb, kb, adm, ck
+
+
 class DABSNRead(nn.Module):
     """The canonical DABSN memory read: ``seq`` (causal prefix), ``field`` (the whole
     sequence) or ``hybrid`` (both, mixed by ``sigmoid(hybrid_gate)``)."""
@@ -165,16 +212,17 @@ class DABSNRead(nn.Module):
         next_idx = (idx + 1).clamp(max=length - 1)
         return n_max, idx, valid, next_idx, rank, fold
 
-    def _bank(self, cocktail_bank: Tensor, key_bias: Tensor, admission: Tensor, length: int,
-              query_start: int, width: int | None = None,
+    def _bank(self, glue, length: int, query_start: int, width: int | None = None,
               members: tuple[Tensor, Tensor] | None = None) -> dict[str, object]:
-        """Slot selection and the per-slot glue gathered for the read (read.py:185-256,
-        298-303): n_max, idx, valid, next_idx, rank, the bank's cocktail, key bias and
-        admission, the read scale and the slot positions relative to the query chunk.
-        ``members`` = (slot list [B, cap], counts [B]) kept incrementally by a carried bank
-        (inference): the selection is read from it instead of rerun over the bank."""
+        """Slot selection and the per-slot glue for the read (read.py:185-256, 298-303):
+        n_max, idx, valid, next_idx, rank, the slots' cocktail, key bias and admission, the
+        query cocktails, the read scale and the slot positions relative to the query chunk.
+        ``glue``: an _ArrayGlue or _StatsGlue. ``members`` = (slot list [B, cap], counts
+        [B]) kept incrementally by a carried bank (inference): the selection is read from it
+        instead of rerun over the bank."""
         fold = None
         if members is None:
+            admission = glue.admission_for_select()
             # The successor fold serves the training read (gather + read under autograd).
             want_fold = torch.is_grad_enabled() and admission.is_cuda
             n_max, idx, valid, next_idx, rank, fold = self._select(admission, length, width,
@@ -190,13 +238,11 @@ class DABSNRead(nn.Module):
                      < counts.clamp_min(1).unsqueeze(1))
             next_idx = (idx + 1).clamp(max=length - 1)
             rank = idx.new_empty((0,), dtype=torch.int32)  # the gather's backward only
+        cb, kb, adm, ck = glue.slots(idx)
         return {
             "n_max": n_max, "idx": idx, "valid": valid, "next_idx": next_idx, "rank": rank,
-            "fold": fold,
-            "cocktail": torch.gather(cocktail_bank, 1, idx.unsqueeze(-1).expand(-1, -1, 4)),
-            "key_bias": torch.gather(key_bias, 1, idx),
-            "admission": torch.gather(admission, 1, idx),
-            "scale": self._scale(),
+            "fold": fold, "cocktail": cb, "key_bias": kb, "admission": adm,
+            "query_cocktail": ck, "scale": self._scale(),
             "read_idx": idx if query_start == 0 else idx - query_start,
         }
 
@@ -247,16 +293,18 @@ class DABSNRead(nn.Module):
             "query_start": int(query_start),
         }
 
-    def _read_core(self, query, cocktail, bank_write, norm_w, key_bias, admission, length: int,
-                   query_start: int, width: int | None = None,
-                   members: tuple[Tensor, Tensor] | None = None, gather=None):
-        """``gather`` (optional): called as gather(bank_write, norm_w, idx, next_idx, rank,
-        fold) -> (K, V, Vn or None) in place of the bank gather op on the training path."""
-        bank = self._bank(cocktail[1], key_bias, admission, length, query_start, width, members)
+    def _read_core(self, query, glue, bank_write, norm_w, length: int, query_start: int,
+                   width: int | None = None, members: tuple[Tensor, Tensor] | None = None,
+                   gather=None):
+        """The read of ``query`` rows against the bank (glue: see ``_bank``). ``gather``
+        (optional): called as gather(bank_write, norm_w, idx, next_idx, rank, fold) ->
+        (K, V, Vn or None) in place of the bank gather op on the training path."""
+        bank = self._bank(glue, length, query_start, width, members)
         n_max, idx, valid, next_idx, rank = (bank[k] for k in ("n_max", "idx", "valid",
                                                                 "next_idx", "rank"))
         self.last_n_max = n_max
         bank_cocktail, bank_bias, bank_adm = bank["cocktail"], bank["key_bias"], bank["admission"]
+        query_cocktail = bank["query_cocktail"]
         scale, read_idx = bank["scale"], bank["read_idx"]
         hidden = int(query.shape[-1])
         rows = int(query.shape[1])
@@ -291,7 +339,7 @@ class DABSNRead(nn.Module):
                             B=int(query.shape[0]), T=rows, H=hidden, dtype=dtype)
         if decode:
             retrieved = ops.read3_decode(
-                query, bank_write, norm_w, idx, next_idx, read_idx, valid, cocktail[0],
+                query, bank_write, norm_w, idx, next_idx, read_idx, valid, query_cocktail,
                 bank_cocktail, bank_bias, bank_adm, scale,
                 (self.short_gain, self.pad_gain, self.induct_gain, self.cocktail_gain))
         else:
@@ -310,7 +358,7 @@ class DABSNRead(nn.Module):
                 # mode 0: causal masks (seq); mode 1: every admitted slot for every query
                 # (field), read.py:283-314
                 return ops.admitted_three_way_read_train(
-                    query, K, V, Vn, cocktail[0], bank_cocktail, bank_bias, bank_adm, scale,
+                    query, K, V, Vn, query_cocktail, bank_cocktail, bank_bias, bank_adm, scale,
                     read_idx, valid, mode, self.short_gain, self.pad_gain, self.induct_gain,
                     self.cocktail_gain, fold=fold)
 
@@ -367,25 +415,18 @@ class DABSNRead(nn.Module):
 
     def _glue(self, expression, write, novelty, plasticity, energy, saturation):
         """Per-position glue of the read (read.py:154-183): the tape statistics rows, the
-        normalised query, key bias, admission and cocktail."""
-        rp = self.short_read
+        normalised query and the glue (key bias, admission, cocktail) of every position."""
         hidden = int(expression.shape[-1])
         stats = ops.direct.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
-        mean_e, mean_c, mean_n, mean_p = _tape_means(stats, energy, saturation, novelty, plasticity)
         query = ops.direct.normalize_rows(expression, stats[..., 4].detach())
-        key_bias = rp.key_bias_from_means(mean_n, mean_p, hidden)
-        admission = rp.admission_from_means(mean_e, mean_c, mean_n, mean_p, hidden)
-        cocktail = _cocktail(mean_e, mean_c, mean_n, mean_p)
-        return stats, query, key_bias, admission, cocktail
+        return stats, query, self._glue_from_stats(stats, stats, expression.dtype, hidden)
 
     def _unified_forward(self, y, budget, expression, write, novelty, plasticity, energy,
                          saturation) -> Tensor:
         rp = self.short_read
         seq_len = int(expression.shape[1])
-        stats, query, key_bias, admission, cocktail = self._glue(
-            expression, write, novelty, plasticity, energy, saturation)
-        retrieved = self._read_core(query, (cocktail, cocktail), write, stats[..., 5].detach(),
-                                    key_bias, admission, seq_len, 0)
+        stats, query, glue = self._glue(expression, write, novelty, plasticity, energy, saturation)
+        retrieved = self._read_core(query, glue, write, stats[..., 5].detach(), seq_len, 0)
         output = rp.project(y, budget, retrieved.to(y.dtype))
         long = self._long_scan(write, plasticity, novelty)
         return ops.direct.read_output(output, long, self.long_gain)
@@ -437,14 +478,10 @@ class DABSNRead(nn.Module):
         q_stats = ops.direct.read_tape_stats(novelty, plasticity, energy, saturation, expression, write)
         b_stats = ops.direct.read_tape_stats(bank_novelty, bank_p, bank_energy, bank_saturation,
                                       bank_write, bank_write)
-        qe, qc, qn, qp = _tape_means(q_stats, energy, saturation, novelty, plasticity)
-        be, bc, bn, bp = _tape_means(b_stats, bank_energy, bank_saturation, bank_novelty, bank_p)
         query = ops.direct.normalize_rows(expression, q_stats[..., 4].detach())
-        key_bias = rp.key_bias_from_means(bn, bp, hidden)
-        admission = rp.admission_from_means(be, bc, bn, bp, hidden)
-        cocktails = (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
-        retrieved = self._read_core(query, cocktails, bank_write, b_stats[..., 5].detach(),
-                                    key_bias, admission, bank_len, int(query_start))
+        glue = self._glue_from_stats(q_stats, b_stats, bank_write.dtype, hidden)
+        retrieved = self._read_core(query, glue, bank_write, b_stats[..., 5].detach(), bank_len,
+                                    int(query_start))
         short_output = rp.project(y, budget, retrieved.to(y.dtype))
         result = self._long_scan_from_state(write, plasticity, novelty,
                                             initial_state=initial_long_state,
@@ -496,23 +533,23 @@ class DABSNRead(nn.Module):
                     and query.dtype == bank_store.write.dtype):
                 retrieved = self._read_members(query, bank_store, int(bank_len), int(width),
                                                int(query_start))
-            cocktails = (bank_cocktail[:, bank_len - rows:], bank_cocktail)
+            glue = _ArrayGlue(key_bias, admission, bank_cocktail,
+                              bank_cocktail[:, bank_len - rows:])
         elif not torch.is_grad_enabled() and bank_stats.is_cuda:
             # Inference (streaming decode): the per-position glue of the whole bank in one
             # kernel instead of ~25 small ones per layer and token.
             prm = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain,
                    rp.adm_novelty_gain, rp.adm_saturation_gain, rp.adm_energy_gain, rp.adm_bias)
             key_bias, admission, bank_cocktail = ops.means_glue(bank_stats, hidden, prm, tape_dtype)
-            cocktails = (ops.means_glue(query_stats, hidden, prm, tape_dtype)[2], bank_cocktail)
             if tape_dtype == torch.bfloat16 and rp.adm_bias.dtype == torch.bfloat16:
                 # The reference's admission is a bf16 tensor here: its floor is bf16 too.
                 admission = admission.to(torch.bfloat16)
+            glue = _ArrayGlue(key_bias, admission, bank_cocktail,
+                              ops.means_glue(query_stats, hidden, prm, tape_dtype)[2])
         else:
-            key_bias, admission, cocktails = self._glue_from_stats(query_stats, bank_stats,
-                                                                   tape_dtype, hidden)
+            glue = self._glue_from_stats(query_stats, bank_stats, tape_dtype, hidden)
         if retrieved is None:
-            retrieved = self._read_core(query, cocktails, bank_write,
-                                        bank_stats[..., 5].detach(), key_bias, admission,
+            retrieved = self._read_core(query, glue, bank_write, bank_stats[..., 5].detach(),
                                         bank_len, int(query_start), bank_width, members)
         short_output = rp.project(y, budget, retrieved.to(y.dtype))
         long, final_state = self._long_scan_from_state(write, plasticity, None,
@@ -529,14 +566,18 @@ class DABSNRead(nn.Module):
 
 
     def _glue_from_stats(self, query_stats, bank_stats, tape_dtype, hidden: int):
-        """Key bias and admission of the bank rows and the (query, bank) cocktails from
-        statistics rows, with the means in the tape dtype (read.py:58-72, 161-183)."""
+        """The glue (key bias, admission, cocktails; read.py:58-72, 161-183) of the bank rows
+        ``bank_stats`` and the query rows ``query_stats``, with the means in the tape dtype:
+        evaluated by the device kernels on the GPU (_StatsGlue), by the torch expressions
+        elsewhere (_ArrayGlue)."""
+        if bank_stats.is_cuda and bank_stats.dtype == torch.float32:
+            return _StatsGlue(self, query_stats, bank_stats, tape_dtype, hidden)
         rp = self.short_read
         qe, qc, qn, qp = (m.to(tape_dtype) for m in query_stats.unbind(-1)[:4])
         be, bc, bn, bp = (m.to(tape_dtype) for m in bank_stats.unbind(-1)[:4])
         key_bias = rp.key_bias_from_means(bn, bp, hidden)
         admission = rp.admission_from_means(be, bc, bn, bp, hidden)
-        return key_bias, admission, (_cocktail(qe, qc, qn, qp), _cocktail(be, bc, bn, bp))
+        return _ArrayGlue(key_bias, admission, _cocktail(be, bc, bn, bp), _cocktail(qe, qc, qn, qp))
 
     def query_bank_retrieved(self, expression, *, query_stats, bank_write, bank_norms,
                              bank_stats, query_start: int, gather=None) -> Tensor:
@@ -549,10 +590,9 @@ class DABSNRead(nn.Module):
         self._require_seq()
         hidden = int(expression.shape[-1])
         query = ops.direct.normalize_rows(expression, query_stats[..., 4].detach())
-        key_bias, admission, cocktails = self._glue_from_stats(query_stats, bank_stats,
-                                                               bank_write.dtype, hidden)
-        return self._read_core(query, cocktails, bank_write, bank_norms, key_bias, admission,
-                               int(bank_stats.shape[1]), int(query_start), gather=gather)
+        glue = self._glue_from_stats(query_stats, bank_stats, bank_write.dtype, hidden)
+        return self._read_core(query, glue, bank_write, bank_norms, int(bank_stats.shape[1]),
+                               int(query_start), gather=gather)
 
 
 def collect_traces_enabled() -> bool:

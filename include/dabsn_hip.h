@@ -247,6 +247,30 @@ int dabsn_hip_normalize_rows_bwd(int dtype, int64_t rows, int64_t H, const void*
 int dabsn_hip_means_glue(int64_t B, int64_t N, int64_t ld, const float* stats, int64_t hidden,
                          const float* const* params, int mode, float* key_bias, float* admission,
                          float* cocktail, hipStream_t stream);
+/* The same expressions for the admitted slots of a read (replaces read.py:241-256's
+ * torch.gather of the key bias, admission and cocktail by slot): for slot j of row b,
+ * the glue of bank row idx[b][j] (clamped into [0, L)) of stats (rows of batch b at stats +
+ * b * ld). Outputs [B, N] and [B, N, 4] (16-byte aligned). */
+int dabsn_hip_glue_slots(int64_t B, int64_t N, int64_t L, int64_t ld, const float* stats,
+                         const int64_t* idx, int64_t hidden, const float* const* params, int mode,
+                         float* key_bias, float* admission, float* cocktail, hipStream_t stream);
+/* Backward of dabsn_hip_glue_slots: the four mean gradients of slot j's bank row are written
+ * to gstats + b * ldg + 6 idx[b][j] (columns 0..3; the slots of a row are distinct
+ * positions, every other row is left as it is), and gparams[8] receives the eight
+ * parameter gradients, summed in a fixed order through `partial`
+ * (dabsn_hip_glue_slots_partials(B, N) bytes). Evaluated in fp32 from the forward's means
+ * and intermediates, rounded as the forward rounds them. */
+size_t dabsn_hip_glue_slots_partials(int64_t B, int64_t N);
+int dabsn_hip_glue_slots_bwd(int64_t B, int64_t N, int64_t L, int64_t ld, const float* stats,
+                             const int64_t* idx, int64_t hidden, const float* const* params,
+                             int mode, const float* gkey_bias, const float* gadmission,
+                             const float* gcocktail, float* gstats, int64_t ldg, float* partial,
+                             float* gparams, hipStream_t stream);
+/* Backward of the cocktail of rows (b, t), t < T, of stats (batch rows ld floats apart):
+ * the four mean gradients written to gstats + b * ldg + 6 t (columns 0..3). */
+int dabsn_hip_glue_rows_bwd(int64_t B, int64_t T, int64_t ld, const float* stats, int mode,
+                            const float* gcocktail, float* gstats, int64_t ldg,
+                            hipStream_t stream);
 /* Admitted-slot selection (src/dabsn/read.py:185-239): per row, floor = cummax(adm) -
  * window (whole = 0, seq geometry) or max over the row of adm - window (whole = 1, field
  * and hybrid geometry, read.py:189-191), member = adm >= floor, order = stable partition

@@ -106,11 +106,12 @@ def read_pieces(read, tapes):
     """The product's read pieces for full tapes: glue, selection, bank gather."""
     y, budget, ay, w, nov, pl, en, sat = tapes
     T = int(ay.shape[1])
-    stats, q, kb, adm, ck = read._glue(ay, w, nov, pl, en, sat)
-    bank = read._bank(ck, kb, adm, T, 0)
+    stats, q, glue = read._glue(ay, w, nov, pl, en, sat)
+    bank = read._bank(glue, T, 0)
     K, V, Vn = ops.bank_gather(w, stats[..., 5], bank["idx"], bank["next_idx"], bank["rank"])
-    return {"stats": stats, "q": q, "key_bias": kb, "admission": adm, "cocktail": ck,
-            "K": K, "V": V, "Vn": Vn, **{f"bank_{k}": v for k, v in bank.items()}, "T": T}
+    return {"stats": stats, "q": q, "admission": glue.admission_for_select(),
+            "cocktail": bank["query_cocktail"], "K": K, "V": V, "Vn": Vn,
+            **{f"bank_{k}": v for k, v in bank.items()}, "T": T}
 
 
 def read_gains(read):
