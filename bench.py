@@ -112,9 +112,9 @@ class ScanRead(torch.nn.Module):
         if self.pipelined and pipeline.pipeline_applies(self.read, Wx, self.chunk):
             # The read of query chunk k beside the scan of chunk k + 1 (and in reverse in the
             # backward), on the two halves of the device.
-            U, read = pipeline.pipelined_scan_read(self.read, self.chunk, Wx, Wgx,
-                                                   self.core.scan_inputs())
-            return U.split(self.state, dim=-1)[0], read
+            y, _, read = pipeline.pipelined_scan_read(self.read, self.chunk, Wx, Wgx,
+                                                      self.core.scan_inputs())
+            return y, read
         U, nov, p, ay, w, e, c = self.scan(Wx, Wgx)
         y, budget = U.split(self.state, dim=-1)
         return y, self.read(y, budget, ay, w, nov, p, e, c)

@@ -136,15 +136,19 @@ class _ChunkedCoreScan(torch.autograd.Function):
         carry = [x.float().contiguous() for x in (b0, e0, c0)]
         Wx_c, Wgx_c, ldx = ops.scan_inputs(Wx, Wgx, dt)
         out = _Tapes(Wx_c, B, T, H)
-        starts = []
+        starts, calls = [], []
         for t0, t1 in _chunks(T, chunk):
             starts.append(torch.stack(carry))
             f = _Fwd(code, Wx_c, Wgx_c, GA, params, *carry, out, t0, t1, ldx)
             tk = ops.KernelTimer.begin("core_scan_fwd", Wx)
             f.launch(stream)
             ops.KernelTimer.end(tk)
-            ops._record_error_word(f.ws, "core scan forward")
+            calls.append(f)
             carry = f.finals
+        # Error words after every chunk is enqueued (a checking sync per chunk would leave
+        # the device idle between chunks).
+        for f in calls:
+            ops._record_error_word(f.ws, "core scan forward")
         del keep
         finals = [f.to(x.dtype) for f, x in zip(carry, (b0, e0, c0))]
         ctx.chunk = chunk
@@ -180,16 +184,19 @@ class _ChunkedCoreScan(torch.autograd.Function):
         gWx, gWgx, day = (_empty((B, T, H), Wx) for _ in range(3))
         gvec = torch.zeros((16, H), device=Wx.device, dtype=torch.float32)
         gscal = torch.zeros((3,), device=Wx.device, dtype=torch.float32)
+        calls = []
         for k in range(K - 1, -1, -1):
             bw = _Bwd(code, GAT, params, starts[k, 0].contiguous(), starts[k, 2].contiguous(),
                       fwd_out, up, carry, (gWx, gWgx, day), *bounds[k])
             tk = ops.KernelTimer.begin("core_scan_bwd", Wx)
             bw.launch(stream)
             ops.KernelTimer.end(tk)
-            ops._record_error_word(bw.ws, "core scan backward")
+            calls.append(bw)
             gvec += bw.part_vec.sum(0)
             gscal += bw.part_scal.sum(0)
             carry = bw.g0
+        for bw in calls:
+            ops._record_error_word(bw.ws, "core scan backward")
         del keep
         # grad [Ug; A] = [gWgx; day]^T y over the whole sequence (y = first half of U).
         y = fwd_out.U.reshape(B * T, 2 * H)[:, :H]

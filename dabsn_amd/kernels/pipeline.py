@@ -10,12 +10,16 @@ it runs. Here the scan runs on one CU-masked stream (16 CUs of every XCD, plain 
 
 * forward: the scan of chunk k + 1 runs while the read of query chunk k (its statistics,
   selection, bank gather, three-way read and output projection against the bank of
-  positions [0, end of chunk k)) runs beside it; the last chunk's read, the long channel
-  (one scan over the whole sequence) and the read output follow on the whole device;
-* backward: the read output and the long channel first, then per chunk, last chunk first,
-  the read backward of query chunk k completes the tape gradients of window k (its query
-  rows, and the bank rows of window k, which only query chunks >= k read), the reverse scan
-  of chunk k starts on the scan's half, and the read backward of chunk k - 1 runs beside it.
+  positions [0, end of chunk k)) and the long channel over window k (its recurrent state
+  carried from window k - 1) run beside it; the last chunk's read and the read output
+  follow on the whole device, the last window's long channel beside them;
+* backward: the read output first, the long channel's last two windows on the read half
+  beside the last chunk's projection and read backward, then per chunk, last chunk first,
+  the projection, read and long-channel backward of window k complete its tape gradients
+  (its query rows, and the bank rows of window k, which only query chunks >= k read), the
+  reverse scan of chunk k starts on the scan's half, and the backward of chunk k - 1 runs
+  beside it, as do the core weight gradients of the windows whose reverse scans have
+  finished.
 
 Each query chunk's read is its own small autograd graph built under ``enable_grad`` inside
 this function's forward, on detached leaves (the chunk's y, budget and expression windows,
@@ -35,6 +39,7 @@ import os
 from typing import Optional, Sequence
 
 import torch
+import torch.nn.functional as F
 from torch import Tensor
 
 from .. import _lib, events
@@ -157,6 +162,15 @@ def _stats_bwd_window(gstats: Tensor, outs: Sequence[Optional[Tensor]], accumula
         stream), "tape statistics backward")
 
 
+def _check_scans(S, calls, what: str) -> None:
+    """The scans' error words, read on the scan stream once everything is enqueued: a
+    checking read then waits for the scans only (not for the read half's work), and none
+    sits between two launches."""
+    with torch.cuda.stream(S):
+        for c in calls:
+            ops._record_error_word(c.ws, what)
+
+
 class _PipelinedScanRead(torch.autograd.Function):
     @staticmethod
     def forward(ctx, read, chunk: int, names: tuple, Wx: Tensor, Wgx: Tensor, *rest: Tensor):
@@ -182,6 +196,7 @@ class _PipelinedScanRead(torch.autograd.Function):
         retr = torch.empty((B, T, H), device=dev, dtype=dt)    # the three-way read
         short = torch.empty((B, T, H), device=dev, dtype=dt)   # its output projection
         sink = torch.zeros((B, T, H), device=dev, dtype=dt)    # bank-write gradient (backward)
+        long_out = torch.empty((B, T, H), device=dev, dtype=dt)  # the long channel
         bounds = chunked._chunks(T, chunk)
         K = len(bounds)
         for st in (M, S, R):
@@ -199,7 +214,6 @@ class _PipelinedScanRead(torch.autograd.Function):
                     tk = ops.KernelTimer.begin("core_scan_fwd", Wx)
                     f.launch(S)
                     ops.KernelTimer.end(tk)
-                    ops._record_error_word(f.ws, "core scan forward")
                     e = torch.cuda.Event()
                     e.record(S)
                     scan_done.append(e)
@@ -210,12 +224,13 @@ class _PipelinedScanRead(torch.autograd.Function):
             U = out.U
             ay, w, pl = out.tapes[2], out.tapes[3], out.tapes[1]
             w_leaf = w.detach().requires_grad_(True)
-            p_leaf = pl.detach().requires_grad_(True)
             stats_leaf = stats.detach().requires_grad_(True)
             short_leaf = short.detach().requires_grad_(True)
             param_leaves = {n: p.detach().requires_grad_(p.requires_grad)
                             for n, p in zip(names, read_params)}
             norms = stats_leaf[..., 5].detach()
+            Wd = read.short_read.out.weight.detach().to(dt)
+            bd = read.short_read.out.bias.detach().to(dt)
 
             def gather(bank_write, norm_w, idx, next_idx, rank, fold):
                 return _SinkGather.apply(sink, bank_write, norm_w, idx,
@@ -224,10 +239,14 @@ class _PipelinedScanRead(torch.autograd.Function):
             def read_chunk(k: int):
                 # Statistics of window k, the three-way read of query chunk k against the
                 # bank [0, t1) (its own autograd graph) and, without autograd, its output
-                # projection (differentiated by hand in the backward).
+                # projection (differentiated by hand in the backward): the [y, budget] block
+                # with the bias first (enqueued ahead of the read's host sync on the bank
+                # width), then the retrieved block added.
                 t0, t1 = bounds[k]
+                C = t1 - t0
                 st = torch.cuda.current_stream(dev)
                 _stats_window(out, stats, t0, t1, st.cuda_stream)
+                pre = F.linear(U[:, t0:t1].reshape(B * C, 2 * H), Wd[:, :2 * H], bd)
                 with torch.enable_grad():
                     ay_leaf = ay[:, t0:t1].detach().requires_grad_(True)
                     r = read.query_bank_retrieved(
@@ -236,12 +255,32 @@ class _PipelinedScanRead(torch.autograd.Function):
                         gather=gather)
                 rd = r.detach().to(dt)
                 retr[:, t0:t1].copy_(rd)
-                # The projection as the training path evaluates it (three products in the
-                # same order, so the output rounds the same); its graph is dropped at once.
-                with torch.enable_grad():
-                    sh = read.short_read.project(U[:, t0:t1, :H], U[:, t0:t1, H:], rd)
-                short[:, t0:t1].copy_(sh.detach())
+                sh = torch.addmm(pre, rd.reshape(B * C, H), Wd[:, 2 * H:].t())
+                short[:, t0:t1].copy_(sh.view(B, C, H))
                 return r, ay_leaf
+
+            # The long channel window by window, each window its own graph with leaves on its
+            # write and plasticity rows and on the recurrent state it starts from (the state
+            # the previous window ends in), so that the backward can walk the windows one
+            # at a time: per window (long rows, final state, initial-state leaves or None,
+            # write leaf, plasticity leaf).
+            longs = []
+            carried = None
+
+            def long_window(k: int) -> None:
+                nonlocal carried
+                t0, t1 = bounds[k]
+                with torch.enable_grad():
+                    # Contiguous window copies (the scan reads them so in any case), kept
+                    # for the backward.
+                    wk = w[:, t0:t1].contiguous().requires_grad_(True)
+                    pk = pl[:, t0:t1].contiguous().requires_grad_(True)
+                    init = (None if carried is None
+                            else tuple(x.detach().requires_grad_(True) for x in carried))
+                    lk, carried = read._long_scan_from_state(
+                        wk, pk, None, initial_state=init, return_final_state=True)
+                long_out[:, t0:t1].copy_(lk.detach())
+                longs.append((lk, carried, init, wk, pk))
 
             chunks = []
             with _parameters_as(read, param_leaves):
@@ -249,22 +288,25 @@ class _PipelinedScanRead(torch.autograd.Function):
                     for k in range(K - 1):
                         R.wait_event(scan_done[k])
                         chunks.append(read_chunk(k))
-                    r_chunks = torch.cuda.Event()
-                    r_chunks.record(R)
-                    # The long channel over the whole sequence, beside the last chunk's read.
+                        if k == K - 2:
+                            r_chunks = torch.cuda.Event()
+                            r_chunks.record(R)
+                        long_window(k)
+                    # The last window's long channel beside the last chunk's read.
                     R.wait_event(scan_done[K - 1])
-                    with torch.enable_grad():
-                        long = read._long_scan(w_leaf, p_leaf, None)
+                    long_window(K - 1)
                     r_long = torch.cuda.Event()
                     r_long.record(R)
                 M.wait_event(scan_done[K - 1])
                 M.wait_event(r_chunks)
                 chunks.append(read_chunk(K - 1))
                 M.wait_event(r_long)
-                long_leaf = long.detach().requires_grad_(True)
+                long_leaf = long_out.detach().requires_grad_(True)
                 with torch.enable_grad():
                     read_out = ops.direct.read_output(short_leaf, long_leaf, read.long_gain)
             M.wait_stream(S)
+        _check_scans(S, fwd_calls, "core scan forward")
+        ambient.wait_stream(S)
         ambient.wait_stream(M)
         read_out.record_stream(ambient)
         del keep
@@ -272,20 +314,20 @@ class _PipelinedScanRead(torch.autograd.Function):
         ctx.read, ctx.chunk, ctx.names = read, chunk, names
         ctx.bounds = bounds
         ctx.meta = [(x.dtype, tuple(x.shape)) for x in (Wx, Wgx, *core_in)]
-        ctx.graph = (chunks, read_out, long, w_leaf, p_leaf, stats_leaf, short_leaf, long_leaf,
+        ctx.graph = (chunks, read_out, longs, w_leaf, stats_leaf, short_leaf, long_leaf,
                      param_leaves, sink)
         ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, starts, retr, out.U, *out.tapes)
         ctx.set_materialize_grads(False)
-        return U, read_out.detach()
+        return U[..., :H], U[..., H:], read_out.detach()
 
     @staticmethod
-    def backward(ctx, gU_out, g_read):
+    def backward(ctx, g_y, g_budget, g_read):
         saved = ctx.saved_tensors
         Wx, Wgx, Ug, A = saved[:4]
         vecs, scal = saved[4:20], saved[20:23]
         starts, retr = saved[23], saved[24]
         fwd_out = chunked._Tapes(None, 0, 0, 0, existing=saved[25:33])
-        (chunks, read_out, long, w_leaf, p_leaf, stats_leaf, short_leaf, long_leaf, param_leaves,
+        (chunks, read_out, longs, w_leaf, stats_leaf, short_leaf, long_leaf, param_leaves,
          sink) = ctx.graph
         read = ctx.read
         B, T, H = Wx.shape
@@ -306,42 +348,83 @@ class _PipelinedScanRead(torch.autograd.Function):
         bias = param_leaves["short_read.out.bias"]
         Wd = W.detach().to(dt)
         # Tape gradients of the reverse scans, full length, filled window by window.
-        gU = (torch.zeros((B, T, 2 * H), device=dev, dtype=dt) if gU_out is None
-              else gU_out.to(dt).contiguous().clone())
-        g_nov, g_ay, g_e, g_c, g_r = (torch.empty((B, T, H), device=dev, dtype=dt)
+        gU = torch.empty((B, T, 2 * H), device=dev, dtype=dt)
+        g_halves = [None if g is None else g.to(dt) for g in (g_y, g_budget)]
+        g_nov, g_p, g_ay, g_e, g_c = (torch.empty((B, T, H), device=dev, dtype=dt)
                                       for _ in range(5))
         gWx, gWgx, day = (torch.empty((B, T, H), device=dev, dtype=dt) for _ in range(3))
         g_read = torch.zeros_like(read_out) if g_read is None else g_read.contiguous()
+        # dL/dUg and dL/dA summed over windows as their reverse scans finish.
+        gUg_sum, gA_sum = (torch.zeros((H, H), device=dev, dtype=torch.float32) for _ in range(2))
         for st in (M, S, R):
             st.wait_stream(ambient)
 
+        def projection_grads(g_short3: Tensor, k: int) -> Tensor:
+            # out(cat[y, budget, retrieved]) over query chunk k: one product gives the
+            # gradients of all three inputs; y's and budget's plus their own upstream
+            # gradients fill U's gradient window, the retrieved rows' gradient is returned.
+            t0, t1 = bounds[k]
+            C = t1 - t0
+            prod = torch.mm(g_short3[:, t0:t1].reshape(B * C, H), Wd)
+            for i, g_in in enumerate(g_halves):
+                g_proj = prod[:, i * H:(i + 1) * H].view(B, C, H)
+                dst = gU[:, t0:t1, i * H:(i + 1) * H]
+                if g_in is None:
+                    dst.copy_(g_proj)
+                else:
+                    torch.add(g_in[:, t0:t1], g_proj, out=dst)
+            return prod[:, 2 * H:].view(B, C, H)
+
+        def core_weight_grads(t0: int, t1: int) -> None:
+            # dL/dUg and dL/dA over window [t0, t1): the reverse scan's dWgx and da_y rows
+            # times the trajectory's y rows, summed over the window's rows.
+            y = fwd_out.U[:, t0:t1, :H].reshape(-1, H)
+            gUg_sum.add_(gWgx[:, t0:t1].reshape(-1, H).t() @ y)
+            gA_sum.add_(day[:, t0:t1].reshape(-1, H).t() @ y)
+
+        state_grad: list = [None]
+
+        def long_backward(k: int) -> None:
+            # Window k of the long channel: its rows' gradient plus the gradient of the state
+            # it ends in (from window k + 1's backward); leaves the gradient of the state it
+            # starts from for window k - 1.
+            lk, fin, init, wk, pk = longs[k]
+            t0, t1 = bounds[k]
+            outs, grads = [lk], [g_long[:, t0:t1]]
+            for f, g in zip(fin, state_grad[0] or ()):
+                if g is not None:
+                    outs.append(f)
+                    grads.append(g)
+            torch.autograd.backward(outs, grads, inputs=[wk, pk, *trainable, *(init or ())])
+            state_grad[0] = None if init is None else [x.grad for x in init]
+
         with torch.cuda.stream(M):
-            # The read output's backward, then the long channel's on the read half beside
-            # the projection and last chunk's read backward on the whole device.
+            # The read output's backward; then the long channel's last windows on the read
+            # half (enqueued first, so that its kernels hold their CUs) beside the last
+            # chunk's projection and read backward on the whole device.
             torch.autograd.backward([read_out], [g_read], inputs=[short_leaf, long_leaf, *trainable])
-            g_short = short_leaf.grad.reshape(B * T, H).to(dt)
+            g_short3 = short_leaf.grad.to(dt)
+            g_long = long_leaf.grad
             head = torch.cuda.Event()
             head.record(M)
             R.wait_event(head)
+            head_windows = min(K, 2) if g_long is not None else 0
             with torch.cuda.stream(R):
-                if long_leaf.grad is not None:
-                    torch.autograd.backward([long], [long_leaf.grad],
-                                            inputs=[w_leaf, p_leaf, *trainable])
-            # out(cat[y, budget, retrieved]): gradients of its inputs (the [y, budget] half
-            # straight into U's layout).
-            gU.view(B * T, 2 * H).addmm_(g_short, Wd[:, :2 * H])
-            torch.mm(g_short, Wd[:, 2 * H:], out=g_r.view(B * T, H))
+                for k in range(K - 1, K - 1 - head_windows, -1):
+                    long_backward(k)
 
             carry = [None, None, None]
             bws = []
+            scan_back: list[Optional[torch.cuda.Event]] = [None] * K
             for k in range(K - 1, -1, -1):
                 t0, t1 = bounds[k]
                 r, ay_leaf = chunks[k]
                 st = M if k == K - 1 else R
                 with torch.cuda.stream(st):
+                    g_r = projection_grads(g_short3, k)
                     # w_leaf is listed so that the engine runs the gather's backward, whose
                     # gradient goes to the sink (it returns none for w_leaf itself).
-                    torch.autograd.backward([r], [g_r[:, t0:t1]],
+                    torch.autograd.backward([r], [g_r],
                                             inputs=[ay_leaf, w_leaf, stats_leaf, *trainable])
                     if ay_leaf.grad is not None:
                         g_ay[:, t0:t1].copy_(ay_leaf.grad)
@@ -352,17 +435,27 @@ class _PipelinedScanRead(torch.autograd.Function):
                     done.record(st)
                     R.wait_event(done)
                 with torch.cuda.stream(R):
-                    if k == K - 1 and w_leaf.grad is not None:
-                        sink.add_(w_leaf.grad)  # the long channel's write gradient
-                    if p_leaf.grad is None:
-                        p_leaf.grad = torch.zeros_like(p_leaf)
-                    g_p = p_leaf.grad
+                    if g_long is not None and k < K - head_windows:
+                        long_backward(k)
+                    # Window k of the write gradient is complete (only query chunks >= k
+                    # read it): the long channel's share joins it.
+                    wk, pk = longs[k][3:]
+                    if wk.grad is not None:
+                        sink[:, t0:t1].add_(wk.grad)
+                    if pk.grad is None:
+                        g_p[:, t0:t1].zero_()
+                    else:
+                        g_p[:, t0:t1].copy_(pk.grad)
                     gs = stats_leaf.grad
                     gs = torch.zeros_like(stats_leaf) if gs is None else gs.contiguous()
                     _stats_bwd_window(gs, (g_nov, None, g_e, g_c), False, t0, t1, R.cuda_stream)
                     _stats_bwd_window(gs, (None, g_p, None, None), True, t0, t1, R.cuda_stream)
                     tapes_ready = torch.cuda.Event()
                     tapes_ready.record(R)
+                    # The reverse scan of window k + 2 finished before that of k + 1 began.
+                    if k + 2 < K:
+                        R.wait_event(scan_back[k + 2])
+                        core_weight_grads(*bounds[k + 2])
                 with torch.cuda.stream(S):
                     S.wait_event(tapes_ready)
                     up = [gU, g_nov, g_p, g_ay, sink, g_e, g_c]
@@ -372,26 +465,32 @@ class _PipelinedScanRead(torch.autograd.Function):
                     tk = ops.KernelTimer.begin("core_scan_bwd", Wx)
                     bw.launch(S)
                     ops.KernelTimer.end(tk)
-                    ops._record_error_word(bw.ws, "core scan backward")
                     bws.append(bw)
                     carry = bw.g0
+                    ev = torch.cuda.Event()
+                    ev.record(S)
+                    scan_back[k] = ev
             with torch.cuda.stream(R):
                 # The projection's weight gradients, beside the last reverse scan.
                 U2 = fwd_out.U.reshape(B * T, 2 * H)
+                g_short = g_short3.reshape(B * T, H)
                 gw = torch.cat((g_short.t() @ U2, g_short.t() @ retr.reshape(B * T, H)), dim=1)
                 W.grad = gw.to(W.dtype)
                 bias.grad = g_short.float().sum(0).to(bias.dtype)
+                if K > 1:
+                    R.wait_event(scan_back[1])
+                    core_weight_grads(*bounds[1])
             M.wait_stream(S)
             M.wait_stream(R)
+            core_weight_grads(*bounds[0])
             gvec = torch.stack([bw.part_vec.sum(0) for bw in bws]).sum(0)
             gscal = torch.stack([bw.part_scal.sum(0) for bw in bws]).sum(0)
-            y = fwd_out.U.reshape(B * T, 2 * H)[:, :H]
-            gUg = (gWgx.view(B * T, H).t() @ y).float()
-            gA = (day.view(B * T, H).t() @ y).float()
-            core = [gWx, gWgx, gUg, gA, *[gvec[i] for i in range(16)],
+            core = [gWx, gWgx, gUg_sum, gA_sum, *[gvec[i] for i in range(16)],
                     *[gscal[i] for i in range(3)]]
             core = [g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(core, ctx.meta)]
             grads = [p.grad for p in pleaves]
+        _check_scans(S, bws, "core scan backward")
+        ambient.wait_stream(S)
         ambient.wait_stream(M)
         for g in (*core, *grads):
             if g is not None:
@@ -402,12 +501,14 @@ class _PipelinedScanRead(torch.autograd.Function):
 
 
 def pipelined_scan_read(read, chunk: int, Wx: Tensor, Wgx: Tensor,
-                        core_params: Sequence[Tensor]) -> tuple[Tensor, Tensor]:
-    """(U [B, T, 2H], read output [B, T, H]) of a seq block's core scan over ``chunk``-step
-    windows from the zero state and its read, with the read of query chunk k overlapping
-    the scan of chunk k + 1 (forward) and the reverse scan of chunk k overlapping the read
-    backward of chunk k - 1 (backward). ``core_params``: the 21 parameter inputs of
-    dabsn::core_scan_batched (``DABSNCore.scan_inputs()``)."""
+                        core_params: Sequence[Tensor]) -> tuple[Tensor, Tensor, Tensor]:
+    """(y, budget, read output), each [B, T, H], of a seq block's core scan over
+    ``chunk``-step windows from the zero state and its read, with the read of query chunk k
+    overlapping the scan of chunk k + 1 (forward) and the reverse scan of chunk k
+    overlapping the read backward of chunk k - 1 (backward). y and budget are the two halves
+    of the trajectory U [B, T, 2H] (views), returned apart so that a caller that uses one
+    of them hands back no gradient for the other. ``core_params``: the 21 parameter inputs
+    of dabsn::core_scan_batched (``DABSNCore.scan_inputs()``)."""
     if read.read_geometry != "seq":
         raise ValueError("the pipelined scan + read is the seq geometry's (causal banks)")
     names = tuple(n for n, _ in read.named_parameters())

@@ -124,9 +124,8 @@ class DABSNBlock(nn.Module):
             # Training on the device with block chunking: the read of query chunk k runs
             # beside the scan of chunk k + 1 on the other half of the device.
             Wx, Wgx = self.core.projections(inputs)
-            trajectory, read = pipeline.pipelined_scan_read(self.read, chunk_t, Wx, Wgx,
-                                                            self.core.scan_inputs())
-            y = trajectory.split(self.state_dim, dim=-1)[0]
+            y, _, read = pipeline.pipelined_scan_read(self.read, chunk_t, Wx, Wgx,
+                                                      self.core.scan_inputs())
         else:
             trajectory, novelty, plasticity, expression, write, energy, saturation = (
                 self.core_tapes(inputs))

@@ -4,8 +4,8 @@ one piece after the other (time-chunked core scan, then the whole-sequence read)
 The pipeline reads each query chunk against the bank that ends with it (read.py:650-838,
 the same rows as the whole-sequence read) and sums the tape gradients chunk by chunk, so
 only summation orders differ:
-  * the trajectory U: bit-identical (the same scan kernels, launched plainly on a CU-masked
-    stream instead of cooperatively);
+  * the trajectory halves y and budget: bit-identical (the same scan kernels, launched
+    plainly on a CU-masked stream instead of cooperatively);
   * fp32: read output and every gradient (input projections, core and read parameters)
     normwise 1e-5 (scalar parameter gradients that sum O(B*T*N) terms 1e-4);
   * bf16 at state width 2048 (the config-4 kernel instances): read output and gradients
@@ -15,12 +15,12 @@ only summation orders differ:
     sum many cancelling terms move by up to a few 1e-2 under bf16 rounding in either
     schedule);
   * dense banks (the successor fold) and partially admitted ones (no fold, a bank width
-    that grows chunk by chunk); a DABSNBlock with block chunking, pipelined or not.
+    that grows chunk by chunk); losses with and without budget (a block mixes only y into
+    its output); a DABSNBlock with block chunking, pipelined or not.
 """
 
 from __future__ import annotations
 
-import os
 
 import pytest
 import torch
@@ -46,23 +46,26 @@ def _sequential(core, read, chunk, Wx, Wgx):
     outs = chunked_core_scan(chunk, Wx, Wgx, *core.scan_inputs(), z, torch.ones_like(z), z.clone())
     U, nov, p, ay, w, e, c = outs[:7]
     y, budget = U.split(H, dim=-1)
-    return U, read(y, budget, ay, w, nov, p, e, c)
+    return y, budget, read(y, budget, ay, w, nov, p, e, c)
 
 
-def _run(fn, core, read, x, gU, gr, dtype):
+def _run(fn, core, read, x, ups, dtype):
+    """Outputs (y, budget, read) of ``fn`` and every gradient of a backward from the
+    upstream gradients ``ups`` (None: that output takes no part in the loss)."""
     core.zero_grad(set_to_none=True)
     read.zero_grad(set_to_none=True)
     xl = x.clone().requires_grad_(True)
     with torch.autocast("cuda", dtype=dtype, enabled=dtype != torch.float32):
         Wx, Wgx = core.projections(xl)
-        U, r = fn(core, read, Wx, Wgx)
-    torch.autograd.backward([U, r], [gU.to(U.dtype), gr.to(r.dtype)])
+        outs = fn(core, read, Wx, Wgx)
+    pairs = [(o, u.to(o.dtype)) for o, u in zip(outs, ups) if u is not None]
+    torch.autograd.backward([o for o, _ in pairs], [u for _, u in pairs])
     grads = {"x": xl.grad}
     for prefix, m in (("core", core), ("read", read)):
         for n, p in m.named_parameters():
             if p.grad is not None:
                 grads[f"{prefix}.{n}"] = p.grad.detach().clone()
-    return U.detach(), r.detach(), grads, read.last_n_max
+    return [o.detach() for o in outs], grads, read.last_n_max
 
 
 def _rel(a, b, fro, floor=1e-30):
@@ -79,22 +82,23 @@ def _floor(grads):
     return 1e-3 * max(float(g.abs().max()) for g in grads.values())
 
 
-@pytest.mark.parametrize("dtype,B,T,H,chunk,window,ref32", [
-    (torch.float32, 3, 96, 64, 32, 50.0, False),
-    (torch.float32, 3, 96, 64, 32, 0.3, False),
-    (torch.float32, 2, 100, 48, 24, 50.0, False),
-    (torch.bfloat16, 16, 512, 2048, 128, 50.0, False),
-    (torch.bfloat16, 16, 384, 2048, 128, 0.3, False),
-    (torch.bfloat16, 16, 512, 512, 128, 50.0, True),
+@pytest.mark.parametrize("dtype,B,T,H,chunk,window,ref32,budget_grad", [
+    (torch.float32, 3, 96, 64, 32, 50.0, False, True),
+    (torch.float32, 3, 96, 64, 32, 0.3, False, False),
+    (torch.float32, 2, 100, 48, 24, 50.0, False, True),
+    (torch.bfloat16, 16, 512, 2048, 128, 50.0, False, True),
+    (torch.bfloat16, 16, 384, 2048, 128, 0.3, False, False),
+    (torch.bfloat16, 16, 512, 512, 128, 50.0, True, True),
 ])
 def test_pipelined_scan_read_matches_sequential(cuda_device, dtype, B, T, H, chunk, window,
-                                                ref32):
+                                                ref32, budget_grad):
     din = 32
     core, read = _modules(11 + T, din, H, window, cuda_device)
     g = torch.Generator().manual_seed(12)
     x = torch.randn(B, T, din, generator=g).to(cuda_device)
-    gU = (torch.randn(B, T, 2 * H, generator=g) * 1e-2).to(cuda_device)
+    gy, gb = ((torch.randn(B, T, H, generator=g) * 1e-2).to(cuda_device) for _ in range(2))
     gr = torch.randn(B, T, H, generator=g).to(cuda_device)
+    ups = (gy, gb if budget_grad else None, gr)
 
     def piped(c, r, Wx, Wgx):
         return pipeline.pipelined_scan_read(r, chunk, Wx, Wgx, c.scan_inputs())
@@ -102,10 +106,10 @@ def test_pipelined_scan_read_matches_sequential(cuda_device, dtype, B, T, H, chu
     def seq(c, r, Wx, Wgx):
         return _sequential(c, r, chunk, Wx, Wgx)
 
-    U1, r1, g1, n1 = _run(piped, core, read, x, gU, gr, dtype)
-    U0, r0, g0, n0 = _run(seq, core, read, x, gU, gr, dtype)
+    (y1, b1, r1), g1, n1 = _run(piped, core, read, x, ups, dtype)
+    (y0, b0, r0), g0, n0 = _run(seq, core, read, x, ups, dtype)
     assert n1 == n0
-    assert torch.equal(U1, U0), "trajectory"
+    assert torch.equal(y1, y0) and torch.equal(b1, b0), "trajectory"
     fro = dtype != torch.float32
     tol = 2e-2 if fro else 1e-5
     assert _rel(r1, r0, fro) <= tol, f"read output {_rel(r1, r0, fro):.3e}"
@@ -119,7 +123,7 @@ def test_pipelined_scan_read_matches_sequential(cuda_device, dtype, B, T, H, chu
             assert err <= limit, f"gradient {n}: {err:.3e}"
             worst = max(worst, (n, err), key=lambda v: v[1])
     else:
-        _, _, gf, _ = _run(seq, core, read, x, gU, gr, torch.float32)
+        _, gf, _ = _run(seq, core, read, x, ups, torch.float32)
         floor = _floor(gf)
         for n in gf:
             err = _rel(g1[n], gf[n], True, floor)
