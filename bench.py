@@ -2,10 +2,11 @@
 
 Workload ("config 4"): one seq DABSN layer, state width 2048,
 read/hidden width 4096, vocabulary 32,000, batch 16, T = 4096, bf16, block chunking
-enabled (chunk 1024, checkpointed: each chunk's forward scan is recomputed in the
-backward). One step = forward + backward of the scan+read region: the chunked core scan
+enabled (chunk 1024; the chunks' tapes are kept for the reverse scans instead of
+recomputed). One step = forward + backward of the scan+read region: the chunked core scan
 (op dabsn::core_scan_batched), read statistics, admitted-slot selection, bank gather,
-three-way read, read output projection and the long-memory scan, from input projections
+three-way read, read output projection and the long-memory scan, pipelined over the
+chunks on the two halves of the device (--no-pipeline: one after the other), from input projections
 Wx = W x, Wgx = Wg x that are already resident in HBM (the input projections are plain
 GEMMs timed separately, as the metric excludes them). Synthetic data: random token ids
 through a random embedding, random-initialised weights.

@@ -322,6 +322,11 @@ class _PipelinedScanRead(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_y, g_budget, g_read):
+        if ctx.graph is None:
+            raise RuntimeError(
+                "pipelined scan + read: the backward runs once per forward (it walks and frees "
+                "the per-chunk read graphs); DABSN_PIPELINE=0 gives the block a backward that "
+                "can run again on a retained graph")
         saved = ctx.saved_tensors
         Wx, Wgx, Ug, A = saved[:4]
         vecs, scal = saved[4:20], saved[20:23]

@@ -12,6 +12,7 @@ launches a plain elementwise copy of known size (reads and writes ``mib`` MiB on
 launch), so the same counters read on it give the scale between counter units and bytes.
 
     python -m dabsn_amd.profiling <results.db> [--top N] [--match REGEX] [--tail MARKER:N]
+    python -m dabsn_amd.profiling <results.db> --categories STEPS
     python -m dabsn_amd.profiling --pmc-summary <dir> [--match REGEX]
     python -m dabsn_amd.profiling --copy-probe <MiB>
     python -m dabsn_amd.profiling --pmc-json <out.json> --fetch <dir> --write <dir> \
@@ -60,6 +61,35 @@ def kernel_stats(db_path: str, match: str | None = None,
                     "max_ms": max(durations) / 1e6})
     out.sort(key=lambda r: -r["total_ms"])
     return out
+
+
+# Kernel categories of the scan+read step (first matching rule wins).
+CATEGORIES = (
+    ("core reverse scans", r"core_bwd_kernel"),
+    ("core forward scans", r"core_fwd_kernel"),
+    ("read GEMMs (gemm.hpp)", r"dabsn::gemm::gemm_kernel"),
+    ("read row kernels (softmax, grad rows/tiles, reductions, ranges)",
+     r"read3::(softmax_fwd|grad_rows|grad_tile|reduce_|ranges)"),
+    ("read transposes", r"transpose_kernel"),
+    ("hipBLASLt (read output projection, grad [Ug;A])", r"^(Custom_)?Cijk|^_UIOFGRO|^AV_"),
+    ("long scan fwd+bwd", r"longmem::"),
+    ("read glue (stats, normalise, select, gather, slot glue, read output)",
+     r"dabsn::glue::|glue_|read_out|means_glue"),
+    ("torch elementwise, copies, fills, reductions", r"at::native|rocclr"),
+)
+
+
+def categories(stats: list[dict[str, object]], steps: int) -> str:
+    """Milliseconds per step by kernel category (``CATEGORIES``), from ``kernel_stats``."""
+    total: dict[str, float] = defaultdict(float)
+    for r in stats:
+        cat = next((c for c, rx in CATEGORIES if re.search(rx, r["name"])), "other")
+        total[cat] += r["total_ms"] / steps
+    lines = ["| category | ms / step |", "|---|---|"]
+    for cat, ms in sorted(total.items(), key=lambda kv: -kv[1]):
+        lines.append(f"| {cat} | {ms:.2f} |")
+    lines.append(f"| **sum of kernel durations** | **{sum(total.values()):.2f}** |")
+    return "\n".join(lines)
 
 
 def format_table(stats: list[dict[str, object]], top: int) -> str:
@@ -156,6 +186,8 @@ def main() -> None:
     p.add_argument("--match", default=None)
     p.add_argument("--tail", default=None, metavar="MARKER:N",
                    help="only the last N repetitions of a step launching MARKER once")
+    p.add_argument("--categories", type=int, default=None, metavar="STEPS",
+                   help="milliseconds per step by kernel category, the trace holding STEPS steps")
     p.add_argument("--pmc-summary", default=None)
     p.add_argument("--copy-probe", type=int, default=None)
     p.add_argument("--pmc-json", default=None)
@@ -185,7 +217,11 @@ def main() -> None:
         if args.tail:
             marker, _, n = args.tail.rpartition(":")
             tail = (marker, int(n))
-        print(format_table(kernel_stats(args.db, args.match, tail), args.top))
+        stats = kernel_stats(args.db, args.match, tail)
+        if args.categories:
+            print(categories(stats, args.categories))
+        else:
+            print(format_table(stats, args.top))
 
 
 if __name__ == "__main__":
