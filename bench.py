@@ -134,7 +134,10 @@ def build_workload(args, device, dtype, batch, seq):
     Wx = Wx.detach().requires_grad_(True)
     Wgx = Wgx.detach().requires_grad_(True)
     gy = (torch.randn(batch, seq, args.state, generator=g) * 1e-3).to(device=device, dtype=dtype)
-    gr = (torch.randn(batch, seq, args.state, generator=g) * 1e-3).to(device=device, dtype=dtype)
+    # The read output is fp32 under the reference's type promotion (bf16 projection plus the
+    # fp32 gain times the long channel, read.py:435-438), so its upstream gradient is too.
+    gr = (torch.randn(batch, seq, args.state, generator=g) * 1e-3).to(device=device,
+                                                                      dtype=torch.float32)
     return model, Wx, Wgx, gy, gr
 
 
@@ -144,7 +147,7 @@ def step(model, Wx, Wgx, gy, gr, device_type, dtype):
     Wgx.grad = None
     with torch.autocast(device_type, dtype=dtype, enabled=dtype != torch.float32):
         y, read = model(Wx, Wgx)
-    torch.autograd.backward([y, read.to(dtype)], [gy, gr])
+    torch.autograd.backward([y, read], [gy, gr if gr.dtype == read.dtype else gr.to(read.dtype)])
 
 
 PMC_FILE = os.path.join(ROOT, "profiles", "core_scan_config4_pmc.json")

@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _lock = threading.Lock()
 _lib = None
@@ -108,6 +108,8 @@ _SIGNATURES = {
     "dabsn_hip_admit_step": (
         [i32, i64, i64, i64, i64, vp, i64, PTR8, vp, i32, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_fold": ([i64, i64, i64, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_bank_width": ([i64, i64, vp, vp, i32, vp, vp], i32),
+    "dabsn_hip_bank_slots": ([i64, i64, i64, vp, vp, i64, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_glue_slots": ([i64, i64, i64, i64, vp, vp, i64, PTR8, i32, vp, vp, vp, vp], i32),
     "dabsn_hip_glue_slots_partials": ([i64, i64], sz),
     "dabsn_hip_glue_slots_bwd": (

@@ -343,6 +343,56 @@ __global__ void __launch_bounds__(256) fold_kernel(int T, int N, const int64_t* 
     __hip_atomic_fetch_or(unfoldable, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The bank width a read needs and whether its successor rows fold (one host read of two
+// int64 values instead of a reduction, a flag kernel and their stacking): out[0] = the
+// largest admitted count over the rows, out[1] = 1 when some admitted slot's successor is
+// neither the next slot's position nor its own (fold_kernel's code 2). out is zeroed first.
+__global__ void __launch_bounds__(256) width_kernel(int T, const int64_t* order,
+                                                    const int64_t* counts, int check_fold,
+                                                    unsigned long long* out) {
+  const int b = blockIdx.y;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const int64_t cnt = counts[b];
+  if (j == 0) atomicMax(out, static_cast<unsigned long long>(cnt > 0 ? cnt : 0));
+  if (!check_fold) return;
+  bool bad = false;
+  if (j < T && j < cnt) {
+    const int64_t* ob = order + static_cast<size_t>(b) * T;
+    const int64_t i = ob[j];
+    const int64_t nx = i + 1 < T ? i + 1 : T - 1;
+    bad = nx != i && !(j + 1 < cnt && ob[j + 1] == nx);
+  }
+  if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(out + 1, 1ull);
+}
+
+// The slot arrays of a read of width N from a bank_select result (read.py:233-239 after the
+// host read of the width): idx = order[:, :N], valid = j < max(count, 1), next_idx =
+// min(idx + 1, T - 1), read_idx = idx - query_start and, optionally, the fold codes of
+// fold_kernel. One thread per slot.
+__global__ void __launch_bounds__(256) slots_kernel(int T, int N, int64_t query_start,
+                                                    const int64_t* order, const int64_t* counts,
+                                                    int64_t* idx, uint8_t* valid,
+                                                    int64_t* next_idx, int64_t* read_idx,
+                                                    int8_t* codes) {
+  const int b = blockIdx.y;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= N) return;
+  const int64_t cnt = counts[b];
+  const int64_t* ob = order + static_cast<size_t>(b) * T;
+  const int64_t i = ob[j];
+  const int64_t nx = i + 1 < T ? i + 1 : T - 1;
+  const size_t o = static_cast<size_t>(b) * N + j;
+  idx[o] = i;
+  valid[o] = j < (cnt > 1 ? cnt : 1) ? 1 : 0;
+  next_idx[o] = nx;
+  read_idx[o] = i - query_start;
+  if (codes) {
+    int code = 0;
+    if (j < cnt) code = nx == i ? 0 : (j + 1 < cnt && ob[j + 1] == nx ? 1 : 2);
+    codes[o] = static_cast<int8_t>(code);
+  }
+}
+
 }  // namespace glue
 }  // namespace dabsn
 
@@ -766,6 +816,35 @@ int dabsn_hip_bank_fold(int64_t B, int64_t T, int64_t N, const int64_t* order,
   if (width == 0) return DABSN_OK;
   hipLaunchKernelGGL(fold_kernel, dim3(blocks_for(width, 256), (unsigned)B), dim3(256), 0, stream,
                      (int)T, (int)N, order, counts, codes, unfoldable);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_bank_width(int64_t B, int64_t T, const int64_t* order, const int64_t* counts,
+                         int check_fold, int64_t* out, hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && B < 65536 && T > 0 && T < (1ll << 31), "bank_width: bad shape");
+  DABSN_REQUIRE(counts && out && (order || !check_fold), "bank_width: null pointer");
+  const int rc = dabsn_hip_zero(out, 2 * sizeof(int64_t), stream);
+  if (rc != DABSN_OK) return rc;
+  const unsigned xb = check_fold ? blocks_for(T, 256) : 1u;
+  hipLaunchKernelGGL(width_kernel, dim3(xb, (unsigned)B), dim3(256), 0, stream, (int)T, order,
+                     counts, check_fold ? 1 : 0, reinterpret_cast<unsigned long long*>(out));
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_bank_slots(int64_t B, int64_t T, int64_t N, const int64_t* order,
+                         const int64_t* counts, int64_t query_start, int64_t* idx,
+                         uint8_t* valid, int64_t* next_idx, int64_t* read_idx, int8_t* codes,
+                         hipStream_t stream) {
+  DABSN_REQUIRE(B > 0 && B < 65536 && T > 0 && N >= 0 && N <= T && T < (1ll << 31),
+                "bank_slots: bad shape");
+  if (N == 0) return DABSN_OK;
+  DABSN_REQUIRE(order && counts && idx && valid && next_idx && read_idx,
+                "bank_slots: null pointer");
+  hipLaunchKernelGGL(slots_kernel, dim3(blocks_for(N, 256), (unsigned)B), dim3(256), 0, stream,
+                     (int)T, (int)N, query_start, order, counts, idx, valid, next_idx, read_idx,
+                     codes);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }

@@ -1398,6 +1398,40 @@ def bank_fold(order: Tensor, counts: Tensor, width: Optional[int] = None):
     return codes
 
 
+def bank_width(order: Tensor, counts: Tensor, check_fold: bool) -> Tensor:
+    """[largest admitted count, unfoldable flag] of a ``bank_select`` result as one int64
+    device tensor of two values (``dabsn_hip_bank_width``; the flag is 0 without
+    ``check_fold``), for one host read."""
+    lib = _lib.load()
+    B, T = order.shape
+    o, c = order.contiguous(), counts.contiguous()
+    out = torch.empty((2,), device=order.device, dtype=torch.int64)
+    _lib.check(lib.dabsn_hip_bank_width(B, T, _p(o), _p(c), 1 if check_fold else 0, _p(out),
+                                        _stream(o)), "bank width")
+    return out
+
+
+def bank_slots(order: Tensor, counts: Tensor, width: int, query_start: int,
+               fold: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Optional[Tensor]]:
+    """(idx, valid, next_idx, read_idx, fold codes or None), each [B, width], of a read of
+    ``width`` slots from a ``bank_select`` result in one launch (``dabsn_hip_bank_slots``):
+    idx = order[:, :width], valid = slot < max(count, 1), next_idx = min(idx + 1, T - 1),
+    read_idx = idx - query_start."""
+    lib = _lib.load()
+    B, T = order.shape
+    N = int(width)
+    o, c = order.contiguous(), counts.contiguous()
+    dev = order.device
+    idx, next_idx, read_idx = (torch.empty((B, N), device=dev, dtype=torch.int64)
+                               for _ in range(3))
+    valid = torch.empty((B, N), device=dev, dtype=torch.bool)
+    codes = torch.empty((B, N), device=dev, dtype=torch.int8) if fold else None
+    _lib.check(lib.dabsn_hip_bank_slots(B, T, N, _p(o), _p(c), int(query_start), _p(idx),
+                                        _p(valid), _p(next_idx), _p(read_idx), _p(codes),
+                                        _stream(o)), "bank slots")
+    return idx, valid, next_idx, read_idx, codes
+
+
 # ---------------------------------------------------------------------------
 # Three-way admitted read (compact ABI)
 # ---------------------------------------------------------------------------

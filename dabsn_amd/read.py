@@ -184,18 +184,32 @@ class DABSNRead(nn.Module):
 
     # ---- selection ------------------------------------------------------------
     def _select(self, admission: Tensor, length: int, width: int | None = None,
-                want_fold: bool = False):
-        """Slot selection: (n_max, idx, valid, next_idx, rank, fold). ``fold`` is the
-        successor-fold code array [B, n_max] when ``want_fold`` and every admitted slot's next
-        position is a bank row (``ops.bank_fold``), else None; the check rides on the host
-        sync of the bank width."""
+                want_fold: bool = False, query_start: int = 0):
+        """Slot selection: (n_max, idx, valid, next_idx, rank, fold, read_idx). ``fold`` is
+        the successor-fold code array [B, n_max] when ``want_fold`` and every admitted slot's
+        next position is a bank row (``ops.bank_fold``), else None; the check rides on the
+        host sync of the bank width. ``read_idx`` = idx - query_start. On the device the
+        width and fold flag come back in one read and the slot arrays in one launch, so
+        little is left to enqueue after the sync."""
         window = F.softplus(self.admit_window)
         # seq: floor from the causal prefix max; field / hybrid: the whole sequence's max
         # (read.py:185-191)
         whole = 0 if self.read_geometry == "seq" else 1
         order, counts, rank = ops.direct.bank_select(admission.detach(), window.detach(), whole)
         fold = None
-        if width or self._capture_bank_width:
+        fixed = width or self._capture_bank_width
+        if order.is_cuda:
+            if fixed:
+                # A fixed width needs no host sync; slots past a row's admitted count are
+                # masked out by `valid`.
+                n_max, bad = max(1, min(int(fixed), length)), True
+            else:
+                top, bad = ops.bank_width(order, counts, want_fold).tolist()  # as read.py:233
+                n_max = max(int(top), 1)
+            idx, valid, next_idx, read_idx, fold = ops.bank_slots(
+                order, counts, n_max, query_start, want_fold and not bad)
+            return n_max, idx, valid, next_idx, rank, fold, read_idx
+        if fixed:
             # A fixed width needs no host sync; slots past a row's admitted count are
             # masked out by `valid`.
             n_max = max(1, min(int(width or self._capture_bank_width), length))
@@ -210,7 +224,8 @@ class DABSNRead(nn.Module):
         idx = order[:, :n_max]
         valid = torch.arange(n_max, device=admission.device).unsqueeze(0) < counts.clamp_min(1).unsqueeze(1)
         next_idx = (idx + 1).clamp(max=length - 1)
-        return n_max, idx, valid, next_idx, rank, fold
+        read_idx = idx if query_start == 0 else idx - query_start
+        return n_max, idx, valid, next_idx, rank, fold, read_idx
 
     def _bank(self, glue, length: int, query_start: int, width: int | None = None,
               members: tuple[Tensor, Tensor] | None = None) -> dict[str, object]:
@@ -221,12 +236,13 @@ class DABSNRead(nn.Module):
         [B]) kept incrementally by a carried bank (inference): the selection is read from it
         instead of rerun over the bank."""
         fold = None
+        scale = self._scale()  # ahead of the selection's host sync
         if members is None:
             admission = glue.admission_for_select()
             # The successor fold serves the training read (gather + read under autograd).
             want_fold = torch.is_grad_enabled() and admission.is_cuda
-            n_max, idx, valid, next_idx, rank, fold = self._select(admission, length, width,
-                                                                   want_fold)
+            n_max, idx, valid, next_idx, rank, fold, read_idx = self._select(
+                admission, length, width, want_fold, query_start)
         else:
             slots, counts = members
             if width or self._capture_bank_width:
@@ -238,12 +254,12 @@ class DABSNRead(nn.Module):
                      < counts.clamp_min(1).unsqueeze(1))
             next_idx = (idx + 1).clamp(max=length - 1)
             rank = idx.new_empty((0,), dtype=torch.int32)  # the gather's backward only
+            read_idx = idx if query_start == 0 else idx - query_start
         cb, kb, adm, ck = glue.slots(idx)
         return {
             "n_max": n_max, "idx": idx, "valid": valid, "next_idx": next_idx, "rank": rank,
             "fold": fold, "cocktail": cb, "key_bias": kb, "admission": adm,
-            "query_cocktail": ck, "scale": self._scale(),
-            "read_idx": idx if query_start == 0 else idx - query_start,
+            "query_cocktail": ck, "scale": scale, "read_idx": read_idx,
         }
 
     def _scale(self, fp32: bool = False) -> Tensor:

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 12
+#define DABSN_HIP_ABI_VERSION 13
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -310,6 +310,23 @@ int dabsn_hip_admit_step(int mode, int64_t B, int64_t n, int64_t base, int64_t c
 int dabsn_hip_bank_fold(int64_t B, int64_t T, int64_t N, const int64_t* order,
                         const int64_t* counts, int8_t* codes, uint32_t* unfoldable,
                         hipStream_t stream);
+
+/* The width a read of a bank_select result needs (read.py:233: the host reads the largest
+ * admitted count) and, with check_fold, whether the successor fold applies: out[0] (int64) =
+ * max over rows of counts, out[1] = 1 when some admitted slot codes 2 in
+ * dabsn_hip_bank_fold's terms, else 0. order [B,T], counts [B] as bank_select returns them;
+ * order may be NULL without check_fold. One device read of out replaces the reduction, the
+ * flag and their stacking. */
+int dabsn_hip_bank_width(int64_t B, int64_t T, const int64_t* order, const int64_t* counts,
+                         int check_fold, int64_t* out, hipStream_t stream);
+/* The slot arrays of a read of width N <= T (read.py:233-239, 298-303) in one launch, all
+ * [B,N]: idx = order[:, :N] (int64), valid = j < max(counts, 1) (one byte, 0/1),
+ * next_idx = min(idx + 1, T - 1), read_idx = idx - query_start (int64) and, when codes is
+ * not NULL, the fold codes of dabsn_hip_bank_fold (int8). */
+int dabsn_hip_bank_slots(int64_t B, int64_t T, int64_t N, const int64_t* order,
+                         const int64_t* counts, int64_t query_start, int64_t* idx,
+                         uint8_t* valid, int64_t* next_idx, int64_t* read_idx, int8_t* codes,
+                         hipStream_t stream);
 
 /* Bank gather (read.py:241-256, 298-303): for j < N, K = w[idx]/max(|w[idx]|,eps),
  * V = w[idx], Vn = w[next_idx] ([B,N,H]). norm_w [B,T] fp32. Vn may be null (then

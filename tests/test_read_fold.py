@@ -8,7 +8,8 @@ successor rows, no gO Vn^T and no P_Vn^T gO GEMM. The reference computes the two
 separately (admitted.py:16-65); the fold changes the summation order only.
 
   * fold codes and the unfoldable flag against a brute-force restatement of their
-    definition on random, dense and suffix banks: bit-exact;
+    definition on random, dense and suffix banks: bit-exact; likewise the bank width read
+    and the slot arrays (idx, valid, next_idx, read_idx, codes) built in one launch;
   * the folded read against the oracle's unfolded read (fp32, 1e-5 normwise), with the
     successor-row gradients of the oracle mapped onto the rows they fold into;
   * bf16 folded against unfolded on the same inputs (2e-2 Frobenius, the bf16 bar);
@@ -79,6 +80,35 @@ def test_fold_codes_match_their_definition(cuda_device, kind, B, T):
     assert np.array_equal(codes.cpu().numpy(), want)
     if kind != "random" or T == 1:
         assert not bad, "dense and suffix banks fold"
+
+
+@pytest.mark.parametrize("kind", ["random", "dense", "suffix"])
+@pytest.mark.parametrize("B,T", [(3, 1), (2, 37), (4, 300)])
+def test_bank_width_and_slots_match_their_definition(cuda_device, kind, B, T):
+    """``ops.bank_width`` / ``ops.bank_slots`` (the selection's host read and slot arrays in
+    one launch each) against the same values from their definitions on the bank_select
+    result: the largest count, the unfoldable flag, order[:, :N], valid = j < max(count, 1),
+    min(idx + 1, T - 1), idx - query_start and the fold codes; bit-exact, at the bank's own
+    width and at a fixed larger width."""
+    g = torch.Generator().manual_seed(11 + T)
+    adm, window, whole = _admissions(kind, B, T, g)
+    order, counts, _ = ops.bank_select(adm.to(cuda_device), torch.tensor([window], device=cuda_device),
+                                       whole)
+    o, c = order.cpu().numpy(), counts.cpu().numpy()
+    want_codes, bad = _brute_fold(o, c, T)
+    top, flag = ops.bank_width(order, counts, True).tolist()
+    assert (top, flag) == (int(c.max()), int(bad))
+    assert ops.bank_width(order, counts, False).tolist() == [int(c.max()), 0]
+    for N in sorted({max(int(c.max()), 1), T}):
+        for qs in (0, T // 2):
+            idx, valid, nxt, rid, codes = (x.cpu().numpy() if x is not None else None
+                                           for x in ops.bank_slots(order, counts, N, qs, True))
+            assert np.array_equal(idx, o[:, :N])
+            assert np.array_equal(valid, np.arange(N)[None, :] < np.maximum(c, 1)[:, None])
+            assert np.array_equal(nxt, np.minimum(o[:, :N] + 1, T - 1))
+            assert np.array_equal(rid, o[:, :N] - qs)
+            assert np.array_equal(codes, want_codes[:, :N])
+    assert ops.bank_slots(order, counts, 1, 0, False)[4] is None
 
 
 def _case(seed, B, T, H, kind):
@@ -186,7 +216,8 @@ def test_read_module_fold_equals_unfolded(cuda_device):
         read.zero_grad(set_to_none=True)
         if not fold:
             orig = read._select
-            read._select = lambda a, n, width=None, want_fold=False: orig(a, n, width, False)
+            read._select = (lambda a, n, width=None, want_fold=False, query_start=0:
+                            orig(a, n, width, False, query_start))
         try:
             out = read(*leaves)
             (out * w).sum().backward()
