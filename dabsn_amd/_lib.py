@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _lock = threading.Lock()
 _lib = None
@@ -99,6 +99,10 @@ _SIGNATURES = {
     "dabsn_hip_read_output_partials": ([i64], sz),
     "dabsn_hip_read_output_bwd": (
         [i32, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
+    "dabsn_hip_read_output_window": (
+        [i32, i32, i32, i32, i64, i64, i64, vp, vp, vp, vp, vp], i32),
+    "dabsn_hip_read_output_bwd_window": (
+        [i32, i32, i32, i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_read_mix": ([i32, i64, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_rms_norm": ([i32, i64, i64, vp, vp, ctypes.c_float, vp, vp], i32),
     "dabsn_hip_relu_square": ([i32, i64, vp, vp, vp], i32),

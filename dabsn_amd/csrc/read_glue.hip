@@ -415,12 +415,20 @@ static inline bool vec_ok(int64_t H, std::initializer_list<const void*> ptrs) {
 // reference's two tensor operations under type promotion -- the product in the dtype of
 // (gain, long), rounded to bf16 when prod_bf16, then the sum in the dtype of (proj, product),
 // rounded by the store to O. No contraction into a fused multiply-add.
+// Elements are addressed as segments: chunk i of V elements lies in segment i / seg (seg
+// chunks each, segments ld chunks apart), so a time window [t0, t1) of [B, T, H] tensors is
+// B segments of (t1 - t0) H elements, T H apart. A flat array is one segment.
+__device__ __forceinline__ size_t seg_offset(uint32_t i, uint32_t seg, uint64_t ld) {
+  return static_cast<size_t>(i / seg) * ld + (i % seg);
+}
+
 template <typename P, typename L, typename O, int V>
-__global__ void __launch_bounds__(256) read_out_kernel(uint32_t chunks, const P* proj, const L* lng,
+__global__ void __launch_bounds__(256) read_out_kernel(uint32_t chunks, uint32_t seg, uint64_t ld,
+                                                       const P* proj, const L* lng,
                                                        const float* gain, int prod_bf16, O* out) {
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   if (i >= chunks) return;
-  const size_t o = static_cast<size_t>(i) * V;
+  const size_t o = seg_offset(i, seg, ld) * V;
   const float g = gain[0];
   float a[V], l[V];
   ldv<P, V>(proj + o, a);
@@ -439,7 +447,8 @@ __global__ void __launch_bounds__(256) read_out_kernel(uint32_t chunks, const P*
 // gradient sums gp * long (each term in the product dtype, the sum in fp32), one partial per
 // workgroup, reduced in a fixed order by read_out_reduce_kernel.
 template <typename O, typename P, typename L, int V>
-__global__ void __launch_bounds__(256) read_out_bwd_kernel(uint32_t chunks, const O* gout,
+__global__ void __launch_bounds__(256) read_out_bwd_kernel(uint32_t chunks, uint32_t seg,
+                                                           uint64_t ld, const O* gout,
                                                            const L* lng, const float* gain,
                                                            int prod_bf16, P* gproj, L* glong,
                                                            float* partial) {
@@ -447,7 +456,7 @@ __global__ void __launch_bounds__(256) read_out_bwd_kernel(uint32_t chunks, cons
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   float acc = 0.0f;
   if (i < chunks) {
-    const size_t o = static_cast<size_t>(i) * V;
+    const size_t o = seg_offset(i, seg, ld) * V;
     const float g = gain[0];
     float go[V], l[V], gl[V];
     ldv<O, V>(gout + o, go);
@@ -915,7 +924,7 @@ static bool read_out_vec(int64_t n, std::initializer_list<const void*> ptrs) {
   do {                                                                                    \
     DABSN_REQUIRE((da == kF32 || da == kBF16) && (db == kF32 || db == kBF16) &&           \
                       (dc == kF32 || dc == kBF16),                                        \
-                  what ": dtype codes must be 0 (fp32) or 1 (bf16)");                     \
+                  "%s: dtype codes must be 0 (fp32) or 1 (bf16)", what);                  \
     const int code = (da == kBF16 ? 4 : 0) | (db == kBF16 ? 2 : 0) | (dc == kBF16 ? 1 : 0); \
     switch (code * 2 + (vec ? 1 : 0)) {                                                   \
       case 0: LAUNCH(float, float, float, 1); break;                                      \
@@ -937,24 +946,78 @@ static bool read_out_vec(int64_t n, std::initializer_list<const void*> ptrs) {
     }                                                                                     \
   } while (0)
 
+// read_output over `rows` segments of row_len elements, ld elements apart (a flat array:
+// one row). The vector path needs row_len and ld multiples of 8 and 16-byte aligned bases.
+static int read_output_rows(const char* what, int proj_dtype, int long_dtype, int prod_dtype,
+                            int out_dtype, int64_t rows, int64_t row_len, int64_t ld,
+                            const void* proj, const void* lng, const float* gain, void* out,
+                            hipStream_t stream) {
+  DABSN_REQUIRE(rows >= 0 && row_len >= 0 && (rows <= 1 || ld >= row_len), "%s: bad size", what);
+  const int64_t n = rows * row_len;
+  if (n == 0) return DABSN_OK;
+  DABSN_REQUIRE(proj && lng && gain && out, "%s: null pointer", what);
+  DABSN_REQUIRE(prod_dtype == kF32 || prod_dtype == kBF16, "%s: bad product dtype", what);
+  const bool vec = read_out_vec(row_len, {proj, lng, out}) && (rows <= 1 || ld % 8 == 0);
+  const int64_t V = vec ? 8 : 1;
+  const int64_t chunks = n / V, seg = row_len / V, ldc = rows <= 1 ? seg : ld / V;
+  DABSN_REQUIRE(chunks < (1ll << 32), "%s: too many elements", what);
+  const dim3 grid(blocks_for(chunks, 256)), block(256);
+#define L(P, Lt, O, VV)                                                                        \
+  hipLaunchKernelGGL((read_out_kernel<P, Lt, O, VV>), grid, block, 0, stream, (uint32_t)chunks,  \
+                     (uint32_t)seg, (uint64_t)ldc, (const P*)proj, (const Lt*)lng, gain,        \
+                     prod_dtype == kBF16 ? 1 : 0, (O*)out)
+  READ_OUT_TYPES(what, proj_dtype, long_dtype, out_dtype, vec, L);
+#undef L
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+static int read_output_bwd_rows(const char* what, int out_dtype, int proj_dtype, int long_dtype,
+                                int prod_dtype, int64_t rows, int64_t row_len, int64_t ld,
+                                const void* gout, const void* lng, const float* gain,
+                                void* gproj, void* glong, float* ggain, float* partials,
+                                size_t partial_count, hipStream_t stream) {
+  DABSN_REQUIRE(rows >= 0 && row_len >= 0 && (rows <= 1 || ld >= row_len), "%s: bad size", what);
+  DABSN_REQUIRE(ggain && partials, "%s: null pointer", what);
+  const int64_t n = rows * row_len;
+  if (n == 0) return dabsn_hip_zero(ggain, 4, stream);
+  DABSN_REQUIRE(gout && lng && gain && gproj && glong, "%s: null pointer", what);
+  DABSN_REQUIRE(prod_dtype == kF32 || prod_dtype == kBF16, "%s: bad product dtype", what);
+  const bool vec =
+      read_out_vec(row_len, {gout, lng, gproj, glong}) && (rows <= 1 || ld % 8 == 0);
+  const int64_t V = vec ? 8 : 1;
+  const int64_t chunks = n / V, seg = row_len / V, ldc = rows <= 1 ? seg : ld / V;
+  DABSN_REQUIRE(chunks < (1ll << 32), "%s: too many elements", what);
+  const unsigned nblk = blocks_for(chunks, 256);
+  DABSN_REQUIRE(partial_count >= nblk, "%s: %zu partials < %u", what, partial_count, nblk);
+  const dim3 grid(nblk), block(256);
+#define L(O, P, Lt, VV)                                                                        \
+  hipLaunchKernelGGL((read_out_bwd_kernel<O, P, Lt, VV>), grid, block, 0, stream,              \
+                     (uint32_t)chunks, (uint32_t)seg, (uint64_t)ldc, (const O*)gout,            \
+                     (const Lt*)lng, gain, prod_dtype == kBF16 ? 1 : 0, (P*)gproj, (Lt*)glong,  \
+                     partials)
+  READ_OUT_TYPES(what, out_dtype, proj_dtype, long_dtype, vec, L);
+#undef L
+  DABSN_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(read_out_reduce_kernel, dim3(1), dim3(256), 0, stream, nblk, partials, ggain);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
 int dabsn_hip_read_output(int proj_dtype, int long_dtype, int prod_dtype, int out_dtype,
                           int64_t n, const void* proj, const void* lng, const float* gain,
                           void* out, hipStream_t stream) {
   DABSN_REQUIRE(n >= 0, "read_output: bad size");
-  if (n == 0) return DABSN_OK;
-  DABSN_REQUIRE(proj && lng && gain && out, "read_output: null pointer");
-  DABSN_REQUIRE(prod_dtype == kF32 || prod_dtype == kBF16, "read_output: bad product dtype");
-  const bool vec = read_out_vec(n, {proj, lng, out});
-  const int64_t chunks = n / (vec ? 8 : 1);
-  DABSN_REQUIRE(chunks < (1ll << 32), "read_output: too many elements");
-  const dim3 grid(blocks_for(chunks, 256)), block(256);
-#define L(P, Lt, O, V)                                                                      \
-  hipLaunchKernelGGL((read_out_kernel<P, Lt, O, V>), grid, block, 0, stream, (uint32_t)chunks, \
-                     (const P*)proj, (const Lt*)lng, gain, prod_dtype == kBF16 ? 1 : 0, (O*)out)
-  READ_OUT_TYPES("read_output", proj_dtype, long_dtype, out_dtype, vec, L);
-#undef L
-  DABSN_HIP_CHECK(hipGetLastError());
-  return DABSN_OK;
+  return read_output_rows("read_output", proj_dtype, long_dtype, prod_dtype, out_dtype, 1, n, n,
+                          proj, lng, gain, out, stream);
+}
+
+int dabsn_hip_read_output_window(int proj_dtype, int long_dtype, int prod_dtype, int out_dtype,
+                                 int64_t rows, int64_t row_len, int64_t ld, const void* proj,
+                                 const void* lng, const float* gain, void* out,
+                                 hipStream_t stream) {
+  return read_output_rows("read_output window", proj_dtype, long_dtype, prod_dtype, out_dtype,
+                          rows, row_len, ld, proj, lng, gain, out, stream);
 }
 
 size_t dabsn_hip_read_output_partials(int64_t n) {
@@ -967,27 +1030,19 @@ int dabsn_hip_read_output_bwd(int out_dtype, int proj_dtype, int long_dtype, int
                               void* gproj, void* glong, float* ggain, float* partials,
                               size_t partial_count, hipStream_t stream) {
   DABSN_REQUIRE(n >= 0, "read_output backward: bad size");
-  DABSN_REQUIRE(ggain && partials, "read_output backward: null pointer");
-  if (n == 0) return dabsn_hip_zero(ggain, 4, stream);
-  DABSN_REQUIRE(gout && lng && gain && gproj && glong, "read_output backward: null pointer");
-  DABSN_REQUIRE(prod_dtype == kF32 || prod_dtype == kBF16, "read_output backward: bad product dtype");
-  const bool vec = read_out_vec(n, {gout, lng, gproj, glong});
-  const int64_t chunks = n / (vec ? 8 : 1);
-  DABSN_REQUIRE(chunks < (1ll << 32), "read_output backward: too many elements");
-  const unsigned nblk = blocks_for(chunks, 256);
-  DABSN_REQUIRE(partial_count >= nblk, "read_output backward: %zu partials < %u", partial_count,
-                nblk);
-  const dim3 grid(nblk), block(256);
-#define L(O, P, Lt, V)                                                                          \
-  hipLaunchKernelGGL((read_out_bwd_kernel<O, P, Lt, V>), grid, block, 0, stream,               \
-                     (uint32_t)chunks, (const O*)gout, (const Lt*)lng, gain,                   \
-                     prod_dtype == kBF16 ? 1 : 0, (P*)gproj, (Lt*)glong, partials)
-  READ_OUT_TYPES("read_output backward", out_dtype, proj_dtype, long_dtype, vec, L);
-#undef L
-  DABSN_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(read_out_reduce_kernel, dim3(1), dim3(256), 0, stream, nblk, partials, ggain);
-  DABSN_HIP_CHECK(hipGetLastError());
-  return DABSN_OK;
+  return read_output_bwd_rows("read_output backward", out_dtype, proj_dtype, long_dtype,
+                              prod_dtype, 1, n, n, gout, lng, gain, gproj, glong, ggain,
+                              partials, partial_count, stream);
+}
+
+int dabsn_hip_read_output_bwd_window(int out_dtype, int proj_dtype, int long_dtype,
+                                     int prod_dtype, int64_t rows, int64_t row_len, int64_t ld,
+                                     const void* gout, const void* lng, const float* gain,
+                                     void* gproj, void* glong, float* ggain, float* partials,
+                                     size_t partial_count, hipStream_t stream) {
+  return read_output_bwd_rows("read_output window backward", out_dtype, proj_dtype, long_dtype,
+                              prod_dtype, rows, row_len, ld, gout, lng, gain, gproj, glong,
+                              ggain, partials, partial_count, stream);
 }
 
 int dabsn_hip_admit_step(int mode, int64_t B, int64_t n, int64_t base, int64_t cap,

@@ -197,6 +197,9 @@ class _PipelinedScanRead(torch.autograd.Function):
         short = torch.empty((B, T, H), device=dev, dtype=dt)   # its output projection
         sink = torch.zeros((B, T, H), device=dev, dtype=dt)    # bank-write gradient (backward)
         long_out = torch.empty((B, T, H), device=dev, dtype=dt)  # the long channel
+        gain = read_params[names.index("long_gain")]
+        read_out = torch.empty((B, T, H), device=dev,  # short + long_gain * long
+                               dtype=ops._read_output_dtypes(short, long_out, gain)[1])
         bounds = chunked._chunks(T, chunk)
         K = len(bounds)
         for st in (M, S, R):
@@ -225,7 +228,6 @@ class _PipelinedScanRead(torch.autograd.Function):
             ay, w, pl = out.tapes[2], out.tapes[3], out.tapes[1]
             w_leaf = w.detach().requires_grad_(True)
             stats_leaf = stats.detach().requires_grad_(True)
-            short_leaf = short.detach().requires_grad_(True)
             param_leaves = {n: p.detach().requires_grad_(p.requires_grad)
                             for n, p in zip(names, read_params)}
             norms = stats_leaf[..., 5].detach()
@@ -292,6 +294,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                             r_chunks = torch.cuda.Event()
                             r_chunks.record(R)
                         long_window(k)
+                        ops.read_output_window(short, long_out, gain, read_out, *bounds[k])
                     # The last window's long channel beside the last chunk's read.
                     R.wait_event(scan_done[K - 1])
                     long_window(K - 1)
@@ -301,9 +304,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                 M.wait_event(r_chunks)
                 chunks.append(read_chunk(K - 1))
                 M.wait_event(r_long)
-                long_leaf = long_out.detach().requires_grad_(True)
-                with torch.enable_grad():
-                    read_out = ops.direct.read_output(short_leaf, long_leaf, read.long_gain)
+                ops.read_output_window(short, long_out, gain, read_out, *bounds[K - 1])
             M.wait_stream(S)
         _check_scans(S, fwd_calls, "core scan forward")
         ambient.wait_stream(S)
@@ -314,11 +315,11 @@ class _PipelinedScanRead(torch.autograd.Function):
         ctx.read, ctx.chunk, ctx.names = read, chunk, names
         ctx.bounds = bounds
         ctx.meta = [(x.dtype, tuple(x.shape)) for x in (Wx, Wgx, *core_in)]
-        ctx.graph = (chunks, read_out, longs, w_leaf, stats_leaf, short_leaf, long_leaf,
-                     param_leaves, sink)
+        ctx.graph = (chunks, longs, w_leaf, stats_leaf, param_leaves, sink, long_out)
+        ctx.out_dtype = read_out.dtype
         ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, starts, retr, out.U, *out.tapes)
         ctx.set_materialize_grads(False)
-        return U[..., :H], U[..., H:], read_out.detach()
+        return U[..., :H], U[..., H:], read_out
 
     @staticmethod
     def backward(ctx, g_y, g_budget, g_read):
@@ -332,8 +333,7 @@ class _PipelinedScanRead(torch.autograd.Function):
         vecs, scal = saved[4:20], saved[20:23]
         starts, retr = saved[23], saved[24]
         fwd_out = chunked._Tapes(None, 0, 0, 0, existing=saved[25:33])
-        (chunks, read_out, longs, w_leaf, stats_leaf, short_leaf, long_leaf, param_leaves,
-         sink) = ctx.graph
+        chunks, longs, w_leaf, stats_leaf, param_leaves, sink, long_out = ctx.graph
         read = ctx.read
         B, T, H = Wx.shape
         dt = Wx.dtype
@@ -358,7 +358,15 @@ class _PipelinedScanRead(torch.autograd.Function):
         g_nov, g_p, g_ay, g_e, g_c = (torch.empty((B, T, H), device=dev, dtype=dt)
                                       for _ in range(5))
         gWx, gWgx, day = (torch.empty((B, T, H), device=dev, dtype=dt) for _ in range(3))
-        g_read = torch.zeros_like(read_out) if g_read is None else g_read.contiguous()
+        g_read = (torch.zeros((B, T, H), device=dev, dtype=ctx.out_dtype) if g_read is None
+                  else g_read.to(ctx.out_dtype).contiguous())
+        # The read output's gradients, window by window: the projection's and the long
+        # channel's, and the gain's share of each window.
+        g_short3 = torch.empty((B, T, H), device=dev, dtype=dt)
+        g_long = torch.empty_like(long_out)
+        gain_leaf = param_leaves["long_gain"]
+        gain_parts = torch.zeros((K,), device=dev, dtype=torch.float32)
+        out_done = [False] * K
         # dL/dUg and dL/dA summed over windows as their reverse scans finish.
         gUg_sum, gA_sum = (torch.zeros((H, H), device=dev, dtype=torch.float32) for _ in range(2))
         for st in (M, S, R):
@@ -387,6 +395,12 @@ class _PipelinedScanRead(torch.autograd.Function):
             gUg_sum.add_(gWgx[:, t0:t1].reshape(-1, H).t() @ y)
             gA_sum.add_(day[:, t0:t1].reshape(-1, H).t() @ y)
 
+        def read_out_backward(k: int) -> None:
+            if not out_done[k]:
+                ops.read_output_bwd_window(g_read, long_out, gain_leaf, g_short3, g_long,
+                                           gain_parts[k:k + 1], *bounds[k])
+                out_done[k] = True
+
         state_grad: list = [None]
 
         def long_backward(k: int) -> None:
@@ -404,18 +418,17 @@ class _PipelinedScanRead(torch.autograd.Function):
             state_grad[0] = None if init is None else [x.grad for x in init]
 
         with torch.cuda.stream(M):
-            # The read output's backward; then the long channel's last windows on the read
-            # half (enqueued first, so that its kernels hold their CUs) beside the last
-            # chunk's projection and read backward on the whole device.
-            torch.autograd.backward([read_out], [g_read], inputs=[short_leaf, long_leaf, *trainable])
-            g_short3 = short_leaf.grad.to(dt)
-            g_long = long_leaf.grad
+            # The read output's backward over the last window; then the long channel's last
+            # windows on the read half (enqueued first, so that its kernels hold their CUs)
+            # beside the last chunk's projection and read backward on the whole device.
+            read_out_backward(K - 1)
             head = torch.cuda.Event()
             head.record(M)
             R.wait_event(head)
-            head_windows = min(K, 2) if g_long is not None else 0
+            head_windows = min(K, 2)
             with torch.cuda.stream(R):
                 for k in range(K - 1, K - 1 - head_windows, -1):
+                    read_out_backward(k)
                     long_backward(k)
 
             carry = [None, None, None]
@@ -426,6 +439,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                 r, ay_leaf = chunks[k]
                 st = M if k == K - 1 else R
                 with torch.cuda.stream(st):
+                    read_out_backward(k)
                     g_r = projection_grads(g_short3, k)
                     # w_leaf is listed so that the engine runs the gather's backward, whose
                     # gradient goes to the sink (it returns none for w_leaf itself).
@@ -440,7 +454,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                     done.record(st)
                     R.wait_event(done)
                 with torch.cuda.stream(R):
-                    if g_long is not None and k < K - head_windows:
+                    if k < K - head_windows:
                         long_backward(k)
                     # Window k of the write gradient is complete (only query chunks >= k
                     # read it): the long channel's share joins it.
@@ -488,6 +502,8 @@ class _PipelinedScanRead(torch.autograd.Function):
             M.wait_stream(S)
             M.wait_stream(R)
             core_weight_grads(*bounds[0])
+            if gain_leaf.requires_grad:
+                gain_leaf.grad = gain_parts.sum().reshape(gain_leaf.shape).to(gain_leaf.dtype)
             gvec = torch.stack([bw.part_vec.sum(0) for bw in bws]).sum(0)
             gscal = torch.stack([bw.part_scal.sum(0) for bw in bws]).sum(0)
             core = [gWx, gWgx, gUg_sum, gA_sum, *[gvec[i] for i in range(16)],
