@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 _lock = threading.Lock()
 _lib = None
@@ -113,6 +113,8 @@ _SIGNATURES = {
         [i32, i64, i64, i64, i64, vp, i64, PTR8, vp, i32, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_fold": ([i64, i64, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_bank_width": ([i64, i64, vp, vp, i32, vp, vp], i32),
+    "dabsn_hip_window_add": ([i32, i64, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64, i64, vp],
+                             i32),
     "dabsn_hip_bank_slots": ([i64, i64, i64, vp, vp, i64, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_glue_slots": ([i64, i64, i64, i64, vp, vp, i64, PTR8, i32, vp, vp, vp, vp], i32),
     "dabsn_hip_glue_slots_partials": ([i64, i64], sz),

@@ -343,6 +343,32 @@ __global__ void __launch_bounds__(256) fold_kernel(int T, int N, const int64_t* 
     __hip_atomic_fetch_or(unfoldable, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// out = a (+ x) over a [B, R, C] box whose operands each have their own batch and row
+// strides (elements; the columns are contiguous): a time window of [B, T, H] tensors, a
+// column block of a wider row, or a dense buffer. One thread per V elements of a row; V = 8
+// moves 16 bytes per access (bf16) and needs C and every stride a multiple of 8 and 16-byte
+// aligned bases. bf16 sums are formed in fp32 and rounded once, as torch's add rounds them.
+template <typename E, int V>
+__global__ void __launch_bounds__(256) window_add_kernel(uint32_t chunks, uint32_t cpr, uint32_t R,
+                                                         const E* a, int64_t a_sb, int64_t a_sr,
+                                                         const E* x, int64_t x_sb, int64_t x_sr,
+                                                         E* out, int64_t o_sb, int64_t o_sr) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= chunks) return;
+  const int64_t c = static_cast<int64_t>(i % cpr) * V;
+  const uint32_t rr = i / cpr;
+  const int64_t r = rr % R, b = rr / R;
+  float va[V];
+  ldv<E, V>(a + b * a_sb + r * a_sr + c, va);
+  if (x != nullptr) {
+    float vx[V];
+    ldv<E, V>(x + b * x_sb + r * x_sr + c, vx);
+#pragma unroll
+    for (int e = 0; e < V; ++e) va[e] += vx[e];
+  }
+  stv<E, V>(out + b * o_sb + r * o_sr + c, va);
+}
+
 // The bank width a read needs and whether its successor rows fold (one host read of two
 // int64 values instead of a reduction, a flag kernel and their stacking): out[0] = the
 // largest admitted count over the rows, out[1] = 1 when some admitted slot's successor is
@@ -825,6 +851,30 @@ int dabsn_hip_bank_fold(int64_t B, int64_t T, int64_t N, const int64_t* order,
   if (width == 0) return DABSN_OK;
   hipLaunchKernelGGL(fold_kernel, dim3(blocks_for(width, 256), (unsigned)B), dim3(256), 0, stream,
                      (int)T, (int)N, order, counts, codes, unfoldable);
+  DABSN_HIP_CHECK(hipGetLastError());
+  return DABSN_OK;
+}
+
+int dabsn_hip_window_add(int dtype, int64_t B, int64_t R, int64_t C, const void* a, int64_t a_sb,
+                         int64_t a_sr, const void* x, int64_t x_sb, int64_t x_sr, void* out,
+                         int64_t o_sb, int64_t o_sr, hipStream_t stream) {
+  DABSN_REQUIRE(B >= 0 && R >= 0 && C >= 0, "window_add: bad shape");
+  if (B == 0 || R == 0 || C == 0) return DABSN_OK;
+  DABSN_REQUIRE(a && out, "window_add: null pointer");
+  bool vec = C % 8 == 0 && a_sb % 8 == 0 && a_sr % 8 == 0 && o_sb % 8 == 0 && o_sr % 8 == 0;
+  for (const void* q : {a, x, static_cast<const void*>(out)})
+    if (q && (reinterpret_cast<uintptr_t>(q) & 15u) != 0) vec = false;
+  if (x && (x_sb % 8 != 0 || x_sr % 8 != 0)) vec = false;
+  const int64_t cpr = C / (vec ? 8 : 1);
+  const int64_t chunks = B * R * cpr;
+  DABSN_REQUIRE(chunks < (1ll << 32) && R < (1ll << 32), "window_add: too many elements");
+  const dim3 grid(blocks_for(chunks, 256)), block(256);
+#define L(E, VV)                                                                              \
+  hipLaunchKernelGGL((window_add_kernel<E, VV>), grid, block, 0, stream, (uint32_t)chunks,      \
+                     (uint32_t)cpr, (uint32_t)R, (const E*)a, a_sb, a_sr, (const E*)x, x_sb,    \
+                     x_sr, (E*)out, o_sb, o_sr)
+  GLUE_DISPATCH("window_add", dtype, vec, L);
+#undef L
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }

@@ -1442,6 +1442,28 @@ def bank_fold(order: Tensor, counts: Tensor, width: Optional[int] = None):
     return codes
 
 
+def window_add(out: Tensor, a: Tensor, x: Optional[Tensor] = None) -> Tensor:
+    """out = a (+ x) for [B, R, C] views with contiguous columns and any batch and row
+    strides (``dabsn_hip_window_add``): time windows of [B, T, C] tensors, column blocks of
+    wider rows. Returns out."""
+    ops_ = [t for t in (out, a, x) if t is not None]
+    if any(t.dim() != 3 or t.shape != out.shape or t.dtype != out.dtype or t.stride(2) != 1
+           or t.device != out.device for t in ops_):
+        raise ValueError("window_add: [B, R, C] views of one shape and dtype, columns contiguous")
+    lib = _lib.load()
+    B, R, C = out.shape
+    xs = (0, 0) if x is None else (x.stride(0), x.stride(1))
+    _lib.check(lib.dabsn_hip_window_add(_code(out.dtype), B, R, C, _p(a), a.stride(0), a.stride(1),
+                                        _p(x), *xs, _p(out), out.stride(0), out.stride(1),
+                                        _stream(out)), "window add")
+    return out
+
+
+def window_copy(a: Tensor) -> Tensor:
+    """A contiguous copy of the [B, R, C] view ``a`` (``window_add`` with no second term)."""
+    return window_add(torch.empty(a.shape, device=a.device, dtype=a.dtype), a)
+
+
 def bank_width(order: Tensor, counts: Tensor, check_fold: bool) -> Tensor:
     """[largest admitted count, unfoldable flag] of a ``bank_select`` result as one int64
     device tensor of two values (``dabsn_hip_bank_width``; the flag is 0 without

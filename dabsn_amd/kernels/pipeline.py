@@ -46,6 +46,9 @@ from .. import _lib, events
 from . import chunked, ops
 
 _PAIRS: dict[int, tuple] = {}
+# The long channel's four coefficient logits, in the order of dabsn::long_scan_fused.
+_LONG_LOGITS = ("logit_expect_retain", "logit_retention_decay", "logit_retain",
+                "logit_retention_strength")
 
 
 def stream_pair(device: torch.device):
@@ -198,6 +201,8 @@ class _PipelinedScanRead(torch.autograd.Function):
         sink = torch.zeros((B, T, H), device=dev, dtype=dt)    # bank-write gradient (backward)
         long_out = torch.empty((B, T, H), device=dev, dtype=dt)  # the long channel
         gain = read_params[names.index("long_gain")]
+        logits = [read_params[names.index(n)] for n in _LONG_LOGITS]
+        long_state0 = read.initial_long_scan_state(B, H, device=dev)
         read_out = torch.empty((B, T, H), device=dev,  # short + long_gain * long
                                dtype=ops._read_output_dtypes(short, long_out, gain)[1])
         bounds = chunked._chunks(T, chunk)
@@ -248,7 +253,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                 C = t1 - t0
                 st = torch.cuda.current_stream(dev)
                 _stats_window(out, stats, t0, t1, st.cuda_stream)
-                pre = F.linear(U[:, t0:t1].reshape(B * C, 2 * H), Wd[:, :2 * H], bd)
+                pre = F.linear(ops.window_copy(U[:, t0:t1]).view(B * C, 2 * H), Wd[:, :2 * H], bd)
                 with torch.enable_grad():
                     ay_leaf = ay[:, t0:t1].detach().requires_grad_(True)
                     r = read.query_bank_retrieved(
@@ -256,33 +261,28 @@ class _PipelinedScanRead(torch.autograd.Function):
                         bank_norms=norms, bank_stats=stats_leaf[:, :t1], query_start=t0,
                         gather=gather)
                 rd = r.detach().to(dt)
-                retr[:, t0:t1].copy_(rd)
+                ops.window_add(retr[:, t0:t1], rd)
                 sh = torch.addmm(pre, rd.reshape(B * C, H), Wd[:, 2 * H:].t())
-                short[:, t0:t1].copy_(sh.view(B, C, H))
+                ops.window_add(short[:, t0:t1], sh.view(B, C, H))
                 return r, ay_leaf
 
-            # The long channel window by window, each window its own graph with leaves on its
-            # write and plasticity rows and on the recurrent state it starts from (the state
-            # the previous window ends in), so that the backward can walk the windows one
-            # at a time: per window (long rows, final state, initial-state leaves or None,
-            # write leaf, plasticity leaf).
+            # The long channel (long.py:492-579) window by window from the state the previous
+            # window ends in, differentiated by hand: per window its write and plasticity
+            # rows (contiguous copies, kept) and the states entering every step.
+            events.announce("recurrent_long_read", "rocm_chunk_parallel_scan", B=B, T=T, H=H,
+                            dtype="bf16" if code == 1 else "fp32")
             longs = []
-            carried = None
+            carried = long_state0
 
             def long_window(k: int) -> None:
                 nonlocal carried
                 t0, t1 = bounds[k]
-                with torch.enable_grad():
-                    # Contiguous window copies (the scan reads them so in any case), kept
-                    # for the backward.
-                    wk = w[:, t0:t1].contiguous().requires_grad_(True)
-                    pk = pl[:, t0:t1].contiguous().requires_grad_(True)
-                    init = (None if carried is None
-                            else tuple(x.detach().requires_grad_(True) for x in carried))
-                    lk, carried = read._long_scan_from_state(
-                        wk, pk, None, initial_state=init, return_final_state=True)
-                long_out[:, t0:t1].copy_(lk.detach())
-                longs.append((lk, carried, init, wk, pk))
+                wk = ops.window_copy(w[:, t0:t1])
+                pk = ops.window_copy(pl[:, t0:t1])
+                lk, lf, ef, rf, states = ops.direct.long_scan_fused(wk, pk, *logits, *carried)
+                carried = (lf, ef, rf)
+                ops.window_add(long_out[:, t0:t1], lk)
+                longs.append((wk, pk, states))
 
             chunks = []
             with _parameters_as(read, param_leaves):
@@ -378,22 +378,24 @@ class _PipelinedScanRead(torch.autograd.Function):
             # gradients fill U's gradient window, the retrieved rows' gradient is returned.
             t0, t1 = bounds[k]
             C = t1 - t0
-            prod = torch.mm(g_short3[:, t0:t1].reshape(B * C, H), Wd)
+            prod = torch.mm(ops.window_copy(g_short3[:, t0:t1]).view(B * C, H), Wd)
             for i, g_in in enumerate(g_halves):
                 g_proj = prod[:, i * H:(i + 1) * H].view(B, C, H)
                 dst = gU[:, t0:t1, i * H:(i + 1) * H]
                 if g_in is None:
-                    dst.copy_(g_proj)
+                    ops.window_add(dst, g_proj)
+                elif g_in.stride(2) == 1:
+                    ops.window_add(dst, g_in[:, t0:t1], g_proj)
                 else:
                     torch.add(g_in[:, t0:t1], g_proj, out=dst)
-            return prod[:, 2 * H:].view(B, C, H)
+            return ops.window_copy(prod[:, 2 * H:].view(B, C, H))
 
         def core_weight_grads(t0: int, t1: int) -> None:
             # dL/dUg and dL/dA over window [t0, t1): the reverse scan's dWgx and da_y rows
             # times the trajectory's y rows, summed over the window's rows.
-            y = fwd_out.U[:, t0:t1, :H].reshape(-1, H)
-            gUg_sum.add_(gWgx[:, t0:t1].reshape(-1, H).t() @ y)
-            gA_sum.add_(day[:, t0:t1].reshape(-1, H).t() @ y)
+            y = ops.window_copy(fwd_out.U[:, t0:t1, :H]).view(-1, H)
+            gUg_sum.add_(ops.window_copy(gWgx[:, t0:t1]).view(-1, H).t() @ y)
+            gA_sum.add_(ops.window_copy(day[:, t0:t1]).view(-1, H).t() @ y)
 
         def read_out_backward(k: int) -> None:
             if not out_done[k]:
@@ -401,21 +403,22 @@ class _PipelinedScanRead(torch.autograd.Function):
                                            gain_parts[k:k + 1], *bounds[k])
                 out_done[k] = True
 
-        state_grad: list = [None]
+        logit_leaves = [param_leaves[n] for n in _LONG_LOGITS]
+        long_grads: list = [None] * K     # per window: (g_write, g_plasticity)
+        logit_parts: list = [None] * K    # per window: the four logits' shares
+        state_grad: list = [None, None, None]
 
         def long_backward(k: int) -> None:
             # Window k of the long channel: its rows' gradient plus the gradient of the state
             # it ends in (from window k + 1's backward); leaves the gradient of the state it
             # starts from for window k - 1.
-            lk, fin, init, wk, pk = longs[k]
+            wk, pk, states = longs[k]
             t0, t1 = bounds[k]
-            outs, grads = [lk], [g_long[:, t0:t1]]
-            for f, g in zip(fin, state_grad[0] or ()):
-                if g is not None:
-                    outs.append(f)
-                    grads.append(g)
-            torch.autograd.backward(outs, grads, inputs=[wk, pk, *trainable, *(init or ())])
-            state_grad[0] = None if init is None else [x.grad for x in init]
+            g = ops.long_scan_fused_backward(wk, pk, logit_leaves, states,
+                                             ops.window_copy(g_long[:, t0:t1]), *state_grad)
+            long_grads[k] = (g[0], g[1])
+            logit_parts[k] = g[2:6]
+            state_grad[:] = g[6:9]
 
         with torch.cuda.stream(M):
             # The read output's backward over the last window; then the long channel's last
@@ -446,7 +449,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                     torch.autograd.backward([r], [g_r],
                                             inputs=[ay_leaf, w_leaf, stats_leaf, *trainable])
                     if ay_leaf.grad is not None:
-                        g_ay[:, t0:t1].copy_(ay_leaf.grad)
+                        ops.window_add(g_ay[:, t0:t1], ay_leaf.grad.to(dt))
                     else:
                         g_ay[:, t0:t1].zero_()
                 if st is not R:
@@ -458,13 +461,9 @@ class _PipelinedScanRead(torch.autograd.Function):
                         long_backward(k)
                     # Window k of the write gradient is complete (only query chunks >= k
                     # read it): the long channel's share joins it.
-                    wk, pk = longs[k][3:]
-                    if wk.grad is not None:
-                        sink[:, t0:t1].add_(wk.grad)
-                    if pk.grad is None:
-                        g_p[:, t0:t1].zero_()
-                    else:
-                        g_p[:, t0:t1].copy_(pk.grad)
+                    gwk, gpk = long_grads[k]
+                    ops.window_add(sink[:, t0:t1], sink[:, t0:t1], gwk)
+                    ops.window_add(g_p[:, t0:t1], gpk)
                     gs = stats_leaf.grad
                     gs = torch.zeros_like(stats_leaf) if gs is None else gs.contiguous()
                     _stats_bwd_window(gs, (g_nov, None, g_e, g_c), False, t0, t1, R.cuda_stream)
@@ -504,6 +503,12 @@ class _PipelinedScanRead(torch.autograd.Function):
             core_weight_grads(*bounds[0])
             if gain_leaf.requires_grad:
                 gain_leaf.grad = gain_parts.sum().reshape(gain_leaf.shape).to(gain_leaf.dtype)
+            for i, leaf in enumerate(logit_leaves):
+                if leaf.requires_grad:
+                    total = logit_parts[K - 1][i]
+                    for k in range(K - 2, -1, -1):  # the order the windows were walked
+                        total = total + logit_parts[k][i]
+                    leaf.grad = total.reshape(leaf.shape).to(leaf.dtype)
             gvec = torch.stack([bw.part_vec.sum(0) for bw in bws]).sum(0)
             gscal = torch.stack([bw.part_scal.sum(0) for bw in bws]).sum(0)
             core = [gWx, gWgx, gUg_sum, gA_sum, *[gvec[i] for i in range(16)],

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 14
+#define DABSN_HIP_ABI_VERSION 15
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -326,6 +326,15 @@ int dabsn_hip_bank_fold(int64_t B, int64_t T, int64_t N, const int64_t* order,
                         const int64_t* counts, int8_t* codes, uint32_t* unfoldable,
                         hipStream_t stream);
 
+/* out = a + x (x may be NULL: out = a) over a [B, R, C] box of `dtype` elements whose
+ * operands each have a batch and a row stride in elements (columns contiguous): a time
+ * window [t0, t0 + R) of [B, T, C] tensors has strides (T C, C), a column block of a wider
+ * row the row's width. bf16 sums are formed in fp32 and rounded once (torch's add). out may
+ * alias a or x elementwise. No reference counterpart: it moves the windows a time-chunked
+ * read hands between its pieces without a copy per operand. */
+int dabsn_hip_window_add(int dtype, int64_t B, int64_t R, int64_t C, const void* a, int64_t a_sb,
+                         int64_t a_sr, const void* x, int64_t x_sb, int64_t x_sr, void* out,
+                         int64_t o_sb, int64_t o_sr, hipStream_t stream);
 /* The width a read of a bank_select result needs (read.py:233: the host reads the largest
  * admitted count) and, with check_fold, whether the successor fold applies: out[0] (int64) =
  * max over rows of counts, out[1] = 1 when some admitted slot codes 2 in
