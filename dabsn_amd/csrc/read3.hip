@@ -223,47 +223,213 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_kernel(int64_t rows, RowCtx c
   }
 }
 
-// Per-row reductions needed by the score gradient: rs = sum Ps dPV, rp = sum Pp dPV,
-// ri = sum Pi dPVn (unscaled by the gains). One wave per query row.
-__global__ void __launch_bounds__(NTH) grad_rows_kernel(int64_t rows, RowCtx c, Gains g,
-                                                        const float* scale_p,
-                                                        const int32_t* rs_rng, const float* stats,
-                                                        const int8_t* fold, const float* dPV,
-                                                        const float* dPVn, float* rowA) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * NWV + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int b = static_cast<int>(row / c.T), t = static_cast<int>(row % c.T);
-  c.scale = scale_p[0];
-  c.cg = g.p[3][0];
-  const int QT = (c.T + TILE - 1) / TILE;
-  const int nhi = rs_rng[(static_cast<size_t>(b) * QT + t / TILE) * 3 + 2];
-  const float* st6 = stats + static_cast<size_t>(row) * 6;
-  const float is = st6[1] > 0.f ? 1.0f / st6[1] : 0.f, ip = st6[3] > 0.f ? 1.0f / st6[3] : 0.f,
-              ii = st6[5] > 0.f ? 1.0f / st6[5] : 0.f;
-  const float* ckt = c.ck + static_cast<size_t>(row) * 4;
-  const int64_t* ib = c.idx + static_cast<size_t>(b) * c.N;
-  const uint8_t* vb = c.valid + static_cast<size_t>(b) * c.N;
-  const int8_t* fb = fold ? fold + static_cast<size_t>(b) * c.N : nullptr;
-  float rsum = 0.f, psum = 0.f, isum = 0.f;
-  for (int j = lane; j < nhi; j += 64) {
-    float ss, sp, cc, sr;
-    scores(c, b, t, j, ckt, ss, sp, cc, sr);
-    const size_t o = static_cast<size_t>(row) * c.N + j;
-    if (allow_at(c.mode, ib[j], vb[j] != 0, t)) {
-      const float d = dPV[o];
-      rsum += __expf(ss - st6[0]) * is * d;
-      psum += __expf(sp - st6[2]) * ip * d;
-    }
-    if (induct_at(c.mode, ib[j], vb[j] != 0, t, c.T))
-      isum += __expf(ss - st6[4]) * ii * (fb ? dPV[o + fb[j]] : dPVn[o]);
+// Per-slot operands of the row kernels, packed once per read (32 bytes, two 16-byte loads):
+// key bias + admission, the bank cocktail, and the two mask limits -- slot j is readable by
+// query t when alim <= t and enters the induction softmax when ilim < t (INT_MAX: never,
+// INT_MIN: always), which is allow_at / induct_at of its index and validity.
+struct alignas(16) SlotPack {
+  float kbadm, c0, c1, c2, c3;
+  int alim, ilim, pad;
+};
+
+__global__ void __launch_bounds__(256) pack_kernel(int T, int N, int mode, const float* kb,
+                                                   const float* adm, const float* cb,
+                                                   const int64_t* idx, const uint8_t* valid,
+                                                   SlotPack* pk) {
+  const int b = blockIdx.y;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= N) return;
+  const size_t bj = static_cast<size_t>(b) * N + j;
+  SlotPack s;
+  s.kbadm = kb[bj] + adm[bj];
+  s.c0 = cb[bj * 4 + 0];
+  s.c1 = cb[bj * 4 + 1];
+  s.c2 = cb[bj * 4 + 2];
+  s.c3 = cb[bj * 4 + 3];
+  const int64_t i = idx[bj];
+  const int ii = static_cast<int>(i < INT_MIN ? INT_MIN : (i > INT_MAX ? INT_MAX : i));
+  if (valid[bj] == 0) {
+    s.alim = s.ilim = INT_MAX;
+  } else if (mode != 0) {
+    s.alim = INT_MIN;
+    s.ilim = i < T - 1 ? INT_MIN : INT_MAX;
+  } else {
+    s.alim = ii;
+    s.ilim = ii;
   }
-  rsum = wave_sum(rsum);
-  psum = wave_sum(psum);
-  isum = wave_sum(isum);
-  if (lane == 0) {
-    float* o = rowA + static_cast<size_t>(row) * 3;
-    o[0] = rsum; o[1] = psum; o[2] = isum;
+  s.pad = 0;
+  pk[bj] = s;
+}
+
+// Query rows per wave of the grouped row kernels: RW consecutive rows of one batch row share
+// the slot loads and the slot limit of their 128-row tile (RW divides TILE). Measured at
+// config 4: the softmax is fastest with 2 rows per wave, the gradient row sums with 1
+// (their three loads per element already keep a wave busy).
+constexpr int RW_SOFTMAX = 2, RW_GRAD = 1;
+static_assert(TILE % RW_SOFTMAX == 0 && TILE % RW_GRAD == 0,
+              "row groups must not straddle a query tile");
+
+// softmax_fwd_kernel for RW rows per wave: the row statistics and (PV non-null) P_V / P_Vn,
+// with the slot operands read once per RW rows from the pack.
+template <typename E, int RW>
+__global__ void __launch_bounds__(NTH) softmax_fwd_rows_kernel(int B, RowCtx c, Gains g,
+                                                               const float* scale_p,
+                                                               const int32_t* rs,
+                                                               const SlotPack* pk,
+                                                               const int8_t* fold, float* stats,
+                                                               E* PV, E* PVn) {
+  const int lane = threadIdx.x & 63;
+  const int groups = (c.T + RW - 1) / RW;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * NWV + (threadIdx.x >> 6);
+  if (gid >= static_cast<int64_t>(B) * groups) return;
+  const int b = static_cast<int>(gid / groups), t0 = static_cast<int>(gid % groups) * RW;
+  const int nr = min(RW, c.T - t0);
+  const float scale = scale_p[0], sg = g.p[0][0], pg = g.p[1][0], ig = g.p[2][0], cg = g.p[3][0];
+  const int QT = (c.T + TILE - 1) / TILE;
+  const int nhi = rs[(static_cast<size_t>(b) * QT + t0 / TILE) * 3 + 2];
+  const size_t row0 = static_cast<size_t>(b) * c.T + t0;
+  float ck[RW][4], ms[RW], ls[RW], mp[RW], lp[RW], mi[RW], li[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ck[r][k] = r < nr ? c.ck[(row0 + r) * 4 + k] : 0.f;
+    ms[r] = mp[r] = mi[r] = -INFINITY;
+    ls[r] = lp[r] = li[r] = 0.f;
+  }
+  const SlotPack* pb = pk + static_cast<size_t>(b) * c.N;
+  const float* Sr = c.S + row0 * c.N;
+  for (int j = lane; j < nhi; j += 64) {
+    const SlotPack sp = pb[j];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      if (r >= nr) continue;
+      const int t = t0 + r;
+      const float ss = Sr[static_cast<size_t>(r) * c.N + j] * scale + sp.kbadm;
+      const float cc = ck[r][0] * sp.c0 + ck[r][1] * sp.c1 + ck[r][2] * sp.c2 + ck[r][3] * sp.c3;
+      if (sp.alim <= t) {
+        online_add(ss, ms[r], ls[r]);
+        online_add(ss + cc * cg, mp[r], lp[r]);
+      }
+      if (sp.ilim < t) online_add(ss, mi[r], li[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    wave_softmax_stats(ms[r], ls[r]);
+    wave_softmax_stats(mp[r], lp[r]);
+    wave_softmax_stats(mi[r], li[r]);
+    if (lane == 0 && r < nr) {
+      float* o = stats + (row0 + r) * 6;
+      o[0] = ms[r]; o[1] = ls[r]; o[2] = mp[r]; o[3] = lp[r]; o[4] = mi[r]; o[5] = li[r];
+    }
+  }
+  if (PV == nullptr) return;
+  float is[RW], ip[RW], ii[RW], carry[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    is[r] = ls[r] > 0.f ? 1.0f / ls[r] : 0.f;
+    ip[r] = lp[r] > 0.f ? 1.0f / lp[r] : 0.f;
+    ii[r] = li[r] > 0.f ? 1.0f / li[r] : 0.f;
+    carry[r] = 0.f;
+  }
+  const int8_t* fb = fold ? fold + static_cast<size_t>(b) * c.N : nullptr;
+  // Folded: as softmax_fwd_kernel, per row (the induction weight of slot j moves to column
+  // j + 1 through a lane shuffle, lane 63's to the next 64 columns through carry[r]).
+  for (int j0 = 0; j0 < nhi; j0 += 64) {
+    const int j = j0 + lane;
+    const bool in = j < nhi;
+    SlotPack sp = pb[in ? j : 0];
+    const int fj = (fb && in) ? fb[j] : 0;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      if (r >= nr) continue;
+      const int t = t0 + r;
+      float pv = 0.f, pn = 0.f;
+      if (in) {
+        const float ss = Sr[static_cast<size_t>(r) * c.N + j] * scale + sp.kbadm;
+        const float cc = ck[r][0] * sp.c0 + ck[r][1] * sp.c1 + ck[r][2] * sp.c2 + ck[r][3] * sp.c3;
+        if (sp.alim <= t)
+          pv = sg * (__expf(ss - ms[r]) * is[r]) + pg * (__expf(ss + cc * cg - mp[r]) * ip[r]);
+        if (sp.ilim < t) pn = ig * (__expf(ss - mi[r]) * ii[r]);
+      }
+      const size_t o = (row0 + r) * c.N + j;
+      if (fb) {
+        const float ahead = fj == 1 ? pn : 0.f;
+        float from_prev = __shfl_up(ahead, 1, 64);
+        if (lane == 0) from_prev = carry[r];
+        carry[r] = __shfl(ahead, 63, 64);
+        if (in) st(PV, o, (pv + (fj == 0 ? pn : 0.f)) + from_prev);
+      } else if (in) {
+        st(PV, o, pv);
+        st(PVn, o, pn);
+      }
+    }
+  }
+}
+
+// Per-row reductions needed by the score gradient, rowA = (sum Ps dPV, sum Pp dPV,
+// sum Pi dPVn) unscaled by the gains, for RW rows per wave with the packed slot operands
+// (with a successor fold the induction term reads column j + fold[j] of dP_V).
+template <int RW>
+__global__ void __launch_bounds__(NTH) grad_rows_grouped_kernel(int B, RowCtx c, Gains g,
+                                                                const float* scale_p,
+                                                                const int32_t* rs_rng,
+                                                                const SlotPack* pk,
+                                                                const float* stats,
+                                                                const int8_t* fold,
+                                                                const float* dPV,
+                                                                const float* dPVn, float* rowA) {
+  const int lane = threadIdx.x & 63;
+  const int groups = (c.T + RW - 1) / RW;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * NWV + (threadIdx.x >> 6);
+  if (gid >= static_cast<int64_t>(B) * groups) return;
+  const int b = static_cast<int>(gid / groups), t0 = static_cast<int>(gid % groups) * RW;
+  const int nr = min(RW, c.T - t0);
+  const float scale = scale_p[0], cg = g.p[3][0];
+  const int QT = (c.T + TILE - 1) / TILE;
+  const int nhi = rs_rng[(static_cast<size_t>(b) * QT + t0 / TILE) * 3 + 2];
+  const size_t row0 = static_cast<size_t>(b) * c.T + t0;
+  float ck[RW][4], m[RW][3], inv[RW][3], acc[RW][3];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const float* st6 = stats + (row0 + min(r, nr - 1)) * 6;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      m[r][k] = st6[2 * k];
+      inv[r][k] = st6[2 * k + 1] > 0.f ? 1.0f / st6[2 * k + 1] : 0.f;
+      acc[r][k] = 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ck[r][k] = c.ck[(row0 + min(r, nr - 1)) * 4 + k];
+  }
+  const SlotPack* pb = pk + static_cast<size_t>(b) * c.N;
+  const int8_t* fb = fold ? fold + static_cast<size_t>(b) * c.N : nullptr;
+  for (int j = lane; j < nhi; j += 64) {
+    const SlotPack sp = pb[j];
+    const int dn = fb ? fb[j] : 0;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      if (r >= nr) continue;
+      const int t = t0 + r;
+      const size_t o = (row0 + r) * c.N + j;
+      const float ss = c.S[o] * scale + sp.kbadm;
+      if (sp.alim <= t) {
+        const float cc = ck[r][0] * sp.c0 + ck[r][1] * sp.c1 + ck[r][2] * sp.c2 + ck[r][3] * sp.c3;
+        const float d = dPV[o];
+        acc[r][0] += __expf(ss - m[r][0]) * inv[r][0] * d;
+        acc[r][1] += __expf(ss + cc * cg - m[r][1]) * inv[r][1] * d;
+      }
+      if (sp.ilim < t)
+        acc[r][2] += __expf(ss - m[r][2]) * inv[r][2] * (fb ? dPV[o + dn] : dPVn[o]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const float a0 = wave_sum(acc[r][0]), a1 = wave_sum(acc[r][1]), a2 = wave_sum(acc[r][2]);
+    if (lane == 0 && r < nr) {
+      float* o = rowA + (row0 + r) * 3;
+      o[0] = a0; o[1] = a1; o[2] = a2;
+    }
   }
 }
 
@@ -548,7 +714,8 @@ __global__ void __launch_bounds__(xpose::TNT) fold_transpose_kernel(int R, int C
 
 // Workspace planning.
 struct Plan {
-  size_t off_S, off_rs, off_ro, off_rb, off_stats, off_PV, off_PVn, off_VT, off_VnT, end_fwd;
+  size_t off_S, off_rs, off_ro, off_rb, off_stats, off_PV, off_PVn, off_VT, off_VnT, off_pack,
+      end_fwd;
   size_t off_dPV, off_dPVn, off_Gs, off_rowA, off_rowB, off_colp, off_part, off_KT, off_QT,
       off_gOT, off_GsT, off_PVT, off_PVnT, end_bwd;
 };
@@ -571,6 +738,7 @@ static Plan plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
   const size_t NH = static_cast<size_t>(B) * N * H, TH = static_cast<size_t>(B) * T * H;
   p.off_VT = o; o = align_up(o + NH * e);
   p.off_VnT = o; o = align_up(o + NH * e);
+  p.off_pack = o; o = align_up(o + static_cast<size_t>(B) * N * sizeof(SlotPack));
   p.end_fwd = o;
   const size_t NCC = (N + CC - 1) / CC, RTILES = (T + RT - 1) / RT;
   p.off_dPV = o; o = align_up(o + TN * 4);
@@ -637,9 +805,17 @@ static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, 
     DABSN_HIP_CHECK((gemm::launch<E, float>(a, (int)B, stream)));
   }
   RowCtx c{(int)T, (int)N, mode, S, kb, adm, cb, ck, idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
-  const unsigned row_blocks = static_cast<unsigned>((B * T + NWV - 1) / NWV);
-  hipLaunchKernelGGL(softmax_fwd_kernel<E>, dim3(row_blocks), dim3(NTH), 0, stream, B * T, c, g,
-                     scale, rs, fold, stats, write_p ? PV : static_cast<E*>(nullptr),
+  SlotPack* pk = ws.at<SlotPack>(p.off_pack);
+  if (N > 0) {
+    hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)B), dim3(256), 0,
+                       stream, (int)T, (int)N, mode, kb, adm, cb, idx, valid, pk);
+    DABSN_HIP_CHECK(hipGetLastError());
+  }
+  const int64_t groups = B * ((T + RW_SOFTMAX - 1) / RW_SOFTMAX);
+  hipLaunchKernelGGL((softmax_fwd_rows_kernel<E, RW_SOFTMAX>),
+                     dim3((unsigned)((groups + NWV - 1) / NWV)),
+                     dim3(NTH), 0, stream, (int)B, c, g, scale, rs, pk, fold, stats,
+                     write_p ? PV : static_cast<E*>(nullptr),
                      write_p && !fold ? PVn : static_cast<E*>(nullptr));
   DABSN_HIP_CHECK(hipGetLastError());
   if (!write_p) return DABSN_OK;
@@ -705,8 +881,18 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
     DABSN_HIP_CHECK((gemm::launch<E, float>(a, (int)B, stream)));
   }
   RowCtx c{(int)T, (int)N, mode, S, kb, adm, cb, ck, idx, valid, 0.f, 0.f, 0.f, 0.f, 0.f};
-  hipLaunchKernelGGL(grad_rows_kernel, dim3((unsigned)((B * T + NWV - 1) / NWV)), dim3(NTH), 0,
-                     stream, B * T, c, g, scale, rs, stats, fold, dPV, dPVn, rowA);
+  // The slot pack lives in the forward's scratch, which a kept-workspace forward does not
+  // hand over: rebuilt here (B N 32 bytes).
+  SlotPack* pk = ws.at<SlotPack>(p.off_pack);
+  if (N > 0) {
+    hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)B), dim3(256), 0,
+                       stream, (int)T, (int)N, mode, kb, adm, cb, idx, valid, pk);
+    DABSN_HIP_CHECK(hipGetLastError());
+  }
+  const int64_t groups = B * ((T + RW_GRAD - 1) / RW_GRAD);
+  hipLaunchKernelGGL(grad_rows_grouped_kernel<RW_GRAD>, dim3((unsigned)((groups + NWV - 1) / NWV)),
+                     dim3(NTH), 0, stream, (int)B, c, g, scale, rs, pk, stats, fold, dPV, dPVn,
+                     rowA);
   DABSN_HIP_CHECK(hipGetLastError());
   const int NCC = static_cast<int>((N + CC - 1) / CC), RTILES = static_cast<int>((T + RT - 1) / RT);
   if (N > 0) {

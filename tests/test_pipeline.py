@@ -164,3 +164,42 @@ def test_block_pipelined_matches_sequential(cuda_device, monkeypatch):
         limit = 1e-4 if g0[n].numel() == 1 else 1e-5
         err = _rel(g1[n], g0[n], False, floor)
         assert err <= limit, f"{n}: {err:.3e}"
+
+
+@pytest.mark.parametrize("dtypes", [(torch.bfloat16, torch.bfloat16, torch.float32),
+                                    (torch.float32, torch.float32, torch.float32),
+                                    (torch.bfloat16, torch.bfloat16, torch.bfloat16)])
+@pytest.mark.parametrize("B,T,H,bounds", [(3, 40, 24, [(0, 16), (16, 31), (31, 40)]),
+                                          (2, 17, 5, [(0, 9), (9, 17)])])
+def test_read_output_windows_equal_the_whole_op(cuda_device, dtypes, B, T, H, bounds):
+    """``ops.read_output_window`` / ``read_output_bwd_window`` over a partition of the time
+    axis against ``read_output`` and its backward on the whole tensors: outputs and the
+    projection / long gradients bit for bit (the same arithmetic per element, vector path at
+    H = 24, scalar path at H = 5), the gain gradient as the sum of the window shares (another
+    summation order: within 1e-6 of the sum of its terms' magnitudes)."""
+    from dabsn_amd.kernels import ops
+
+    pd, ld, gd = dtypes
+    g = torch.Generator().manual_seed(T + H)
+    proj = torch.randn(B, T, H, generator=g).to(cuda_device, pd)
+    lng = torch.randn(B, T, H, generator=g).to(cuda_device, ld)
+    gain = torch.tensor([0.37], device=cuda_device, dtype=gd).reshape(())
+    whole = ops.read_output(proj, lng, gain)
+    out = torch.full_like(whole, float("nan"))
+    for t0, t1 in bounds:
+        ops.read_output_window(proj, lng, gain, out, t0, t1)
+    assert torch.equal(out, whole)
+
+    grad = torch.randn(B, T, H, generator=g).to(cuda_device, whole.dtype)
+    gp_w, gl_w, gg_w = ops.read_output_backward(grad, lng, gain, ops._code(pd))
+    gp, gl = torch.empty_like(proj), torch.empty_like(lng)
+    shares = torch.zeros(len(bounds), device=cuda_device, dtype=torch.float32)
+    for k, (t0, t1) in enumerate(bounds):
+        ops.read_output_bwd_window(grad, lng, gain, gp, gl, shares[k:k + 1], t0, t1)
+    assert torch.equal(gp, gp_w) and torch.equal(gl, gl_w)
+    want = float(gg_w.float())
+    # Relative to the sum of |terms|: the gain's gradient sums B*T*H products of both signs.
+    scale = float((grad.double() * lng.double()).abs().sum())
+    # read_output_backward returns the gain's gradient in the gain's dtype (bf16: rounded).
+    rounding = abs(want) * 2.0 ** -8 if gd == torch.bfloat16 else 0.0
+    assert abs(float(shares.sum()) - want) <= 1e-6 * scale + rounding
