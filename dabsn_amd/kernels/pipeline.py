@@ -255,7 +255,9 @@ class _PipelinedScanRead(torch.autograd.Function):
                 _stats_window(out, stats, t0, t1, st.cuda_stream)
                 pre = F.linear(ops.window_copy(U[:, t0:t1]).view(B * C, 2 * H), Wd[:, :2 * H], bd)
                 with torch.enable_grad():
-                    ay_leaf = ay[:, t0:t1].detach().requires_grad_(True)
+                    # A contiguous copy of the expression window as the leaf (the read's
+                    # normalisation reads it densely).
+                    ay_leaf = ops.window_copy(ay[:, t0:t1]).requires_grad_(True)
                     r = read.query_bank_retrieved(
                         ay_leaf, query_stats=stats_leaf[:, t0:t1], bank_write=w_leaf,
                         bank_norms=norms, bank_stats=stats_leaf[:, :t1], query_start=t0,
@@ -492,9 +494,11 @@ class _PipelinedScanRead(torch.autograd.Function):
                 # The projection's weight gradients, beside the last reverse scan.
                 U2 = fwd_out.U.reshape(B * T, 2 * H)
                 g_short = g_short3.reshape(B * T, H)
-                gw = torch.cat((g_short.t() @ U2, g_short.t() @ retr.reshape(B * T, H)), dim=1)
-                W.grad = gw.to(W.dtype)
-                bias.grad = g_short.float().sum(0).to(bias.dtype)
+                gw = torch.empty((H, 3 * H), device=dev, dtype=W.dtype)
+                gw[:, :2 * H] = g_short.t() @ U2
+                gw[:, 2 * H:] = g_short.t() @ retr.reshape(B * T, H)
+                W.grad = gw
+                bias.grad = torch.sum(g_short, dim=0, dtype=torch.float32).to(bias.dtype)
                 if K > 1:
                     R.wait_event(scan_back[1])
                     core_weight_grads(*bounds[1])

@@ -14,6 +14,7 @@ launch), so the same counters read on it give the scale between counter units an
     python -m dabsn_amd.profiling <results.db> [--top N] [--match REGEX] [--tail MARKER:N]
     python -m dabsn_amd.profiling <results.db> --categories STEPS
     python -m dabsn_amd.profiling --pmc-summary <dir> [--match REGEX]
+    python -m dabsn_amd.profiling --mfma-dispatches <dir>
     python -m dabsn_amd.profiling --copy-probe <MiB>
     python -m dabsn_amd.profiling --pmc-json <out.json> --fetch <dir> --write <dir> \
         --copy-fetch <dir> --copy-write <dir> --copy-mib 512 --batch B --seq T --state H --chunk C
@@ -122,6 +123,34 @@ def pmc_summary(directory: str, match: str | None = None) -> list[dict[str, obje
     return out
 
 
+def mfma_dispatches(directory: str, cus: int = 256, simds_per_cu: int = 4,
+                    xcds: int = 8) -> list[dict[str, object]]:
+    """Per dispatch of a ``--pmc SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_VALU_MFMA_BUSY_CYCLES
+    GRBM_GUI_ACTIVE`` run, in dispatch order: bf16 MFMA flops (512 per MOPS unit), MFMA
+    utilisation = busy SIMD cycles / (GRBM_GUI_ACTIVE / xcds x SIMDs) and the profiled
+    duration."""
+    import csv
+    import glob
+    rows: dict[int, dict[str, object]] = {}
+    for path in glob.glob(f"{directory}/**/*counter_collection.csv", recursive=True):
+        with open(path, newline="") as fh:
+            for r in csv.DictReader(fh):
+                d = rows.setdefault(int(r["Dispatch_Id"]), {
+                    "kernel": r["Kernel_Name"], "grid": int(r["Grid_Size"]),
+                    "ms": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6})
+                d[r["Counter_Name"]] = float(r["Counter_Value"])
+    out = []
+    for did in sorted(rows):
+        d = rows[did]
+        busy = d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+        active = d.get("GRBM_GUI_ACTIVE", 0.0) / xcds * cus * simds_per_cu
+        flops = 512.0 * d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
+        out.append({"dispatch": did, "kernel": d["kernel"], "grid": d["grid"], "ms": d["ms"],
+                    "tflop": flops / 1e12, "busy": busy, "active": active,
+                    "util": busy / active if active else 0.0})
+    return out
+
+
 def copy_probe(mib: int, reps: int = 5) -> None:
     """Launch ``reps`` elementwise copies (torch.neg) that each read and write ``mib`` MiB."""
     import torch
@@ -189,6 +218,8 @@ def main() -> None:
     p.add_argument("--categories", type=int, default=None, metavar="STEPS",
                    help="milliseconds per step by kernel category, the trace holding STEPS steps")
     p.add_argument("--pmc-summary", default=None)
+    p.add_argument("--mfma-dispatches", default=None, metavar="DIR",
+                   help="per-dispatch MFMA flops and utilisation of a counter run")
     p.add_argument("--copy-probe", type=int, default=None)
     p.add_argument("--pmc-json", default=None)
     for k in ("fetch", "write", "copy-fetch", "copy-write"):
@@ -208,6 +239,18 @@ def main() -> None:
                   f"({k['dispatches']} dispatches)")
     elif args.copy_probe:
         copy_probe(args.copy_probe)
+    elif args.mfma_dispatches:
+        rows = mfma_dispatches(args.mfma_dispatches)
+        print("| dispatch | output | grid | TFLOP | MFMA busy cycles | util | ms (profiled) | TFLOP/s |")
+        print("|---|---|---|---|---|---|---|---|")
+        for r in rows:
+            outt = "fp32" if ", float," in r["kernel"] else "bf16"
+            print(f"| {r['dispatch']} | {outt} | {r['grid']} | {r['tflop']:.3f} | {r['busy']:.3e} | "
+                  f"{r['util']:.3f} | {r['ms']:.3f} | {r['tflop'] / r['ms'] * 1e3 if r['ms'] else 0:.0f} |")
+        busy = sum(r["busy"] for r in rows)
+        active = sum(r["active"] for r in rows)
+        print(f"\n{len(rows)} dispatches: {sum(r['tflop'] for r in rows):.2f} TFLOP, MFMA utilisation "
+              f"{busy / active if active else 0:.3f} (busy-cycle weighted)")
     elif args.pmc_summary:
         for r in pmc_summary(args.pmc_summary, args.match):
             name = r["kernel"] if len(r["kernel"]) <= 90 else r["kernel"][:87] + "..."
