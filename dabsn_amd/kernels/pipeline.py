@@ -13,7 +13,7 @@ it runs. Here the scan runs on one CU-masked stream (16 CUs of every XCD, plain 
   positions [0, end of chunk k)) and the long channel over window k (its recurrent state
   carried from window k - 1) run beside it; the last chunk's read and the read output
   follow on the whole device, the last window's long channel beside them;
-* backward: the read output first, the long channel's last two windows on the read half
+* backward: the read output first, the long channel's last window on the read half
   beside the last chunk's projection and read backward, then per chunk, last chunk first,
   the projection, read and long-channel backward of window k complete its tape gradients
   (its query rows, and the bank rows of window k, which only query chunks >= k read), the
@@ -424,17 +424,17 @@ class _PipelinedScanRead(torch.autograd.Function):
 
         with torch.cuda.stream(M):
             # The read output's backward over the last window; then the long channel's last
-            # windows on the read half (enqueued first, so that its kernels hold their CUs)
-            # beside the last chunk's projection and read backward on the whole device.
+            # window on the read half (enqueued first, so that its kernels hold their CUs)
+            # beside the last chunk's projection and read backward on the whole device. The
+            # other windows' long channel runs in the read half's per-chunk work (measured:
+            # a second window at the head slows the last chunk's read backward by 0.45 ms,
+            # more than it saves later).
             read_out_backward(K - 1)
             head = torch.cuda.Event()
             head.record(M)
             R.wait_event(head)
-            head_windows = min(K, 2)
             with torch.cuda.stream(R):
-                for k in range(K - 1, K - 1 - head_windows, -1):
-                    read_out_backward(k)
-                    long_backward(k)
+                long_backward(K - 1)
 
             carry = [None, None, None]
             bws = []
@@ -459,7 +459,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                     done.record(st)
                     R.wait_event(done)
                 with torch.cuda.stream(R):
-                    if k < K - head_windows:
+                    if k < K - 1:
                         long_backward(k)
                     # Window k of the write gradient is complete (only query chunks >= k
                     # read it): the long channel's share joins it.
