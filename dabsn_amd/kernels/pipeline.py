@@ -369,8 +369,11 @@ class _PipelinedScanRead(torch.autograd.Function):
         gain_leaf = param_leaves["long_gain"]
         gain_parts = torch.zeros((K,), device=dev, dtype=torch.float32)
         out_done = [False] * K
-        # dL/dUg and dL/dA summed over windows as their reverse scans finish.
-        gUg_sum, gA_sum = (torch.zeros((H, H), device=dev, dtype=torch.float32) for _ in range(2))
+        # dL/d[Ug; A] summed over windows as their reverse scans finish, with the scans'
+        # per-workgroup parameter partials.
+        gUA_sum = torch.zeros((2 * H, H), device=dev, dtype=torch.float32)
+        vec_parts: list = []
+        scal_parts: list = []
         for st in (M, S, R):
             st.wait_stream(ambient)
 
@@ -392,12 +395,18 @@ class _PipelinedScanRead(torch.autograd.Function):
                     torch.add(g_in[:, t0:t1], g_proj, out=dst)
             return ops.window_copy(prod[:, 2 * H:].view(B, C, H))
 
-        def core_weight_grads(t0: int, t1: int) -> None:
-            # dL/dUg and dL/dA over window [t0, t1): the reverse scan's dWgx and da_y rows
-            # times the trajectory's y rows, summed over the window's rows.
+        def core_weight_grads(k: int) -> None:
+            # dL/d[Ug; A] over window k: the reverse scan's [dWgx, da_y] rows times the
+            # trajectory's y rows, summed over the window's rows (one GEMM), and the scan's
+            # parameter partials reduced.
+            t0, t1 = bounds[k]
             y = ops.window_copy(fwd_out.U[:, t0:t1, :H]).view(-1, H)
-            gUg_sum.add_(ops.window_copy(gWgx[:, t0:t1]).view(-1, H).t() @ y)
-            gA_sum.add_(ops.window_copy(day[:, t0:t1]).view(-1, H).t() @ y)
+            gd = torch.empty((B, t1 - t0, 2 * H), device=dev, dtype=dt)
+            ops.window_add(gd[..., :H], gWgx[:, t0:t1])
+            ops.window_add(gd[..., H:], day[:, t0:t1])
+            gUA_sum.add_(gd.view(-1, 2 * H).t() @ y)
+            vec_parts.append(bw_of[k].part_vec.sum(0))
+            scal_parts.append(bw_of[k].part_scal.sum(0))
 
         def read_out_backward(k: int) -> None:
             if not out_done[k]:
@@ -407,7 +416,7 @@ class _PipelinedScanRead(torch.autograd.Function):
 
         logit_leaves = [param_leaves[n] for n in _LONG_LOGITS]
         long_grads: list = [None] * K     # per window: (g_write, g_plasticity)
-        logit_parts: list = [None] * K    # per window: the four logits' shares
+        logit_sum: list = [None]          # the four logits' gradients, summed window by window
         state_grad: list = [None, None, None]
 
         def long_backward(k: int) -> None:
@@ -419,7 +428,8 @@ class _PipelinedScanRead(torch.autograd.Function):
             g = ops.long_scan_fused_backward(wk, pk, logit_leaves, states,
                                              ops.window_copy(g_long[:, t0:t1]), *state_grad)
             long_grads[k] = (g[0], g[1])
-            logit_parts[k] = g[2:6]
+            part = torch.stack(g[2:6])
+            logit_sum[0] = part if logit_sum[0] is None else logit_sum[0] + part
             state_grad[:] = g[6:9]
 
         with torch.cuda.stream(M):
@@ -439,6 +449,7 @@ class _PipelinedScanRead(torch.autograd.Function):
             carry = [None, None, None]
             bws = []
             scan_back: list[Optional[torch.cuda.Event]] = [None] * K
+            bw_of: dict = {}
             for k in range(K - 1, -1, -1):
                 t0, t1 = bounds[k]
                 r, ay_leaf = chunks[k]
@@ -475,7 +486,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                     # The reverse scan of window k + 2 finished before that of k + 1 began.
                     if k + 2 < K:
                         R.wait_event(scan_back[k + 2])
-                        core_weight_grads(*bounds[k + 2])
+                        core_weight_grads(k + 2)
                 with torch.cuda.stream(S):
                     S.wait_event(tapes_ready)
                     up = [gU, g_nov, g_p, g_ay, sink, g_e, g_c]
@@ -486,6 +497,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                     bw.launch(S)
                     ops.KernelTimer.end(tk)
                     bws.append(bw)
+                    bw_of[k] = bw
                     carry = bw.g0
                     ev = torch.cuda.Event()
                     ev.record(S)
@@ -501,21 +513,18 @@ class _PipelinedScanRead(torch.autograd.Function):
                 bias.grad = torch.sum(g_short, dim=0, dtype=torch.float32).to(bias.dtype)
                 if K > 1:
                     R.wait_event(scan_back[1])
-                    core_weight_grads(*bounds[1])
+                    core_weight_grads(1)
             M.wait_stream(S)
             M.wait_stream(R)
-            core_weight_grads(*bounds[0])
+            core_weight_grads(0)
             if gain_leaf.requires_grad:
                 gain_leaf.grad = gain_parts.sum().reshape(gain_leaf.shape).to(gain_leaf.dtype)
             for i, leaf in enumerate(logit_leaves):
                 if leaf.requires_grad:
-                    total = logit_parts[K - 1][i]
-                    for k in range(K - 2, -1, -1):  # the order the windows were walked
-                        total = total + logit_parts[k][i]
-                    leaf.grad = total.reshape(leaf.shape).to(leaf.dtype)
-            gvec = torch.stack([bw.part_vec.sum(0) for bw in bws]).sum(0)
-            gscal = torch.stack([bw.part_scal.sum(0) for bw in bws]).sum(0)
-            core = [gWx, gWgx, gUg_sum, gA_sum, *[gvec[i] for i in range(16)],
+                    leaf.grad = logit_sum[0][i].reshape(leaf.shape).to(leaf.dtype)
+            gvec = torch.stack(vec_parts).sum(0)
+            gscal = torch.stack(scal_parts).sum(0)
+            core = [gWx, gWgx, gUA_sum[:H], gUA_sum[H:], *[gvec[i] for i in range(16)],
                     *[gscal[i] for i in range(3)]]
             core = [g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(core, ctx.meta)]
             grads = [p.grad for p in pleaves]
