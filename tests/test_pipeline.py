@@ -16,7 +16,9 @@ only summation orders differ:
     schedule);
   * dense banks (the successor fold) and partially admitted ones (no fold, a bank width
     that grows chunk by chunk); losses with and without budget (a block mixes only y into
-    its output); a DABSNBlock with block chunking, pipelined or not.
+    its output); a DABSNBlock with block chunking, pipelined or not;
+  * the window entry points the pipeline hands its pieces through (read output and its
+    backward per window, window copies and adds) against the whole-tensor operations.
 """
 
 from __future__ import annotations
@@ -203,3 +205,30 @@ def test_read_output_windows_equal_the_whole_op(cuda_device, dtypes, B, T, H, bo
     # read_output_backward returns the gain's gradient in the gain's dtype (bf16: rounded).
     rounding = abs(want) * 2.0 ** -8 if gd == torch.bfloat16 else 0.0
     assert abs(float(shares.sum()) - want) <= 1e-6 * scale + rounding
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("H", [24, 5])
+def test_window_add_equals_torch(cuda_device, dtype, H):
+    """``ops.window_add`` / ``window_copy`` on time windows and column blocks of strided
+    tensors against torch's copy and add: bit for bit (the bf16 sum formed in fp32 and
+    rounded once, as torch's add), on the 16-byte path (H = 24) and the scalar path (H = 5),
+    in place (out aliasing a) and with the operands' strides all different."""
+    from dabsn_amd.kernels import ops
+
+    g = torch.Generator().manual_seed(H)
+    B, T = 3, 37
+    a = torch.randn(B, T, 2 * H, generator=g).to(cuda_device, dtype)
+    x = torch.randn(B, T + 5, H, generator=g).to(cuda_device, dtype)
+    out = torch.randn(B, T, H, generator=g).to(cuda_device, dtype)
+    t0, t1 = 9, 30
+    want = out.clone()
+    want[:, t0:t1] = a[:, t0:t1, H:] + x[:, t0 + 2:t1 + 2]
+    ops.window_add(out[:, t0:t1], a[:, t0:t1, H:], x[:, t0 + 2:t1 + 2])
+    assert torch.equal(out, want)
+    before = out.clone()
+    ops.window_add(out[:, t0:t1], out[:, t0:t1], x[:, :t1 - t0])  # in place
+    assert torch.equal(out[:, t0:t1], before[:, t0:t1] + x[:, :t1 - t0])
+    assert torch.equal(out[:, :t0], before[:, :t0]) and torch.equal(out[:, t1:], before[:, t1:])
+    c = ops.window_copy(a[:, t0:t1, :H])
+    assert c.is_contiguous() and torch.equal(c, a[:, t0:t1, :H])
