@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 _lock = threading.Lock()
 _lib = None
@@ -76,6 +76,7 @@ _SIGNATURES = {
     ),
     "dabsn_hip_stream_pair": (
         [ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(i32), ctypes.POINTER(i32)], i32),
+    "dabsn_hip_stream_destroy": ([vp], i32),
     "dabsn_hip_tape_stats_window": (
         [i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i64, vp], i32),
     "dabsn_hip_tape_stats_bwd_window": (

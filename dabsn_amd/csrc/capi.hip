@@ -79,4 +79,11 @@ int dabsn_hip_stream_pair(hipStream_t* a, hipStream_t* b, int* cus_a, int* cus_b
   return DABSN_OK;
 }
 
+int dabsn_hip_stream_destroy(hipStream_t stream) {
+  DABSN_REQUIRE(stream != nullptr, "stream destroy: null stream");
+  DABSN_HIP_CHECK(hipStreamSynchronize(stream));
+  DABSN_HIP_CHECK(hipStreamDestroy(stream));
+  return DABSN_OK;
+}
+
 }  // extern "C"

@@ -33,6 +33,7 @@ the whole-sequence read's rows; the tape gradients sum their chunk contributions
 
 from __future__ import annotations
 
+import atexit
 import contextlib
 import ctypes
 import os
@@ -74,8 +75,25 @@ def stream_pair(device: torch.device):
         pair = (torch.cuda.ExternalStream(a.value, device=dev),
                 torch.cuda.ExternalStream(b.value, device=dev), int(ca.value),
                 torch.cuda.Stream(device=dev))
+        if not _PAIRS:
+            atexit.register(release_streams)
         _PAIRS[idx] = pair
     return pair
+
+
+def release_streams() -> None:
+    """Wait for and destroy the CU-masked stream pairs (each is a hardware queue of its own).
+    Registered to run at interpreter exit, ahead of the HIP runtime's own teardown: a
+    process that still holds such queues when the runtime's library destructors run ends
+    with a fault there under a profiler."""
+    lib = _lib.load()
+    for idx, (S, R, _, _) in list(_PAIRS.items()):
+        with torch.cuda.device(idx):
+            torch.cuda.synchronize()
+            for st in (S, R):
+                _lib.check(lib.dabsn_hip_stream_destroy(ctypes.c_void_p(st.cuda_stream)),
+                           "stream destroy")
+        del _PAIRS[idx]
 
 
 @contextlib.contextmanager

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 15
+#define DABSN_HIP_ABI_VERSION 16
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -150,8 +150,13 @@ int dabsn_hip_core_scan_bwd_call(const dabsn_core_bwd_call* bwd, hipStream_t str
  * on MI355X each gets 16 CUs of every XCD), for overlapping the persistent core scan
  * (plain launches with coresident_cus = *cus_a) with other work. No reference
  * counterpart: the reference's scan is a sequence of per-step launches. *cus_a and *cus_b
- * receive the CU counts of the two masks. Release with hipStreamDestroy. */
+ * receive the CU counts of the two masks. Release each with dabsn_hip_stream_destroy. */
 int dabsn_hip_stream_pair(hipStream_t* a, hipStream_t* b, int* cus_a, int* cus_b);
+
+/* Waits for the work on a stream made by dabsn_hip_stream_pair and destroys it. No
+ * reference counterpart (the reference makes no streams of its own); the Python binding
+ * calls it at interpreter exit, before the runtime's own teardown. */
+int dabsn_hip_stream_destroy(hipStream_t stream);
 
 /* ---- linear recurrence -----------------------------------------------------------
  * Replaces dabsn::linear_recurrence / dabsn::_linrec_backward

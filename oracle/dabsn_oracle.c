@@ -88,7 +88,9 @@ void oracle_core_scan_fwd(int64_t B, int64_t T, int64_t H,
   const float lam = softplus_(log_lambda);
   const float c_suppress = sigm(logit_c_suppress);
   int64_t bi;
-#pragma omp parallel for schedule(static)
+  /* Rows are independent: with a single row the matvec's output units are split over the
+   * threads instead (each unit's dot product keeps its serial order). */
+#pragma omp parallel for schedule(static) if (B > 1)
   for (bi = 0; bi < B; ++bi) {
     float* b = (float*)malloc(sizeof(float) * H * 6);
     float* e = b + H;
@@ -105,7 +107,9 @@ void oracle_core_scan_fwd(int64_t B, int64_t T, int64_t H,
       const float* wx = Wx + (bi * T + t) * H;
       const float* wgx = Wgx + (bi * T + t) * H;
       for (int64_t i = 0; i < H; ++i) y[i] = tanhf(wx[i] + b[i]);
-      for (int64_t i = 0; i < H; ++i) {
+      int64_t i;
+#pragma omp parallel for schedule(static) if (B == 1)
+      for (i = 0; i < H; ++i) {
         const float* gu = GA + i * H;
         const float* ga = GA + (H + i) * H;
         float su = 0.0f, sa = 0.0f;
@@ -185,8 +189,13 @@ void oracle_core_scan_bwd(int64_t B, int64_t T, int64_t H, const float* GA,
   const float suppress = sigm(logit_c_suppress);
   float* part_vec = (float*)calloc((size_t)B * P_COUNT * H, sizeof(float));
   float* part_scal = (float*)calloc((size_t)B * 3, sizeof(float));
+  /* [Ug; A] transposed once, so the recurrent adjoint below reads each unit's 2H weights
+   * contiguously; its sums run over r in the same order as through GA's columns. */
+  float* GAT = (float*)malloc(sizeof(float) * 2 * H * H);
+  for (int64_t r0 = 0; r0 < 2 * H; ++r0)
+    for (int64_t j = 0; j < H; ++j) GAT[j * 2 * H + r0] = GA[r0 * H + j];
   int64_t bi;
-#pragma omp parallel for schedule(static)
+#pragma omp parallel for schedule(static) if (B > 1)
   for (bi = 0; bi < B; ++bi) {
     float* gbn = (float*)calloc((size_t)H * 6, sizeof(float));
     float* gen = gbn + H;
@@ -298,10 +307,14 @@ void oracle_core_scan_bwd(int64_t B, int64_t T, int64_t H, const float* GA,
         sacc[1] += gb_new * (p * ay) * sig_lam;
         sacc[2] += gnov_eff * nov * (-c_new) * suppress * (1.0f - suppress);
       }
-      /* recurrent adjoint: [dgate_pre; d_expr] @ [Ug; A] -> [H] */
-      for (int64_t j = 0; j < H; ++j) {
+      /* recurrent adjoint: [dgate_pre; d_expr] @ [Ug; A] -> [H] (a single row splits the
+       * units over the threads) */
+      int64_t j;
+#pragma omp parallel for schedule(static) if (B == 1)
+      for (j = 0; j < H; ++j) {
         float s = 0.0f;
-        for (int64_t r = 0; r < 2 * H; ++r) s += dg[r] * GA[r * H + j];
+        const float* gat = GAT + j * 2 * H;
+        for (int64_t r = 0; r < 2 * H; ++r) s += dg[r] * gat[r];
         const float y = u_t[j];
         const float gy = gyx[j] + s;
         const float gpre = gy * (1.0f - y * y);
@@ -334,6 +347,7 @@ void oracle_core_scan_bwd(int64_t B, int64_t T, int64_t H, const float* GA,
   }
   free(part_vec);
   free(part_scal);
+  free(GAT);
   /* grad [Ug; A] = [gWgx; day]^T @ y over all (b, t) */
   int64_t r;
 #pragma omp parallel for schedule(static)

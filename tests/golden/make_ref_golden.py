@@ -19,6 +19,9 @@ Fixtures (reference file:line of the function evaluated):
   reference's own bf16 path, tests/test_batched_runtime.py:83-162) and, on the same
   values, in fp32: outputs and gradients of both, so the reference's bf16-vs-fp32 gap is
   known per gradient.
+* ``core_bf16_gap`` -- the reference's bf16-vs-fp32 distance of the same op at B=2 T=256
+  H=512 and B=1 T=1024 H=2048, per output and gradient, with seeded sketches of its fp32
+  results; the inputs are rebuilt from ``golden_cases.bf16_gap_case``.
 * ``core_loop_fp64`` -- ``DABSNCore._reference_forward_from_state`` (core.py:111-246), the
   per-step torch loop, differentiated by autograd.
 * ``read_seq_fp32`` -- ``DABSNRead.forward`` in seq geometry (read.py:139-438) on a
@@ -170,6 +173,96 @@ def core_op_bf16() -> None:
     arrays.update({f"grad16_{i}": _np(g) for i, g in enumerate(g16) if g is not None})
     arrays.update({f"grad32_{i}": _np(g) for i, g in enumerate(g32) if g is not None})
     _save("core_op_bf16", arrays)
+
+
+def core_bf16_gap() -> None:
+    """The reference's own bf16-vs-fp32 distance of dabsn::core_scan_batched at two larger
+    shapes (B=2 T=256 H=512 and B=1 T=1024 H=2048), per output (normwise max) and per
+    gradient (Frobenius): the bf16 run casts Wx, Wgx, Ug and A (tests/test_batched_runtime.py
+    :83-113), the fp32 run takes the same values in fp32. Inputs and upstream gradients come
+    from the seeded recipe ``golden_cases.bf16_gap_case`` (no large tensor is stored);
+    the fp32 outputs and gradients are kept as seeded sketches and norms, which pin the CPU
+    oracle to the reference's fp32 run at these shapes."""
+    import torch
+
+    import dabsn.kernels.batched_runtime  # noqa: F401  (registers dabsn::core_scan_batched)
+
+    sys.path.insert(0, str(HERE.parent))
+    import golden_cases as gc
+
+    os.environ["DABSN_BATCHED_STEP_COMPILE"] = "0"
+    arrays = {}
+    for name in gc.BF16_GAP_SHAPES:
+        inputs, gout = gc.bf16_gap_case(name)
+        leaves16 = [(x.to(torch.bfloat16) if i < 4 else x).clone().requires_grad_(True)
+                    for i, x in enumerate(inputs)]
+        leaves32 = [x.clone().requires_grad_(True) for x in inputs]
+        outs16 = torch.ops.dabsn.core_scan_batched(*leaves16)
+        outs32 = torch.ops.dabsn.core_scan_batched(*leaves32)
+
+        def loss(outs):
+            return sum((o.float() * g).sum() for o, g in zip(outs, gout) if g is not None)
+
+        g16 = torch.autograd.grad(loss(outs16), leaves16, allow_unused=True)
+        g32 = torch.autograd.grad(loss(outs32), leaves32, allow_unused=True)
+        arrays[f"{name}.checksum_in"] = np.array([float(x.double().sum()) for x in inputs])
+        for i, (a, b) in enumerate(zip(outs16, outs32)):
+            a64, b64 = _np(a).astype(np.float64), _np(b).astype(np.float64)
+            arrays[f"{name}.gap_out{i}"] = np.array(
+                np.abs(a64 - b64).max() / max(np.abs(b64).max(), 1e-30))
+            arrays[f"{name}.sketch_out{i}"] = gc.sketch(b64, 1000 + i)
+            arrays[f"{name}.norm_out{i}"] = np.array(np.linalg.norm(b64))
+        for i, (a, b) in enumerate(zip(g16, g32)):
+            if b is None:
+                continue
+            a64, b64 = _np(a).astype(np.float64), _np(b).astype(np.float64)
+            arrays[f"{name}.gap_grad{i}"] = np.array(
+                np.linalg.norm(a64 - b64) / max(np.linalg.norm(b64), 1e-30))
+            arrays[f"{name}.sketch_grad{i}"] = gc.sketch(b64, 2000 + i)
+            arrays[f"{name}.sketch16_grad{i}"] = gc.sketch(a64, 2000 + i)
+            arrays[f"{name}.norm_grad{i}"] = np.array(np.linalg.norm(b64))
+            if b64.size == 1:
+                arrays[f"{name}.val16_grad{i}"] = a64.reshape(())
+                arrays[f"{name}.val32_grad{i}"] = b64.reshape(())
+        worst = max((float(arrays[k]), k) for k in arrays if k.startswith(f"{name}.gap_grad"))
+        print(f"  {name}: worst reference bf16 gradient gap {worst[0]:.3e} ({worst[1]})")
+    # The end-to-end bf16 cases of tests/test_gpu_ops.py: inputs helpers.core_case(200 + H,
+    # B, T, H) with Wx, Wgx, Ug, A cast to bf16 for the bf16 run and unrounded for the fp32
+    # run, upstream gradients seeded 9 and rounded to bf16 values for both.
+    sys.path.insert(0, str(HERE.parent.parent))
+    from helpers import core_case
+
+    for B, T, H in gc.OPS_BF16_CASES:
+        name = f"ops_B{B}_T{T}_H{H}"
+        inputs = core_case(200 + H, B, T, H)
+        g = torch.Generator().manual_seed(9)
+        shapes = [(B, T, 2 * H)] + [(B, T, H)] * 7 + [(B, H)] * 3
+        ups = [torch.randn(sh, generator=g).to(torch.bfloat16).float() for sh in shapes]
+        leaves16 = [(x.to(torch.bfloat16) if i < 4 else x).clone().requires_grad_(True)
+                    for i, x in enumerate(inputs)]
+        leaves32 = [x.clone().requires_grad_(True) for x in inputs]
+        outs16 = torch.ops.dabsn.core_scan_batched(*leaves16)
+        outs32 = torch.ops.dabsn.core_scan_batched(*leaves32)
+
+        def loss2(outs):
+            return sum((o.float() * u).sum() for i, (o, u) in enumerate(zip(outs, ups)) if i != 7)
+
+        g16 = torch.autograd.grad(loss2(outs16), leaves16, allow_unused=True)
+        g32 = torch.autograd.grad(loss2(outs32), leaves32, allow_unused=True)
+        for i, (a, b) in enumerate(zip(g16, g32)):
+            if b is None:
+                continue
+            a64, b64 = _np(a).astype(np.float64), _np(b).astype(np.float64)
+            arrays[f"{name}.gap_grad{i}"] = np.array(
+                np.linalg.norm(a64 - b64) / max(np.linalg.norm(b64), 1e-30))
+            arrays[f"{name}.sketch16_grad{i}"] = gc.sketch(a64, 2000 + i)
+            arrays[f"{name}.sketch_grad{i}"] = gc.sketch(b64, 2000 + i)
+            if b64.size == 1:
+                arrays[f"{name}.val16_grad{i}"] = a64.reshape(())
+                arrays[f"{name}.val32_grad{i}"] = b64.reshape(())
+        worst = max((float(arrays[k]), k) for k in arrays if k.startswith(f"{name}.gap_grad"))
+        print(f"  {name}: worst reference bf16 gradient gap {worst[0]:.3e} ({worst[1]})")
+    _save("core_bf16_gap", arrays)
 
 
 def core_loop() -> None:
@@ -455,6 +548,7 @@ def op_schemas() -> None:
 
 
 FIXTURES = {"core_op": lambda: core_op("fp32"), "core_op_bf16": core_op_bf16,
+            "core_bf16_gap": core_bf16_gap,
             "core_loop": core_loop, "read_seq": read_seq,
             "read_field": lambda: read_seq("field"), "read_hybrid": lambda: read_seq("hybrid"),
             "read_seq_bf16": read_seq_bf16, "query_bank": query_bank, "model_c1": model_c1,

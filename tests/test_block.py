@@ -154,13 +154,16 @@ def test_field_and_hybrid_read_gpu_match_cpu_oracle(cuda_device, geometry):
     assert rel_err(out_g, out_c) <= 1e-5
     scalar = [b for b in g_c[8:] if b is not None and b.numel() == 1]
     s_max = max(float(b.abs()) for b in scalar)
+    worst = 0.0
     for i, (a, b) in enumerate(zip(g_g, g_c)):
         if b is None:
             continue
         if b.numel() == 1:
+            worst = max(worst, float((a - b).abs()) / s_max)
             assert float((a - b).abs()) <= 1e-4 * s_max, f"grad {i}: {float(a)} vs {float(b)}"
         else:
             assert rel_err(a, b) <= 1e-5, f"grad {i}: {rel_err(a, b):.3e}"
+    print(f"{geometry} read: worst scalar gradient difference {worst:.2e} of the largest")
 
 
 @pytest.mark.gpu
@@ -192,7 +195,10 @@ def test_config1_two_layer_model_gpu_matches_cpu_oracle(cuda_device):
     # every logit of a softmax equally), so both sides hold rounding noise there; the
     # normwise denominator is floored at 1e-3 of the largest gradient in the model.
     floor = 1e-3 * max(float(g.abs().max()) for g in grads_c.values())
+    worst = 0.0
     for n in grads_c:
         a, e = grads_g[n].cpu().double(), grads_c[n].double()
         err = float((a - e).abs().max()) / max(float(e.abs().max()), floor)
+        worst = max(worst, err)
         assert err <= 1e-4, f"{n}: {err:.3e} (max|grad| {float(e.abs().max()):.3e})"
+    print(f"config-1 model vs oracle: worst parameter gradient error {worst:.2e}")

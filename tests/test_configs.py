@@ -7,7 +7,7 @@ Configurations (BASELINE.json ``configs``; test ids carry the config number):
   * config 2 -- copy-task LM, 2 seq layers of state 256, fp32, batch 32:
       - training shape T=64: forward, chunked cross-entropy and backward of the whole LM
         on the GPU against the same LM on the CPU oracle (loss 1e-5, logits and every
-        parameter gradient 1e-4);
+        parameter gradient 1e-5);
       - evaluation shape T=3200: layer 0 at full size, piece by piece against the oracle
         (tests/config_checks.py): core windows 1e-5, statistics 1e-5, selection and
         gather bit-exact, read query windows 1e-5, long scan 1e-5;
@@ -20,7 +20,7 @@ Configurations (BASELINE.json ``configs``; test ids carry the config number):
     for bit; core windows (including one across a chunk boundary) within the bf16 bar
     2e-2 of the fp32 oracle restarted from the GPU's state; tape statistics 1e-5;
     selection over the whole sequence bit-exact; gather bit-exact; read query windows
-    2e-2; the read backward of one query window (Frobenius 2e-2, scalar gradients 5e-2);
+    2e-2; the read backward of one query window (Frobenius 2e-2, scalar gradients 2e-2);
     the chunked core backward of windows (one across a chunk boundary) against the
     oracle's reverse scan on the same bf16 tapes (Frobenius 2e-2); the 1024-step chunked
     backward against the unchunked one at full size (5e-3); long scan 1e-2;
@@ -103,7 +103,7 @@ def _lm_step(model, ids, targets):
     return loss.detach(), h.detach()
 
 
-def lm_against_oracle(model, ids, targets, device, tol=1e-4):
+def lm_against_oracle(model, ids, targets, device, tol=1e-5):
     """The whole LM step on the GPU against the same LM on the CPU oracle kernels."""
     gpu = copy.deepcopy(model).to(device)
     loss_g, h_g = _lm_step(gpu, ids.to(device), targets.to(device))
@@ -280,7 +280,7 @@ def test_config4_read_windows_vs_oracle(c4, c4_read):
 def test_config4_read_backward_window_vs_oracle(c4, c4_read):
     _, P = c4_read
     worst = cc.check_read_backward_window(P, c4["read"], r=5, t0=4064, t1=4096, tol=2e-2,
-                                          scalar_tol=5e-2)
+                                          scalar_tol=2e-2)
     print(f"config4 read backward window: worst error {worst:.2e}")
 
 

@@ -7,9 +7,14 @@ Tolerances (stated per north star):
     size of the oracle's own fp32 summation error for these sums (the oracle pins use the
     same bound against fp64 autograd).
   * bf16 runs against the fp32 oracle: forward tapes normwise relative <= 2e-2;
-    gradients relative Frobenius error ||hip - oracle||_2 / ||oracle||_2 <= 2e-2 (the
-    reverse scan reads bf16 tapes, so isolated elements at hard mask boundaries --
-    clamp, sign -- may take the other branch, as in the reference's own bf16 path).
+    gradients on the same bf16 tapes relative Frobenius error ||hip - oracle||_2 /
+    ||oracle||_2 <= 2e-2; end to end (bf16 tapes, then the reverse scan) against the
+    all-fp32 oracle per gradient by golden_cases.bf16_gap_verdict: within max(2e-2, 1.2 x
+    the reference's own bf16 distance from its fp32 run on the same inputs) -- the reverse
+    scan reads bf16 tapes, so isolated elements at hard mask boundaries (clamp, sign) take
+    the other branch, as in the reference's own bf16 path, and two bf16 evaluations do not
+    share every such element -- and the three whole-batch scalar sums within 2e-2 or
+    nearer the reference's bf16 value than that value is to fp32.
   * index outputs (admitted-slot selection): bit-exact.
 """
 
@@ -22,10 +27,12 @@ import torch.nn.functional as F
 
 import oracle
 from dabsn_amd.kernels import ops
+from golden_cases import GOLDEN, OPS_BF16_CASES, bf16_gap_verdict, sketch
 from helpers import assert_rel, core_case, np32, oracle_core_bwd, oracle_core_fwd, rel_err
 
 pytestmark = pytest.mark.gpu
 
+GAP_FILE = GOLDEN / "ref" / "core_bf16_gap.npz"
 OUT_NAMES = ("U", "novelty", "plasticity", "expression", "write", "energy", "saturation", "gate",
              "final_b", "final_e", "final_c")
 
@@ -61,9 +68,12 @@ def _compare_core_bwd(res, ob, H, tol_t, tol_s, metric):
     want = [ob[0], ob[1], ob[2][:H], ob[2][H:], *[ob[3][i] for i in range(16)]]
     for n, a, b in zip(names, mine, want):
         assert metric(a, b) <= tol_t, f"{n}: {metric(a, b):.3e} > {tol_t}"
+    worst = 0.0
     for i, n in enumerate(("logit_alpha", "log_lambda", "logit_c_suppress")):
         a, b = float(res[20 + i]), float(ob[4][i])
+        worst = max(worst, abs(a - b) / max(abs(b), 1e-6))
         assert abs(a - b) <= tol_s * max(abs(b), 1e-6), f"g_{n}: {a} vs {b}"
+    print(f"core backward H={H}: worst scalar gradient error {worst:.2e} (bar {tol_s})")
     for n, a, b in zip(("gb0", "ge0", "gc0"), res[23:26], ob[5:8]):
         assert metric(a, b) <= tol_t, f"{n}: {metric(a, b):.3e} > {tol_t}"
 
@@ -99,14 +109,35 @@ def test_core_scan_bf16_within_tolerance_of_fp32_oracle(cuda_device, B, T, H):
     ob_same = oracle_core_bwd(inp, same_tapes, grads)
     _compare_core_bwd(res, ob_same, H, 2e-2, 2e-2, rel_fro)
     # End to end against the all-fp32 pipeline: tape rounding moves isolated elements
-    # across hard mask boundaries, so this uses the reference's own bf16 bar (5e-2,
-    # tests/test_batched_runtime.py:152-162 of the reference). The scalar gradients are sums
-    # over all B*T*H elements; with a few hundred terms that cancel to a small total, the
-    # tapes' bf16 rounding alone moves them past that bar, so the end-to-end comparison
-    # starts at a few thousand terms (the reference's own cases are larger).
-    if B * T * H >= 4096:
+    # across hard mask boundaries. Each gradient is held to the reference's own bf16
+    # distance from its fp32 run on the same inputs, recorded for these cases in
+    # tests/golden/ref/core_bf16_gap.npz (tests/golden/make_ref_golden.py), by the rule of
+    # golden_cases.bf16_gap_verdict.
+    if (B, T, H) in OPS_BF16_CASES:
         ob = oracle_core_bwd(inp, fwd, grads)
-        _compare_core_bwd(res, ob, H, 5e-2, 5e-2, rel_fro)
+        gaps = np.load(GAP_FILE)
+        want = [ob[0], ob[1], ob[2][:H], ob[2][H:], *[ob[3][i] for i in range(16)],
+                *[np.asarray(ob[4][i]) for i in range(3)], ob[5], ob[6], ob[7]]
+        rows = []
+        name = f"ops_B{B}_T{T}_H{H}"
+        for i, (a, b) in enumerate(zip(res, want)):
+            key = f"{name}.gap_grad{i}"
+            if key in gaps.files:
+                err = rel_fro(a, b)
+                ok, bar = bf16_gap_verdict(gaps, name, i, err,
+                                           float(a.reshape(-1)[0]) if a.numel() == 1 else None)
+                rows.append((i, err, float(gaps[key]), ok, bar))
+                # distance to the reference's own bf16 result, from the seeded sketches
+                s16 = gaps[f"ops_B{B}_T{T}_H{H}.sketch16_grad{i}"]
+                s32 = gaps[f"ops_B{B}_T{T}_H{H}.sketch_grad{i}"]
+                sh = sketch(np32(a), 2000 + i)
+                print(f"  grad {i}: hip-vs-ref16 {np.sqrt(np.mean((sh - s16) ** 2)):.3e} "
+                      f"ref16-vs-ref32 {np.sqrt(np.mean((s16 - s32) ** 2)):.3e} "
+                      f"hip-vs-ref32 {np.sqrt(np.mean((sh - s32) ** 2)):.3e}")
+        print(f"bf16 B={B} T={T} H={H}: "
+              + ", ".join(f"{i}: {a:.2e} (ref {b:.2e})" for i, a, b, _, _ in rows))
+        bad = [(i, a, bar) for i, a, _, ok, bar in rows if not ok]
+        assert not bad, f"gradients outside the bf16 bar: {bad}"
 
 
 @pytest.mark.parametrize("H", [1024, 2048])

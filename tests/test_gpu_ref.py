@@ -11,8 +11,7 @@ operators and modules reproduce them on the GPU:
   * the bf16 read: admission values and slot selection bit-exact, through the HIP tape
     statistics, the training-path glue and the fused decode glue;
   * ``forward_query_bank`` with ``query_start > 0`` and a carried long state: 1e-5;
-  * the config-1-shaped model, block by block: 1e-4 (MFMA products and several fp32 ops
-    in sequence, each within 1e-5);
+  * the config-1-shaped model, block by block: 1e-5;
   * a ``.dmem`` file written by the reference, continued on the GPU: 1e-5.
 """
 
@@ -67,10 +66,9 @@ def _fro(a, b) -> float:
 def test_core_bf16_gap_against_the_references_own_bf16_path(cuda_device):
     """bf16 activations and recurrent weights, fp32 state (the reference's bf16 path,
     tests/test_batched_runtime.py:83-162). Per gradient, the HIP bf16 result's Frobenius
-    distance from the reference's fp32 result must stay within 2e-2 or, where the
-    reference's own bf16 result is farther than 2e-2 / 1.5 from its fp32 one, within
-    1.5x the reference's own gap (both bf16 paths round the same tapes and GEMM outputs,
-    in different summation orders). Forward outputs: within 2e-2 normwise of fp32."""
+    distance from the reference's fp32 result must stay within max(2e-2, the reference's
+    own bf16 distance from its fp32 result). Forward outputs: within 2e-2 normwise of
+    fp32."""
     z = _load("core_op_bf16")
     leaves = []
     for i in range(26):
@@ -92,7 +90,49 @@ def test_core_bf16_gap_against_the_references_own_bf16_path(cuda_device):
         rows.append((CORE_GRAD_NAMES[i], e_hip, e_ref))
     print("\n".join(f"{n}: hip bf16 {a:.2e}, reference bf16 {b:.2e}" for n, a, b in rows))
     for n, e_hip, e_ref in rows:
-        assert e_hip <= max(2e-2, 1.5 * e_ref), f"g_{n}: {e_hip:.3e} (reference {e_ref:.3e})"
+        assert e_hip <= max(2e-2, e_ref), f"g_{n}: {e_hip:.3e} (reference {e_ref:.3e})"
+
+
+@pytest.mark.parametrize("name", ["B2_T256_H512", "B1_T1024_H2048"])
+def test_core_bf16_within_the_references_gap_at_size(cuda_device, name):
+    """Two larger shapes (tests/golden/ref/core_bf16_gap.npz, inputs from the seeded recipe
+    golden_cases.bf16_gap_case): the HIP bf16 op (Wx, Wgx, Ug, A in bf16) against the fp32
+    oracle on the same values -- which tests/test_ref_pins.py pins to the reference's fp32
+    run at these shapes. Outputs (normwise) within max(2e-2, the reference's own bf16
+    distance from fp32 there); gradients (Frobenius) by golden_cases.bf16_gap_verdict:
+    within max(2e-2, 1.2 x the reference's distance), the three whole-batch scalar sums
+    within 2e-2 or nearer the reference's bf16 value than that value is to fp32."""
+    import golden_cases as gc
+
+    z = _load("core_bf16_gap")
+    inputs, gout = gc.bf16_gap_case(name)
+    outs32, grads32 = gc.core_oracle_case(inputs, gout)
+    leaves = [(t.to(cuda_device, torch.bfloat16) if i < 4 else t.to(cuda_device)).requires_grad_(True)
+              for i, t in enumerate(inputs)]
+    outs = ops.core_scan_batched(*leaves)
+    rows = []
+    for i in range(11):
+        err = rel_err(outs[i].detach().float().cpu(), outs32[i])
+        gap = float(z[f"{name}.gap_out{i}"])
+        rows.append((f"output {i}", err, gap, err <= max(2e-2, gap), f"{max(2e-2, gap):.3e}"))
+    loss = sum((o.float() * g.to(cuda_device)).sum() for o, g in zip(outs, gout) if g is not None)
+    grads = torch.autograd.grad(loss, leaves, allow_unused=True)
+    for i, g in enumerate(grads):
+        if f"{name}.gap_grad{i}" not in z:
+            continue
+        gh = g.detach().float().cpu().numpy()
+        err = _fro(gh, grads32[i])
+        ok, bar = gc.bf16_gap_verdict(z, name, i, err, gh.reshape(-1)[0] if gh.size == 1 else None)
+        rows.append((f"g_{CORE_GRAD_NAMES[i]}", err, float(z[f"{name}.gap_grad{i}"]), ok, bar))
+        # How far the HIP bf16 result is from the reference's bf16 result, estimated from
+        # the seeded sketches (scalars: exactly), relative to the fp32 norm.
+        s_hip = gc.sketch(gh, 2000 + i)
+        near = float(np.sqrt(np.mean((s_hip - z[f"{name}.sketch16_grad{i}"]) ** 2)))
+        print(f"  g_{CORE_GRAD_NAMES[i]}: hip-vs-ref16 {near / float(z[f'{name}.norm_grad{i}']):.2e}"
+              f" hip-vs-fp32 {err:.2e} ref16-vs-fp32 {float(z[f'{name}.gap_grad{i}']):.2e}")
+    print(f"{name}: " + ", ".join(f"{n} hip {a:.2e} ref {b:.2e}" for n, a, b, _, _ in rows))
+    bad = [(n, a, bar) for n, a, _, ok, bar in rows if not ok]
+    assert not bad, f"outside the bf16 bar: {bad}"
 
 
 @pytest.mark.parametrize("geometry", ["seq", "field", "hybrid"])
@@ -160,7 +200,7 @@ def test_query_bank_vs_reference_fixture_gpu(cuda_device):
 
 @pytest.mark.parametrize("k", [0, 1])
 def test_config1_blocks_vs_reference_fixture_gpu(cuda_device, k):
-    c1_block_check(_load("model_c1"), k, cuda_device, tol=1e-4)
+    c1_block_check(_load("model_c1"), k, cuda_device, tol=1e-5)
 
 
 def test_reference_written_memory_file_continues_exactly_gpu(cuda_device):
