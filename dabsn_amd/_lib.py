@@ -142,6 +142,8 @@ _SIGNATURES = {
     "dabsn_hip_read3_decode_workspace_bytes": ([i32, i64, i64, i64, i64], sz),
     "dabsn_hip_read_dense_workspace_bytes": ([i64, i64, i64, i64, i32], sz),
     "dabsn_hip_read_dense_fwd": ([i64] * 4 + [vp] * 8 + [vp] * 4 + [vp, vp, vp, sz, vp], i32),
+    "dabsn_hip_read_dense_fwd_weights": (
+        [i64] * 4 + [vp] * 8 + [vp] * 4 + [vp, vp, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_read_dense_bwd": (
         [i64] * 4 + [vp] + [vp] * 8 + [vp] * 4 + [vp] + [vp] * 9 + [vp, sz, vp], i32),
     "dabsn_hip_permanent_scan_fwd": ([i64, i64, i64, vp, vp, vp, vp, vp], i32),

@@ -165,8 +165,10 @@ __device__ __forceinline__ void weights(const Row& r, int n, float& ps, float& p
   pi = softmax_weight(r.iel, ia, sh, r.m_i, r.z_i);
 }
 
-// Forward rows: W1 = g_s P_s + g_p P_p, W2 = g_i P_i.
-__global__ void __launch_bounds__(NT) rows_fwd_kernel(RowArgs a, float* W1, float* W2) {
+// Forward rows: W1 = g_s P_s + g_p P_p, W2 = g_i P_i; with Ps non-null also the three
+// softmaxes themselves (the 4-output op returns them).
+__global__ void __launch_bounds__(NT) rows_fwd_kernel(RowArgs a, float* W1, float* W2, float* Ps,
+                                                      float* Pp, float* Pi) {
   __shared__ float shm[3 * 4];
   const int row = blockIdx.x;
   Row r(a, row);
@@ -178,6 +180,11 @@ __global__ void __launch_bounds__(NT) rows_fwd_kernel(RowArgs a, float* W1, floa
     weights(r, n, ps, pp, pi);
     W1[ro + n] = sg * ps + pg * pp;
     W2[ro + n] = ig * pi;
+    if (Ps) {
+      Ps[ro + n] = ps;
+      Pp[ro + n] = pp;
+      Pi[ro + n] = pi;
+    }
   }
 }
 
@@ -395,7 +402,28 @@ int dabsn_hip_read_dense_fwd(int64_t B, int64_t T, int64_t N, int64_t H, const f
                              const uint8_t* induct_allow, const uint8_t* eligible,
                              const uint8_t* induct_eligible, const float* scalars, float* out,
                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return dabsn_hip_read_dense_fwd_weights(B, T, N, H, query, bank_keys, bank_writes, next_writes,
+                                          cocktail, bank_cocktail, bank_key_bias, bank_admission,
+                                          allow, induct_allow, eligible, induct_eligible, scalars,
+                                          out, nullptr, nullptr, nullptr, workspace,
+                                          workspace_bytes, stream);
+}
+
+int dabsn_hip_read_dense_fwd_weights(int64_t B, int64_t T, int64_t N, int64_t H,
+                                     const float* query, const float* bank_keys,
+                                     const float* bank_writes, const float* next_writes,
+                                     const float* cocktail, const float* bank_cocktail,
+                                     const float* bank_key_bias, const float* bank_admission,
+                                     const uint8_t* allow, const uint8_t* induct_allow,
+                                     const uint8_t* eligible, const uint8_t* induct_eligible,
+                                     const float* scalars, float* out, float* short_weights,
+                                     float* permanent_weights, float* induct_weights,
+                                     void* workspace, size_t workspace_bytes,
+                                     hipStream_t stream) {
   DENSE_TRY(check_shape(B, T, N, H));
+  DABSN_REQUIRE((short_weights == nullptr) == (permanent_weights == nullptr) &&
+                    (short_weights == nullptr) == (induct_weights == nullptr),
+                "dense read: the three weight outputs are given together or not at all");
   DABSN_REQUIRE(query && bank_keys && bank_writes && next_writes && cocktail && bank_cocktail &&
                     bank_key_bias && bank_admission && allow && induct_allow && eligible &&
                     induct_eligible && scalars && out && workspace,
@@ -416,7 +444,7 @@ int dabsn_hip_read_dense_fwd(int64_t B, int64_t T, int64_t N, int64_t H, const f
   const RowArgs ra{t, n, S, cocktail, bank_cocktail, bank_key_bias, bank_admission, allow,
                    induct_allow, eligible, induct_eligible, scalars};
   hipLaunchKernelGGL(rows_fwd_kernel, dim3(static_cast<unsigned>(B * T)), dim3(NT), 0, stream, ra,
-                     W1, W2);
+                     W1, W2, short_weights, permanent_weights, induct_weights);
   DABSN_HIP_CHECK(hipGetLastError());
   DABSN_HIP_CHECK(xpose::transpose(bank_writes, Vt, b, n, h, stream));
   DABSN_HIP_CHECK(xpose::transpose(next_writes, Vnt, b, n, h, stream));

@@ -30,6 +30,7 @@ from .ops import (
     local_field_gather_backward,
     long_scan_fused,
     normalize_rows,
+    parameters_changed,
     permanent_delta_scan,
     read_tape_stats,
 )
@@ -169,6 +170,7 @@ __all__ = [
     "local_field_gather_backward",
     "long_scan_fused",
     "normalize_rows",
+    "parameters_changed",
     "permanent_delta_read",
     "permanent_delta_scan",
     "primitive_map",

@@ -61,7 +61,9 @@ def _q(name: str) -> str:
 
 _DTYPES = {torch.float32: 0, torch.bfloat16: 1}
 
-# Sticky device-side error words of persistent kernels, checked by check_errors().
+# Sticky device-side error words of persistent kernels (int32 [1] per device): a kernel's
+# error word is OR-ed in on the device after each launch, and read by check_errors() or,
+# at no extra synchronisation, together with the read's bank width (pending_error_word).
 _STICKY: dict[int, Tensor] = {}
 
 
@@ -83,8 +85,30 @@ def _p(t: Optional[Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-def _sync_mode() -> str:
-    return os.environ.get("DABSN_HIP_ERROR_CHECK", "sync")
+def _sync_mode(input_check: bool = False) -> str:
+    """How a kernel's error word is read. ``DABSN_HIP_ERROR_CHECK=sync`` reads every op's
+    word right after it (one host synchronisation per op); ``deferred`` keeps every word on
+    the device until ``check_errors()`` or the next read's bank-width read. Unset, the
+    persistent scans' barrier word is deferred (no host synchronisation inside the scan
+    ops, so they can be captured in a graph) and the words that validate caller input
+    (target and patch indices) are read at once, so a bad argument raises from the call
+    that received it. Under graph capture every word is deferred."""
+    mode = os.environ.get("DABSN_HIP_ERROR_CHECK")
+    if mode is None:
+        mode = "sync" if input_check else "deferred"
+    if mode == "sync" and torch.cuda.is_initialized() and torch.cuda.is_current_stream_capturing():
+        return "deferred"
+    return mode
+
+
+def _capture_cus(device: torch.device) -> int:
+    """CUs a persistent scan may assume it owns when launched as a plain kernel: all of the
+    device's while the current stream is being captured into a graph (a cooperative launch
+    is not recorded as such; a captured scan must not run beside other work on the device
+    when the graph is replayed), else 0 (cooperative launch)."""
+    if not torch.cuda.is_current_stream_capturing():
+        return 0
+    return int(torch.cuda.get_device_properties(device).multi_processor_count)
 
 
 # Derived copies of parameters (fp32 copies of bf16 parameter vectors and scalars, the
@@ -92,12 +116,28 @@ def _sync_mode() -> str:
 # parameters, and these copies were a third of its kernel launches. Inside
 # `reuse_parameter_copies()` (the carried-memory inference entry points) an entry is
 # reused while every source is the same nn.Parameter object with the same storage and
-# version counter: an in-place update, a `.data` swap or a new module rebuilds it. An edit
-# through `p.data` in place (`p.data.copy_(...)`) leaves the version counter alone, so
-# such edits must not happen between calls inside the context. Elsewhere nothing is
-# cached.
+# version counter: an in-place update (load_state_dict's copy included), a `.data` swap or
+# a new module rebuilds it. An edit through `p.data` in place (`p.data.copy_(...)`,
+# `p.data.add_(...)`, an EMA swap) leaves the version counter alone: whoever edits weights
+# that way calls `parameters_changed()` before the next call. Elsewhere nothing is cached.
 _DERIVED: dict[tuple, tuple] = {}
 _REUSE_DEPTH = 0
+# Bumped by parameters_changed(): part of every kept copy's stamp and of a carried bank's
+# admission key (memory.BankStore), so both are rebuilt after such an edit.
+_GENERATION = 0
+
+
+def parameters_changed() -> None:
+    """Declare that parameters were edited in place without their version counter moving
+    (through ``p.data``): drops every kept parameter copy, and carried banks rebuild their
+    admission glue and admitted-slot lists on their next use."""
+    global _GENERATION
+    _GENERATION += 1
+    _DERIVED.clear()
+
+
+def parameter_generation() -> int:
+    return _GENERATION
 
 
 class reuse_parameter_copies:
@@ -115,7 +155,8 @@ class reuse_parameter_copies:
 
 
 def clear_parameter_copies() -> None:
-    _DERIVED.clear()
+    """Alias of ``parameters_changed()``."""
+    parameters_changed()
 
 
 def _derived(tag: str, sources: Sequence[Tensor], build: Callable[..., object]):
@@ -136,7 +177,7 @@ def _derived(tag: str, sources: Sequence[Tensor], build: Callable[..., object]):
             key.append((id(o), tuple(t.shape), t.stride(), t.storage_offset()))
     key = tuple(key)
     # Device pointers are unique across devices, so the pointer also stands for the device.
-    stamp = tuple((o.data_ptr(), o._version, o.dtype) for o in owners)
+    stamp = (_GENERATION, tuple((o.data_ptr(), o._version, o.dtype) for o in owners))
     hit = _DERIVED.get(key)
     if hit is not None and hit[1] == stamp and all(r() is o for r, o in zip(hit[0], owners)):
         return hit[2]
@@ -162,8 +203,11 @@ def _f32_scalar(t: Tensor) -> Tensor:
 
 
 def _record_error_word(ws: Tensor, what: str, meaning: str | None = None) -> None:
+    """Check a launch's error word (the first 4 bytes of ``ws``). ``meaning`` describes an
+    input-validation word (see _sync_mode); without it the word is a persistent scan's
+    barrier timeout."""
     word = ws[:4].view(torch.int32)
-    if _sync_mode() == "sync":
+    if _sync_mode(input_check=meaning is not None) == "sync":
         value = int(word.item())
         if value != 0:
             raise RuntimeError(
@@ -172,22 +216,45 @@ def _record_error_word(ws: Tensor, what: str, meaning: str | None = None) -> Non
                    "persistent scan were not all co-resident") + f" (error word {value})"
             )
         return
-    dev = ws.device.index or 0
+    sticky = _sticky(ws.device)
+    torch.bitwise_or(sticky, word, out=sticky)
+
+
+def _sticky(device: torch.device) -> Tensor:
+    dev = device.index if device.index is not None else torch.cuda.current_device()
     sticky = _STICKY.get(dev)
     if sticky is None:
-        sticky = torch.zeros(1, dtype=torch.int32, device=ws.device)
+        sticky = torch.zeros(1, dtype=torch.int32, device=device)
         _STICKY[dev] = sticky
-    torch.bitwise_or(sticky, word, out=sticky)
+    return sticky
+
+
+def pending_error_word(device: torch.device) -> Optional[Tensor]:
+    """The device's sticky error word as an int64 [1] tensor (None when nothing was
+    launched in deferred mode), for a caller that reads it together with another value
+    in one host read."""
+    dev = device.index if device.index is not None else torch.cuda.current_device()
+    sticky = _STICKY.get(dev)
+    return None if sticky is None else sticky.to(torch.int64)
+
+
+def raise_error_word(value: int, device: torch.device) -> None:
+    """Clear the device's sticky word and raise for a non-zero ``value`` read from it."""
+    if value != 0:
+        _sticky(device).zero_()
+        raise RuntimeError(
+            f"DABSN HIP kernel on {device} reported error word {value} (a persistent scan's "
+            "step barrier timed out, or an index argument was out of range; see the op's "
+            "documentation)")
 
 
 def check_errors() -> None:
     """Raise if any kernel launched in deferred-check mode reported an error (a persistent
-    scan's barrier timeout, or an out-of-range local-field patch index)."""
+    scan's barrier timeout, or an out-of-range local-field patch index or target). The
+    documented check point of the default deferred mode; the training read also carries
+    the word along with its bank-width read."""
     for dev, sticky in _STICKY.items():
-        value = int(sticky.item())
-        if value != 0:
-            sticky.zero_()
-            raise RuntimeError(f"DABSN HIP kernel on cuda:{dev} reported error word {value}")
+        raise_error_word(int(sticky.item()), torch.device("cuda", dev))
 
 
 class KernelTimer:
@@ -352,7 +419,7 @@ def core_scan_batched(
     call = _lib.CoreFwdCall(code, B, T, H, T, ldx, _p(Wx_c), _p(Wgx_c), _p(GA),
                             ctypes.pointer(params), _p(b0), _p(e0), _p(c0), _p(U),
                             *[_p(t) for t in tapes], *[_p(f) for f in finals], _p(ws), nbytes,
-                            _code(sdt))
+                            _code(sdt), _capture_cus(Wx.device))
     tk = KernelTimer.begin("core_scan_fwd", Wx)
     rc = lib.dabsn_hip_core_scan_fwd_call(ctypes.byref(call), _stream(Wx))
     KernelTimer.end(tk)
@@ -422,11 +489,13 @@ def core_scan_batched_backward(
     nbytes = lib.dabsn_hip_core_scan_workspace_bytes(code, B, H, 1)
     core_launch_check(code, B, T, H, True)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=U.device)
+    call = _lib.CoreBwdCall(code, B, T, H, T, _p(GAT), ctypes.pointer(params), _p(b0), _p(c0),
+                            *[_p(x) for x in saved], *[_p(g) for g in grads],
+                            *[_p(g) for g in gfin], _p(gWx), _p(gWgx), _p(day), _p(part_vec),
+                            _p(part_scal), _p(gb0), _p(ge0), _p(gc0), _p(ws), nbytes,
+                            _capture_cus(U.device))
     tk = KernelTimer.begin("core_scan_bwd", U)
-    rc = lib.dabsn_hip_core_scan_bwd(
-        code, B, T, H, _p(GAT), ctypes.byref(params), _p(b0), _p(c0), *[_p(x) for x in saved],
-        *[_p(g) for g in grads], *[_p(g) for g in gfin], _p(gWx), _p(gWgx), _p(day),
-        _p(part_vec), _p(part_scal), _p(gb0), _p(ge0), _p(gc0), _p(ws), nbytes, _stream(U))
+    rc = lib.dabsn_hip_core_scan_bwd_call(ctypes.byref(call), _stream(U))
     KernelTimer.end(tk)
     _lib.check(rc, "core scan backward")
     _record_error_word(ws, "core scan backward")
@@ -1788,6 +1857,48 @@ def admitted_three_way_read_native(
 @admitted_three_way_read_native.register_fake
 def _dense_read_fake(query, *rest):
     return torch.empty_like(query)
+
+
+@torch.library.custom_op(_q("admitted_three_way_read"), mutates_args=(), device_types="cuda")
+def admitted_three_way_read(
+    query: Tensor, bank_keys: Tensor, bank_writes: Tensor, next_writes: Tensor, cocktail: Tensor,
+    bank_cocktail: Tensor, bank_key_bias: Tensor, bank_admission: Tensor, scale: Tensor,
+    allow: Tensor, induct_allow: Tensor, eligible: Tensor, induct_eligible: Tensor,
+    short_gain: Tensor, pad_gain: Tensor, induct_gain: Tensor, cocktail_gain: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """The reference's 4-output dense read (admitted.py:16-65): (output in the query's dtype,
+    short, permanent and induction softmax weights [B, T, N] in fp32 for bf16/fp16 queries,
+    else in the query's dtype). Registered without autograd here: the reference's own
+    formula (admitted.py:126-247) differentiates it from the saved weights in a process
+    that binds this kernel to the reference's operator (``reference_backend``); this
+    package's reads use the compact and dense-mask operators, which have HIP backwards."""
+    (B, T, N, H), f, m, scal = _dense_inputs(
+        query, bank_keys, bank_writes, next_writes, cocktail, bank_cocktail, bank_key_bias,
+        bank_admission, scale, allow, induct_allow, eligible, induct_eligible, short_gain,
+        pad_gain, induct_gain, cocktail_gain)
+    wdt = torch.float32 if query.dtype in (torch.float16, torch.bfloat16) else query.dtype
+    if min(B, T, N, H) == 0:
+        z = torch.zeros((B, T, N), device=query.device, dtype=wdt)
+        return (torch.zeros(query.shape, device=query.device, dtype=query.dtype), z, z.clone(),
+                z.clone())
+    lib = _lib.load()
+    out = torch.empty((B, T, H), device=query.device, dtype=torch.float32)
+    w = [torch.empty((B, T, N), device=query.device, dtype=torch.float32) for _ in range(3)]
+    nbytes = lib.dabsn_hip_read_dense_workspace_bytes(B, T, N, H, 0)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=query.device)
+    _lib.check(lib.dabsn_hip_read_dense_fwd_weights(
+        B, T, N, H, *[_p(x) for x in f], *[_p(x) for x in m], _p(scal), _p(out),
+        *[_p(x) for x in w], _p(ws), ws.numel(), _stream(out)), "dense three-way read")
+    return (out.to(query.dtype), *[x.to(wdt) for x in w])
+
+
+@admitted_three_way_read.register_fake
+def _dense_read4_fake(query, bank_keys, *rest):
+    B, T, _ = query.shape
+    N = bank_keys.shape[1]
+    wdt = torch.float32 if query.dtype in (torch.float16, torch.bfloat16) else query.dtype
+    w = query.new_empty((B, T, N), dtype=wdt)
+    return torch.empty_like(query), w, w.clone(), w.clone()
 
 
 @torch.library.custom_op(_q("_admitted_three_way_read_backward"), mutates_args=(),

@@ -228,107 +228,112 @@ class _PipelinedScanRead(torch.autograd.Function):
         for st in (M, S, R):
             st.wait_stream(ambient)
 
-        with torch.cuda.stream(M):
-            # Scan of every chunk on the scan half; an event after each.
-            scan_done, starts, fwd_calls = [], [], []
-            with torch.cuda.stream(S):
-                zeros = torch.zeros(B, H, device=dev, dtype=torch.float32)
-                carry = [zeros, torch.ones_like(zeros), zeros.clone()]
-                for t0, t1 in bounds:
-                    starts.append(torch.stack(carry))
-                    f = chunked._Fwd(code, Wx_c, Wgx_c, GA, params, *carry, out, t0, t1, ldx, cus)
-                    tk = ops.KernelTimer.begin("core_scan_fwd", Wx)
-                    f.launch(S)
-                    ops.KernelTimer.end(tk)
-                    e = torch.cuda.Event()
-                    e.record(S)
-                    scan_done.append(e)
-                    fwd_calls.append(f)
-                    carry = f.finals
-                starts = torch.stack(starts)
+        try:
+            with torch.cuda.stream(M):
+                # Scan of every chunk on the scan half; an event after each.
+                scan_done, starts, fwd_calls = [], [], []
+                with torch.cuda.stream(S):
+                    zeros = torch.zeros(B, H, device=dev, dtype=torch.float32)
+                    carry = [zeros, torch.ones_like(zeros), zeros.clone()]
+                    for t0, t1 in bounds:
+                        starts.append(torch.stack(carry))
+                        f = chunked._Fwd(code, Wx_c, Wgx_c, GA, params, *carry, out, t0, t1, ldx, cus)
+                        tk = ops.KernelTimer.begin("core_scan_fwd", Wx)
+                        f.launch(S)
+                        ops.KernelTimer.end(tk)
+                        e = torch.cuda.Event()
+                        e.record(S)
+                        scan_done.append(e)
+                        fwd_calls.append(f)
+                        carry = f.finals
+                    starts = torch.stack(starts)
 
-            U = out.U
-            ay, w, pl = out.tapes[2], out.tapes[3], out.tapes[1]
-            w_leaf = w.detach().requires_grad_(True)
-            stats_leaf = stats.detach().requires_grad_(True)
-            param_leaves = {n: p.detach().requires_grad_(p.requires_grad)
-                            for n, p in zip(names, read_params)}
-            norms = stats_leaf[..., 5].detach()
-            Wd = read.short_read.out.weight.detach().to(dt)
-            bd = read.short_read.out.bias.detach().to(dt)
+                U = out.U
+                ay, w, pl = out.tapes[2], out.tapes[3], out.tapes[1]
+                w_leaf = w.detach().requires_grad_(True)
+                stats_leaf = stats.detach().requires_grad_(True)
+                param_leaves = {n: p.detach().requires_grad_(p.requires_grad)
+                                for n, p in zip(names, read_params)}
+                norms = stats_leaf[..., 5].detach()
+                Wd = read.short_read.out.weight.detach().to(dt)
+                bd = read.short_read.out.bias.detach().to(dt)
 
-            def gather(bank_write, norm_w, idx, next_idx, rank, fold):
-                return _SinkGather.apply(sink, bank_write, norm_w, idx,
-                                         None if fold is not None else next_idx, rank)
+                def gather(bank_write, norm_w, idx, next_idx, rank, fold):
+                    return _SinkGather.apply(sink, bank_write, norm_w, idx,
+                                             None if fold is not None else next_idx, rank)
 
-            def read_chunk(k: int):
-                # Statistics of window k, the three-way read of query chunk k against the
-                # bank [0, t1) (its own autograd graph) and, without autograd, its output
-                # projection (differentiated by hand in the backward): the [y, budget] block
-                # with the bias first (enqueued ahead of the read's host sync on the bank
-                # width), then the retrieved block added.
-                t0, t1 = bounds[k]
-                C = t1 - t0
-                st = torch.cuda.current_stream(dev)
-                _stats_window(out, stats, t0, t1, st.cuda_stream)
-                pre = F.linear(ops.window_copy(U[:, t0:t1]).view(B * C, 2 * H), Wd[:, :2 * H], bd)
-                with torch.enable_grad():
-                    # A contiguous copy of the expression window as the leaf (the read's
-                    # normalisation reads it densely).
-                    ay_leaf = ops.window_copy(ay[:, t0:t1]).requires_grad_(True)
-                    r = read.query_bank_retrieved(
-                        ay_leaf, query_stats=stats_leaf[:, t0:t1], bank_write=w_leaf,
-                        bank_norms=norms, bank_stats=stats_leaf[:, :t1], query_start=t0,
-                        gather=gather)
-                rd = r.detach().to(dt)
-                ops.window_add(retr[:, t0:t1], rd)
-                sh = torch.addmm(pre, rd.reshape(B * C, H), Wd[:, 2 * H:].t())
-                ops.window_add(short[:, t0:t1], sh.view(B, C, H))
-                return r, ay_leaf
+                def read_chunk(k: int):
+                    # Statistics of window k, the three-way read of query chunk k against the
+                    # bank [0, t1) (its own autograd graph) and, without autograd, its output
+                    # projection (differentiated by hand in the backward): the [y, budget] block
+                    # with the bias first (enqueued ahead of the read's host sync on the bank
+                    # width), then the retrieved block added.
+                    t0, t1 = bounds[k]
+                    C = t1 - t0
+                    st = torch.cuda.current_stream(dev)
+                    _stats_window(out, stats, t0, t1, st.cuda_stream)
+                    pre = F.linear(ops.window_copy(U[:, t0:t1]).view(B * C, 2 * H), Wd[:, :2 * H], bd)
+                    with torch.enable_grad():
+                        # A contiguous copy of the expression window as the leaf (the read's
+                        # normalisation reads it densely).
+                        ay_leaf = ops.window_copy(ay[:, t0:t1]).requires_grad_(True)
+                        r = read.query_bank_retrieved(
+                            ay_leaf, query_stats=stats_leaf[:, t0:t1], bank_write=w_leaf,
+                            bank_norms=norms, bank_stats=stats_leaf[:, :t1], query_start=t0,
+                            gather=gather)
+                    rd = r.detach().to(dt)
+                    ops.window_add(retr[:, t0:t1], rd)
+                    sh = torch.addmm(pre, rd.reshape(B * C, H), Wd[:, 2 * H:].t())
+                    ops.window_add(short[:, t0:t1], sh.view(B, C, H))
+                    return r, ay_leaf
 
-            # The long channel (long.py:492-579) window by window from the state the previous
-            # window ends in, differentiated by hand: per window its write and plasticity
-            # rows (contiguous copies, kept) and the states entering every step.
-            events.announce("recurrent_long_read", "rocm_chunk_parallel_scan", B=B, T=T, H=H,
-                            dtype="bf16" if code == 1 else "fp32")
-            longs = []
-            carried = long_state0
+                # The long channel (long.py:492-579) window by window from the state the previous
+                # window ends in, differentiated by hand: per window its write and plasticity
+                # rows (contiguous copies, kept) and the states entering every step.
+                events.announce("recurrent_long_read", "rocm_chunk_parallel_scan", B=B, T=T, H=H,
+                                dtype="bf16" if code == 1 else "fp32")
+                longs = []
+                carried = long_state0
 
-            def long_window(k: int) -> None:
-                nonlocal carried
-                t0, t1 = bounds[k]
-                wk = ops.window_copy(w[:, t0:t1])
-                pk = ops.window_copy(pl[:, t0:t1])
-                lk, lf, ef, rf, states = ops.direct.long_scan_fused(wk, pk, *logits, *carried)
-                carried = (lf, ef, rf)
-                ops.window_add(long_out[:, t0:t1], lk)
-                longs.append((wk, pk, states))
+                def long_window(k: int) -> None:
+                    nonlocal carried
+                    t0, t1 = bounds[k]
+                    wk = ops.window_copy(w[:, t0:t1])
+                    pk = ops.window_copy(pl[:, t0:t1])
+                    lk, lf, ef, rf, states = ops.direct.long_scan_fused(wk, pk, *logits, *carried)
+                    carried = (lf, ef, rf)
+                    ops.window_add(long_out[:, t0:t1], lk)
+                    longs.append((wk, pk, states))
 
-            chunks = []
-            with _parameters_as(read, param_leaves):
-                with torch.cuda.stream(R):
-                    for k in range(K - 1):
-                        R.wait_event(scan_done[k])
-                        chunks.append(read_chunk(k))
-                        if k == K - 2:
-                            r_chunks = torch.cuda.Event()
-                            r_chunks.record(R)
-                        long_window(k)
-                        ops.read_output_window(short, long_out, gain, read_out, *bounds[k])
-                    # The last window's long channel beside the last chunk's read.
-                    R.wait_event(scan_done[K - 1])
-                    long_window(K - 1)
-                    r_long = torch.cuda.Event()
-                    r_long.record(R)
-                M.wait_event(scan_done[K - 1])
-                M.wait_event(r_chunks)
-                chunks.append(read_chunk(K - 1))
-                M.wait_event(r_long)
-                ops.read_output_window(short, long_out, gain, read_out, *bounds[K - 1])
-            M.wait_stream(S)
-        _check_scans(S, fwd_calls, "core scan forward")
-        ambient.wait_stream(S)
-        ambient.wait_stream(M)
+                chunks = []
+                with _parameters_as(read, param_leaves):
+                    with torch.cuda.stream(R):
+                        for k in range(K - 1):
+                            R.wait_event(scan_done[k])
+                            chunks.append(read_chunk(k))
+                            if k == K - 2:
+                                r_chunks = torch.cuda.Event()
+                                r_chunks.record(R)
+                            long_window(k)
+                            ops.read_output_window(short, long_out, gain, read_out, *bounds[k])
+                        # The last window's long channel beside the last chunk's read.
+                        R.wait_event(scan_done[K - 1])
+                        long_window(K - 1)
+                        r_long = torch.cuda.Event()
+                        r_long.record(R)
+                    M.wait_event(scan_done[K - 1])
+                    M.wait_event(r_chunks)
+                    chunks.append(read_chunk(K - 1))
+                    M.wait_event(r_long)
+                    ops.read_output_window(short, long_out, gain, read_out, *bounds[K - 1])
+                M.wait_stream(S)
+            _check_scans(S, fwd_calls, "core scan forward")
+        finally:
+            # Also when an exception leaves: the caller's stream waits for all three
+            # streams, so buffers allocated on it are not reused while work still runs.
+            M.wait_stream(R)
+            ambient.wait_stream(S)
+            ambient.wait_stream(M)
         read_out.record_stream(ambient)
         del keep
 
@@ -450,105 +455,110 @@ class _PipelinedScanRead(torch.autograd.Function):
             logit_sum[0] = part if logit_sum[0] is None else logit_sum[0] + part
             state_grad[:] = g[6:9]
 
-        with torch.cuda.stream(M):
-            # The read output's backward over the last window; then the long channel's last
-            # window on the read half (enqueued first, so that its kernels hold their CUs)
-            # beside the last chunk's projection and read backward on the whole device. The
-            # other windows' long channel runs in the read half's per-chunk work (measured:
-            # a second window at the head slows the last chunk's read backward by 0.45 ms,
-            # more than it saves later).
-            read_out_backward(K - 1)
-            head = torch.cuda.Event()
-            head.record(M)
-            R.wait_event(head)
-            with torch.cuda.stream(R):
-                long_backward(K - 1)
-
-            carry = [None, None, None]
-            bws = []
-            scan_back: list[Optional[torch.cuda.Event]] = [None] * K
-            bw_of: dict = {}
-            for k in range(K - 1, -1, -1):
-                t0, t1 = bounds[k]
-                r, ay_leaf = chunks[k]
-                st = M if k == K - 1 else R
-                with torch.cuda.stream(st):
-                    read_out_backward(k)
-                    g_r = projection_grads(g_short3, k)
-                    # w_leaf is listed so that the engine runs the gather's backward, whose
-                    # gradient goes to the sink (it returns none for w_leaf itself).
-                    torch.autograd.backward([r], [g_r],
-                                            inputs=[ay_leaf, w_leaf, stats_leaf, *trainable])
-                    if ay_leaf.grad is not None:
-                        ops.window_add(g_ay[:, t0:t1], ay_leaf.grad.to(dt))
-                    else:
-                        g_ay[:, t0:t1].zero_()
-                if st is not R:
-                    done = torch.cuda.Event()
-                    done.record(st)
-                    R.wait_event(done)
+        try:
+            with torch.cuda.stream(M):
+                # The read output's backward over the last window; then the long channel's last
+                # window on the read half (enqueued first, so that its kernels hold their CUs)
+                # beside the last chunk's projection and read backward on the whole device. The
+                # other windows' long channel runs in the read half's per-chunk work (measured:
+                # a second window at the head slows the last chunk's read backward by 0.45 ms,
+                # more than it saves later).
+                read_out_backward(K - 1)
+                head = torch.cuda.Event()
+                head.record(M)
+                R.wait_event(head)
                 with torch.cuda.stream(R):
-                    if k < K - 1:
-                        long_backward(k)
-                    # Window k of the write gradient is complete (only query chunks >= k
-                    # read it): the long channel's share joins it.
-                    gwk, gpk = long_grads[k]
-                    ops.window_add(sink[:, t0:t1], sink[:, t0:t1], gwk)
-                    ops.window_add(g_p[:, t0:t1], gpk)
-                    gs = stats_leaf.grad
-                    gs = torch.zeros_like(stats_leaf) if gs is None else gs.contiguous()
-                    _stats_bwd_window(gs, (g_nov, None, g_e, g_c), False, t0, t1, R.cuda_stream)
-                    _stats_bwd_window(gs, (None, g_p, None, None), True, t0, t1, R.cuda_stream)
-                    tapes_ready = torch.cuda.Event()
-                    tapes_ready.record(R)
-                    # The reverse scan of window k + 2 finished before that of k + 1 began.
-                    if k + 2 < K:
-                        R.wait_event(scan_back[k + 2])
-                        core_weight_grads(k + 2)
-                with torch.cuda.stream(S):
-                    S.wait_event(tapes_ready)
-                    up = [gU, g_nov, g_p, g_ay, sink, g_e, g_c]
-                    bw = chunked._Bwd(code, GAT, params, starts[k, 0].contiguous(),
-                                      starts[k, 2].contiguous(), fwd_out, up, carry,
-                                      (gWx, gWgx, day), t0, t1, cus)
-                    tk = ops.KernelTimer.begin("core_scan_bwd", Wx)
-                    bw.launch(S)
-                    ops.KernelTimer.end(tk)
-                    bws.append(bw)
-                    bw_of[k] = bw
-                    carry = bw.g0
-                    ev = torch.cuda.Event()
-                    ev.record(S)
-                    scan_back[k] = ev
-            with torch.cuda.stream(R):
-                # The projection's weight gradients, beside the last reverse scan.
-                U2 = fwd_out.U.reshape(B * T, 2 * H)
-                g_short = g_short3.reshape(B * T, H)
-                gw = torch.empty((H, 3 * H), device=dev, dtype=W.dtype)
-                gw[:, :2 * H] = g_short.t() @ U2
-                gw[:, 2 * H:] = g_short.t() @ retr.reshape(B * T, H)
-                W.grad = gw
-                bias.grad = torch.sum(g_short, dim=0, dtype=torch.float32).to(bias.dtype)
-                if K > 1:
-                    R.wait_event(scan_back[1])
-                    core_weight_grads(1)
-            M.wait_stream(S)
+                    long_backward(K - 1)
+
+                carry = [None, None, None]
+                bws = []
+                scan_back: list[Optional[torch.cuda.Event]] = [None] * K
+                bw_of: dict = {}
+                for k in range(K - 1, -1, -1):
+                    t0, t1 = bounds[k]
+                    r, ay_leaf = chunks[k]
+                    st = M if k == K - 1 else R
+                    with torch.cuda.stream(st):
+                        read_out_backward(k)
+                        g_r = projection_grads(g_short3, k)
+                        # w_leaf is listed so that the engine runs the gather's backward, whose
+                        # gradient goes to the sink (it returns none for w_leaf itself).
+                        torch.autograd.backward([r], [g_r],
+                                                inputs=[ay_leaf, w_leaf, stats_leaf, *trainable])
+                        if ay_leaf.grad is not None:
+                            ops.window_add(g_ay[:, t0:t1], ay_leaf.grad.to(dt))
+                        else:
+                            g_ay[:, t0:t1].zero_()
+                    if st is not R:
+                        done = torch.cuda.Event()
+                        done.record(st)
+                        R.wait_event(done)
+                    with torch.cuda.stream(R):
+                        if k < K - 1:
+                            long_backward(k)
+                        # Window k of the write gradient is complete (only query chunks >= k
+                        # read it): the long channel's share joins it.
+                        gwk, gpk = long_grads[k]
+                        ops.window_add(sink[:, t0:t1], sink[:, t0:t1], gwk)
+                        ops.window_add(g_p[:, t0:t1], gpk)
+                        gs = stats_leaf.grad
+                        gs = torch.zeros_like(stats_leaf) if gs is None else gs.contiguous()
+                        _stats_bwd_window(gs, (g_nov, None, g_e, g_c), False, t0, t1, R.cuda_stream)
+                        _stats_bwd_window(gs, (None, g_p, None, None), True, t0, t1, R.cuda_stream)
+                        tapes_ready = torch.cuda.Event()
+                        tapes_ready.record(R)
+                        # The reverse scan of window k + 2 finished before that of k + 1 began.
+                        if k + 2 < K:
+                            R.wait_event(scan_back[k + 2])
+                            core_weight_grads(k + 2)
+                    with torch.cuda.stream(S):
+                        S.wait_event(tapes_ready)
+                        up = [gU, g_nov, g_p, g_ay, sink, g_e, g_c]
+                        bw = chunked._Bwd(code, GAT, params, starts[k, 0].contiguous(),
+                                          starts[k, 2].contiguous(), fwd_out, up, carry,
+                                          (gWx, gWgx, day), t0, t1, cus)
+                        tk = ops.KernelTimer.begin("core_scan_bwd", Wx)
+                        bw.launch(S)
+                        ops.KernelTimer.end(tk)
+                        bws.append(bw)
+                        bw_of[k] = bw
+                        carry = bw.g0
+                        ev = torch.cuda.Event()
+                        ev.record(S)
+                        scan_back[k] = ev
+                with torch.cuda.stream(R):
+                    # The projection's weight gradients, beside the last reverse scan.
+                    U2 = fwd_out.U.reshape(B * T, 2 * H)
+                    g_short = g_short3.reshape(B * T, H)
+                    gw = torch.empty((H, 3 * H), device=dev, dtype=W.dtype)
+                    gw[:, :2 * H] = g_short.t() @ U2
+                    gw[:, 2 * H:] = g_short.t() @ retr.reshape(B * T, H)
+                    W.grad = gw
+                    bias.grad = torch.sum(g_short, dim=0, dtype=torch.float32).to(bias.dtype)
+                    if K > 1:
+                        R.wait_event(scan_back[1])
+                        core_weight_grads(1)
+                M.wait_stream(S)
+                M.wait_stream(R)
+                core_weight_grads(0)
+                if gain_leaf.requires_grad:
+                    gain_leaf.grad = gain_parts.sum().reshape(gain_leaf.shape).to(gain_leaf.dtype)
+                for i, leaf in enumerate(logit_leaves):
+                    if leaf.requires_grad:
+                        leaf.grad = logit_sum[0][i].reshape(leaf.shape).to(leaf.dtype)
+                gvec = torch.stack(vec_parts).sum(0)
+                gscal = torch.stack(scal_parts).sum(0)
+                core = [gWx, gWgx, gUA_sum[:H], gUA_sum[H:], *[gvec[i] for i in range(16)],
+                        *[gscal[i] for i in range(3)]]
+                core = [g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(core, ctx.meta)]
+                grads = [p.grad for p in pleaves]
+            _check_scans(S, bws, "core scan backward")
+        finally:
+            # Also when an exception leaves: the caller's stream waits for all three
+            # streams, so buffers allocated on it are not reused while work still runs.
             M.wait_stream(R)
-            core_weight_grads(0)
-            if gain_leaf.requires_grad:
-                gain_leaf.grad = gain_parts.sum().reshape(gain_leaf.shape).to(gain_leaf.dtype)
-            for i, leaf in enumerate(logit_leaves):
-                if leaf.requires_grad:
-                    leaf.grad = logit_sum[0][i].reshape(leaf.shape).to(leaf.dtype)
-            gvec = torch.stack(vec_parts).sum(0)
-            gscal = torch.stack(scal_parts).sum(0)
-            core = [gWx, gWgx, gUA_sum[:H], gUA_sum[H:], *[gvec[i] for i in range(16)],
-                    *[gscal[i] for i in range(3)]]
-            core = [g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(core, ctx.meta)]
-            grads = [p.grad for p in pleaves]
-        _check_scans(S, bws, "core scan backward")
-        ambient.wait_stream(S)
-        ambient.wait_stream(M)
+            ambient.wait_stream(S)
+            ambient.wait_stream(M)
         for g in (*core, *grads):
             if g is not None:
                 g.record_stream(ambient)

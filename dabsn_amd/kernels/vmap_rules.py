@@ -88,6 +88,7 @@ def register() -> None:
         ops.local_field_gather: (0,),
         ops.admitted_three_way_read_compact_flash: (0, 1, 2, 3, 4, 5, 6, 7, 9, 10),
         ops.admitted_three_way_read_native: (0, 1, 2, 3, 4, 5, 6, 7, 9, 10, 11, 12),
+        ops.admitted_three_way_read: (0, 1, 2, 3, 4, 5, 6, 7, 9, 10, 11, 12),
         ops.long_scan_fused: (0, 1, 6, 7, 8),
     }
     out_rows = {ops.long_scan_fused: (0, 0, 0, 0, 1)}  # the saved states are [3, B, T, H]

@@ -115,8 +115,7 @@ class BankStore:
         rp = read.short_read
         prm = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain, rp.adm_novelty_gain,
                rp.adm_saturation_gain, rp.adm_energy_gain, rp.adm_bias)
-        watched = (*prm, read.admit_window)
-        key = (tuple((p.data_ptr(), p._version, p.dtype) for p in watched), tape_dtype, hidden)
+        key = self.glue_key(read, tape_dtype, hidden)
         if key != self._glue_key or self.admitted > length:
             self._glue_key, self.admitted = key, 0
         lo = self.admitted
@@ -132,6 +131,18 @@ class BankStore:
             self.admitted = length
         return (self.key_bias[:, :length], self.adm[:, :length], self.cocktail[:, :length],
                 (self.members, self.mcount))
+
+    @staticmethod
+    def glue_key(read, tape_dtype: torch.dtype, hidden: int) -> tuple:
+        """What the kept glue and slot lists depend on besides the bank rows: the admission
+        parameters (storage, version counter, dtype), the tape dtype, the width and the
+        parameter generation. An in-place edit through ``.data`` moves none of the first,
+        so it must be followed by ``ops.parameters_changed()`` (which moves the last)."""
+        rp = read.short_read
+        watched = (rp.p_gain, rp.novelty_gain, rp.null_bias, rp.adm_p_gain, rp.adm_novelty_gain,
+                   rp.adm_saturation_gain, rp.adm_energy_gain, rp.adm_bias, read.admit_window)
+        return (tuple((p.data_ptr(), p._version, p.dtype) for p in watched), tape_dtype, hidden,
+                ops.parameter_generation())
 
     def append(self, write: Tensor, stats: Tensor) -> None:
         """Write a chunk's rows after the live prefix (doubling the storage when full)."""
@@ -392,9 +403,10 @@ def forward_with_memory(model: DABSNSequenceLM, ids: Tensor, memory: DABSNMemory
     so repeated independent queries see the same context; with ``extend=True`` the query
     tokens are appended (streaming decode). Banks are extended in place: a memory that was
     extended should not be used through an older handle afterwards. The ops reuse their
-    fp32 copies of the model's parameters across calls while each parameter keeps its
-    storage and version counter; a weight edited in place through ``.data`` between calls
-    needs ``dabsn_amd.kernels.ops.clear_parameter_copies()``."""
+    fp32 copies of the model's parameters, and the banks their admission glue and slot
+    lists, across calls while each parameter keeps its storage and version counter
+    (``load_state_dict`` moves the counter); a weight edited in place through ``.data``
+    between calls needs ``dabsn_amd.kernels.ops.parameters_changed()``."""
     hidden, result = _run(model, ids, memory, chunk_size=chunk_size, extend=extend)
     if return_hidden:
         return hidden, result

@@ -204,7 +204,14 @@ class DABSNRead(nn.Module):
                 # masked out by `valid`.
                 n_max, bad = max(1, min(int(fixed), length)), True
             else:
-                top, bad = ops.bank_width(order, counts, want_fold).tolist()  # as read.py:233
+                # One host read, as read.py:233, that also carries the device's deferred
+                # kernel error word.
+                width = ops.bank_width(order, counts, want_fold)
+                word = ops.pending_error_word(order.device)
+                vals = (width if word is None else torch.cat((width, word))).tolist()
+                top, bad = vals[:2]
+                if len(vals) > 2:
+                    ops.raise_error_word(int(vals[2]), order.device)
                 n_max = max(int(top), 1)
             idx, valid, next_idx, read_idx, fold = ops.bank_slots(
                 order, counts, n_max, query_start, want_fold and not bad)

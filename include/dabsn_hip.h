@@ -559,6 +559,21 @@ int dabsn_hip_read_dense_fwd(int64_t B, int64_t T, int64_t N, int64_t H, const f
                              const uint8_t* induct_allow, const uint8_t* eligible,
                              const uint8_t* induct_eligible, const float* scalars, float* out,
                              void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* The same read returning also its three masked softmaxes (fp32 [B, T, N] each: short,
+ * permanent, induction), as the reference's 4-output operator dabsn::admitted_three_way_read
+ * does (src/dabsn/kernels/admitted.py:16-65; its autograd, admitted.py:126-247, works from
+ * those saved weights). The weight pointers are all given or all null. */
+int dabsn_hip_read_dense_fwd_weights(int64_t B, int64_t T, int64_t N, int64_t H,
+                                     const float* query, const float* bank_keys,
+                                     const float* bank_writes, const float* next_writes,
+                                     const float* cocktail, const float* bank_cocktail,
+                                     const float* bank_key_bias, const float* bank_admission,
+                                     const uint8_t* allow, const uint8_t* induct_allow,
+                                     const uint8_t* eligible, const uint8_t* induct_eligible,
+                                     const float* scalars, float* out, float* short_weights,
+                                     float* permanent_weights, float* induct_weights,
+                                     void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 int dabsn_hip_read_dense_bwd(int64_t B, int64_t T, int64_t N, int64_t H, const float* grad_out,
                              const float* query, const float* bank_keys, const float* bank_writes,
                              const float* next_writes, const float* cocktail,

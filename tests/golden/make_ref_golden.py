@@ -46,7 +46,7 @@ Fixtures (reference file:line of the function evaluated):
   ``forward_with_memory`` token.
 * ``op_schemas.json`` -- the dispatcher schema of every registered ``dabsn::`` operator
   this build replaces (kernels/batched_runtime.py:1507, compact_flash.py:71 and 182,
-  long.py:392 and 410, permanent.py:384, local_field.py:208, admitted.py:384 and 509), as
+  long.py:392 and 410, permanent.py:384, local_field.py:208, admitted.py:16, 384 and 509), as
   ``torch`` prints it: the interface a backend's kernels must accept.
 
 ``python tests/golden/make_ref_golden.py NAME ...`` writes only the named fixtures.
@@ -526,7 +526,8 @@ def memory_lm() -> None:
 SCHEMA_OPS = ("core_scan_batched", "admitted_three_way_read_compact_flash",
               "_admitted_three_way_read_compact_flash_backward", "linear_recurrence",
               "_linrec_backward", "permanent_delta_scan", "local_field_gather",
-              "admitted_three_way_read_native", "_admitted_three_way_read_backward")
+              "admitted_three_way_read_native", "_admitted_three_way_read_backward",
+              "admitted_three_way_read")
 
 
 def op_schemas() -> None:

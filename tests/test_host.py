@@ -212,3 +212,15 @@ def test_direct_calls_dispatch_outside_inference_and_for_host_tensors():
         "print('ok')\n")
     r = _run(code)
     assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
+
+
+def test_error_word_modes(monkeypatch):
+    """Unset, the scans' barrier word is deferred (no host synchronisation inside a scan
+    op) and input-validation words are read at once; the variable sets both."""
+    from dabsn_amd.kernels import ops
+
+    monkeypatch.delenv("DABSN_HIP_ERROR_CHECK", raising=False)
+    assert ops._sync_mode() == "deferred" and ops._sync_mode(input_check=True) == "sync"
+    for mode in ("sync", "deferred"):
+        monkeypatch.setenv("DABSN_HIP_ERROR_CHECK", mode)
+        assert ops._sync_mode() == mode and ops._sync_mode(input_check=True) == mode

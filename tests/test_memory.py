@@ -97,6 +97,34 @@ def test_bank_store_appends_in_place_and_doubles():
     assert bank.capacity == 16 and torch.equal(w, rows) and torch.equal(s, stats)
 
 
+def test_parameter_edits_through_data_need_parameters_changed():
+    """Kept parameter copies and a carried bank's admission key follow a parameter's storage
+    and version counter; an in-place edit through ``.data`` moves neither (the contract:
+    call ``parameters_changed()`` after it), ``load_state_dict`` does."""
+    from dabsn_amd.kernels import ops
+
+    p = torch.nn.Parameter(torch.ones(3))
+    twice = lambda x: x * 2  # noqa: E731
+    with ops.reuse_parameter_copies():
+        a = ops._derived("test_twice", (p,), twice)
+        p.data.copy_(torch.full((3,), 5.0))
+        assert torch.equal(ops._derived("test_twice", (p,), twice), a)  # kept: stale
+        dabsn_amd.kernels.parameters_changed()
+        assert torch.equal(ops._derived("test_twice", (p,), twice), torch.full((3,), 10.0))
+        with torch.no_grad():
+            p.copy_(torch.full((3,), 7.0))  # what load_state_dict does: the version moves
+        assert torch.equal(ops._derived("test_twice", (p,), twice), torch.full((3,), 14.0))
+    read = dabsn_amd.DABSNRead(8)
+    key = mem.BankStore.glue_key(read, torch.float32, 8)
+    read.short_read.adm_bias.data.copy_(torch.tensor([0.5]))
+    assert mem.BankStore.glue_key(read, torch.float32, 8) == key
+    dabsn_amd.kernels.parameters_changed()
+    assert mem.BankStore.glue_key(read, torch.float32, 8) != key
+    read.load_state_dict(dabsn_amd.DABSNRead(8).state_dict())
+    moved = mem.BankStore.glue_key(read, torch.float32, 8)
+    assert moved[0] != key[0]
+
+
 def test_memory_refuses_other_architecture_or_batch():
     model = _model("cpu")
     memory = mem.DABSNMemory(layers=[], position=0, batch_size=2,

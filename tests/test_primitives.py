@@ -165,6 +165,18 @@ def test_local_field_gather_rejects_out_of_range_indices(cuda_device):
 
 
 @pytest.mark.gpu
+def test_deferred_error_words_raise_at_check_errors(cuda_device, monkeypatch):
+    """With DABSN_HIP_ERROR_CHECK=deferred the same bad index does not synchronise the call:
+    the word stays on the device until ops.check_errors(), which raises once and clears it."""
+    monkeypatch.setenv("DABSN_HIP_ERROR_CHECK", "deferred")
+    x = torch.randn(1, 5, 4, device=cuda_device)
+    ops.local_field_gather(x, torch.tensor([[0, 7]], device=cuda_device))
+    with pytest.raises(RuntimeError, match="error word"):
+        ops.check_errors()
+    ops.check_errors()  # cleared
+
+
+@pytest.mark.gpu
 def test_local_field_helper_reports_its_route(cuda_device):
     x = torch.randn(2, 9, 6, device=cuda_device)
     out, route = K.local_field_gather(x, GATE_PATCH.to(cuda_device))
