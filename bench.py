@@ -43,12 +43,12 @@ def parse():
     p.add_argument("--hidden", type=int, default=4096)
     p.add_argument("--vocab", type=int, default=32000)
     p.add_argument("--chunk", type=int, default=1024)
-    p.add_argument("--cpu-seq", type=int, default=64, help="T of the bounded CPU sample")
+    p.add_argument("--cpu-seq", type=int, default=256, help="T of the bounded CPU sample")
     p.add_argument("--no-pipeline", action="store_true",
                    help="train: scan and read one after the other on the whole device")
     p.add_argument("--no-proj", action="store_true",
                    help="skip the separate timing of the input projections (profiling runs)")
-    p.add_argument("--cpu-trials", type=int, default=5,
+    p.add_argument("--cpu-trials", type=int, default=2,
                    help="timed CPU steps after one untimed warm-up step")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--workload", choices=("train", "decode", "primitives"), default="train",
@@ -180,7 +180,9 @@ def time_projections(args, model, device, dtype, reps: int = 5):
     """The block's input projections Wx = W x and Wgx = Wg x + b (core.py:281-282), which
     the scan+read step takes as resident inputs, timed on their own: forward (two GEMMs)
     and backward (input gradient as two accumulating GEMMs, two weight-gradient GEMMs) on
-    hipBLASLt through torch, bf16, [B*T, hidden] x [hidden, state]."""
+    hipBLASLt through torch, bf16, [B*T, hidden] x [hidden, state]; and the block combine's
+    state_to_hidden (model.py:336-337, [B*T, state] x [state, hidden]): forward one GEMM,
+    backward two (input and weight gradients)."""
     F = torch.nn.functional
     rows, D, H = args.batch * args.seq, args.hidden, args.state
     g = torch.Generator(device=device).manual_seed(3)
@@ -198,8 +200,20 @@ def time_projections(args, model, device, dtype, reps: int = 5):
         gx = torch.addmm(gy @ W, gz, Wg)
         return gx, gy.t() @ x, gz.t() @ x
 
+    Wsh = (torch.randn(D, H, device=device, generator=g) / H ** 0.5).to(dtype)
+    ysh = torch.randn(rows, H, device=device, dtype=dtype, generator=g)
+    gsh = torch.randn(rows, D, device=device, dtype=dtype, generator=g)
+
+    def sh_fwd():
+        return F.linear(ysh, Wsh)
+
+    def sh_bwd():
+        return gsh @ Wsh, gsh.t() @ ysh
+
     out = {}
-    for name, fn, gemms in (("forward", fwd, 2), ("backward", bwd, 4)):
+    for name, fn, gemms in (("forward", fwd, 2), ("backward", bwd, 4),
+                            ("state_to_hidden_forward", sh_fwd, 1),
+                            ("state_to_hidden_backward", sh_bwd, 2)):
         fn()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -212,7 +226,9 @@ def time_projections(args, model, device, dtype, reps: int = 5):
         tflops = gemms * 2.0 * rows * D * H / (ms / 1e3) / 1e12
         out[name] = {"ms": round(ms, 3), "tflops": round(tflops, 1),
                      "frac_bf16_peak": round(tflops / 2500.0, 4)}
-    out["note"] = ("not part of value: the scan+read step starts from resident Wx, Wgx; "
+    out["note"] = ("not part of value: the scan+read step starts from resident Wx, Wgx and "
+                   "ends at the read output; input projections [rows, hidden] x [hidden, state] "
+                   "and state_to_hidden [rows, state] x [state, hidden], "
                    f"rows {rows}, hidden {D}, state {H}, bf16, hipBLASLt via torch")
     return out
 
@@ -225,17 +241,35 @@ def cpu_baseline(args):
 
     oracle.build()
     torch_backend.register()
-    threads = int(os.environ.get("OMP_NUM_THREADS", min(16, os.cpu_count() or 1)))
+    omp_env = os.environ.get("OMP_NUM_THREADS")
+    threads = int(omp_env or min(16, os.cpu_count() or 1))
     oracle.set_num_threads(threads)
     torch.set_num_threads(threads)
     seq = int(args.cpu_seq)
-    model, Wx, Wgx, gy, gr = build_workload(args, torch.device("cpu"), torch.float32, args.batch, seq)
-    step(model, Wx, Wgx, gy, gr, "cpu", torch.float32)  # warm-up (page-in, thread pools)
-    times = []
-    for _ in range(max(1, int(args.cpu_trials))):
-        t0 = time.perf_counter()
-        step(model, Wx, Wgx, gy, gr, "cpu", torch.float32)
-        times.append(time.perf_counter() - t0)
+
+    def sample(T, trials):
+        model, Wx, Wgx, gy, gr = build_workload(args, torch.device("cpu"), torch.float32,
+                                                args.batch, T)
+        step(model, Wx, Wgx, gy, gr, "cpu", torch.float32)  # warm-up (page-in, thread pools)
+        out = []
+        for _ in range(max(1, trials)):
+            t0 = time.perf_counter()
+            step(model, Wx, Wgx, gy, gr, "cpu", torch.float32)
+            out.append(time.perf_counter() - t0)
+        return model, out
+
+    model, times = sample(seq, int(args.cpu_trials))
+    # A second, half-length sample fixes the two terms of the step time t(T) = a T + b T^2:
+    # the scan, the glue and the long channel are linear in T, the dense-bank read (every
+    # query against every earlier slot) quadratic. The fit extrapolates to the workload's T.
+    seq_half = max(1, seq // 2)
+    _, times_half = sample(seq_half, max(2, int(args.cpu_trials) // 2))
+    t1, t2 = sum(times_half) / len(times_half), sum(times) / len(times)
+    b_coef = (t2 / seq - t1 / seq_half) / (seq - seq_half)
+    a_coef = t1 / seq_half - b_coef * seq_half
+    if b_coef < 0 or a_coef < 0:  # timing noise on a tiny sample: keep the fit's sign sane
+        a_coef, b_coef = (t2 / seq, 0.0) if b_coef < 0 else (0.0, t2 / seq ** 2)
+    t_full = a_coef * args.seq + b_coef * args.seq ** 2
     tokens = args.batch * seq
     rates = [tokens / t for t in times]
     n = len(rates)
@@ -249,6 +283,13 @@ def cpu_baseline(args):
         "value": mean,
         "unit": "tokens/s",
         "cores": threads,
+        "threads": {"os_cpu_count": os.cpu_count(), "OMP_NUM_THREADS": omp_env,
+                    "torch_get_num_threads": torch.get_num_threads(),
+                    "oracle_threads": oracle.num_threads()},
+        "extrapolated": {"seq_len": args.seq, "tokens_per_s": args.batch * args.seq / t_full,
+                         "seconds_per_step": t_full, "linear_s_per_token_step": a_coef,
+                         "quadratic_s": b_coef, "fit": f"t(T) = a T + b T^2 through the mean "
+                         f"step times at T={seq_half} ({t1:.2f} s) and T={seq} ({t2:.2f} s)"},
         "kind": "port",
         "ci95": [mean - half, mean + half] if half is not None else None,
         "trials": n,
@@ -257,7 +298,7 @@ def cpu_baseline(args):
                    f"n_max={model.read.last_n_max}: 1 warm-up + {n} timed, mean "
                    f"{sum(times) / n:.2f} s each; T-truncated proxy of the T={args.seq} workload "
                    f"(scan cost scales with T, read with T*n_max)"),
-        "seconds": sum(times),
+        "seconds": sum(times) + sum(times_half),
     }
 
 

@@ -830,6 +830,10 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
   constexpr int NT = NW * 64;
   constexpr int KSTEP = M::KSTEP;
   constexpr int KB = 2 * KSTEPS;  // per-wave k-steps over the 2*KP adjoint input
+  // Exchange operands held at once: all KB k-steps, or groups of KC when the weights of a
+  // wide tile leave no room (64 fp32 / 16 bf16 k-steps: 64 registers per lane).
+  constexpr int KC = KB <= (is_bf16<E>::value ? 16 : 64) ? KB : (is_bf16<E>::value ? 8 : 32);
+  static_assert(KB % KC == 0, "exchange groups must divide the k-steps");
   constexpr int MTB = (CH + 15) / 16;
   constexpr int PAIRS = CH * NB;
   constexpr int NACC = 19;
@@ -1032,28 +1036,52 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
     if (s_abort) return;
 
     const uint32_t sbase = static_cast<uint32_t>(n & 1) * a.slot_bytes;
-    typename M::Reg breg[KB];
-#pragma unroll
-    for (int s = 0; s < KB; ++s)
-      breg[s] = M::load_x(xr, sbase + static_cast<uint32_t>((wave * KB + s) * 64 + lane) * M::UNIT);
-    // Keep every exchange load ahead of the first MFMA (all in flight at once).
-    __builtin_amdgcn_sched_barrier(0);
-    // Tapes of t - 2 are requested after the exchange loads. Completions are counted in
-    // issue order and the loads are unconditional in every wave (clamped indices), so the
-    // waits before the MFMAs count the exchange loads exactly and do not wait for these.
-    // Staged: one 16-byte load per chunk instead of 16 scattered loads per pair.
-    if constexpr (STAGE) {
-      load_chunks(t - 2, chunk);
-    } else {
-      load_tape(a, lrow0, lc, t - 2, nxt);
-    }
     f32x4 accm[MTB];
 #pragma unroll
     for (int mt = 0; mt < MTB; ++mt) accm[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if constexpr (KC == KB) {
+      typename M::Reg breg[KB];
 #pragma unroll
-    for (int s = 0; s < KB; ++s) {
+      for (int s = 0; s < KB; ++s)
+        breg[s] = M::load_x(xr, sbase + static_cast<uint32_t>((wave * KB + s) * 64 + lane) * M::UNIT);
+      // Keep every exchange load ahead of the first MFMA (all in flight at once).
+      __builtin_amdgcn_sched_barrier(0);
+      // Tapes of t - 2 are requested after the exchange loads. Completions are counted in
+      // issue order and the loads are unconditional in every wave (clamped indices), so the
+      // waits before the MFMAs count the exchange loads exactly and do not wait for these.
+      // Staged: one 16-byte load per chunk instead of 16 scattered loads per pair.
+      if constexpr (STAGE) {
+        load_chunks(t - 2, chunk);
+      } else {
+        load_tape(a, lrow0, lc, t - 2, nxt);
+      }
 #pragma unroll
-      for (int mt = 0; mt < MTB; ++mt) accm[mt] = M::mma(wreg[mt][s], breg[s], accm[mt]);
+      for (int s = 0; s < KB; ++s) {
+#pragma unroll
+        for (int mt = 0; mt < MTB; ++mt) accm[mt] = M::mma(wreg[mt][s], breg[s], accm[mt]);
+      }
+    } else {
+      // Wide tiles: the exchange operands come in groups of KC k-steps (the weights already
+      // fill most of the registers), the products in the same order as above.
+      if constexpr (STAGE) {
+        load_chunks(t - 2, chunk);
+      } else {
+        load_tape(a, lrow0, lc, t - 2, nxt);
+      }
+#pragma unroll
+      for (int s0 = 0; s0 < KB; s0 += KC) {
+        typename M::Reg breg[KC];
+#pragma unroll
+        for (int s = 0; s < KC; ++s)
+          breg[s] = M::load_x(
+              xr, sbase + static_cast<uint32_t>((wave * KB + s0 + s) * 64 + lane) * M::UNIT);
+#pragma unroll
+        for (int s = 0; s < KC; ++s) {
+#pragma unroll
+          for (int mt = 0; mt < MTB; ++mt)
+            accm[mt] = M::mma(wreg[mt][s0 + s], breg[s], accm[mt]);
+        }
+      }
     }
 #pragma unroll
     for (int mt = 0; mt < MTB; ++mt) {
@@ -1188,13 +1216,14 @@ struct Cfg {
 static Cfg pick(int dtype, int64_t B, int64_t H) {
   Cfg c;
   const int kstep = dtype == kBF16 ? 32 : 4;
-  // bf16 beyond H = 1024 uses 8 waves, each holding half as many weights.
-  c.nw = (dtype == kBF16 && H > 1024) ? 8 : 4;
+  // Beyond H = 1024, 8 waves, each holding half as many weights (bf16 up to H = 4096 with
+  // 16 k-steps of 32 per wave, fp32 up to H = 2048 with 64 k-steps of 4).
+  c.nw = H > 1024 ? 8 : 4;
   const int need = static_cast<int>((H + c.nw * kstep - 1) / (c.nw * kstep));
-  static const int bf_steps[] = {1, 2, 4, 8};
+  static const int bf_steps[] = {1, 2, 4, 8, 16};
   static const int f_steps[] = {1, 2, 4, 8, 16, 32, 64};
   const int* list = dtype == kBF16 ? bf_steps : f_steps;
-  const int nlist = dtype == kBF16 ? 4 : 7;
+  const int nlist = dtype == kBF16 ? 5 : 7;
   for (int i = 0; i < nlist; ++i) {
     if (list[i] >= need) {
       c.ksteps = list[i];
@@ -1369,9 +1398,9 @@ static int slab_count(K kernel, int threads, const Cfg& c, int64_t* launches) {
 
 // (CH, KSTEPS, NW) combinations compiled per dtype.
 #define DABSN_CORE_CASES_BF16(X) \
-  X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(16, 8, 4) X(16, 8, 8)
+  X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(16, 8, 4) X(16, 8, 8) X(16, 16, 8)
 #define DABSN_CORE_CASES_F32(X) \
-  X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(8, 16, 4) X(8, 32, 4) X(8, 64, 4)
+  X(8, 1, 4) X(8, 2, 4) X(8, 4, 4) X(8, 8, 4) X(8, 16, 4) X(8, 32, 4) X(8, 64, 4) X(8, 64, 8)
 
 // One-step scans: y_0, the recurrent products as one GEMM, the step. Decode batches of a
 // few hundred rows give only tens of 128 x 128 tiles (B=256, H=2048: 64 workgroups on 256
@@ -1516,10 +1545,6 @@ static int check_bwd(const dabsn_core_bwd_call& b, Cfg& c) {
   DABSN_REQUIRE(b.T == 0 || (b.U && b.plast && b.expr && b.energy && b.sat && b.gate && b.gWx &&
                              b.gWgx && b.day),
                 "core scan backward: null tape pointer");
-  if (b.dtype == kF32 && c.ksteps > 32) {
-    dabsn::set_error("core scan backward: fp32 supports H <= 512 per workgroup register budget");
-    return DABSN_ERR_UNSUPPORTED;
-  }
   if (b.dtype == kBF16 && c.ch == 16 && b.T > 0) {
     // The 16-unit bf16 kernels fetch tapes and grads as 16-byte chunks of 8 units.
     DABSN_REQUIRE(b.H % 16 == 0, "core scan backward: bf16 with H >= 1024 needs H %% 16 == 0 (H=%lld)",

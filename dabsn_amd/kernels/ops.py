@@ -362,6 +362,15 @@ def core_launch_check(code: int, B: int, T: int, H: int, backward: bool) -> int:
     return n
 
 
+def core_channel_tiles(code: int, B: int, H: int) -> int:
+    """Workgroups of one batch group of the core scan (its channel tiles) for dtype code
+    ``code`` at width ``H`` (a large number when the width is unsupported)."""
+    ch, ks, nw = _lib.i32(), _lib.i32(), _lib.i32()
+    rc = _lib.load().dabsn_hip_core_scan_config(code, B, H, ctypes.byref(ch), ctypes.byref(ks),
+                                               ctypes.byref(nw))
+    return -(-H // ch.value) if rc == 0 and ch.value > 0 else 1 << 30
+
+
 def scan_inputs(Wx: Tensor, Wgx: Tensor, dt: torch.dtype) -> tuple[Tensor, Tensor, int]:
     """(Wx, Wgx, ldx) as the scan reads them: unchanged when both are row-strided views
     with unit element stride and a common time stride ldx (the two halves of one

@@ -588,7 +588,25 @@ def enabled() -> bool:
     return os.environ.get("DABSN_PIPELINE", "1") != "0"
 
 
-def pipeline_applies(read, Wx: Tensor, chunk: int) -> bool:
-    """The pipelined path serves training of a seq block on the device with 2+ chunks."""
-    return (Wx.is_cuda and torch.is_grad_enabled() and read.read_geometry == "seq"
-            and 0 < chunk < int(Wx.shape[1]))
+def pipeline_applies(read, Wx: Tensor, chunk: int, state: Optional[int] = None,
+                     dtype: Optional[torch.dtype] = None) -> bool:
+    """The pipelined path serves training of a seq block on the device with 2+ chunks whose
+    scan fits one CU-masked half: the channel tiles of a batch group must be resident there
+    together (fp32 beyond H = 1024 needs the whole device). ``state`` and ``dtype``: the
+    scan's width and activation dtype when ``Wx`` stands for the block input."""
+    if not (Wx.is_cuda and torch.is_grad_enabled() and read.read_geometry == "seq"
+            and 0 < chunk < int(Wx.shape[1])):
+        return False
+    H = int(state if state is not None else Wx.shape[-1])
+    dt = dtype if dtype is not None else Wx.dtype
+    tiles = ops.core_channel_tiles(ops._code(dt), int(Wx.shape[0]), H)
+    half = stream_pair(Wx.device)[2]
+    if tiles > half:
+        events.report_fallback(
+            "core_scan_chunked", "the scan's channel tiles do not fit one half of the device",
+            requested_path="rocm_pipelined_scan_read",
+            selected_path="chunked scan, then the read, on the whole device",
+            corrective_action="train in bf16 (16-unit tiles) or at H <= 1024 in fp32",
+            H=H, dtype=str(dt), tiles=tiles, half_cus=half)
+        return False
+    return True

@@ -119,8 +119,10 @@ class DABSNBlock(nn.Module):
 
     def forward_world(self, inputs: Tensor) -> Tensor:
         chunk_t = self._resolve_block_chunk_t(inputs)
-        if self.training and pipeline.enabled() and pipeline.pipeline_applies(self.read, inputs,
-                                                                              chunk_t):
+        scan_dtype = (torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda")
+                      else inputs.dtype)
+        if self.training and pipeline.enabled() and pipeline.pipeline_applies(
+                self.read, inputs, chunk_t, state=self.state_dim, dtype=scan_dtype):
             # Training on the device with block chunking: the read of query chunk k runs
             # beside the scan of chunk k + 1 on the other half of the device.
             Wx, Wgx = self.core.projections(inputs)

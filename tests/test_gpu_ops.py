@@ -79,7 +79,8 @@ def _compare_core_bwd(res, ob, H, tol_t, tol_s, metric):
 
 
 @pytest.mark.parametrize("B,T,H", [(3, 5, 6), (1, 1, 8), (9, 1, 300), (8, 256, 96), (8, 256, 128),
-                                   (32, 64, 256), (16, 128, 512), (17, 20, 40)])
+                                   (32, 64, 256), (16, 128, 512), (17, 20, 40), (4, 32, 1024),
+                                   (2, 24, 2048)])
 def test_core_scan_fp32_forward_backward_match_oracle(cuda_device, B, T, H):
     inp = core_case(100 + H + T, B, T, H)
     fwd = oracle_core_fwd(inp)
@@ -93,7 +94,7 @@ def test_core_scan_fp32_forward_backward_match_oracle(cuda_device, B, T, H):
 
 
 @pytest.mark.parametrize("B,T,H", [(3, 5, 6), (5, 1, 36), (40, 1, 2048), (8, 64, 128),
-                                   (16, 64, 2048)])
+                                   (16, 64, 2048), (4, 16, 4096)])
 def test_core_scan_bf16_within_tolerance_of_fp32_oracle(cuda_device, B, T, H):
     inp = core_case(200 + H, B, T, H)
     fwd = oracle_core_fwd(inp)

@@ -232,3 +232,25 @@ def test_window_add_equals_torch(cuda_device, dtype, H):
     assert torch.equal(out[:, :t0], before[:, :t0]) and torch.equal(out[:, t1:], before[:, t1:])
     c = ops.window_copy(a[:, t0:t1, :H])
     assert c.is_contiguous() and torch.equal(c, a[:, t0:t1, :H])
+
+
+def test_pipeline_needs_the_scan_to_fit_one_half(cuda_device):
+    """The scan runs on the CU-masked half: fp32 at width 2048 (256 channel tiles of 8
+    units) does not fit there, so the block keeps the sequential path and a performance
+    fallback event says why; bf16 at the same width (128 tiles of 16) pipelines."""
+    from dabsn_amd import events
+
+    seen = []
+    listen = seen.append
+    events.add_event_listener(listen)
+    try:
+        _, read = _modules(1, 8, 2048, 0.7, cuda_device)
+        x = torch.zeros(2, 64, 2048, device=cuda_device)
+        with torch.enable_grad():
+            assert pipeline.pipeline_applies(read, x.bfloat16(), 32)
+            events.reset_routing_log()
+            assert not pipeline.pipeline_applies(read, x, 32)
+        falls = [e for e in seen if e.fallback and e.component_id == "core_scan_chunked"]
+        assert falls and "half" in falls[0].fields["reason"]
+    finally:
+        events.remove_event_listener(listen)
