@@ -843,7 +843,10 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
   __shared__ float accs[NB][CH][NACC];
   __shared__ int s_abort;
   constexpr bool STAGE = is_bf16<E>::value && CH == 16;
-  constexpr int CPT = STAGE ? (kTapeChunks + NT - 1) / NT : 1;  // chunks per thread
+  // Staged prefetch: waves 1.. load the chunks (wave 0 polls the step barrier, and a poll
+  // waits for every earlier load of its wave).
+  constexpr int NL = NT - 64;                                   // loading threads
+  constexpr int CPT = STAGE ? (kTapeChunks + NL - 1) / NL : 1;  // chunks per loading thread
   __shared__ __attribute__((aligned(16))) bf16 tape[STAGE ? kTapeStreams : 1][NB][16];
   // Per-unit parameters of the tile, shared by its 16 batch rows: read from LDS at each
   // reverse step instead of holding 17 registers per thread for the whole scan.
@@ -925,10 +928,11 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
   const E* ch_ptr[CPT];
   uint32_t ch_rs[CPT];
   bool ch_prev[CPT];
+  const int lt = tid - 64;  // loading thread index (waves 1..)
   if constexpr (STAGE) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int q = min(tid + i * NT, kTapeChunks - 1);
+      const int q = min(max(lt, 0) + i * NL, kTapeChunks - 1);
       const int sidx = q / (NB * 2), r = (q / 2) % NB, hh = q & 1;
       const TapeStream<E> ts = tape_stream(a, sidx);
       const int bb = bg * NB + r;
@@ -950,8 +954,8 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
   auto park_chunks = [&](const u32x4 (&v)[CPT]) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int q = tid + i * NT;
-      if (q < kTapeChunks)
+      const int q = lt + i * NL;
+      if (lt >= 0 && q < kTapeChunks)
         *reinterpret_cast<u32x4*>(&tape[q / (NB * 2)][(q / 2) % NB][(q & 1) * 8]) = v[i];
     }
   };
@@ -967,6 +971,42 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
     return r;
   };
   u32x4 chunk[CPT];
+
+  // Staged output stores (as the forward's tapes): a step's three outputs per pair -- gWgx
+  // and da_y of t, gWx of t + 1 -- are parked in LDS (two buffers, alternating by step) and
+  // written out as 16-byte chunks during the next step by waves 1.., so the polling wave 0
+  // has no stores queued ahead of its counter polls.
+  constexpr int GSN = 3;
+  constexpr int GCH = GSN * NB * 2;                     // chunks per step
+  constexpr int GCPT = STAGE ? (GCH + NL - 1) / NL : 1;  // chunks per loading thread
+  __shared__ __attribute__((aligned(16))) bf16 gpark[STAGE ? 2 : 1][STAGE ? GSN : 1][NB][16];
+  E* g_ptr[GCPT];
+  int g_q[GCPT];
+  if constexpr (STAGE) {
+#pragma unroll
+    for (int i = 0; i < GCPT; ++i) {
+      const int q = lt + i * NL;
+      const int sidx = q / (NB * 2), r = (q / 2) % NB, hh = q & 1;
+      const int bb = bg * NB + r;
+      const bool ok = lt >= 0 && q < GCH && bb < B;
+      E* const dst[GSN] = {a.gWgx, a.day, a.gWx};
+      g_q[i] = ok ? q : -1;
+      g_ptr[i] = ok ? dst[sidx] + static_cast<size_t>(bb) * static_cast<size_t>(a.ldt) * H +
+                          ct * 16 + hh * 8
+                    : nullptr;
+    }
+  }
+  // Write out the outputs parked at step n (time t): gWx of t + 1 only for n > 0.
+  auto gflush = [&](int n, int t) {
+#pragma unroll
+    for (int i = 0; i < GCPT; ++i) {
+      const int q = g_q[i];
+      const int sidx = q / (NB * 2);
+      if (q >= 0 && (sidx < 2 || n > 0))
+        gstore16(g_ptr[i] + static_cast<size_t>(sidx < 2 ? t : t + 1) * H,
+                 *reinterpret_cast<const u32x4*>(&gpark[n & 1][sidx][(q / 2) % NB][(q & 1) * 8]));
+    }
+  };
 
   // Pipeline state at the top of the step for time t: dg/dx are the final adjoint inputs
   // of t, keep_* the final carried grads towards t - 1 (budget without the pre-activation
@@ -1012,14 +1052,30 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
       publish<E, CH, 2>(xr, a.slot_bytes, n & 1, kb2, v, is_pair, cl, bl);
       if (tid == 0) arrive(counter);
     }
+    // Staged: the tapes of t - 2 are requested right after the exchange stores drained, so
+    // they have the whole step to land before the next step parks them (the next drain
+    // waits for every load of the wave).
+    if constexpr (STAGE) {
+      if (wave > 0) load_chunks(t - 2, chunk);
+    }
     // Off the critical path: outputs of t (and the pre-activation grad of t + 1) and the
     // X = 0 part of the reverse step at t - 1.
+    if constexpr (STAGE) {
+      if (n > 0) gflush(n - 1, t + 1);
+      if (is_pair) {
+        gpark[n & 1][0][bl][cl] = f2bf(dg);
+        gpark[n & 1][1][bl][cl] = f2bf(dx);
+        gpark[n & 1][2][bl][cl] = f2bf(xprev);
+      }
+    }
     Pending pd = {};
     if (act) {
-      const size_t rt = (row0 + t) * H + c;
-      st(a.gWgx, rt, dg);
-      st(a.day, rt, dx);
-      if (n > 0) st(a.gWx, rt + H, xprev);
+      if constexpr (!STAGE) {
+        const size_t rt = (row0 + t) * H + c;
+        st(a.gWgx, rt, dg);
+        st(a.day, rt, dx);
+        if (n > 0) st(a.gWx, rt + H, xprev);
+      }
       if (t >= 1) {
         const UnitParams upl = upar[cl];
         if constexpr (STAGE) {
@@ -1046,15 +1102,11 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
         breg[s] = M::load_x(xr, sbase + static_cast<uint32_t>((wave * KB + s) * 64 + lane) * M::UNIT);
       // Keep every exchange load ahead of the first MFMA (all in flight at once).
       __builtin_amdgcn_sched_barrier(0);
-      // Tapes of t - 2 are requested after the exchange loads. Completions are counted in
-      // issue order and the loads are unconditional in every wave (clamped indices), so the
-      // waits before the MFMAs count the exchange loads exactly and do not wait for these.
-      // Staged: one 16-byte load per chunk instead of 16 scattered loads per pair.
-      if constexpr (STAGE) {
-        load_chunks(t - 2, chunk);
-      } else {
-        load_tape(a, lrow0, lc, t - 2, nxt);
-      }
+      // Unstaged: tapes of t - 2 are requested after the exchange loads. Completions are
+      // counted in issue order and the loads are unconditional in every wave (clamped
+      // indices), so the waits before the MFMAs count the exchange loads exactly and do not
+      // wait for these.
+      if constexpr (!STAGE) load_tape(a, lrow0, lc, t - 2, nxt);
 #pragma unroll
       for (int s = 0; s < KB; ++s) {
 #pragma unroll
@@ -1063,11 +1115,7 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
     } else {
       // Wide tiles: the exchange operands come in groups of KC k-steps (the weights already
       // fill most of the registers), the products in the same order as above.
-      if constexpr (STAGE) {
-        load_chunks(t - 2, chunk);
-      } else {
-        load_tape(a, lrow0, lc, t - 2, nxt);
-      }
+      if constexpr (!STAGE) load_tape(a, lrow0, lc, t - 2, nxt);
 #pragma unroll
       for (int s0 = 0; s0 < KB; s0 += KC) {
         typename M::Reg breg[KC];
@@ -1113,6 +1161,10 @@ __device__ __forceinline__ void bwd_body(const BwdArgs<E>& a, int bid, int grid)
     }
   }
 
+  if constexpr (STAGE) {
+    // The last step's parked outputs (made visible by that step's barriers).
+    if (T > 0) gflush(T - 1, 0);
+  }
   if (act) {
     if (T > 0) st(a.gWx, row0 * H + c, xprev);
     a.gb0[bh] = T > 0 ? keep_b : (a.gbF ? a.gbF[bh] : 0.0f);
@@ -1550,7 +1602,7 @@ static int check_bwd(const dabsn_core_bwd_call& b, Cfg& c) {
     DABSN_REQUIRE(b.H % 16 == 0, "core scan backward: bf16 with H >= 1024 needs H %% 16 == 0 (H=%lld)",
                   (long long)b.H);
     const void* streams[] = {b.U, b.plast, b.expr, b.energy, b.sat, b.gate, b.gU, b.gNov,
-                             b.gP, b.gAy, b.gW, b.gE, b.gC};
+                             b.gP, b.gAy, b.gW, b.gE, b.gC, b.gWx, b.gWgx, b.day};
     for (const void* q : streams)
       DABSN_REQUIRE(q == nullptr || (reinterpret_cast<uintptr_t>(q) & 15u) == 0,
                     "core scan backward: bf16 tape and grad pointers must be 16-byte aligned");

@@ -16,9 +16,13 @@
 // T is cut into chunks of CK steps. For each recurrence in turn, a chunk-parallel pass
 // computes every chunk's end value from a zero start (plus the product of eff_t for L),
 // and a per-channel pass over the chunks turns those into the true chunk-start values
-// (a checkpoint in the workspace). A last chunk pass writes the output and, for the
-// backward, the states entering every step. The backward composes each chunk's affine map of the three adjoints (see the
-// backward kernels below) and carries the maps across chunks in one per-channel pass.
+// (the checkpoint, [B][nseg][3][H] fp32, kept for the backward). A last chunk pass writes
+// the output. The backward composes each chunk's affine map of the three adjoints (see the
+// backward kernels below) and carries the maps across chunks in one per-channel pass; both
+// of its chunk passes replay the forward recurrence over their chunk from the checkpoint
+// (the same step function as the forward, so the replayed states are the forward's bits)
+// instead of reading per-step states, which would be 12 bytes per (row, step, unit) written
+// once and read twice.
 #include "../../include/dabsn_hip.h"
 #include "capi.hpp"
 #include "common.hpp"
@@ -103,6 +107,20 @@ struct Logits {
   const float* p[4];
 };
 
+// One step of the three recurrences from the states entering it (L, E, R), in the step
+// order of long.py:492-579: pe = tanh|w - E|, then E, R, the retention eff and L advance.
+// Every pass that walks the recurrence (forward, and the backward's replays) calls this,
+// so the states a replay produces are bit-identical to the forward's.
+__device__ __forceinline__ void advance(const Coef& k, float wt, float pt, float& L, float& Ev,
+                                        float& R, float& pe, float& eff) {
+  pe = tanhf(fabsf(wt - Ev));
+  Ev = k.er * Ev + (1.0f - k.er) * wt;
+  R = k.rd * R + (1.0f - k.rd) * (1.0f - pe);
+  const float sal = pt * pe;
+  eff = k.ret + (1.0f - k.ret) * k.rs * R;
+  L = eff * L + (1.0f - eff) * (sal * wt);
+}
+
 // er^n for n <= CK by repeated multiplication (fixed order).
 __device__ __forceinline__ float powi(float x, int n) {
   float r = 1.0f;
@@ -133,12 +151,11 @@ __device__ __forceinline__ bool chunk_idx(int B, int T, int H, ChunkIdx& c) {
 
 // Forward chunk pass. PHASE 0: E from 0 -> loc0 = E end. PHASE 1: E from its true start,
 // R from 0 -> loc0 = R end. PHASE 2: E, R from true starts, L from 0 -> loc0 = L end,
-// loc1 = prod eff. PHASE 3: all from true starts -> out, and (if `states` is given) the
-// states entering every step, [3][B][T][H] fp32 = (L, E, R)_{t-1}, for the backward.
+// loc1 = prod eff. PHASE 3: all from true starts (the checkpoint) -> out.
 template <typename E, int PHASE>
 __global__ void __launch_bounds__(NT) long_fwd_chunk(int B, int T, int H, const E* w, const E* p,
                                                      Logits lg, const float* ckpt, float* loc0,
-                                                     float* loc1, E* out, float* states) {
+                                                     float* loc1, E* out) {
   ChunkIdx c;
   if (!chunk_idx(B, T, H, c)) return;
   const Coef k = load_coef(lg.p);
@@ -155,15 +172,14 @@ __global__ void __launch_bounds__(NT) long_fwd_chunk(int B, int T, int H, const 
   float R = PHASE >= 2 ? ckpt[c.cbase + 2 * H] : 0.0f;
   float L = PHASE >= 3 ? ckpt[c.cbase] : 0.0f;
   float prod = 1.0f;
-  const size_t bth = static_cast<size_t>(B) * T * H;
 #pragma unroll
   for (int i = 0; i < CK; ++i) {
     if (i < c.len) {
-      if (PHASE == 3 && states) {
-        const size_t o = c.base + static_cast<size_t>(c.t0 + i) * H;
-        states[o] = L;
-        states[bth + o] = Ev;
-        states[2 * bth + o] = R;
+      if (PHASE == 3) {
+        float pe, eff;
+        advance(k, wv[i], pv[i], L, Ev, R, pe, eff);
+        st(out, c.base + static_cast<size_t>(c.t0 + i) * H, L);
+        continue;
       }
       const float pe = PHASE >= 1 ? tanhf(fabsf(wv[i] - Ev)) : 0.0f;
       Ev = k.er * Ev + (1.0f - k.er) * wv[i];
@@ -173,7 +189,6 @@ __global__ void __launch_bounds__(NT) long_fwd_chunk(int B, int T, int H, const 
         const float eff = k.ret + (1.0f - k.ret) * k.rs * R;
         L = eff * L + (1.0f - eff) * (sal * wv[i]);
         prod *= eff;
-        if (PHASE == 3) st(out, c.base + static_cast<size_t>(c.t0 + i) * H, L);
       }
     }
   }
@@ -189,32 +204,28 @@ __global__ void __launch_bounds__(NT) long_fwd_chunk(int B, int T, int H, const 
 // A sequence of at most one chunk (T <= CK: streaming decode, short query chunks): the
 // three recurrences walked once per channel from the given initial state, in the step
 // order of long.py:492-579 (as phase 3 above), with the final state taken from the walk.
+// The checkpoint (if given) of the one chunk is the initial state.
 template <typename E>
 __global__ void __launch_bounds__(NT) long_fwd_single(int B, int T, int H, const E* w, const E* p,
                                                       Logits lg, const float* L0, const float* E0,
                                                       const float* R0, E* out, float* LF,
-                                                      float* EF, float* RF, float* states) {
+                                                      float* EF, float* RF, float* ckpt) {
   const int64_t ch = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
   if (ch >= static_cast<int64_t>(B) * H) return;
   const Coef k = load_coef(lg.p);
   const int b = static_cast<int>(ch / H), h = static_cast<int>(ch % H);
   const size_t base = static_cast<size_t>(b) * T * H + h;
-  const size_t bth = static_cast<size_t>(B) * T * H;
   float L = L0[ch], Ev = E0[ch], R = R0[ch];
+  if (ckpt) {
+    float* cp = ckpt + static_cast<size_t>(b) * 3 * H + h;
+    cp[0] = L;
+    cp[H] = Ev;
+    cp[2 * H] = R;
+  }
   for (int t = 0; t < T; ++t) {
     const size_t o = base + static_cast<size_t>(t) * H;
-    const float wv = ld(w, o), pv = ld(p, o);
-    if (states) {
-      states[o] = L;
-      states[bth + o] = Ev;
-      states[2 * bth + o] = R;
-    }
-    const float pe = tanhf(fabsf(wv - Ev));
-    Ev = k.er * Ev + (1.0f - k.er) * wv;
-    R = k.rd * R + (1.0f - k.rd) * (1.0f - pe);
-    const float sal = pv * pe;
-    const float eff = k.ret + (1.0f - k.ret) * k.rs * R;
-    L = eff * L + (1.0f - eff) * (sal * wv);
+    float pe, eff;
+    advance(k, ld(w, o), ld(p, o), L, Ev, R, pe, eff);
     st(out, o, L);
   }
   LF[ch] = L;
@@ -257,9 +268,8 @@ __global__ void __launch_bounds__(NT) long_fwd_carry(int B, int T, int H, Logits
 // with A = M_0 ... M_{len-1} and v = sum_i (M_0 ... M_{i-1}) M_i g_i e0, both accumulated
 // in forward time order, so one forward pass over each chunk yields its map; a per-channel pass over the chunks then gives the exact
 // adjoints entering each chunk, and a last pass walks each chunk backward with those
-// adjoints to produce gw, gp and the logit partials. Both chunk passes read the forward
-// values around each step from the per-step states the forward wrote, so they stream
-// instead of replaying the recurrence.
+// adjoints to produce gw, gp and the logit partials. Both chunk passes replay the forward
+// recurrence over their chunk from its checkpoint for the values around each step.
 
 // Per-step coefficients of M_t from the forward values around step t.
 struct StepMap {
@@ -283,54 +293,50 @@ __device__ __forceinline__ StepMap step_map(const Coef& k, float wt, float pt, f
 }
 
 // Chunk maps: A (lower triangular, 6 entries) and v (3 entries), stored component-major
-// in `maps` [9][nseg][B*H]. The forward values around each step are read from `states`.
+// in `maps` [9][nseg][B*H]. The forward values around each step are replayed from the
+// chunk's checkpoint.
 template <typename E>
 __global__ void __launch_bounds__(NT) long_bwd_map(int B, int T, int H, const E* w, const E* p,
-                                                   Logits lg, const float* states, const E* gout,
+                                                   Logits lg, const float* ckpt, const E* gout,
                                                    float* maps) {
   ChunkIdx c;
   if (!chunk_idx(B, T, H, c)) return;
   const Coef k = load_coef(lg.p);
-  const size_t bth = static_cast<size_t>(B) * T * H;
+  float wv[CK], pv[CK], gv[CK];
+#pragma unroll
+  for (int i = 0; i < CK; ++i) {
+    // Clamped, unconditional loads so all requests are in flight at once (steps past the
+    // chunk end are never used).
+    const size_t o = c.base + static_cast<size_t>(c.t0 + min(i, c.len - 1)) * H;
+    wv[i] = ld(w, o);
+    pv[i] = ld(p, o);
+    gv[i] = ld(gout, o);
+  }
+  float L = ckpt[c.cbase], Ev = ckpt[c.cbase + H], R = ckpt[c.cbase + 2 * H];
   float p00 = 1.f, p10 = 0.f, p11 = 1.f, p20 = 0.f, p21 = 0.f, p22 = 1.f;
   float v0 = 0.f, v1 = 0.f, v2 = 0.f;
-  constexpr int LB = 8;  // steps loaded ahead
-  for (int i0 = 0; i0 < c.len; i0 += LB) {
-    float wv[LB], pv[LB], gv[LB], Lv[LB], Ev[LB], Rv[LB];
 #pragma unroll
-    for (int j = 0; j < LB; ++j) {
-      // Clamped, unconditional loads (steps past the chunk end are never used).
-      const size_t o = c.base + static_cast<size_t>(c.t0 + min(i0 + j, c.len - 1)) * H;
-      wv[j] = ld(w, o);
-      pv[j] = ld(p, o);
-      gv[j] = ld(gout, o);
-      Lv[j] = states[o];
-      Ev[j] = states[bth + o];
-      Rv[j] = states[2 * bth + o];
-    }
-#pragma unroll
-    for (int j = 0; j < LB; ++j) {
-      if (i0 + j < c.len) {
-        const float pe = tanhf(fabsf(wv[j] - Ev[j]));
-        const float Rcur = k.rd * Rv[j] + (1.0f - k.rd) * (1.0f - pe);
-        const float eff = k.ret + (1.0f - k.ret) * k.rs * Rcur;
-        const StepMap m = step_map(k, wv[j], pv[j], Lv[j], Ev[j], pe, eff);
-        // v += P (M_i g_i e0)
-        const float u0 = m.m00 * gv[j], u1 = m.m10 * gv[j], u2 = m.m20 * gv[j];
-        v0 += p00 * u0;
-        v1 += p10 * u0 + p11 * u1;
-        v2 += p20 * u0 + p21 * u1 + p22 * u2;
-        // P = P M_i
-        const float n20 = p20 * m.m00 + p21 * m.m10 + p22 * m.m20;
-        const float n21 = p21 * m.m11 + p22 * m.m21;
-        const float n10 = p10 * m.m00 + p11 * m.m10;
-        p00 *= m.m00;
-        p10 = n10;
-        p11 *= m.m11;
-        p20 = n20;
-        p21 = n21;
-        p22 *= m.m22;
-      }
+  for (int i = 0; i < CK; ++i) {
+    if (i < c.len) {
+      const float Lp = L, Ep = Ev;
+      float pe, eff;
+      advance(k, wv[i], pv[i], L, Ev, R, pe, eff);
+      const StepMap m = step_map(k, wv[i], pv[i], Lp, Ep, pe, eff);
+      // v += P (M_i g_i e0)
+      const float u0 = m.m00 * gv[i], u1 = m.m10 * gv[i], u2 = m.m20 * gv[i];
+      v0 += p00 * u0;
+      v1 += p10 * u0 + p11 * u1;
+      v2 += p20 * u0 + p21 * u1 + p22 * u2;
+      // P = P M_i
+      const float n20 = p20 * m.m00 + p21 * m.m10 + p22 * m.m20;
+      const float n21 = p21 * m.m11 + p22 * m.m21;
+      const float n10 = p10 * m.m00 + p11 * m.m10;
+      p00 *= m.m00;
+      p10 = n10;
+      p11 *= m.m11;
+      p20 = n20;
+      p21 = n21;
+      p22 *= m.m22;
     }
   }
   const size_t stride = static_cast<size_t>(c.nseg) * B * H;
@@ -378,12 +384,12 @@ __global__ void __launch_bounds__(NT) long_bwd_carry(int B, int T, int H, const 
   gE0[ch] = x2;
 }
 
-// Final pass: walk each chunk backward from the exact entering adjoints (maps components
-// 0..2), reading the forward values from `states`; writes gw, gp and reduces the logit
-// gradients per block (fixed order).
+// Final pass: replay the chunk forward from its checkpoint (the states entering every step
+// kept in registers), then walk it backward from the exact entering adjoints (maps
+// components 0..2); writes gw, gp and reduces the logit gradients per block (fixed order).
 template <typename E>
 __global__ void __launch_bounds__(NT) long_bwd_final(int B, int T, int H, const E* w, const E* p,
-                                                     Logits lg, const float* states,
+                                                     Logits lg, const float* ckpt,
                                                      const E* gout, const float* maps, E* gw,
                                                      E* gp, float* part) {
   __shared__ float red[4][NT];
@@ -392,53 +398,55 @@ __global__ void __launch_bounds__(NT) long_bwd_final(int B, int T, int H, const 
   const Coef k = load_coef(lg.p);
   float d_er = 0.f, d_rd = 0.f, d_ret = 0.f, d_rs = 0.f;
   if (ok) {
-    const size_t bth = static_cast<size_t>(B) * T * H;
+    float wv[CK], pv[CK], gv[CK], Lv[CK], Ev[CK], Rv[CK];
+#pragma unroll
+    for (int i = 0; i < CK; ++i) {
+      // Clamped, unconditional loads (steps past the chunk end are never used).
+      const size_t o = c.base + static_cast<size_t>(c.t0 + min(i, c.len - 1)) * H;
+      wv[i] = ld(w, o);
+      pv[i] = ld(p, o);
+      gv[i] = ld(gout, o);
+    }
+    float L = ckpt[c.cbase], Es = ckpt[c.cbase + H], R = ckpt[c.cbase + 2 * H];
+#pragma unroll
+    for (int i = 0; i < CK; ++i) {
+      Lv[i] = L;
+      Ev[i] = Es;
+      Rv[i] = R;
+      if (i < c.len) {
+        float pe, eff;
+        advance(k, wv[i], pv[i], L, Es, R, pe, eff);
+      }
+    }
     const size_t stride = static_cast<size_t>(c.nseg) * B * H;
     const size_t li = static_cast<size_t>(c.k) * B * H + c.ch;
     float gLc = maps[li], gRc = maps[li + stride], gEc = maps[li + 2 * stride];
-    constexpr int LB = 8;  // steps loaded ahead (walking backward)
-    for (int i1 = c.len - 1; i1 >= 0; i1 -= LB) {
-      float wv[LB], pv[LB], gv[LB], Lv[LB], Ev[LB], Rv[LB];
 #pragma unroll
-      for (int j = 0; j < LB; ++j) {
-        const int i = i1 - j;
-        // Clamped, unconditional loads (steps before the chunk start are never used).
-        const size_t o = c.base + static_cast<size_t>(c.t0 + (i < 0 ? 0 : i)) * H;
-        wv[j] = ld(w, o);
-        pv[j] = ld(p, o);
-        gv[j] = ld(gout, o);
-        Lv[j] = states[o];
-        Ev[j] = states[bth + o];
-        Rv[j] = states[2 * bth + o];
-      }
-#pragma unroll
-      for (int j = 0; j < LB; ++j) {
-        const int i = i1 - j;
-        if (i >= 0) {
-          const float wt = wv[j], pt = pv[j];
-          const float diff = wt - Ev[j];
-          const float pe = tanhf(fabsf(diff));
-          const float sal = pt * pe;
-          const float Rcur = k.rd * Rv[j] + (1.0f - k.rd) * (1.0f - pe);
-          const float eff = k.ret + (1.0f - k.ret) * k.rs * Rcur;
-          const float gL = gv[j] + gLc;
-          const float deff = gL * (Lv[j] - sal * wt);
-          const float dsal = gL * (1.0f - eff) * wt;
-          gLc = gL * eff;
-          const float dR = gRc + deff * (1.0f - k.ret) * k.rs;
-          gRc = dR * k.rd;
-          const float dpe = dsal * pt - dR * (1.0f - k.rd);
-          const float darg = dpe * (1.0f - pe * pe) * signf_(diff);
-          const float dE = gEc;
-          gEc = k.er * dE - darg;
-          const size_t o = c.base + static_cast<size_t>(c.t0 + i) * H;
-          st(gp, o, dsal * pe);
-          st(gw, o, gL * (1.0f - eff) * sal + darg + (1.0f - k.er) * dE);
-          d_er += dE * (Ev[j] - wt);
-          d_rd += dR * (Rv[j] - (1.0f - pe));
-          d_ret += deff * (1.0f - k.rs * Rcur);
-          d_rs += deff * (1.0f - k.ret) * Rcur;
-        }
+    for (int i = CK - 1; i >= 0; --i) {
+      if (i < c.len) {
+        const float wt = wv[i], pt = pv[i];
+        const float diff = wt - Ev[i];
+        const float pe = tanhf(fabsf(diff));
+        const float sal = pt * pe;
+        const float Rcur = k.rd * Rv[i] + (1.0f - k.rd) * (1.0f - pe);
+        const float eff = k.ret + (1.0f - k.ret) * k.rs * Rcur;
+        const float gL = gv[i] + gLc;
+        const float deff = gL * (Lv[i] - sal * wt);
+        const float dsal = gL * (1.0f - eff) * wt;
+        gLc = gL * eff;
+        const float dR = gRc + deff * (1.0f - k.ret) * k.rs;
+        gRc = dR * k.rd;
+        const float dpe = dsal * pt - dR * (1.0f - k.rd);
+        const float darg = dpe * (1.0f - pe * pe) * signf_(diff);
+        const float dE = gEc;
+        gEc = k.er * dE - darg;
+        const size_t o = c.base + static_cast<size_t>(c.t0 + i) * H;
+        st(gp, o, dsal * pe);
+        st(gw, o, gL * (1.0f - eff) * sal + darg + (1.0f - k.er) * dE);
+        d_er += dE * (Ev[i] - wt);
+        d_rd += dR * (Rv[i] - (1.0f - pe));
+        d_ret += deff * (1.0f - k.rs * Rcur);
+        d_rs += deff * (1.0f - k.ret) * Rcur;
       }
     }
   }
@@ -471,44 +479,45 @@ using namespace dabsn::longmem;
 template <typename E>
 static int long_fwd_impl(int B, int T, int H, const E* w, const E* p, Logits lg, const float* L0,
                          const float* E0, const float* R0, E* out, float* LF, float* EF, float* RF,
-                         float* states, float* ws, hipStream_t stream) {
+                         float* keep, float* ws, hipStream_t stream) {
   const int gx = grid_for(B, H);
   const int nseg = (T + CK - 1) / CK;
   float* loc0 = ws;
   float* loc1 = ws + static_cast<size_t>(nseg) * B * H;
-  float* ckpt = ws + 2 * static_cast<size_t>(nseg) * B * H;  // [B][nseg][3][H]
+  // [B][nseg][3][H]: the caller's buffer when it keeps the checkpoint, else the workspace.
+  float* ckpt = keep ? keep : ws + 2 * static_cast<size_t>(nseg) * B * H;
   const dim3 cg(gx, nseg), blk(NT);
   if (nseg == 1) {  // one chunk: a single walk, no chunk-parallel passes
     hipLaunchKernelGGL((long_fwd_single<E>), dim3(gx), blk, 0, stream, B, T, H, w, p, lg, L0, E0,
-                       R0, out, LF, EF, RF, states);
+                       R0, out, LF, EF, RF, keep);
     DABSN_HIP_CHECK(hipGetLastError());
     return DABSN_OK;
   }
-  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 0>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out, states);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 0>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out);
   hipLaunchKernelGGL(long_fwd_carry<1>, dim3(gx), blk, 0, stream, B, T, H, lg, E0, loc0, loc1, ckpt, EF);
-  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 1>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out, states);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 1>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out);
   hipLaunchKernelGGL(long_fwd_carry<2>, dim3(gx), blk, 0, stream, B, T, H, lg, R0, loc0, loc1, ckpt, RF);
-  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 2>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out, states);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 2>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out);
   hipLaunchKernelGGL(long_fwd_carry<0>, dim3(gx), blk, 0, stream, B, T, H, lg, L0, loc0, loc1, ckpt, LF);
-  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 3>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out, states);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 3>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
 
 template <typename E>
 static int long_bwd_impl(int B, int T, int H, const E* w, const E* p, Logits lg,
-                         const float* states, const E* gout, const float* gLF, const float* gEF,
+                         const float* ckpt, const E* gout, const float* gLF, const float* gEF,
                          const float* gRF, E* gw, E* gp, float* gL0, float* gE0, float* gR0,
                          float* part, float* ws, hipStream_t stream) {
   const int gx = grid_for(B, H);
   const int nseg = (T + CK - 1) / CK;
   const dim3 cg(gx, nseg), blk(NT);
   if (nseg > 0)
-    hipLaunchKernelGGL(long_bwd_map<E>, cg, blk, 0, stream, B, T, H, w, p, lg, states, gout, ws);
+    hipLaunchKernelGGL(long_bwd_map<E>, cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, gout, ws);
   hipLaunchKernelGGL(long_bwd_carry, dim3(gx), blk, 0, stream, B, T, H, gLF, gRF, gEF, ws, gL0,
                      gR0, gE0);
   if (nseg > 0)
-    hipLaunchKernelGGL(long_bwd_final<E>, cg, blk, 0, stream, B, T, H, w, p, lg, states, gout,
+    hipLaunchKernelGGL(long_bwd_final<E>, cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, gout,
                        ws, gw, gp, part);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
@@ -563,14 +572,15 @@ int dabsn_hip_linrec_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void*
 
 size_t dabsn_hip_long_workspace_bytes(int64_t B, int64_t T, int64_t H, int backward) {
   const int64_t nseg = (T + CK - 1) / CK;
-  // forward: two chunk-end arrays + the chunk-start checkpoint (3 per chunk);
+  // forward: two chunk-end arrays + the chunk-start checkpoint (3 per chunk; used when the
+  // caller passes no checkpoint buffer of its own);
   // backward: the 9-component chunk maps.
   return static_cast<size_t>(backward ? 9 : 5) * static_cast<size_t>(nseg) * B * H * sizeof(float);
 }
 
 int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
                        const float* const* logits, const float* L0, const float* E0,
-                       const float* R0, void* out, float* LF, float* EF, float* RF, float* states,
+                       const float* R0, void* out, float* LF, float* EF, float* RF, float* ckpt,
                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
   DABSN_SHAPE_CHECK(B, T, H);
   DABSN_REQUIRE(w && p && logits && L0 && E0 && R0 && (out || T == 0) && LF && EF && RF &&
@@ -584,10 +594,10 @@ int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w
   Logits lg{{logits[0], logits[1], logits[2], logits[3]}};
   if (dtype == kBF16)
     return long_fwd_impl<bf16>((int)B, (int)T, (int)H, (const bf16*)w, (const bf16*)p, lg, L0,
-                               E0, R0, (bf16*)out, LF, EF, RF, states, (float*)workspace, stream);
+                               E0, R0, (bf16*)out, LF, EF, RF, ckpt, (float*)workspace, stream);
   if (dtype == kF32)
     return long_fwd_impl<float>((int)B, (int)T, (int)H, (const float*)w, (const float*)p, lg, L0,
-                                E0, R0, (float*)out, LF, EF, RF, states, (float*)workspace,
+                                E0, R0, (float*)out, LF, EF, RF, ckpt, (float*)workspace,
                                 stream);
   DABSN_REQUIRE(false, "long scan: bad dtype %d", dtype);
   return DABSN_OK;
@@ -598,12 +608,12 @@ int64_t dabsn_hip_long_partials(int64_t B, int64_t T, int64_t H) {
 }
 
 int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
-                       const float* const* logits, const float* states, const void* gout,
+                       const float* const* logits, const float* ckpt, const void* gout,
                        const float* gLF, const float* gEF, const float* gRF, void* gw, void* gp,
                        float* gL0, float* gE0, float* gR0, float* part_logit, void* workspace,
                        size_t workspace_bytes, hipStream_t stream) {
   DABSN_SHAPE_CHECK(B, T, H);
-  DABSN_REQUIRE(w && p && logits && (states || T == 0) && (gout || T == 0) && gL0 && gE0 && gR0 &&
+  DABSN_REQUIRE(w && p && logits && (ckpt || T == 0) && (gout || T == 0) && gL0 && gE0 && gR0 &&
                     (part_logit || T == 0) && (workspace || T == 0) && ((gw && gp) || T == 0),
                 "long scan backward: null pointer");
   for (int i = 0; i < 4; ++i) DABSN_REQUIRE(logits[i], "long scan backward: null logit %d", i);
@@ -613,11 +623,11 @@ int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w
   DABSN_REQUIRE((T + CK - 1) / CK < 65536, "long scan backward: T too long");
   Logits lg{{logits[0], logits[1], logits[2], logits[3]}};
   if (dtype == kBF16)
-    return long_bwd_impl<bf16>((int)B, (int)T, (int)H, (const bf16*)w, (const bf16*)p, lg, states,
+    return long_bwd_impl<bf16>((int)B, (int)T, (int)H, (const bf16*)w, (const bf16*)p, lg, ckpt,
                                (const bf16*)gout, gLF, gEF, gRF, (bf16*)gw, (bf16*)gp, gL0, gE0,
                                gR0, part_logit, (float*)workspace, stream);
   if (dtype == kF32)
-    return long_bwd_impl<float>((int)B, (int)T, (int)H, (const float*)w, (const float*)p, lg, states,
+    return long_bwd_impl<float>((int)B, (int)T, (int)H, (const float*)w, (const float*)p, lg, ckpt,
                                 (const float*)gout, gLF, gEF, gRF, (float*)gw, (float*)gp, gL0,
                                 gE0, gR0, part_logit, (float*)workspace, stream);
   DABSN_REQUIRE(false, "long scan backward: bad dtype %d", dtype);

@@ -1110,6 +1110,14 @@ torch.library.register_autograd(_q("read_output"), _read_output_bwd,
 # ---------------------------------------------------------------------------
 # Fused recurrent long-memory scan
 # ---------------------------------------------------------------------------
+LONG_CKPT = 32  # steps per chunk of the long scan (DABSN_LONG_CKPT)
+
+
+def long_segments(T: int) -> int:
+    """Chunks of the long scan over T steps (rows of its checkpoint)."""
+    return -(-int(T) // LONG_CKPT)
+
+
 @torch.library.custom_op(_q("long_scan_fused"), mutates_args=(), device_types="cuda")
 def long_scan_fused(
     write: Tensor, plasticity: Tensor, logit_expect_retain: Tensor,
@@ -1117,8 +1125,9 @@ def long_scan_fused(
     long0: Tensor, expected0: Tensor, retention0: Tensor,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """The three recurrences of long.py:492-579, chunked over time. Returns (long [B,T,H],
-    final long, final expected, final retention [B,H] fp32, per-step states [3,B,T,H] fp32
-    saved for the backward)."""
+    final long, final expected, final retention [B,H] fp32, and the checkpoint the backward
+    replays from: the states (L, E, R) entering every 32-step chunk, [B, ceil(T/32), 3, H]
+    fp32)."""
     _require_cuda(write)
     lib = _lib.load()
     B, T, H = write.shape
@@ -1131,32 +1140,33 @@ def long_scan_fused(
     L0, E0, R0 = (x.float().contiguous() for x in (long0, expected0, retention0))
     out = torch.empty_like(w)
     LF, EF, RF = (torch.empty((B, H), device=w.device, dtype=torch.float32) for _ in range(3))
-    states = torch.empty((3, B, T, H), device=w.device, dtype=torch.float32)
+    ckpt = torch.empty((B, long_segments(T), 3, H), device=w.device, dtype=torch.float32)
     nbytes = lib.dabsn_hip_long_workspace_bytes(B, T, H, 0)
     ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=w.device)
     tk = KernelTimer.begin("long_scan_fwd", w)
     _lib.check(lib.dabsn_hip_long_fwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(L0), _p(E0),
-                                      _p(R0), _p(out), _p(LF), _p(EF), _p(RF), _p(states),
+                                      _p(R0), _p(out), _p(LF), _p(EF), _p(RF), _p(ckpt),
                                       _p(ws), nbytes, _stream(w)), "long scan")
     KernelTimer.end(tk)
-    return out, LF, EF, RF, states
+    return out, LF, EF, RF, ckpt
 
 
 @long_scan_fused.register_fake
 def _long_scan_fused_fake(write, plasticity, l1, l2, l3, l4, long0, expected0, retention0):
     B, T, H = write.shape
     f = lambda *s: write.new_empty(s, dtype=torch.float32)  # noqa: E731
-    return torch.empty_like(write), f(B, H), f(B, H), f(B, H), f(3, B, T, H)
+    return torch.empty_like(write), f(B, H), f(B, H), f(B, H), f(B, long_segments(T), 3, H)
 
 
 @torch.library.custom_op(_q("_long_scan_fused_backward"), mutates_args=(),
                          device_types="cuda")
 def long_scan_fused_backward(
-    write: Tensor, plasticity: Tensor, logits: list[Tensor], states: Tensor, grad_long: Tensor,
-    g_long_final: Optional[Tensor], g_expected_final: Optional[Tensor],
+    write: Tensor, plasticity: Tensor, logits: list[Tensor], checkpoint: Tensor,
+    grad_long: Tensor, g_long_final: Optional[Tensor], g_expected_final: Optional[Tensor],
     g_retention_final: Optional[Tensor],
 ) -> list[Tensor]:
-    """Reverse of long_scan_fused: [g_write, g_plasticity, 4 logit grads, gL0, gE0, gR0]."""
+    """Reverse of long_scan_fused from its checkpoint: [g_write, g_plasticity, 4 logit
+    grads, gL0, gE0, gR0]."""
     _require_cuda(write)
     lib = _lib.load()
     B, T, H = write.shape
@@ -1176,7 +1186,10 @@ def long_scan_fused_backward(
     nbytes = lib.dabsn_hip_long_workspace_bytes(B, T, H, 1)
     ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=w.device)
     tk = KernelTimer.begin("long_scan_bwd", w)
-    st = states.float().contiguous()
+    st = checkpoint.float().contiguous()
+    if tuple(st.shape) != (B, long_segments(T), 3, H):
+        raise ValueError(f"long scan backward: checkpoint shape {tuple(st.shape)}, expected "
+                         f"{(B, long_segments(T), 3, H)}")
     _lib.check(lib.dabsn_hip_long_bwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(st), _p(gout),
                                       *[_p(x) for x in gf], _p(gw), _p(gp), *[_p(x) for x in g0],
                                       _p(part), _p(ws), nbytes, _stream(w)), "long scan backward")
@@ -1186,7 +1199,7 @@ def long_scan_fused_backward(
 
 
 @long_scan_fused_backward.register_fake
-def _long_scan_fused_backward_fake(write, plasticity, logits, states, grad_long, a, b, c):
+def _long_scan_fused_backward_fake(write, plasticity, logits, checkpoint, grad_long, a, b, c):
     B, T, H = write.shape
     f = lambda *s: write.new_empty(s, dtype=torch.float32)  # noqa: E731
     return [torch.empty_like(write), torch.empty_like(plasticity), f(), f(), f(), f(),
@@ -1197,17 +1210,17 @@ def _long_setup(ctx, inputs, output):
     write, plasticity, l1, l2, l3, l4, L0, E0, R0 = inputs
     ctx.save_for_backward(write, plasticity, l1, l2, l3, l4, output[4])
     ctx.meta = [(x.dtype, tuple(x.shape)) for x in inputs]
-    # The per-step states are saved for the backward, not a result anyone differentiates;
+    # The checkpoint is saved for the backward, not a result anyone differentiates;
     # with grads left unmaterialised, unused outputs bring None instead of zero tensors.
     ctx.mark_non_differentiable(output[4])
     ctx.set_materialize_grads(False)
 
 
-def _long_bwd(ctx, g_long, g_lf, g_ef, g_rf, _g_states):
-    write, plasticity, l1, l2, l3, l4, states = ctx.saved_tensors
+def _long_bwd(ctx, g_long, g_lf, g_ef, g_rf, _g_ckpt):
+    write, plasticity, l1, l2, l3, l4, ckpt = ctx.saved_tensors
     if g_long is None:
         g_long = torch.zeros_like(write)
-    grads = long_scan_fused_backward(write, plasticity, [l1, l2, l3, l4], states, g_long, g_lf,
+    grads = long_scan_fused_backward(write, plasticity, [l1, l2, l3, l4], ckpt, g_long, g_lf,
                                      g_ef, g_rf)
     return tuple(g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(grads, ctx.meta))
 

@@ -250,11 +250,18 @@ class _PipelinedScanRead(torch.autograd.Function):
 
                 U = out.U
                 ay, w, pl = out.tapes[2], out.tapes[3], out.tapes[1]
-                w_leaf = w.detach().requires_grad_(True)
-                stats_leaf = stats.detach().requires_grad_(True)
-                param_leaves = {n: p.detach().requires_grad_(p.requires_grad)
-                                for n, p in zip(names, read_params)}
-                norms = stats_leaf[..., 5].detach()
+                # Leaves of the per-chunk read graphs, one set for the chunks read on the read
+                # half and one for the last chunk's read on the whole-device stream: a leaf's
+                # gradient accumulator belongs to the stream of the graph that first uses it,
+                # and a gradient produced on another stream makes the engine synchronise the
+                # two. The backward sums the two sets.
+                def leaf_set():
+                    return (w.detach().requires_grad_(True), stats.detach().requires_grad_(True),
+                            {n: p.detach().requires_grad_(p.requires_grad)
+                             for n, p in zip(names, read_params)})
+
+                sets = (leaf_set(), leaf_set())
+                norms = stats[..., 5]
                 Wd = read.short_read.out.weight.detach().to(dt)
                 bd = read.short_read.out.bias.detach().to(dt)
 
@@ -262,7 +269,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                     return _SinkGather.apply(sink, bank_write, norm_w, idx,
                                              None if fold is not None else next_idx, rank)
 
-                def read_chunk(k: int):
+                def read_chunk(k: int, leaves):
                     # Statistics of window k, the three-way read of query chunk k against the
                     # bank [0, t1) (its own autograd graph) and, without autograd, its output
                     # projection (differentiated by hand in the backward): the [y, budget] block
@@ -273,6 +280,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                     st = torch.cuda.current_stream(dev)
                     _stats_window(out, stats, t0, t1, st.cuda_stream)
                     pre = F.linear(ops.window_copy(U[:, t0:t1]).view(B * C, 2 * H), Wd[:, :2 * H], bd)
+                    w_leaf, stats_leaf, _ = leaves
                     with torch.enable_grad():
                         # A contiguous copy of the expression window as the leaf (the read's
                         # normalisation reads it densely).
@@ -289,7 +297,7 @@ class _PipelinedScanRead(torch.autograd.Function):
 
                 # The long channel (long.py:492-579) window by window from the state the previous
                 # window ends in, differentiated by hand: per window its write and plasticity
-                # rows (contiguous copies, kept) and the states entering every step.
+                # rows (contiguous copies, kept) and the checkpoint its backward replays from.
                 events.announce("recurrent_long_read", "rocm_chunk_parallel_scan", B=B, T=T, H=H,
                                 dtype="bf16" if code == 1 else "fp32")
                 longs = []
@@ -300,17 +308,17 @@ class _PipelinedScanRead(torch.autograd.Function):
                     t0, t1 = bounds[k]
                     wk = ops.window_copy(w[:, t0:t1])
                     pk = ops.window_copy(pl[:, t0:t1])
-                    lk, lf, ef, rf, states = ops.direct.long_scan_fused(wk, pk, *logits, *carried)
+                    lk, lf, ef, rf, ckpt = ops.direct.long_scan_fused(wk, pk, *logits, *carried)
                     carried = (lf, ef, rf)
                     ops.window_add(long_out[:, t0:t1], lk)
-                    longs.append((wk, pk, states))
+                    longs.append((wk, pk, ckpt))
 
                 chunks = []
-                with _parameters_as(read, param_leaves):
+                with _parameters_as(read, sets[0][2]):
                     with torch.cuda.stream(R):
                         for k in range(K - 1):
                             R.wait_event(scan_done[k])
-                            chunks.append(read_chunk(k))
+                            chunks.append(read_chunk(k, sets[0]))
                             if k == K - 2:
                                 r_chunks = torch.cuda.Event()
                                 r_chunks.record(R)
@@ -321,9 +329,10 @@ class _PipelinedScanRead(torch.autograd.Function):
                         long_window(K - 1)
                         r_long = torch.cuda.Event()
                         r_long.record(R)
-                    M.wait_event(scan_done[K - 1])
-                    M.wait_event(r_chunks)
-                    chunks.append(read_chunk(K - 1))
+                M.wait_event(scan_done[K - 1])
+                M.wait_event(r_chunks)
+                with _parameters_as(read, sets[1][2]):
+                    chunks.append(read_chunk(K - 1, sets[1]))
                     M.wait_event(r_long)
                     ops.read_output_window(short, long_out, gain, read_out, *bounds[K - 1])
                 M.wait_stream(S)
@@ -340,7 +349,7 @@ class _PipelinedScanRead(torch.autograd.Function):
         ctx.read, ctx.chunk, ctx.names = read, chunk, names
         ctx.bounds = bounds
         ctx.meta = [(x.dtype, tuple(x.shape)) for x in (Wx, Wgx, *core_in)]
-        ctx.graph = (chunks, longs, w_leaf, stats_leaf, param_leaves, sink, long_out)
+        ctx.graph = (chunks, longs, sets, sink, long_out)
         ctx.out_dtype = read_out.dtype
         ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, starts, retr, out.U, *out.tapes)
         ctx.set_materialize_grads(False)
@@ -358,7 +367,11 @@ class _PipelinedScanRead(torch.autograd.Function):
         vecs, scal = saved[4:20], saved[20:23]
         starts, retr = saved[23], saved[24]
         fwd_out = chunked._Tapes(None, 0, 0, 0, existing=saved[25:33])
-        chunks, longs, w_leaf, stats_leaf, param_leaves, sink, long_out = ctx.graph
+        chunks, longs, sets, sink, long_out = ctx.graph
+        # Leaves of the read-half chunks, and of the last chunk (whole-device stream): the
+        # hand-differentiated parameters' gradients go to the first set, and the second
+        # set's gradients are added to it at the end.
+        (_, stats_leaf, param_leaves), (_, stats_last, last_leaves) = sets
         read = ctx.read
         B, T, H = Wx.shape
         dt = Wx.dtype
@@ -373,7 +386,7 @@ class _PipelinedScanRead(torch.autograd.Function):
         GAT = GA.t().contiguous()
         params, keep = ops._core_params(vecs, scal)
         pleaves = list(param_leaves.values())
-        trainable = [p for p in pleaves if p.requires_grad]
+        trainable = [[p for p in s[2].values() if p.requires_grad] for s in sets]
         W = param_leaves["short_read.out.weight"]
         bias = param_leaves["short_read.out.bias"]
         Wd = W.detach().to(dt)
@@ -446,9 +459,9 @@ class _PipelinedScanRead(torch.autograd.Function):
             # Window k of the long channel: its rows' gradient plus the gradient of the state
             # it ends in (from window k + 1's backward); leaves the gradient of the state it
             # starts from for window k - 1.
-            wk, pk, states = longs[k]
+            wk, pk, ckpt = longs[k]
             t0, t1 = bounds[k]
-            g = ops.long_scan_fused_backward(wk, pk, logit_leaves, states,
+            g = ops.long_scan_fused_backward(wk, pk, logit_leaves, ckpt,
                                              ops.window_copy(g_long[:, t0:t1]), *state_grad)
             long_grads[k] = (g[0], g[1])
             part = torch.stack(g[2:6])
@@ -478,13 +491,14 @@ class _PipelinedScanRead(torch.autograd.Function):
                     t0, t1 = bounds[k]
                     r, ay_leaf = chunks[k]
                     st = M if k == K - 1 else R
+                    side = 1 if k == K - 1 else 0
                     with torch.cuda.stream(st):
                         read_out_backward(k)
                         g_r = projection_grads(g_short3, k)
-                        # w_leaf is listed so that the engine runs the gather's backward, whose
-                        # gradient goes to the sink (it returns none for w_leaf itself).
-                        torch.autograd.backward([r], [g_r],
-                                                inputs=[ay_leaf, w_leaf, stats_leaf, *trainable])
+                        # The write leaf is listed so that the engine runs the gather's backward,
+                        # whose gradient goes to the sink (it returns none for the leaf itself).
+                        torch.autograd.backward([r], [g_r], inputs=[ay_leaf, sets[side][0],
+                                                                     sets[side][1], *trainable[side]])
                         if ay_leaf.grad is not None:
                             ops.window_add(g_ay[:, t0:t1], ay_leaf.grad.to(dt))
                         else:
@@ -501,6 +515,9 @@ class _PipelinedScanRead(torch.autograd.Function):
                         gwk, gpk = long_grads[k]
                         ops.window_add(sink[:, t0:t1], sink[:, t0:t1], gwk)
                         ops.window_add(g_p[:, t0:t1], gpk)
+                        if k == K - 1:
+                            # Later chunks of the read half add theirs to the last chunk's.
+                            stats_leaf.grad = stats_last.grad
                         gs = stats_leaf.grad
                         gs = torch.zeros_like(stats_leaf) if gs is None else gs.contiguous()
                         _stats_bwd_window(gs, (g_nov, None, g_e, g_c), False, t0, t1, R.cuda_stream)
@@ -551,6 +568,10 @@ class _PipelinedScanRead(torch.autograd.Function):
                 core = [gWx, gWgx, gUA_sum[:H], gUA_sum[H:], *[gvec[i] for i in range(16)],
                         *[gscal[i] for i in range(3)]]
                 core = [g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(core, ctx.meta)]
+                for n, leaf in last_leaves.items():
+                    if leaf.grad is not None:
+                        mine = param_leaves[n]
+                        mine.grad = leaf.grad if mine.grad is None else mine.grad + leaf.grad
                 grads = [p.grad for p in pleaves]
             _check_scans(S, bws, "core scan backward")
         finally:

@@ -91,7 +91,7 @@ def register() -> None:
         ops.admitted_three_way_read: (0, 1, 2, 3, 4, 5, 6, 7, 9, 10, 11, 12),
         ops.long_scan_fused: (0, 1, 6, 7, 8),
     }
-    out_rows = {ops.long_scan_fused: (0, 0, 0, 0, 1)}  # the saved states are [3, B, T, H]
+    out_rows = {ops.long_scan_fused: (0, 0, 0, 0, 0)}  # the checkpoint is [B, nseg, 3, H]
     for op, rows in fold.items():
         torch.library.register_vmap(op, _fold_rule(op, rows, out_rows.get(op)))
 

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 16
+#define DABSN_HIP_ABI_VERSION 17
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -174,23 +174,23 @@ int dabsn_hip_linrec_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void*
  * Fused form of the three recurrences of src/dabsn/kernels/long.py:492-579 (loop form
  * read.py:625-636). logits[4] point at fp32 scalars (logit_expect_retain,
  * logit_retention_decay, logit_retain, logit_retention_strength). State L0/E0/R0 [B,H]
- * fp32 in, LF/EF/RF out. `states` (may be NULL) receives the fp32 states entering every
- * step, [3][B][T][H] = (L, E, R)_{t-1}; the backward reads them. Both directions are
- * chunked over time (chunks of DABSN_LONG_CKPT steps) and need
- * dabsn_hip_long_workspace_bytes() bytes of workspace. */
+ * fp32 in, LF/EF/RF out. Both directions are chunked over time (chunks of DABSN_LONG_CKPT
+ * steps) and need dabsn_hip_long_workspace_bytes() bytes of workspace. `ckpt` (may be NULL)
+ * receives the checkpoint the backward replays each chunk from: the fp32 states entering
+ * every chunk, [B][ceil(T / DABSN_LONG_CKPT)][3][H] = (L, E, R). */
 #define DABSN_LONG_CKPT 32
 size_t dabsn_hip_long_workspace_bytes(int64_t B, int64_t T, int64_t H, int backward);
 int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
                        const float* const* logits, const float* L0, const float* E0,
-                       const float* R0, void* out, float* LF, float* EF, float* RF, float* states,
+                       const float* R0, void* out, float* LF, float* EF, float* RF, float* ckpt,
                        void* workspace, size_t workspace_bytes, hipStream_t stream);
-/* Backward: gout [B,T,H], gLF/gEF/gRF (may be NULL), the forward's `states`. Outputs gw, gp
+/* Backward: gout [B,T,H], gLF/gEF/gRF (may be NULL), the forward's `ckpt`. Outputs gw, gp
  * [B,T,H], gL0, gE0, gR0 [B,H], and part_logit [nblocks][4] with nblocks =
  * dabsn_hip_long_partials(B, T, H): per-block partial sums of the gradient w.r.t. the four
  * logits. */
 int64_t dabsn_hip_long_partials(int64_t B, int64_t T, int64_t H);
 int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
-                       const float* const* logits, const float* states, const void* gout,
+                       const float* const* logits, const float* ckpt, const void* gout,
                        const float* gLF, const float* gEF, const float* gRF, void* gw, void* gp,
                        float* gL0, float* gE0, float* gR0, float* part_logit, void* workspace,
                        size_t workspace_bytes, hipStream_t stream);

@@ -73,19 +73,19 @@ def _long(write, plasticity, l1, l2, l3, l4, L0, E0, R0):
     out, (LF, EF, RF) = oracle.long_fwd(_np(write), _np(plasticity), _coef(l1, l2, l3, l4),
                                         _np(L0), _np(E0), _np(R0))
     B, T, H = write.shape
-    # The op's saved states [3,B,T,H]; the oracle backward only needs the ones entering
-    # step 0 (the initial state) and replays the rest itself.
-    states = torch.zeros((3, B, T, H))
+    # The op's checkpoint [B, ceil(T/32), 3, H]; the oracle backward only needs the states
+    # entering the first chunk (the initial state) and replays the rest itself.
+    ckpt = torch.zeros((B, -(-T // 32), 3, H))
     if T > 0:
-        states[0, :, 0] = L0.float()
-        states[1, :, 0] = E0.float()
-        states[2, :, 0] = R0.float()
-    return _t(out, write.dtype), _t(LF), _t(EF), _t(RF), states
+        ckpt[:, 0, 0] = L0.float()
+        ckpt[:, 0, 1] = E0.float()
+        ckpt[:, 0, 2] = R0.float()
+    return _t(out, write.dtype), _t(LF), _t(EF), _t(RF), ckpt
 
 
-def _long_bwd(write, plasticity, logits, states, grad_long, gLF, gEF, gRF):
+def _long_bwd(write, plasticity, logits, checkpoint, grad_long, gLF, gEF, gRF):
     coef = _coef(*logits)
-    L0, E0, R0 = (_np(states[k, :, 0]) for k in range(3))
+    L0, E0, R0 = (_np(checkpoint[:, 0, k]) for k in range(3))
     gw, gp, (gL0, gE0, gR0), gcoef = oracle.long_bwd(
         _np(write), _np(plasticity), coef, L0, E0, R0, _np(grad_long),
         [None if g is None else _np(g) for g in (gLF, gEF, gRF)])
