@@ -38,6 +38,13 @@ __device__ __forceinline__ float ld<bf16>(const bf16* p, size_t i) { return bf2f
 
 __device__ __forceinline__ float to_f(float v) { return v; }
 __device__ __forceinline__ float to_f(bf16 v) { return bf2f(v); }
+// The element of type E that st() stores for v.
+template <typename E>
+__device__ __forceinline__ E from_f(float v);
+template <>
+__device__ __forceinline__ float from_f<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ bf16 from_f<bf16>(float v) { return f2bf(v); }
 
 template <typename E>
 __device__ __forceinline__ void st(E* p, size_t i, float v);

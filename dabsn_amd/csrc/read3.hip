@@ -680,9 +680,15 @@ __global__ void reduce_final_kernel(int nblocks, const float* part, float* out5)
 template <typename E>
 __global__ void __launch_bounds__(xpose::TNT) fold_transpose_kernel(int R, int C, const E* PV,
                                                                    const E* PVn,
-                                                                   const int8_t* fold, E* out) {
+                                                                   const int8_t* fold, E* out,
+                                                                   bool aligned) {
   constexpr int TT = xpose::TT, PITCH = TT + 2;
-  __shared__ float tile[TT][PITCH];
+  constexpr int VEC = 16 / static_cast<int>(sizeof(E));  // elements per 16-byte vector
+  constexpr int VPR = TT / VEC;                          // vectors per tile row
+  // P_V and P_Vn tiles as stored (no rounding on the way in); the P_Vn tile is one column
+  // wider on the left (index cc + 1 holds column c0 + cc).
+  __shared__ E tpv[TT][PITCH];
+  __shared__ E tpn[TT][PITCH];
   __shared__ int8_t fl[TT + 1];
   const int b = blockIdx.z;
   const int r0 = blockIdx.y * TT, c0 = blockIdx.x * TT;
@@ -693,22 +699,56 @@ __global__ void __launch_bounds__(xpose::TNT) fold_transpose_kernel(int R, int C
     const int c = c0 - 1 + i;
     fl[i] = (c >= 0 && c < C) ? fb[c] : int8_t(2);  // 2: nothing folds from or into here
   }
-  __syncthreads();
-  for (int q = threadIdx.x; q < TT * TT; q += xpose::TNT) {
-    const int r = q / TT, cc = q % TT;
-    const int rr = r0 + r, c = c0 + cc;
-    if (rr >= R || c >= C) continue;
-    const size_t o = static_cast<size_t>(rr) * C + c;
-    float v = to_f(pv[o]);
-    if (fl[cc + 1] == 0) v += to_f(pn[o]);
-    if (fl[cc] == 1) v += to_f(pn[o - 1]);
-    tile[r][cc] = v;
+  const bool full = aligned && r0 + TT <= R && c0 + TT <= C && (C % VEC) == 0 && (R % VEC) == 0;
+  if (full) {
+    for (int q = threadIdx.x; q < TT * VPR; q += xpose::TNT) {
+      const int r = q / VPR, cv = (q % VPR) * VEC;
+      const size_t o = static_cast<size_t>(r0 + r) * C + c0 + cv;
+      E a[VEC], n[VEC];
+      *reinterpret_cast<u32x4*>(a) = *reinterpret_cast<const u32x4*>(pv + o);
+      *reinterpret_cast<u32x4*>(n) = *reinterpret_cast<const u32x4*>(pn + o);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        tpv[r][cv + k] = a[k];
+        tpn[r][cv + k + 1] = n[k];
+      }
+    }
+    for (int r = threadIdx.x; r < TT; r += xpose::TNT)
+      tpn[r][0] = c0 > 0 ? pn[static_cast<size_t>(r0 + r) * C + c0 - 1] : E(0);
+  } else {
+    for (int q = threadIdx.x; q < TT * (TT + 1); q += xpose::TNT) {
+      const int r = q / (TT + 1), i = q % (TT + 1);
+      const int rr = r0 + r, c = c0 - 1 + i;
+      const bool in = rr < R && c >= 0 && c < C;
+      const size_t o = static_cast<size_t>(rr) * C + c;
+      tpn[r][i] = in ? pn[o] : E(0);
+      if (i > 0) tpv[r][i - 1] = in ? pv[o] : E(0);
+    }
   }
   __syncthreads();
+  // out[c][r] = P_V[r][c] (+ P_Vn[r][c] when slot c keeps its own successor weight)
+  // (+ P_Vn[r][c - 1] when slot c - 1 hands its weight on), summed in fp32 in that order.
+  auto value = [&](int r, int c) {
+    float v = to_f(tpv[r][c]);
+    if (fl[c + 1] == 0) v += to_f(tpn[r][c + 1]);
+    if (fl[c] == 1) v += to_f(tpn[r][c]);
+    return v;
+  };
   E* dst = out + static_cast<size_t>(b) * R * C;
-  for (int q = threadIdx.x; q < TT * TT; q += xpose::TNT) {
-    const int c = q / TT, r = q % TT;
-    if (r0 + r < R && c0 + c < C) st(dst, static_cast<size_t>(c0 + c) * R + r0 + r, tile[r][c]);
+  if (full) {
+    for (int q = threadIdx.x; q < TT * VPR; q += xpose::TNT) {
+      const int c = q / VPR, rv = (q % VPR) * VEC;
+      E e[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) e[k] = from_f<E>(value(rv + k, c));
+      *reinterpret_cast<u32x4*>(dst + static_cast<size_t>(c0 + c) * R + r0 + rv) =
+          *reinterpret_cast<const u32x4*>(e);
+    }
+  } else {
+    for (int q = threadIdx.x; q < TT * TT; q += xpose::TNT) {
+      const int c = q / TT, r = q % TT;
+      if (r0 + r < R && c0 + c < C) st(dst, static_cast<size_t>(c0 + c) * R + r0 + r, value(r, c));
+    }
   }
 }
 
@@ -913,8 +953,10 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
   if (fold) {
     const dim3 grid((unsigned)((N + xpose::TT - 1) / xpose::TT),
                     (unsigned)((T + xpose::TT - 1) / xpose::TT), (unsigned)B);
+    const bool aligned = ((reinterpret_cast<uintptr_t>(PV) | reinterpret_cast<uintptr_t>(PVn) |
+                           reinterpret_cast<uintptr_t>(PVT)) & 15u) == 0;
     hipLaunchKernelGGL(fold_transpose_kernel<E>, grid, dim3(xpose::TNT), 0, stream, (int)T,
-                       (int)N, PV, PVn, fold, PVT);
+                       (int)N, PV, PVn, fold, PVT, aligned);
     DABSN_HIP_CHECK(hipGetLastError());
   } else {
     DABSN_HIP_CHECK(xpose::transpose<E>(PV, PVT, (int)B, (int)T, (int)N, stream));

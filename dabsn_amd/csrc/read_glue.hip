@@ -269,22 +269,39 @@ __global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int ldg, int N, 
   const float nrm = norm_w[pos];
   const float n = fmaxf(nrm, kEps);
   float dot = 0.0f;
+  // The slot's K and gK rows are read once: the first RC vectors of each thread stay in
+  // registers from the dot product to the update (H <= 256 V RC, e.g. 4096 in bf16).
+  constexpr int RC = 2;
+  float kc[RC][V], gc[RC][V];
   if (in0 && nrm > kEps) {
     const size_t kb = (static_cast<size_t>(b) * N + r0) * H;
     float s = 0.0f;
-    for (int h = threadIdx.x * V; h < H; h += 256 * V) {
+    int i = 0;
+    for (int h = threadIdx.x * V; h < H; h += 256 * V, ++i) {
       float k[V], g[V];
       ldv<E, V>(K + kb + h, k);
       ldv<E, V>(gK + kb + h, g);
 #pragma unroll
       for (int e = 0; e < V; ++e) s += k[e] * g[e];
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        if (c == i) {
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            kc[c][e] = k[e];
+            gc[c][e] = g[e];
+          }
+        }
+      }
     }
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
     __syncthreads();
     dot = part[0] + part[1] + part[2] + part[3];
   }
-  for (int h = threadIdx.x * V; h < H; h += 256 * V) {
+  const bool cached = in0 && nrm > kEps;
+  int i = 0;
+  for (int h = threadIdx.x * V; h < H; h += 256 * V, ++i) {
     const size_t o = static_cast<size_t>(pos) * H + h;
     float acc[V];
     if (accumulate) {
@@ -296,9 +313,22 @@ __global__ void __launch_bounds__(256) gather_bwd_kernel(int T, int ldg, int N, 
     if (in0) {
       const size_t kb = (static_cast<size_t>(b) * N + r0) * H + h;
       float gk[V], gv[V], k[V];
-      ldv<E, V>(gK + kb, gk);
       ldv<E, V>(gV + kb, gv);
-      ldv<E, V>(K + kb, k);
+      if (cached && i < RC) {
+#pragma unroll
+        for (int c = 0; c < RC; ++c) {
+          if (c == i) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+              k[e] = kc[c][e];
+              gk[e] = gc[c][e];
+            }
+          }
+        }
+      } else {
+        ldv<E, V>(gK + kb, gk);
+        ldv<E, V>(K + kb, k);
+      }
 #pragma unroll
       for (int e = 0; e < V; ++e)
         acc[e] += gv[e] + (nrm > kEps ? (gk[e] - k[e] * dot) / n : gk[e] / n);
