@@ -48,7 +48,7 @@ def parse():
                    help="train: scan and read one after the other on the whole device")
     p.add_argument("--no-proj", action="store_true",
                    help="skip the separate timing of the input projections (profiling runs)")
-    p.add_argument("--cpu-trials", type=int, default=2,
+    p.add_argument("--cpu-trials", type=int, default=3,
                    help="timed CPU steps after one untimed warm-up step")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--workload", choices=("train", "decode", "primitives"), default="train",

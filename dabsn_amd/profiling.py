@@ -16,6 +16,7 @@ launch), so the same counters read on it give the scale between counter units an
     python -m dabsn_amd.profiling --pmc-summary <dir> [--match REGEX]
     python -m dabsn_amd.profiling --mfma-dispatches <dir>
     python -m dabsn_amd.profiling --copy-probe <MiB>
+    python -m dabsn_amd.profiling --gemm-shapes
     python -m dabsn_amd.profiling --pmc-json <out.json> --fetch <dir> --write <dir> \
         --copy-fetch <dir> --copy-write <dir> --copy-mib 512 --batch B --seq T --state H --chunk C
 
@@ -165,6 +166,38 @@ def copy_probe(mib: int, reps: int = 5) -> None:
           f"{n * 2} bytes read and {n * 2} bytes written per launch")
 
 
+def gemm_shapes(reps: int = 10) -> list[tuple[str, float, float]]:
+    """hipBLASLt (through torch.bmm) on the full shapes of the three-way read's GEMMs for the
+    last 1,024-query chunk of config 4 (16 batch rows, 4,096 bank slots, width 2,048, bf16
+    operands): (name, ms per launch, TFLOP/s), ``reps`` timed launches after one warm-up."""
+    import torch
+
+    B, T, N, H = 16, 1024, 4096, 2048
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(B, T, H, device="cuda", generator=g).bfloat16()
+    kt = torch.randn(B, H, N, device="cuda", generator=g).bfloat16()
+    p = torch.randn(B, T, N, device="cuda", generator=g).bfloat16()
+    v = torch.randn(B, N, H, device="cuda", generator=g).bfloat16()
+    cases = [("S = Q K^T, bf16 out", lambda: torch.bmm(q, kt)),
+             ("S = Q K^T, fp32 out", lambda: torch.bmm(q, kt, out_dtype=torch.float32)),
+             ("O = P V, bf16 out", lambda: torch.bmm(p, v)),
+             ("gK = G^T Q, left operand a transposed view", lambda: torch.bmm(p.transpose(1, 2), q))]
+    flops = 2.0 * B * T * N * H
+    out = []
+    for name, fn in cases:
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / reps
+        out.append((name, ms, flops / ms / 1e9))
+    return out
+
+
 # Core scan kernels by the names bench.py reports them under.
 _CORE_KERNELS = {"core_fwd_kernel": "core_scan_fwd", "core_bwd_kernel": "core_scan_bwd"}
 
@@ -221,6 +254,8 @@ def main() -> None:
     p.add_argument("--mfma-dispatches", default=None, metavar="DIR",
                    help="per-dispatch MFMA flops and utilisation of a counter run")
     p.add_argument("--copy-probe", type=int, default=None)
+    p.add_argument("--gemm-shapes", action="store_true",
+                   help="hipBLASLt on the read GEMM shapes of the last config-4 chunk")
     p.add_argument("--pmc-json", default=None)
     for k in ("fetch", "write", "copy-fetch", "copy-write"):
         p.add_argument(f"--{k}", default=None)
@@ -239,6 +274,9 @@ def main() -> None:
                   f"({k['dispatches']} dispatches)")
     elif args.copy_probe:
         copy_probe(args.copy_probe)
+    elif args.gemm_shapes:
+        for name, ms, tf in gemm_shapes():
+            print(f"{name:45s} {ms:.3f} ms {tf:.0f} TFLOP/s")
     elif args.mfma_dispatches:
         rows = mfma_dispatches(args.mfma_dispatches)
         print("| dispatch | output | grid | TFLOP | MFMA busy cycles | util | ms (profiled) | TFLOP/s |")
