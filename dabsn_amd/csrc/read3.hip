@@ -268,10 +268,16 @@ __global__ void __launch_bounds__(256) pack_kernel(int T, int N, int mode, const
 constexpr int RW_SOFTMAX = 2, RW_GRAD = 1;
 static_assert(TILE % RW_SOFTMAX == 0 && TILE % RW_GRAD == 0,
               "row groups must not straddle a query tile");
+// 64-column groups a row kernel loads together: every load of UC groups is issued (at
+// clamped, in-row addresses) before any of them is used, so a wave waits for one memory
+// round trip per UC groups instead of one per dependent load of every group. Each lane
+// still visits its columns in increasing order, so the sums are the same as one group at
+// a time.
+constexpr int UC = 4;
 
 // softmax_fwd_kernel for RW rows per wave: the row statistics and (PV non-null) P_V / P_Vn,
 // with the slot operands read once per RW rows from the pack.
-template <typename E, int RW>
+template <typename E, int RW, bool FOLD>
 __global__ void __launch_bounds__(NTH) softmax_fwd_rows_kernel(int B, RowCtx c, Gains g,
                                                                const float* scale_p,
                                                                const int32_t* rs,
@@ -298,19 +304,32 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_rows_kernel(int B, RowCtx c, 
   }
   const SlotPack* pb = pk + static_cast<size_t>(b) * c.N;
   const float* Sr = c.S + row0 * c.N;
-  for (int j = lane; j < nhi; j += 64) {
-    const SlotPack sp = pb[j];
+  for (int j0 = lane; j0 < nhi; j0 += 64 * UC) {
+    SlotPack spu[UC];
+    float sv[UC][RW];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      if (r >= nr) continue;
-      const int t = t0 + r;
-      const float ss = Sr[static_cast<size_t>(r) * c.N + j] * scale + sp.kbadm;
-      const float cc = ck[r][0] * sp.c0 + ck[r][1] * sp.c1 + ck[r][2] * sp.c2 + ck[r][3] * sp.c3;
-      if (sp.alim <= t) {
-        online_add(ss, ms[r], ls[r]);
-        online_add(ss + cc * cg, mp[r], lp[r]);
+    for (int u = 0; u < UC; ++u) {
+      const int j = min(j0 + 64 * u, nhi - 1);
+      spu[u] = pb[j];
+#pragma unroll
+      for (int r = 0; r < RW; ++r) sv[u][r] = Sr[static_cast<size_t>(min(r, nr - 1)) * c.N + j];
+    }
+#pragma unroll
+    for (int u = 0; u < UC; ++u) {
+      if (j0 + 64 * u >= nhi) continue;
+      const SlotPack& sp = spu[u];
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        if (r >= nr) continue;
+        const int t = t0 + r;
+        const float ss = sv[u][r] * scale + sp.kbadm;
+        const float cc = ck[r][0] * sp.c0 + ck[r][1] * sp.c1 + ck[r][2] * sp.c2 + ck[r][3] * sp.c3;
+        if (sp.alim <= t) {
+          online_add(ss, ms[r], ls[r]);
+          online_add(ss + cc * cg, mp[r], lp[r]);
+        }
+        if (sp.ilim < t) online_add(ss, mi[r], li[r]);
       }
-      if (sp.ilim < t) online_add(ss, mi[r], li[r]);
     }
   }
 #pragma unroll
@@ -332,36 +351,53 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_rows_kernel(int B, RowCtx c, 
     ii[r] = li[r] > 0.f ? 1.0f / li[r] : 0.f;
     carry[r] = 0.f;
   }
-  const int8_t* fb = fold ? fold + static_cast<size_t>(b) * c.N : nullptr;
+  const int8_t* fb = FOLD ? fold + static_cast<size_t>(b) * c.N : nullptr;
   // Folded: as softmax_fwd_kernel, per row (the induction weight of slot j moves to column
   // j + 1 through a lane shuffle, lane 63's to the next 64 columns through carry[r]).
-  for (int j0 = 0; j0 < nhi; j0 += 64) {
-    const int j = j0 + lane;
-    const bool in = j < nhi;
-    SlotPack sp = pb[in ? j : 0];
-    const int fj = (fb && in) ? fb[j] : 0;
+  for (int g0 = 0; g0 < nhi; g0 += 64 * UC) {
+    SlotPack spu[UC];
+    int fju[UC];
+    float sv[UC][RW];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      if (r >= nr) continue;
-      const int t = t0 + r;
-      float pv = 0.f, pn = 0.f;
-      if (in) {
-        const float ss = Sr[static_cast<size_t>(r) * c.N + j] * scale + sp.kbadm;
-        const float cc = ck[r][0] * sp.c0 + ck[r][1] * sp.c1 + ck[r][2] * sp.c2 + ck[r][3] * sp.c3;
-        if (sp.alim <= t)
-          pv = sg * (__expf(ss - ms[r]) * is[r]) + pg * (__expf(ss + cc * cg - mp[r]) * ip[r]);
-        if (sp.ilim < t) pn = ig * (__expf(ss - mi[r]) * ii[r]);
-      }
-      const size_t o = (row0 + r) * c.N + j;
-      if (fb) {
-        const float ahead = fj == 1 ? pn : 0.f;
-        float from_prev = __shfl_up(ahead, 1, 64);
-        if (lane == 0) from_prev = carry[r];
-        carry[r] = __shfl(ahead, 63, 64);
-        if (in) st(PV, o, (pv + (fj == 0 ? pn : 0.f)) + from_prev);
-      } else if (in) {
-        st(PV, o, pv);
-        st(PVn, o, pn);
+    for (int u = 0; u < UC; ++u) {
+      const int j = g0 + 64 * u + lane;
+      const int jc = j < nhi ? j : 0;
+      spu[u] = pb[jc];
+      fju[u] = FOLD ? fb[jc] : 0;
+#pragma unroll
+      for (int r = 0; r < RW; ++r) sv[u][r] = Sr[static_cast<size_t>(min(r, nr - 1)) * c.N + jc];
+    }
+#pragma unroll
+    for (int u = 0; u < UC; ++u) {
+      const int j0 = g0 + 64 * u;
+      if (j0 >= nhi) break;
+      const int j = j0 + lane;
+      const bool in = j < nhi;
+      const SlotPack& sp = spu[u];
+      const int fj = in ? fju[u] : 0;
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        if (r >= nr) continue;
+        const int t = t0 + r;
+        float pv = 0.f, pn = 0.f;
+        if (in) {
+          const float ss = sv[u][r] * scale + sp.kbadm;
+          const float cc = ck[r][0] * sp.c0 + ck[r][1] * sp.c1 + ck[r][2] * sp.c2 + ck[r][3] * sp.c3;
+          if (sp.alim <= t)
+            pv = sg * (__expf(ss - ms[r]) * is[r]) + pg * (__expf(ss + cc * cg - mp[r]) * ip[r]);
+          if (sp.ilim < t) pn = ig * (__expf(ss - mi[r]) * ii[r]);
+        }
+        const size_t o = (row0 + r) * c.N + j;
+        if constexpr (FOLD) {
+          const float ahead = fj == 1 ? pn : 0.f;
+          float from_prev = __shfl_up(ahead, 1, 64);
+          if (lane == 0) from_prev = carry[r];
+          carry[r] = __shfl(ahead, 63, 64);
+          if (in) st(PV, o, (pv + (fj == 0 ? pn : 0.f)) + from_prev);
+        } else if (in) {
+          st(PV, o, pv);
+          st(PVn, o, pn);
+        }
       }
     }
   }
@@ -370,7 +406,7 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_rows_kernel(int B, RowCtx c, 
 // Per-row reductions needed by the score gradient, rowA = (sum Ps dPV, sum Pp dPV,
 // sum Pi dPVn) unscaled by the gains, for RW rows per wave with the packed slot operands
 // (with a successor fold the induction term reads column j + fold[j] of dP_V).
-template <int RW>
+template <int RW, bool FOLD>
 __global__ void __launch_bounds__(NTH) grad_rows_grouped_kernel(int B, RowCtx c, Gains g,
                                                                 const float* scale_p,
                                                                 const int32_t* rs_rng,
@@ -403,24 +439,45 @@ __global__ void __launch_bounds__(NTH) grad_rows_grouped_kernel(int B, RowCtx c,
     for (int k = 0; k < 4; ++k) ck[r][k] = c.ck[(row0 + min(r, nr - 1)) * 4 + k];
   }
   const SlotPack* pb = pk + static_cast<size_t>(b) * c.N;
-  const int8_t* fb = fold ? fold + static_cast<size_t>(b) * c.N : nullptr;
-  for (int j = lane; j < nhi; j += 64) {
-    const SlotPack sp = pb[j];
-    const int dn = fb ? fb[j] : 0;
+  const int8_t* fb = FOLD ? fold + static_cast<size_t>(b) * c.N : nullptr;
+  for (int j0 = lane; j0 < nhi; j0 += 64 * UC) {
+    // The induction term reads dP_Vn[:, j], which with a successor fold is dP_V[:, j + 1]
+    // (fold code 1) or dP_V[:, j] (code 0): both candidates are loaded, the code selects.
+    SlotPack spu[UC];
+    int dn[UC];
+    float sv[UC][RW], dv[UC][RW], nv[UC][RW];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      if (r >= nr) continue;
-      const int t = t0 + r;
-      const size_t o = (row0 + r) * c.N + j;
-      const float ss = c.S[o] * scale + sp.kbadm;
-      if (sp.alim <= t) {
-        const float cc = ck[r][0] * sp.c0 + ck[r][1] * sp.c1 + ck[r][2] * sp.c2 + ck[r][3] * sp.c3;
-        const float d = dPV[o];
-        acc[r][0] += __expf(ss - m[r][0]) * inv[r][0] * d;
-        acc[r][1] += __expf(ss + cc * cg - m[r][1]) * inv[r][1] * d;
+    for (int u = 0; u < UC; ++u) {
+      const int j = min(j0 + 64 * u, nhi - 1);
+      const int jn = FOLD ? min(j + 1, c.N - 1) : j;
+      spu[u] = pb[j];
+      dn[u] = FOLD ? fb[j] : 0;
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        const size_t o = (row0 + min(r, nr - 1)) * c.N;
+        sv[u][r] = c.S[o + j];
+        dv[u][r] = dPV[o + j];
+        nv[u][r] = FOLD ? dPV[o + jn] : dPVn[o + j];
       }
-      if (sp.ilim < t)
-        acc[r][2] += __expf(ss - m[r][2]) * inv[r][2] * (fb ? dPV[o + dn] : dPVn[o]);
+    }
+#pragma unroll
+    for (int u = 0; u < UC; ++u) {
+      if (j0 + 64 * u >= nhi) continue;
+      const SlotPack& sp = spu[u];
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        if (r >= nr) continue;
+        const int t = t0 + r;
+        const float ss = sv[u][r] * scale + sp.kbadm;
+        if (sp.alim <= t) {
+          const float cc = ck[r][0] * sp.c0 + ck[r][1] * sp.c1 + ck[r][2] * sp.c2 + ck[r][3] * sp.c3;
+          const float d = dv[u][r];
+          acc[r][0] += __expf(ss - m[r][0]) * inv[r][0] * d;
+          acc[r][1] += __expf(ss + cc * cg - m[r][1]) * inv[r][1] * d;
+        }
+        if (sp.ilim < t)
+          acc[r][2] += __expf(ss - m[r][2]) * inv[r][2] * (FOLD && dn[u] == 0 ? dv[u][r] : nv[u][r]);
+      }
     }
   }
 #pragma unroll
@@ -852,8 +909,9 @@ static int forward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* q, 
     DABSN_HIP_CHECK(hipGetLastError());
   }
   const int64_t groups = B * ((T + RW_SOFTMAX - 1) / RW_SOFTMAX);
-  hipLaunchKernelGGL((softmax_fwd_rows_kernel<E, RW_SOFTMAX>),
-                     dim3((unsigned)((groups + NWV - 1) / NWV)),
+  auto softmax_rows = fold ? softmax_fwd_rows_kernel<E, RW_SOFTMAX, true>
+                          : softmax_fwd_rows_kernel<E, RW_SOFTMAX, false>;
+  hipLaunchKernelGGL(softmax_rows, dim3((unsigned)((groups + NWV - 1) / NWV)),
                      dim3(NTH), 0, stream, (int)B, c, g, scale, rs, pk, fold, stats,
                      write_p ? PV : static_cast<E*>(nullptr),
                      write_p && !fold ? PVn : static_cast<E*>(nullptr));
@@ -930,7 +988,9 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
     DABSN_HIP_CHECK(hipGetLastError());
   }
   const int64_t groups = B * ((T + RW_GRAD - 1) / RW_GRAD);
-  hipLaunchKernelGGL(grad_rows_grouped_kernel<RW_GRAD>, dim3((unsigned)((groups + NWV - 1) / NWV)),
+  auto grad_rows = fold ? grad_rows_grouped_kernel<RW_GRAD, true>
+                       : grad_rows_grouped_kernel<RW_GRAD, false>;
+  hipLaunchKernelGGL(grad_rows, dim3((unsigned)((groups + NWV - 1) / NWV)),
                      dim3(NTH), 0, stream, (int)B, c, g, scale, rs, pk, stats, fold, dPV, dPVn,
                      rowA);
   DABSN_HIP_CHECK(hipGetLastError());

@@ -115,11 +115,13 @@ def _parameters_as(module: torch.nn.Module, leaves: dict[str, Tensor]):
 class _SinkGather(torch.autograd.Function):
     """Bank gather over a prefix of a full-length write tape whose backward adds the bank
     rows' gradient into ``sink`` (the write tape's gradient buffer) over the bank's positions
-    only, instead of returning a full-length gradient. Returns (K, V, Vn or None)."""
+    only, instead of returning a full-length gradient. Returns (K, V, Vn or None).
+    ``wait[0]``, when an event at backward time, is waited for before the add (another
+    stream's earlier writes into the same rows)."""
 
     @staticmethod
     def forward(ctx, sink: Tensor, write: Tensor, norm_w: Tensor, idx: Tensor,
-                next_idx: Optional[Tensor], rank: Tensor):
+                next_idx: Optional[Tensor], rank: Tensor, wait: list):
         lib = _lib.load()
         B, T, H = write.shape
         N = idx.shape[1]
@@ -134,6 +136,7 @@ class _SinkGather(torch.autograd.Function):
                    "bank gather")
         ctx.save_for_backward(nw, rank, K)
         ctx.sink = sink
+        ctx.wait = wait
         ctx.shape = (B, T, H)
         ctx.set_materialize_grads(False)
         return K, V, Vn
@@ -148,12 +151,14 @@ class _SinkGather(torch.autograd.Function):
         gKc, gVc = z(gK), z(gV)
         gVnc = None if gVn is None else gVn.to(dt).contiguous()
         rk = rank.to(torch.int32).contiguous()
+        if ctx.wait[0] is not None:
+            torch.cuda.current_stream(K.device).wait_event(ctx.wait[0])
         lib = _lib.load()
         _lib.check(lib.dabsn_hip_bank_gather_bwd_prefix(
             ops._code(dt), B, int(rk.shape[1]), T, N, H, ops._p(nw), ops._p(rk), ops._p(K),
             ops._p(gKc), ops._p(gVc), ops._p(gVnc), 1, ops._p(ctx.sink), ops._stream(K)),
             "bank gather backward")
-        return None, None, None, None, None, None
+        return None, None, None, None, None, None, None
 
 
 def _stats_window(tapes: chunked._Tapes, stats: Tensor, t0: int, t1: int, stream) -> None:
@@ -210,6 +215,12 @@ class _PipelinedScanRead(torch.autograd.Function):
         ops.core_launch_check(code, B, min(T, chunk), H, False)
         # Buffers that outlive the call come from the caller's stream, before any work.
         GA = torch.cat((Ug, A), dim=0).to(dt).contiguous()
+        # Transposed copies the backward takes as they are: [Ug; A]^T for the reverse scans
+        # and the output projection's weight as [3H, H] for its input-gradient product (the
+        # layout hipBLASLt runs fastest), filled on the read half before its first chunk.
+        W_out = read.short_read.out.weight
+        GAT = torch.empty((H, 2 * H), device=dev, dtype=dt)
+        WdT = torch.empty((W_out.shape[1], W_out.shape[0]), device=dev, dtype=dt)
         params, keep = ops._core_params(vecs, scal)
         Wx_c, Wgx_c, ldx = ops.scan_inputs(Wx, Wgx, dt)
         out = chunked._Tapes(Wx_c, B, T, H)
@@ -265,23 +276,33 @@ class _PipelinedScanRead(torch.autograd.Function):
                 Wd = read.short_read.out.weight.detach().to(dt)
                 bd = read.short_read.out.bias.detach().to(dt)
 
+                sink_wait: list = [None]
+
                 def gather(bank_write, norm_w, idx, next_idx, rank, fold):
                     return _SinkGather.apply(sink, bank_write, norm_w, idx,
-                                             None if fold is not None else next_idx, rank)
+                                             None if fold is not None else next_idx, rank,
+                                             sink_wait)
 
                 def read_chunk(k: int, leaves):
                     # Statistics of window k, the three-way read of query chunk k against the
                     # bank [0, t1) (its own autograd graph) and, without autograd, its output
                     # projection (differentiated by hand in the backward): the [y, budget] block
-                    # with the bias first (enqueued ahead of the read's host sync on the bank
-                    # width), then the retrieved block added.
+                    # with the bias (enqueued while the read's host read of the bank width is
+                    # in flight, so the device has it to run while the host waits), then the
+                    # retrieved block added.
                     t0, t1 = bounds[k]
                     C = t1 - t0
                     st = torch.cuda.current_stream(dev)
                     _stats_window(out, stats, t0, t1, st.cuda_stream)
-                    pre = F.linear(ops.window_copy(U[:, t0:t1]).view(B * C, 2 * H), Wd[:, :2 * H], bd)
+                    pre = []
+
+                    def project_y_budget():
+                        with torch.no_grad():
+                            pre.append(F.linear(ops.window_copy(U[:, t0:t1]).view(B * C, 2 * H),
+                                                Wd[:, :2 * H], bd))
+
                     w_leaf, stats_leaf, _ = leaves
-                    with torch.enable_grad():
+                    with torch.enable_grad(), read.during_width_read(project_y_budget):
                         # A contiguous copy of the expression window as the leaf (the read's
                         # normalisation reads it densely).
                         ay_leaf = ops.window_copy(ay[:, t0:t1]).requires_grad_(True)
@@ -291,7 +312,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                             gather=gather)
                     rd = r.detach().to(dt)
                     ops.window_add(retr[:, t0:t1], rd)
-                    sh = torch.addmm(pre, rd.reshape(B * C, H), Wd[:, 2 * H:].t())
+                    sh = torch.addmm(pre[0], rd.reshape(B * C, H), Wd[:, 2 * H:].t())
                     ops.window_add(short[:, t0:t1], sh.view(B, C, H))
                     return r, ay_leaf
 
@@ -316,6 +337,8 @@ class _PipelinedScanRead(torch.autograd.Function):
                 chunks = []
                 with _parameters_as(read, sets[0][2]):
                     with torch.cuda.stream(R):
+                        GAT.copy_(GA.t())
+                        WdT.copy_(W_out.detach().t())
                         for k in range(K - 1):
                             R.wait_event(scan_done[k])
                             chunks.append(read_chunk(k, sets[0]))
@@ -349,7 +372,8 @@ class _PipelinedScanRead(torch.autograd.Function):
         ctx.read, ctx.chunk, ctx.names = read, chunk, names
         ctx.bounds = bounds
         ctx.meta = [(x.dtype, tuple(x.shape)) for x in (Wx, Wgx, *core_in)]
-        ctx.graph = (chunks, longs, sets, sink, long_out)
+        ctx.graph = (chunks, longs, sets, sink, sink_wait, long_out)
+        ctx.transposed = (GAT, WdT)
         ctx.out_dtype = read_out.dtype
         ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, starts, retr, out.U, *out.tapes)
         ctx.set_materialize_grads(False)
@@ -367,7 +391,8 @@ class _PipelinedScanRead(torch.autograd.Function):
         vecs, scal = saved[4:20], saved[20:23]
         starts, retr = saved[23], saved[24]
         fwd_out = chunked._Tapes(None, 0, 0, 0, existing=saved[25:33])
-        chunks, longs, sets, sink, long_out = ctx.graph
+        chunks, longs, sets, sink, sink_wait, long_out = ctx.graph
+        GAT, WdT = ctx.transposed
         # Leaves of the read-half chunks, and of the last chunk (whole-device stream): the
         # hand-differentiated parameters' gradients go to the first set, and the second
         # set's gradients are added to it at the end.
@@ -382,14 +407,11 @@ class _PipelinedScanRead(torch.autograd.Function):
         bounds = ctx.bounds
         K = len(bounds)
         ops.core_launch_check(code, B, min(T, ctx.chunk), H, True)
-        GA = torch.cat((Ug, A), dim=0).to(dt).contiguous()
-        GAT = GA.t().contiguous()
         params, keep = ops._core_params(vecs, scal)
         pleaves = list(param_leaves.values())
         trainable = [[p for p in s[2].values() if p.requires_grad] for s in sets]
         W = param_leaves["short_read.out.weight"]
         bias = param_leaves["short_read.out.bias"]
-        Wd = W.detach().to(dt)
         # Tape gradients of the reverse scans, full length, filled window by window.
         gU = torch.empty((B, T, 2 * H), device=dev, dtype=dt)
         g_halves = [None if g is None else g.to(dt) for g in (g_y, g_budget)]
@@ -419,7 +441,7 @@ class _PipelinedScanRead(torch.autograd.Function):
             # gradients fill U's gradient window, the retrieved rows' gradient is returned.
             t0, t1 = bounds[k]
             C = t1 - t0
-            prod = torch.mm(ops.window_copy(g_short3[:, t0:t1]).view(B * C, H), Wd)
+            prod = F.linear(ops.window_copy(g_short3[:, t0:t1]).view(B * C, H), WdT)
             for i, g_in in enumerate(g_halves):
                 g_proj = prod[:, i * H:(i + 1) * H].view(B, C, H)
                 dst = gU[:, t0:t1, i * H:(i + 1) * H]
@@ -468,6 +490,15 @@ class _PipelinedScanRead(torch.autograd.Function):
             logit_sum[0] = part if logit_sum[0] is None else logit_sum[0] + part
             state_grad[:] = g[6:9]
 
+        def long_shares(k: int) -> None:
+            # Window k's long-channel gradients join the write-gradient sink (the gather
+            # backward of every query chunk >= k adds into those rows too) and the
+            # plasticity gradient (which the statistics backward then adds to).
+            t0, t1 = bounds[k]
+            gwk, gpk = long_grads[k]
+            ops.window_add(sink[:, t0:t1], sink[:, t0:t1], gwk)
+            ops.window_add(g_p[:, t0:t1], gpk)
+
         try:
             with torch.cuda.stream(M):
                 # The read output's backward over the last window; then the long channel's last
@@ -482,6 +513,13 @@ class _PipelinedScanRead(torch.autograd.Function):
                 R.wait_event(head)
                 with torch.cuda.stream(R):
                     long_backward(K - 1)
+                    # Its shares of the last window's write and plasticity gradients, ahead of
+                    # the last chunk's gather backward (which waits for them) and statistics
+                    # backward, off the path to the last reverse scan.
+                    long_shares(K - 1)
+                    last_shares = torch.cuda.Event()
+                    last_shares.record(R)
+                sink_wait[0] = last_shares
 
                 carry = [None, None, None]
                 bws = []
@@ -510,11 +548,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                     with torch.cuda.stream(R):
                         if k < K - 1:
                             long_backward(k)
-                        # Window k of the write gradient is complete (only query chunks >= k
-                        # read it): the long channel's share joins it.
-                        gwk, gpk = long_grads[k]
-                        ops.window_add(sink[:, t0:t1], sink[:, t0:t1], gwk)
-                        ops.window_add(g_p[:, t0:t1], gpk)
+                            long_shares(k)
                         if k == K - 1:
                             # Later chunks of the read half add theirs to the last chunk's.
                             stats_leaf.grad = stats_last.grad

@@ -12,6 +12,7 @@ gather, the three-way read and the fused long-memory scan. The [B,T]-sized glue
 
 from __future__ import annotations
 
+import contextlib
 import os
 
 import torch
@@ -181,6 +182,39 @@ class DABSNRead(nn.Module):
         self.logit_retention_strength = _parameter(1.4)
         # Optional static bank width (read.py:224-231): a capture-safe, sync-free width.
         self._capture_bank_width: int | None = None
+        # Work to enqueue while the host waits for the bank width (during_width_read).
+        self._width_wait_work = None
+
+    @contextlib.contextmanager
+    def during_width_read(self, work):
+        """Run ``work()`` (device work on the current stream, enqueued by the host) while the
+        next read's host read of the bank width is in flight: the read copies the width into
+        pinned memory, calls ``work``, and only then waits, so the device has ``work`` to run
+        while the host waits and then enqueues the read's remaining kernels. If no such read
+        happens inside the block (a fixed width, or no GPU), ``work`` runs at its end."""
+        self._width_wait_work = work
+        try:
+            yield
+        except BaseException:
+            self._width_wait_work = None
+            raise
+        pending, self._width_wait_work = self._width_wait_work, None
+        if pending is not None:
+            pending()
+
+    def _host_values(self, values: Tensor) -> list:
+        """``values.tolist()`` for a small device tensor, running the pending
+        ``during_width_read`` work between the copy and the wait."""
+        work, self._width_wait_work = self._width_wait_work, None
+        if work is None:
+            return values.tolist()
+        host = torch.empty(values.shape, dtype=values.dtype, pin_memory=True)
+        host.copy_(values, non_blocking=True)
+        copied = torch.cuda.Event()
+        copied.record(torch.cuda.current_stream(values.device))
+        work()
+        copied.synchronize()
+        return host.tolist()
 
     # ---- selection ------------------------------------------------------------
     def _select(self, admission: Tensor, length: int, width: int | None = None,
@@ -208,7 +242,7 @@ class DABSNRead(nn.Module):
                 # kernel error word.
                 width = ops.bank_width(order, counts, want_fold)
                 word = ops.pending_error_word(order.device)
-                vals = (width if word is None else torch.cat((width, word))).tolist()
+                vals = self._host_values(width if word is None else torch.cat((width, word)))
                 top, bad = vals[:2]
                 if len(vals) > 2:
                     ops.raise_error_word(int(vals[2]), order.device)

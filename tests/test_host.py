@@ -224,3 +224,19 @@ def test_error_word_modes(monkeypatch):
     for mode in ("sync", "deferred"):
         monkeypatch.setenv("DABSN_HIP_ERROR_CHECK", mode)
         assert ops._sync_mode() == mode and ops._sync_mode(input_check=True) == mode
+
+
+def test_width_read_work_runs_once_at_the_latest_at_the_block_end():
+    """DABSNRead.during_width_read: without a device read of the bank width inside the
+    block, the work runs once at its end; when the block raises, it does not run."""
+    from dabsn_amd import DABSNRead
+
+    read = DABSNRead(8)
+    calls = []
+    with read.during_width_read(lambda: calls.append("work")):
+        calls.append("body")
+    assert calls == ["body", "work"] and read._width_wait_work is None
+    with pytest.raises(RuntimeError):
+        with read.during_width_read(lambda: calls.append("not run")):
+            raise RuntimeError("inside the block")
+    assert calls == ["body", "work"] and read._width_wait_work is None

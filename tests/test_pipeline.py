@@ -254,3 +254,20 @@ def test_pipeline_needs_the_scan_to_fit_one_half(cuda_device):
         assert falls and "half" in falls[0].fields["reason"]
     finally:
         events.remove_event_listener(listen)
+
+
+def test_width_read_work_runs_inside_the_read(cuda_device):
+    """DABSNRead.during_width_read on the device: the work runs once, inside the read's host
+    read of the bank width (before the read returns), and the read's output is the same."""
+    core, read = _modules(5, 8, 64, 0.7, cuda_device)
+    x = torch.randn(2, 48, 8, generator=torch.Generator().manual_seed(5)).to(cuda_device)
+    with torch.no_grad():
+        Wx, Wgx = core.projections(x)
+        _, _, ref = _sequential(core, read, 16, Wx, Wgx)
+        order = []
+        side = torch.zeros(4, device=cuda_device)
+        with read.during_width_read(lambda: (order.append("work"), side.add_(1.0))):
+            _, _, out = _sequential(core, read, 16, Wx, Wgx)
+            order.append("read returned")
+    assert order == ["work", "read returned"]
+    assert torch.equal(out, ref) and torch.equal(side.cpu(), torch.ones(4))
