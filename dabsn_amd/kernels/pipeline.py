@@ -312,7 +312,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                             gather=gather)
                     rd = r.detach().to(dt)
                     ops.window_add(retr[:, t0:t1], rd)
-                    sh = torch.addmm(pre[0], rd.reshape(B * C, H), Wd[:, 2 * H:].t())
+                    sh = pre[0].addmm_(rd.reshape(B * C, H), Wd[:, 2 * H:].t())
                     ops.window_add(short[:, t0:t1], sh.view(B, C, H))
                     return r, ay_leaf
 
@@ -435,13 +435,11 @@ class _PipelinedScanRead(torch.autograd.Function):
         for st in (M, S, R):
             st.wait_stream(ambient)
 
-        def projection_grads(g_short3: Tensor, k: int) -> Tensor:
-            # out(cat[y, budget, retrieved]) over query chunk k: one product gives the
-            # gradients of all three inputs; y's and budget's plus their own upstream
-            # gradients fill U's gradient window, the retrieved rows' gradient is returned.
+        def fill_gU(prod: Tensor, k: int) -> None:
+            # y's and budget's projection gradients (columns [0, 2H) of prod) plus their own
+            # upstream gradients fill U's gradient window k.
             t0, t1 = bounds[k]
             C = t1 - t0
-            prod = F.linear(ops.window_copy(g_short3[:, t0:t1]).view(B * C, H), WdT)
             for i, g_in in enumerate(g_halves):
                 g_proj = prod[:, i * H:(i + 1) * H].view(B, C, H)
                 dst = gU[:, t0:t1, i * H:(i + 1) * H]
@@ -451,7 +449,27 @@ class _PipelinedScanRead(torch.autograd.Function):
                     ops.window_add(dst, g_in[:, t0:t1], g_proj)
                 else:
                     torch.add(g_in[:, t0:t1], g_proj, out=dst)
-            return ops.window_copy(prod[:, 2 * H:].view(B, C, H))
+
+        def projection_grads(g_short3: Tensor, k: int, u_stream=None) -> Tensor:
+            # out(cat[y, budget, retrieved]) over query chunk k: one product gives the
+            # gradients of all three inputs; the retrieved rows' gradient is returned. With
+            # u_stream, the retrieved third is its own product, after which the read's
+            # backward can start, and the [y, budget] part runs on u_stream.
+            t0, t1 = bounds[k]
+            C = t1 - t0
+            gs = ops.window_copy(g_short3[:, t0:t1]).view(B * C, H)
+            if u_stream is None:
+                prod = F.linear(gs, WdT)
+                fill_gU(prod, k)
+                return ops.window_copy(prod[:, 2 * H:].view(B, C, H))
+            g_r = F.linear(gs, WdT[2 * H:]).view(B, C, H)
+            ready = torch.cuda.Event()
+            ready.record(torch.cuda.current_stream(dev))
+            u_stream.wait_event(ready)
+            gs.record_stream(u_stream)
+            with torch.cuda.stream(u_stream):
+                fill_gU(F.linear(gs, WdT[:2 * H]), k)
+            return g_r
 
         def core_weight_grads(k: int) -> None:
             # dL/d[Ug; A] over window k: the reverse scan's [dWgx, da_y] rows times the
@@ -532,7 +550,9 @@ class _PipelinedScanRead(torch.autograd.Function):
                     side = 1 if k == K - 1 else 0
                     with torch.cuda.stream(st):
                         read_out_backward(k)
-                        g_r = projection_grads(g_short3, k)
+                        # The last chunk's [y, budget] product on the scan half, idle until
+                        # that chunk's reverse scan, which the scan stream's order puts after it.
+                        g_r = projection_grads(g_short3, k, S if k == K - 1 else None)
                         # The write leaf is listed so that the engine runs the gather's backward,
                         # whose gradient goes to the sink (it returns none for the leaf itself).
                         torch.autograd.backward([r], [g_r], inputs=[ay_leaf, sets[side][0],
