@@ -313,6 +313,14 @@ CoreScanOutputs = tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, 
                         Tensor, Tensor]
 
 
+def _separate(v: Tensor, n: int) -> list[Tensor]:
+    """The n elements of a 1-D fp32 tensor as n separate scalar tensors (operator outputs
+    must not alias each other), copied in one fused launch instead of n."""
+    outs = [torch.empty((), device=v.device, dtype=v.dtype) for _ in range(n)]
+    torch._foreach_copy_(outs, list(v.unbind(0)))
+    return outs
+
+
 def _core_params(vecs: Sequence[Tensor], scal: Sequence[Tensor]):
     """The kernel's parameter table (fp32 copies of the 16 vectors and 3 scalars and the
     ctypes struct pointing at them), one cache entry for all 19 parameters."""
@@ -1158,15 +1166,14 @@ def _long_scan_fused_fake(write, plasticity, l1, l2, l3, l4, long0, expected0, r
     return torch.empty_like(write), f(B, H), f(B, H), f(B, H), f(B, long_segments(T), 3, H)
 
 
-@torch.library.custom_op(_q("_long_scan_fused_backward"), mutates_args=(),
-                         device_types="cuda")
-def long_scan_fused_backward(
+def long_scan_backward_parts(
     write: Tensor, plasticity: Tensor, logits: list[Tensor], checkpoint: Tensor,
     grad_long: Tensor, g_long_final: Optional[Tensor], g_expected_final: Optional[Tensor],
     g_retention_final: Optional[Tensor],
-) -> list[Tensor]:
-    """Reverse of long_scan_fused from its checkpoint: [g_write, g_plasticity, 4 logit
-    grads, gL0, gE0, gR0]."""
+) -> tuple[Tensor, Tensor, Tensor, list[Tensor]]:
+    """long_scan_fused_backward's results as (g_write, g_plasticity in the write dtype, the
+    four logit gradients as one [4] fp32 tensor, [gL0, gE0, gR0]), for callers that need
+    no separate tensor per logit."""
     _require_cuda(write)
     lib = _lib.load()
     B, T, H = write.shape
@@ -1194,8 +1201,22 @@ def long_scan_fused_backward(
                                       *[_p(x) for x in gf], _p(gw), _p(gp), *[_p(x) for x in g0],
                                       _p(part), _p(ws), nbytes, _stream(w)), "long scan backward")
     KernelTimer.end(tk)
-    glog = part.sum(0)
-    return [gw, gp.to(plasticity.dtype), *[glog[i].clone() for i in range(4)], *g0]
+    return gw, gp, part.sum(0), g0
+
+
+@torch.library.custom_op(_q("_long_scan_fused_backward"), mutates_args=(),
+                         device_types="cuda")
+def long_scan_fused_backward(
+    write: Tensor, plasticity: Tensor, logits: list[Tensor], checkpoint: Tensor,
+    grad_long: Tensor, g_long_final: Optional[Tensor], g_expected_final: Optional[Tensor],
+    g_retention_final: Optional[Tensor],
+) -> list[Tensor]:
+    """Reverse of long_scan_fused from its checkpoint: [g_write, g_plasticity, 4 logit
+    grads, gL0, gE0, gR0]."""
+    gw, gp, glog, g0 = long_scan_backward_parts(write, plasticity, logits, checkpoint,
+                                                grad_long, g_long_final, g_expected_final,
+                                                g_retention_final)
+    return [gw, gp.to(plasticity.dtype), *_separate(glog, 4), *g0]
 
 
 @long_scan_fused_backward.register_fake
@@ -1778,11 +1799,8 @@ def admitted_three_way_read_compact_flash_backward(
     return (gq, gK.to(bank_keys.dtype), gV.to(bank_writes.dtype), gVn.to(next_writes.dtype),
             gck.to(cocktail.dtype), gcb.to(bank_cocktail.dtype), gkb.to(bank_key_bias.dtype),
             gadm.to(bank_admission.dtype),
-            g5[0].clone().reshape_as(scale).to(scale.dtype),
-            g5[1].clone().reshape_as(short_gain).to(short_gain.dtype),
-            g5[2].clone().reshape_as(pad_gain).to(pad_gain.dtype),
-            g5[3].clone().reshape_as(induct_gain).to(induct_gain.dtype),
-            g5[4].clone().reshape_as(cocktail_gain).to(cocktail_gain.dtype))
+            *(g.reshape_as(x).to(x.dtype) for g, x in zip(
+                _separate(g5, 5), (scale, short_gain, pad_gain, induct_gain, cocktail_gain))))
 
 
 @admitted_three_way_read_compact_flash_backward.register_fake
@@ -2091,11 +2109,8 @@ def read3_bwd_kept(
             gVn if next_writes is None else gVn.to(next_writes.dtype),
             gck.to(cocktail.dtype), gcb.to(bank_cocktail.dtype), gkb.to(bank_key_bias.dtype),
             gadm.to(bank_admission.dtype),
-            g5[0].clone().reshape_as(scale).to(scale.dtype),
-            g5[1].clone().reshape_as(short_gain).to(short_gain.dtype),
-            g5[2].clone().reshape_as(pad_gain).to(pad_gain.dtype),
-            g5[3].clone().reshape_as(induct_gain).to(induct_gain.dtype),
-            g5[4].clone().reshape_as(cocktail_gain).to(cocktail_gain.dtype))
+            *(g.reshape_as(x).to(x.dtype) for g, x in zip(
+                _separate(g5, 5), (scale, short_gain, pad_gain, induct_gain, cocktail_gain))))
 
 
 @read3_bwd_kept.register_fake

@@ -501,12 +501,11 @@ class _PipelinedScanRead(torch.autograd.Function):
             # starts from for window k - 1.
             wk, pk, ckpt = longs[k]
             t0, t1 = bounds[k]
-            g = ops.long_scan_fused_backward(wk, pk, logit_leaves, ckpt,
-                                             ops.window_copy(g_long[:, t0:t1]), *state_grad)
-            long_grads[k] = (g[0], g[1])
-            part = torch.stack(g[2:6])
+            gw, gp, part, g0 = ops.long_scan_backward_parts(
+                wk, pk, logit_leaves, ckpt, ops.window_copy(g_long[:, t0:t1]), *state_grad)
+            long_grads[k] = (gw, gp)
             logit_sum[0] = part if logit_sum[0] is None else logit_sum[0] + part
-            state_grad[:] = g[6:9]
+            state_grad[:] = g0
 
         def long_shares(k: int) -> None:
             # Window k's long-channel gradients join the write-gradient sink (the gather
