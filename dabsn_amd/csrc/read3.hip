@@ -143,6 +143,24 @@ __device__ __forceinline__ void online_add(float x, float& m, float& l) {
   }
 }
 
+// Online (max, sum) update of one softmax with UC scores at once (-inf for masked ones):
+// one rescale to the group's new maximum, then the group's terms, so a lane evaluates
+// UC + 1 exponentials per group (and no branch that diverges whenever some lane's maximum
+// grows).
+template <int U>
+__device__ __forceinline__ void online_add_group(const float (&x)[U], float& m, float& l) {
+  float g = x[0];
+#pragma unroll
+  for (int u = 1; u < U; ++u) g = fmaxf(g, x[u]);
+  const float mn = fmaxf(m, g);
+  if (mn == -INFINITY) return;  // every score so far masked: l stays 0
+  float acc = l * __expf(m - mn);  // m = -inf: l = 0 and exp(-inf) = 0
+#pragma unroll
+  for (int u = 0; u < U; ++u) acc += __expf(x[u] - mn);
+  l = acc;
+  m = mn;
+}
+
 // Combine the per-lane (max, sum) of one softmax across the wave.
 __device__ __forceinline__ void wave_softmax_stats(float& m, float& l) {
   const float M = wave_max(m);
@@ -315,21 +333,24 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_rows_kernel(int B, RowCtx c, 
       for (int r = 0; r < RW; ++r) sv[u][r] = Sr[static_cast<size_t>(min(r, nr - 1)) * c.N + j];
     }
 #pragma unroll
-    for (int u = 0; u < UC; ++u) {
-      if (j0 + 64 * u >= nhi) continue;
-      const SlotPack& sp = spu[u];
+    for (int r = 0; r < RW; ++r) {
+      if (r >= nr) continue;
+      const int t = t0 + r;
+      float xs[UC], xp[UC], xi[UC];
 #pragma unroll
-      for (int r = 0; r < RW; ++r) {
-        if (r >= nr) continue;
-        const int t = t0 + r;
+      for (int u = 0; u < UC; ++u) {
+        const SlotPack& sp = spu[u];
+        const bool in = j0 + 64 * u < nhi;
         const float ss = sv[u][r] * scale + sp.kbadm;
         const float cc = ck[r][0] * sp.c0 + ck[r][1] * sp.c1 + ck[r][2] * sp.c2 + ck[r][3] * sp.c3;
-        if (sp.alim <= t) {
-          online_add(ss, ms[r], ls[r]);
-          online_add(ss + cc * cg, mp[r], lp[r]);
-        }
-        if (sp.ilim < t) online_add(ss, mi[r], li[r]);
+        const bool al = in && sp.alim <= t, il = in && sp.ilim < t;
+        xs[u] = al ? ss : -INFINITY;
+        xp[u] = al ? ss + cc * cg : -INFINITY;
+        xi[u] = il ? ss : -INFINITY;
       }
+      online_add_group(xs, ms[r], ls[r]);
+      online_add_group(xp, mp[r], lp[r]);
+      online_add_group(xi, mi[r], li[r]);
     }
   }
 #pragma unroll
@@ -490,13 +511,28 @@ __global__ void __launch_bounds__(NTH) grad_rows_grouped_kernel(int B, RowCtx c,
   }
 }
 
+// Four consecutive values of E stored with one 8-byte (bf16) or 16-byte (fp32) store.
+template <typename E>
+__device__ __forceinline__ void st4(E* p, float a, float b, float c, float d);
+template <>
+__device__ __forceinline__ void st4<bf16>(bf16* p, float a, float b, float c, float d) {
+  const uint32_t lo = static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+  const uint32_t hi = static_cast<uint32_t>(f2bf(c)) | (static_cast<uint32_t>(f2bf(d)) << 16);
+  *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+}
+template <>
+__device__ __forceinline__ void st4<float>(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+}
+
 // Score gradient for a tile of RT rows x CC columns. Writes Gs = scale*G, P_V, P_Vn;
 // per-(row, column chunk, wave) partials rowB = (G.S, dSp.cc, cg dSp cb[0..3]) and
 // per-(row tile, column) partials colp = (sum G, cg sum dSp ck[0..3]).
-// Each thread owns CJ columns: their per-slot operands (key bias + admission, bank
-// cocktail, index, validity) are loaded once, and the next row's S / dP_V / dP_Vn are
-// requested before the current row is evaluated, so a wave always has a row of loads in
-// flight.
+// Each thread owns CJ = 4 consecutive columns: their per-slot operands (key bias +
+// admission, bank cocktail, index, validity) are loaded once; a row's S / dP_V / dP_Vn
+// come as 16-byte loads and its Gs / P_V / P_Vn go out as one vector store each when the
+// rows are 16-byte aligned (N % 4 == 0); and the next row's loads are issued before the
+// current row is evaluated, so a wave always has a row of loads in flight.
 template <typename E>
 __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const float* scale_p,
                                                         const int32_t* rs_rng, const float* stats,
@@ -504,6 +540,7 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
                                                         const float* dPV, const float* dPVn, E* Gs,
                                                         E* PV, E* PVn, float* rowB, float* colp) {
   constexpr int CJ = CC / NTH;
+  static_assert(CJ == 4, "a thread owns one 4-column group");
   const int b = blockIdx.z, rt = blockIdx.y, cch = blockIdx.x;
   const int NCC = (c.N + CC - 1) / CC;
   const int RTILES = (c.T + RT - 1) / RT;
@@ -512,6 +549,10 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
   const int QT = (c.T + TILE - 1) / TILE;
   const int t0 = rt * RT, t1 = min(c.T, t0 + RT);
   const int wave = threadIdx.x >> 6;
+  const int jb = cch * CC + threadIdx.x * CJ;  // this thread's first column
+  // 16-byte rows: the workspace bases are 256-byte aligned, so N % 4 == 0 suffices; the
+  // write limits (multiples of 128, or N) then never split a thread's group.
+  const bool vec = (c.N & 3) == 0;
   auto jlim_of = [&](int t) {
     const int nhi = rs_rng[(static_cast<size_t>(b) * QT + t / TILE) * 3 + 2];
     // The transposed GEMMs read whole 128-wide slot tiles of any row inside their
@@ -529,7 +570,7 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
     }
 #pragma unroll
     for (int q = 0; q < CJ; ++q) {
-      const int j = cch * CC + q * NTH + threadIdx.x;
+      const int j = jb + q;
       if (j >= c.N) continue;
       float* o = colp + ((static_cast<size_t>(b) * RTILES + rt) * c.N + j) * 5;
       o[0] = o[1] = o[2] = o[3] = o[4] = 0.f;
@@ -561,7 +602,7 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
   int slot[CJ], dnoff[CJ];
 #pragma unroll
   for (int q = 0; q < CJ; ++q) {
-    const int j = cch * CC + q * NTH + threadIdx.x;
+    const int j = jb + q;
     const bool ok = j < c.N && vb[min(j, c.N - 1)] != 0;
     const size_t bj = static_cast<size_t>(b) * c.N + min(j, c.N - 1);
     kbadm[q] = c.kb[bj] + c.adm[bj];
@@ -581,9 +622,29 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
   auto fetch = [&](int t) {
     njl = rlim[t - t0][1];
     const size_t rowoff = (static_cast<size_t>(b) * c.T + t) * c.N;
+    if (vec && jb < njl) {
+      // the whole group is inside the row's write limit (a multiple of 4)
+      const float4 s4 = *reinterpret_cast<const float4*>(c.S + rowoff + jb);
+      const float4 d4 = *reinterpret_cast<const float4*>(dPV + rowoff + jb);
+      nS[0] = s4.x; nS[1] = s4.y; nS[2] = s4.z; nS[3] = s4.w;
+      nD[0] = d4.x; nD[1] = d4.y; nD[2] = d4.z; nD[3] = d4.w;
+      if (fold) {
+        // column j + 1 of the last column: the next group's first (a code of 1 implies
+        // that column exists)
+        const float d5 = jb + CJ < c.N ? dPV[rowoff + jb + CJ] : 0.f;
+        nDn[0] = dnoff[0] ? d4.y : d4.x;
+        nDn[1] = dnoff[1] ? d4.z : d4.y;
+        nDn[2] = dnoff[2] ? d4.w : d4.z;
+        nDn[3] = dnoff[3] ? d5 : d4.w;
+      } else {
+        const float4 n4 = *reinterpret_cast<const float4*>(dPVn + rowoff + jb);
+        nDn[0] = n4.x; nDn[1] = n4.y; nDn[2] = n4.z; nDn[3] = n4.w;
+      }
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < CJ; ++q) {
-      const int j = cch * CC + q * NTH + threadIdx.x;
+      const int j = jb + q;
       const bool in = j < njl;
       nS[q] = in ? c.S[rowoff + j] : 0.f;
       nD[q] = in ? dPV[rowoff + j] : 0.f;
@@ -610,11 +671,10 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
     const float ra = sr[6], rp = sr[7], ri = sr[8];
     const float ck0 = sr[9], ck1 = sr[10], ck2 = sr[11], ck3 = sr[12];
     float gsc = 0.f, gcg = 0.f, gk0 = 0.f, gk1 = 0.f, gk2 = 0.f, gk3 = 0.f;
+    float oG[CJ], oV[CJ], oN[CJ];
 #pragma unroll
     for (int q = 0; q < CJ; ++q) {
-      const int j = cch * CC + q * NTH + threadIdx.x;
-      if (j >= jlim) continue;
-      const size_t o = row * c.N + j;
+      const int j = jb + q;
       float ps = 0.f, pp = 0.f, pi = 0.f, G = 0.f, dsp = 0.f;
       if (j < nhi) {
         const float cc = ck0 * cbv[q][0] + ck1 * cbv[q][1] + ck2 * cbv[q][2] + ck3 * cbv[q][3];
@@ -640,9 +700,24 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
         colC[q][0] += w * ck0; colC[q][1] += w * ck1;
         colC[q][2] += w * ck2; colC[q][3] += w * ck3;
       }
-      st(Gs, o, G * c.scale);
-      st(PV, o, c.sg * ps + c.pg * pp);
-      st(PVn, o, c.ig * pi);
+      oG[q] = G * c.scale;
+      oV[q] = c.sg * ps + c.pg * pp;
+      oN[q] = c.ig * pi;
+    }
+    if (vec && jb < jlim) {
+      const size_t o = row * c.N + jb;
+      st4(Gs + o, oG[0], oG[1], oG[2], oG[3]);
+      st4(PV + o, oV[0], oV[1], oV[2], oV[3]);
+      st4(PVn + o, oN[0], oN[1], oN[2], oN[3]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < CJ; ++q) {
+        if (jb + q >= jlim) continue;
+        const size_t o = row * c.N + jb + q;
+        st(Gs, o, oG[q]);
+        st(PV, o, oV[q]);
+        st(PVn, o, oN[q]);
+      }
     }
     gsc = wave_sum(gsc);
     gcg = wave_sum(gcg);
@@ -657,7 +732,7 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
   }
 #pragma unroll
   for (int q = 0; q < CJ; ++q) {
-    const int j = cch * CC + q * NTH + threadIdx.x;
+    const int j = jb + q;
     if (j >= c.N) continue;
     float* o = colp + ((static_cast<size_t>(b) * RTILES + rt) * c.N + j) * 5;
     o[0] = colG[q];
