@@ -435,25 +435,28 @@ def _to_payload(memory: DABSNMemory) -> dict[str, object]:
 def _from_payload(payload) -> DABSNMemory:
     if not isinstance(payload, Mapping) or payload.get("format") != FORMAT:
         fmt = payload.get("format") if isinstance(payload, Mapping) else type(payload).__name__
-        raise ValueError(f"not a DABSN memory payload: format={fmt!r}, expected {FORMAT!r}")
+        raise ValueError(f"not a DABSN memory payload: its format tag is {fmt!r}, this "
+                         f"loader reads {FORMAT!r}")
     raw_layers = payload.get("layers")
     if not isinstance(raw_layers, Sequence):
-        raise ValueError("memory payload layers must be a sequence")
+        raise ValueError("DABSN memory payload: 'layers' holds no list of layer entries")
     layers = []
     for entry in raw_layers:
         bank = entry.get("bank") if isinstance(entry, Mapping) else None
         if not isinstance(bank, Mapping):
-            raise ValueError("memory payload layer bank must be an object")
+            raise ValueError("DABSN memory payload: a layer entry has no 'bank' mapping")
         missing = [k for k in BANK_FIELDS if k not in bank]
         if missing:
-            raise ValueError(f"memory payload is missing bank fields: {missing}")
+            raise ValueError(f"DABSN memory payload: a layer's bank lacks {missing}")
         core, long = entry.get("core"), entry.get("long")
         if not (isinstance(core, Sequence) and len(core) == 3 and isinstance(long, Sequence)
                 and len(long) == 3):
-            raise ValueError("memory payload core and long states must hold three tensors each")
+            raise ValueError("DABSN memory payload: a layer's 'core' and 'long' entries are "
+                             "not three state tensors each")
         write = bank["write"]
         if not isinstance(write, Tensor) or write.dim() != 3:
-            raise ValueError("memory payload bank write must be a [B, N, H] tensor")
+            raise ValueError("DABSN memory payload: a layer's bank 'write' is not a 3-D "
+                             "[B, N, H] tensor")
         stats = bank.get("stats")
         if not isinstance(stats, Tensor):
             # A file written by the reference: the means are stored, the write norms are not.

@@ -390,3 +390,37 @@ def test_config5_decode_vs_dense_and_oracle(cuda_device):
     err_oracle = rel_err(dec[rows].cpu(), want)
     assert err_oracle <= 2e-2, f"decode vs CPU oracle: {err_oracle:.3e}"
     print(f"config5 decode: vs dense {err_dense:.2e}, vs oracle {err_oracle:.2e}")
+
+
+def test_config5_decode_after_long_prompt_vs_oracle(cuda_device):
+    """Config-5 widths (H=2048) decoding 32 tokens after a 1,024-token prompt, so each read
+    runs against a bank of about a thousand rows: every decode step's logits against the CPU
+    oracle's full forward over the same tokens (drift over many steps would show as a
+    growing per-step error)."""
+    B, H, L, prompt, steps = 2, 2048, 2, 1024, 32
+    torch.manual_seed(1)
+    model = dabsn_amd.DABSNSequenceLM(32000, H, L, layers=[(H, H)] * L, residual=True,
+                                      mlp_ratio=4.0)
+    g = torch.Generator().manual_seed(9)
+    with torch.no_grad():
+        for blk in model.blocks:
+            blk.mlp_fc2.weight.normal_(0.0, 0.02, generator=g)
+    model = model.to(torch.bfloat16).eval()
+    ids = torch.randint(0, 32000, (B, prompt + steps), generator=g)
+    gpu = copy.deepcopy(model).to(cuda_device)
+    idg = ids.to(cuda_device)
+    with torch.no_grad():
+        memory = mem.ingest(gpu, idg[:, :prompt], chunk_size=256)
+        memory.reserve(prompt + steps)
+        dec = []
+        for t in range(prompt, prompt + steps):
+            logits, memory = mem.forward_with_memory(gpu, idg[:, t:t + 1], memory, extend=True)
+            dec.append(logits.float())
+        dec = torch.cat(dec, dim=1).cpu()
+        want = model(ids)[:, prompt:].float()
+    assert memory.position == prompt + steps
+    per_step = [rel_err(dec[:, i], want[:, i]) for i in range(steps)]
+    worst = max(per_step)
+    assert worst <= 2e-2, f"decode step {per_step.index(worst)} vs CPU oracle: {worst:.3e}"
+    print(f"config5 long-prompt decode vs oracle: first step {per_step[0]:.2e}, "
+          f"last {per_step[-1]:.2e}, worst {worst:.2e}")
