@@ -788,12 +788,14 @@ __global__ void reduce_rows_kernel(int64_t rows, int NCC, const float* rowA, con
   }
 }
 
-__global__ void reduce_final_kernel(int nblocks, const float* part, float* out5) {
-  const int k = threadIdx.x;
-  if (k >= 5) return;
+// One wave per scalar (5 waves): lane l sums the partials of blocks l, l + 64, ... in
+// order, then the wave's lanes are combined in a fixed tree order.
+__global__ void __launch_bounds__(320) reduce_final_kernel(int nblocks, const float* part, float* out5) {
+  const int k = threadIdx.x >> 6, lane = threadIdx.x & 63;
   float s = 0.f;
-  for (int i = 0; i < nblocks; ++i) s += part[static_cast<size_t>(i) * 5 + k];
-  out5[k] = s;
+  for (int i = lane; i < nblocks; i += 64) s += part[static_cast<size_t>(i) * 5 + k];
+  s = wave_sum(s);
+  if (lane == 0) out5[k] = s;
 }
 
 // Successor fold. The read module's banks hold V[j] = write[idx[j]] and Vn[j] =
@@ -1133,7 +1135,7 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
   hipLaunchKernelGGL(reduce_rows_kernel, dim3(nblk), dim3(NTH), 0, stream, rows, NCC, rowA, rowB,
                      gck, part);
   DABSN_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(reduce_final_kernel, dim3(1), dim3(64), 0, stream, nblk, part, gscal5);
+  hipLaunchKernelGGL(reduce_final_kernel, dim3(1), dim3(320), 0, stream, nblk, part, gscal5);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }

@@ -537,15 +537,28 @@ __global__ void __launch_bounds__(256) read_out_bwd_kernel(uint32_t chunks, uint
 }
 
 // One workgroup: strided partial sums per thread, then the wave/LDS tree; fixed order.
-__global__ void __launch_bounds__(256) read_out_reduce_kernel(uint32_t n, const float* partial,
-                                                              float* out) {
-  __shared__ float sh[4];
+// One workgroup of 1024 threads: thread i sums partials i, i + 1024, ... in order (four
+// loads in flight), then the waves' sums are combined in a fixed tree order.
+__global__ void __launch_bounds__(1024) read_out_reduce_kernel(uint32_t n, const float* partial,
+                                                               float* out) {
+  __shared__ float sh[16];
   float acc = 0.0f;
-  for (uint32_t k = threadIdx.x; k < n; k += 256u) acc += partial[k];
+  uint32_t k = threadIdx.x;
+  for (; k + 3u * 1024u < n; k += 4u * 1024u) {
+    const float a = partial[k], b = partial[k + 1024u], c = partial[k + 2048u],
+                d = partial[k + 3072u];
+    acc = acc + a + b + c + d;
+  }
+  for (; k < n; k += 1024u) acc += partial[k];
   acc = wave_sum(acc);
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
   __syncthreads();
-  if (threadIdx.x == 0) out[0] = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  if (threadIdx.x == 0) {
+    float s8[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) s8[w] = sh[2 * w] + sh[2 * w + 1];
+    out[0] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+  }
 }
 
 // Runs LAUNCH(E, V) for the dtype code, with V = 8 when `vec` holds and V = 1 otherwise.
@@ -696,12 +709,15 @@ __global__ void __launch_bounds__(256) glue_slots_bwd_kernel(
   }
 }
 
-__global__ void glue_params_reduce_kernel(int nblocks, const float* partial, float* gparams) {
-  const int k = threadIdx.x;
-  if (k >= 8) return;
+// One wave per parameter (8 waves): lane l sums the partials of blocks l, l + 64, ... in
+// order, then the wave's lanes are combined in a fixed tree order.
+__global__ void __launch_bounds__(512) glue_params_reduce_kernel(int nblocks, const float* partial,
+                                                                 float* gparams) {
+  const int k = threadIdx.x >> 6, lane = threadIdx.x & 63;
   float acc = 0.0f;
-  for (int i = 0; i < nblocks; ++i) acc += partial[static_cast<size_t>(i) * 8 + k];
-  gparams[k] = acc;
+  for (int i = lane; i < nblocks; i += 64) acc += partial[static_cast<size_t>(i) * 8 + k];
+  acc = wave_sum(acc);
+  if (lane == 0) gparams[k] = acc;
 }
 
 // Backward of the query cocktails (means_glue rows with only the cocktail output): rows
@@ -1079,7 +1095,7 @@ static int read_output_bwd_rows(const char* what, int out_dtype, int proj_dtype,
   READ_OUT_TYPES(what, out_dtype, proj_dtype, long_dtype, vec, L);
 #undef L
   DABSN_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(read_out_reduce_kernel, dim3(1), dim3(256), 0, stream, nblk, partials, ggain);
+  hipLaunchKernelGGL(read_out_reduce_kernel, dim3(1), dim3(1024), 0, stream, nblk, partials, ggain);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
@@ -1208,7 +1224,7 @@ int dabsn_hip_glue_slots_bwd(int64_t B, int64_t N, int64_t L, int64_t ld, const 
                      ld, stats, idx, static_cast<float>(hidden), prm, mode, gkey_bias, gadmission,
                      gcocktail, gstats, ldg, partial);
   DABSN_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(glue_params_reduce_kernel, dim3(1), dim3(64), 0, stream, (int)nblk, partial,
+  hipLaunchKernelGGL(glue_params_reduce_kernel, dim3(1), dim3(512), 0, stream, (int)nblk, partial,
                      gparams);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
