@@ -281,9 +281,8 @@ __global__ void __launch_bounds__(256) pack_kernel(int T, int N, int mode, const
 
 // Query rows per wave of the grouped row kernels: RW consecutive rows of one batch row share
 // the slot loads and the slot limit of their 128-row tile (RW divides TILE). Measured at
-// config 4: the softmax is fastest with 2 rows per wave, the gradient row sums with 1
-// (their three loads per element already keep a wave busy).
-constexpr int RW_SOFTMAX = 2, RW_GRAD = 1;
+// config 4 with the grouped loads below: 2 rows per wave for both (4 slowed the softmax).
+constexpr int RW_SOFTMAX = 2, RW_GRAD = 2;
 static_assert(TILE % RW_SOFTMAX == 0 && TILE % RW_GRAD == 0,
               "row groups must not straddle a query tile");
 // 64-column groups a row kernel loads together: every load of UC groups is issued (at
