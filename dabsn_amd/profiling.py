@@ -241,6 +241,86 @@ def pmc_json(out: str, fetch_dir: str, write_dir: str, copy_fetch_dir: str, copy
     return doc
 
 
+def _dispatch_counters(directory: str) -> dict[int, dict[str, object]]:
+    """Dispatch id -> (kernel, queue, counter value) of a single-counter rocprofv3 CSV run."""
+    import csv
+    from pathlib import Path
+
+    out: dict[int, dict[str, object]] = {}
+    for path in sorted(Path(directory).rglob("*counter_collection.csv")):
+        with open(path, newline="") as fh:
+            for r in csv.DictReader(fh):
+                out[int(r["Dispatch_Id"])] = {"kernel": r["Kernel_Name"], "queue": int(r["Queue_Id"]),
+                                              "value": float(r["Counter_Value"])}
+    return out
+
+
+def _short(name: str) -> str:
+    return re.sub(r"^dabsn::", "", re.sub(r"\(.*", "", name).replace("void ", ""))
+
+
+def step_traffic(fetch_dir: str, write_dir: str, copy_fetch_dir: str, copy_write_dir: str,
+                 copy_mib: int, trace_db: str, match: str) -> str:
+    """Markdown tables of the HBM traffic of the last traced step: FETCH_SIZE and
+    WRITE_SIZE per dispatch (copy-calibrated) from two counter runs of the bench, durations
+    from a kernel-trace run of the same bench (dispatches of the step paired with trace
+    records by kernel name and order). The step starts at its first forward-scan
+    dispatch (4 per step); the whole-device stream is the queue of the step's last
+    statistics kernel."""
+    import sqlite3
+
+    nbytes = copy_mib * 1024 * 1024
+    ff = nbytes / (_one(pmc_summary(copy_fetch_dir), "FETCH_SIZE", "neg")["mean"] * 1024.0)
+    wf = nbytes / (_one(pmc_summary(copy_write_dir), "WRITE_SIZE", "neg")["mean"] * 1024.0)
+    fe, wr = _dispatch_counters(fetch_dir), _dispatch_counters(write_dir)
+    ids = sorted(fe)
+    fwd = [i for i in ids if "core_fwd_kernel" in str(fe[i]["kernel"])]
+    step = [i for i in ids if i >= fwd[-4]]
+    rx = re.compile(match)
+    con = sqlite3.connect(trace_db)
+    rows = [r for r in con.execute("select name, start, end from kernels order by start")
+            if rx.search(r[0])]
+    tf = [k for k, r in enumerate(rows) if "core_fwd_kernel" in r[0]]
+    durations: dict[str, list[float]] = defaultdict(list)
+    for name, start, end in rows[tf[-4]:]:
+        durations[_short(name)].append((end - start) / 1e3)
+    seen: dict[str, int] = defaultdict(int)
+    recs = []
+    for i in step:
+        n = _short(str(fe[i]["kernel"]))
+        k = seen[n]
+        seen[n] += 1
+        d = durations[n][k] if k < len(durations[n]) else float("nan")
+        f = float(fe[i]["value"]) * 1024.0 * ff
+        w = float(wr[i]["value"]) * 1024.0 * wf if i in wr else float("nan")
+        recs.append((i, n, int(fe[i]["queue"]), f, w, d))
+    whole = [q for _, n, q, *_ in recs if n.startswith("glue::stats_kernel")][-1]
+    lines = [f"calibration: fetch factor {ff:.5f}, write factor {wf:.5f}", "",
+             "| # | kernel | FETCH MB | WRITE MB | traffic MB | us | GB/s | frac of 8 TB/s |",
+             "|---|---|---|---|---|---|---|---|"]
+    for i, n, q, f, w, d in recs:
+        if q != whole:
+            continue
+        t = (f + w) / 1e6
+        lines.append(f"| {i} | `{n[:70]}` | {f / 1e6:.1f} | {w / 1e6:.1f} | {t:.1f} | {d:.0f} | "
+                     f"{t / d * 1e3:.0f} | {t / d * 1e3 / 8000:.3f} |")
+    lines += ["", "| kernel | launches | FETCH MB | WRITE MB | us | GB/s |",
+              "|---|---|---|---|---|---|"]
+    agg: dict[str, list[float]] = defaultdict(lambda: [0, 0.0, 0.0, 0.0])
+    for _, n, q, f, w, d in recs:
+        if q == whole or "core_" in n:
+            continue
+        a = agg[n]
+        a[0] += 1
+        a[1] += f
+        a[2] += w
+        a[3] += d
+    for n, (c, f, w, d) in sorted(agg.items(), key=lambda kv: -kv[1][3]):
+        lines.append(f"| `{n[:70]}` | {int(c)} | {f / 1e6:.0f} | {w / 1e6:.0f} | {d:.0f} | "
+                     f"{(f + w) / 1e6 / d * 1e3:.0f} |")
+    return "\n".join(lines)
+
+
 def main() -> None:
     p = argparse.ArgumentParser()
     p.add_argument("db", nargs="?")
@@ -257,6 +337,9 @@ def main() -> None:
     p.add_argument("--gemm-shapes", action="store_true",
                    help="hipBLASLt on the read GEMM shapes of the last config-4 chunk")
     p.add_argument("--pmc-json", default=None)
+    p.add_argument("--step-traffic", default=None, metavar="TRACE_DB",
+                   help="per-dispatch HBM traffic of the last traced step (with --fetch, --write, "
+                        "--copy-fetch, --copy-write, --match)")
     for k in ("fetch", "write", "copy-fetch", "copy-write"):
         p.add_argument(f"--{k}", default=None)
     p.add_argument("--copy-mib", type=int, default=512)
@@ -264,7 +347,11 @@ def main() -> None:
         p.add_argument(f"--{k}", type=int, default=d)
     p.add_argument("--dtype", default="bf16")
     args = p.parse_args()
-    if args.pmc_json:
+    if args.step_traffic:
+        print(step_traffic(args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_mib,
+                           args.step_traffic,
+                           args.match or "read3|glue|longmem|xpose|gemm_kernel|read_out|core_"))
+    elif args.pmc_json:
         doc = pmc_json(args.pmc_json, args.fetch, args.write, args.copy_fetch, args.copy_write,
                        args.copy_mib, {"batch": args.batch, "seq_len": args.seq,
                                        "state": args.state, "chunk_t": args.chunk,
