@@ -293,7 +293,9 @@ static_assert(TILE % RW_SOFTMAX == 0 && TILE % RW_GRAD == 0,
 constexpr int UC = 4;
 
 // softmax_fwd_kernel for RW rows per wave: the row statistics and (PV non-null) P_V / P_Vn,
-// with the slot operands read once per RW rows from the pack.
+// with the slot operands read once per RW rows from the pack. P_V and P_Vn are written up
+// to the row's write limit jlim = min(N, roundup(nhi, TILE)), zeros in [nhi, jlim): the
+// backward's transposed GEMMs read whole 128-slot tiles of the P_V this call leaves.
 template <typename E, int RW, bool FOLD>
 __global__ void __launch_bounds__(NTH) softmax_fwd_rows_kernel(int B, RowCtx c, Gains g,
                                                                const float* scale_p,
@@ -372,9 +374,10 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_rows_kernel(int B, RowCtx c, 
     carry[r] = 0.f;
   }
   const int8_t* fb = FOLD ? fold + static_cast<size_t>(b) * c.N : nullptr;
+  const int jlim = min(c.N, ((nhi + TILE - 1) / TILE) * TILE);
   // Folded: as softmax_fwd_kernel, per row (the induction weight of slot j moves to column
   // j + 1 through a lane shuffle, lane 63's to the next 64 columns through carry[r]).
-  for (int g0 = 0; g0 < nhi; g0 += 64 * UC) {
+  for (int g0 = 0; g0 < jlim; g0 += 64 * UC) {
     SlotPack spu[UC];
     int fju[UC];
     float sv[UC][RW];
@@ -390,9 +393,9 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_rows_kernel(int B, RowCtx c, 
 #pragma unroll
     for (int u = 0; u < UC; ++u) {
       const int j0 = g0 + 64 * u;
-      if (j0 >= nhi) break;
+      if (j0 >= jlim) break;
       const int j = j0 + lane;
-      const bool in = j < nhi;
+      const bool in = j < nhi, out = j < jlim;
       const SlotPack& sp = spu[u];
       const int fj = in ? fju[u] : 0;
 #pragma unroll
@@ -413,8 +416,8 @@ __global__ void __launch_bounds__(NTH) softmax_fwd_rows_kernel(int B, RowCtx c, 
           float from_prev = __shfl_up(ahead, 1, 64);
           if (lane == 0) from_prev = carry[r];
           carry[r] = __shfl(ahead, 63, 64);
-          if (in) st(PV, o, (pv + (fj == 0 ? pn : 0.f)) + from_prev);
-        } else if (in) {
+          if (out) st(PV, o, (pv + (fj == 0 ? pn : 0.f)) + from_prev);
+        } else if (out) {
           st(PV, o, pv);
           st(PVn, o, pn);
         }
@@ -524,7 +527,8 @@ __device__ __forceinline__ void st4<float>(float* p, float a, float b, float c, 
   *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
 }
 
-// Score gradient for a tile of RT rows x CC columns. Writes Gs = scale*G, P_V, P_Vn;
+// Score gradient for a tile of RT rows x CC columns. Writes Gs = scale*G, and P_V / P_Vn
+// where those pointers are non-null;
 // per-(row, column chunk, wave) partials rowB = (G.S, dSp.cc, cg dSp cb[0..3]) and
 // per-(row tile, column) partials colp = (sum G, cg sum dSp ck[0..3]).
 // Each thread owns CJ = 4 consecutive columns: their per-slot operands (key bias +
@@ -706,16 +710,16 @@ __global__ void __launch_bounds__(NTH) grad_tile_kernel(RowCtx c, Gains g, const
     if (vec && jb < jlim) {
       const size_t o = row * c.N + jb;
       st4(Gs + o, oG[0], oG[1], oG[2], oG[3]);
-      st4(PV + o, oV[0], oV[1], oV[2], oV[3]);
-      st4(PVn + o, oN[0], oN[1], oN[2], oN[3]);
+      if (PV) st4(PV + o, oV[0], oV[1], oV[2], oV[3]);
+      if (PVn) st4(PVn + o, oN[0], oN[1], oN[2], oN[3]);
     } else {
 #pragma unroll
       for (int q = 0; q < CJ; ++q) {
         if (jb + q >= jlim) continue;
         const size_t o = row * c.N + jb + q;
         st(Gs, o, oG[q]);
-        st(PV, o, oV[q]);
-        st(PVn, o, oN[q]);
+        if (PV) st(PV, o, oV[q]);
+        if (PVn) st(PVn, o, oN[q]);
       }
     }
     gsc = wave_sum(gsc);
@@ -889,6 +893,7 @@ __global__ void __launch_bounds__(xpose::TNT) fold_transpose_kernel(int R, int C
 struct Plan {
   size_t off_S, off_rs, off_ro, off_rb, off_stats, off_PV, off_PVn, off_VT, off_VnT, off_pack,
       end_fwd;
+  size_t split;  // end of the kept part: scores, tile ranges, row statistics and P_V
   size_t off_dPV, off_dPVn, off_Gs, off_rowA, off_rowB, off_colp, off_part, off_KT, off_QT,
       off_gOT, off_GsT, off_PVT, off_PVnT, end_bwd;
 };
@@ -907,6 +912,7 @@ static Plan plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
   p.off_rb = o; o = align_up(o + B * BT * 3 * 4);
   p.off_stats = o; o = align_up(o + static_cast<size_t>(B) * T * 6 * 4);
   p.off_PV = o; o = align_up(o + TN * e);
+  p.split = o;
   p.off_PVn = o; o = align_up(o + TN * e);
   const size_t NH = static_cast<size_t>(B) * N * H, TH = static_cast<size_t>(B) * T * H;
   p.off_VT = o; o = align_up(o + NH * e);
@@ -931,10 +937,10 @@ static Plan plan(int dtype, int64_t B, int64_t T, int64_t N, int64_t H) {
   return p;
 }
 
-// A workspace in two parts. `kept` holds the plan's regions below off_PV -- the scores,
-// the tile ranges and the row statistics, which a forward leaves for a later backward and
-// which that backward only reads; `scratch` holds every region from off_PV on. A single
-// buffer is the case scratch = kept + off_PV.
+// A workspace in two parts. `kept` holds the plan's regions below `split` -- the scores,
+// the tile ranges, the row statistics and P_V (folded when the read folds), which a
+// forward leaves for a later backward and which that backward only reads; `scratch` holds
+// every region from `split` on. A single buffer is the case scratch = kept + split.
 struct Ws {
   uint8_t* kept;
   uint8_t* scratch;
@@ -947,7 +953,7 @@ struct Ws {
 
 static Ws single_ws(void* ws, const Plan& p) {
   uint8_t* b = static_cast<uint8_t*>(ws);
-  return Ws{b, b + p.off_PV, p.off_PV};
+  return Ws{b, b + p.split, p.split};
 }
 
 template <typename E>
@@ -1023,7 +1029,9 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
                          float* gck, float* gcb, float* gkb, float* gadm, float* gscal5,
                          const Ws& ws, const Plan& p, bool recompute, hipStream_t stream) {
   // The tile ranges, S and the row statistics: recomputed here, or left in the workspace
-  // by the forward call on the same inputs (which also wrote P_V / P_Vn, rebuilt below).
+  // by the forward call on the same inputs, which also left P_V there (folded when the read
+  // folds, zeros up to each row's write limit). Recomputed, P_V and P_Vn are rebuilt below
+  // by grad_tile_kernel; kept, only the unfolded read's P_Vn is.
   if (recompute) {
     const int rc = forward_impl<E>(B, T, N, H, q, K, V, Vn, ck, cb, kb, adm, scale, idx, valid,
                                    fold, mode, g, nullptr, ws, p, false, stream);
@@ -1073,7 +1081,9 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
   const int NCC = static_cast<int>((N + CC - 1) / CC), RTILES = static_cast<int>((T + RT - 1) / RT);
   if (N > 0) {
     hipLaunchKernelGGL(grad_tile_kernel<E>, dim3(NCC, RTILES, (unsigned)B), dim3(NTH), 0, stream, c,
-                       g, scale, rs, stats, rowA, fold, dPV, dPVn, Gs, PV, PVn, rowB, colp);
+                       g, scale, rs, stats, rowA, fold, dPV, dPVn, Gs,
+                       recompute ? PV : static_cast<E*>(nullptr),
+                       recompute || !fold ? PVn : static_cast<E*>(nullptr), rowB, colp);
     DABSN_HIP_CHECK(hipGetLastError());
   }
   E* KT = ws.at<E>(p.off_KT);
@@ -1086,7 +1096,7 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
   DABSN_HIP_CHECK(xpose::transpose<E>(q, QTr, (int)B, (int)T, (int)H, stream));
   DABSN_HIP_CHECK(xpose::transpose<E>(gout, gOT, (int)B, (int)T, (int)H, stream));
   DABSN_HIP_CHECK(xpose::transpose<E>(Gs, GsT, (int)B, (int)T, (int)N, stream));
-  if (fold) {
+  if (fold && recompute) {
     const dim3 grid((unsigned)((N + xpose::TT - 1) / xpose::TT),
                     (unsigned)((T + xpose::TT - 1) / xpose::TT), (unsigned)B);
     const bool aligned = ((reinterpret_cast<uintptr_t>(PV) | reinterpret_cast<uintptr_t>(PVn) |
@@ -1096,7 +1106,7 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
     DABSN_HIP_CHECK(hipGetLastError());
   } else {
     DABSN_HIP_CHECK(xpose::transpose<E>(PV, PVT, (int)B, (int)T, (int)N, stream));
-    DABSN_HIP_CHECK(xpose::transpose<E>(PVn, PVnT, (int)B, (int)T, (int)N, stream));
+    if (!fold) DABSN_HIP_CHECK(xpose::transpose<E>(PVn, PVnT, (int)B, (int)T, (int)N, stream));
   }
   {
     gemm::Args<E, E> a{};  // gQ = Gs K, B operand as K^T [H][N]
@@ -1109,8 +1119,8 @@ static int backward_impl(int64_t B, int64_t T, int64_t N, int64_t H, const E* go
     DABSN_HIP_CHECK((gemm::launch<E, E>(a, (int)B, stream)));
   }
   // Entries of G, P_V, P_Vn the GEMMs read (rows t >= the bank tile's earliest query,
-  // whole 128-slot tiles below roundup(nhi)) are all written by grad_tile_kernel; the
-  // transposes copy them unchanged.
+  // whole 128-slot tiles below roundup(nhi)) are all written, by grad_tile_kernel or the
+  // forward's softmax_fwd_rows_kernel; the transposes copy them unchanged.
   const E* lhs[3] = {GsT, PVT, PVnT};
   const E* rhs[3] = {QTr, gOT, gOT};
   E* dst[3] = {gK, gV, gVn};
@@ -1899,9 +1909,9 @@ size_t dabsn_hip_read3_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t 
   switch (part) {
     case 0: return p.end_fwd;
     case 1: return p.end_bwd;
-    case 2: return p.off_PV;
-    case 3: return p.end_fwd - p.off_PV;
-    case 4: return p.end_bwd - p.off_PV;
+    case 2: return p.split;
+    case 3: return p.end_fwd - p.split;
+    case 4: return p.end_bwd - p.split;
     default: return 0;
   }
 }
@@ -1927,10 +1937,10 @@ static int read3_fwd_entry(int dtype, int64_t B, int64_t T, int64_t N, int64_t H
     DABSN_REQUIRE(kept_bytes >= p.end_fwd, "read3: workspace %zu < %zu", kept_bytes, p.end_fwd);
     w = single_ws(kept, p);
   } else {
-    DABSN_REQUIRE(kept_bytes >= p.off_PV && scratch_bytes >= p.end_fwd - p.off_PV,
-                  "read3: kept %zu < %zu or scratch %zu < %zu", kept_bytes, p.off_PV,
-                  scratch_bytes, p.end_fwd - p.off_PV);
-    w = Ws{static_cast<uint8_t*>(kept), static_cast<uint8_t*>(scratch), p.off_PV};
+    DABSN_REQUIRE(kept_bytes >= p.split && scratch_bytes >= p.end_fwd - p.split,
+                  "read3: kept %zu < %zu or scratch %zu < %zu", kept_bytes, p.split,
+                  scratch_bytes, p.end_fwd - p.split);
+    w = Ws{static_cast<uint8_t*>(kept), static_cast<uint8_t*>(scratch), p.split};
   }
   Gains g{{gains[0], gains[1], gains[2], gains[3]}};
   if (dtype == kBF16)
@@ -2003,10 +2013,10 @@ static int read3_bwd_entry(bool recompute, int dtype, int64_t B, int64_t T, int6
                   p.end_bwd);
     w = single_ws(kept, p);
   } else {
-    DABSN_REQUIRE(kept_bytes >= p.off_PV && scratch_bytes >= p.end_bwd - p.off_PV,
-                  "read3 backward: kept %zu < %zu or scratch %zu < %zu", kept_bytes, p.off_PV,
-                  scratch_bytes, p.end_bwd - p.off_PV);
-    w = Ws{static_cast<uint8_t*>(kept), static_cast<uint8_t*>(scratch), p.off_PV};
+    DABSN_REQUIRE(kept_bytes >= p.split && scratch_bytes >= p.end_bwd - p.split,
+                  "read3 backward: kept %zu < %zu or scratch %zu < %zu", kept_bytes, p.split,
+                  scratch_bytes, p.end_bwd - p.split);
+    w = Ws{static_cast<uint8_t*>(kept), static_cast<uint8_t*>(scratch), p.split};
   }
   Gains g{{gains[0], gains[1], gains[2], gains[3]}};
   if (dtype == kBF16)

@@ -409,7 +409,7 @@ int dabsn_hip_relu_square(int dtype, int64_t n, const void* x, void* out, hipStr
  *
  * Workspace sizes by `part`: 0 = one buffer for dabsn_hip_read3_fwd, 1 = one buffer for
  * dabsn_hip_read3_bwd (which recomputes the forward), 2 = the kept part (scores, tile
- * ranges, row statistics) that dabsn_hip_read3_fwd_keep fills for
+ * ranges, row statistics, the read weights P_V) that dabsn_hip_read3_fwd_keep fills for
  * dabsn_hip_read3_bwd_after_fwd, 3 = the forward scratch beside it, 4 = the backward
  * scratch beside it. */
 size_t dabsn_hip_read3_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
@@ -433,8 +433,9 @@ int dabsn_hip_read3_bwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H, c
                         size_t workspace_bytes, hipStream_t stream);
 /* The forward for a caller that will run the backward on the same inputs: as
  * dabsn_hip_read3_fwd, with the workspace in two buffers. `kept` (part 2 bytes) receives
- * the scores, tile ranges and row statistics; `scratch` (part 3 bytes) is free once the
- * call's work has completed.
+ * the scores, tile ranges, row statistics and the read weights P_V [B,T,N] (the folded
+ * weights with `fold`); `scratch` (part 3 bytes) is free once the call's work has
+ * completed.
  * `fold` (optional, int8 [B,N]; the successor fold): fold[b][j] in {0, 1} states that the
  * successor row of every valid slot is a bank row, Vn[j] = V[j + fold[j]] (1: slot j + 1
  * holds the next position; 0: the clamped last position, Vn[j] = V[j]). The induction
@@ -451,8 +452,9 @@ int dabsn_hip_read3_fwd_keep(int dtype, int64_t B, int64_t T, int64_t N, int64_t
 /* The backward without recomputing the forward's scores and row statistics: `kept` is the
  * buffer a dabsn_hip_read3_fwd_keep call on the same inputs filled; it is only read, so
  * the backward can run again on it. `scratch` holds part 4 bytes. Saves the score GEMM
- * and softmax-row pass of the recompute at the cost of keeping B*T*N*4 bytes of scores
- * (plus the row statistics) between forward and backward. With the forward's `fold`, Vn
+ * and softmax-row pass of the recompute, and the rebuild and transpose-fold of P_V, at
+ * the cost of keeping B*T*N*(4 + element size) bytes of scores and weights (plus the row
+ * statistics) between forward and backward. With the forward's `fold`, Vn
  * and gVn may be null: gVn is not formed, the gradient of slot j's successor row is added
  * to gV[j + fold[j]] (no gO Vn^T and no P_Vn^T gO GEMM). */
 int dabsn_hip_read3_bwd_after_fwd(int dtype, int64_t B, int64_t T, int64_t N, int64_t H,
