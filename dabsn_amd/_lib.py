@@ -101,9 +101,10 @@ _SIGNATURES = {
     "dabsn_hip_read_output_bwd": (
         [i32, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_read_output_window": (
-        [i32, i32, i32, i32, i64, i64, i64, vp, vp, vp, vp, vp], i32),
+        [i32, i32, i32, i32, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_read_output_bwd_window": (
-        [i32, i32, i32, i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
+        [i32, i32, i32, i32, i64, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, sz, vp],
+        i32),
     "dabsn_hip_read_mix": ([i32, i64, vp, vp, vp, vp, vp, vp, vp], i32),
     "dabsn_hip_rms_norm": ([i32, i64, i64, vp, vp, ctypes.c_float, vp, vp], i32),
     "dabsn_hip_relu_square": ([i32, i64, vp, vp, vp], i32),

@@ -472,30 +472,36 @@ static inline bool vec_ok(int64_t H, std::initializer_list<const void*> ptrs) {
 // (gain, long), rounded to bf16 when prod_bf16, then the sum in the dtype of (proj, product),
 // rounded by the store to O. No contraction into a fused multiply-add.
 // Elements are addressed as segments: chunk i of V elements lies in segment i / seg (seg
-// chunks each, segments ld chunks apart), so a time window [t0, t1) of [B, T, H] tensors is
-// B segments of (t1 - t0) H elements, T H apart. A flat array is one segment.
-__device__ __forceinline__ size_t seg_offset(uint32_t i, uint32_t seg, uint64_t ld) {
-  return static_cast<size_t>(i / seg) * ld + (i % seg);
+// chunks each), and each tensor has its own segment stride (in chunks), so a time window
+// [t0, t1) of [B, T, H] tensors is B segments of (t1 - t0) H elements, T H apart, and a
+// contiguous [B, t1 - t0, H] block the same segments (t1 - t0) H apart. A flat array is one
+// segment.
+struct SegLd {
+  uint64_t ld[4];
+};
+
+__device__ __forceinline__ size_t seg_offset(uint32_t s, uint32_t r, uint64_t ld) {
+  return static_cast<size_t>(s) * ld + r;
 }
 
 template <typename P, typename L, typename O, int V>
-__global__ void __launch_bounds__(256) read_out_kernel(uint32_t chunks, uint32_t seg, uint64_t ld,
+__global__ void __launch_bounds__(256) read_out_kernel(uint32_t chunks, uint32_t seg, SegLd ld,
                                                        const P* proj, const L* lng,
                                                        const float* gain, int prod_bf16, O* out) {
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   if (i >= chunks) return;
-  const size_t o = seg_offset(i, seg, ld) * V;
+  const uint32_t s = i / seg, r = i % seg;
   const float g = gain[0];
   float a[V], l[V];
-  ldv<P, V>(proj + o, a);
-  ldv<L, V>(lng + o, l);
+  ldv<P, V>(proj + seg_offset(s, r, ld.ld[0]) * V, a);
+  ldv<L, V>(lng + seg_offset(s, r, ld.ld[1]) * V, l);
 #pragma unroll
   for (int e = 0; e < V; ++e) {
     float prod = g * l[e];
     if (prod_bf16) prod = round_to<bf16>(prod);
     a[e] = a[e] + prod;
   }
-  stv<O, V>(out + o, a);
+  stv<O, V>(out + seg_offset(s, r, ld.ld[2]) * V, a);
 }
 
 // Its backward, as autograd evaluates it: gproj = gout cast to P; the product's gradient
@@ -504,7 +510,7 @@ __global__ void __launch_bounds__(256) read_out_kernel(uint32_t chunks, uint32_t
 // workgroup, reduced in a fixed order by read_out_reduce_kernel.
 template <typename O, typename P, typename L, int V>
 __global__ void __launch_bounds__(256) read_out_bwd_kernel(uint32_t chunks, uint32_t seg,
-                                                           uint64_t ld, const O* gout,
+                                                           SegLd ld, const O* gout,
                                                            const L* lng, const float* gain,
                                                            int prod_bf16, P* gproj, L* glong,
                                                            float* partial) {
@@ -512,11 +518,11 @@ __global__ void __launch_bounds__(256) read_out_bwd_kernel(uint32_t chunks, uint
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   float acc = 0.0f;
   if (i < chunks) {
-    const size_t o = seg_offset(i, seg, ld) * V;
+    const uint32_t s = i / seg, r = i % seg;
     const float g = gain[0];
     float go[V], l[V], gl[V];
-    ldv<O, V>(gout + o, go);
-    ldv<L, V>(lng + o, l);
+    ldv<O, V>(gout + seg_offset(s, r, ld.ld[0]) * V, go);
+    ldv<L, V>(lng + seg_offset(s, r, ld.ld[1]) * V, l);
 #pragma unroll
     for (int e = 0; e < V; ++e) {
       const float gp = prod_bf16 ? round_to<bf16>(go[e]) : go[e];
@@ -527,8 +533,8 @@ __global__ void __launch_bounds__(256) read_out_bwd_kernel(uint32_t chunks, uint
       if (prod_bf16) t = round_to<bf16>(t);
       acc += t;
     }
-    stv<P, V>(gproj + o, go);
-    stv<L, V>(glong + o, gl);
+    stv<P, V>(gproj + seg_offset(s, r, ld.ld[2]) * V, go);
+    stv<L, V>(glong + seg_offset(s, r, ld.ld[3]) * V, gl);
   }
   acc = wave_sum(acc);
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
@@ -1042,25 +1048,41 @@ static bool read_out_vec(int64_t n, std::initializer_list<const void*> ptrs) {
     }                                                                                     \
   } while (0)
 
-// read_output over `rows` segments of row_len elements, ld elements apart (a flat array:
-// one row). The vector path needs row_len and ld multiples of 8 and 16-byte aligned bases.
+// Segment strides of `n` tensors in V-element chunks (one segment: the row length); false
+// when a stride is shorter than a row or, on the vector path, not a multiple of 8.
+static bool seg_strides(int64_t rows, int64_t row_len, const int64_t* ld, int n, int64_t V,
+                        SegLd& out) {
+  for (int k = 0; k < n; ++k) {
+    if (rows > 1 && (ld[k] < row_len || ld[k] % V != 0)) return false;
+    out.ld[k] = static_cast<uint64_t>((rows <= 1 ? row_len : ld[k]) / V);
+  }
+  return true;
+}
+
+// read_output over `rows` segments of row_len elements, ld[k] elements apart in tensor k
+// (proj, long, out; a flat array: one row). The vector path needs row_len and every ld
+// multiples of 8 and 16-byte aligned bases.
 static int read_output_rows(const char* what, int proj_dtype, int long_dtype, int prod_dtype,
-                            int out_dtype, int64_t rows, int64_t row_len, int64_t ld,
+                            int out_dtype, int64_t rows, int64_t row_len, const int64_t ld[3],
                             const void* proj, const void* lng, const float* gain, void* out,
                             hipStream_t stream) {
-  DABSN_REQUIRE(rows >= 0 && row_len >= 0 && (rows <= 1 || ld >= row_len), "%s: bad size", what);
+  SegLd sl{};
+  DABSN_REQUIRE(rows >= 0 && row_len >= 0 && seg_strides(rows, row_len, ld, 3, 1, sl),
+                "%s: bad size", what);
   const int64_t n = rows * row_len;
   if (n == 0) return DABSN_OK;
   DABSN_REQUIRE(proj && lng && gain && out, "%s: null pointer", what);
   DABSN_REQUIRE(prod_dtype == kF32 || prod_dtype == kBF16, "%s: bad product dtype", what);
-  const bool vec = read_out_vec(row_len, {proj, lng, out}) && (rows <= 1 || ld % 8 == 0);
+  const bool vec =
+      read_out_vec(row_len, {proj, lng, out}) && seg_strides(rows, row_len, ld, 3, 8, sl);
+  if (!vec) seg_strides(rows, row_len, ld, 3, 1, sl);
   const int64_t V = vec ? 8 : 1;
-  const int64_t chunks = n / V, seg = row_len / V, ldc = rows <= 1 ? seg : ld / V;
+  const int64_t chunks = n / V, seg = row_len / V;
   DABSN_REQUIRE(chunks < (1ll << 32), "%s: too many elements", what);
   const dim3 grid(blocks_for(chunks, 256)), block(256);
 #define L(P, Lt, O, VV)                                                                        \
   hipLaunchKernelGGL((read_out_kernel<P, Lt, O, VV>), grid, block, 0, stream, (uint32_t)chunks,  \
-                     (uint32_t)seg, (uint64_t)ldc, (const P*)proj, (const Lt*)lng, gain,        \
+                     (uint32_t)seg, sl, (const P*)proj, (const Lt*)lng, gain,                   \
                      prod_dtype == kBF16 ? 1 : 0, (O*)out)
   READ_OUT_TYPES(what, proj_dtype, long_dtype, out_dtype, vec, L);
 #undef L
@@ -1068,28 +1090,32 @@ static int read_output_rows(const char* what, int proj_dtype, int long_dtype, in
   return DABSN_OK;
 }
 
+// Its backward; ld[k] for gout, long, gproj, glong.
 static int read_output_bwd_rows(const char* what, int out_dtype, int proj_dtype, int long_dtype,
-                                int prod_dtype, int64_t rows, int64_t row_len, int64_t ld,
-                                const void* gout, const void* lng, const float* gain,
-                                void* gproj, void* glong, float* ggain, float* partials,
-                                size_t partial_count, hipStream_t stream) {
-  DABSN_REQUIRE(rows >= 0 && row_len >= 0 && (rows <= 1 || ld >= row_len), "%s: bad size", what);
+                                int prod_dtype, int64_t rows, int64_t row_len,
+                                const int64_t ld[4], const void* gout, const void* lng,
+                                const float* gain, void* gproj, void* glong, float* ggain,
+                                float* partials, size_t partial_count, hipStream_t stream) {
+  SegLd sl{};
+  DABSN_REQUIRE(rows >= 0 && row_len >= 0 && seg_strides(rows, row_len, ld, 4, 1, sl),
+                "%s: bad size", what);
   DABSN_REQUIRE(ggain && partials, "%s: null pointer", what);
   const int64_t n = rows * row_len;
   if (n == 0) return dabsn_hip_zero(ggain, 4, stream);
   DABSN_REQUIRE(gout && lng && gain && gproj && glong, "%s: null pointer", what);
   DABSN_REQUIRE(prod_dtype == kF32 || prod_dtype == kBF16, "%s: bad product dtype", what);
-  const bool vec =
-      read_out_vec(row_len, {gout, lng, gproj, glong}) && (rows <= 1 || ld % 8 == 0);
+  const bool vec = read_out_vec(row_len, {gout, lng, gproj, glong}) &&
+                   seg_strides(rows, row_len, ld, 4, 8, sl);
+  if (!vec) seg_strides(rows, row_len, ld, 4, 1, sl);
   const int64_t V = vec ? 8 : 1;
-  const int64_t chunks = n / V, seg = row_len / V, ldc = rows <= 1 ? seg : ld / V;
+  const int64_t chunks = n / V, seg = row_len / V;
   DABSN_REQUIRE(chunks < (1ll << 32), "%s: too many elements", what);
   const unsigned nblk = blocks_for(chunks, 256);
   DABSN_REQUIRE(partial_count >= nblk, "%s: %zu partials < %u", what, partial_count, nblk);
   const dim3 grid(nblk), block(256);
 #define L(O, P, Lt, VV)                                                                        \
   hipLaunchKernelGGL((read_out_bwd_kernel<O, P, Lt, VV>), grid, block, 0, stream,              \
-                     (uint32_t)chunks, (uint32_t)seg, (uint64_t)ldc, (const O*)gout,            \
+                     (uint32_t)chunks, (uint32_t)seg, sl, (const O*)gout,                       \
                      (const Lt*)lng, gain, prod_dtype == kBF16 ? 1 : 0, (P*)gproj, (Lt*)glong,  \
                      partials)
   READ_OUT_TYPES(what, out_dtype, proj_dtype, long_dtype, vec, L);
@@ -1104,14 +1130,17 @@ int dabsn_hip_read_output(int proj_dtype, int long_dtype, int prod_dtype, int ou
                           int64_t n, const void* proj, const void* lng, const float* gain,
                           void* out, hipStream_t stream) {
   DABSN_REQUIRE(n >= 0, "read_output: bad size");
-  return read_output_rows("read_output", proj_dtype, long_dtype, prod_dtype, out_dtype, 1, n, n,
+  const int64_t ld[3] = {n, n, n};
+  return read_output_rows("read_output", proj_dtype, long_dtype, prod_dtype, out_dtype, 1, n, ld,
                           proj, lng, gain, out, stream);
 }
 
 int dabsn_hip_read_output_window(int proj_dtype, int long_dtype, int prod_dtype, int out_dtype,
-                                 int64_t rows, int64_t row_len, int64_t ld, const void* proj,
+                                 int64_t rows, int64_t row_len, int64_t ld_proj,
+                                 int64_t ld_long, int64_t ld_out, const void* proj,
                                  const void* lng, const float* gain, void* out,
                                  hipStream_t stream) {
+  const int64_t ld[3] = {ld_proj, ld_long, ld_out};
   return read_output_rows("read_output window", proj_dtype, long_dtype, prod_dtype, out_dtype,
                           rows, row_len, ld, proj, lng, gain, out, stream);
 }
@@ -1126,16 +1155,19 @@ int dabsn_hip_read_output_bwd(int out_dtype, int proj_dtype, int long_dtype, int
                               void* gproj, void* glong, float* ggain, float* partials,
                               size_t partial_count, hipStream_t stream) {
   DABSN_REQUIRE(n >= 0, "read_output backward: bad size");
+  const int64_t ld[4] = {n, n, n, n};
   return read_output_bwd_rows("read_output backward", out_dtype, proj_dtype, long_dtype,
-                              prod_dtype, 1, n, n, gout, lng, gain, gproj, glong, ggain,
+                              prod_dtype, 1, n, ld, gout, lng, gain, gproj, glong, ggain,
                               partials, partial_count, stream);
 }
 
 int dabsn_hip_read_output_bwd_window(int out_dtype, int proj_dtype, int long_dtype,
-                                     int prod_dtype, int64_t rows, int64_t row_len, int64_t ld,
-                                     const void* gout, const void* lng, const float* gain,
-                                     void* gproj, void* glong, float* ggain, float* partials,
-                                     size_t partial_count, hipStream_t stream) {
+                                     int prod_dtype, int64_t rows, int64_t row_len,
+                                     int64_t ld_gout, int64_t ld_long, int64_t ld_gproj,
+                                     int64_t ld_glong, const void* gout, const void* lng,
+                                     const float* gain, void* gproj, void* glong, float* ggain,
+                                     float* partials, size_t partial_count, hipStream_t stream) {
+  const int64_t ld[4] = {ld_gout, ld_long, ld_gproj, ld_glong};
   return read_output_bwd_rows("read_output window backward", out_dtype, proj_dtype, long_dtype,
                               prod_dtype, rows, row_len, ld, gout, lng, gain, gproj, glong,
                               ggain, partials, partial_count, stream);

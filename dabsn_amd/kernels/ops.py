@@ -1021,47 +1021,48 @@ def _read_output_fake(proj, long, gain):
     return proj.new_empty(proj.shape, dtype=_read_output_dtypes(proj, long, gain)[1])
 
 
-def _window_ptr(x: Tensor, t0: int) -> int:
-    return x.data_ptr() + t0 * x.shape[2] * x.element_size()
+def _row_blocks(what: str, *xs: Tensor) -> tuple[int, int, list[int]]:
+    """(B, C * H, per-tensor batch strides) of [B, C, H] views whose (C, H) block is
+    contiguous: time windows of [B, T, H] tensors or contiguous [B, C, H] tensors."""
+    B, C, H = xs[0].shape
+    for x in xs:
+        if (x.dim() != 3 or tuple(x.shape) != (B, C, H) or x.stride(2) != 1
+                or (C > 1 and x.stride(1) != H)):
+            raise ValueError(f"{what}: [B, C, H] views of one shape with contiguous (C, H) "
+                             "blocks")
+    return B, C * H, [x.stride(0) for x in xs]
 
 
-def read_output_window(proj: Tensor, long: Tensor, gain: Tensor, out: Tensor, t0: int,
-                       t1: int) -> None:
-    """out[:, t0:t1] = proj + gain * long over the time window [t0, t1) of contiguous
-    [B, T, H] tensors, in place (``dabsn_hip_read_output_window``; ``read_output``'s
-    arithmetic). ``gain``: the parameter (one value)."""
-    B, T, H = proj.shape
-    if not all(x.is_contiguous() and x.shape == proj.shape for x in (proj, long, out)):
-        raise ValueError("read_output_window: contiguous [B, T, H] tensors of one shape")
+def read_output_window(proj: Tensor, long: Tensor, gain: Tensor, out: Tensor) -> None:
+    """out = proj + gain * long over [B, C, H] views with contiguous (C, H) blocks (time
+    windows of [B, T, H] tensors or contiguous blocks, each its own batch stride), in place
+    (``dabsn_hip_read_output_window``; ``read_output``'s arithmetic). ``gain``: the parameter
+    (one value)."""
+    B, n, ld = _row_blocks("read_output_window", proj, long, out)
     prod_dt, out_dt = _read_output_dtypes(proj, long, gain)
     if out.dtype != out_dt:
         raise TypeError(f"read_output_window: out must be {out_dt}")
     lib = _lib.load()
     g = _f32_scalar(gain)
     _lib.check(lib.dabsn_hip_read_output_window(
-        _code(proj.dtype), _code(long.dtype), _code(prod_dt), _code(out_dt), B, (t1 - t0) * H,
-        T * H, _window_ptr(proj, t0), _window_ptr(long, t0), _p(g), _window_ptr(out, t0),
-        _stream(proj)), "read output window")
+        _code(proj.dtype), _code(long.dtype), _code(prod_dt), _code(out_dt), B, n, *ld,
+        _p(proj), _p(long), _p(g), _p(out), _stream(proj)), "read output window")
 
 
 def read_output_bwd_window(grad: Tensor, long: Tensor, gain: Tensor, gproj: Tensor,
-                           glong: Tensor, ggain: Tensor, t0: int, t1: int) -> None:
-    """``read_output``'s backward over the time window [t0, t1) of contiguous [B, T, H]
-    tensors, in place: gproj and glong windows written, ``ggain`` (one fp32 value) the
-    window's share of the gain gradient, summed in a fixed order."""
-    B, T, H = grad.shape
-    if not all(x.is_contiguous() and x.shape == grad.shape for x in (grad, long, gproj, glong)):
-        raise ValueError("read_output_bwd_window: contiguous [B, T, H] tensors of one shape")
+                           glong: Tensor, ggain: Tensor) -> None:
+    """``read_output``'s backward over [B, C, H] views as ``read_output_window`` takes, in
+    place: gproj and glong written, ``ggain`` (one fp32 value) the views' share of the gain
+    gradient, summed in a fixed order."""
+    B, n, ld = _row_blocks("read_output_bwd_window", grad, long, gproj, glong)
     prod_dt = torch.result_type(gain, long)
     lib = _lib.load()
     g = _f32_scalar(gain)
-    n = B * (t1 - t0) * H
-    count = lib.dabsn_hip_read_output_partials(n)
+    count = lib.dabsn_hip_read_output_partials(B * n)
     partials = torch.empty((max(count, 1),), device=grad.device, dtype=torch.float32)
     _lib.check(lib.dabsn_hip_read_output_bwd_window(
-        _code(grad.dtype), _code(gproj.dtype), _code(long.dtype), _code(prod_dt), B,
-        (t1 - t0) * H, T * H, _window_ptr(grad, t0), _window_ptr(long, t0), _p(g),
-        _window_ptr(gproj, t0), _window_ptr(glong, t0), _p(ggain), _p(partials),
+        _code(grad.dtype), _code(gproj.dtype), _code(long.dtype), _code(prod_dt), B, n, *ld,
+        _p(grad), _p(long), _p(g), _p(gproj), _p(glong), _p(ggain), _p(partials),
         partials.numel(), _stream(grad)), "read output window backward")
 
 

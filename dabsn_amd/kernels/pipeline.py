@@ -225,15 +225,18 @@ class _PipelinedScanRead(torch.autograd.Function):
         Wx_c, Wgx_c, ldx = ops.scan_inputs(Wx, Wgx, dt)
         out = chunked._Tapes(Wx_c, B, T, H)
         stats = torch.empty((B, T, 6), device=dev, dtype=torch.float32)
-        retr = torch.empty((B, T, H), device=dev, dtype=dt)    # the three-way read
-        short = torch.empty((B, T, H), device=dev, dtype=dt)   # its output projection
+        # Chunk-major row blocks (window k: rows [B t0, B t1), batch-major inside), kept for
+        # the backward: the projection's [y, budget] input and the three-way read, each
+        # window a contiguous matrix for the products that take it.
+        U_rows = torch.empty((B * T, 2 * H), device=dev, dtype=dt)
+        retr_rows = torch.empty((B * T, H), device=dev, dtype=dt)
         sink = torch.zeros((B, T, H), device=dev, dtype=dt)    # bank-write gradient (backward)
-        long_out = torch.empty((B, T, H), device=dev, dtype=dt)  # the long channel
         gain = read_params[names.index("long_gain")]
         logits = [read_params[names.index(n)] for n in _LONG_LOGITS]
         long_state0 = read.initial_long_scan_state(B, H, device=dev)
+        like = Wx.new_empty((1, 1, 1))
         read_out = torch.empty((B, T, H), device=dev,  # short + long_gain * long
-                               dtype=ops._read_output_dtypes(short, long_out, gain)[1])
+                               dtype=ops._read_output_dtypes(like, like, gain)[1])
         bounds = chunked._chunks(T, chunk)
         K = len(bounds)
         for st in (M, S, R):
@@ -283,6 +286,8 @@ class _PipelinedScanRead(torch.autograd.Function):
                                              None if fold is not None else next_idx, rank,
                                              sink_wait)
 
+                shorts: dict = {}
+
                 def read_chunk(k: int, leaves):
                     # Statistics of window k, the three-way read of query chunk k against the
                     # bank [0, t1) (its own autograd graph) and, without autograd, its output
@@ -298,8 +303,9 @@ class _PipelinedScanRead(torch.autograd.Function):
 
                     def project_y_budget():
                         with torch.no_grad():
-                            pre.append(F.linear(ops.window_copy(U[:, t0:t1]).view(B * C, 2 * H),
-                                                Wd[:, :2 * H], bd))
+                            Uk = U_rows[B * t0:B * t1]
+                            ops.window_add(Uk.view(B, C, 2 * H), U[:, t0:t1])
+                            pre.append(F.linear(Uk, Wd[:, :2 * H], bd))
 
                     w_leaf, stats_leaf, _ = leaves
                     with torch.enable_grad(), read.during_width_read(project_y_budget):
@@ -311,14 +317,15 @@ class _PipelinedScanRead(torch.autograd.Function):
                             bank_norms=norms, bank_stats=stats_leaf[:, :t1], query_start=t0,
                             gather=gather)
                     rd = r.detach().to(dt)
-                    ops.window_add(retr[:, t0:t1], rd)
+                    ops.window_add(retr_rows[B * t0:B * t1].view(B, C, H), rd)
                     sh = pre[0].addmm_(rd.reshape(B * C, H), Wd[:, 2 * H:].t())
-                    ops.window_add(short[:, t0:t1], sh.view(B, C, H))
+                    shorts[k] = sh.view(B, C, H)
                     return r, ay_leaf
 
                 # The long channel (long.py:492-579) window by window from the state the previous
                 # window ends in, differentiated by hand: per window its write and plasticity
-                # rows (contiguous copies, kept) and the checkpoint its backward replays from.
+                # rows (contiguous copies), the checkpoint its backward replays from and its
+                # output, kept.
                 events.announce("recurrent_long_read", "rocm_chunk_parallel_scan", B=B, T=T, H=H,
                                 dtype="bf16" if code == 1 else "fp32")
                 longs = []
@@ -331,8 +338,14 @@ class _PipelinedScanRead(torch.autograd.Function):
                     pk = ops.window_copy(pl[:, t0:t1])
                     lk, lf, ef, rf, ckpt = ops.direct.long_scan_fused(wk, pk, *logits, *carried)
                     carried = (lf, ef, rf)
-                    ops.window_add(long_out[:, t0:t1], lk)
-                    longs.append((wk, pk, ckpt))
+                    longs.append((wk, pk, ckpt, lk))
+
+                def read_output(k: int) -> None:
+                    # short + long_gain * long over window k, into the full-length output.
+                    t0, t1 = bounds[k]
+                    lk = longs[k][3]
+                    lk.record_stream(torch.cuda.current_stream(dev))
+                    ops.read_output_window(shorts.pop(k), lk, gain, read_out[:, t0:t1])
 
                 chunks = []
                 with _parameters_as(read, sets[0][2]):
@@ -346,7 +359,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                                 r_chunks = torch.cuda.Event()
                                 r_chunks.record(R)
                             long_window(k)
-                            ops.read_output_window(short, long_out, gain, read_out, *bounds[k])
+                            read_output(k)
                         # The last window's long channel beside the last chunk's read.
                         R.wait_event(scan_done[K - 1])
                         long_window(K - 1)
@@ -357,7 +370,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                 with _parameters_as(read, sets[1][2]):
                     chunks.append(read_chunk(K - 1, sets[1]))
                     M.wait_event(r_long)
-                    ops.read_output_window(short, long_out, gain, read_out, *bounds[K - 1])
+                    read_output(K - 1)
                 M.wait_stream(S)
             _check_scans(S, fwd_calls, "core scan forward")
         finally:
@@ -372,10 +385,11 @@ class _PipelinedScanRead(torch.autograd.Function):
         ctx.read, ctx.chunk, ctx.names = read, chunk, names
         ctx.bounds = bounds
         ctx.meta = [(x.dtype, tuple(x.shape)) for x in (Wx, Wgx, *core_in)]
-        ctx.graph = (chunks, longs, sets, sink, sink_wait, long_out)
+        ctx.graph = (chunks, longs, sets, sink, sink_wait)
         ctx.transposed = (GAT, WdT)
         ctx.out_dtype = read_out.dtype
-        ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, starts, retr, out.U, *out.tapes)
+        ctx.save_for_backward(Wx_c, Wgx_c, Ug, A, *vecs, *scal, starts, retr_rows, U_rows, out.U,
+                              *out.tapes)
         ctx.set_materialize_grads(False)
         return U[..., :H], U[..., H:], read_out
 
@@ -389,9 +403,9 @@ class _PipelinedScanRead(torch.autograd.Function):
         saved = ctx.saved_tensors
         Wx, Wgx, Ug, A = saved[:4]
         vecs, scal = saved[4:20], saved[20:23]
-        starts, retr = saved[23], saved[24]
-        fwd_out = chunked._Tapes(None, 0, 0, 0, existing=saved[25:33])
-        chunks, longs, sets, sink, sink_wait, long_out = ctx.graph
+        starts, retr_rows, U_rows = saved[23], saved[24], saved[25]
+        fwd_out = chunked._Tapes(None, 0, 0, 0, existing=saved[26:34])
+        chunks, longs, sets, sink, sink_wait = ctx.graph
         GAT, WdT = ctx.transposed
         # Leaves of the read-half chunks, and of the last chunk (whole-device stream): the
         # hand-differentiated parameters' gradients go to the first set, and the second
@@ -421,9 +435,10 @@ class _PipelinedScanRead(torch.autograd.Function):
         g_read = (torch.zeros((B, T, H), device=dev, dtype=ctx.out_dtype) if g_read is None
                   else g_read.to(ctx.out_dtype).contiguous())
         # The read output's gradients, window by window: the projection's and the long
-        # channel's, and the gain's share of each window.
-        g_short3 = torch.empty((B, T, H), device=dev, dtype=dt)
-        g_long = torch.empty_like(long_out)
+        # channel's (chunk-major rows, as the forward's kept rows), and the gain's share of
+        # each window.
+        gs_rows = torch.empty((B * T, H), device=dev, dtype=dt)
+        gl_rows = torch.empty((B * T, H), device=dev, dtype=dt)
         gain_leaf = param_leaves["long_gain"]
         gain_parts = torch.zeros((K,), device=dev, dtype=torch.float32)
         out_done = [False] * K
@@ -450,14 +465,14 @@ class _PipelinedScanRead(torch.autograd.Function):
                 else:
                     torch.add(g_in[:, t0:t1], g_proj, out=dst)
 
-        def projection_grads(g_short3: Tensor, k: int, u_stream=None) -> Tensor:
+        def projection_grads(k: int, u_stream=None) -> Tensor:
             # out(cat[y, budget, retrieved]) over query chunk k: one product gives the
             # gradients of all three inputs; the retrieved rows' gradient is returned. With
             # u_stream, the retrieved third is its own product, after which the read's
             # backward can start, and the [y, budget] part runs on u_stream.
             t0, t1 = bounds[k]
             C = t1 - t0
-            gs = ops.window_copy(g_short3[:, t0:t1]).view(B * C, H)
+            gs = gs_rows[B * t0:B * t1]
             if u_stream is None:
                 prod = F.linear(gs, WdT)
                 fill_gU(prod, k)
@@ -476,7 +491,7 @@ class _PipelinedScanRead(torch.autograd.Function):
             # trajectory's y rows, summed over the window's rows (one GEMM), and the scan's
             # parameter partials reduced.
             t0, t1 = bounds[k]
-            y = ops.window_copy(fwd_out.U[:, t0:t1, :H]).view(-1, H)
+            y = U_rows[B * t0:B * t1, :H]
             gd = torch.empty((B, t1 - t0, 2 * H), device=dev, dtype=dt)
             ops.window_add(gd[..., :H], gWgx[:, t0:t1])
             ops.window_add(gd[..., H:], day[:, t0:t1])
@@ -486,8 +501,14 @@ class _PipelinedScanRead(torch.autograd.Function):
 
         def read_out_backward(k: int) -> None:
             if not out_done[k]:
-                ops.read_output_bwd_window(g_read, long_out, gain_leaf, g_short3, g_long,
-                                           gain_parts[k:k + 1], *bounds[k])
+                t0, t1 = bounds[k]
+                C = t1 - t0
+                lk = longs[k][3]
+                lk.record_stream(torch.cuda.current_stream(dev))
+                ops.read_output_bwd_window(g_read[:, t0:t1], lk, gain_leaf,
+                                           gs_rows[B * t0:B * t1].view(B, C, H),
+                                           gl_rows[B * t0:B * t1].view(B, C, H),
+                                           gain_parts[k:k + 1])
                 out_done[k] = True
 
         logit_leaves = [param_leaves[n] for n in _LONG_LOGITS]
@@ -499,10 +520,11 @@ class _PipelinedScanRead(torch.autograd.Function):
             # Window k of the long channel: its rows' gradient plus the gradient of the state
             # it ends in (from window k + 1's backward); leaves the gradient of the state it
             # starts from for window k - 1.
-            wk, pk, ckpt = longs[k]
+            wk, pk, ckpt, _ = longs[k]
             t0, t1 = bounds[k]
             gw, gp, part, g0 = ops.long_scan_backward_parts(
-                wk, pk, logit_leaves, ckpt, ops.window_copy(g_long[:, t0:t1]), *state_grad)
+                wk, pk, logit_leaves, ckpt, gl_rows[B * t0:B * t1].view(B, t1 - t0, H),
+                *state_grad)
             long_grads[k] = (gw, gp)
             logit_sum[0] = part if logit_sum[0] is None else logit_sum[0] + part
             state_grad[:] = g0
@@ -551,7 +573,7 @@ class _PipelinedScanRead(torch.autograd.Function):
                         read_out_backward(k)
                         # The last chunk's [y, budget] product on the scan half, idle until
                         # that chunk's reverse scan, which the scan stream's order puts after it.
-                        g_r = projection_grads(g_short3, k, S if k == K - 1 else None)
+                        g_r = projection_grads(k, S if k == K - 1 else None)
                         # The write leaf is listed so that the engine runs the gather's backward,
                         # whose gradient goes to the sink (it returns none for the leaf itself).
                         torch.autograd.backward([r], [g_r], inputs=[ay_leaf, sets[side][0],
@@ -597,14 +619,13 @@ class _PipelinedScanRead(torch.autograd.Function):
                         ev.record(S)
                         scan_back[k] = ev
                 with torch.cuda.stream(R):
-                    # The projection's weight gradients, beside the last reverse scan.
-                    U2 = fwd_out.U.reshape(B * T, 2 * H)
-                    g_short = g_short3.reshape(B * T, H)
+                    # The projection's weight gradients, beside the last reverse scan (rows
+                    # paired in the chunk-major order of all three).
                     gw = torch.empty((H, 3 * H), device=dev, dtype=W.dtype)
-                    gw[:, :2 * H] = g_short.t() @ U2
-                    gw[:, 2 * H:] = g_short.t() @ retr.reshape(B * T, H)
+                    gw[:, :2 * H] = gs_rows.t() @ U_rows
+                    gw[:, 2 * H:] = gs_rows.t() @ retr_rows
                     W.grad = gw
-                    bias.grad = torch.sum(g_short, dim=0, dtype=torch.float32).to(bias.dtype)
+                    bias.grad = torch.sum(gs_rows, dim=0, dtype=torch.float32).to(bias.dtype)
                     if K > 1:
                         R.wait_event(scan_back[1])
                         core_weight_grads(1)

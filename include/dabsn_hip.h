@@ -233,21 +233,24 @@ int dabsn_hip_read_output_bwd(int out_dtype, int proj_dtype, int long_dtype, int
                               int64_t n, const void* gout, const void* lng, const float* gain,
                               void* gproj, void* glong, float* ggain, float* partials,
                               size_t partial_count, hipStream_t stream);
-/* The two above on a window of rows: `rows` segments of row_len elements, ld elements
- * apart in every tensor (a time window [t0, t1) of [B, T, H] tensors: rows = B,
- * row_len = (t1 - t0) H, ld = T H, pointers at step t0 of batch row 0). The backward's
- * partial_count >= dabsn_hip_read_output_partials(rows * row_len); ggain receives the
- * window's share of the gain gradient. No reference counterpart: they let a time-chunked
- * read form its output and gradient window by window. */
+/* The two above on a window of rows: `rows` segments of row_len elements, each tensor's
+ * segments its own ld_* elements apart (a time window [t0, t1) of a [B, T, H] tensor:
+ * rows = B, row_len = (t1 - t0) H, ld = T H, pointer at step t0 of batch row 0; a
+ * contiguous [B, t1 - t0, H] block: ld = row_len). The backward's partial_count >=
+ * dabsn_hip_read_output_partials(rows * row_len); ggain receives the window's share of the
+ * gain gradient. No reference counterpart: they let a time-chunked read form its output and
+ * gradient window by window. */
 int dabsn_hip_read_output_window(int proj_dtype, int long_dtype, int prod_dtype, int out_dtype,
-                                 int64_t rows, int64_t row_len, int64_t ld, const void* proj,
+                                 int64_t rows, int64_t row_len, int64_t ld_proj,
+                                 int64_t ld_long, int64_t ld_out, const void* proj,
                                  const void* lng, const float* gain, void* out,
                                  hipStream_t stream);
 int dabsn_hip_read_output_bwd_window(int out_dtype, int proj_dtype, int long_dtype,
-                                     int prod_dtype, int64_t rows, int64_t row_len, int64_t ld,
-                                     const void* gout, const void* lng, const float* gain,
-                                     void* gproj, void* glong, float* ggain, float* partials,
-                                     size_t partial_count, hipStream_t stream);
+                                     int prod_dtype, int64_t rows, int64_t row_len,
+                                     int64_t ld_gout, int64_t ld_long, int64_t ld_gproj,
+                                     int64_t ld_glong, const void* gout, const void* lng,
+                                     const float* gain, void* gproj, void* glong, float* ggain,
+                                     float* partials, size_t partial_count, hipStream_t stream);
 /* Row normalisation q = x / max(|x|, 1e-12) given norms [B*T] (F.normalize, read.py:154). */
 int dabsn_hip_normalize_rows(int dtype, int64_t rows, int64_t H, const void* x, const float* norms,
                              void* q, hipStream_t stream);

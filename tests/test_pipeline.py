@@ -178,7 +178,9 @@ def test_read_output_windows_equal_the_whole_op(cuda_device, dtypes, B, T, H, bo
     axis against ``read_output`` and its backward on the whole tensors: outputs and the
     projection / long gradients bit for bit (the same arithmetic per element, vector path at
     H = 24, scalar path at H = 5), the gain gradient as the sum of the window shares (another
-    summation order: within 1e-6 of the sum of its terms' magnitudes)."""
+    summation order: within 1e-6 of the sum of its terms' magnitudes). Every other window
+    passes its inputs (forward) or outputs (backward) as contiguous [B, C, H] blocks beside
+    time-window views of the full tensors, so the tensors' batch strides differ."""
     from dabsn_amd.kernels import ops
 
     pd, ld, gd = dtypes
@@ -188,8 +190,11 @@ def test_read_output_windows_equal_the_whole_op(cuda_device, dtypes, B, T, H, bo
     gain = torch.tensor([0.37], device=cuda_device, dtype=gd).reshape(())
     whole = ops.read_output(proj, lng, gain)
     out = torch.full_like(whole, float("nan"))
-    for t0, t1 in bounds:
-        ops.read_output_window(proj, lng, gain, out, t0, t1)
+    for k, (t0, t1) in enumerate(bounds):
+        p_k, l_k = proj[:, t0:t1], lng[:, t0:t1]
+        if k % 2:
+            p_k, l_k = p_k.contiguous(), l_k.contiguous()
+        ops.read_output_window(p_k, l_k, gain, out[:, t0:t1])
     assert torch.equal(out, whole)
 
     grad = torch.randn(B, T, H, generator=g).to(cuda_device, whole.dtype)
@@ -197,7 +202,14 @@ def test_read_output_windows_equal_the_whole_op(cuda_device, dtypes, B, T, H, bo
     gp, gl = torch.empty_like(proj), torch.empty_like(lng)
     shares = torch.zeros(len(bounds), device=cuda_device, dtype=torch.float32)
     for k, (t0, t1) in enumerate(bounds):
-        ops.read_output_bwd_window(grad, lng, gain, gp, gl, shares[k:k + 1], t0, t1)
+        if k % 2:
+            gp_k, gl_k = torch.empty_like(gp[:, t0:t1]), torch.empty_like(gl[:, t0:t1])
+        else:
+            gp_k, gl_k = gp[:, t0:t1], gl[:, t0:t1]
+        ops.read_output_bwd_window(grad[:, t0:t1], lng[:, t0:t1], gain, gp_k, gl_k,
+                                   shares[k:k + 1])
+        if k % 2:
+            gp[:, t0:t1], gl[:, t0:t1] = gp_k, gl_k
     assert torch.equal(gp, gp_w) and torch.equal(gl, gl_w)
     want = float(gg_w.float())
     # Relative to the sum of |terms|: the gain's gradient sums B*T*H products of both signs.
