@@ -88,10 +88,11 @@ _SIGNATURES = {
     "dabsn_hip_linrec_bwd": ([i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_long_workspace_bytes": ([i64, i64, i64, i32], sz),
     "dabsn_hip_long_fwd": (
-        [i32, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
+        [i32, i64, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_long_partials": ([i64, i64, i64], i64),
     "dabsn_hip_long_bwd": (
-        [i32, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp],
+        [i32, i64, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+         sz, vp],
         i32,
     ),
     "dabsn_hip_tape_stats": ([i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),

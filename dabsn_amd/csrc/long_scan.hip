@@ -132,10 +132,11 @@ struct ChunkIdx {
   int64_t ch;       // b * H + h
   int b, h, k, t0, len, nseg;
   size_t base;      // offset of (b, 0, h) in [B, T, H]
+  size_t ibase;     // offset of (b, 0, h) in the inputs w, p (batch rows ldx apart)
   size_t cbase;     // offset of (b, k, 0, h) in the checkpoint [B][nseg][3][H]
 };
 
-__device__ __forceinline__ bool chunk_idx(int B, int T, int H, ChunkIdx& c) {
+__device__ __forceinline__ bool chunk_idx(int B, int T, int H, int64_t ldx, ChunkIdx& c) {
   c.ch = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
   if (c.ch >= static_cast<int64_t>(B) * H) return false;
   c.b = static_cast<int>(c.ch / H);
@@ -145,6 +146,7 @@ __device__ __forceinline__ bool chunk_idx(int B, int T, int H, ChunkIdx& c) {
   c.len = min(CK, T - c.t0);
   c.nseg = (T + CK - 1) / CK;
   c.base = static_cast<size_t>(c.b) * T * H + c.h;
+  c.ibase = static_cast<size_t>(c.b) * ldx + c.h;
   c.cbase = (static_cast<size_t>(c.b) * c.nseg + c.k) * 3 * H + c.h;
   return true;
 }
@@ -153,18 +155,19 @@ __device__ __forceinline__ bool chunk_idx(int B, int T, int H, ChunkIdx& c) {
 // R from 0 -> loc0 = R end. PHASE 2: E, R from true starts, L from 0 -> loc0 = L end,
 // loc1 = prod eff. PHASE 3: all from true starts (the checkpoint) -> out.
 template <typename E, int PHASE>
-__global__ void __launch_bounds__(NT) long_fwd_chunk(int B, int T, int H, const E* w, const E* p,
-                                                     Logits lg, const float* ckpt, float* loc0,
+__global__ void __launch_bounds__(NT) long_fwd_chunk(int B, int T, int H, int64_t ldx,
+                                                     const E* w, const E* p, Logits lg,
+                                                     const float* ckpt, float* loc0,
                                                      float* loc1, E* out) {
   ChunkIdx c;
-  if (!chunk_idx(B, T, H, c)) return;
+  if (!chunk_idx(B, T, H, ldx, c)) return;
   const Coef k = load_coef(lg.p);
   float wv[CK], pv[CK];
 #pragma unroll
   for (int i = 0; i < CK; ++i) {
     // Clamped, unconditional loads so all CK requests are in flight at once (steps past
     // the chunk end are never used).
-    const size_t o = c.base + static_cast<size_t>(c.t0 + min(i, c.len - 1)) * H;
+    const size_t o = c.ibase + static_cast<size_t>(c.t0 + min(i, c.len - 1)) * H;
     wv[i] = ld(w, o);
     if (PHASE >= 2) pv[i] = ld(p, o);
   }
@@ -206,8 +209,9 @@ __global__ void __launch_bounds__(NT) long_fwd_chunk(int B, int T, int H, const 
 // order of long.py:492-579 (as phase 3 above), with the final state taken from the walk.
 // The checkpoint (if given) of the one chunk is the initial state.
 template <typename E>
-__global__ void __launch_bounds__(NT) long_fwd_single(int B, int T, int H, const E* w, const E* p,
-                                                      Logits lg, const float* L0, const float* E0,
+__global__ void __launch_bounds__(NT) long_fwd_single(int B, int T, int H, int64_t ldx,
+                                                      const E* w, const E* p, Logits lg,
+                                                      const float* L0, const float* E0,
                                                       const float* R0, E* out, float* LF,
                                                       float* EF, float* RF, float* ckpt) {
   const int64_t ch = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
@@ -215,6 +219,7 @@ __global__ void __launch_bounds__(NT) long_fwd_single(int B, int T, int H, const
   const Coef k = load_coef(lg.p);
   const int b = static_cast<int>(ch / H), h = static_cast<int>(ch % H);
   const size_t base = static_cast<size_t>(b) * T * H + h;
+  const size_t ibase = static_cast<size_t>(b) * ldx + h;
   float L = L0[ch], Ev = E0[ch], R = R0[ch];
   if (ckpt) {
     float* cp = ckpt + static_cast<size_t>(b) * 3 * H + h;
@@ -223,9 +228,9 @@ __global__ void __launch_bounds__(NT) long_fwd_single(int B, int T, int H, const
     cp[2 * H] = R;
   }
   for (int t = 0; t < T; ++t) {
-    const size_t o = base + static_cast<size_t>(t) * H;
+    const size_t o = base + static_cast<size_t>(t) * H, io = ibase + static_cast<size_t>(t) * H;
     float pe, eff;
-    advance(k, ld(w, o), ld(p, o), L, Ev, R, pe, eff);
+    advance(k, ld(w, io), ld(p, io), L, Ev, R, pe, eff);
     st(out, o, L);
   }
   LF[ch] = L;
@@ -296,21 +301,22 @@ __device__ __forceinline__ StepMap step_map(const Coef& k, float wt, float pt, f
 // in `maps` [9][nseg][B*H]. The forward values around each step are replayed from the
 // chunk's checkpoint.
 template <typename E>
-__global__ void __launch_bounds__(NT) long_bwd_map(int B, int T, int H, const E* w, const E* p,
-                                                   Logits lg, const float* ckpt, const E* gout,
+__global__ void __launch_bounds__(NT) long_bwd_map(int B, int T, int H, int64_t ldx,
+                                                   const E* w, const E* p, Logits lg,
+                                                   const float* ckpt, const E* gout,
                                                    float* maps) {
   ChunkIdx c;
-  if (!chunk_idx(B, T, H, c)) return;
+  if (!chunk_idx(B, T, H, ldx, c)) return;
   const Coef k = load_coef(lg.p);
   float wv[CK], pv[CK], gv[CK];
 #pragma unroll
   for (int i = 0; i < CK; ++i) {
     // Clamped, unconditional loads so all requests are in flight at once (steps past the
     // chunk end are never used).
-    const size_t o = c.base + static_cast<size_t>(c.t0 + min(i, c.len - 1)) * H;
-    wv[i] = ld(w, o);
-    pv[i] = ld(p, o);
-    gv[i] = ld(gout, o);
+    const size_t t = static_cast<size_t>(c.t0 + min(i, c.len - 1)) * H;
+    wv[i] = ld(w, c.ibase + t);
+    pv[i] = ld(p, c.ibase + t);
+    gv[i] = ld(gout, c.base + t);
   }
   float L = ckpt[c.cbase], Ev = ckpt[c.cbase + H], R = ckpt[c.cbase + 2 * H];
   float p00 = 1.f, p10 = 0.f, p11 = 1.f, p20 = 0.f, p21 = 0.f, p22 = 1.f;
@@ -388,13 +394,14 @@ __global__ void __launch_bounds__(NT) long_bwd_carry(int B, int T, int H, const 
 // kept in registers), then walk it backward from the exact entering adjoints (maps
 // components 0..2); writes gw, gp and reduces the logit gradients per block (fixed order).
 template <typename E>
-__global__ void __launch_bounds__(NT) long_bwd_final(int B, int T, int H, const E* w, const E* p,
-                                                     Logits lg, const float* ckpt,
-                                                     const E* gout, const float* maps, E* gw,
-                                                     E* gp, float* part) {
+__global__ void __launch_bounds__(NT) long_bwd_final(int B, int T, int H, int64_t ldx,
+                                                     const E* w, const E* p, Logits lg,
+                                                     const float* ckpt, const E* gout,
+                                                     const float* maps, E* gw, E* gp,
+                                                     float* part) {
   __shared__ float red[4][NT];
   ChunkIdx c;
-  const bool ok = chunk_idx(B, T, H, c);
+  const bool ok = chunk_idx(B, T, H, ldx, c);
   const Coef k = load_coef(lg.p);
   float d_er = 0.f, d_rd = 0.f, d_ret = 0.f, d_rs = 0.f;
   if (ok) {
@@ -402,10 +409,10 @@ __global__ void __launch_bounds__(NT) long_bwd_final(int B, int T, int H, const 
 #pragma unroll
     for (int i = 0; i < CK; ++i) {
       // Clamped, unconditional loads (steps past the chunk end are never used).
-      const size_t o = c.base + static_cast<size_t>(c.t0 + min(i, c.len - 1)) * H;
-      wv[i] = ld(w, o);
-      pv[i] = ld(p, o);
-      gv[i] = ld(gout, o);
+      const size_t t = static_cast<size_t>(c.t0 + min(i, c.len - 1)) * H;
+      wv[i] = ld(w, c.ibase + t);
+      pv[i] = ld(p, c.ibase + t);
+      gv[i] = ld(gout, c.base + t);
     }
     float L = ckpt[c.cbase], Es = ckpt[c.cbase + H], R = ckpt[c.cbase + 2 * H];
 #pragma unroll
@@ -477,7 +484,8 @@ using namespace dabsn::longmem;
                 "bad shape B=%lld T=%lld H=%lld", (long long)(B), (long long)(T), (long long)(H))
 
 template <typename E>
-static int long_fwd_impl(int B, int T, int H, const E* w, const E* p, Logits lg, const float* L0,
+static int long_fwd_impl(int B, int T, int H, int64_t ldx, const E* w, const E* p, Logits lg,
+                         const float* L0,
                          const float* E0, const float* R0, E* out, float* LF, float* EF, float* RF,
                          float* keep, float* ws, hipStream_t stream) {
   const int gx = grid_for(B, H);
@@ -488,24 +496,24 @@ static int long_fwd_impl(int B, int T, int H, const E* w, const E* p, Logits lg,
   float* ckpt = keep ? keep : ws + 2 * static_cast<size_t>(nseg) * B * H;
   const dim3 cg(gx, nseg), blk(NT);
   if (nseg == 1) {  // one chunk: a single walk, no chunk-parallel passes
-    hipLaunchKernelGGL((long_fwd_single<E>), dim3(gx), blk, 0, stream, B, T, H, w, p, lg, L0, E0,
+    hipLaunchKernelGGL((long_fwd_single<E>), dim3(gx), blk, 0, stream, B, T, H, ldx, w, p, lg, L0, E0,
                        R0, out, LF, EF, RF, keep);
     DABSN_HIP_CHECK(hipGetLastError());
     return DABSN_OK;
   }
-  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 0>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 0>), cg, blk, 0, stream, B, T, H, ldx, w, p, lg, ckpt, loc0, loc1, out);
   hipLaunchKernelGGL(long_fwd_carry<1>, dim3(gx), blk, 0, stream, B, T, H, lg, E0, loc0, loc1, ckpt, EF);
-  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 1>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 1>), cg, blk, 0, stream, B, T, H, ldx, w, p, lg, ckpt, loc0, loc1, out);
   hipLaunchKernelGGL(long_fwd_carry<2>, dim3(gx), blk, 0, stream, B, T, H, lg, R0, loc0, loc1, ckpt, RF);
-  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 2>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 2>), cg, blk, 0, stream, B, T, H, ldx, w, p, lg, ckpt, loc0, loc1, out);
   hipLaunchKernelGGL(long_fwd_carry<0>, dim3(gx), blk, 0, stream, B, T, H, lg, L0, loc0, loc1, ckpt, LF);
-  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 3>), cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, loc0, loc1, out);
+  if (nseg > 0) hipLaunchKernelGGL((long_fwd_chunk<E, 3>), cg, blk, 0, stream, B, T, H, ldx, w, p, lg, ckpt, loc0, loc1, out);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
 }
 
 template <typename E>
-static int long_bwd_impl(int B, int T, int H, const E* w, const E* p, Logits lg,
+static int long_bwd_impl(int B, int T, int H, int64_t ldx, const E* w, const E* p, Logits lg,
                          const float* ckpt, const E* gout, const float* gLF, const float* gEF,
                          const float* gRF, E* gw, E* gp, float* gL0, float* gE0, float* gR0,
                          float* part, float* ws, hipStream_t stream) {
@@ -513,11 +521,12 @@ static int long_bwd_impl(int B, int T, int H, const E* w, const E* p, Logits lg,
   const int nseg = (T + CK - 1) / CK;
   const dim3 cg(gx, nseg), blk(NT);
   if (nseg > 0)
-    hipLaunchKernelGGL(long_bwd_map<E>, cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, gout, ws);
+    hipLaunchKernelGGL(long_bwd_map<E>, cg, blk, 0, stream, B, T, H, ldx, w, p, lg, ckpt, gout,
+                       ws);
   hipLaunchKernelGGL(long_bwd_carry, dim3(gx), blk, 0, stream, B, T, H, gLF, gRF, gEF, ws, gL0,
                      gR0, gE0);
   if (nseg > 0)
-    hipLaunchKernelGGL(long_bwd_final<E>, cg, blk, 0, stream, B, T, H, w, p, lg, ckpt, gout,
+    hipLaunchKernelGGL(long_bwd_final<E>, cg, blk, 0, stream, B, T, H, ldx, w, p, lg, ckpt, gout,
                        ws, gw, gp, part);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
@@ -578,11 +587,23 @@ size_t dabsn_hip_long_workspace_bytes(int64_t B, int64_t T, int64_t H, int backw
   return static_cast<size_t>(backward ? 9 : 5) * static_cast<size_t>(nseg) * B * H * sizeof(float);
 }
 
-int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
-                       const float* const* logits, const float* L0, const float* E0,
-                       const float* R0, void* out, float* LF, float* EF, float* RF, float* ckpt,
-                       void* workspace, size_t workspace_bytes, hipStream_t stream) {
+// Batch stride of the inputs w, p: ldx elements (0: T H, the contiguous layout); at least
+// T H, so a time window of longer [B, T', H] tapes can be passed in place.
+static int64_t input_stride(int64_t B, int64_t T, int64_t H, int64_t ldx) {
+  if (ldx == 0) return T * H;
+  if (ldx < T * H || (B - 1) * ldx + T * H >= (1ll << 46)) return -1;
+  return ldx;
+}
+
+int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldx, const void* w,
+                       const void* p, const float* const* logits, const float* L0,
+                       const float* E0, const float* R0, void* out, float* LF, float* EF,
+                       float* RF, float* ckpt, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
   DABSN_SHAPE_CHECK(B, T, H);
+  const int64_t lx = input_stride(B, T, H, ldx);
+  DABSN_REQUIRE(lx >= 0, "long scan: bad input batch stride %lld for T=%lld H=%lld",
+                (long long)ldx, (long long)T, (long long)H);
   DABSN_REQUIRE(w && p && logits && L0 && E0 && R0 && (out || T == 0) && LF && EF && RF &&
                     (workspace || T == 0),
                 "long scan: null pointer");
@@ -593,11 +614,12 @@ int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w
   DABSN_REQUIRE((T + CK - 1) / CK < 65536, "long scan: T too long");
   Logits lg{{logits[0], logits[1], logits[2], logits[3]}};
   if (dtype == kBF16)
-    return long_fwd_impl<bf16>((int)B, (int)T, (int)H, (const bf16*)w, (const bf16*)p, lg, L0,
-                               E0, R0, (bf16*)out, LF, EF, RF, ckpt, (float*)workspace, stream);
+    return long_fwd_impl<bf16>((int)B, (int)T, (int)H, lx, (const bf16*)w, (const bf16*)p, lg,
+                               L0, E0, R0, (bf16*)out, LF, EF, RF, ckpt, (float*)workspace,
+                               stream);
   if (dtype == kF32)
-    return long_fwd_impl<float>((int)B, (int)T, (int)H, (const float*)w, (const float*)p, lg, L0,
-                                E0, R0, (float*)out, LF, EF, RF, ckpt, (float*)workspace,
+    return long_fwd_impl<float>((int)B, (int)T, (int)H, lx, (const float*)w, (const float*)p, lg,
+                                L0, E0, R0, (float*)out, LF, EF, RF, ckpt, (float*)workspace,
                                 stream);
   DABSN_REQUIRE(false, "long scan: bad dtype %d", dtype);
   return DABSN_OK;
@@ -607,12 +629,16 @@ int64_t dabsn_hip_long_partials(int64_t B, int64_t T, int64_t H) {
   return static_cast<int64_t>(grid_for(B, H)) * ((T + CK - 1) / CK);
 }
 
-int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
-                       const float* const* logits, const float* ckpt, const void* gout,
-                       const float* gLF, const float* gEF, const float* gRF, void* gw, void* gp,
-                       float* gL0, float* gE0, float* gR0, float* part_logit, void* workspace,
-                       size_t workspace_bytes, hipStream_t stream) {
+int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldx, const void* w,
+                       const void* p, const float* const* logits, const float* ckpt,
+                       const void* gout, const float* gLF, const float* gEF, const float* gRF,
+                       void* gw, void* gp, float* gL0, float* gE0, float* gR0,
+                       float* part_logit, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
   DABSN_SHAPE_CHECK(B, T, H);
+  const int64_t lx = input_stride(B, T, H, ldx);
+  DABSN_REQUIRE(lx >= 0, "long scan backward: bad input batch stride %lld for T=%lld H=%lld",
+                (long long)ldx, (long long)T, (long long)H);
   DABSN_REQUIRE(w && p && logits && (ckpt || T == 0) && (gout || T == 0) && gL0 && gE0 && gR0 &&
                     (part_logit || T == 0) && (workspace || T == 0) && ((gw && gp) || T == 0),
                 "long scan backward: null pointer");
@@ -623,13 +649,13 @@ int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w
   DABSN_REQUIRE((T + CK - 1) / CK < 65536, "long scan backward: T too long");
   Logits lg{{logits[0], logits[1], logits[2], logits[3]}};
   if (dtype == kBF16)
-    return long_bwd_impl<bf16>((int)B, (int)T, (int)H, (const bf16*)w, (const bf16*)p, lg, ckpt,
-                               (const bf16*)gout, gLF, gEF, gRF, (bf16*)gw, (bf16*)gp, gL0, gE0,
-                               gR0, part_logit, (float*)workspace, stream);
+    return long_bwd_impl<bf16>((int)B, (int)T, (int)H, lx, (const bf16*)w, (const bf16*)p, lg,
+                               ckpt, (const bf16*)gout, gLF, gEF, gRF, (bf16*)gw, (bf16*)gp, gL0,
+                               gE0, gR0, part_logit, (float*)workspace, stream);
   if (dtype == kF32)
-    return long_bwd_impl<float>((int)B, (int)T, (int)H, (const float*)w, (const float*)p, lg, ckpt,
-                                (const float*)gout, gLF, gEF, gRF, (float*)gw, (float*)gp, gL0,
-                                gE0, gR0, part_logit, (float*)workspace, stream);
+    return long_bwd_impl<float>((int)B, (int)T, (int)H, lx, (const float*)w, (const float*)p, lg,
+                                ckpt, (const float*)gout, gLF, gEF, gRF, (float*)gw, (float*)gp,
+                                gL0, gE0, gR0, part_logit, (float*)workspace, stream);
   DABSN_REQUIRE(false, "long scan backward: bad dtype %d", dtype);
   return DABSN_OK;
 }

@@ -1127,6 +1127,20 @@ def long_segments(T: int) -> int:
     return -(-int(T) // LONG_CKPT)
 
 
+def _long_inputs(write: Tensor, plasticity: Tensor) -> tuple[Tensor, Tensor, int]:
+    """(w, p, batch stride) for the long scan: [B, T, H] views with contiguous (T, H) blocks
+    and one batch stride (time windows of longer tapes) pass as they are, anything else as
+    contiguous copies."""
+    dt = write.dtype
+    w, p = write, plasticity.to(dt)
+    B, T, H = w.shape
+    ok = all(x.stride(2) == 1 and (T <= 1 or x.stride(1) == H) and x.stride(0) >= T * H
+             for x in (w, p)) and w.stride(0) == p.stride(0)
+    if not ok:
+        w, p = w.contiguous(), p.contiguous()
+    return w, p, (w.stride(0) if B > 1 else T * H)
+
+
 @torch.library.custom_op(_q("long_scan_fused"), mutates_args=(), device_types="cuda")
 def long_scan_fused(
     write: Tensor, plasticity: Tensor, logit_expect_retain: Tensor,
@@ -1138,23 +1152,32 @@ def long_scan_fused(
     replays from: the states (L, E, R) entering every 32-step chunk, [B, ceil(T/32), 3, H]
     fp32)."""
     _require_cuda(write)
+    return long_scan_window(write, plasticity, [logit_expect_retain, logit_retention_decay,
+                                                logit_retain, logit_retention_strength],
+                            long0, expected0, retention0)
+
+
+def long_scan_window(write: Tensor, plasticity: Tensor, logits: list[Tensor], long0: Tensor,
+                     expected0: Tensor, retention0: Tensor
+                     ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """long_scan_fused's results for inputs that may be time windows of longer [B, T', H]
+    tapes (read in place, ``dabsn_hip_long_fwd``'s input batch stride); the outputs are
+    contiguous."""
     lib = _lib.load()
     B, T, H = write.shape
     dt = write.dtype
-    w = write.contiguous()
-    p = plasticity.to(dt).contiguous()
-    logits = [_f32_scalar(x) for x in
-              (logit_expect_retain, logit_retention_decay, logit_retain, logit_retention_strength)]
+    w, p, ldx = _long_inputs(write, plasticity)
+    logits = [_f32_scalar(x) for x in logits]
     ptrs = _lib.PTR4(*[x.data_ptr() for x in logits])
     L0, E0, R0 = (x.float().contiguous() for x in (long0, expected0, retention0))
-    out = torch.empty_like(w)
+    out = torch.empty((B, T, H), device=w.device, dtype=dt)
     LF, EF, RF = (torch.empty((B, H), device=w.device, dtype=torch.float32) for _ in range(3))
     ckpt = torch.empty((B, long_segments(T), 3, H), device=w.device, dtype=torch.float32)
     nbytes = lib.dabsn_hip_long_workspace_bytes(B, T, H, 0)
     ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=w.device)
     tk = KernelTimer.begin("long_scan_fwd", w)
-    _lib.check(lib.dabsn_hip_long_fwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(L0), _p(E0),
-                                      _p(R0), _p(out), _p(LF), _p(EF), _p(RF), _p(ckpt),
+    _lib.check(lib.dabsn_hip_long_fwd(_code(dt), B, T, H, ldx, _p(w), _p(p), ptrs, _p(L0),
+                                      _p(E0), _p(R0), _p(out), _p(LF), _p(EF), _p(RF), _p(ckpt),
                                       _p(ws), nbytes, _stream(w)), "long scan")
     KernelTimer.end(tk)
     return out, LF, EF, RF, ckpt
@@ -1174,22 +1197,25 @@ def long_scan_backward_parts(
 ) -> tuple[Tensor, Tensor, Tensor, list[Tensor]]:
     """long_scan_fused_backward's results as (g_write, g_plasticity in the write dtype, the
     four logit gradients as one [4] fp32 tensor, [gL0, gE0, gR0]), for callers that need
-    no separate tensor per logit."""
+    no separate tensor per logit. write and plasticity may be time windows of longer tapes
+    (read in place, as ``long_scan_window``)."""
     _require_cuda(write)
     lib = _lib.load()
     B, T, H = write.shape
     dt = write.dtype
-    w = write.contiguous()
-    p = plasticity.to(dt).contiguous()
+    w, p, ldx = _long_inputs(write, plasticity)
     lg = [_f32_scalar(x) for x in logits]
     ptrs = _lib.PTR4(*[x.data_ptr() for x in lg])
     gout = grad_long.to(dt).contiguous()
     gf = [None if x is None else x.float().contiguous()
           for x in (g_long_final, g_expected_final, g_retention_final)]
-    gw, gp = torch.empty_like(w), torch.empty_like(p)
+    gw, gp = (torch.empty((B, T, H), device=w.device, dtype=dt) for _ in range(2))
     g0 = [torch.empty((B, H), device=w.device, dtype=torch.float32) for _ in range(3)]
     nparts = lib.dabsn_hip_long_partials(B, T, H)
-    part = torch.empty((max(nparts, 1), 4), device=w.device, dtype=torch.float32)
+    # Partials padded to whole groups of 64 rows (zeros), summed per group and then over
+    # the groups: a fixed order with 64 times the parallelism of one pass over the rows.
+    rows = -(-max(nparts, 1) // 64) * 64
+    part = torch.empty((rows, 4), device=w.device, dtype=torch.float32)
     part[nparts:].zero_()
     nbytes = lib.dabsn_hip_long_workspace_bytes(B, T, H, 1)
     ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=w.device)
@@ -1198,11 +1224,12 @@ def long_scan_backward_parts(
     if tuple(st.shape) != (B, long_segments(T), 3, H):
         raise ValueError(f"long scan backward: checkpoint shape {tuple(st.shape)}, expected "
                          f"{(B, long_segments(T), 3, H)}")
-    _lib.check(lib.dabsn_hip_long_bwd(_code(dt), B, T, H, _p(w), _p(p), ptrs, _p(st), _p(gout),
-                                      *[_p(x) for x in gf], _p(gw), _p(gp), *[_p(x) for x in g0],
-                                      _p(part), _p(ws), nbytes, _stream(w)), "long scan backward")
+    _lib.check(lib.dabsn_hip_long_bwd(_code(dt), B, T, H, ldx, _p(w), _p(p), ptrs, _p(st),
+                                      _p(gout), *[_p(x) for x in gf], _p(gw), _p(gp),
+                                      *[_p(x) for x in g0], _p(part), _p(ws), nbytes,
+                                      _stream(w)), "long scan backward")
     KernelTimer.end(tk)
-    return gw, gp, part.sum(0), g0
+    return gw, gp, part.view(-1, 64, 4).sum(1).sum(0), g0
 
 
 @torch.library.custom_op(_q("_long_scan_fused_backward"), mutates_args=(),

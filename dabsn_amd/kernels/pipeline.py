@@ -324,8 +324,8 @@ class _PipelinedScanRead(torch.autograd.Function):
 
                 # The long channel (long.py:492-579) window by window from the state the previous
                 # window ends in, differentiated by hand: per window its write and plasticity
-                # rows (contiguous copies), the checkpoint its backward replays from and its
-                # output, kept.
+                # rows (windows of the tapes, read in place), the checkpoint its backward
+                # replays from and its output, kept.
                 events.announce("recurrent_long_read", "rocm_chunk_parallel_scan", B=B, T=T, H=H,
                                 dtype="bf16" if code == 1 else "fp32")
                 longs = []
@@ -334,9 +334,8 @@ class _PipelinedScanRead(torch.autograd.Function):
                 def long_window(k: int) -> None:
                     nonlocal carried
                     t0, t1 = bounds[k]
-                    wk = ops.window_copy(w[:, t0:t1])
-                    pk = ops.window_copy(pl[:, t0:t1])
-                    lk, lf, ef, rf, ckpt = ops.direct.long_scan_fused(wk, pk, *logits, *carried)
+                    wk, pk = w[:, t0:t1], pl[:, t0:t1]
+                    lk, lf, ef, rf, ckpt = ops.long_scan_window(wk, pk, logits, *carried)
                     carried = (lf, ef, rf)
                     longs.append((wk, pk, ckpt, lk))
 
@@ -466,18 +465,17 @@ class _PipelinedScanRead(torch.autograd.Function):
                     torch.add(g_in[:, t0:t1], g_proj, out=dst)
 
         def projection_grads(k: int, u_stream=None) -> Tensor:
-            # out(cat[y, budget, retrieved]) over query chunk k: one product gives the
-            # gradients of all three inputs; the retrieved rows' gradient is returned. With
-            # u_stream, the retrieved third is its own product, after which the read's
-            # backward can start, and the [y, budget] part runs on u_stream.
+            # out(cat[y, budget, retrieved]) over query chunk k: the retrieved rows' gradient
+            # (returned, each row contiguous for the read's backward), then the [y, budget]
+            # rows' gradient into U's (on u_stream when given, after which the read's
+            # backward can start).
             t0, t1 = bounds[k]
             C = t1 - t0
             gs = gs_rows[B * t0:B * t1]
-            if u_stream is None:
-                prod = F.linear(gs, WdT)
-                fill_gU(prod, k)
-                return ops.window_copy(prod[:, 2 * H:].view(B, C, H))
             g_r = F.linear(gs, WdT[2 * H:]).view(B, C, H)
+            if u_stream is None:
+                fill_gU(F.linear(gs, WdT[:2 * H]), k)
+                return g_r
             ready = torch.cuda.Event()
             ready.record(torch.cuda.current_stream(dev))
             u_stream.wait_event(ready)

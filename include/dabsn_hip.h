@@ -177,23 +177,27 @@ int dabsn_hip_linrec_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void*
  * fp32 in, LF/EF/RF out. Both directions are chunked over time (chunks of DABSN_LONG_CKPT
  * steps) and need dabsn_hip_long_workspace_bytes() bytes of workspace. `ckpt` (may be NULL)
  * receives the checkpoint the backward replays each chunk from: the fp32 states entering
- * every chunk, [B][ceil(T / DABSN_LONG_CKPT)][3][H] = (L, E, R). */
+ * every chunk, [B][ceil(T / DABSN_LONG_CKPT)][3][H] = (L, E, R). `ldx`: elements between
+ * the batch rows of w and p (0: T H, contiguous; otherwise >= T H, e.g. a time window of
+ * longer [B, T', H] tapes read in place); out and every other tensor are contiguous. */
 #define DABSN_LONG_CKPT 32
 size_t dabsn_hip_long_workspace_bytes(int64_t B, int64_t T, int64_t H, int backward);
-int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
-                       const float* const* logits, const float* L0, const float* E0,
-                       const float* R0, void* out, float* LF, float* EF, float* RF, float* ckpt,
-                       void* workspace, size_t workspace_bytes, hipStream_t stream);
-/* Backward: gout [B,T,H], gLF/gEF/gRF (may be NULL), the forward's `ckpt`. Outputs gw, gp
- * [B,T,H], gL0, gE0, gR0 [B,H], and part_logit [nblocks][4] with nblocks =
- * dabsn_hip_long_partials(B, T, H): per-block partial sums of the gradient w.r.t. the four
- * logits. */
+int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldx, const void* w,
+                       const void* p, const float* const* logits, const float* L0,
+                       const float* E0, const float* R0, void* out, float* LF, float* EF,
+                       float* RF, float* ckpt, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+/* Backward: gout [B,T,H], gLF/gEF/gRF (may be NULL), the forward's `ckpt`, w and p with
+ * the forward's `ldx`. Outputs gw, gp [B,T,H] (contiguous), gL0, gE0, gR0 [B,H], and
+ * part_logit [nblocks][4] with nblocks = dabsn_hip_long_partials(B, T, H): per-block partial
+ * sums of the gradient w.r.t. the four logits. */
 int64_t dabsn_hip_long_partials(int64_t B, int64_t T, int64_t H);
-int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, const void* w, const void* p,
-                       const float* const* logits, const float* ckpt, const void* gout,
-                       const float* gLF, const float* gEF, const float* gRF, void* gw, void* gp,
-                       float* gL0, float* gE0, float* gR0, float* part_logit, void* workspace,
-                       size_t workspace_bytes, hipStream_t stream);
+int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldx, const void* w,
+                       const void* p, const float* const* logits, const float* ckpt,
+                       const void* gout, const float* gLF, const float* gEF, const float* gRF,
+                       void* gw, void* gp, float* gL0, float* gE0, float* gR0,
+                       float* part_logit, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
 
 /* ---- read glue ----------------------------------------------------------------------
  * Per-position statistics of the read (src/dabsn/read.py:58-72, 154-183): stats[B,T,6] =

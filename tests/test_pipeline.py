@@ -220,6 +220,35 @@ def test_read_output_windows_equal_the_whole_op(cuda_device, dtypes, B, T, H, bo
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,T,H,t0,t1", [(3, 100, 24, 37, 90), (2, 70, 5, 0, 33),
+                                         (1, 40, 8, 8, 40)])
+def test_long_scan_on_tape_windows_equals_contiguous_copies(cuda_device, dtype, B, T, H, t0, t1):
+    """``ops.long_scan_window`` and ``long_scan_backward_parts`` read time windows of longer
+    tapes in place (the batch stride passed to the library): the same outputs, final states,
+    checkpoint and gradients as on contiguous copies of the windows, bit for bit."""
+    from dabsn_amd.kernels import ops
+
+    g = torch.Generator().manual_seed(T + H + t0)
+    w = torch.randn(B, T, H, generator=g).to(cuda_device, dtype)
+    pl = torch.rand(B, T, H, generator=g).to(cuda_device, dtype)
+    logits = [torch.tensor([v], device=cuda_device) for v in (0.3, -0.2, 0.5, 0.1)]
+    state = [torch.randn(B, H, generator=g).to(cuda_device) for _ in range(3)]
+    wk, pk = w[:, t0:t1], pl[:, t0:t1]
+    a = ops.long_scan_window(wk, pk, logits, *state)
+    b = ops.long_scan_window(wk.contiguous(), pk.contiguous(), logits, *state)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    gl = torch.randn(B, t1 - t0, H, generator=g).to(cuda_device, dtype)
+    gf = [torch.randn(B, H, generator=g).to(cuda_device) for _ in range(3)]
+    ga = ops.long_scan_backward_parts(wk, pk, logits, a[4], gl, *gf)
+    gb = ops.long_scan_backward_parts(wk.contiguous(), pk.contiguous(), logits, a[4], gl, *gf)
+    for x, y in zip(ga[:3], gb[:3]):
+        assert torch.equal(x, y)
+    for x, y in zip(ga[3], gb[3]):
+        assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("H", [24, 5])
 def test_window_add_equals_torch(cuda_device, dtype, H):
     """``ops.window_add`` / ``window_copy`` on time windows and column blocks of strided
