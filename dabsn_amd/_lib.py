@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libdabsn_hip.so"
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 _lock = threading.Lock()
 _lib = None
@@ -91,8 +91,8 @@ _SIGNATURES = {
         [i32, i64, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp], i32),
     "dabsn_hip_long_partials": ([i64, i64, i64], i64),
     "dabsn_hip_long_bwd": (
-        [i32, i64, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
-         sz, vp],
+        [i32, i64, i64, i64, i64, vp, vp, PTR4, vp, vp, vp, vp, vp, vp, vp, i64, i32, vp, vp, vp,
+         vp, vp, sz, vp],
         i32,
     ),
     "dabsn_hip_tape_stats": ([i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp], i32),

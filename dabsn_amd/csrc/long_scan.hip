@@ -390,70 +390,111 @@ __global__ void __launch_bounds__(NT) long_bwd_carry(int B, int T, int H, const 
   gE0[ch] = x2;
 }
 
-// Final pass: replay the chunk forward from its checkpoint (the states entering every step
-// kept in registers), then walk it backward from the exact entering adjoints (maps
-// components 0..2); writes gw, gp and reduces the logit gradients per block (fixed order).
-template <typename E>
+// Final pass: walk the chunk backward from the exact entering adjoints (maps components
+// 0..2), in sub-blocks of SB steps from the last: each sub-block replays its forward steps
+// from its entering states (found by one replay of the chunk from its checkpoint) and keeps
+// them in registers for its backward walk, so a thread holds SB steps of states instead of
+// CK (the replays call `advance`, so every state equals the forward's bit for bit). Writes
+// gw, gp (batch rows ldo apart) and reduces the logit gradients per block (fixed order).
+// ACC: gw += the gradient rounded to E, the sum formed in fp32 and rounded once (an add of
+// the rounded gradient into an existing gradient buffer).
+constexpr int SB = 8;
+static_assert(CK % SB == 0, "whole sub-blocks per chunk");
+
+template <typename E, bool ACC>
 __global__ void __launch_bounds__(NT) long_bwd_final(int B, int T, int H, int64_t ldx,
-                                                     const E* w, const E* p, Logits lg,
-                                                     const float* ckpt, const E* gout,
-                                                     const float* maps, E* gw, E* gp,
-                                                     float* part) {
+                                                     int64_t ldo, const E* w, const E* p,
+                                                     Logits lg, const float* ckpt,
+                                                     const E* gout, const float* maps, E* gw,
+                                                     E* gp, float* part) {
+  constexpr int NSB = CK / SB;
   __shared__ float red[4][NT];
   ChunkIdx c;
   const bool ok = chunk_idx(B, T, H, ldx, c);
   const Coef k = load_coef(lg.p);
   float d_er = 0.f, d_rd = 0.f, d_ret = 0.f, d_rs = 0.f;
   if (ok) {
-    float wv[CK], pv[CK], gv[CK], Lv[CK], Ev[CK], Rv[CK];
+    const size_t obase = static_cast<size_t>(c.b) * ldo + c.h;
+    float wv[CK], pv[CK];
 #pragma unroll
     for (int i = 0; i < CK; ++i) {
       // Clamped, unconditional loads (steps past the chunk end are never used).
       const size_t t = static_cast<size_t>(c.t0 + min(i, c.len - 1)) * H;
       wv[i] = ld(w, c.ibase + t);
       pv[i] = ld(p, c.ibase + t);
-      gv[i] = ld(gout, c.base + t);
     }
-    float L = ckpt[c.cbase], Es = ckpt[c.cbase + H], R = ckpt[c.cbase + 2 * H];
+    float Ls[NSB], Es[NSB], Rs[NSB];
+    {
+      float L = ckpt[c.cbase], Ev = ckpt[c.cbase + H], R = ckpt[c.cbase + 2 * H];
 #pragma unroll
-    for (int i = 0; i < CK; ++i) {
-      Lv[i] = L;
-      Ev[i] = Es;
-      Rv[i] = R;
-      if (i < c.len) {
-        float pe, eff;
-        advance(k, wv[i], pv[i], L, Es, R, pe, eff);
+      for (int i = 0; i < CK; ++i) {
+        if (i % SB == 0) {
+          Ls[i / SB] = L;
+          Es[i / SB] = Ev;
+          Rs[i / SB] = R;
+        }
+        if (i < c.len) {
+          float pe, eff;
+          advance(k, wv[i], pv[i], L, Ev, R, pe, eff);
+        }
       }
     }
     const size_t stride = static_cast<size_t>(c.nseg) * B * H;
     const size_t li = static_cast<size_t>(c.k) * B * H + c.ch;
     float gLc = maps[li], gRc = maps[li + stride], gEc = maps[li + 2 * stride];
 #pragma unroll
-    for (int i = CK - 1; i >= 0; --i) {
-      if (i < c.len) {
-        const float wt = wv[i], pt = pv[i];
-        const float diff = wt - Ev[i];
-        const float pe = tanhf(fabsf(diff));
-        const float sal = pt * pe;
-        const float Rcur = k.rd * Rv[i] + (1.0f - k.rd) * (1.0f - pe);
-        const float eff = k.ret + (1.0f - k.ret) * k.rs * Rcur;
-        const float gL = gv[i] + gLc;
-        const float deff = gL * (Lv[i] - sal * wt);
-        const float dsal = gL * (1.0f - eff) * wt;
-        gLc = gL * eff;
-        const float dR = gRc + deff * (1.0f - k.ret) * k.rs;
-        gRc = dR * k.rd;
-        const float dpe = dsal * pt - dR * (1.0f - k.rd);
-        const float darg = dpe * (1.0f - pe * pe) * signf_(diff);
-        const float dE = gEc;
-        gEc = k.er * dE - darg;
-        const size_t o = c.base + static_cast<size_t>(c.t0 + i) * H;
-        st(gp, o, dsal * pe);
-        st(gw, o, gL * (1.0f - eff) * sal + darg + (1.0f - k.er) * dE);
-        d_er += dE * (Ev[i] - wt);
-        d_rd += dR * (Rv[i] - (1.0f - pe));
-        d_ret += deff * (1.0f - k.rs * Rcur);
-        d_rs += deff * (1.0f - k.ret) * Rcur;
+    for (int sb = NSB - 1; sb >= 0; --sb) {
+      float gv[SB], sv[ACC ? SB : 1], Lv[SB], Ev[SB], Rv[SB];
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const size_t t = static_cast<size_t>(c.t0 + min(sb * SB + j, c.len - 1)) * H;
+        gv[j] = ld(gout, c.base + t);
+        if constexpr (ACC) sv[j] = ld(gw, obase + t);
+      }
+      float L = Ls[sb], Es_ = Es[sb], R = Rs[sb];
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const int i = sb * SB + j;
+        Lv[j] = L;
+        Ev[j] = Es_;
+        Rv[j] = R;
+        if (i < c.len) {
+          float pe, eff;
+          advance(k, wv[i], pv[i], L, Es_, R, pe, eff);
+        }
+      }
+#pragma unroll
+      for (int j = SB - 1; j >= 0; --j) {
+        const int i = sb * SB + j;
+        if (i < c.len) {
+          const float wt = wv[i], pt = pv[i];
+          const float diff = wt - Ev[j];
+          const float pe = tanhf(fabsf(diff));
+          const float sal = pt * pe;
+          const float Rcur = k.rd * Rv[j] + (1.0f - k.rd) * (1.0f - pe);
+          const float eff = k.ret + (1.0f - k.ret) * k.rs * Rcur;
+          const float gL = gv[j] + gLc;
+          const float deff = gL * (Lv[j] - sal * wt);
+          const float dsal = gL * (1.0f - eff) * wt;
+          gLc = gL * eff;
+          const float dR = gRc + deff * (1.0f - k.ret) * k.rs;
+          gRc = dR * k.rd;
+          const float dpe = dsal * pt - dR * (1.0f - k.rd);
+          const float darg = dpe * (1.0f - pe * pe) * signf_(diff);
+          const float dE = gEc;
+          gEc = k.er * dE - darg;
+          const size_t o = obase + static_cast<size_t>(c.t0 + i) * H;
+          st(gp, o, dsal * pe);
+          const float gwv = gL * (1.0f - eff) * sal + darg + (1.0f - k.er) * dE;
+          if constexpr (ACC)
+            st(gw, o, sv[j] + round_to<E>(gwv));
+          else
+            st(gw, o, gwv);
+          d_er += dE * (Ev[j] - wt);
+          d_rd += dR * (Rv[j] - (1.0f - pe));
+          d_ret += deff * (1.0f - k.rs * Rcur);
+          d_rs += deff * (1.0f - k.ret) * Rcur;
+        }
       }
     }
   }
@@ -515,8 +556,8 @@ static int long_fwd_impl(int B, int T, int H, int64_t ldx, const E* w, const E* 
 template <typename E>
 static int long_bwd_impl(int B, int T, int H, int64_t ldx, const E* w, const E* p, Logits lg,
                          const float* ckpt, const E* gout, const float* gLF, const float* gEF,
-                         const float* gRF, E* gw, E* gp, float* gL0, float* gE0, float* gR0,
-                         float* part, float* ws, hipStream_t stream) {
+                         const float* gRF, E* gw, E* gp, int64_t ldo, bool acc, float* gL0,
+                         float* gE0, float* gR0, float* part, float* ws, hipStream_t stream) {
   const int gx = grid_for(B, H);
   const int nseg = (T + CK - 1) / CK;
   const dim3 cg(gx, nseg), blk(NT);
@@ -525,8 +566,9 @@ static int long_bwd_impl(int B, int T, int H, int64_t ldx, const E* w, const E* 
                        ws);
   hipLaunchKernelGGL(long_bwd_carry, dim3(gx), blk, 0, stream, B, T, H, gLF, gRF, gEF, ws, gL0,
                      gR0, gE0);
+  auto final_pass = acc ? long_bwd_final<E, true> : long_bwd_final<E, false>;
   if (nseg > 0)
-    hipLaunchKernelGGL(long_bwd_final<E>, cg, blk, 0, stream, B, T, H, ldx, w, p, lg, ckpt, gout,
+    hipLaunchKernelGGL(final_pass, cg, blk, 0, stream, B, T, H, ldx, ldo, w, p, lg, ckpt, gout,
                        ws, gw, gp, part);
   DABSN_HIP_CHECK(hipGetLastError());
   return DABSN_OK;
@@ -587,9 +629,9 @@ size_t dabsn_hip_long_workspace_bytes(int64_t B, int64_t T, int64_t H, int backw
   return static_cast<size_t>(backward ? 9 : 5) * static_cast<size_t>(nseg) * B * H * sizeof(float);
 }
 
-// Batch stride of the inputs w, p: ldx elements (0: T H, the contiguous layout); at least
-// T H, so a time window of longer [B, T', H] tapes can be passed in place.
-static int64_t input_stride(int64_t B, int64_t T, int64_t H, int64_t ldx) {
+// Batch stride of [B, T, H] operands: ldx elements (0: T H, the contiguous layout); at least
+// T H, so a time window of longer [B, T', H] tapes can be passed in place; -1 if invalid.
+static int64_t batch_stride(int64_t B, int64_t T, int64_t H, int64_t ldx) {
   if (ldx == 0) return T * H;
   if (ldx < T * H || (B - 1) * ldx + T * H >= (1ll << 46)) return -1;
   return ldx;
@@ -601,7 +643,7 @@ int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldx, 
                        float* RF, float* ckpt, void* workspace, size_t workspace_bytes,
                        hipStream_t stream) {
   DABSN_SHAPE_CHECK(B, T, H);
-  const int64_t lx = input_stride(B, T, H, ldx);
+  const int64_t lx = batch_stride(B, T, H, ldx);
   DABSN_REQUIRE(lx >= 0, "long scan: bad input batch stride %lld for T=%lld H=%lld",
                 (long long)ldx, (long long)T, (long long)H);
   DABSN_REQUIRE(w && p && logits && L0 && E0 && R0 && (out || T == 0) && LF && EF && RF &&
@@ -632,13 +674,14 @@ int64_t dabsn_hip_long_partials(int64_t B, int64_t T, int64_t H) {
 int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldx, const void* w,
                        const void* p, const float* const* logits, const float* ckpt,
                        const void* gout, const float* gLF, const float* gEF, const float* gRF,
-                       void* gw, void* gp, float* gL0, float* gE0, float* gR0,
-                       float* part_logit, void* workspace, size_t workspace_bytes,
-                       hipStream_t stream) {
+                       void* gw, void* gp, int64_t ldo, int gw_accumulate, float* gL0,
+                       float* gE0, float* gR0, float* part_logit, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
   DABSN_SHAPE_CHECK(B, T, H);
-  const int64_t lx = input_stride(B, T, H, ldx);
-  DABSN_REQUIRE(lx >= 0, "long scan backward: bad input batch stride %lld for T=%lld H=%lld",
-                (long long)ldx, (long long)T, (long long)H);
+  const int64_t lx = batch_stride(B, T, H, ldx), lo = batch_stride(B, T, H, ldo);
+  DABSN_REQUIRE(lx >= 0 && lo >= 0,
+                "long scan backward: bad batch stride (inputs %lld, outputs %lld) for T=%lld "
+                "H=%lld", (long long)ldx, (long long)ldo, (long long)T, (long long)H);
   DABSN_REQUIRE(w && p && logits && (ckpt || T == 0) && (gout || T == 0) && gL0 && gE0 && gR0 &&
                     (part_logit || T == 0) && (workspace || T == 0) && ((gw && gp) || T == 0),
                 "long scan backward: null pointer");
@@ -650,12 +693,14 @@ int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldx, 
   Logits lg{{logits[0], logits[1], logits[2], logits[3]}};
   if (dtype == kBF16)
     return long_bwd_impl<bf16>((int)B, (int)T, (int)H, lx, (const bf16*)w, (const bf16*)p, lg,
-                               ckpt, (const bf16*)gout, gLF, gEF, gRF, (bf16*)gw, (bf16*)gp, gL0,
-                               gE0, gR0, part_logit, (float*)workspace, stream);
+                               ckpt, (const bf16*)gout, gLF, gEF, gRF, (bf16*)gw, (bf16*)gp, lo,
+                               gw_accumulate != 0, gL0, gE0, gR0, part_logit, (float*)workspace,
+                               stream);
   if (dtype == kF32)
     return long_bwd_impl<float>((int)B, (int)T, (int)H, lx, (const float*)w, (const float*)p, lg,
                                 ckpt, (const float*)gout, gLF, gEF, gRF, (float*)gw, (float*)gp,
-                                gL0, gE0, gR0, part_logit, (float*)workspace, stream);
+                                lo, gw_accumulate != 0, gL0, gE0, gR0, part_logit,
+                                (float*)workspace, stream);
   DABSN_REQUIRE(false, "long scan backward: bad dtype %d", dtype);
   return DABSN_OK;
 }

@@ -1193,12 +1193,18 @@ def _long_scan_fused_fake(write, plasticity, l1, l2, l3, l4, long0, expected0, r
 def long_scan_backward_parts(
     write: Tensor, plasticity: Tensor, logits: list[Tensor], checkpoint: Tensor,
     grad_long: Tensor, g_long_final: Optional[Tensor], g_expected_final: Optional[Tensor],
-    g_retention_final: Optional[Tensor],
+    g_retention_final: Optional[Tensor], gw_into: Optional[Tensor] = None,
+    gp_into: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor, list[Tensor]]:
     """long_scan_fused_backward's results as (g_write, g_plasticity in the write dtype, the
     four logit gradients as one [4] fp32 tensor, [gL0, gE0, gR0]), for callers that need
     no separate tensor per logit. write and plasticity may be time windows of longer tapes
-    (read in place, as ``long_scan_window``)."""
+    (read in place, as ``long_scan_window``). ``gw_into`` / ``gp_into`` (together, [B, T, H]
+    views in the write dtype with contiguous (T, H) blocks and one batch stride, e.g. time
+    windows of full-length gradient buffers): the write gradient is added into ``gw_into``
+    (rounded to the dtype, the sum formed in fp32 and rounded once, as a tensor add) and the
+    plasticity gradient written into ``gp_into``; they are returned in place of new
+    tensors."""
     _require_cuda(write)
     lib = _lib.load()
     B, T, H = write.shape
@@ -1209,13 +1215,22 @@ def long_scan_backward_parts(
     gout = grad_long.to(dt).contiguous()
     gf = [None if x is None else x.float().contiguous()
           for x in (g_long_final, g_expected_final, g_retention_final)]
-    gw, gp = (torch.empty((B, T, H), device=w.device, dtype=dt) for _ in range(2))
+    if (gw_into is None) != (gp_into is None):
+        raise ValueError("long scan backward: gw_into and gp_into go together")
+    if gw_into is None:
+        gw, gp = (torch.empty((B, T, H), device=w.device, dtype=dt) for _ in range(2))
+        ldo, acc = T * H, 0
+    else:
+        gw, gp = gw_into, gp_into
+        if any(tuple(x.shape) != (B, T, H) or x.dtype != dt or x.stride(2) != 1
+               or (T > 1 and x.stride(1) != H) or x.stride(0) < T * H for x in (gw, gp)) \
+                or gw.stride(0) != gp.stride(0):
+            raise ValueError("long scan backward: gw_into / gp_into must be [B, T, H] views of "
+                             "the write dtype with contiguous (T, H) blocks and one batch stride")
+        ldo, acc = (gw.stride(0) if B > 1 else T * H), 1
     g0 = [torch.empty((B, H), device=w.device, dtype=torch.float32) for _ in range(3)]
     nparts = lib.dabsn_hip_long_partials(B, T, H)
-    # Partials padded to whole groups of 64 rows (zeros), summed per group and then over
-    # the groups: a fixed order with 64 times the parallelism of one pass over the rows.
-    rows = -(-max(nparts, 1) // 64) * 64
-    part = torch.empty((rows, 4), device=w.device, dtype=torch.float32)
+    part = torch.empty((max(nparts, 1), 4), device=w.device, dtype=torch.float32)
     part[nparts:].zero_()
     nbytes = lib.dabsn_hip_long_workspace_bytes(B, T, H, 1)
     ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=w.device)
@@ -1225,11 +1240,13 @@ def long_scan_backward_parts(
         raise ValueError(f"long scan backward: checkpoint shape {tuple(st.shape)}, expected "
                          f"{(B, long_segments(T), 3, H)}")
     _lib.check(lib.dabsn_hip_long_bwd(_code(dt), B, T, H, ldx, _p(w), _p(p), ptrs, _p(st),
-                                      _p(gout), *[_p(x) for x in gf], _p(gw), _p(gp),
+                                      _p(gout), *[_p(x) for x in gf], _p(gw), _p(gp), ldo, acc,
                                       *[_p(x) for x in g0], _p(part), _p(ws), nbytes,
                                       _stream(w)), "long scan backward")
     KernelTimer.end(tk)
-    return gw, gp, part.view(-1, 64, 4).sum(1).sum(0), g0
+    # The partials as four contiguous rows: a reduction along rows spreads each sum over many
+    # threads (summing down the columns in place runs serially).
+    return gw, gp, part.t().contiguous().sum(1), g0
 
 
 @torch.library.custom_op(_q("_long_scan_fused_backward"), mutates_args=(),
@@ -1652,7 +1669,9 @@ def _read_common(query, bank_keys, bank_writes, next_writes, cocktail, bank_cock
     sc = scale.float().reshape(()).contiguous()
     g = [_f32_scalar(x) for x in gains]
     idx = bank_idx.to(torch.int64).contiguous()
-    valid = bank_valid.to(torch.uint8).contiguous()
+    # A bool mask is already one 0/1 byte per slot: reinterpreted, not converted.
+    valid = (bank_valid.view(torch.uint8) if bank_valid.dtype == torch.bool
+             else bank_valid.to(torch.uint8)).contiguous()
     if cocktail.shape[-1] != 4 or bank_cocktail.shape[-1] != 4:
         raise ValueError("the HIP read expects a 4-component cocktail")
     return dt, q, K, V, Vn, ck, cb, kb, adm, sc, g, idx, valid

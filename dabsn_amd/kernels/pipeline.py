@@ -510,31 +510,23 @@ class _PipelinedScanRead(torch.autograd.Function):
                 out_done[k] = True
 
         logit_leaves = [param_leaves[n] for n in _LONG_LOGITS]
-        long_grads: list = [None] * K     # per window: (g_write, g_plasticity)
         logit_sum: list = [None]          # the four logits' gradients, summed window by window
         state_grad: list = [None, None, None]
 
         def long_backward(k: int) -> None:
             # Window k of the long channel: its rows' gradient plus the gradient of the state
             # it ends in (from window k + 1's backward); leaves the gradient of the state it
-            # starts from for window k - 1.
+            # starts from for window k - 1. The write gradient is added into the sink's rows
+            # (the gather backward of every query chunk >= k adds into them too) and the
+            # plasticity gradient written into g_p's (the statistics backward then adds to
+            # it), both in place.
             wk, pk, ckpt, _ = longs[k]
             t0, t1 = bounds[k]
-            gw, gp, part, g0 = ops.long_scan_backward_parts(
+            _, _, part, g0 = ops.long_scan_backward_parts(
                 wk, pk, logit_leaves, ckpt, gl_rows[B * t0:B * t1].view(B, t1 - t0, H),
-                *state_grad)
-            long_grads[k] = (gw, gp)
+                *state_grad, gw_into=sink[:, t0:t1], gp_into=g_p[:, t0:t1])
             logit_sum[0] = part if logit_sum[0] is None else logit_sum[0] + part
             state_grad[:] = g0
-
-        def long_shares(k: int) -> None:
-            # Window k's long-channel gradients join the write-gradient sink (the gather
-            # backward of every query chunk >= k adds into those rows too) and the
-            # plasticity gradient (which the statistics backward then adds to).
-            t0, t1 = bounds[k]
-            gwk, gpk = long_grads[k]
-            ops.window_add(sink[:, t0:t1], sink[:, t0:t1], gwk)
-            ops.window_add(g_p[:, t0:t1], gpk)
 
         try:
             with torch.cuda.stream(M):
@@ -549,11 +541,10 @@ class _PipelinedScanRead(torch.autograd.Function):
                 head.record(M)
                 R.wait_event(head)
                 with torch.cuda.stream(R):
+                    # With its shares of the last window's write and plasticity gradients,
+                    # ahead of the last chunk's gather backward (which waits for them) and
+                    # statistics backward, off the path to the last reverse scan.
                     long_backward(K - 1)
-                    # Its shares of the last window's write and plasticity gradients, ahead of
-                    # the last chunk's gather backward (which waits for them) and statistics
-                    # backward, off the path to the last reverse scan.
-                    long_shares(K - 1)
                     last_shares = torch.cuda.Event()
                     last_shares.record(R)
                 sink_wait[0] = last_shares
@@ -587,7 +578,6 @@ class _PipelinedScanRead(torch.autograd.Function):
                     with torch.cuda.stream(R):
                         if k < K - 1:
                             long_backward(k)
-                            long_shares(k)
                         if k == K - 1:
                             # Later chunks of the read half add theirs to the last chunk's.
                             stats_leaf.grad = stats_last.grad

@@ -17,7 +17,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#define DABSN_HIP_ABI_VERSION 17
+#define DABSN_HIP_ABI_VERSION 18
 
 /* Status codes returned by every entry point. */
 #define DABSN_OK 0
@@ -187,17 +187,20 @@ int dabsn_hip_long_fwd(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldx, 
                        const float* E0, const float* R0, void* out, float* LF, float* EF,
                        float* RF, float* ckpt, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
-/* Backward: gout [B,T,H], gLF/gEF/gRF (may be NULL), the forward's `ckpt`, w and p with
- * the forward's `ldx`. Outputs gw, gp [B,T,H] (contiguous), gL0, gE0, gR0 [B,H], and
- * part_logit [nblocks][4] with nblocks = dabsn_hip_long_partials(B, T, H): per-block partial
- * sums of the gradient w.r.t. the four logits. */
+/* Backward: gout [B,T,H] (contiguous), gLF/gEF/gRF (may be NULL), the forward's `ckpt`, w
+ * and p with the forward's `ldx`. Outputs gw, gp [B,T,H] with batch stride `ldo` (0: T H;
+ * e.g. time windows of full-length gradient buffers written in place), gL0, gE0, gR0 [B,H],
+ * and part_logit [nblocks][4] with nblocks = dabsn_hip_long_partials(B, T, H): per-block
+ * partial sums of the gradient w.r.t. the four logits. gw_accumulate != 0: gw receives
+ * gw + (the gradient rounded to dtype), summed in fp32 and rounded once -- an add into an
+ * existing gradient buffer. */
 int64_t dabsn_hip_long_partials(int64_t B, int64_t T, int64_t H);
 int dabsn_hip_long_bwd(int dtype, int64_t B, int64_t T, int64_t H, int64_t ldx, const void* w,
                        const void* p, const float* const* logits, const float* ckpt,
                        const void* gout, const float* gLF, const float* gEF, const float* gRF,
-                       void* gw, void* gp, float* gL0, float* gE0, float* gR0,
-                       float* part_logit, void* workspace, size_t workspace_bytes,
-                       hipStream_t stream);
+                       void* gw, void* gp, int64_t ldo, int gw_accumulate, float* gL0,
+                       float* gE0, float* gR0, float* part_logit, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
 
 /* ---- read glue ----------------------------------------------------------------------
  * Per-position statistics of the read (src/dabsn/read.py:58-72, 154-183): stats[B,T,6] =

@@ -225,7 +225,10 @@ def test_read_output_windows_equal_the_whole_op(cuda_device, dtypes, B, T, H, bo
 def test_long_scan_on_tape_windows_equals_contiguous_copies(cuda_device, dtype, B, T, H, t0, t1):
     """``ops.long_scan_window`` and ``long_scan_backward_parts`` read time windows of longer
     tapes in place (the batch stride passed to the library): the same outputs, final states,
-    checkpoint and gradients as on contiguous copies of the windows, bit for bit."""
+    checkpoint and gradients as on contiguous copies of the windows, bit for bit; and with
+    ``gw_into`` / ``gp_into`` windows of full-length buffers, the write gradient added into
+    its window as ``window_add`` adds it and the plasticity gradient written into its own,
+    bit for bit, the rows outside the windows untouched."""
     from dabsn_amd.kernels import ops
 
     g = torch.Generator().manual_seed(T + H + t0)
@@ -246,6 +249,15 @@ def test_long_scan_on_tape_windows_equals_contiguous_copies(cuda_device, dtype, 
         assert torch.equal(x, y)
     for x, y in zip(ga[3], gb[3]):
         assert torch.equal(x, y)
+    sink = torch.randn(B, T, H, generator=g).to(cuda_device, dtype)
+    gpb = torch.randn(B, T, H, generator=g).to(cuda_device, dtype)
+    want_sink, want_gp = sink.clone(), gpb.clone()
+    ops.window_add(want_sink[:, t0:t1], want_sink[:, t0:t1], ga[0])
+    want_gp[:, t0:t1] = ga[1]
+    gc = ops.long_scan_backward_parts(wk, pk, logits, a[4], gl, *gf, gw_into=sink[:, t0:t1],
+                                      gp_into=gpb[:, t0:t1])
+    assert torch.equal(sink, want_sink) and torch.equal(gpb, want_gp)
+    assert torch.equal(gc[2], ga[2])
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
