@@ -188,6 +188,37 @@ def _stats_bwd_window(gstats: Tensor, outs: Sequence[Optional[Tensor]], accumula
         stream), "tape statistics backward")
 
 
+def windows(T: int, chunk: int) -> list[tuple[int, int]]:
+    """The pipeline's time windows for a block chunked every ``chunk`` steps: one window more
+    than the chunks, of lengths in multiples of 128 that do not grow toward the end (the
+    scan and read results do not depend on where the windows fall). The read of window k
+    runs beside the scan of window k + 1 and costs more per query the later the window (the
+    bank grows), while the last window's read and its backward run alone: shorter late
+    windows shrink that exposed part, the extra window's fixed costs bound how short they
+    get. Lengths: the 256-multiple below T / n for every window, the remainder added in
+    128-step units from the front. At B=16, T=4096, H=2048, chunk 1024 (windows 896, 896,
+    768, 768, 768) this measured 0.4-0.5 ms per step faster than 4 x 1024 and than the other
+    five- and six-window schedules tried. Fewer than 256 steps per window: the chunks as
+    they are."""
+    n = -(-T // chunk) + 1
+    base = (T // n) // 256 * 256
+    if chunk >= T or base < 256:
+        return chunked._chunks(T, chunk)
+    lens = [base] * n
+    extra = T - n * base
+    i = 0
+    while extra >= 128:
+        lens[i % n] += 128
+        extra -= 128
+        i += 1
+    lens[0] += extra
+    out, t = [], 0
+    for length in lens:
+        out.append((t, t + length))
+        t += length
+    return out
+
+
 def _check_scans(S, calls, what: str) -> None:
     """The scans' error words, read on the scan stream once everything is enqueued: a
     checking read then waits for the scans only (not for the read half's work), and none
@@ -237,7 +268,7 @@ class _PipelinedScanRead(torch.autograd.Function):
         like = Wx.new_empty((1, 1, 1))
         read_out = torch.empty((B, T, H), device=dev,  # short + long_gain * long
                                dtype=ops._read_output_dtypes(like, like, gain)[1])
-        bounds = chunked._chunks(T, chunk)
+        bounds = windows(T, chunk)
         K = len(bounds)
         for st in (M, S, R):
             st.wait_stream(ambient)
