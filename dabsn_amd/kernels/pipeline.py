@@ -645,26 +645,38 @@ class _PipelinedScanRead(torch.autograd.Function):
                     gw[:, 2 * H:] = gs_rows.t() @ retr_rows
                     W.grad = gw
                     bias.grad = torch.sum(gs_rows, dim=0, dtype=torch.float32).to(bias.dtype)
+                    # The read's parameter gradients are final here (every chunk's read
+                    # backward has run, the last chunk's on the whole-device stream, which
+                    # this stream waited for): the two leaf sets summed, the read output's
+                    # gain and the long channel's logits, beside the last reverse scan
+                    # rather than after it.
+                    if gain_leaf.requires_grad:
+                        gain_leaf.grad = gain_parts.sum().reshape(gain_leaf.shape).to(
+                            gain_leaf.dtype)
+                    for i, leaf in enumerate(logit_leaves):
+                        if leaf.requires_grad:
+                            leaf.grad = logit_sum[0][i].reshape(leaf.shape).to(leaf.dtype)
+                    for n, leaf in last_leaves.items():
+                        if leaf.grad is not None:
+                            mine = param_leaves[n]
+                            mine.grad = leaf.grad if mine.grad is None else mine.grad + leaf.grad
                     if K > 1:
                         R.wait_event(scan_back[1])
                         core_weight_grads(1)
+                    # The scans' parameter partials of windows 1.. summed ahead of window 0's.
+                    vec_rest = torch.stack(vec_parts).sum(0) if vec_parts else None
+                    scal_rest = torch.stack(scal_parts).sum(0) if scal_parts else None
                 M.wait_stream(S)
                 M.wait_stream(R)
+                vec_parts.clear()
+                scal_parts.clear()
                 core_weight_grads(0)
-                if gain_leaf.requires_grad:
-                    gain_leaf.grad = gain_parts.sum().reshape(gain_leaf.shape).to(gain_leaf.dtype)
-                for i, leaf in enumerate(logit_leaves):
-                    if leaf.requires_grad:
-                        leaf.grad = logit_sum[0][i].reshape(leaf.shape).to(leaf.dtype)
-                gvec = torch.stack(vec_parts).sum(0)
-                gscal = torch.stack(scal_parts).sum(0)
+                gvec, gscal = vec_parts[0], scal_parts[0]
+                if vec_rest is not None:
+                    gvec, gscal = gvec + vec_rest, gscal + scal_rest
                 core = [gWx, gWgx, gUA_sum[:H], gUA_sum[H:], *[gvec[i] for i in range(16)],
                         *[gscal[i] for i in range(3)]]
                 core = [g.reshape(shape).to(dtype) for g, (dtype, shape) in zip(core, ctx.meta)]
-                for n, leaf in last_leaves.items():
-                    if leaf.grad is not None:
-                        mine = param_leaves[n]
-                        mine.grad = leaf.grad if mine.grad is None else mine.grad + leaf.grad
                 grads = [p.grad for p in pleaves]
             _check_scans(S, bws, "core scan backward")
         finally:

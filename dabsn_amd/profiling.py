@@ -260,13 +260,13 @@ def _short(name: str) -> str:
 
 
 def step_traffic(fetch_dir: str, write_dir: str, copy_fetch_dir: str, copy_write_dir: str,
-                 copy_mib: int, trace_db: str, match: str) -> str:
+                 copy_mib: int, trace_db: str, match: str, scans_per_step: int) -> str:
     """Markdown tables of the HBM traffic of the last traced step: FETCH_SIZE and
     WRITE_SIZE per dispatch (copy-calibrated) from two counter runs of the bench, durations
     from a kernel-trace run of the same bench (dispatches of the step paired with trace
     records by kernel name and order). The step starts at its first forward-scan
-    dispatch (4 per step); the whole-device stream is the queue of the step's last
-    statistics kernel."""
+    dispatch (``scans_per_step`` per step); the whole-device stream is the queue of the
+    step's last statistics kernel."""
     import sqlite3
 
     nbytes = copy_mib * 1024 * 1024
@@ -275,14 +275,14 @@ def step_traffic(fetch_dir: str, write_dir: str, copy_fetch_dir: str, copy_write
     fe, wr = _dispatch_counters(fetch_dir), _dispatch_counters(write_dir)
     ids = sorted(fe)
     fwd = [i for i in ids if "core_fwd_kernel" in str(fe[i]["kernel"])]
-    step = [i for i in ids if i >= fwd[-4]]
+    step = [i for i in ids if i >= fwd[-scans_per_step]]
     rx = re.compile(match)
     con = sqlite3.connect(trace_db)
     rows = [r for r in con.execute("select name, start, end from kernels order by start")
             if rx.search(r[0])]
     tf = [k for k, r in enumerate(rows) if "core_fwd_kernel" in r[0]]
     durations: dict[str, list[float]] = defaultdict(list)
-    for name, start, end in rows[tf[-4]:]:
+    for name, start, end in rows[tf[-scans_per_step]:]:
         durations[_short(name)].append((end - start) / 1e3)
     seen: dict[str, int] = defaultdict(int)
     recs = []
@@ -348,9 +348,12 @@ def main() -> None:
     p.add_argument("--dtype", default="bf16")
     args = p.parse_args()
     if args.step_traffic:
+        from dabsn_amd.kernels.pipeline import windows
+
         print(step_traffic(args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_mib,
                            args.step_traffic,
-                           args.match or "read3|glue|longmem|xpose|gemm_kernel|read_out|core_"))
+                           args.match or "read3|glue|longmem|xpose|gemm_kernel|read_out|core_",
+                           len(windows(args.seq, args.chunk))))
     elif args.pmc_json:
         doc = pmc_json(args.pmc_json, args.fetch, args.write, args.copy_fetch, args.copy_write,
                        args.copy_mib, {"batch": args.batch, "seq_len": args.seq,
