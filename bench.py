@@ -535,7 +535,10 @@ def main():
     }
     weights_bytes = 2 * H * H * el
     if dom in per_token:
-        launch_tokens = args.batch * chunk
+        # The launches of one step cover the sequence once (the pipeline's windows, or the
+        # block's chunks): the average launch scans tokens / launches-per-step tokens.
+        launches = kernels[dom]["calls"] / args.steps
+        launch_tokens = int(round(tokens / launches))
         alg_bytes = per_token[dom] * launch_tokens + weights_bytes
         achieved = alg_bytes / (kernels[dom]["avg_ms"] / 1e3) / 1e9
         traffic, traffic_src = measured_traffic(dom, args, chunk)
