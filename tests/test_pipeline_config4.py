@@ -6,8 +6,8 @@ bf16 autocast over fp32 parameters, the initialised read whose bank admits every
 Checks:
   * trajectory: y and budget bit-identical to ``chunked_core_scan`` on the same inputs, whose
     windows are checked against the oracle here too (2e-2, the bf16 bar);
-  * read output: query windows inside every chunk and across each chunk boundary, rows 0 and
-    15, against the oracle's composition on the same tapes -- the product's statistics,
+  * read output: query windows inside every chunk and across each chunk boundary and each
+    boundary of the pipeline's own windows (``pipeline.windows``), rows 0 and 15, against the oracle's composition on the same tapes -- the product's statistics,
     selection and gather checked against the oracle (1e-5, bit-exact, bit-exact), the
     oracle's three-way read of the window, the oracle's long channel of the row, and the
     output projection in fp64: 2e-2 normwise;
@@ -118,10 +118,18 @@ def test_pipeline_trajectory_equals_chunked_scan(c4p, piped, tapes):
     assert torch.equal(piped["y"], tapes[0][..., :H])
     counts = _dense_counts(c4p, tapes)
     assert int(counts.min()) == C4.seq, "the initialised read admits every position"
+    wins = [(1016, 1032), (3064, 3080)] + [(b - 8, b + 8) for _, b in _pipeline_windows()[:-1]]
     worst = cc.check_core_windows(c4p["model"].core, c4p["Wx"].detach(), c4p["Wgx"].detach(),
-                                  tapes, rows=(0, 15), windows=[(1016, 1032), (3064, 3080)],
-                                  tol=TOL)
+                                  tapes, rows=(0, 15), windows=wins, tol=TOL)
     print(f"config4 pipeline trajectory: bit-identical; core windows {worst:.2e}")
+
+
+def _pipeline_windows():
+    from dabsn_amd.kernels.pipeline import windows
+
+    w = windows(C4.seq, C4.chunk)
+    assert len(w) > C4.seq // C4.chunk, "the pipeline's windows differ from the chunks here"
+    return w
 
 
 def _pieces(c4p, tapes):
@@ -141,7 +149,8 @@ def _dense_counts(c4p, tapes):
 
 
 def test_pipeline_read_output_windows_vs_oracle(c4p, piped, tapes):
-    """Rows 0 and 15, windows inside each of the four chunks and across each boundary."""
+    """Rows 0 and 15, windows inside each of the four chunks and across each boundary of the
+    chunks and of the pipeline's windows."""
     read = c4p["model"].read
     P, t = _pieces(c4p, tapes)
     y, budget, ay, w, nov, pl, en, sat = t
@@ -157,6 +166,7 @@ def test_pipeline_read_output_windows_vs_oracle(c4p, piped, tapes):
         read.logit_retention_strength)], np.float32)
     windows = [(0, 32), (500, 532), (1008, 1040), (1500, 1532), (2032, 2064), (2500, 2532),
                (3056, 3088), (3500, 3532), (4064, 4096)]
+    windows += [(b - 16, b + 16) for _, b in _pipeline_windows()[:-1]]
     H = C4.state
     worst = 0.0
     for r in rows:
