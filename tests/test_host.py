@@ -240,3 +240,28 @@ def test_width_read_work_runs_once_at_the_latest_at_the_block_end():
         with read.during_width_read(lambda: calls.append("not run")):
             raise RuntimeError("inside the block")
     assert calls == ["body", "work"] and read._width_wait_work is None
+
+
+def test_pipeline_windows_cover_the_sequence():
+    """The pipeline's time windows (kernels/pipeline.py ``windows``) tile [0, T) in order,
+    one more than the block's chunks when each gets at least 256 steps, with lengths that
+    are 128-step multiples past the first window and never grow toward the end; shorter
+    sequences keep the chunks as they are (the reference's block chunking, model.py:274-307)."""
+    from dabsn_amd.kernels import chunked, pipeline
+
+    assert pipeline.windows(4096, 1024) == [(0, 896), (896, 1792), (1792, 2560),
+                                            (2560, 3328), (3328, 4096)]
+    for T in (64, 300, 512, 1000, 1024, 1536, 2048, 2049, 3000, 4096, 5000, 8192, 16384):
+        for chunk in (128, 256, 512, 1000, 1024, 2048, 4096):
+            w = pipeline.windows(T, chunk)
+            assert w[0][0] == 0 and w[-1][1] == T
+            assert all(a[1] == b[0] for a, b in zip(w, w[1:]))
+            lens = [b - a for a, b in w]
+            assert min(lens) > 0
+            n = -(-T // chunk) + 1
+            if chunk >= T or (T // n) < 256:
+                assert w == chunked._chunks(T, chunk)
+                continue
+            assert len(w) == n
+            assert all(x % 128 == 0 and x >= 256 for x in lens[1:])
+            assert all(a >= b for a, b in zip(lens, lens[1:]))
