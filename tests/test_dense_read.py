@@ -11,11 +11,12 @@ Checkers, none of them the HIP path:
 
 Tolerances: fp32 outputs and tensor gradients normwise 1e-5 against the C++ (fp32 on
 both sides, different summation orders); scalar gradients (sums over every (query, slot)
-term) 1e-4 relative to a floor of 1e-3 x the largest scalar gradient; against fp64, the
-same. Semantics the C++ does not share: an eligible row with no allowed slot gives NaN
-weights in the reference's registered Python op (softmax over all -inf), which is what
-runs on a device in the reference; the C++ CPU kernel returns zeros for such a row. The
-HIP op follows the registered op and is checked against the fp64 restatement there.
+term) 5e-5 relative to a floor of 1e-3 x the largest scalar gradient (worst seen on the
+GPU 2.4e-5, the cocktail gain at B=1, T=96, N=1000); against fp64, the same. Semantics
+the C++ does not share: an eligible row with no allowed slot gives NaN weights in the
+reference's registered Python op (softmax over all -inf), which is what runs on a device
+in the reference; the C++ CPU kernel returns zeros for such a row. The HIP op follows the
+registered op and is checked against the fp64 restatement there.
 bf16 inputs compute in fp32 (the reference's compute dtype), so they must equal the fp32
 op on the same values, rounded to bf16, bit for bit.
 """
@@ -106,7 +107,7 @@ def _check_grads(got, want, tol, label):
         assert a.shape == b.shape, f"{label} {name}: shape {a.shape} != {b.shape}"
         if i in SCALARS:
             err = float(np.abs(a - b).max()) / max(float(np.abs(b).max()), scalar_floor)
-            assert err <= 1e-4, f"{label} g_{name}: {err:.3e}"
+            assert err <= 5e-5, f"{label} g_{name}: {err:.3e}"
         else:
             assert rel_err(a, b) <= tol, f"{label} g_{name}: {rel_err(a, b):.3e} > {tol}"
 

@@ -2,10 +2,12 @@
 
 Tolerances (stated per north star):
   * fp32 tensors: normwise relative error max|hip - oracle| / max|oracle| <= 1e-5.
-  * fp32 scalar gradients that reduce O(B*T*N) signed terms (core: logit_alpha,
-    log_lambda, logit_c_suppress; read: scale and the four gains): relative 1e-4, the
-    size of the oracle's own fp32 summation error for these sums (the oracle pins use the
-    same bound against fp64 autograd).
+  * fp32 scalar gradients that reduce O(B*T*N) signed terms in another order than the
+    oracle: the core's (logit_alpha, log_lambda, logit_c_suppress) relative 3e-5 (worst
+    seen 1.5e-5, log_lambda at B=32, T=64, H=256); the long channel's four logit
+    gradients, sums over every (b, t, h) of products of three recurrences, 1e-4 (worst
+    seen 5.6e-5); the read's scale and four gains against fp64 autograd of the dense op,
+    2e-5. All are the size of fp32 summation error for such sums.
   * bf16 runs against the fp32 oracle: forward tapes normwise relative <= 2e-2;
     gradients on the same bf16 tapes relative Frobenius error ||hip - oracle||_2 /
     ||oracle||_2 <= 2e-2; end to end (bf16 tapes, then the reverse scan) against the
@@ -90,7 +92,7 @@ def test_core_scan_fp32_forward_backward_match_oracle(cuda_device, B, T, H):
     grads = _core_grads(7 + B, out)
     res = _hip_core_bwd(x, out, grads, torch.float32, cuda_device)
     ob = oracle_core_bwd(inp, fwd, grads)
-    _compare_core_bwd(res, ob, H, 1e-5, 1e-4, rel_err)
+    _compare_core_bwd(res, ob, H, 1e-5, 3e-5, rel_err)
 
 
 @pytest.mark.parametrize("B,T,H", [(3, 5, 6), (5, 1, 36), (40, 1, 2048), (8, 64, 128),
