@@ -35,8 +35,8 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=3)
-    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--batch", type=int, default=None, help="default 16 (train), 256 (decode)")
     p.add_argument("--seq", type=int, default=4096)
     p.add_argument("--state", type=int, default=2048)
