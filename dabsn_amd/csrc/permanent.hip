@@ -14,10 +14,14 @@
 //   dv_t[row] = beta_t Ak,  dbeta_t += Ak e  (sum over rows)
 //   dk_t += g_t[row] s_t + beta_t e a - beta_t Ak s_t  (sum over rows, s_t = state before t)
 //   a = a + g_t[row] k_t - beta_t Ak k_t
-// Workgroups of R waves own R rows; each first recomputes its rows' states s_t into a tape
-// (as the reference's reverse pass does), then runs the adjoint. The sums over rows are
-// deterministic: the R rows of a workgroup are summed through LDS into a per-block
-// partial, and reduce kernels add the blocks (dk) and rows (dbeta) in index order.
+// Workgroups of R waves own R rows; each first recomputes its rows' states, keeping r_t and
+// every kCkpt-th state s_t (plus the final s_T), then runs the adjoint. The adjoint rebuilds
+// s_t from s_{t+1} by undoing the row's update, s_t = s_{t+1} - beta_t (v_t - r_t) k_t, with
+// the same e_t the forward used (r_t is taped), and restarts from a kept state at every
+// checkpoint, so rounding drift spans at most kCkpt - 1 steps. The reference's reverse
+// pass keeps every s_t instead (B H T H floats). The sums over rows are deterministic: the
+// R rows of a workgroup are summed through LDS into a per-block partial, and reduce
+// kernels add the blocks (dk) and rows (dbeta) in index order.
 #include <algorithm>
 
 #include "../../include/dabsn_hip.h"
@@ -29,6 +33,11 @@ namespace permanent {
 
 constexpr int kRowsPerBlock = 8;  // backward: waves (value rows) per workgroup
 constexpr int kFwdRows = 4;       // forward: waves per workgroup
+constexpr int kCkpt = 8;          // backward: steps between kept states
+
+// Kept states of the backward: s_t at index t / kCkpt for t % kCkpt == 0, t < T, and the
+// final state s_T at index ceil(T / kCkpt).
+__host__ __device__ inline int64_t ckpt_slots(int64_t T) { return (T + kCkpt - 1) / kCkpt + 1; }
 
 // Lane's columns c = lane + 64 j, j < CPL; columns past H read and hold zero.
 template <int CPL>
@@ -78,7 +87,7 @@ __global__ void __launch_bounds__(kFwdRows * 64) perm_fwd_kernel(int T, int H,
   }
 }
 
-// Workspace of the backward: state tape [B][H][T][H], r tape [B][T][H], per-block dk
+// Workspace of the backward: kept states [B][H][ckpt_slots(T)][H], r tape [B][T][H], per-block dk
 // partials [B][T][nrb][H], per-row dbeta partials [B][T][H] (fp32, 256-byte aligned).
 struct BwdLayout {
   size_t tape, rtape, pdk, pbeta, end;
@@ -90,7 +99,7 @@ static BwdLayout bwd_layout(int64_t B, int64_t T, int64_t H) {
   const size_t nrb = static_cast<size_t>((H + kRowsPerBlock - 1) / kRowsPerBlock);
   BwdLayout l{};
   size_t o = 0;
-  l.tape = o; o = align_up(o + static_cast<size_t>(B) * H * T * H * 4);
+  l.tape = o; o = align_up(o + static_cast<size_t>(B) * H * ckpt_slots(T) * H * 4);
   l.rtape = o; o = align_up(o + static_cast<size_t>(B) * T * H * 4);
   l.pdk = o; o = align_up(o + static_cast<size_t>(B) * T * nrb * H * 4);
   l.pbeta = o; o = align_up(o + static_cast<size_t>(B) * T * H * 4);
@@ -111,20 +120,21 @@ __global__ void __launch_bounds__(kRowsPerBlock * 64) perm_bwd_kernel(
   const int row = rb * kRowsPerBlock + w;
   const bool live = row < H;  // waves past H take part in the barriers with zeros
   const size_t base = static_cast<size_t>(b) * T * H;
-  float* my_tape = tape + (static_cast<size_t>(b) * H + (live ? row : 0)) * T * H;
+  const int64_t nck = ckpt_slots(T);
+  float* my_tape = tape + (static_cast<size_t>(b) * H + (live ? row : 0)) * nck * H;
 
-  // Forward recompute: s_t (state before step t) and r_t of this row.
+  // Forward recompute: r_t of this row, and the kept states.
   float s[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) s[j] = 0.0f;
   for (int t = 0; t < T; ++t) {
     float kt[CPL];
     load_cols<CPL>(k + base + static_cast<size_t>(t) * H, lane, H, kt);
-    if (live) {
+    if (live && t % kCkpt == 0) {
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = lane + 64 * j;
-        if (c < H) my_tape[static_cast<size_t>(t) * H + c] = s[j];
+        if (c < H) my_tape[static_cast<size_t>(t / kCkpt) * H + c] = s[j];
       }
     }
     const size_t o = base + static_cast<size_t>(t) * H + (live ? row : 0);
@@ -134,24 +144,45 @@ __global__ void __launch_bounds__(kRowsPerBlock * 64) perm_bwd_kernel(
 #pragma unroll
     for (int j = 0; j < CPL; ++j) s[j] = fmaf(e, kt[j], s[j]);
   }
-
-  // Adjoint.
-  float a[CPL];
+  if (live) {
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) a[j] = 0.0f;
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      if (c < H) my_tape[static_cast<size_t>(nck - 1) * H + c] = s[j];
+    }
+  }
+
+  // Adjoint. s_t is the kept state at checkpoint steps (exact, s_0 = 0 among them), else
+  // rebuilt from sn = s_{t+1}: the kept final state at t = T - 1, otherwise the previous
+  // iteration's s_t.
+  float a[CPL], sn[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    a[j] = 0.0f;
+    sn[j] = 0.0f;
+  }
+  if (live && T % kCkpt != 1) load_cols<CPL>(my_tape + static_cast<size_t>(nck - 1) * H, lane, H, sn);
   for (int t = T - 1; t >= 0; --t) {
     float kt[CPL], st[CPL];
     load_cols<CPL>(k + base + static_cast<size_t>(t) * H, lane, H, kt);
-    if (live) {
-      load_cols<CPL>(my_tape + static_cast<size_t>(t) * H, lane, H, st);
-    } else {
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) st[j] = 0.0f;
-    }
     const size_t o = base + static_cast<size_t>(t) * H + (live ? row : 0);
     const float bt = beta[static_cast<size_t>(b) * T + t];
     const float gr = live ? g[o] : 0.0f;
     const float e = live ? v[o] - rtape[o] : 0.0f;
+    if (t % kCkpt == 0) {
+      if (live) {
+        load_cols<CPL>(my_tape + static_cast<size_t>(t / kCkpt) * H, lane, H, st);
+      } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) st[j] = 0.0f;
+      }
+    } else {
+      const float eb = bt * e;  // the forward's beta_t (v_t - r_t), bit for bit
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) st[j] = fmaf(-eb, kt[j], sn[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) sn[j] = st[j];
     const float ak = dot_cols<CPL>(a, kt);
     if (live && lane == 0) {
       dv[o] = bt * ak;

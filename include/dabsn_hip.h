@@ -604,9 +604,10 @@ int dabsn_hip_read_dense_bwd(int64_t B, int64_t T, int64_t N, int64_t H, const f
  * key, value [B,T,H], beta [B,T], fp32 (the op converts other dtypes). Per batch row a
  * state S [H,H] starts at zero; out_t = S k_t, then S += beta_t (v_t - out_t) k_t^T.
  * H <= 2048. Backward: dkey, dvalue [B,T,H], dbeta [B,T] fp32 from grad_out [B,T,H]; it
- * recomputes the per-row state trajectory into the workspace
- * (dabsn_hip_permanent_scan_workspace_bytes(): 4 B T H^2 bytes plus partial sums), as the
- * reference's reverse pass keeps its state tape. Results are deterministic. */
+ * recomputes the per-row states into the workspace, keeping every 8th one and the last
+ * (dabsn_hip_permanent_scan_workspace_bytes(): 4 B (ceil(T/8)+1) H^2 bytes plus r_t and
+ * partial sums), and rebuilds the states in between by undoing each step's update; the
+ * reference's reverse pass keeps all T states. Results are deterministic. */
 int dabsn_hip_permanent_scan_fwd(int64_t B, int64_t T, int64_t H, const float* key,
                                  const float* value, const float* beta, float* out,
                                  hipStream_t stream);

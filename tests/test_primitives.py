@@ -71,10 +71,12 @@ def test_backend_registry_lists_the_primitives():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("B,T,H,unit", [(2, 7, 6, False), (3, 40, 64, True), (2, 33, 100, True),
-                                        (1, 16, 300, True), (2, 1, 16, True), (1, 6, 2048, True)])
+                                        (1, 16, 300, True), (2, 1, 16, True), (1, 6, 2048, True),
+                                        (1, 301, 128, True), (1, 29, 2048, True)])
 def test_permanent_scan_matches_oracle(cuda_device, B, T, H, unit):
     """(2, 7, 6) with raw keys is the reference's release-gate case; unit keys elsewhere
-    keep long scans bounded (|1 - beta| < 1 along k)."""
+    keep long scans bounded (|1 - beta| < 1 along k). T = 301 and (29, 2048) run the
+    backward's state rebuild across many kept-state checkpoints and a ragged last one."""
     k, v, beta, up = _permanent_case(10 + H + T, B, T, H, unit)
     want = oracle.permanent_fwd(k.numpy(), v.numpy(), beta.numpy())
     wdk, wdv, wdb = oracle.permanent_bwd(k.numpy(), v.numpy(), beta.numpy(), up.numpy())
